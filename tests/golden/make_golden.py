@@ -1,0 +1,114 @@
+"""Write the golden fixtures under tests/golden from the reference build.
+
+Runs in the build container only (it needs /root/reference and
+oracle/_ref/tgc_ref, built by `make -C oracle ref`). For every model in
+tests/golden/models (written for this repository from BASELINE.json's configs
+and the reference's feature list, not copied from the reference), the
+reference's own code:
+  1. lowers the surface model to canonical TGIR   (tgc_ref ir       -> src/lower.c, src/ir.c)
+  2. quantizes it                                   (tgc_ref quantize -> src/quant.c)
+  3. runs it over seeded rows                       (tgc_ref batch    -> src/vm.c, src/par.c;
+                                                     --fixed          -> runtime/tg_rtq.h)
+and the results are stored as data: <name>.tgir (model text) and <name>.npz
+(inputs, f32 outputs, Q16.16 inputs/outputs, steps). Run:
+    python tests/golden/make_golden.py
+"""
+import itertools
+import os
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+from oracle import oracle as O  # noqa: E402
+
+MODELS = os.path.join(HERE, "models")
+
+# name: (source model, quantize args or None, fixed-point run?, min-size)
+VARIANTS = {
+    "qmlp_f32": ("qmlp", None, True),
+    "qmlp_q8": ("qmlp", ["--bits", "8"], True),
+    "qmlp_q4": ("qmlp", ["--bits", "4"], True),
+    "qmlp_q4g": ("qmlp", ["--bits", "4", "--method", "gptq", "--calib", "@calib"], True),
+    "mlp3s_q8": ("mlp3s", ["--bits", "8"], True),
+    "mlp3s_q4": ("mlp3s", ["--bits", "4"], False),
+    "odd_f32": ("odd", None, False),
+    "odd_q4": ("odd", ["--bits", "4", "--min-size", "1"], True),
+    "odd_q8": ("odd", ["--bits", "8", "--min-size", "1"], False),
+    "ssm_small_f32": ("ssm_small", None, True),
+    "ssm_small_q8": ("ssm_small", ["--bits", "8", "--min-size", "1"], True),
+    "latent_f32": ("latent", None, True),
+    "latent_q4g": ("latent", ["--bits", "4", "--method", "gptq", "--calib", "@calib", "--min-size", "1"], True),
+    "haltm_f32": ("haltm", None, True),
+    "opsmix_f32": ("opsmix", None, True),
+}
+
+def rows_for(name, per, seed):
+    rng = np.random.default_rng(seed)
+    if name.startswith("latent"):
+        bits = np.array(list(itertools.product([0, 1], repeat=8)), np.float32)  # the whole {0,1}^8 domain
+        return np.concatenate([bits, rng.normal(size=(256, 8)).astype(np.float32)])
+    if name.startswith("opsmix"):
+        x = rng.normal(size=(64, 4)).astype(np.float32) * 2
+        r = rng.integers(-1, 7, size=(64, 2)).astype(np.float32)  # includes out-of-range rows (-1, 6)
+        return np.concatenate([x, r], axis=1)
+    n = 97 if per > 1000 else 64
+    x = rng.normal(size=(n, per)).astype(np.float32)
+    x[0] = 0  # an all-zero row
+    x[1] *= 1e-3  # small values
+    x[2] *= 50  # large values
+    return x
+
+
+def main():
+    if not O.have_ref():
+        sys.exit("oracle/_ref/tgc_ref is missing: run make -C oracle ref")
+    tmp = tempfile.mkdtemp()
+    lowered = {}
+    for f in sorted(os.listdir(MODELS)):
+        if f.endswith(".tg"):
+            base = f[:-3]
+            lowered[base] = O.ref_ir(os.path.join(MODELS, f))
+    for i, (name, (src, qargs, fixed)) in enumerate(sorted(VARIANTS.items())):
+        f32_path = os.path.join(tmp, src + ".tgir")
+        with open(f32_path, "w") as fh:
+            fh.write(lowered[src])
+        m = O.Model(lowered[src])
+        x = rows_for(name, m.per, 1000 + i)
+        extra = {}
+        if qargs is None:
+            text = lowered[src]
+        else:
+            args = list(qargs)
+            if "@calib" in args:
+                calib = np.random.default_rng(7 + i).uniform(-1, 1, size=(300, m.per)).astype(np.float32)
+                cpath = os.path.join(tmp, name + ".calib.csv")
+                with open(cpath, "w") as fh:
+                    for r in calib:
+                        fh.write(",".join("%.9g" % v for v in r) + "\n")
+                args[args.index("@calib")] = cpath
+                extra["calib"] = calib
+            qpath = os.path.join(tmp, name + ".tgir")
+            O.ref_run(["quantize", f32_path, "-o", qpath] + args)
+            with open(qpath) as fh:
+                text = fh.read()
+            extra["qargs"] = np.array(" ".join(qargs))
+        with open(os.path.join(HERE, name + ".tgir"), "w") as fh:
+            fh.write(text)
+        mpath = os.path.join(HERE, name + ".tgir")
+        y, st, _ = O.ref_batch(mpath, x, m.per, m.nout, m.nthink, tmp, threads=4)
+        data = dict(x=x, y=y, steps=st, **extra)
+        if fixed:
+            xq = O.to_fixed_rows(x)
+            yq, sq, _ = O.ref_batch(mpath, xq, m.per, m.nout, m.nthink, tmp, threads=4, fixed=True)
+            data.update(xq=xq, yq=yq, stepsq=sq)
+        np.savez_compressed(os.path.join(HERE, name + ".npz"), **data)
+        print("%-16s rows %4d per %4d out %4d think %d%s" % (name, x.shape[0], m.per, m.nout, m.nthink, " +fixed" if fixed else ""))
+
+
+if __name__ == "__main__":
+    main()

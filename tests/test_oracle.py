@@ -1,0 +1,215 @@
+"""The CPU oracle against the reference's golden vectors, known answers and
+closed forms (CPU only). The fixtures in tests/golden were written by the
+reference's own code (tests/golden/make_golden.py); the oracle must reproduce
+them bit for bit before any GPU result is compared with it."""
+import ctypes
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+NAMES = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(GOLDEN, "*.npz")))
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    if not os.path.exists(O.LIB_PATH):
+        O.build(ref=False)
+
+
+def load(name):
+    with open(os.path.join(GOLDEN, name + ".tgir")) as f:
+        text = f.read()
+    return text, np.load(os.path.join(GOLDEN, name + ".npz"))
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_f32_matches_reference_bit_for_bit(name):
+    text, d = load(name)
+    m = O.Model(text)
+    y, steps = m.batch(d["x"], threads=4)
+    assert np.array_equal(bits(y), bits(d["y"])), "f32 outputs differ from the reference VM"
+    assert np.array_equal(steps, d["steps"])
+
+
+@pytest.mark.parametrize("name", [n for n in NAMES if "xq" in np.load(os.path.join(GOLDEN, n + ".npz")).files])
+def test_fixed_matches_reference_bit_for_bit(name):
+    text, d = load(name)
+    m = O.Model(text)
+    assert np.array_equal(O.to_fixed_rows(d["x"]), d["xq"])
+    yq, sq = m.batch_fixed(d["xq"], threads=4)
+    assert np.array_equal(yq, d["yq"]), "Q16.16 outputs differ from the reference kernels"
+    assert np.array_equal(sq, d["stepsq"])
+
+
+@pytest.mark.parametrize("name", [n for n in NAMES if "qargs" in np.load(os.path.join(GOLDEN, n + ".npz")).files])
+def test_quantizer_matches_reference(name):
+    """Codes and scales from the oracle's quantizer equal the reference's
+    (written by its ir_write), byte for byte, including GPTQ with calibration."""
+    src = name.rsplit("_", 1)[0] + "_f32"
+    if not os.path.exists(os.path.join(GOLDEN, src + ".tgir")):
+        pytest.skip("the f32 source of %s is not kept as a fixture" % name)
+    want, d = load(name)
+    f32_text, _ = load(src)
+    args = str(d["qargs"]).split()
+    bits_ = int(args[args.index("--bits") + 1])
+    gptq = "--method" in args and args[args.index("--method") + 1] == "gptq"
+    min_size = int(args[args.index("--min-size") + 1]) if "--min-size" in args else 256
+    m = O.Model(f32_text)
+    m.quantize(bits_, gptq=gptq, calib=d["calib"] if gptq else None, min_size=min_size)
+    assert m.write() == want
+
+
+def test_writer_is_a_fixed_point():
+    for name in NAMES:
+        text, _ = load(name)
+        assert O.Model(text).write() == text, name
+
+
+def test_latent_reasoner_known_answer():
+    """README.md:49-51 of the reference: `tgc run examples/latent_reasoner.tg
+    1,0,0,1,0,1,1,0` prints 0.225605994 0.24476327 0.162138939 0.367491812,
+    steps 0 9."""
+    text, _ = load("latent_f32")
+    y, s = O.Model(text).batch(np.array([[1, 0, 0, 1, 0, 1, 1, 0]], np.float32))
+    assert ["%.9g" % v for v in y[0]] == ["0.225605994", "0.24476327", "0.162138939", "0.367491812"]
+    assert s[0, 0] == 9
+
+
+def test_rand_initializer_reproduces_lowered_params():
+    """rand(seed, scale) (src/lower.c:661-775): the lowered w_emb/w_core/
+    w_inj/w_out of the latent model are rand(11, .35), rand(23, .12),
+    rand(37, .10), rand(41, .5)."""
+    text, _ = load("latent_f32")
+    for name, seed, scale, n in [("w_emb", 11, 0.35, 128), ("w_core", 23, 0.12, 256), ("w_inj", 37, 0.10, 256), ("w_out", 41, 0.5, 64)]:
+        i = text.index("(param %s " % name)
+        body = text[text.index("(data", i) + 5:text.index("))", i)]
+        vals = np.array([float(t) for t in body.split()], np.float32)
+        assert np.array_equal(bits(vals), bits(O.rand(seed, scale, n))), name
+
+
+def test_fixed_vs_float_bound():
+    """tests/run.sh:306-322: a fixed-point unit stays within 5e-4 of the float VM."""
+    for name in ("latent_f32", "latent_q4g", "qmlp_q4g", "qmlp_q8", "ssm_small_q8"):
+        text, d = load(name)
+        m = O.Model(text)
+        x = d["x"][3:64]  # rows 0-2 are the zero / tiny / x50 edge rows
+        y, _ = m.batch(x)
+        yq, _ = m.batch_fixed(O.to_fixed_rows(x))
+        err = np.abs(yq / 65536.0 - y.astype(np.float64))
+        assert err.max() < 5e-4, (name, err.max())
+
+
+def test_thread_invariance():
+    """tests/run.sh:114-127: -j 1 and -j N are byte-identical."""
+    text, d = load("mlp3s_q8")
+    m = O.Model(text)
+    y1, _ = m.batch(d["x"], threads=1)
+    y8, _ = m.batch(d["x"], threads=8)
+    assert np.array_equal(bits(y1), bits(y8))
+
+
+def test_int4_nibble_rule():
+    """tg_qget (runtime/tg_rt.h:124-129): element i in byte i/2, low nibble
+    first, sign-extended; checked against the codes the reference wrote."""
+    text, _ = load("odd_q4")
+    i = text.index("(param W ")
+    codes = np.array(text[text.index("(codes", i) + 6:text.index(")", text.index("(codes", i))].split(), int)
+    assert codes.size == 33 * 513 and codes.size % 2 == 1
+    assert codes.min() >= -7 and codes.max() <= 7
+
+
+# ---- Q16.16 primitives against their mathematical definitions ----
+
+def prim(op, a, b=0):
+    f = O.lib().tgo_fx_prim
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
+    return f(op, a, b)
+
+
+def test_exp_coefficients_are_inverse_factorials():
+    for j in range(9):
+        assert prim(8, j) == int(round((1 << 30) / math.factorial(j) + 1e-12)), j
+
+
+def test_isqrt64_is_floor_sqrt():
+    rng = np.random.default_rng(3)
+    vals = [0, 1, 2, 3, 4, 15, 16, 17, (1 << 32) - 1, 1 << 32, (1 << 62) - 1, (1 << 62), (1 << 63) - 1]
+    vals += [int(v) for v in rng.integers(0, 1 << 62, size=2000, dtype=np.int64)]
+    for v in vals:
+        assert prim(4, v) == math.isqrt(v), v
+
+
+def test_fdiv_rounding():
+    """tg_fdiv (runtime/tg_rtq.h:32-37): with a positive divisor the quotient
+    a * 2^16 / b is rounded half away from zero. With a negative divisor the
+    reference adds the half-divisor on the wrong side, so the magnitude is
+    floor((|n| - h) / |b|), one below the rounded value for most inputs (e.g.
+    1 / -2 gives -32767, not -32768). The oracle keeps that behaviour because
+    the reference's kernels (golden vectors) do."""
+    rng = np.random.default_rng(4)
+    for _ in range(5000):
+        a, b = (int(v) for v in rng.integers(-(1 << 31), 1 << 31, size=2))
+        if b == 0:
+            continue
+        n, h = a * 65536, abs(b) // 2
+        if b > 0:
+            mag = (abs(n) * 2 + b) // (2 * b)
+        else:
+            mag = max(abs(n) - h, 0) // abs(b)
+            exact = abs(n) / abs(b)
+            assert mag in (round(exact) - 1, round(exact), math.floor(exact)) or abs(mag - exact) <= 1
+        q = mag if (n >= 0) == (b > 0) else -mag
+        q = max(-(1 << 31), min((1 << 31) - 1, q))
+        assert prim(1, a, b) == q, (a, b)
+    assert prim(1, 1, -2) == -32767 and prim(1, 1, 2) == 32768
+    assert prim(1, 5, 0) == (1 << 31) - 1 and prim(1, -5, 0) == -(1 << 31) and prim(1, 0, 0) == 0
+
+
+def test_fmul_rounds_half_up():
+    rng = np.random.default_rng(5)
+    for _ in range(5000):
+        a, b = (int(v) for v in rng.integers(-(1 << 31), 1 << 31, size=2))
+        q = (a * b + 32768) >> 16
+        assert prim(0, a, b) == max(-(1 << 31), min((1 << 31) - 1, q))
+
+
+def test_expq_tracks_exp():
+    for x in np.linspace(-12, 10.39, 4001):
+        q = int(round(x * 65536))
+        got = prim(2, q) / 65536.0
+        want = math.exp(q / 65536.0)
+        assert abs(got - want) <= 3e-5 * max(1.0, want), x  # degree-8 polynomial in Q30
+    assert prim(2, 11 * 65536) == (1 << 31) - 1 and prim(2, -13 * 65536) == 0
+
+
+def test_tanhq_and_sigmoidq_track_float():
+    for x in np.linspace(-10, 10, 2001):
+        q = int(round(x * 65536))
+        assert abs(prim(6, q) / 65536.0 - math.tanh(q / 65536.0)) < 4e-5
+        assert abs(prim(7, q) / 65536.0 - 1 / (1 + math.exp(-q / 65536.0))) < 4e-5
+
+
+def test_planted_mistake_is_caught():
+    """A plausible oracle mistake (a transposed quantized operand) must fail the
+    golden comparison: swap W's axis on a copy of the model and re-run."""
+    text, d = load("qmlp_q8")
+    broken = text.replace("(quant 8 0", "(quant 8 1", 1)
+    with pytest.raises(ValueError):
+        O.Model(broken)  # the channel count no longer matches: the reader refuses it
+    text4, d4 = load("odd_q4")
+    m = O.Model(text4)
+    y, _ = m.batch(d4["x"])
+    assert np.array_equal(bits(y), bits(d4["y"]))
+    y_bad, _ = m.batch(d4["x"][:, ::-1].copy())  # a reversed input order changes the sums
+    assert not np.array_equal(bits(y_bad), bits(d4["y"]))
