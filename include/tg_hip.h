@@ -1,0 +1,101 @@
+/* tg_hip: MI355X (gfx950) batch backend for Technograd's quantized `tgc batch`.
+ *
+ * A plain C ABI: no C++ or framework types, caller-owned host buffers, int
+ * status codes (0 ok, < 0 error) with the message in tg_hip_error(). The
+ * library never exits the process and never prints.
+ *
+ * Reference seams this replaces (file:line in the reference tree):
+ *   tg_hip_load        the per-row interpreter setup `load_module` + `plan`
+ *                      (src/util.c:335-369, src/plan.c:154-224): the model is
+ *                      handed over as canonical TGIR text (what `ir_write`,
+ *                      src/ir.c:150-202, writes for a loaded Module), and its
+ *                      arena becomes one device allocation.
+ *   tg_hip_batch       the block loop of `tgc batch` (src/main.c:431-441):
+ *                      par_for(batch_rows) -> vm_run_into per row
+ *                      (src/main.c:231-242, src/vm.c:475-481), for stateless
+ *                      models (m->nupd == 0, src/main.c:435).
+ *   tg_hip_batch_fixed the same over Q16.16 integers, with the kernels of a
+ *                      `tgc c --fixed` unit (runtime/tg_rtq.h, src/cgen.c:100-314).
+ *   tg_hip_matmul_q    one quantized matmul with tg_matmul_qa / tg_matmul_qb's
+ *                      arguments (runtime/tg_rt.h:132-151), the per-instruction
+ *                      dispatch point src/vm.c:277-281.
+ *
+ * Numerics: integer and Q16.16 results are bit-exact with the reference. f32
+ * results are bit-exact except for transcendentals (device libm) and, on the
+ * fast path, quantized matmuls, which use int8 matrix cores with exact
+ * integer products and round the dot product once (TG_HIP_EXACT selects the
+ * reference's sequential f32 order instead). */
+#ifndef TG_HIP_H
+#define TG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct tg_hip_prog tg_hip_prog;
+
+/* tg_hip_load flags */
+#define TG_HIP_FIXED   1  /* run in Q16.16 (the `--fixed` number system) */
+#define TG_HIP_EXACT   2  /* quantized matmuls in the reference's sequential f32 order */
+#define TG_HIP_ROWPROG 4  /* force the one-lane-per-row executor for any model */
+#define TG_HIP_TIMING  8  /* time every kernel with HIP events (tg_hip_stats) */
+
+typedef struct {
+	int executor;        /* 0: layer executor, 1: row-program executor */
+	int rows;            /* rows of the last batch */
+	double batch_ms;     /* device time of the last batch call (HIP events) */
+	double qgemm_ms;     /* time in quantized-matmul kernels (TG_HIP_TIMING) */
+	long qgemm_calls;
+	double digits_ms;    /* time in activation-digit kernels (TG_HIP_TIMING) */
+	double other_ms;     /* time in the remaining kernels (TG_HIP_TIMING) */
+	double weight_bytes; /* packed quantized weight bytes the program reads per pass */
+	double macs;         /* multiply-adds of quantized matmuls per row */
+	long arena_bytes;    /* device arena of the program at its row capacity */
+} tg_hip_stats_t;
+
+/* Select the device (ordinal) for subsequent calls; 0 on success. */
+int tg_hip_init(int device);
+
+/* Build a device program from TGIR text. max_rows bounds the rows of one
+ * device pass (larger batches run in passes). Returns NULL when the model is
+ * outside what the backend runs (state updates, unsupported ops) or on a
+ * device error; the caller then keeps the CPU interpreter. */
+tg_hip_prog *tg_hip_load(const char *tgir, size_t len, int flags, int max_rows);
+
+/* Row layout: floats per input row, per output row, think loops (steps per row). */
+int tg_hip_info(const tg_hip_prog *p, int *per, int *nout, int *nthink);
+
+/* Host buffers: rows [nrows][per] -> out [nrows][nout], steps [nrows][max(nthink,1)]
+ * (steps may be NULL). Synchronous. */
+int tg_hip_batch(tg_hip_prog *p, const float *rows, long nrows, float *out, int *steps);
+int tg_hip_batch_fixed(tg_hip_prog *p, const int32_t *rows, long nrows, int32_t *out, int *steps);
+
+/* Device buffers (from tg_hip_dev_alloc), nrows <= max_rows. Asynchronous on
+ * the program's stream; tg_hip_sync waits. */
+int tg_hip_batch_device(tg_hip_prog *p, const void *d_rows, long nrows, void *d_out, int *d_steps);
+int tg_hip_sync(tg_hip_prog *p);
+
+/* One quantized matmul with the reference kernel's arguments, host buffers:
+ * axis 0: o[m,n] = diag(s) Q[m,k] @ b[k,n]  (tg_matmul_qa)
+ * axis 1: o[m,n] = b[m,k] @ Q[k,n] diag(s)  (tg_matmul_qb; b is the left operand) */
+int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, const float *b, int m, int k, int n, int axis,
+		    int flags);
+
+void tg_hip_free(tg_hip_prog *p);
+const char *tg_hip_error(void);
+int tg_hip_stats(const tg_hip_prog *p, tg_hip_stats_t *st);
+int tg_hip_reset_stats(tg_hip_prog *p);
+
+/* Device memory helpers for callers without their own allocator. */
+void *tg_hip_dev_alloc(size_t bytes);
+int tg_hip_dev_free(void *d);
+int tg_hip_h2d(void *d, const void *h, size_t bytes);
+int tg_hip_d2h(void *h, const void *d, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,238 @@
+// Layer-executor kernels: one launch per model instruction over a block of
+// batch rows. Values of a batch live as [rows][numel] in one device arena;
+// params and constants are shared by all rows (row stride 0).
+//
+// Arithmetic follows the reference kernels (runtime/tg_rt.h) operation for
+// operation: the same expression shapes, sums in index order from 0.0f,
+// separate multiply and add (this file is compiled with -ffp-contract=off),
+// correctly rounded division and square root. Transcendentals come from the
+// ROCm device library, so only they differ from glibc (by a few ulp).
+#include "tg_kern.h"
+#include "tgm.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr int TPB = 256;
+
+inline unsigned blocks_for(long n) { return (unsigned)((n + TPB - 1) / TPB); }
+
+__device__ inline float bop(int op, float x, float y)
+{
+	switch (op) {
+	case TGK_ADD: return x + y;
+	case TGK_SUB: return x - y;
+	case TGK_MUL: return x * y;
+	case TGK_DIV: return x / y;
+	case TGK_MAX: return x > y ? x : y;
+	default: return x < y ? x : y;
+	}
+}
+
+__global__ void binary_k(int op, float *o, long ors, int n, tgk_opd a, int am, const int *amap, tgk_opd b, int bm, const int *bmap,
+			 long total)
+{
+	long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+	if (t >= total) return;
+	long r = t / n;
+	int i = (int)(t - r * n);
+	int ia = am == 0 ? i : am == 1 ? 0 : amap[i];
+	int ib = bm == 0 ? i : bm == 1 ? 0 : bmap[i];
+	o[r * ors + i] = bop(op, a.p[r * a.rs + ia], b.p[r * b.rs + ib]);
+}
+
+// tg_rt.h:40-75
+__device__ inline float uop(int op, float x)
+{
+	switch (op) {
+	case TGM_NEG: return -x;
+	case TGM_TANH: return tanhf(x);
+	case TGM_RELU: return x > 0.0f ? x : 0.0f;
+	case TGM_SIGMOID: return 1.0f / (1.0f + expf(-x));
+	case TGM_EXP: return expf(x);
+	case TGM_SQRT: return sqrtf(x);
+	case TGM_GELU: return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
+	case TGM_SILU: return x / (1.0f + expf(-x));
+	case TGM_SOFTPLUS: return (x > 0.0f ? x : 0.0f) + log1pf(expf(-fabsf(x)));
+	case TGM_LOG: return logf(x);
+	case TGM_SIN: return sinf(x);
+	case TGM_COS: return cosf(x);
+	case TGM_FLOOR: return floorf(x);
+	default: return x > 0.0f ? 1.0f : 0.0f; // step
+	}
+}
+
+__global__ void unary_k(int op, float *o, long ors, tgk_opd a, int n, long total)
+{
+	long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+	if (t >= total) return;
+	long r = t / n;
+	int i = (int)(t - r * n);
+	o[r * ors + i] = uop(op, a.p[r * a.rs + i]);
+}
+
+__device__ inline int code_at(const uint8_t *q, int bits, long i)
+{
+	if (bits == 8) return (signed char)q[i];
+	int b = (signed char)q[i >> 1];
+	return (i & 1) ? (b >> 4) : (int)(signed char)(unsigned char)((unsigned)b << 4) >> 4;
+}
+
+__global__ void mm_exact_k(tgk_mm d, long total)
+{
+	long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+	if (t >= total) return;
+	int j = (int)(t % d.n);
+	long u = t / d.n;
+	int i = (int)(u % d.m);
+	u /= d.m;
+	int g = (int)(u % d.g);
+	long r = u / d.g;
+	const float *A = d.a.p + r * d.a.rs + g * d.ag + i * d.ai;
+	const float *B = d.b.p + r * d.b.rs + g * d.bg + (long)j * d.bj;
+	float acc = 0.0f;
+	if (d.quant == 1) {
+		long base = (long)g * d.m * d.k + (long)i * d.k;
+		for (int p = 0; p < d.k; p++) acc += (float)code_at(d.codes, d.bits, base + p) * B[p * d.bp];
+		acc = d.scale[i] * acc;
+	} else if (d.quant == 2) {
+		for (int p = 0; p < d.k; p++) acc += A[p * d.ap] * (float)code_at(d.codes, d.bits, (long)p * d.n + j);
+		acc = d.scale[j] * acc;
+	} else {
+		for (int p = 0; p < d.k; p++) acc += A[p * d.ap] * B[p * d.bp];
+	}
+	d.o[r * d.ors + g * d.og + i * d.oi + (long)j * d.oj] = acc;
+}
+
+// tg_rt.h:154-175
+__global__ void rowop_k(int op, float *o, long ors, tgk_opd a, int nrow, int cols, long total)
+{
+	long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+	if (t >= total) return;
+	long r = t / nrow;
+	int q = (int)(t - r * nrow);
+	const float *x = a.p + r * a.rs + (long)q * cols;
+	float *y = o + r * ors + (long)q * cols;
+	if (op == TGM_SOFTMAX) {
+		float mx = x[0], s = 0.0f;
+		for (int i = 1; i < cols; i++)
+			if (x[i] > mx) mx = x[i];
+		for (int i = 0; i < cols; i++) {
+			y[i] = expf(x[i] - mx);
+			s += y[i];
+		}
+		for (int i = 0; i < cols; i++) y[i] /= s;
+	} else {
+		float s = 0.0f;
+		for (int i = 0; i < cols; i++) s += x[i] * x[i];
+		float inv = 1.0f / sqrtf(s / (float)cols + 1e-6f);
+		for (int i = 0; i < cols; i++) y[i] = x[i] * inv;
+	}
+}
+
+__global__ void reduce_k(int op, float *o, long ors, tgk_opd a, int n, int rows)
+{
+	int r = blockIdx.x * blockDim.x + threadIdx.x;
+	if (r >= rows) return;
+	const float *x = a.p + (long)r * a.rs;
+	float s = 0.0f;
+	for (int i = 0; i < n; i++) s += x[i];
+	o[(long)r * ors] = op == TGM_SUM ? s : s / (float)n;
+}
+
+__global__ void transpose_k(float *o, long ors, tgk_opd a, int g, int R, int C, long total)
+{
+	long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+	if (t >= total) return;
+	long per = (long)g * R * C;
+	long r = t / per, e = t - r * per;
+	int z = (int)(e / ((long)R * C)), rem = (int)(e % ((long)R * C)), i = rem / C, j = rem % C;
+	o[r * ors + (long)z * R * C + (long)j * R + i] = a.p[r * a.rs + e];
+}
+
+__global__ void outer_k(float *o, long ors, tgk_opd a, int m, tgk_opd b, int n, long total)
+{
+	long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+	if (t >= total) return;
+	long per = (long)m * n, r = t / per;
+	int e = (int)(t - r * per), i = e / n, j = e % n;
+	o[r * ors + e] = a.p[r * a.rs + i] * b.p[r * b.rs + j];
+}
+
+// tg_rt.h:200-204 (index rounding) and :316-323
+__global__ void take_k(float *o, long ors, tgk_opd w, tgk_opd idx, int cnt, int d, int h, long total)
+{
+	long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+	if (t >= total) return;
+	long per = (long)cnt * h, r = t / per;
+	int e = (int)(t - r * per), i = e / h, j = e % h;
+	float rr = floorf(idx.p[r * idx.rs + i] + 0.5f);
+	int row = rr >= 0.0f && rr < (float)d ? (int)rr : -1;
+	o[r * ors + e] = row >= 0 ? w.p[r * w.rs + (long)row * h + j] : 0.0f;
+}
+
+__global__ void copy_k(float *o, long ors, long ooff, tgk_opd a, long aoff, int w, long total)
+{
+	long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+	if (t >= total) return;
+	long r = t / w;
+	int i = (int)(t - r * w);
+	o[r * ors + ooff + i] = a.p[r * a.rs + aoff + i];
+}
+
+} // namespace
+
+void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int amode, const int *amap, tgk_opd b, int bmode,
+		const int *bmap, int rows)
+{
+	long total = (long)rows * n;
+	if (total > 0) binary_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, n, a, amode, amap, b, bmode, bmap, total);
+}
+
+void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows)
+{
+	long total = (long)rows * n;
+	if (total > 0) unary_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, n, total);
+}
+
+void tgk_matmul_exact(hipStream_t s, const tgk_mm *d, int rows)
+{
+	long total = (long)rows * d->g * d->m * d->n;
+	if (total > 0) mm_exact_k<<<blocks_for(total), TPB, 0, s>>>(*d, total);
+}
+
+void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, int cols, int rows)
+{
+	long total = (long)rows * nrow;
+	if (total > 0) rowop_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, nrow, cols, total);
+}
+
+void tgk_reduce(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows)
+{
+	if (rows > 0) reduce_k<<<blocks_for(rows), TPB, 0, s>>>(op, o, ors, a, n, rows);
+}
+
+void tgk_transpose(hipStream_t s, float *o, long ors, tgk_opd a, int g, int r, int c, int rows)
+{
+	long total = (long)rows * g * r * c;
+	if (total > 0) transpose_k<<<blocks_for(total), TPB, 0, s>>>(o, ors, a, g, r, c, total);
+}
+
+void tgk_outer(hipStream_t s, float *o, long ors, tgk_opd a, int m, tgk_opd b, int n, int rows)
+{
+	long total = (long)rows * m * n;
+	if (total > 0) outer_k<<<blocks_for(total), TPB, 0, s>>>(o, ors, a, m, b, n, total);
+}
+
+void tgk_take(hipStream_t s, float *o, long ors, tgk_opd w, tgk_opd idx, int cnt, int d, int h, int rows)
+{
+	long total = (long)rows * cnt * h;
+	if (total > 0) take_k<<<blocks_for(total), TPB, 0, s>>>(o, ors, w, idx, cnt, d, h, total);
+}
+
+void tgk_copy(hipStream_t s, float *o, long ors, long ooff, tgk_opd a, long aoff, int w, int rows)
+{
+	long total = (long)rows * w;
+	if (total > 0) copy_k<<<blocks_for(total), TPB, 0, s>>>(o, ors, ooff, a, aoff, w, total);
+}

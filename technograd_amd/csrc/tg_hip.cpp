@@ -1,0 +1,1247 @@
+// tg_hip: device programs for Technograd models on MI355X, behind a C ABI.
+//
+// A model (TGIR text) becomes one of two device programs:
+//
+//  * layer program: every instruction is one kernel over a block of batch
+//    rows; values of the block live as [rows][numel] in one device arena
+//    (the reference's per-row static arena, src/plan.c:154-224, widened to a
+//    block of rows and allocated once); quantized matmuls run on the int8
+//    matrix cores (kern_qgemm.hip), everything else on the exact kernels of
+//    kern_layer.hip. Scans step through time on the host, each step a few
+//    kernels over all rows.
+//  * row program: one lane per batch row interprets the whole model
+//    (kern_rowprog.hip). Used for think loops (per-row halting), for Q16.16,
+//    and on request.
+//
+// The batch loop mirrors `tgc batch` (src/main.c:400-444): rows are processed
+// in blocks (here: device passes of up to max_rows rows), outputs come back in
+// input order, and steps per row are reported for every think loop.
+#include "tg_hip.h"
+#include "tg_kern.h"
+#include "tgm.h"
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local char g_err[512];
+
+void seterr(const char *fmt, ...)
+{
+	va_list ap;
+	va_start(ap, fmt);
+	vsnprintf(g_err, sizeof g_err, fmt, ap);
+	va_end(ap);
+}
+
+bool hipok(hipError_t e, const char *what)
+{
+	if (e == hipSuccess) return true;
+	seterr("%s: %s", what, hipGetErrorString(e));
+	return false;
+}
+
+enum { SP_ARENA, SP_IN, SP_POOL, SP_OUT, SP_NONE };
+
+struct Opnd {
+	int space = SP_NONE;
+	long off = 0; // SP_ARENA: per-row float offset of the value; others: float offset
+	long rs = 0;  // row stride in floats (0 for pool values)
+};
+
+enum { ST_BIN, ST_UN, ST_MM, ST_QGEMM, ST_ROW, ST_RED, ST_TRANS, ST_OUTER, ST_TAKE, ST_COPY, ST_SCAN, ST_FILL_STEPS };
+
+struct Step {
+	int kind = 0, op = 0;
+	Opnd o, a, b;
+	int n = 0, amode = 0, bmode = 0;
+	long amap = 0, bmap = 0;
+	// generic matmul
+	int g = 1, m = 1, k = 1, nn = 1, quant = 0, bits = 0;
+	long ag = 0, ai = 0, ap = 0, bg = 0, bp = 0, bj = 0, og = 0, oi = 0, oj = 0;
+	long codes = 0, scale = 0; // offsets into the code / scale pools
+	// quantized GEMM
+	int qw = -1, ni = 1;
+	long xr = 0, xj = 0, xk = 0, orr = 0, oc = 0, ojj = 0;
+	// row ops, transpose, take
+	int p0 = 0, p1 = 0, p2 = 0;
+	// copy
+	long ooff = 0, aoff = 0;
+	int dyn_a = 0, dyn_o = 0;
+	// scan
+	int T = 0, reverse = 0, body_lo = 0, body_hi = 0, stid = -1;
+};
+
+} // namespace
+
+struct tg_hip_prog {
+	tgm_module *m = nullptr;
+	int flags = 0, executor = 0, fixed = 0;
+	int max_rows = 0;
+	hipStream_t st = nullptr;
+	// pools
+	float *d_pool = nullptr;
+	int *d_imap = nullptr;
+	uint8_t *d_codes = nullptr;
+	float *d_fscale = nullptr;
+	int *d_qscale = nullptr;
+	// layer program
+	std::vector<Step> steps;
+	std::vector<tgk_qweight> qws;
+	long arena_floats = 0; // per row
+	float *d_arena = nullptr;
+	void *d_scratch = nullptr;
+	size_t scratch_bytes = 0;
+	Opnd out;
+	// row program
+	std::vector<rp_ins> rprog;
+	rp_ins *d_rprog = nullptr;
+	long rp_arena = 0;
+	int rp_in_slot = 0, rp_out_ref = 0;
+	// batch buffers
+	float *d_in = nullptr, *d_out = nullptr;
+	int *d_steps = nullptr;
+	// stats
+	tg_hip_stats_t stats{};
+	hipEvent_t ev0 = nullptr, ev1 = nullptr;
+	std::vector<hipEvent_t> tev;
+};
+
+namespace {
+
+// ---------------------------------------------------------------- pools ----
+
+struct Pools {
+	std::vector<float> f;      // params and constants (f32, or Q16.16 words when fixed)
+	std::vector<int> imap;     // broadcast index maps
+	std::vector<uint8_t> codes;
+	std::vector<float> fscale;
+	std::vector<int> qscale;   // Q7.24
+	std::vector<long> pool_of; // value -> pool offset, -1 if none
+	std::vector<long> codes_of, scale_of;
+};
+
+int32_t to_fixed(double v, int frac)
+{
+	double s = v * (double)(1LL << frac);
+	if (s >= 2147483647.0) return INT32_MAX;
+	if (s <= -2147483648.0) return INT32_MIN;
+	return (int32_t)llround(s);
+}
+
+float fixed_word(double v) // a Q16.16 integer stored in a float slot
+{
+	int32_t q = to_fixed(v, 16);
+	float f;
+	memcpy(&f, &q, 4);
+	return f;
+}
+
+long pool_param(Pools &P, const tgm_module *m, int v, bool fixed)
+{
+	if (P.pool_of[v] >= 0) return P.pool_of[v];
+	const tgm_value &x = m->val[v];
+	long off = (long)P.f.size();
+	for (long i = 0; i < x.n; i++) P.f.push_back(fixed ? fixed_word(x.data[i]) : x.data[i]);
+	while (P.f.size() % 16) P.f.push_back(0.0f);
+	P.pool_of[v] = off;
+	return off;
+}
+
+long pool_codes(Pools &P, const tgm_module *m, int v)
+{
+	if (P.codes_of[v] >= 0) return P.codes_of[v];
+	const tgm_value &x = m->val[v];
+	long off = (long)P.codes.size(), nb = x.qbits == 8 ? x.n : (x.n + 1) / 2;
+	P.codes.insert(P.codes.end(), x.q, x.q + nb);
+	while (P.codes.size() % 16) P.codes.push_back(0);
+	int nch = x.sh.dim[x.qaxis];
+	P.scale_of[v] = (long)P.fscale.size();
+	for (int i = 0; i < nch; i++) {
+		P.fscale.push_back(x.qs[i]);
+		P.qscale.push_back(to_fixed(x.qs[i], 24));
+	}
+	P.codes_of[v] = off;
+	return off;
+}
+
+// ------------------------------------------------------- shape helpers ----
+
+long numel(const tgm_shape &s) { return tgm_numel(&s); }
+
+void matmul_dims(const tgm_shape &a, const tgm_shape &b, int &m, int &k, int &n, int &g)
+{
+	g = a.rank == 3 && b.rank == 3 ? a.dim[0] : 1;
+	m = a.rank == 3 ? (g > 1 || b.rank == 3 ? a.dim[1] : a.dim[0] * a.dim[1]) : a.rank == 2 ? a.dim[0] : 1;
+	k = a.dim[a.rank - 1];
+	n = b.rank >= 2 ? b.dim[b.rank - 1] : 1;
+}
+
+// which axis a param needs as operand of a matmul (src/ops.c:310-320)
+int q_axis_for(const tgm_module *m, int v, const tgm_ins &in)
+{
+	if (m->val[v].sh.rank != 2 || in.op != TGM_MATMUL) return -1;
+	if (in.a[0] == v && in.a[1] != v) return 0;
+	if (in.a[1] == v && in.a[0] != v) return 1;
+	return -1;
+}
+
+// Broadcast index maps: for every output element, the element of each operand
+// it reads (NumPy broadcasting, dimensions aligned from the right), or mode 0
+// (same element) / 1 (the single element) when no map is needed.
+void bcast(const tgm_shape &so, const tgm_shape &sa, std::vector<int> &imap, int &mode, long &mapoff)
+{
+	long n = numel(so), na = numel(sa);
+	mapoff = 0;
+	if (na == n) {
+		mode = 0;
+		return;
+	}
+	if (na == 1) {
+		mode = 1;
+		return;
+	}
+	mode = 2;
+	mapoff = (long)imap.size();
+	int r = so.rank, idx[TGM_MAXRANK] = { 0 };
+	long st[TGM_MAXRANK], acc = 1;
+	for (int i = r - 1; i >= 0; i--) {
+		int j = i - (r - sa.rank), d = j >= 0 ? sa.dim[j] : 1;
+		st[i] = d == 1 ? 0 : acc;
+		acc *= d;
+	}
+	for (long e = 0; e < n; e++) {
+		long ia = 0;
+		for (int i = 0; i < r; i++) ia += idx[i] * st[i];
+		imap.push_back((int)ia);
+		for (int i = r - 1; i >= 0; i--) {
+			if (++idx[i] < so.dim[i]) break;
+			idx[i] = 0;
+		}
+	}
+}
+
+bool has_think(const tgm_block *b)
+{
+	for (int i = 0; i < b->len; i++) {
+		if (b->v[i].op == TGM_THINK) return true;
+		if (b->v[i].body && has_think(b->v[i].body)) return true;
+	}
+	return false;
+}
+
+// ------------------------------------------------------ layer program ----
+
+struct LB {
+	tg_hip_prog *p;
+	tgm_module *m;
+	Pools P;
+	std::vector<Opnd> where; // value -> operand
+	std::vector<char> loopw; // values written in place by loops (scan carries, slices, stacks)
+};
+
+Opnd value_opnd(LB &L, int v)
+{
+	Opnd &w = L.where[v];
+	if (w.space != SP_NONE) return w;
+	const tgm_value &x = L.m->val[v];
+	if (x.kind == TGM_PARAM || x.kind == TGM_STATE) {
+		w.space = SP_POOL;
+		w.off = pool_param(L.P, L.m, v, false);
+		w.rs = 0;
+	} else if (x.kind == TGM_INPUT) {
+		w.space = SP_IN;
+		w.off = x.in_off;
+		w.rs = L.m->per;
+	} else {
+		w.space = SP_ARENA;
+		w.off = L.p->arena_floats;
+		w.rs = x.n;
+		L.p->arena_floats += (x.n + 63) / 64 * 64;
+	}
+	return w;
+}
+
+bool layer_block(LB &L, const tgm_block *b);
+
+bool layer_ins(LB &L, const tgm_ins &in)
+{
+	tgm_module *m = L.m;
+	auto &S = L.p->steps;
+	Step s;
+	switch (in.op) {
+	case TGM_CONST: {
+		long off = (long)L.P.f.size();
+		L.P.f.push_back(in.k);
+		while (L.P.f.size() % 16) L.P.f.push_back(0.0f);
+		Opnd &w = L.where[in.out];
+		w.space = SP_POOL;
+		w.off = off;
+		w.rs = 0;
+		return true;
+	}
+	case TGM_RESHAPE: {
+		Opnd a = value_opnd(L, in.a[0]);
+		if (!L.loopw[in.a[0]] && !L.loopw[in.out]) { // same elements, new shape: share the operand
+			L.where[in.out] = a;
+			return true;
+		}
+		s.kind = ST_COPY;
+		s.o = value_opnd(L, in.out);
+		s.a = a;
+		s.n = (int)m->val[in.out].n;
+		break;
+	}
+	case TGM_ADD: case TGM_SUB: case TGM_MUL: case TGM_DIV: case TGM_MAX: case TGM_MIN:
+		s.kind = ST_BIN;
+		s.op = in.op - TGM_ADD;
+		s.a = value_opnd(L, in.a[0]);
+		s.b = value_opnd(L, in.a[1]);
+		s.o = value_opnd(L, in.out);
+		s.n = (int)m->val[in.out].n;
+		bcast(m->val[in.out].sh, m->val[in.a[0]].sh, L.P.imap, s.amode, s.amap);
+		bcast(m->val[in.out].sh, m->val[in.a[1]].sh, L.P.imap, s.bmode, s.bmap);
+		break;
+	case TGM_NEG: case TGM_TANH: case TGM_RELU: case TGM_SIGMOID: case TGM_EXP: case TGM_SQRT: case TGM_GELU:
+	case TGM_SILU: case TGM_SOFTPLUS: case TGM_LOG: case TGM_SIN: case TGM_COS: case TGM_FLOOR: case TGM_STEP:
+		s.kind = ST_UN;
+		s.op = in.op;
+		s.a = value_opnd(L, in.a[0]);
+		s.o = value_opnd(L, in.out);
+		s.n = (int)m->val[in.out].n;
+		break;
+	case TGM_MATMUL: {
+		const tgm_value &va = m->val[in.a[0]], &vb = m->val[in.a[1]];
+		int mm, kk, nn, gg;
+		matmul_dims(va.sh, vb.sh, mm, kk, nn, gg);
+		int quant = 0;
+		if (gg == 1 && va.qbits && q_axis_for(m, in.a[0], in) == va.qaxis) quant = 1;
+		else if (gg == 1 && vb.qbits && q_axis_for(m, in.a[1], in) == vb.qaxis) quant = 2;
+		s.o = value_opnd(L, in.out);
+		if (quant && !(L.p->flags & TG_HIP_EXACT)) {
+			const tgm_value &w = quant == 1 ? va : vb;
+			int v = quant == 1 ? in.a[0] : in.a[1];
+			Opnd x = value_opnd(L, quant == 1 ? in.a[1] : in.a[0]);
+			tgk_qweight qw;
+			int C = w.sh.dim[w.qaxis], K = w.sh.dim[1 - w.qaxis];
+			if (tgk_qweight_pack(&qw, w.q, w.qs, w.qbits, w.qaxis, C, K, L.p->st)) {
+				seterr("cannot place the weights of '%s' on the device", w.name ? w.name : "?");
+				return false;
+			}
+			(void)v;
+			L.p->qws.push_back(qw);
+			s.kind = ST_QGEMM;
+			s.qw = (int)L.p->qws.size() - 1;
+			s.a = x;
+			if (quant == 1) { // W[C][K] @ x[K][n]: rows (r, j), element k at k*n
+				s.ni = nn;
+				s.xr = x.rs, s.xj = 1, s.xk = nn;
+				s.orr = s.o.rs, s.oc = nn, s.ojj = 1;
+			} else { // x[m][K] @ W[K][C]: rows (r, i), element k at i*K + k
+				s.ni = mm;
+				s.xr = x.rs, s.xj = kk, s.xk = 1;
+				s.orr = s.o.rs, s.oc = 1, s.ojj = nn;
+			}
+			size_t need = tgk_qgemm_scratch(L.p->max_rows * s.ni, qw.Kp);
+			if (need > L.p->scratch_bytes) L.p->scratch_bytes = need;
+			L.p->stats.weight_bytes += (double)qw.Cp * (qw.bits == 8 ? qw.Kp : qw.Kp / 2) + 4.0 * qw.Cp;
+			L.p->stats.macs += (double)C * K * s.ni;
+			break;
+		}
+		s.kind = ST_MM;
+		s.g = gg, s.m = mm, s.k = kk, s.nn = nn, s.quant = quant;
+		s.a = quant == 1 ? Opnd{ SP_NONE, 0, 0 } : value_opnd(L, in.a[0]);
+		s.b = quant == 2 ? Opnd{ SP_NONE, 0, 0 } : value_opnd(L, in.a[1]);
+		if (quant == 1) s.b = value_opnd(L, in.a[1]);
+		if (quant == 2) s.a = value_opnd(L, in.a[0]);
+		s.ag = (long)mm * kk, s.ai = kk, s.ap = 1;
+		s.bg = (long)kk * nn, s.bp = nn, s.bj = 1;
+		s.og = (long)mm * nn, s.oi = nn, s.oj = 1;
+		if (quant) {
+			int v = quant == 1 ? in.a[0] : in.a[1];
+			s.bits = m->val[v].qbits;
+			s.codes = pool_codes(L.P, m, v);
+			s.scale = L.P.scale_of[v];
+			L.p->stats.macs += (double)mm * kk * nn;
+		}
+		break;
+	}
+	case TGM_SOFTMAX: case TGM_RMSNORM: {
+		const tgm_shape &sa = m->val[in.a[0]].sh;
+		s.kind = ST_ROW;
+		s.op = in.op;
+		s.a = value_opnd(L, in.a[0]);
+		s.o = value_opnd(L, in.out);
+		s.p1 = sa.rank ? sa.dim[sa.rank - 1] : 1;
+		s.p0 = (int)(numel(sa) / s.p1);
+		break;
+	}
+	case TGM_SUM: case TGM_MEAN:
+		s.kind = ST_RED;
+		s.op = in.op;
+		s.a = value_opnd(L, in.a[0]);
+		s.o = value_opnd(L, in.out);
+		s.n = (int)m->val[in.a[0]].n;
+		break;
+	case TGM_TRANSPOSE: {
+		const tgm_shape &sa = m->val[in.a[0]].sh;
+		s.kind = ST_TRANS;
+		s.a = value_opnd(L, in.a[0]);
+		s.o = value_opnd(L, in.out);
+		s.p0 = sa.rank == 3 ? sa.dim[0] : 1;
+		s.p1 = sa.dim[sa.rank - 2];
+		s.p2 = sa.dim[sa.rank - 1];
+		break;
+	}
+	case TGM_OUTER:
+		s.kind = ST_OUTER;
+		s.a = value_opnd(L, in.a[0]);
+		s.b = value_opnd(L, in.a[1]);
+		s.o = value_opnd(L, in.out);
+		s.p0 = (int)m->val[in.a[0]].n;
+		s.p1 = (int)m->val[in.a[1]].n;
+		break;
+	case TGM_TAKE: {
+		const tgm_shape &sw = m->val[in.a[0]].sh;
+		s.kind = ST_TAKE;
+		s.a = value_opnd(L, in.a[0]);
+		s.b = value_opnd(L, in.a[1]);
+		s.o = value_opnd(L, in.out);
+		s.p0 = m->val[in.a[1]].sh.dim[0];
+		s.p1 = sw.dim[0];
+		s.p2 = (int)(numel(sw) / sw.dim[0]);
+		break;
+	}
+	case TGM_SCAN: {
+		for (int k = 0; k < in.nc; k++) {
+			Step c;
+			c.kind = ST_COPY;
+			c.o = value_opnd(L, in.c[k]);
+			c.a = value_opnd(L, in.cinit[k]);
+			c.n = (int)m->val[in.c[k]].n;
+			S.push_back(c);
+		}
+		Step sc;
+		sc.kind = ST_SCAN;
+		sc.T = in.T;
+		sc.reverse = in.reverse;
+		sc.stid = in.stid;
+		size_t at = S.size();
+		S.push_back(sc);
+		for (int j = 0; j < in.nx; j++) {
+			Step c;
+			c.kind = ST_COPY;
+			c.o = value_opnd(L, in.xt[j]);
+			c.a = value_opnd(L, in.x[j]);
+			c.n = (int)m->val[in.xt[j]].n;
+			c.dyn_a = 1;
+			S.push_back(c);
+		}
+		if (!layer_block(L, in.body)) return false;
+		for (int y = 0; y < in.ny; y++) {
+			Step c;
+			c.kind = ST_COPY;
+			c.o = value_opnd(L, in.ys[y]);
+			c.a = value_opnd(L, in.y[y]);
+			c.n = (int)m->val[in.y[y]].n;
+			c.dyn_o = 1;
+			S.push_back(c);
+		}
+		for (int k = 0; k < in.nc; k++) {
+			Step c;
+			c.kind = ST_COPY;
+			c.o = value_opnd(L, in.c[k]);
+			c.a = value_opnd(L, in.cnext[k]);
+			c.n = (int)m->val[in.c[k]].n;
+			S.push_back(c);
+		}
+		S[at].body_lo = (int)at + 1;
+		S[at].body_hi = (int)S.size();
+		return true;
+	}
+	default:
+		seterr("op '%s' is not supported by the layer executor", tgm_op_name(in.op));
+		return false;
+	}
+	S.push_back(s);
+	return true;
+}
+
+void mark_loop_values(const tgm_block *b, std::vector<char> &lw)
+{
+	for (int i = 0; i < b->len; i++) {
+		const tgm_ins &in = b->v[i];
+		if (in.op == TGM_SCAN) {
+			for (int k = 0; k < in.nc; k++) lw[in.c[k]] = 1;
+			for (int j = 0; j < in.nx; j++) lw[in.xt[j]] = 1;
+			for (int y = 0; y < in.ny; y++) lw[in.ys[y]] = 1;
+		}
+		if (in.op == TGM_THINK) lw[in.out] = 1;
+		if (in.body) mark_loop_values(in.body, lw);
+	}
+}
+
+bool layer_block(LB &L, const tgm_block *b)
+{
+	for (int i = 0; i < b->len; i++)
+		if (!layer_ins(L, b->v[i])) return false;
+	return true;
+}
+
+// -------------------------------------------------------- row program ----
+
+struct RB {
+	tg_hip_prog *p;
+	tgm_module *m;
+	Pools P;
+	std::vector<int> ref; // value -> rp reference (INT_MIN: not yet placed)
+	long slots = 0;
+	bool fixed;
+};
+
+int rp_ref(RB &B, int v)
+{
+	if (B.ref[v] != INT_MIN) return B.ref[v];
+	const tgm_value &x = B.m->val[v];
+	if (x.kind == TGM_PARAM || x.kind == TGM_STATE) {
+		B.ref[v] = (int)(-pool_param(B.P, B.m, v, B.fixed) - 1);
+	} else if (x.kind == TGM_INPUT) {
+		B.ref[v] = B.p->rp_in_slot + (int)x.in_off;
+	} else {
+		B.ref[v] = (int)B.slots;
+		B.slots += x.n;
+	}
+	return B.ref[v];
+}
+
+rp_ins rpi(int kind)
+{
+	rp_ins r;
+	memset(&r, 0, sizeof r);
+	r.kind = kind;
+	return r;
+}
+
+int fbits(float f)
+{
+	int i;
+	memcpy(&i, &f, 4);
+	return i;
+}
+
+bool rp_block(RB &B, const tgm_block *b);
+
+bool rp_ins_of(RB &B, const tgm_ins &in)
+{
+	tgm_module *m = B.m;
+	auto &Pr = B.p->rprog;
+	rp_ins r = rpi(RP_NOP);
+	switch (in.op) {
+	case TGM_CONST: {
+		long off = (long)B.P.f.size();
+		B.P.f.push_back(B.fixed ? fixed_word(in.k) : in.k);
+		while (B.P.f.size() % 16) B.P.f.push_back(0.0f);
+		B.ref[in.out] = (int)(-off - 1);
+		return true;
+	}
+	case TGM_RESHAPE:
+		r.kind = RP_COPY;
+		r.out = rp_ref(B, in.out);
+		r.a = rp_ref(B, in.a[0]);
+		r.n = (int)m->val[in.out].n;
+		break;
+	case TGM_ADD: case TGM_SUB: case TGM_MUL: case TGM_DIV: case TGM_MAX: case TGM_MIN: {
+		r.kind = RP_BIN;
+		r.op = in.op - TGM_ADD;
+		r.a = rp_ref(B, in.a[0]);
+		r.b = rp_ref(B, in.a[1]);
+		r.out = rp_ref(B, in.out);
+		r.n = (int)m->val[in.out].n;
+		long ao, bo;
+		bcast(m->val[in.out].sh, m->val[in.a[0]].sh, B.P.imap, r.p[0], ao);
+		bcast(m->val[in.out].sh, m->val[in.a[1]].sh, B.P.imap, r.p[2], bo);
+		r.p[1] = (int)ao;
+		r.p[3] = (int)bo;
+		break;
+	}
+	case TGM_NEG: case TGM_TANH: case TGM_RELU: case TGM_SIGMOID: case TGM_EXP: case TGM_SQRT: case TGM_GELU:
+	case TGM_SILU: case TGM_SOFTPLUS: case TGM_LOG: case TGM_SIN: case TGM_COS: case TGM_FLOOR: case TGM_STEP:
+		r.kind = RP_UN;
+		r.op = in.op;
+		r.a = rp_ref(B, in.a[0]);
+		r.out = rp_ref(B, in.out);
+		r.n = (int)m->val[in.out].n;
+		break;
+	case TGM_MATMUL: {
+		const tgm_value &va = m->val[in.a[0]], &vb = m->val[in.a[1]];
+		int mm, kk, nn, gg;
+		matmul_dims(va.sh, vb.sh, mm, kk, nn, gg);
+		int quant = 0;
+		if (gg == 1 && va.qbits && q_axis_for(m, in.a[0], in) == va.qaxis) quant = 1;
+		else if (gg == 1 && vb.qbits && q_axis_for(m, in.a[1], in) == vb.qaxis) quant = 2;
+		r.kind = RP_MM;
+		r.out = rp_ref(B, in.out);
+		r.a = quant == 1 ? 0 : rp_ref(B, in.a[0]);
+		r.b = quant == 2 ? 0 : rp_ref(B, in.a[1]);
+		r.p[0] = gg, r.p[1] = mm, r.p[2] = kk, r.p[3] = nn, r.p[4] = quant;
+		if (quant) {
+			int v = quant == 1 ? in.a[0] : in.a[1];
+			r.p[5] = m->val[v].qbits;
+			r.p[6] = (int)pool_codes(B.P, m, v);
+			r.p[7] = (int)B.P.scale_of[v];
+		}
+		break;
+	}
+	case TGM_SOFTMAX: case TGM_RMSNORM: {
+		const tgm_shape &sa = m->val[in.a[0]].sh;
+		r.kind = RP_ROW;
+		r.op = in.op;
+		r.a = rp_ref(B, in.a[0]);
+		r.out = rp_ref(B, in.out);
+		r.p[1] = sa.rank ? sa.dim[sa.rank - 1] : 1;
+		r.p[0] = (int)(numel(sa) / r.p[1]);
+		break;
+	}
+	case TGM_SUM: case TGM_MEAN:
+		r.kind = RP_RED;
+		r.op = in.op;
+		r.a = rp_ref(B, in.a[0]);
+		r.out = rp_ref(B, in.out);
+		r.n = (int)m->val[in.a[0]].n;
+		break;
+	case TGM_TRANSPOSE: {
+		const tgm_shape &sa = m->val[in.a[0]].sh;
+		r.kind = RP_TRANS;
+		r.a = rp_ref(B, in.a[0]);
+		r.out = rp_ref(B, in.out);
+		r.p[0] = sa.rank == 3 ? sa.dim[0] : 1;
+		r.p[1] = sa.dim[sa.rank - 2];
+		r.p[2] = sa.dim[sa.rank - 1];
+		break;
+	}
+	case TGM_OUTER:
+		r.kind = RP_OUTER;
+		r.a = rp_ref(B, in.a[0]);
+		r.b = rp_ref(B, in.a[1]);
+		r.out = rp_ref(B, in.out);
+		r.p[0] = (int)m->val[in.a[0]].n;
+		r.p[1] = (int)m->val[in.a[1]].n;
+		break;
+	case TGM_TAKE: {
+		const tgm_shape &sw = m->val[in.a[0]].sh;
+		r.kind = RP_TAKE;
+		r.a = rp_ref(B, in.a[0]);
+		r.b = rp_ref(B, in.a[1]);
+		r.out = rp_ref(B, in.out);
+		r.p[0] = m->val[in.a[1]].sh.dim[0];
+		r.p[1] = sw.dim[0];
+		r.p[2] = (int)(numel(sw) / sw.dim[0]);
+		break;
+	}
+	case TGM_THINK: {
+		rp_ins t = rpi(RP_THINK);
+		t.out = rp_ref(B, in.out);
+		t.a = rp_ref(B, in.init);
+		t.n = (int)m->val[in.out].n;
+		t.p[1] = in.maxit;
+		t.p[2] = in.eps >= 0 ? fbits(in.eps) : fbits(-1.0f);
+		t.p[4] = fbits(in.hthr);
+		t.p[5] = in.tid;
+		if (in.eps >= 0) { // a positive threshold stays positive in Q16.16 (src/cgen.c:286-290)
+			int32_t q = to_fixed(in.eps, 16);
+			t.p[7] = (q > 0 || in.eps == 0) ? q : 1;
+		}
+		t.p[8] = to_fixed(in.hthr, 16);
+		int at = (int)Pr.size();
+		Pr.push_back(t);
+		if (!rp_block(B, in.body)) return false;
+		Pr[at].p[0] = rp_ref(B, in.yield);
+		Pr[at].p[3] = in.halt >= 0 ? rp_ref(B, in.halt) : INT_MIN;
+		rp_ins e = rpi(RP_THINK_END);
+		e.p[0] = at;
+		Pr.push_back(e);
+		return true;
+	}
+	case TGM_SCAN: {
+		for (int k = 0; k < in.nc; k++) {
+			rp_ins c = rpi(RP_COPY);
+			c.out = rp_ref(B, in.c[k]);
+			c.a = rp_ref(B, in.cinit[k]);
+			c.n = (int)m->val[in.c[k]].n;
+			Pr.push_back(c);
+		}
+		rp_ins s = rpi(RP_SCAN);
+		s.p[0] = in.T;
+		s.p[1] = in.reverse;
+		s.p[2] = in.stid;
+		int at = (int)Pr.size();
+		Pr.push_back(s);
+		for (int j = 0; j < in.nx; j++) {
+			rp_ins c = rpi(RP_COPY);
+			c.out = rp_ref(B, in.xt[j]);
+			c.a = rp_ref(B, in.x[j]);
+			c.n = (int)m->val[in.xt[j]].n;
+			c.p[2] = 1;
+			Pr.push_back(c);
+		}
+		if (!rp_block(B, in.body)) return false;
+		for (int y = 0; y < in.ny; y++) {
+			rp_ins c = rpi(RP_COPY);
+			c.out = rp_ref(B, in.ys[y]);
+			c.a = rp_ref(B, in.y[y]);
+			c.n = (int)m->val[in.y[y]].n;
+			c.p[3] = 1;
+			Pr.push_back(c);
+		}
+		for (int k = 0; k < in.nc; k++) {
+			rp_ins c = rpi(RP_COPY);
+			c.out = rp_ref(B, in.c[k]);
+			c.a = rp_ref(B, in.cnext[k]);
+			c.n = (int)m->val[in.c[k]].n;
+			Pr.push_back(c);
+		}
+		rp_ins e = rpi(RP_SCAN_END);
+		e.p[0] = at;
+		Pr.push_back(e);
+		return true;
+	}
+	default:
+		seterr("op '%s' is not supported by the row executor", tgm_op_name(in.op));
+		return false;
+	}
+	Pr.push_back(r);
+	return true;
+}
+
+bool rp_block(RB &B, const tgm_block *b)
+{
+	for (int i = 0; i < b->len; i++)
+		if (!rp_ins_of(B, b->v[i])) return false;
+	return true;
+}
+
+template <class T>
+bool upload(T **d, const std::vector<T> &h, hipStream_t st)
+{
+	size_t nb = (h.size() ? h.size() : 1) * sizeof(T);
+	if (!hipok(hipMalloc((void **)d, nb), "hipMalloc")) return false;
+	if (h.size() && !hipok(hipMemcpyAsync(*d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice, st), "upload")) return false;
+	return true;
+}
+
+bool upload_pools(tg_hip_prog *p, Pools &P)
+{
+	return upload(&p->d_pool, P.f, p->st) && upload(&p->d_imap, P.imap, p->st) && upload(&p->d_codes, P.codes, p->st) &&
+	       upload(&p->d_fscale, P.fscale, p->st) && upload(&p->d_qscale, P.qscale, p->st) &&
+	       hipok(hipStreamSynchronize(p->st), "upload");
+}
+
+// ------------------------------------------------------------ execution ----
+
+struct Run {
+	tg_hip_prog *p;
+	const float *in;
+	float *out;
+	int rows;
+	int t; // current scan step
+};
+
+tgk_opd resolve(const Run &R, const Opnd &o)
+{
+	switch (o.space) {
+	case SP_ARENA: return tgk_opd{ R.p->d_arena + o.off * (long)R.p->max_rows, o.rs };
+	case SP_IN: return tgk_opd{ R.in + o.off, o.rs };
+	case SP_POOL: return tgk_opd{ R.p->d_pool + o.off, 0 };
+	case SP_OUT: return tgk_opd{ R.out, o.rs }; // the model's output is computed in place
+	}
+	return tgk_opd{ nullptr, 0 };
+}
+
+float *dst(const Run &R, const Opnd &o) { return const_cast<float *>(resolve(R, o).p); }
+
+// With TG_HIP_TIMING every launch is bracketed by HIP events on the program's
+// stream; `which` says where its time is accounted (0 other, 1 MFMA, 2 digits).
+struct Timer {
+	tg_hip_prog *p;
+	hipEvent_t a = nullptr;
+	int which;
+	Timer(tg_hip_prog *p_, int w) : p(p_), which(w)
+	{
+		if (p->flags & TG_HIP_TIMING) {
+			hipEventCreate(&a);
+			hipEventRecord(a, p->st);
+		}
+	}
+	~Timer()
+	{
+		if (!a) return;
+		hipEvent_t b;
+		hipEventCreate(&b);
+		hipEventRecord(b, p->st);
+		p->tev.push_back(a);
+		p->tev.push_back(b);
+		p->tev.push_back((hipEvent_t)(intptr_t)which);
+	}
+};
+
+void exec_step(Run &R, const Step &s)
+{
+	tg_hip_prog *p = R.p;
+	hipStream_t st = p->st;
+	switch (s.kind) {
+	case ST_BIN:
+		tgk_binary(st, s.op, dst(R, s.o), s.o.rs, s.n, resolve(R, s.a), s.amode, p->d_imap + s.amap, resolve(R, s.b), s.bmode,
+			   p->d_imap + s.bmap, R.rows);
+		break;
+	case ST_UN: tgk_unary(st, s.op, dst(R, s.o), s.o.rs, resolve(R, s.a), s.n, R.rows); break;
+	case ST_MM: {
+		tgk_mm d;
+		d.g = s.g, d.m = s.m, d.k = s.k, d.n = s.nn;
+		d.a = s.quant == 1 ? tgk_opd{ nullptr, 0 } : resolve(R, s.a);
+		d.ag = s.ag, d.ai = s.ai, d.ap = s.ap;
+		d.b = s.quant == 2 ? tgk_opd{ nullptr, 0 } : resolve(R, s.b);
+		d.bg = s.bg, d.bp = s.bp, d.bj = s.bj;
+		d.o = dst(R, s.o);
+		d.ors = s.o.rs, d.og = s.og, d.oi = s.oi, d.oj = s.oj;
+		d.quant = s.quant, d.bits = s.bits;
+		d.codes = p->d_codes + s.codes;
+		d.scale = p->d_fscale + s.scale;
+		tgk_matmul_exact(st, &d, R.rows);
+		break;
+	}
+	case ST_QGEMM: {
+		tgk_qgemm_args a;
+		a.w = &p->qws[s.qw];
+		tgk_opd x = resolve(R, s.a);
+		a.x = x.p;
+		a.xr = s.xr, a.xj = s.xj, a.xk = s.xk, a.ni = s.ni;
+		a.o = dst(R, s.o);
+		a.orr = s.orr, a.oc = s.oc, a.oj = s.ojj;
+		a.M = R.rows * s.ni;
+		{
+			Timer t(p, 2);
+			tgk_qgemm_digits(st, &a, p->d_scratch);
+		}
+		{
+			Timer t(p, 1);
+			tgk_qgemm_mfma(st, &a, p->d_scratch);
+		}
+		break;
+	}
+	case ST_ROW: tgk_rowop(st, s.op, dst(R, s.o), s.o.rs, resolve(R, s.a), s.p0, s.p1, R.rows); break;
+	case ST_RED: tgk_reduce(st, s.op, dst(R, s.o), s.o.rs, resolve(R, s.a), s.n, R.rows); break;
+	case ST_TRANS: tgk_transpose(st, dst(R, s.o), s.o.rs, resolve(R, s.a), s.p0, s.p1, s.p2, R.rows); break;
+	case ST_OUTER: tgk_outer(st, dst(R, s.o), s.o.rs, resolve(R, s.a), s.p0, resolve(R, s.b), s.p1, R.rows); break;
+	case ST_TAKE: tgk_take(st, dst(R, s.o), s.o.rs, resolve(R, s.a), resolve(R, s.b), s.p0, s.p1, s.p2, R.rows); break;
+	case ST_COPY:
+		tgk_copy(st, dst(R, s.o), s.o.rs, s.dyn_o ? (long)R.t * s.n : 0, resolve(R, s.a), s.dyn_a ? (long)R.t * s.n : 0, s.n,
+			 R.rows);
+		break;
+	}
+}
+
+void run_range(Run &R, int lo, int hi)
+{
+	tg_hip_prog *p = R.p;
+	for (int i = lo; i < hi; i++) {
+		const Step &s = p->steps[i];
+		if (s.kind == ST_SCAN) {
+			int saved = R.t;
+			for (int step = 0; step < s.T; step++) {
+				R.t = s.reverse ? s.T - 1 - step : step;
+				run_range(R, s.body_lo, s.body_hi);
+			}
+			R.t = saved;
+			i = s.body_hi - 1;
+			continue;
+		}
+		if (s.kind == ST_QGEMM) {
+			exec_step(R, s); /* times its two launches itself */
+		} else {
+			Timer t(p, 0);
+			exec_step(R, s);
+		}
+	}
+}
+
+void collect_timing(tg_hip_prog *p)
+{
+	for (size_t i = 0; i + 3 <= p->tev.size(); i += 3) {
+		float ms = 0;
+		hipEventElapsedTime(&ms, p->tev[i], p->tev[i + 1]);
+		int which = (int)(intptr_t)p->tev[i + 2];
+		if (which == 1) {
+			p->stats.qgemm_ms += ms;
+			p->stats.qgemm_calls++;
+		} else if (which == 2) {
+			p->stats.digits_ms += ms;
+		} else {
+			p->stats.other_ms += ms;
+		}
+		hipEventDestroy(p->tev[i]);
+		hipEventDestroy(p->tev[i + 1]);
+	}
+	p->tev.clear();
+}
+
+// the steps of scans with a `steps` slot (fixed budget), row program excluded
+void scan_tids(const tgm_block *b, std::vector<std::pair<int, int>> &out)
+{
+	for (int i = 0; i < b->len; i++) {
+		if (b->v[i].op == TGM_SCAN && b->v[i].stid >= 0) out.push_back({ b->v[i].stid, b->v[i].T });
+		if (b->v[i].body) scan_tids(b->v[i].body, out);
+	}
+}
+
+int run_pass(tg_hip_prog *p, const float *d_in, int rows, float *d_out, int *d_steps)
+{
+	if (p->executor == 1) {
+		rp_args a;
+		memset(&a, 0, sizeof a);
+		a.prog = p->d_rprog;
+		a.nins = (int)p->rprog.size();
+		a.pool = p->d_pool;
+		a.imap = p->d_imap;
+		a.codes = p->d_codes;
+		a.fscale = p->d_fscale;
+		a.qscale = p->d_qscale;
+		a.arena = p->d_arena;
+		a.arena_n = p->rp_arena;
+		a.R = p->max_rows;
+		a.in = d_in;
+		a.per = (int)p->m->per;
+		a.in_slot = p->rp_in_slot;
+		a.out = d_out;
+		a.nout = (int)p->m->nout;
+		a.out_ref = p->rp_out_ref;
+		a.steps = d_steps;
+		a.nthink = p->m->nthink ? p->m->nthink : 1;
+		a.rows = rows;
+		a.fixed = p->fixed;
+		tgk_rowprog(p->st, &a);
+		return hipok(hipGetLastError(), "row program launch") ? 0 : -1;
+	}
+	Run R{ p, d_in, d_out, rows, 0 };
+	run_range(R, 0, (int)p->steps.size());
+	if (p->out.space != SP_OUT) {
+		tgk_opd o = resolve(R, p->out);
+		tgk_copy(p->st, d_out, p->m->nout, 0, o, 0, (int)p->m->nout, rows);
+	}
+	if (d_steps && p->m->nthink) {
+		std::vector<std::pair<int, int>> t;
+		scan_tids(&p->m->top, t);
+		std::vector<int> h((size_t)rows * p->m->nthink, 0);
+		for (int r = 0; r < rows; r++)
+			for (auto &x : t) h[(size_t)r * p->m->nthink + x.first] = x.second;
+		if (!hipok(hipMemcpyAsync(d_steps, h.data(), h.size() * sizeof(int), hipMemcpyHostToDevice, p->st), "steps")) return -1;
+		if (!hipok(hipStreamSynchronize(p->st), "steps")) return -1;
+	}
+	return hipok(hipGetLastError(), "layer program launch") ? 0 : -1;
+}
+
+bool build_layer(tg_hip_prog *p)
+{
+	LB L;
+	L.p = p;
+	L.m = p->m;
+	L.where.assign(p->m->nval, Opnd{});
+	L.loopw.assign(p->m->nval, 0);
+	L.P.pool_of.assign(p->m->nval, -1);
+	L.P.codes_of.assign(p->m->nval, -1);
+	L.P.scale_of.assign(p->m->nval, -1);
+	mark_loop_values(&p->m->top, L.loopw);
+	if (p->m->val[p->m->output].kind == TGM_TMP) { /* written straight into the caller's output rows */
+		L.where[p->m->output].space = SP_OUT;
+		L.where[p->m->output].off = 0;
+		L.where[p->m->output].rs = p->m->nout;
+	}
+	if (!layer_block(L, &p->m->top)) return false;
+	p->out = value_opnd(L, p->m->output);
+	if (!upload_pools(p, L.P)) return false;
+	size_t ab = (size_t)(p->arena_floats ? p->arena_floats : 1) * p->max_rows * sizeof(float);
+	p->stats.arena_bytes = (long)ab;
+	if (!hipok(hipMalloc(&p->d_arena, ab), "arena")) return false;
+	if (p->scratch_bytes && !hipok(hipMalloc(&p->d_scratch, p->scratch_bytes), "scratch")) return false;
+	return true;
+}
+
+bool build_rowprog(tg_hip_prog *p)
+{
+	RB B;
+	B.p = p;
+	B.m = p->m;
+	B.fixed = p->fixed != 0;
+	B.ref.assign(p->m->nval, INT_MIN);
+	B.P.pool_of.assign(p->m->nval, -1);
+	B.P.codes_of.assign(p->m->nval, -1);
+	B.P.scale_of.assign(p->m->nval, -1);
+	p->rp_in_slot = 0;
+	B.slots = p->m->per;
+	if (!rp_block(B, &p->m->top)) return false;
+	p->rp_out_ref = rp_ref(B, p->m->output);
+	p->rp_arena = B.slots ? B.slots : 1;
+	if (!upload_pools(p, B.P) || !upload(&p->d_rprog, p->rprog, p->st)) return false;
+	size_t ab = (size_t)p->rp_arena * p->max_rows * sizeof(float);
+	p->stats.arena_bytes = (long)ab;
+	return hipok(hipMalloc(&p->d_arena, ab), "arena") && hipok(hipStreamSynchronize(p->st), "upload");
+}
+
+void destroy(tg_hip_prog *p)
+{
+	if (!p) return;
+	for (auto &q : p->qws) tgk_qweight_free(&q);
+	void *bufs[] = { p->d_pool, p->d_imap, p->d_codes, p->d_fscale, p->d_qscale, p->d_arena, p->d_scratch, p->d_rprog,
+			 p->d_in, p->d_out, p->d_steps };
+	for (void *b : bufs)
+		if (b) hipFree(b);
+	if (p->ev0) hipEventDestroy(p->ev0);
+	if (p->ev1) hipEventDestroy(p->ev1);
+	if (p->st) hipStreamDestroy(p->st);
+	tgm_free(p->m);
+	delete p;
+}
+
+int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *steps)
+{
+	if (!p) {
+		seterr("no program");
+		return -1;
+	}
+	const long per = p->m->per, nout = p->m->nout, nt = p->m->nthink ? p->m->nthink : 1;
+	if (!p->d_in) {
+		if (!hipok(hipMalloc(&p->d_in, (size_t)p->max_rows * per * 4), "input buffer") ||
+		    !hipok(hipMalloc(&p->d_out, (size_t)p->max_rows * nout * 4), "output buffer") ||
+		    !hipok(hipMalloc(&p->d_steps, (size_t)p->max_rows * nt * 4), "steps buffer"))
+			return -1;
+	}
+	float ms_total = 0;
+	for (long r0 = 0; r0 < nrows; r0 += p->max_rows) {
+		int cnt = (int)(nrows - r0 < p->max_rows ? nrows - r0 : p->max_rows);
+		if (!hipok(hipMemcpyAsync(p->d_in, (const char *)rows + (size_t)r0 * per * 4, (size_t)cnt * per * 4, hipMemcpyHostToDevice,
+					  p->st),
+			   "rows to device"))
+			return -1;
+		hipEventRecord(p->ev0, p->st);
+		if (run_pass(p, p->d_in, cnt, p->d_out, p->d_steps)) return -1;
+		hipEventRecord(p->ev1, p->st);
+		if (!hipok(hipMemcpyAsync((char *)out + (size_t)r0 * nout * 4, p->d_out, (size_t)cnt * nout * 4, hipMemcpyDeviceToHost, p->st),
+			   "outputs to host"))
+			return -1;
+		if (steps && p->m->nthink &&
+		    !hipok(hipMemcpyAsync(steps + (size_t)r0 * nt, p->d_steps, (size_t)cnt * nt * 4, hipMemcpyDeviceToHost, p->st),
+			   "steps to host"))
+			return -1;
+		if (!hipok(hipStreamSynchronize(p->st), "batch")) return -1;
+		float ms = 0;
+		hipEventElapsedTime(&ms, p->ev0, p->ev1);
+		ms_total += ms;
+		collect_timing(p);
+	}
+	if (steps && !p->m->nthink) memset(steps, 0, (size_t)nrows * sizeof *steps); /* no think loop: one zero slot per row */
+	p->stats.rows = (int)nrows;
+	p->stats.batch_ms = ms_total;
+	return 0;
+}
+
+} // namespace
+
+extern "C" {
+
+int tg_hip_init(int device)
+{
+	return hipok(hipSetDevice(device), "hipSetDevice") ? 0 : -1;
+}
+
+tg_hip_prog *tg_hip_load(const char *tgir, size_t len, int flags, int max_rows)
+{
+	char err[512];
+	tgm_module *m = tgm_read(tgir, len, err, sizeof err);
+	if (!m) {
+		seterr("%s", err);
+		return nullptr;
+	}
+	if (m->nupd) {
+		seterr("model %s updates its state: rows depend on each other and stay on the CPU", m->name);
+		tgm_free(m);
+		return nullptr;
+	}
+	tg_hip_prog *p = new tg_hip_prog;
+	p->m = m;
+	p->flags = flags;
+	p->fixed = (flags & TG_HIP_FIXED) != 0;
+	p->max_rows = max_rows > 0 ? max_rows : 4096;
+	p->executor = (p->fixed || (flags & TG_HIP_ROWPROG) || has_think(&m->top)) ? 1 : 0;
+	p->stats.executor = p->executor;
+	bool ok = hipok(hipStreamCreate(&p->st), "hipStreamCreate") && hipok(hipEventCreate(&p->ev0), "event") &&
+		  hipok(hipEventCreate(&p->ev1), "event");
+	if (ok) ok = p->executor ? build_rowprog(p) : build_layer(p);
+	if (!ok) {
+		destroy(p);
+		return nullptr;
+	}
+	return p;
+}
+
+int tg_hip_info(const tg_hip_prog *p, int *per, int *nout, int *nthink)
+{
+	if (!p) return -1;
+	if (per) *per = (int)p->m->per;
+	if (nout) *nout = (int)p->m->nout;
+	if (nthink) *nthink = p->m->nthink;
+	return 0;
+}
+
+int tg_hip_batch(tg_hip_prog *p, const float *rows, long nrows, float *out, int *steps)
+{
+	if (p && p->fixed) {
+		seterr("this program runs in Q16.16: use tg_hip_batch_fixed");
+		return -1;
+	}
+	return batch_host(p, rows, nrows, out, steps);
+}
+
+int tg_hip_batch_fixed(tg_hip_prog *p, const int32_t *rows, long nrows, int32_t *out, int *steps)
+{
+	if (p && !p->fixed) {
+		seterr("this program runs in f32: load it with TG_HIP_FIXED");
+		return -1;
+	}
+	return batch_host(p, rows, nrows, out, steps);
+}
+
+int tg_hip_batch_device(tg_hip_prog *p, const void *d_rows, long nrows, void *d_out, int *d_steps)
+{
+	if (!p) return -1;
+	if (nrows > p->max_rows) {
+		seterr("%ld rows exceed the program's %d-row capacity", nrows, p->max_rows);
+		return -1;
+	}
+	if (!d_steps && p->m->nthink) {
+		if (!p->d_steps && !hipok(hipMalloc(&p->d_steps, (size_t)p->max_rows * p->m->nthink * 4), "steps buffer")) return -1;
+		d_steps = p->d_steps;
+	}
+	hipEventRecord(p->ev0, p->st);
+	int rc = run_pass(p, (const float *)d_rows, (int)nrows, (float *)d_out, d_steps);
+	hipEventRecord(p->ev1, p->st);
+	p->stats.rows = (int)nrows;
+	return rc;
+}
+
+int tg_hip_sync(tg_hip_prog *p)
+{
+	if (!p) return -1;
+	if (!hipok(hipStreamSynchronize(p->st), "sync")) return -1;
+	float ms = 0;
+	if (hipEventElapsedTime(&ms, p->ev0, p->ev1) == hipSuccess) p->stats.batch_ms = ms;
+	collect_timing(p);
+	return 0;
+}
+
+int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, const float *b, int m, int k, int n, int axis, int flags)
+{
+	if ((bits != 8 && bits != 4) || (axis != 0 && axis != 1) || m < 1 || k < 1 || n < 1) {
+		seterr("tg_hip_matmul_q: bad arguments");
+		return -1;
+	}
+	hipStream_t st;
+	if (!hipok(hipStreamCreate(&st), "stream")) return -1;
+	int rc = -1;
+	long nq = (long)(axis == 0 ? m : k) * (axis == 0 ? k : n), qb = bits == 8 ? nq : (nq + 1) / 2;
+	long bn = axis == 0 ? (long)k * n : (long)m * k, on = (long)m * n, nch = axis == 0 ? m : n;
+	float *db = nullptr, *dout = nullptr, *ds = nullptr;
+	uint8_t *dq = nullptr;
+	void *scr = nullptr;
+	tgk_qweight w{};
+	do {
+		if (!hipok(hipMalloc(&db, bn * 4), "alloc") || !hipok(hipMalloc(&dout, on * 4), "alloc")) break;
+		if (!hipok(hipMemcpyAsync(db, b, bn * 4, hipMemcpyHostToDevice, st), "copy")) break;
+		if (flags & TG_HIP_EXACT) {
+			if (!hipok(hipMalloc(&dq, qb), "alloc") || !hipok(hipMalloc(&ds, nch * 4), "alloc")) break;
+			hipMemcpyAsync(dq, q, qb, hipMemcpyHostToDevice, st);
+			hipMemcpyAsync(ds, s, nch * 4, hipMemcpyHostToDevice, st);
+			tgk_mm d{};
+			d.g = 1, d.m = m, d.k = k, d.n = n;
+			d.quant = axis == 0 ? 1 : 2;
+			d.bits = bits;
+			d.codes = dq;
+			d.scale = ds;
+			d.a = tgk_opd{ axis == 1 ? db : nullptr, 0 };
+			d.ai = k, d.ap = 1;
+			d.b = tgk_opd{ axis == 0 ? db : nullptr, 0 };
+			d.bp = n, d.bj = 1;
+			d.o = dout;
+			d.oi = n, d.oj = 1;
+			tgk_matmul_exact(st, &d, 1);
+		} else {
+			int C = axis == 0 ? m : n, K = k;
+			if (tgk_qweight_pack(&w, (const uint8_t *)q, s, bits, axis, C, K, st)) {
+				seterr("tg_hip_matmul_q: weight upload failed");
+				break;
+			}
+			tgk_qgemm_args a{};
+			a.w = &w;
+			a.x = db;
+			a.o = dout;
+			if (axis == 0) { // rows j of b^T: element k at k * n
+				a.ni = n, a.xr = 0, a.xj = 1, a.xk = n, a.M = n;
+				a.orr = 0, a.oc = n, a.oj = 1;
+			} else {
+				a.ni = m, a.xr = 0, a.xj = k, a.xk = 1, a.M = m;
+				a.orr = 0, a.oc = 1, a.oj = n;
+			}
+			if (!hipok(hipMalloc(&scr, tgk_qgemm_scratch(a.M, w.Kp)), "alloc")) break;
+			tgk_qgemm(st, &a, scr);
+		}
+		if (!hipok(hipGetLastError(), "launch")) break;
+		if (!hipok(hipMemcpyAsync(o, dout, on * 4, hipMemcpyDeviceToHost, st), "copy")) break;
+		if (!hipok(hipStreamSynchronize(st), "sync")) break;
+		rc = 0;
+	} while (0);
+	tgk_qweight_free(&w);
+	void *bufs[] = { db, dout, ds, dq, scr };
+	for (void *x : bufs)
+		if (x) hipFree(x);
+	hipStreamDestroy(st);
+	return rc;
+}
+
+void tg_hip_free(tg_hip_prog *p) { destroy(p); }
+
+const char *tg_hip_error(void) { return g_err; }
+
+int tg_hip_stats(const tg_hip_prog *p, tg_hip_stats_t *st)
+{
+	if (!p || !st) return -1;
+	*st = p->stats;
+	return 0;
+}
+
+int tg_hip_reset_stats(tg_hip_prog *p)
+{
+	if (!p) return -1;
+	p->stats.qgemm_ms = p->stats.other_ms = p->stats.digits_ms = 0;
+	p->stats.qgemm_calls = 0;
+	return 0;
+}
+
+void *tg_hip_dev_alloc(size_t bytes)
+{
+	void *d = nullptr;
+	if (!hipok(hipMalloc(&d, bytes ? bytes : 1), "hipMalloc")) return nullptr;
+	return d;
+}
+
+int tg_hip_dev_free(void *d) { return hipok(hipFree(d), "hipFree") ? 0 : -1; }
+int tg_hip_h2d(void *d, const void *h, size_t bytes) { return hipok(hipMemcpy(d, h, bytes, hipMemcpyHostToDevice), "h2d") ? 0 : -1; }
+int tg_hip_d2h(void *h, const void *d, size_t bytes) { return hipok(hipMemcpy(h, d, bytes, hipMemcpyDeviceToHost), "d2h") ? 0 : -1; }
+
+} // extern "C"

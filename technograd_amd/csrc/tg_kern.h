@@ -1,0 +1,128 @@
+/* Kernel launch interface shared by the program builder (tg_hip.hip) and the
+ * kernel files (kern_*.hip). All launches take the program's stream. */
+#ifndef TG_KERN_H
+#define TG_KERN_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+/* A per-row operand: element i of row r is p[r * rs + i]; rs == 0 for values
+ * shared by every row (params, constants). */
+typedef struct {
+	const float *p;
+	long rs;
+} tgk_opd;
+
+/* ---- layer executor kernels (kern_layer.hip) ---- */
+
+enum { TGK_ADD, TGK_SUB, TGK_MUL, TGK_DIV, TGK_MAX, TGK_MIN };
+
+/* o[r, i] = a[r, ia(i)] (op) b[r, ib(i)]; ia(i) = i, 0 or amap[i] (amode 0, 1, 2) */
+void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int amode, const int *amap, tgk_opd b, int bmode,
+		const int *bmap, int rows);
+/* unary op codes are the model op codes (TGM_NEG .. TGM_STEP) */
+void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows);
+
+/* General matmul, one thread per output, products summed in order p = 0..k-1
+ * from 0.0f with separate multiply and add (the reference's order): the exact
+ * path. o[r][g][i][j] = sum_p A[r][g][i][p] B[r][g][p][j]; quant 1: A is codes
+ * (element g*m*k + i*k + p of the packed param) times scale[i]; quant 2: B is
+ * codes (element p*n + j) times scale[j]. */
+typedef struct {
+	int g, m, k, n;
+	tgk_opd a;
+	long ag, ai, ap;
+	tgk_opd b;
+	long bg, bp, bj;
+	float *o;
+	long ors, og, oi, oj;
+	int quant, bits;
+	const uint8_t *codes;
+	const float *scale;
+} tgk_mm;
+void tgk_matmul_exact(hipStream_t s, const tgk_mm *d, int rows);
+
+/* softmax (op TGM_SOFTMAX) or rmsnorm over `cols`-long rows, `nrow` of them per batch row */
+void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, int cols, int rows);
+/* sum or mean of the n elements of a row */
+void tgk_reduce(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows);
+void tgk_transpose(hipStream_t s, float *o, long ors, tgk_opd a, int g, int r, int c, int rows);
+void tgk_outer(hipStream_t s, float *o, long ors, tgk_opd a, int m, tgk_opd b, int n, int rows);
+void tgk_take(hipStream_t s, float *o, long ors, tgk_opd w, tgk_opd idx, int cnt, int d, int h, int rows);
+/* o[r*ors + ooff + i] = a[r*a.rs + aoff + i], i < w */
+void tgk_copy(hipStream_t s, float *o, long ors, long ooff, tgk_opd a, long aoff, int w, int rows);
+
+/* ---- quantized GEMM on int8 MFMA (kern_qgemm.hip) ----
+ * Y = X Wq^T with X [M][K] f32 (row m at x + (m / ni) * xr + (m % ni) * xj,
+ * element k at + k * xk), Wq repacked (see tgk_qweight). Exact integer
+ * products of int8/int4 codes with 3 balanced int8 limbs of each
+ * activation row's 24-bit fixed-point form; the dot product is rounded to f32
+ * once, then multiplied by the channel scale. */
+typedef struct {
+	int C, K, Kp, bits;      /* channels, inputs, inputs padded to 64 */
+	int Cp;                  /* channels padded to 64 */
+	uint8_t *w;              /* int8: [Cp][Kp]; int4: [Cp][Kp/2] offset-binary nibbles (see kern_qgemm.hip) */
+	float *scale;            /* [Cp] */
+	uint8_t *orig;           /* original packed codes, for the exact fallback of special rows */
+	int axis;                /* original layout: 0 = [C][K], 1 = [K][C] */
+} tgk_qweight;
+
+int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, int bits, int axis, int C, int K, hipStream_t s);
+void tgk_qweight_free(tgk_qweight *w);
+
+typedef struct {
+	const tgk_qweight *w;
+	const float *x;
+	long xr, xj, xk;        /* activation strides: batch row, inner row, k */
+	int ni;                 /* inner rows per batch row (m = r * ni + j) */
+	float *o;
+	long orr, oc, oj;       /* output strides: batch row, channel, inner row */
+	int M;                  /* rows of X = batch rows * ni */
+} tgk_qgemm_args;
+
+/* scratch: bytes needed for M rows of K inputs */
+size_t tgk_qgemm_scratch(int M, int Kp);
+void tgk_qgemm(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
+/* the two launches of tgk_qgemm: activation digits, then the MFMA kernel */
+void tgk_qgemm_digits(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
+void tgk_qgemm_mfma(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
+
+/* ---- row-program interpreter (kern_rowprog.hip) ---- */
+
+/* One instruction of a row program (one lane runs one batch row through the
+ * whole program). Operand references: ref >= 0 is an arena slot (element
+ * ref + i of the lane's arena), ref < 0 is the pool word -ref - 1 + i
+ * (params and constants, shared by all lanes). */
+enum {
+	RP_CONST, RP_BIN, RP_UN, RP_MM, RP_ROW, RP_RED, RP_TRANS, RP_OUTER, RP_COPY, RP_TAKE,
+	RP_THINK, RP_THINK_END, RP_SCAN, RP_SCAN_STEP, RP_SCAN_END, RP_NOP
+};
+
+typedef struct {
+	int kind, op, out, a, b, n;
+	int p[10];
+} rp_ins;
+
+typedef struct {
+	const rp_ins *prog;
+	int nins;
+	const float *pool;      /* f32 params/constants, or Q16.16 words when fixed */
+	const int *imap;        /* broadcast maps referenced by RP_BIN */
+	const uint8_t *codes;   /* quantized params (packed as in the model) */
+	const float *fscale;    /* f32 scales */
+	const int *qscale;      /* Q7.24 scales */
+	float *arena;           /* [arena][R] */
+	long arena_n, R;
+	const float *in;        /* [rows][per] */
+	int per, in_slot;
+	float *out;             /* [rows][nout] */
+	int nout, out_ref;
+	int *steps;             /* [rows][nthink] */
+	int nthink;
+	int rows;
+	int fixed;
+} rp_args;
+
+void tgk_rowprog(hipStream_t s, const rp_args *a);
+
+#endif

@@ -1,0 +1,160 @@
+"""ctypes binding of the MI355X batch backend's C ABI (include/tg_hip.h).
+
+The library is built in-tree (technograd_amd/lib/libtg_hip.so, see
+technograd_amd/Makefile). There is no CPU fallback: if the library is missing
+or a call fails, these functions raise.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libtg_hip.so")
+
+FIXED, EXACT, ROWPROG, TIMING = 1, 2, 4, 8
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [
+        ("executor", ctypes.c_int), ("rows", ctypes.c_int), ("batch_ms", ctypes.c_double), ("qgemm_ms", ctypes.c_double),
+        ("qgemm_calls", ctypes.c_long), ("digits_ms", ctypes.c_double), ("other_ms", ctypes.c_double),
+        ("weight_bytes", ctypes.c_double), ("macs", ctypes.c_double), ("arena_bytes", ctypes.c_long),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("technograd_amd: %s is not built; run technograd_amd.build.build()" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        vp, ip, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        L.tg_hip_init.argtypes = [ip]
+        L.tg_hip_load.restype = vp
+        L.tg_hip_load.argtypes = [ctypes.c_char_p, sz, ip, ip]
+        L.tg_hip_info.argtypes = [vp, ctypes.POINTER(ip), ctypes.POINTER(ip), ctypes.POINTER(ip)]
+        L.tg_hip_batch.argtypes = [vp, vp, ctypes.c_long, vp, vp]
+        L.tg_hip_batch_fixed.argtypes = [vp, vp, ctypes.c_long, vp, vp]
+        L.tg_hip_batch_device.argtypes = [vp, vp, ctypes.c_long, vp, vp]
+        L.tg_hip_sync.argtypes = [vp]
+        L.tg_hip_matmul_q.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip, ip, ip]
+        L.tg_hip_free.argtypes = [vp]
+        L.tg_hip_error.restype = ctypes.c_char_p
+        L.tg_hip_stats.argtypes = [vp, ctypes.POINTER(Stats)]
+        L.tg_hip_reset_stats.argtypes = [vp]
+        L.tg_hip_dev_alloc.restype = vp
+        L.tg_hip_dev_alloc.argtypes = [sz]
+        L.tg_hip_dev_free.argtypes = [vp]
+        L.tg_hip_h2d.argtypes = [vp, vp, sz]
+        L.tg_hip_d2h.argtypes = [vp, vp, sz]
+        _lib = L
+    return _lib
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise RuntimeError("%s: %s" % (what, lib().tg_hip_error().decode()))
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def init(device=0):
+    _check(lib().tg_hip_init(device), "tg_hip_init")
+
+
+class DeviceBuffer:
+    """Device memory from tg_hip_dev_alloc."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = lib().tg_hip_dev_alloc(self.nbytes)
+        if not self.ptr:
+            raise RuntimeError("tg_hip_dev_alloc: " + lib().tg_hip_error().decode())
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        _check(lib().tg_hip_h2d(b.ptr, _p(a), a.nbytes), "tg_hip_h2d")
+        return b
+
+    def to_array(self, dtype, shape):
+        out = np.empty(shape, dtype)
+        _check(lib().tg_hip_d2h(_p(out), self.ptr, out.nbytes), "tg_hip_d2h")
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().tg_hip_dev_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        self.free()
+
+
+class Program:
+    """A model loaded on the device (tg_hip_load)."""
+
+    def __init__(self, tgir, flags=0, max_rows=4096):
+        if isinstance(tgir, str):
+            tgir = tgir.encode()
+        self.flags = flags
+        self.h = lib().tg_hip_load(tgir, len(tgir), flags, max_rows)
+        if not self.h:
+            raise RuntimeError("tg_hip_load: " + lib().tg_hip_error().decode())
+        per, nout, nthink = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        _check(lib().tg_hip_info(self.h, ctypes.byref(per), ctypes.byref(nout), ctypes.byref(nthink)), "tg_hip_info")
+        self.per, self.nout, self.nthink = per.value, nout.value, nthink.value
+        self.max_rows = max_rows
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().tg_hip_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def batch(self, rows):
+        rows = np.ascontiguousarray(rows, dtype=np.float32).reshape(-1, self.per)
+        out = np.empty((rows.shape[0], self.nout), np.float32)
+        steps = np.zeros((rows.shape[0], max(self.nthink, 1)), np.int32)
+        _check(lib().tg_hip_batch(self.h, _p(rows), rows.shape[0], _p(out), _p(steps)), "tg_hip_batch")
+        return out, steps
+
+    def batch_fixed(self, rows_q16):
+        rows = np.ascontiguousarray(rows_q16, dtype=np.int32).reshape(-1, self.per)
+        out = np.empty((rows.shape[0], self.nout), np.int32)
+        steps = np.zeros((rows.shape[0], max(self.nthink, 1)), np.int32)
+        _check(lib().tg_hip_batch_fixed(self.h, _p(rows), rows.shape[0], _p(out), _p(steps)), "tg_hip_batch_fixed")
+        return out, steps
+
+    def batch_device(self, d_rows, nrows, d_out, d_steps=None):
+        _check(lib().tg_hip_batch_device(self.h, d_rows, nrows, d_out, d_steps), "tg_hip_batch_device")
+
+    def sync(self):
+        _check(lib().tg_hip_sync(self.h), "tg_hip_sync")
+
+    def stats(self):
+        s = Stats()
+        _check(lib().tg_hip_stats(self.h, ctypes.byref(s)), "tg_hip_stats")
+        return s
+
+    def reset_stats(self):
+        _check(lib().tg_hip_reset_stats(self.h), "tg_hip_reset_stats")
+
+
+def matmul_q(q, bits, s, b, m, k, n, axis, flags=0):
+    """tg_matmul_qa (axis 0) / tg_matmul_qb (axis 1) on the device, host arrays."""
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    o = np.empty((m, n), np.float32)
+    _check(lib().tg_hip_matmul_q(_p(o), _p(q), bits, _p(s), _p(b), m, k, n, axis, flags), "tg_hip_matmul_q")
+    return o

@@ -1,0 +1,251 @@
+"""Synthetic models and rows for the benchmark configurations.
+
+Host preparation only (never timed): seeded weights and inputs, the
+round-to-nearest quantizer that `tgc quantize` applies to these layers, and
+TGIR text the backend (and the reference) load.
+
+* rand(seed, scale): the reference's initializer (src/lower.c:661-668,
+  :766-775): xorshift32 (13, 17, 5), seed 0 replaced by 0x9e3779b9,
+  u = (x >> 8) / 2^24 in f32, value (2u - 1) * scale in f32. xorshift32 is
+  linear over GF(2), so blocks of the stream are produced at once from
+  precomputed powers of the step matrix.
+* normal(seed, sigma): N(0, sigma) by Box-Muller over the same xorshift32
+  stream (pairs u1 = ((x >> 8) + 1) / 2^24, u2 = (x >> 8) / 2^24, computed in
+  f64, rounded to f32). The reference has no normal initializer; BASELINE's
+  N(0, sigma) configs use this one.
+* quantize_rtn: per-channel round-to-nearest with the MSE clip search of
+  src/quant.c:176-200 (10 candidate scales amax (1 - 0.05 g) / lim, error
+  summed in order, first strict minimum wins, codes nearbyint, scale stored
+  as f32). GPTQ needs calibration activations and falls back to this for
+  K > 2048 in the reference (src/quant.c:345-346), which is every quantized
+  layer of configs 2 and 3 wider than 2048 inputs.
+"""
+import numpy as np
+
+_BLOCK = 4096
+_POW = None
+
+
+def _step(x):
+    x = x ^ ((x << np.uint32(13)) & np.uint32(0xFFFFFFFF))
+    x = x ^ (x >> np.uint32(17))
+    x = x ^ ((x << np.uint32(5)) & np.uint32(0xFFFFFFFF))
+    return x
+
+
+def _powers():
+    """cols[k, i] = step^(k+1)(1 << i) for k < _BLOCK: the columns of the
+    GF(2) matrices of 1.._BLOCK xorshift steps."""
+    global _POW
+    if _POW is None:
+        cols = np.empty((_BLOCK, 32), np.uint32)
+        v = (np.uint32(1) << np.arange(32, dtype=np.uint32)).astype(np.uint32)
+        for k in range(_BLOCK):
+            v = _step(v)
+            cols[k] = v
+        _POW = cols
+    return _POW
+
+
+def xorshift_stream(seed, n):
+    """The first n outputs of xorshift32 from `seed` (0 -> 0x9e3779b9)."""
+    s = np.uint32(seed if seed else 0x9E3779B9)
+    cols = _powers()
+    out = np.empty(n, np.uint32)
+    done = 0
+    while done < n:
+        take = min(_BLOCK, n - done)
+        acc = np.zeros(take, np.uint32)
+        for i in range(32):
+            if (int(s) >> i) & 1:
+                acc ^= cols[:take, i]
+        out[done:done + take] = acc
+        s = np.uint32(acc[-1]) if take == _BLOCK else s
+        done += take
+    return out
+
+
+def rand(seed, scale, n):
+    x = xorshift_stream(seed, n)
+    u = (x >> np.uint32(8)).astype(np.float32) / np.float32(16777216.0)
+    return ((np.float32(2.0) * u - np.float32(1.0)) * np.float32(scale)).astype(np.float32)
+
+
+def normal(seed, sigma, n):
+    m = (n + 1) // 2
+    x = xorshift_stream(seed, 2 * m)
+    u1 = ((x[0::2] >> np.uint32(8)).astype(np.float64) + 1.0) / 16777216.0
+    u2 = (x[1::2] >> np.uint32(8)).astype(np.float64) / 16777216.0
+    r = np.sqrt(-2.0 * np.log(u1))
+    z = np.empty(2 * m, np.float64)
+    z[0::2] = r * np.cos(2.0 * np.pi * u2)
+    z[1::2] = r * np.sin(2.0 * np.pi * u2)
+    return (z[:n] * sigma).astype(np.float32)
+
+
+def bits01(seed, n):
+    """Uniform {0, 1} entries: the top bit of each xorshift32 output."""
+    return (xorshift_stream(seed, n) >> np.uint32(31)).astype(np.float32)
+
+
+def quantize_rtn(w, bits, axis):
+    """w: f32 param (rank 2). Returns (codes int8 in the param's own layout,
+    scales f32 per channel) as `tgc quantize --method rtn` writes them."""
+    lim = 127 if bits == 8 else 7
+    W = np.asarray(w, np.float64)
+    if axis == 1:
+        W = W.T  # channels are columns
+    C, K = W.shape
+    amax = np.abs(W).max(axis=1)
+    best = np.full(C, np.inf)
+    bs = np.where(amax == 0, 1e-8, amax / lim)
+    for g in range(10):
+        s = amax * (1.0 - 0.05 * g) / lim
+        with np.errstate(divide="ignore", invalid="ignore"):
+            code = np.clip(np.rint(W / s[:, None]), -lim, lim)
+        code = np.where(s[:, None] > 0, code, 0.0)
+        d = W - s[:, None] * code
+        e = np.cumsum(d * d, axis=1)[:, -1]  # summed in index order, as the reference does
+        better = (e < best) & (amax > 0)
+        best = np.where(better, e, best)
+        bs = np.where(better, s, bs)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        codes = np.clip(np.rint(W / bs[:, None]), -lim, lim)
+    codes = np.where(bs[:, None] > 0, codes, 0.0).astype(np.int8)
+    if axis == 1:
+        codes = codes.T
+    return np.ascontiguousarray(codes), bs.astype(np.float32)
+
+
+# ---- TGIR text ----
+
+def _num_block(vals, fmt="%.9g", per_line=8, pad="\n         "):
+    """Numbers the way the reference's ir_write lays them out (src/ir.c:166,
+    :174-177): each as ' %.9g', a line break before every per_line-th."""
+    out = []
+    for i, v in enumerate(np.asarray(vals).ravel()):
+        if i and i % per_line == 0:
+            out.append(pad)
+        out.append(" " + fmt % v)
+    return "".join(out)
+
+
+def _codes_text(codes):
+    """Codes as fixed-width tokens, 24 per line (any spacing is valid TGIR):
+    3 characters for int4 codes, 5 for int8."""
+    c = np.asarray(codes, np.int64).ravel()
+    w = 3 if c.size == 0 or np.abs(c).max() <= 7 else 5
+    dt = "S%d" % w
+    table = np.array([("%*d" % (w, v)).encode() for v in range(-127, 128)], dtype=dt)
+    toks = table[c + 127]
+    n = toks.size
+    pad = (-n) % 24
+    if pad:
+        toks = np.concatenate([toks, np.array([b""] * pad, dtype=dt)])
+    lines = toks.reshape(-1, 24)
+    body = b"\n            ".join(b"".join(row) for row in lines)
+    return body.decode()
+
+
+def param_f32(name, arr):
+    arr = np.asarray(arr, np.float32)
+    shape = " ".join(str(d) for d in arr.shape)
+    return "  (param %s (f32 %s)\n    (data%s))\n" % (name, shape, _num_block(arr.ravel()))
+
+
+def param_quant(name, codes, scales, bits, axis):
+    shape = " ".join(str(d) for d in codes.shape)
+    sc = _num_block(scales, per_line=8, pad="\n            ")
+    return "  (param %s (f32 %s)\n    (quant %d %d\n      (scale%s)\n      (codes %s)))\n" % (
+        name, shape, bits, axis, sc, _codes_text(codes))
+
+
+def mlp3_tgir(name, weights, bits):
+    """rmsnorm(W3 @ tanh(W2 @ tanh(W1 @ x))) with int-`bits` W (axis 0)."""
+    W1, W2, W3 = weights
+    out = ["(tgir 1\n  (model %s)\n" % name]
+    for nm, w in (("W1", W1), ("W2", W2), ("W3", W3)):
+        if bits:
+            c, s = quantize_rtn(w, bits, 0)
+            out.append(param_quant(nm, c, s, bits, 0))
+        else:
+            out.append(param_f32(nm, w))
+    d_in, h1, h2, d_out = W1.shape[1], W1.shape[0], W2.shape[0], W3.shape[0]
+    out.append("  (input x (f32 %d))\n  (block\n" % d_in)
+    out.append("    (%%0 (f32 %d) (matmul W1 x))\n    (%%1 (f32 %d) (tanh %%0))\n" % (h1, h1))
+    out.append("    (%%2 (f32 %d) (matmul W2 %%1))\n    (%%3 (f32 %d) (tanh %%2))\n" % (h2, h2))
+    out.append("    (%%4 (f32 %d) (matmul W3 %%3))\n    (%%5 (f32 %d) (rmsnorm %%4))\n" % (d_out, d_out))
+    out.append("  )\n  (output %5))\n")
+    return "".join(out)
+
+
+def linear_tgir(name, W, bits):
+    """W @ x with W quantized per output channel (axis 0)."""
+    c, s = quantize_rtn(W, bits, 0)
+    C, K = W.shape
+    return "".join([
+        "(tgir 1\n  (model %s)\n" % name, param_quant("W", c, s, bits, 0),
+        "  (input x (f32 %d))\n  (block\n    (%%0 (f32 %d) (matmul W x))\n  )\n  (output %%0))\n" % (K, C),
+    ])
+
+
+# ---- BASELINE.json configurations ----
+
+def config1(rows=65536):
+    """Config 1: 512 -> 2048 -> 2048 -> 512 MLP, tanh, rmsnorm, --bits 8, weights
+    rand(1, 0.05) (each param restarts the seed-1 stream, as three
+    `rand(1, 0.05)` initializers would), inputs N(0, 1) seed 0."""
+    W1 = rand(1, 0.05, 2048 * 512).reshape(2048, 512)
+    W2 = rand(1, 0.05, 2048 * 2048).reshape(2048, 2048)
+    W3 = rand(1, 0.05, 512 * 2048).reshape(512, 2048)
+    x = normal(0, 1.0, rows * 512).reshape(rows, 512)
+    return mlp3_tgir("mlp3", (W1, W2, W3), 8), x
+
+
+def config2_weight():
+    """Config 2: W 4096 x 4096 ~ N(0, 0.02) (seed 102: BASELINE gives no weight
+    seed), int4 per output channel."""
+    return normal(102, 0.02, 4096 * 4096).reshape(4096, 4096)
+
+
+def config2(rows=4096):
+    W = config2_weight()
+    x = normal(2, 1.0, rows * 4096).reshape(rows, 4096)
+    return linear_tgir("linear4096", W, 4), x
+
+
+def latent_reasoner_tgir():
+    """Config 4's model: examples/latent_reasoner's architecture with rand
+    seeds 11/23/37/41 and b_core = fill(0.01), in the instruction order the
+    reference lowers it to."""
+    w_emb = rand(11, 0.35, 128).reshape(16, 8)
+    w_core = rand(23, 0.12, 256).reshape(16, 16)
+    w_inj = rand(37, 0.10, 256).reshape(16, 16)
+    w_out = rand(41, 0.5, 64).reshape(4, 16)
+    parts = ["(tgir 1\n  (model latent_reasoner)\n"]
+    for nm, v in (("w_emb", w_emb), ("b_emb", np.zeros(16, np.float32)), ("w_core", w_core), ("w_inj", w_inj),
+                  ("b_core", np.full(16, 0.01, np.float32)), ("w_out", w_out), ("b_out", np.zeros(4, np.float32))):
+        parts.append(param_f32(nm, v))
+    parts.append("""  (input x (f32 8))
+  (block
+    (%8 (f32 16) (matmul w_emb x))
+    (%9 (f32 16) (add %8 b_emb))
+    (%10 (f32 16) (rmsnorm %9))
+    (%11 (f32 16) (think %10 32 9.99999975e-05
+      (%12 (f32 16) (matmul w_core %11))
+      (%13 (f32 16) (matmul w_inj %10))
+      (%14 (f32 16) (add %12 %13))
+      (%15 (f32 16) (add %14 b_core))
+      (%16 (f32 16) (tanh %15))
+      (yield %16)))
+    (%17 (f32 4) (matmul w_out %11))
+    (%18 (f32 4) (add %17 b_out))
+    (%19 (f32 4) (softmax %18))
+  )
+  (output %19))
+""")
+    return "".join(parts)
+
+
+def config4_rows(rows=1048576):
+    return bits01(4, rows * 8).reshape(rows, 8)

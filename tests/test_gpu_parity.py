@@ -1,0 +1,191 @@
+"""GPU parity: the HIP backend, called through its C ABI, against the
+reference's golden vectors (tests/golden, written by the reference's own
+code) and the CPU oracle pinned to them. Integer and Q16.16 results are
+compared bit for bit; f32 with the predicates of tests/parity.py."""
+import glob
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from technograd_amd import hip, synth
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+import parity  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+NAMES = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(GOLDEN, "*.npz")))
+# models whose outputs involve no transcendental: the exact paths must match bit for bit
+NO_LIBM = {"odd_f32", "odd_q4", "odd_q8"}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    print("gpu parity: tg_hip_init(0)", flush=True)
+    hip.init(0)
+
+
+def load(name):
+    with open(os.path.join(GOLDEN, name + ".tgir")) as f:
+        text = f.read()
+    return text, np.load(os.path.join(GOLDEN, name + ".npz"))
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_default_path_against_reference(name):
+    print("case", name, flush=True)
+    text, d = load(name)
+    p = hip.Program(text, max_rows=128)
+    y, steps = p.batch(d["x"])
+    parity.check_model(y, d["y"])
+    if "latent" not in name and "haltm" not in name:
+        assert np.array_equal(steps, d["steps"])
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_exact_path_against_reference(name):
+    """TG_HIP_EXACT: quantized matmuls in the reference's sequential order."""
+    print("case", name, flush=True)
+    text, d = load(name)
+    p = hip.Program(text, flags=hip.EXACT, max_rows=128)
+    y, steps = p.batch(d["x"])
+    if name in NO_LIBM:
+        assert np.array_equal(bits(y), bits(d["y"]))
+    else:
+        parity.check_model(y, d["y"])
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_row_program_against_reference(name):
+    """One lane per row: think loops, scans and every op in the VM's order."""
+    print("case", name, flush=True)
+    text, d = load(name)
+    p = hip.Program(text, flags=hip.ROWPROG, max_rows=128)
+    y, steps = p.batch(d["x"])
+    if name in NO_LIBM:
+        assert np.array_equal(bits(y), bits(d["y"]))
+    else:
+        parity.check_model(y, d["y"])
+    if "latent" in name or "haltm" in name:
+        # halting decisions compare a delta with a threshold; device libm may
+        # move a row across it only when its delta ties the threshold to a few ulp
+        assert (steps == d["steps"]).mean() > 0.98
+
+
+@pytest.mark.parametrize("name", [n for n in NAMES if "xq" in np.load(os.path.join(GOLDEN, n + ".npz")).files])
+def test_fixed_point_bit_exact(name):
+    """Q16.16 (the --fixed number system): outputs and steps bit for bit."""
+    print("case", name, flush=True)
+    text, d = load(name)
+    p = hip.Program(text, flags=hip.FIXED, max_rows=256)
+    yq, sq = p.batch_fixed(d["xq"])
+    assert np.array_equal(yq, d["yq"])
+    assert np.array_equal(sq, d["stepsq"])
+
+
+def test_latent_reasoner_all_inputs_fixed_and_steps():
+    """Config 4's model over its whole {0,1}^8 input domain, 4096 rows in one
+    pass (rows are repeated: the backend must not depend on row position)."""
+    text = synth.latent_reasoner_tgir()
+    x = np.tile(synth.config4_rows(256), (16, 1))
+    xq = O.to_fixed_rows(x)
+    want, wsteps = O.Model(text).batch_fixed(xq)
+    got, steps = hip.Program(text, flags=hip.FIXED, max_rows=1000).batch_fixed(xq)  # 5 device passes
+    assert np.array_equal(got, want) and np.array_equal(steps, wsteps)
+
+
+@pytest.mark.parametrize("bits_,axis,m,k,n", [(4, 0, 37, 513, 1), (8, 0, 64, 256, 3), (4, 1, 5, 200, 33), (8, 1, 70, 64, 130),
+                                              (4, 0, 256, 1024, 16)])
+def test_matmul_q_entry_point(bits_, axis, m, k, n):
+    """tg_hip_matmul_q (tg_matmul_qa / tg_matmul_qb arguments) against the
+    oracle: exact flag bit for bit, matrix-core path within the bound."""
+    print("case matmul_q", bits_, axis, m, k, n, flush=True)
+    rng = np.random.default_rng(m * 7 + k)
+    lim = 127 if bits_ == 8 else 7
+    C = m if axis == 0 else n
+    shape = (m, k) if axis == 0 else (k, n)
+    codes = rng.integers(-lim, lim + 1, size=shape).astype(np.int8)
+    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
+    if bits_ == 4:
+        flat = codes.ravel().astype(np.int64)
+        if flat.size % 2:
+            flat = np.concatenate([flat, [0]])
+        packed = ((flat[0::2] & 15) | ((flat[1::2] & 15) << 4)).astype(np.uint8).view(np.int8)
+    else:
+        packed = codes.ravel()
+    b = rng.normal(size=(k, n) if axis == 0 else (m, k)).astype(np.float32)
+    # oracle: a one-instruction model
+    text = "(tgir 1\n  (model mq)\n" + synth.param_quant("W", codes, scales, bits_, axis)
+    if axis == 0:
+        text += "  (input b (f32 %d %d))\n  (block\n    (%%0 (f32 %d %d) (matmul W b))\n  )\n  (output %%0))\n" % (k, n, m, n)
+    else:
+        text += "  (input b (f32 %d %d))\n  (block\n    (%%0 (f32 %d %d) (matmul b W))\n  )\n  (output %%0))\n" % (m, k, m, n)
+    want, _ = O.Model(text).batch(b.reshape(1, -1))
+    want = want.reshape(m, n)
+    exact = hip.matmul_q(packed, bits_, scales, b, m, k, n, axis, flags=hip.EXACT)
+    assert np.array_equal(bits(exact), bits(want))
+    fast = hip.matmul_q(packed, bits_, scales, b, m, k, n, axis)
+    if axis == 0:  # o[i, j] = s[i] sum_p code[i, p] b[p, j]: rows of b^T are the activations
+        frac = parity.check_qmatmul(fast.T, want.T, codes, scales, b.T)
+    else:
+        frac = parity.check_qmatmul(fast, want, codes.T, scales, b)
+    assert frac < 0.05
+
+
+def test_special_rows_follow_reference():
+    """A row with inf or nan takes the reference's sequential f32 loop."""
+    W = synth.normal(9, 0.02, 64 * 256).reshape(64, 256)
+    text = synth.linear_tgir("sp", W, 4)
+    x = synth.normal(10, 1.0, 4 * 256).reshape(4, 256)
+    x[1, 7] = np.inf
+    x[2, 100] = np.nan
+    x[3, 5] = 3e38
+    want, _ = O.Model(text).batch(x)
+    got, _ = hip.Program(text, max_rows=8).batch(x)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = np.isfinite(want)
+    assert np.array_equal(bits(got[1:][fin[1:]]), bits(want[1:][fin[1:]]))
+    parity.check_model(got[:1], want[:1])
+
+
+@pytest.mark.parametrize("B", [1, 16, 256, 4096])
+def test_config2_full_size(B):
+    """Config 2 (int4 4096 x 4096) at every benchmark batch, matrix-core path.
+
+    At K = 4096 the reference's own sequential f32 sum differs from the exact
+    dot product by more than 1e-5 relative on a few percent of outputs (those
+    whose sum cancels). The integer path is exact up to its 24-bit activation
+    grid, so on those outputs it cannot sit within 1e-5 of the reference's
+    value; it must instead be within the reference's provable rounding bound
+    (tests/parity.py) and at least as close to the exact value as the
+    reference is. The exact path (TG_HIP_EXACT, the reference's order,
+    bit-identical to the oracle in the tests above) stands in for the
+    reference at this size."""
+    print("case config2 B", B, flush=True)
+    W = synth.config2_weight()
+    text = synth.linear_tgir("linear4096", W, 4)
+    x = synth.normal(2, 1.0, B * 4096).reshape(B, 4096)
+    fast, _ = hip.Program(text, max_rows=B).batch(x)
+    sub_rows = min(B, 256)  # the sequential path is slow: compare its first 256 rows
+    exact, _ = hip.Program(text, flags=hip.EXACT, max_rows=sub_rows).batch(x[:sub_rows])
+    fast, x = fast[:sub_rows], x[:sub_rows]
+    strict = parity.strict_ok(fast, exact).mean()
+    codes, scales = synth.quantize_rtn(W, 4, 0)
+    truth = (x.astype(np.float64) @ codes.astype(np.float64).T) * scales.astype(np.float64)
+    err_fast = np.abs(fast - truth)
+    err_ref = np.abs(exact - truth)
+    assert err_fast.mean() < err_ref.mean()  # the integer path is the more accurate one
+    assert np.abs(fast - truth).max() <= np.abs(truth).max() * 1e-5
+    rows = min(sub_rows, 2)  # the full bound needs all K partial sums: check it on two rows
+    parity.check_qmatmul(fast[:rows], exact[:rows], codes, scales, x[:rows])
+    print("config2 B=%d: %.4f of outputs within 1e-5/4ulp of the reference order; mean |err| vs exact: "
+          "matrix cores %.3g, reference order %.3g" % (B, strict, err_fast.mean(), err_ref.mean()), flush=True)
+    assert strict > 0.9
