@@ -46,7 +46,9 @@ typedef struct tg_hip_prog tg_hip_prog;
 typedef struct {
 	int executor;        /* 0: layer executor, 1: row-program executor */
 	int rows;            /* rows of the last batch */
-	double batch_ms;     /* device time of the last batch call (HIP events) */
+	double batch_ms;     /* device time from the first tg_hip_batch_device call after a
+	                        tg_hip_sync to the end of the last one (HIP events);
+	                        for tg_hip_batch, the last call */
 	double qgemm_ms;     /* time in quantized-matmul kernels (TG_HIP_TIMING) */
 	long qgemm_calls;
 	double digits_ms;    /* time in activation-digit kernels (TG_HIP_TIMING) */
@@ -77,6 +79,15 @@ int tg_hip_batch_fixed(tg_hip_prog *p, const int32_t *rows, long nrows, int32_t 
  * the program's stream; tg_hip_sync waits. */
 int tg_hip_batch_device(tg_hip_prog *p, const void *d_rows, long nrows, void *d_out, int *d_steps);
 int tg_hip_sync(tg_hip_prog *p);
+
+/* Launch on `stream` (a hipStream_t of the caller's, e.g. PyTorch's current
+ * stream) instead of the program's own; NULL restores the program's stream.
+ * Work already queued on the previous stream is waited for first. No
+ * counterpart in the reference (its interpreter has no streams): for callers
+ * that order the backend's work with their own. */
+int tg_hip_set_stream(tg_hip_prog *p, void *stream);
+/* The hipStream_t the program launches on (to order other work after it). */
+void *tg_hip_get_stream(const tg_hip_prog *p);
 
 /* One quantized matmul with the reference kernel's arguments, host buffers:
  * axis 0: o[m,n] = diag(s) Q[m,k] @ b[k,n]  (tg_matmul_qa)

@@ -4,12 +4,13 @@
 // f32 running sum (runtime/tg_rt.h:132-151). Here each activation row is
 // written exactly as a 24-bit fixed-point vector q = rint(x * 2^(23-E)) with E
 // the row's exponent (max |x| < 2^E), and q is split into three balanced int8
-// digits q = d0 + 256 d1 + 65536 d2. v_mfma_i32_16x16x64_i8 sums code * d_l in
+// digits q = d0 + 256 d1 + 65536 d2. v_mfma_i32_32x32x32_i8 sums code * d_l in
 // int32 exactly for each digit l; the digit sums are combined in int64, scaled
 // by 2^(E-23) in double (exact) and rounded to f32 once, then multiplied by
 // the channel scale in f32 like the reference. The only approximation is the
 // 24-bit activation grid (error <= 2^-24 max|x| per element), far below the
-// reference's own f32 summation error at these K.
+// reference's own f32 summation error at these K. Every step depends on the
+// row alone, so a row's outputs do not depend on the batch it came in.
 //
 // Rows with a non-finite or huge entry are flagged by the digit kernel and
 // their outputs are recomputed in the epilogue with the reference's exact
@@ -17,41 +18,41 @@
 //
 // Operand layouts in global memory are the MFMA fragment order of
 // v_mfma_i32_32x32x32_i8 (lane l holds row or channel l % 32 and inputs
-// 16 (l / 32) .. +15 of a 32-input block), so the K loop copies contiguous
-// 1 KiB chunks straight into LDS (global_load_lds_dwordx4) and every fragment
-// read is one contiguous 16- or 8-byte lane read:
+// 16 (l / 32) .. +15 of a 32-input block), so every fragment is one contiguous
+// 1 KiB (or 512 B) block: the large-batch kernel copies them straight into LDS
+// (global_load_lds_dwordx4) and the small-batch kernel straight into registers.
 //   digits   [row / 32][k / 32][digit 0..2][lane 0..63][16 bytes]
 //   int8 w   [channel / 32][k / 32][lane][16 codes]
 //   int4 w   [channel / 32][k / 32][lane][8 bytes]: byte b holds t(b) in its
 //            low nibble and t(b + 8) in its high nibble of the lane's 16
 //            inputs, t = code + 8 in [0, 15] (offset binary), so unpacking is
-//            two masks per 4 bytes; the +8 bias is removed with the per-row
-//            digit sums: sum t d = sum code d + 8 sum d.
-// Weights are repacked once at load (channels padded to 128, K to 64).
+//            two masks per 4 bytes; the +8 bias is removed with the row's sum
+//            of q: sum_k t q = sum_k code q + 8 sum_k q.
+// Weights are repacked once at load (channels padded to 256, K to 64).
 #include "tg_kern.h"
 
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
+
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int KB = 64;        // inputs per K step of the MFMA kernel
-constexpr int BM = 128;       // rows (activations) per workgroup tile
-constexpr int BN = 128;       // channels per workgroup tile (weights are padded to it)
+constexpr int KB = 64;        // K padding (one K step of the LDS kernel)
+constexpr int BM = 128;       // rows per tile of the LDS kernel (activation rows are padded to it)
+constexpr int BN = 256;       // channels per tile of the LDS kernel (weights are padded to it)
 
 inline long round_up(long x, long m) { return (x + m - 1) / m * m; }
 
-typedef int v16i __attribute__((ext_vector_type(16)));
-#define LDSP(p) ((__attribute__((address_space(3))) void *)(p))
-
 struct Scratch {
-	int8_t *dig;    // digits in fragment order (see above)
-	int *e;         // [Mp] row exponent E
-	int *sum;       // [3][Mp] digit sums
-	int *special;   // [Mp]
+	int8_t *dig;       // digits in fragment order (see above)
+	long long *qsum;   // [Mp] sum over k of the row's fixed-point values q
+	int *e;            // [Mp] row exponent E
+	int *special;      // [Mp] 1: the row takes the reference's sequential loop
 };
 
 Scratch carve(void *base, int Mp, int Kp)
@@ -59,84 +60,146 @@ Scratch carve(void *base, int Mp, int Kp)
 	Scratch s;
 	char *p = (char *)base;
 	s.dig = (int8_t *)p;
-	p += (size_t)Mp * Kp * 3;
+	p += (size_t)Mp * Kp * 3; // Kp is a multiple of 64: 8-byte alignment holds
+	s.qsum = (long long *)p;
+	p += (size_t)Mp * sizeof(long long);
 	s.e = (int *)p;
 	p += (size_t)Mp * sizeof(int);
-	s.sum = (int *)p;
-	p += (size_t)3 * Mp * sizeof(int);
 	s.special = (int *)p;
 	return s;
 }
 
-// element k of activation row m
+// element 0 of activation row m
 __device__ inline const float *xrow(const tgk_qgemm_args &a, int m)
 {
 	int r = m / a.ni, j = m - r * a.ni;
 	return a.x + (long)r * a.xr + (long)j * a.xj;
 }
 
-// One workgroup per activation row: exponent, digits, digit sums, special flag.
+__device__ inline float wave_max(float v)
+{
+	for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+	return v;
+}
+
+__device__ inline long long wave_sum(long long v)
+{
+	for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+	return v;
+}
+
+// balanced base-256 digits of |q| < 2^23: q = d0 + 256 d1 + 65536 d2, d_l in [-128, 127]
+__device__ inline void split3(int q, int &d0, int &d1, int &d2)
+{
+	d0 = (int)(int8_t)(q & 255);
+	const int q1 = (q - d0) >> 8;
+	d1 = (int)(int8_t)(q1 & 255);
+	d2 = (q1 - d1) >> 8;
+}
+
+// inputs k0 .. k0 + 15 of a row, zero at and beyond K. The addresses are
+// clamped into the row instead of branched on, so the loads of several
+// calls can all be in flight before the first value is used. vec: unit
+// stride, 16-byte aligned row, K a multiple of 16 (whole float4s).
+template <bool VEC>
+__device__ inline void load16(float *v, const float *x, long xk, int k0, int K)
+{
+	const bool in = k0 < K;
+	if (VEC) {
+		const float *p = x + (in ? k0 : 0);
+		for (int i = 0; i < 4; i++) {
+			const float4 f = *(const float4 *)(p + 4 * i);
+			v[4 * i] = in ? f.x : 0.0f, v[4 * i + 1] = in ? f.y : 0.0f;
+			v[4 * i + 2] = in ? f.z : 0.0f, v[4 * i + 3] = in ? f.w : 0.0f;
+		}
+	} else {
+		for (int i = 0; i < 16; i++) {
+			const int k = k0 + i;
+			const float f = x[(long)(k < K ? k : K - 1) * xk];
+			v[i] = k < K ? f : 0.0f;
+		}
+	}
+}
+
+// digits of 16 consecutive inputs (row m, inputs k0 .. k0 + 15) into their
+// three 16-byte chunks; returns the sum of their q
+__device__ inline long long put16(int8_t *blk, int k0, const float *v, int E, bool zero)
+{
+	unsigned w0[4] = {0, 0, 0, 0}, w1[4] = {0, 0, 0, 0}, w2[4] = {0, 0, 0, 0};
+	int qs = 0; // |sum of 16 q| < 2^27
+	if (!zero) {
+		for (int i = 0; i < 16; i++) {
+			const int q = (int)rintf(ldexpf(v[i], 23 - E)); // exact: |q| < 2^23
+			qs += q;
+			int d0, d1, d2;
+			split3(q, d0, d1, d2);
+			const int sh = (i & 3) * 8;
+			w0[i >> 2] |= (unsigned)(d0 & 255) << sh;
+			w1[i >> 2] |= (unsigned)(d1 & 255) << sh;
+			w2[i >> 2] |= (unsigned)(d2 & 255) << sh;
+		}
+	}
+	int8_t *p = blk + (k0 >> 5) * 3072 + ((k0 >> 4) & 1) * 512;
+	*(v4i *)p = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
+	*(v4i *)(p + 1024) = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+	*(v4i *)(p + 2048) = v4i{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
+	return qs;
+}
+
+// One wave per activation row (4 rows per block): exponent, digits, sum of q,
+// special flag. Lane l owns inputs 1024 s + 16 l .. +15 of each 1024-input
+// slab s. Rows of up to SL slabs are read once into registers; longer rows are
+// read twice (max, then digits), the second time from cache.
 __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
 {
-	__shared__ float red[256];
-	__shared__ int ired[3][256];
-	__shared__ int bad;
-	const int m = blockIdx.x, t = threadIdx.x;
-	const float *x = m < M ? xrow(a, m) : a.x;
+	constexpr int SL = 4;
+	const int lane = threadIdx.x & 63;
+	const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+	if (m >= M) return; // the whole wave leaves; the kernel has no block barrier
+	const float *x = xrow(a, m);
 	const long xk = a.xk;
-	if (t == 0) bad = 0;
-	__syncthreads();
+	const bool vec = xk == 1 && ((size_t)x & 15) == 0 && (K & 15) == 0;
+	const int nsl = (Kp + 1023) / 1024;
+	float v[SL][16];
 	float mx = 0.0f;
-	if (m < M)
-		for (int k = t; k < K; k += 256) {
-			float v = x[k * xk];
-			if (!isfinite(v)) bad = 1;
-			mx = fmaxf(mx, fabsf(v));
-		}
-	red[t] = mx;
-	__syncthreads();
-	for (int w = 128; w > 0; w >>= 1) {
-		if (t < w) red[t] = fmaxf(red[t], red[t + w]);
-		__syncthreads();
+	int bad = 0;
+	// slabs t0 .. t0 + SL - 1 into v, loads first; slabs past the row read as
+	// zeros (no branch, so every load is in flight before the first use)
+	auto fetch = [&](int t0) {
+		if (vec)
+			for (int t = 0; t < SL; t++) load16<true>(v[t], x, xk, (t0 + t) * 1024 + lane * 16, K);
+		else
+			for (int t = 0; t < SL; t++) load16<false>(v[t], x, xk, (t0 + t) * 1024 + lane * 16, K);
+	};
+	for (int t0 = 0; t0 < nsl; t0 += SL) {
+		fetch(t0);
+		for (int t = 0; t < SL; t++)
+			for (int i = 0; i < 16; i++) {
+				bad |= !isfinite(v[t][i]);
+				mx = fmaxf(mx, fabsf(v[t][i]));
+			}
 	}
-	const float amax = red[0];
-	const int special = bad || amax > 0x1p100f;
+	const float amax = wave_max(mx); // nan never wins fmaxf; such rows are flagged by `bad`
+	const int special = __any(bad) || amax > 0x1p100f;
 	int E = 0;
 	if (!special && amax > 0.0f) {
 		frexpf(amax, &E); // amax = f 2^E, f in [0.5, 1)
 		if (rintf(ldexpf(amax, 23 - E)) > 8355328.0f) E += 1; // keep the top digit within int8
 	}
-	int s0 = 0, s1 = 0, s2 = 0;
-	const int kblocks = Kp / 32, r = m & 31;
-	int8_t *blk = s.dig + (long)(m >> 5) * kblocks * 3072;
-	for (int k = t; k < Kp; k += 256) {
-		int q = 0;
-		if (m < M && k < K && !special) q = (int)rintf(ldexpf(x[k * xk], 23 - E)); // exact: |q| < 2^23
-		int d0 = (int)(int8_t)(q & 255);
-		int q1 = (q - d0) >> 8;
-		int d1 = (int)(int8_t)(q1 & 255);
-		int d2 = (q1 - d1) >> 8;
-		int8_t *p = blk + (k >> 5) * 3072 + (((k >> 4) & 1) * 32 + r) * 16 + (k & 15);
-		p[0] = (int8_t)d0;
-		p[1024] = (int8_t)d1;
-		p[2048] = (int8_t)d2;
-		s0 += d0;
-		s1 += d1;
-		s2 += d2;
+	long long qs = 0;
+	int8_t *blk = s.dig + (long)(m >> 5) * (Kp / 32) * 3072 + (m & 31) * 16;
+	for (int t0 = 0; t0 < nsl; t0 += SL) {
+		if (nsl > SL) fetch(t0); // rows of up to SL slabs are still in v
+		for (int t = 0; t < SL; t++) {
+			const int k0 = (t0 + t) * 1024 + lane * 16;
+			if (t0 + t < nsl && k0 < Kp) qs += put16(blk, k0, v[t], E, special);
+		}
 	}
-	ired[0][t] = s0;
-	ired[1][t] = s1;
-	ired[2][t] = s2;
-	__syncthreads();
-	for (int w = 128; w > 0; w >>= 1) {
-		if (t < w)
-			for (int l = 0; l < 3; l++) ired[l][t] += ired[l][t + w];
-		__syncthreads();
-	}
-	if (t == 0) {
+	qs = wave_sum(qs);
+	if (lane == 0) {
 		s.e[m] = E;
 		s.special[m] = special;
-		for (int l = 0; l < 3; l++) s.sum[(long)l * gridDim.x + m] = ired[l][0];
+		s.qsum[m] = qs;
 	}
 }
 
@@ -159,8 +222,14 @@ __device__ inline v4i unpack4(unsigned w0, unsigned w1)
 	return r;
 }
 
-__device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int Mp, int m, int c, int acc0,
-				int acc1, int acc2, long corr)
+// digit sums -> sum_k t q (exact: |.| < 2^53)
+__device__ inline long long combine(int acc0, int acc1, int acc2)
+{
+	return (long long)acc0 + (long long)acc1 * 256 + (long long)acc2 * 65536;
+}
+
+// output (m, c) from tot = sum_k t[c][k] q[m][k]
+__device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot)
 {
 	if (m >= a.M || c >= w.C) return;
 	float acc32;
@@ -170,54 +239,46 @@ __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 		for (int k = 0; k < w.K; k++) t += (float)code_orig(w, c, k) * x[k * a.xk];
 		acc32 = t;
 	} else {
-		long t0 = (long)acc0 - corr * s.sum[m];
-		long t1 = (long)acc1 - corr * s.sum[Mp + m];
-		long t2 = (long)acc2 - corr * s.sum[2 * Mp + m];
-		long tot = t0 + t1 * 256 + t2 * 65536; // exact: |tot| < 2^53
+		if (w.bits == 4) tot -= 8 * s.qsum[m];
 		acc32 = (float)ldexp((double)tot, s.e[m] - 23);
 	}
 	int r = m / a.ni, jj = m - r * a.ni;
 	a.o[(long)r * a.orr + (long)c * a.oc + (long)jj * a.oj] = w.scale[c] * acc32;
 }
 
-// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0], expcnt [6:4], lgkmcnt [11:8]):
-// wait until at most n vector-memory loads of this wave are outstanding and
-// every LDS access has completed.
-template <int N>
-__device__ inline void wait_vm_lgkm0() { __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4)); }
+// s_waitcnt immediate (gfx9 encoding: vmcnt [3:0], expcnt [6:4], lgkmcnt
+// [11:8]): wait until every vector-memory load of this wave has completed.
+__device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
 
-// One 1 KiB global -> LDS copy by a wave: lane l moves 16 bytes from src to
-// LDS address lds + 16 l. Issued with inline assembly so that the compiler,
-// which cannot tell these copies apart from the LDS reads of other ring
-// stages, does not drain all outstanding copies before every read; the K
-// loop waits for exactly the stage it needs (wait_vm_lgkm0) instead.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ inline void copy_to_lds(const void *src, unsigned lds)
+// One 1 KiB global -> LDS copy by a wave: lane l moves the 16 bytes at
+// sbase + voff into LDS address lds + 16 l (voff = 16 l). Issued with inline
+// assembly so that the compiler, which cannot tell these copies apart from
+// the LDS reads of other ring stages, does not drain all outstanding copies
+// before every read; the K loop waits for its stage explicitly (wait_vm0).
+__device__ inline void copy_to_lds(const uint8_t *sbase, unsigned voff, unsigned lds)
 {
-	asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+	asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
-#pragma clang diagnostic pop
 
-// 512 threads = 8 waves; the workgroup computes a 128 x 128 tile (rows x
-// channels), wave (wm, wn) a 32 x 64 block as two 32 x 32 blocks of
-// v_mfma_i32_32x32x32_i8 for each of the three digit planes (96 accumulator
-// registers). Each 64-input step needs 24 KiB of digits and 4 or 8 KiB of
-// weights, copied by the waves straight from global memory into a ring of S
-// LDS stages (global_load_lds, 1 KiB per wave instruction, no registers), so
-// S - 1 steps are in flight while the waves multiply out of the oldest stage,
-// with one barrier per step.
+// Large batches. 512 threads = 8 waves; the workgroup computes a 128 x 256
+// tile (rows x channels), wave (wm, wn) a 32 x 128 block as four 32 x 32
+// blocks of v_mfma_i32_32x32x32_i8 for each of the three digit planes (192
+// accumulator registers). Each 64-input step needs 24 KiB of digits and 8
+// (int4) or 16 (int8) KiB of weights, copied by the waves straight from global
+// memory into a ring of 3 LDS stages (global_load_lds, 1 KiB per wave
+// instruction, no registers): stage kt + 2 is in flight while the waves
+// multiply out of stage kt. Fragments are read from LDS one 32-input substep
+// ahead of the MFMAs that use them, across the step's single barrier.
 template <int BITS>
-__global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int Mp, int gx, int gy)
+__global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int gx, int gy)
 {
-	constexpr int S = BITS == 4 ? 5 : 4;              // ring stages
-	constexpr int AST = 24 * 1024;                   // 4 row blocks x 2 substeps x 3 digits x 1 KiB
-	constexpr int BST = BITS == 4 ? 4096 : 8192;     // 4 channel blocks x 2 substeps x 512 B or 1 KiB
-	constexpr int STG = AST + BST, NL = STG / 1024;   // 1 KiB wave copies per stage: 28 or 32
-	constexpr int LW = 4;                            // copies per wave (wave 7 has none for int4)
+	constexpr int S = 3;                                  // ring stages
+	constexpr int AST = 24 * 1024;                        // 4 row blocks x 2 substeps x 3 digits x 1 KiB
+	constexpr int BST = BITS == 4 ? 8192 : 16384;         // 8 channel blocks x 2 substeps x 512 B or 1 KiB
+	constexpr int STG = AST + BST, NP = STG / 1024, PW = NP / 8; // 1 KiB pieces per stage, per wave
 	__shared__ __attribute__((aligned(1024))) uint8_t lds[S * STG];
-	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-	const int wm = wave & 3, wn = wave >> 2;
+	const int tid = threadIdx.x, lane = tid & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave & 3, wn = wave >> 2;
 	// XCD-aware tile order: workgroups are dealt to the 8 XCDs round robin, so
 	// renumber them to give each XCD a contiguous band of row tiles (its L2
 	// then holds those rows' digits for every channel tile).
@@ -227,77 +288,159 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 	const int m0 = bm * BM, c0 = bn * BN, nk = w.Kp / KB, kblocks = w.Kp / 32;
 	const uint8_t *gA = (const uint8_t *)s.dig + (long)(m0 / 32) * kblocks * 3072;
 	const uint8_t *gB = w.w + (long)(c0 / 32) * kblocks * (BITS == 4 ? 512 : 1024);
-	// this wave's copies: source at step 0 (lane offset included) and bytes per step
-	const uint8_t *src0[LW];
-	long sstep[LW];
-	int nq = 0;
-	for (int i = 0; i < LW; i++) {
-		const int q = wave * LW + i;
-		if (q >= NL) break;
-		nq++;
-		if (q < 24) {
-			src0[i] = gA + (long)(q / 6) * kblocks * 3072 + (q % 6) * 1024;
-			sstep[i] = 6144;
-		} else if (BITS == 4) {
-			src0[i] = gB + (long)(q - 24) * kblocks * 512;
-			sstep[i] = 1024;
-		} else {
-			src0[i] = gB + (long)((q - 24) >> 1) * kblocks * 1024 + ((q - 24) & 1) * 1024;
-			sstep[i] = 2048;
-		}
-		src0[i] += lane * 16;
-	}
+	// piece q of stage kt: digits of row block q / 6 (6 KiB per step), or
+	// weights: channel block q - 24 (int4, 1 KiB per step) or (q - 24) / 2, half (q - 24) % 2 (int8)
+	auto piece = [&](int q, int kt) -> const uint8_t * {
+		if (q < 24) return gA + (long)(q / 6) * kblocks * 3072 + (q % 6) * 1024 + (long)kt * 6144;
+		const int p = q - 24;
+		if (BITS == 4) return gB + (long)p * kblocks * 512 + (long)kt * 1024;
+		return gB + (long)(p >> 1) * kblocks * 1024 + (p & 1) * 1024 + (long)kt * 2048;
+	};
+	const unsigned voff = lane * 16;
 	const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) uint8_t *)lds;
 	auto issue = [&](int kt) {
-		const unsigned dst = lds0 + (unsigned)((kt % S) * STG + wave * LW * 1024);
-		for (int i = 0; i < nq; i++) copy_to_lds(src0[i] + kt * sstep[i], __builtin_amdgcn_readfirstlane(dst + i * 1024));
+		const unsigned dst = lds0 + (unsigned)((kt % S) * STG);
+		for (int i = 0; i < PW; i++) {
+			const int q = wave * PW + i;
+			copy_to_lds(piece(q, kt), voff, dst + q * 1024);
+		}
 	};
-	v16i acc[3][2];
+	v16i acc[3][4];
 	for (int l = 0; l < 3; l++)
-		for (int j = 0; j < 2; j++)
+		for (int j = 0; j < 4; j++)
 			for (int v = 0; v < 16; v++) acc[l][j][v] = 0;
+	typedef typename std::conditional<BITS == 4, uint2, v4i>::type bfrag;
+	v4i af[2][3];
+	bfrag bf[2][4];
+	auto fread = [&](int kt, int kk, int b) {
+		const uint8_t *A = lds + (kt % S) * STG + wm * 6144 + kk * 3072 + lane * 16;
+		for (int l = 0; l < 3; l++) af[b][l] = *(const v4i *)(A + l * 1024);
+		if (BITS == 4) {
+			const uint8_t *B = lds + (kt % S) * STG + AST + wn * 4096 + kk * 512 + lane * 8;
+			for (int j = 0; j < 4; j++) bf[b][j] = *(const bfrag *)(B + j * 1024);
+		} else {
+			const uint8_t *B = lds + (kt % S) * STG + AST + wn * 8192 + kk * 1024 + lane * 16;
+			for (int j = 0; j < 4; j++) bf[b][j] = *(const bfrag *)(B + j * 2048);
+		}
+	};
+	auto mm = [&](int b) {
+		for (int j = 0; j < 4; j++) {
+			v4i wv;
+			if constexpr (BITS == 4) wv = unpack4(bf[b][j].x, bf[b][j].y);
+			else wv = bf[b][j];
+			for (int l = 0; l < 3; l++) acc[l][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[b][l], wv, acc[l][j], 0, 0, 0);
+		}
+	};
 	for (int st = 0; st < S - 1; st++)
 		if (st < nk) issue(st);
+	wait_vm0();
+	__builtin_amdgcn_s_barrier();
+	asm volatile("" ::: "memory"); // LDS changed behind the compiler's back: reload it
+	fread(0, 0, 0);
 	for (int kt = 0; kt < nk; kt++) {
-		const int later = nk - 1 - kt < S - 2 ? nk - 1 - kt : S - 2; // stages issued after kt, maybe in flight
-		if (nq == LW) { // a wave without copies has nothing to wait for
-			switch (later) {
-			case 0: wait_vm_lgkm0<0>(); break;
-			case 1: wait_vm_lgkm0<LW>(); break;
-			case 2: wait_vm_lgkm0<2 * LW>(); break;
-			default: wait_vm_lgkm0<3 * LW>(); break;
-			}
-		} else {
-			wait_vm_lgkm0<0>();
+		fread(kt, 1, 1);
+		mm(0);
+		if (kt + 1 < nk) {
+			wait_vm0(); // this wave's copies of stage kt + 1 (the only stage in flight) have landed
+			__builtin_amdgcn_s_barrier(); // ... and every wave's; stage kt - 1 is no longer read
+			if (kt + S - 1 < nk) issue(kt + S - 1); // into the slot of stage kt - 1
+			asm volatile("" ::: "memory");
+			fread(kt + 1, 0, 0);
 		}
-		__builtin_amdgcn_sched_barrier(0);
-		__builtin_amdgcn_s_barrier(); // stage kt is in LDS for every wave; stage kt - 1 is no longer read
-		__builtin_amdgcn_sched_barrier(0);
-		asm volatile("" ::: "memory"); // LDS changed behind the compiler's back: reload it
-		if (kt + S - 1 < nk) issue(kt + S - 1);
-		const uint8_t *A = lds + (kt % S) * STG, *B = A + AST;
-		for (int kk = 0; kk < 2; kk++) {
-			v4i af[3], bf[2];
-			for (int l = 0; l < 3; l++) af[l] = *(const v4i *)(A + (wm * 6 + kk * 3 + l) * 1024 + lane * 16);
-			for (int j = 0; j < 2; j++) {
-				const int cb = wn * 2 + j;
-				if (BITS == 4) {
-					uint2 u = *(const uint2 *)(B + cb * 1024 + kk * 512 + lane * 8);
-					bf[j] = unpack4(u.x, u.y);
-				} else {
-					bf[j] = *(const v4i *)(B + (cb * 2 + kk) * 1024 + lane * 16);
-				}
+		mm(1);
+	}
+	const int r32 = lane & 31, h = lane >> 5;
+	for (int j = 0; j < 4; j++)
+		for (int v = 0; v < 16; v++) // 32 x 32 accumulator: column lane % 32, row 8 (v / 4) + 4 (lane / 32) + v % 4
+			epilogue(a, w, s, m0 + wm * 32 + 8 * (v >> 2) + 4 * h + (v & 3), c0 + wn * 128 + j * 32 + r32,
+				 combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]));
+}
+
+// Small and medium batches. A workgroup of W waves computes a 32 x 32 NB tile
+// (rows x channels); wave w sums the 32-input blocks kb = w, w + W, ..., loading
+// its fragments straight from global memory into registers P blocks ahead
+// (no LDS staging: no fragment is shared between the waves). Lanes of rows at
+// or beyond M load nothing, so a one-row batch fetches one row of digits.
+// The waves' int64 partial sums are added in LDS and wave 0 writes the tile.
+template <int BITS, int NB, int W>
+__global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int gx)
+{
+	constexpr int P = 4;                          // blocks in flight per wave
+	constexpr int LB = BITS == 4 ? 8 : 16;        // weight bytes per lane per block
+	typedef typename std::conditional<BITS == 4, uint2, v4i>::type bfrag;
+	__shared__ long long red[(W > 1 ? W - 1 : 1) * NB * 16 * 64];
+	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int bx = blockIdx.x % gx, by = blockIdx.x / gx;
+	const int m0 = by * 32, c0 = bx * NB * 32, kblocks = w.Kp / 32;
+	const bool rowok = m0 + (lane & 31) < a.M;
+	const int8_t *A = s.dig + (long)(m0 / 32) * kblocks * 3072 + lane * 16;
+	const uint8_t *B = w.w + (long)(c0 / 32) * kblocks * (LB * 64) + lane * LB;
+	v16i acc[3][NB];
+	for (int l = 0; l < 3; l++)
+		for (int j = 0; j < NB; j++)
+			for (int v = 0; v < 16; v++) acc[l][j][v] = 0;
+	v4i af[P][3];
+	bfrag bf[P][NB];
+	const int n = (kblocks - wave + W - 1) / W; // blocks of this wave
+	// block i of this wave into register slot u; past the last block the slot
+	// holds zeros (all-zero operands add nothing), so the loop below has no
+	// early exit and the accumulators stay in place
+	auto load = [&](int u, int i) {
+		const long kb = wave + (long)i * W;
+		const bool live = i < n;
+		for (int l = 0; l < 3; l++) af[u][l] = live && rowok ? *(const v4i *)(A + (kb * 3 + l) * 1024) : v4i{0, 0, 0, 0};
+		for (int j = 0; j < NB; j++) bf[u][j] = live ? *(const bfrag *)(B + ((long)j * kblocks + kb) * (LB * 64)) : bfrag{};
+	};
+	for (int u = 0; u < P; u++) load(u, u);
+	for (int i0 = 0; i0 < n; i0 += P) {
+		for (int u = 0; u < P; u++) {
+			for (int j = 0; j < NB; j++) {
+				v4i wv;
+				if constexpr (BITS == 4) wv = unpack4(bf[u][j].x, bf[u][j].y);
+				else wv = bf[u][j];
+				for (int l = 0; l < 3; l++) acc[l][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[u][l], wv, acc[l][j], 0, 0, 0);
 			}
-			for (int l = 0; l < 3; l++)
-				for (int j = 0; j < 2; j++) acc[l][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[l], bf[j], acc[l][j], 0, 0, 0);
+			load(u, i0 + u + P);
 		}
 	}
-	const long corr = BITS == 4 ? 8 : 0;
+	if (W > 1) {
+		if (wave > 0)
+			for (int j = 0; j < NB; j++)
+				for (int v = 0; v < 16; v++)
+					red[(((wave - 1) * NB + j) * 16 + v) * 64 + lane] = combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+		__syncthreads();
+		if (wave != 0) return;
+	}
 	const int r32 = lane & 31, h = lane >> 5;
-	for (int j = 0; j < 2; j++)
-		for (int v = 0; v < 16; v++) // 32 x 32 accumulator: column lane % 32, row 8 (v / 4) + 4 (lane / 32) + v % 4
-			epilogue(a, w, s, Mp, m0 + wm * 32 + 8 * (v >> 2) + 4 * h + (v & 3), c0 + wn * 64 + j * 32 + r32, acc[0][j][v], acc[1][j][v],
-				 acc[2][j][v], corr);
+	for (int j = 0; j < NB; j++)
+		for (int v = 0; v < 16; v++) {
+			long long tot = combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+			for (int u = 0; u < W - 1; u++) tot += red[((u * NB + j) * 16 + v) * 64 + lane];
+			epilogue(a, w, s, m0 + 8 * (v >> 2) + 4 * h + (v & 3), c0 + j * 32 + r32, tot);
+		}
+}
+
+template <int BITS, int NB, int W>
+void launch_gemv(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
+{
+	const int gx = a->w->Cp / (32 * NB), gy = (int)round_up(a->M, 32) / 32;
+	qgemv_k<BITS, NB, W><<<gx * gy, 64 * W, 0, st>>>(*a, *a->w, s, gx);
+}
+
+template <int BITS>
+void launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
+{
+	const tgk_qweight *w = a->w;
+	const int gx = w->Cp / BN, gy = Mp / BM;
+	if ((long)gx * gy >= 128) { // enough 128 x 256 tiles for the LDS kernel
+		qgemm_k<BITS><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy);
+		return;
+	}
+	// smaller batches: as many 32 x (32 NB) tiles as fill the device
+	const long rt = round_up(a->M, 32) / 32, cb = w->Cp / 32;
+	if (rt * cb / 4 >= 256) launch_gemv<BITS, 4, 4>(st, a, s);
+	else if (rt * cb / 2 >= 256) launch_gemv<BITS, 2, 4>(st, a, s);
+	else launch_gemv<BITS, 1, 8>(st, a, s);
 }
 
 } // namespace
@@ -357,16 +500,16 @@ int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, i
 
 void tgk_qweight_free(tgk_qweight *w)
 {
-	if (w->w) hipFree(w->w);
-	if (w->scale) hipFree(w->scale);
-	if (w->orig) hipFree(w->orig);
+	if (w->w) (void)hipFree(w->w);
+	if (w->scale) (void)hipFree(w->scale);
+	if (w->orig) (void)hipFree(w->orig);
 	memset(w, 0, sizeof *w);
 }
 
 size_t tgk_qgemm_scratch(int M, int Kp)
 {
 	long Mp = round_up(M, BM);
-	return (size_t)Mp * Kp * 3 + (size_t)Mp * sizeof(int) * 5 + 256;
+	return (size_t)Mp * Kp * 3 + (size_t)Mp * (sizeof(long long) + 2 * sizeof(int)) + 256;
 }
 
 void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
@@ -374,7 +517,7 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 	const tgk_qweight *w = a->w;
 	if (!w || !w->w || !a->x || !scratch || a->M <= 0 || a->ni <= 0) return; /* nothing valid to launch */
 	int Mp = (int)round_up(a->M, BM);
-	digits_k<<<Mp, 256, 0, st>>>(*a, carve(scratch, Mp, w->Kp), w->K, w->Kp, a->M);
+	digits_k<<<(a->M + 3) / 4, 256, 0, st>>>(*a, carve(scratch, Mp, w->Kp), w->K, w->Kp, a->M);
 }
 
 void tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
@@ -383,9 +526,8 @@ void tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 	if (!w || !w->w || !w->scale || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return;
 	int Mp = (int)round_up(a->M, BM);
 	Scratch s = carve(scratch, Mp, w->Kp);
-	int gx = w->Cp / BN, gy = Mp / BM;
-	if (w->bits == 8) qgemm_k<8><<<gx * gy, 512, 0, st>>>(*a, *w, s, Mp, gx, gy);
-	else qgemm_k<4><<<gx * gy, 512, 0, st>>>(*a, *w, s, Mp, gx, gy);
+	if (w->bits == 8) launch_gemm<8>(st, a, s, Mp);
+	else launch_gemm<4>(st, a, s, Mp);
 }
 
 void tgk_qgemm(hipStream_t st, const tgk_qgemm_args *a, void *scratch)

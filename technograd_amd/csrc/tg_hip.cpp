@@ -87,7 +87,8 @@ struct tg_hip_prog {
 	tgm_module *m = nullptr;
 	int flags = 0, executor = 0, fixed = 0;
 	int max_rows = 0;
-	hipStream_t st = nullptr;
+	hipStream_t st = nullptr;      // stream every launch goes to
+	hipStream_t own_st = nullptr;  // the program's own stream (st unless tg_hip_set_stream)
 	// pools
 	float *d_pool = nullptr;
 	int *d_imap = nullptr;
@@ -113,6 +114,7 @@ struct tg_hip_prog {
 	// stats
 	tg_hip_stats_t stats{};
 	hipEvent_t ev0 = nullptr, ev1 = nullptr;
+	bool span_open = false; // ev0 marks the first device batch since the last sync
 	std::vector<hipEvent_t> tev;
 };
 
@@ -1005,7 +1007,7 @@ void destroy(tg_hip_prog *p)
 		if (b) hipFree(b);
 	if (p->ev0) hipEventDestroy(p->ev0);
 	if (p->ev1) hipEventDestroy(p->ev1);
-	if (p->st) hipStreamDestroy(p->st);
+	if (p->own_st) (void)hipStreamDestroy(p->own_st);
 	tgm_free(p->m);
 	delete p;
 }
@@ -1081,8 +1083,9 @@ tg_hip_prog *tg_hip_load(const char *tgir, size_t len, int flags, int max_rows)
 	p->max_rows = max_rows > 0 ? max_rows : 4096;
 	p->executor = (p->fixed || (flags & TG_HIP_ROWPROG) || has_think(&m->top)) ? 1 : 0;
 	p->stats.executor = p->executor;
-	bool ok = hipok(hipStreamCreate(&p->st), "hipStreamCreate") && hipok(hipEventCreate(&p->ev0), "event") &&
+	bool ok = hipok(hipStreamCreate(&p->own_st), "hipStreamCreate") && hipok(hipEventCreate(&p->ev0), "event") &&
 		  hipok(hipEventCreate(&p->ev1), "event");
+	p->st = p->own_st;
 	if (ok) ok = p->executor ? build_rowprog(p) : build_layer(p);
 	if (!ok) {
 		destroy(p);
@@ -1129,9 +1132,11 @@ int tg_hip_batch_device(tg_hip_prog *p, const void *d_rows, long nrows, void *d_
 		if (!p->d_steps && !hipok(hipMalloc(&p->d_steps, (size_t)p->max_rows * p->m->nthink * 4), "steps buffer")) return -1;
 		d_steps = p->d_steps;
 	}
-	hipEventRecord(p->ev0, p->st);
+	if (!p->span_open) {
+		(void)hipEventRecord(p->ev0, p->st);
+		p->span_open = true;
+	}
 	int rc = run_pass(p, (const float *)d_rows, (int)nrows, (float *)d_out, d_steps);
-	hipEventRecord(p->ev1, p->st);
 	p->stats.rows = (int)nrows;
 	return rc;
 }
@@ -1139,12 +1144,27 @@ int tg_hip_batch_device(tg_hip_prog *p, const void *d_rows, long nrows, void *d_
 int tg_hip_sync(tg_hip_prog *p)
 {
 	if (!p) return -1;
+	/* the span's end is marked here, not after every call: an event per call
+	   would put a queue barrier between back-to-back batches */
+	if (p->span_open && !hipok(hipEventRecord(p->ev1, p->st), "event")) return -1;
 	if (!hipok(hipStreamSynchronize(p->st), "sync")) return -1;
 	float ms = 0;
-	if (hipEventElapsedTime(&ms, p->ev0, p->ev1) == hipSuccess) p->stats.batch_ms = ms;
+	if (p->span_open && hipEventElapsedTime(&ms, p->ev0, p->ev1) == hipSuccess) p->stats.batch_ms = ms;
+	p->span_open = false;
 	collect_timing(p);
 	return 0;
 }
+
+int tg_hip_set_stream(tg_hip_prog *p, void *stream)
+{
+	if (!p) return -1;
+	if (!hipok(hipStreamSynchronize(p->st), "set_stream")) return -1; /* finish what is queued on the old stream */
+	p->st = stream ? (hipStream_t)stream : p->own_st;
+	p->span_open = false;
+	return 0;
+}
+
+void *tg_hip_get_stream(const tg_hip_prog *p) { return p ? (void *)p->st : nullptr; }
 
 int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, const float *b, int m, int k, int n, int axis, int flags)
 {

@@ -46,6 +46,9 @@ def lib():
         L.tg_hip_error.restype = ctypes.c_char_p
         L.tg_hip_stats.argtypes = [vp, ctypes.POINTER(Stats)]
         L.tg_hip_reset_stats.argtypes = [vp]
+        L.tg_hip_set_stream.argtypes = [vp, vp]
+        L.tg_hip_get_stream.restype = vp
+        L.tg_hip_get_stream.argtypes = [vp]
         L.tg_hip_dev_alloc.restype = vp
         L.tg_hip_dev_alloc.argtypes = [sz]
         L.tg_hip_dev_free.argtypes = [vp]
@@ -148,6 +151,16 @@ class Program:
 
     def reset_stats(self):
         _check(lib().tg_hip_reset_stats(self.h), "tg_hip_reset_stats")
+
+    def stream(self):
+        """The hipStream_t (as an int) this program launches on."""
+        return lib().tg_hip_get_stream(self.h)
+
+    def set_stream(self, stream):
+        """Launch on another hipStream_t (an int handle, e.g. another
+        program's stream() or torch.cuda.current_stream().cuda_stream);
+        None restores the program's own stream."""
+        _check(lib().tg_hip_set_stream(self.h, stream), "tg_hip_set_stream")
 
 
 def matmul_q(q, bits, s, b, m, k, n, axis, flags=0):
