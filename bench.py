@@ -12,12 +12,17 @@ roofline: the dominant kernel is the int8-MFMA GEMM at batch 4096; its
 average duration comes from HIP events on the backend's stream (a separate
 program built with TG_HIP_TIMING), and achieved = 2*4096^3 algorithmic int8
 ops (one multiply-add = 2 ops, counted once whatever the limb count) /
-duration, against 5000 TOP/s dense int8. The "sweep" field repeats this per
-batch. Every timed call there follows a pass, on the same stream, that
-streams 1 GiB through HBM, so neither the 8 MiB weight nor the rows can be
-served from the 256 MB Infinity Cache, and the device is never idle while
-the host queues the next call (HIP events then time kernels, not launch
-latency).
+duration, against 5000 TOP/s dense int8. traffic = HBM bytes per launch of
+that kernel from two rocprofv3 --pmc runs of this script's --profile-child
+mode (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
+counter reads for the 1 GiB flush pass (512 MiB read + 512 MiB written, an
+elementwise kernel of known traffic) in the same run.
+
+The "sweep" field repeats the kernel timings per batch. Every timed call
+there follows a pass, on the same stream, that streams 1 GiB through HBM, so
+neither the 8 MiB weight nor the rows can be served from the 256 MB Infinity
+Cache, and the device is never idle while the host queues the next call (HIP
+events then time kernels, not launch latency).
 
 cpu_baseline: the reference's own interpreter (oracle/_ref/tgc_ref, compiled
 from the reference sources) on this host's cores over a sample of rows of the
@@ -25,8 +30,11 @@ same layer; falls back to the oracle restatement when the reference build is
 absent.
 """
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
 import subprocess
 import sys
 import tempfile
@@ -41,6 +49,7 @@ C = 4096
 METRIC = "quantized rows/sec via tgc batch at 1 GPU; % of HBM / int8-MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 MFMA_I8_PEAK_TOPS = 5000.0
+FLUSH_ROWS, FLUSH_COLS = 2048, 65536  # the flush pass: x * c over 512 MiB in, 512 MiB out
 
 
 def log(msg):
@@ -49,11 +58,11 @@ def log(msg):
 
 def flush_program(hip):
     """x * 2 over 2048 rows of 64 Ki floats: 512 MiB read + 512 MiB written."""
-    text = ("(tgir 1\n  (model flush)\n  (param c (f32)\n    (data 2))\n  (input x (f32 65536))\n  (block\n"
-            "    (%0 (f32 65536) (mul x c))\n  )\n  (output %0))\n")
-    p = hip.Program(text, max_rows=2048)
-    buf_in = hip.DeviceBuffer(2048 * 65536 * 4)
-    buf_out = hip.DeviceBuffer(2048 * 65536 * 4)
+    text = ("(tgir 1\n  (model flush)\n  (param c (f32)\n    (data 2))\n  (input x (f32 %d))\n  (block\n"
+            "    (%%0 (f32 %d) (mul x c))\n  )\n  (output %%0))\n" % (FLUSH_COLS, FLUSH_COLS))
+    p = hip.Program(text, max_rows=FLUSH_ROWS)
+    buf_in = hip.DeviceBuffer(FLUSH_ROWS * FLUSH_COLS * 4)
+    buf_out = hip.DeviceBuffer(FLUSH_ROWS * FLUSH_COLS * 4)
     return p, buf_in, buf_out
 
 
@@ -73,9 +82,86 @@ def cpu_baseline(text, X, sample_rows, threads):
         m.batch(x, threads=threads)
         ms = (time.perf_counter() - t0) * 1e3
         kind = "port"
+    shutil.rmtree(tmp, ignore_errors=True)
     return {"value": sample_rows / (ms / 1e3), "unit": "rows/s", "cores": threads, "kind": kind,
             "sample": "%d rows of config 2 (int4 4096x4096) through the %s interpreter, -j %d, compute time only" % (
                 sample_rows, "reference's" if kind == "reference" else "oracle's", threads)}
+
+
+def setup(synth):
+    W = synth.config2_weight()
+    text = synth.linear_tgir("linear4096", W, 4)
+    X = synth.normal(2, 1.0, 4096 * K).reshape(4096, K)
+    return text, X
+
+
+def profile_child():
+    """What the traffic runs profile: two cold B = 4096 calls, each after a
+    flush pass, on one stream."""
+    from technograd_amd import hip, synth
+    hip.init(0)
+    text, X = setup(synth)
+    prog = hip.Program(text, max_rows=4096)
+    d_x = hip.DeviceBuffer.from_array(X)
+    d_y = hip.DeviceBuffer(4096 * C * 4)
+    fprog, fin, fout = flush_program(hip)
+    fprog.set_stream(prog.stream())
+    for _ in range(2):
+        fprog.batch_device(fin.ptr, FLUSH_ROWS, fout.ptr)
+        prog.batch_device(d_x.ptr, 4096, d_y.ptr)
+    prog.sync()
+
+
+def pmc_run(counter, outdir):
+    """Per-kernel average of one counter (KiB per dispatch) over a profiled
+    --profile-child run: {'qgemm': v, 'flush': v}, or None."""
+    d = os.path.join(outdir, counter)
+    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
+           sys.executable, os.path.abspath(__file__), "--profile-child"]
+    env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=150, env=env, cwd=ROOT)
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if r.returncode != 0 and not files:
+        log("rocprofv3 --pmc %s failed (rc %d): %s" % (counter, r.returncode, r.stdout.decode(errors="replace")[-400:]))
+        return None
+    vals = {"qgemm": [], "flush": []}
+    for f in files:
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row["Kernel_Name"]
+                if "qgemm_k<4>" in name:
+                    vals["qgemm"].append(float(row["Counter_Value"]))
+                elif "binary_k" in name and int(row.get("Grid_Size", 0) or 0) >= FLUSH_ROWS * FLUSH_COLS // 4:
+                    vals["flush"].append(float(row["Counter_Value"]))
+    if not vals["qgemm"] or not vals["flush"]:
+        log("rocprofv3 --pmc %s: kernels not found in %s" % (counter, files))
+        return None
+    return {k: sum(v) / len(v) for k, v in vals.items()}
+
+
+def measure_traffic(alg_bytes):
+    """HBM bytes per launch of the B = 4096 GEMM (calibrated FETCH_SIZE + WRITE_SIZE)."""
+    if not shutil.which("rocprofv3"):
+        return None, "rocprofv3 not found"
+    out = tempfile.mkdtemp(prefix="tgpmc")
+    try:
+        f = pmc_run("FETCH_SIZE", out)
+        w = pmc_run("WRITE_SIZE", out) if f else None
+    except subprocess.TimeoutExpired:
+        return None, "rocprofv3 timed out"
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+    if not f or not w:
+        return None, "rocprofv3 --pmc gave no data"
+    half = FLUSH_ROWS * FLUSH_COLS * 4  # bytes read (and written) by one flush pass
+    rf = half / (f["flush"] * 1024.0)
+    rw = half / (w["flush"] * 1024.0)
+    traffic = f["qgemm"] * 1024.0 * rf + w["qgemm"] * 1024.0 * rw
+    note = ("FETCH_SIZE %.0f KiB x %.4f + WRITE_SIZE %.0f KiB x %.4f per dispatch (factors: 512 MiB / the flush "
+            "pass's reading); algorithmic %.1f MB" % (f["qgemm"], rf, w["qgemm"], rw, alg_bytes / 1e6))
+    return traffic, note
 
 
 def main():
@@ -86,8 +172,13 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=96)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
     ap.add_argument("--reps", type=int, default=10, help="kernel-timing repetitions per batch")
+    ap.add_argument("--profile-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.profile_child:
+        profile_child()
+        return
     if args.gpus != 1:
         print("bench.py: this backend runs on one GPU per process and this build measures one GPU only; "
               "rows shard across GPUs with no collective (see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
@@ -98,9 +189,7 @@ def main():
 
     hip.init(0)
     log("building config 2 (int4 4096x4096)")
-    W = synth.config2_weight()
-    text = synth.linear_tgir("linear4096", W, 4)
-    X = synth.normal(2, 1.0, 4096 * K).reshape(4096, K)
+    text, X = setup(synth)
     log("loading programs")
     prog = hip.Program(text, max_rows=4096)
     tprog = hip.Program(text, flags=hip.TIMING, max_rows=4096)
@@ -134,7 +223,7 @@ def main():
         tprog.sync()
         tprog.reset_stats()
         for _ in range(args.reps):
-            fprog.batch_device(fin.ptr, 2048, fout.ptr)
+            fprog.batch_device(fin.ptr, FLUSH_ROWS, fout.ptr)
             tprog.batch_device(d_x.ptr, b, d_y.ptr)
         tprog.sync()
         st = tprog.stats()
@@ -153,8 +242,25 @@ def main():
         })
         log("batch %4d: mfma %.2f us, digits %.2f us" % (b, mfma_us, dig_us))
     big = sweep[-1]
+    fprog.set_stream(None)
+
+    # ---- host buffers (PCIe included): reported beside value, never as value ----
+    xh = np.ascontiguousarray(X, np.float32)
+    prog.batch(xh)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        prog.batch(xh)
+    pcie_rps = 3 * 4096 / (time.perf_counter() - t0)
+    log("host-buffer batch 4096: %.0f rows/s (PCIe in and out included)" % pcie_rps)
+
+    traffic, tnote = None, "skipped (--no-traffic)"
+    if not args.no_traffic:
+        log("traffic: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
+        traffic, tnote = measure_traffic(big["alg_bytes"])
+        log("traffic: %s" % tnote)
     roofline = {"bound": "mfma", "achieved": big["mfma_TOPs"], "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
-                "frac": big["mfma_frac"], "traffic": None,
+                "frac": big["mfma_frac"], "traffic": None if traffic is None else round(traffic),
+                "traffic_note": tnote,
                 "kernel": "qgemm_k<4> (int8 MFMA, 3 activation digits) at batch 4096",
                 "alg_ops_per_launch": big["alg_ops"], "avg_kernel_us": big["mfma_kernel_us"]}
 
@@ -171,6 +277,8 @@ def main():
         "config": {"workload": "config 2: int4 4096x4096 linear, one pass at each batch of {1,16,256,4096} rows per step",
                    "rows_per_step": rows_per_step, "parallelism": "1 GPU"},
         "roofline": roofline, "cpu_baseline": cpu, "sweep": sweep,
+        "pcie_inclusive": {"rows_per_s": round(pcie_rps, 1), "batch": 4096,
+                           "note": "tg_hip_batch with host buffers: 64 MiB in and 64 MiB out over PCIe per call"},
     }
     print(json.dumps(out), flush=True)
 
