@@ -372,7 +372,6 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int bx = blockIdx.x % gx, by = blockIdx.x / gx;
 	const int m0 = by * 32, c0 = bx * NB * 32, kblocks = w.Kp / 32;
-	const bool rowok = m0 + (lane & 31) < a.M;
 	const int8_t *A = s.dig + (long)(m0 / 32) * kblocks * 3072 + lane * 16;
 	const uint8_t *B = w.w + (long)(c0 / 32) * kblocks * (LB * 64) + lane * LB;
 	v16i acc[3][NB];
@@ -382,23 +381,29 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 	v4i af[P][3];
 	bfrag bf[P][NB];
 	const int n = (kblocks - wave + W - 1) / W; // blocks of this wave
-	// block i of this wave into register slot u; past the last block the slot
-	// holds zeros (all-zero operands add nothing), so the loop below has no
-	// early exit and the accumulators stay in place
+	// block i of this wave into register slot u. Loads are unconditional (the
+	// block index is clamped into the matrix) and a slot past the wave's last
+	// block is simply not multiplied: a branch around a load, or a select on
+	// its value, would make the compiler wait for every load in flight where
+	// the branches join. Rows at or beyond M need no masking: they only feed
+	// their own outputs, which are not written, and lie in the scratch, which
+	// is padded to 128 rows.
 	auto load = [&](int u, int i) {
-		const long kb = wave + (long)i * W;
-		const bool live = i < n;
-		for (int l = 0; l < 3; l++) af[u][l] = live && rowok ? *(const v4i *)(A + (kb * 3 + l) * 1024) : v4i{0, 0, 0, 0};
-		for (int j = 0; j < NB; j++) bf[u][j] = live ? *(const bfrag *)(B + ((long)j * kblocks + kb) * (LB * 64)) : bfrag{};
+		long kb = wave + (long)i * W;
+		kb = kb < kblocks ? kb : kblocks - 1;
+		for (int l = 0; l < 3; l++) af[u][l] = *(const v4i *)(A + (kb * 3 + l) * 1024);
+		for (int j = 0; j < NB; j++) bf[u][j] = *(const bfrag *)(B + ((long)j * kblocks + kb) * (LB * 64));
 	};
 	for (int u = 0; u < P; u++) load(u, u);
 	for (int i0 = 0; i0 < n; i0 += P) {
 		for (int u = 0; u < P; u++) {
-			for (int j = 0; j < NB; j++) {
-				v4i wv;
-				if constexpr (BITS == 4) wv = unpack4(bf[u][j].x, bf[u][j].y);
-				else wv = bf[u][j];
-				for (int l = 0; l < 3; l++) acc[l][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[u][l], wv, acc[l][j], 0, 0, 0);
+			if (i0 + u < n) {
+				for (int j = 0; j < NB; j++) {
+					v4i wv;
+					if constexpr (BITS == 4) wv = unpack4(bf[u][j].x, bf[u][j].y);
+					else wv = bf[u][j];
+					for (int l = 0; l < 3; l++) acc[l][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[u][l], wv, acc[l][j], 0, 0, 0);
+				}
 			}
 			load(u, i0 + u + P);
 		}
