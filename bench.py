@@ -164,6 +164,130 @@ def measure_traffic(alg_bytes):
     return traffic, note
 
 
+def ref_cpu(text, rows, per, nout, nthink, threads, fixed, what):
+    """The reference interpreter (or the oracle restatement) over `rows`."""
+    from oracle import oracle as O
+    tmp = tempfile.mkdtemp(prefix="tgbench")
+    try:
+        if O.have_ref():
+            mpath = os.path.join(tmp, "model.tgir")
+            with open(mpath, "w") as f:
+                f.write(text)
+            _, _, ms = O.ref_batch(mpath, rows, per, nout, nthink, tmp, threads=threads, fixed=fixed)
+            kind = "reference"
+        else:
+            m = O.Model(text)
+            t0 = time.perf_counter()
+            (m.batch_fixed if fixed else m.batch)(rows, threads=threads)
+            ms = (time.perf_counter() - t0) * 1e3
+            kind = "port"
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return {"value": len(rows) / (ms / 1e3), "unit": "rows/s", "cores": threads, "kind": kind,
+            "sample": "%d rows of %s through the %s interpreter, -j %d, compute time only" % (
+                len(rows), what, "reference's" if kind == "reference" else "oracle's", threads)}
+
+
+def bench_config1(args):
+    """Config 1: int8 MLP 512 -> 2048 -> 2048 -> 512 (tanh, tanh, rmsnorm), 65,536
+    rows in one device pass. roofline: the three quantized GEMMs, 12.58 M
+    algorithmic ops per row, against 5000 TOP/s dense int8."""
+    import numpy as np
+    from technograd_amd import hip, synth
+    rows = 65536
+    hip.init(0)
+    log("building config 1 (int8 MLP, %d rows)" % rows)
+    text, X = synth.config1(rows)
+    prog = hip.Program(text, max_rows=rows)
+    tprog = hip.Program(text, flags=hip.TIMING, max_rows=rows)
+    d_x = hip.DeviceBuffer.from_array(X)
+    d_y = hip.DeviceBuffer(rows * 512 * 4)
+    for _ in range(args.warmup):
+        prog.batch_device(d_x.ptr, rows, d_y.ptr)
+    prog.sync()
+    steps = max(1, min(args.steps, 10))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        prog.batch_device(d_x.ptr, rows, d_y.ptr)
+    prog.sync()
+    elapsed = time.perf_counter() - t0
+    y = d_y.to_array(np.float32, (rows, 512))
+    assert np.isfinite(y).all()
+    tprog.batch_device(d_x.ptr, rows, d_y.ptr)
+    tprog.sync()
+    tprog.reset_stats()
+    for _ in range(3):
+        tprog.batch_device(d_x.ptr, rows, d_y.ptr)
+    tprog.sync()
+    st = tprog.stats()
+    mfma_us, dig_us, oth_us = (v / 3 * 1e3 for v in (st.qgemm_ms, st.digits_ms, st.other_ms))
+    ops = 2.0 * (2048 * 512 + 2048 * 2048 + 512 * 2048) * rows
+    log("config 1: %.1f ms per pass: GEMMs %.0f us, digits %.0f us, other %.0f us" % (
+        elapsed / steps * 1e3, mfma_us, dig_us, oth_us))
+    cpu = None if args.no_cpu else ref_cpu(text, X[:2048], 512, 512, 0, args.cpu_threads, False,
+                                           "config 1 (int8 MLP 512-2048-2048-512)")
+    out = {
+        "metric": "config 1 int8 MLP rows/sec at 1 GPU; % of int8-MFMA roofline", "value": round(rows * steps / elapsed, 1),
+        "unit": "rows/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed / steps * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic (rand(1, 0.05) weights quantized int8 RTN, N(0,1) rows seed 0)",
+        "config": {"workload": "config 1: int8 MLP 512-2048-2048-512, tanh, rmsnorm; 65,536 rows per step"},
+        "roofline": {"bound": "mfma", "achieved": round(ops / mfma_us / 1e6, 2), "peak": MFMA_I8_PEAK_TOPS,
+                     "unit": "TOP/s", "frac": round(ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "the three quantized GEMMs of a pass (qgemm_k<8>), summed",
+                     "alg_ops_per_launch": ops, "avg_kernel_us": round(mfma_us, 1)},
+        "cpu_baseline": cpu,
+        "breakdown_us": {"gemm": round(mfma_us, 1), "digits": round(dig_us, 1), "other": round(oth_us, 1)},
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_config4(args):
+    """Config 4: the Q16.16 latent reasoner (think <= 32 steps, halting at
+    d <= 7) over 1,048,576 rows of {0, 1}^8, one device pass. Integer VALU
+    work; the HBM fraction is reported for completeness."""
+    import numpy as np
+    from technograd_amd import hip, synth
+    rows = 1048576
+    hip.init(0)
+    log("building config 4 (Q16.16 latent reasoner, %d rows)" % rows)
+    text = synth.latent_reasoner_tgir()
+    X = synth.config4_rows(rows)
+    xq = (X * 65536.0).astype(np.int32)  # inputs are 0 or 1: exact in Q16.16
+    prog = hip.Program(text, flags=hip.FIXED, max_rows=rows)
+    d_x = hip.DeviceBuffer.from_array(xq)
+    d_y = hip.DeviceBuffer(rows * 4 * 4)
+    d_s = hip.DeviceBuffer(rows * 4)
+    for _ in range(args.warmup):
+        prog.batch_device(d_x.ptr, rows, d_y.ptr, d_s.ptr)
+    prog.sync()
+    steps = max(1, min(args.steps, 10))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        prog.batch_device(d_x.ptr, rows, d_y.ptr, d_s.ptr)
+    prog.sync()
+    elapsed = time.perf_counter() - t0
+    st = d_s.to_array(np.int32, (rows,))
+    byts = rows * (8 * 4 + 4 * 4 + 4)
+    t = elapsed / steps
+    log("config 4: %.2f ms per pass, mean think steps %.2f" % (t * 1e3, st.mean()))
+    cpu = None if args.no_cpu else ref_cpu(text, xq[:65536], 8, 4, 1, args.cpu_threads, True,
+                                           "config 4 (Q16.16 latent reasoner)")
+    out = {
+        "metric": "config 4 Q16.16 latent reasoner rows/sec at 1 GPU", "value": round(rows / t, 1), "unit": "rows/s",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q16.16 (int32)",
+        "data": "synthetic (rows uniform in {0,1}^8, seed 4)",
+        "config": {"workload": "config 4: latent reasoner, think <= 32 steps, 1,048,576 rows per step",
+                   "mean_think_steps": round(float(st.mean()), 3)},
+        "roofline": {"bound": "hbm", "achieved": round(byts / t / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(byts / t / 1e9 / HBM_PEAK_GBS, 5), "traffic": None,
+                     "kernel": "rowprog_k<true> (one lane per row, integer VALU bound; HBM shown for completeness)"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -174,10 +298,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
     ap.add_argument("--reps", type=int, default=10, help="kernel-timing repetitions per batch")
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 4),
+                    help="BASELINE configuration: 2 (default, the headline metric), 1 (int8 MLP), 4 (Q16.16 reasoner)")
     ap.add_argument("--profile-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.profile_child:
         profile_child()
+        return
+    if args.config != 2 and args.gpus == 1:
+        {1: bench_config1, 4: bench_config4}[args.config](args)
         return
     if args.gpus != 1:
         print("bench.py: this backend runs on one GPU per process and this build measures one GPU only; "
