@@ -249,3 +249,109 @@ def latent_reasoner_tgir():
 
 def config4_rows(rows=1048576):
     return bits01(4, rows * 8).reshape(rows, 8)
+
+
+def ssm_tgir(name="ssm", d_model=256, d_inner=512, n_state=16, dt_rank=16, T=512, blocks=4, classes=8, bits=8,
+             seed=105):
+    """Config 5's model: a Mamba-1-style selective-SSM sequence classifier.
+
+    The reference has no builtin SSM block; this is the block (one sequence
+    of T steps, rows of the tensors are time steps):
+        xi = x @ Wx, z = x @ Wz                      (d_model -> d_inner each)
+        u  = silu(xi)
+        dt = softplus((u @ Wdtin) @ Wdt + bdt)       (d_inner -> dt_rank -> d_inner)
+        B  = u @ WB, C = u @ WC                      (d_inner -> n_state)
+        scan over t, carry h[d_inner, n_state] = 0:
+            h   = exp(dt_t[:, None] * A) * h + outer(dt_t * u_t, B_t)
+            y_t = h @ C_t
+        y  = (y + u * D) * silu(z)
+        x' = rmsnorm(x + y @ Wo)                     (d_inner -> d_model)
+    and the head: p = mean over t of x (a matmul with a 1/T vector),
+    softmax(p @ Whead). A = -(1 .. n_state) per channel (A_log = log n), D = 1,
+    bdt = softplus^-1(0.01). Every matmul weight is N(0, 0.02), drawn in
+    order from one normal(seed) stream, and quantized per output channel on
+    axis 1 (x @ W, as tgc quantize writes x @ W params)."""
+    shapes = []
+    for b in range(blocks):
+        shapes += [("Wx%d" % b, (d_model, d_inner)), ("Wz%d" % b, (d_model, d_inner)),
+                   ("Wdtin%d" % b, (d_inner, dt_rank)), ("Wdt%d" % b, (dt_rank, d_inner)),
+                   ("WB%d" % b, (d_inner, n_state)), ("WC%d" % b, (d_inner, n_state)), ("Wo%d" % b, (d_inner, d_model))]
+    shapes.append(("Whead", (d_model, classes)))
+    total = sum(r * c for _, (r, c) in shapes)
+    stream = normal(seed, 0.02, total)
+    parts = ["(tgir 1\n  (model %s)\n" % name]
+    off = 0
+    for nm, (r, c) in shapes:
+        w = stream[off:off + r * c].reshape(r, c)
+        off += r * c
+        if bits:
+            codes, sc = quantize_rtn(w, bits, 1)
+            parts.append(param_quant(nm, codes, sc, bits, 1))
+        else:
+            parts.append(param_f32(nm, w))
+    A = -np.tile(np.arange(1, n_state + 1, dtype=np.float32), (d_inner, 1))
+    parts.append(param_f32("A", A))
+    parts.append(param_f32("D", np.ones(d_inner, np.float32)))
+    parts.append(param_f32("bdt", np.full(d_inner, np.log(np.expm1(0.01)), np.float32)))
+    parts.append(param_f32("h0", np.zeros((d_inner, n_state), np.float32)))
+    parts.append(param_f32("pool", np.full(T, 1.0 / T, np.float32)))
+    parts.append("  (input x (f32 %d %d))\n  (block\n" % (T, d_model))
+    v = [0]
+
+    def new():
+        v[0] += 1
+        return "%%%d" % v[0]
+
+    lines = []
+
+    def op(shape, expr):
+        r = new()
+        lines.append("    (%s (f32 %s) %s)\n" % (r, " ".join(str(d) for d in shape), expr))
+        return r
+
+    x = "x"
+    for b in range(blocks):
+        xi = op((T, d_inner), "(matmul %s Wx%d)" % (x, b))
+        z = op((T, d_inner), "(matmul %s Wz%d)" % (x, b))
+        u = op((T, d_inner), "(silu %s)" % xi)
+        dtl = op((T, dt_rank), "(matmul %s Wdtin%d)" % (u, b))
+        dtp = op((T, d_inner), "(matmul %s Wdt%d)" % (dtl, b))
+        dta = op((T, d_inner), "(add %s bdt)" % dtp)
+        dt = op((T, d_inner), "(softplus %s)" % dta)
+        Bm = op((T, n_state), "(matmul %s WB%d)" % (u, b))
+        Cm = op((T, n_state), "(matmul %s WC%d)" % (u, b))
+        du = op((T, d_inner), "(mul %s %s)" % (dt, u))
+        h, dtt, dut, bt, ct = new(), new(), new(), new(), new()
+        dtc, da0, da, ha, dbu, hn, yt, ys = (new() for _ in range(8))
+        lines.append("    (scan %d forward\n" % T)
+        lines.append("      (carry %s (f32 %d %d) h0)\n" % (h, d_inner, n_state))
+        lines.append("      (in %s (f32 %d) %s)\n      (in %s (f32 %d) %s)\n" % (dtt, d_inner, dt, dut, d_inner, du))
+        lines.append("      (in %s (f32 %d) %s)\n      (in %s (f32 %d) %s)\n" % (bt, n_state, Bm, ct, n_state, Cm))
+        lines.append("      (body\n")
+        lines.append("        (%s (f32 %d 1) (reshape %s))\n" % (dtc, d_inner, dtt))
+        lines.append("        (%s (f32 %d %d) (mul %s A))\n" % (da0, d_inner, n_state, dtc))
+        lines.append("        (%s (f32 %d %d) (exp %s))\n" % (da, d_inner, n_state, da0))
+        lines.append("        (%s (f32 %d %d) (mul %s %s))\n" % (ha, d_inner, n_state, da, h))
+        lines.append("        (%s (f32 %d %d) (outer %s %s))\n" % (dbu, d_inner, n_state, dut, bt))
+        lines.append("        (%s (f32 %d %d) (add %s %s))\n" % (hn, d_inner, n_state, ha, dbu))
+        lines.append("        (%s (f32 %d) (matmul %s %s))\n" % (yt, d_inner, hn, ct))
+        lines.append("      )\n      (next %s %s)\n      (emit %s (f32 %d %d) %s)\n    )\n" % (h, hn, ys, T, d_inner, yt))
+        yd = op((T, d_inner), "(mul %s D)" % u)
+        y1 = op((T, d_inner), "(add %s %s)" % (ys, yd))
+        sz = op((T, d_inner), "(silu %s)" % z)
+        y2 = op((T, d_inner), "(mul %s %s)" % (y1, sz))
+        o = op((T, d_model), "(matmul %s Wo%d)" % (y2, b))
+        r = op((T, d_model), "(add %s %s)" % (x, o))
+        x = op((T, d_model), "(rmsnorm %s)" % r)
+    xt = op((d_model, T), "(transpose %s)" % x)
+    p = op((d_model,), "(matmul %s pool)" % xt)
+    lg = op((classes,), "(matmul %s Whead)" % p)
+    out = op((classes,), "(softmax %s)" % lg)
+    parts.extend(lines)
+    parts.append("  )\n  (output %s))\n" % out)
+    return "".join(parts)
+
+
+def config5_rows(rows=4096, T=512, d_model=256, seed=5):
+    """Config 5 inputs: rows sequences of T steps of f32[d_model] ~ N(0, 1)."""
+    return normal(seed, 1.0, rows * T * d_model).reshape(rows, T * d_model)

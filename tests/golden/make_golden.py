@@ -10,8 +10,11 @@ reference's own code:
   3. runs it over seeded rows                       (tgc_ref batch    -> src/vm.c, src/par.c;
                                                      --fixed          -> runtime/tg_rtq.h)
 and the results are stored as data: <name>.tgir (model text) and <name>.npz
-(inputs, f32 outputs, Q16.16 inputs/outputs, steps). Run:
-    python tests/golden/make_golden.py
+(inputs, f32 outputs, Q16.16 inputs/outputs, steps). Models in SYNTH are
+written as TGIR by this repository's builders (technograd_amd/synth.py) and
+then put through the same three reference steps (`ir` canonicalizes them).
+Run (all variants, or the named ones):
+    python tests/golden/make_golden.py [NAME ...]
 """
 import itertools
 import os
@@ -47,6 +50,18 @@ VARIANTS = {
     "opsmix_f32": ("opsmix", None, True),
 }
 
+# name: builder of TGIR text (already quantized where the builder quantizes)
+def _synth():
+    from technograd_amd import synth
+    return {
+        # config 5's block at reduced sizes (two blocks, every op of the full model)
+        "ssm5_tiny": lambda: synth.ssm_tgir("ssm5_tiny", d_model=16, d_inner=32, n_state=4, dt_rank=4, T=6, blocks=2,
+                                            classes=3),
+        "ssm5_small": lambda: synth.ssm_tgir("ssm5_small", d_model=64, d_inner=128, n_state=16, dt_rank=8, T=24,
+                                             blocks=2, classes=8),
+    }
+
+
 def rows_for(name, per, seed):
     rng = np.random.default_rng(seed)
     if name.startswith("latent"):
@@ -68,12 +83,30 @@ def main():
     if not O.have_ref():
         sys.exit("oracle/_ref/tgc_ref is missing: run make -C oracle ref")
     tmp = tempfile.mkdtemp()
+    only = set(sys.argv[1:])
+    for i, (name, build) in enumerate(sorted(_synth().items())):
+        if only and name not in only:
+            continue
+        spath = os.path.join(tmp, name + ".src.tgir")
+        with open(spath, "w") as fh:
+            fh.write(build())
+        text = O.ref_ir(spath)  # the reference's canonical form of the model
+        with open(os.path.join(HERE, name + ".tgir"), "w") as fh:
+            fh.write(text)
+        mpath = os.path.join(HERE, name + ".tgir")
+        m = O.Model(text)
+        x = rows_for(name, m.per, 2000 + i)
+        y, st, _ = O.ref_batch(mpath, x, m.per, m.nout, m.nthink, tmp, threads=4)
+        np.savez_compressed(os.path.join(HERE, name + ".npz"), x=x, y=y, steps=st)
+        print("%-16s rows %4d per %4d out %4d (synth)" % (name, x.shape[0], m.per, m.nout))
     lowered = {}
     for f in sorted(os.listdir(MODELS)):
         if f.endswith(".tg"):
             base = f[:-3]
             lowered[base] = O.ref_ir(os.path.join(MODELS, f))
     for i, (name, (src, qargs, fixed)) in enumerate(sorted(VARIANTS.items())):
+        if only and name not in only:
+            continue
         f32_path = os.path.join(tmp, src + ".tgir")
         with open(f32_path, "w") as fh:
             fh.write(lowered[src])
