@@ -288,6 +288,73 @@ def bench_config4(args):
     print(json.dumps(out), flush=True)
 
 
+def bench_config5(args):
+    """Config 5: int8 selective-SSM classifier (4 blocks, d_model 256, state 16,
+    expand 2, T = 512) over 4096 sequences in device passes of `pass_rows`
+    sequences. roofline: the int8 projections, 2 x 426 K MACs per step per
+    block, against 5000 TOP/s (the f32 scan runs on the VALU)."""
+    import numpy as np
+    from technograd_amd import hip, synth
+    rows, T, dm = 4096, 512, 256
+    per = T * dm
+    hip.init(0)
+    log("building config 5 (selective SSM, %d sequences of %d x %d)" % (rows, T, dm))
+    text = synth.ssm_tgir("ssm")
+    X = synth.config5_rows(rows, T, dm)
+    probe = hip.Program(text, max_rows=8)
+    arena_row = probe.stats().arena_bytes / 8
+    probe.close()
+    pass_rows = int(max(8, min(512, (24 << 30) // max(arena_row, 1))))
+    pass_rows = 1 << (pass_rows.bit_length() - 1)
+    log("config 5: %.1f MiB of arena per sequence, passes of %d sequences" % (arena_row / 2**20, pass_rows))
+    prog = hip.Program(text, max_rows=pass_rows)
+    tprog = hip.Program(text, flags=hip.TIMING, max_rows=pass_rows)
+    d_x = hip.DeviceBuffer.from_array(X)
+    d_y = hip.DeviceBuffer(rows * 8 * 4)
+
+    def run(p):
+        for r0 in range(0, rows, pass_rows):
+            n = min(pass_rows, rows - r0)
+            p.batch_device(d_x.ptr + r0 * per * 4, n, d_y.ptr + r0 * 8 * 4)
+
+    run(prog)
+    prog.sync()
+    steps = max(1, min(args.steps, 3))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run(prog)
+    prog.sync()
+    t = (time.perf_counter() - t0) / steps
+    y = d_y.to_array(np.float32, (rows, 8))
+    assert np.isfinite(y).all()
+    tprog.reset_stats()
+    tprog.batch_device(d_x.ptr, pass_rows, d_y.ptr)
+    tprog.sync()
+    st = tprog.stats()
+    scale = rows / pass_rows
+    mfma_us, dig_us, oth_us = (v * scale * 1e3 for v in (st.qgemm_ms, st.digits_ms, st.other_ms))
+    macs = 4 * T * (2 * dm * 512 + 3 * 512 * 16 + 16 * 512 + 512 * dm) + dm * 8
+    ops = 2.0 * macs * rows
+    log("config 5: %.1f ms per 4096 sequences: projections %.0f us, digits %.0f us, other (scan, elementwise) %.0f us"
+        % (t * 1e3, mfma_us, dig_us, oth_us))
+    cpu = None if args.no_cpu else ref_cpu(text, X[:32], per, 8, 0, args.cpu_threads, False,
+                                           "config 5 (selective SSM, 4 blocks, T 512)")
+    out = {
+        "metric": "config 5 selective-SSM sequences/sec at 1 GPU", "value": round(rows / t, 1), "unit": "sequences/s",
+        "n_gpus": 1, "steps": steps, "warmup": 1, "ms_per_step": round(t * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8 projections, f32 scan",
+        "data": "synthetic (N(0,0.02) weights seed 105 quantized int8 per channel, N(0,1) inputs seed 5)",
+        "config": {"workload": "config 5: 4 Mamba-style blocks d_model 256, state 16, expand 2, T 512; 4096 sequences "
+                               "per step", "pass_rows": pass_rows},
+        "roofline": {"bound": "mfma", "achieved": round(ops / mfma_us / 1e6, 2), "peak": MFMA_I8_PEAK_TOPS,
+                     "unit": "TOP/s", "frac": round(ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "the quantized projections of a pass, summed (the scan is f32 VALU work)"},
+        "cpu_baseline": cpu,
+        "breakdown_us": {"projections": round(mfma_us, 1), "digits": round(dig_us, 1), "other": round(oth_us, 1)},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -298,15 +365,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
     ap.add_argument("--reps", type=int, default=10, help="kernel-timing repetitions per batch")
-    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 4),
-                    help="BASELINE configuration: 2 (default, the headline metric), 1 (int8 MLP), 4 (Q16.16 reasoner)")
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 4, 5),
+                    help="BASELINE configuration: 2 (default, the headline metric), 1 (int8 MLP), 4 (Q16.16 "
+                         "reasoner), 5 (selective-SSM classifier)")
     ap.add_argument("--profile-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.profile_child:
         profile_child()
         return
     if args.config != 2 and args.gpus == 1:
-        {1: bench_config1, 4: bench_config4}[args.config](args)
+        {1: bench_config1, 4: bench_config4, 5: bench_config5}[args.config](args)
         return
     if args.gpus != 1:
         print("bench.py: this backend runs on one GPU per process and this build measures one GPU only; "

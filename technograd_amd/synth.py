@@ -47,9 +47,63 @@ def _powers():
     return _POW
 
 
+def _apply(cols, v):
+    """GF(2) matrix (32 columns, uint32) times state(s) v."""
+    v = np.asarray(v, np.uint32)
+    acc = np.zeros(v.shape, np.uint32)
+    for i in range(32):
+        bit = (v >> np.uint32(i)) & np.uint32(1)
+        acc ^= bit * cols[i]
+    return acc
+
+
+def _matmul(a, b):
+    """GF(2) product a . b of matrices given as 32 uint32 columns."""
+    return _apply(a, b)
+
+
+def _matpow(cols, e):
+    r = (np.uint32(1) << np.arange(32, dtype=np.uint32)).astype(np.uint32)  # identity
+    base = cols.copy()
+    while e:
+        if e & 1:
+            r = _matmul(base, r)
+        base = _matmul(base, base)
+        e >>= 1
+    return r
+
+
+def _stream_lanes(s0, n, L=4096, B=256):
+    """Stream outputs 0 .. n-1 computed on J = ceil(n / L) lanes at once:
+    lane j starts from the state after j L steps (GF(2) jumps, two levels:
+    blocks of B lanes apart sequentially, lanes within a block vectorized)."""
+    one = _powers()[0]                    # columns of one step
+    jl = _matpow(one, L)                  # L steps
+    jlb = _matpow(one, L * B)             # L B steps
+    J = -(-n // L)
+    nb = -(-J // B)
+    heads = np.empty(nb, np.uint32)
+    h = np.uint32(s0)
+    for b in range(nb):
+        heads[b] = h
+        h = _apply(jlb, h)
+    starts = np.empty((nb, B), np.uint32)
+    starts[:, 0] = heads
+    for k in range(1, B):
+        starts[:, k] = _apply(jl, starts[:, k - 1])
+    x = starts.ravel()[:J].copy()
+    out = np.empty((J, L), np.uint32)
+    for t in range(L):
+        x = _step(x)
+        out[:, t] = x
+    return out.ravel()[:n]
+
+
 def xorshift_stream(seed, n):
     """The first n outputs of xorshift32 from `seed` (0 -> 0x9e3779b9)."""
     s = np.uint32(seed if seed else 0x9E3779B9)
+    if n > (1 << 24):
+        return _stream_lanes(s, n)
     cols = _powers()
     out = np.empty(n, np.uint32)
     done = 0
@@ -72,15 +126,21 @@ def rand(seed, scale, n):
 
 
 def normal(seed, sigma, n):
+    """N(0, sigma) by Box-Muller over consecutive xorshift32 pairs (in f64,
+    rounded once to f32); processed in chunks so that large n stays within
+    about 3 x (4 n) bytes of memory."""
     m = (n + 1) // 2
     x = xorshift_stream(seed, 2 * m)
-    u1 = ((x[0::2] >> np.uint32(8)).astype(np.float64) + 1.0) / 16777216.0
-    u2 = (x[1::2] >> np.uint32(8)).astype(np.float64) / 16777216.0
-    r = np.sqrt(-2.0 * np.log(u1))
-    z = np.empty(2 * m, np.float64)
-    z[0::2] = r * np.cos(2.0 * np.pi * u2)
-    z[1::2] = r * np.sin(2.0 * np.pi * u2)
-    return (z[:n] * sigma).astype(np.float32)
+    out = np.empty(2 * m, np.float32)
+    step = 1 << 24
+    for i in range(0, m, step):
+        j = min(m, i + step)
+        u1 = ((x[2 * i:2 * j:2] >> np.uint32(8)).astype(np.float64) + 1.0) / 16777216.0
+        u2 = (x[2 * i + 1:2 * j:2] >> np.uint32(8)).astype(np.float64) / 16777216.0
+        r = np.sqrt(-2.0 * np.log(u1))
+        out[2 * i:2 * j:2] = (r * np.cos(2.0 * np.pi * u2) * sigma).astype(np.float32)
+        out[2 * i + 1:2 * j:2] = (r * np.sin(2.0 * np.pi * u2) * sigma).astype(np.float32)
+    return out[:n]
 
 
 def bits01(seed, n):

@@ -90,3 +90,21 @@ def test_config2_model_text_round_trips_through_the_oracle():
     c, s = synth.quantize_rtn(W, 4, 0)
     dq = c.astype(np.float32) * s[:, None]
     assert np.allclose(y, x @ dq.T, rtol=1e-4, atol=1e-5)
+
+
+def test_xorshift_lanes_equal_sequential_stream():
+    """The jump-ahead stream (used for large inputs) is the same stream."""
+    import numpy as np
+    from technograd_amd import synth
+    n = 2 * 4096 * 64 + 4096 * 3 + 11
+    lanes = synth._stream_lanes(np.uint32(5), n, L=4096, B=64)
+    assert np.array_equal(lanes, synth.xorshift_stream(5, n))
+
+
+def test_normal_is_chunk_invariant():
+    """normal() of a prefix equals the prefix of a longer normal()."""
+    import numpy as np
+    from technograd_amd import synth
+    a = synth.normal(3, 1.0, 1001)
+    b = synth.normal(3, 1.0, 5000)
+    assert np.array_equal(a, b[:1001])
