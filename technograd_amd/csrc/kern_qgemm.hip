@@ -246,39 +246,56 @@ __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 	a.o[(long)r * a.orr + (long)c * a.oc + (long)jj * a.oj] = w.scale[c] * acc32;
 }
 
-// s_waitcnt immediate (gfx9 encoding: vmcnt [3:0], expcnt [6:4], lgkmcnt
-// [11:8]): wait until every vector-memory load of this wave has completed.
-__device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
+// Wait until at most N vector-memory loads of this wave are outstanding
+// (loads complete in order; copies to LDS count as loads).
+template <int N>
+__device__ inline void wait_vm()
+{
+	static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+	asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // One 1 KiB global -> LDS copy by a wave: lane l moves the 16 bytes at
 // sbase + voff into LDS address lds + 16 l (voff = 16 l). Issued with inline
 // assembly so that the compiler, which cannot tell these copies apart from
 // the LDS reads of other ring stages, does not drain all outstanding copies
-// before every read; the K loop waits for its stage explicitly (wait_vm0).
+// before every read; the K loop waits for its stage explicitly (wait_vm).
 __device__ inline void copy_to_lds(const uint8_t *sbase, unsigned voff, unsigned lds)
 {
 	asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 
 // Large batches. 512 threads = 8 waves; the workgroup computes a 128 x 256
-// tile (rows x channels), wave (wm, wn) a 32 x 128 block as four 32 x 32
-// blocks of v_mfma_i32_32x32x32_i8 for each of the three digit planes (192
-// accumulator registers). Each 64-input step needs 24 KiB of digits and 8
-// (int4) or 16 (int8) KiB of weights, copied by the waves straight from global
-// memory into a ring of 3 LDS stages (global_load_lds, 1 KiB per wave
-// instruction, no registers): stage kt + 2 is in flight while the waves
-// multiply out of stage kt. Fragments are read from LDS one 32-input substep
-// ahead of the MFMAs that use them, across the step's single barrier.
+// tile (rows x channels): wave w (group g = w / 4, rows wm = w % 4) a 32 x 128
+// block as four 32 x 32 blocks of v_mfma_i32_32x32x32_i8 for each of the three
+// digit planes (192 accumulator registers). Each 64-input step needs 24 KiB of
+// digits and 8 (int4) or 16 (int8) KiB of weights, copied straight from global
+// memory into a ring of 4 LDS stages (global_load_lds, 1 KiB per wave
+// instruction, no registers): group 0 copies the digits, group 1 the weights,
+// 3 stages ahead.
+//
+// The two waves on a SIMD (w and w + 4) belong to different groups and take
+// turns: the kernel runs in barrier-separated slots, and in each slot one
+// group reads its next step's fragments from LDS (and issues its copies) while
+// the other runs the 24 MFMAs of its current step, group 1 one slot behind
+// group 0. The matrix cores of every SIMD so always have a wave with operands
+// in registers. Per stage kt: group 0 reads it in slot 2 kt, multiplies in
+// 2 kt + 1; group 1 reads in 2 kt + 1, multiplies in 2 kt + 2. Stage kt + 3
+// is copied in the reading slot of stage kt into the ring slot of stage
+// kt - 1, whose last reader (group 1) finished in slot 2 kt - 1; a wave waits
+// for its copies of stage kt + 1 at the end of its reading slot of stage kt,
+// before the barrier that precedes the first read of stage kt + 1.
 template <int BITS>
 __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int gx, int gy)
 {
-	constexpr int S = 3;                                  // ring stages
-	constexpr int AST = 24 * 1024;                        // 4 row blocks x 2 substeps x 3 digits x 1 KiB
-	constexpr int BST = BITS == 4 ? 8192 : 16384;         // 8 channel blocks x 2 substeps x 512 B or 1 KiB
-	constexpr int STG = AST + BST, NP = STG / 1024, PW = NP / 8; // 1 KiB pieces per stage, per wave
+	constexpr int S = 4;                          // ring stages (128 or 160 KiB)
+	constexpr int AST = 24 * 1024;                // 4 row blocks x 2 substeps x 3 digits x 1 KiB
+	constexpr int BST = BITS == 4 ? 8192 : 16384; // 8 channel blocks x 2 substeps x 512 B or 1 KiB
+	constexpr int STG = AST + BST;
+	constexpr int GA = 6, GB = BST / 1024 / 4;    // copies per wave per stage: group 0, group 1
 	__shared__ __attribute__((aligned(1024))) uint8_t lds[S * STG];
 	const int tid = threadIdx.x, lane = tid & 63;
-	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave & 3, wn = wave >> 2;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = wave >> 2, wm = wave & 3;
 	// XCD-aware tile order: workgroups are dealt to the 8 XCDs round robin, so
 	// renumber them to give each XCD a contiguous band of row tiles (its L2
 	// then holds those rows' digits for every channel tile).
@@ -288,21 +305,23 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 	const int m0 = bm * BM, c0 = bn * BN, nk = w.Kp / KB, kblocks = w.Kp / 32;
 	const uint8_t *gA = (const uint8_t *)s.dig + (long)(m0 / 32) * kblocks * 3072;
 	const uint8_t *gB = w.w + (long)(c0 / 32) * kblocks * (BITS == 4 ? 512 : 1024);
-	// piece q of stage kt: digits of row block q / 6 (6 KiB per step), or
-	// weights: channel block q - 24 (int4, 1 KiB per step) or (q - 24) / 2, half (q - 24) % 2 (int8)
-	auto piece = [&](int q, int kt) -> const uint8_t * {
-		if (q < 24) return gA + (long)(q / 6) * kblocks * 3072 + (q % 6) * 1024 + (long)kt * 6144;
-		const int p = q - 24;
-		if (BITS == 4) return gB + (long)p * kblocks * 512 + (long)kt * 1024;
-		return gB + (long)(p >> 1) * kblocks * 1024 + (p & 1) * 1024 + (long)kt * 2048;
-	};
 	const unsigned voff = lane * 16;
 	const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) uint8_t *)lds;
+	// group 0 wave wm: digit pieces of row block wm (6 KiB per step);
+	// group 1 wave wm: weight pieces GB wm .. GB wm + GB - 1 (channel block p for
+	// int4, p / 2 and half p % 2 for int8)
 	auto issue = [&](int kt) {
 		const unsigned dst = lds0 + (unsigned)((kt % S) * STG);
-		for (int i = 0; i < PW; i++) {
-			const int q = wave * PW + i;
-			copy_to_lds(piece(q, kt), voff, dst + q * 1024);
+		if (g == 0) {
+			const uint8_t *src = gA + (long)wm * kblocks * 3072 + (long)kt * 6144;
+			for (int i = 0; i < GA; i++) copy_to_lds(src + i * 1024, voff, dst + (wm * GA + i) * 1024);
+		} else {
+			for (int i = 0; i < GB; i++) {
+				const int p = wm * GB + i;
+				const uint8_t *src = BITS == 4 ? gB + (long)p * kblocks * 512 + (long)kt * 1024
+							       : gB + (long)(p >> 1) * kblocks * 1024 + (p & 1) * 1024 + (long)kt * 2048;
+				copy_to_lds(src, voff, dst + AST + p * 1024);
+			}
 		}
 	};
 	v16i acc[3][4];
@@ -312,68 +331,113 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 	typedef typename std::conditional<BITS == 4, uint2, v4i>::type bfrag;
 	v4i af[2][3];
 	bfrag bf[2][4];
-	auto fread = [&](int kt, int kk, int b) {
-		const uint8_t *A = lds + (kt % S) * STG + wm * 6144 + kk * 3072 + lane * 16;
-		for (int l = 0; l < 3; l++) af[b][l] = *(const v4i *)(A + l * 1024);
-		if (BITS == 4) {
-			const uint8_t *B = lds + (kt % S) * STG + AST + wn * 4096 + kk * 512 + lane * 8;
-			for (int j = 0; j < 4; j++) bf[b][j] = *(const bfrag *)(B + j * 1024);
-		} else {
-			const uint8_t *B = lds + (kt % S) * STG + AST + wn * 8192 + kk * 1024 + lane * 16;
-			for (int j = 0; j < 4; j++) bf[b][j] = *(const bfrag *)(B + j * 2048);
+	auto fread = [&](int kt) {
+		for (int kk = 0; kk < 2; kk++) {
+			const uint8_t *A = lds + (kt % S) * STG + wm * 6144 + kk * 3072 + lane * 16;
+			for (int l = 0; l < 3; l++) af[kk][l] = *(const v4i *)(A + l * 1024);
+			if (BITS == 4) {
+				const uint8_t *B = lds + (kt % S) * STG + AST + g * 4096 + kk * 512 + lane * 8;
+				for (int j = 0; j < 4; j++) bf[kk][j] = *(const bfrag *)(B + j * 1024);
+			} else {
+				const uint8_t *B = lds + (kt % S) * STG + AST + g * 8192 + kk * 1024 + lane * 16;
+				for (int j = 0; j < 4; j++) bf[kk][j] = *(const bfrag *)(B + j * 2048);
+			}
 		}
 	};
-	auto mm = [&](int b) {
-		for (int j = 0; j < 4; j++) {
-			v4i wv;
-			if constexpr (BITS == 4) wv = unpack4(bf[b][j].x, bf[b][j].y);
-			else wv = bf[b][j];
-			for (int l = 0; l < 3; l++) acc[l][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[b][l], wv, acc[l][j], 0, 0, 0);
-		}
+	auto mm = [&]() {
+		for (int kk = 0; kk < 2; kk++)
+			for (int j = 0; j < 4; j++) {
+				v4i wv;
+				if constexpr (BITS == 4) wv = unpack4(bf[kk][j].x, bf[kk][j].y);
+				else wv = bf[kk][j];
+				for (int l = 0; l < 3; l++) acc[l][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[kk][l], wv, acc[l][j], 0, 0, 0);
+			}
+	};
+	auto bar = [&]() {
+		__builtin_amdgcn_sched_barrier(0);
+		__builtin_amdgcn_s_barrier();
+		__builtin_amdgcn_sched_barrier(0);
+		asm volatile("" ::: "memory"); // LDS changed behind the compiler's back: reload it
 	};
 	for (int st = 0; st < S - 1; st++)
 		if (st < nk) issue(st);
-	wait_vm0();
-	__builtin_amdgcn_s_barrier();
-	asm volatile("" ::: "memory"); // LDS changed behind the compiler's back: reload it
-	fread(0, 0, 0);
+	wait_vm<0>();
+	bar();
+	if (g == 1) bar(); // group 1 runs one slot behind
 	for (int kt = 0; kt < nk; kt++) {
-		fread(kt, 1, 1);
-		mm(0);
-		if (kt + 1 < nk) {
-			wait_vm0(); // this wave's copies of stage kt + 1 (the only stage in flight) have landed
-			__builtin_amdgcn_s_barrier(); // ... and every wave's; stage kt - 1 is no longer read
-			if (kt + S - 1 < nk) issue(kt + S - 1); // into the slot of stage kt - 1
-			asm volatile("" ::: "memory");
-			fread(kt + 1, 0, 0);
+		// reading slot
+		if (kt + S - 1 < nk) issue(kt + S - 1);
+		fread(kt);
+		__builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the fragments are in registers
+		if (kt + 1 < nk) { // this wave's copies of stage kt + 1 have landed (later stages may be in flight)
+			const int later = (kt + S - 1 < nk ? S - 1 : nk - 1 - kt) - 1;
+			if (g == 0) {
+				if (later <= 0) wait_vm<0>();
+				else if (later == 1) wait_vm<GA>();
+				else wait_vm<2 * GA>();
+			} else {
+				if (later <= 0) wait_vm<0>();
+				else if (later == 1) wait_vm<GB>();
+				else wait_vm<2 * GB>();
+			}
 		}
-		mm(1);
+		bar();
+		// multiplying slot
+		mm();
+		bar();
 	}
+	if (g == 0) bar(); // both groups pass the same number of barriers
 	const int r32 = lane & 31, h = lane >> 5;
 	for (int j = 0; j < 4; j++)
 		for (int v = 0; v < 16; v++) // 32 x 32 accumulator: column lane % 32, row 8 (v / 4) + 4 (lane / 32) + v % 4
-			epilogue(a, w, s, m0 + wm * 32 + 8 * (v >> 2) + 4 * h + (v & 3), c0 + wn * 128 + j * 32 + r32,
+			epilogue(a, w, s, m0 + wm * 32 + 8 * (v >> 2) + 4 * h + (v & 3), c0 + g * 128 + j * 32 + r32,
 				 combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]));
 }
 
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+
+// Register loads of the small-batch kernel, issued with inline assembly: the
+// compiler does not track them, so each ring slot is waited for explicitly
+// (wait_vm) and then "touched" (an empty asm that reads and writes the slot's
+// registers), which keeps every use of the slot below the wait.
+__device__ inline void ld16(v4i &d, const void *sbase, unsigned voff)
+{
+	asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(d) : "v"(voff), "s"(sbase) : "memory");
+}
+__device__ inline void ld8(v2u &d, const void *sbase, unsigned voff)
+{
+	asm volatile("global_load_dwordx2 %0, %1, %2" : "=v"(d) : "v"(voff), "s"(sbase) : "memory");
+}
+__device__ inline void touch(v4i &x) { asm volatile("" : "+v"(x)); }
+__device__ inline void touch(v2u &x) { asm volatile("" : "+v"(x)); }
+
 // Small and medium batches. A workgroup of W waves computes a 32 x 32 NB tile
 // (rows x channels); wave w sums the 32-input blocks kb = w, w + W, ..., loading
-// its fragments straight from global memory into registers P blocks ahead
-// (no LDS staging: no fragment is shared between the waves). Lanes of rows at
-// or beyond M load nothing, so a one-row batch fetches one row of digits.
-// The waves' int64 partial sums are added in LDS and wave 0 writes the tile.
+// its fragments straight from global memory into a ring of P register slots
+// (no LDS staging: no fragment is shared between the waves), so P blocks are
+// in flight per wave. Lanes of rows at or beyond M read row 0's bytes (the
+// same addresses as row 0's lanes, served by the same memory requests): a
+// one-row batch fetches one row of digits, and those rows' outputs are not
+// written. Past a wave's last block the loads repeat the last block (the
+// index is clamped) and the slot is not multiplied, so there is no branch
+// around a load. The waves' int64 partial sums are added in LDS and wave 0
+// writes the tile.
 template <int BITS, int NB, int W>
 __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int gx)
 {
-	constexpr int P = 4;                          // blocks in flight per wave
+	constexpr int P = 4;                          // ring slots (blocks in flight per wave)
 	constexpr int LB = BITS == 4 ? 8 : 16;        // weight bytes per lane per block
-	typedef typename std::conditional<BITS == 4, uint2, v4i>::type bfrag;
+	constexpr int NL = 3 + NB;                    // load instructions per block
+	typedef typename std::conditional<BITS == 4, v2u, v4i>::type bfrag;
 	__shared__ long long red[(W > 1 ? W - 1 : 1) * NB * 16 * 64];
 	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int bx = blockIdx.x % gx, by = blockIdx.x / gx;
 	const int m0 = by * 32, c0 = bx * NB * 32, kblocks = w.Kp / 32;
-	const int8_t *A = s.dig + (long)(m0 / 32) * kblocks * 3072 + lane * 16;
-	const uint8_t *B = w.w + (long)(c0 / 32) * kblocks * (LB * 64) + lane * LB;
+	const int mrem = a.M - m0; // rows of this tile that exist (>= 1)
+	const unsigned voffA = (unsigned)(((lane >> 5) * 32 + ((lane & 31) < mrem ? (lane & 31) : 0)) * 16);
+	const unsigned voffB = (unsigned)(lane * LB);
+	const int8_t *A = s.dig + (long)(m0 / 32) * kblocks * 3072;
+	const uint8_t *B = w.w + (long)(c0 / 32) * kblocks * (LB * 64);
 	v16i acc[3][NB];
 	for (int l = 0; l < 3; l++)
 		for (int j = 0; j < NB; j++)
@@ -381,22 +445,22 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 	v4i af[P][3];
 	bfrag bf[P][NB];
 	const int n = (kblocks - wave + W - 1) / W; // blocks of this wave
-	// block i of this wave into register slot u. Loads are unconditional (the
-	// block index is clamped into the matrix) and a slot past the wave's last
-	// block is simply not multiplied: a branch around a load, or a select on
-	// its value, would make the compiler wait for every load in flight where
-	// the branches join. Rows at or beyond M need no masking: they only feed
-	// their own outputs, which are not written, and lie in the scratch, which
-	// is padded to 128 rows.
 	auto load = [&](int u, int i) {
 		long kb = wave + (long)i * W;
 		kb = kb < kblocks ? kb : kblocks - 1;
-		for (int l = 0; l < 3; l++) af[u][l] = *(const v4i *)(A + (kb * 3 + l) * 1024);
-		for (int j = 0; j < NB; j++) bf[u][j] = *(const bfrag *)(B + ((long)j * kblocks + kb) * (LB * 64));
+		for (int l = 0; l < 3; l++) ld16(af[u][l], A + (kb * 3 + l) * 1024, voffA);
+		for (int j = 0; j < NB; j++) {
+			const uint8_t *b = B + ((long)j * kblocks + kb) * (LB * 64);
+			if constexpr (BITS == 4) ld8(bf[u][j], b, voffB);
+			else ld16(bf[u][j], b, voffB);
+		}
 	};
 	for (int u = 0; u < P; u++) load(u, u);
 	for (int i0 = 0; i0 < n; i0 += P) {
 		for (int u = 0; u < P; u++) {
+			wait_vm<(P - 1) * NL>(); // slot u's loads are the oldest P - 1 groups back
+			for (int l = 0; l < 3; l++) touch(af[u][l]);
+			for (int j = 0; j < NB; j++) touch(bf[u][j]);
 			if (i0 + u < n) {
 				for (int j = 0; j < NB; j++) {
 					v4i wv;
@@ -408,6 +472,7 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 			load(u, i0 + u + P);
 		}
 	}
+	wait_vm<0>(); // the ring's last (unused) loads have landed before the wave goes on
 	if (W > 1) {
 		if (wave > 0)
 			for (int j = 0; j < NB; j++)
