@@ -246,6 +246,49 @@ __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 	a.o[(long)r * a.orr + (long)c * a.oc + (long)jj * a.oj] = w.scale[c] * acc32;
 }
 
+// One lane's outputs of a 32-row block: rows mbase + 8 (v / 4) + 4 (lane / 32)
+// + v % 4 (v = 0 .. 15, the 32 x 32 accumulator layout) for NB column blocks
+// cbase + 32 j + lane % 32; tot(j, v) gives sum_k t q. A wave without a
+// special row (the common case) takes a straight-line path that reads each
+// row's exponent and sum once and each column's scale once; otherwise every
+// output goes through epilogue().
+template <int NB, class Tot>
+__device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int mbase, int cbase, int lane,
+				  Tot tot)
+{
+	const int r32 = lane & 31, h = lane >> 5;
+	int sp = 0;
+	for (int v = 0; v < 16; v++) {
+		const int m = mbase + 8 * (v >> 2) + 4 * h + (v & 3);
+		if (m < a.M) sp |= s.special[m];
+	}
+	if (__any(sp)) {
+		for (int j = 0; j < NB; j++)
+			for (int v = 0; v < 16; v++) epilogue(a, w, s, mbase + 8 * (v >> 2) + 4 * h + (v & 3), cbase + j * 32 + r32, tot(j, v));
+		return;
+	}
+	float sc[NB];
+	long coff[NB];
+	for (int j = 0; j < NB; j++) {
+		const int c = cbase + j * 32 + r32;
+		sc[j] = w.scale[c < w.Cp ? c : 0]; // scales are padded to Cp; columns at or beyond C are not written
+		coff[j] = (long)c * a.oc;
+	}
+	for (int v = 0; v < 16; v++) {
+		const int m = mbase + 8 * (v >> 2) + 4 * h + (v & 3);
+		if (m >= a.M) continue;
+		const int E = s.e[m];
+		const long long q8 = w.bits == 4 ? 8 * s.qsum[m] : 0;
+		int r = m, jj = 0;
+		if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
+		float *orow = a.o + (long)r * a.orr + (long)jj * a.oj;
+		for (int j = 0; j < NB; j++) {
+			if (cbase + j * 32 + r32 >= w.C) continue;
+			orow[coff[j]] = sc[j] * (float)ldexp((double)(tot(j, v) - q8), E - 23);
+		}
+	}
+}
+
 // Wait until at most N vector-memory loads of this wave are outstanding
 // (loads complete in order; copies to LDS count as loads).
 template <int N>
@@ -387,11 +430,8 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 		bar();
 	}
 	if (g == 0) bar(); // both groups pass the same number of barriers
-	const int r32 = lane & 31, h = lane >> 5;
-	for (int j = 0; j < 4; j++)
-		for (int v = 0; v < 16; v++) // 32 x 32 accumulator: column lane % 32, row 8 (v / 4) + 4 (lane / 32) + v % 4
-			epilogue(a, w, s, m0 + wm * 32 + 8 * (v >> 2) + 4 * h + (v & 3), c0 + g * 128 + j * 32 + r32,
-				 combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]));
+	store_tile<4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane,
+		      [&](int j, int v) { return combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]); });
 }
 
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
@@ -481,13 +521,11 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 		__syncthreads();
 		if (wave != 0) return;
 	}
-	const int r32 = lane & 31, h = lane >> 5;
-	for (int j = 0; j < NB; j++)
-		for (int v = 0; v < 16; v++) {
-			long long tot = combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
-			for (int u = 0; u < W - 1; u++) tot += red[((u * NB + j) * 16 + v) * 64 + lane];
-			epilogue(a, w, s, m0 + 8 * (v >> 2) + 4 * h + (v & 3), c0 + j * 32 + r32, tot);
-		}
+	store_tile<NB>(a, w, s, m0, c0, lane, [&](int j, int v) {
+		long long tot = combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+		for (int u = 0; u < W - 1; u++) tot += red[((u * NB + j) * 16 + v) * 64 + lane];
+		return tot;
+	});
 }
 
 template <int BITS, int NB, int W>
