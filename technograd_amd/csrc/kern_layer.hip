@@ -236,3 +236,63 @@ void tgk_copy(hipStream_t s, float *o, long ors, long ooff, tgk_opd a, long aoff
 	long total = (long)rows * w;
 	if (total > 0) copy_k<<<blocks_for(total), TPB, 0, s>>>(o, ors, ooff, a, aoff, w, total);
 }
+
+namespace {
+
+// The selective-scan recurrence of a Mamba-style block (the scan body
+//   dA = exp(reshape(dt_t) * A); h = dA * h + outer(du_t, B_t); y_t = h @ C_t
+// recognized by the program builder), fused over all T steps: one thread
+// per (row, channel d) keeps h[d, 0..N-1] and A[d, :] in registers. Each
+// product, exponential and sum is the one the per-instruction kernels compute
+// (binary_k, unary_k, outer_k, mm_exact_k; this file is built with
+// -ffp-contract=off), in the same order, so the results are bit-identical to
+// running the body one instruction per launch. A block covers channels of
+// a single row, so B_t and C_t are the same for every lane of a wave.
+template <int N>
+__global__ __launch_bounds__(256) void sscan_k(float *h, long hrs, tgk_opd dt, tgk_opd du, tgk_opd Bq, tgk_opd Cq, tgk_opd A,
+					       float *ys, long yrs, int D, int T, int reverse, int dblocks)
+{
+	const int r = blockIdx.x / dblocks;
+	const int d = (blockIdx.x - r * dblocks) * 256 + threadIdx.x;
+	if (d >= D) return;
+	float hv[N], av[N];
+	float *hp = h + (long)r * hrs + (long)d * N;
+	for (int n = 0; n < N; n++) {
+		hv[n] = hp[n];
+		av[n] = A.p[(long)r * A.rs + (long)d * N + n];
+	}
+	const float *dtp = dt.p + (long)r * dt.rs, *dup = du.p + (long)r * du.rs;
+	const float *bp = Bq.p + (long)r * Bq.rs, *cp = Cq.p + (long)r * Cq.rs;
+	float *yp = ys + (long)r * yrs;
+	for (int s = 0; s < T; s++) {
+		const int t = reverse ? T - 1 - s : s;
+		const float dtv = dtp[(long)t * D + d], duv = dup[(long)t * D + d];
+		float y = 0.0f;
+		for (int n = 0; n < N; n++) {
+			const float da = expf(dtv * av[n]);
+			const float hn = da * hv[n] + duv * bp[(long)t * N + n];
+			hv[n] = hn;
+			y = y + hn * cp[(long)t * N + n];
+		}
+		yp[(long)t * D + d] = y;
+	}
+	for (int n = 0; n < N; n++) hp[n] = hv[n];
+}
+
+} // namespace
+
+bool tgk_sscan_supported(int N) { return N == 4 || N == 8 || N == 16; }
+
+void tgk_sscan(hipStream_t s, float *h, long hrs, tgk_opd dt, tgk_opd du, tgk_opd Bq, tgk_opd Cq, tgk_opd A, float *ys, long yrs, int D,
+	       int N, int T, int reverse, int rows)
+{
+	if (rows <= 0 || D <= 0) return;
+	const int dblocks = (D + 255) / 256;
+	const unsigned grid = (unsigned)(rows * dblocks);
+	switch (N) {
+	case 4: sscan_k<4><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks); break;
+	case 8: sscan_k<8><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks); break;
+	case 16: sscan_k<16><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks); break;
+	default: break;
+	}
+}

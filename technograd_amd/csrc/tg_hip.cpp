@@ -58,7 +58,7 @@ struct Opnd {
 	long rs = 0;  // row stride in floats (0 for pool values)
 };
 
-enum { ST_BIN, ST_UN, ST_MM, ST_QGEMM, ST_ROW, ST_RED, ST_TRANS, ST_OUTER, ST_TAKE, ST_COPY, ST_SCAN, ST_FILL_STEPS };
+enum { ST_BIN, ST_UN, ST_MM, ST_QGEMM, ST_ROW, ST_RED, ST_TRANS, ST_OUTER, ST_TAKE, ST_COPY, ST_SCAN, ST_FILL_STEPS, ST_SSCAN };
 
 struct Step {
 	int kind = 0, op = 0;
@@ -79,6 +79,8 @@ struct Step {
 	int dyn_a = 0, dyn_o = 0;
 	// scan
 	int T = 0, reverse = 0, body_lo = 0, body_hi = 0, stid = -1;
+	// fused selective scan: B and C sequences, A, stacked outputs
+	Opnd e0, e1, e2, e3;
 };
 
 } // namespace
@@ -275,6 +277,63 @@ Opnd value_opnd(LB &L, int v)
 
 bool layer_block(LB &L, const tgm_block *b);
 
+// A scan whose body is exactly the selective-state-space recurrence
+//   (x0 [D 1] (reshape dt)) (x1 [D N] (mul x0 A)) (x2 (exp x1)) (x3 (mul x2 h))
+//   (x4 (outer du B)) (x5 (add x3 x4)) (y [D] (matmul x5 C)), next h = x5, emit y
+// (dt, du [D] and B, C [N] the scan's four sequence slices, A a [D N] param,
+// h the only carry; commuted mul/add operands accepted) runs as one fused
+// kernel (tgk_sscan) instead of seven launches per step. Any other body takes
+// the general path.
+bool match_sscan(LB &L, const tgm_ins &in, Step &st)
+{
+	const tgm_module *m = L.m;
+	if (in.nc != 1 || in.ny != 1 || in.nx != 4 || in.stid >= 0 || !in.body || in.body->len != 7) return false;
+	const tgm_ins *b = in.body->v;
+	const int h = in.c[0];
+	const tgm_shape &hs = m->val[h].sh;
+	if (hs.rank != 2) return false;
+	const int D = hs.dim[0], N = hs.dim[1];
+	if (!tgk_sscan_supported(N)) return false;
+	auto slice = [&](int v) {
+		for (int j = 0; j < in.nx; j++)
+			if (in.xt[j] == v) return j;
+		return -1;
+	};
+	auto shaped = [&](int v, int rank, int d0, int d1) {
+		const tgm_shape &x = m->val[v].sh;
+		return x.rank == rank && x.dim[0] == d0 && (rank < 2 || x.dim[1] == d1);
+	};
+	auto pair = [](const tgm_ins &i, int u, int v) { return (i.a[0] == u && i.a[1] == v) || (i.a[0] == v && i.a[1] == u); };
+	if (b[0].op != TGM_RESHAPE || !shaped(b[0].out, 2, D, 1) || !shaped(b[0].a[0], 1, D, 0)) return false;
+	const int jdt = slice(b[0].a[0]);
+	if (b[1].op != TGM_MUL || !shaped(b[1].out, 2, D, N)) return false;
+	const int A = b[1].a[0] == b[0].out ? b[1].a[1] : b[1].a[1] == b[0].out ? b[1].a[0] : -1;
+	if (A < 0 || m->val[A].kind != TGM_PARAM || m->val[A].qbits || !shaped(A, 2, D, N)) return false;
+	if (b[2].op != TGM_EXP || b[2].a[0] != b[1].out) return false;
+	if (b[3].op != TGM_MUL || !pair(b[3], b[2].out, h)) return false;
+	if (b[4].op != TGM_OUTER || !shaped(b[4].a[0], 1, D, 0) || !shaped(b[4].a[1], 1, N, 0)) return false;
+	const int jdu = slice(b[4].a[0]), jb = slice(b[4].a[1]);
+	if (b[5].op != TGM_ADD || !pair(b[5], b[3].out, b[4].out)) return false;
+	if (b[6].op != TGM_MATMUL || b[6].a[0] != b[5].out || !shaped(b[6].out, 1, D, 0) || !shaped(b[6].a[1], 1, N, 0)) return false;
+	const int jc = slice(b[6].a[1]);
+	if (jdt < 0 || jdu < 0 || jb < 0 || jc < 0) return false;
+	if (jdt == jdu || jdt == jb || jdt == jc || jdu == jb || jdu == jc || jb == jc) return false;
+	if (in.cnext[0] != b[5].out || in.y[0] != b[6].out) return false;
+	st.kind = ST_SSCAN;
+	st.o = value_opnd(L, h);
+	st.a = value_opnd(L, in.x[jdt]);
+	st.b = value_opnd(L, in.x[jdu]);
+	st.e0 = value_opnd(L, in.x[jb]);
+	st.e1 = value_opnd(L, in.x[jc]);
+	st.e2 = value_opnd(L, A);
+	st.e3 = value_opnd(L, in.ys[0]);
+	st.p0 = D;
+	st.p1 = N;
+	st.T = in.T;
+	st.reverse = in.reverse;
+	return true;
+}
+
 bool layer_ins(LB &L, const tgm_ins &in)
 {
 	tgm_module *m = L.m;
@@ -431,6 +490,11 @@ bool layer_ins(LB &L, const tgm_ins &in)
 			c.a = value_opnd(L, in.cinit[k]);
 			c.n = (int)m->val[in.c[k]].n;
 			S.push_back(c);
+		}
+		Step fused;
+		if (match_sscan(L, in, fused)) {
+			S.push_back(fused);
+			return true;
 		}
 		Step sc;
 		sc.kind = ST_SCAN;
@@ -847,6 +911,10 @@ void exec_step(Run &R, const Step &s)
 	case ST_COPY:
 		tgk_copy(st, dst(R, s.o), s.o.rs, s.dyn_o ? (long)R.t * s.n : 0, resolve(R, s.a), s.dyn_a ? (long)R.t * s.n : 0, s.n,
 			 R.rows);
+		break;
+	case ST_SSCAN:
+		tgk_sscan(st, dst(R, s.o), s.o.rs, resolve(R, s.a), resolve(R, s.b), resolve(R, s.e0), resolve(R, s.e1), resolve(R, s.e2),
+			  dst(R, s.e3), s.e3.rs, s.p0, s.p1, s.T, s.reverse, R.rows);
 		break;
 	}
 }

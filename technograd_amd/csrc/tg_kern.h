@@ -52,6 +52,15 @@ void tgk_take(hipStream_t s, float *o, long ors, tgk_opd w, tgk_opd idx, int cnt
 /* o[r*ors + ooff + i] = a[r*a.rs + aoff + i], i < w */
 void tgk_copy(hipStream_t s, float *o, long ors, long ooff, tgk_opd a, long aoff, int w, int rows);
 
+/* A whole selective scan (T steps) of the body
+ *   h = exp(reshape(dt_t) * A) * h + outer(du_t, B_t); y_t = h @ C_t
+ * per row: h [D][N] (carry, updated in place), dt, du [T][D], B, C [T][N],
+ * A [D][N], ys [T][D]; results bit-identical to the per-instruction kernels.
+ * N must be one tgk_sscan_supported() accepts. */
+bool tgk_sscan_supported(int N);
+void tgk_sscan(hipStream_t s, float *h, long hrs, tgk_opd dt, tgk_opd du, tgk_opd Bq, tgk_opd Cq, tgk_opd A, float *ys, long yrs, int D,
+	       int N, int T, int reverse, int rows);
+
 /* ---- quantized GEMM on int8 MFMA (kern_qgemm.hip) ----
  * Y = X Wq^T with X [M][K] f32 (row m at x + (m / ni) * xr + (m % ni) * xj,
  * element k at + k * xk), Wq repacked (see tgk_qweight). Exact integer
