@@ -72,6 +72,51 @@ __global__ void unary_k(int op, float *o, long ors, tgk_opd a, int n, long total
 	o[r * ors + i] = uop(op, a.p[r * a.rs + i]);
 }
 
+// Rows of at least ROWK elements: the grid is rows x chunks of EPT * TPB
+// elements, so a thread finds its row with one division of the block index
+// (the same for the whole block) instead of a 64-bit division per element.
+// Each thread handles EPT elements TPB apart: its loads are all issued before
+// the first result is stored.
+constexpr int EPT = 4, ROWK = 512;
+
+template <int OP>
+__global__ __launch_bounds__(256) void binary_rows_k(float *o, long ors, int n, tgk_opd a, int am, const int *amap, tgk_opd b, int bm,
+						     const int *bmap, int cpr)
+{
+	const int r = blockIdx.x / cpr;
+	const int i0 = (blockIdx.x - r * cpr) * (TPB * EPT) + threadIdx.x;
+	const float *ap = a.p + (long)r * a.rs, *bp = b.p + (long)r * b.rs;
+	float x[EPT], y[EPT];
+	for (int j = 0; j < EPT; j++) {
+		const int i = i0 + j * TPB, ic = i < n ? i : n - 1;
+		x[j] = ap[am == 0 ? ic : am == 1 ? 0 : amap[ic]];
+		y[j] = bp[bm == 0 ? ic : bm == 1 ? 0 : bmap[ic]];
+	}
+	float *op = o + (long)r * ors;
+	for (int j = 0; j < EPT; j++) {
+		const int i = i0 + j * TPB;
+		if (i < n) op[i] = bop(OP, x[j], y[j]);
+	}
+}
+
+template <int OP>
+__global__ __launch_bounds__(256) void unary_rows_k(float *o, long ors, tgk_opd a, int n, int cpr)
+{
+	const int r = blockIdx.x / cpr;
+	const int i0 = (blockIdx.x - r * cpr) * (TPB * EPT) + threadIdx.x;
+	const float *ap = a.p + (long)r * a.rs;
+	float x[EPT];
+	for (int j = 0; j < EPT; j++) {
+		const int i = i0 + j * TPB;
+		x[j] = ap[i < n ? i : n - 1];
+	}
+	float *op = o + (long)r * ors;
+	for (int j = 0; j < EPT; j++) {
+		const int i = i0 + j * TPB;
+		if (i < n) op[i] = uop(OP, x[j]);
+	}
+}
+
 __device__ inline int code_at(const uint8_t *q, int bits, long i)
 {
 	if (bits == 8) return (signed char)q[i];
@@ -131,6 +176,54 @@ __global__ void rowop_k(int op, float *o, long ors, tgk_opd a, int nrow, int col
 	}
 }
 
+// The same per-line loops with the lines staged through LDS: a block takes
+// lpb consecutive lines of one batch row (lpb divides nrow), which are
+// contiguous in memory, so loads and stores are coalesced; thread l then runs
+// line l's loops in the reference's order on its LDS copy. LDS lines are
+// `stride` floats apart, stride odd, so the lanes' sequential walks fall in
+// distinct banks.
+__global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, tgk_opd a, int nrow, int cols, int lpb, int stride)
+{
+	extern __shared__ float lds[];
+	const int bpr = nrow / lpb, r = blockIdx.x / bpr, q0 = (blockIdx.x - r * bpr) * lpb;
+	const int tot = lpb * cols;
+	const float *x = a.p + (long)r * a.rs + (long)q0 * cols;
+	constexpr int U = 8;
+	for (int e0 = 0; e0 < tot; e0 += U * TPB) {
+		float v[U];
+		for (int j = 0; j < U; j++) {
+			const int e = e0 + j * TPB + threadIdx.x;
+			v[j] = x[e < tot ? e : tot - 1];
+		}
+		for (int j = 0; j < U; j++) {
+			const int e = e0 + j * TPB + threadIdx.x;
+			if (e < tot) lds[(e / cols) * stride + e % cols] = v[j];
+		}
+	}
+	__syncthreads();
+	if ((int)threadIdx.x < lpb) {
+		float *y = lds + threadIdx.x * stride;
+		if (op == TGM_SOFTMAX) {
+			float mx = y[0], sum = 0.0f;
+			for (int i = 1; i < cols; i++)
+				if (y[i] > mx) mx = y[i];
+			for (int i = 0; i < cols; i++) {
+				y[i] = expf(y[i] - mx);
+				sum += y[i];
+			}
+			for (int i = 0; i < cols; i++) y[i] /= sum;
+		} else {
+			float sum = 0.0f;
+			for (int i = 0; i < cols; i++) sum += y[i] * y[i];
+			const float inv = 1.0f / sqrtf(sum / (float)cols + 1e-6f);
+			for (int i = 0; i < cols; i++) y[i] = y[i] * inv;
+		}
+	}
+	__syncthreads();
+	float *out = o + (long)r * ors + (long)q0 * cols;
+	for (int e = threadIdx.x; e < tot; e += TPB) out[e] = lds[(e / cols) * stride + e % cols];
+}
+
 __global__ void reduce_k(int op, float *o, long ors, tgk_opd a, int n, int rows)
 {
 	int r = blockIdx.x * blockDim.x + threadIdx.x;
@@ -187,13 +280,38 @@ void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int
 		const int *bmap, int rows)
 {
 	long total = (long)rows * n;
-	if (total > 0) binary_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, n, a, amode, amap, b, bmode, bmap, total);
+	if (total <= 0) return;
+	if (n >= ROWK) {
+		const int cpr = (n + TPB * EPT - 1) / (TPB * EPT);
+		const unsigned grid = (unsigned)((long)rows * cpr);
+		switch (op) {
+#define BIN(K) \
+	case K: binary_rows_k<K><<<grid, TPB, 0, s>>>(o, ors, n, a, amode, amap, b, bmode, bmap, cpr); break;
+			BIN(TGK_ADD) BIN(TGK_SUB) BIN(TGK_MUL) BIN(TGK_DIV) BIN(TGK_MAX) BIN(TGK_MIN)
+#undef BIN
+		default: break;
+		}
+	} else
+		binary_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, n, a, amode, amap, b, bmode, bmap, total);
 }
 
 void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows)
 {
 	long total = (long)rows * n;
-	if (total > 0) unary_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, n, total);
+	if (total <= 0) return;
+	if (n >= ROWK) {
+		const int cpr = (n + TPB * EPT - 1) / (TPB * EPT);
+		const unsigned grid = (unsigned)((long)rows * cpr);
+		switch (op) {
+#define UN(K) \
+	case K: unary_rows_k<K><<<grid, TPB, 0, s>>>(o, ors, a, n, cpr); break;
+			UN(TGM_NEG) UN(TGM_TANH) UN(TGM_RELU) UN(TGM_SIGMOID) UN(TGM_EXP) UN(TGM_SQRT) UN(TGM_GELU) UN(TGM_SILU)
+			UN(TGM_SOFTPLUS) UN(TGM_LOG) UN(TGM_SIN) UN(TGM_COS) UN(TGM_FLOOR) UN(TGM_STEP)
+#undef UN
+		default: break;
+		}
+	} else
+		unary_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, n, total);
 }
 
 void tgk_matmul_exact(hipStream_t s, const tgk_mm *d, int rows)
@@ -205,7 +323,14 @@ void tgk_matmul_exact(hipStream_t s, const tgk_mm *d, int rows)
 void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, int cols, int rows)
 {
 	long total = (long)rows * nrow;
-	if (total > 0) rowop_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, nrow, cols, total);
+	if (total <= 0) return;
+	const int stride = cols | 1;
+	int lpb = 32;
+	while (lpb > 1 && ((long)lpb * stride * 4 > 65536 || nrow % lpb)) lpb >>= 1;
+	if (cols >= 32 && (long)lpb * stride * 4 <= 65536 && (long)rows * (nrow / lpb) < (1L << 31))
+		rowop_lds_k<<<(unsigned)(rows * (long)(nrow / lpb)), TPB, (size_t)lpb * stride * 4, s>>>(op, o, ors, a, nrow, cols, lpb, stride);
+	else
+		rowop_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, nrow, cols, total);
 }
 
 void tgk_reduce(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows)
@@ -252,31 +377,79 @@ template <int N>
 __global__ __launch_bounds__(256) void sscan_k(float *h, long hrs, tgk_opd dt, tgk_opd du, tgk_opd Bq, tgk_opd Cq, tgk_opd A,
 					       float *ys, long yrs, int D, int T, int reverse, int dblocks)
 {
+	// Steps go in chunks of U. While chunk c is computed, chunk c + 1's dt and
+	// du are in flight into registers and its B and C into registers bound
+	// for the other LDS buffer, so the step loop never waits on memory.
+	constexpr int U = 16, BC = U * 2 * N, PER = (BC + 255) / 256;
+	__shared__ float bc[2][BC]; // [step][B_0 .. B_N-1, C_0 .. C_N-1]
 	const int r = blockIdx.x / dblocks;
 	const int d = (blockIdx.x - r * dblocks) * 256 + threadIdx.x;
-	if (d >= D) return;
+	const bool live = d < D;
+	const int dd = live ? d : D - 1; // lanes past D shadow channel D - 1 and store nothing
 	float hv[N], av[N];
-	float *hp = h + (long)r * hrs + (long)d * N;
+	float *hp = h + (long)r * hrs + (long)dd * N;
 	for (int n = 0; n < N; n++) {
 		hv[n] = hp[n];
-		av[n] = A.p[(long)r * A.rs + (long)d * N + n];
+		av[n] = A.p[(long)r * A.rs + (long)dd * N + n];
 	}
 	const float *dtp = dt.p + (long)r * dt.rs, *dup = du.p + (long)r * du.rs;
 	const float *bp = Bq.p + (long)r * Bq.rs, *cp = Cq.p + (long)r * Cq.rs;
 	float *yp = ys + (long)r * yrs;
-	for (int s = 0; s < T; s++) {
-		const int t = reverse ? T - 1 - s : s;
-		const float dtv = dtp[(long)t * D + d], duv = dup[(long)t * D + d];
-		float y = 0.0f;
-		for (int n = 0; n < N; n++) {
-			const float da = expf(dtv * av[n]);
-			const float hn = da * hv[n] + duv * bp[(long)t * N + n];
-			hv[n] = hn;
-			y = y + hn * cp[(long)t * N + n];
+	auto tstep = [&](int s) { return reverse ? T - 1 - s : s; };
+	auto load_dd = [&](int s0, float *a, float *b) {
+		for (int u = 0; u < U; u++) {
+			const int t = tstep(s0 + u < T ? s0 + u : T - 1);
+			a[u] = dtp[(long)t * D + dd];
+			b[u] = dup[(long)t * D + dd];
 		}
-		yp[(long)t * D + d] = y;
+	};
+	float bcr[PER];
+	auto load_bc = [&](int s0) {
+		for (int j = 0; j < PER; j++) {
+			const int e = (int)threadIdx.x + j * 256, ec = e < BC ? e : BC - 1;
+			const int u = ec / (2 * N), q = ec - u * (2 * N);
+			const int t = tstep(s0 + u < T ? s0 + u : T - 1);
+			bcr[j] = q < N ? bp[(long)t * N + q] : cp[(long)t * N + q - N];
+		}
+	};
+	auto store_bc = [&](int buf) {
+		for (int j = 0; j < PER; j++) {
+			const int e = (int)threadIdx.x + j * 256;
+			if (e < BC) bc[buf][e] = bcr[j];
+		}
+	};
+	float dtc[U], duc[U], dtn[U], dun[U];
+	load_dd(0, dtc, duc);
+	load_bc(0);
+	store_bc(0);
+	__syncthreads();
+	for (int s0 = 0, c = 0; s0 < T; s0 += U, c++) {
+		const bool more = s0 + U < T;
+		if (more) {
+			load_dd(s0 + U, dtn, dun);
+			load_bc(s0 + U);
+		}
+		const float *bcb = bc[c & 1];
+		for (int u = 0; u < U; u++) {
+			if (s0 + u < T) {
+				float y = 0.0f;
+				for (int n = 0; n < N; n++) {
+					const float da = expf(dtc[u] * av[n]);
+					const float hn = da * hv[n] + duc[u] * bcb[u * 2 * N + n];
+					hv[n] = hn;
+					y = y + hn * bcb[u * 2 * N + N + n];
+				}
+				if (live) yp[(long)tstep(s0 + u) * D + d] = y;
+			}
+		}
+		if (more) {
+			store_bc((c + 1) & 1);
+			for (int u = 0; u < U; u++) dtc[u] = dtn[u], duc[u] = dun[u];
+		}
+		__syncthreads();
 	}
-	for (int n = 0; n < N; n++) hp[n] = hv[n];
+	if (live)
+		for (int n = 0; n < N; n++) hp[n] = hv[n];
 }
 
 } // namespace
@@ -286,7 +459,7 @@ bool tgk_sscan_supported(int N) { return N == 4 || N == 8 || N == 16; }
 void tgk_sscan(hipStream_t s, float *h, long hrs, tgk_opd dt, tgk_opd du, tgk_opd Bq, tgk_opd Cq, tgk_opd A, float *ys, long yrs, int D,
 	       int N, int T, int reverse, int rows)
 {
-	if (rows <= 0 || D <= 0) return;
+	if (rows <= 0 || D <= 0 || T <= 0) return; // T = 0: the carry keeps its initial value
 	const int dblocks = (D + 255) / 256;
 	const unsigned grid = (unsigned)(rows * dblocks);
 	switch (N) {

@@ -150,9 +150,9 @@ __device__ inline long long put16(int8_t *blk, int k0, const float *v, int E, bo
 // special flag. Lane l owns inputs 1024 s + 16 l .. +15 of each 1024-input
 // slab s. Rows of up to SL slabs are read once into registers; longer rows are
 // read twice (max, then digits), the second time from cache.
+template <int SL>
 __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
 {
-	constexpr int SL = 4;
 	const int lane = threadIdx.x & 63;
 	const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
 	if (m >= M) return; // the whole wave leaves; the kernel has no block barrier
@@ -200,6 +200,68 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 		s.e[m] = E;
 		s.special[m] = special;
 		s.qsum[m] = qs;
+	}
+}
+
+// Many rows of at most 2048 inputs: one block per 32-row block of the digit
+// layout, W = blockDim / 64 waves. Lane l of wave w owns row m0 + (l & 31) and
+// the half (l >> 5) of 32-input blocks w, w + W, ... (NKB of them, held in
+// registers). The block's loads are 128-byte row segments, and each digit
+// plane of a 32-input block is one contiguous 1 KiB store per wave. The
+// row's max, non-finite flag and sum of q are combined through LDS. Results
+// (exponent, digits, sum of q, special) are those of digits_k. VEC: every
+// row unit stride and 16-byte aligned, K a multiple of 16.
+template <int NKB, bool VEC>
+__global__ __launch_bounds__(1024) void digits_tile_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
+{
+	__shared__ float smx[16][64];
+	__shared__ int sbad[16][64];
+	__shared__ long long sqs[16][64];
+	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
+	const int m0 = blockIdx.x * 32, half = lane >> 5, mr = lane & 31;
+	const float *x = xrow(a, m0 + mr < M ? m0 + mr : M - 1); // rows past M repeat row M - 1
+	const int nkb = Kp / 32;
+	float v[NKB][16];
+	float mx = 0.0f;
+	int bad = 0;
+	for (int j = 0; j < NKB; j++) {
+		const int kb = w + j * W;
+		load16<VEC>(v[j], x, a.xk, kb < nkb ? kb * 32 + half * 16 : K, K); // past the row: zeros
+	}
+	for (int j = 0; j < NKB; j++)
+		for (int i = 0; i < 16; i++) {
+			bad |= !isfinite(v[j][i]);
+			mx = fmaxf(mx, fabsf(v[j][i]));
+		}
+	smx[w][lane] = mx;
+	sbad[w][lane] = bad;
+	__syncthreads();
+	float amax = 0.0f;
+	bad = 0;
+	for (int u = 0; u < W; u++) {
+		amax = fmaxf(amax, fmaxf(smx[u][mr], smx[u][mr + 32]));
+		bad |= sbad[u][mr] | sbad[u][mr + 32];
+	}
+	const int special = bad || amax > 0x1p100f;
+	int E = 0;
+	if (!special && amax > 0.0f) {
+		frexpf(amax, &E);
+		if (rintf(ldexpf(amax, 23 - E)) > 8355328.0f) E += 1;
+	}
+	int8_t *blk = s.dig + (long)blockIdx.x * nkb * 3072 + mr * 16;
+	long long qs = 0;
+	for (int j = 0; j < NKB; j++) {
+		const int kb = w + j * W;
+		if (kb < nkb) qs += put16(blk, kb * 32 + half * 16, v[j], E, special);
+	}
+	sqs[w][lane] = qs;
+	__syncthreads();
+	if (w == 0 && half == 0 && m0 + mr < M) {
+		long long t = 0;
+		for (int u = 0; u < W; u++) t += sqs[u][mr] + sqs[u][mr + 32];
+		s.e[m0 + mr] = E;
+		s.special[m0 + mr] = special;
+		s.qsum[m0 + mr] = t;
 	}
 }
 
@@ -625,7 +687,26 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 	const tgk_qweight *w = a->w;
 	if (!w || !w->w || !a->x || !scratch || a->M <= 0 || a->ni <= 0) return; /* nothing valid to launch */
 	int Mp = (int)round_up(a->M, BM);
-	digits_k<<<(a->M + 3) / 4, 256, 0, st>>>(*a, carve(scratch, Mp, w->Kp), w->K, w->Kp, a->M);
+	const Scratch s = carve(scratch, Mp, w->Kp);
+	const int nkb = w->Kp / 32, M = a->M, K = w->K;
+	if (M >= 512 && nkb <= 64) {
+		const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) &&
+				 (K & 15) == 0;
+		const int W = nkb < 16 ? nkb : 16, nb = (M + 31) / 32;
+		if (nkb <= 16) {
+			if (vec) digits_tile_k<1, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+			else digits_tile_k<1, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+		} else if (nkb <= 32) {
+			if (vec) digits_tile_k<2, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+			else digits_tile_k<2, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+		} else {
+			if (vec) digits_tile_k<4, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+			else digits_tile_k<4, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+		}
+	} else if (w->Kp <= 1024)
+		digits_k<1><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
+	else
+		digits_k<4><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
 }
 
 void tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)

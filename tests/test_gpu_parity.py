@@ -103,7 +103,10 @@ def test_latent_reasoner_all_inputs_fixed_and_steps():
 
 
 @pytest.mark.parametrize("bits_,axis,m,k,n", [(4, 0, 37, 513, 1), (8, 0, 64, 256, 3), (4, 1, 5, 200, 33), (8, 1, 70, 64, 130),
-                                              (4, 0, 256, 1024, 16)])
+                                              (4, 0, 256, 1024, 16),
+                                              # 512 and more activation rows: the row-block digit kernel
+                                              (8, 1, 600, 16, 40), (4, 1, 1000, 200, 64), (8, 1, 513, 512, 96),
+                                              (4, 0, 96, 2048, 700), (8, 1, 640, 1500, 64)])
 def test_matmul_q_entry_point(bits_, axis, m, k, n):
     """tg_hip_matmul_q (tg_matmul_qa / tg_matmul_qb arguments) against the
     oracle: exact flag bit for bit, matrix-core path within the bound."""
@@ -140,20 +143,29 @@ def test_matmul_q_entry_point(bits_, axis, m, k, n):
     assert frac < 0.05
 
 
-def test_special_rows_follow_reference():
-    """A row with inf or nan takes the reference's sequential f32 loop."""
+@pytest.mark.parametrize("rows", [4, 700])
+def test_special_rows_follow_reference(rows):
+    """A row with inf or nan takes the reference's sequential f32 loop (4
+    rows: one wave per row; 700: the row-block digit kernel)."""
+    print("case special rows", rows, flush=True)
     W = synth.normal(9, 0.02, 64 * 256).reshape(64, 256)
     text = synth.linear_tgir("sp", W, 4)
-    x = synth.normal(10, 1.0, 4 * 256).reshape(4, 256)
+    x = synth.normal(10, 1.0, rows * 256).reshape(rows, 256)
+    sp = [1, 2, 3] + ([40, 41, 698] if rows > 4 else [])
     x[1, 7] = np.inf
     x[2, 100] = np.nan
     x[3, 5] = 3e38
+    if rows > 4:
+        x[40, 255] = -np.inf
+        x[41, 0] = 2e30
+        x[698, 31] = np.nan
     want, _ = O.Model(text).batch(x)
-    got, _ = hip.Program(text, max_rows=8).batch(x)
+    got, _ = hip.Program(text, max_rows=rows).batch(x)
     assert np.array_equal(np.isnan(got), np.isnan(want))
     fin = np.isfinite(want)
-    assert np.array_equal(bits(got[1:][fin[1:]]), bits(want[1:][fin[1:]]))
-    parity.check_model(got[:1], want[:1])
+    assert np.array_equal(bits(got[sp][fin[sp]]), bits(want[sp][fin[sp]]))
+    ok = np.setdiff1d(np.arange(rows), sp)
+    parity.check_model(got[ok], want[ok])
 
 
 @pytest.mark.parametrize("B", [1, 16, 256, 4096])
