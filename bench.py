@@ -304,7 +304,7 @@ def bench_config5(args):
     probe = hip.Program(text, max_rows=8)
     arena_row = probe.stats().arena_bytes / 8
     probe.close()
-    pass_rows = int(max(8, min(512, (24 << 30) // max(arena_row, 1))))
+    pass_rows = int(max(8, min(4096, (32 << 30) // max(arena_row, 1))))
     pass_rows = 1 << (pass_rows.bit_length() - 1)
     log("config 5: %.1f MiB of arena per sequence, passes of %d sequences" % (arena_row / 2**20, pass_rows))
     prog = hip.Program(text, max_rows=pass_rows)

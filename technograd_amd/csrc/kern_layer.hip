@@ -430,16 +430,20 @@ __global__ __launch_bounds__(256) void sscan_k(float *h, long hrs, tgk_opd dt, t
 			load_bc(s0 + U);
 		}
 		const float *bcb = bc[c & 1];
+		float *yt = yp + (long)tstep(s0) * D + d;
+		const long ystep = reverse ? -(long)D : (long)D;
+#pragma unroll
 		for (int u = 0; u < U; u++) {
 			if (s0 + u < T) {
 				float y = 0.0f;
+#pragma unroll
 				for (int n = 0; n < N; n++) {
 					const float da = expf(dtc[u] * av[n]);
 					const float hn = da * hv[n] + duc[u] * bcb[u * 2 * N + n];
 					hv[n] = hn;
 					y = y + hn * bcb[u * 2 * N + N + n];
 				}
-				if (live) yp[(long)tstep(s0 + u) * D + d] = y;
+				if (live) yt[u * ystep] = y;
 			}
 		}
 		if (more) {

@@ -22,6 +22,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
@@ -268,11 +269,103 @@ Opnd value_opnd(LB &L, int v)
 		w.rs = L.m->per;
 	} else {
 		w.space = SP_ARENA;
-		w.off = L.p->arena_floats;
+		w.off = v; // the value's id until place_arena assigns its offset
 		w.rs = x.n;
-		L.p->arena_floats += (x.n + 63) / 64 * 64;
 	}
 	return w;
+}
+
+// Arena placement by lifetime. Every arena operand of a step names its value
+// (Opnd::off holds the value id while the steps are built). A value lives from
+// the first to the last step that names it, both included, so a step's output
+// never shares memory with its inputs. A value whose lifetime crosses the
+// boundary of a scan body (read inside but made outside, a carry, a stacked
+// output) lives for the whole scan, since the body runs T times; values made
+// and used within one pass of a body stay local to it. Offsets are then
+// assigned in order of first use, best fit among the blocks freed so far.
+void place_arena(tg_hip_prog *p, const tgm_module *m)
+{
+	auto &S = p->steps;
+	const int nv = m->nval;
+	std::vector<long> first(nv, -1), last(nv, -1);
+	auto touch = [&](const Opnd &o, long i) {
+		if (o.space != SP_ARENA) return;
+		const int v = (int)o.off;
+		if (first[v] < 0) first[v] = i;
+		if (i > last[v]) last[v] = i;
+		if (i < first[v]) first[v] = i;
+	};
+	for (long i = 0; i < (long)S.size(); i++) {
+		const Step &st = S[i];
+		for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 }) touch(*o, i);
+	}
+	touch(p->out, (long)S.size());
+	// scans, innermost first (shorter ranges are nested in longer ones)
+	std::vector<std::pair<long, long>> scans;
+	for (long i = 0; i < (long)S.size(); i++)
+		if (S[i].kind == ST_SCAN) scans.push_back({ i, (long)S[i].body_hi - 1 });
+	std::sort(scans.begin(), scans.end(), [](const std::pair<long, long> &x, const std::pair<long, long> &y) {
+		return x.second - x.first < y.second - y.first;
+	});
+	for (auto &sc : scans)
+		for (int v = 0; v < nv; v++) {
+			if (first[v] < 0 || last[v] < sc.first || first[v] > sc.second) continue; // disjoint
+			if (first[v] > sc.first && last[v] <= sc.second) continue;                 // local to the body
+			first[v] = std::min(first[v], sc.first);
+			last[v] = std::max(last[v], sc.second);
+		}
+	std::vector<int> order;
+	for (int v = 0; v < nv; v++)
+		if (first[v] >= 0) order.push_back(v);
+	std::sort(order.begin(), order.end(), [&](int x, int y) { return first[x] < first[y] || (first[x] == first[y] && x < y); });
+	std::vector<long> off(nv, -1);
+	std::vector<std::pair<long, long>> freel; // (offset, size) blocks
+	std::vector<int> live;
+	long end = 0;
+	for (int v : order) {
+		for (size_t j = 0; j < live.size();) { // free what ended before v begins
+			const int u = live[j];
+			if (last[u] < first[v]) {
+				freel.push_back({ off[u], (m->val[u].n + 63) / 64 * 64 });
+				live[j] = live.back();
+				live.pop_back();
+			} else
+				j++;
+		}
+		std::sort(freel.begin(), freel.end());
+		for (size_t j = 0; j + 1 < freel.size();) { // merge neighbours
+			if (freel[j].first + freel[j].second == freel[j + 1].first) {
+				freel[j].second += freel[j + 1].second;
+				freel.erase(freel.begin() + (long)j + 1);
+			} else
+				j++;
+		}
+		const long need = (m->val[v].n + 63) / 64 * 64;
+		long best = -1;
+		for (size_t j = 0; j < freel.size(); j++)
+			if (freel[j].second >= need && (best < 0 || freel[j].second < freel[(size_t)best].second)) best = (long)j;
+		if (best >= 0) {
+			off[v] = freel[(size_t)best].first;
+			freel[(size_t)best].first += need;
+			freel[(size_t)best].second -= need;
+			if (!freel[(size_t)best].second) freel.erase(freel.begin() + best);
+		} else if (!freel.empty() && freel.back().first + freel.back().second == end) { // grow the last free block
+			off[v] = freel.back().first;
+			end = off[v] + need;
+			freel.pop_back();
+		} else {
+			off[v] = end;
+			end += need;
+		}
+		live.push_back(v);
+	}
+	auto fix = [&](Opnd &o) {
+		if (o.space == SP_ARENA) o.off = off[(int)o.off];
+	};
+	for (Step &st : S)
+		for (Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 }) fix(*o);
+	fix(p->out);
+	p->arena_floats = end;
 }
 
 bool layer_block(LB &L, const tgm_block *b);
@@ -1036,6 +1129,7 @@ bool build_layer(tg_hip_prog *p)
 	}
 	if (!layer_block(L, &p->m->top)) return false;
 	p->out = value_opnd(L, p->m->output);
+	place_arena(p, p->m);
 	if (!upload_pools(p, L.P)) return false;
 	size_t ab = (size_t)(p->arena_floats ? p->arena_floats : 1) * p->max_rows * sizeof(float);
 	p->stats.arena_bytes = (long)ab;
