@@ -99,6 +99,29 @@ __global__ __launch_bounds__(256) void binary_rows_k(float *o, long ors, int n, 
 	}
 }
 
+// Both operands elementwise, rows 16-byte aligned, n a multiple of 4: EPT
+// float4s per thread, TPB float4s apart.
+template <int OP>
+__global__ __launch_bounds__(256) void binary_rows4_k(float *o, long ors, int n, tgk_opd a, tgk_opd b, int cpr)
+{
+	const int r = blockIdx.x / cpr;
+	const int i0 = ((blockIdx.x - r * cpr) * (TPB * EPT) + threadIdx.x) * 4;
+	const float *ap = a.p + (long)r * a.rs, *bp = b.p + (long)r * b.rs;
+	float4 x[EPT], y[EPT];
+	for (int j = 0; j < EPT; j++) {
+		const int i = i0 + j * TPB * 4, ic = i < n ? i : 0;
+		x[j] = *(const float4 *)(ap + ic);
+		y[j] = *(const float4 *)(bp + ic);
+	}
+	float *op = o + (long)r * ors;
+	for (int j = 0; j < EPT; j++) {
+		const int i = i0 + j * TPB * 4;
+		if (i < n)
+			*(float4 *)(op + i) = make_float4(bop(OP, x[j].x, y[j].x), bop(OP, x[j].y, y[j].y), bop(OP, x[j].z, y[j].z),
+							  bop(OP, x[j].w, y[j].w));
+	}
+}
+
 template <int OP>
 __global__ __launch_bounds__(256) void unary_rows_k(float *o, long ors, tgk_opd a, int n, int cpr)
 {
@@ -114,6 +137,80 @@ __global__ __launch_bounds__(256) void unary_rows_k(float *o, long ors, tgk_opd 
 	for (int j = 0; j < EPT; j++) {
 		const int i = i0 + j * TPB;
 		if (i < n) op[i] = uop(OP, x[j]);
+	}
+}
+
+template <int OP>
+__global__ __launch_bounds__(256) void unary_rows4_k(float *o, long ors, tgk_opd a, int n, int cpr)
+{
+	const int r = blockIdx.x / cpr;
+	const int i0 = ((blockIdx.x - r * cpr) * (TPB * EPT) + threadIdx.x) * 4;
+	const float *ap = a.p + (long)r * a.rs;
+	float4 x[EPT];
+	for (int j = 0; j < EPT; j++) {
+		const int i = i0 + j * TPB * 4;
+		x[j] = *(const float4 *)(ap + (i < n ? i : 0));
+	}
+	float *op = o + (long)r * ors;
+	for (int j = 0; j < EPT; j++) {
+		const int i = i0 + j * TPB * 4;
+		if (i < n) *(float4 *)(op + i) = make_float4(uop(OP, x[j].x), uop(OP, x[j].y), uop(OP, x[j].z), uop(OP, x[j].w));
+	}
+}
+
+inline bool al16(const void *p, long rs) { return ((size_t)p & 15) == 0 && rs % 4 == 0; }
+
+// A fused elementwise run (tgk_ew): four consecutive elements per thread.
+// The N0 elementwise inputs (the first ones) are loaded as straight-line
+// float4 loads, all in flight together, then the others (a scalar per row,
+// or through an index map). The instruction list, the same for every
+// thread, then works on a small register file indexed by block-uniform
+// register numbers. Each instruction is the operation of binary_k or unary_k,
+// so the stored values are bit-identical to running the instructions one
+// launch at a time. VEC: elementwise inputs and all outputs are 16-byte
+// aligned rows and n is a multiple of 4; otherwise N0 is 0 and every input
+// takes the general path.
+__device__ inline void ew_gather(const tgk_ew &E, int j, int r, int i0, int n, float *v)
+{
+	const float *p = E.in[j] + (long)r * E.in_rs[j];
+	const int mode = E.in_mode[j];
+	if (mode == 1) {
+		const float x = p[0];
+		for (int e = 0; e < 4; e++) v[e] = x;
+	} else {
+		for (int e = 0; e < 4; e++) {
+			const int ic = i0 + e < n ? i0 + e : n - 1;
+			v[e] = p[mode == 0 ? ic : E.in_map[j][ic]];
+		}
+	}
+}
+
+template <int N0, bool VEC>
+__global__ __launch_bounds__(256) void ew_k(tgk_ew E, int n, int cpr)
+{
+	const int r = blockIdx.x / cpr;
+	const int i0 = ((blockIdx.x - r * cpr) * TPB + threadIdx.x) * 4;
+	float reg[TGK_EW_REGS][4];
+	for (int j = 0; j < N0; j++) {
+		const float4 v = *(const float4 *)(E.in[j] + (long)r * E.in_rs[j] + (i0 < n ? i0 : 0));
+		reg[j][0] = v.x, reg[j][1] = v.y, reg[j][2] = v.z, reg[j][3] = v.w;
+	}
+	for (int j = N0; j < E.nin; j++) ew_gather(E, j, r, i0, n, reg[j]);
+	for (int k = 0; k < E.nins; k++) {
+		const tgk_ew_ins I = E.ins[k];
+		if (I.kind == TGK_EW_BIN) {
+			for (int e = 0; e < 4; e++) reg[I.dst][e] = bop(I.op, reg[I.a][e], reg[I.b][e]);
+		} else if (I.kind == TGK_EW_UN) {
+			for (int e = 0; e < 4; e++) reg[I.dst][e] = uop(I.op, reg[I.a][e]);
+		} else {
+			float *p = E.out[I.dst] + (long)r * E.out_rs[I.dst];
+			if (VEC) {
+				if (i0 < n) *(float4 *)(p + i0) = make_float4(reg[I.a][0], reg[I.a][1], reg[I.a][2], reg[I.a][3]);
+			} else {
+				for (int e = 0; e < 4; e++)
+					if (i0 + e < n) p[i0 + e] = reg[I.a][e];
+			}
+		}
 	}
 }
 
@@ -281,7 +378,17 @@ void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int
 {
 	long total = (long)rows * n;
 	if (total <= 0) return;
-	if (n >= ROWK) {
+	if (n >= ROWK && n % 4 == 0 && amode == 0 && bmode == 0 && al16(o, ors) && al16(a.p, a.rs) && al16(b.p, b.rs)) {
+		const int cpr = (n + TPB * EPT * 4 - 1) / (TPB * EPT * 4);
+		const unsigned grid = (unsigned)((long)rows * cpr);
+		switch (op) {
+#define BIN(K) \
+	case K: binary_rows4_k<K><<<grid, TPB, 0, s>>>(o, ors, n, a, b, cpr); break;
+			BIN(TGK_ADD) BIN(TGK_SUB) BIN(TGK_MUL) BIN(TGK_DIV) BIN(TGK_MAX) BIN(TGK_MIN)
+#undef BIN
+		default: break;
+		}
+	} else if (n >= ROWK) {
 		const int cpr = (n + TPB * EPT - 1) / (TPB * EPT);
 		const unsigned grid = (unsigned)((long)rows * cpr);
 		switch (op) {
@@ -299,7 +406,18 @@ void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int 
 {
 	long total = (long)rows * n;
 	if (total <= 0) return;
-	if (n >= ROWK) {
+	if (n >= ROWK && n % 4 == 0 && al16(o, ors) && al16(a.p, a.rs)) {
+		const int cpr = (n + TPB * EPT * 4 - 1) / (TPB * EPT * 4);
+		const unsigned grid = (unsigned)((long)rows * cpr);
+		switch (op) {
+#define UN(K) \
+	case K: unary_rows4_k<K><<<grid, TPB, 0, s>>>(o, ors, a, n, cpr); break;
+			UN(TGM_NEG) UN(TGM_TANH) UN(TGM_RELU) UN(TGM_SIGMOID) UN(TGM_EXP) UN(TGM_SQRT) UN(TGM_GELU) UN(TGM_SILU)
+			UN(TGM_SOFTPLUS) UN(TGM_LOG) UN(TGM_SIN) UN(TGM_COS) UN(TGM_FLOOR) UN(TGM_STEP)
+#undef UN
+		default: break;
+		}
+	} else if (n >= ROWK) {
 		const int cpr = (n + TPB * EPT - 1) / (TPB * EPT);
 		const unsigned grid = (unsigned)((long)rows * cpr);
 		switch (op) {
@@ -312,6 +430,31 @@ void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int 
 		}
 	} else
 		unary_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, n, total);
+}
+
+void tgk_ew_run(hipStream_t s, const tgk_ew *e, int n, int rows)
+{
+	if (rows <= 0 || n <= 0 || e->nin < 1 || e->nin > TGK_EW_MAXIN) return;
+	bool vec = n % 4 == 0;
+	int n0 = 0; // leading elementwise inputs
+	while (n0 < e->nin && e->in_mode[n0] == 0) n0++;
+	for (int j = 0; j < n0; j++) vec = vec && ((size_t)e->in[j] & 15) == 0 && e->in_rs[j] % 4 == 0;
+	for (int j = 0; j < e->nout; j++) vec = vec && ((size_t)e->out[j] & 15) == 0 && e->out_rs[j] % 4 == 0;
+	const int cpr = (n + TPB * 4 - 1) / (TPB * 4);
+	const unsigned grid = (unsigned)((long)rows * cpr);
+	if (!vec) {
+		ew_k<0, false><<<grid, TPB, 0, s>>>(*e, n, cpr);
+		return;
+	}
+	switch (n0) {
+	case 0: ew_k<0, true><<<grid, TPB, 0, s>>>(*e, n, cpr); break;
+	case 1: ew_k<1, true><<<grid, TPB, 0, s>>>(*e, n, cpr); break;
+	case 2: ew_k<2, true><<<grid, TPB, 0, s>>>(*e, n, cpr); break;
+	case 3: ew_k<3, true><<<grid, TPB, 0, s>>>(*e, n, cpr); break;
+	case 4: ew_k<4, true><<<grid, TPB, 0, s>>>(*e, n, cpr); break;
+	case 5: ew_k<5, true><<<grid, TPB, 0, s>>>(*e, n, cpr); break;
+	default: ew_k<6, true><<<grid, TPB, 0, s>>>(*e, n, cpr); break;
+	}
 }
 
 void tgk_matmul_exact(hipStream_t s, const tgk_mm *d, int rows)

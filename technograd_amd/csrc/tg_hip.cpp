@@ -59,7 +59,32 @@ struct Opnd {
 	long rs = 0;  // row stride in floats (0 for pool values)
 };
 
-enum { ST_BIN, ST_UN, ST_MM, ST_QGEMM, ST_ROW, ST_RED, ST_TRANS, ST_OUTER, ST_TAKE, ST_COPY, ST_SCAN, ST_FILL_STEPS, ST_SSCAN };
+enum { ST_BIN, ST_UN, ST_MM, ST_QGEMM, ST_ROW, ST_RED, ST_TRANS, ST_OUTER, ST_TAKE, ST_COPY, ST_SCAN, ST_FILL_STEPS, ST_SSCAN, ST_EW };
+
+inline bool same_value(const Opnd &x, const Opnd &y) { return x.space == y.space && x.off == y.off && x.space != SP_NONE; }
+
+// A run of consecutive elementwise instructions over rows of n elements, run
+// as one fused launch (tgk_ew). While the program is built, `ops` holds the
+// instructions with operands as local ids: j < LOCAL for input j, LOCAL + k
+// for the result of op k. finish_ew then keeps a store for each result read
+// outside the run, puts the elementwise inputs first and assigns registers.
+struct EwStep {
+	static constexpr int LOCAL = 1 << 16;
+	struct In {
+		Opnd o;
+		int mode;
+		long map;
+	};
+	struct Op {
+		int kind, op, a, b;
+		Opnd o;
+	};
+	int n = 0;
+	std::vector<In> in;
+	std::vector<Op> ops;
+	std::vector<Opnd> out;
+	std::vector<tgk_ew_ins> ins;
+};
 
 struct Step {
 	int kind = 0, op = 0;
@@ -82,6 +107,10 @@ struct Step {
 	int T = 0, reverse = 0, body_lo = 0, body_hi = 0, stid = -1;
 	// fused selective scan: B and C sequences, A, stacked outputs
 	Opnd e0, e1, e2, e3;
+	// fused elementwise run (index into tg_hip_prog::ews)
+	int ew = -1;
+	// quantized GEMM whose activation digits the previous step left in the scratch
+	int reuse_digits = 0;
 };
 
 } // namespace
@@ -100,6 +129,7 @@ struct tg_hip_prog {
 	int *d_qscale = nullptr;
 	// layer program
 	std::vector<Step> steps;
+	std::vector<EwStep> ews;
 	std::vector<tgk_qweight> qws;
 	long arena_floats = 0; // per row
 	float *d_arena = nullptr;
@@ -298,6 +328,10 @@ void place_arena(tg_hip_prog *p, const tgm_module *m)
 	for (long i = 0; i < (long)S.size(); i++) {
 		const Step &st = S[i];
 		for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 }) touch(*o, i);
+		if (st.kind == ST_EW) {
+			for (const EwStep::In &x : p->ews[(size_t)st.ew].in) touch(x.o, i);
+			for (const Opnd &x : p->ews[(size_t)st.ew].out) touch(x, i);
+		}
 	}
 	touch(p->out, (long)S.size());
 	// scans, innermost first (shorter ranges are nested in longer ones)
@@ -364,11 +398,170 @@ void place_arena(tg_hip_prog *p, const tgm_module *m)
 	};
 	for (Step &st : S)
 		for (Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 }) fix(*o);
+	for (EwStep &E : p->ews) {
+		for (EwStep::In &x : E.in) fix(x.o);
+		for (Opnd &x : E.out) fix(x);
+	}
 	fix(p->out);
 	p->arena_floats = end;
 }
 
 bool layer_block(LB &L, const tgm_block *b);
+
+// Adds one elementwise instruction, to the fused run the previous step holds
+// when it can (same row length, room left, operands that the run computed
+// read elementwise), else to a new run. The run's inputs plus its results
+// never exceed the kernel's register file, so every run has registers.
+void ew_append(LB &L, int kind, int op, const Opnd &a, int amode, long amap, const Opnd &b, int bmode, long bmap, const Opnd &o, int n)
+{
+	auto &S = L.p->steps;
+	auto local = [](const EwStep &E, const Opnd &x) {
+		for (size_t k = 0; k < E.ops.size(); k++)
+			if (same_value(E.ops[k].o, x)) return (int)k;
+		return -1;
+	};
+	auto input = [](const EwStep &E, const Opnd &x, int mode, long map) {
+		for (size_t j = 0; j < E.in.size(); j++)
+			if (same_value(E.in[j].o, x) && E.in[j].o.rs == x.rs && E.in[j].mode == mode && (mode != 2 || E.in[j].map == map))
+				return (int)j;
+		return -1;
+	};
+	const int nops = kind == TGK_EW_BIN ? 2 : 1;
+	const Opnd *opd[2] = { &a, &b };
+	const int mode[2] = { amode, bmode };
+	const long map[2] = { amap, bmap };
+	bool fits = !S.empty() && S.back().kind == ST_EW;
+	if (fits) {
+		const EwStep &E = L.p->ews[(size_t)S.back().ew];
+		int new_in = 0;
+		for (int j = 0; j < nops; j++) {
+			const int k = local(E, *opd[j]);
+			if (k >= 0 && mode[j] != 0) fits = false;
+			if (k < 0 && input(E, *opd[j], mode[j], map[j]) < 0 && !(j == 1 && same_value(a, b) && a.rs == b.rs && amode == bmode && (amode != 2 || amap == bmap)))
+				new_in++;
+		}
+		fits = fits && E.n == n && (int)E.in.size() + new_in <= TGK_EW_MAXIN &&
+		       (int)(E.in.size() + new_in + E.ops.size() + 1) <= TGK_EW_REGS && (int)E.ops.size() < TGK_EW_MAXOUT;
+	}
+	if (!fits) {
+		Step st;
+		st.kind = ST_EW;
+		st.ew = (int)L.p->ews.size();
+		L.p->ews.emplace_back();
+		L.p->ews.back().n = n;
+		S.push_back(st);
+	}
+	EwStep &E = L.p->ews[(size_t)S.back().ew];
+	int id[2] = { 0, 0 };
+	for (int j = 0; j < nops; j++) {
+		const int k = local(E, *opd[j]);
+		if (k >= 0) {
+			id[j] = EwStep::LOCAL + k;
+			continue;
+		}
+		int q = input(E, *opd[j], mode[j], map[j]);
+		if (q < 0) {
+			E.in.push_back({ *opd[j], mode[j], map[j] });
+			q = (int)E.in.size() - 1;
+		}
+		id[j] = q;
+	}
+	E.ops.push_back({ kind, op, id[0], id[1], o });
+}
+
+// Completes every fused run once all steps exist: which results are read
+// outside their run (they are stored, the others live only in registers),
+// elementwise inputs first, registers by lifetime.
+void finish_ew(tg_hip_prog *p)
+{
+	std::vector<Opnd> used; // operands read or written by steps other than fused runs, plus the output
+	for (const Step &st : p->steps)
+		if (st.kind != ST_EW)
+			for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 })
+				if (o->space == SP_ARENA || o->space == SP_OUT) used.push_back(*o);
+	for (const EwStep &E : p->ews)
+		for (const EwStep::In &x : E.in) used.push_back(x.o);
+	used.push_back(p->out);
+	auto read_outside = [&](const Opnd &o) {
+		if (o.space == SP_OUT) return true;
+		for (const Opnd &u : used)
+			if (same_value(u, o)) return true;
+		return false;
+	};
+	for (Step &st : p->steps) { // a run of one instruction takes the specialised kernel
+		if (st.kind != ST_EW || p->ews[(size_t)st.ew].ops.size() != 1) continue;
+		EwStep &E = p->ews[(size_t)st.ew];
+		const EwStep::Op &q = E.ops[0];
+		st.kind = q.kind == TGK_EW_BIN ? ST_BIN : ST_UN;
+		st.op = q.op;
+		st.n = E.n;
+		st.o = q.o;
+		st.a = E.in[(size_t)q.a].o;
+		st.amode = E.in[(size_t)q.a].mode;
+		st.amap = E.in[(size_t)q.a].map;
+		if (q.kind == TGK_EW_BIN) {
+			st.b = E.in[(size_t)q.b].o;
+			st.bmode = E.in[(size_t)q.b].mode;
+			st.bmap = E.in[(size_t)q.b].map;
+		}
+		st.ew = -1;
+		E = EwStep{};
+	}
+	for (EwStep &E : p->ews) {
+		if (E.ops.empty()) continue;
+		const int nin = (int)E.in.size(), nop = (int)E.ops.size();
+		// elementwise inputs first
+		std::vector<int> order, pos(nin);
+		for (int j = 0; j < nin; j++)
+			if (E.in[j].mode == 0) order.push_back(j);
+		for (int j = 0; j < nin; j++)
+			if (E.in[j].mode != 0) order.push_back(j);
+		std::vector<EwStep::In> in2;
+		for (int j = 0; j < nin; j++) {
+			pos[order[j]] = j;
+			in2.push_back(E.in[order[j]]);
+		}
+		E.in = in2;
+		auto remap = [&](int id) { return id < EwStep::LOCAL ? pos[id] : id; };
+		// last reader of each local value
+		std::vector<int> last_in(nin, -1), last_op(nop, -1);
+		for (int k = 0; k < nop; k++) {
+			EwStep::Op &q = E.ops[k];
+			q.a = remap(q.a);
+			if (q.kind == TGK_EW_BIN) q.b = remap(q.b);
+			for (int id : { q.a, q.kind == TGK_EW_BIN ? q.b : q.a }) {
+				if (id < EwStep::LOCAL) last_in[id] = k;
+				else last_op[id - EwStep::LOCAL] = k;
+			}
+		}
+		std::vector<int> reg_of_op(nop, -1), busy(TGK_EW_REGS, 0);
+		for (int j = 0; j < nin; j++) busy[j] = 1; // input j is loaded into register j
+		E.ins.clear();
+		E.out.clear();
+		auto reg = [&](int id) { return id < EwStep::LOCAL ? id : reg_of_op[id - EwStep::LOCAL]; };
+		for (int k = 0; k < nop; k++) {
+			const EwStep::Op &q = E.ops[k];
+			tgk_ew_ins I{ q.kind, q.op, -1, reg(q.a), q.kind == TGK_EW_BIN ? reg(q.b) : 0 };
+			// operands read for the last time here free their registers (the
+			// kernel reads both operands of an element before writing it)
+			for (int id : { q.a, q.kind == TGK_EW_BIN ? q.b : q.a }) {
+				const int lu = id < EwStep::LOCAL ? last_in[id] : last_op[id - EwStep::LOCAL];
+				if (lu == k) busy[reg(id)] = 0;
+			}
+			int r = 0;
+			while (busy[r]) r++; // the append limits guarantee a free register
+			busy[r] = 1;
+			I.dst = r;
+			reg_of_op[k] = r;
+			E.ins.push_back(I);
+			if (read_outside(q.o)) {
+				E.ins.push_back({ TGK_EW_STORE, 0, (int)E.out.size(), r, 0 });
+				E.out.push_back(q.o);
+			}
+			if (last_op[k] < 0) busy[r] = 0; // not read again inside the run
+		}
+	}
+}
 
 // A scan whose body is exactly the selective-state-space recurrence
 //   (x0 [D 1] (reshape dt)) (x1 [D N] (mul x0 A)) (x2 (exp x1)) (x3 (mul x2 h))
@@ -455,24 +648,20 @@ bool layer_ins(LB &L, const tgm_ins &in)
 		s.n = (int)m->val[in.out].n;
 		break;
 	}
-	case TGM_ADD: case TGM_SUB: case TGM_MUL: case TGM_DIV: case TGM_MAX: case TGM_MIN:
-		s.kind = ST_BIN;
-		s.op = in.op - TGM_ADD;
-		s.a = value_opnd(L, in.a[0]);
-		s.b = value_opnd(L, in.a[1]);
-		s.o = value_opnd(L, in.out);
-		s.n = (int)m->val[in.out].n;
-		bcast(m->val[in.out].sh, m->val[in.a[0]].sh, L.P.imap, s.amode, s.amap);
-		bcast(m->val[in.out].sh, m->val[in.a[1]].sh, L.P.imap, s.bmode, s.bmap);
-		break;
+	case TGM_ADD: case TGM_SUB: case TGM_MUL: case TGM_DIV: case TGM_MAX: case TGM_MIN: {
+		int amode, bmode;
+		long amap, bmap;
+		bcast(m->val[in.out].sh, m->val[in.a[0]].sh, L.P.imap, amode, amap);
+		bcast(m->val[in.out].sh, m->val[in.a[1]].sh, L.P.imap, bmode, bmap);
+		ew_append(L, TGK_EW_BIN, in.op - TGM_ADD, value_opnd(L, in.a[0]), amode, amap, value_opnd(L, in.a[1]), bmode, bmap,
+			  value_opnd(L, in.out), (int)m->val[in.out].n);
+		return true;
+	}
 	case TGM_NEG: case TGM_TANH: case TGM_RELU: case TGM_SIGMOID: case TGM_EXP: case TGM_SQRT: case TGM_GELU:
 	case TGM_SILU: case TGM_SOFTPLUS: case TGM_LOG: case TGM_SIN: case TGM_COS: case TGM_FLOOR: case TGM_STEP:
-		s.kind = ST_UN;
-		s.op = in.op;
-		s.a = value_opnd(L, in.a[0]);
-		s.o = value_opnd(L, in.out);
-		s.n = (int)m->val[in.out].n;
-		break;
+		ew_append(L, TGK_EW_UN, in.op, value_opnd(L, in.a[0]), 0, 0, Opnd{}, 0, 0, value_opnd(L, in.out),
+			  (int)m->val[in.out].n);
+		return true;
 	case TGM_MATMUL: {
 		const tgm_value &va = m->val[in.a[0]], &vb = m->val[in.a[1]];
 		int mm, kk, nn, gg;
@@ -504,6 +693,12 @@ bool layer_ins(LB &L, const tgm_ins &in)
 				s.ni = mm;
 				s.xr = x.rs, s.xj = kk, s.xk = 1;
 				s.orr = s.o.rs, s.oc = 1, s.ojj = nn;
+			}
+			if (!S.empty() && S.back().kind == ST_QGEMM) { // same activations as the GEMM before: its digits stand
+				const Step &pv = S.back();
+				const tgk_qweight &pw = L.p->qws[(size_t)pv.qw];
+				s.reuse_digits = same_value(pv.a, s.a) && pv.a.rs == s.a.rs && pv.ni == s.ni && pv.xr == s.xr &&
+						 pv.xj == s.xj && pv.xk == s.xk && pw.K == qw.K && pw.Kp == qw.Kp;
 			}
 			size_t need = tgk_qgemm_scratch(L.p->max_rows * s.ni, qw.Kp);
 			if (need > L.p->scratch_bytes) L.p->scratch_bytes = need;
@@ -986,7 +1181,7 @@ void exec_step(Run &R, const Step &s)
 		a.o = dst(R, s.o);
 		a.orr = s.orr, a.oc = s.oc, a.oj = s.ojj;
 		a.M = R.rows * s.ni;
-		{
+		if (!s.reuse_digits) {
 			Timer t(p, 2);
 			tgk_qgemm_digits(st, &a, p->d_scratch);
 		}
@@ -1005,6 +1200,28 @@ void exec_step(Run &R, const Step &s)
 		tgk_copy(st, dst(R, s.o), s.o.rs, s.dyn_o ? (long)R.t * s.n : 0, resolve(R, s.a), s.dyn_a ? (long)R.t * s.n : 0, s.n,
 			 R.rows);
 		break;
+	case ST_EW: {
+		const EwStep &E = p->ews[(size_t)s.ew];
+		tgk_ew e;
+		memset(&e, 0, sizeof e);
+		e.nin = (int)E.in.size();
+		e.nout = (int)E.out.size();
+		e.nins = (int)E.ins.size();
+		for (int j = 0; j < e.nin; j++) {
+			const tgk_opd x = resolve(R, E.in[(size_t)j].o);
+			e.in[j] = x.p;
+			e.in_rs[j] = x.rs;
+			e.in_mode[j] = E.in[(size_t)j].mode;
+			e.in_map[j] = p->d_imap + E.in[(size_t)j].map;
+		}
+		for (int j = 0; j < e.nout; j++) {
+			e.out[j] = dst(R, E.out[(size_t)j]);
+			e.out_rs[j] = E.out[(size_t)j].rs;
+		}
+		for (int k = 0; k < e.nins; k++) e.ins[k] = E.ins[(size_t)k];
+		tgk_ew_run(st, &e, E.n, R.rows);
+		break;
+	}
 	case ST_SSCAN:
 		tgk_sscan(st, dst(R, s.o), s.o.rs, resolve(R, s.a), resolve(R, s.b), resolve(R, s.e0), resolve(R, s.e1), resolve(R, s.e2),
 			  dst(R, s.e3), s.e3.rs, s.p0, s.p1, s.T, s.reverse, R.rows);
@@ -1129,6 +1346,7 @@ bool build_layer(tg_hip_prog *p)
 	}
 	if (!layer_block(L, &p->m->top)) return false;
 	p->out = value_opnd(L, p->m->output);
+	finish_ew(p);
 	place_arena(p, p->m);
 	if (!upload_pools(p, L.P)) return false;
 	size_t ab = (size_t)(p->arena_floats ? p->arena_floats : 1) * p->max_rows * sizeof(float);

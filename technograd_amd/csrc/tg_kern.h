@@ -23,6 +23,33 @@ void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int
 /* unary op codes are the model op codes (TGM_NEG .. TGM_STEP) */
 void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows);
 
+/* A fused run of elementwise instructions over rows of n elements: inputs are
+ * loaded once into registers, each instruction computes one register, and a
+ * store writes a register to an output. Instruction kinds: TGK_EW_BIN (op one
+ * of TGK_ADD..TGK_MIN on registers a, b), TGK_EW_UN (op a unary TGM_ op on
+ * register a), TGK_EW_STORE (register a to output dst). Input modes are those
+ * of tgk_binary: 0 elementwise, 1 one scalar per row, 2 through an index map;
+ * inputs of mode 0 come first, and input j is loaded into register j. */
+#define TGK_EW_MAXIN 6
+#define TGK_EW_MAXOUT 6
+#define TGK_EW_MAXINS 24
+#define TGK_EW_REGS 8
+enum { TGK_EW_BIN = 1, TGK_EW_UN = 2, TGK_EW_STORE = 3 };
+typedef struct {
+	int kind, op, dst, a, b;
+} tgk_ew_ins;
+typedef struct {
+	const float *in[TGK_EW_MAXIN];
+	long in_rs[TGK_EW_MAXIN];
+	const int *in_map[TGK_EW_MAXIN];
+	int in_mode[TGK_EW_MAXIN];
+	float *out[TGK_EW_MAXOUT];
+	long out_rs[TGK_EW_MAXOUT];
+	tgk_ew_ins ins[TGK_EW_MAXINS];
+	int nin, nout, nins;
+} tgk_ew;
+void tgk_ew_run(hipStream_t s, const tgk_ew *e, int n, int rows);
+
 /* General matmul, one thread per output, products summed in order p = 0..k-1
  * from 0.0f with separate multiply and add (the reference's order): the exact
  * path. o[r][g][i][j] = sum_p A[r][g][i][p] B[r][g][p][j]; quant 1: A is codes

@@ -326,7 +326,7 @@ def ssm_tgir(name="ssm", d_model=256, d_inner=512, n_state=16, dt_rank=16, T=512
             y_t = h @ C_t
         y  = (y + u * D) * silu(z)
         x' = rmsnorm(x + y @ Wo)                     (d_inner -> d_model)
-    and the head: p = mean over t of x (a matmul with a 1/T vector),
+    and the head: p = mean over t of x (pool @ x, pool the 1/T vector),
     softmax(p @ Whead). A = -(1 .. n_state) per channel (A_log = log n), D = 1,
     bdt = softplus^-1(0.01). Every matmul weight is N(0, 0.02), drawn in
     order from one normal(seed) stream, and quantized per output channel on
@@ -375,11 +375,11 @@ def ssm_tgir(name="ssm", d_model=256, d_inner=512, n_state=16, dt_rank=16, T=512
         z = op((T, d_inner), "(matmul %s Wz%d)" % (x, b))
         u = op((T, d_inner), "(silu %s)" % xi)
         dtl = op((T, dt_rank), "(matmul %s Wdtin%d)" % (u, b))
+        Bm = op((T, n_state), "(matmul %s WB%d)" % (u, b))
+        Cm = op((T, n_state), "(matmul %s WC%d)" % (u, b))
         dtp = op((T, d_inner), "(matmul %s Wdt%d)" % (dtl, b))
         dta = op((T, d_inner), "(add %s bdt)" % dtp)
         dt = op((T, d_inner), "(softplus %s)" % dta)
-        Bm = op((T, n_state), "(matmul %s WB%d)" % (u, b))
-        Cm = op((T, n_state), "(matmul %s WC%d)" % (u, b))
         du = op((T, d_inner), "(mul %s %s)" % (dt, u))
         h, dtt, dut, bt, ct = new(), new(), new(), new(), new()
         dtc, da0, da, ha, dbu, hn, yt, ys = (new() for _ in range(8))
@@ -403,8 +403,7 @@ def ssm_tgir(name="ssm", d_model=256, d_inner=512, n_state=16, dt_rank=16, T=512
         o = op((T, d_model), "(matmul %s Wo%d)" % (y2, b))
         r = op((T, d_model), "(add %s %s)" % (x, o))
         x = op((T, d_model), "(rmsnorm %s)" % r)
-    xt = op((d_model, T), "(transpose %s)" % x)
-    p = op((d_model,), "(matmul %s pool)" % xt)
+    p = op((d_model,), "(matmul pool %s)" % x)
     lg = op((classes,), "(matmul %s Whead)" % p)
     out = op((classes,), "(softmax %s)" % lg)
     parts.extend(lines)
