@@ -30,15 +30,21 @@ __device__ inline float bop(int op, float x, float y)
 	}
 }
 
-__global__ void binary_k(int op, float *o, long ors, int n, tgk_opd a, int am, const int *amap, tgk_opd b, int bm, const int *bmap,
-			 long total)
+// operand index of output element i (modes of tgk_binary)
+__device__ inline int bidx(int mode, int i, const int *map, int per)
+{
+	return mode == 0 ? i : mode == 1 ? 0 : mode == 3 ? i % per : map[i];
+}
+
+__global__ void binary_k(int op, float *o, long ors, int n, tgk_opd a, int am, const int *amap, int aper, tgk_opd b, int bm,
+			 const int *bmap, int bper, long total)
 {
 	long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
 	if (t >= total) return;
 	long r = t / n;
 	int i = (int)(t - r * n);
-	int ia = am == 0 ? i : am == 1 ? 0 : amap[i];
-	int ib = bm == 0 ? i : bm == 1 ? 0 : bmap[i];
+	int ia = bidx(am, i, amap, aper);
+	int ib = bidx(bm, i, bmap, bper);
 	o[r * ors + i] = bop(op, a.p[r * a.rs + ia], b.p[r * b.rs + ib]);
 }
 
@@ -80,8 +86,8 @@ __global__ void unary_k(int op, float *o, long ors, tgk_opd a, int n, long total
 constexpr int EPT = 4, ROWK = 512;
 
 template <int OP>
-__global__ __launch_bounds__(256) void binary_rows_k(float *o, long ors, int n, tgk_opd a, int am, const int *amap, tgk_opd b, int bm,
-						     const int *bmap, int cpr)
+__global__ __launch_bounds__(256) void binary_rows_k(float *o, long ors, int n, tgk_opd a, int am, const int *amap, int aper, tgk_opd b,
+						     int bm, const int *bmap, int bper, int cpr)
 {
 	const int r = blockIdx.x / cpr;
 	const int i0 = (blockIdx.x - r * cpr) * (TPB * EPT) + threadIdx.x;
@@ -89,8 +95,8 @@ __global__ __launch_bounds__(256) void binary_rows_k(float *o, long ors, int n, 
 	float x[EPT], y[EPT];
 	for (int j = 0; j < EPT; j++) {
 		const int i = i0 + j * TPB, ic = i < n ? i : n - 1;
-		x[j] = ap[am == 0 ? ic : am == 1 ? 0 : amap[ic]];
-		y[j] = bp[bm == 0 ? ic : bm == 1 ? 0 : bmap[ic]];
+		x[j] = ap[bidx(am, ic, amap, aper)];
+		y[j] = bp[bidx(bm, ic, bmap, bper)];
 	}
 	float *op = o + (long)r * ors;
 	for (int j = 0; j < EPT; j++) {
@@ -180,7 +186,7 @@ __device__ inline void ew_gather(const tgk_ew &E, int j, int r, int i0, int n, f
 	} else {
 		for (int e = 0; e < 4; e++) {
 			const int ic = i0 + e < n ? i0 + e : n - 1;
-			v[e] = p[mode == 0 ? ic : E.in_map[j][ic]];
+			v[e] = p[bidx(mode, ic, E.in_map[j], E.in_per[j])];
 		}
 	}
 }
@@ -191,8 +197,9 @@ __global__ __launch_bounds__(256) void ew_k(tgk_ew E, int n, int cpr)
 	const int r = blockIdx.x / cpr;
 	const int i0 = ((blockIdx.x - r * cpr) * TPB + threadIdx.x) * 4;
 	float reg[TGK_EW_REGS][4];
-	for (int j = 0; j < N0; j++) {
-		const float4 v = *(const float4 *)(E.in[j] + (long)r * E.in_rs[j] + (i0 < n ? i0 : 0));
+	for (int j = 0; j < N0; j++) { // mode 0, or mode 3 with a period that is a multiple of 4
+		const int ic = i0 < n ? i0 : 0;
+		const float4 v = *(const float4 *)(E.in[j] + (long)r * E.in_rs[j] + (E.in_mode[j] == 3 ? ic % E.in_per[j] : ic));
 		reg[j][0] = v.x, reg[j][1] = v.y, reg[j][2] = v.z, reg[j][3] = v.w;
 	}
 	for (int j = N0; j < E.nin; j++) ew_gather(E, j, r, i0, n, reg[j]);
@@ -373,8 +380,8 @@ __global__ void copy_k(float *o, long ors, long ooff, tgk_opd a, long aoff, int 
 
 } // namespace
 
-void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int amode, const int *amap, tgk_opd b, int bmode,
-		const int *bmap, int rows)
+void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int amode, const int *amap, int aper, tgk_opd b, int bmode,
+		const int *bmap, int bper, int rows)
 {
 	long total = (long)rows * n;
 	if (total <= 0) return;
@@ -393,13 +400,13 @@ void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int
 		const unsigned grid = (unsigned)((long)rows * cpr);
 		switch (op) {
 #define BIN(K) \
-	case K: binary_rows_k<K><<<grid, TPB, 0, s>>>(o, ors, n, a, amode, amap, b, bmode, bmap, cpr); break;
+	case K: binary_rows_k<K><<<grid, TPB, 0, s>>>(o, ors, n, a, amode, amap, aper, b, bmode, bmap, bper, cpr); break;
 			BIN(TGK_ADD) BIN(TGK_SUB) BIN(TGK_MUL) BIN(TGK_DIV) BIN(TGK_MAX) BIN(TGK_MIN)
 #undef BIN
 		default: break;
 		}
 	} else
-		binary_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, n, a, amode, amap, b, bmode, bmap, total);
+		binary_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, n, a, amode, amap, aper, b, bmode, bmap, bper, total);
 }
 
 void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows)
@@ -436,8 +443,8 @@ void tgk_ew_run(hipStream_t s, const tgk_ew *e, int n, int rows)
 {
 	if (rows <= 0 || n <= 0 || e->nin < 1 || e->nin > TGK_EW_MAXIN) return;
 	bool vec = n % 4 == 0;
-	int n0 = 0; // leading elementwise inputs
-	while (n0 < e->nin && e->in_mode[n0] == 0) n0++;
+	int n0 = 0; // leading inputs that load as float4
+	while (n0 < e->nin && (e->in_mode[n0] == 0 || (e->in_mode[n0] == 3 && e->in_per[n0] % 4 == 0))) n0++;
 	for (int j = 0; j < n0; j++) vec = vec && ((size_t)e->in[j] & 15) == 0 && e->in_rs[j] % 4 == 0;
 	for (int j = 0; j < e->nout; j++) vec = vec && ((size_t)e->out[j] & 15) == 0 && e->out_rs[j] % 4 == 0;
 	const int cpr = (n + TPB * 4 - 1) / (TPB * 4);

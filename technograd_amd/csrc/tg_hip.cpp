@@ -408,6 +408,20 @@ void place_arena(tg_hip_prog *p, const tgm_module *m)
 
 bool layer_block(LB &L, const tgm_block *b);
 
+// Operand shape sa broadcast to so by repeating it whole (sa, leading 1s
+// dropped, is a suffix of so): element e reads e mod numel(sa). Such operands
+// take mode 3 (period numel(sa)) instead of an index map.
+bool suffix_broadcast(const tgm_shape &so, const tgm_shape &sa)
+{
+	int lo = 0;
+	while (lo < sa.rank && sa.dim[lo] == 1) lo++;
+	const int ra = sa.rank - lo;
+	if (ra > so.rank) return false;
+	for (int i = 0; i < ra; i++)
+		if (sa.dim[lo + i] != so.dim[so.rank - ra + i]) return false;
+	return true;
+}
+
 // Adds one elementwise instruction, to the fused run the previous step holds
 // when it can (same row length, room left, operands that the run computed
 // read elementwise), else to a new run. The run's inputs plus its results
@@ -422,7 +436,7 @@ void ew_append(LB &L, int kind, int op, const Opnd &a, int amode, long amap, con
 	};
 	auto input = [](const EwStep &E, const Opnd &x, int mode, long map) {
 		for (size_t j = 0; j < E.in.size(); j++)
-			if (same_value(E.in[j].o, x) && E.in[j].o.rs == x.rs && E.in[j].mode == mode && (mode != 2 || E.in[j].map == map))
+			if (same_value(E.in[j].o, x) && E.in[j].o.rs == x.rs && E.in[j].mode == mode && E.in[j].map == map)
 				return (int)j;
 		return -1;
 	};
@@ -437,7 +451,7 @@ void ew_append(LB &L, int kind, int op, const Opnd &a, int amode, long amap, con
 		for (int j = 0; j < nops; j++) {
 			const int k = local(E, *opd[j]);
 			if (k >= 0 && mode[j] != 0) fits = false;
-			if (k < 0 && input(E, *opd[j], mode[j], map[j]) < 0 && !(j == 1 && same_value(a, b) && a.rs == b.rs && amode == bmode && (amode != 2 || amap == bmap)))
+			if (k < 0 && input(E, *opd[j], mode[j], map[j]) < 0 && !(j == 1 && same_value(a, b) && a.rs == b.rs && amode == bmode && amap == bmap))
 				new_in++;
 		}
 		fits = fits && E.n == n && (int)E.in.size() + new_in <= TGK_EW_MAXIN &&
@@ -510,12 +524,13 @@ void finish_ew(tg_hip_prog *p)
 	for (EwStep &E : p->ews) {
 		if (E.ops.empty()) continue;
 		const int nin = (int)E.in.size(), nop = (int)E.ops.size();
-		// elementwise inputs first
+		// elementwise inputs first, then whole-row repeats of a multiple of 4
+		// elements (both load as float4), then the rest
 		std::vector<int> order, pos(nin);
-		for (int j = 0; j < nin; j++)
-			if (E.in[j].mode == 0) order.push_back(j);
-		for (int j = 0; j < nin; j++)
-			if (E.in[j].mode != 0) order.push_back(j);
+		auto cls = [&](int j) { return E.in[j].mode == 0 ? 0 : E.in[j].mode == 3 && E.in[j].map % 4 == 0 ? 1 : 2; };
+		for (int c = 0; c < 3; c++)
+			for (int j = 0; j < nin; j++)
+				if (cls(j) == c) order.push_back(j);
 		std::vector<EwStep::In> in2;
 		for (int j = 0; j < nin; j++) {
 			pos[order[j]] = j;
@@ -652,7 +667,17 @@ bool layer_ins(LB &L, const tgm_ins &in)
 		int amode, bmode;
 		long amap, bmap;
 		bcast(m->val[in.out].sh, m->val[in.a[0]].sh, L.P.imap, amode, amap);
+		if (amode == 2 && suffix_broadcast(m->val[in.out].sh, m->val[in.a[0]].sh)) {
+			L.P.imap.resize((size_t)amap); // the map just added is not needed
+			amode = 3;
+			amap = m->val[in.a[0]].n;
+		}
 		bcast(m->val[in.out].sh, m->val[in.a[1]].sh, L.P.imap, bmode, bmap);
+		if (bmode == 2 && suffix_broadcast(m->val[in.out].sh, m->val[in.a[1]].sh)) {
+			L.P.imap.resize((size_t)bmap);
+			bmode = 3;
+			bmap = m->val[in.a[1]].n;
+		}
 		ew_append(L, TGK_EW_BIN, in.op - TGM_ADD, value_opnd(L, in.a[0]), amode, amap, value_opnd(L, in.a[1]), bmode, bmap,
 			  value_opnd(L, in.out), (int)m->val[in.out].n);
 		return true;
@@ -1153,8 +1178,9 @@ void exec_step(Run &R, const Step &s)
 	hipStream_t st = p->st;
 	switch (s.kind) {
 	case ST_BIN:
-		tgk_binary(st, s.op, dst(R, s.o), s.o.rs, s.n, resolve(R, s.a), s.amode, p->d_imap + s.amap, resolve(R, s.b), s.bmode,
-			   p->d_imap + s.bmap, R.rows);
+		tgk_binary(st, s.op, dst(R, s.o), s.o.rs, s.n, resolve(R, s.a), s.amode, p->d_imap + (s.amode == 2 ? s.amap : 0),
+			   s.amode == 3 ? (int)s.amap : 1, resolve(R, s.b), s.bmode, p->d_imap + (s.bmode == 2 ? s.bmap : 0),
+			   s.bmode == 3 ? (int)s.bmap : 1, R.rows);
 		break;
 	case ST_UN: tgk_unary(st, s.op, dst(R, s.o), s.o.rs, resolve(R, s.a), s.n, R.rows); break;
 	case ST_MM: {
@@ -1212,7 +1238,8 @@ void exec_step(Run &R, const Step &s)
 			e.in[j] = x.p;
 			e.in_rs[j] = x.rs;
 			e.in_mode[j] = E.in[(size_t)j].mode;
-			e.in_map[j] = p->d_imap + E.in[(size_t)j].map;
+			e.in_map[j] = E.in[(size_t)j].mode == 2 ? p->d_imap + E.in[(size_t)j].map : p->d_imap;
+			e.in_per[j] = E.in[(size_t)j].mode == 3 ? (int)E.in[(size_t)j].map : 1;
 		}
 		for (int j = 0; j < e.nout; j++) {
 			e.out[j] = dst(R, E.out[(size_t)j]);

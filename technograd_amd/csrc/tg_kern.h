@@ -17,9 +17,10 @@ typedef struct {
 
 enum { TGK_ADD, TGK_SUB, TGK_MUL, TGK_DIV, TGK_MAX, TGK_MIN };
 
-/* o[r, i] = a[r, ia(i)] (op) b[r, ib(i)]; ia(i) = i, 0 or amap[i] (amode 0, 1, 2) */
-void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int amode, const int *amap, tgk_opd b, int bmode,
-		const int *bmap, int rows);
+/* o[r, i] = a[r, ia(i)] (op) b[r, ib(i)]; ia(i) = i, 0, amap[i] or i mod aper
+ * (amode 0, 1, 2, 3) */
+void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int amode, const int *amap, int aper, tgk_opd b, int bmode,
+		const int *bmap, int bper, int rows);
 /* unary op codes are the model op codes (TGM_NEG .. TGM_STEP) */
 void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows);
 
@@ -28,8 +29,10 @@ void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int 
  * store writes a register to an output. Instruction kinds: TGK_EW_BIN (op one
  * of TGK_ADD..TGK_MIN on registers a, b), TGK_EW_UN (op a unary TGM_ op on
  * register a), TGK_EW_STORE (register a to output dst). Input modes are those
- * of tgk_binary: 0 elementwise, 1 one scalar per row, 2 through an index map;
- * inputs of mode 0 come first, and input j is loaded into register j. */
+ * of tgk_binary: 0 elementwise, 1 one scalar per row, 2 through an index map,
+ * 3 whole-row repeats (element i mod in_per). Inputs of mode 0, then those of
+ * mode 3 with in_per a multiple of 4, come first; input j is loaded into
+ * register j. */
 #define TGK_EW_MAXIN 6
 #define TGK_EW_MAXOUT 6
 #define TGK_EW_MAXINS 24
@@ -43,6 +46,7 @@ typedef struct {
 	long in_rs[TGK_EW_MAXIN];
 	const int *in_map[TGK_EW_MAXIN];
 	int in_mode[TGK_EW_MAXIN];
+	int in_per[TGK_EW_MAXIN]; /* mode 3: input element i mod in_per */
 	float *out[TGK_EW_MAXOUT];
 	long out_rs[TGK_EW_MAXOUT];
 	tgk_ew_ins ins[TGK_EW_MAXINS];
