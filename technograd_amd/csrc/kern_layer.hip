@@ -6,7 +6,9 @@
 // operation: the same expression shapes, sums in index order from 0.0f,
 // separate multiply and add (this file is compiled with -ffp-contract=off),
 // correctly rounded division and square root. Transcendentals come from the
-// ROCm device library, so only they differ from glibc (by a few ulp).
+// ROCm device library, so only they differ from glibc (by a few ulp); the
+// log1pf of softplus is this backend's own (tg_devmath.h), correctly rounded.
+#include "tg_devmath.h"
 #include "tg_kern.h"
 #include "tgm.h"
 
@@ -60,7 +62,7 @@ __device__ inline float uop(int op, float x)
 	case TGM_SQRT: return sqrtf(x);
 	case TGM_GELU: return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
 	case TGM_SILU: return x / (1.0f + expf(-x));
-	case TGM_SOFTPLUS: return (x > 0.0f ? x : 0.0f) + log1pf(expf(-fabsf(x)));
+	case TGM_SOFTPLUS: return (x > 0.0f ? x : 0.0f) + tg_log1p_unit(expf(-fabsf(x)));
 	case TGM_LOG: return logf(x);
 	case TGM_SIN: return sinf(x);
 	case TGM_COS: return cosf(x);
@@ -167,15 +169,17 @@ __global__ __launch_bounds__(256) void unary_rows4_k(float *o, long ors, tgk_opd
 inline bool al16(const void *p, long rs) { return ((size_t)p & 15) == 0 && rs % 4 == 0; }
 
 // A fused elementwise run (tgk_ew): four consecutive elements per thread.
-// The N0 elementwise inputs (the first ones) are loaded as straight-line
-// float4 loads, all in flight together, then the others (a scalar per row,
-// or through an index map). The instruction list, the same for every
-// thread, then works on a small register file indexed by block-uniform
-// register numbers. Each instruction is the operation of binary_k or unary_k,
-// so the stored values are bit-identical to running the instructions one
-// launch at a time. VEC: elementwise inputs and all outputs are 16-byte
-// aligned rows and n is a multiple of 4; otherwise N0 is 0 and every input
-// takes the general path.
+// The N0 elementwise (or aligned whole-row repeat) inputs, the first ones, are
+// loaded as straight-line float4 loads, all in flight together, then the
+// others. The instruction list, the same for every thread, drives an
+// accumulator (a float4 in VGPRs); the register file lives in LDS, one
+// 16-byte slot per register and thread, which only that thread touches (no
+// barriers). Kept in VGPRs, a register file indexed by run-time register
+// numbers is copied whole at every loop iteration. Each instruction is the
+// operation of binary_k or unary_k, so the stored values are bit-identical to
+// running the instructions one launch at a time. VEC: the float4 inputs and
+// all outputs are 16-byte aligned rows and n is a multiple of 4; otherwise N0
+// is 0 and every input takes the general path.
 __device__ inline void ew_gather(const tgk_ew &E, int j, int r, int i0, int n, float *v)
 {
 	const float *p = E.in[j] + (long)r * E.in_rs[j];
@@ -194,29 +198,67 @@ __device__ inline void ew_gather(const tgk_ew &E, int j, int r, int i0, int n, f
 template <int N0, bool VEC>
 __global__ __launch_bounds__(256) void ew_k(tgk_ew E, int n, int cpr)
 {
+	__shared__ float4 R[TGK_EW_REGS][TPB];
 	const int r = blockIdx.x / cpr;
 	const int i0 = ((blockIdx.x - r * cpr) * TPB + threadIdx.x) * 4;
-	float reg[TGK_EW_REGS][4];
+	float4 v0[N0 > 0 ? N0 : 1];
 	for (int j = 0; j < N0; j++) { // mode 0, or mode 3 with a period that is a multiple of 4
-		const int ic = i0 < n ? i0 : 0;
-		const float4 v = *(const float4 *)(E.in[j] + (long)r * E.in_rs[j] + (E.in_mode[j] == 3 ? ic % E.in_per[j] : ic));
-		reg[j][0] = v.x, reg[j][1] = v.y, reg[j][2] = v.z, reg[j][3] = v.w;
+		int idx = i0 < n ? i0 : 0;
+		if (E.in_mode[j] == 3) {
+			// idx mod per from a float quotient estimate: with fewer than 2^22
+			// repeats the estimate is off by at most one, which the two
+			// corrections absorb
+			const int per = E.in_per[j];
+			const int q = (int)((float)idx * E.in_inv[j]);
+			int rr = idx - q * per;
+			rr = rr < 0 ? rr + per : rr;
+			idx = rr >= per ? rr - per : rr;
+		}
+		v0[j] = *(const float4 *)(E.in[j] + (long)r * E.in_rs[j] + idx);
 	}
-	for (int j = N0; j < E.nin; j++) ew_gather(E, j, r, i0, n, reg[j]);
+	for (int j = 0; j < N0; j++) R[j][threadIdx.x] = v0[j];
+	for (int j = N0; j < TGK_EW_MAXIN; j++) // argument indices stay compile-time constants
+		if (j < E.nin) {
+			float g[4];
+			ew_gather(E, j, r, i0, n, g);
+			R[j][threadIdx.x] = make_float4(g[0], g[1], g[2], g[3]);
+		}
+	float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 	for (int k = 0; k < E.nins; k++) {
 		const tgk_ew_ins I = E.ins[k];
-		if (I.kind == TGK_EW_BIN) {
-			for (int e = 0; e < 4; e++) reg[I.dst][e] = bop(I.op, reg[I.a][e], reg[I.b][e]);
-		} else if (I.kind == TGK_EW_UN) {
-			for (int e = 0; e < 4; e++) reg[I.dst][e] = uop(I.op, reg[I.a][e]);
-		} else {
+		switch (I.kind) {
+		case TGK_EW_LOAD: acc = R[I.a][threadIdx.x]; break;
+		case TGK_EW_SAVE: R[I.dst][threadIdx.x] = acc; break;
+		case TGK_EW_BIN: case TGK_EW_BINR: {
+			const float4 o = R[I.a][threadIdx.x];
+			const float4 x = I.kind == TGK_EW_BIN ? acc : o, y = I.kind == TGK_EW_BIN ? o : acc;
+			switch (I.op) { // the op outside the element loop: each case is straight-line code
+#define EWB(K) \
+	case K: acc = make_float4(bop(K, x.x, y.x), bop(K, x.y, y.y), bop(K, x.z, y.z), bop(K, x.w, y.w)); break;
+				EWB(TGK_ADD) EWB(TGK_SUB) EWB(TGK_MUL) EWB(TGK_DIV) EWB(TGK_MAX) EWB(TGK_MIN)
+#undef EWB
+			}
+			break;
+		}
+		case TGK_EW_UN:
+			switch (I.op) {
+#define EWU(K) \
+	case K: acc = make_float4(uop(K, acc.x), uop(K, acc.y), uop(K, acc.z), uop(K, acc.w)); break;
+				EWU(TGM_NEG) EWU(TGM_TANH) EWU(TGM_RELU) EWU(TGM_SIGMOID) EWU(TGM_EXP) EWU(TGM_SQRT) EWU(TGM_GELU)
+				EWU(TGM_SILU) EWU(TGM_SOFTPLUS) EWU(TGM_LOG) EWU(TGM_SIN) EWU(TGM_COS) EWU(TGM_FLOOR) EWU(TGM_STEP)
+#undef EWU
+			}
+			break;
+		default: { // TGK_EW_STORE
 			float *p = E.out[I.dst] + (long)r * E.out_rs[I.dst];
 			if (VEC) {
-				if (i0 < n) *(float4 *)(p + i0) = make_float4(reg[I.a][0], reg[I.a][1], reg[I.a][2], reg[I.a][3]);
+				if (i0 < n) *(float4 *)(p + i0) = acc;
 			} else {
+				const float a4[4] = { acc.x, acc.y, acc.z, acc.w };
 				for (int e = 0; e < 4; e++)
-					if (i0 + e < n) p[i0 + e] = reg[I.a][e];
+					if (i0 + e < n) p[i0 + e] = a4[e];
 			}
+		}
 		}
 	}
 }
@@ -444,7 +486,8 @@ void tgk_ew_run(hipStream_t s, const tgk_ew *e, int n, int rows)
 	if (rows <= 0 || n <= 0 || e->nin < 1 || e->nin > TGK_EW_MAXIN) return;
 	bool vec = n % 4 == 0;
 	int n0 = 0; // leading inputs that load as float4
-	while (n0 < e->nin && (e->in_mode[n0] == 0 || (e->in_mode[n0] == 3 && e->in_per[n0] % 4 == 0))) n0++;
+	while (n0 < e->nin && (e->in_mode[n0] == 0 || (e->in_mode[n0] == 3 && e->in_per[n0] % 4 == 0 && n / e->in_per[n0] < (1 << 22))))
+		n0++;
 	for (int j = 0; j < n0; j++) vec = vec && ((size_t)e->in[j] & 15) == 0 && e->in_rs[j] % 4 == 0;
 	for (int j = 0; j < e->nout; j++) vec = vec && ((size_t)e->out[j] & 15) == 0 && e->out_rs[j] % 4 == 0;
 	const int cpr = (n + TPB * 4 - 1) / (TPB * 4);

@@ -290,6 +290,13 @@ __device__ inline long long combine(int acc0, int acc1, int acc2)
 	return (long long)acc0 + (long long)acc1 * 256 + (long long)acc2 * 65536;
 }
 
+// the same sum in f64, also exact: every term and partial sum is an integer
+// below 2^48 in magnitude (int32 digit sums times at most 2^16)
+__device__ inline double combine_d(int acc0, int acc1, int acc2)
+{
+	return (double)acc0 + (double)acc1 * 256.0 + (double)acc2 * 65536.0;
+}
+
 // output (m, c) from tot = sum_k t[c][k] q[m][k]
 __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot)
 {
@@ -314,9 +321,9 @@ __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 // special row (the common case) takes a straight-line path that reads each
 // row's exponent and sum once and each column's scale once; otherwise every
 // output goes through epilogue().
-template <int NB, class Tot>
+template <int NB, class Tot, class TotD>
 __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int mbase, int cbase, int lane,
-				  Tot tot)
+				  Tot tot, TotD totd)
 {
 	const int r32 = lane & 31, h = lane >> 5;
 	int sp = 0;
@@ -340,13 +347,14 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 		const int m = mbase + 8 * (v >> 2) + 4 * h + (v & 3);
 		if (m >= a.M) continue;
 		const int E = s.e[m];
-		const long long q8 = w.bits == 4 ? 8 * s.qsum[m] : 0;
+		// f64 arithmetic on integers below 2^53: (double)(tot - 8 qsum) exactly
+		const double q8 = w.bits == 4 ? 8.0 * (double)s.qsum[m] : 0.0;
 		int r = m, jj = 0;
 		if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
 		float *orow = a.o + (long)r * a.orr + (long)jj * a.oj;
 		for (int j = 0; j < NB; j++) {
 			if (cbase + j * 32 + r32 >= w.C) continue;
-			orow[coff[j]] = sc[j] * (float)ldexp((double)(tot(j, v) - q8), E - 23);
+			orow[coff[j]] = sc[j] * (float)ldexp(totd(j, v) - q8, E - 23);
 		}
 	}
 }
@@ -492,8 +500,9 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 		bar();
 	}
 	if (g == 0) bar(); // both groups pass the same number of barriers
-	store_tile<4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane,
-		      [&](int j, int v) { return combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]); });
+	store_tile<4>(
+		a, w, s, m0 + wm * 32, c0 + g * 128, lane, [&](int j, int v) { return combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]); },
+		[&](int j, int v) { return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]); });
 }
 
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
@@ -583,11 +592,12 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 		__syncthreads();
 		if (wave != 0) return;
 	}
-	store_tile<NB>(a, w, s, m0, c0, lane, [&](int j, int v) {
-		long long tot = combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
-		for (int u = 0; u < W - 1; u++) tot += red[((u * NB + j) * 16 + v) * 64 + lane];
-		return tot;
-	});
+	auto tot = [&](int j, int v) {
+		long long t = combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+		for (int u = 0; u < W - 1; u++) t += red[((u * NB + j) * 16 + v) * 64 + lane];
+		return t;
+	};
+	store_tile<NB>(a, w, s, m0, c0, lane, tot, [&](int j, int v) { return (double)tot(j, v); });
 }
 
 template <int BITS, int NB, int W>

@@ -16,6 +16,7 @@
 // Q16.16 results are bit-exact with the reference, including its tg_fdiv
 // rounding for negative divisors (the half-divisor is added on the side that
 // makes the quotient's magnitude one smaller for most inputs).
+#include "tg_devmath.h"
 #include "tg_kern.h"
 #include "tgm.h"
 
@@ -186,7 +187,7 @@ __device__ inline float unf(int op, float x)
 	case TGM_SQRT: return sqrtf(x);
 	case TGM_GELU: return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
 	case TGM_SILU: return x / (1.0f + expf(-x));
-	case TGM_SOFTPLUS: return (x > 0.0f ? x : 0.0f) + log1pf(expf(-fabsf(x)));
+	case TGM_SOFTPLUS: return (x > 0.0f ? x : 0.0f) + tg_log1p_unit(expf(-fabsf(x)));
 	case TGM_LOG: return logf(x);
 	case TGM_SIN: return sinf(x);
 	case TGM_COS: return cosf(x);

@@ -1,0 +1,46 @@
+// Device math routines of this backend's own, written from the mathematics.
+// The header also compiles as plain C++ so the routines can be checked on the
+// host against the C library (tests/test_host.py builds it with g++).
+#pragma once
+
+#include <math.h>
+
+#ifdef __HIPCC__
+#define TG_HD __host__ __device__
+#else
+#define TG_HD
+#endif
+
+// log(1 + y) for y in [0, 1] (and NaN), rounded once to f32: the argument of
+// softplus's log1pf(expf(-|x|)) is always in that range. Evaluated in f64,
+// which issues at the f32 rate on CDNA, instead of the library's compensated
+// f32 log1pf:
+//   with u = 1 + y, f = u - 1 is y itself when u <= sqrt(2); above, u is
+//   halved and ln 2 added, f = (y - 1) / 2 (exact in f64), so u = 1 + f lies
+//   in [sqrt(2)/2, sqrt(2)]. With s = f / (2 + f),
+//   |s| <= 0.1716, log u = 2 atanh(s) = 2 s (1 + z/3 + z^2/5 + ... + z^9/19)
+//   with z = s^2 <= 0.0295; the first omitted term is below 3e-17 of the
+//   result, so the f64 value is within a few 1e-16 of log(1 + y) and its f32
+//   rounding is the correctly rounded log1pf(y) except within that distance
+//   of a rounding boundary.
+TG_HD inline float tg_log1p_unit(float y)
+{
+	double f = (double)y, k = 0.0;
+	if (f > 0.41421356237309503) {
+		f = (f - 1.0) * 0.5;
+		k = 1.0;
+	}
+	const double s = f / (2.0 + f);
+	const double z = s * s;
+	double p = 1.0 / 19; // Horner steps as fused multiply-adds, the same on host and device
+	p = fma(p, z, 1.0 / 17);
+	p = fma(p, z, 1.0 / 15);
+	p = fma(p, z, 1.0 / 13);
+	p = fma(p, z, 1.0 / 11);
+	p = fma(p, z, 1.0 / 9);
+	p = fma(p, z, 1.0 / 7);
+	p = fma(p, z, 1.0 / 5);
+	p = fma(p, z, 1.0 / 3);
+	p = fma(p, z, 1.0);
+	return (float)(k * 0.6931471805599453 + 2.0 * s * p);
+}

@@ -527,7 +527,9 @@ void finish_ew(tg_hip_prog *p)
 		// elementwise inputs first, then whole-row repeats of a multiple of 4
 		// elements (both load as float4), then the rest
 		std::vector<int> order, pos(nin);
-		auto cls = [&](int j) { return E.in[j].mode == 0 ? 0 : E.in[j].mode == 3 && E.in[j].map % 4 == 0 ? 1 : 2; };
+		auto cls = [&](int j) {
+			return E.in[j].mode == 0 ? 0 : E.in[j].mode == 3 && E.in[j].map % 4 == 0 && E.n / E.in[j].map < (1 << 22) ? 1 : 2;
+		};
 		for (int c = 0; c < 3; c++)
 			for (int j = 0; j < nin; j++)
 				if (cls(j) == c) order.push_back(j);
@@ -537,43 +539,57 @@ void finish_ew(tg_hip_prog *p)
 			in2.push_back(E.in[order[j]]);
 		}
 		E.in = in2;
-		auto remap = [&](int id) { return id < EwStep::LOCAL ? pos[id] : id; };
-		// last reader of each local value
-		std::vector<int> last_in(nin, -1), last_op(nop, -1);
-		for (int k = 0; k < nop; k++) {
-			EwStep::Op &q = E.ops[k];
-			q.a = remap(q.a);
-			if (q.kind == TGK_EW_BIN) q.b = remap(q.b);
-			for (int id : { q.a, q.kind == TGK_EW_BIN ? q.b : q.a }) {
-				if (id < EwStep::LOCAL) last_in[id] = k;
-				else last_op[id - EwStep::LOCAL] = k;
-			}
-		}
-		std::vector<int> reg_of_op(nop, -1), busy(TGK_EW_REGS, 0);
-		for (int j = 0; j < nin; j++) busy[j] = 1; // input j is loaded into register j
-		E.ins.clear();
-		E.out.clear();
-		auto reg = [&](int id) { return id < EwStep::LOCAL ? id : reg_of_op[id - EwStep::LOCAL]; };
+		// local values densely: input j is j, the result of op k is nin + k
+		auto dense = [&](int id) { return id < EwStep::LOCAL ? pos[id] : nin + (id - EwStep::LOCAL); };
+		std::vector<int> lastd(nin + nop, -1); // last op reading each value
 		for (int k = 0; k < nop; k++) {
 			const EwStep::Op &q = E.ops[k];
-			tgk_ew_ins I{ q.kind, q.op, -1, reg(q.a), q.kind == TGK_EW_BIN ? reg(q.b) : 0 };
-			// operands read for the last time here free their registers (the
-			// kernel reads both operands of an element before writing it)
-			for (int id : { q.a, q.kind == TGK_EW_BIN ? q.b : q.a }) {
-				const int lu = id < EwStep::LOCAL ? last_in[id] : last_op[id - EwStep::LOCAL];
-				if (lu == k) busy[reg(id)] = 0;
-			}
+			lastd[dense(q.a)] = k;
+			if (q.kind == TGK_EW_BIN) lastd[dense(q.b)] = k;
+		}
+		// Linearise for the accumulator machine. A value leaves the accumulator
+		// for a register (SAVE) only when it is read again later; inputs start
+		// in registers 0 .. nin - 1. The append limits (inputs + ops within the
+		// register file) guarantee a free register whenever one is needed.
+		std::vector<int> rg(nin + nop, -1), busy(TGK_EW_REGS, 0);
+		for (int j = 0; j < nin; j++) rg[j] = j, busy[j] = 1;
+		int acc = -1;
+		E.ins.clear();
+		E.out.clear();
+		auto keep = [&](int v) { // v (in the accumulator) is read again after this op: give it a register
+			if (rg[v] >= 0) return;
 			int r = 0;
-			while (busy[r]) r++; // the append limits guarantee a free register
+			while (busy[r]) r++;
 			busy[r] = 1;
-			I.dst = r;
-			reg_of_op[k] = r;
-			E.ins.push_back(I);
+			rg[v] = r;
+			E.ins.push_back({ TGK_EW_SAVE, 0, r, 0, 0 });
+		};
+		for (int k = 0; k < nop; k++) {
+			for (int v = 0; v < nin + nop; v++) // registers of values no longer read
+				if (rg[v] >= 0 && lastd[v] < k) busy[rg[v]] = 0, rg[v] = -1;
+			const EwStep::Op &q = E.ops[k];
+			const int a = dense(q.a), b = q.kind == TGK_EW_BIN ? dense(q.b) : -1;
+			if (q.kind == TGK_EW_UN || (a != acc && b != acc)) { // the first operand goes to the accumulator
+				if (a != acc) {
+					if (acc >= 0 && lastd[acc] >= k) keep(acc);
+					E.ins.push_back({ TGK_EW_LOAD, 0, 0, rg[a], 0 });
+					acc = a;
+				}
+				if (lastd[a] > k || (b == a)) keep(a);
+				if (q.kind == TGK_EW_UN) E.ins.push_back({ TGK_EW_UN, q.op, 0, 0, 0 });
+				else E.ins.push_back({ TGK_EW_BIN, q.op, 0, rg[b], 0 });
+			} else if (a == acc) { // acc = acc op b
+				if (lastd[a] > k || b == a) keep(a);
+				E.ins.push_back({ TGK_EW_BIN, q.op, 0, rg[b], 0 });
+			} else { // b in the accumulator: acc = a op acc
+				if (lastd[b] > k) keep(b);
+				E.ins.push_back({ TGK_EW_BINR, q.op, 0, rg[a], 0 });
+			}
+			acc = nin + k;
 			if (read_outside(q.o)) {
-				E.ins.push_back({ TGK_EW_STORE, 0, (int)E.out.size(), r, 0 });
+				E.ins.push_back({ TGK_EW_STORE, 0, (int)E.out.size(), 0, 0 });
 				E.out.push_back(q.o);
 			}
-			if (last_op[k] < 0) busy[r] = 0; // not read again inside the run
 		}
 	}
 }
@@ -1240,6 +1256,7 @@ void exec_step(Run &R, const Step &s)
 			e.in_mode[j] = E.in[(size_t)j].mode;
 			e.in_map[j] = E.in[(size_t)j].mode == 2 ? p->d_imap + E.in[(size_t)j].map : p->d_imap;
 			e.in_per[j] = E.in[(size_t)j].mode == 3 ? (int)E.in[(size_t)j].map : 1;
+			e.in_inv[j] = 1.0f / (float)e.in_per[j];
 		}
 		for (int j = 0; j < e.nout; j++) {
 			e.out[j] = dst(R, E.out[(size_t)j]);

@@ -24,20 +24,22 @@ void tgk_binary(hipStream_t s, int op, float *o, long ors, int n, tgk_opd a, int
 /* unary op codes are the model op codes (TGM_NEG .. TGM_STEP) */
 void tgk_unary(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows);
 
-/* A fused run of elementwise instructions over rows of n elements: inputs are
- * loaded once into registers, each instruction computes one register, and a
- * store writes a register to an output. Instruction kinds: TGK_EW_BIN (op one
- * of TGK_ADD..TGK_MIN on registers a, b), TGK_EW_UN (op a unary TGM_ op on
- * register a), TGK_EW_STORE (register a to output dst). Input modes are those
+/* A fused run of elementwise instructions over rows of n elements, as an
+ * accumulator machine: inputs are loaded once into registers, and each
+ * instruction works on the accumulator. Kinds: TGK_EW_LOAD (acc = register a),
+ * TGK_EW_SAVE (register dst = acc), TGK_EW_BIN (acc = acc op register a, op
+ * one of TGK_ADD..TGK_MIN), TGK_EW_BINR (acc = register a op acc), TGK_EW_UN
+ * (acc = op(acc), op a unary TGM_ op), TGK_EW_STORE (output dst = acc). Input
+ * modes are those
  * of tgk_binary: 0 elementwise, 1 one scalar per row, 2 through an index map,
  * 3 whole-row repeats (element i mod in_per). Inputs of mode 0, then those of
- * mode 3 with in_per a multiple of 4, come first; input j is loaded into
- * register j. */
+ * mode 3 with in_per a multiple of 4 (and fewer than 2^22 repeats in a row),
+ * come first; input j is loaded into register j. */
 #define TGK_EW_MAXIN 6
 #define TGK_EW_MAXOUT 6
 #define TGK_EW_MAXINS 24
 #define TGK_EW_REGS 8
-enum { TGK_EW_BIN = 1, TGK_EW_UN = 2, TGK_EW_STORE = 3 };
+enum { TGK_EW_BIN = 1, TGK_EW_UN = 2, TGK_EW_STORE = 3, TGK_EW_LOAD = 4, TGK_EW_SAVE = 5, TGK_EW_BINR = 6 };
 typedef struct {
 	int kind, op, dst, a, b;
 } tgk_ew_ins;
@@ -46,7 +48,8 @@ typedef struct {
 	long in_rs[TGK_EW_MAXIN];
 	const int *in_map[TGK_EW_MAXIN];
 	int in_mode[TGK_EW_MAXIN];
-	int in_per[TGK_EW_MAXIN]; /* mode 3: input element i mod in_per */
+	int in_per[TGK_EW_MAXIN];   /* mode 3: input element i mod in_per */
+	float in_inv[TGK_EW_MAXIN]; /* mode 3: 1 / in_per, for the quotient estimate */
 	float *out[TGK_EW_MAXOUT];
 	long out_rs[TGK_EW_MAXOUT];
 	tgk_ew_ins ins[TGK_EW_MAXINS];
