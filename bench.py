@@ -133,7 +133,7 @@ def pmc_run(counter, outdir):
                 name = row["Kernel_Name"]
                 if "qgemm_k<4>" in name:
                     vals["qgemm"].append(float(row["Counter_Value"]))
-                elif "binary_k" in name and int(row.get("Grid_Size", 0) or 0) >= FLUSH_ROWS * FLUSH_COLS // 4:
+                elif "binary" in name and int(row.get("Grid_Size", 0) or 0) >= FLUSH_ROWS * FLUSH_COLS // 16:
                     vals["flush"].append(float(row["Counter_Value"]))
     if not vals["qgemm"] or not vals["flush"]:
         log("rocprofv3 --pmc %s: kernels not found in %s" % (counter, files))

@@ -411,6 +411,140 @@ def ssm_tgir(name="ssm", d_model=256, d_inner=512, n_state=16, dt_rank=16, T=512
     return "".join(parts)
 
 
+def qwen3_weights(L, D, NQ, NKV, HD, FF, V, seed=3, sigma=0.02):
+    """Random-init weights of a Qwen3-shaped decoder, drawn in order from one
+    normal(seed, sigma) stream: E [V, D], then per layer Wq_h (D, HD) for the
+    NQ query heads, Wk_j and Wv_j (D, HD) for the NKV KV heads, Wo_h (HD, D),
+    Wg and Wu (D, FF), Wd (FF, D). RMSNorm gains are 1 (the usual init) and
+    the LM head is E transposed (tied embeddings, examples/qwen3/import.py:49)."""
+    shapes = [("E", (V, D))]
+    for l in range(L):
+        shapes += [("Wq_%d_%d" % (l, h), (D, HD)) for h in range(NQ)]
+        shapes += [("Wk_%d_%d" % (l, j), (D, HD)) for j in range(NKV)]
+        shapes += [("Wv_%d_%d" % (l, j), (D, HD)) for j in range(NKV)]
+        shapes += [("Wo_%d_%d" % (l, h), (HD, D)) for h in range(NQ)]
+        shapes += [("Wg_%d" % l, (D, FF)), ("Wu_%d" % l, (D, FF)), ("Wd_%d" % l, (FF, D))]
+    total = sum(r * c for _, (r, c) in shapes)
+    stream = normal(seed, sigma, total)
+    w, off = {}, 0
+    for nm, (r, c) in shapes:
+        w[nm] = stream[off:off + r * c].reshape(r, c)
+        off += r * c
+    return w
+
+
+def rope_tables(T, HD, theta=1e6):
+    """cos/sin [T, HD] (rotate-half convention) and the [HD, HD] matrix with
+    x @ Rot = rotate_half(x), as examples/qwen3/import.py:80-89 builds them."""
+    inv = theta ** (-(np.arange(0, HD, 2) / HD))
+    ang = np.outer(np.arange(T), inv)
+    cos = np.concatenate([np.cos(ang), np.cos(ang)], axis=1).astype(np.float32)
+    sin = np.concatenate([np.sin(ang), np.sin(ang)], axis=1).astype(np.float32)
+    rot = np.zeros((HD, HD), np.float32)
+    for i in range(HD // 2):
+        rot[i + HD // 2, i] = -1.0
+        rot[i, i + HD // 2] = 1.0
+    return cos, sin, rot
+
+
+def qwen3_tgir(name="qwen3", L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, V=151936, T=512, bits=4, seed=3):
+    """Config 3's model at fixed sequence length T: the graph
+    examples/qwen3/import.py:110-130 emits (per-head rank-2 matmuls, GQA with
+    NQ / NKV query heads per KV head, rotate-half RoPE as x * cos + (x @ Rot)
+    * sin, causal mask added before softmax, SwiGLU MLP, tied LM head, output
+    the logits of the last position), lowered to TGIR. One row is one
+    sequence: f32[T] token ids. Every param `tgc quantize --bits 4` would
+    quantize (rank-2 matmul operands: all linear weights, the LM head and Rot)
+    is quantized RTN int`bits` on axis 1 (x @ W); E, the RoPE tables and the
+    mask stay f32."""
+    w = qwen3_weights(L, D, NQ, NKV, HD, FF, V, seed)
+    cos, sin, rot = rope_tables(T, HD)
+    mask = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
+    ones_d, ones_hd = np.ones(D, np.float32), np.ones(HD, np.float32)
+    parts = ["(tgir 1\n  (model %s)\n" % name]
+
+    def quant(nm, arr):
+        codes, sc = quantize_rtn(arr, bits, 1)
+        parts.append(param_quant(nm, codes, sc, bits, 1))
+
+    parts.append(param_f32("E", w["E"]))
+    quant("LM", np.ascontiguousarray(w["E"].T))
+    parts.append(param_f32("lnf", ones_d))
+    parts.append(param_f32("cosT", cos))
+    parts.append(param_f32("sinT", sin))
+    quant("Rot", rot)
+    parts.append(param_f32("mask", mask))
+    parts.append(param_f32("lastidx", np.array([T - 1], np.float32)))
+    for l in range(L):
+        for nm in ("ln1_%d", "ln2_%d"):
+            parts.append(param_f32(nm % l, ones_d))
+        for nm in ("qn_%d", "kn_%d"):
+            parts.append(param_f32(nm % l, ones_hd))
+        for h in range(NQ):
+            quant("Wq_%d_%d" % (l, h), w["Wq_%d_%d" % (l, h)])
+            quant("Wo_%d_%d" % (l, h), w["Wo_%d_%d" % (l, h)])
+        for j in range(NKV):
+            quant("Wk_%d_%d" % (l, j), w["Wk_%d_%d" % (l, j)])
+            quant("Wv_%d_%d" % (l, j), w["Wv_%d_%d" % (l, j)])
+        for nm in ("Wg_%d", "Wu_%d", "Wd_%d"):
+            quant(nm % l, w[nm % l])
+    parts.append("  (input ids (f32 %d))\n  (block\n" % T)
+    v = [0]
+    lines = []
+
+    def op(shape, expr):
+        v[0] += 1
+        r = "%%%d" % v[0]
+        lines.append("    (%s (f32%s) %s)\n" % (r, "".join(" %d" % d for d in shape), expr))
+        return r
+
+    def rotary(x):  # x * cosT + (x @ Rot) * sinT
+        a = op((T, HD), "(mul %s cosT)" % x)
+        b = op((T, HD), "(matmul %s Rot)" % x)
+        c = op((T, HD), "(mul %s sinT)" % b)
+        return op((T, HD), "(add %s %s)" % (a, c))
+
+    scale = op((), "(const %.9g)" % (1.0 / np.sqrt(HD)))
+    h = op((T, D), "(take E ids)")
+    for l in range(L):
+        n = op((T, D), "(mul %s ln1_%d)" % (op((T, D), "(rmsnorm %s)" % h), l))
+        ks, vs = [], []
+        for j in range(NKV):
+            a = op((T, HD), "(matmul %s Wk_%d_%d)" % (n, l, j))
+            ks.append(rotary(op((T, HD), "(mul %s kn_%d)" % (op((T, HD), "(rmsnorm %s)" % a), l))))
+            vs.append(op((T, HD), "(matmul %s Wv_%d_%d)" % (n, l, j)))
+        terms = []
+        for hh in range(NQ):
+            j = hh // (NQ // NKV)
+            a = op((T, HD), "(matmul %s Wq_%d_%d)" % (n, l, hh))
+            q = rotary(op((T, HD), "(mul %s qn_%d)" % (op((T, HD), "(rmsnorm %s)" % a), l)))
+            kt = op((HD, T), "(transpose %s)" % ks[j])
+            sc = op((T, T), "(mul %s %s)" % (op((T, T), "(matmul %s %s)" % (q, kt)), scale))
+            s = op((T, T), "(softmax %s)" % op((T, T), "(add %s mask)" % sc))
+            terms.append(op((T, D), "(matmul %s Wo_%d_%d)" % (op((T, HD), "(matmul %s %s)" % (s, vs[j])), l, hh)))
+        acc = terms[0]
+        for t_ in terms[1:]:
+            acc = op((T, D), "(add %s %s)" % (acc, t_))
+        h = op((T, D), "(add %s %s)" % (h, acc))
+        n = op((T, D), "(mul %s ln2_%d)" % (op((T, D), "(rmsnorm %s)" % h), l))
+        g = op((T, FF), "(silu %s)" % op((T, FF), "(matmul %s Wg_%d)" % (n, l)))
+        u = op((T, FF), "(matmul %s Wu_%d)" % (n, l))
+        h = op((T, D), "(add %s %s)" % (h, op((T, D), "(matmul %s Wd_%d)" % (op((T, FF), "(mul %s %s)" % (g, u)), l))))
+    nf = op((T, D), "(mul %s lnf)" % op((T, D), "(rmsnorm %s)" % h))
+    logits = op((T, V), "(matmul %s LM)" % nf)
+    out = op((V,), "(reshape %s)" % op((1, V), "(take %s lastidx)" % logits))
+    parts.extend(lines)
+    parts.append("  )\n  (output %s))\n" % out)
+    return "".join(parts)
+
+
+def config3_prompts(seqs=64, T=512, V=151936, seed=3):
+    """Config 3 prompts: seqs rows of T token ids uniform in [0, V), as f32
+    (exact below 2^24), from xorshift32(seed): id = x mod V."""
+    x = xorshift_stream(seed, seqs * T)
+    return (x % np.uint32(V)).astype(np.float32).reshape(seqs, T)
+
+
 def config5_rows(rows=4096, T=512, d_model=256, seed=5):
     """Config 5 inputs: rows sequences of T steps of f32[d_model] ~ N(0, 1)."""
     return normal(seed, 1.0, rows * T * d_model).reshape(rows, T * d_model)

@@ -59,7 +59,14 @@ def _synth():
                                             classes=3),
         "ssm5_small": lambda: synth.ssm_tgir("ssm5_small", d_model=64, d_inner=128, n_state=16, dt_rank=8, T=24,
                                              blocks=2, classes=8),
+        # config 3's decoder at reduced sizes (every op of the full model, GQA with 2 query heads per KV head)
+        "qwen3_tiny": lambda: synth.qwen3_tgir("qwen3_tiny", L=1, D=32, NQ=2, NKV=1, HD=8, FF=48, V=64, T=4),
+        "qwen3_small": lambda: synth.qwen3_tgir("qwen3_small", L=2, D=64, NQ=4, NKV=2, HD=16, FF=96, V=320, T=12),
     }
+
+
+# vocabulary sizes of the token-id models (rows are token ids)
+VOCAB = {"qwen3_tiny": 64, "qwen3_small": 320}
 
 
 def rows_for(name, per, seed):
@@ -71,6 +78,11 @@ def rows_for(name, per, seed):
         x = rng.normal(size=(64, 4)).astype(np.float32) * 2
         r = rng.integers(-1, 7, size=(64, 2)).astype(np.float32)  # includes out-of-range rows (-1, 6)
         return np.concatenate([x, r], axis=1)
+    if name in VOCAB:
+        ids = rng.integers(0, VOCAB[name], size=(24, per)).astype(np.float32)
+        ids[0] = 0  # the first and last vocabulary entries
+        ids[1] = VOCAB[name] - 1
+        return ids
     n = 97 if per > 1000 else 64
     x = rng.normal(size=(n, per)).astype(np.float32)
     x[0] = 0  # an all-zero row
