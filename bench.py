@@ -288,6 +288,101 @@ def bench_config4(args):
     print(json.dumps(out), flush=True)
 
 
+def q3_macs_per_token(L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, T=512):
+    """Quantized-projection MACs per prompt token of config 3 (all layers):
+    q, k, v, o, gate, up, down and the RoPE rotations (x @ Rot per q and k
+    head); the attention products and the LM head are counted apart."""
+    per_layer = D * NQ * HD + 2 * D * NKV * HD + NQ * HD * D + 3 * D * FF + (NQ + NKV) * HD * HD
+    return L * per_layer
+
+
+def bench_config3(args):
+    """Config 3, prefill: the Qwen3-0.6B-shaped int4 decoder at fixed T = 512
+    over 64 prompts of uniform token ids, one device pass; each sequence's
+    output is its last position's 151,936 logits (the importer's graph,
+    examples/qwen3/import.py:129-130). Throughput = prompt tokens per second.
+    roofline: the int4 projections (q3_macs_per_token x 2 ops per token)
+    against 5000 TOP/s dense int8 MFMA. cpu_baseline: the reference at 1 and
+    2 layers (full widths, T = 512, a 2048-token vocabulary), extrapolated to
+    28 layers and the full LM head (the full model is hours of CPU time)."""
+    import numpy as np
+    from technograd_amd import hip, synth
+    seqs, T, V = 64, 512, 151936
+    hip.init(0)
+    tmp = tempfile.mkdtemp(prefix="tgq3")
+    try:
+        log("building config 3 (Qwen3-0.6B-shaped int4 decoder, %d prompts x %d tokens)" % (seqs, T))
+        t0 = time.perf_counter()
+        text = synth.qwen3_tgir("qwen3", T=T, files=tmp, quantizer=hip.quantize_rtn)
+        X = synth.config3_prompts(seqs, T, V)
+        log("config 3: weights written in %.0f s; loading" % (time.perf_counter() - t0))
+        t0 = time.perf_counter()
+        prog = hip.Program(text, max_rows=seqs)
+        log("config 3: loaded in %.0f s, %.1f MiB of arena per sequence" % (time.perf_counter() - t0,
+                                                                          prog.stats().arena_bytes / seqs / 2**20))
+        d_x = hip.DeviceBuffer.from_array(X)
+        d_y = hip.DeviceBuffer(seqs * V * 4)
+        prog.batch_device(d_x.ptr, seqs, d_y.ptr)
+        prog.sync()
+        steps = max(1, min(args.steps, 3))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            prog.batch_device(d_x.ptr, seqs, d_y.ptr)
+        prog.sync()
+        t = (time.perf_counter() - t0) / steps
+        y = d_y.to_array(np.float32, (seqs, V))
+        assert np.isfinite(y).all()
+        log("config 3: %.1f ms per pass of %d x %d tokens; first sequences' next tokens %s"
+            % (t * 1e3, seqs, T, y[:4].argmax(axis=1).tolist()))
+        prog.close()
+        tprog = hip.Program(text, flags=hip.TIMING, max_rows=seqs)
+        tprog.batch_device(d_x.ptr, seqs, d_y.ptr)
+        tprog.sync()
+        st = tprog.stats()
+        tprog.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    mfma_us, dig_us, oth_us = (v * 1e3 for v in (st.qgemm_ms, st.digits_ms, st.other_ms))
+    ops = 2.0 * q3_macs_per_token() * seqs * T
+    log("config 3: projections %.0f us, digits %.0f us, other (attention, norms, elementwise) %.0f us"
+        % (mfma_us, dig_us, oth_us))
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        if O.have_ref():
+            cs = 16
+            Xs = synth.config3_prompts(cs, T, 2048, seed=33)
+            secs = []
+            for L in (1, 2):
+                log("config 3: cpu baseline, the reference at %d layer(s)" % L)
+                tx = synth.qwen3_tgir("q3cpu", L=L, V=2048, T=T)
+                r = ref_cpu(tx, Xs, T, 2048, 0, args.cpu_threads, False, "")
+                secs.append(cs / r["value"])
+            layer = secs[1] - secs[0]
+            rest = secs[0] - layer  # embedding and the 2048-column LM head
+            full = 28 * layer + rest * V / 2048.0
+            cpu = {"value": round(cs * T / full, 2), "unit": "prompt tokens/s", "cores": args.cpu_threads,
+                   "kind": "reference",
+                   "sample": "%d prompts x %d tokens through the reference's interpreter at 1 and 2 layers (full widths, "
+                             "vocabulary 2048, -j %d): %.1f s per added layer, %.1f s for the rest; extrapolated to 28 "
+                             "layers and the 151,936-column LM head: %.0f s for the %d prompts"
+                             % (cs, T, args.cpu_threads, layer, rest, full, cs)}
+    out = {
+        "metric": "config 3 prefill prompt tokens/sec at 1 GPU (decode: see DESIGN.md)", "value": round(seqs * T / t, 1),
+        "unit": "prompt tokens/s", "n_gpus": 1, "steps": steps, "warmup": 1, "ms_per_step": round(t * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int4 projections, f32 attention",
+        "data": "synthetic (N(0,0.02) weights seed 3 quantized int4 RTN per channel, token ids uniform seed 3)",
+        "config": {"workload": "config 3 prefill: Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads of "
+                               "128, SwiGLU 3072, vocab 151,936), 64 prompts x 512 tokens per step"},
+        "roofline": {"bound": "mfma", "achieved": round(ops / mfma_us / 1e6, 2), "peak": MFMA_I8_PEAK_TOPS,
+                     "unit": "TOP/s", "frac": round(ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "the int4 projections of a pass, summed"},
+        "cpu_baseline": cpu,
+        "breakdown_us": {"projections": round(mfma_us, 1), "digits": round(dig_us, 1), "other": round(oth_us, 1)},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def bench_config5(args):
     """Config 5: int8 selective-SSM classifier (4 blocks, d_model 256, state 16,
     expand 2, T = 512) over 4096 sequences in device passes of `pass_rows`
@@ -365,16 +460,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
     ap.add_argument("--reps", type=int, default=10, help="kernel-timing repetitions per batch")
-    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 4, 5),
-                    help="BASELINE configuration: 2 (default, the headline metric), 1 (int8 MLP), 4 (Q16.16 "
-                         "reasoner), 5 (selective-SSM classifier)")
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
+                    help="BASELINE configuration: 2 (default, the headline metric), 1 (int8 MLP), 3 (Qwen3-shaped "
+                         "decoder, prefill), 4 (Q16.16 reasoner), 5 (selective-SSM classifier)")
     ap.add_argument("--profile-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.profile_child:
         profile_child()
         return
     if args.config != 2 and args.gpus == 1:
-        {1: bench_config1, 4: bench_config4, 5: bench_config5}[args.config](args)
+        {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}[args.config](args)
         return
     if args.gpus != 1:
         print("bench.py: this backend runs on one GPU per process and this build measures one GPU only; "

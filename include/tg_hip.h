@@ -100,6 +100,14 @@ const char *tg_hip_error(void);
 int tg_hip_stats(const tg_hip_prog *p, tg_hip_stats_t *st);
 int tg_hip_reset_stats(tg_hip_prog *p);
 
+/* RTN quantization of a rank-2 f32 param on the host, as `tgc quantize
+ * --method rtn` does it (src/quant.c:176-200, :258-316): per output channel
+ * (axis 0: rows, W[C][K]; axis 1: columns, W[K][C]) the best of ten clipped
+ * scales, codes in [-7, 7] or [-127, 127] one int8 per element in w's layout,
+ * one f32 scale per channel. Channels are spread over `threads` threads. No
+ * device is used. 0 on success, -1 on bad arguments. */
+int tg_hip_quantize_rtn(const float *w, int rows, int cols, int bits, int axis, signed char *codes, float *scales, int threads);
+
 /* Device memory helpers for callers without their own allocator. */
 void *tg_hip_dev_alloc(size_t bytes);
 int tg_hip_dev_free(void *d);

@@ -507,10 +507,85 @@ void tgk_ew_run(hipStream_t s, const tgk_ew *e, int n, int rows)
 	}
 }
 
+// f32 products (quant 0) in tiles: a block computes a TS x TS tile of one
+// (batch row, group) product, each of its 16 x 16 threads a TS/16 x TS/16
+// block of it. A and B pass through LDS 16 values of p at a time, and every
+// output adds its products in order p = 0..k-1 from 0.0f with separate
+// multiply and add, exactly as mm_exact_k does, so the results are
+// bit-identical to it. Tile rows, columns and p values past m, n and k read
+// as zeros; the p loop stops at k and nothing past m or n is stored.
+template <int TS>
+__global__ __launch_bounds__(256) void mm_tile_k(tgk_mm d, int tm, int tn)
+{
+	constexpr int KC = 16, R = TS / 16;
+	__shared__ float As[KC][TS + 4]; // As[p][i]
+	__shared__ float Bs[KC][TS + 4]; // Bs[p][j]
+	const int tiles = tm * tn;
+	const long rg = blockIdx.x / tiles;
+	const int t = (int)(blockIdx.x - rg * tiles), ti = t / tn, tj = t - ti * tn;
+	const long r = rg / d.g;
+	const int g = (int)(rg - r * d.g);
+	const float *A = d.a.p + r * d.a.rs + g * d.ag, *B = d.b.p + r * d.b.rs + g * d.bg;
+	const int i0 = ti * TS, j0 = tj * TS;
+	const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+	float acc[R][R];
+	for (int u = 0; u < R; u++)
+		for (int v = 0; v < R; v++) acc[u][v] = 0.0f;
+	for (int p0 = 0; p0 < d.k; p0 += KC) {
+		for (int e = threadIdx.x; e < TS * KC; e += 256) { // A tile, coalesced along whichever of i, p is unit stride
+			int i, p;
+			if (d.ap == 1) i = e / KC, p = e % KC;
+			else p = e / TS, i = e % TS;
+			const bool in = i0 + i < d.m && p0 + p < d.k;
+			const float x = A[in ? (long)(i0 + i) * d.ai + (long)(p0 + p) * d.ap : 0];
+			As[p][i] = in ? x : 0.0f;
+		}
+		for (int e = threadIdx.x; e < TS * KC; e += 256) { // B tile
+			int j, p;
+			if (d.bj == 1 || d.bp != 1) p = e / TS, j = e % TS;
+			else j = e / KC, p = e % KC;
+			const bool in = j0 + j < d.n && p0 + p < d.k;
+			const float x = B[in ? (long)(p0 + p) * d.bp + (long)(j0 + j) * d.bj : 0];
+			Bs[p][j] = in ? x : 0.0f;
+		}
+		__syncthreads();
+		const int kk = d.k - p0 < KC ? d.k - p0 : KC;
+		for (int p = 0; p < kk; p++) {
+			float a[R], b[R];
+			for (int u = 0; u < R; u++) a[u] = As[p][ty * R + u];
+			for (int v = 0; v < R; v++) b[v] = Bs[p][tx * R + v];
+			for (int u = 0; u < R; u++)
+				for (int v = 0; v < R; v++) acc[u][v] = acc[u][v] + a[u] * b[v];
+		}
+		__syncthreads();
+	}
+	float *O = d.o + r * d.ors + g * d.og;
+	for (int u = 0; u < R; u++) {
+		const int i = i0 + ty * R + u;
+		if (i >= d.m) break;
+		for (int v = 0; v < R; v++) {
+			const int j = j0 + tx * R + v;
+			if (j < d.n) O[(long)i * d.oi + (long)j * d.oj] = acc[u][v];
+		}
+	}
+}
+
 void tgk_matmul_exact(hipStream_t s, const tgk_mm *d, int rows)
 {
 	long total = (long)rows * d->g * d->m * d->n;
-	if (total > 0) mm_exact_k<<<blocks_for(total), TPB, 0, s>>>(*d, total);
+	if (total <= 0) return;
+	if (d->quant == 0 && (long)d->m * d->n >= 64 * 64 && d->k >= 16) {
+		const long rg = (long)rows * d->g;
+		const int tm = (d->m + 127) / 128, tn = (d->n + 127) / 128;
+		if (rg * tm * tn >= 1024) { // enough 128 x 128 tiles to fill the chip
+			mm_tile_k<128><<<(unsigned)(rg * tm * tn), 256, 0, s>>>(*d, tm, tn);
+		} else {
+			const int sm = (d->m + 63) / 64, sn = (d->n + 63) / 64;
+			mm_tile_k<64><<<(unsigned)(rg * sm * sn), 256, 0, s>>>(*d, sm, sn);
+		}
+		return;
+	}
+	mm_exact_k<<<blocks_for(total), TPB, 0, s>>>(*d, total);
 }
 
 void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, int cols, int rows)

@@ -1172,16 +1172,16 @@ struct Timer {
 	Timer(tg_hip_prog *p_, int w) : p(p_), which(w)
 	{
 		if (p->flags & TG_HIP_TIMING) {
-			hipEventCreate(&a);
-			hipEventRecord(a, p->st);
+			(void)hipEventCreate(&a);
+			(void)hipEventRecord(a, p->st);
 		}
 	}
 	~Timer()
 	{
 		if (!a) return;
 		hipEvent_t b;
-		hipEventCreate(&b);
-		hipEventRecord(b, p->st);
+		(void)hipEventCreate(&b);
+		(void)hipEventRecord(b, p->st);
 		p->tev.push_back(a);
 		p->tev.push_back(b);
 		p->tev.push_back((hipEvent_t)(intptr_t)which);
@@ -1301,7 +1301,7 @@ void collect_timing(tg_hip_prog *p)
 {
 	for (size_t i = 0; i + 3 <= p->tev.size(); i += 3) {
 		float ms = 0;
-		hipEventElapsedTime(&ms, p->tev[i], p->tev[i + 1]);
+		(void)hipEventElapsedTime(&ms, p->tev[i], p->tev[i + 1]);
 		int which = (int)(intptr_t)p->tev[i + 2];
 		if (which == 1) {
 			p->stats.qgemm_ms += ms;
@@ -1311,8 +1311,8 @@ void collect_timing(tg_hip_prog *p)
 		} else {
 			p->stats.other_ms += ms;
 		}
-		hipEventDestroy(p->tev[i]);
-		hipEventDestroy(p->tev[i + 1]);
+		(void)hipEventDestroy(p->tev[i]);
+		(void)hipEventDestroy(p->tev[i + 1]);
 	}
 	p->tev.clear();
 }
@@ -1372,8 +1372,89 @@ int run_pass(tg_hip_prog *p, const float *d_in, int rows, float *d_out, int *d_s
 	return hipok(hipGetLastError(), "layer program launch") ? 0 : -1;
 }
 
+// ------------------------------------------- rows read through take ----
+
+void count_uses(const tgm_block *b, std::vector<int> &u)
+{
+	for (int i = 0; i < b->len; i++) {
+		const tgm_ins &in = b->v[i];
+		for (int j = 0; j < in.na; j++) u[(size_t)in.a[j]]++;
+		if (in.op == TGM_SCAN) {
+			for (int k = 0; k < in.nc; k++) u[(size_t)in.cinit[k]]++, u[(size_t)in.cnext[k]]++;
+			for (int k = 0; k < in.nx; k++) u[(size_t)in.x[k]]++;
+			for (int k = 0; k < in.ny; k++) u[(size_t)in.y[k]]++;
+		}
+		if (in.op == TGM_THINK) {
+			u[(size_t)in.init]++;
+			u[(size_t)in.yield]++;
+			if (in.halt >= 0) u[(size_t)in.halt]++;
+		}
+		if (in.body) count_uses(in.body, u);
+	}
+}
+
+// o = take(v, idx) with v = matmul(X, W) read by nothing else, X [M K] and W
+// [K N] rank 2, idx a param whose entries all round into [0, M): row c of o
+// is row idx[c] of X times W, so the program computes take(X, idx) and
+// multiplies only those rows (the tied LM head of a decoder, read at the last
+// position: one row instead of T). Each output row of a matmul depends only
+// on its own input row, in every kernel here, so the values are unchanged.
+// An index outside [0, M) would give a zero row, whose product with a W
+// holding inf or nan is not zero: such indices keep the original program.
+void push_take_into_matmul(tgm_module *m)
+{
+	tgm_block &b = m->top;
+	std::vector<int> uses((size_t)m->nval, 0);
+	count_uses(&b, uses);
+	uses[(size_t)m->output]++;
+	for (int i = 0; i < b.len; i++) {
+		tgm_ins &tk = b.v[i];
+		if (tk.op != TGM_TAKE || tk.na != 2) continue;
+		const int v = tk.a[0], idx = tk.a[1];
+		int j = i - 1;
+		while (j >= 0 && b.v[j].out != v) j--;
+		if (j < 0 || b.v[j].op != TGM_MATMUL || uses[(size_t)v] != 1) continue;
+		tgm_ins &mm = b.v[j];
+		const int X = mm.a[0], W = mm.a[1];
+		const tgm_shape &sx = m->val[X].sh, &sw = m->val[W].sh;
+		if (sx.rank != 2 || sw.rank != 2 || sx.dim[1] != sw.dim[0] || m->val[idx].kind != TGM_PARAM || !m->val[idx].data) continue;
+		const int M = sx.dim[0], K = sx.dim[1];
+		const long cnt = m->val[idx].n;
+		bool in_range = cnt > 0;
+		for (long c = 0; c < cnt && in_range; c++) {
+			const float r = floorf(m->val[idx].data[c] + 0.5f);
+			in_range = r >= 0.0f && r < (float)M;
+		}
+		if (!in_range) continue;
+		if (m->nval == m->cap) {
+			const int cap = m->cap ? 2 * m->cap : 64;
+			tgm_value *nv = (tgm_value *)realloc(m->val, (size_t)cap * sizeof *nv);
+			if (!nv) return; // keep the original program
+			m->val = nv;
+			m->cap = cap;
+		}
+		tgm_value &t = m->val[m->nval];
+		memset(&t, 0, sizeof t);
+		t.kind = TGM_TMP;
+		t.sh.rank = 2;
+		t.sh.dim[0] = (int)cnt;
+		t.sh.dim[1] = K;
+		t.n = cnt * K;
+		const int tmp = m->nval++;
+		mm.op = TGM_TAKE; // at the product's place (idx, a param, is defined throughout): tmp = take(X, idx)
+		mm.out = tmp;
+		mm.na = 2;
+		mm.a[0] = X;
+		mm.a[1] = idx;
+		tk.op = TGM_MATMUL; // at the take's place: o = tmp @ W
+		tk.a[0] = tmp;
+		tk.a[1] = W;
+	}
+}
+
 bool build_layer(tg_hip_prog *p)
 {
+	push_take_into_matmul(p->m);
 	LB L;
 	L.p = p;
 	L.m = p->m;
@@ -1428,9 +1509,9 @@ void destroy(tg_hip_prog *p)
 	void *bufs[] = { p->d_pool, p->d_imap, p->d_codes, p->d_fscale, p->d_qscale, p->d_arena, p->d_scratch, p->d_rprog,
 			 p->d_in, p->d_out, p->d_steps };
 	for (void *b : bufs)
-		if (b) hipFree(b);
-	if (p->ev0) hipEventDestroy(p->ev0);
-	if (p->ev1) hipEventDestroy(p->ev1);
+		if (b) (void)hipFree(b);
+	if (p->ev0) (void)hipEventDestroy(p->ev0);
+	if (p->ev1) (void)hipEventDestroy(p->ev1);
 	if (p->own_st) (void)hipStreamDestroy(p->own_st);
 	tgm_free(p->m);
 	delete p;
@@ -1456,9 +1537,9 @@ int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *ste
 					  p->st),
 			   "rows to device"))
 			return -1;
-		hipEventRecord(p->ev0, p->st);
+		(void)hipEventRecord(p->ev0, p->st);
 		if (run_pass(p, p->d_in, cnt, p->d_out, p->d_steps)) return -1;
-		hipEventRecord(p->ev1, p->st);
+		(void)hipEventRecord(p->ev1, p->st);
 		if (!hipok(hipMemcpyAsync((char *)out + (size_t)r0 * nout * 4, p->d_out, (size_t)cnt * nout * 4, hipMemcpyDeviceToHost, p->st),
 			   "outputs to host"))
 			return -1;
@@ -1468,7 +1549,7 @@ int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *ste
 			return -1;
 		if (!hipok(hipStreamSynchronize(p->st), "batch")) return -1;
 		float ms = 0;
-		hipEventElapsedTime(&ms, p->ev0, p->ev1);
+		(void)hipEventElapsedTime(&ms, p->ev0, p->ev1);
 		ms_total += ms;
 		collect_timing(p);
 	}
@@ -1610,8 +1691,8 @@ int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, co
 		if (!hipok(hipMemcpyAsync(db, b, bn * 4, hipMemcpyHostToDevice, st), "copy")) break;
 		if (flags & TG_HIP_EXACT) {
 			if (!hipok(hipMalloc(&dq, qb), "alloc") || !hipok(hipMalloc(&ds, nch * 4), "alloc")) break;
-			hipMemcpyAsync(dq, q, qb, hipMemcpyHostToDevice, st);
-			hipMemcpyAsync(ds, s, nch * 4, hipMemcpyHostToDevice, st);
+			(void)hipMemcpyAsync(dq, q, qb, hipMemcpyHostToDevice, st);
+			(void)hipMemcpyAsync(ds, s, nch * 4, hipMemcpyHostToDevice, st);
 			tgk_mm d{};
 			d.g = 1, d.m = m, d.k = k, d.n = n;
 			d.quant = axis == 0 ? 1 : 2;
@@ -1653,8 +1734,8 @@ int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, co
 	tgk_qweight_free(&w);
 	void *bufs[] = { db, dout, ds, dq, scr };
 	for (void *x : bufs)
-		if (x) hipFree(x);
-	hipStreamDestroy(st);
+		if (x) (void)hipFree(x);
+	(void)hipStreamDestroy(st);
 	return rc;
 }
 

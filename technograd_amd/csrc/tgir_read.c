@@ -16,7 +16,14 @@
  * reference narrows them (scales, data, constants, thresholds).
  *
  * The reader streams over the text: a 16.8 M-code int4 layer is packed as it
- * is read, without building an expression tree. */
+ * is read, without building an expression tree.
+ *
+ * Extension (not in the reference's grammar), for models whose weights are
+ * too large to travel as text: a param's values may come from a file of raw
+ * little-endian arrays, `(data-file PATH)` for f32 data, and inside `quant`
+ * `(scale-file PATH)` (f32, one per channel) and `(codes-file PATH)` (int8,
+ * one code per element, the text form's order), checked and packed exactly
+ * like their text forms. PATH is one token (no blanks or parentheses). */
 #include "tgm.h"
 
 #include <ctype.h>
@@ -39,6 +46,7 @@ typedef struct {
 		int v;
 	} *scope;
 	int ns, scap;
+	signed char *codes; /* codes read from a file, until packed */
 } Rd;
 
 static void bad(Rd *r, const char *fmt, ...)
@@ -492,6 +500,19 @@ static void items(Rd *r, tgm_block *b, int in_think)
 	}
 }
 
+/* `bytes` of raw data from the file named by the next token into dst */
+static void file_data(Rd *r, void *dst, size_t bytes, const char *what)
+{
+	Atom path;
+	atom(r, &path);
+	FILE *f = fopen(path.t, "rb");
+	if (!f) bad(r, "cannot open %s file '%s'", what, path.t);
+	const size_t got = fread(dst, 1, bytes, f);
+	const int extra = fgetc(f) != EOF;
+	fclose(f);
+	if (got != bytes || extra) bad(r, "%s file '%s' must hold exactly %zu bytes", what, path.t, bytes);
+}
+
 static void param_form(Rd *r, int kind)
 {
 	tgm_module *m = r->m;
@@ -513,18 +534,36 @@ static void param_form(Rd *r, int kind)
 		x->q = mem(r, (size_t)(x->qbits == 8 ? x->n : (x->n + 1) / 2), 1);
 		x->data = mem(r, (size_t)x->n, sizeof(float));
 		lp(r);
-		if (!sym_is(r, "scale")) bad(r, "malformed quant scales");
-		for (long j = 0; j < nch; j++) {
-			if (look(r) == ')') bad(r, "quant needs one scale per channel");
-			x->qs[j] = (float)num(r, "a scale");
+		Atom h;
+		sym(r, &h);
+		if (!strcmp(h.t, "scale-file")) {
+			file_data(r, x->qs, (size_t)nch * sizeof(float), "scale");
+		} else {
+			if (strcmp(h.t, "scale")) bad(r, "malformed quant scales");
+			for (long j = 0; j < nch; j++) {
+				if (look(r) == ')') bad(r, "quant needs one scale per channel");
+				x->qs[j] = (float)num(r, "a scale");
+			}
 		}
 		rp(r);
 		lp(r);
-		if (!sym_is(r, "codes")) bad(r, "malformed quant codes");
+		sym(r, &h);
+		signed char *raw = NULL; /* codes from a file (owned by r until freed, so a failure frees them) */
+		if (!strcmp(h.t, "codes-file")) {
+			raw = r->codes = mem(r, (size_t)x->n, 1);
+			file_data(r, raw, (size_t)x->n, "codes");
+		} else if (strcmp(h.t, "codes")) {
+			bad(r, "malformed quant codes");
+		}
 		int lim = x->qbits == 8 ? 127 : 7;
 		for (long j = 0; j < x->n; j++) {
-			if (look(r) == ')') bad(r, "quant needs one code per element");
-			double cd = num(r, "a code");
+			double cd;
+			if (raw) {
+				cd = raw[j];
+			} else {
+				if (look(r) == ')') bad(r, "quant needs one code per element");
+				cd = num(r, "a code");
+			}
 			if (cd != floor(cd) || fabs(cd) > lim) bad(r, "code out of range");
 			int code = (int)cd;
 			if (x->qbits == 8) x->q[j] = (unsigned char)(signed char)code;
@@ -533,7 +572,13 @@ static void param_form(Rd *r, int kind)
 			long ch = x->qaxis == 0 ? j / sh.dim[1] : j % sh.dim[1];
 			x->data[j] = (float)code * x->qs[ch];
 		}
+		free(raw);
+		r->codes = NULL;
 		rp(r);
+		rp(r);
+	} else if (!strcmp(a.t, "data-file")) {
+		x->data = mem(r, (size_t)x->n, sizeof(float));
+		file_data(r, x->data, (size_t)x->n * sizeof(float), "data");
 		rp(r);
 	} else if (!strcmp(a.t, "data")) {
 		x->data = mem(r, (size_t)x->n, sizeof(float));
@@ -570,6 +615,7 @@ tgm_module *tgm_read(const char *text, size_t len, char *err, size_t errn)
 	if (setjmp(r.fail)) {
 		unbind_to(&r, 0);
 		free(r.scope);
+		free(r.codes);
 		tgm_free(r.m);
 		return NULL;
 	}

@@ -42,6 +42,7 @@ def lib():
         L.tg_hip_batch_device.argtypes = [vp, vp, ctypes.c_long, vp, vp]
         L.tg_hip_sync.argtypes = [vp]
         L.tg_hip_matmul_q.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip, ip, ip]
+        L.tg_hip_quantize_rtn.argtypes = [vp, ip, ip, ip, ip, vp, vp, ip]
         L.tg_hip_free.argtypes = [vp]
         L.tg_hip_error.restype = ctypes.c_char_p
         L.tg_hip_stats.argtypes = [vp, ctypes.POINTER(Stats)]
@@ -171,3 +172,16 @@ def matmul_q(q, bits, s, b, m, k, n, axis, flags=0):
     o = np.empty((m, n), np.float32)
     _check(lib().tg_hip_matmul_q(_p(o), _p(q), bits, _p(s), _p(b), m, k, n, axis, flags), "tg_hip_matmul_q")
     return o
+
+
+def quantize_rtn(w, bits, axis, threads=None):
+    """tg_hip_quantize_rtn on the host (no device): (codes int8 in w's
+    layout, scales f32 per channel), as `tgc quantize --method rtn` writes
+    them."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    codes = np.empty((rows, cols), np.int8)
+    scales = np.empty(rows if axis == 0 else cols, np.float32)
+    t = threads or min(16, os.cpu_count() or 1)
+    _check(lib().tg_hip_quantize_rtn(_p(w), rows, cols, bits, axis, _p(codes), _p(scales), t), "tg_hip_quantize_rtn")
+    return codes, scales

@@ -20,6 +20,8 @@ TGIR text the backend (and the reference) load.
   K > 2048 in the reference (src/quant.c:345-346), which is every quantized
   layer of configs 2 and 3 wider than 2048 inputs.
 """
+import os
+
 import numpy as np
 
 _BLOCK = 4096
@@ -447,7 +449,8 @@ def rope_tables(T, HD, theta=1e6):
     return cos, sin, rot
 
 
-def qwen3_tgir(name="qwen3", L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, V=151936, T=512, bits=4, seed=3):
+def qwen3_tgir(name="qwen3", L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, V=151936, T=512, bits=4, seed=3, files=None,
+               quantizer=None):
     """Config 3's model at fixed sequence length T: the graph
     examples/qwen3/import.py:110-130 emits (per-head rank-2 matmuls, GQA with
     NQ / NKV query heads per KV head, rotate-half RoPE as x * cos + (x @ Rot)
@@ -456,30 +459,52 @@ def qwen3_tgir(name="qwen3", L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, V=1519
     sequence: f32[T] token ids. Every param `tgc quantize --bits 4` would
     quantize (rank-2 matmul operands: all linear weights, the LM head and Rot)
     is quantized RTN int`bits` on axis 1 (x @ W); E, the RoPE tables and the
-    mask stay f32."""
+    mask stay f32.
+
+    files: a directory; the params are then written there as raw arrays and
+    the text refers to them with the backend's data-file / scale-file /
+    codes-file forms (a full-size model as TGIR text would be several GB).
+    quantizer: an RTN function with quantize_rtn's signature (the library's
+    native one for full size); quantize_rtn by default."""
     w = qwen3_weights(L, D, NQ, NKV, HD, FF, V, seed)
     cos, sin, rot = rope_tables(T, HD)
     mask = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
     ones_d, ones_hd = np.ones(D, np.float32), np.ones(HD, np.float32)
     parts = ["(tgir 1\n  (model %s)\n" % name]
+    rtn = quantizer or quantize_rtn
+
+    def f32p(nm, arr):
+        if files is None:
+            return param_f32(nm, arr)
+        arr = np.ascontiguousarray(arr, np.float32)
+        path = os.path.join(files, nm + ".f32")
+        arr.tofile(path)
+        return "  (param %s (f32 %s)\n    (data-file %s))\n" % (nm, " ".join(str(d) for d in arr.shape), path)
 
     def quant(nm, arr):
-        codes, sc = quantize_rtn(arr, bits, 1)
-        parts.append(param_quant(nm, codes, sc, bits, 1))
+        codes, sc = rtn(arr, bits, 1)
+        if files is None:
+            parts.append(param_quant(nm, codes, sc, bits, 1))
+            return
+        cpath, spath = os.path.join(files, nm + ".codes"), os.path.join(files, nm + ".scale")
+        np.ascontiguousarray(codes, np.int8).tofile(cpath)
+        np.ascontiguousarray(sc, np.float32).tofile(spath)
+        parts.append("  (param %s (f32 %s)\n    (quant %d 1 (scale-file %s) (codes-file %s)))\n"
+                     % (nm, " ".join(str(d) for d in codes.shape), bits, spath, cpath))
 
-    parts.append(param_f32("E", w["E"]))
+    parts.append(f32p("E", w["E"]))
     quant("LM", np.ascontiguousarray(w["E"].T))
-    parts.append(param_f32("lnf", ones_d))
-    parts.append(param_f32("cosT", cos))
-    parts.append(param_f32("sinT", sin))
+    parts.append(f32p("lnf", ones_d))
+    parts.append(f32p("cosT", cos))
+    parts.append(f32p("sinT", sin))
     quant("Rot", rot)
-    parts.append(param_f32("mask", mask))
-    parts.append(param_f32("lastidx", np.array([T - 1], np.float32)))
+    parts.append(f32p("mask", mask))
+    parts.append(f32p("lastidx", np.array([T - 1], np.float32)))
     for l in range(L):
         for nm in ("ln1_%d", "ln2_%d"):
-            parts.append(param_f32(nm % l, ones_d))
+            parts.append(f32p(nm % l, ones_d))
         for nm in ("qn_%d", "kn_%d"):
-            parts.append(param_f32(nm % l, ones_hd))
+            parts.append(f32p(nm % l, ones_hd))
         for h in range(NQ):
             quant("Wq_%d_%d" % (l, h), w["Wq_%d_%d" % (l, h)])
             quant("Wo_%d_%d" % (l, h), w["Wo_%d_%d" % (l, h)])

@@ -201,3 +201,39 @@ def test_config2_full_size(B):
     print("config2 B=%d: %.4f of outputs within 1e-5/4ulp of the reference order; mean |err| vs exact: "
           "matrix cores %.3g, reference order %.3g" % (B, strict, err_fast.mean(), err_ref.mean()), flush=True)
     assert strict > 0.9
+
+
+def _f32_matmul_models():
+    rng = np.random.default_rng(31)
+    W1 = rng.normal(size=(150, 260)).astype(np.float32)
+    W2 = rng.normal(size=(33, 200)).astype(np.float32)
+    W3 = rng.normal(size=(3, 20, 80)).astype(np.float32)
+    head = "(tgir 1\n  (model mm)\n"
+    return {
+        # W [150, 260] @ x [260, 90]: parameter on the left
+        "left": (head + synth.param_f32("W", W1) + "  (input x (f32 260 90))\n  (block\n"
+                 "    (%0 (f32 150 90) (matmul W x))\n  )\n  (output %0))\n", 260 * 90),
+        # x [70, 33] @ W [33, 200]: parameter on the right
+        "right": (head + synth.param_f32("W", W2) + "  (input x (f32 70 33))\n  (block\n"
+                  "    (%0 (f32 70 200) (matmul x W))\n  )\n  (output %0))\n", 70 * 33),
+        # x [130, 40] @ transpose(x): both operands from the row, k = 40
+        "gram": (head + "  (input x (f32 130 40))\n  (block\n    (%0 (f32 40 130) (transpose x))\n"
+                 "    (%1 (f32 130 130) (matmul x %0))\n  )\n  (output %1))\n", 130 * 40),
+        # batched: x [3, 70, 20] @ W [3, 20, 80]
+        "batched": (head + synth.param_f32("W", W3) + "  (input x (f32 3 70 20))\n  (block\n"
+                    "    (%0 (f32 3 70 80) (matmul x W))\n  )\n  (output %0))\n", 3 * 70 * 20),
+    }
+
+
+@pytest.mark.parametrize("case", ["left", "right", "gram", "batched"])
+def test_f32_matmul_tiles_bit_exact(case):
+    """Unquantized matmuls large enough for the tiled kernel sum their
+    products in the reference's order (p = 0..k-1, multiply then add): bit
+    for bit equal to the oracle, over several batch rows."""
+    print("case f32 matmul", case, flush=True)
+    text, per = _f32_matmul_models()[case]
+    x = np.random.default_rng(7).normal(size=(5, per)).astype(np.float32)
+    x[1] *= 1e-20  # tiny products
+    want, _ = O.Model(text).batch(x)
+    got, _ = hip.Program(text, max_rows=8).batch(x)
+    assert np.array_equal(bits(got), bits(want))

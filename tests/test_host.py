@@ -108,3 +108,25 @@ def test_normal_is_chunk_invariant():
     a = synth.normal(3, 1.0, 1001)
     b = synth.normal(3, 1.0, 5000)
     assert np.array_equal(a, b[:1001])
+
+
+@pytest.mark.parametrize("bits,axis,shape", [(4, 0, (70, 130)), (4, 1, (130, 70)), (8, 0, (33, 257)), (8, 1, (257, 200)),
+                                             (4, 1, (64, 1000))])
+def test_native_rtn_quantizer_matches_python(bits, axis, shape):
+    """tg_hip_quantize_rtn (the library's host quantizer, used for models too
+    large for numpy) writes the same codes and scales as synth.quantize_rtn,
+    itself pinned to the reference's quantizer; all-zero and constant
+    channels included."""
+    from technograd_amd import hip
+    rng = np.random.default_rng(sum(shape) + bits)
+    w = rng.normal(0, 0.02, size=shape).astype(np.float32)
+    if axis == 0:
+        w[3] = 0.0
+        w[5] = 0.25
+    else:
+        w[:, 3] = 0.0
+        w[:, 5] = -0.5
+    c1, s1 = synth.quantize_rtn(w, bits, axis)
+    c2, s2 = hip.quantize_rtn(w, bits, axis, threads=3)
+    assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+    assert np.array_equal(c1, c2)
