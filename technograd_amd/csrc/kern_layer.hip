@@ -322,15 +322,20 @@ __global__ void rowop_k(int op, float *o, long ors, tgk_opd a, int nrow, int col
 	}
 }
 
-// The same per-line loops with the lines staged through LDS: a block takes
+// The same per-line results with the lines staged through LDS: a block takes
 // lpb consecutive lines of one batch row (lpb divides nrow), which are
-// contiguous in memory, so loads and stores are coalesced; thread l then runs
-// line l's loops in the reference's order on its LDS copy. LDS lines are
-// `stride` floats apart, stride odd, so the lanes' sequential walks fall in
-// distinct banks.
+// contiguous in memory, so loads and stores are coalesced. Only the sums
+// keep one thread per line, walking its line in the reference's order; the
+// max, the exponentials, the division and the rmsnorm scaling are
+// elementwise or order-free and use every thread. LDS lines are `stride`
+// floats apart, stride odd, so the sequential walks fall in distinct banks.
+// Softmax's max: x[0] when it is nan, else the largest of x[0] and the
+// non-nan x[i] (the reference's `if (x[i] > mx) mx = x[i]`); its sign of zero
+// cannot change expf(x - mx).
 __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, tgk_opd a, int nrow, int cols, int lpb, int stride)
 {
 	extern __shared__ float lds[];
+	float *lv = lds + lpb * stride; // one value per line (max, then sum or inverse rms)
 	const int bpr = nrow / lpb, r = blockIdx.x / bpr, q0 = (blockIdx.x - r * bpr) * lpb;
 	const int tot = lpb * cols;
 	const float *x = a.p + (long)r * a.rs + (long)q0 * cols;
@@ -347,22 +352,42 @@ __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, t
 		}
 	}
 	__syncthreads();
-	if ((int)threadIdx.x < lpb) {
-		float *y = lds + threadIdx.x * stride;
-		if (op == TGM_SOFTMAX) {
-			float mx = y[0], sum = 0.0f;
-			for (int i = 1; i < cols; i++)
-				if (y[i] > mx) mx = y[i];
-			for (int i = 0; i < cols; i++) {
-				y[i] = expf(y[i] - mx);
-				sum += y[i];
-			}
-			for (int i = 0; i < cols; i++) y[i] /= sum;
-		} else {
+	if (op == TGM_SOFTMAX) {
+		// max: TPB / lpb threads per line, consecutive lanes of one wave (lpb >= 4)
+		const int tpl = TPB / lpb, l = threadIdx.x / tpl, sub = threadIdx.x - l * tpl;
+		float m = -INFINITY;
+		const float *y = lds + l * stride;
+		for (int i = 1 + sub; i < cols; i += tpl) m = fmaxf(m, y[i]);
+		for (int w = tpl / 2; w > 0; w >>= 1) m = fmaxf(m, __shfl_xor(m, w));
+		if (sub == 0) lv[l] = isnan(y[0]) ? y[0] : fmaxf(y[0], m);
+		__syncthreads();
+		for (int e = threadIdx.x; e < tot; e += TPB) {
+			float *z = lds + (e / cols) * stride + e % cols;
+			*z = expf(*z - lv[e / cols]);
+		}
+		__syncthreads();
+		if ((int)threadIdx.x < lpb) {
+			const float *z = lds + threadIdx.x * stride;
 			float sum = 0.0f;
-			for (int i = 0; i < cols; i++) sum += y[i] * y[i];
-			const float inv = 1.0f / sqrtf(sum / (float)cols + 1e-6f);
-			for (int i = 0; i < cols; i++) y[i] = y[i] * inv;
+			for (int i = 0; i < cols; i++) sum += z[i];
+			lv[threadIdx.x] = sum;
+		}
+		__syncthreads();
+		for (int e = threadIdx.x; e < tot; e += TPB) {
+			float *z = lds + (e / cols) * stride + e % cols;
+			*z = *z / lv[e / cols];
+		}
+	} else {
+		if ((int)threadIdx.x < lpb) {
+			const float *z = lds + threadIdx.x * stride;
+			float sum = 0.0f;
+			for (int i = 0; i < cols; i++) sum += z[i] * z[i];
+			lv[threadIdx.x] = 1.0f / sqrtf(sum / (float)cols + 1e-6f);
+		}
+		__syncthreads();
+		for (int e = threadIdx.x; e < tot; e += TPB) {
+			float *z = lds + (e / cols) * stride + e % cols;
+			*z = *z * lv[e / cols];
 		}
 	}
 	__syncthreads();
@@ -593,10 +618,11 @@ void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, i
 	long total = (long)rows * nrow;
 	if (total <= 0) return;
 	const int stride = cols | 1;
-	int lpb = 32;
-	while (lpb > 1 && ((long)lpb * stride * 4 > 65536 || nrow % lpb)) lpb >>= 1;
-	if (cols >= 32 && (long)lpb * stride * 4 <= 65536 && (long)rows * (nrow / lpb) < (1L << 31))
-		rowop_lds_k<<<(unsigned)(rows * (long)(nrow / lpb)), TPB, (size_t)lpb * stride * 4, s>>>(op, o, ors, a, nrow, cols, lpb, stride);
+	int lpb = 32; // a power of two, so TPB / lpb threads share a line's max
+	while (lpb > 1 && ((long)lpb * (stride + 1) * 4 > 65536 || nrow % lpb)) lpb >>= 1;
+	if (cols >= 32 && lpb >= 4 && (long)lpb * (stride + 1) * 4 <= 65536 && (long)rows * (nrow / lpb) < (1L << 31))
+		rowop_lds_k<<<(unsigned)(rows * (long)(nrow / lpb)), TPB, (size_t)lpb * (stride + 1) * 4, s>>>(op, o, ors, a, nrow, cols, lpb,
+														stride);
 	else
 		rowop_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, nrow, cols, total);
 }

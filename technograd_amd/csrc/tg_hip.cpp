@@ -282,7 +282,33 @@ struct LB {
 	Pools P;
 	std::vector<Opnd> where; // value -> operand
 	std::vector<char> loopw; // values written in place by loops (scan carries, slices, stacks)
+	std::vector<int> tview;  // rank-2 transposes read only by one f32 matmul: the transposed value (else -1)
 };
+
+void count_uses(const tgm_block *b, std::vector<int> &u);
+
+// A rank-2 transpose whose only reader is an unquantized rank-2 matmul of the
+// top block is not materialised: the matmul reads the transpose's input with
+// its strides swapped (same elements, same products, same order).
+void mark_transpose_views(LB &L)
+{
+	const tgm_module *m = L.m;
+	L.tview.assign((size_t)m->nval, -1);
+	std::vector<int> uses((size_t)m->nval, 0);
+	count_uses(&m->top, uses);
+	uses[(size_t)m->output]++;
+	const tgm_block &b = m->top;
+	std::vector<int> src((size_t)m->nval, -1);
+	for (int i = 0; i < b.len; i++) {
+		const tgm_ins &in = b.v[i];
+		if (in.op == TGM_TRANSPOSE && m->val[in.a[0]].sh.rank == 2 && uses[(size_t)in.out] == 1) src[(size_t)in.out] = in.a[0];
+		if (in.op != TGM_MATMUL) continue;
+		const tgm_value &va = m->val[in.a[0]], &vb = m->val[in.a[1]];
+		if (va.sh.rank != 2 || vb.sh.rank != 2 || va.qbits || vb.qbits || in.a[0] == in.a[1]) continue;
+		for (int j = 0; j < 2; j++)
+			if (src[(size_t)in.a[j]] >= 0) L.tview[(size_t)in.a[j]] = src[(size_t)in.a[j]];
+	}
+}
 
 Opnd value_opnd(LB &L, int v)
 {
@@ -756,6 +782,14 @@ bool layer_ins(LB &L, const tgm_ins &in)
 		s.ag = (long)mm * kk, s.ai = kk, s.ap = 1;
 		s.bg = (long)kk * nn, s.bp = nn, s.bj = 1;
 		s.og = (long)mm * nn, s.oi = nn, s.oj = 1;
+		if (!quant && L.tview[(size_t)in.a[0]] >= 0) { // A = transpose(X), X [k m]: A[i][p] = X[p][i]
+			s.a = value_opnd(L, L.tview[(size_t)in.a[0]]);
+			s.ai = 1, s.ap = mm;
+		}
+		if (!quant && L.tview[(size_t)in.a[1]] >= 0) { // B = transpose(Y), Y [n k]: B[p][j] = Y[j][p]
+			s.b = value_opnd(L, L.tview[(size_t)in.a[1]]);
+			s.bp = 1, s.bj = kk;
+		}
 		if (quant) {
 			int v = quant == 1 ? in.a[0] : in.a[1];
 			s.bits = m->val[v].qbits;
@@ -783,6 +817,7 @@ bool layer_ins(LB &L, const tgm_ins &in)
 		s.n = (int)m->val[in.a[0]].n;
 		break;
 	case TGM_TRANSPOSE: {
+		if (L.tview[(size_t)in.out] >= 0) return true; // read in place by its matmul
 		const tgm_shape &sa = m->val[in.a[0]].sh;
 		s.kind = ST_TRANS;
 		s.a = value_opnd(L, in.a[0]);
@@ -1464,6 +1499,7 @@ bool build_layer(tg_hip_prog *p)
 	L.P.codes_of.assign(p->m->nval, -1);
 	L.P.scale_of.assign(p->m->nval, -1);
 	mark_loop_values(&p->m->top, L.loopw);
+	mark_transpose_views(L);
 	if (p->m->val[p->m->output].kind == TGM_TMP) { /* written straight into the caller's output rows */
 		L.where[p->m->output].space = SP_OUT;
 		L.where[p->m->output].off = 0;

@@ -237,3 +237,30 @@ def test_f32_matmul_tiles_bit_exact(case):
     want, _ = O.Model(text).batch(x)
     got, _ = hip.Program(text, max_rows=8).batch(x)
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("op,nrow,cols", [("rmsnorm", 64, 32), ("rmsnorm", 24, 1000), ("softmax", 64, 32),
+                                          ("softmax", 48, 100), ("softmax", 32, 512), ("softmax", 5, 33)])
+def test_row_ops_against_oracle(op, nrow, cols):
+    """rmsnorm and softmax over lines of `cols` (the LDS-staged row kernel for
+    32 and more columns): rmsnorm bit for bit (square root and division are
+    correctly rounded), softmax within the f32 bound; nan in the first and in
+    later positions, -inf lines and a line of zeros."""
+    print("case row op", op, nrow, cols, flush=True)
+    text = ("(tgir 1\n  (model ro)\n  (input x (f32 %d %d))\n  (block\n    (%%0 (f32 %d %d) (%s x))\n  )\n"
+            "  (output %%0))\n" % (nrow, cols, nrow, cols, op))
+    x = np.random.default_rng(cols).normal(size=(3, nrow, cols)).astype(np.float32) * 3
+    x[0, 0, 0] = np.nan
+    x[0, 1, cols // 2] = np.nan
+    x[0, 2, :] = -np.inf
+    x[0, 3, :] = 0.0
+    x[1, 4, 0] = -np.inf
+    x = x.reshape(3, -1)
+    want, _ = O.Model(text).batch(x)
+    got, _ = hip.Program(text, max_rows=4).batch(x)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    if op == "rmsnorm":
+        assert np.array_equal(bits(got), bits(want))
+    else:
+        ok = ~np.isnan(want)
+        parity.check_model(np.where(ok, got, 0), np.where(ok, want, 0))
