@@ -298,6 +298,25 @@ __device__ inline double combine_d(int acc0, int acc1, int acc2)
 }
 
 // output (m, c) from tot = sum_k t[c][k] q[m][k]
+// output column c: its segment's base (shifted to the column) and row strides
+struct OutCol {
+	float *p;
+	long orr, oj;
+};
+__device__ inline OutCol out_col(const tgk_qgemm_args &a, int c)
+{
+	if (a.nseg <= 1) return OutCol{ a.o + (long)c * a.oc, a.orr, a.oj };
+	int g = 0;
+	while (g + 1 < a.nseg && c >= a.seg_c0[g + 1]) g++;
+	return OutCol{ a.seg_o[g] + (long)(c - a.seg_c0[g]) * a.oc, a.seg_orr[g], a.seg_oj[g] };
+}
+
+__device__ inline float *out_at(const tgk_qgemm_args &a, int r, int jj, int c)
+{
+	const OutCol o = out_col(a, c);
+	return o.p + (long)r * o.orr + (long)jj * o.oj;
+}
+
 __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot)
 {
 	if (m >= a.M || c >= w.C) return;
@@ -312,7 +331,7 @@ __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 		acc32 = (float)ldexp((double)tot, s.e[m] - 23);
 	}
 	int r = m / a.ni, jj = m - r * a.ni;
-	a.o[(long)r * a.orr + (long)c * a.oc + (long)jj * a.oj] = w.scale[c] * acc32;
+	*out_at(a, r, jj, c) = w.scale[c] * acc32;
 }
 
 // One lane's outputs of a 32-row block: rows mbase + 8 (v / 4) + 4 (lane / 32)
@@ -337,12 +356,32 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 		return;
 	}
 	float sc[NB];
-	long coff[NB];
 	for (int j = 0; j < NB; j++) {
 		const int c = cbase + j * 32 + r32;
 		sc[j] = w.scale[c < w.Cp ? c : 0]; // scales are padded to Cp; columns at or beyond C are not written
-		coff[j] = (long)c * a.oc;
 	}
+	if (a.nseg > 1) { // a merged GEMM: each column's own output
+		OutCol oc[NB];
+		for (int j = 0; j < NB; j++) {
+			const int c = cbase + j * 32 + r32;
+			oc[j] = out_col(a, c < w.C ? c : 0);
+		}
+		for (int v = 0; v < 16; v++) {
+			const int m = mbase + 8 * (v >> 2) + 4 * h + (v & 3);
+			if (m >= a.M) continue;
+			const int E = s.e[m];
+			const double q8 = w.bits == 4 ? 8.0 * (double)s.qsum[m] : 0.0;
+			int r = m, jj = 0;
+			if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
+			for (int j = 0; j < NB; j++) {
+				if (cbase + j * 32 + r32 >= w.C) continue;
+				oc[j].p[(long)r * oc[j].orr + (long)jj * oc[j].oj] = sc[j] * (float)ldexp(totd(j, v) - q8, E - 23);
+			}
+		}
+		return;
+	}
+	long coff[NB];
+	for (int j = 0; j < NB; j++) coff[j] = (long)(cbase + j * 32 + r32) * a.oc;
 	for (int v = 0; v < 16; v++) {
 		const int m = mbase + 8 * (v >> 2) + 4 * h + (v & 3);
 		if (m >= a.M) continue;
@@ -675,6 +714,18 @@ int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, i
 		rc = -1;
 	free(h);
 	free(hs);
+	return rc;
+}
+
+int tgk_qweight_pack_i8(tgk_qweight *w, const int8_t *codes, const float *scale, int bits, int C, int K, hipStream_t st)
+{
+	if (bits == 8) return tgk_qweight_pack(w, (const uint8_t *)codes, scale, 8, 0, C, K, st);
+	const size_t n = (size_t)C * K; /* int4: two codes per byte, element i in byte i / 2, low nibble first */
+	uint8_t *q = (uint8_t *)calloc((n + 1) / 2, 1);
+	if (!q) return -1;
+	for (size_t i = 0; i < n; i++) q[i >> 1] |= (uint8_t)(((unsigned)codes[i] & 15u) << ((i & 1) * 4));
+	const int rc = tgk_qweight_pack(w, q, scale, 4, 0, C, K, st);
+	free(q);
 	return rc;
 }
 

@@ -59,7 +59,14 @@ struct Opnd {
 	long rs = 0;  // row stride in floats (0 for pool values)
 };
 
-enum { ST_BIN, ST_UN, ST_MM, ST_QGEMM, ST_ROW, ST_RED, ST_TRANS, ST_OUTER, ST_TAKE, ST_COPY, ST_SCAN, ST_FILL_STEPS, ST_SSCAN, ST_EW };
+enum { ST_BIN, ST_UN, ST_MM, ST_QGEMM, ST_ROW, ST_RED, ST_TRANS, ST_OUTER, ST_TAKE, ST_COPY, ST_SCAN, ST_FILL_STEPS, ST_SSCAN, ST_EW, ST_NOP };
+
+// one member of a merged quantized GEMM: its output and where its columns start
+struct QSegOut {
+	Opnd o;
+	int c0;
+	long orr, oj;
+};
 
 inline bool same_value(const Opnd &x, const Opnd &y) { return x.space == y.space && x.off == y.off && x.space != SP_NONE; }
 
@@ -111,6 +118,8 @@ struct Step {
 	int ew = -1;
 	// quantized GEMM whose activation digits the previous step left in the scratch
 	int reuse_digits = 0;
+	// quantized GEMM: the weight's model value (-1 for a merged weight) and its output segments
+	int qv = -1, seg = -1;
 };
 
 } // namespace
@@ -130,6 +139,7 @@ struct tg_hip_prog {
 	// layer program
 	std::vector<Step> steps;
 	std::vector<EwStep> ews;
+	std::vector<std::vector<QSegOut>> qsegs; // output segments of merged GEMMs
 	std::vector<tgk_qweight> qws;
 	long arena_floats = 0; // per row
 	float *d_arena = nullptr;
@@ -358,6 +368,8 @@ void place_arena(tg_hip_prog *p, const tgm_module *m)
 			for (const EwStep::In &x : p->ews[(size_t)st.ew].in) touch(x.o, i);
 			for (const Opnd &x : p->ews[(size_t)st.ew].out) touch(x, i);
 		}
+		if (st.kind == ST_QGEMM && st.seg >= 0)
+			for (const QSegOut &x : p->qsegs[(size_t)st.seg]) touch(x.o, i);
 	}
 	touch(p->out, (long)S.size());
 	// scans, innermost first (shorter ranges are nested in longer ones)
@@ -428,6 +440,8 @@ void place_arena(tg_hip_prog *p, const tgm_module *m)
 		for (EwStep::In &x : E.in) fix(x.o);
 		for (Opnd &x : E.out) fix(x);
 	}
+	for (auto &g : p->qsegs)
+		for (QSegOut &x : g) fix(x.o);
 	fix(p->out);
 	p->arena_floats = end;
 }
@@ -516,9 +530,11 @@ void finish_ew(tg_hip_prog *p)
 {
 	std::vector<Opnd> used; // operands read or written by steps other than fused runs, plus the output
 	for (const Step &st : p->steps)
-		if (st.kind != ST_EW)
+		if (st.kind != ST_EW && st.kind != ST_NOP)
 			for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 })
 				if (o->space == SP_ARENA || o->space == SP_OUT) used.push_back(*o);
+	for (const auto &g : p->qsegs)
+		for (const QSegOut &x : g) used.push_back(x.o);
 	for (const EwStep &E : p->ews)
 		for (const EwStep::In &x : E.in) used.push_back(x.o);
 	used.push_back(p->out);
@@ -741,16 +757,15 @@ bool layer_ins(LB &L, const tgm_ins &in)
 			const tgm_value &w = quant == 1 ? va : vb;
 			int v = quant == 1 ? in.a[0] : in.a[1];
 			Opnd x = value_opnd(L, quant == 1 ? in.a[1] : in.a[0]);
-			tgk_qweight qw;
+			tgk_qweight qw; // packed once every step exists (GEMMs on the same activations are merged first)
+			memset(&qw, 0, sizeof qw);
 			int C = w.sh.dim[w.qaxis], K = w.sh.dim[1 - w.qaxis];
-			if (tgk_qweight_pack(&qw, w.q, w.qs, w.qbits, w.qaxis, C, K, L.p->st)) {
-				seterr("cannot place the weights of '%s' on the device", w.name ? w.name : "?");
-				return false;
-			}
-			(void)v;
+			qw.C = C, qw.K = K, qw.bits = w.qbits, qw.axis = w.qaxis;
+			qw.Kp = (K + 63) / 64 * 64, qw.Cp = (C + 255) / 256 * 256;
 			L.p->qws.push_back(qw);
 			s.kind = ST_QGEMM;
 			s.qw = (int)L.p->qws.size() - 1;
+			s.qv = v;
 			s.a = x;
 			if (quant == 1) { // W[C][K] @ x[K][n]: rows (r, j), element k at k*n
 				s.ni = nn;
@@ -761,15 +776,8 @@ bool layer_ins(LB &L, const tgm_ins &in)
 				s.xr = x.rs, s.xj = kk, s.xk = 1;
 				s.orr = s.o.rs, s.oc = 1, s.ojj = nn;
 			}
-			if (!S.empty() && S.back().kind == ST_QGEMM) { // same activations as the GEMM before: its digits stand
-				const Step &pv = S.back();
-				const tgk_qweight &pw = L.p->qws[(size_t)pv.qw];
-				s.reuse_digits = same_value(pv.a, s.a) && pv.a.rs == s.a.rs && pv.ni == s.ni && pv.xr == s.xr &&
-						 pv.xj == s.xj && pv.xk == s.xk && pw.K == qw.K && pw.Kp == qw.Kp;
-			}
 			size_t need = tgk_qgemm_scratch(L.p->max_rows * s.ni, qw.Kp);
 			if (need > L.p->scratch_bytes) L.p->scratch_bytes = need;
-			L.p->stats.weight_bytes += (double)qw.Cp * (qw.bits == 8 ? qw.Kp : qw.Kp / 2) + 4.0 * qw.Cp;
 			L.p->stats.macs += (double)C * K * s.ni;
 			break;
 		}
@@ -1249,9 +1257,22 @@ void exec_step(Run &R, const Step &s)
 		tgk_matmul_exact(st, &d, R.rows);
 		break;
 	}
+	case ST_NOP: break;
 	case ST_QGEMM: {
 		tgk_qgemm_args a;
+		memset(&a, 0, sizeof a);
 		a.w = &p->qws[s.qw];
+		if (s.seg >= 0) {
+			const std::vector<QSegOut> &g = p->qsegs[(size_t)s.seg];
+			a.nseg = (int)g.size();
+			for (size_t k = 0; k < g.size(); k++) {
+				a.seg_c0[k] = g[k].c0;
+				a.seg_o[k] = dst(R, g[k].o);
+				a.seg_orr[k] = g[k].orr;
+				a.seg_oj[k] = g[k].oj;
+			}
+			a.seg_c0[g.size()] = a.w->C;
+		}
 		tgk_opd x = resolve(R, s.a);
 		a.x = x.p;
 		a.xr = s.xr, a.xj = s.xj, a.xk = s.xk, a.ni = s.ni;
@@ -1407,6 +1428,143 @@ int run_pass(tg_hip_prog *p, const float *d_in, int rows, float *d_out, int *d_s
 	return hipok(hipGetLastError(), "layer program launch") ? 0 : -1;
 }
 
+// ------------------------------------------------ quantized GEMMs ----
+
+// activation digits depend on the activation operand, its strides and K
+bool same_activation(const Step &x, const Step &y, const std::vector<tgk_qweight> &q)
+{
+	const tgk_qweight &a = q[(size_t)x.qw], &b = q[(size_t)y.qw];
+	return same_value(x.a, y.a) && x.a.rs == y.a.rs && x.ni == y.ni && x.xr == y.xr && x.xj == y.xj && x.xk == y.xk && a.K == b.K &&
+	       a.Kp == b.Kp;
+}
+
+// steps that a scan body runs (they may not move)
+std::vector<char> in_scan(const std::vector<Step> &S)
+{
+	std::vector<char> in(S.size(), 0);
+	for (size_t i = 0; i < S.size(); i++)
+		if (S[i].kind == ST_SCAN)
+			for (int j = S[i].body_lo; j < S[i].body_hi; j++) in[(size_t)j] = 1;
+	return in;
+}
+
+// Quantized GEMMs of the top level that read the same activations (same
+// operand, strides, K and weight width) become one GEMM over their weights
+// concatenated along C, at the first one's place: its digits are computed
+// once and narrow weights share tiles. Column c of member g is column
+// c0[g] + c of the merged weight and goes to member g's output (TGK_QSEG
+// output segments); every output value is the one the member computes alone.
+// Moving a member up to the first one's place is safe: it reads only the
+// activation, defined before the first one, and a param.
+void merge_qgemms(tg_hip_prog *p, std::vector<std::vector<int8_t>> &mcodes, std::vector<std::vector<float>> &mscales)
+{
+	auto &S = p->steps;
+	const std::vector<char> inscan = in_scan(S);
+	std::vector<char> done(S.size(), 0);
+	for (size_t i = 0; i < S.size(); i++) {
+		if (S[i].kind != ST_QGEMM || inscan[i] || done[i]) continue;
+		std::vector<size_t> g{ i };
+		const tgk_qweight &w0 = p->qws[(size_t)S[i].qw];
+		long ctot = w0.C;
+		for (size_t j = i + 1; j < S.size() && g.size() < TGK_QSEG; j++) {
+			const Step &t = S[j];
+			if (t.kind != ST_QGEMM || inscan[j] || done[j] || !same_activation(S[i], t, p->qws) || t.oc != S[i].oc) continue;
+			const tgk_qweight &w = p->qws[(size_t)t.qw];
+			if (w.bits != w0.bits || ctot + w.C > (1L << 20)) continue;
+			g.push_back(j);
+			ctot += w.C;
+		}
+		if (g.size() < 2) continue;
+		const tgm_module *m = p->m;
+		const int K = w0.K;
+		std::vector<int8_t> codes((size_t)ctot * K);
+		std::vector<float> scales((size_t)ctot);
+		std::vector<QSegOut> segs;
+		long c0 = 0;
+		for (size_t u : g) {
+			const Step &t = S[u];
+			const tgm_value &v = m->val[t.qv];
+			const tgk_qweight &w = p->qws[(size_t)t.qw];
+			for (int c = 0; c < w.C; c++) {
+				for (int k = 0; k < K; k++)
+					codes[(size_t)(c0 + c) * K + k] = (int8_t)tgm_code(&v, v.qaxis == 0 ? (long)c * K + k : (long)k * w.C + c);
+				scales[(size_t)(c0 + c)] = v.qs[c];
+			}
+			segs.push_back({ t.o, (int)c0, t.orr, t.ojj });
+			c0 += w.C;
+			done[u] = 1;
+		}
+		tgk_qweight mw;
+		memset(&mw, 0, sizeof mw);
+		mw.C = (int)ctot, mw.K = K, mw.bits = w0.bits, mw.axis = 0;
+		mw.Kp = w0.Kp, mw.Cp = (int)((ctot + 255) / 256 * 256);
+		p->qws.push_back(mw);
+		mcodes.resize(p->qws.size());
+		mscales.resize(p->qws.size());
+		mcodes.back() = std::move(codes);
+		mscales.back() = std::move(scales);
+		Step &h = S[i];
+		h.qw = (int)p->qws.size() - 1;
+		h.qv = -1;
+		h.seg = (int)p->qsegs.size();
+		p->qsegs.push_back(std::move(segs));
+		for (size_t k = 1; k < g.size(); k++) S[g[k]].kind = ST_NOP;
+	}
+}
+
+// Pack every weight a GEMM step uses: a merged weight from its concatenated
+// codes, any other from its model value.
+bool pack_weights(tg_hip_prog *p, std::vector<std::vector<int8_t>> &mcodes, std::vector<std::vector<float>> &mscales)
+{
+	mcodes.resize(p->qws.size());
+	mscales.resize(p->qws.size());
+	std::vector<char> used(p->qws.size(), 0);
+	std::vector<int> src(p->qws.size(), -1);
+	for (const Step &t : p->steps)
+		if (t.kind == ST_QGEMM) used[(size_t)t.qw] = 1, src[(size_t)t.qw] = t.qv;
+	for (size_t i = 0; i < p->qws.size(); i++) {
+		tgk_qweight &w = p->qws[i];
+		if (!used[i]) {
+			memset(&w, 0, sizeof w);
+			continue;
+		}
+		int rc;
+		const char *name = "a merged weight";
+		if (src[i] >= 0) {
+			const tgm_value &v = p->m->val[src[i]];
+			name = v.name ? v.name : "?";
+			rc = tgk_qweight_pack(&w, v.q, v.qs, v.qbits, v.qaxis, w.C, w.K, p->st);
+		} else {
+			rc = tgk_qweight_pack_i8(&w, mcodes[i].data(), mscales[i].data(), w.bits, w.C, w.K, p->st);
+		}
+		std::vector<int8_t>().swap(mcodes[i]);
+		std::vector<float>().swap(mscales[i]);
+		if (rc) {
+			seterr("cannot place the weights of %s on the device", name);
+			return false;
+		}
+		p->stats.weight_bytes += (double)w.Cp * (w.bits == 8 ? w.Kp : w.Kp / 2) + 4.0 * w.Cp;
+	}
+	return true;
+}
+
+// A GEMM whose activation digits are already in the scratch: the last GEMM
+// run before it, with nothing but non-GEMM steps between (which leave the
+// scratch alone), read the same activations. Scan bodies start afresh.
+void mark_digit_reuse(tg_hip_prog *p)
+{
+	auto &S = p->steps;
+	const std::vector<char> inscan = in_scan(S);
+	int last = -1;
+	for (size_t i = 0; i < S.size(); i++) {
+		Step &t = S[i];
+		if (t.kind == ST_SCAN || (i > 0 && inscan[i] != inscan[i - 1])) last = -1;
+		if (t.kind != ST_QGEMM) continue;
+		t.reuse_digits = last >= 0 && !inscan[i] && same_activation(S[(size_t)last], t, p->qws);
+		last = inscan[i] ? -1 : (int)i;
+	}
+}
+
 // ------------------------------------------- rows read through take ----
 
 void count_uses(const tgm_block *b, std::vector<int> &u)
@@ -1507,6 +1665,11 @@ bool build_layer(tg_hip_prog *p)
 	}
 	if (!layer_block(L, &p->m->top)) return false;
 	p->out = value_opnd(L, p->m->output);
+	std::vector<std::vector<int8_t>> mcodes;
+	std::vector<std::vector<float>> mscales;
+	merge_qgemms(p, mcodes, mscales);
+	if (!pack_weights(p, mcodes, mscales)) return false;
+	mark_digit_reuse(p);
 	finish_ew(p);
 	place_arena(p, p->m);
 	if (!upload_pools(p, L.P)) return false;

@@ -111,8 +111,16 @@ typedef struct {
 } tgk_qweight;
 
 int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, int bits, int axis, int C, int K, hipStream_t s);
+/* the same from int8 codes one per element, laid out [C][K] (axis 0) */
+int tgk_qweight_pack_i8(tgk_qweight *w, const int8_t *codes, const float *scale, int bits, int C, int K, hipStream_t s);
 void tgk_qweight_free(tgk_qweight *w);
 
+/* Output segments of a merged GEMM (several weights that read the same
+ * activations, concatenated along C): columns seg_c0[s] .. seg_c0[s + 1] - 1
+ * go to segment s, column c as column c - seg_c0[s] of an output with base
+ * seg_o[s], batch-row stride seg_orr[s], inner-row stride seg_oj[s] and the
+ * common channel stride oc. nseg <= 1: one output (o, orr, oc, oj). */
+#define TGK_QSEG 32
 typedef struct {
 	const tgk_qweight *w;
 	const float *x;
@@ -121,6 +129,10 @@ typedef struct {
 	float *o;
 	long orr, oc, oj;       /* output strides: batch row, channel, inner row */
 	int M;                  /* rows of X = batch rows * ni */
+	int nseg;
+	int seg_c0[TGK_QSEG + 1];
+	float *seg_o[TGK_QSEG];
+	long seg_orr[TGK_QSEG], seg_oj[TGK_QSEG];
 } tgk_qgemm_args;
 
 /* scratch: bytes needed for M rows of K inputs */
