@@ -108,6 +108,27 @@ int tg_hip_reset_stats(tg_hip_prog *p);
  * device is used. 0 on success, -1 on bad arguments. */
 int tg_hip_quantize_rtn(const float *w, int rows, int cols, int bits, int axis, signed char *codes, float *scales, int threads);
 
+/* KV-cache greedy decoding for models in the layout of the reference's Qwen3
+ * importer (examples/qwen3/import.py:46-130: params E, LM, Rot, lnf, ln1_l,
+ * ln2_l, qn_l, kn_l, Wq_l_h, Wk_l_j, Wv_l_j, Wo_l_h, Wg_l, Wu_l, Wd_l, all
+ * matmul weights quantized on axis 1), plus RoPE tables `rope_cos` and
+ * `rope_sin` with a row per position. No counterpart in the reference, which
+ * runs such a model at one fixed length and has no cache: for callers that
+ * generate text. Each generated token's logits equal the fixed-length forward's
+ * at that position, bit for bit (finite activations). The decoder packs its
+ * own copy of the weights and sizes its cache for max_seqs x max_len
+ * positions; the program p must outlive it. */
+typedef struct tg_hip_dec tg_hip_dec;
+tg_hip_dec *tg_hip_dec_create(const tg_hip_prog *p, int max_seqs, int max_prompt, int max_len);
+/* Prompts d_prompt [seqs][prompt_len] (f32 token ids, device memory): prefill,
+ * then `steps` greedy tokens per sequence into d_tokens [seqs][steps] (int32,
+ * device; may be NULL), the logits of each step into d_logits
+ * [steps][seqs][vocab] (device; may be NULL). Asynchronous on the program's
+ * stream (tg_hip_sync waits). 0 on success. */
+int tg_hip_dec_generate(tg_hip_dec *d, const float *d_prompt, int seqs, int prompt_len, int steps, int *d_tokens, float *d_logits);
+int tg_hip_dec_info(const tg_hip_dec *d, int *layers, int *vocab);
+void tg_hip_dec_free(tg_hip_dec *d);
+
 /* Device memory helpers for callers without their own allocator. */
 void *tg_hip_dev_alloc(size_t bytes);
 int tg_hip_dev_free(void *d);

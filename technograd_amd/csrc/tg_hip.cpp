@@ -1760,6 +1760,11 @@ int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *ste
 
 } // namespace
 
+// for the decoder (tg_decode.cpp): the program's model and stream
+const tgm_module *tgh_prog_module(const tg_hip_prog *p) { return p->m; }
+hipStream_t tgh_prog_stream(const tg_hip_prog *p) { return p->st; }
+void tgh_set_error(const char *msg) { seterr("%s", msg); }
+
 extern "C" {
 
 int tg_hip_init(int device)

@@ -110,6 +110,31 @@ typedef struct {
 	int axis;                /* original layout: 0 = [C][K], 1 = [K][C] */
 } tgk_qweight;
 
+/* KV-cache decoder kernels (kern_decode.hip). The caches are
+ * [seq][layer][kv head][position][HD] f32: kv_seq floats per sequence,
+ * kv_layer the offset of the current layer. */
+typedef struct {
+	const float *hq, *rt;    /* normed, scaled q and k lines [rows][NQ + NKV][HD], and their x @ Rot */
+	const float *qkv;        /* projection output [rows][ctot] (v after q and k) */
+	long ctot;
+	const float *cosT, *sinT; /* [P][HD] */
+	float *qr, *K, *V;        /* rotated q [rows][NQ][HD]; caches */
+	long kv_seq, kv_layer;
+	int T0, p0, NQ, NKV, HD, P;
+} tgk_dec_rope_args;
+void tgk_dec_rope(hipStream_t s, const tgk_dec_rope_args *a, int rows);
+typedef struct {
+	const float *qr;          /* [seqs][NQ][HD] */
+	const float *K, *V;
+	float *att;               /* [seqs][NQ][HD] */
+	long kv_seq, kv_layer;
+	int NQ, NKV, HD, P, p;    /* keys at positions 0 .. p */
+	float scale;
+} tgk_dec_attn_args;
+void tgk_dec_attn(hipStream_t s, const tgk_dec_attn_args *a, int seqs);
+void tgk_dec_sumchain(hipStream_t s, float *h, const float *o, int NQ, long per_head);
+void tgk_dec_argmax(hipStream_t s, const float *x, long xrs, int V, int rows, float *idf, int *idi, long idi_stride);
+
 int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, int bits, int axis, int C, int K, hipStream_t s);
 /* the same from int8 codes one per element, laid out [C][K] (axis 0) */
 int tgk_qweight_pack_i8(tgk_qweight *w, const int8_t *codes, const float *scale, int bits, int C, int K, hipStream_t s);

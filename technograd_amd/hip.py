@@ -43,6 +43,11 @@ def lib():
         L.tg_hip_sync.argtypes = [vp]
         L.tg_hip_matmul_q.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip, ip, ip]
         L.tg_hip_quantize_rtn.argtypes = [vp, ip, ip, ip, ip, vp, vp, ip]
+        L.tg_hip_dec_create.restype = vp
+        L.tg_hip_dec_create.argtypes = [vp, ip, ip, ip]
+        L.tg_hip_dec_generate.argtypes = [vp, vp, ip, ip, ip, vp, vp]
+        L.tg_hip_dec_info.argtypes = [vp, ctypes.POINTER(ip), ctypes.POINTER(ip)]
+        L.tg_hip_dec_free.argtypes = [vp]
         L.tg_hip_free.argtypes = [vp]
         L.tg_hip_error.restype = ctypes.c_char_p
         L.tg_hip_stats.argtypes = [vp, ctypes.POINTER(Stats)]
@@ -185,3 +190,47 @@ def quantize_rtn(w, bits, axis, threads=None):
     t = threads or min(16, os.cpu_count() or 1)
     _check(lib().tg_hip_quantize_rtn(_p(w), rows, cols, bits, axis, _p(codes), _p(scales), t), "tg_hip_quantize_rtn")
     return codes, scales
+
+
+class Decoder:
+    """tg_hip_dec_*: KV-cache greedy decoding of a loaded program in the
+    Qwen3 importer's layout (the program must outlive the decoder)."""
+
+    def __init__(self, prog, max_seqs, max_prompt, max_len):
+        self.prog = prog
+        self.h = lib().tg_hip_dec_create(prog.h, max_seqs, max_prompt, max_len)
+        if not self.h:
+            raise RuntimeError("tg_hip_dec_create: " + lib().tg_hip_error().decode())
+        layers, vocab = ctypes.c_int(), ctypes.c_int()
+        lib().tg_hip_dec_info(self.h, ctypes.byref(layers), ctypes.byref(vocab))
+        self.layers, self.vocab = layers.value, vocab.value
+
+    def generate_device(self, d_prompt, seqs, prompt_len, steps, d_tokens=None, d_logits=None):
+        """Asynchronous, device buffers (DeviceBuffer or raw pointers)."""
+        ptr = lambda b: None if b is None else (b.ptr if hasattr(b, "ptr") else b)
+        _check(lib().tg_hip_dec_generate(self.h, ptr(d_prompt), seqs, prompt_len, steps, ptr(d_tokens), ptr(d_logits)),
+               "tg_hip_dec_generate")
+
+    def generate(self, prompts, steps, logits=False):
+        """Host arrays: prompts [seqs][prompt_len] token ids -> tokens
+        [seqs][steps] (int32), and logits [steps][seqs][vocab] if asked."""
+        prompts = np.ascontiguousarray(prompts, np.float32)
+        seqs, plen = prompts.shape
+        dp = DeviceBuffer.from_array(prompts)
+        dt = DeviceBuffer(seqs * steps * 4)
+        dl = DeviceBuffer(steps * seqs * self.vocab * 4) if logits else None
+        self.generate_device(dp, seqs, plen, steps, dt, dl)
+        self.prog.sync()
+        tokens = dt.to_array(np.int32, (seqs, steps))
+        return (tokens, dl.to_array(np.float32, (steps, seqs, self.vocab))) if logits else tokens
+
+    def close(self):
+        if self.h:
+            lib().tg_hip_dec_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

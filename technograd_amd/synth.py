@@ -450,7 +450,7 @@ def rope_tables(T, HD, theta=1e6):
 
 
 def qwen3_tgir(name="qwen3", L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, V=151936, T=512, bits=4, seed=3, files=None,
-               quantizer=None):
+               quantizer=None, rope_len=None):
     """Config 3's model at fixed sequence length T: the graph
     examples/qwen3/import.py:110-130 emits (per-head rank-2 matmuls, GQA with
     NQ / NKV query heads per KV head, rotate-half RoPE as x * cos + (x @ Rot)
@@ -465,7 +465,10 @@ def qwen3_tgir(name="qwen3", L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, V=1519
     the text refers to them with the backend's data-file / scale-file /
     codes-file forms (a full-size model as TGIR text would be several GB).
     quantizer: an RTN function with quantize_rtn's signature (the library's
-    native one for full size); quantize_rtn by default."""
+    native one for full size); quantize_rtn by default.
+    rope_len: also emit the RoPE tables `rope_cos` / `rope_sin` with that many
+    rows (the KV-cache decoder reads them for positions beyond T; the
+    fixed-length graph does not use them). Row p equals row p of cosT / sinT."""
     w = qwen3_weights(L, D, NQ, NKV, HD, FF, V, seed)
     cos, sin, rot = rope_tables(T, HD)
     mask = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
@@ -499,6 +502,10 @@ def qwen3_tgir(name="qwen3", L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, V=1519
     parts.append(f32p("sinT", sin))
     quant("Rot", rot)
     parts.append(f32p("mask", mask))
+    if rope_len:
+        rc, rs, _ = rope_tables(rope_len, HD)
+        parts.append(f32p("rope_cos", rc))
+        parts.append(f32p("rope_sin", rs))
     parts.append(f32p("lastidx", np.array([T - 1], np.float32)))
     for l in range(L):
         for nm in ("ln1_%d", "ln2_%d"):
