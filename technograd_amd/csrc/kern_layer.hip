@@ -617,6 +617,12 @@ void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, i
 {
 	long total = (long)rows * nrow;
 	if (total <= 0) return;
+	if (a.rs == (long)nrow * cols && ors == (long)nrow * cols && total < (1L << 31)) {
+		// rows back to back in memory on both sides: all lines of the pass are one row's lines
+		// (lets one-line rows, such as one token each, share blocks)
+		nrow = (int)total;
+		rows = 1;
+	}
 	const int stride = cols | 1;
 	int lpb = 32; // a power of two, so TPB / lpb threads share a line's max
 	while (lpb > 1 && ((long)lpb * (stride + 1) * 4 > 65536 || nrow % lpb)) lpb >>= 1;

@@ -38,6 +38,8 @@ struct tg_hip_dec {
 	const float *E = nullptr, *lnf = nullptr, *cosT = nullptr, *sinT = nullptr, *dscale = nullptr;
 	std::vector<const float *> ln1, ln2, qkg;
 	std::vector<int> wqkv, wgu, wd, wo; // indices into ws (wo: L x NQ)
+	std::vector<const int *> wo_codes;  // per layer: all heads' output projections for a step, int32 [NQ][HD/4][D]
+	std::vector<const float *> wo_scales; // per layer: [NQ][D]
 	int wrot = -1, wlm = -1;
 	// cache and work buffers
 	float *K = nullptr, *Vc = nullptr;
@@ -99,6 +101,31 @@ bool upload(tg_hip_dec *d, const float **dst, const float *src, size_t n)
 	if (!alloc(d, &q, n)) return false;
 	*dst = q;
 	return hip_ok(hipMemcpyAsync(q, src, n * sizeof(float), hipMemcpyHostToDevice, d->st), "decoder upload");
+}
+
+// one layer's per-head output projections W_h [HD][D] (axis-1 scales) as
+// the step kernel's code words: int32 [NQ][HD/4][D], codes of k = 4 k4 .. 4 k4
+// + 3 in bytes 0 .. 3 of word (h, k4, c); scales [NQ][D]
+bool pack_heads(tg_hip_dec *d, const tgm_module *m, const std::vector<int> &vs, const int **codes, const float **scales)
+{
+	const int HD = d->HD, D = d->D, NQ = (int)vs.size();
+	std::vector<int> w((size_t)NQ * (HD / 4) * D, 0);
+	std::vector<float> sc((size_t)NQ * D);
+	for (int h = 0; h < NQ; h++) {
+		const tgm_value &x = m->val[vs[(size_t)h]];
+		if (x.sh.rank != 2 || x.sh.dim[0] != HD || x.sh.dim[1] != D || !x.qbits || x.qaxis != 1) return false;
+		for (int k = 0; k < HD; k++)
+			for (int c = 0; c < D; c++) {
+				const unsigned b = (unsigned)(tgm_code(&x, (long)k * D + c) & 255);
+				w[((size_t)h * (HD / 4) + k / 4) * D + c] |= (int)(b << (8 * (k % 4)));
+			}
+		memcpy(&sc[(size_t)h * D], x.qs, (size_t)D * sizeof(float));
+	}
+	int *q;
+	if (!alloc(d, &q, w.size()) || !hip_ok(hipMemcpyAsync(q, w.data(), w.size() * sizeof(int), hipMemcpyHostToDevice, d->st), "decoder upload"))
+		return false;
+	*codes = q;
+	return upload(d, scales, sc.data(), sc.size());
 }
 
 // pack params (each [K][C_i], quantized on axis 1, x @ W) concatenated along C
@@ -209,9 +236,12 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 				tgk_matmul_exact(st, &m, S);
 			}
 		}
-		for (int hh = 0; hh < d->NQ; hh++)
-			gemm(d, d->wo[(size_t)l * d->NQ + hh], d->att + (long)hh * d->HD, (long)d->NQ * d->HD, 1, 0, rows, d->wout + (long)hh * rows * D,
-			     D, 0);
+		if (T0 == 1 && tgk_dec_wo_lds(rows, d->HD) <= 65536) // a step: all heads in one launch, the same values
+			tgk_dec_wo(st, d->att, d->wo_codes[(size_t)l], d->wo_scales[(size_t)l], d->wout, rows, d->NQ, d->HD, d->D);
+		else
+			for (int hh = 0; hh < d->NQ; hh++)
+				gemm(d, d->wo[(size_t)l * d->NQ + hh], d->att + (long)hh * d->HD, (long)d->NQ * d->HD, 1, 0, rows,
+				     d->wout + (long)hh * rows * D, D, 0);
 		tgk_dec_sumchain(st, d->h, d->wout, d->NQ, (long)rows * D);
 		norm_gain(d, d->n, d->h, D, 1, d->D, d->ln2[(size_t)l], rows);
 		gemm(d, d->wgu[(size_t)l], d->n, D, 1, 0, rows, d->gu, 2L * d->FF, 0);
@@ -263,6 +293,11 @@ bool build(tg_hip_dec *d)
 	if (!d->L || !d->NQ || !d->NKV || d->NQ % d->NKV) return err("decoder: no layers or heads in the importer's naming");
 	d->HD = m->val[find(m, "Wq_0_0")].sh.dim[1];
 	d->FF = m->val[find(m, "Wg_0")].sh.dim[1];
+	// one step's attention block: the scores of all positions in LDS; 1, 2, 4 or 8 query heads per KV head
+	const long grp = d->NQ / d->NKV, lds = (grp * d->P + grp * d->HD + grp) * 4;
+	if ((grp != 1 && grp != 2 && grp != 4 && grp != 8) || d->HD % 16)
+		return err("decoder: needs 1, 2, 4 or 8 query heads per KV head and a head size that is a multiple of 16%s", "");
+	if (lds > 65536) return err("decoder: %s%ld positions do not fit one step's attention (LDS)", "", d->P);
 	if (m->val[vcos].sh.rank != 2 || m->val[vcos].sh.dim[1] != d->HD || m->val[vcos].sh.dim[0] < d->P)
 		return err("decoder: rope tables need %s%ld rows", "", d->P);
 	d->scale = 0.0f; // the graph's attention scale: its first constant (the importer writes 1/sqrt(HD) first)
@@ -298,12 +333,17 @@ bool build(tg_hip_dec *d)
 		const int i1 = pack_concat(d, m, qkv), i2 = pack_concat(d, m, gu), i3 = pack_concat(d, m, { find(m, nm("Wd_%d", l)) });
 		if (i1 < 0 || i2 < 0 || i3 < 0) return err("decoder: cannot place layer %s%ld's weights", "", l);
 		d->wqkv.push_back(i1), d->wgu.push_back(i2), d->wd.push_back(i3);
+		std::vector<int> wo;
 		for (int h = 0; h < d->NQ; h++) {
 			const int v = find(m, nm("Wo_%d_%d", l, h));
 			const int i = v < 0 ? -1 : pack_concat(d, m, { v });
 			if (i < 0) return err("decoder: cannot place layer %s%ld's output projections", "", l);
-			d->wo.push_back(i);
+			d->wo.push_back(i), wo.push_back(v);
 		}
+		const int *woc = nullptr;
+		const float *wos = nullptr;
+		if (!pack_heads(d, m, wo, &woc, &wos)) return err("decoder: cannot place layer %s%ld's output projections", "", l);
+		d->wo_codes.push_back(woc), d->wo_scales.push_back(wos);
 	}
 	d->wrot = pack_concat(d, m, { vRot });
 	d->wlm = pack_concat(d, m, { vLM });

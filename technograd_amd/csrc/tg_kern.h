@@ -133,6 +133,11 @@ typedef struct {
 } tgk_dec_attn_args;
 void tgk_dec_attn(hipStream_t s, const tgk_dec_attn_args *a, int seqs);
 void tgk_dec_sumchain(hipStream_t s, float *h, const float *o, int NQ, long per_head);
+/* per-head output projections of `rows` token rows, all heads in one launch,
+ * values equal to the digit + matrix-core path; codes int32 [NQ][HD/4][D],
+ * 4 consecutive k's int8 codes per word */
+size_t tgk_dec_wo_lds(int rows, int HD);
+void tgk_dec_wo(hipStream_t s, const float *att, const int *codes, const float *scales, float *out, int rows, int NQ, int HD, int D);
 void tgk_dec_argmax(hipStream_t s, const float *x, long xrs, int V, int rows, float *idf, int *idi, long idi_stride);
 
 int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, int bits, int axis, int C, int K, hipStream_t s);
