@@ -4,6 +4,7 @@
 // order (this file is compiled with -ffp-contract=off), so a decoded token's
 // logits equal the fixed-length forward's at that position bit for bit.
 #include "tg_kern.h"
+#include "tg_qdigits.h"
 
 #include <math.h>
 
@@ -44,72 +45,134 @@ __global__ void rope_cache_k(tgk_dec_rope_args a, long total)
 // division; out[d] = sum over keys of prob * v[d] in key order. The
 // fixed-length graph's row for this position has further keys whose masked
 // scores give probabilities of exactly 0: they change neither the max nor the
-// sums. A thread takes one key for all GRP query heads (K read once, GRP
-// independent chains) and loads its K values 16 at a time before the ordered
-// multiply-adds; the P V chain of each (head, d) loads 8 keys ahead. Every
-// score and every output stays one thread's sum in order. HD % 16 == 0.
-template <int GRP>
-__global__ __launch_bounds__(256) void dec_attn_k(tgk_dec_attn_args a)
+// sums. K, then V, stream through LDS in chunks of ck keys: every thread
+// loads its share of the next chunk (16-byte loads) before the current one is
+// used, so a chunk's loads are in flight while the previous chunk's chains
+// run. Each score, each sum and each output stays one thread's sum in order:
+// a (key, head) thread per score, a (head, d) thread per output, carried
+// across chunks. LDS rows are HD + 4 floats apart: 16-byte reads of
+// consecutive rows by consecutive lanes hit distinct banks. HD % 16 == 0.
+constexpr int ATT_TPB = 512, ATT_R = 4; // threads; float4 loads per thread and chunk
+
+int attn_chunk(int HD) // keys per chunk: ATT_R float4 loads per thread, at most 64
 {
-	extern __shared__ float sh[];
-	const int n = a.p + 1, HD = a.HD;
-	const int s = blockIdx.x / a.NKV, j = blockIdx.x - s * a.NKV;
-	float *sc = sh;          // [GRP][n]
-	float *q = sc + GRP * n; // [GRP][HD]
-	float *lv = q + GRP * HD; // [GRP] max, then sum
+	int ck = 64;
+	while (ck > 1 && ck * (HD / 4) > ATT_R * ATT_TPB) ck >>= 1;
+	return ck;
+}
+
+// sum of z[0 .. n) in index order, z 16-byte aligned: loads 32 ahead of the adds
+__device__ inline float ordered_sum(const float *z, int n)
+{
+	float sum = 0.0f;
+	int i = 0;
+	for (; i + 32 <= n; i += 32) {
+		float4 b[8];
+		for (int j = 0; j < 8; j++) b[j] = *(const float4 *)(z + i + 4 * j);
+		for (int j = 0; j < 8; j++) {
+			sum += b[j].x;
+			sum += b[j].y;
+			sum += b[j].z;
+			sum += b[j].w;
+		}
+	}
+	for (; i < n; i++) sum += z[i];
+	return sum;
+}
+
+template <int GRP>
+__global__ __launch_bounds__(ATT_TPB) void dec_attn_k(tgk_dec_attn_args a, int ck)
+{
+	extern __shared__ float4 sh4[];
+	const int n = a.p + 1, HD = a.HD, H4 = HD / 4, KS = H4 + 1, nst = (n + 3) & ~3, per = ck * H4;
+	float4 *kv = sh4;                  // [ck][KS] the staged chunk of K or V
+	float *q = (float *)(kv + ck * KS); // [GRP][HD]
+	float *sc = q + GRP * HD;           // [GRP][nst] scores, then probabilities
+	float *lv = sc + GRP * nst;         // [GRP] max, then sum
+	const int tid = threadIdx.x, s = blockIdx.x / a.NKV, j = blockIdx.x - s * a.NKV;
 	const float *K = a.K + (long)s * a.kv_seq + a.kv_layer + (long)j * a.P * HD;
 	const float *V = a.V + (long)s * a.kv_seq + a.kv_layer + (long)j * a.P * HD;
-	for (int e = threadIdx.x; e < GRP * HD; e += blockDim.x) q[e] = a.qr[((long)s * a.NQ + j * GRP) * HD + e];
-	__syncthreads();
-	for (int key = threadIdx.x; key < n; key += blockDim.x) {
-		const float4 *kr = (const float4 *)(K + (long)key * HD);
-		float acc[GRP];
-		for (int g = 0; g < GRP; g++) acc[g] = 0.0f;
-		for (int d0 = 0; d0 < HD; d0 += 16) {
-			float k[16];
-			for (int u = 0; u < 4; u++) {
-				const float4 v = kr[d0 / 4 + u];
-				k[4 * u] = v.x, k[4 * u + 1] = v.y, k[4 * u + 2] = v.z, k[4 * u + 3] = v.w;
-			}
-			for (int dd = 0; dd < 16; dd++)
-				for (int g = 0; g < GRP; g++) acc[g] = acc[g] + q[g * HD + d0 + dd] * k[dd];
+	float4 rg[ATT_R];
+	auto fetch = [&](const float *base, int c0) { // chunk of keys c0 .. c0 + ck - 1 into registers
+		for (int u = 0; u < ATT_R; u++) {
+			const int e = tid + u * ATT_TPB, key = c0 + e / H4;
+			rg[u] = e < per && key < n ? ((const float4 *)(base + (long)key * HD))[e % H4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 		}
-		for (int g = 0; g < GRP; g++) sc[g * n + key] = acc[g] * a.scale + 0.0f;
+	};
+	auto stash = [&]() {
+		for (int u = 0; u < ATT_R; u++) {
+			const int e = tid + u * ATT_TPB;
+			if (e < per) kv[(e / H4) * KS + e % H4] = rg[u];
+		}
+	};
+	for (int e = tid; e < GRP * HD; e += ATT_TPB) q[e] = a.qr[((long)s * a.NQ + j * GRP) * HD + e];
+	fetch(K, 0);
+	for (int c0 = 0; c0 < n; c0 += ck) {
+		__syncthreads(); // the previous chunk's chains are done with kv
+		stash();
+		__syncthreads();
+		fetch(c0 + ck < n ? K : V, c0 + ck < n ? c0 + ck : 0); // next chunk (or V's first) in flight meanwhile
+		for (int it = tid; it < ck * GRP; it += ATT_TPB) {
+			const int g = it / ck, kk = it - g * ck;
+			if (c0 + kk >= n) continue;
+			const float4 *kr = kv + kk * KS, *qg = (const float4 *)(q + g * HD);
+			float acc = 0.0f;
+			for (int d4 = 0; d4 < H4; d4++) {
+				const float4 k4 = kr[d4], q4 = qg[d4];
+				acc = acc + q4.x * k4.x;
+				acc = acc + q4.y * k4.y;
+				acc = acc + q4.z * k4.z;
+				acc = acc + q4.w * k4.w;
+			}
+			sc[g * nst + c0 + kk] = acc * a.scale + 0.0f;
+		}
 	}
 	__syncthreads();
-	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-	for (int g = wave; g < GRP; g += blockDim.x >> 6) { // max: a wave per query head
-		const float *r = sc + g * n;
+	const int wave = tid >> 6, lane = tid & 63;
+	for (int g = wave; g < GRP; g += ATT_TPB >> 6) { // max: a wave per query head
+		const float *r = sc + g * nst;
 		float m = -INFINITY;
 		for (int key = 1 + lane; key < n; key += 64) m = fmaxf(m, r[key]);
 		for (int w = 32; w > 0; w >>= 1) m = fmaxf(m, __shfl_xor(m, w));
 		if (lane == 0) lv[g] = isnan(r[0]) ? r[0] : fmaxf(r[0], m);
 	}
 	__syncthreads();
-	for (int e = threadIdx.x; e < GRP * n; e += blockDim.x) sc[e] = expf(sc[e] - lv[e / n]);
-	__syncthreads();
-	if ((int)threadIdx.x < GRP) {
-		const float *r = sc + threadIdx.x * n;
-		float sum = 0.0f;
-		for (int key = 0; key < n; key++) sum += r[key];
-		lv[threadIdx.x] = sum;
+	for (int e = tid; e < GRP * nst; e += ATT_TPB) {
+		const int g = e / nst;
+		if (e - g * nst < n) sc[e] = expf(sc[e] - lv[g]);
 	}
 	__syncthreads();
-	for (int e = threadIdx.x; e < GRP * n; e += blockDim.x) sc[e] = sc[e] / lv[e / n];
+	if (tid < GRP) lv[tid] = ordered_sum(sc + tid * nst, n);
 	__syncthreads();
-	for (int e = threadIdx.x; e < GRP * HD; e += blockDim.x) {
-		const int g = e / HD, d = e - g * HD;
-		const float *r = sc + g * n;
-		const float *vp = V + d;
-		float acc = 0.0f;
-		int key = 0;
-		for (; key + 8 <= n; key += 8) {
-			float v[8];
-			for (int u = 0; u < 8; u++) v[u] = vp[(long)(key + u) * HD];
-			for (int u = 0; u < 8; u++) acc = acc + r[key + u] * v[u];
+	for (int e = tid; e < GRP * nst; e += ATT_TPB) {
+		const int g = e / nst;
+		if (e - g * nst < n) sc[e] = sc[e] / lv[g];
+	}
+	constexpr int OI = (GRP * 256 + ATT_TPB - 1) / ATT_TPB; // outputs per thread (HD <= 256)
+	float acc[OI];
+	for (int u = 0; u < OI; u++) acc[u] = 0.0f;
+	for (int c0 = 0; c0 < n; c0 += ck) {
+		__syncthreads(); // probabilities final; the previous chunk's chains are done with kv
+		stash();
+		__syncthreads();
+		if (c0 + ck < n) fetch(V, c0 + ck);
+		const int m = min(ck, n - c0);
+		const float *vb = (const float *)kv;
+		for (int u = 0; u < OI; u++) {
+			const int it = tid + u * ATT_TPB;
+			if (it >= GRP * HD) break;
+			const int g = it / HD, d = it - g * HD;
+			const float *r = sc + g * nst + c0;
+			float x = acc[u];
+			for (int kk = 0; kk < m; kk++) x = x + r[kk] * vb[kk * (HD + 4) + d];
+			acc[u] = x;
 		}
-		for (; key < n; key++) acc = acc + r[key] * vp[(long)key * HD];
-		a.att[((long)s * a.NQ + j * GRP + g) * HD + d] = acc;
+	}
+	for (int u = 0; u < OI; u++) {
+		const int it = tid + u * ATT_TPB;
+		if (it >= GRP * HD) break;
+		const int g = it / HD, d = it - g * HD;
+		a.att[((long)s * a.NQ + j * GRP + g) * HD + d] = acc[u];
 	}
 }
 
@@ -126,51 +189,69 @@ __global__ __launch_bounds__(256) void dec_attn_k(tgk_dec_attn_args a)
 // columns): the rows' digits and the head's code tile sit in LDS; a wave
 // handles 4 rows at a time, a lane one column.
 // codes: int32 [NQ][HD/4][D], 4 consecutive k's int8 codes per word (k = 4
-// k4 + i in byte i); scales [NQ][D]; HD a multiple of 4.
-__global__ __launch_bounds__(256) void dec_wo_k(const float *att, const int *codes, const float *scales, float *out, int rows, int NQ,
-						int HD, int D)
+// k4 + i in byte i); scales [NQ][D]; HD a multiple of 4, att 16-byte aligned.
+constexpr int WO_TPB = 512;
+__global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *codes, const float *scales, float *out, int rows, int NQ,
+						   int HD, int D)
 {
 	extern __shared__ int4 dg[]; // [rows][HD/4] digit words {d0, d1, d2, 0} of 4 k's
-	const int H4 = HD / 4;
+	const int H4 = HD / 4, n = rows * H4;
 	int *Es = (int *)(dg + (long)rows * H4), *sp = Es + rows, *ct = sp + rows; // ct: [HD/4][64] code words
 	const int ctiles = (D + 63) / 64, g = blockIdx.x / ctiles, c0 = (blockIdx.x - g * ctiles) * 64;
-	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-	for (int t = wave; t < rows; t += nw) { // a wave per token row
-		const float *x = att + ((long)t * NQ + g) * HD;
-		float mx = 0.0f;
-		int bad = 0;
-		for (int k = lane; k < HD; k += 64) {
-			bad |= !isfinite(x[k]);
-			mx = fmaxf(mx, fabsf(x[k]));
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	constexpr int U = 4, nw = WO_TPB / 64;
+	auto xat = [&](int e) { // the 4 inputs of item e = (row t, k4)
+		const int t = e / H4;
+		return *(const float4 *)(att + ((long)t * NQ + g) * HD + 4 * (e - t * H4));
+	};
+	// rows' max |x| (as bits: non-negative floats order as their bits) and flags
+	unsigned *mxb = (unsigned *)Es;
+	for (int t = tid; t < rows; t += WO_TPB) mxb[t] = 0, sp[t] = 0;
+	for (int e = tid; e < H4 * 64; e += WO_TPB) {
+		const int k4 = e >> 6, c = e & 63;
+		ct[e] = c0 + c < D ? codes[((long)g * H4 + k4) * D + c0 + c] : 0;
+	}
+	__syncthreads();
+	for (int b = tid; b < n; b += U * WO_TPB) {
+		float4 u[U];
+		for (int j = 0; j < U; j++) u[j] = xat(min(b + j * WO_TPB, n - 1));
+		for (int j = 0; j < U; j++) {
+			const int e = b + j * WO_TPB;
+			if (e >= n) continue;
+			const float4 v = u[j];
+			const int bad = !isfinite(v.x) || !isfinite(v.y) || !isfinite(v.z) || !isfinite(v.w);
+			const float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); // a nan never wins fmaxf
+			atomicMax(&mxb[e / H4], __float_as_uint(m));
+			if (bad) atomicOr(&sp[e / H4], 1);
 		}
-		for (int w = 32; w > 0; w >>= 1) {
-			mx = fmaxf(mx, __shfl_xor(mx, w));
-			bad |= __shfl_xor(bad, w);
-		}
-		const int special = bad || mx > 0x1p100f;
-		int E = 0;
-		if (!special && mx > 0.0f) {
-			frexpf(mx, &E);
-			if (rintf(ldexpf(mx, 23 - E)) > 8355328.0f) E += 1;
-		}
-		for (int k4 = lane; k4 < H4; k4 += 64) {
+	}
+	__syncthreads();
+	for (int t = tid; t < rows; t += WO_TPB) {
+		const float mx = __uint_as_float(mxb[t]);
+		const int special = tgq_special(sp[t], mx);
+		Es[t] = tgq_exponent(mx, special), sp[t] = special;
+	}
+	__syncthreads();
+	for (int b = tid; b < n; b += U * WO_TPB) {
+		float4 u[U];
+		for (int j = 0; j < U; j++) u[j] = xat(min(b + j * WO_TPB, n - 1));
+		for (int j = 0; j < U; j++) {
+			const int e = b + j * WO_TPB;
+			if (e >= n) continue;
+			const int t = e / H4, E = Es[t];
+			const float xv[4] = { u[j].x, u[j].y, u[j].z, u[j].w };
 			unsigned w0 = 0, w1 = 0, w2 = 0;
-			if (!special)
+			if (!sp[t])
 				for (int i = 0; i < 4; i++) {
-					const int q = (int)rintf(ldexpf(x[4 * k4 + i], 23 - E)); // exact: |q| < 2^23
-					const int d0 = (int)(int8_t)(q & 255), q1 = (q - d0) >> 8;
-					const int d1 = (int)(int8_t)(q1 & 255), d2 = (q1 - d1) >> 8;
+					const int q = (int)rintf(ldexpf(xv[i], 23 - E)); // exact: |q| < 2^23
+					int d0, d1, d2;
+					tgq_split3(q, d0, d1, d2);
 					w0 |= (unsigned)(d0 & 255) << (8 * i);
 					w1 |= (unsigned)(d1 & 255) << (8 * i);
 					w2 |= (unsigned)(d2 & 255) << (8 * i);
 				}
-			dg[(long)t * H4 + k4] = make_int4((int)w0, (int)w1, (int)w2, 0);
+			dg[e] = make_int4((int)w0, (int)w1, (int)w2, 0);
 		}
-		if (lane == 0) Es[t] = E, sp[t] = special;
-	}
-	for (int e = threadIdx.x; e < H4 * 64; e += blockDim.x) {
-		const int k4 = e >> 6, c = e & 63;
-		ct[e] = c0 + c < D ? codes[((long)g * H4 + k4) * D + c0 + c] : 0;
 	}
 	__syncthreads();
 	const int c = lane;
@@ -206,50 +287,235 @@ __global__ __launch_bounds__(256) void dec_wo_k(const float *att, const int *cod
 	}
 }
 
-// h = h + ((o_0 + o_1) + ... + o_{NQ-1}): the graph's sum of the per-head
-// output projections, then the residual add
-__global__ void sumchain_k(float *h, const float *o, int NQ, long per_head, long total)
+// Block-wide reductions (blockDim a multiple of 64, at most 1024); red is
+// LDS scratch of 16 entries. Every thread gets the result.
+__device__ inline float blk_max(float v, float *red)
 {
-	const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
-	if (t >= total) return;
-	float acc = o[t];
-	for (int k = 1; k < NQ; k++) acc = acc + o[(long)k * per_head + t];
-	h[t] = h[t] + acc;
+	for (int w = 32; w > 0; w >>= 1) v = fmaxf(v, __shfl_xor(v, w));
+	__syncthreads();
+	if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+	__syncthreads();
+	float m = red[0];
+	for (int i = 1; i < (int)(blockDim.x >> 6); i++) m = fmaxf(m, red[i]);
+	return m;
+}
+
+__device__ inline long long blk_sum(long long v, long long *red)
+{
+	for (int w = 32; w > 0; w >>= 1) v += __shfl_xor(v, w);
+	__syncthreads();
+	if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+	__syncthreads();
+	long long t = 0;
+	for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += red[i];
+	return t;
+}
+
+// digits of row m, values z[0 .. Kp) in LDS (zero from the row's length on),
+// from this thread's share of max |z| and of the non-finite flag
+__device__ inline void blk_digits(const float *z, int Kp, float mx, int bad, const tgk_qdig &q, int m, float *redf, long long *redl)
+{
+	const float amax = blk_max(mx, redf); // nan never wins fmaxf; such rows are flagged by bad
+	const int anybad = __syncthreads_or(bad);
+	const int special = tgq_special(anybad, amax), E = tgq_exponent(amax, special);
+	int8_t *blk = tgq_row_base(q.dig, m, Kp);
+	long long qs = 0;
+	for (int j = threadIdx.x; j < Kp / 16; j += blockDim.x) {
+		float v[16];
+		for (int u = 0; u < 16; u++) v[u] = z[16 * j + u];
+		qs += tgq_put16(blk, 16 * j, v, E, special);
+	}
+	qs = blk_sum(qs, redl);
+	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = special, q.qsum[m] = qs;
+}
+
+// tgk_dec_norm: one block per token row. The row's sum of squares is the
+// reference's sequential loop over the squares (computed in parallel), the
+// scale 1 / sqrtf(sum / D + 1e-6) as the row-op kernel, then (h * inv) * g.
+__global__ __launch_bounds__(256) void dec_norm_k(tgk_dec_norm_args a)
+{
+	extern __shared__ float4 zs4[]; // [Kp] values, [Kp] squares (16-byte aligned)
+	float *zs = (float *)zs4;
+	__shared__ float redf[16], inv_s;
+	__shared__ long long redl[16];
+	const int t = blockIdx.x, D = a.D, Kp = a.Kp;
+	float *z = zs, *sq = zs + Kp, *hr = a.h + (long)t * a.hs;
+	for (int i = threadIdx.x; i < Kp; i += blockDim.x) {
+		float v = 0.0f;
+		if (i < D) {
+			v = hr[i];
+			if (a.mode == 1) {
+				v = v + a.add[(long)t * a.adds + i];
+				hr[i] = v;
+			} else if (a.mode == 2) {
+				const float *o = a.o + (long)t * D + i;
+				float acc = o[0];
+				for (int k = 1; k < a.nh; k++) acc = acc + o[(long)k * a.ohead];
+				v = v + acc;
+				hr[i] = v;
+			}
+		}
+		z[i] = v;
+		sq[i] = v * v;
+	}
+	__syncthreads();
+	if (threadIdx.x == 0) inv_s = 1.0f / sqrtf(ordered_sum(sq, D) / (float)D + 1e-6f);
+	__syncthreads();
+	const float inv = inv_s;
+	float mx = 0.0f;
+	int bad = 0;
+	for (int i = threadIdx.x; i < D; i += blockDim.x) {
+		const float nv = z[i] * inv * a.g[i];
+		a.out[(long)t * a.outs + i] = nv;
+		z[i] = nv;
+		bad |= !isfinite(nv);
+		mx = fmaxf(mx, fabsf(nv));
+	}
+	__syncthreads();
+	blk_digits(z, Kp, mx, bad, a.q, t, redf, redl);
+}
+
+// tgk_dec_hnorm: one wave per head line (4 per block, no block barrier:
+// lines past the end leave at once). Same operations as tgk_dec_norm.
+__global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
+{
+	extern __shared__ float4 hs4[]; // per wave: [Kp] values, [Kp] squares (16-byte aligned)
+	float *hs = (float *)hs4;
+	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, L = blockIdx.x * 4 + w, HD = a.HD, Kp = a.Kp;
+	if (L >= a.rows * a.NH) return;
+	const int t = L / a.NH, j = L - t * a.NH;
+	float *z = hs + (long)w * 2 * Kp, *sq = z + Kp;
+	const float *x = a.x + (long)t * a.xs + (long)j * HD;
+	for (int i = lane; i < Kp; i += 64) {
+		const float v = i < HD ? x[i] : 0.0f;
+		z[i] = v;
+		sq[i] = v * v;
+	}
+	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+	__builtin_amdgcn_wave_barrier();
+	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+	float inv = 0.0f;
+	if (lane == 0) inv = 1.0f / sqrtf(ordered_sum(sq, HD) / (float)HD + 1e-6f);
+	inv = __shfl(inv, 0);
+	float mx = 0.0f;
+	int bad = 0;
+	for (int i = lane; i < HD; i += 64) {
+		const float nv = z[i] * inv * a.g[(long)j * HD + i];
+		a.out[(long)L * HD + i] = nv;
+		z[i] = nv;
+		bad |= !isfinite(nv);
+		mx = fmaxf(mx, fabsf(nv));
+	}
+	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+	__builtin_amdgcn_wave_barrier();
+	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+	for (int o = 32; o > 0; o >>= 1) {
+		mx = fmaxf(mx, __shfl_xor(mx, o));
+		bad |= __shfl_xor(bad, o);
+	}
+	const int special = tgq_special(bad, mx), E = tgq_exponent(mx, special);
+	int8_t *blk = tgq_row_base(a.q.dig, L, Kp);
+	long long qs = 0;
+	for (int g = lane; g < Kp / 16; g += 64) {
+		float v[16];
+		for (int u = 0; u < 16; u++) v[u] = z[16 * g + u];
+		qs += tgq_put16(blk, 16 * g, v, E, special);
+	}
+	for (int o = 32; o > 0; o >>= 1) qs += __shfl_xor(qs, o);
+	if (lane == 0) a.q.e[L] = E, a.q.special[L] = special, a.q.qsum[L] = qs;
+}
+
+// tgk_dec_silu: one block per row; silu as the element-wise kernels compute it
+__global__ __launch_bounds__(256) void dec_silu_k(tgk_dec_silu_args a)
+{
+	extern __shared__ float4 zs4[]; // [Kp]
+	float *zs = (float *)zs4;
+	__shared__ float redf[16];
+	__shared__ long long redl[16];
+	const int t = blockIdx.x, FF = a.FF;
+	const float *g = a.gu + (long)t * a.gus, *u = g + FF;
+	float mx = 0.0f;
+	int bad = 0;
+	for (int i = threadIdx.x; i < a.Kp; i += blockDim.x) {
+		float v = 0.0f;
+		if (i < FF) {
+			const float x = g[i];
+			v = x / (1.0f + expf(-x)) * u[i];
+			a.out[(long)t * FF + i] = v;
+			bad |= !isfinite(v);
+			mx = fmaxf(mx, fabsf(v));
+		}
+		zs[i] = v;
+	}
+	__syncthreads();
+	blk_digits(zs, a.Kp, mx, bad, a.q, t, redf, redl);
 }
 
 // Greedy choice per row: the index of the largest logit, the first one on
-// ties, a nan counting as largest (numpy's argmax). Written as an f32 token id
-// (the model's input format) and as an int.
-__global__ __launch_bounds__(256) void argmax_k(const float *x, long xrs, int V, float *idf, int *idi, long idi_stride)
+// ties, a nan counting as largest (numpy's argmax). (nan-ness, value, -index)
+// is a total order, so any grouping of the comparisons finds the same index:
+// argmax_part_k takes the best of each of a row's parts (blocks of `chunk`
+// columns, loads in batches of 8 per thread), argmax_fin_k the best of the
+// parts, written as an f32 token id (the model's input format) and as an int.
+__device__ inline bool am_better(float a, int ia, float b, int ib) // is (a, ia) the better candidate?
 {
-	__shared__ float bv[256];
-	__shared__ int bi[256];
-	const float *r = x + (long)blockIdx.x * xrs;
+	if (ib < 0) return ia >= 0;
+	if (ia < 0) return false;
+	const bool na = isnan(a), nb = isnan(b);
+	if (na != nb) return na;
+	if (!na && a != b) return a > b;
+	return ia < ib;
+}
+
+__device__ inline void am_wave(float &v, int &i)
+{
+	for (int w = 32; w > 0; w >>= 1) {
+		const float ov = __shfl_xor(v, w);
+		const int oi = __shfl_xor(i, w);
+		if (am_better(ov, oi, v, i)) v = ov, i = oi;
+	}
+}
+
+__global__ __launch_bounds__(256) void argmax_part_k(const float *x, long xrs, int V, int chunk, int nparts, float *pv, int *pi)
+{
+	__shared__ float bv[4];
+	__shared__ int bi[4];
+	const int row = blockIdx.x / nparts, part = blockIdx.x - row * nparts;
+	const float *r = x + (long)row * xrs;
+	const int k0 = part * chunk, k1 = min(V, k0 + chunk);
 	float v = 0.0f;
 	int i = -1;
-	auto better = [](float a, int ia, float b, int ib) { // is (a, ia) the better candidate?
-		if (ib < 0) return ia >= 0;
-		if (ia < 0) return false;
-		const bool na = isnan(a), nb = isnan(b);
-		if (na != nb) return na;
-		if (!na && a != b) return a > b;
-		return ia < ib;
-	};
-	for (int k = threadIdx.x; k < V; k += blockDim.x)
-		if (better(r[k], k, v, i)) v = r[k], i = k;
-	bv[threadIdx.x] = v;
-	bi[threadIdx.x] = i;
-	__syncthreads();
-	for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-		if ((int)threadIdx.x < w && better(bv[threadIdx.x + w], bi[threadIdx.x + w], bv[threadIdx.x], bi[threadIdx.x])) {
-			bv[threadIdx.x] = bv[threadIdx.x + w];
-			bi[threadIdx.x] = bi[threadIdx.x + w];
+	for (int b = k0; b < k1; b += 8 * 256) {
+		float u[8];
+		for (int j = 0; j < 8; j++) {
+			const int k = b + j * 256 + (int)threadIdx.x;
+			u[j] = r[k < k1 ? k : k1 - 1];
 		}
-		__syncthreads();
+		for (int j = 0; j < 8; j++) {
+			const int k = b + j * 256 + (int)threadIdx.x;
+			if (k < k1 && am_better(u[j], k, v, i)) v = u[j], i = k;
+		}
 	}
+	am_wave(v, i);
+	if ((threadIdx.x & 63) == 0) bv[threadIdx.x >> 6] = v, bi[threadIdx.x >> 6] = i;
+	__syncthreads();
 	if (threadIdx.x == 0) {
-		idf[blockIdx.x] = (float)bi[0];
-		if (idi) idi[(long)blockIdx.x * idi_stride] = bi[0];
+		for (int w = 1; w < 4; w++)
+			if (am_better(bv[w], bi[w], v, i)) v = bv[w], i = bi[w];
+		pv[blockIdx.x] = v;
+		pi[blockIdx.x] = i;
+	}
+}
+
+__global__ __launch_bounds__(64) void argmax_fin_k(const float *pv, const int *pi, int nparts, float *idf, int *idi, long idi_stride)
+{
+	const int row = blockIdx.x, l = threadIdx.x;
+	float v = l < nparts ? pv[(long)row * nparts + l] : 0.0f;
+	int i = l < nparts ? pi[(long)row * nparts + l] : -1;
+	am_wave(v, i);
+	if (l == 0) {
+		idf[row] = (float)i;
+		if (idi) idi[(long)row * idi_stride] = i;
 	}
 }
 
@@ -257,6 +523,13 @@ constexpr int TPB = 256;
 inline unsigned blocks(long n) { return (unsigned)((n + TPB - 1) / TPB); }
 
 } // namespace
+
+size_t tgk_dec_attn_lds(int GRP, int HD, int n)
+{
+	const long nst = (n + 3) & ~3;
+	return (size_t)((long)attn_chunk(HD) * (HD + 4) + (long)GRP * HD + GRP * nst + GRP) * sizeof(float);
+}
+
 
 void tgk_dec_rope(hipStream_t s, const tgk_dec_rope_args *a, int rows)
 {
@@ -266,32 +539,46 @@ void tgk_dec_rope(hipStream_t s, const tgk_dec_rope_args *a, int rows)
 
 void tgk_dec_attn(hipStream_t s, const tgk_dec_attn_args *a, int seqs)
 {
-	const int GRP = a->NQ / a->NKV;
-	const size_t lds = ((size_t)GRP * (a->p + 1) + (size_t)GRP * a->HD + GRP) * sizeof(float);
+	const int GRP = a->NQ / a->NKV, ck = attn_chunk(a->HD);
+	const size_t lds = tgk_dec_attn_lds(GRP, a->HD, a->p + 1);
 	const unsigned grid = (unsigned)(seqs * a->NKV);
 	if (seqs <= 0) return;
-	switch (GRP) { // the decoder checks GRP and HD when it is created
-	case 1: dec_attn_k<1><<<grid, TPB, lds, s>>>(*a); break;
-	case 2: dec_attn_k<2><<<grid, TPB, lds, s>>>(*a); break;
-	case 4: dec_attn_k<4><<<grid, TPB, lds, s>>>(*a); break;
-	case 8: dec_attn_k<8><<<grid, TPB, lds, s>>>(*a); break;
+	switch (GRP) { // the decoder checks GRP, HD and the LDS size when it is created
+	case 1: dec_attn_k<1><<<grid, ATT_TPB, lds, s>>>(*a, ck); break;
+	case 2: dec_attn_k<2><<<grid, ATT_TPB, lds, s>>>(*a, ck); break;
+	case 4: dec_attn_k<4><<<grid, ATT_TPB, lds, s>>>(*a, ck); break;
+	case 8: dec_attn_k<8><<<grid, ATT_TPB, lds, s>>>(*a, ck); break;
 	default: break;
 	}
+}
+
+void tgk_dec_norm(hipStream_t s, const tgk_dec_norm_args *a)
+{
+	if (a->rows > 0) dec_norm_k<<<(unsigned)a->rows, TPB, (size_t)a->Kp * 2 * sizeof(float), s>>>(*a);
+}
+
+void tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a)
+{
+	const long lines = (long)a->rows * a->NH;
+	if (lines > 0) dec_hnorm_k<<<(unsigned)((lines + 3) / 4), TPB, (size_t)a->Kp * 8 * sizeof(float), s>>>(*a);
+}
+
+void tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a)
+{
+	if (a->rows > 0) dec_silu_k<<<(unsigned)a->rows, TPB, (size_t)a->Kp * sizeof(float), s>>>(*a);
 }
 
 size_t tgk_dec_wo_lds(int rows, int HD) { return (size_t)rows * HD * 4 + (size_t)rows * 8 + (size_t)HD * 64; }
 
 void tgk_dec_wo(hipStream_t s, const float *att, const int *codes, const float *scales, float *out, int rows, int NQ, int HD, int D)
 {
-	if (rows > 0) dec_wo_k<<<(unsigned)(NQ * ((D + 63) / 64)), TPB, tgk_dec_wo_lds(rows, HD), s>>>(att, codes, scales, out, rows, NQ, HD, D);
+	if (rows > 0) dec_wo_k<<<(unsigned)(NQ * ((D + 63) / 64)), WO_TPB, tgk_dec_wo_lds(rows, HD), s>>>(att, codes, scales, out, rows, NQ, HD, D);
 }
 
-void tgk_dec_sumchain(hipStream_t s, float *h, const float *o, int NQ, long per_head)
+void tgk_dec_argmax(hipStream_t s, const float *x, long xrs, int V, int rows, float *idf, int *idi, long idi_stride, float *pv, int *pi)
 {
-	if (per_head > 0) sumchain_k<<<blocks(per_head), TPB, 0, s>>>(h, o, NQ, per_head, per_head);
-}
-
-void tgk_dec_argmax(hipStream_t s, const float *x, long xrs, int V, int rows, float *idf, int *idi, long idi_stride)
-{
-	if (rows > 0) argmax_k<<<(unsigned)rows, TPB, 0, s>>>(x, xrs, V, idf, idi, idi_stride);
+	if (rows <= 0 || V <= 0) return;
+	const int np0 = (V + 2047) / 2048, nparts = np0 < TGK_AM_PARTS ? np0 : TGK_AM_PARTS, chunk = (V + nparts - 1) / nparts;
+	argmax_part_k<<<(unsigned)(rows * nparts), TPB, 0, s>>>(x, xrs, V, chunk, nparts, pv, pi);
+	argmax_fin_k<<<(unsigned)rows, 64, 0, s>>>(pv, pi, nparts, idf, idi, idi_stride);
 }

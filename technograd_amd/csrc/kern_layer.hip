@@ -332,6 +332,35 @@ __global__ void rowop_k(int op, float *o, long ors, tgk_opd a, int nrow, int col
 // Softmax's max: x[0] when it is nan, else the largest of x[0] and the
 // non-nan x[i] (the reference's `if (x[i] > mx) mx = x[i]`); its sign of zero
 // cannot change expf(x - mx).
+// sum_i z_i (SQ: z_i * z_i) in index order, as the reference's loop: one
+// thread, one add after another; the loads run ahead in batches of 32 (16-byte
+// LDS reads when the line is 16-byte aligned) so only the adds are serial
+template <bool SQ> __device__ inline float line_sum(const float *z, int cols)
+{
+	float sum = 0.0f;
+	int i = 0;
+	if ((((size_t)z) & 15) == 0)
+		for (; i + 32 <= cols; i += 32) {
+			float4 b[8];
+			for (int j = 0; j < 8; j++) b[j] = *(const float4 *)(z + i + 4 * j);
+			for (int j = 0; j < 8; j++) {
+				if (SQ) {
+					sum += b[j].x * b[j].x;
+					sum += b[j].y * b[j].y;
+					sum += b[j].z * b[j].z;
+					sum += b[j].w * b[j].w;
+				} else {
+					sum += b[j].x;
+					sum += b[j].y;
+					sum += b[j].z;
+					sum += b[j].w;
+				}
+			}
+		}
+	for (; i < cols; i++) sum += SQ ? z[i] * z[i] : z[i];
+	return sum;
+}
+
 __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, tgk_opd a, int nrow, int cols, int lpb, int stride)
 {
 	extern __shared__ float lds[];
@@ -366,24 +395,21 @@ __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, t
 			*z = expf(*z - lv[e / cols]);
 		}
 		__syncthreads();
-		if ((int)threadIdx.x < lpb) {
-			const float *z = lds + threadIdx.x * stride;
-			float sum = 0.0f;
-			for (int i = 0; i < cols; i++) sum += z[i];
-			lv[threadIdx.x] = sum;
-		}
+		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = line_sum<false>(lds + threadIdx.x * stride, cols);
 		__syncthreads();
 		for (int e = threadIdx.x; e < tot; e += TPB) {
 			float *z = lds + (e / cols) * stride + e % cols;
 			*z = *z / lv[e / cols];
 		}
 	} else {
-		if ((int)threadIdx.x < lpb) {
-			const float *z = lds + threadIdx.x * stride;
-			float sum = 0.0f;
-			for (int i = 0; i < cols; i++) sum += z[i] * z[i];
-			lv[threadIdx.x] = 1.0f / sqrtf(sum / (float)cols + 1e-6f);
+		// the squares in parallel into a second area, so the ordered chain only adds
+		float *sq = lv + ((lpb + 3) & ~3);
+		for (int e = threadIdx.x; e < tot; e += TPB) {
+			const int l = e / cols, i = e - l * cols;
+			sq[l * stride + i] = lds[l * stride + i] * lds[l * stride + i];
 		}
+		__syncthreads();
+		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = 1.0f / sqrtf(line_sum<false>(sq + threadIdx.x * stride, cols) / (float)cols + 1e-6f);
 		__syncthreads();
 		for (int e = threadIdx.x; e < tot; e += TPB) {
 			float *z = lds + (e / cols) * stride + e % cols;
@@ -623,12 +649,15 @@ void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, i
 		nrow = (int)total;
 		rows = 1;
 	}
-	const int stride = cols | 1;
+	// lines 16-byte aligned and 4 banks apart when cols is a multiple of 4, else an odd stride
+	const int stride = cols % 4 == 0 ? cols + 4 : cols | 1;
+	// LDS: the lines, one value per line (padded to 4), and for rmsnorm the lines' squares
+	auto lds_bytes = [&](long l) { return ((op == TGM_SOFTMAX ? 1 : 2) * l * stride + ((l + 3) & ~3L)) * 4; };
 	int lpb = 32; // a power of two, so TPB / lpb threads share a line's max
-	while (lpb > 1 && ((long)lpb * (stride + 1) * 4 > 65536 || nrow % lpb)) lpb >>= 1;
-	if (cols >= 32 && lpb >= 4 && (long)lpb * (stride + 1) * 4 <= 65536 && (long)rows * (nrow / lpb) < (1L << 31))
-		rowop_lds_k<<<(unsigned)(rows * (long)(nrow / lpb)), TPB, (size_t)lpb * (stride + 1) * 4, s>>>(op, o, ors, a, nrow, cols, lpb,
-														stride);
+	while (lpb > 1 && (lds_bytes(lpb) > 65536 || nrow % lpb)) lpb >>= 1;
+	while (lpb > 4 && (long)rows * (nrow / lpb) < 512) lpb >>= 1; // few lines: spread them over more blocks
+	if (cols >= 32 && lpb >= 4 && lds_bytes(lpb) <= 65536 && (long)rows * (nrow / lpb) < (1L << 31))
+		rowop_lds_k<<<(unsigned)(rows * (long)(nrow / lpb)), TPB, (size_t)lds_bytes(lpb), s>>>(op, o, ors, a, nrow, cols, lpb, stride);
 	else
 		rowop_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, nrow, cols, total);
 }

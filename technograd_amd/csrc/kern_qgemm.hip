@@ -30,6 +30,7 @@
 //            of q: sum_k t q = sum_k code q + 8 sum_k q.
 // Weights are repacked once at load (channels padded to 256, K to 64).
 #include "tg_kern.h"
+#include "tg_qdigits.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -88,15 +89,6 @@ __device__ inline long long wave_sum(long long v)
 	return v;
 }
 
-// balanced base-256 digits of |q| < 2^23: q = d0 + 256 d1 + 65536 d2, d_l in [-128, 127]
-__device__ inline void split3(int q, int &d0, int &d1, int &d2)
-{
-	d0 = (int)(int8_t)(q & 255);
-	const int q1 = (q - d0) >> 8;
-	d1 = (int)(int8_t)(q1 & 255);
-	d2 = (q1 - d1) >> 8;
-}
-
 // inputs k0 .. k0 + 15 of a row, zero at and beyond K. The addresses are
 // clamped into the row instead of branched on, so the loads of several
 // calls can all be in flight before the first value is used. vec: unit
@@ -119,31 +111,6 @@ __device__ inline void load16(float *v, const float *x, long xk, int k0, int K)
 			v[i] = k < K ? f : 0.0f;
 		}
 	}
-}
-
-// digits of 16 consecutive inputs (row m, inputs k0 .. k0 + 15) into their
-// three 16-byte chunks; returns the sum of their q
-__device__ inline long long put16(int8_t *blk, int k0, const float *v, int E, bool zero)
-{
-	unsigned w0[4] = {0, 0, 0, 0}, w1[4] = {0, 0, 0, 0}, w2[4] = {0, 0, 0, 0};
-	int qs = 0; // |sum of 16 q| < 2^27
-	if (!zero) {
-		for (int i = 0; i < 16; i++) {
-			const int q = (int)rintf(ldexpf(v[i], 23 - E)); // exact: |q| < 2^23
-			qs += q;
-			int d0, d1, d2;
-			split3(q, d0, d1, d2);
-			const int sh = (i & 3) * 8;
-			w0[i >> 2] |= (unsigned)(d0 & 255) << sh;
-			w1[i >> 2] |= (unsigned)(d1 & 255) << sh;
-			w2[i >> 2] |= (unsigned)(d2 & 255) << sh;
-		}
-	}
-	int8_t *p = blk + (k0 >> 5) * 3072 + ((k0 >> 4) & 1) * 512;
-	*(v4i *)p = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
-	*(v4i *)(p + 1024) = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
-	*(v4i *)(p + 2048) = v4i{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
-	return qs;
 }
 
 // One wave per activation row (4 rows per block): exponent, digits, sum of q,
@@ -180,19 +147,14 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 			}
 	}
 	const float amax = wave_max(mx); // nan never wins fmaxf; such rows are flagged by `bad`
-	const int special = __any(bad) || amax > 0x1p100f;
-	int E = 0;
-	if (!special && amax > 0.0f) {
-		frexpf(amax, &E); // amax = f 2^E, f in [0.5, 1)
-		if (rintf(ldexpf(amax, 23 - E)) > 8355328.0f) E += 1; // keep the top digit within int8
-	}
+	const int special = tgq_special(__any(bad), amax), E = tgq_exponent(amax, special);
 	long long qs = 0;
-	int8_t *blk = s.dig + (long)(m >> 5) * (Kp / 32) * 3072 + (m & 31) * 16;
+	int8_t *blk = tgq_row_base(s.dig, m, Kp);
 	for (int t0 = 0; t0 < nsl; t0 += SL) {
 		if (nsl > SL) fetch(t0); // rows of up to SL slabs are still in v
 		for (int t = 0; t < SL; t++) {
 			const int k0 = (t0 + t) * 1024 + lane * 16;
-			if (t0 + t < nsl && k0 < Kp) qs += put16(blk, k0, v[t], E, special);
+			if (t0 + t < nsl && k0 < Kp) qs += tgq_put16(blk, k0, v[t], E, special);
 		}
 	}
 	qs = wave_sum(qs);
@@ -242,17 +204,12 @@ __global__ __launch_bounds__(1024) void digits_tile_k(tgk_qgemm_args a, Scratch 
 		amax = fmaxf(amax, fmaxf(smx[u][mr], smx[u][mr + 32]));
 		bad |= sbad[u][mr] | sbad[u][mr + 32];
 	}
-	const int special = bad || amax > 0x1p100f;
-	int E = 0;
-	if (!special && amax > 0.0f) {
-		frexpf(amax, &E);
-		if (rintf(ldexpf(amax, 23 - E)) > 8355328.0f) E += 1;
-	}
+	const int special = tgq_special(bad, amax), E = tgq_exponent(amax, special);
 	int8_t *blk = s.dig + (long)blockIdx.x * nkb * 3072 + mr * 16;
 	long long qs = 0;
 	for (int j = 0; j < NKB; j++) {
 		const int kb = w + j * W;
-		if (kb < nkb) qs += put16(blk, kb * 32 + half * 16, v[j], E, special);
+		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special);
 	}
 	sqs[w][lane] = qs;
 	__syncthreads();
@@ -741,6 +698,12 @@ size_t tgk_qgemm_scratch(int M, int Kp)
 {
 	long Mp = round_up(M, BM);
 	return (size_t)Mp * Kp * 3 + (size_t)Mp * (sizeof(long long) + 2 * sizeof(int)) + 256;
+}
+
+tgk_qdig tgk_qgemm_digit_area(void *scratch, int M, int Kp)
+{
+	const Scratch s = carve(scratch, (int)round_up(M, BM), Kp);
+	return tgk_qdig{ s.dig, s.qsum, s.e, s.special };
 }
 
 void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)

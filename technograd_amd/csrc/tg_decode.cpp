@@ -44,9 +44,11 @@ struct tg_hip_dec {
 	// cache and work buffers
 	float *K = nullptr, *Vc = nullptr;
 	long kv_seq = 0;
-	float *ids = nullptr, *h = nullptr, *t1 = nullptr, *n = nullptr, *qkv = nullptr, *hq = nullptr, *rt = nullptr;
+	float *ids = nullptr, *h = nullptr, *n = nullptr, *qkv = nullptr, *hq = nullptr, *rt = nullptr;
 	float *qr = nullptr, *att = nullptr, *wout = nullptr, *gu = nullptr, *act = nullptr, *dbuf = nullptr;
 	float *sc = nullptr, *mask = nullptr, *lastn = nullptr, *logits = nullptr;
+	float *am_v = nullptr; // argmax workspace: TGK_AM_PARTS per sequence
+	int *am_i = nullptr;
 	int mask_T = 0;
 	void *scratch = nullptr;
 	size_t scratch_bytes = 0;
@@ -172,12 +174,34 @@ bool gemm(tg_hip_dec *d, int wi, const float *x, long xr, int ni, long xj, int r
 	return true;
 }
 
-// the rmsnorm-then-gain pair of the graph: o = rmsnorm(x) * g, lines of `cols`
-void norm_gain(tg_hip_dec *d, float *o, const float *x, long rs, int nrow, int cols, const float *g, int rows)
+// o[rows][C] = x @ W with the activation digits already written (by the
+// fused norm and silu kernels) into the GEMM's digit area for these rows
+bool gemm_pre(tg_hip_dec *d, int wi, const float *x, long xr, int ni, long xj, int rows, float *o, long orr, long oj)
 {
-	tgk_rowop(d->st, TGM_RMSNORM, d->t1, (long)nrow * cols, tgk_opd{ x, rs }, nrow, cols, rows);
-	tgk_binary(d->st, TGK_MUL, o, (long)nrow * cols, nrow * cols, tgk_opd{ d->t1, (long)nrow * cols }, 0, nullptr, 1, tgk_opd{ g, 0 }, 0,
-		   nullptr, 1, rows);
+	tgk_qgemm_args a;
+	memset(&a, 0, sizeof a);
+	a.w = &d->ws[(size_t)wi];
+	a.x = x;
+	a.xr = xr, a.xj = xj, a.xk = 1, a.ni = ni;
+	a.o = o;
+	a.orr = orr, a.oc = 1, a.oj = oj;
+	a.M = rows * ni;
+	tgk_qgemm_mfma(d->st, &a, d->scratch);
+	return true;
+}
+
+// the graph's rmsnorm-then-gain of token rows, fused with the update of h
+// before it (mode 1: h += add; mode 2: h += the heads' output projections in
+// order) and the activation digits of weight wi's GEMM
+void norm(tg_hip_dec *d, int mode, float *h, long hs, int rows, const float *add, long adds, const float *g, float *out, int wi)
+{
+	tgk_dec_norm_args a;
+	memset(&a, 0, sizeof a);
+	a.h = h, a.hs = hs, a.mode = mode, a.add = add, a.adds = adds;
+	a.o = d->wout, a.ohead = (long)rows * d->D, a.nh = d->NQ;
+	a.g = g, a.out = out, a.outs = d->D, a.D = d->D, a.Kp = d->ws[(size_t)wi].Kp, a.rows = rows;
+	a.q = tgk_qgemm_digit_area(d->scratch, rows, a.Kp);
+	tgk_dec_norm(d->st, &a);
 }
 
 // the graph over positions p0 .. p0 + T0 - 1 of S sequences, token ids in
@@ -190,10 +214,15 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 	tgk_take(st, d->h, (long)T0 * D, tgk_opd{ d->E, 0 }, tgk_opd{ d->ids, T0 }, T0, d->V, d->D, S);
 	for (int l = 0; l < d->L; l++) {
 		const long kv_layer = (long)l * d->NKV * d->P * d->HD;
-		norm_gain(d, d->n, d->h, D, 1, d->D, d->ln1[(size_t)l], rows);
-		gemm(d, d->wqkv[(size_t)l], d->n, D, 1, 0, rows, d->qkv, ctot, 0);
-		norm_gain(d, d->hq, d->qkv, ctot, NH, d->HD, d->qkg[(size_t)l], rows);
-		gemm(d, d->wrot, d->hq, qk, NH, d->HD, rows, d->rt, qk, d->HD);
+		// h (plus the previous layer's MLP output), rmsnorm * ln1, q k v projections
+		norm(d, l == 0 ? 0 : 1, d->h, D, rows, d->dbuf, D, d->ln1[(size_t)l], d->n, d->wqkv[(size_t)l]);
+		gemm_pre(d, d->wqkv[(size_t)l], d->n, D, 1, 0, rows, d->qkv, ctot, 0);
+		tgk_dec_hnorm_args hn; // per-head rmsnorm * gain of the q and k heads, then the rotation matmul
+		hn.x = d->qkv, hn.xs = ctot, hn.g = d->qkg[(size_t)l], hn.out = d->hq;
+		hn.NH = NH, hn.HD = d->HD, hn.Kp = d->ws[(size_t)d->wrot].Kp, hn.rows = rows;
+		hn.q = tgk_qgemm_digit_area(d->scratch, rows * NH, hn.Kp);
+		tgk_dec_hnorm(st, &hn);
+		gemm_pre(d, d->wrot, d->hq, qk, NH, d->HD, rows, d->rt, qk, d->HD);
 		tgk_dec_rope_args r;
 		r.hq = d->hq, r.rt = d->rt, r.qkv = d->qkv, r.ctot = ctot, r.cosT = d->cosT, r.sinT = d->sinT;
 		r.qr = d->qr, r.K = d->K, r.V = d->Vc, r.kv_seq = d->kv_seq, r.kv_layer = kv_layer;
@@ -242,27 +271,18 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 			for (int hh = 0; hh < d->NQ; hh++)
 				gemm(d, d->wo[(size_t)l * d->NQ + hh], d->att + (long)hh * d->HD, (long)d->NQ * d->HD, 1, 0, rows,
 				     d->wout + (long)hh * rows * D, D, 0);
-		tgk_dec_sumchain(st, d->h, d->wout, d->NQ, (long)rows * D);
-		norm_gain(d, d->n, d->h, D, 1, d->D, d->ln2[(size_t)l], rows);
-		gemm(d, d->wgu[(size_t)l], d->n, D, 1, 0, rows, d->gu, 2L * d->FF, 0);
-		tgk_ew e; // act = silu(g) * u
-		memset(&e, 0, sizeof e);
-		e.nin = 2, e.nout = 1, e.nins = 4;
-		e.in[0] = d->gu, e.in_rs[0] = 2L * d->FF;
-		e.in[1] = d->gu + d->FF, e.in_rs[1] = 2L * d->FF;
-		for (int q = 0; q < 2; q++) e.in_mode[q] = 0, e.in_map[q] = nullptr, e.in_per[q] = 1, e.in_inv[q] = 1.0f;
-		e.out[0] = d->act, e.out_rs[0] = d->FF;
-		e.ins[0] = tgk_ew_ins{ TGK_EW_LOAD, 0, 0, 0, 0 };
-		e.ins[1] = tgk_ew_ins{ TGK_EW_UN, TGM_SILU, 0, 0, 0 };
-		e.ins[2] = tgk_ew_ins{ TGK_EW_BIN, TGK_MUL, 0, 1, 0 };
-		e.ins[3] = tgk_ew_ins{ TGK_EW_STORE, 0, 0, 0, 0 };
-		tgk_ew_run(st, &e, d->FF, rows);
-		gemm(d, d->wd[(size_t)l], d->act, d->FF, 1, 0, rows, d->dbuf, D, 0);
-		tgk_binary(st, TGK_ADD, d->h, D, d->D, tgk_opd{ d->h, D }, 0, nullptr, 1, tgk_opd{ d->dbuf, D }, 0, nullptr, 1, rows);
+		// h + the heads' output projections (in head order), rmsnorm * ln2, gate and up projections
+		norm(d, 2, d->h, D, rows, nullptr, 0, d->ln2[(size_t)l], d->n, d->wgu[(size_t)l]);
+		gemm_pre(d, d->wgu[(size_t)l], d->n, D, 1, 0, rows, d->gu, 2L * d->FF, 0);
+		tgk_dec_silu_args sa; // act = silu(g) * u, then the down projection
+		sa.gu = d->gu, sa.gus = 2L * d->FF, sa.out = d->act, sa.FF = d->FF, sa.Kp = d->ws[(size_t)d->wd[(size_t)l]].Kp, sa.rows = rows;
+		sa.q = tgk_qgemm_digit_area(d->scratch, rows, sa.Kp);
+		tgk_dec_silu(st, &sa);
+		gemm_pre(d, d->wd[(size_t)l], d->act, d->FF, 1, 0, rows, d->dbuf, D, 0);
 	}
-	// the last position of each sequence: rmsnorm, gain, LM head
-	norm_gain(d, d->lastn, d->h + (long)(T0 - 1) * D, (long)T0 * D, 1, d->D, d->lnf, S);
-	gemm(d, d->wlm, d->lastn, D, 1, 0, S, d->logits, d->V, 0);
+	// the last position of each sequence: h + the last MLP output, rmsnorm * lnf, LM head
+	norm(d, 1, d->h + (long)(T0 - 1) * D, (long)T0 * D, S, d->dbuf + (long)(T0 - 1) * D, (long)T0 * D, d->lnf, d->lastn, d->wlm);
+	gemm_pre(d, d->wlm, d->lastn, D, 1, 0, S, d->logits, d->V, 0);
 	return hip_ok(hipGetLastError(), "decoder launch");
 }
 
@@ -294,10 +314,10 @@ bool build(tg_hip_dec *d)
 	d->HD = m->val[find(m, "Wq_0_0")].sh.dim[1];
 	d->FF = m->val[find(m, "Wg_0")].sh.dim[1];
 	// one step's attention block: the scores of all positions in LDS; 1, 2, 4 or 8 query heads per KV head
-	const long grp = d->NQ / d->NKV, lds = (grp * d->P + grp * d->HD + grp) * 4;
-	if ((grp != 1 && grp != 2 && grp != 4 && grp != 8) || d->HD % 16)
-		return err("decoder: needs 1, 2, 4 or 8 query heads per KV head and a head size that is a multiple of 16%s", "");
-	if (lds > 65536) return err("decoder: %s%ld positions do not fit one step's attention (LDS)", "", d->P);
+	const int grp = d->NQ / d->NKV;
+	if ((grp != 1 && grp != 2 && grp != 4 && grp != 8) || d->HD % 16 || d->HD > 256)
+		return err("decoder: needs 1, 2, 4 or 8 query heads per KV head and a head size that is a multiple of 16, at most 256%s", "");
+	if (tgk_dec_attn_lds(grp, d->HD, d->P) > 65536) return err("decoder: %s%ld positions do not fit one step's attention (LDS)", "", d->P);
 	if (m->val[vcos].sh.rank != 2 || m->val[vcos].sh.dim[1] != d->HD || m->val[vcos].sh.dim[0] < d->P)
 		return err("decoder: rope tables need %s%ld rows", "", d->P);
 	d->scale = 0.0f; // the graph's attention scale: its first constant (the importer writes 1/sqrt(HD) first)
@@ -352,13 +372,14 @@ bool build(tg_hip_dec *d)
 	const long rows = (long)d->S * d->TP;
 	d->kv_seq = (long)d->L * d->NKV * d->P * HD;
 	if (!alloc(d, &d->K, (size_t)(d->S * d->kv_seq)) || !alloc(d, &d->Vc, (size_t)(d->S * d->kv_seq)) || !alloc(d, &d->ids, (size_t)rows) ||
-	    !alloc(d, &d->h, (size_t)(rows * d->D)) || !alloc(d, &d->t1, (size_t)(rows * std::max<long>(d->D, NH * HD))) ||
+	    !alloc(d, &d->h, (size_t)(rows * d->D)) ||
 	    !alloc(d, &d->n, (size_t)(rows * d->D)) || !alloc(d, &d->qkv, (size_t)(rows * ctot)) || !alloc(d, &d->hq, (size_t)(rows * NH * HD)) ||
 	    !alloc(d, &d->rt, (size_t)(rows * NH * HD)) || !alloc(d, &d->qr, (size_t)(rows * d->NQ * HD)) ||
 	    !alloc(d, &d->att, (size_t)(rows * d->NQ * HD)) || !alloc(d, &d->wout, (size_t)(rows * d->NQ * d->D)) ||
 	    !alloc(d, &d->gu, (size_t)(rows * 2 * d->FF)) || !alloc(d, &d->act, (size_t)(rows * d->FF)) || !alloc(d, &d->dbuf, (size_t)(rows * d->D)) ||
 	    !alloc(d, &d->sc, (size_t)((long)d->S * d->TP * d->TP)) || !alloc(d, &d->mask, (size_t)((long)d->TP * d->TP)) ||
-	    !alloc(d, &d->lastn, (size_t)((long)d->S * d->D)) || !alloc(d, &d->logits, (size_t)((long)d->S * d->V)))
+	    !alloc(d, &d->lastn, (size_t)((long)d->S * d->D)) || !alloc(d, &d->logits, (size_t)((long)d->S * d->V)) ||
+	    !alloc(d, &d->am_v, (size_t)d->S * TGK_AM_PARTS) || !alloc(d, &d->am_i, (size_t)d->S * TGK_AM_PARTS))
 		return false;
 	size_t sb = 0;
 	auto need = [&](long M, int wi) { sb = std::max(sb, tgk_qgemm_scratch((int)M, d->ws[(size_t)wi].Kp)); };
@@ -404,7 +425,7 @@ int tg_hip_dec_generate(tg_hip_dec *d, const float *d_prompt, int seqs, int prom
 					   hipMemcpyDeviceToDevice, d->st),
 			    "logits"))
 			return -1;
-		tgk_dec_argmax(d->st, d->logits, d->V, d->V, seqs, d->ids, d_tokens ? d_tokens + s : nullptr, steps);
+		tgk_dec_argmax(d->st, d->logits, d->V, d->V, seqs, d->ids, d_tokens ? d_tokens + s : nullptr, steps, d->am_v, d->am_i);
 	}
 	return hip_ok(hipGetLastError(), "decoder") ? 0 : -1;
 }

@@ -13,6 +13,14 @@ typedef struct {
 	long rs;
 } tgk_opd;
 
+/* a GEMM's activation-digit area: digits in fragment order, and per row the
+ * sum of its fixed-point values, its exponent and its special flag */
+typedef struct {
+	int8_t *dig;
+	long long *qsum;
+	int *e, *special;
+} tgk_qdig;
+
 /* ---- layer executor kernels (kern_layer.hip) ---- */
 
 enum { TGK_ADD, TGK_SUB, TGK_MUL, TGK_DIV, TGK_MAX, TGK_MIN };
@@ -131,14 +139,57 @@ typedef struct {
 	int NQ, NKV, HD, P, p;    /* keys at positions 0 .. p */
 	float scale;
 } tgk_dec_attn_args;
+/* LDS bytes of one step's attention block for n keys (at most 65536 to launch) */
+size_t tgk_dec_attn_lds(int GRP, int HD, int n);
 void tgk_dec_attn(hipStream_t s, const tgk_dec_attn_args *a, int seqs);
-void tgk_dec_sumchain(hipStream_t s, float *h, const float *o, int NQ, long per_head);
+/* token-row normalization of a step or prompt chunk, fused: h += add (mode
+ * 1) or h += (o_0 + ... + o_{nh-1}) in order (mode 2, the heads' output
+ * projections), then out = rmsnorm(h) * g as the row-op and multiply kernels
+ * compute it, and the activation digits of out for the next GEMM */
+typedef struct {
+	float *h;
+	long hs;
+	int mode;
+	const float *add;
+	long adds;
+	const float *o;
+	long ohead;
+	int nh;
+	const float *g;
+	float *out;
+	long outs;
+	int D, Kp, rows;
+	tgk_qdig q;
+} tgk_dec_norm_args;
+void tgk_dec_norm(hipStream_t s, const tgk_dec_norm_args *a);
+/* per-head rmsnorm * gain of the q and k heads (line (t, j) at x + t xs + j HD),
+ * into out [rows][NH][HD] and the digits of its rows t NH + j */
+typedef struct {
+	const float *x;
+	long xs;
+	const float *g;
+	float *out;
+	int NH, HD, Kp, rows;
+	tgk_qdig q;
+} tgk_dec_hnorm_args;
+void tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a);
+/* out = silu(g) * u of rows [g (FF) | u (FF)] and the digits of out */
+typedef struct {
+	const float *gu;
+	long gus;
+	float *out;
+	int FF, Kp, rows;
+	tgk_qdig q;
+} tgk_dec_silu_args;
+void tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a);
 /* per-head output projections of `rows` token rows, all heads in one launch,
  * values equal to the digit + matrix-core path; codes int32 [NQ][HD/4][D],
  * 4 consecutive k's int8 codes per word */
 size_t tgk_dec_wo_lds(int rows, int HD);
 void tgk_dec_wo(hipStream_t s, const float *att, const int *codes, const float *scales, float *out, int rows, int NQ, int HD, int D);
-void tgk_dec_argmax(hipStream_t s, const float *x, long xrs, int V, int rows, float *idf, int *idi, long idi_stride);
+/* pv, pi: TGK_AM_PARTS per row of workspace (each row's parts' best) */
+#define TGK_AM_PARTS 64
+void tgk_dec_argmax(hipStream_t s, const float *x, long xrs, int V, int rows, float *idf, int *idi, long idi_stride, float *pv, int *pi);
 
 int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, int bits, int axis, int C, int K, hipStream_t s);
 /* the same from int8 codes one per element, laid out [C][K] (axis 0) */
@@ -168,6 +219,10 @@ typedef struct {
 /* scratch: bytes needed for M rows of K inputs */
 size_t tgk_qgemm_scratch(int M, int Kp);
 void tgk_qgemm(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
+/* the digit area tgk_qgemm uses in `scratch` for M rows of Kp inputs, for
+ * kernels that write a GEMM's activation digits themselves (tg_qdigits.h)
+ * before tgk_qgemm_mfma */
+tgk_qdig tgk_qgemm_digit_area(void *scratch, int M, int Kp);
 /* the two launches of tgk_qgemm: activation digits, then the MFMA kernel */
 void tgk_qgemm_digits(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 void tgk_qgemm_mfma(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
