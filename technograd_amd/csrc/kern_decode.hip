@@ -4,6 +4,7 @@
 // order (this file is compiled with -ffp-contract=off), so a decoded token's
 // logits equal the fixed-length forward's at that position bit for bit.
 #include "tg_kern.h"
+#include "tg_devmath.h"
 #include "tg_qdigits.h"
 
 #include <math.h>
@@ -59,25 +60,6 @@ int attn_chunk(int HD) // keys per chunk: ATT_R float4 loads per thread, at most
 	int ck = 64;
 	while (ck > 1 && ck * (HD / 4) > ATT_R * ATT_TPB) ck >>= 1;
 	return ck;
-}
-
-// sum of z[0 .. n) in index order, z 16-byte aligned: loads 32 ahead of the adds
-__device__ inline float ordered_sum(const float *z, int n)
-{
-	float sum = 0.0f;
-	int i = 0;
-	for (; i + 32 <= n; i += 32) {
-		float4 b[8];
-		for (int j = 0; j < 8; j++) b[j] = *(const float4 *)(z + i + 4 * j);
-		for (int j = 0; j < 8; j++) {
-			sum += b[j].x;
-			sum += b[j].y;
-			sum += b[j].z;
-			sum += b[j].w;
-		}
-	}
-	for (; i < n; i++) sum += z[i];
-	return sum;
 }
 
 template <int GRP>
@@ -142,7 +124,7 @@ __global__ __launch_bounds__(ATT_TPB) void dec_attn_k(tgk_dec_attn_args a, int c
 		if (e - g * nst < n) sc[e] = expf(sc[e] - lv[g]);
 	}
 	__syncthreads();
-	if (tid < GRP) lv[tid] = ordered_sum(sc + tid * nst, n);
+	if (tid < GRP) lv[tid] = tg_ordered_sum<4>(sc + tid * nst, n);
 	__syncthreads();
 	for (int e = tid; e < GRP * nst; e += ATT_TPB) {
 		const int g = e / nst;
@@ -329,43 +311,66 @@ __device__ inline void blk_digits(const float *z, int Kp, float mx, int bad, con
 	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = special, q.qsum[m] = qs;
 }
 
-// tgk_dec_norm: one block per token row. The row's sum of squares is the
-// reference's sequential loop over the squares (computed in parallel), the
-// scale 1 / sqrtf(sum / D + 1e-6) as the row-op kernel, then (h * inv) * g.
-__global__ __launch_bounds__(256) void dec_norm_k(tgk_dec_norm_args a)
+// tgk_dec_norm: one block per token row, NORM_TPB threads, each with at most
+// NORM_EPT elements (D <= NORM_TPB * NORM_EPT) whose loads are all issued
+// first. The row's sum of squares is the reference's sequential loop over the
+// squares (computed in parallel), the scale 1 / sqrtf(sum / D + 1e-6) as the
+// row-op kernel, then (h * inv) * g.
+constexpr int NORM_TPB = 1024, NORM_EPT = 4;
+static_assert(NORM_TPB * NORM_EPT == TGK_DEC_NORM_MAX, "tgk_dec_norm row size");
+__global__ __launch_bounds__(NORM_TPB) void dec_norm_k(tgk_dec_norm_args a)
 {
 	extern __shared__ float4 zs4[]; // [Kp] values, [Kp] squares (16-byte aligned)
 	float *zs = (float *)zs4;
 	__shared__ float redf[16], inv_s;
 	__shared__ long long redl[16];
-	const int t = blockIdx.x, D = a.D, Kp = a.Kp;
+	const int t = blockIdx.x, D = a.D, Kp = a.Kp, tid = threadIdx.x;
 	float *z = zs, *sq = zs + Kp, *hr = a.h + (long)t * a.hs;
-	for (int i = threadIdx.x; i < Kp; i += blockDim.x) {
-		float v = 0.0f;
-		if (i < D) {
-			v = hr[i];
-			if (a.mode == 1) {
-				v = v + a.add[(long)t * a.adds + i];
-				hr[i] = v;
-			} else if (a.mode == 2) {
-				const float *o = a.o + (long)t * D + i;
-				float acc = o[0];
-				for (int k = 1; k < a.nh; k++) acc = acc + o[(long)k * a.ohead];
-				v = v + acc;
-				hr[i] = v;
-			}
+	float v[NORM_EPT], g[NORM_EPT];
+	for (int u = 0; u < NORM_EPT; u++) {
+		const int i = tid + u * NORM_TPB, ic = i < D ? i : D - 1;
+		v[u] = hr[ic];
+		g[u] = a.g[ic];
+	}
+	if (a.mode == 1) {
+		float b[NORM_EPT];
+		for (int u = 0; u < NORM_EPT; u++) {
+			const int i = tid + u * NORM_TPB;
+			b[u] = a.add[(long)t * a.adds + (i < D ? i : D - 1)];
 		}
-		z[i] = v;
-		sq[i] = v * v;
+		for (int u = 0; u < NORM_EPT; u++) v[u] = v[u] + b[u];
+	} else if (a.mode == 2) { // v + ((o_0 + o_1) + ... + o_{nh-1}), 16 heads' loads at a time
+		for (int u = 0; u < NORM_EPT; u++) {
+			const int i = tid + u * NORM_TPB;
+			if (u > 0 && i >= D) break;
+			const float *o = a.o + (long)t * D + (i < D ? i : D - 1);
+			float acc = o[0];
+			for (int k0 = 1; k0 < a.nh; k0 += 16) {
+				float b[16];
+				for (int k = 0; k < 16; k++) b[k] = o[(long)(k0 + k < a.nh ? k0 + k : 0) * a.ohead];
+				for (int k = 0; k < 16 && k0 + k < a.nh; k++) acc = acc + b[k];
+			}
+			v[u] = v[u] + acc;
+		}
+	}
+	for (int u = 0; u < NORM_EPT; u++) {
+		const int i = tid + u * NORM_TPB;
+		if (i >= Kp) break;
+		if (i >= D) v[u] = 0.0f;
+		else if (a.mode) hr[i] = v[u];
+		z[i] = v[u];
+		sq[i] = v[u] * v[u];
 	}
 	__syncthreads();
-	if (threadIdx.x == 0) inv_s = 1.0f / sqrtf(ordered_sum(sq, D) / (float)D + 1e-6f);
+	if (tid == 0) inv_s = 1.0f / sqrtf(tg_ordered_sum<8>(sq, D) / (float)D + 1e-6f);
 	__syncthreads();
 	const float inv = inv_s;
 	float mx = 0.0f;
 	int bad = 0;
-	for (int i = threadIdx.x; i < D; i += blockDim.x) {
-		const float nv = z[i] * inv * a.g[i];
+	for (int u = 0; u < NORM_EPT; u++) {
+		const int i = tid + u * NORM_TPB;
+		if (i >= D) break;
+		const float nv = v[u] * inv * g[u];
 		a.out[(long)t * a.outs + i] = nv;
 		z[i] = nv;
 		bad |= !isfinite(nv);
@@ -395,7 +400,7 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 	__builtin_amdgcn_wave_barrier();
 	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 	float inv = 0.0f;
-	if (lane == 0) inv = 1.0f / sqrtf(ordered_sum(sq, HD) / (float)HD + 1e-6f);
+	if (lane == 0) inv = 1.0f / sqrtf(tg_ordered_sum<8>(sq, HD) / (float)HD + 1e-6f);
 	inv = __shfl(inv, 0);
 	float mx = 0.0f;
 	int bad = 0;
@@ -426,7 +431,7 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 }
 
 // tgk_dec_silu: one block per row; silu as the element-wise kernels compute it
-__global__ __launch_bounds__(256) void dec_silu_k(tgk_dec_silu_args a)
+__global__ __launch_bounds__(1024) void dec_silu_k(tgk_dec_silu_args a)
 {
 	extern __shared__ float4 zs4[]; // [Kp]
 	float *zs = (float *)zs4;
@@ -554,7 +559,7 @@ void tgk_dec_attn(hipStream_t s, const tgk_dec_attn_args *a, int seqs)
 
 void tgk_dec_norm(hipStream_t s, const tgk_dec_norm_args *a)
 {
-	if (a->rows > 0) dec_norm_k<<<(unsigned)a->rows, TPB, (size_t)a->Kp * 2 * sizeof(float), s>>>(*a);
+	if (a->rows > 0) dec_norm_k<<<(unsigned)a->rows, NORM_TPB, (size_t)a->Kp * 2 * sizeof(float), s>>>(*a);
 }
 
 void tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a)
@@ -565,7 +570,7 @@ void tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a)
 
 void tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a)
 {
-	if (a->rows > 0) dec_silu_k<<<(unsigned)a->rows, TPB, (size_t)a->Kp * sizeof(float), s>>>(*a);
+	if (a->rows > 0) dec_silu_k<<<(unsigned)a->rows, 1024, (size_t)a->Kp * sizeof(float), s>>>(*a);
 }
 
 size_t tgk_dec_wo_lds(int rows, int HD) { return (size_t)rows * HD * 4 + (size_t)rows * 8 + (size_t)HD * 64; }

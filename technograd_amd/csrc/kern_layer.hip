@@ -332,32 +332,13 @@ __global__ void rowop_k(int op, float *o, long ors, tgk_opd a, int nrow, int col
 // Softmax's max: x[0] when it is nan, else the largest of x[0] and the
 // non-nan x[i] (the reference's `if (x[i] > mx) mx = x[i]`); its sign of zero
 // cannot change expf(x - mx).
-// sum_i z_i (SQ: z_i * z_i) in index order, as the reference's loop: one
-// thread, one add after another; the loads run ahead in batches of 32 (16-byte
-// LDS reads when the line is 16-byte aligned) so only the adds are serial
-template <bool SQ> __device__ inline float line_sum(const float *z, int cols)
+// sum_i z_i in index order, as the reference's loop: one thread, one add
+// after another (tg_ordered_sum when the line is 16-byte aligned)
+__device__ inline float line_sum(const float *z, int cols)
 {
+	if ((((size_t)z) & 15) == 0) return tg_ordered_sum<8>(z, cols);
 	float sum = 0.0f;
-	int i = 0;
-	if ((((size_t)z) & 15) == 0)
-		for (; i + 32 <= cols; i += 32) {
-			float4 b[8];
-			for (int j = 0; j < 8; j++) b[j] = *(const float4 *)(z + i + 4 * j);
-			for (int j = 0; j < 8; j++) {
-				if (SQ) {
-					sum += b[j].x * b[j].x;
-					sum += b[j].y * b[j].y;
-					sum += b[j].z * b[j].z;
-					sum += b[j].w * b[j].w;
-				} else {
-					sum += b[j].x;
-					sum += b[j].y;
-					sum += b[j].z;
-					sum += b[j].w;
-				}
-			}
-		}
-	for (; i < cols; i++) sum += SQ ? z[i] * z[i] : z[i];
+	for (int i = 0; i < cols; i++) sum += z[i];
 	return sum;
 }
 
@@ -395,7 +376,7 @@ __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, t
 			*z = expf(*z - lv[e / cols]);
 		}
 		__syncthreads();
-		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = line_sum<false>(lds + threadIdx.x * stride, cols);
+		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = line_sum(lds + threadIdx.x * stride, cols);
 		__syncthreads();
 		for (int e = threadIdx.x; e < tot; e += TPB) {
 			float *z = lds + (e / cols) * stride + e % cols;
@@ -409,7 +390,7 @@ __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, t
 			sq[l * stride + i] = lds[l * stride + i] * lds[l * stride + i];
 		}
 		__syncthreads();
-		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = 1.0f / sqrtf(line_sum<false>(sq + threadIdx.x * stride, cols) / (float)cols + 1e-6f);
+		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = 1.0f / sqrtf(line_sum(sq + threadIdx.x * stride, cols) / (float)cols + 1e-6f);
 		__syncthreads();
 		for (int e = threadIdx.x; e < tot; e += TPB) {
 			float *z = lds + (e / cols) * stride + e % cols;

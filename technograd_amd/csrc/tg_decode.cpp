@@ -317,6 +317,7 @@ bool build(tg_hip_dec *d)
 	const int grp = d->NQ / d->NKV;
 	if ((grp != 1 && grp != 2 && grp != 4 && grp != 8) || d->HD % 16 || d->HD > 256)
 		return err("decoder: needs 1, 2, 4 or 8 query heads per KV head and a head size that is a multiple of 16, at most 256%s", "");
+	if (d->D > TGK_DEC_NORM_MAX) return err("decoder: a model width above %s%ld", "", TGK_DEC_NORM_MAX);
 	if (tgk_dec_attn_lds(grp, d->HD, d->P) > 65536) return err("decoder: %s%ld positions do not fit one step's attention (LDS)", "", d->P);
 	if (m->val[vcos].sh.rank != 2 || m->val[vcos].sh.dim[1] != d->HD || m->val[vcos].sh.dim[0] < d->P)
 		return err("decoder: rope tables need %s%ld rows", "", d->P);

@@ -44,3 +44,50 @@ TG_HD inline float tg_log1p_unit(float y)
 	p = fma(p, z, 1.0);
 	return (float)(k * 0.6931471805599453 + 2.0 * s * p);
 }
+
+#ifdef __HIPCC__
+#include <hip/hip_runtime.h>
+
+// sum of z[0 .. n) in index order, one f32 rounding per add as in a
+// sequential loop; z 16-byte aligned (an LDS line). The loop runs in steps of
+// 64 NB values, fully unrolled and with no loaded value carried across its
+// back edge, so the compiler issues each step's 16-byte loads ahead of its
+// adds and only the adds wait on each other (plus one load latency per step).
+template <int NB> __device__ __attribute__((always_inline)) inline float tg_ordered_sum(const float *z, int n)
+{
+	constexpr int S = 64 * NB, B = 32;
+	float sum = 0.0f;
+	int i = 0;
+	for (; i + S <= n; i += S) {
+#pragma unroll
+		for (int c = 0; c < S / 4; c++) {
+			const float4 v = ((const float4 *)(z + i))[c];
+			sum += v.x;
+			sum += v.y;
+			sum += v.z;
+			sum += v.w;
+		}
+	}
+	for (; i + B <= n; i += B) {
+		float4 v[B / 4];
+#pragma unroll
+		for (int c = 0; c < B / 4; c++) v[c] = ((const float4 *)(z + i))[c];
+#pragma unroll
+		for (int c = 0; c < B / 4; c++) {
+			sum += v[c].x;
+			sum += v[c].y;
+			sum += v[c].z;
+			sum += v[c].w;
+		}
+	}
+	if (i < n) { // fewer than B left: load them all, then add in order
+		float t[B];
+#pragma unroll
+		for (int k = 0; k < B; k++) t[k] = z[i + k < n ? i + k : n - 1];
+#pragma unroll
+		for (int k = 0; k < B; k++)
+			if (i + k < n) sum += t[k];
+	}
+	return sum;
+}
+#endif

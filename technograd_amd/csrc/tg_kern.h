@@ -161,6 +161,7 @@ typedef struct {
 	int D, Kp, rows;
 	tgk_qdig q;
 } tgk_dec_norm_args;
+#define TGK_DEC_NORM_MAX 4096 /* largest D of tgk_dec_norm */
 void tgk_dec_norm(hipStream_t s, const tgk_dec_norm_args *a);
 /* per-head rmsnorm * gain of the q and k heads (line (t, j) at x + t xs + j HD),
  * into out [rows][NH][HD] and the digits of its rows t NH + j */
