@@ -302,20 +302,21 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 				  Tot tot, TotD totd)
 {
 	const int r32 = lane & 31, h = lane >> 5;
-	int sp = 0;
-	for (int v = 0; v < 16; v++) {
-		const int m = mbase + 8 * (v >> 2) + 4 * h + (v & 3);
-		if (m < a.M) sp |= s.special[m];
-	}
-	if (__any(sp)) {
-		for (int j = 0; j < NB; j++)
-			for (int v = 0; v < 16; v++) epilogue(a, w, s, mbase + 8 * (v >> 2) + 4 * h + (v & 3), cbase + j * 32 + r32, tot(j, v));
-		return;
-	}
+	// Lane l fetches row mbase + l % 32's exponent, sum of q and flag, and the
+	// scales of its columns, all in one round trip; a lane's 16 rows then come
+	// from the lanes that hold them (shuffles), not from 16 dependent loads.
+	const int mr = mbase + r32, mrc = mr < a.M ? mr : a.M - 1;
+	const int Er = s.e[mrc], spr = mr < a.M ? s.special[mrc] : 0;
+	const long long Qr = w.bits == 4 ? s.qsum[mrc] : 0;
 	float sc[NB];
 	for (int j = 0; j < NB; j++) {
 		const int c = cbase + j * 32 + r32;
 		sc[j] = w.scale[c < w.Cp ? c : 0]; // scales are padded to Cp; columns at or beyond C are not written
+	}
+	if (__any(spr)) {
+		for (int j = 0; j < NB; j++)
+			for (int v = 0; v < 16; v++) epilogue(a, w, s, mbase + 8 * (v >> 2) + 4 * h + (v & 3), cbase + j * 32 + r32, tot(j, v));
+		return;
 	}
 	if (a.nseg > 1) { // a merged GEMM: each column's own output
 		OutCol oc[NB];
@@ -324,10 +325,10 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 			oc[j] = out_col(a, c < w.C ? c : 0);
 		}
 		for (int v = 0; v < 16; v++) {
-			const int m = mbase + 8 * (v >> 2) + 4 * h + (v & 3);
+			const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
+			const int E = __shfl(Er, rv);
+			const double q8 = 8.0 * (double)__shfl(Qr, rv); // 0 for int8 weights
 			if (m >= a.M) continue;
-			const int E = s.e[m];
-			const double q8 = w.bits == 4 ? 8.0 * (double)s.qsum[m] : 0.0;
 			int r = m, jj = 0;
 			if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
 			for (int j = 0; j < NB; j++) {
@@ -340,11 +341,11 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 	long coff[NB];
 	for (int j = 0; j < NB; j++) coff[j] = (long)(cbase + j * 32 + r32) * a.oc;
 	for (int v = 0; v < 16; v++) {
-		const int m = mbase + 8 * (v >> 2) + 4 * h + (v & 3);
-		if (m >= a.M) continue;
-		const int E = s.e[m];
+		const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
+		const int E = __shfl(Er, rv);
 		// f64 arithmetic on integers below 2^53: (double)(tot - 8 qsum) exactly
-		const double q8 = w.bits == 4 ? 8.0 * (double)s.qsum[m] : 0.0;
+		const double q8 = 8.0 * (double)__shfl(Qr, rv); // 0 for int8 weights
+		if (m >= a.M) continue;
 		int r = m, jj = 0;
 		if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
 		float *orow = a.o + (long)r * a.orr + (long)jj * a.oj;
@@ -536,7 +537,7 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 	constexpr int LB = BITS == 4 ? 8 : 16;        // weight bytes per lane per block
 	constexpr int NL = 3 + NB;                    // load instructions per block
 	typedef typename std::conditional<BITS == 4, v2u, v4i>::type bfrag;
-	__shared__ long long red[(W > 1 ? W - 1 : 1) * NB * 16 * 64];
+	__shared__ double red[(W > 1 ? W - 1 : 1) * NB * 16 * 64]; // other waves' partial sums (integers below 2^48: exact)
 	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int bx = blockIdx.x % gx, by = blockIdx.x / gx;
 	const int m0 = by * 32, c0 = bx * NB * 32, kblocks = w.Kp / 32;
@@ -580,20 +581,29 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 		}
 	}
 	wait_vm<0>(); // the ring's last (unused) loads have landed before the wave goes on
+	// ... and until then every ring register stays allocated to its load: the
+	// compiler sees each slot read here, after the wait, so it cannot hand a
+	// register with a load still in flight to another value (an in-flight
+	// load would overwrite it)
+	for (int u = 0; u < P; u++) {
+		for (int l = 0; l < 3; l++) touch(af[u][l]);
+		for (int j = 0; j < NB; j++) touch(bf[u][j]);
+	}
 	if (W > 1) {
 		if (wave > 0)
 			for (int j = 0; j < NB; j++)
 				for (int v = 0; v < 16; v++)
-					red[(((wave - 1) * NB + j) * 16 + v) * 64 + lane] = combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+					red[(((wave - 1) * NB + j) * 16 + v) * 64 + lane] = combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
 		__syncthreads();
 		if (wave != 0) return;
 	}
-	auto tot = [&](int j, int v) {
-		long long t = combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+	// the block's sum: integers below 2^51 in magnitude, so the f64 sum is exact
+	auto totd = [&](int j, int v) {
+		double t = combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
 		for (int u = 0; u < W - 1; u++) t += red[((u * NB + j) * 16 + v) * 64 + lane];
 		return t;
 	};
-	store_tile<NB>(a, w, s, m0, c0, lane, tot, [&](int j, int v) { return (double)tot(j, v); });
+	store_tile<NB>(a, w, s, m0, c0, lane, [&](int j, int v) { return (long long)totd(j, v); }, totd);
 }
 
 template <int BITS, int NB, int W>
@@ -608,15 +618,29 @@ void launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 {
 	const tgk_qweight *w = a->w;
 	const int gx = w->Cp / BN, gy = Mp / BM;
-	if ((long)gx * gy >= 128) { // enough 128 x 256 tiles for the LDS kernel
+	const long rt = round_up(a->M, 32) / 32, cb = w->Cp / 32;
+	if ((long)gx * gy >= 128 && rt > 2) { // enough 128 x 256 tiles for the LDS kernel
 		qgemm_k<BITS><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy);
 		return;
 	}
-	// smaller batches: as many 32 x (32 NB) tiles as fill the device
-	const long rt = round_up(a->M, 32) / 32, cb = w->Cp / 32;
-	if (rt * cb / 4 >= 256) launch_gemv<BITS, 4, 4>(st, a, s);
-	else if (rt * cb / 2 >= 256) launch_gemv<BITS, 2, 4>(st, a, s);
-	else launch_gemv<BITS, 1, 8>(st, a, s);
+	// up to 64 rows, or too few tiles: 32 x (32 NB) tiles, NB as large as
+	// still fills the device; W waves split K, about 16 32-input blocks each
+	// (each further wave adds partial sums for the epilogue to read)
+	const int kb = w->Kp / 32;
+	if (rt * cb / 4 >= 256) {
+		if (kb >= 128) launch_gemv<BITS, 4, 4>(st, a, s);
+		else if (kb >= 64) launch_gemv<BITS, 4, 2>(st, a, s);
+		else launch_gemv<BITS, 4, 1>(st, a, s);
+	} else if (rt * cb / 2 >= 256) {
+		if (kb >= 128) launch_gemv<BITS, 2, 4>(st, a, s);
+		else if (kb >= 64) launch_gemv<BITS, 2, 2>(st, a, s);
+		else launch_gemv<BITS, 2, 1>(st, a, s);
+	} else {
+		if (kb >= 128) launch_gemv<BITS, 1, 8>(st, a, s);
+		else if (kb >= 64) launch_gemv<BITS, 1, 4>(st, a, s);
+		else if (kb >= 32) launch_gemv<BITS, 1, 2>(st, a, s);
+		else launch_gemv<BITS, 1, 1>(st, a, s);
+	}
 }
 
 } // namespace

@@ -1,0 +1,76 @@
+"""Register-ring check of the small-batch GEMM (technograd_amd/csrc/kern_qgemm.hip,
+qgemv_k), on the gfx950 assembly hipcc writes for it (no GPU needed).
+
+qgemv_k loads its operands with inline-assembly loads the compiler does not
+track: it believes a load's destination registers hold their value as soon as
+the instruction is issued. A ring register whose load is still in flight must
+therefore not be given to any other value, or the load overwrites that value
+when it lands. This test walks each qgemv_k instantiation from the last full
+wait before its final ring load to the first full wait after it, retiring
+loads in order at each vmcnt(N), and fails if an instruction after the final
+ring load writes a register that an outstanding load will write. (The kernel
+prevents this by reading every ring register after its final wait; without
+that, the epilogue's row index was computed into such registers, and the
+index was overwritten before the row-info loads used it.)"""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+
+def _vregs(tok):
+    m = re.match(r"v\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"v(\d+)$", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def ring_hazards(asm_lines):
+    """{kernel: [instructions writing an in-flight ring register]} for every qgemv_k."""
+    found = {}
+    starts = [i for i, l in enumerate(asm_lines) if re.match(r"^_Z\S*qgemv_k\S*:", l)]
+    for s in starts:
+        e = next(i for i in range(s, len(asm_lines)) if "s_endpgm" in asm_lines[i])
+        body = [l.strip() for l in asm_lines[s:e] if l.strip() and not l.strip().startswith(";")]
+        ring = [i for i, t in enumerate(body) if re.match(r"global_load_dwordx[24] v\S+, v\d+, s\[", t)]
+        assert ring, "no ring loads found in " + asm_lines[s]
+        last = ring[-1]
+        w0 = max([i for i in range(last) if "vmcnt(0)" in body[i]] + [0])
+        end = next(i for i in range(last, len(body)) if "vmcnt(0)" in body[i])
+        out, hits = [], []
+        for k in range(w0 + 1, end):
+            t = body[k]
+            p = re.split(r"[\s,]+", t)
+            if p[0] == "s_waitcnt":
+                m = re.search(r"vmcnt\((\d+)\)", t)
+                if m:
+                    n = int(m.group(1))
+                    out = out[len(out) - n:] if n < len(out) else out
+                continue
+            if p[0].startswith("global_load") or p[0].startswith("buffer_load"):
+                out.append(_vregs(p[1]))
+                continue
+            if k > last and p[0].startswith("v_") and not p[0].startswith("v_cmp") and len(p) > 1:
+                if any(_vregs(p[1]) & o for o in out):
+                    hits.append(t)
+        found[asm_lines[s].split(":")[0]] = hits
+    return found
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC) and not shutil.which("hipcc"), reason="hipcc not installed")
+def test_qgemv_ring_registers_not_reused_in_flight(tmp_path):
+    csrc = os.path.join(ROOT, "technograd_amd", "csrc")
+    asm = tmp_path / "kern_qgemm.s"
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
+                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", os.path.join(ROOT, "include"), "-I", csrc,
+                    "--cuda-device-only", "-S", os.path.join(csrc, "kern_qgemm.hip"), "-o", str(asm)], check=True, capture_output=True)
+    found = ring_hazards(asm.read_text().split("\n"))
+    assert len(found) >= 6  # every instantiation the launcher uses was checked
+    bad = {k: v for k, v in found.items() if v}
+    assert not bad, bad
