@@ -430,6 +430,141 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 	if (lane == 0) a.q.e[L] = E, a.q.special[L] = special, a.q.qsum[L] = qs;
 }
 
+// Many lines at once (a prompt's token rows, or its head lines): a block of
+// NL_TPB threads holds R = NL_E / Kp whole lines, NL_EPT elements per thread
+// (all loaded before any is used), and the lines' R sequential sums of squares
+// run side by side, one thread each. Line L = t npr + j reads h + t hs + j D
+// (updated in place by modes 1 and 2, which need npr == 1), takes gain
+// g + j gs, writes out + L D and the digits of row L. The values are the
+// same as tgk_dec_norm's and tgk_dec_hnorm's: (h * inv) * g with
+// inv = 1 / sqrtf(sum / D + 1e-6), sum the ordered sum of the squares.
+struct NormLines {
+	float *h;
+	long hs;
+	int mode;
+	const float *add;
+	long adds;
+	const float *o;
+	long ohead;
+	int nh;
+	const float *g;
+	long gs;
+	float *out;
+	int D, Kp, npr;
+	long lines;
+	tgk_qdig q;
+	int kshift; // Kp = 1 << kshift
+};
+constexpr int NL_TPB = 256, NL_EPT = 16, NL_E = NL_TPB * NL_EPT;
+
+// LDS: R lines of Kp + 4 floats (16-byte aligned, consecutive lines 4 banks
+// apart), then per line its offsets, 1 / rms, exponent and flag
+size_t norm_lines_lds(int Kp) { return (size_t)(NL_E / Kp) * ((Kp + 4) * 4 + 8 + 4 * 4); }
+
+__global__ __launch_bounds__(NL_TPB) void norm_lines_k(NormLines a)
+{
+	extern __shared__ float4 sh4[];
+	const int Kp = a.Kp, D = a.D, ks = a.kshift, km = Kp - 1, R = NL_E >> ks, ZS = Kp + 4, tid = threadIdx.x;
+	float *z = (float *)sh4; // [R][ZS]: the squares, then the normalized values (0 from D on)
+	long *lh = (long *)(z + R * ZS); // line l's offset in h (t hs + j D)
+	int *lg = (int *)(lh + R), *lE = lg + R, *lsp = lE + R;
+	float *linv = (float *)(lsp + R);
+	const long L0 = (long)blockIdx.x * R;
+	if (tid < R) { // per line, once (lines past the end repeat the last)
+		const long L = L0 + tid < a.lines ? L0 + tid : a.lines - 1;
+		const long t = L / a.npr, j = L - t * a.npr;
+		lh[tid] = t * a.hs + j * D;
+		lg[tid] = (int)(j * a.gs);
+	}
+	__syncthreads();
+	// element u of this thread: e = tid + u NL_TPB, line e >> ks, column e & km
+	float v[NL_EPT];
+	for (int u = 0; u < NL_EPT; u++) {
+		const int e = tid + u * NL_TPB, l = e >> ks, i = e & km;
+		v[u] = a.h[lh[l] + (i < D ? i : D - 1)];
+	}
+	if (a.mode == 1) { // npr == 1: line l is token row L0 + l
+		float b[NL_EPT];
+		for (int u = 0; u < NL_EPT; u++) {
+			const int e = tid + u * NL_TPB, l = e >> ks, i = e & km;
+			const long L = L0 + l < a.lines ? L0 + l : a.lines - 1;
+			b[u] = a.add[L * a.adds + (i < D ? i : D - 1)];
+		}
+		for (int u = 0; u < NL_EPT; u++) v[u] = v[u] + b[u];
+	} else if (a.mode == 2) { // v + ((o_0 + o_1) + ... + o_{nh-1})
+		for (int u = 0; u < NL_EPT; u++) {
+			const int e = tid + u * NL_TPB, l = e >> ks, i = e & km;
+			const long L = L0 + l < a.lines ? L0 + l : a.lines - 1;
+			const float *o = a.o + L * D + (i < D ? i : D - 1);
+			float acc = o[0];
+			for (int k0 = 1; k0 < a.nh; k0 += 16) {
+				float b[16];
+				for (int k = 0; k < 16; k++) b[k] = o[(long)(k0 + k < a.nh ? k0 + k : 0) * a.ohead];
+				for (int k = 0; k < 16 && k0 + k < a.nh; k++) acc = acc + b[k];
+			}
+			v[u] = v[u] + acc;
+		}
+	}
+	for (int u = 0; u < NL_EPT; u++) {
+		const int e = tid + u * NL_TPB, l = e >> ks, i = e & km;
+		const bool in = L0 + l < a.lines && i < D;
+		if (in && a.mode) a.h[lh[l] + i] = v[u];
+		z[l * ZS + i] = in ? v[u] * v[u] : 0.0f;
+	}
+	__syncthreads();
+	if (tid < R && L0 + tid < a.lines) linv[tid] = 1.0f / sqrtf(tg_ordered_sum<8>(z + tid * ZS, D) / (float)D + 1e-6f);
+	__syncthreads();
+	{
+		float gv[NL_EPT]; // the gains, all loaded before the first is used
+		for (int u = 0; u < NL_EPT; u++) {
+			const int e = tid + u * NL_TPB, l = e >> ks, i = e & km;
+			gv[u] = a.g[lg[l] + (i < D ? i : D - 1)];
+		}
+		for (int u = 0; u < NL_EPT; u++) {
+			const int e = tid + u * NL_TPB, l = e >> ks, i = e & km;
+			const bool in = L0 + l < a.lines && i < D;
+			float nv = 0.0f;
+			if (in) {
+				nv = v[u] * linv[l] * gv[u];
+				a.out[(L0 + l) * D + i] = nv;
+			}
+			z[l * ZS + i] = nv;
+		}
+	}
+	__syncthreads();
+	// per line: TPL = NL_TPB / R consecutive lanes (within one wave) take its max
+	// and flag, then its 16-input digit groups (Kp / 16 / TPL = 2 each) and
+	// the sum of their q, combined by shuffles
+	const int TPL = NL_TPB / R, l = tid / TPL, k = tid - l * TPL;
+	const float *zl = z + l * ZS;
+	float mx = 0.0f;
+	int bad = 0;
+	for (int m = k; m < Kp; m += TPL) {
+		const float x = zl[m];
+		bad |= !isfinite(x);
+		mx = fmaxf(mx, fabsf(x)); // a nan never wins fmaxf; such lines are flagged
+	}
+	for (int o = 1; o < TPL; o <<= 1) {
+		mx = fmaxf(mx, __shfl_xor(mx, o));
+		bad |= __shfl_xor(bad, o);
+	}
+	const int special = tgq_special(bad, mx), E = tgq_exponent(mx, special);
+	long long qs = 0;
+	if (L0 + l < a.lines) {
+		int8_t *blk = tgq_row_base(a.q.dig, (int)(L0 + l), Kp);
+		for (int gi = k; gi < Kp / 16; gi += TPL) {
+			float w16[16];
+			for (int q = 0; q < 16; q++) w16[q] = zl[gi * 16 + q];
+			qs += tgq_put16(blk, gi * 16, w16, E, special);
+		}
+	}
+	for (int o = 1; o < TPL; o <<= 1) qs += __shfl_xor(qs, o);
+	if (k == 0 && L0 + l < a.lines) {
+		const long L = L0 + l;
+		a.q.e[L] = E, a.q.special[L] = special, a.q.qsum[L] = qs;
+	}
+}
+
 // tgk_dec_silu: one block per row; silu as the element-wise kernels compute it
 __global__ __launch_bounds__(1024) void dec_silu_k(tgk_dec_silu_args a)
 {
@@ -557,15 +692,34 @@ void tgk_dec_attn(hipStream_t s, const tgk_dec_attn_args *a, int seqs)
 	}
 }
 
+// many lines (a prompt): norm_lines_k; few (a step): a block per row or a wave per head line
+constexpr long NL_MIN_LINES = 2048;
+inline bool nl_fits(int Kp) { return Kp >= 64 && Kp <= NL_E && (Kp & (Kp - 1)) == 0; } // a power of two: lines by shifts
+inline int ilog2(int x) { int k = 0; while ((1 << (k + 1)) <= x) k++; return k; }
+
 void tgk_dec_norm(hipStream_t s, const tgk_dec_norm_args *a)
 {
-	if (a->rows > 0) dec_norm_k<<<(unsigned)a->rows, NORM_TPB, (size_t)a->Kp * 2 * sizeof(float), s>>>(*a);
+	if (a->rows <= 0) return;
+	if (a->rows >= NL_MIN_LINES && nl_fits(a->Kp) && a->outs == a->D) {
+		NormLines n{ a->h, a->hs, a->mode, a->add, a->adds, a->o, a->ohead, a->nh, a->g, 0, a->out, a->D, a->Kp, 1, a->rows, a->q, ilog2(a->Kp) };
+		const long R = NL_E / a->Kp;
+		norm_lines_k<<<(unsigned)((a->rows + R - 1) / R), NL_TPB, norm_lines_lds(a->Kp), s>>>(n);
+		return;
+	}
+	dec_norm_k<<<(unsigned)a->rows, NORM_TPB, (size_t)a->Kp * 2 * sizeof(float), s>>>(*a);
 }
 
 void tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a)
 {
 	const long lines = (long)a->rows * a->NH;
-	if (lines > 0) dec_hnorm_k<<<(unsigned)((lines + 3) / 4), TPB, (size_t)a->Kp * 8 * sizeof(float), s>>>(*a);
+	if (lines <= 0) return;
+	if (lines >= NL_MIN_LINES && nl_fits(a->Kp)) {
+		NormLines n{ (float *)a->x, a->xs, 0, nullptr, 0, nullptr, 0, 0, a->g, a->HD, a->out, a->HD, a->Kp, a->NH, lines, a->q, ilog2(a->Kp) };
+		const long R = NL_E / a->Kp;
+		norm_lines_k<<<(unsigned)((lines + R - 1) / R), NL_TPB, norm_lines_lds(a->Kp), s>>>(n);
+		return;
+	}
+	dec_hnorm_k<<<(unsigned)((lines + 3) / 4), TPB, (size_t)a->Kp * 8 * sizeof(float), s>>>(*a);
 }
 
 void tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a)

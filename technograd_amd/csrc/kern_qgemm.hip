@@ -165,6 +165,107 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 	}
 }
 
+// Many rows, 16 per block (twice the blocks of the 32-row kernel below, for
+// batches that would leave the device half idle with 32): lane l of wave w
+// owns row m0 + (l & 15), half (l >> 4) & 1 and parity l >> 5 of 32-input
+// block pairs w, w + W, ... (NKB pairs in registers). In each digit plane a
+// block writes its 16 rows' two 256-byte runs. The row's max, non-finite
+// flag and sum of q are combined through LDS. Results are those of digits_k.
+template <int NKB, bool VEC>
+__global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
+{
+	__shared__ float smx[16][64];
+	__shared__ int sbad[16][64];
+	__shared__ long long sqs[16][64];
+	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
+	const int m0 = blockIdx.x * 16, mr = lane & 15, half = (lane >> 4) & 1, par = lane >> 5;
+	const float *x = xrow(a, m0 + mr < M ? m0 + mr : M - 1); // rows past M repeat row M - 1
+	const int nkb = Kp / 32;
+	float v[NKB][16];
+	float mx = 0.0f;
+	int bad = 0;
+	for (int j = 0; j < NKB; j++) {
+		const int kb = 2 * (w + j * W) + par;
+		load16<VEC>(v[j], x, a.xk, kb < nkb ? kb * 32 + half * 16 : K, K); // past the row: zeros
+		for (int i = 0; i < 16; i++) {
+			bad |= !isfinite(v[j][i]);
+			mx = fmaxf(mx, fabsf(v[j][i]));
+		}
+	}
+	smx[w][lane] = mx;
+	sbad[w][lane] = bad;
+	__syncthreads();
+	float amax = 0.0f;
+	bad = 0;
+	for (int u = 0; u < W; u++)
+		for (int q = 0; q < 4; q++) {
+			amax = fmaxf(amax, smx[u][mr + 16 * q]);
+			bad |= sbad[u][mr + 16 * q];
+		}
+	const int special = tgq_special(bad, amax), E = tgq_exponent(amax, special);
+	int8_t *blk = s.dig + (long)(m0 >> 5) * nkb * 3072 + ((m0 & 31) + mr) * 16;
+	long long qs = 0;
+	for (int j = 0; j < NKB; j++) {
+		const int kb = 2 * (w + j * W) + par;
+		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special);
+	}
+	sqs[w][lane] = qs;
+	__syncthreads();
+	if (w == 0 && lane < 16 && m0 + mr < M) {
+		long long t = 0;
+		for (int u = 0; u < W; u++)
+			for (int q = 0; q < 4; q++) t += sqs[u][mr + 16 * q];
+		s.e[m0 + mr] = E;
+		s.special[m0 + mr] = special;
+		s.qsum[m0 + mr] = t;
+	}
+}
+
+// Few, long rows: one block of 256 threads per row, thread t taking the
+// 16-input groups t, t + 256, ... (G of them, in registers). The row's max,
+// non-finite flag and sum of q are combined across the block. Results are
+// those of digits_k.
+template <int G, bool VEC>
+__global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
+{
+	__shared__ float smx[4];
+	__shared__ int sbad[4];
+	__shared__ long long sqs[4];
+	const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, ng = Kp / 16;
+	const float *x = xrow(a, m);
+	float v[G][16];
+	float mx = 0.0f;
+	int bad = 0;
+	for (int g = 0; g < G; g++) {
+		const int j = tid + g * 256;
+		load16<VEC>(v[g], x, a.xk, j < ng ? j * 16 : K, K); // past the row: zeros
+		for (int i = 0; i < 16; i++) {
+			bad |= !isfinite(v[g][i]);
+			mx = fmaxf(mx, fabsf(v[g][i]));
+		}
+	}
+	mx = wave_max(mx); // nan never wins fmaxf; such rows are flagged by `bad`
+	bad = __any(bad);
+	if (lane == 0) smx[w] = mx, sbad[w] = bad;
+	__syncthreads();
+	const float amax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
+	const int special = tgq_special(sbad[0] | sbad[1] | sbad[2] | sbad[3], amax), E = tgq_exponent(amax, special);
+	int8_t *blk = tgq_row_base(s.dig, m, Kp);
+	long long qs = 0;
+	for (int g = 0; g < G; g++) {
+		const int j = tid + g * 256;
+		if (j < ng) qs += tgq_put16(blk, j * 16, v[g], E, special);
+	}
+	qs = wave_sum(qs);
+	if (lane == 0) sqs[w] = qs;
+	__syncthreads();
+	if (tid == 0) {
+		s.e[m] = E;
+		s.special[m] = special;
+		s.qsum[m] = sqs[0] + sqs[1] + sqs[2] + sqs[3];
+	}
+}
+
 // Many rows of at most 2048 inputs: one block per 32-row block of the digit
 // layout, W = blockDim / 64 waves. Lane l of wave w owns row m0 + (l & 31) and
 // the half (l >> 5) of 32-input blocks w, w + W, ... (NKB of them, held in
@@ -737,7 +838,21 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 	int Mp = (int)round_up(a->M, BM);
 	const Scratch s = carve(scratch, Mp, w->Kp);
 	const int nkb = w->Kp / 32, M = a->M, K = w->K;
-	if (M >= 512 && nkb <= 64) {
+	if (M >= 512 && M < 8192 && nkb <= 128) { // 16 rows per block: at least 32 (up to 512) blocks of 16 waves
+		const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) &&
+				 (K & 15) == 0;
+		const int W = nkb / 2 < 16 ? (nkb + 1) / 2 : 16, nb = (M + 15) / 16, pairs = (nkb + 1) / 2;
+		if (pairs <= W) {
+			if (vec) digits_tile16_k<1, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+			else digits_tile16_k<1, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+		} else if (pairs <= 2 * W) {
+			if (vec) digits_tile16_k<2, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+			else digits_tile16_k<2, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+		} else {
+			if (vec) digits_tile16_k<4, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+			else digits_tile16_k<4, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+		}
+	} else if (M >= 512 && nkb <= 64) {
 		const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) &&
 				 (K & 15) == 0;
 		const int W = nkb < 16 ? nkb : 16, nb = (M + 31) / 32;
@@ -750,6 +865,20 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 		} else {
 			if (vec) digits_tile_k<4, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
 			else digits_tile_k<4, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+		}
+	} else if (M < 512 && w->Kp >= 2048 && w->Kp <= 16384) { // few long rows: a block per row
+		const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) &&
+				 (K & 15) == 0;
+		const int G = (w->Kp / 16 + 255) / 256;
+		if (G <= 1) {
+			if (vec) digits_row_k<1, true><<<M, 256, 0, st>>>(*a, s, K, w->Kp, M);
+			else digits_row_k<1, false><<<M, 256, 0, st>>>(*a, s, K, w->Kp, M);
+		} else if (G <= 2) {
+			if (vec) digits_row_k<2, true><<<M, 256, 0, st>>>(*a, s, K, w->Kp, M);
+			else digits_row_k<2, false><<<M, 256, 0, st>>>(*a, s, K, w->Kp, M);
+		} else {
+			if (vec) digits_row_k<4, true><<<M, 256, 0, st>>>(*a, s, K, w->Kp, M);
+			else digits_row_k<4, false><<<M, 256, 0, st>>>(*a, s, K, w->Kp, M);
 		}
 	} else if (w->Kp <= 1024)
 		digits_k<1><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
