@@ -591,6 +591,52 @@ __global__ __launch_bounds__(1024) void dec_silu_k(tgk_dec_silu_args a)
 	blk_digits(zs, a.Kp, mx, bad, a.q, t, redf, redl);
 }
 
+// A prompt chunk's causal softmax of one head's scores, line (sequence, t)
+// of sc = q_t . k_u for u <= t (the products above the diagonal are not
+// computed). The graph's operations on the valid part: x_u = s_u * scale + 0
+// (the mask's 0), the row op's max rule, expf(x_u - max), the sum in key
+// order, e_u / sum. Above the diagonal the graph adds -1e9: for finite scores
+// that entry never wins the max and its expf is exactly 0, which leaves the
+// sum unchanged and gives p_u = 0, written here directly. lpb lines per block
+// (a power of two >= 4) staged in LDS, stride T0 + 4 floats (16-byte aligned).
+__global__ __launch_bounds__(256) void causal_softmax_k(float *sc, int T0, long nlines, float scale, int lpb, int stride)
+{
+	extern __shared__ float4 sh4[];
+	float *z = (float *)sh4, *lv = z + lpb * stride; // lv: per line max, then sum
+	const long L0 = (long)blockIdx.x * lpb;
+	const int tid = threadIdx.x, t0 = (int)(L0 % T0);
+	const int nl = nlines - L0 < lpb ? (int)(nlines - L0) : lpb; // lines of this block
+	auto pos = [&](int ll) { return (t0 + ll) % T0; };          // line ll's position t
+	for (int ll = 0; ll < nl; ll++) {
+		const int t = pos(ll);
+		const float *src = sc + (L0 + ll) * T0;
+		for (int u = tid; u <= t; u += 256) z[ll * stride + u] = src[u] * scale + 0.0f;
+	}
+	__syncthreads();
+	{ // max: 256 / lpb consecutive lanes of one wave per line
+		const int tpl = 256 / lpb, l = tid / tpl, sub = tid - l * tpl;
+		const int t = l < nl ? pos(l) : 0;
+		const float *y = z + l * stride;
+		float m = -INFINITY;
+		for (int u = 1 + sub; u <= t; u += tpl) m = fmaxf(m, y[u]);
+		for (int w = tpl / 2; w > 0; w >>= 1) m = fmaxf(m, __shfl_xor(m, w));
+		if (sub == 0) lv[l] = isnan(y[0]) ? y[0] : fmaxf(y[0], m);
+	}
+	__syncthreads();
+	for (int ll = 0; ll < nl; ll++) {
+		const int t = pos(ll);
+		for (int u = tid; u <= t; u += 256) z[ll * stride + u] = expf(z[ll * stride + u] - lv[ll]);
+	}
+	__syncthreads();
+	if (tid < nl) lv[tid] = tg_ordered_sum<8>(z + tid * stride, pos(tid) + 1);
+	__syncthreads();
+	for (int ll = 0; ll < nl; ll++) {
+		const int t = pos(ll);
+		float *dst = sc + (L0 + ll) * T0;
+		for (int u = tid; u < T0; u += 256) dst[u] = u <= t ? z[ll * stride + u] / lv[ll] : 0.0f;
+	}
+}
+
 // Greedy choice per row: the index of the largest logit, the first one on
 // ties, a nan counting as largest (numpy's argmax). (nan-ness, value, -index)
 // is a total order, so any grouping of the comparisons finds the same index:
@@ -725,6 +771,15 @@ void tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a)
 void tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a)
 {
 	if (a->rows > 0) dec_silu_k<<<(unsigned)a->rows, 1024, (size_t)a->Kp * sizeof(float), s>>>(*a);
+}
+
+void tgk_dec_causal_softmax(hipStream_t s, float *sc, int T0, long nlines, float scale)
+{
+	if (nlines <= 0 || T0 <= 0) return;
+	const int stride = (T0 + 3) / 4 * 4 + 4;
+	int lpb = 64; // a power of two >= 4: lines per block
+	while (lpb > 4 && (long)lpb * stride * 4 + lpb * 4 > 65536) lpb >>= 1;
+	causal_softmax_k<<<(unsigned)((nlines + lpb - 1) / lpb), 256, (size_t)lpb * stride * 4 + lpb * 4, s>>>(sc, T0, nlines, scale, lpb, stride);
 }
 
 size_t tgk_dec_wo_lds(int rows, int HD) { return (size_t)rows * HD * 4 + (size_t)rows * 8 + (size_t)HD * 64; }

@@ -542,46 +542,60 @@ void tgk_ew_run(hipStream_t s, const tgk_ew *e, int n, int rows)
 // f32 products (quant 0) in tiles: a block computes a TS x TS tile of one
 // (batch row, group) product, each of its 16 x 16 threads a TS/16 x TS/16
 // block of it. A and B pass through LDS 16 values of p at a time, and every
-// output adds its products in order p = 0..k-1 from 0.0f with separate
+// output adds its products in order p = 0..kend-1 from 0.0f with separate
 // multiply and add, exactly as mm_exact_k does, so the results are
 // bit-identical to it. Tile rows, columns and p values past m, n and k read
-// as zeros; the p loop stops at k and nothing past m or n is stored.
+// as zeros; the p loop stops at kend and nothing past m or n is stored.
 template <int TS>
-__global__ __launch_bounds__(256) void mm_tile_k(tgk_mm d, int tm, int tn)
+__device__ inline void mm_tile(const tgk_mm &d, const float *A, const float *B, float *O, int i0, int j0, int kend, float (*As)[TS + 4],
+			       float (*Bs)[TS + 4])
 {
-	constexpr int KC = 16, R = TS / 16;
-	__shared__ float As[KC][TS + 4]; // As[p][i]
-	__shared__ float Bs[KC][TS + 4]; // Bs[p][j]
-	const int tiles = tm * tn;
-	const long rg = blockIdx.x / tiles;
-	const int t = (int)(blockIdx.x - rg * tiles), ti = t / tn, tj = t - ti * tn;
-	const long r = rg / d.g;
-	const int g = (int)(rg - r * d.g);
-	const float *A = d.a.p + r * d.a.rs + g * d.ag, *B = d.b.p + r * d.b.rs + g * d.bg;
-	const int i0 = ti * TS, j0 = tj * TS;
+	constexpr int KC = 16, R = TS / 16, NE = TS * KC / 256; // tile elements per thread and chunk
 	const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
 	float acc[R][R];
 	for (int u = 0; u < R; u++)
 		for (int v = 0; v < R; v++) acc[u][v] = 0.0f;
-	for (int p0 = 0; p0 < d.k; p0 += KC) {
-		for (int e = threadIdx.x; e < TS * KC; e += 256) { // A tile, coalesced along whichever of i, p is unit stride
+	// chunk p0's A and B elements of this thread into registers (the next
+	// chunk's loads are in flight while the current one is multiplied)
+	float ra[NE], rb[NE];
+	auto fetch = [&](int p0) {
+		for (int q = 0; q < NE; q++) { // A, coalesced along whichever of i, p is unit stride
+			const int e = threadIdx.x + q * 256;
 			int i, p;
 			if (d.ap == 1) i = e / KC, p = e % KC;
 			else p = e / TS, i = e % TS;
 			const bool in = i0 + i < d.m && p0 + p < d.k;
 			const float x = A[in ? (long)(i0 + i) * d.ai + (long)(p0 + p) * d.ap : 0];
-			As[p][i] = in ? x : 0.0f;
+			ra[q] = in ? x : 0.0f;
 		}
-		for (int e = threadIdx.x; e < TS * KC; e += 256) { // B tile
+		for (int q = 0; q < NE; q++) { // B
+			const int e = threadIdx.x + q * 256;
 			int j, p;
 			if (d.bj == 1 || d.bp != 1) p = e / TS, j = e % TS;
 			else j = e / KC, p = e % KC;
 			const bool in = j0 + j < d.n && p0 + p < d.k;
 			const float x = B[in ? (long)(p0 + p) * d.bp + (long)(j0 + j) * d.bj : 0];
-			Bs[p][j] = in ? x : 0.0f;
+			rb[q] = in ? x : 0.0f;
 		}
-		__syncthreads();
-		const int kk = d.k - p0 < KC ? d.k - p0 : KC;
+	};
+	auto stash = [&]() {
+		for (int q = 0; q < NE; q++) {
+			const int e = threadIdx.x + q * 256;
+			if (d.ap == 1) As[e % KC][e / KC] = ra[q];
+			else As[e / TS][e % TS] = ra[q];
+			if (d.bj == 1 || d.bp != 1) Bs[e / TS][e % TS] = rb[q];
+			else Bs[e % KC][e / KC] = rb[q];
+		}
+	};
+	if (kend > 0) {
+		fetch(0);
+		stash();
+	}
+	__syncthreads();
+	for (int p0 = 0; p0 < kend; p0 += KC) {
+		const bool more = p0 + KC < kend;
+		if (more) fetch(p0 + KC);
+		const int kk = kend - p0 < KC ? kend - p0 : KC;
 		for (int p = 0; p < kk; p++) {
 			float a[R], b[R];
 			for (int u = 0; u < R; u++) a[u] = As[p][ty * R + u];
@@ -590,8 +604,11 @@ __global__ __launch_bounds__(256) void mm_tile_k(tgk_mm d, int tm, int tn)
 				for (int v = 0; v < R; v++) acc[u][v] = acc[u][v] + a[u] * b[v];
 		}
 		__syncthreads();
+		if (more) {
+			stash();
+			__syncthreads();
+		}
 	}
-	float *O = d.o + r * d.ors + g * d.og;
 	for (int u = 0; u < R; u++) {
 		const int i = i0 + ty * R + u;
 		if (i >= d.m) break;
@@ -602,18 +619,65 @@ __global__ __launch_bounds__(256) void mm_tile_k(tgk_mm d, int tm, int tn)
 	}
 }
 
+// The grid: tm x tn tiles per (batch row, group). Causal products (square
+// tiles, mode = d.causal as the launcher allows it): mode 1 enumerates only the tiles on or below the diagonal
+// (tn counts them, ti >= tj, all of equal work); mode 2 gives a block the row
+// tiles p and tm - 1 - p of one column tile (tm counts the pairs), whose sums
+// run to the end of each tile's rows, so every block has the same work.
+template <int TS>
+__global__ __launch_bounds__(256) void mm_tile_k(tgk_mm d, int tm, int tn, int nt, int mode)
+{
+	__shared__ float As[16][TS + 4]; // As[p][i]
+	__shared__ float Bs[16][TS + 4]; // Bs[p][j]
+	const int tiles = tm * tn;
+	const long rg = blockIdx.x / tiles;
+	const int t = (int)(blockIdx.x - rg * tiles);
+	const long r = rg / d.g;
+	const int g = (int)(rg - r * d.g);
+	const float *A = d.a.p + r * d.a.rs + g * d.ag, *B = d.b.p + r * d.b.rs + g * d.bg;
+	float *O = d.o + r * d.ors + g * d.og;
+	if (mode == 1) { // lower-triangle tile t: ti (ti + 1) / 2 <= t < (ti + 1) (ti + 2) / 2
+		int ti = (int)((sqrtf(8.0f * t + 1.0f) - 1.0f) * 0.5f);
+		while (ti * (ti + 1) / 2 > t) ti--;
+		while ((ti + 1) * (ti + 2) / 2 <= t) ti++;
+		const int tj = t - ti * (ti + 1) / 2;
+		mm_tile<TS>(d, A, B, O, ti * TS, tj * TS, d.k, As, Bs);
+	} else if (mode == 2) {
+		const int pr = t / tn, tj = t - pr * tn;
+		for (int h = 0; h < 2; h++) {
+			const int ti = h == 0 ? pr : nt - 1 - pr;
+			if (h == 1 && ti == pr) break; // the middle tile of an odd count
+			const int i0 = ti * TS, kend = i0 + TS < d.k ? i0 + TS : d.k;
+			mm_tile<TS>(d, A, B, O, i0, tj * TS, kend, As, Bs);
+		}
+	} else {
+		const int ti = t / tn, tj = t - ti * tn;
+		mm_tile<TS>(d, A, B, O, ti * TS, tj * TS, d.k, As, Bs);
+	}
+}
+
 void tgk_matmul_exact(hipStream_t s, const tgk_mm *d, int rows)
 {
 	long total = (long)rows * d->g * d->m * d->n;
 	if (total <= 0) return;
 	if (d->quant == 0 && (long)d->m * d->n >= 64 * 64 && d->k >= 16) {
 		const long rg = (long)rows * d->g;
+		if (d->causal == 1 && d->m == d->n) { // 64 x 64 tiles on or below the diagonal
+			const int nt = (d->m + 63) / 64, ntri = nt * (nt + 1) / 2;
+			mm_tile_k<64><<<(unsigned)(rg * ntri), 256, 0, s>>>(*d, 1, ntri, nt, 1);
+			return;
+		}
+		if (d->causal == 2) { // pairs of 64-row tiles
+			const int nt = (d->m + 63) / 64, sn = (d->n + 63) / 64;
+			mm_tile_k<64><<<(unsigned)(rg * ((nt + 1) / 2) * sn), 256, 0, s>>>(*d, (nt + 1) / 2, sn, nt, 2);
+			return;
+		}
 		const int tm = (d->m + 127) / 128, tn = (d->n + 127) / 128;
 		if (rg * tm * tn >= 1024) { // enough 128 x 128 tiles to fill the chip
-			mm_tile_k<128><<<(unsigned)(rg * tm * tn), 256, 0, s>>>(*d, tm, tn);
+			mm_tile_k<128><<<(unsigned)(rg * tm * tn), 256, 0, s>>>(*d, tm, tn, tm, 0);
 		} else {
 			const int sm = (d->m + 63) / 64, sn = (d->n + 63) / 64;
-			mm_tile_k<64><<<(unsigned)(rg * sm * sn), 256, 0, s>>>(*d, sm, sn);
+			mm_tile_k<64><<<(unsigned)(rg * sm * sn), 256, 0, s>>>(*d, sm, sn, sm, 0);
 		}
 		return;
 	}

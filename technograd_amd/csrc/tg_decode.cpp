@@ -35,7 +35,7 @@ struct tg_hip_dec {
 	std::vector<void *> allocs;
 	std::vector<tgk_qweight> ws; // every packed weight, freed at the end
 	// params
-	const float *E = nullptr, *lnf = nullptr, *cosT = nullptr, *sinT = nullptr, *dscale = nullptr;
+	const float *E = nullptr, *lnf = nullptr, *cosT = nullptr, *sinT = nullptr;
 	std::vector<const float *> ln1, ln2, qkg;
 	std::vector<int> wqkv, wgu, wd, wo; // indices into ws (wo: L x NQ)
 	std::vector<const int *> wo_codes;  // per layer: all heads' output projections for a step, int32 [NQ][HD/4][D]
@@ -46,10 +46,9 @@ struct tg_hip_dec {
 	long kv_seq = 0;
 	float *ids = nullptr, *h = nullptr, *n = nullptr, *qkv = nullptr, *hq = nullptr, *rt = nullptr;
 	float *qr = nullptr, *att = nullptr, *wout = nullptr, *gu = nullptr, *act = nullptr, *dbuf = nullptr;
-	float *sc = nullptr, *mask = nullptr, *lastn = nullptr, *logits = nullptr;
+	float *sc = nullptr, *lastn = nullptr, *logits = nullptr;
 	float *am_v = nullptr; // argmax workspace: TGK_AM_PARTS per sequence
 	int *am_i = nullptr;
-	int mask_T = 0;
 	void *scratch = nullptr;
 	size_t scratch_bytes = 0;
 };
@@ -233,32 +232,19 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 			a.qr = d->qr, a.K = d->K, a.V = d->Vc, a.att = d->att, a.kv_seq = d->kv_seq, a.kv_layer = kv_layer;
 			a.NQ = d->NQ, a.NKV = d->NKV, a.HD = d->HD, a.P = d->P, a.p = p0, a.scale = d->scale;
 			tgk_dec_attn(st, &a, S);
-		} else { // a prompt from position 0: the graph's per-head products, softmax and mask
+		} else { // a prompt from position 0: per head, the graph's products, scale, mask and softmax (causal)
 			for (int hh = 0; hh < d->NQ; hh++) {
 				const int j = hh / GRP;
 				tgk_mm m;
 				memset(&m, 0, sizeof m);
-				m.g = 1, m.m = T0, m.k = d->HD, m.n = T0;
+				m.g = 1, m.m = T0, m.k = d->HD, m.n = T0, m.causal = 1;
 				m.a = tgk_opd{ d->qr + (long)hh * d->HD, (long)T0 * d->NQ * d->HD }, m.ai = (long)d->NQ * d->HD, m.ap = 1;
 				m.b = tgk_opd{ d->K + kv_layer + (long)j * d->P * d->HD, d->kv_seq }, m.bp = 1, m.bj = d->HD;
 				m.o = d->sc, m.ors = (long)T0 * T0, m.oi = T0, m.oj = 1;
 				tgk_matmul_exact(st, &m, S);
-				tgk_ew e;
-				memset(&e, 0, sizeof e);
-				e.nin = 3, e.nout = 1, e.nins = 4;
-				e.in[0] = d->sc, e.in_rs[0] = (long)T0 * T0, e.in_mode[0] = 0;
-				e.in[1] = d->mask, e.in_rs[1] = 0, e.in_mode[1] = 0;
-				e.in[2] = d->dscale, e.in_rs[2] = 0, e.in_mode[2] = 1;
-				for (int q = 0; q < 3; q++) e.in_map[q] = nullptr, e.in_per[q] = 1, e.in_inv[q] = 1.0f;
-				e.out[0] = d->sc, e.out_rs[0] = (long)T0 * T0;
-				e.ins[0] = tgk_ew_ins{ TGK_EW_LOAD, 0, 0, 0, 0 };
-				e.ins[1] = tgk_ew_ins{ TGK_EW_BIN, TGK_MUL, 0, 2, 0 }; // scores * scale
-				e.ins[2] = tgk_ew_ins{ TGK_EW_BIN, TGK_ADD, 0, 1, 0 }; // + mask
-				e.ins[3] = tgk_ew_ins{ TGK_EW_STORE, 0, 0, 0, 0 };
-				tgk_ew_run(st, &e, T0 * T0, S);
-				tgk_rowop(st, TGM_SOFTMAX, d->sc, (long)T0 * T0, tgk_opd{ d->sc, (long)T0 * T0 }, T0, T0, S);
+				tgk_dec_causal_softmax(st, d->sc, T0, (long)S * T0, d->scale);
 				memset(&m, 0, sizeof m);
-				m.g = 1, m.m = T0, m.k = T0, m.n = d->HD;
+				m.g = 1, m.m = T0, m.k = T0, m.n = d->HD, m.causal = 2;
 				m.a = tgk_opd{ d->sc, (long)T0 * T0 }, m.ai = T0, m.ap = 1;
 				m.b = tgk_opd{ d->Vc + kv_layer + (long)j * d->P * d->HD, d->kv_seq }, m.bp = d->HD, m.bj = 1;
 				m.o = d->att + (long)hh * d->HD, m.ors = (long)T0 * d->NQ * d->HD, m.oi = (long)d->NQ * d->HD, m.oj = 1;
@@ -284,19 +270,6 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 	norm(d, 1, d->h + (long)(T0 - 1) * D, (long)T0 * D, S, d->dbuf + (long)(T0 - 1) * D, (long)T0 * D, d->lnf, d->lastn, d->wlm);
 	gemm_pre(d, d->wlm, d->lastn, D, 1, 0, S, d->logits, d->V, 0);
 	return hip_ok(hipGetLastError(), "decoder launch");
-}
-
-bool setup_mask(tg_hip_dec *d, int T0)
-{
-	if (d->mask_T == T0) return true;
-	std::vector<float> m((size_t)T0 * T0);
-	for (int i = 0; i < T0; i++)
-		for (int j = 0; j < T0; j++) m[(size_t)i * T0 + j] = j <= i ? 0.0f : -1e9f; // the importer's causal mask
-	if (!hip_ok(hipMemcpyAsync(d->mask, m.data(), m.size() * sizeof(float), hipMemcpyHostToDevice, d->st), "mask") ||
-	    !hip_ok(hipStreamSynchronize(d->st), "mask"))
-		return false;
-	d->mask_T = T0;
-	return true;
 }
 
 bool build(tg_hip_dec *d)
@@ -333,7 +306,7 @@ bool build(tg_hip_dec *d)
 	memcpy(tab.data(), m->val[vcos].data, tab.size() * sizeof(float));
 	if (!upload(d, &d->cosT, tab.data(), tab.size())) return false;
 	memcpy(tab.data(), m->val[vsin].data, tab.size() * sizeof(float));
-	if (!upload(d, &d->sinT, tab.data(), tab.size()) || !upload(d, &d->dscale, &d->scale, 1)) return false;
+	if (!upload(d, &d->sinT, tab.data(), tab.size())) return false;
 	d->ln1.resize((size_t)d->L), d->ln2.resize((size_t)d->L), d->qkg.resize((size_t)d->L);
 	for (int l = 0; l < d->L; l++) {
 		const int a = find(m, nm("ln1_%d", l)), b = find(m, nm("ln2_%d", l)), q = find(m, nm("qn_%d", l)), k = find(m, nm("kn_%d", l));
@@ -378,7 +351,7 @@ bool build(tg_hip_dec *d)
 	    !alloc(d, &d->rt, (size_t)(rows * NH * HD)) || !alloc(d, &d->qr, (size_t)(rows * d->NQ * HD)) ||
 	    !alloc(d, &d->att, (size_t)(rows * d->NQ * HD)) || !alloc(d, &d->wout, (size_t)(rows * d->NQ * d->D)) ||
 	    !alloc(d, &d->gu, (size_t)(rows * 2 * d->FF)) || !alloc(d, &d->act, (size_t)(rows * d->FF)) || !alloc(d, &d->dbuf, (size_t)(rows * d->D)) ||
-	    !alloc(d, &d->sc, (size_t)((long)d->S * d->TP * d->TP)) || !alloc(d, &d->mask, (size_t)((long)d->TP * d->TP)) ||
+	    !alloc(d, &d->sc, (size_t)((long)d->S * d->TP * d->TP)) ||
 	    !alloc(d, &d->lastn, (size_t)((long)d->S * d->D)) || !alloc(d, &d->logits, (size_t)((long)d->S * d->V)) ||
 	    !alloc(d, &d->am_v, (size_t)d->S * TGK_AM_PARTS) || !alloc(d, &d->am_i, (size_t)d->S * TGK_AM_PARTS))
 		return false;
@@ -399,6 +372,10 @@ tg_hip_dec *tg_hip_dec_create(const tg_hip_prog *p, int max_seqs, int max_prompt
 		err("tg_hip_dec_create: bad arguments");
 		return nullptr;
 	}
+	if (max_prompt > TGK_DEC_PROMPT_MAX) {
+		err("tg_hip_dec_create: prompts of at most %s%ld tokens", "", TGK_DEC_PROMPT_MAX);
+		return nullptr;
+	}
 	tg_hip_dec *d = new tg_hip_dec;
 	d->p = p, d->S = max_seqs, d->TP = max_prompt, d->P = max_len;
 	if (!build(d)) {
@@ -415,7 +392,6 @@ int tg_hip_dec_generate(tg_hip_dec *d, const float *d_prompt, int seqs, int prom
 		err("tg_hip_dec_generate: bad arguments (sequences, prompt length or steps beyond the decoder's sizes)");
 		return -1;
 	}
-	if (!setup_mask(d, prompt_len)) return -1;
 	if (!hip_ok(hipMemcpyAsync(d->ids, d_prompt, (size_t)seqs * prompt_len * sizeof(float), hipMemcpyDeviceToDevice, d->st), "prompt"))
 		return -1;
 	for (int s = 0; s < steps; s++) {

@@ -1243,7 +1243,7 @@ void exec_step(Run &R, const Step &s)
 		break;
 	case ST_UN: tgk_unary(st, s.op, dst(R, s.o), s.o.rs, resolve(R, s.a), s.n, R.rows); break;
 	case ST_MM: {
-		tgk_mm d;
+		tgk_mm d{};
 		d.g = s.g, d.m = s.m, d.k = s.k, d.n = s.nn;
 		d.a = s.quant == 1 ? tgk_opd{ nullptr, 0 } : resolve(R, s.a);
 		d.ag = s.ag, d.ai = s.ai, d.ap = s.ap;

@@ -81,6 +81,12 @@ typedef struct {
 	int quant, bits;
 	const uint8_t *codes;
 	const float *scale;
+	/* causal products of a prompt's attention (tiled path only; 0 elsewhere):
+	 * 1: o[i][j] is needed for j <= i only, tiles wholly above the diagonal
+	 * are skipped; 2: A[i][p] is an exact 0 for p > i, so a tile of rows
+	 * i0 .. i0 + TS - 1 sums p = 0 .. i0 + TS - 1 only (the omitted terms add
+	 * +0 to sums that are never -0) */
+	int causal;
 } tgk_mm;
 void tgk_matmul_exact(hipStream_t s, const tgk_mm *d, int rows);
 
@@ -187,6 +193,11 @@ void tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a);
  * values equal to the digit + matrix-core path; codes int32 [NQ][HD/4][D],
  * 4 consecutive k's int8 codes per word */
 size_t tgk_dec_wo_lds(int rows, int HD);
+/* one head's causal softmax over a prompt chunk's scores sc [lines][T0]
+ * (line L is position L % T0 of its sequence): x = s * scale + 0 and the
+ * softmax on u <= t, p = 0 above the diagonal; T0 <= TGK_DEC_PROMPT_MAX */
+#define TGK_DEC_PROMPT_MAX 4088 /* 4 lines of T0 + 4 floats in 64 KiB of LDS */
+void tgk_dec_causal_softmax(hipStream_t s, float *sc, int T0, long nlines, float scale);
 void tgk_dec_wo(hipStream_t s, const float *att, const int *codes, const float *scales, float *out, int rows, int NQ, int HD, int D);
 /* pv, pi: TGK_AM_PARTS per row of workspace (each row's parts' best) */
 #define TGK_AM_PARTS 64
