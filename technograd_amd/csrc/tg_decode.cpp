@@ -212,7 +212,7 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 	hipStream_t st = d->st;
 	tgk_take(st, d->h, (long)T0 * D, tgk_opd{ d->E, 0 }, tgk_opd{ d->ids, T0 }, T0, d->V, d->D, S);
 	for (int l = 0; l < d->L; l++) {
-		const long kv_layer = (long)l * d->NKV * d->P * d->HD;
+		const long kv_layer = (long)l * d->S * d->kv_seq; // the cache is layer-major: [layer][sequence][KV head][position][HD]
 		// h (plus the previous layer's MLP output), rmsnorm * ln1, q k v projections
 		norm(d, l == 0 ? 0 : 1, d->h, D, rows, d->dbuf, D, d->ln1[(size_t)l], d->n, d->wqkv[(size_t)l]);
 		gemm_pre(d, d->wqkv[(size_t)l], d->n, D, 1, 0, rows, d->qkv, ctot, 0);
@@ -344,8 +344,8 @@ bool build(tg_hip_dec *d)
 	if (d->wrot < 0 || d->wlm < 0) return err("decoder: cannot place Rot or the LM head");
 	// cache and buffers
 	const long rows = (long)d->S * d->TP;
-	d->kv_seq = (long)d->L * d->NKV * d->P * HD;
-	if (!alloc(d, &d->K, (size_t)(d->S * d->kv_seq)) || !alloc(d, &d->Vc, (size_t)(d->S * d->kv_seq)) || !alloc(d, &d->ids, (size_t)rows) ||
+	d->kv_seq = (long)d->NKV * d->P * HD; // one sequence's K (or V) of one layer; a layer holds S of them
+	if (!alloc(d, &d->K, (size_t)(d->L * d->S * d->kv_seq)) || !alloc(d, &d->Vc, (size_t)(d->L * d->S * d->kv_seq)) || !alloc(d, &d->ids, (size_t)rows) ||
 	    !alloc(d, &d->h, (size_t)(rows * d->D)) ||
 	    !alloc(d, &d->n, (size_t)(rows * d->D)) || !alloc(d, &d->qkv, (size_t)(rows * ctot)) || !alloc(d, &d->hq, (size_t)(rows * NH * HD)) ||
 	    !alloc(d, &d->rt, (size_t)(rows * NH * HD)) || !alloc(d, &d->qr, (size_t)(rows * d->NQ * HD)) ||

@@ -124,9 +124,10 @@ typedef struct {
 	int axis;                /* original layout: 0 = [C][K], 1 = [K][C] */
 } tgk_qweight;
 
-/* KV-cache decoder kernels (kern_decode.hip). The caches are
- * [seq][layer][kv head][position][HD] f32: kv_seq floats per sequence,
- * kv_layer the offset of the current layer. */
+/* KV-cache decoder kernels (kern_decode.hip). Element (sequence s, KV head j,
+ * position t, d) of the current layer's cache is at
+ * s kv_seq + kv_layer + (j P + t) HD + d (the decoder keeps the caches
+ * layer-major: [layer][sequence][KV head][position][HD] f32). */
 typedef struct {
 	const float *hq, *rt;    /* normed, scaled q and k lines [rows][NQ + NKV][HD], and their x @ Rot */
 	const float *qkv;        /* projection output [rows][ctot] (v after q and k) */
