@@ -89,20 +89,21 @@ __device__ inline long long wave_sum(long long v)
 	return v;
 }
 
-// inputs k0 .. k0 + 15 of a row, zero at and beyond K. The addresses are
-// clamped into the row instead of branched on, so the loads of several
-// calls can all be in flight before the first value is used. vec: unit
-// stride, 16-byte aligned row, K a multiple of 16 (whole float4s).
+// inputs k0 .. k0 + 15 of a row. The addresses are clamped into the row
+// instead of branched on, so the loads of several calls can all be in flight
+// before the first value is used. vec (unit stride, 16-byte aligned row, K a
+// multiple of 16, so whole float4s): a group at or past K reads the row's
+// first 16 inputs instead, which leave the row's max and NaN flag unchanged;
+// the caller writes such a group as zero digits (tgq_put16's `zero`).
+// Otherwise inputs at and beyond K read as zeros.
 template <bool VEC>
 __device__ inline void load16(float *v, const float *x, long xk, int k0, int K)
 {
-	const bool in = k0 < K;
 	if (VEC) {
-		const float *p = x + (in ? k0 : 0);
+		const float *p = x + (k0 < K ? k0 : 0);
 		for (int i = 0; i < 4; i++) {
 			const float4 f = *(const float4 *)(p + 4 * i);
-			v[4 * i] = in ? f.x : 0.0f, v[4 * i + 1] = in ? f.y : 0.0f;
-			v[4 * i + 2] = in ? f.z : 0.0f, v[4 * i + 3] = in ? f.w : 0.0f;
+			v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
 		}
 	} else {
 		for (int i = 0; i < 16; i++) {
@@ -128,8 +129,7 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 	const bool vec = xk == 1 && ((size_t)x & 15) == 0 && (K & 15) == 0;
 	const int nsl = (Kp + 1023) / 1024;
 	float v[SL][16];
-	float mx = 0.0f;
-	int bad = 0;
+	unsigned mb = 0; // max |x| as bits (tgq_scan16)
 	// slabs t0 .. t0 + SL - 1 into v, loads first; slabs past the row read as
 	// zeros (no branch, so every load is in flight before the first use)
 	auto fetch = [&](int t0) {
@@ -141,12 +141,12 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 	for (int t0 = 0; t0 < nsl; t0 += SL) {
 		fetch(t0);
 		for (int t = 0; t < SL; t++)
-			for (int i = 0; i < 16; i++) {
-				bad |= !isfinite(v[t][i]);
-				mx = fmaxf(mx, fabsf(v[t][i]));
-			}
+			tgq_scan16(v[t], mb);
 	}
-	const float amax = wave_max(mx); // nan never wins fmaxf; such rows are flagged by `bad`
+	float mx;
+	int bad;
+	tgq_scan_end(mb, mx, bad);
+	const float amax = wave_max(mx); // a NaN lane reads 0 here; its row is flagged by `bad`
 	const int special = tgq_special(__any(bad), amax), E = tgq_exponent(amax, special);
 	long long qs = 0;
 	int8_t *blk = tgq_row_base(s.dig, m, Kp);
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 		if (nsl > SL) fetch(t0); // rows of up to SL slabs are still in v
 		for (int t = 0; t < SL; t++) {
 			const int k0 = (t0 + t) * 1024 + lane * 16;
-			if (t0 + t < nsl && k0 < Kp) qs += tgq_put16(blk, k0, v[t], E, special);
+			if (t0 + t < nsl && k0 < Kp) qs += tgq_put16(blk, k0, v[t], E, special || k0 >= K);
 		}
 	}
 	qs = wave_sum(qs);
@@ -182,16 +182,15 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 	const float *x = xrow(a, m0 + mr < M ? m0 + mr : M - 1); // rows past M repeat row M - 1
 	const int nkb = Kp / 32;
 	float v[NKB][16];
-	float mx = 0.0f;
-	int bad = 0;
+	unsigned mb = 0; // max |x| as bits (tgq_scan16)
 	for (int j = 0; j < NKB; j++) {
 		const int kb = 2 * (w + j * W) + par;
 		load16<VEC>(v[j], x, a.xk, kb < nkb ? kb * 32 + half * 16 : K, K); // past the row: zeros
-		for (int i = 0; i < 16; i++) {
-			bad |= !isfinite(v[j][i]);
-			mx = fmaxf(mx, fabsf(v[j][i]));
-		}
+		tgq_scan16(v[j], mb);
 	}
+	float mx;
+	int bad;
+	tgq_scan_end(mb, mx, bad);
 	smx[w][lane] = mx;
 	sbad[w][lane] = bad;
 	__syncthreads();
@@ -207,7 +206,7 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 	long long qs = 0;
 	for (int j = 0; j < NKB; j++) {
 		const int kb = 2 * (w + j * W) + par;
-		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special);
+		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K);
 	}
 	sqs[w][lane] = qs;
 	__syncthreads();
@@ -234,17 +233,16 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 	const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, ng = Kp / 16;
 	const float *x = xrow(a, m);
 	float v[G][16];
-	float mx = 0.0f;
-	int bad = 0;
+	unsigned mb = 0; // max |x| as bits (tgq_scan16)
 	for (int g = 0; g < G; g++) {
 		const int j = tid + g * 256;
 		load16<VEC>(v[g], x, a.xk, j < ng ? j * 16 : K, K); // past the row: zeros
-		for (int i = 0; i < 16; i++) {
-			bad |= !isfinite(v[g][i]);
-			mx = fmaxf(mx, fabsf(v[g][i]));
-		}
+		tgq_scan16(v[g], mb);
 	}
-	mx = wave_max(mx); // nan never wins fmaxf; such rows are flagged by `bad`
+	float mx;
+	int bad;
+	tgq_scan_end(mb, mx, bad);
+	mx = wave_max(mx); // a NaN lane reads 0 here; its row is flagged by `bad`
 	bad = __any(bad);
 	if (lane == 0) smx[w] = mx, sbad[w] = bad;
 	__syncthreads();
@@ -254,7 +252,7 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 	long long qs = 0;
 	for (int g = 0; g < G; g++) {
 		const int j = tid + g * 256;
-		if (j < ng) qs += tgq_put16(blk, j * 16, v[g], E, special);
+		if (j < ng) qs += tgq_put16(blk, j * 16, v[g], E, special || j * 16 >= K);
 	}
 	qs = wave_sum(qs);
 	if (lane == 0) sqs[w] = qs;
@@ -285,17 +283,16 @@ __global__ __launch_bounds__(1024) void digits_tile_k(tgk_qgemm_args a, Scratch 
 	const float *x = xrow(a, m0 + mr < M ? m0 + mr : M - 1); // rows past M repeat row M - 1
 	const int nkb = Kp / 32;
 	float v[NKB][16];
-	float mx = 0.0f;
-	int bad = 0;
+	unsigned mb = 0; // max |x| as bits (tgq_scan16)
 	for (int j = 0; j < NKB; j++) {
 		const int kb = w + j * W;
 		load16<VEC>(v[j], x, a.xk, kb < nkb ? kb * 32 + half * 16 : K, K); // past the row: zeros
 	}
 	for (int j = 0; j < NKB; j++)
-		for (int i = 0; i < 16; i++) {
-			bad |= !isfinite(v[j][i]);
-			mx = fmaxf(mx, fabsf(v[j][i]));
-		}
+		tgq_scan16(v[j], mb);
+	float mx;
+	int bad;
+	tgq_scan_end(mb, mx, bad);
 	smx[w][lane] = mx;
 	sbad[w][lane] = bad;
 	__syncthreads();
@@ -310,7 +307,7 @@ __global__ __launch_bounds__(1024) void digits_tile_k(tgk_qgemm_args a, Scratch 
 	long long qs = 0;
 	for (int j = 0; j < NKB; j++) {
 		const int kb = w + j * W;
-		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special);
+		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K);
 	}
 	sqs[w][lane] = qs;
 	__syncthreads();
@@ -629,16 +626,20 @@ __device__ inline void touch(v2u &x) { asm volatile("" : "+v"(x)); }
 // one-row batch fetches one row of digits, and those rows' outputs are not
 // written. Past a wave's last block the loads repeat the last block (the
 // index is clamped) and the slot is not multiplied, so there is no branch
-// around a load. The waves' int64 partial sums are added in LDS and wave 0
-// writes the tile.
-template <int BITS, int NB, int W>
+// around a load. The waves' partial sums are added in one LDS area: wave 0
+// stores its sums, the other waves add theirs with LDS f64 atomics, and wave
+// 0 writes the tile. Each partial sum and every sum of them is an integer
+// below 2^48 in magnitude, so each f64 addition is exact and the total does
+// not depend on the order the atomics land in.
+template <int BITS, int NB, int W, int P = 4>
 __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int gx)
 {
-	constexpr int P = 4;                          // ring slots (blocks in flight per wave)
+	// P ring slots (blocks in flight per wave)
 	constexpr int LB = BITS == 4 ? 8 : 16;        // weight bytes per lane per block
 	constexpr int NL = 3 + NB;                    // load instructions per block
+	static_assert((P - 1) * NL < 64, "the ring's wait count must fit vmcnt");
 	typedef typename std::conditional<BITS == 4, v2u, v4i>::type bfrag;
-	__shared__ double red[(W > 1 ? W - 1 : 1) * NB * 16 * 64]; // other waves' partial sums (integers below 2^48: exact)
+	__shared__ double red[W > 1 ? NB * 16 * 64 : 1]; // the tile's sums, wave by wave
 	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int bx = blockIdx.x % gx, by = blockIdx.x / gx;
 	const int m0 = by * 32, c0 = bx * NB * 32, kblocks = w.Kp / 32;
@@ -691,27 +692,29 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 		for (int j = 0; j < NB; j++) touch(bf[u][j]);
 	}
 	if (W > 1) {
+		if (wave == 0)
+			for (int j = 0; j < NB; j++)
+				for (int v = 0; v < 16; v++) red[(j * 16 + v) * 64 + lane] = combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+		__syncthreads();
 		if (wave > 0)
 			for (int j = 0; j < NB; j++)
-				for (int v = 0; v < 16; v++)
-					red[(((wave - 1) * NB + j) * 16 + v) * 64 + lane] = combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+				for (int v = 0; v < 16; v++) atomicAdd(&red[(j * 16 + v) * 64 + lane], combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]));
 		__syncthreads();
 		if (wave != 0) return;
 	}
-	// the block's sum: integers below 2^51 in magnitude, so the f64 sum is exact
+	// the block's sum (exact, as above)
 	auto totd = [&](int j, int v) {
-		double t = combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
-		for (int u = 0; u < W - 1; u++) t += red[((u * NB + j) * 16 + v) * 64 + lane];
-		return t;
+		if constexpr (W > 1) return red[(j * 16 + v) * 64 + lane];
+		else return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
 	};
 	store_tile<NB>(a, w, s, m0, c0, lane, [&](int j, int v) { return (long long)totd(j, v); }, totd);
 }
 
-template <int BITS, int NB, int W>
+template <int BITS, int NB, int W, int P = 4>
 void launch_gemv(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
 {
 	const int gx = a->w->Cp / (32 * NB), gy = (int)round_up(a->M, 32) / 32;
-	qgemv_k<BITS, NB, W><<<gx * gy, 64 * W, 0, st>>>(*a, *a->w, s, gx);
+	qgemv_k<BITS, NB, W, P><<<gx * gy, 64 * W, 0, st>>>(*a, *a->w, s, gx);
 }
 
 template <int BITS>
@@ -834,7 +837,7 @@ tgk_qdig tgk_qgemm_digit_area(void *scratch, int M, int Kp)
 void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
 	const tgk_qweight *w = a->w;
-	if (!w || !w->w || !a->x || !scratch || a->M <= 0 || a->ni <= 0) return; /* nothing valid to launch */
+	if (!w || !w->w || !a->x || !scratch || a->M <= 0 || a->ni <= 0 || w->K <= 0) return; /* nothing valid to launch */
 	int Mp = (int)round_up(a->M, BM);
 	const Scratch s = carve(scratch, Mp, w->Kp);
 	const int nkb = w->Kp / 32, M = a->M, K = w->K;

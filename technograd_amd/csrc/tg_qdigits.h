@@ -44,25 +44,61 @@ __device__ inline int tgq_exponent(float amax, int special)
 // row m's first fragment byte in a digit area of Kp inputs per row
 __device__ inline int8_t *tgq_row_base(int8_t *dig, int m, int Kp) { return dig + (long)(m >> 5) * (Kp / 32) * 3072 + (m & 31) * 16; }
 
+// Row scan: the running max of |x| over a lane's inputs, kept as the bit
+// pattern of |x| (unsigned order is the order of magnitudes, and every NaN
+// pattern lies above +inf's 0x7f800000): two inputs per max3, no compare.
+__device__ inline void tgq_scan16(const float *v, unsigned &mb)
+{
+	for (int i = 0; i < 16; i += 2) {
+		const unsigned a = __float_as_uint(v[i]) & 0x7fffffffu, b = __float_as_uint(v[i + 1]) & 0x7fffffffu;
+		mb = max(mb, max(a, b));
+	}
+}
+
+// a lane's max |x| and NaN flag from its scan (a NaN lane's max is not used:
+// the flag makes the row special). An infinite input is not flagged here: it
+// makes max |x| infinite, which tgq_special treats as special all the same.
+__device__ inline void tgq_scan_end(unsigned mb, float &mx, int &nan)
+{
+	nan = mb > 0x7f800000u;
+	mx = nan ? 0.0f : __uint_as_float(mb);
+}
+
 // digits of 16 consecutive inputs (inputs k0 .. k0 + 15 of the row at blk)
-// into their three 16-byte chunks; zero digits when `zero`; returns the sum of q
+// into their three 16-byte chunks; zero digits when `zero`; returns the sum of q.
+// With u = q + 0x808080 (|q| <= 8355328, so 0 <= u < 2^24), byte l of u is
+// d_l + 128: the balanced digits are u's bytes with the top bit flipped. The
+// bytes of four inputs are gathered into each plane's 32-bit word with byte
+// permutes (v_perm_b32 selects bytes of a register pair: 0-3 the second
+// operand's, 4-7 the first's, 12 a zero byte).
 __device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E, bool zero)
 {
-	unsigned w0[4] = {0, 0, 0, 0}, w1[4] = {0, 0, 0, 0}, w2[4] = {0, 0, 0, 0};
+	int8_t *p = blk + (k0 >> 5) * 3072 + ((k0 >> 4) & 1) * 512;
+	if (__builtin_expect(zero, 0)) {
+		*(tgq_v4i *)p = tgq_v4i{0, 0, 0, 0};
+		*(tgq_v4i *)(p + 1024) = tgq_v4i{0, 0, 0, 0};
+		*(tgq_v4i *)(p + 2048) = tgq_v4i{0, 0, 0, 0};
+		return 0;
+	}
+	unsigned w0[4], w1[4], w2[4];
 	int qs = 0; // |sum of 16 q| < 2^27
-	if (!zero) {
-		for (int i = 0; i < 16; i++) {
-			const int q = (int)rintf(ldexpf(v[i], 23 - E)); // exact: |q| < 2^23
-			qs += q;
-			int d0, d1, d2;
-			tgq_split3(q, d0, d1, d2);
-			const int sh = (i & 3) * 8;
-			w0[i >> 2] |= (unsigned)(d0 & 255) << sh;
-			w1[i >> 2] |= (unsigned)(d1 & 255) << sh;
-			w2[i >> 2] |= (unsigned)(d2 & 255) << sh;
+	{
+		for (int g = 0; g < 4; g++) {
+			unsigned u[4];
+			for (int i = 0; i < 4; i++) {
+				const int q = (int)rintf(ldexpf(v[4 * g + i], 23 - E)); // exact: |q| < 2^23
+				qs += q;
+				u[i] = (unsigned)(q + 0x808080);
+			}
+			const unsigned t01 = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u); // u0.b0 u1.b0 u0.b1 u1.b1
+			const unsigned t23 = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u); // u2.b0 u3.b0 u2.b1 u3.b1
+			const unsigned s01 = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0602u); // u0.b2 u1.b2 0 0
+			const unsigned s23 = __builtin_amdgcn_perm(u[3], u[2], 0x06020c0cu); // 0 0 u2.b2 u3.b2
+			w0[g] = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+			w1[g] = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+			w2[g] = (s01 | s23) ^ 0x80808080u;
 		}
 	}
-	int8_t *p = blk + (k0 >> 5) * 3072 + ((k0 >> 4) & 1) * 512;
 	*(tgq_v4i *)p = tgq_v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
 	*(tgq_v4i *)(p + 1024) = tgq_v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
 	*(tgq_v4i *)(p + 2048) = tgq_v4i{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
