@@ -19,10 +19,11 @@ counter reads for the 1 GiB flush pass (512 MiB read + 512 MiB written, an
 elementwise kernel of known traffic) in the same run.
 
 The "sweep" field repeats the kernel timings per batch. Every timed call
-there follows a pass, on the same stream, that streams 1 GiB through HBM, so
-neither the 8 MiB weight nor the rows can be served from the 256 MB Infinity
-Cache, and the device is never idle while the host queues the next call (HIP
-events then time kernels, not launch latency).
+there follows a pass, on the same stream, that reads 512 MiB of other data
+(a row sum: it writes next to nothing, so no dirty lines are left to write
+back), so neither the 8 MiB weight nor the rows can be served from the 256 MB
+Infinity Cache, and the device is never idle while the host queues the next
+call (HIP events then time kernels, not launch latency).
 
 cpu_baseline: the reference's own interpreter (oracle/_ref/tgc_ref, compiled
 from the reference sources) on this host's cores over a sample of rows of the
@@ -54,6 +55,18 @@ FLUSH_ROWS, FLUSH_COLS = 2048, 65536  # the flush pass: x * c over 512 MiB in, 5
 
 def log(msg):
     print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+def evict_program(hip):
+    """sum over 2048 rows of 64 Ki floats: 512 MiB read, 8 KiB written. Run before each timed call of the
+    sweep, it leaves the Infinity Cache holding clean lines of other data, so the timed kernel reads its
+    operands from HBM without also paying for the write-back of another kernel's dirty lines."""
+    text = ("(tgir 1\n  (model evict)\n  (input x (f32 %d))\n  (block\n"
+            "    (%%0 (f32) (sum x))\n  )\n  (output %%0))\n" % FLUSH_COLS)
+    p = hip.Program(text, max_rows=FLUSH_ROWS)
+    buf_in = hip.DeviceBuffer(FLUSH_ROWS * FLUSH_COLS * 4)
+    buf_out = hip.DeviceBuffer(FLUSH_ROWS * 4)
+    return p, buf_in, buf_out
 
 
 def flush_program(hip):
@@ -538,8 +551,8 @@ def main():
     assert np.isfinite(y).all()
 
     # ---- kernel durations per batch (HIP events on the backend's stream) ----
-    fprog, fin, fout = flush_program(hip)
-    fprog.set_stream(tprog.stream())  # flush passes and timed calls in one queue
+    fprog, fin, fout = evict_program(hip)
+    fprog.set_stream(tprog.stream())  # eviction passes and timed calls in one queue
     wbytes = C * K / 2 + 4 * C
     sweep = []
     for b in BATCHES:

@@ -402,13 +402,18 @@ __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, t
 	for (int e = threadIdx.x; e < tot; e += TPB) out[e] = lds[(e / cols) * stride + e % cols];
 }
 
+// sum / mean of each row, one thread per row adding in index order (the
+// reference's sequential f32 loop); a 16-byte aligned row is read with float4
+// loads issued ahead of the adds (tg_ordered_sum), others one float at a time
 __global__ void reduce_k(int op, float *o, long ors, tgk_opd a, int n, int rows)
 {
 	int r = blockIdx.x * blockDim.x + threadIdx.x;
 	if (r >= rows) return;
 	const float *x = a.p + (long)r * a.rs;
 	float s = 0.0f;
-	for (int i = 0; i < n; i++) s += x[i];
+	if (((size_t)x & 15) == 0) s = tg_ordered_sum<4>(x, n);
+	else
+		for (int i = 0; i < n; i++) s += x[i];
 	o[(long)r * ors] = op == TGM_SUM ? s : s / (float)n;
 }
 
@@ -709,7 +714,10 @@ void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, i
 
 void tgk_reduce(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows)
 {
-	if (rows > 0) reduce_k<<<blocks_for(rows), TPB, 0, s>>>(op, o, ors, a, n, rows);
+	// one wave per block while that leaves fewer than 1024 blocks: long rows
+	// then spread over more compute units (each thread's adds are sequential)
+	const int tpb = rows < 1024 * 64 ? 64 : TPB;
+	if (rows > 0) reduce_k<<<(unsigned)((rows + tpb - 1) / tpb), tpb, 0, s>>>(op, o, ors, a, n, rows);
 }
 
 void tgk_transpose(hipStream_t s, float *o, long ors, tgk_opd a, int g, int r, int c, int rows)
