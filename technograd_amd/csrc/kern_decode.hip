@@ -109,7 +109,9 @@ __global__ __launch_bounds__(ATT_TPB) void dec_attn_k(tgk_dec_attn_args a, int c
 			sc[g * nst + c0 + kk] = acc * a.scale + 0.0f;
 		}
 	}
-	__syncthreads();
+	__syncthreads(); // the score chains are done with kv
+	stash();         // V's first chunk (fetched during the last K chunk) into kv,
+	if (ck < n) fetch(V, ck); // and its second in flight, both during the softmax
 	const int wave = tid >> 6, lane = tid & 63;
 	for (int g = wave; g < GRP; g += ATT_TPB >> 6) { // max: a wave per query head
 		const float *r = sc + g * nst;
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(ATT_TPB) void dec_attn_k(tgk_dec_attn_args a, int c
 		if (e - g * nst < n) sc[e] = expf(sc[e] - lv[g]);
 	}
 	__syncthreads();
-	if (tid < GRP) lv[tid] = tg_ordered_sum<4>(sc + tid * nst, n);
+	if (tid < GRP) lv[tid] = tg_ordered_sum_pp<6>(sc + tid * nst, n);
 	__syncthreads();
 	for (int e = tid; e < GRP * nst; e += ATT_TPB) {
 		const int g = e / nst;
@@ -135,9 +137,11 @@ __global__ __launch_bounds__(ATT_TPB) void dec_attn_k(tgk_dec_attn_args a, int c
 	for (int u = 0; u < OI; u++) acc[u] = 0.0f;
 	for (int c0 = 0; c0 < n; c0 += ck) {
 		__syncthreads(); // probabilities final; the previous chunk's chains are done with kv
-		stash();
-		__syncthreads();
-		if (c0 + ck < n) fetch(V, c0 + ck);
+		if (c0 > 0) {    // (the first chunk is in kv already)
+			stash();
+			__syncthreads();
+			if (c0 + ck < n) fetch(V, c0 + ck);
+		}
 		const int m = min(ck, n - c0);
 		const float *vb = (const float *)kv;
 		for (int u = 0; u < OI; u++) {
@@ -362,7 +366,7 @@ __global__ __launch_bounds__(NORM_TPB) void dec_norm_k(tgk_dec_norm_args a)
 		sq[i] = v[u] * v[u];
 	}
 	__syncthreads();
-	if (tid == 0) inv_s = 1.0f / sqrtf(tg_ordered_sum<8>(sq, D) / (float)D + 1e-6f);
+	if (tid == 0) inv_s = 1.0f / sqrtf(tg_ordered_sum_pp<6>(sq, D) / (float)D + 1e-6f);
 	__syncthreads();
 	const float inv = inv_s;
 	float mx = 0.0f;
@@ -400,7 +404,7 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 	__builtin_amdgcn_wave_barrier();
 	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 	float inv = 0.0f;
-	if (lane == 0) inv = 1.0f / sqrtf(tg_ordered_sum<8>(sq, HD) / (float)HD + 1e-6f);
+	if (lane == 0) inv = 1.0f / sqrtf(tg_ordered_sum_pp<6>(sq, HD) / (float)HD + 1e-6f);
 	inv = __shfl(inv, 0);
 	float mx = 0.0f;
 	int bad = 0;
@@ -512,7 +516,7 @@ __global__ __launch_bounds__(NL_TPB) void norm_lines_k(NormLines a)
 		z[l * ZS + i] = in ? v[u] * v[u] : 0.0f;
 	}
 	__syncthreads();
-	if (tid < R && L0 + tid < a.lines) linv[tid] = 1.0f / sqrtf(tg_ordered_sum<8>(z + tid * ZS, D) / (float)D + 1e-6f);
+	if (tid < R && L0 + tid < a.lines) linv[tid] = 1.0f / sqrtf(tg_ordered_sum_pp<6>(z + tid * ZS, D) / (float)D + 1e-6f);
 	__syncthreads();
 	{
 		float gv[NL_EPT]; // the gains, all loaded before the first is used
@@ -628,7 +632,7 @@ __global__ __launch_bounds__(256) void causal_softmax_k(float *sc, int T0, long 
 		for (int u = tid; u <= t; u += 256) z[ll * stride + u] = expf(z[ll * stride + u] - lv[ll]);
 	}
 	__syncthreads();
-	if (tid < nl) lv[tid] = tg_ordered_sum<8>(z + tid * stride, pos(tid) + 1);
+	if (tid < nl) lv[tid] = tg_ordered_sum_pp<6>(z + tid * stride, pos(tid) + 1);
 	__syncthreads();
 	for (int ll = 0; ll < nl; ll++) {
 		const int t = pos(ll);

@@ -336,7 +336,7 @@ __global__ void rowop_k(int op, float *o, long ors, tgk_opd a, int nrow, int col
 // after another (tg_ordered_sum when the line is 16-byte aligned)
 __device__ inline float line_sum(const float *z, int cols)
 {
-	if ((((size_t)z) & 15) == 0) return tg_ordered_sum<8>(z, cols);
+	if ((((size_t)z) & 15) == 0) return tg_ordered_sum_pp<6>(z, cols);
 	float sum = 0.0f;
 	for (int i = 0; i < cols; i++) sum += z[i];
 	return sum;
@@ -411,7 +411,7 @@ __global__ void reduce_k(int op, float *o, long ors, tgk_opd a, int n, int rows)
 	if (r >= rows) return;
 	const float *x = a.p + (long)r * a.rs;
 	float s = 0.0f;
-	if (((size_t)x & 15) == 0) s = tg_ordered_sum<4>(x, n);
+	if (((size_t)x & 15) == 0) s = tg_ordered_sum_pp<6>(x, n);
 	else
 		for (int i = 0; i < n; i++) s += x[i];
 	o[(long)r * ors] = op == TGM_SUM ? s : s / (float)n;

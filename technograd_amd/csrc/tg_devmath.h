@@ -90,4 +90,50 @@ template <int NB> __device__ __attribute__((always_inline)) inline float tg_orde
 	}
 	return sum;
 }
+
+// The same sum for a single long chain whose loads would otherwise wait on
+// each other: values go through two register buffers of 4 V in turn, the
+// next buffer's 16-byte loads in flight while the current one's adds run (no
+// copy between the buffers, so nothing waits for the loads just issued).
+template <int V> __device__ __attribute__((always_inline)) inline float tg_ordered_sum_pp(const float *z, int n)
+{
+	constexpr int W = 4 * V; // values per buffer
+	const float4 *z4 = (const float4 *)z;
+	const int nb = n / W; // whole buffers
+	float sum = 0.0f;
+	float4 A[V], B[V];
+	auto add = [&](const float4 *v) {
+#pragma unroll
+		for (int j = 0; j < V; j++) {
+			sum += v[j].x;
+			sum += v[j].y;
+			sum += v[j].z;
+			sum += v[j].w;
+		}
+	};
+	if (nb > 0)
+#pragma unroll
+		for (int j = 0; j < V; j++) A[j] = z4[j];
+	int b = 0;
+	for (; b + 1 < nb; b += 2) {
+#pragma unroll
+		for (int j = 0; j < V; j++) B[j] = z4[(b + 1) * V + j];
+		add(A);
+		if (b + 2 < nb)
+#pragma unroll
+			for (int j = 0; j < V; j++) A[j] = z4[(b + 2) * V + j];
+		add(B);
+	}
+	if (b < nb) add(A); // an odd buffer count ends in A
+	const int i = nb * W;
+	if (i < n) { // fewer than W left: load them all, then add in order
+		float t[W];
+#pragma unroll
+		for (int k = 0; k < W; k++) t[k] = z[i + k < n ? i + k : n - 1];
+#pragma unroll
+		for (int k = 0; k < W; k++)
+			if (i + k < n) sum += t[k];
+	}
+	return sum;
+}
 #endif
