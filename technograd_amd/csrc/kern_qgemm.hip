@@ -395,22 +395,53 @@ __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 // special row (the common case) takes a straight-line path that reads each
 // row's exponent and sum once and each column's scale once; otherwise every
 // output goes through epilogue().
-template <int NB, class Tot, class TotD>
-__device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int mbase, int cbase, int lane,
-				  Tot tot, TotD totd)
-{
-	const int r32 = lane & 31, h = lane >> 5;
-	// Lane l fetches row mbase + l % 32's exponent, sum of q and flag, and the
-	// scales of its columns, all in one round trip; a lane's 16 rows then come
-	// from the lanes that hold them (shuffles), not from 16 dependent loads.
-	const int mr = mbase + r32, mrc = mr < a.M ? mr : a.M - 1;
-	const int Er = s.e[mrc], spr = mr < a.M ? s.special[mrc] : 0;
-	const long long Qr = w.bits == 4 ? s.qsum[mrc] : 0;
+// What a lane's epilogue reads besides its sums: row mbase + lane % 32's
+// exponent, sum of q and special flag, and the scales of its columns, all in
+// one round trip; a lane's 16 rows then come from the lanes that hold them
+// (shuffles), not from 16 dependent loads. A kernel may fetch it before its
+// K loop, so that the loads' latency is hidden behind the loop.
+template <int NB>
+struct TileRows {
+	int Er, spr;
+	long long Qr;
 	float sc[NB];
+};
+template <int NB>
+__device__ inline TileRows<NB> tile_rows(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int mbase, int cbase, int lane)
+{
+	TileRows<NB> t;
+	const int r32 = lane & 31, mr = mbase + r32, mrc = mr < a.M ? mr : a.M - 1;
+	t.Er = s.e[mrc];
+	t.spr = mr < a.M ? s.special[mrc] : 0;
+	t.Qr = w.bits == 4 ? s.qsum[mrc] : 0;
 	for (int j = 0; j < NB; j++) {
 		const int c = cbase + j * 32 + r32;
-		sc[j] = w.scale[c < w.Cp ? c : 0]; // scales are padded to Cp; columns at or beyond C are not written
+		t.sc[j] = w.scale[c < w.Cp ? c : 0]; // scales are padded to Cp; columns at or beyond C are not written
 	}
+	return t;
+}
+
+// HOIST: take all 16 rows' exponents and sums of q from their lanes before the
+// first store (the shuffles then wait once, not once per row; 48 more live
+// registers, for kernels that have them free at the epilogue).
+template <int NB, bool HOIST, class Tot, class TotD>
+__device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int mbase, int cbase, int lane,
+				  const TileRows<NB> &t, Tot tot, TotD totd)
+{
+	const int r32 = lane & 31, h = lane >> 5;
+	const int Er = t.Er, spr = t.spr;
+	const long long Qr = t.Qr;
+	const float *sc = t.sc;
+	int Ev[HOIST ? 16 : 1];
+	long long Qv[HOIST ? 16 : 1];
+	if constexpr (HOIST)
+		for (int v = 0; v < 16; v++) {
+			const int rv = 8 * (v >> 2) + 4 * h + (v & 3);
+			Ev[v] = __shfl(Er, rv);
+			Qv[v] = __shfl(Qr, rv);
+		}
+	auto row_e = [&](int v, int rv) { if constexpr (HOIST) return Ev[v]; else return __shfl(Er, rv); };
+	auto row_q = [&](int v, int rv) { if constexpr (HOIST) return Qv[v]; else return __shfl(Qr, rv); };
 	if (__any(spr)) {
 		for (int j = 0; j < NB; j++)
 			for (int v = 0; v < 16; v++) epilogue(a, w, s, mbase + 8 * (v >> 2) + 4 * h + (v & 3), cbase + j * 32 + r32, tot(j, v));
@@ -424,8 +455,8 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 		}
 		for (int v = 0; v < 16; v++) {
 			const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
-			const int E = __shfl(Er, rv);
-			const double q8 = 8.0 * (double)__shfl(Qr, rv); // 0 for int8 weights
+			const int E = row_e(v, rv);
+			const double q8 = 8.0 * (double)row_q(v, rv); // 0 for int8 weights
 			if (m >= a.M) continue;
 			int r = m, jj = 0;
 			if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
@@ -440,9 +471,9 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 	for (int j = 0; j < NB; j++) coff[j] = (long)(cbase + j * 32 + r32) * a.oc;
 	for (int v = 0; v < 16; v++) {
 		const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
-		const int E = __shfl(Er, rv);
+		const int E = row_e(v, rv);
 		// f64 arithmetic on integers below 2^53: (double)(tot - 8 qsum) exactly
-		const double q8 = 8.0 * (double)__shfl(Qr, rv); // 0 for int8 weights
+		const double q8 = 8.0 * (double)row_q(v, rv); // 0 for int8 weights
 		if (m >= a.M) continue;
 		int r = m, jj = 0;
 		if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
@@ -595,8 +626,9 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 		bar();
 	}
 	if (g == 0) bar(); // both groups pass the same number of barriers
-	store_tile<4>(
-		a, w, s, m0 + wm * 32, c0 + g * 128, lane, [&](int j, int v) { return combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]); },
+	store_tile<4, false>(
+		a, w, s, m0 + wm * 32, c0 + g * 128, lane, tile_rows<4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane),
+		[&](int j, int v) { return combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]); },
 		[&](int j, int v) { return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]); });
 }
 
@@ -666,6 +698,11 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 		}
 	};
 	for (int u = 0; u < P; u++) load(u, u);
+	// the epilogue's row data, fetched now for the narrow tiles (its latency
+	// then hides behind the K loop; the wide tiles keep the registers)
+	constexpr bool PRE = NB <= 2;
+	TileRows<NB> rows;
+	if constexpr (PRE) rows = tile_rows<NB>(a, w, s, m0, c0, lane);
 	for (int i0 = 0; i0 < n; i0 += P) {
 		for (int u = 0; u < P; u++) {
 			wait_vm<(P - 1) * NL>(); // slot u's loads are the oldest P - 1 groups back
@@ -707,7 +744,8 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 		if constexpr (W > 1) return red[(j * 16 + v) * 64 + lane];
 		else return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
 	};
-	store_tile<NB>(a, w, s, m0, c0, lane, [&](int j, int v) { return (long long)totd(j, v); }, totd);
+	if constexpr (!PRE) rows = tile_rows<NB>(a, w, s, m0, c0, lane);
+	store_tile<NB, true>(a, w, s, m0, c0, lane, rows, [&](int j, int v) { return (long long)totd(j, v); }, totd);
 }
 
 template <int BITS, int NB, int W, int P = 4>
