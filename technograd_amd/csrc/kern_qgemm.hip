@@ -658,11 +658,11 @@ __device__ inline void touch(v2u &x) { asm volatile("" : "+v"(x)); }
 // one-row batch fetches one row of digits, and those rows' outputs are not
 // written. Past a wave's last block the loads repeat the last block (the
 // index is clamped) and the slot is not multiplied, so there is no branch
-// around a load. The waves' partial sums are added in one LDS area: wave 0
-// stores its sums, the other waves add theirs with LDS f64 atomics, and wave
-// 0 writes the tile. Each partial sum and every sum of them is an integer
-// below 2^48 in magnitude, so each f64 addition is exact and the total does
-// not depend on the order the atomics land in.
+// around a load. The first min(NB, W) waves write the tile's column blocks
+// (each wave's share of the epilogue runs beside the others'); every wave
+// leaves its partial sums in LDS and each writer adds its blocks' W partial
+// sums. Each partial sum and every sum of them is an integer below 2^48 in
+// magnitude, so each f64 addition is exact.
 template <int BITS, int NB, int W, int P = 4>
 __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int gx)
 {
@@ -671,7 +671,7 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 	constexpr int NL = 3 + NB;                    // load instructions per block
 	static_assert((P - 1) * NL < 64, "the ring's wait count must fit vmcnt");
 	typedef typename std::conditional<BITS == 4, v2u, v4i>::type bfrag;
-	__shared__ double red[W > 1 ? NB * 16 * 64 : 1]; // the tile's sums, wave by wave
+	__shared__ double red[W > 1 ? NB * W * 16 * 64 : 1]; // every wave's sums of every column block
 	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 	const int bx = blockIdx.x % gx, by = blockIdx.x / gx;
 	const int m0 = by * 32, c0 = bx * NB * 32, kblocks = w.Kp / 32;
@@ -698,11 +698,16 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 		}
 	};
 	for (int u = 0; u < P; u++) load(u, u);
-	// the epilogue's row data, fetched now for the narrow tiles (its latency
-	// then hides behind the K loop; the wide tiles keep the registers)
+	// The tile's outputs are written by min(NB, W) waves, NBW column blocks
+	// each (wave w blocks w NBW ..). Their row data are fetched now for the
+	// narrow tiles (the latency then hides behind the K loop; the wide tiles
+	// keep the registers).
+	constexpr int NBW = W >= NB ? 1 : NB / W;
+	const bool writer = wave < (W >= NB ? NB : W);
+	const int jw = wave * NBW;
 	constexpr bool PRE = NB <= 2;
-	TileRows<NB> rows;
-	if constexpr (PRE) rows = tile_rows<NB>(a, w, s, m0, c0, lane);
+	TileRows<NBW> rows;
+	if constexpr (PRE) rows = tile_rows<NBW>(a, w, s, m0, c0 + 32 * jw, lane);
 	for (int i0 = 0; i0 < n; i0 += P) {
 		for (int u = 0; u < P; u++) {
 			wait_vm<(P - 1) * NL>(); // slot u's loads are the oldest P - 1 groups back
@@ -728,24 +733,23 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 		for (int l = 0; l < 3; l++) touch(af[u][l]);
 		for (int j = 0; j < NB; j++) touch(bf[u][j]);
 	}
-	if (W > 1) {
-		if (wave == 0)
-			for (int j = 0; j < NB; j++)
-				for (int v = 0; v < 16; v++) red[(j * 16 + v) * 64 + lane] = combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+	if (W > 1) { // slot (column block j, wave u): red[((j W + u) 16 + v) 64 + lane]
+		for (int j = 0; j < NB; j++)
+			for (int v = 0; v < 16; v++) red[((j * W + wave) * 16 + v) * 64 + lane] = combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
 		__syncthreads();
-		if (wave > 0)
-			for (int j = 0; j < NB; j++)
-				for (int v = 0; v < 16; v++) atomicAdd(&red[(j * 16 + v) * 64 + lane], combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]));
-		__syncthreads();
-		if (wave != 0) return;
+		if (!writer) return;
 	}
-	// the block's sum (exact, as above)
+	// the block's sum of this wave's column block jw + j (exact, as above)
 	auto totd = [&](int j, int v) {
-		if constexpr (W > 1) return red[(j * 16 + v) * 64 + lane];
-		else return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+		if constexpr (W > 1) {
+			double t = 0.0;
+			for (int u = 0; u < W; u++) t += red[(((jw + j) * W + u) * 16 + v) * 64 + lane];
+			return t;
+		} else
+			return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
 	};
-	if constexpr (!PRE) rows = tile_rows<NB>(a, w, s, m0, c0, lane);
-	store_tile<NB, true>(a, w, s, m0, c0, lane, rows, [&](int j, int v) { return (long long)totd(j, v); }, totd);
+	if constexpr (!PRE) rows = tile_rows<NBW>(a, w, s, m0, c0 + 32 * jw, lane);
+	store_tile<NBW, true>(a, w, s, m0, c0 + 32 * jw, lane, rows, [&](int j, int v) { return (long long)totd(j, v); }, totd);
 }
 
 template <int BITS, int NB, int W, int P = 4>
@@ -767,7 +771,8 @@ void launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 	}
 	// up to 64 rows, or too few tiles: 32 x (32 NB) tiles, NB as large as
 	// still fills the device; W waves split K, about 16 32-input blocks each
-	// (each further wave adds partial sums for the epilogue to read)
+	// for the wider tiles and 8-32 for one-block-wide ones (measured: at one
+	// block wide, four waves beat eight at K = 4096 and two at K = 1024)
 	const int kb = w->Kp / 32;
 	if (rt * cb / 4 >= 256) {
 		if (kb >= 128) launch_gemv<BITS, 4, 4>(st, a, s);
@@ -778,9 +783,9 @@ void launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 		else if (kb >= 64) launch_gemv<BITS, 2, 2>(st, a, s);
 		else launch_gemv<BITS, 2, 1>(st, a, s);
 	} else {
-		if (kb >= 128) launch_gemv<BITS, 1, 8>(st, a, s);
-		else if (kb >= 64) launch_gemv<BITS, 1, 4>(st, a, s);
-		else if (kb >= 32) launch_gemv<BITS, 1, 2>(st, a, s);
+		if (kb >= 256) launch_gemv<BITS, 1, 8>(st, a, s);
+		else if (kb >= 32) launch_gemv<BITS, 1, 4>(st, a, s);
+		else if (kb >= 16) launch_gemv<BITS, 1, 2>(st, a, s);
 		else launch_gemv<BITS, 1, 1>(st, a, s);
 	}
 }
