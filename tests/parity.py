@@ -60,3 +60,25 @@ def check_model(gpu, ref, row_atol=2e-6):
     ok = strict_ok(gpu, ref) | (np.abs(g - r) <= floor)
     assert ok.all(), "f32 outputs outside tolerance: worst %g at %s" % (
         np.nanmax(np.abs(g - r)), np.argwhere(~ok)[:5].tolist())
+
+
+def digit_path_matmul(x_mk, codes_kc, scale_c):
+    """The matrix-core path's arithmetic, restated on the host (not the
+    reference's order): per row, E from max |x| (frexp; raised by one when
+    rint(max |x| 2^(23-E)) > 8355328), q = rint(x 2^(23-E)) exactly, the exact
+    integer sum t = sum_k code[k, c] q[m, k], then f32(t 2^(E-23)) * s[c] in
+    f32. Rows with a NaN or max |x| above 2^100 (inf included) are special:
+    the device runs the reference's loop for them; they are returned masked.
+    Returns (f32 [M, C], special [M])."""
+    x = np.asarray(x_mk, np.float32)
+    amax = np.abs(x).max(axis=1)
+    special = np.isnan(x).any(axis=1) | (amax > np.float32(2.0 ** 100))
+    _, E = np.frexp(np.where(special, 0, amax).astype(np.float64))
+    E = np.where(amax > 0, E, 0).astype(np.int64)
+    top = np.rint(np.ldexp(np.where(special, 0, amax).astype(np.float64), 23 - E))
+    E = np.where((top > 8355328) & ~special, E + 1, E)
+    xs = np.where(special[:, None], 0, x).astype(np.float64)
+    q = np.rint(np.ldexp(xs, (23 - E)[:, None]))                        # exact integers, |q| < 2^23
+    t = q @ np.asarray(codes_kc, np.float64)                              # exact: every partial sum < 2^53
+    v = np.ldexp(t, (E - 23)[:, None]).astype(np.float32)                 # one rounding to f32
+    return (v * np.asarray(scale_c, np.float32)[None, :]).astype(np.float32), special

@@ -1,0 +1,54 @@
+"""Every launch shape of the matrix-core path (technograd_amd/csrc/kern_qgemm.hip,
+launch_gemm): the large-batch LDS kernel and each (NB column blocks, W waves)
+instantiation of the small-batch kernel, int4 and int8 weights, checked bit
+for bit against the path's own arithmetic restated on the host
+(tests/parity.py: digit_path_matmul). The reference-order parity of the same
+entry point is in test_gpu_parity.py."""
+import numpy as np
+import pytest
+
+from parity import digit_path_matmul
+
+pytestmark = pytest.mark.gpu
+
+# (bits, M rows, K inputs, C channels): the comment names the kernel launch_gemm picks
+SHAPES = [
+    (4, 1024, 256, 4096),  # qgemm_k: 128 x 256 tiles, 128 of them
+    (8, 1024, 320, 4096),  # qgemm_k, int8 weights, K not a multiple of 64
+    (4, 256, 4096, 4096),  # qgemv_k NB=4 W=4
+    (4, 256, 2048, 4096),  # NB=4 W=2
+    (8, 256, 512, 4096),   # NB=4 W=1
+    (4, 128, 4096, 4096),  # NB=2 W=4
+    (8, 128, 2048, 4096),  # NB=2 W=2
+    (4, 100, 256, 4096),   # NB=2 W=1, rows not a multiple of 32
+    (4, 16, 8192, 4096),   # NB=1 W=8
+    (8, 16, 1024, 4096),   # NB=1 W=4
+    (4, 3, 640, 4096),     # NB=1 W=2
+    (4, 1, 256, 4096),     # NB=1 W=1
+    (4, 64, 1024, 1000),   # NB=1, channels not a multiple of 32
+]
+
+
+@pytest.mark.parametrize("bits_,M,K,C", SHAPES)
+def test_launch_shape_bit_exact(bits_, M, K, C):
+    from technograd_amd import hip
+    print("case launch shape", bits_, M, K, C, flush=True)
+    rng = np.random.default_rng(M * 131 + K * 7 + C + bits_)
+    lim = 127 if bits_ == 8 else 7
+    codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)  # x @ W: W [K][C], axis 1
+    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
+    if bits_ == 4:
+        flat = codes.ravel().astype(np.int64)
+        if flat.size % 2:
+            flat = np.concatenate([flat, [0]])
+        packed = ((flat[0::2] & 15) | ((flat[1::2] & 15) << 4)).astype(np.uint8).view(np.int8)
+    else:
+        packed = codes.ravel()
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    x[0, : min(K, 5)] *= 1e3  # rows of different magnitudes: different exponents per row
+    if M > 2:
+        x[2] *= 1e-30
+    got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
+    want, special = digit_path_matmul(x, codes, scales)
+    assert not special.any()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.argwhere(got != want)[:5].tolist()
