@@ -55,6 +55,28 @@ __device__ inline void tgq_scan16(const float *v, unsigned &mb)
 	}
 }
 
+// the same over 4 inputs
+__device__ inline void tgq_scan16_4(const float *v, unsigned &mb)
+{
+	for (int i = 0; i < 4; i += 2) {
+		const unsigned a = __float_as_uint(v[i]) & 0x7fffffffu, b = __float_as_uint(v[i + 1]) & 0x7fffffffu;
+		mb = max(mb, max(a, b));
+	}
+}
+
+// four inputs' u = q + 0x808080 -> their digit bytes in the three plane words
+// (byte i of plane l's word: d_l of input i; the layout tgq_put16 writes)
+__device__ inline void tgq_pack4(const unsigned *u, unsigned &w0, unsigned &w1, unsigned &w2)
+{
+	const unsigned t01 = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u); // u0.b0 u1.b0 u0.b1 u1.b1
+	const unsigned t23 = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u); // u2.b0 u3.b0 u2.b1 u3.b1
+	const unsigned s01 = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0602u); // u0.b2 u1.b2 0 0
+	const unsigned s23 = __builtin_amdgcn_perm(u[3], u[2], 0x06020c0cu); // 0 0 u2.b2 u3.b2
+	w0 = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
+	w1 = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
+	w2 = (s01 | s23) ^ 0x80808080u;
+}
+
 // a lane's max |x| and NaN flag from its scan (a NaN lane's max is not used:
 // the flag makes the row special). An infinite input is not flagged here: it
 // makes max |x| infinite, which tgq_special treats as special all the same.
@@ -90,13 +112,7 @@ __device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E
 				qs += q;
 				u[i] = (unsigned)(q + 0x808080);
 			}
-			const unsigned t01 = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u); // u0.b0 u1.b0 u0.b1 u1.b1
-			const unsigned t23 = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u); // u2.b0 u3.b0 u2.b1 u3.b1
-			const unsigned s01 = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0602u); // u0.b2 u1.b2 0 0
-			const unsigned s23 = __builtin_amdgcn_perm(u[3], u[2], 0x06020c0cu); // 0 0 u2.b2 u3.b2
-			w0[g] = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;
-			w1[g] = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;
-			w2[g] = (s01 | s23) ^ 0x80808080u;
+			tgq_pack4(u, w0[g], w1[g], w2[g]);
 		}
 	}
 	*(tgq_v4i *)p = tgq_v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
