@@ -190,43 +190,27 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 		const int t = e / H4;
 		return *(const float4 *)(att + ((long)t * NQ + g) * HD + 4 * (e - t * H4));
 	};
-	// rows' max |x| (as bits: non-negative floats order as their bits) and NaN
-	// flags. A row's H4 items sit in consecutive lanes; when H4 is a power of
-	// two (at most 64), each wave first reduces its lanes' maxima per row with
-	// shuffles and one lane per row updates LDS, else every lane does.
+	// rows' max |x| (as bits: non-negative floats order as their bits) and flags
 	unsigned *mxb = (unsigned *)Es;
 	for (int t = tid; t < rows; t += WO_TPB) mxb[t] = 0, sp[t] = 0;
 	for (int e = tid; e < H4 * 64; e += WO_TPB) {
 		const int k4 = e >> 6, c = e & 63;
 		ct[e] = c0 + c < D ? codes[((long)g * H4 + k4) * D + c0 + c] : 0;
 	}
-	constexpr int NX = 8; // items held in registers for both passes when n <= NX * WO_TPB
-	float4 u[NX];
-	const bool held = n <= NX * WO_TPB;
-	if (held)
-		for (int j = 0; j < NX; j++) u[j] = xat(min(tid + j * WO_TPB, n - 1));
 	__syncthreads();
-	const int seg = (H4 & (H4 - 1)) == 0 ? H4 : 1; // lanes per row segment (H4 <= 64)
-	for (int b = 0; b < n; b += NX * WO_TPB)
-		for (int j = 0; j < NX; j++) {
-			const int e0 = b + j * WO_TPB, e = e0 + tid; // e0 is a multiple of 64: segments align with waves
-			if (e0 >= n) break;
-			const float4 v = held ? u[j] : xat(min(e, n - 1));
-			unsigned m = 0;
-			int nan = 0;
-			if (e < n) {
-				const float xs[4] = { v.x, v.y, v.z, v.w };
-				tgq_scan16_4(xs, m);
-				nan = m > 0x7f800000u;
-			}
-			for (int o = 1; o < seg; o <<= 1) m = max(m, (unsigned)__shfl_xor((int)m, o));
-			const unsigned long long anynan = __ballot(nan);
-			if ((lane & (seg - 1)) == 0 && e < n) {
-				const unsigned long long mask = (seg == 64 ? ~0ull : ((1ull << seg) - 1)) << lane;
-				if (m > 0x7f800000u || (anynan & mask)) atomicOr(&sp[e / H4], 1);
-				else atomicMax(&mxb[e / H4], m);
-			}
+	for (int b = tid; b < n; b += U * WO_TPB) {
+		float4 u[U];
+		for (int j = 0; j < U; j++) u[j] = xat(min(b + j * WO_TPB, n - 1));
+		for (int j = 0; j < U; j++) {
+			const int e = b + j * WO_TPB;
+			if (e >= n) continue;
+			const float4 v = u[j];
+			const int bad = !isfinite(v.x) || !isfinite(v.y) || !isfinite(v.z) || !isfinite(v.w);
+			const float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); // a nan never wins fmaxf
+			atomicMax(&mxb[e / H4], __float_as_uint(m));
+			if (bad) atomicOr(&sp[e / H4], 1);
 		}
+	}
 	__syncthreads();
 	for (int t = tid; t < rows; t += WO_TPB) {
 		const float mx = __uint_as_float(mxb[t]);
@@ -234,22 +218,27 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 		Es[t] = tgq_exponent(mx, special), sp[t] = special;
 	}
 	__syncthreads();
-	for (int b = 0; b < n; b += NX * WO_TPB)
-		for (int j = 0; j < NX; j++) {
-			const int e = b + j * WO_TPB + tid;
-			if (b + j * WO_TPB >= n) break;
+	for (int b = tid; b < n; b += U * WO_TPB) {
+		float4 u[U];
+		for (int j = 0; j < U; j++) u[j] = xat(min(b + j * WO_TPB, n - 1));
+		for (int j = 0; j < U; j++) {
+			const int e = b + j * WO_TPB;
 			if (e >= n) continue;
-			const float4 v = held ? u[j] : xat(e);
 			const int t = e / H4, E = Es[t];
+			const float xv[4] = { u[j].x, u[j].y, u[j].z, u[j].w };
 			unsigned w0 = 0, w1 = 0, w2 = 0;
-			if (!sp[t]) {
-				unsigned q[4];
-				const float xv[4] = { v.x, v.y, v.z, v.w };
-				for (int i = 0; i < 4; i++) q[i] = (unsigned)((int)rintf(ldexpf(xv[i], 23 - E)) + 0x808080); // exact: |q| < 2^23
-				tgq_pack4(q, w0, w1, w2);
-			}
+			if (!sp[t])
+				for (int i = 0; i < 4; i++) {
+					const int q = (int)rintf(ldexpf(xv[i], 23 - E)); // exact: |q| < 2^23
+					int d0, d1, d2;
+					tgq_split3(q, d0, d1, d2);
+					w0 |= (unsigned)(d0 & 255) << (8 * i);
+					w1 |= (unsigned)(d1 & 255) << (8 * i);
+					w2 |= (unsigned)(d2 & 255) << (8 * i);
+				}
 			dg[e] = make_int4((int)w0, (int)w1, (int)w2, 0);
 		}
+	}
 	__syncthreads();
 	const int c = lane;
 	if (c0 + c >= D) return;
@@ -377,7 +366,7 @@ __global__ __launch_bounds__(NORM_TPB) void dec_norm_k(tgk_dec_norm_args a)
 		sq[i] = v[u] * v[u];
 	}
 	__syncthreads();
-	if (tid == 0) inv_s = 1.0f / sqrtf(tg_ordered_sum_pp<6>(sq, D) / (float)D + 1e-6f);
+	if (tid == 0) inv_s = 1.0f / sqrtf(tg_ordered_sum<8>(sq, D) / (float)D + 1e-6f);
 	__syncthreads();
 	const float inv = inv_s;
 	float mx = 0.0f;
@@ -415,7 +404,7 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 	__builtin_amdgcn_wave_barrier();
 	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 	float inv = 0.0f;
-	if (lane == 0) inv = 1.0f / sqrtf(tg_ordered_sum_pp<6>(sq, HD) / (float)HD + 1e-6f);
+	if (lane == 0) inv = 1.0f / sqrtf(tg_ordered_sum<8>(sq, HD) / (float)HD + 1e-6f);
 	inv = __shfl(inv, 0);
 	float mx = 0.0f;
 	int bad = 0;

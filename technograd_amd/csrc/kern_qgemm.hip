@@ -749,7 +749,7 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 			return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
 	};
 	if constexpr (!PRE) rows = tile_rows<NBW>(a, w, s, m0, c0 + 32 * jw, lane);
-	store_tile<NBW, true>(a, w, s, m0, c0 + 32 * jw, lane, rows, [&](int j, int v) { return (long long)totd(j, v); }, totd);
+	store_tile<NBW, NBW <= 2>(a, w, s, m0, c0 + 32 * jw, lane, rows, [&](int j, int v) { return (long long)totd(j, v); }, totd);
 }
 
 template <int BITS, int NB, int W, int P = 4>

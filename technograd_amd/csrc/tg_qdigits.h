@@ -55,15 +55,6 @@ __device__ inline void tgq_scan16(const float *v, unsigned &mb)
 	}
 }
 
-// the same over 4 inputs
-__device__ inline void tgq_scan16_4(const float *v, unsigned &mb)
-{
-	for (int i = 0; i < 4; i += 2) {
-		const unsigned a = __float_as_uint(v[i]) & 0x7fffffffu, b = __float_as_uint(v[i + 1]) & 0x7fffffffu;
-		mb = max(mb, max(a, b));
-	}
-}
-
 // four inputs' u = q + 0x808080 -> their digit bytes in the three plane words
 // (byte i of plane l's word: d_l of input i; the layout tgq_put16 writes)
 __device__ inline void tgq_pack4(const unsigned *u, unsigned &w0, unsigned &w1, unsigned &w2)
