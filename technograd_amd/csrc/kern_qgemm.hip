@@ -372,6 +372,9 @@ __device__ inline float *out_at(const tgk_qgemm_args &a, int r, int jj, int c)
 	return o.p + (long)r * o.orr + (long)jj * o.oj;
 }
 
+// the output as the instruction after the product would compute it
+__device__ inline float act(const tgk_qgemm_args &a, float v) { return a.act == TGK_ACT_TANH ? tanhf(v) : v; }
+
 __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot)
 {
 	if (m >= a.M || c >= w.C) return;
@@ -386,7 +389,7 @@ __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 		acc32 = (float)ldexp((double)tot, s.e[m] - 23);
 	}
 	int r = m / a.ni, jj = m - r * a.ni;
-	*out_at(a, r, jj, c) = w.scale[c] * acc32;
+	*out_at(a, r, jj, c) = act(a, w.scale[c] * acc32);
 }
 
 // One lane's outputs of a 32-row block: rows mbase + 8 (v / 4) + 4 (lane / 32)
@@ -462,7 +465,7 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 			if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
 			for (int j = 0; j < NB; j++) {
 				if (cbase + j * 32 + r32 >= w.C) continue;
-				oc[j].p[(long)r * oc[j].orr + (long)jj * oc[j].oj] = sc[j] * (float)ldexp(totd(j, v) - q8, E - 23);
+				oc[j].p[(long)r * oc[j].orr + (long)jj * oc[j].oj] = act(a, sc[j] * (float)ldexp(totd(j, v) - q8, E - 23));
 			}
 		}
 		return;
@@ -480,7 +483,7 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 		float *orow = a.o + (long)r * a.orr + (long)jj * a.oj;
 		for (int j = 0; j < NB; j++) {
 			if (cbase + j * 32 + r32 >= w.C) continue;
-			orow[coff[j]] = sc[j] * (float)ldexp(totd(j, v) - q8, E - 23);
+			orow[coff[j]] = act(a, sc[j] * (float)ldexp(totd(j, v) - q8, E - 23));
 		}
 	}
 }

@@ -103,7 +103,7 @@ struct Step {
 	long ag = 0, ai = 0, ap = 0, bg = 0, bp = 0, bj = 0, og = 0, oi = 0, oj = 0;
 	long codes = 0, scale = 0; // offsets into the code / scale pools
 	// quantized GEMM
-	int qw = -1, ni = 1;
+	int qw = -1, ni = 1, act = TGK_ACT_NONE;
 	long xr = 0, xj = 0, xk = 0, orr = 0, oc = 0, ojj = 0;
 	// row ops, transpose, take
 	int p0 = 0, p1 = 0, p2 = 0;
@@ -693,6 +693,18 @@ bool match_sscan(LB &L, const tgm_ins &in, Step &st)
 	return true;
 }
 
+// which operand of a matmul is a quantized parameter read along its channel
+// axis (1: a, 2: b), 0 when none: those products run as quantized GEMMs
+int matmul_quant(const tgm_module *m, const tgm_ins &in)
+{
+	const tgm_value &va = m->val[in.a[0]], &vb = m->val[in.a[1]];
+	int mm, kk, nn, gg;
+	matmul_dims(va.sh, vb.sh, mm, kk, nn, gg);
+	if (gg == 1 && va.qbits && q_axis_for(m, in.a[0], in) == va.qaxis) return 1;
+	if (gg == 1 && vb.qbits && q_axis_for(m, in.a[1], in) == vb.qaxis) return 2;
+	return 0;
+}
+
 bool layer_ins(LB &L, const tgm_ins &in)
 {
 	tgm_module *m = L.m;
@@ -749,9 +761,7 @@ bool layer_ins(LB &L, const tgm_ins &in)
 		const tgm_value &va = m->val[in.a[0]], &vb = m->val[in.a[1]];
 		int mm, kk, nn, gg;
 		matmul_dims(va.sh, vb.sh, mm, kk, nn, gg);
-		int quant = 0;
-		if (gg == 1 && va.qbits && q_axis_for(m, in.a[0], in) == va.qaxis) quant = 1;
-		else if (gg == 1 && vb.qbits && q_axis_for(m, in.a[1], in) == vb.qaxis) quant = 2;
+		const int quant = matmul_quant(m, in);
 		s.o = value_opnd(L, in.out);
 		if (quant && !(L.p->flags & TG_HIP_EXACT)) {
 			const tgm_value &w = quant == 1 ? va : vb;
@@ -928,10 +938,46 @@ void mark_loop_values(const tgm_block *b, std::vector<char> &lw)
 	}
 }
 
+// how many times value v is read anywhere in block b (nested bodies included)
+int value_reads(const tgm_block *b, int v)
+{
+	int n = 0;
+	auto cnt = [&](const int *p, int k) {
+		for (int i = 0; p && i < k; i++) n += p[i] == v;
+	};
+	for (int i = 0; i < b->len; i++) {
+		const tgm_ins &in = b->v[i];
+		cnt(in.a, in.na);
+		if (in.op == TGM_THINK) n += (in.init == v) + (in.yield == v) + (in.halt == v);
+		if (in.op == TGM_SCAN) {
+			cnt(in.c, in.nc), cnt(in.cinit, in.nc), cnt(in.cnext, in.nc);
+			cnt(in.x, in.nx), cnt(in.xt, in.nx), cnt(in.y, in.ny), cnt(in.ys, in.ny);
+		}
+		if (in.body) n += value_reads(in.body, v);
+	}
+	return n;
+}
+
 bool layer_block(LB &L, const tgm_block *b)
 {
-	for (int i = 0; i < b->len; i++)
-		if (!layer_ins(L, b->v[i])) return false;
+	for (int i = 0; i < b->len; i++) {
+		const tgm_ins &in = b->v[i];
+		// a quantized product read only by the tanh right after it (C1's layers): the
+		// GEMM writes tanh's output and applies tanhf in its epilogue (same values)
+		if (in.op == TGM_MATMUL && i + 1 < b->len && b == &L.m->top && !(L.p->flags & TG_HIP_EXACT) && matmul_quant(L.m, in)) {
+			const tgm_ins &nx = b->v[i + 1];
+			if (nx.op == TGM_TANH && nx.a[0] == in.out && in.out != L.m->output && !L.loopw[(size_t)in.out] &&
+			    value_reads(&L.m->top, in.out) == 1) {
+				tgm_ins fused = in;
+				fused.out = nx.out;
+				if (!layer_ins(L, fused)) return false;
+				L.p->steps.back().act = TGK_ACT_TANH;
+				i++; // the tanh is done
+				continue;
+			}
+		}
+		if (!layer_ins(L, in)) return false;
+	}
 	return true;
 }
 
@@ -1279,6 +1325,7 @@ void exec_step(Run &R, const Step &s)
 		a.o = dst(R, s.o);
 		a.orr = s.orr, a.oc = s.oc, a.oj = s.ojj;
 		a.M = R.rows * s.ni;
+		a.act = s.act;
 		if (!s.reuse_digits) {
 			Timer t(p, 2);
 			tgk_qgemm_digits(st, &a, p->d_scratch);
@@ -1462,13 +1509,15 @@ void merge_qgemms(tg_hip_prog *p, std::vector<std::vector<int8_t>> &mcodes, std:
 	const std::vector<char> inscan = in_scan(S);
 	std::vector<char> done(S.size(), 0);
 	for (size_t i = 0; i < S.size(); i++) {
-		if (S[i].kind != ST_QGEMM || inscan[i] || done[i]) continue;
+		if (S[i].kind != ST_QGEMM || inscan[i] || done[i] || S[i].act != TGK_ACT_NONE) continue;
 		std::vector<size_t> g{ i };
 		const tgk_qweight &w0 = p->qws[(size_t)S[i].qw];
 		long ctot = w0.C;
 		for (size_t j = i + 1; j < S.size() && g.size() < TGK_QSEG; j++) {
 			const Step &t = S[j];
-			if (t.kind != ST_QGEMM || inscan[j] || done[j] || !same_activation(S[i], t, p->qws) || t.oc != S[i].oc) continue;
+			if (t.kind != ST_QGEMM || inscan[j] || done[j] || t.act != TGK_ACT_NONE || !same_activation(S[i], t, p->qws) ||
+			    t.oc != S[i].oc)
+				continue;
 			const tgk_qweight &w = p->qws[(size_t)t.qw];
 			if (w.bits != w0.bits || ctot + w.C > (1L << 20)) continue;
 			g.push_back(j);

@@ -227,7 +227,11 @@ typedef struct {
 	int seg_c0[TGK_QSEG + 1];
 	float *seg_o[TGK_QSEG];
 	long seg_orr[TGK_QSEG], seg_oj[TGK_QSEG];
+	int act;                /* TGK_ACT_TANH: every output goes through tanhf (a tanh instruction that
+	                           only reads this product, applied in the GEMM's epilogue) */
 } tgk_qgemm_args;
+#define TGK_ACT_NONE 0
+#define TGK_ACT_TANH 1
 
 /* scratch: bytes needed for M rows of K inputs */
 size_t tgk_qgemm_scratch(int M, int Kp);
