@@ -18,6 +18,9 @@ SHAPES = [
     (4, 256, 4096, 4096),  # qgemv_k NB=4 W=4
     (4, 256, 2048, 4096),  # NB=4 W=2
     (8, 256, 512, 4096),   # NB=4 W=1
+    (8, 256, 4096, 4096),  # NB=4 W=4, int8 weights
+    (8, 256, 2048, 4096),  # NB=4 W=2, int8
+    (8, 250, 2048, 2016),  # NB=2 W=2, int8, rows and channels not multiples of 32
     (4, 128, 4096, 4096),  # NB=2 W=4
     (8, 128, 2048, 4096),  # NB=2 W=2
     (4, 100, 256, 4096),   # NB=2 W=1, rows not a multiple of 32
@@ -25,6 +28,7 @@ SHAPES = [
     (8, 16, 1024, 4096),   # NB=1 W=4
     (4, 3, 640, 4096),     # NB=1 W=2
     (4, 1, 256, 4096),     # NB=1 W=1
+    (8, 2, 8192, 2048),    # NB=1 W=8, int8
     (4, 64, 1024, 1000),   # NB=1, channels not a multiple of 32
 ]
 
