@@ -20,11 +20,12 @@
  * polynomial uses round(2^30 / j!) for j = 0..8; ln 2, pi, pi/2, 2 pi and the
  * gelu coefficients are round(value * 2^16); 1e-6 in Q32 is round(1e-6 * 2^32).
  *
- * Pinned by: the tests/golden fixtures that carry Q16.16 data (the
- * reference's own tg_rtq.h kernels, compiled from /root/reference by
- * oracle/Makefile into oracle/_ref, over all
- * 256 inputs of latent_reasoner's {0,1}^8 domain and random inputs:
- * byte-identical outputs and steps), closed forms in tests/ (isqrt64 against
+ * Pinned by: the tests/golden fixtures that carry Q16.16 data (outputs and
+ * steps of the reference's own emitted `tgc c --fixed` unit: src/cgen.c
+ * compiled from /root/reference by oracle/Makefile into oracle/_ref, the unit
+ * compiled with cc, over all 256 inputs of latent_reasoner's {0,1}^8 domain
+ * and random inputs: byte-identical outputs and steps; a test also runs the
+ * unit on 8448 fresh rows of config 4's model), closed forms in tests/ (isqrt64 against
  * integer square roots, fdiv against exact rational rounding, expq against
  * exp within its polynomial error), and the reference's fixed-vs-float bound
  * (tests/run.sh:306-322: max |fixed - float| < 5e-4). */
@@ -37,6 +38,12 @@
 #define ONE 65536
 #define MAXV 2147483647
 #define MINV (-2147483647 - 1)
+
+
+/* Test-only: a planted mistake in the think loop's halting test, so a test can
+ * show that comparing with the reference's emitted unit catches it
+ * (0 = none, 1 = `d < thr` for `d <= thr`, 2 = threshold one below). */
+int tgo_plant;
 
 static int32_t sat(int64_t v) { return v > MAXV ? MAXV : v < MINV ? MINV : (int32_t)v; }
 static int64_t asr(int64_t v, int s) { return v >> s; } /* arithmetic, as gcc and clang implement >> on int64 */
@@ -481,7 +488,7 @@ static void exec_one(VM *vm, const tgo_ins *in)
 			const int32_t *y = ptr(vm, in->yield);
 			int32_t d = delta(y, o, n);
 			copy(o, y, n);
-			if (in->eps >= 0 && d <= thr) break;
+			if (in->eps >= 0 && (tgo_plant == 1 ? d < thr : tgo_plant == 2 ? d <= thr - 1 : d <= thr)) break;
 			if (in->halt >= 0) {
 				int32_t h = *ptr(vm, in->halt), p = h < 0 ? 0 : h > ONE ? ONE : h;
 				sv = fmul(sv, ONE - p);

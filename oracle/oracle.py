@@ -165,3 +165,25 @@ def ref_batch(model_path, rows, per, nout, nthink, workdir, threads=1, fixed=Fal
         if line.startswith("ref-batch"):
             ms = float(line.split()[-1])
     return out, steps, ms
+
+
+def ref_unit(model_path, rows_q16, nout, nthink, workdir):
+    """Run the reference's own `tgc c --fixed` unit over Q16.16 rows.
+
+    src/cgen.c (compiled into _ref/tgc_ref) emits the freestanding unit for the
+    model, as `tgc c MODEL --fixed` does; it is compiled the way the
+    reference's tests compile such units (tests/run.sh:309, cc -std=c99 -O2),
+    with the raw-row driver tgc_ref writes beside it instead of the unit's own
+    decimal driver. Returns (int32 outputs [rows, nout], int32 steps [rows,
+    max(nthink, 1)])."""
+    d = os.path.join(workdir, "unit_" + os.path.basename(model_path).replace(".", "_"))
+    os.makedirs(d, exist_ok=True)
+    unit, main, exe = (os.path.join(d, n) for n in ("unit.c", "main.c", "unit"))
+    ref_run(["c", model_path, "-o", unit, "--fixed", "--harness", main])
+    subprocess.run([os.environ.get("CC", "cc"), "-std=c99", "-O2", "-o", exe, main], check=True, capture_output=True)
+    inp, outp, stp = (os.path.join(d, n) for n in ("in.bin", "out.bin", "steps.bin"))
+    np.ascontiguousarray(rows_q16, dtype="<i4").tofile(inp)
+    subprocess.run([exe, inp, outp, stp], check=True, capture_output=True)
+    out = np.fromfile(outp, dtype="<i4").reshape(-1, nout)
+    steps = np.fromfile(stp, dtype="<i4").reshape(-1, max(nthink, 1))
+    return out, steps

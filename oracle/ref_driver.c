@@ -16,7 +16,14 @@
  *   tgc_ref batch MODEL ROWS.bin -o OUT.bin [-j N] [--steps S.bin] [--fixed]
  *       ROWS: raw f32 (or raw int32 Q16.16 with --fixed); OUT likewise;
  *       S: raw int32 steps per row and think loop. Prints compute time (ms)
- *       and threads on stderr as `ref-batch rows R threads T ms M`. */
+ *       and threads on stderr as `ref-batch rows R threads T ms M`.
+ *   tgc_ref c MODEL -o UNIT.c [--fixed] [--harness MAIN.c]
+ *       the reference's C generator (src/cgen.c, cgen_mode) on the loaded and
+ *       planned module, as `tgc c` runs it (src/main.c:446-470). --harness
+ *       also writes a driver of this file's own that includes UNIT.c and runs
+ *       tg_<model>_run over raw rows: `main ROWS OUT STEPS` reads each row's
+ *       inputs (raw words, in input order), writes the raw output words and
+ *       the int32 tg_<model>_steps values (one per think loop, at least one). */
 #include "tg.h"
 
 #include <stdlib.h>
@@ -126,10 +133,67 @@ static int batch(int argc, char **argv)
 	return 0;
 }
 
+/* The raw-row driver for a unit: every input row in, every output and steps
+ * word out, with no decimal conversion in between. */
+static void write_harness(const Module *m, const char *unit, FILE *f, int fixed)
+{
+	const char *ty = fixed ? "tg_t" : "float", *nm = m->name;
+	int outn = shape_numel(&m->val[m->output].sh);
+	fprintf(f, "/* raw-row driver for the generated unit %s (written by oracle/ref_driver.c) */\n", unit);
+	fprintf(f, "#include \"%s\"\n#include <stdio.h>\n\n", unit);
+	fputs("int main(int argc, char **argv)\n{\n", f);
+	for (int i = 0; i < m->ninputs; i++) fprintf(f, "\tstatic %s in%d[%d];\n", ty, i, shape_numel(&m->val[m->inputs[i]].sh));
+	fprintf(f, "\tstatic %s out[%d];\n", ty, outn);
+	fputs("\tif (argc != 4) { fputs(\"usage: main ROWS OUT STEPS\\n\", stderr); return 2; }\n", f);
+	fputs("\tFILE *fi = fopen(argv[1], \"rb\"), *fo = fopen(argv[2], \"wb\"), *fs = fopen(argv[3], \"wb\");\n", f);
+	fputs("\tif (!fi || !fo || !fs) { fputs(\"cannot open files\\n\", stderr); return 2; }\n", f);
+	fputs("\tfor (long r = 0;; r++) {\n", f);
+	for (int i = 0; i < m->ninputs; i++) {
+		int n = shape_numel(&m->val[m->inputs[i]].sh);
+		fprintf(f, "\t\tif (fread(in%d, sizeof in%d[0], %d, fi) != %d) { if (%d == 0 && feof(fi)) break; fputs(\"short row\\n\", stderr); return 2; }\n",
+			i, i, n, n, i);
+	}
+	if (m->ninputs == 0) fputs("\t\tif (r == 1) break;\n", f);
+	fprintf(f, "\t\ttg_%s_run(", nm);
+	for (int i = 0; i < m->ninputs; i++) fprintf(f, "in%d, ", i);
+	fputs("out);\n", f);
+	fprintf(f, "\t\tfwrite(out, sizeof out[0], %d, fo);\n", outn);
+	fprintf(f, "\t\tfwrite(tg_%s_steps, sizeof(int), %d, fs);\n", nm, m->nthink ? m->nthink : 1);
+	fputs("\t}\n\treturn fclose(fo) || fclose(fs) ? 1 : 0;\n}\n", f);
+}
+
+static int unit(int argc, char **argv)
+{
+	const char *model = NULL, *opath = NULL, *hpath = NULL;
+	int fixed = 0;
+	for (int i = 2; i < argc; i++) {
+		if (!strcmp(argv[i], "-o") && i + 1 < argc) opath = argv[++i];
+		else if (!strcmp(argv[i], "--harness") && i + 1 < argc) hpath = argv[++i];
+		else if (!strcmp(argv[i], "--fixed")) fixed = 1;
+		else if (!model) model = argv[i];
+		else die(NULL, 0, "unexpected argument '%s'", argv[i]);
+	}
+	if (!model || !opath) die(NULL, 0, "usage: tgc_ref c MODEL -o UNIT.c [--fixed] [--harness MAIN.c]");
+	Module *m = load_module(model);
+	plan(m);
+	FILE *f = fopen(opath, "w");
+	if (!f) die(NULL, 0, "cannot write '%s'", opath);
+	cgen_mode(m, f, fixed);
+	if (fclose(f)) die(NULL, 0, "write failed '%s'", opath);
+	if (hpath) {
+		const char *base = strrchr(opath, '/');
+		f = fopen(hpath, "w");
+		if (!f) die(NULL, 0, "cannot write '%s'", hpath);
+		write_harness(m, base ? base + 1 : opath, f, fixed);
+		if (fclose(f)) die(NULL, 0, "write failed '%s'", hpath);
+	}
+	return 0;
+}
+
 int main(int argc, char **argv)
 {
 	if (argc < 3) {
-		fputs("usage: tgc_ref ir|quantize|batch MODEL ...\n", stderr);
+		fputs("usage: tgc_ref ir|quantize|batch|c MODEL ...\n", stderr);
 		return 2;
 	}
 	if (!strcmp(argv[1], "quantize")) {
@@ -143,6 +207,7 @@ int main(int argc, char **argv)
 		return 0;
 	}
 	if (!strcmp(argv[1], "batch")) return batch(argc, argv);
+	if (!strcmp(argv[1], "c")) return unit(argc, argv);
 	fputs("unknown command\n", stderr);
 	return 2;
 }

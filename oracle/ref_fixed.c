@@ -1,19 +1,16 @@
-/* TEST INFRASTRUCTURE ONLY — Q16.16 execution with the reference's own kernels.
+/* TEST INFRASTRUCTURE ONLY — Q16.16 execution with the reference's own kernels,
+ * kept as a cross-check of the emitted units.
  *
- * `tgc c --fixed` emits a C unit that calls the kernels of runtime/tg_rtq.h
- * once per instruction (src/cgen.c:100-314); building that generator needs
- * headers produced at build time, so oracle/_ref does not build it. This file
- * includes runtime/tg_rtq.h from /root/reference unchanged and walks the
- * reference's own Module (loaded and planned by the reference's load_module and
- * plan) issuing the same kernel calls the emitted unit would, with the same
- * conversions: params to_fixed(v, 16), quant scales to_fixed(s, 24) as Q7.24,
- * constants to_fixed(k, 16), think thresholds kept positive (cgen.c:76-89,
- * :286-290, :295-305, :435-455). Arena offsets are the reference planner's.
- *
- * What this pins: every tg_rtq.h kernel bit for bit. The instruction order is
- * restated from cgen.c and is shared with the oracle (oracle/fixed.c); it is
- * cross-checked by the reference's own bound |fixed - float VM| < 5e-4
- * (tests/run.sh:306-322) against the float VM compiled from src/vm.c. */
+ * The Q16.16 goldens come from the reference's `tgc c --fixed` unit itself
+ * (src/cgen.c compiled into oracle/_ref; `tgc_ref c`). This file is a second,
+ * independent route to the same numbers: it includes runtime/tg_rtq.h from
+ * /root/reference unchanged and walks the reference's own Module (loaded and
+ * planned by the reference's load_module and plan) issuing the kernel calls
+ * the emitted unit makes, with the same conversions: params to_fixed(v, 16),
+ * quant scales to_fixed(s, 24) as Q7.24, constants to_fixed(k, 16), think
+ * thresholds kept positive (cgen.c:76-89, :286-290, :295-305, :435-455).
+ * Arena offsets are the reference planner's. tests/golden/make_golden.py
+ * requires both routes to agree bit for bit before it writes a fixture. */
 #include "tg.h"
 #include "tg_rtq.h"
 

@@ -7,8 +7,10 @@ and the reference's feature list, not copied from the reference), the
 reference's own code:
   1. lowers the surface model to canonical TGIR   (tgc_ref ir       -> src/lower.c, src/ir.c)
   2. quantizes it                                   (tgc_ref quantize -> src/quant.c)
-  3. runs it over seeded rows                       (tgc_ref batch    -> src/vm.c, src/par.c;
-                                                     --fixed          -> runtime/tg_rtq.h)
+  3. runs it over seeded rows                       (tgc_ref batch    -> src/vm.c, src/par.c)
+  4. for Q16.16 variants, emits the model's `tgc c --fixed` unit, compiles it
+     and runs it over the same rows in Q16.16     (tgc_ref c        -> src/cgen.c, runtime/tg_rtq.h;
+                                                     cross-checked against tgc_ref batch --fixed)
 and the results are stored as data: <name>.tgir (model text) and <name>.npz
 (inputs, f32 outputs, Q16.16 inputs/outputs, steps). Models in SYNTH are
 written as TGIR by this repository's builders (technograd_amd/synth.py) and
@@ -149,7 +151,10 @@ def main():
         data = dict(x=x, y=y, steps=st, **extra)
         if fixed:
             xq = O.to_fixed_rows(x)
-            yq, sq, _ = O.ref_batch(mpath, xq, m.per, m.nout, m.nthink, tmp, threads=4, fixed=True)
+            yq, sq = O.ref_unit(mpath, xq, m.nout, m.nthink, tmp)  # the emitted `tgc c --fixed` unit
+            yw, sw, _ = O.ref_batch(mpath, xq, m.per, m.nout, m.nthink, tmp, threads=4, fixed=True)
+            if not (np.array_equal(yw, yq) and np.array_equal(sw, sq)):
+                sys.exit("%s: the reference's kernels walked over its Module disagree with its emitted unit" % name)
             data.update(xq=xq, yq=yq, stepsq=sq)
         np.savez_compressed(os.path.join(HERE, name + ".npz"), **data)
         print("%-16s rows %4d per %4d out %4d think %d%s" % (name, x.shape[0], m.per, m.nout, m.nthink, " +fixed" if fixed else ""))

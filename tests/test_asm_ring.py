@@ -11,7 +11,11 @@ loads in order at each vmcnt(N), and fails if an instruction after the final
 ring load writes a register that an outstanding load will write. (The kernel
 prevents this by reading every ring register after its final wait; without
 that, the epilogue's row index was computed into such registers, and the
-index was overwritten before the row-info loads used it.)"""
+index was overwritten before the row-info loads used it.)
+
+The large-batch kernel (qgemm_k) sets m0 in inline assembly before each of
+its global-to-LDS copies; a second test checks that nothing else in that
+kernel uses m0."""
 import os
 import re
 import shutil
@@ -63,14 +67,69 @@ def ring_hazards(asm_lines):
     return found
 
 
-@pytest.mark.skipif(not os.path.exists(HIPCC) and not shutil.which("hipcc"), reason="hipcc not installed")
-def test_qgemv_ring_registers_not_reused_in_flight(tmp_path):
+# instructions that read m0 without naming it (moves indexed by m0, messages,
+# LDS-destination loads other than the kernel's copies, interpolation, GWS)
+M0_IMPLICIT = re.compile(r"^(v_movrel|s_movrel|s_sendmsg|ds_gws|v_interp|buffer_load\S*.*\blds\b)")
+
+
+def m0_hazards(asm_lines):
+    """{kernel: [instructions that use m0 outside the copy pairs]} for every qgemm_k.
+
+    qgemm_k's copies (copy_to_lds) set m0 in inline assembly right before each
+    global_load_lds_dwordx4. The compiler does not know that m0 changes there
+    (m0 is a reserved register and cannot be declared clobbered), so any other
+    use of m0 by compiled code in the kernel could see a copy's LDS address."""
+    found = {}
+    starts = [i for i, l in enumerate(asm_lines) if re.match(r"^_Z\S*qgemm_k\S*:", l)]
+    for s in starts:
+        e = next(i for i in range(s, len(asm_lines)) if "s_endpgm" in asm_lines[i])
+        body = [l.strip() for l in asm_lines[s:e] if l.strip() and not l.strip().startswith(";")
+                and not l.strip().startswith(".")]
+        hits, copies = [], 0
+        for k, t in enumerate(body):
+            op = t.split()[0]
+            if op == "global_load_lds_dwordx4":
+                if not (k > 0 and re.match(r"s_mov_b32 m0, s\d+$", body[k - 1])):
+                    hits.append(t)
+                copies += 1
+                continue
+            if re.match(r"s_mov_b32 m0, s\d+$", t) and k + 1 < len(body) and body[k + 1].startswith("global_load_lds_dwordx4"):
+                continue
+            if re.search(r"\bm0\b", t) or M0_IMPLICIT.match(t):
+                hits.append(t)
+        assert copies, "no LDS copies found in " + asm_lines[s]
+        found[asm_lines[s].split(":")[0]] = hits
+    return found
+
+
+@pytest.fixture(scope="module")
+def qgemm_asm(tmp_path_factory):
+    if not os.path.exists(HIPCC) and not shutil.which("hipcc"):
+        pytest.skip("hipcc not installed")
     csrc = os.path.join(ROOT, "technograd_amd", "csrc")
-    asm = tmp_path / "kern_qgemm.s"
+    asm = tmp_path_factory.mktemp("asm") / "kern_qgemm.s"
     subprocess.run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
                     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", os.path.join(ROOT, "include"), "-I", csrc,
                     "--cuda-device-only", "-S", os.path.join(csrc, "kern_qgemm.hip"), "-o", str(asm)], check=True, capture_output=True)
-    found = ring_hazards(asm.read_text().split("\n"))
+    return asm.read_text().split("\n")
+
+
+def test_qgemv_ring_registers_not_reused_in_flight(qgemm_asm):
+    found = ring_hazards(qgemm_asm)
     assert len(found) >= 6  # every instantiation the launcher uses was checked
     bad = {k: v for k, v in found.items() if v}
     assert not bad, bad
+
+
+def test_qgemm_m0_only_set_for_lds_copies(qgemm_asm):
+    found = m0_hazards(qgemm_asm)
+    assert len(found) >= 2  # the int4 and int8 instantiations
+    bad = {k: v for k, v in found.items() if v}
+    assert not bad, bad
+
+
+def test_m0_check_sees_a_foreign_use():
+    """The m0 scan flags an m0 read that is not one of the copy pairs."""
+    lines = ["_Z7qgemm_kILi4EEvv:", "s_mov_b32 m0, s4", "global_load_lds_dwordx4 v1, s[2:3]",
+             "s_mov_b32 m0, s5", "v_readlane_b32 s6, v2, m0", "s_endpgm"]
+    assert m0_hazards(lines) == {"_Z7qgemm_kILi4EEvv": ["s_mov_b32 m0, s5", "v_readlane_b32 s6, v2, m0"]}

@@ -43,12 +43,66 @@ def test_f32_matches_reference_bit_for_bit(name):
 
 @pytest.mark.parametrize("name", [n for n in NAMES if "xq" in np.load(os.path.join(GOLDEN, n + ".npz")).files])
 def test_fixed_matches_reference_bit_for_bit(name):
+    """xq/yq/stepsq come from the reference's emitted `tgc c --fixed` unit."""
     text, d = load(name)
     m = O.Model(text)
     assert np.array_equal(O.to_fixed_rows(d["x"]), d["xq"])
     yq, sq = m.batch_fixed(d["xq"], threads=4)
     assert np.array_equal(yq, d["yq"]), "Q16.16 outputs differ from the reference kernels"
     assert np.array_equal(sq, d["stepsq"])
+
+
+@pytest.mark.parametrize("plant", [1, 2])
+def test_planted_halting_mistake_is_caught(plant):
+    """The Q16.16 goldens (outputs and steps of the reference's emitted
+    `tgc c --fixed` unit) catch a slip in the think loop's halting test: `<`
+    for `<=` (plant 1) or a threshold one below to_fixed(1e-4, 16) = 7
+    (plant 2), each planted in the oracle."""
+    text, d = load("latent_f32")
+    m = O.Model(text)
+    knob = ctypes.c_int.in_dll(O.lib(), "tgo_plant")
+    knob.value = plant
+    try:
+        yq, sq = m.batch_fixed(d["xq"], threads=4)
+    finally:
+        knob.value = 0
+    assert not np.array_equal(sq, d["stepsq"]) and not np.array_equal(yq, d["yq"])
+    yq, sq = m.batch_fixed(d["xq"], threads=4)
+    assert np.array_equal(sq, d["stepsq"]) and np.array_equal(yq, d["yq"])
+
+
+@pytest.mark.skipif(not O.have_ref(), reason="needs the reference build (oracle/_ref, made from /root/reference)")
+def test_fixed_oracle_matches_emitted_unit_on_fresh_rows(tmp_path):
+    """Config 4's model through the reference's own emitted Q16.16 unit
+    (src/cgen.c, compiled with cc as tests/run.sh:309 does) on rows that are
+    not in the goldens: the whole {0,1}^8 domain again, 4096 N(0,1) rows and
+    4096 rows uniform in [-3, 3]. Outputs and steps bit for bit."""
+    import itertools
+    text, _ = load("latent_f32")
+    m = O.Model(text)
+    rng = np.random.default_rng(5)
+    dom = np.array(list(itertools.product([0, 1], repeat=8)), np.float32)
+    x = np.concatenate([dom, rng.normal(size=(4096, 8)).astype(np.float32),
+                        rng.uniform(-3, 3, size=(4096, 8)).astype(np.float32)])
+    xq = O.to_fixed_rows(x)
+    yu, su = O.ref_unit(os.path.join(GOLDEN, "latent_f32.tgir"), xq, m.nout, m.nthink, str(tmp_path))
+    yo, so = m.batch_fixed(xq, threads=4)
+    assert np.array_equal(so, su) and np.array_equal(yo, yu)
+    assert len(np.unique(su)) >= 3  # rows halt at different steps
+
+
+@pytest.mark.skipif(not O.have_ref(), reason="needs the reference build (oracle/_ref, made from /root/reference)")
+@pytest.mark.parametrize("name", [n for n in NAMES if "xq" in np.load(os.path.join(GOLDEN, n + ".npz")).files])
+def test_fixed_goldens_are_the_emitted_units(name, tmp_path):
+    """Every Q16.16 golden is what the reference's emitted unit computes, and
+    the reference's kernels walked over its Module (tgc_ref --fixed) agree."""
+    text, d = load(name)
+    m = O.Model(text)
+    path = os.path.join(GOLDEN, name + ".tgir")
+    yu, su = O.ref_unit(path, d["xq"], m.nout, m.nthink, str(tmp_path))
+    assert np.array_equal(yu, d["yq"]) and np.array_equal(su, d["stepsq"])
+    yw, sw, _ = O.ref_batch(path, d["xq"], m.per, m.nout, m.nthink, str(tmp_path), threads=2, fixed=True)
+    assert np.array_equal(yw, yu) and np.array_equal(sw, su)
 
 
 @pytest.mark.parametrize("name", [n for n in NAMES if "qargs" in np.load(os.path.join(GOLDEN, n + ".npz")).files])
