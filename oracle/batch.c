@@ -36,7 +36,7 @@ static void *worker(void *arg)
 	Job *j = arg;
 	const tgo_module *m = j->m;
 	int nt = m->nthink ? m->nthink : 1;
-	void *arena = malloc((size_t)m->arena * 4);
+	void *arena = malloc((size_t)(m->arena ? m->arena : 1) * (j->fixed == 2 ? 8 : 4));
 	int *tmp = malloc((size_t)nt * sizeof *tmp);
 	if (!arena || !tmp) {
 		atomic_store(&j->failed, 1);
@@ -51,7 +51,9 @@ static void *worker(void *arg)
 		for (long r = lo; r < hi; r++) {
 			int *st = j->steps ? j->steps + r * nt : tmp;
 			for (int t = 0; t < nt; t++) st[t] = 0;
-			if (j->fixed)
+			if (j->fixed == 2)
+				tgo_run_row64(m, (const double *)j->rows + r * m->per, (double *)j->out + r * m->nout, st, arena);
+			else if (j->fixed)
 				tgo_run_row_fixed(m, (const int32_t *)j->rows + r * m->per, (int32_t *)j->out + r * m->nout, st, arena);
 			else
 				tgo_run_row(m, (const float *)j->rows + r * m->per, (float *)j->out + r * m->nout, st, arena);
@@ -88,6 +90,13 @@ int tgo_batch_fixed(tgo_module *m, const int32_t *rows, long nrows, int32_t *out
 {
 	if (tgo_prepare_fixed(m)) return -1;
 	return run(m, rows, nrows, out, steps, threads, 1);
+}
+
+/* the double-precision interpreter (vm64.c) over double rows: a truth for tests */
+int tgo_batch64(tgo_module *m, const double *rows, long nrows, double *out, int *steps, int threads)
+{
+	if (tgo_prepare_f64(m)) return -1;
+	return run(m, rows, nrows, out, steps, threads, 2);
 }
 
 static uint32_t xorshift(uint32_t *s)

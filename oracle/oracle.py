@@ -42,6 +42,7 @@ def lib():
         L.tgo_info.argtypes = [vp, ctypes.POINTER(ip), ctypes.POINTER(ip), ctypes.POINTER(ip), ctypes.POINTER(ctypes.c_long)]
         L.tgo_batch.argtypes = [vp, vp, ctypes.c_long, vp, vp, ip]
         L.tgo_batch_fixed.argtypes = [vp, vp, ctypes.c_long, vp, vp, ip]
+        L.tgo_batch64.argtypes = [vp, vp, ctypes.c_long, vp, vp, ip]
         L.tgo_quantize.argtypes = [vp, ip, ip, vp, ctypes.c_long, ip, cp, ip]
         L.tgo_write.restype = ctypes.c_void_p
         L.tgo_write.argtypes = [vp]
@@ -87,6 +88,17 @@ class Model:
         rc = lib().tgo_batch(self.h, _ptr(rows), rows.shape[0], _ptr(out), _ptr(steps), threads)
         if rc:
             raise RuntimeError("oracle batch failed (%d)" % rc)
+        return out, steps
+
+    def batch64(self, rows, threads=8):
+        """The same interpreter in double precision (vm64.c): a high-precision
+        truth for tests, not the reference's arithmetic."""
+        rows = np.ascontiguousarray(rows, dtype=np.float32).astype(np.float64).reshape(-1, self.per)
+        out = np.empty((rows.shape[0], self.nout), np.float64)
+        steps = np.zeros((rows.shape[0], max(self.nthink, 1)), np.int32)
+        rc = lib().tgo_batch64(self.h, _ptr(rows), rows.shape[0], _ptr(out), _ptr(steps), threads)
+        if rc:
+            raise RuntimeError("oracle f64 batch failed (%d)" % rc)
         return out, steps
 
     def batch_fixed(self, rows_q16, threads=8):

@@ -683,6 +683,7 @@ void tgo_free(tgo_module *m)
 		tgo_value *x = &m->val[v];
 		free(x->name);
 		free(x->data);
+		free(x->d64);
 		free(x->q);
 		free(x->qs);
 		free(x->fx);

@@ -45,6 +45,7 @@ typedef struct {
 	int n;          /* element count */
 	char *name;     /* NULL for unnamed temporaries */
 	float *data;    /* params: f32 values (dequantized for quantized params, src/ir.c:507) */
+	double *d64;    /* params: the same values as double, for the double-precision interpreter (vm64.c) */
 	int qbits, qaxis;
 	signed char *q; /* int8 codes, or int4 packed two per byte, low nibble first */
 	float *qs;      /* one scale per channel */
@@ -109,6 +110,9 @@ int tgo_q_axis_for(const tgo_module *m, int param, const tgo_ins *in);
 int tgo_qget(const signed char *q, int bits, long i);
 int tgo_bcast_desc(const tgo_shape *out, const tgo_shape *a, const tgo_shape *b, int *d);
 void tgo_run_row(const tgo_module *m, const float *in, float *out, int *steps, float *arena);
+void tgo_run_row64(const tgo_module *m, const double *in, double *out, int *steps, double *arena);
+int tgo_prepare_f64(tgo_module *m);
+int tgo_batch64(tgo_module *m, const double *rows, long nrows, double *out, int *steps, int threads);
 void tgo_run_row_fixed(const tgo_module *m, const int32_t *in, int32_t *out, int *steps, int32_t *arena);
 int tgo_prepare_fixed(tgo_module *m);
 /* matmul observer used by GPTQ calibration (restates vm_matmul_hook, src/vm.c:50, :276) */

@@ -30,31 +30,52 @@
 #include <math.h>
 #include <string.h>
 
+/* This file is compiled twice: as the f32 oracle (the reference's arithmetic),
+ * and by vm64.c with TGO_F64 as the same interpreter in double precision,
+ * which tests use as a high-precision truth (the same operations in the same
+ * order on the same f32 params, constants and inputs, rounded to double). */
+#ifdef TGO_F64
+typedef double real;
+#define LM(fn) fn
+#define TGO_RUN_ROW tgo_run_row64
+#else
+typedef float real;
+#define LM(fn) fn##f
+#define TGO_RUN_ROW tgo_run_row
+#endif
+
+#ifndef TGO_F64
 void (*tgo_matmul_hook)(void *ctx, const tgo_module *m, const tgo_ins *in, const float *a, const float *b);
 void *tgo_hook_ctx;
+#endif
 
 typedef struct {
 	const tgo_module *m;
-	float *arena;
-	const float *in;
+	real *arena;
+	const real *in;
 	int *steps;
 } VM;
 
-static float *ptr(VM *vm, int v)
+static real *ptr(VM *vm, int v)
 {
 	const tgo_value *x = &vm->m->val[v];
 	switch (x->kind) {
 	case TGO_PARAM:
+#ifdef TGO_F64
+	case TGO_STATE: return x->d64;
+#else
 	case TGO_STATE: return x->data;
+#endif
 	case TGO_INPUT: {
 		long off = 0;
 		for (int i = 0; i < x->index; i++) off += vm->m->val[vm->m->inputs[i]].n;
-		return (float *)vm->in + off;
+		return (real *)vm->in + off;
 	}
 	}
 	return vm->arena + x->off;
 }
 
+#ifndef TGO_F64
 void tgo_matmul_dims(const tgo_shape *a, const tgo_shape *b, int *m, int *k, int *n, int *g)
 {
 	*g = a->rank == 3 && b->rank == 3 ? a->dim[0] : 1;
@@ -73,9 +94,11 @@ int tgo_q_axis_for(const tgo_module *m, int param, const tgo_ins *in)
 	return -1;
 }
 
+#endif
+
 /* ---- binary elementwise ---- */
 
-static float bop(int op, float x, float y)
+static real bop(int op, real x, real y)
 {
 	switch (op) {
 	case O_ADD: return x + y;
@@ -87,7 +110,7 @@ static float bop(int op, float x, float y)
 	}
 }
 
-static void kbin(int op, float *o, const float *a, int sa, const float *b, int sb, int n)
+static void kbin(int op, real *o, const real *a, int sa, const real *b, int sb, int n)
 {
 	for (int i = 0; i < n; i++) o[i] = bop(op, a[i * sa], b[i * sb]);
 }
@@ -108,6 +131,7 @@ static int seq(const tgo_shape *a, const tgo_shape *b)
 	return 1;
 }
 
+#ifndef TGO_F64
 int tgo_bcast_desc(const tgo_shape *out, const tgo_shape *a, const tgo_shape *b, int *d)
 {
 	int r = out->rank, dim[TGO_MAXRANK], st[2][TGO_MAXRANK];
@@ -155,8 +179,9 @@ int tgo_bcast_desc(const tgo_shape *out, const tgo_shape *a, const tgo_shape *b,
 	}
 	return 1 + 3 * nr;
 }
+#endif
 
-static void bin(VM *vm, const tgo_ins *in, float *o, const float *a, const float *b)
+static void bin(VM *vm, const tgo_ins *in, real *o, const real *a, const real *b)
 {
 	const tgo_module *m = vm->m;
 	const tgo_shape *so = &m->val[in->out].sh, *s0 = &m->val[in->a[0]].sh, *s1 = &m->val[in->a[1]].sh;
@@ -191,24 +216,24 @@ static void bin(VM *vm, const tgo_ins *in, float *o, const float *a, const float
 
 /* ---- unary elementwise ---- */
 
-static void unary(int op, float *o, const float *a, int n)
+static void unary(int op, real *o, const real *a, int n)
 {
 	for (int i = 0; i < n; i++) {
-		float x = a[i];
+		real x = a[i];
 		switch (op) {
 		case O_NEG: o[i] = -x; break;
-		case O_TANH: o[i] = tanhf(x); break;
+		case O_TANH: o[i] = LM(tanh)(x); break;
 		case O_RELU: o[i] = x > 0.0f ? x : 0.0f; break;
-		case O_SIGMOID: o[i] = 1.0f / (1.0f + expf(-x)); break;
-		case O_EXP: o[i] = expf(x); break;
-		case O_SQRT: o[i] = sqrtf(x); break;
-		case O_GELU: o[i] = 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x))); break;
-		case O_SILU: o[i] = x / (1.0f + expf(-x)); break;
-		case O_SOFTPLUS: o[i] = (x > 0.0f ? x : 0.0f) + log1pf(expf(-fabsf(x))); break;
-		case O_LOG: o[i] = logf(x); break;
-		case O_SIN: o[i] = sinf(x); break;
-		case O_COS: o[i] = cosf(x); break;
-		case O_FLOOR: o[i] = floorf(x); break;
+		case O_SIGMOID: o[i] = 1.0f / (1.0f + LM(exp)(-x)); break;
+		case O_EXP: o[i] = LM(exp)(x); break;
+		case O_SQRT: o[i] = LM(sqrt)(x); break;
+		case O_GELU: o[i] = 0.5f * x * (1.0f + LM(tanh)(0.7978845608f * (x + 0.044715f * x * x * x))); break;
+		case O_SILU: o[i] = x / (1.0f + LM(exp)(-x)); break;
+		case O_SOFTPLUS: o[i] = (x > 0.0f ? x : 0.0f) + LM(log1p)(LM(exp)(-LM(fabs)(x))); break;
+		case O_LOG: o[i] = LM(log)(x); break;
+		case O_SIN: o[i] = LM(sin)(x); break;
+		case O_COS: o[i] = LM(cos)(x); break;
+		case O_FLOOR: o[i] = LM(floor)(x); break;
 		case O_STEP: o[i] = x > 0.0f ? 1.0f : 0.0f; break;
 		}
 	}
@@ -216,77 +241,77 @@ static void unary(int op, float *o, const float *a, int n)
 
 /* ---- matmuls ---- */
 
-static void matmul_f32(float *o, const float *a, const float *b, int m, int k, int n)
+static void matmul_f32(real *o, const real *a, const real *b, int m, int k, int n)
 {
 	for (int i = 0; i < m; i++)
 		for (int j = 0; j < n; j++) {
-			float s = 0.0f;
+			real s = 0.0f;
 			for (int p = 0; p < k; p++) s += a[(long)i * k + p] * b[(long)p * n + j];
 			o[(long)i * n + j] = s;
 		}
 }
 
-static void matmul_qa(float *o, const signed char *q, int bits, const float *s, const float *b, int m, int k, int n)
+static void matmul_qa(real *o, const signed char *q, int bits, const float *s, const real *b, int m, int k, int n)
 {
 	for (int i = 0; i < m; i++)
 		for (int j = 0; j < n; j++) {
-			float acc = 0.0f;
-			for (int p = 0; p < k; p++) acc += (float)tgo_qget(q, bits, (long)i * k + p) * b[(long)p * n + j];
+			real acc = 0.0f;
+			for (int p = 0; p < k; p++) acc += (real)tgo_qget(q, bits, (long)i * k + p) * b[(long)p * n + j];
 			o[(long)i * n + j] = s[i] * acc;
 		}
 }
 
-static void matmul_qb(float *o, const float *a, const signed char *q, int bits, const float *s, int m, int k, int n)
+static void matmul_qb(real *o, const real *a, const signed char *q, int bits, const float *s, int m, int k, int n)
 {
 	for (int i = 0; i < m; i++)
 		for (int j = 0; j < n; j++) {
-			float acc = 0.0f;
-			for (int p = 0; p < k; p++) acc += a[(long)i * k + p] * (float)tgo_qget(q, bits, (long)p * n + j);
+			real acc = 0.0f;
+			for (int p = 0; p < k; p++) acc += a[(long)i * k + p] * (real)tgo_qget(q, bits, (long)p * n + j);
 			o[(long)i * n + j] = s[j] * acc;
 		}
 }
 
 /* ---- row ops ---- */
 
-static void softmax(float *o, const float *a, int rows, int cols)
+static void softmax(real *o, const real *a, int rows, int cols)
 {
 	for (int r = 0; r < rows; r++) {
-		const float *x = a + (long)r * cols;
-		float *y = o + (long)r * cols;
-		float mx = x[0], s = 0.0f;
+		const real *x = a + (long)r * cols;
+		real *y = o + (long)r * cols;
+		real mx = x[0], s = 0.0f;
 		for (int i = 1; i < cols; i++)
 			if (x[i] > mx) mx = x[i];
 		for (int i = 0; i < cols; i++) {
-			y[i] = expf(x[i] - mx);
+			y[i] = LM(exp)(x[i] - mx);
 			s += y[i];
 		}
 		for (int i = 0; i < cols; i++) y[i] /= s;
 	}
 }
 
-static void rmsnorm(float *o, const float *a, int rows, int cols)
+static void rmsnorm(real *o, const real *a, int rows, int cols)
 {
 	for (int r = 0; r < rows; r++) {
-		const float *x = a + (long)r * cols;
-		float *y = o + (long)r * cols;
-		float s = 0.0f;
+		const real *x = a + (long)r * cols;
+		real *y = o + (long)r * cols;
+		real s = 0.0f;
 		for (int i = 0; i < cols; i++) s += x[i] * x[i];
-		float inv = 1.0f / sqrtf(s / (float)cols + 1e-6f);
+		real inv = 1.0f / LM(sqrt)(s / (real)cols + 1e-6f);
 		for (int i = 0; i < cols; i++) y[i] = x[i] * inv;
 	}
 }
 
-static float delta(const float *a, const float *b, int n)
+static real delta(const real *a, const real *b, int n)
 {
-	float d = 0.0f;
+	real d = 0.0f;
 	for (int i = 0; i < n; i++) {
-		float e = fabsf(a[i] - b[i]);
+		real e = LM(fabs)(a[i] - b[i]);
 		if (e > d) d = e;
 	}
 	return d;
 }
 
-static void copy(float *o, const float *a, long n)
+static void copy(real *o, const real *a, long n)
 {
 	if (o != a) memmove(o, a, (size_t)n * sizeof *o);
 }
@@ -314,10 +339,10 @@ static void exec_one(VM *vm, const tgo_ins *in)
 		if (in->stid >= 0) vm->steps[in->stid] = in->T;
 		return;
 	}
-	float *o = ptr(vm, in->out);
+	real *o = ptr(vm, in->out);
 	int n = m->val[in->out].n;
-	const float *a = in->na > 0 ? ptr(vm, in->a[0]) : NULL;
-	const float *c = in->na > 1 ? ptr(vm, in->a[1]) : NULL;
+	const real *a = in->na > 0 ? ptr(vm, in->a[0]) : NULL;
+	const real *c = in->na > 1 ? ptr(vm, in->a[1]) : NULL;
 	switch (in->op) {
 	case O_CONST: o[0] = in->k; break;
 	case O_ADD: case O_SUB: case O_MUL: case O_DIV: case O_MAX: case O_MIN: bin(vm, in, o, a, c); break;
@@ -332,7 +357,9 @@ static void exec_one(VM *vm, const tgo_ins *in)
 				matmul_f32(o + (long)g * mm * nn, a + (long)g * mm * kk, c + (long)g * kk * nn, mm, kk, nn);
 			break;
 		}
+#ifndef TGO_F64
 		if (tgo_matmul_hook) tgo_matmul_hook(tgo_hook_ctx, m, in, a, c);
+#endif
 		if (qa->qbits && tgo_q_axis_for(m, in->a[0], in) == qa->qaxis) matmul_qa(o, qa->q, qa->qbits, qa->qs, c, mm, kk, nn);
 		else if (qb->qbits && tgo_q_axis_for(m, in->a[1], in) == qb->qaxis) matmul_qb(o, a, qb->q, qb->qbits, qb->qs, mm, kk, nn);
 		else matmul_f32(o, a, c, mm, kk, nn);
@@ -349,9 +376,9 @@ static void exec_one(VM *vm, const tgo_ins *in)
 	case O_SUM:
 	case O_MEAN: {
 		int k = m->val[in->a[0]].n;
-		float s = 0.0f;
+		real s = 0.0f;
 		for (int i = 0; i < k; i++) s += a[i];
-		o[0] = in->op == O_SUM ? s : s / (float)k;
+		o[0] = in->op == O_SUM ? s : s / (real)k;
 		break;
 	}
 	case O_TRANSPOSE: {
@@ -373,8 +400,8 @@ static void exec_one(VM *vm, const tgo_ins *in)
 		const tgo_shape *s0 = &m->val[in->a[0]].sh;
 		int cnt = m->val[in->a[1]].sh.dim[0], d = s0->dim[0], h = tgo_numel(s0) / s0->dim[0];
 		for (int i = 0; i < cnt; i++) {
-			float rr = floorf(c[i] + 0.5f);
-			int t = rr >= 0.0f && rr < (float)d ? (int)rr : -1;
+			real rr = LM(floor)(c[i] + 0.5f);
+			int t = rr >= 0.0f && rr < (real)d ? (int)rr : -1;
 			for (int j = 0; j < h; j++) o[(long)i * h + j] = t >= 0 ? a[(long)t * h + j] : 0.0f;
 		}
 		break;
@@ -382,16 +409,16 @@ static void exec_one(VM *vm, const tgo_ins *in)
 	case O_THINK: {
 		copy(o, ptr(vm, in->init), n);
 		int it = 0;
-		float survive = 1.0f;
+		real survive = 1.0f;
 		while (it < in->maxit) {
 			exec(vm, in->body);
 			it++;
-			const float *y = ptr(vm, in->yield);
-			float d = delta(y, o, n);
+			const real *y = ptr(vm, in->yield);
+			real d = delta(y, o, n);
 			copy(o, y, n);
 			if (in->eps >= 0 && d <= in->eps) break;
 			if (in->halt >= 0) {
-				float p = *ptr(vm, in->halt);
+				real p = *ptr(vm, in->halt);
 				survive *= 1.0f - (p < 0.0f ? 0.0f : p > 1.0f ? 1.0f : p);
 				if (1.0f - survive > in->hthr) break;
 			}
@@ -407,7 +434,7 @@ static void exec(VM *vm, const tgo_block *b)
 	for (int i = 0; i < b->len; i++) exec_one(vm, &b->v[i]);
 }
 
-void tgo_run_row(const tgo_module *m, const float *in, float *out, int *steps, float *arena)
+void TGO_RUN_ROW(const tgo_module *m, const real *in, real *out, int *steps, real *arena)
 {
 	VM vm = { m, arena, in, steps };
 	exec(&vm, &m->top);

@@ -171,7 +171,8 @@ __global__ __launch_bounds__(ATT_TPB) void dec_attn_k(tgk_dec_attn_args a, int c
 // sum_k code_k q_k = s0 + 256 s1 + 65536 s2 (s_i = sum_k code_k digit_i,k by
 // 4-way int8 dot products), scaled by 2^(E-23) in f64, rounded once to f32
 // and multiplied by the channel scale; rows with inf, nan or an entry above
-// 2^100 take the reference's sequential f32 loop. One block per (head, 64
+// 2^100, and peaked rows (tg_qdigits.h), take the reference's sequential f32
+// loop. One block per (head, 64
 // columns): the rows' digits and the head's code tile sit in LDS; a wave
 // handles 4 rows at a time, a lane one column.
 // codes: int32 [NQ][HD/4][D], 4 consecutive k's int8 codes per word (k = 4
@@ -183,6 +184,8 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 	extern __shared__ int4 dg[]; // [rows][HD/4] digit words {d0, d1, d2, 0} of 4 k's
 	const int H4 = HD / 4, n = rows * H4;
 	int *Es = (int *)(dg + (long)rows * H4), *sp = Es + rows, *ct = sp + rows; // ct: [HD/4][64] code words
+	int *tin = ct + H4 * 64, *tbl = tin + rows; // per row: entries in the band, nonzero entries below it
+	float *bnd = (float *)(tbl + rows);         // per row: the band's floor
 	const int ctiles = (D + 63) / 64, g = blockIdx.x / ctiles, c0 = (blockIdx.x - g * ctiles) * 64;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	constexpr int U = 4, nw = WO_TPB / 64;
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 	};
 	// rows' max |x| (as bits: non-negative floats order as their bits) and flags
 	unsigned *mxb = (unsigned *)Es;
-	for (int t = tid; t < rows; t += WO_TPB) mxb[t] = 0, sp[t] = 0;
+	for (int t = tid; t < rows; t += WO_TPB) mxb[t] = 0, sp[t] = 0, tin[t] = 0, tbl[t] = 0;
 	for (int e = tid; e < H4 * 64; e += WO_TPB) {
 		const int k4 = e >> 6, c = e & 63;
 		ct[e] = c0 + c < D ? codes[((long)g * H4 + k4) * D + c0 + c] : 0;
@@ -215,7 +218,7 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 	for (int t = tid; t < rows; t += WO_TPB) {
 		const float mx = __uint_as_float(mxb[t]);
 		const int special = tgq_special(sp[t], mx);
-		Es[t] = tgq_exponent(mx, special), sp[t] = special;
+		Es[t] = tgq_exponent(mx, special), sp[t] = special, bnd[t] = tgq_band(mx);
 	}
 	__syncthreads();
 	for (int b = tid; b < n; b += U * WO_TPB) {
@@ -227,6 +230,16 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 			const int t = e / H4, E = Es[t];
 			const float xv[4] = { u[j].x, u[j].y, u[j].z, u[j].w };
 			unsigned w0 = 0, w1 = 0, w2 = 0;
+			if (!sp[t]) {
+				int in = 0, below = 0;
+				for (int i = 0; i < 4; i++) {
+					const float av = fabsf(xv[i]);
+					in += av >= bnd[t] && av != 0.0f;
+					below += av < bnd[t] && av != 0.0f;
+				}
+				if (in) atomicAdd(&tin[t], in);
+				if (below) atomicAdd(&tbl[t], below);
+			}
 			if (!sp[t])
 				for (int i = 0; i < 4; i++) {
 					const int q = (int)rintf(ldexpf(xv[i], 23 - E)); // exact: |q| < 2^23
@@ -239,6 +252,9 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 			dg[e] = make_int4((int)w0, (int)w1, (int)w2, 0);
 		}
 	}
+	__syncthreads();
+	for (int t = tid; t < rows; t += WO_TPB)
+		if (!sp[t]) sp[t] = tgq_peaked((long long)tin[t] + ((long long)tbl[t] << 32), HD);
 	__syncthreads();
 	const int c = lane;
 	if (c0 + c >= D) return;
@@ -297,22 +313,24 @@ __device__ inline long long blk_sum(long long v, long long *red)
 	return t;
 }
 
-// digits of row m, values z[0 .. Kp) in LDS (zero from the row's length on),
-// from this thread's share of max |z| and of the non-finite flag
-__device__ inline void blk_digits(const float *z, int Kp, float mx, int bad, const tgk_qdig &q, int m, float *redf, long long *redl)
+// digits of row m of K inputs, values z[0 .. Kp) in LDS (zero from K on), from
+// this thread's share of max |z| and of the non-finite flag
+__device__ inline void blk_digits(const float *z, int K, int Kp, float mx, int bad, const tgk_qdig &q, int m, float *redf, long long *redl)
 {
 	const float amax = blk_max(mx, redf); // nan never wins fmaxf; such rows are flagged by bad
 	const int anybad = __syncthreads_or(bad);
 	const int special = tgq_special(anybad, amax), E = tgq_exponent(amax, special);
+	const float band = tgq_band(amax);
 	int8_t *blk = tgq_row_base(q.dig, m, Kp);
-	long long qs = 0;
+	long long qs = 0, tl = 0;
 	for (int j = threadIdx.x; j < Kp / 16; j += blockDim.x) {
 		float v[16];
 		for (int u = 0; u < 16; u++) v[u] = z[16 * j + u];
-		qs += tgq_put16(blk, 16 * j, v, E, special);
+		qs += tgq_put16(blk, 16 * j, v, E, special, band, tl);
 	}
 	qs = blk_sum(qs, redl);
-	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = special, q.qsum[m] = qs;
+	tl = blk_sum(tl, redl);
+	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = special || tgq_peaked(tl, K), q.qsum[m] = qs;
 }
 
 // tgk_dec_norm: one block per token row, NORM_TPB threads, each with at most
@@ -381,7 +399,7 @@ __global__ __launch_bounds__(NORM_TPB) void dec_norm_k(tgk_dec_norm_args a)
 		mx = fmaxf(mx, fabsf(nv));
 	}
 	__syncthreads();
-	blk_digits(z, Kp, mx, bad, a.q, t, redf, redl);
+	blk_digits(z, D, Kp, mx, bad, a.q, t, redf, redl);
 }
 
 // tgk_dec_hnorm: one wave per head line (4 per block, no block barrier:
@@ -423,15 +441,16 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 		bad |= __shfl_xor(bad, o);
 	}
 	const int special = tgq_special(bad, mx), E = tgq_exponent(mx, special);
+	const float band = tgq_band(mx);
 	int8_t *blk = tgq_row_base(a.q.dig, L, Kp);
-	long long qs = 0;
+	long long qs = 0, tl = 0;
 	for (int g = lane; g < Kp / 16; g += 64) {
 		float v[16];
 		for (int u = 0; u < 16; u++) v[u] = z[16 * g + u];
-		qs += tgq_put16(blk, 16 * g, v, E, special);
+		qs += tgq_put16(blk, 16 * g, v, E, special, band, tl);
 	}
-	for (int o = 32; o > 0; o >>= 1) qs += __shfl_xor(qs, o);
-	if (lane == 0) a.q.e[L] = E, a.q.special[L] = special, a.q.qsum[L] = qs;
+	for (int o = 32; o > 0; o >>= 1) qs += __shfl_xor(qs, o), tl += __shfl_xor(tl, o);
+	if (lane == 0) a.q.e[L] = E, a.q.special[L] = special || tgq_peaked(tl, HD), a.q.qsum[L] = qs;
 }
 
 // Many lines at once (a prompt's token rows, or its head lines): a block of
@@ -553,19 +572,20 @@ __global__ __launch_bounds__(NL_TPB) void norm_lines_k(NormLines a)
 		bad |= __shfl_xor(bad, o);
 	}
 	const int special = tgq_special(bad, mx), E = tgq_exponent(mx, special);
-	long long qs = 0;
+	const float band = tgq_band(mx);
+	long long qs = 0, tl = 0;
 	if (L0 + l < a.lines) {
 		int8_t *blk = tgq_row_base(a.q.dig, (int)(L0 + l), Kp);
 		for (int gi = k; gi < Kp / 16; gi += TPL) {
 			float w16[16];
 			for (int q = 0; q < 16; q++) w16[q] = zl[gi * 16 + q];
-			qs += tgq_put16(blk, gi * 16, w16, E, special);
+			qs += tgq_put16(blk, gi * 16, w16, E, special, band, tl);
 		}
 	}
-	for (int o = 1; o < TPL; o <<= 1) qs += __shfl_xor(qs, o);
+	for (int o = 1; o < TPL; o <<= 1) qs += __shfl_xor(qs, o), tl += __shfl_xor(tl, o);
 	if (k == 0 && L0 + l < a.lines) {
 		const long L = L0 + l;
-		a.q.e[L] = E, a.q.special[L] = special, a.q.qsum[L] = qs;
+		a.q.e[L] = E, a.q.special[L] = special || tgq_peaked(tl, D), a.q.qsum[L] = qs;
 	}
 }
 
@@ -592,7 +612,7 @@ __global__ __launch_bounds__(1024) void dec_silu_k(tgk_dec_silu_args a)
 		zs[i] = v;
 	}
 	__syncthreads();
-	blk_digits(zs, a.Kp, mx, bad, a.q, t, redf, redl);
+	blk_digits(zs, FF, a.Kp, mx, bad, a.q, t, redf, redl);
 }
 
 // A prompt chunk's causal softmax of one head's scores, line (sequence, t)
@@ -786,7 +806,7 @@ void tgk_dec_causal_softmax(hipStream_t s, float *sc, int T0, long nlines, float
 	causal_softmax_k<<<(unsigned)((nlines + lpb - 1) / lpb), 256, (size_t)lpb * stride * 4 + lpb * 4, s>>>(sc, T0, nlines, scale, lpb, stride);
 }
 
-size_t tgk_dec_wo_lds(int rows, int HD) { return (size_t)rows * HD * 4 + (size_t)rows * 8 + (size_t)HD * 64; }
+size_t tgk_dec_wo_lds(int rows, int HD) { return (size_t)rows * HD * 4 + (size_t)rows * 20 + (size_t)HD * 64; }
 
 void tgk_dec_wo(hipStream_t s, const float *att, const int *codes, const float *scales, float *out, int rows, int NQ, int HD, int D)
 {

@@ -12,9 +12,11 @@
 // reference's own f32 summation error at these K. Every step depends on the
 // row alone, so a row's outputs do not depend on the batch it came in.
 //
-// Rows with a non-finite or huge entry are flagged by the digit kernel and
-// their outputs are recomputed in the epilogue with the reference's exact
-// sequential f32 loop, so inf/nan propagate as they do in the reference.
+// Rows with a non-finite or huge entry, and peaked rows (a few entries far
+// above all others, tg_qdigits.h), are flagged by the digit kernel and their
+// outputs are recomputed in the epilogue with the reference's exact
+// sequential f32 loop, so inf/nan propagate as they do in the reference and
+// an outlier does not coarsen the other entries of its row.
 //
 // Operand layouts in global memory are the MFMA fragment order of
 // v_mfma_i32_32x32x32_i8 (lane l holds row or channel l % 32 and inputs
@@ -148,19 +150,21 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 	tgq_scan_end(mb, mx, bad);
 	const float amax = wave_max(mx); // a NaN lane reads 0 here; its row is flagged by `bad`
 	const int special = tgq_special(__any(bad), amax), E = tgq_exponent(amax, special);
-	long long qs = 0;
+	const float band = tgq_band(amax);
+	long long qs = 0, tl = 0;
 	int8_t *blk = tgq_row_base(s.dig, m, Kp);
 	for (int t0 = 0; t0 < nsl; t0 += SL) {
 		if (nsl > SL) fetch(t0); // rows of up to SL slabs are still in v
 		for (int t = 0; t < SL; t++) {
 			const int k0 = (t0 + t) * 1024 + lane * 16;
-			if (t0 + t < nsl && k0 < Kp) qs += tgq_put16(blk, k0, v[t], E, special || k0 >= K);
+			if (t0 + t < nsl && k0 < Kp) qs += tgq_put16(blk, k0, v[t], E, special || k0 >= K, band, tl);
 		}
 	}
 	qs = wave_sum(qs);
+	tl = wave_sum(tl);
 	if (lane == 0) {
 		s.e[m] = E;
-		s.special[m] = special;
+		s.special[m] = special || tgq_peaked(tl, K);
 		s.qsum[m] = qs;
 	}
 }
@@ -176,7 +180,7 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 {
 	__shared__ float smx[16][64];
 	__shared__ int sbad[16][64];
-	__shared__ long long sqs[16][64];
+	__shared__ long long sqs[16][64], stl[16][64];
 	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
 	const int m0 = blockIdx.x * 16, mr = lane & 15, half = (lane >> 4) & 1, par = lane >> 5;
 	const float *x = xrow(a, m0 + mr < M ? m0 + mr : M - 1); // rows past M repeat row M - 1
@@ -202,20 +206,22 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 			bad |= sbad[u][mr + 16 * q];
 		}
 	const int special = tgq_special(bad, amax), E = tgq_exponent(amax, special);
+	const float band = tgq_band(amax);
 	int8_t *blk = s.dig + (long)(m0 >> 5) * nkb * 3072 + ((m0 & 31) + mr) * 16;
-	long long qs = 0;
+	long long qs = 0, tl = 0;
 	for (int j = 0; j < NKB; j++) {
 		const int kb = 2 * (w + j * W) + par;
-		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K);
+		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K, band, tl);
 	}
 	sqs[w][lane] = qs;
+	stl[w][lane] = tl;
 	__syncthreads();
 	if (w == 0 && lane < 16 && m0 + mr < M) {
-		long long t = 0;
+		long long t = 0, u2 = 0;
 		for (int u = 0; u < W; u++)
-			for (int q = 0; q < 4; q++) t += sqs[u][mr + 16 * q];
+			for (int q = 0; q < 4; q++) t += sqs[u][mr + 16 * q], u2 += stl[u][mr + 16 * q];
 		s.e[m0 + mr] = E;
-		s.special[m0 + mr] = special;
+		s.special[m0 + mr] = special || tgq_peaked(u2, K);
 		s.qsum[m0 + mr] = t;
 	}
 }
@@ -229,7 +235,7 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 {
 	__shared__ float smx[4];
 	__shared__ int sbad[4];
-	__shared__ long long sqs[4];
+	__shared__ long long sqs[4], stl[4];
 	const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, ng = Kp / 16;
 	const float *x = xrow(a, m);
 	float v[G][16];
@@ -248,18 +254,20 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 	__syncthreads();
 	const float amax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
 	const int special = tgq_special(sbad[0] | sbad[1] | sbad[2] | sbad[3], amax), E = tgq_exponent(amax, special);
+	const float band = tgq_band(amax);
 	int8_t *blk = tgq_row_base(s.dig, m, Kp);
-	long long qs = 0;
+	long long qs = 0, tl = 0;
 	for (int g = 0; g < G; g++) {
 		const int j = tid + g * 256;
-		if (j < ng) qs += tgq_put16(blk, j * 16, v[g], E, special || j * 16 >= K);
+		if (j < ng) qs += tgq_put16(blk, j * 16, v[g], E, special || j * 16 >= K, band, tl);
 	}
 	qs = wave_sum(qs);
-	if (lane == 0) sqs[w] = qs;
+	tl = wave_sum(tl);
+	if (lane == 0) sqs[w] = qs, stl[w] = tl;
 	__syncthreads();
 	if (tid == 0) {
 		s.e[m] = E;
-		s.special[m] = special;
+		s.special[m] = special || tgq_peaked(stl[0] + stl[1] + stl[2] + stl[3], K);
 		s.qsum[m] = sqs[0] + sqs[1] + sqs[2] + sqs[3];
 	}
 }
@@ -277,7 +285,7 @@ __global__ __launch_bounds__(1024) void digits_tile_k(tgk_qgemm_args a, Scratch 
 {
 	__shared__ float smx[16][64];
 	__shared__ int sbad[16][64];
-	__shared__ long long sqs[16][64];
+	__shared__ long long sqs[16][64], stl[16][64];
 	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
 	const int m0 = blockIdx.x * 32, half = lane >> 5, mr = lane & 31;
 	const float *x = xrow(a, m0 + mr < M ? m0 + mr : M - 1); // rows past M repeat row M - 1
@@ -303,19 +311,21 @@ __global__ __launch_bounds__(1024) void digits_tile_k(tgk_qgemm_args a, Scratch 
 		bad |= sbad[u][mr] | sbad[u][mr + 32];
 	}
 	const int special = tgq_special(bad, amax), E = tgq_exponent(amax, special);
+	const float band = tgq_band(amax);
 	int8_t *blk = s.dig + (long)blockIdx.x * nkb * 3072 + mr * 16;
-	long long qs = 0;
+	long long qs = 0, tl = 0;
 	for (int j = 0; j < NKB; j++) {
 		const int kb = w + j * W;
-		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K);
+		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K, band, tl);
 	}
 	sqs[w][lane] = qs;
+	stl[w][lane] = tl;
 	__syncthreads();
 	if (w == 0 && half == 0 && m0 + mr < M) {
-		long long t = 0;
-		for (int u = 0; u < W; u++) t += sqs[u][mr] + sqs[u][mr + 32];
+		long long t = 0, u2 = 0;
+		for (int u = 0; u < W; u++) t += sqs[u][mr] + sqs[u][mr + 32], u2 += stl[u][mr] + stl[u][mr + 32];
 		s.e[m0 + mr] = E;
-		s.special[m0 + mr] = special;
+		s.special[m0 + mr] = special || tgq_peaked(u2, K);
 		s.qsum[m0 + mr] = t;
 	}
 }

@@ -8,6 +8,23 @@
 // with a non-finite entry or max |x| above 2^100 are "special": their digits
 // are zero and the GEMM's epilogue runs the reference's sequential loop.
 //
+// Peaked rows are special too. The grid step 2^(E-23) is set by the largest
+// entry; when a few entries stand far above all the others (an outlier
+// channel), the others lose precision on that grid, and the reference's
+// sequential sum, which never sees the outlier on a channel whose code is 0,
+// would be the more accurate. The band of a row is |x| >= max|x| / 4. A row
+// is peaked when some nonzero entry lies below its band and at most
+// tgq_peak_max(K) entries lie in it (8, or max(1, K / 4) for K < 32): then
+// max|x| is at most 4 times the row's 9th largest |x| (its largest for
+// short rows), so the grid step stays within a small factor of what the
+// bulk of the row would set. Gaussian-like rows of 64 or more entries are
+// never peaked (the band holds about a third of them), rows whose entries
+// are a few values and zeros (one-hot, {0, 1}) neither; a single entry 14
+// or more standard deviations out is. Every quantity is a count, so the
+// decision does not depend on the order of any sum. Peaked rows are found
+// after their digits are written (the counts come with the sum of q); their
+// digits are then unused.
+//
 // Layout (the MFMA fragment order of v_mfma_i32_32x32x32_i8):
 //   digits [row / 32][k / 32][digit 0..2][lane 0..63][16 bytes],
 //   lane = row % 32 + 32 ((k % 32) / 16).
@@ -29,6 +46,24 @@ __device__ inline void tgq_split3(int q, int &d0, int &d1, int &d2)
 
 // a row is special when an entry is not finite (bad) or max |x| exceeds 2^100
 __device__ inline int tgq_special(int bad, float amax) { return bad || amax > 0x1p100f; }
+
+// the peak test (see above): the band's floor, the per-16 tally (entries in
+// the band + 2^32 nonzero entries below it), and the decision from a row's
+// whole tally
+constexpr int TGQ_BAND_SHIFT = 2, TGQ_PEAK_N = 8;
+__device__ inline float tgq_band(float amax) { return ldexpf(amax, -TGQ_BAND_SHIFT); }
+__device__ inline int tgq_peak_max(int K) { return K >= 4 * TGQ_PEAK_N ? TGQ_PEAK_N : K >= 8 ? K >> 2 : 1; }
+__device__ inline long long tgq_tally16(const float *v, float band)
+{
+	int in = 0, below = 0;
+	for (int i = 0; i < 16; i++) {
+		const float a = fabsf(v[i]);
+		in += a >= band && a != 0.0f;
+		below += a < band && a != 0.0f;
+	}
+	return (long long)in + ((long long)below << 32);
+}
+__device__ inline int tgq_peaked(long long tally, int K) { return (tally >> 32) > 0 && (tally & 0xffffffffll) <= tgq_peak_max(K); }
 
 // the row exponent E from max |x| (0 for special or all-zero rows)
 __device__ inline int tgq_exponent(float amax, int special)
@@ -78,13 +113,15 @@ __device__ inline void tgq_scan_end(unsigned mb, float &mx, int &nan)
 }
 
 // digits of 16 consecutive inputs (inputs k0 .. k0 + 15 of the row at blk)
-// into their three 16-byte chunks; zero digits when `zero`; returns the sum of q.
+// into their three 16-byte chunks; zero digits when `zero`; returns the sum of
+// q and adds the inputs' peak tally (band = tgq_band(max |x|)) to `tally`
+// (nothing for a `zero` group).
 // With u = q + 0x808080 (|q| <= 8355328, so 0 <= u < 2^24), byte l of u is
 // d_l + 128: the balanced digits are u's bytes with the top bit flipped. The
 // bytes of four inputs are gathered into each plane's 32-bit word with byte
 // permutes (v_perm_b32 selects bytes of a register pair: 0-3 the second
 // operand's, 4-7 the first's, 12 a zero byte).
-__device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E, bool zero)
+__device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E, bool zero, float band, long long &tally)
 {
 	int8_t *p = blk + (k0 >> 5) * 3072 + ((k0 >> 4) & 1) * 512;
 	if (__builtin_expect(zero, 0)) {
@@ -93,6 +130,7 @@ __device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E
 		*(tgq_v4i *)(p + 2048) = tgq_v4i{0, 0, 0, 0};
 		return 0;
 	}
+	tally += tgq_tally16(v, band);
 	unsigned w0[4], w1[4], w2[4];
 	int qs = 0; // |sum of 16 q| < 2^27
 	{

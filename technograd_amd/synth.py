@@ -251,6 +251,20 @@ def linear_tgir(name, W, bits):
     ])
 
 
+def linear_tgir_codes(name, codes, scales, bits, axis=1):
+    """One quantized product with the given codes (int8 values, the param's
+    own layout) and per-channel scales: x @ W for axis 1 (W [K][C]), W @ x
+    for axis 0 (W [C][K])."""
+    codes = np.asarray(codes, np.int8)
+    if axis == 1:
+        K, C = codes.shape
+        body = "  (input x (f32 %d))\n  (block\n    (%%0 (f32 %d) (matmul x W))\n  )\n  (output %%0))\n" % (K, C)
+    else:
+        C, K = codes.shape
+        body = "  (input x (f32 %d))\n  (block\n    (%%0 (f32 %d) (matmul W x))\n  )\n  (output %%0))\n" % (K, C)
+    return "(tgir 1\n  (model %s)\n" % name + param_quant("W", codes, scales, bits, axis) + body
+
+
 # ---- BASELINE.json configurations ----
 
 def config1(rows=65536):

@@ -2,10 +2,16 @@
 (parity.digit_path_matmul), which the GPU launch-shape tests compare against
 bit for bit, pinned on the CPU: to the exact real product within the 24-bit
 activation grid's bound, to the reference's sequential order (the oracle)
-within the parity bound, and on cases whose answer is fixed by hand."""
+under the parity predicate, on rows with outliers (the peak test sends them
+to the reference's loop, and without it the predicate fails), and on cases
+whose answer is fixed by hand."""
 import numpy as np
+import pytest
 
-from parity import digit_path_matmul, qmatmul_bound, ulp
+from oracle import oracle as O
+from technograd_amd import synth
+from parity import (check_qmatmul, device_path_matmul, digit_path_matmul, grid_bound, outlier_rows, peaked_rows,
+                    reference_loop, ulp)
 
 
 def _case(seed, M=7, K=96, C=40, lim=7):
@@ -23,24 +29,55 @@ def test_within_the_grid_bound_of_the_exact_product():
         x, codes, scales = _case(seed)
         got, special = digit_path_matmul(x, codes, scales)
         truth = (x.astype(np.float64) @ codes.astype(np.float64)) * scales.astype(np.float64)
-        grid = 2.0 ** -23 * np.abs(x).max(axis=1)[:, None].astype(np.float64) * np.abs(codes).sum(axis=0)[None, :] * scales
         assert not special.any()
-        assert (np.abs(got - truth) <= grid + 2 * ulp(truth)).all()
+        assert (np.abs(got - truth) <= grid_bound(codes.T, scales, x) + 2 * ulp(truth)).all()
 
 
-def test_within_the_parity_bound_of_the_reference_order():
+def test_within_the_parity_predicate_of_the_reference_order():
     for seed in range(3):
         x, codes, scales = _case(seed + 10)
         got, _ = digit_path_matmul(x, codes, scales)
-        ref = np.zeros_like(got)  # the reference's loop: f32 adds in k order, then the scale
-        for m in range(x.shape[0]):
-            for c in range(codes.shape[1]):
-                acc = np.float32(0)
-                for k in range(x.shape[1]):
-                    acc = np.float32(acc + np.float32(codes[k, c]) * x[m, k])
-                ref[m, c] = np.float32(scales[c] * acc)
-        bound = qmatmul_bound(codes.T, scales, x) + 2 * ulp(ref)
-        assert (np.abs(got.astype(np.float64) - ref) <= bound).all()
+        ref = reference_loop(x, codes, scales)
+        check_qmatmul(got, ref, codes.T, scales, x)
+
+
+def test_reference_loop_is_the_oracle():
+    """parity.reference_loop (used for special rows below) equals the oracle's
+    quantized product bit for bit, both axes' layout as x @ W."""
+    rng = np.random.default_rng(4)
+    codes = rng.integers(-7, 8, size=(300, 20)).astype(np.int8)
+    scales = rng.uniform(0.001, 0.1, size=20).astype(np.float32)
+    x = rng.normal(size=(5, 300)).astype(np.float32)
+    x[1, 9] = 1e5
+    text = synth.linear_tgir_codes("lq", codes, scales, 4, axis=1)
+    want, _ = O.Model(text).batch(x)
+    assert np.array_equal(reference_loop(x, codes, scales).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_outlier_rows_against_the_oracle(bits):
+    """K = 4096: rows with one outlier of 1e2 to 1e6 on a zero-code column,
+    cancelling outliers, a 14 sigma entry, and dense rows. What the device
+    computes (the digit path, the reference's loop for special rows) against
+    the oracle: peaked rows are special and bit-identical with the oracle; the
+    rest pass the parity predicate. With the peak test taken out (the per-row
+    grid for every row), the predicate fails."""
+    K, C = 4096, 256
+    lim = 7 if bits == 4 else 127
+    rng = np.random.default_rng(bits)
+    codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)
+    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
+    x, want_special = outlier_rows(K, codes)
+    assert np.array_equal(peaked_rows(x), want_special)
+    text = synth.linear_tgir_codes("lq", codes, scales, bits, axis=1)
+    ref, _ = O.Model(text).batch(x)
+    got, special = device_path_matmul(x, codes, scales)
+    assert np.array_equal(special, want_special)
+    assert np.array_equal(got[special].view(np.uint32), ref[special].view(np.uint32))
+    check_qmatmul(got, ref, codes.T, scales, x)
+    coarse, _ = device_path_matmul(x, codes, scales, peak=False)
+    with pytest.raises(AssertionError):
+        check_qmatmul(coarse, ref, codes.T, scales, x)
 
 
 def test_hand_cases():

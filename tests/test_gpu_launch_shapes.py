@@ -2,12 +2,13 @@
 launch_gemm): the large-batch LDS kernel and each (NB column blocks, W waves)
 instantiation of the small-batch kernel, int4 and int8 weights, checked bit
 for bit against the path's own arithmetic restated on the host
-(tests/parity.py: digit_path_matmul). The reference-order parity of the same
+(tests/parity.py: device_path_matmul: the digit path, and the reference's
+loop for a peaked row). The reference-order parity of the same
 entry point is in test_gpu_parity.py."""
 import numpy as np
 import pytest
 
-from parity import digit_path_matmul
+from parity import device_path_matmul
 
 pytestmark = pytest.mark.gpu
 
@@ -49,10 +50,12 @@ def test_launch_shape_bit_exact(bits_, M, K, C):
     else:
         packed = codes.ravel()
     x = rng.normal(size=(M, K)).astype(np.float32)
-    x[0, : min(K, 5)] *= 1e3  # rows of different magnitudes: different exponents per row
+    x[0] *= 1e3  # rows of different magnitudes: different exponents per row
     if M > 2:
         x[2] *= 1e-30
+    if M > 3:
+        x[3, K // 3] = 1e4  # an outlier: a peaked row, the reference's loop
     got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
-    want, special = digit_path_matmul(x, codes, scales)
-    assert not special.any()
+    want, special = device_path_matmul(x, codes, scales)
+    assert special.sum() == (M > 3)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.argwhere(got != want)[:5].tolist()
