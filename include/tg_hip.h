@@ -95,6 +95,25 @@ void *tg_hip_get_stream(const tg_hip_prog *p);
 int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, const float *b, int m, int k, int n, int axis,
 		    int flags);
 
+/* tg_hip_matmul_q's matrix-core path without any device allocation. No
+ * counterpart in the reference: for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Device buffers: d_q codes and d_s scales in the reference layout and meaning
+ * of tg_hip_matmul_q, d_b the activations, d_o the output (caller-owned).
+ * Asynchronous on `stream` (a hipStream_t; NULL: the null stream). Packed
+ * weights and activation digits go to a fixed device array of
+ * TG_HIP_NOALLOC_SCRATCH bytes that the library holds on every GPU it runs on
+ * until the process ends; a call needs about ceil(C/256)*256 x ceil(K/64)*64
+ * x bits/8 bytes of packed weights plus 3 x ceil(M/128)*128 x ceil(K/64)*64
+ * bytes of digits (C channels, K inputs, M activation rows: config 2's
+ * 4096 x 4096 int4 layer fits at up to 4096 rows); larger calls return -2
+ * with the sizes in tg_hip_error(). Every call on a GPU uses that GPU's one
+ * array: calls that overlap on one GPU (other streams, other threads) race
+ * and must be serialised by the caller. 0 on success. */
+#define TG_HIP_NOALLOC_SCRATCH (64u << 20)
+int tg_hip_matmul_q_noalloc(float *d_o, const signed char *d_q, int bits, const float *d_s, const float *d_b, int m, int k, int n,
+			    int axis, void *stream);
+
 void tg_hip_free(tg_hip_prog *p);
 const char *tg_hip_error(void);
 int tg_hip_stats(const tg_hip_prog *p, tg_hip_stats_t *st);

@@ -803,7 +803,53 @@ void launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 	}
 }
 
+// The repacking of tgk_qweight_pack done on the device, from codes already in
+// device memory: one thread per packed byte (and per padded scale), every
+// byte of the packed area written (padding: code 0).
+__global__ __launch_bounds__(256) void qweight_pack_k(uint8_t *pw, float *ps, const uint8_t *codes, const float *scale, int bits,
+						      int axis, int C, int K, int Kp, int Cp)
+{
+	const long kblocks = Kp / 32, lb = bits == 8 ? 16 : 8, nb = (long)Cp * Kp * bits / 8;
+	tgk_qweight w{};
+	w.orig = (uint8_t *)codes, w.bits = bits, w.axis = axis, w.C = C, w.K = K;
+	auto code = [&](int c, int k) { return c < C && k < K ? code_orig(w, c, k) : 0; };
+	for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < nb + Cp; i += (long)gridDim.x * blockDim.x) {
+		if (i >= nb) { // the scales, padded with zeros to Cp
+			const int c = (int)(i - nb);
+			ps[c] = c < C ? scale[c] : 0.0f;
+			continue;
+		}
+		const long frag = i / (64 * lb), cb = frag / kblocks, kb = frag - cb * kblocks;
+		const int lane = (int)((i / lb) & 63), b = (int)(i % lb);
+		const int c = (int)(cb * 32 + (lane & 31)), k0 = (int)(kb * 32 + (lane >> 5) * 16);
+		if (bits == 8) pw[i] = (uint8_t)(int8_t)code(c, k0 + b);
+		else pw[i] = (uint8_t)((unsigned)(code(c, k0 + b) + 8) | ((unsigned)(code(c, k0 + b + 8) + 8) << 4));
+	}
+}
+
 } // namespace
+
+size_t tgk_qweight_dev_bytes(int bits, int C, int K)
+{
+	const long Kp = round_up(K, KB), Cp = round_up(C, BN);
+	return (size_t)round_up(Cp * Kp * bits / 8, 256) + (size_t)round_up(Cp * 4, 256);
+}
+
+int tgk_qweight_pack_dev(tgk_qweight *w, void *dst, const uint8_t *codes, const float *scale, int bits, int axis, int C, int K,
+			 hipStream_t st)
+{
+	memset(w, 0, sizeof *w);
+	w->C = C, w->K = K, w->bits = bits, w->axis = axis;
+	w->Kp = (int)round_up(K, KB);
+	w->Cp = (int)round_up(C, BN);
+	w->w = (uint8_t *)dst;
+	w->scale = (float *)((uint8_t *)dst + round_up((long)w->Cp * w->Kp * bits / 8, 256));
+	w->orig = (uint8_t *)codes;
+	const long n = (long)w->Cp * w->Kp * bits / 8 + w->Cp;
+	const long blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+	qweight_pack_k<<<(unsigned)blocks, 256, 0, st>>>(w->w, w->scale, codes, scale, bits, axis, C, K, w->Kp, w->Cp);
+	return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, int bits, int axis, int C, int K, hipStream_t st)
 {

@@ -51,6 +51,30 @@ bool hipok(hipError_t e, const char *what)
 	return false;
 }
 
+// Scratch of tg_hip_matmul_q_noalloc: packed weights, padded scales and the
+// activation digits of one call, in device memory every GPU the library runs
+// on holds from module load until the process ends. In host code `scratch`
+// is only a stand-in for the symbol: its device address on each GPU comes
+// from hipGetSymbolAddress (scratch_on), and only that address is used.
+static __device__ __align__(256) uint8_t scratch[TG_HIP_NOALLOC_SCRATCH];
+
+constexpr int MAX_DEVICES = 64;
+void *g_scratch[MAX_DEVICES]; // scratch's address on each device, set once by scratch_on
+
+// scratch's address on `device` (the current device), looked up once per device
+void *scratch_on(int device)
+{
+	if (device < 0 || device >= MAX_DEVICES) {
+		seterr("device %d: beyond the %d devices the scratch table covers", device, MAX_DEVICES);
+		return nullptr;
+	}
+	void *p = __atomic_load_n(&g_scratch[device], __ATOMIC_ACQUIRE);
+	if (p) return p;
+	if (!hipok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)") || !p) return nullptr;
+	__atomic_store_n(&g_scratch[device], p, __ATOMIC_RELEASE);
+	return p;
+}
+
 enum { SP_ARENA, SP_IN, SP_POOL, SP_OUT, SP_NONE };
 
 struct Opnd {
@@ -1818,7 +1842,8 @@ extern "C" {
 
 int tg_hip_init(int device)
 {
-	return hipok(hipSetDevice(device), "hipSetDevice") ? 0 : -1;
+	if (!hipok(hipSetDevice(device), "hipSetDevice")) return -1;
+	return scratch_on(device) ? 0 : -1; // the no-allocation entry point's scratch on this device
 }
 
 tg_hip_prog *tg_hip_load(const char *tgir, size_t len, int flags, int max_rows)
@@ -1990,6 +2015,46 @@ int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, co
 		if (x) (void)hipFree(x);
 	(void)hipStreamDestroy(st);
 	return rc;
+}
+
+int tg_hip_matmul_q_noalloc(float *d_o, const signed char *d_q, int bits, const float *d_s, const float *d_b, int m, int k, int n,
+			    int axis, void *stream)
+{
+	if ((bits != 8 && bits != 4) || (axis != 0 && axis != 1) || m < 1 || k < 1 || n < 1 || !d_o || !d_q || !d_s || !d_b) {
+		seterr("tg_hip_matmul_q_noalloc: bad arguments");
+		return -1;
+	}
+	const int C = axis == 0 ? m : n, K = k, M = axis == 0 ? n : m;
+	const size_t wb = tgk_qweight_dev_bytes(bits, C, K), Kp = (size_t)(K + 63) / 64 * 64;
+	const size_t need = wb + tgk_qgemm_scratch(M, (int)Kp);
+	if (need > TG_HIP_NOALLOC_SCRATCH) {
+		seterr("tg_hip_matmul_q_noalloc: %d x %d weights with %d activation rows need %zu bytes of scratch, more than "
+		       "the %u the library holds (TG_HIP_NOALLOC_SCRATCH)", C, K, M, need, (unsigned)TG_HIP_NOALLOC_SCRATCH);
+		return -2;
+	}
+	int dev = 0;
+	if (!hipok(hipGetDevice(&dev), "hipGetDevice")) return -1;
+	uint8_t *scr = (uint8_t *)scratch_on(dev);
+	if (!scr) return -1;
+	hipStream_t st = (hipStream_t)stream;
+	tgk_qweight w;
+	if (tgk_qweight_pack_dev(&w, scr, (const uint8_t *)d_q, d_s, bits, axis, C, K, st)) {
+		seterr("tg_hip_matmul_q_noalloc: weight packing launch failed");
+		return -1;
+	}
+	tgk_qgemm_args a{};
+	a.w = &w;
+	a.x = d_b;
+	a.o = d_o;
+	if (axis == 0) { // rows j of b^T: element k at k * n
+		a.ni = n, a.xr = 0, a.xj = 1, a.xk = n, a.M = n;
+		a.orr = 0, a.oc = n, a.oj = 1;
+	} else {
+		a.ni = m, a.xr = 0, a.xj = k, a.xk = 1, a.M = m;
+		a.orr = 0, a.oc = 1, a.oj = n;
+	}
+	tgk_qgemm(st, &a, scr + wb); // digits, then the matrix-core product (every byte they read is written first)
+	return hipok(hipGetLastError(), "tg_hip_matmul_q_noalloc launch") ? 0 : -1;
 }
 
 void tg_hip_free(tg_hip_prog *p) { destroy(p); }

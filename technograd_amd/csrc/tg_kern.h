@@ -208,6 +208,14 @@ int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, i
 /* the same from int8 codes one per element, laid out [C][K] (axis 0) */
 int tgk_qweight_pack_i8(tgk_qweight *w, const int8_t *codes, const float *scale, int bits, int C, int K, hipStream_t s);
 void tgk_qweight_free(tgk_qweight *w);
+/* The same repacking on the device from codes and scales already in device
+ * memory (codes in the param's own layout, as tgk_qweight_pack takes them),
+ * into caller memory at dst of tgk_qweight_dev_bytes(bits, C, K) bytes
+ * (256-byte aligned); w->orig points at the caller's codes. Nothing is
+ * allocated; asynchronous on s. Not freed with tgk_qweight_free. */
+size_t tgk_qweight_dev_bytes(int bits, int C, int K);
+int tgk_qweight_pack_dev(tgk_qweight *w, void *dst, const uint8_t *codes, const float *scale, int bits, int axis, int C, int K,
+			 hipStream_t s);
 
 /* Output segments of a merged GEMM (several weights that read the same
  * activations, concatenated along C): columns seg_c0[s] .. seg_c0[s + 1] - 1

@@ -42,6 +42,7 @@ def lib():
         L.tg_hip_batch_device.argtypes = [vp, vp, ctypes.c_long, vp, vp]
         L.tg_hip_sync.argtypes = [vp]
         L.tg_hip_matmul_q.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip, ip, ip]
+        L.tg_hip_matmul_q_noalloc.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip, ip, vp]
         L.tg_hip_quantize_rtn.argtypes = [vp, ip, ip, ip, ip, vp, vp, ip]
         L.tg_hip_dec_create.restype = vp
         L.tg_hip_dec_create.argtypes = [vp, ip, ip, ip]
@@ -177,6 +178,18 @@ def matmul_q(q, bits, s, b, m, k, n, axis, flags=0):
     o = np.empty((m, n), np.float32)
     _check(lib().tg_hip_matmul_q(_p(o), _p(q), bits, _p(s), _p(b), m, k, n, axis, flags), "tg_hip_matmul_q")
     return o
+
+
+def matmul_q_noalloc(d_o, d_q, bits, d_s, d_b, m, k, n, axis, stream=None):
+    """tg_hip_matmul_q_noalloc: device pointers (ints), asynchronous on
+    `stream` (None: the null stream). Returns the C status (0, or -2 when the
+    call is larger than the library's fixed scratch; the message is in
+    error())."""
+    return lib().tg_hip_matmul_q_noalloc(d_o, d_q, bits, d_s, d_b, m, k, n, axis, stream)
+
+
+def error():
+    return lib().tg_hip_error().decode()
 
 
 def quantize_rtn(w, bits, axis, threads=None):
