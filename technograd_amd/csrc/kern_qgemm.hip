@@ -385,21 +385,29 @@ __device__ inline float *out_at(const tgk_qgemm_args &a, int r, int jj, int c)
 // the output as the instruction after the product would compute it
 __device__ inline float act(const tgk_qgemm_args &a, float v) { return a.act == TGK_ACT_TANH ? tanhf(v) : v; }
 
-__device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot)
+// output (m, c) from tot = sum_k t[c][k] q[m][k], given row m's exponent, special flag and sum of q
+__device__ inline void epilogue_with(const tgk_qgemm_args &a, const tgk_qweight &w, int m, int c, long long tot, int E, int special,
+				     long long qsum)
 {
 	if (m >= a.M || c >= w.C) return;
 	float acc32;
-	if (s.special[m]) { // the reference's sequential loop (runtime/tg_rt.h:132-151)
+	if (special) { // the reference's sequential loop (runtime/tg_rt.h:132-151)
 		const float *x = xrow(a, m);
 		float t = 0.0f;
 		for (int k = 0; k < w.K; k++) t += (float)code_orig(w, c, k) * x[k * a.xk];
 		acc32 = t;
 	} else {
-		if (w.bits == 4) tot -= 8 * s.qsum[m];
-		acc32 = (float)ldexp((double)tot, s.e[m] - 23);
+		if (w.bits == 4) tot -= 8 * qsum;
+		acc32 = (float)ldexp((double)tot, E - 23);
 	}
 	int r = m / a.ni, jj = m - r * a.ni;
 	*out_at(a, r, jj, c) = act(a, w.scale[c] * acc32);
+}
+
+__device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot)
+{
+	if (m >= a.M || c >= w.C) return;
+	epilogue_with(a, w, m, c, tot, s.e[m], s.special[m], s.qsum[m]);
 }
 
 // One lane's outputs of a 32-row block: rows mbase + 8 (v / 4) + 4 (lane / 32)
@@ -765,6 +773,306 @@ __global__ __launch_bounds__(64 * W) void qgemv_k(tgk_qgemm_args a, tgk_qweight 
 	store_tile<NBW, NBW <= 2>(a, w, s, m0, c0 + 32 * jw, lane, rows, [&](int j, int v) { return (long long)totd(j, v); }, totd);
 }
 
+// Batches of at most 16 rows: v_mfma_i32_16x16x64_i8 (16 rows x 16 channels
+// x 64 inputs per instruction; lane l holds row or channel l % 16 and inputs
+// 16 (l / 16) .. +15 of the step, and outputs rows 4 (l / 16) .. +3 of
+// channel l % 16). A workgroup of W waves computes one 16-channel tile over
+// all K: wave w takes the 64-input steps w, w + W, ... (NS of them), and
+// issues every load of its steps (weights straight from global memory, the
+// digits of its steps) before its first MFMA, step by step, so a device full
+// of workgroups has all of the weight in flight at once (config 2: 256
+// workgroups, 8 MiB). The loads are inline assembly, as in qgemv_k: step i is
+// waited for with an exact count (the 4 (NS - 1 - i) younger loads may still
+// be in flight) and its registers are touched after the wait, so the
+// compiler neither drains every load before the first MFMA nor hands an
+// in-flight register to another value. Each operand is one contiguous run
+// per 16 lanes of the large-batch layouts: the digit layout's row block 0
+// (rows past M read row 0's bytes, the same addresses), and 8 (int4) or 16
+// (int8) bytes of the 32 x 32 weight fragment holding the lane's channel and
+// inputs. Every wave leaves its exact sums (planes combined in f64: integers
+// below 2^53) in LDS; wave 0 adds them and writes the 256 outputs through
+// epilogue() (special rows take the reference's loop there).
+template <int BITS>
+using gemv16_frag = typename std::conditional<BITS == 4, v2u, v4i>::type;
+
+template <int BITS, int NS, int I>
+__device__ inline void gemv16_steps(v4i (&af)[NS][3], gemv16_frag<BITS> (&bf)[NS], v4i (&acc)[3], int nvalid)
+{
+	if constexpr (I < NS) {
+		wait_vm<4 * (NS - 1 - I)>();
+		touch(bf[I]);
+		for (int l = 0; l < 3; l++) touch(af[I][l]);
+		if (I < nvalid) {
+			v4i wv;
+			if constexpr (BITS == 4) wv = unpack4(bf[I].x, bf[I].y);
+			else wv = bf[I];
+			for (int l = 0; l < 3; l++) acc[l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[I][l], wv, acc[l], 0, 0, 0);
+		}
+		gemv16_steps<BITS, NS, I + 1>(af, bf, acc, nvalid);
+	}
+}
+
+template <int BITS, int NS, int W>
+__global__ __launch_bounds__(64 * W) void gemv16_k(tgk_qgemm_args a, tgk_qweight w, Scratch s)
+{
+	static_assert(4 * NS <= 64, "the wait count must fit vmcnt");
+	__shared__ double red[W][4][64];
+	const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+	const int t = blockIdx.x, r = lane & 15, g = lane >> 4;
+	const int nks = w.Kp / 64, kblocks = w.Kp / 32;
+	constexpr int LB = BITS == 4 ? 8 : 16; // weight bytes per lane per fragment
+	// operand bases (uniform) and the lane's offsets within them
+	const int8_t *A = s.dig;
+	const uint8_t *B = w.w + (long)(t >> 1) * kblocks * (64 * LB);
+	const unsigned offA = (unsigned)((r < a.M ? r : 0) * 16 + (g & 1) * 512 + (g >> 1) * 3072);
+	const unsigned offB = (unsigned)((g >> 1) * (64 * LB) + ((g & 1) * 32 + (t & 1) * 16 + r) * LB);
+	v4i af[NS][3];
+	gemv16_frag<BITS> bf[NS];
+	for (int i = 0; i < NS; i++) {
+		int st = wave + i * W;
+		st = st < nks ? st : nks - 1; // past the wave's last step: reload the last step (not multiplied)
+		if constexpr (BITS == 4) ld8(bf[i], B, offB + (unsigned)st * (2 * 64 * LB));
+		else ld16(bf[i], B, offB + (unsigned)st * (2 * 64 * LB));
+		for (int l = 0; l < 3; l++) ld16(af[i][l], A, offA + (unsigned)st * 6144 + l * 1024);
+	}
+	v4i acc[3] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
+	gemv16_steps<BITS, NS, 0>(af, bf, acc, (nks - wave + W - 1) / W);
+	for (int v = 0; v < 4; v++) red[wave][v][lane] = combine_d(acc[0][v], acc[1][v], acc[2][v]);
+	__syncthreads();
+	if (wave) return;
+	const int c = t * 16 + r;
+	for (int v = 0; v < 4; v++) {
+		double tot = 0.0;
+		for (int u = 0; u < W; u++) tot += red[u][v][lane]; // exact: integers below 2^53
+		epilogue(a, w, s, 4 * g + v, c, (long long)tot);
+	}
+}
+
+template <int BITS, int NS, int W>
+void launch_gemv16(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
+{
+	gemv16_k<BITS, NS, W><<<a->w->Cp / 16, 64 * W, 0, st>>>(*a, *a->w, s);
+}
+
+// gemv1_k's K loop over its NL weight loads: load i is waited for with the
+// NL - 1 - i younger ones still in flight, its registers touched, then used
+template <int NL, int I, class F>
+__device__ inline void gemv1_steps(v4i (&bf)[NL], F &dots)
+{
+	if constexpr (I < NL) {
+		wait_vm<NL - 1 - I>();
+		touch(bf[I]);
+		dots(I, bf[I]);
+		gemv1_steps<NL, I + 1>(bf, dots);
+	}
+}
+
+// One activation row (M = 1) and int4 weights: exact integer dot products by
+// 4-way int8 dot instructions (v_dot4_i32_i8), no MFMA padding. A workgroup
+// of four waves computes 16 channels (half of a 32-channel fragment block)
+// over all K; wave w takes 32-input blocks 4 NL w .. 4 NL w + 4 NL - 1, and
+// lane l of a wave reads, from fragment block 4 i + l / 16 of its range,
+// the 16 bytes of two adjacent channels (l % 8 pairs) of input half
+// (l % 16) / 8: 16-byte loads, each 16 lanes one 128-byte run, NL of them per
+// lane issued at once (config 2: 256 workgroups, 8 lanes' worth of 16 bytes
+// each, the whole 8 MiB in flight). The row's digits are in LDS,
+// [block][digit][half][16 bytes], read by every lane with the same block and
+// half (a broadcast).
+// FUSED: the workgroup makes those digits itself from the row (unit stride,
+// 16-byte aligned, K a multiple of 16): max |x|, exponent, peak test and sum
+// of q by block reductions, exactly as the digit kernels do, so no digit
+// kernel runs before it; workgroup 0 also writes the digits and row data to
+// the scratch (a later product may reuse them). Otherwise the digits come
+// from the scratch. The row and digit loads are issued before the weight
+// loads and waited for with a count that leaves the weights in flight (loads
+// complete in order), all as inline assembly like qgemv_k's.
+template <int NL, bool FUSED>
+__global__ __launch_bounds__(256) void gemv1_k(tgk_qgemm_args a, tgk_qweight w, Scratch s)
+{
+	constexpr int GX = 2; // 16-input groups of the row per thread (FUSED: K <= 8192)
+	__shared__ __attribute__((aligned(16))) int8_t dl[256 * 96]; // digits: [block][digit][half][16]
+	__shared__ int red[4][8][2][3];
+	__shared__ unsigned smx[4];
+	__shared__ int sbad[4];
+	__shared__ long long sq[4], stl[4];
+	const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+	const int t = blockIdx.x, f = lane >> 4, h = (lane >> 3) & 1, pr = lane & 7;
+	const int kblocks = w.Kp / 32, K = w.K;
+	// the row's loads first (inline assembly: counted by the waits below)
+	v4i xv[FUSED ? GX * 4 : 1];
+	v4i dv[FUSED ? 1 : 6];
+	const uint8_t *xb = (const uint8_t *)xrow(a, 0);
+	if constexpr (FUSED) {
+		for (int u = 0; u < GX; u++) {
+			const int k0 = 16 * (tid + 256 * u), kk = k0 < K ? k0 : 0; // past the row: its first group (not used)
+			for (int i = 0; i < 4; i++) ld16(xv[u * 4 + i], xb, (unsigned)(kk + 4 * i) * 4);
+		}
+	} else {
+		for (int u = 0; u < 6; u++) { // chunk c = (block, digit, half) of row 0 in the fragment layout
+			int c = tid + 256 * u;
+			c = c < kblocks * 6 ? c : 0;
+			ld16(dv[u], s.dig, (unsigned)((c / 6) * 3072 + ((c % 6) >> 1) * 1024 + (c & 1) * 512));
+		}
+	}
+	// the weights: NL 16-byte loads per lane
+	const uint8_t *B = w.w + (long)(t >> 1) * kblocks * 512;
+	const unsigned offB = (unsigned)((h * 32 + (t & 1) * 16 + 2 * pr) * 8);
+	v4i bf[NL];
+	for (int i = 0; i < NL; i++) {
+		int kb = wave * 4 * NL + 4 * i + f;
+		kb = kb < kblocks ? kb : kblocks - 1; // past the end: reload the last block (not used)
+		ld16(bf[i], B, offB + (unsigned)kb * 512);
+	}
+	// the row's digits into LDS (the weights stay in flight)
+	wait_vm<NL>();
+	int E = 0, sp0 = 0;
+	float band = 0.0f;
+	float v[FUSED ? GX : 1][16];
+	if constexpr (FUSED) {
+		for (int i = 0; i < GX * 4; i++) touch(xv[i]);
+		unsigned mb = 0;
+		for (int u = 0; u < GX; u++) {
+			for (int i = 0; i < 4; i++)
+				for (int e = 0; e < 4; e++) v[u][4 * i + e] = __int_as_float(xv[u * 4 + i][e]);
+			if (16 * (tid + 256 * u) < K) tgq_scan16(v[u], mb);
+		}
+		float mx;
+		int bad;
+		tgq_scan_end(mb, mx, bad);
+		mx = wave_max(mx); // a NaN lane reads 0 here; its row is flagged by `bad`
+		bad = __any(bad);
+		if (lane == 0) smx[wave] = __float_as_uint(mx), sbad[wave] = bad;
+		__syncthreads();
+		const float amax = fmaxf(fmaxf(__uint_as_float(smx[0]), __uint_as_float(smx[1])),
+					 fmaxf(__uint_as_float(smx[2]), __uint_as_float(smx[3])));
+		sp0 = tgq_special(sbad[0] | sbad[1] | sbad[2] | sbad[3], amax);
+		E = tgq_exponent(amax, sp0);
+		band = tgq_band(amax);
+	} else {
+		for (int u = 0; u < 6; u++) {
+			touch(dv[u]);
+			const int c = tid + 256 * u;
+			if (c < kblocks * 6) *(v4i *)(dl + c * 16) = dv[u]; // chunk c = ((block 3 + digit) 2 + half)
+		}
+	}
+	long long qs = 0, tl = 0; // this thread's share of the sum of q and of the peak tally (FUSED)
+	if constexpr (FUSED) {
+		int8_t *gblk = tgq_row_base(s.dig, 0, w.Kp);
+		for (int u = 0; u < GX; u++) {
+			const int k0 = 16 * (tid + 256 * u);
+			if (k0 >= w.Kp) break;
+			unsigned w0[4] = { 0, 0, 0, 0 }, w1[4] = { 0, 0, 0, 0 }, w2[4] = { 0, 0, 0, 0 }; // zero digits: padding, special rows
+			long long tl0 = 0; // the peak tally is taken after the dot products, off the critical path
+			if (!sp0 && k0 < K) qs += tgq_digits16(v[u], E, 0.0f, w0, w1, w2, tl0);
+			int8_t *p = dl + ((k0 >> 5) * 3 * 2 + ((k0 >> 4) & 1)) * 16;
+			*(v4i *)p = v4i{ (int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3] };
+			*(v4i *)(p + 32) = v4i{ (int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3] };
+			*(v4i *)(p + 64) = v4i{ (int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3] };
+			if (t == 0) { // the scratch copy, for a product that reuses these digits
+				int8_t *g = gblk + (k0 >> 5) * 3072 + ((k0 >> 4) & 1) * 512;
+				*(v4i *)g = v4i{ (int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3] };
+				*(v4i *)(g + 1024) = v4i{ (int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3] };
+				*(v4i *)(g + 2048) = v4i{ (int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3] };
+			}
+		}
+	}
+	__syncthreads();
+	// this lane's digits of its NL blocks, read before the first weight wait
+	// (up to eight loads per lane: beyond that the registers they take make
+	// the compiler move in-flight load registers around, which tests/
+	// test_asm_ring.py catches; then each step reads its digits from LDS)
+	constexpr bool PRE = NL <= 8;
+	const int nkb = kblocks - wave * 4 * NL; // blocks of this wave's range that exist
+	auto digits_of = [&](int i, v4i (&d3)[3]) {
+		const int kbl = 4 * i + f < nkb ? 4 * i + f : 0;
+		const int8_t *d = dl + ((wave * 4 * NL + kbl) * 6 + h) * 16;
+		for (int l = 0; l < 3; l++) d3[l] = *(const v4i *)(d + 32 * l);
+	};
+	v4i dg[PRE ? NL : 1][3];
+	if constexpr (PRE)
+		for (int i = 0; i < NL; i++) digits_of(i, dg[i]);
+	// dot products: channels 2 pr, 2 pr + 1 of the tile, digits 0..2
+	int acc[2][3] = { { 0, 0, 0 }, { 0, 0, 0 } };
+	auto dots = [&](int i, const v4i &b) {
+		if (4 * i + f >= nkb) return;
+		v4i d3[3];
+		if constexpr (PRE)
+			for (int l = 0; l < 3; l++) d3[l] = dg[i][l];
+		else
+			digits_of(i, d3);
+		const v4i c0 = unpack4((unsigned)b.x, (unsigned)b.y), c1 = unpack4((unsigned)b.z, (unsigned)b.w);
+		for (int e = 0; e < 4; e++)
+			for (int l = 0; l < 3; l++) {
+				acc[0][l] = __builtin_amdgcn_sdot4(c0[e], d3[l][e], acc[0][l], false);
+				acc[1][l] = __builtin_amdgcn_sdot4(c1[e], d3[l][e], acc[1][l], false);
+			}
+	};
+	gemv1_steps<NL, 0>(bf, dots);
+	// lanes with the same channel pair: over the input half (lane bit 3) and block (bits 4, 5)
+	for (int o = 8; o < 64; o <<= 1)
+		for (int j = 0; j < 2; j++)
+			for (int l = 0; l < 3; l++) acc[j][l] += __shfl_xor(acc[j][l], o);
+	if (lane < 8)
+		for (int j = 0; j < 2; j++)
+			for (int l = 0; l < 3; l++) red[wave][lane][j][l] = acc[j][l];
+	int special;
+	long long qsum;
+	if constexpr (FUSED) { // the row's sum of q and peak test (needed only from here on)
+		for (int u = 0; u < GX; u++)
+			if (!sp0 && 16 * (tid + 256 * u) < K) tl += tgq_tally16(v[u], band);
+		qs = wave_sum(qs);
+		tl = wave_sum(tl);
+		if (lane == 0) sq[wave] = qs, stl[wave] = tl;
+		__syncthreads();
+		qsum = sq[0] + sq[1] + sq[2] + sq[3];
+		special = sp0 || tgq_peaked(stl[0] + stl[1] + stl[2] + stl[3], K);
+		if (t == 0 && tid == 0) s.e[0] = E, s.special[0] = special, s.qsum[0] = qsum;
+	} else {
+		__syncthreads();
+		E = s.e[0], special = s.special[0], qsum = s.qsum[0];
+	}
+	if (wave || lane >= 16) return;
+	int p3[3] = { 0, 0, 0 };
+	for (int u = 0; u < 4; u++)
+		for (int l = 0; l < 3; l++) p3[l] += red[u][lane >> 1][lane & 1][l];
+	epilogue_with(a, w, 0, t * 16 + lane, combine(p3[0], p3[1], p3[2]), E, special, qsum);
+}
+
+// gemv1_k for a single row of int4 weights: NL 16-byte weight loads per lane,
+// 16 NL >= the row's 32-input blocks (at most 256: K <= 8192)
+template <bool FUSED>
+bool launch_gemv1(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
+{
+	const tgk_qweight *w = a->w;
+	const int kblocks = w->Kp / 32, g = w->Cp / 16;
+	if (a->M != 1 || w->bits != 4 || kblocks > 256) return false;
+	if (kblocks <= 16) gemv1_k<1, FUSED><<<g, 256, 0, st>>>(*a, *w, s);
+	else if (kblocks <= 32) gemv1_k<2, FUSED><<<g, 256, 0, st>>>(*a, *w, s);
+	else if (kblocks <= 64) gemv1_k<4, FUSED><<<g, 256, 0, st>>>(*a, *w, s);
+	else if (kblocks <= 128) gemv1_k<8, FUSED><<<g, 256, 0, st>>>(*a, *w, s);
+	else gemv1_k<16, FUSED><<<g, 256, 0, st>>>(*a, *w, s);
+	return true;
+}
+
+// gemv16_k's instantiation for K: W waves of NS steps each, W * NS >= Kp / 64.
+// No instantiation may spill a register (a spill of a register whose load is
+// still in flight stores the wrong bytes; tests/test_asm_ring.py checks):
+// sixteen waves leave 128 registers per wave, too few for int8 weights at
+// eight steps, so int8 rows longer than 4096 inputs take qgemv_k.
+template <int BITS>
+bool launch_small(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
+{
+	const int nks = a->w->Kp / 64;
+	if (a->M > 16 || nks > 16 * 8 || (BITS == 8 && nks > 64)) return false;
+	if (nks <= 4) launch_gemv16<BITS, 1, 4>(st, a, s);
+	else if (nks <= 8) launch_gemv16<BITS, 2, 4>(st, a, s);
+	else if (nks <= 16) launch_gemv16<BITS, 2, 8>(st, a, s);
+	else if (nks <= 32) launch_gemv16<BITS, 4, 8>(st, a, s);
+	else if (nks <= 64) launch_gemv16<BITS, 8, 8>(st, a, s);
+	else if constexpr (BITS == 4) launch_gemv16<BITS, 8, 16>(st, a, s);
+	return true;
+}
+
 template <int BITS, int NB, int W, int P = 4>
 void launch_gemv(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
 {
@@ -782,6 +1090,8 @@ void launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 		qgemm_k<BITS><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy);
 		return;
 	}
+	if (BITS == 4 && launch_gemv1<false>(st, a, s)) return; // one row
+	if (launch_small<BITS>(st, a, s)) return;               // at most 16 rows
 	// up to 64 rows, or too few tiles: 32 x (32 NB) tiles, NB as large as
 	// still fills the device; W waves split K, about 16 32-input blocks each
 	// for the wider tiles and 8-32 for one-block-wide ones (measured: at one
@@ -1001,8 +1311,32 @@ void tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 	else launch_gemm<4>(st, a, s, Mp);
 }
 
+bool tgk_qgemm_fusable(const tgk_qgemm_args *a)
+{
+	const tgk_qweight *w = a->w;
+	return w && w->w && a->x && a->M == 1 && w->bits == 4 && w->Kp <= 8192 && a->xk == 1 && ((size_t)a->x & 15) == 0 &&
+	       (w->K & 15) == 0;
+}
+
+void tgk_qgemm_fused(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
+{
+	const tgk_qweight *w = a->w;
+	if (!w || !w->w || !w->scale || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return;
+	if (!tgk_qgemm_fusable(a)) {
+		tgk_qgemm_digits(st, a, scratch);
+		tgk_qgemm_mfma(st, a, scratch);
+		return;
+	}
+	const int Mp = (int)round_up(a->M, BM);
+	launch_gemv1<true>(st, a, carve(scratch, Mp, w->Kp));
+}
+
 void tgk_qgemm(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
+	if (tgk_qgemm_fusable(a)) {
+		tgk_qgemm_fused(st, a, scratch);
+		return;
+	}
 	tgk_qgemm_digits(st, a, scratch);
 	tgk_qgemm_mfma(st, a, scratch);
 }

@@ -1350,6 +1350,11 @@ void exec_step(Run &R, const Step &s)
 		a.orr = s.orr, a.oc = s.oc, a.oj = s.ojj;
 		a.M = R.rows * s.ni;
 		a.act = s.act;
+		if (!s.reuse_digits && tgk_qgemm_fusable(&a)) { // one row: the digits are made inside the product's kernel
+			Timer t(p, 1);
+			tgk_qgemm_fused(st, &a, p->d_scratch);
+			break;
+		}
 		if (!s.reuse_digits) {
 			Timer t(p, 2);
 			tgk_qgemm_digits(st, &a, p->d_scratch);

@@ -242,6 +242,12 @@ typedef struct {
 #define TGK_ACT_TANH 1
 
 /* scratch: bytes needed for M rows of K inputs */
+/* One row of int4 weights (M = 1, unit-stride 16-byte-aligned row, K a
+ * multiple of 16, K <= 8192): tgk_qgemm_fused computes the digits inside
+ * the product's own kernel (and leaves them in the scratch like
+ * tgk_qgemm_digits); other cases fall back to digits + product. */
+bool tgk_qgemm_fusable(const tgk_qgemm_args *a);
+void tgk_qgemm_fused(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 size_t tgk_qgemm_scratch(int M, int Kp);
 void tgk_qgemm(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 /* the digit area tgk_qgemm uses in `scratch` for M rows of Kp inputs, for

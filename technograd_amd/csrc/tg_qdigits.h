@@ -112,15 +112,35 @@ __device__ inline void tgq_scan_end(unsigned mb, float &mx, int &nan)
 	mx = nan ? 0.0f : __uint_as_float(mb);
 }
 
-// digits of 16 consecutive inputs (inputs k0 .. k0 + 15 of the row at blk)
-// into their three 16-byte chunks; zero digits when `zero`; returns the sum of
-// q and adds the inputs' peak tally (band = tgq_band(max |x|)) to `tally`
-// (nothing for a `zero` group).
+// the digit words of 16 consecutive inputs: w_l[g] holds plane l's digits of
+// inputs 4 g .. 4 g + 3 (byte i: input 4 g + i); returns the sum of q and
+// adds the inputs' peak tally (band = tgq_band(max |x|)) to `tally`.
 // With u = q + 0x808080 (|q| <= 8355328, so 0 <= u < 2^24), byte l of u is
 // d_l + 128: the balanced digits are u's bytes with the top bit flipped. The
 // bytes of four inputs are gathered into each plane's 32-bit word with byte
 // permutes (v_perm_b32 selects bytes of a register pair: 0-3 the second
 // operand's, 4-7 the first's, 12 a zero byte).
+__device__ inline long long tgq_digits16(const float *v, int E, float band, unsigned (&w0)[4], unsigned (&w1)[4], unsigned (&w2)[4],
+					 long long &tally)
+{
+	tally += tgq_tally16(v, band);
+	int qs = 0; // |sum of 16 q| < 2^27
+	for (int g = 0; g < 4; g++) {
+		unsigned u[4];
+		for (int i = 0; i < 4; i++) {
+			const int q = (int)rintf(ldexpf(v[4 * g + i], 23 - E)); // exact: |q| < 2^23
+			qs += q;
+			u[i] = (unsigned)(q + 0x808080);
+		}
+		tgq_pack4(u, w0[g], w1[g], w2[g]);
+	}
+	return qs;
+}
+
+// digits of 16 consecutive inputs (inputs k0 .. k0 + 15 of the row at blk)
+// into their three 16-byte chunks of the fragment layout; zero digits when
+// `zero`; returns the sum of q and adds the inputs' peak tally to `tally`
+// (nothing for a `zero` group).
 __device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E, bool zero, float band, long long &tally)
 {
 	int8_t *p = blk + (k0 >> 5) * 3072 + ((k0 >> 4) & 1) * 512;
@@ -130,20 +150,8 @@ __device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E
 		*(tgq_v4i *)(p + 2048) = tgq_v4i{0, 0, 0, 0};
 		return 0;
 	}
-	tally += tgq_tally16(v, band);
 	unsigned w0[4], w1[4], w2[4];
-	int qs = 0; // |sum of 16 q| < 2^27
-	{
-		for (int g = 0; g < 4; g++) {
-			unsigned u[4];
-			for (int i = 0; i < 4; i++) {
-				const int q = (int)rintf(ldexpf(v[4 * g + i], 23 - E)); // exact: |q| < 2^23
-				qs += q;
-				u[i] = (unsigned)(q + 0x808080);
-			}
-			tgq_pack4(u, w0[g], w1[g], w2[g]);
-		}
-	}
+	const long long qs = tgq_digits16(v, E, band, w0, w1, w2, tally);
 	*(tgq_v4i *)p = tgq_v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
 	*(tgq_v4i *)(p + 1024) = tgq_v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
 	*(tgq_v4i *)(p + 2048) = tgq_v4i{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};

@@ -1,7 +1,7 @@
 """Register-ring check of the small-batch GEMM (technograd_amd/csrc/kern_qgemm.hip,
 qgemv_k), on the gfx950 assembly hipcc writes for it (no GPU needed).
 
-qgemv_k loads its operands with inline-assembly loads the compiler does not
+qgemv_k (and gemv16_k) load their operands with inline-assembly loads the compiler does not
 track: it believes a load's destination registers hold their value as soon as
 the instruction is issued. A ring register whose load is still in flight must
 therefore not be given to any other value, or the load overwrites that value
@@ -36,13 +36,27 @@ def _vregs(tok):
 
 
 def ring_hazards(asm_lines):
-    """{kernel: [instructions writing an in-flight ring register]} for every qgemv_k."""
+    """{kernel: [instructions writing an in-flight ring register]} for every
+    qgemv_k, gemv16_k and gemv1_k (all load their operands this way). Ring
+    loads are the inline-assembly ones (the compiler marks such text with
+    ;;#ASMSTART / ;;#ASMEND); loads the compiler wrote itself are waited for
+    by the compiler."""
     found = {}
-    starts = [i for i, l in enumerate(asm_lines) if re.match(r"^_Z\S*qgemv_k\S*:", l)]
+    starts = [i for i, l in enumerate(asm_lines) if re.match(r"^_Z\S*(qgemv_k|gemv16_k|gemv1_k)\S*:", l)]
     for s in starts:
         e = next(i for i in range(s, len(asm_lines)) if "s_endpgm" in asm_lines[i])
-        body = [l.strip() for l in asm_lines[s:e] if l.strip() and not l.strip().startswith(";")]
-        ring = [i for i, t in enumerate(body) if re.match(r"global_load_dwordx[24] v\S+, v\d+, s\[", t)]
+        body, inasm, asm_idx = [], False, set()  # loads written as inline assembly (between the ASMSTART/ASMEND markers)
+        for l in asm_lines[s:e]:
+            t = l.strip()
+            if t.startswith(";;#ASMSTART"):
+                inasm = True
+            elif t.startswith(";;#ASMEND"):
+                inasm = False
+            elif t and not t.startswith(";"):
+                if inasm:
+                    asm_idx.add(len(body))
+                body.append(t)
+        ring = [i for i, t in enumerate(body) if i in asm_idx and re.match(r"global_load_dwordx[24] v\S+, v\d+, s\[", t)]
         assert ring, "no ring loads found in " + asm_lines[s]
         last = ring[-1]
         w0 = max([i for i in range(last) if "vmcnt(0)" in body[i]] + [0])
@@ -116,8 +130,36 @@ def qgemm_asm(tmp_path_factory):
 
 def test_qgemv_ring_registers_not_reused_in_flight(qgemm_asm):
     found = ring_hazards(qgemm_asm)
-    assert len(found) >= 6  # every instantiation the launcher uses was checked
+    assert sum("qgemv_k" in k for k in found) >= 6 and sum("gemv16_k" in k for k in found) >= 11 and sum(
+        "gemv1_k" in k for k in found) >= 10  # every instantiation the launchers use
     bad = {k: v for k, v in found.items() if v}
+    assert not bad, bad
+
+
+def spills(asm_lines, pattern):
+    """{kernel: (sgpr spills, vgpr spills)} from the code object metadata of kernels matching pattern."""
+    out, name = {}, None
+    for l in asm_lines:
+        m = re.match(r"\s*(?:- )?\.name:\s+(\S+)", l)
+        if m:
+            name = m.group(1) if re.search(pattern, m.group(1)) else None
+            continue
+        m = re.match(r"\s*\.(sgpr|vgpr)_spill_count:\s+(\d+)", l)
+        if m and name:
+            s, v = out.get(name, (0, 0))
+            out[name] = (s + int(m.group(2)), v) if m.group(1) == "sgpr" else (s, v + int(m.group(2)))
+    return out
+
+
+def test_inline_load_kernels_do_not_spill(qgemm_asm):
+    """A register spilled while its inline-assembly load is in flight is
+    stored before the load lands (the compiler believes it already holds the
+    value): no instantiation of the kernels that load this way may spill.
+    (An int8 gemv16_k at sixteen waves of eight steps did, and computed wrong
+    sums; it is no longer instantiated.)"""
+    found = spills(qgemm_asm, r"(qgemv_k|gemv16_k|gemv1_k)")
+    assert len(found) >= 41
+    bad = {k: v for k, v in found.items() if v != (0, 0)}
     assert not bad, bad
 
 

@@ -25,12 +25,26 @@ SHAPES = [
     (4, 128, 4096, 4096),  # NB=2 W=4
     (8, 128, 2048, 4096),  # NB=2 W=2
     (4, 100, 256, 4096),   # NB=2 W=1, rows not a multiple of 32
-    (4, 16, 8192, 4096),   # NB=1 W=8
-    (8, 16, 1024, 4096),   # NB=1 W=4
-    (4, 3, 640, 4096),     # NB=1 W=2
-    (4, 1, 256, 4096),     # NB=1 W=1
-    (8, 2, 8192, 2048),    # NB=1 W=8, int8
+    (4, 20, 8192, 4096),   # NB=1 W=8
+    (8, 40, 1024, 4096),   # NB=1 W=4
+    (4, 33, 640, 4096),    # NB=1 W=2
+    (4, 50, 256, 4096),    # NB=1 W=1
+    (8, 60, 8192, 2048),   # NB=1 W=8, int8
     (4, 64, 1024, 1000),   # NB=1, channels not a multiple of 32
+    (4, 16, 8192, 4096),   # gemv16_k NS=8 W=16 (at most 16 rows)
+    (4, 1, 4096, 4096),    # gemv1_k fused (one int4 row, digits made in the kernel): config 2 at B=1
+    (4, 1, 8192, 2048),    # gemv1_k fused, NL=16
+    (4, 1, 1000, 4096),    # gemv1_k on the digit kernel's digits (K not a multiple of 16)
+    (8, 1, 4096, 4096),    # one int8 row: gemv16_k NS=8 W=8
+    (4, 16, 4096, 4096),   # NS=8 W=8: config 2 at B=16
+    (8, 5, 2048, 4096),    # NS=4 W=8, int8
+    (8, 7, 4096, 4096),    # NS=8 W=8, int8
+    (8, 16, 1024, 4096),   # NS=2 W=8, int8
+    (4, 3, 640, 4096),     # NS=2 W=8, K not a multiple of 64
+    (4, 4, 448, 1000),     # NS=2 W=4, channels not a multiple of 16
+    (4, 1, 256, 4096),     # gemv1_k fused, NL=1
+    (8, 1, 256, 4096),     # gemv16_k NS=1 W=4
+    (8, 2, 8192, 2048),    # int8 beyond 4096 inputs: qgemv_k NB=1 W=8
 ]
 
 
@@ -59,3 +73,33 @@ def test_launch_shape_bit_exact(bits_, M, K, C):
     want, special = device_path_matmul(x, codes, scales)
     assert special.sum() == (M > 3)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.argwhere(got != want)[:5].tolist()
+
+
+@pytest.mark.parametrize("K", [4096, 1000])
+def test_single_row_kinds(K):
+    """One row at a time (the single-row kernel, fused at K = 4096, fed by
+    the digit kernel at K = 1000): an outlier row (peaked), rows with inf,
+    nan or an entry above 2^100 (special), a row of zeros, a tiny row and a
+    plain row, each bit for bit against the path restated on the host."""
+    from technograd_amd import hip
+    print("case single rows", K, flush=True)
+    rng = np.random.default_rng(K)
+    C = 2048
+    codes = rng.integers(-7, 8, size=(K, C)).astype(np.int8)
+    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
+    flat = codes.ravel().astype(np.int64)
+    packed = ((flat[0::2] & 15) | ((flat[1::2] & 15) << 4)).astype(np.uint8).view(np.int8)
+    rows = rng.normal(size=(7, K)).astype(np.float32)
+    rows[0, K // 2] = 1e4
+    rows[1, 5] = np.inf
+    rows[2, 7] = np.nan
+    rows[3, 9] = 2e30
+    rows[4] = 0
+    rows[5] *= 1e-30
+    want, special = device_path_matmul(rows, codes, scales)
+    assert special.tolist() == [True, True, True, True, False, False, False]
+    for i in range(len(rows)):
+        got = hip.matmul_q(packed, 4, scales, rows[i:i + 1], 1, K, C, 1)
+        assert np.array_equal(np.isnan(got[0]), np.isnan(want[i]))
+        ok = ~np.isnan(want[i])
+        assert np.array_equal(got[0][ok].view(np.uint32), want[i][ok].view(np.uint32)), i

@@ -21,8 +21,7 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 NAMES = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(GOLDEN, "*.npz")))
 # models whose outputs involve no transcendental: the exact paths must match bit for bit
 NO_LIBM = {"odd_f32", "odd_q4", "odd_q8"}
-# f32 think models on the row executor: rows whose halting step moves with device libm (measured on MI355X)
-MOVED_ROWS = {"latent_f32": 8, "latent_q4g": 8, "haltm_f32": 2}
+
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -56,8 +55,7 @@ def test_default_path_against_reference(name):
     y, steps = p.batch(d["x"])
     n = parity.check_model(y, d["y"], *truth(text, d["x"], d["steps"]))
     print("%s: %d of %d outputs within the reference's row error, not 1e-5 of its value" % (name, n, y.size), flush=True)
-    if "latent" not in name and "haltm" not in name:
-        assert np.array_equal(steps, d["steps"])
+    assert np.array_equal(steps, d["steps"])
 
 
 @pytest.mark.parametrize("name", NAMES)
@@ -84,12 +82,9 @@ def test_row_program_against_reference(name):
         assert np.array_equal(bits(y), bits(d["y"]))
     else:
         parity.check_model(y, d["y"], *truth(text, d["x"], d["steps"]))
-    if "latent" in name or "haltm" in name:
-        # halting decisions compare a delta with a threshold; device libm may
-        # move a row across it only when its delta ties the threshold to a few ulp
-        moved = int((steps != d["steps"]).any(axis=1).sum())
-        print("%s: %d of %d rows halt at another step than the reference's" % (name, moved, len(steps)), flush=True)
-        assert moved <= MOVED_ROWS.get(name, 0)
+    # halting compares a delta with a threshold, so device libm could move a
+    # row whose delta ties it to a few ulp; on these goldens none moves
+    assert np.array_equal(steps, d["steps"])
 
 
 @pytest.mark.parametrize("name", [n for n in NAMES if "xq" in np.load(os.path.join(GOLDEN, n + ".npz")).files])
