@@ -12,23 +12,33 @@ roofline: the dominant kernel is the int8-MFMA GEMM at batch 4096; its
 average duration comes from HIP events on the backend's stream (a separate
 program built with TG_HIP_TIMING), and achieved = 2*4096^3 algorithmic int8
 ops (one multiply-add = 2 ops, counted once whatever the limb count) /
-duration, against 5000 TOP/s dense int8. traffic = HBM bytes per launch of
-that kernel from two rocprofv3 --pmc runs of this script's --profile-child
-mode (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
+duration, against 5000 TOP/s dense int8; hw_mfma_frac = 3 x frac (three
+int8 MFMAs per multiply-add). traffic = HBM bytes per launch of that kernel
+from two rocprofv3 --pmc runs of this script's --profile-child mode
+(FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
 counter reads for the 1 GiB flush pass (512 MiB read + 512 MiB written, an
-elementwise kernel of known traffic) in the same run.
+elementwise kernel of known traffic) in the same run. roofline.matvec: the
+int4 matvec at B = 1 and 16 against HBM, from a rocprofv3 kernel trace of
+the same child (cold calls, each after a flush pass) and the same traffic
+counters.
 
-The "sweep" field repeats the kernel timings per batch. Every timed call
-there follows a pass, on the same stream, that reads 512 MiB of other data
-(a row sum: it writes next to nothing, so no dirty lines are left to write
-back), so neither the 8 MiB weight nor the rows can be served from the 256 MB
+The "sweep" field repeats the kernel timings per batch: HIP events around
+each kernel, and the kernel-trace durations. Every timed call follows a
+pass, on the same stream, that reads 512 MiB of other data (a row sum: it
+writes next to nothing, so no dirty lines are left to write back), so
+neither the 8 MiB weight nor the rows can be served from the 256 MB
 Infinity Cache, and the device is never idle while the host queues the next
-call (HIP events then time kernels, not launch latency).
+call.
 
 cpu_baseline: the reference's own interpreter (oracle/_ref/tgc_ref, compiled
-from the reference sources) on this host's cores over a sample of rows of the
-same layer; falls back to the oracle restatement when the reference build is
-absent.
+from the reference sources) on this host's cores, -j auto (one thread per
+CPU the process may run on), median of three runs over a sample of rows of
+the same layer; value = compute time, wall_value = input load to last write;
+falls back to the oracle restatement when the reference build is absent.
+
+legs: config 1 (int8 MLP, 65,536 rows) and config 4 (Q16.16 latent
+reasoner, 1,048,576 rows), three passes each, with their own roofline
+(config 4: VALU instructions from rocprofv3 SQ_INSTS_VALU) and CPU baseline.
 """
 import argparse
 import csv
@@ -79,26 +89,64 @@ def flush_program(hip):
     return p, buf_in, buf_out
 
 
-def cpu_baseline(text, X, sample_rows, threads):
+def cpu_info():
+    """The host's CPU count, the CPUs this process may run on and the CPU model."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpus_usable": len(os.sched_getaffinity(0)), "cpu_model": model}
+
+
+def auto_threads():
+    """`-j auto`: one thread per CPU this process may run on (the reference's
+    par_init(0), src/par.c:84-92, takes the online CPUs; under a CPU set the
+    usable ones are the ones that count)."""
+    return len(os.sched_getaffinity(0))
+
+
+def ref_cpu(text, rows, per, nout, nthink, threads, fixed, what, runs=3):
+    """The reference interpreter (oracle/_ref/tgc_ref, built from the
+    reference's sources; the oracle restatement if that build is absent) over
+    `rows`, `runs` times: median compute and wall (input load to last write)
+    rates."""
     from oracle import oracle as O
     tmp = tempfile.mkdtemp(prefix="tgbench")
-    x = X[:sample_rows]
-    if O.have_ref():
-        mpath = os.path.join(tmp, "linear4096.tgir")
-        with open(mpath, "w") as f:
-            f.write(text)
-        _, _, ms = O.ref_batch(mpath, x, K, C, 0, tmp, threads=threads)
-        kind = "reference"
-    else:
-        m = O.Model(text)
-        t0 = time.perf_counter()
-        m.batch(x, threads=threads)
-        ms = (time.perf_counter() - t0) * 1e3
-        kind = "port"
-    shutil.rmtree(tmp, ignore_errors=True)
-    return {"value": sample_rows / (ms / 1e3), "unit": "rows/s", "cores": threads, "kind": kind,
-            "sample": "%d rows of config 2 (int4 4096x4096) through the %s interpreter, -j %d, compute time only" % (
-                sample_rows, "reference's" if kind == "reference" else "oracle's", threads)}
+    comp, wall = [], []
+    try:
+        if O.have_ref():
+            mpath = os.path.join(tmp, "model.tgir")
+            with open(mpath, "w") as f:
+                f.write(text)
+            for _ in range(runs):
+                _, _, ms, wms = O.ref_batch(mpath, rows, per, nout, nthink, tmp, threads=threads, fixed=fixed, wall=True)
+                comp.append(ms)
+                wall.append(wms)
+            kind = "reference"
+        else:
+            m = O.Model(text)
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                (m.batch_fixed if fixed else m.batch)(rows, threads=threads)
+                comp.append((time.perf_counter() - t0) * 1e3)
+                wall.append(comp[-1])
+            kind = "port"
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    cm, wm = sorted(comp)[len(comp) // 2], sorted(wall)[len(wall) // 2]
+    out = {"value": round(len(rows) / (cm / 1e3), 1), "unit": "rows/s", "cores": threads, "kind": kind,
+           "wall_value": round(len(rows) / (wm / 1e3), 1), "runs": runs,
+           "compute_ms": [round(v, 2) for v in comp], "wall_ms": [round(v, 2) for v in wall],
+           "sample": "%d rows of %s through the %s interpreter, -j auto (%d threads), median of %d runs; value = "
+                     "compute time, wall_value = input load to last write" % (
+                         len(rows), what, "reference's" if kind == "reference" else "oracle's", threads, runs)}
+    out.update(cpu_info())
+    return out
 
 
 def setup(synth):
@@ -108,100 +156,138 @@ def setup(synth):
     return text, X
 
 
-def profile_child():
-    """What the traffic runs profile: two cold B = 4096 calls, each after a
-    flush pass, on one stream."""
+def profile_child(mode):
+    """What the profiled runs see. c2: each batch of BATCHES called twice,
+    every call after a flush pass (512 MiB read and written) on the same
+    stream, so each call reads its weight from HBM and the flush kernels
+    split the dispatches into one segment per call. c4: two passes of
+    config 4, each after a flush pass."""
     from technograd_amd import hip, synth
     hip.init(0)
-    text, X = setup(synth)
-    prog = hip.Program(text, max_rows=4096)
-    d_x = hip.DeviceBuffer.from_array(X)
-    d_y = hip.DeviceBuffer(4096 * C * 4)
+    fprog, fin, fout = None, None, None
+    if mode == "c2":
+        text, X = setup(synth)
+        prog = hip.Program(text, max_rows=4096)
+        d_x = hip.DeviceBuffer.from_array(X)
+        d_y = hip.DeviceBuffer(4096 * C * 4)
+        calls = [(b, lambda b=b: prog.batch_device(d_x.ptr, b, d_y.ptr)) for b in BATCHES] * 2
+    else:
+        import numpy as np
+        rows = 1048576
+        prog = hip.Program(synth.latent_reasoner_tgir(), flags=hip.FIXED, max_rows=rows)
+        d_x = hip.DeviceBuffer.from_array((synth.config4_rows(rows) * 65536.0).astype(np.int32))
+        d_y, d_s = hip.DeviceBuffer(rows * 16), hip.DeviceBuffer(rows * 4)
+        calls = [(rows, lambda: prog.batch_device(d_x.ptr, rows, d_y.ptr, d_s.ptr))] * 2
     fprog, fin, fout = flush_program(hip)
     fprog.set_stream(prog.stream())
-    for _ in range(2):
+    for _, call in calls:
         fprog.batch_device(fin.ptr, FLUSH_ROWS, fout.ptr)
-        prog.batch_device(d_x.ptr, 4096, d_y.ptr)
+        call()
     prog.sync()
 
 
-def pmc_run(counter, outdir):
-    """Per-kernel average of one counter (KiB per dispatch) over a profiled
-    --profile-child run: {'qgemm': v, 'flush': v}, or None."""
-    d = os.path.join(outdir, counter)
-    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
-           sys.executable, os.path.abspath(__file__), "--profile-child"]
+def _short(name):
+    return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+
+
+def _is_flush(name, grid):
+    return "binary" in name and grid >= FLUSH_ROWS * FLUSH_COLS // 16
+
+
+def profiled(tool_args, mode, outdir, tag):
+    """Dispatches of a profiled --profile-child run, in order, split at each
+    flush kernel: [[(kernel, grid, {field: value})...] per call], and the
+    flush kernels' records. None if the run failed."""
+    d = os.path.join(outdir, tag)
+    cmd = ["rocprofv3"] + tool_args + ["--output-format", "csv", "-d", d, "-o", "p", "--",
+                                       sys.executable, os.path.abspath(__file__), "--profile-child", mode]
     env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
-    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=150, env=env, cwd=ROOT)
-    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
-    if r.returncode != 0 and not files:
-        log("rocprofv3 --pmc %s failed (rc %d): %s" % (counter, r.returncode, r.stdout.decode(errors="replace")[-400:]))
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=170, env=env, cwd=ROOT)
+    pmc = "--pmc" in tool_args
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv" if pmc else "*kernel_trace.csv"), recursive=True)
+    if not files:
+        log("rocprofv3 %s failed (rc %d): %s" % (" ".join(tool_args), r.returncode, r.stdout.decode(errors="replace")[-400:]))
         return None
-    vals = {"qgemm": [], "flush": []}
+    disp = {}
     for f in files:
         with open(f) as fh:
             for row in csv.DictReader(fh):
-                if row.get("Counter_Name") != counter:
-                    continue
-                name = row["Kernel_Name"]
-                if "qgemm_k<4>" in name:
-                    vals["qgemm"].append(float(row["Counter_Value"]))
-                elif "binary" in name and int(row.get("Grid_Size", 0) or 0) >= FLUSH_ROWS * FLUSH_COLS // 16:
-                    vals["flush"].append(float(row["Counter_Value"]))
-    if not vals["qgemm"] or not vals["flush"]:
-        log("rocprofv3 --pmc %s: kernels not found in %s" % (counter, files))
-        return None
-    return {k: sum(v) / len(v) for k, v in vals.items()}
+                did = int(row.get("Dispatch_Id") or row.get("Correlation_Id") or len(disp))
+                e = disp.setdefault(did, {"name": row["Kernel_Name"],
+                                          "grid": int(row.get("Grid_Size") or row.get("Grid_Size_X") or 0), "v": {}})
+                if pmc:
+                    e["v"][row["Counter_Name"]] = e["v"].get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+                else:
+                    e["v"]["us"] = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3
+    segs, flushes = [], []
+    for did in sorted(disp):
+        e = disp[did]
+        if _is_flush(e["name"], e["grid"]):
+            flushes.append(e)
+            segs.append([])
+        elif segs:
+            segs[-1].append((_short(e["name"]), e["grid"], e["v"]))
+    return segs, flushes
 
 
-def measure_traffic(alg_bytes):
-    """HBM bytes per launch of the B = 4096 GEMM (calibrated FETCH_SIZE + WRITE_SIZE)."""
+def calibrated_traffic(fetch, write):
+    """Per-call HBM bytes from a FETCH_SIZE and a WRITE_SIZE run (KiB per
+    dispatch), each scaled by what the counter reads for the flush pass
+    (512 MiB read and 512 MiB written): [(bytes per call, per-kernel bytes)]
+    and the two factors."""
+    half = FLUSH_ROWS * FLUSH_COLS * 4
+    rf = half / (sum(e["v"]["FETCH_SIZE"] for e in fetch[1]) / len(fetch[1]) * 1024.0)
+    rw = half / (sum(e["v"]["WRITE_SIZE"] for e in write[1]) / len(write[1]) * 1024.0)
+    out = []
+    for sf, sw in zip(fetch[0], write[0]):
+        per = {}
+        for (n, _, vf), (_, _, vw) in zip(sf, sw):
+            per[n] = per.get(n, 0.0) + vf["FETCH_SIZE"] * 1024.0 * rf + vw["WRITE_SIZE"] * 1024.0 * rw
+        out.append((sum(per.values()), per))
+    return out, rf, rw
+
+
+def profile_c2(alg_bytes):
+    """Cold kernel durations (kernel trace) and calibrated HBM traffic per
+    batch of config 2: {batch: {"kernels_us": {...}, "us": total, "traffic":
+    bytes, "traffic_kernels": {...}}}, and a note."""
     if not shutil.which("rocprofv3"):
         return None, "rocprofv3 not found"
-    out = tempfile.mkdtemp(prefix="tgpmc")
+    out = tempfile.mkdtemp(prefix="tgprof")
     try:
-        f = pmc_run("FETCH_SIZE", out)
-        w = pmc_run("WRITE_SIZE", out) if f else None
+        kt = profiled(["--kernel-trace"], "c2", out, "kt")
+        fe = profiled(["--pmc", "FETCH_SIZE"], "c2", out, "fetch") if kt else None
+        wr = profiled(["--pmc", "WRITE_SIZE"], "c2", out, "write") if fe else None
     except subprocess.TimeoutExpired:
         return None, "rocprofv3 timed out"
     finally:
         shutil.rmtree(out, ignore_errors=True)
-    if not f or not w:
-        return None, "rocprofv3 --pmc gave no data"
-    half = FLUSH_ROWS * FLUSH_COLS * 4  # bytes read (and written) by one flush pass
-    rf = half / (f["flush"] * 1024.0)
-    rw = half / (w["flush"] * 1024.0)
-    traffic = f["qgemm"] * 1024.0 * rf + w["qgemm"] * 1024.0 * rw
-    note = ("FETCH_SIZE %.0f KiB x %.4f + WRITE_SIZE %.0f KiB x %.4f per dispatch (factors: 512 MiB / the flush "
-            "pass's reading); algorithmic %.1f MB" % (f["qgemm"], rf, w["qgemm"], rw, alg_bytes / 1e6))
-    return traffic, note
+    if not kt or len(kt[0]) != 2 * len(BATCHES):
+        return None, "kernel trace: %s segments" % (None if not kt else len(kt[0]))
+    res = {b: {"kernels_us": {}} for b in BATCHES}
+    for i, seg in enumerate(kt[0]):  # two calls per batch: averages
+        r = res[BATCHES[i % len(BATCHES)]]
+        for n, _, v in seg:
+            r["kernels_us"][n] = r["kernels_us"].get(n, 0.0) + v["us"] / 2
+    for r in res.values():
+        r["kernels_us"] = {k: round(v, 3) for k, v in r["kernels_us"].items()}
+        r["us"] = round(sum(r["kernels_us"].values()), 3)
+    note = "kernel trace of two cold calls per batch"
+    if fe and wr and len(fe[0]) == len(wr[0]) == 2 * len(BATCHES):
+        tr, rf, rw = calibrated_traffic(fe, wr)
+        for i, (tot, per) in enumerate(tr):
+            r = res[BATCHES[i % len(BATCHES)]]
+            r["traffic"] = r.get("traffic", 0.0) + tot / 2
+            tk = r.setdefault("traffic_kernels", {})
+            for k, v in per.items():
+                tk[k] = tk.get(k, 0.0) + v / 2
+        note += "; traffic = FETCH_SIZE x %.4f + WRITE_SIZE x %.4f (factors: 512 MiB / the flush pass's reading)" % (rf, rw)
+    else:
+        note += "; traffic counters gave no data"
+    return res, note
 
 
-def ref_cpu(text, rows, per, nout, nthink, threads, fixed, what):
-    """The reference interpreter (or the oracle restatement) over `rows`."""
-    from oracle import oracle as O
-    tmp = tempfile.mkdtemp(prefix="tgbench")
-    try:
-        if O.have_ref():
-            mpath = os.path.join(tmp, "model.tgir")
-            with open(mpath, "w") as f:
-                f.write(text)
-            _, _, ms = O.ref_batch(mpath, rows, per, nout, nthink, tmp, threads=threads, fixed=fixed)
-            kind = "reference"
-        else:
-            m = O.Model(text)
-            t0 = time.perf_counter()
-            (m.batch_fixed if fixed else m.batch)(rows, threads=threads)
-            ms = (time.perf_counter() - t0) * 1e3
-            kind = "port"
-    finally:
-        shutil.rmtree(tmp, ignore_errors=True)
-    return {"value": len(rows) / (ms / 1e3), "unit": "rows/s", "cores": threads, "kind": kind,
-            "sample": "%d rows of %s through the %s interpreter, -j %d, compute time only" % (
-                len(rows), what, "reference's" if kind == "reference" else "oracle's", threads)}
-
-
-def bench_config1(args):
+def config1_leg(args, steps=None):
     """Config 1: int8 MLP 512 -> 2048 -> 2048 -> 512 (tanh, tanh, rmsnorm), 65,536
     rows in one device pass. roofline: the three quantized GEMMs, 12.58 M
     algorithmic ops per row, against 5000 TOP/s dense int8."""
@@ -218,7 +304,7 @@ def bench_config1(args):
     for _ in range(args.warmup):
         prog.batch_device(d_x.ptr, rows, d_y.ptr)
     prog.sync()
-    steps = max(1, min(args.steps, 10))
+    steps = steps or max(1, min(args.steps, 10))
     t0 = time.perf_counter()
     for _ in range(steps):
         prog.batch_device(d_x.ptr, rows, d_y.ptr)
@@ -235,30 +321,61 @@ def bench_config1(args):
     st = tprog.stats()
     mfma_us, dig_us, oth_us = (v / 3 * 1e3 for v in (st.qgemm_ms, st.digits_ms, st.other_ms))
     ops = 2.0 * (2048 * 512 + 2048 * 2048 + 512 * 2048) * rows
-    log("config 1: %.1f ms per pass: GEMMs %.0f us, digits %.0f us, other %.0f us" % (
+    log("config 1: %.2f ms per pass: GEMMs %.0f us, digits %.0f us, other %.0f us" % (
         elapsed / steps * 1e3, mfma_us, dig_us, oth_us))
-    cpu = None if args.no_cpu else ref_cpu(text, X[:2048], 512, 512, 0, args.cpu_threads, False,
+    cpu = None if args.no_cpu else ref_cpu(text, X[:2048], 512, 512, 0, auto_threads(), False,
                                            "config 1 (int8 MLP 512-2048-2048-512)")
-    out = {
+    frac = ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS
+    return {
         "metric": "config 1 int8 MLP rows/sec at 1 GPU; % of int8-MFMA roofline", "value": round(rows * steps / elapsed, 1),
         "unit": "rows/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(elapsed / steps * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8", "data": "synthetic (rand(1, 0.05) weights quantized int8 RTN, N(0,1) rows seed 0)",
+        "dtype": "W8A32", "data": "synthetic (rand(1, 0.05) weights quantized int8 RTN, N(0,1) rows seed 0)",
         "config": {"workload": "config 1: int8 MLP 512-2048-2048-512, tanh, rmsnorm; 65,536 rows per step"},
         "roofline": {"bound": "mfma", "achieved": round(ops / mfma_us / 1e6, 2), "peak": MFMA_I8_PEAK_TOPS,
-                     "unit": "TOP/s", "frac": round(ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS, 4), "traffic": None,
+                     "unit": "TOP/s", "frac": round(frac, 4), "traffic": None,
+                     "limb_factor": 3, "hw_mfma_frac": round(3 * frac, 4),
                      "kernel": "the three quantized GEMMs of a pass (qgemm_k<8>), summed",
                      "alg_ops_per_launch": ops, "avg_kernel_us": round(mfma_us, 1)},
         "cpu_baseline": cpu,
         "breakdown_us": {"gemm": round(mfma_us, 1), "digits": round(dig_us, 1), "other": round(oth_us, 1)},
     }
-    print(json.dumps(out), flush=True)
 
 
-def bench_config4(args):
+def bench_config1(args):
+    print(json.dumps(config1_leg(args)), flush=True)
+
+
+VALU_PEAK_GINST = 256 * 2.4  # wave64 VALU instructions per ns: one per CU per clock (4 SIMDs, 4 clocks each), 2.4 GHz
+
+
+def profile_c4():
+    """config 4's row kernel under rocprofv3: cold kernel duration (kernel
+    trace) and VALU instructions per dispatch (SQ_INSTS_VALU), averaged over
+    two passes; (us, insts) or (None, None)."""
+    if not shutil.which("rocprofv3"):
+        return None, None
+    out = tempfile.mkdtemp(prefix="tgprof")
+    try:
+        kt = profiled(["--kernel-trace"], "c4", out, "kt")
+        pm = profiled(["--pmc", "SQ_INSTS_VALU", "SQ_BUSY_CYCLES"], "c4", out, "valu") if kt else None
+    except subprocess.TimeoutExpired:
+        return None, None
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+    if not kt or not pm:
+        return None, None
+    us = [v["us"] for seg in kt[0] for n, _, v in seg if n.startswith("rowprog_k")]
+    ins = [v.get("SQ_INSTS_VALU", 0.0) for seg in pm[0] for n, _, v in seg if n.startswith("rowprog_k")]
+    return (sum(us) / len(us) if us else None), (sum(ins) / len(ins) if ins else None)
+
+
+def config4_leg(args, steps=None, profile=True):
     """Config 4: the Q16.16 latent reasoner (think <= 32 steps, halting at
     d <= 7) over 1,048,576 rows of {0, 1}^8, one device pass. Integer VALU
-    work; the HBM fraction is reported for completeness."""
+    work: the roofline is VALU instruction issue (rocprofv3 SQ_INSTS_VALU
+    over the kernel's duration) against one wave64 instruction per CU per
+    clock; the HBM fraction is shown beside it."""
     import numpy as np
     from technograd_amd import hip, synth
     rows = 1048576
@@ -274,7 +391,7 @@ def bench_config4(args):
     for _ in range(args.warmup):
         prog.batch_device(d_x.ptr, rows, d_y.ptr, d_s.ptr)
     prog.sync()
-    steps = max(1, min(args.steps, 10))
+    steps = steps or max(1, min(args.steps, 10))
     t0 = time.perf_counter()
     for _ in range(steps):
         prog.batch_device(d_x.ptr, rows, d_y.ptr, d_s.ptr)
@@ -284,21 +401,34 @@ def bench_config4(args):
     byts = rows * (8 * 4 + 4 * 4 + 4)
     t = elapsed / steps
     log("config 4: %.2f ms per pass, mean think steps %.2f" % (t * 1e3, st.mean()))
-    cpu = None if args.no_cpu else ref_cpu(text, xq[:65536], 8, 4, 1, args.cpu_threads, True,
+    kus, ins = profile_c4() if profile else (None, None)
+    if kus and ins:
+        roof = {"bound": "valu", "achieved": round(ins / kus / 1e3, 2), "peak": VALU_PEAK_GINST, "unit": "Ginst/s",
+                "frac": round(ins / kus / 1e3 / VALU_PEAK_GINST, 4), "traffic": None,
+                "valu_insts_per_launch": ins, "avg_kernel_us": round(kus, 1),
+                "hbm_frac": round(byts / (kus * 1e-6) / 1e9 / HBM_PEAK_GBS, 5),
+                "kernel": "rowprog_k<true> (one lane per row; wave64 VALU instructions per second from rocprofv3 "
+                          "SQ_INSTS_VALU over the kernel-trace duration, peak one per CU per clock at 2.4 GHz)"}
+    else:
+        roof = {"bound": "valu", "achieved": None, "peak": VALU_PEAK_GINST, "unit": "Ginst/s", "frac": None,
+                "traffic": None, "hbm_frac": round(byts / t / 1e9 / HBM_PEAK_GBS, 5),
+                "kernel": "rowprog_k<true>: rocprofv3 gave no data"}
+    cpu = None if args.no_cpu else ref_cpu(text, xq[:131072], 8, 4, 1, auto_threads(), True,
                                            "config 4 (Q16.16 latent reasoner)")
-    out = {
+    return {
         "metric": "config 4 Q16.16 latent reasoner rows/sec at 1 GPU", "value": round(rows / t, 1), "unit": "rows/s",
         "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "q16.16 (int32)",
+        "scaling": "weak", "vs_baseline": None, "dtype": "q16.16 (int32, int64 products)",
         "data": "synthetic (rows uniform in {0,1}^8, seed 4)",
         "config": {"workload": "config 4: latent reasoner, think <= 32 steps, 1,048,576 rows per step",
                    "mean_think_steps": round(float(st.mean()), 3)},
-        "roofline": {"bound": "hbm", "achieved": round(byts / t / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(byts / t / 1e9 / HBM_PEAK_GBS, 5), "traffic": None,
-                     "kernel": "rowprog_k<true> (one lane per row, integer VALU bound; HBM shown for completeness)"},
+        "roofline": roof,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
+
+
+def bench_config4(args):
+    print(json.dumps(config4_leg(args)), flush=True)
 
 
 def q3_macs_per_token(L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, T=512):
@@ -393,17 +523,18 @@ def bench_config3(args):
             for L in (1, 2):
                 log("config 3: cpu baseline, the reference at %d layer(s)" % L)
                 tx = synth.qwen3_tgir("q3cpu", L=L, V=2048, T=T)
-                r = ref_cpu(tx, Xs, T, 2048, 0, args.cpu_threads, False, "")
+                r = ref_cpu(tx, Xs, T, 2048, 0, auto_threads(), False, "", runs=1)
                 secs.append(cs / r["value"])
             layer = secs[1] - secs[0]
             rest = secs[0] - layer  # embedding and the 2048-column LM head
             full = 28 * layer + rest * V / 2048.0
-            cpu = {"value": round(cs * T / full, 2), "unit": "prompt tokens/s", "cores": args.cpu_threads,
+            cpu = {"value": round(cs * T / full, 2), "unit": "prompt tokens/s", "cores": auto_threads(),
                    "kind": "reference",
                    "sample": "%d prompts x %d tokens through the reference's interpreter at 1 and 2 layers (full widths, "
                              "vocabulary 2048, -j %d): %.1f s per added layer, %.1f s for the rest; extrapolated to 28 "
                              "layers and the 151,936-column LM head: %.0f s for the %d prompts"
-                             % (cs, T, args.cpu_threads, layer, rest, full, cs)}
+                             % (cs, T, auto_threads(), layer, rest, full, cs)}
+            cpu.update(cpu_info())
     out = {
         "metric": "config 3 generated tokens/sec at 1 GPU (64 sequences: 512-token prompt, 128 greedy tokens)",
         "value": round(seqs * GEN / t_gen, 1), "unit": "generated tokens/s", "n_gpus": 1, "steps": 1, "warmup": 1,
@@ -477,7 +608,7 @@ def bench_config5(args):
     ops = 2.0 * macs * rows
     log("config 5: %.1f ms per 4096 sequences: projections %.0f us, digits %.0f us, other (scan, elementwise) %.0f us"
         % (t * 1e3, mfma_us, dig_us, oth_us))
-    cpu = None if args.no_cpu else ref_cpu(text, X[:32], per, 8, 0, args.cpu_threads, False,
+    cpu = None if args.no_cpu else ref_cpu(text, X[:32], per, 8, 0, auto_threads(), False,
                                            "config 5 (selective SSM, 4 blocks, T 512)")
     out = {
         "metric": "config 5 selective-SSM sequences/sec at 1 GPU", "value": round(rows / t, 1), "unit": "sequences/s",
@@ -500,26 +631,26 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-rows", type=int, default=96)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-rows", type=int, default=2048, help="config 2 rows of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 runs (kernel trace and counters)")
+    ap.add_argument("--no-legs", action="store_true", help="skip the config 1 and config 4 legs")
     ap.add_argument("--reps", type=int, default=10, help="kernel-timing repetitions per batch")
     ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
                     help="BASELINE configuration: 2 (default, the headline metric), 1 (int8 MLP), 3 (Qwen3-shaped "
                          "decoder, prefill), 4 (Q16.16 reasoner), 5 (selective-SSM classifier)")
-    ap.add_argument("--profile-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--profile-child", choices=("c2", "c4"), help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.profile_child:
-        profile_child()
-        return
-    if args.config != 2 and args.gpus == 1:
-        {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}[args.config](args)
+        profile_child(args.profile_child)
         return
     if args.gpus != 1:
         print("bench.py: this backend runs on one GPU per process and this build measures one GPU only; "
               "rows shard across GPUs with no collective (see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.config != 2:
+        {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}[args.config](args)
+        return
 
     import numpy as np
     from technograd_amd import hip, synth
@@ -575,9 +706,9 @@ def main():
             "hbm_frac": round(byts / (mfma_us + dig_us) / 1e3 / HBM_PEAK_GBS, 4),
             "mfma_TOPs": round(ops / mfma_us / 1e6, 2),
             "mfma_frac": round(ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS, 4),
-            "cold_infinity_cache": True,
+            "cold_infinity_cache": True, "timing": "HIP events around each kernel (dispatch latency included)",
         })
-        log("batch %4d: mfma %.2f us, digits %.2f us" % (b, mfma_us, dig_us))
+        log("batch %4d: events: product %.2f us, digits %.2f us" % (b, mfma_us, dig_us))
     big = sweep[-1]
     fprog.set_stream(None)
 
@@ -590,32 +721,65 @@ def main():
     pcie_rps = 3 * 4096 / (time.perf_counter() - t0)
     log("host-buffer batch 4096: %.0f rows/s (PCIe in and out included)" % pcie_rps)
 
-    traffic, tnote = None, "skipped (--no-traffic)"
+    # ---- rocprofv3: cold kernel durations and HBM traffic per batch ----
+    prof, pnote = None, "skipped (--no-traffic)"
     if not args.no_traffic:
-        log("traffic: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
-        traffic, tnote = measure_traffic(big["alg_bytes"])
-        log("traffic: %s" % tnote)
+        log("rocprofv3: kernel trace, FETCH_SIZE, WRITE_SIZE of the profiling child")
+        prof, pnote = profile_c2(big["alg_bytes"])
+        log("rocprofv3: %s" % pnote)
+    if prof:
+        for e in sweep:
+            p = prof[e["batch"]]
+            e["trace_kernels_us"] = p["kernels_us"]
+            e["trace_us"] = p["us"]
+            e["trace_hbm_frac"] = round(e["alg_bytes"] / p["us"] / 1e3 / HBM_PEAK_GBS, 4)
+            if "traffic" in p:
+                e["traffic"] = round(p["traffic"])
+    big_traffic = prof[4096].get("traffic_kernels", {}).get("qgemm_k<4>") if prof else None
     roofline = {"bound": "mfma", "achieved": big["mfma_TOPs"], "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
-                "frac": big["mfma_frac"], "traffic": None if traffic is None else round(traffic),
-                "traffic_note": tnote,
+                "frac": big["mfma_frac"], "traffic": None if big_traffic is None else round(big_traffic),
+                "traffic_note": pnote,
+                "limb_factor": 3, "hw_mfma_frac": round(3 * big["mfma_frac"], 4),
+                "hw_note": "each multiply-add runs as three exact int8 MFMAs (the activation's 24-bit digits): the matrix "
+                           "cores execute 3 x alg_ops; hw_mfma_frac = 3 x frac",
                 "kernel": "qgemm_k<4> (int8 MFMA, 3 activation digits) at batch 4096",
-                "alg_ops_per_launch": big["alg_ops"], "avg_kernel_us": big["mfma_kernel_us"]}
+                "alg_ops_per_launch": big["alg_ops"], "avg_kernel_us": big["mfma_kernel_us"],
+                "trace_kernel_us": None if not prof else prof[4096]["kernels_us"].get("qgemm_k<4>")}
+    if prof:
+        mv = {}
+        for b in (1, 16):
+            p, e = prof[b], sweep[BATCHES.index(b)]
+            mv["b%d" % b] = {"kernels": sorted(p["kernels_us"]), "us": p["us"],
+                             "achieved": round(e["alg_bytes"] / p["us"] / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(e["alg_bytes"] / p["us"] / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": e["alg_bytes"],
+                             "traffic": None if "traffic" not in p else round(p["traffic"])}
+        mv["note"] = ("int4 matvec: algorithmic bytes (weights, scales, rows in and out) over the summed kernel-trace "
+                      "durations of the call's kernels (one kernel at B=1: its digits are made inside it), each call "
+                      "after a 512 MiB flush pass; traffic: calibrated FETCH_SIZE + WRITE_SIZE of the same kernels")
+        roofline["matvec"] = mv
 
     cpu = None
     if not args.no_cpu:
-        log("cpu baseline: %d rows, %d threads" % (args.cpu_rows, args.cpu_threads))
-        cpu = cpu_baseline(text, X, args.cpu_rows, args.cpu_threads)
+        log("cpu baseline: %d rows, -j auto (%d threads), 3 runs" % (args.cpu_rows, auto_threads()))
+        cpu = ref_cpu(text, X[:args.cpu_rows], K, C, 0, auto_threads(), False, "config 2 (int4 4096x4096)")
+
+    legs = None
+    if not args.no_legs:
+        legs = {"config1": config1_leg(args, steps=3), "config4": config4_leg(args, steps=3, profile=not args.no_traffic)}
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "scaling": "weak", "vs_baseline": None, "dtype": "W4A32",
+        "dtype_note": "int4 weights x f32 activations, computed exactly as three int8 digit planes of each row's 24-bit "
+                      "fixed-point form on the int8 matrix cores (int32 sums, combined in int64/f64, one f32 rounding)",
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) rows)",
         "config": {"workload": "config 2: int4 4096x4096 linear, one pass at each batch of {1,16,256,4096} rows per step",
                    "rows_per_step": rows_per_step, "parallelism": "1 GPU"},
         "roofline": roofline, "cpu_baseline": cpu, "sweep": sweep,
         "pcie_inclusive": {"rows_per_s": round(pcie_rps, 1), "batch": 4096,
                            "note": "tg_hip_batch with host buffers: 64 MiB in and 64 MiB out over PCIe per call"},
+        "legs": legs,
     }
     print(json.dumps(out), flush=True)
 

@@ -161,8 +161,10 @@ def ref_ir(model_path):
     return ref_run(["ir", model_path]).stdout.decode()
 
 
-def ref_batch(model_path, rows, per, nout, nthink, workdir, threads=1, fixed=False):
-    """Run the reference VM (or its Q16.16 kernels with fixed=True) over rows."""
+def ref_batch(model_path, rows, per, nout, nthink, workdir, threads=1, fixed=False, wall=False):
+    """Run the reference VM (or its Q16.16 kernels with fixed=True) over rows.
+    Returns (out, steps, compute ms), and the wall ms as a fourth item with
+    wall=True (from before the input load to after the last write)."""
     dt = np.int32 if fixed else np.float32
     inp, outp, stp = (os.path.join(workdir, n) for n in ("ref_in.bin", "ref_out.bin", "ref_steps.bin"))
     np.ascontiguousarray(rows, dtype=dt).astype("<" + dt().dtype.str[1:]).tofile(inp)
@@ -172,11 +174,13 @@ def ref_batch(model_path, rows, per, nout, nthink, workdir, threads=1, fixed=Fal
     r = ref_run(args)
     out = np.fromfile(outp, dtype=dt).reshape(-1, nout)
     steps = np.fromfile(stp, dtype=np.int32).reshape(-1, max(nthink, 1))
-    ms = None
+    ms = wall_ms = None
     for line in r.stderr.decode().splitlines():
         if line.startswith("ref-batch"):
-            ms = float(line.split()[-1])
-    return out, steps, ms
+            f = line.split()
+            ms = float(f[f.index("ms") + 1])
+            wall_ms = float(f[f.index("wall_ms") + 1])
+    return (out, steps, ms, wall_ms) if wall else (out, steps, ms)
 
 
 def ref_unit(model_path, rows_q16, nout, nthink, workdir):

@@ -15,8 +15,10 @@
  *   tgc_ref quantize MODEL [-o OUT] [--bits B] ...    the reference quantizer
  *   tgc_ref batch MODEL ROWS.bin -o OUT.bin [-j N] [--steps S.bin] [--fixed]
  *       ROWS: raw f32 (or raw int32 Q16.16 with --fixed); OUT likewise;
- *       S: raw int32 steps per row and think loop. Prints compute time (ms)
- *       and threads on stderr as `ref-batch rows R threads T ms M`.
+ *       S: raw int32 steps per row and think loop. Prints the compute time
+ *       (ms), the wall time from before the input load to after the last
+ *       write (the reference's `batch` trace, src/main.c:413-443) and the
+ *       threads on stderr as `ref-batch rows R threads T ms M wall_ms W`.
  *   tgc_ref c MODEL -o UNIT.c [--fixed] [--harness MAIN.c]
  *       the reference's C generator (src/cgen.c, cgen_mode) on the loaded and
  *       planned module, as `tgc c` runs it (src/main.c:446-470). --harness
@@ -98,6 +100,7 @@ static int batch(int argc, char **argv)
 	for (int i = 0; i < m->ninputs; i++) per += shape_numel(&m->val[m->inputs[i]].sh);
 	int n = shape_numel(&m->val[m->output].sh), nt = m->nthink ? m->nthink : 1;
 	int cnt;
+	double w0 = now_ms(); /* wall time as the reference's batch trace takes it: input load to last write (src/main.c:413-443) */
 	float *all = io_load(data, &cnt); /* raw little-endian 32-bit words */
 	if (cnt % per) die(NULL, 0, "'%s': %d values is not a multiple of the %d per sample", data, cnt, per);
 	int rows = cnt / per, th = par_threads(), afl = m->arena ? m->arena : 1;
@@ -119,7 +122,6 @@ static int batch(int argc, char **argv)
 		par_for(c, grain > 0 ? grain : 1, rows_fn, &jb);
 	}
 	double ms = now_ms() - t0;
-	fprintf(stderr, "ref-batch rows %d threads %d ms %.3f\n", rows, th, ms);
 	FILE *f = fopen(opath, "wb");
 	if (!f) die(NULL, 0, "cannot write '%s'", opath);
 	fwrite(j.out, 4, (size_t)rows * n, f);
@@ -130,6 +132,7 @@ static int batch(int argc, char **argv)
 		fwrite(j.steps, sizeof(int), (size_t)rows * nt, f);
 		if (fclose(f)) die(NULL, 0, "write failed '%s'", spath);
 	}
+	fprintf(stderr, "ref-batch rows %d threads %d ms %.3f wall_ms %.3f\n", rows, th, ms, now_ms() - w0);
 	return 0;
 }
 
