@@ -1,31 +1,98 @@
 /* tgc-hip: `tgc batch` on the MI355X backend.
  *
- *   tgc-hip batch MODEL.tgir DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v]
+ *   tgc-hip batch MODEL.tgir DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v] [--log FILE]
  *
  * Same input/output contract as the reference's batch command
  * (src/main.c:400-444, src/io.c): DATA is raw little-endian f32 when it ends in
  * .bin or .f32, otherwise text rows of numbers separated by commas or blanks
  * with `#` comments (src/io.c:23-41); every row is validated before anything
- * is computed or the output file is created; outputs are written in input
- * order, text as %.9g with the steps of every think loop appended
- * (src/io.c:79-93), binary as raw f32 without steps. Stateful models and
- * models outside the backend are refused with a message (the reference CLI
- * runs those).
+ * is computed or the output file is created; rows run in blocks (device
+ * passes of up to --rows rows) and each block is written, in input order, as
+ * soon as it is done: text as %.9g with the steps of every think loop
+ * appended (src/io.c:79-93), binary as raw f32 without steps. SIGINT or
+ * SIGTERM stops the batch after the current block and the exit status is
+ * 128 + the signal number (src/main.c:418, :431, :444; src/serve.c:49-69).
+ * Stateful models and models outside the backend are refused with a message
+ * (the reference CLI runs those).
  *
  * --fixed runs the model in Q16.16 (the number system of `tgc c --fixed`
- * units): inputs are converted by rounding x * 2^16 half away from zero
- * (the decimal rule of tg_fx_parse, runtime/tg_rtq.h:375-401), text outputs
- * are printed with 6 decimals (tg_fx_format, :403-418) and binary outputs are
- * the exact f32 values q / 65536. -v prints the batch summary of
- * src/main.c:155-173 on stderr. */
+ * units): text inputs are read with the exact decimal rule of tg_fx_parse
+ * (runtime/tg_rtq.h:375-401: integer digits kept up to the first value of at
+ * least 100000, at most 12 fraction digits, an optional exponent, the
+ * rational value rounded half away from zero to 1/65536 and saturated),
+ * binary inputs by rounding x * 2^16 half away from zero; text outputs are
+ * printed with 6 decimals (tg_fx_format, :403-418) and binary outputs are
+ * the exact f32 values q / 65536.
+ *
+ * The environment variable TGC_HIP_TEST_SIGTERM_AFTER_BLOCKS=N makes the
+ * program send itself SIGTERM after N blocks (tests of the stop path).
+ *
+ * -v prints the batch summary of src/main.c:155-173 on stderr; --log FILE
+ * appends it as JSON Lines events (`batch`, then `think` per loop), the
+ * reference's trace format (src/trace.c: t, level, stage, msg, fields).
+ *
+ *   tgc-hip fxparse TOKEN...   prints each token's Q16.16 value (no device)
+ */
 #include "tg_hip.h"
 
 #include <math.h>
+#include <signal.h>
+#include <stdatomic.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
+
+/* the signal that asked the batch to stop (0: none) */
+static atomic_int stop_sig;
+static void on_signal(int sig) { atomic_store(&stop_sig, sig); }
+
+static void install_signals(void)
+{
+	struct sigaction sa;
+	memset(&sa, 0, sizeof sa);
+	sa.sa_handler = on_signal;
+	sigemptyset(&sa.sa_mask);
+	sigaction(SIGINT, &sa, NULL);
+	sigaction(SIGTERM, &sa, NULL);
+	signal(SIGPIPE, SIG_IGN);
+}
+
+/* One decimal token to Q16.16, the rule of tg_fx_parse: sign; integer digits
+ * accumulated while the value is below 100000 (later ones are dropped);
+ * fraction digits while fewer than 12 are held; exponent; value num / den with
+ * num scaled by 10 per positive exponent step while num <= 2^47 and den by 10
+ * per negative step; q = (num * 65536 + den / 2) / den, saturated, negated
+ * for a minus sign. Returns the end of the token, or NULL without digits. */
+static const char *fx_parse(const char *s, int32_t *v)
+{
+	int neg = 0;
+	if (*s == '-' || *s == '+') neg = *s++ == '-';
+	int64_t ip = 0, fn = 0, fd = 1;
+	int digits = 0;
+	for (; *s >= '0' && *s <= '9'; s++, digits++)
+		if (ip < 100000) ip = ip * 10 + (*s - '0');
+	if (*s == '.')
+		for (s++; *s >= '0' && *s <= '9'; s++, digits++)
+			if (fd < 1000000000000LL) fn = fn * 10 + (*s - '0'), fd *= 10;
+	if (!digits) return NULL;
+	int ex = 0;
+	if (*s == 'e' || *s == 'E') {
+		int eneg = 0;
+		s++;
+		if (*s == '-' || *s == '+') eneg = *s++ == '-';
+		for (; *s >= '0' && *s <= '9'; s++) ex = ex * 10 + (*s - '0');
+		if (eneg) ex = -ex;
+	}
+	int64_t num = ip * fd + fn, den = fd;
+	for (; ex > 0 && num <= ((int64_t)1 << 47); ex--) num *= 10;
+	for (; ex < 0; ex++) den *= 10;
+	int64_t q = (num * 65536 + den / 2) / den;
+	if (neg) q = -q;
+	*v = q > INT32_MAX ? INT32_MAX : q < INT32_MIN ? INT32_MIN : (int32_t)q;
+	return s;
+}
 
 static int die(const char *fmt, const char *a)
 {
@@ -59,15 +126,26 @@ static char *slurp(const char *path, size_t *len)
 	return b;
 }
 
-/* numbers of one text line; -1 on a bad token (src/io.c:25-41 rules) */
-static int parse_row(const char *s, float *v, int max, const char **bad)
+/* numbers of one text line (f32, or Q16.16 words with `fixed`); -1 on a bad
+ * token (src/io.c:25-41 rules) */
+static int parse_row(const char *s, float *v, int max, const char **bad, int fixed)
 {
 	int n = 0;
 	for (;;) {
 		while (*s == ' ' || *s == '\t' || *s == ',' || *s == '\r' || *s == '\n') s++;
 		if (!*s || *s == '#') return n;
-		char *e;
-		float x = strtof(s, &e);
+		const char *e;
+		float x;
+		if (fixed) {
+			int32_t q = 0;
+			e = fx_parse(s, &q);
+			if (!e) e = s;
+			memcpy(&x, &q, 4);
+		} else {
+			char *e2;
+			x = strtof(s, &e2);
+			e = e2;
+		}
 		if (e == s || (*e && !strchr(" \t,\r\n#", *e))) {
 			*bad = s;
 			return -1;
@@ -78,7 +156,9 @@ static int parse_row(const char *s, float *v, int max, const char **bad)
 	}
 }
 
-static float *load_rows(const char *path, int per, long *rows, char *err, size_t errn)
+/* every row of DATA: f32 values, or with `fixed` Q16.16 words (binary inputs
+ * are f32 either way; the caller converts them) */
+static float *load_rows(const char *path, int per, long *rows, char *err, size_t errn, int fixed)
 {
 	size_t len;
 	char *raw = slurp(path, &len);
@@ -112,7 +192,7 @@ static float *load_rows(const char *path, int per, long *rows, char *err, size_t
 			char *nl = strchr(s, '\n');
 			if (nl) *nl = 0;
 			const char *bad;
-			int k = parse_row(s, NULL, 0, &bad);
+			int k = parse_row(s, NULL, 0, &bad, fixed);
 			if (k < 0) {
 				snprintf(err, errn, "%s:%d: bad number near '%.20s'", path, line, bad);
 				free(raw);
@@ -126,7 +206,7 @@ static float *load_rows(const char *path, int per, long *rows, char *err, size_t
 				return NULL;
 			}
 			if (k > 0) {
-				if (pass) parse_row(s, all + (size_t)r * per, per, &bad);
+				if (pass) parse_row(s, all + (size_t)r * per, per, &bad, fixed);
 				r++;
 			}
 			if (nl) *nl = '\n';
@@ -159,13 +239,72 @@ static double now_ms(void)
 	return t.tv_sec * 1e3 + t.tv_nsec / 1e6;
 }
 
+/* one JSON Lines event in the reference's trace format: t, level, stage, msg,
+ * then `fields` (already JSON text, starting with a comma) */
+static void log_event(FILE *lf, const char *stage, const char *msg, const char *fields)
+{
+	if (!lf) return;
+	struct timespec ts;
+	timespec_get(&ts, TIME_UTC);
+	fprintf(lf, "{\"t\":%.3f,\"level\":\"info\",\"stage\":\"%s\",\"msg\":\"%s\"%s}\n", (double)ts.tv_sec + ts.tv_nsec / 1e9, stage,
+		msg, fields);
+	fflush(lf);
+}
+
+static void write_block(FILE *f, int obin, int fixed, const float *out, const int *steps, long n, int nout, int nthink, int nt)
+{
+	char buf[32];
+	for (long r = 0; r < n; r++) {
+		const float *y = out + (size_t)r * nout;
+		if (obin) {
+			for (int i = 0; i < nout; i++) {
+				float v = y[i];
+				if (fixed) {
+					int32_t q;
+					memcpy(&q, &y[i], 4);
+					v = (float)((double)q / 65536.0);
+				}
+				uint32_t w;
+				memcpy(&w, &v, 4);
+				unsigned char b[4] = { (unsigned char)w, (unsigned char)(w >> 8), (unsigned char)(w >> 16), (unsigned char)(w >> 24) };
+				fwrite(b, 1, 4, f);
+			}
+			continue;
+		}
+		for (int i = 0; i < nout; i++) {
+			if (fixed) {
+				int32_t q;
+				memcpy(&q, &y[i], 4);
+				fx_format(q, buf);
+				fprintf(f, "%s%s", i ? "," : "", buf);
+			} else {
+				fprintf(f, "%s%.9g", i ? "," : "", (double)y[i]);
+			}
+		}
+		for (int t = 0; t < nthink; t++) fprintf(f, ",%d", steps[(size_t)r * nt + t]);
+		fputc('\n', f);
+	}
+}
+
+#define USAGE "usage: tgc-hip batch MODEL.tgir DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v] [--log FILE]%s"
+
 int main(int argc, char **argv)
 {
-	const char *model = NULL, *data = NULL, *opath = NULL;
+	const char *model = NULL, *data = NULL, *opath = NULL, *lpath = NULL;
 	int flags = 0, verbose = 0, maxrows = 16384;
-	if (argc < 2 || strcmp(argv[1], "batch")) return die("usage: tgc-hip batch MODEL.tgir DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v]%s", "");
+	if (argc >= 2 && !strcmp(argv[1], "fxparse")) { /* the --fixed text rule, for tests (no device) */
+		for (int i = 2; i < argc; i++) {
+			int32_t q;
+			const char *e = fx_parse(argv[i], &q);
+			if (!e || *e) printf("error\n");
+			else printf("%d\n", q);
+		}
+		return 0;
+	}
+	if (argc < 2 || strcmp(argv[1], "batch")) return die(USAGE, "");
 	for (int i = 2; i < argc; i++) {
 		if (!strcmp(argv[i], "-o") && i + 1 < argc) opath = argv[++i];
+		else if (!strcmp(argv[i], "--log") && i + 1 < argc) lpath = argv[++i];
 		else if (!strcmp(argv[i], "--fixed")) flags |= TG_HIP_FIXED;
 		else if (!strcmp(argv[i], "--exact")) flags |= TG_HIP_EXACT;
 		else if (!strcmp(argv[i], "--rows") && i + 1 < argc) maxrows = atoi(argv[++i]);
@@ -174,7 +313,10 @@ int main(int argc, char **argv)
 		else if (!data) data = argv[i];
 		else return die("unexpected argument '%s'", argv[i]);
 	}
-	if (!model || !data) return die("usage: tgc-hip batch MODEL.tgir DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v]%s", "");
+	if (!model || !data || maxrows < 1) return die(USAGE, "");
+	const int fixed = (flags & TG_HIP_FIXED) != 0;
+	FILE *lf = NULL;
+	if (lpath && !(lf = fopen(lpath, "a"))) return die("cannot open log '%s'", lpath);
 	double t0 = now_ms();
 	size_t mlen;
 	char *text = slurp(model, &mlen);
@@ -188,81 +330,77 @@ int main(int argc, char **argv)
 	int nt = nthink ? nthink : 1;
 	char err[512];
 	long rows;
-	float *all = load_rows(data, per, &rows, err, sizeof err); /* everything is validated before the output exists */
+	double tb = now_ms(); /* the reference's batch timer starts before the input load (src/main.c:413) */
+	float *all = load_rows(data, per, &rows, err, sizeof err, fixed && !is_binary(data)); /* validated before the output exists */
 	if (!all) return die("%s", err);
-	double tb = now_ms();
-	float *out = malloc((size_t)(rows ? rows : 1) * nout * sizeof *out);
-	int *steps = malloc((size_t)(rows ? rows : 1) * nt * sizeof *steps);
-	int rc;
-	if (flags & TG_HIP_FIXED) {
-		int32_t *q = malloc((size_t)(rows ? rows : 1) * per * sizeof *q);
+	if (fixed && is_binary(data)) /* f32 rows: x * 2^16 rounded half away from zero, saturated */
 		for (long i = 0; i < rows * per; i++) {
-			double s = (double)all[i] * 65536.0;
-			q[i] = s >= 2147483647.0 ? INT32_MAX : s <= -2147483648.0 ? INT32_MIN : (int32_t)llround(s);
+			double v = (double)all[i] * 65536.0;
+			int32_t q = v >= 2147483647.0 ? INT32_MAX : v <= -2147483648.0 ? INT32_MIN : (int32_t)llround(v);
+			memcpy(&all[i], &q, 4);
 		}
-		rc = tg_hip_batch_fixed(p, q, rows, (int32_t *)out, steps);
-		free(q);
-	} else {
-		rc = tg_hip_batch(p, all, rows, out, steps);
-	}
-	if (rc) return die("%s", tg_hip_error());
-	double tc = now_ms();
+	install_signals(); /* a stop request ends the batch after the current block */
+	const char *ra = getenv("TGC_HIP_TEST_SIGTERM_AFTER_BLOCKS");
+	const long raise_after = ra ? atol(ra) : 0;
 	int obin = opath && is_binary(opath);
 	FILE *f = opath ? fopen(opath, obin ? "wb" : "w") : stdout;
 	if (!f) return die("cannot write '%s'", opath);
-	char buf[32];
-	for (long r = 0; r < rows; r++) {
-		const float *y = out + (size_t)r * nout;
-		if (obin) {
-			for (int i = 0; i < nout; i++) {
-				float v = y[i];
-				if (flags & TG_HIP_FIXED) {
-					int32_t q;
-					memcpy(&q, &y[i], 4);
-					v = (float)((double)q / 65536.0);
-				}
-				uint32_t w;
-				memcpy(&w, &v, 4);
-				unsigned char b[4] = { (unsigned char)w, (unsigned char)(w >> 8), (unsigned char)(w >> 16), (unsigned char)(w >> 24) };
-				fwrite(b, 1, 4, f);
-			}
-			continue;
-		}
-		for (int i = 0; i < nout; i++) {
-			if (flags & TG_HIP_FIXED) {
-				int32_t q;
-				memcpy(&q, &y[i], 4);
-				fx_format(q, buf);
-				fprintf(f, "%s%s", i ? "," : "", buf);
-			} else {
-				fprintf(f, "%s%.9g", i ? "," : "", (double)y[i]);
-			}
-		}
-		for (int t = 0; t < nthink; t++) fprintf(f, ",%d", steps[(size_t)r * nt + t]);
-		fputc('\n', f);
-	}
-	if (opath && (ferror(f) | fclose(f))) return die("write failed '%s'", opath);
-	if (verbose) {
+	const long block = maxrows;
+	float *out = malloc((size_t)(rows < block ? (rows ? rows : 1) : block) * nout * sizeof *out);
+	int *steps = malloc((size_t)(rows < block ? (rows ? rows : 1) : block) * nt * sizeof *steps);
+	long *ssum = calloc((size_t)nt, sizeof *ssum), done = 0;
+	int *smin = calloc((size_t)nt, sizeof *smin), *smax = calloc((size_t)nt, sizeof *smax);
+	double dev_ms = 0;
+	for (long b0 = 0; b0 < rows && !atomic_load(&stop_sig); b0 += block) {
+		const long n = rows - b0 < block ? rows - b0 : block;
+		int rc = fixed ? tg_hip_batch_fixed(p, (const int32_t *)(all + (size_t)b0 * per), n, (int32_t *)out, steps)
+			       : tg_hip_batch(p, all + (size_t)b0 * per, n, out, steps);
+		if (rc) return die("%s", tg_hip_error());
 		tg_hip_stats_t st;
 		tg_hip_stats(p, &st);
-		double ms = now_ms() - tb;
-		fprintf(stderr, "[batch] %ld row(s) in %.2f ms (%.3f us/row) on gfx950, %s executor, device %.3f ms, load %.1f ms, compute %.2f ms\n",
-			rows, ms, rows ? 1e3 * ms / rows : 0.0, st.executor ? "row-program" : "layer", st.batch_ms, tb - t0, tc - tb);
-		for (int t = 0; t < nthink && rows; t++) {
-			long sum = 0;
-			int mn = steps[t], mx = steps[t];
-			for (long r = 0; r < rows; r++) {
-				int s = steps[(size_t)r * nt + t];
-				sum += s;
-				mn = s < mn ? s : mn;
-				mx = s > mx ? s : mx;
+		dev_ms += st.batch_ms;
+		for (int t = 0; t < nthink; t++)
+			for (long r = 0; r < n; r++) {
+				const int sv = steps[(size_t)r * nt + t];
+				if (!done && !r) smin[t] = smax[t] = sv;
+				ssum[t] += sv;
+				smin[t] = sv < smin[t] ? sv : smin[t];
+				smax[t] = sv > smax[t] ? sv : smax[t];
 			}
-			fprintf(stderr, "[think] think[%d] over batch: steps min %d mean %.2f max %d\n", t, mn, (double)sum / rows, mx);
+		write_block(f, obin, fixed, out, steps, n, nout, nthink, nt);
+		done += n;
+		if (raise_after > 0 && done / block == raise_after) raise(SIGTERM); /* test hook: a stop request from outside */
+	}
+	if (opath && (ferror(f) | fclose(f))) return die("write failed '%s'", opath);
+	const double ms = now_ms() - tb;
+	if (verbose || lf) {
+		tg_hip_stats_t st;
+		tg_hip_stats(p, &st);
+		char msg[512], fields[512];
+		snprintf(msg, sizeof msg, "%ld row(s) in %.2f ms (%.1f us/row) on gfx950, %s executor, device %.3f ms%s", done, ms,
+			 done ? 1e3 * ms / done : 0.0, st.executor ? "row-program" : "layer", dev_ms,
+			 atomic_load(&stop_sig) ? " (stopped by signal)" : "");
+		snprintf(fields, sizeof fields, ",\"rows\":%ld,\"threads\":1,\"sequential_rows\":0,\"ms\":%.9g,\"us_per_row\":%.9g,"
+			 "\"device\":\"gfx950\",\"device_ms\":%.9g,\"load_ms\":%.9g", done, ms, done ? 1e3 * ms / done : 0.0, dev_ms, tb - t0);
+		if (verbose) fprintf(stderr, "[batch] %s\n", msg);
+		log_event(lf, "batch", msg, fields);
+		for (int t = 0; t < nthink && done; t++) {
+			snprintf(msg, sizeof msg, "think[%d] over batch: steps min %d mean %.2f max %d", t, smin[t], (double)ssum[t] / done,
+				 smax[t]);
+			snprintf(fields, sizeof fields, ",\"loop\":%d,\"steps_min\":%d,\"steps_mean\":%.9g,\"steps_max\":%d", t, smin[t],
+				 (double)ssum[t] / done, smax[t]);
+			if (verbose) fprintf(stderr, "[think] %s\n", msg);
+			log_event(lf, "think", msg, fields);
 		}
 	}
+	if (lf) fclose(lf);
 	tg_hip_free(p);
 	free(all);
 	free(out);
 	free(steps);
-	return 0;
+	free(ssum);
+	free(smin);
+	free(smax);
+	const int sig = atomic_load(&stop_sig);
+	return sig ? 128 + sig : 0;
 }

@@ -19,6 +19,7 @@ Run (all variants, or the named ones):
     python tests/golden/make_golden.py [NAME ...]
 """
 import itertools
+import json
 import os
 import subprocess
 import sys
@@ -93,11 +94,66 @@ def rows_for(name, per, seed):
     return x
 
 
+IDENTITY = "(tgir 1\n  (model idn)\n  (input x (f32 1))\n  (block\n    (%0 (f32 1) (reshape x))\n  )\n  (output %0))\n"
+
+
+def fx_tokens():
+    """Decimal tokens for the Q16.16 text rule: hand cases (ties at 1/131072,
+    the 100000 integer cut, 12 fraction digits, exponents, saturation) and
+    seeded random ones."""
+    hand = ["0", "-0", "+0", "1", "-1", "0.5", ".5", "5.", "-.25", "1e3", "1E-3", "2.5e+2", "-2.5e-2", "1e", "0.0000076293945",
+            "0.00000762939453125", "0.0000076293945313", "-0.00000762939453125", "3.00000762939453125", "32767.9999", "32768",
+            "-32768", "-32768.00001", "99999.5", "100000", "123456.75", "1234567.5", "0.123456789012345678", "1.000000000001",
+            "7e-5", "7.62939453125e-6", "1.52587890625e-5", "4.5e-1", "65535.99999", "1e10", "-1e10", "0.1e1", "10e-1"]
+    rng = np.random.default_rng(12)
+    rnd = []
+    for _ in range(1500):
+        ip = str(int(rng.integers(0, 10 ** int(rng.integers(0, 7)))))
+        fr = "".join(str(int(d)) for d in rng.integers(0, 10, size=int(rng.integers(0, 16))))
+        t = ("-" if rng.random() < 0.4 else "") + ip + ("." + fr if fr or rng.random() < 0.2 else "")
+        if rng.random() < 0.2:
+            t += "e%d" % int(rng.integers(-8, 6))
+        rnd.append(t)
+    return hand + rnd
+
+
+def make_fx_parse(tmp):
+    """tests/golden/fx_parse.json: each token's Q16.16 value as the
+    reference's tg_fx_parse reads it, through a `tgc c --fixed` unit of an
+    identity model and its decimal driver (which prints the value with
+    tg_fx_format's 6 decimals; 1/65536 steps are wider than 1e-6, so the
+    printed text names one value), and tokens the driver refuses."""
+    mpath = os.path.join(tmp, "idn.tgir")
+    with open(mpath, "w") as fh:
+        fh.write(IDENTITY)
+    unit, exe = os.path.join(tmp, "idn.c"), os.path.join(tmp, "idn")
+    O.ref_run(["c", mpath, "-o", unit, "--fixed"])
+    subprocess.run(["cc", "-std=c99", "-O2", "-DTG_MAIN", "-o", exe, unit], check=True)
+    toks = fx_tokens()
+    printed = subprocess.run([exe] + toks, check=True, capture_output=True, text=True).stdout.split()
+    assert len(printed) == len(toks)
+    vals = []
+    for t, d in zip(toks, printed):
+        c = int(round(float(d) * 65536))
+        q = [v for v in (c - 1, c, c + 1) if -2 ** 31 <= v < 2 ** 31 and O.fx_format(v) == d]
+        assert len(q) == 1, (t, d)
+        vals.append(q[0])
+    bad = ["abc", "-", ".", "+.", "e5", "--1", "1x", "1.2.3", "0x10", "inf", "nan"]
+    refused = [t for t in bad if subprocess.run([exe, t], capture_output=True).returncode != 0]
+    assert refused == bad, refused
+    with open(os.path.join(HERE, "fx_parse.json"), "w") as fh:
+        json.dump({"tokens": toks, "q16": vals, "refused": bad,
+                   "source": "tg_fx_parse through the reference's `tgc c --fixed` unit of an identity model"}, fh)
+    print("fx_parse         %d tokens, %d refused" % (len(toks), len(bad)))
+
+
 def main():
     if not O.have_ref():
         sys.exit("oracle/_ref/tgc_ref is missing: run make -C oracle ref")
     tmp = tempfile.mkdtemp()
     only = set(sys.argv[1:])
+    if not only or "fx_parse" in only:
+        make_fx_parse(tmp)
     for i, (name, build) in enumerate(sorted(_synth().items())):
         if only and name not in only:
             continue
