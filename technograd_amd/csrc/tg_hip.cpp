@@ -30,6 +30,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 namespace {
@@ -175,9 +176,18 @@ struct tg_hip_prog {
 	rp_ins *d_rprog = nullptr;
 	long rp_arena = 0;
 	int rp_in_slot = 0, rp_out_ref = 0;
-	// batch buffers
-	float *d_in = nullptr, *d_out = nullptr;
-	int *d_steps = nullptr;
+	// host-buffer batches: a two-slot pipeline (pinned staging, device buffers, copy streams, events)
+	struct HostPipe {
+		long chunk = 0;                                      // rows per chunk
+		void *h_in[2] = {}, *h_out[2] = {};                  // pinned staging
+		int *h_steps[2] = {};
+		float *d_in[2] = {}, *d_out[2] = {};
+		int *d_steps[2] = {};
+		hipStream_t h2d = nullptr, d2h = nullptr;            // copy streams (default priority)
+		hipEvent_t up[2] = {}, done[2] = {}, down[2] = {};   // per slot: copied in, computed, copied out
+		hipEvent_t t0[2] = {}, t1[2] = {};                   // per slot: compute span (timing)
+	} hp;
+	int *d_steps = nullptr; // steps of tg_hip_batch_device calls that pass none
 	// stats
 	tg_hip_stats_t stats{};
 	hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -1783,10 +1793,22 @@ void destroy(tg_hip_prog *p)
 {
 	if (!p) return;
 	for (auto &q : p->qws) tgk_qweight_free(&q);
-	void *bufs[] = { p->d_pool, p->d_imap, p->d_codes, p->d_fscale, p->d_qscale, p->d_arena, p->d_scratch, p->d_rprog,
-			 p->d_in, p->d_out, p->d_steps };
+	void *bufs[] = { p->d_pool, p->d_imap, p->d_codes, p->d_fscale, p->d_qscale, p->d_arena, p->d_scratch, p->d_rprog, p->d_steps };
 	for (void *b : bufs)
 		if (b) (void)hipFree(b);
+	auto &h = p->hp;
+	for (int k = 0; k < 2; k++) {
+		void *dev[] = { h.d_in[k], h.d_out[k], h.d_steps[k] }, *host[] = { h.h_in[k], h.h_out[k], h.h_steps[k] };
+		for (void *b : dev)
+			if (b) (void)hipFree(b);
+		for (void *b : host)
+			if (b) (void)hipHostFree(b);
+		hipEvent_t evs[] = { h.up[k], h.done[k], h.down[k], h.t0[k], h.t1[k] };
+		for (hipEvent_t e : evs)
+			if (e) (void)hipEventDestroy(e);
+	}
+	if (h.h2d) (void)hipStreamDestroy(h.h2d);
+	if (h.d2h) (void)hipStreamDestroy(h.d2h);
 	if (p->ev0) (void)hipEventDestroy(p->ev0);
 	if (p->ev1) (void)hipEventDestroy(p->ev1);
 	if (p->own_st) (void)hipStreamDestroy(p->own_st);
@@ -1794,42 +1816,100 @@ void destroy(tg_hip_prog *p)
 	delete p;
 }
 
+// memcpy on a few host threads (pageable caller memory <-> pinned staging)
+void par_copy(void *dst, const void *src, size_t n)
+{
+	const size_t piece = (size_t)4 << 20;
+	const int nt = n < 2 * piece ? 1 : (int)std::min<size_t>(8, n / piece);
+	if (nt == 1) {
+		memcpy(dst, src, n);
+		return;
+	}
+	std::vector<std::thread> th;
+	const size_t per = (n + nt - 1) / nt;
+	for (int t = 0; t < nt; t++) {
+		const size_t a = (size_t)t * per, b = std::min(n, a + per);
+		if (a < b) th.emplace_back([=] { memcpy((char *)dst + a, (const char *)src + a, b - a); });
+	}
+	for (auto &x : th) x.join();
+}
+
+bool host_pipe_init(tg_hip_prog *p)
+{
+	auto &h = p->hp;
+	if (h.chunk) return true;
+	const long per = p->m->per, nout = p->m->nout, nt = p->m->nthink ? p->m->nthink : 1;
+	// about 16 MiB of rows per chunk: copies of one chunk overlap the compute of the next
+	long c = (16l << 20) / (4 * (per > nout ? per : nout));
+	c = c < 256 ? 256 : c;
+	h.chunk = c < p->max_rows ? c : p->max_rows;
+	bool ok = hipok(hipStreamCreate(&h.h2d), "stream") && hipok(hipStreamCreate(&h.d2h), "stream");
+	for (int k = 0; ok && k < 2; k++)
+		ok = hipok(hipHostMalloc(&h.h_in[k], (size_t)h.chunk * per * 4, 0), "pinned input") &&
+		     hipok(hipHostMalloc(&h.h_out[k], (size_t)h.chunk * nout * 4, 0), "pinned output") &&
+		     hipok(hipHostMalloc((void **)&h.h_steps[k], (size_t)h.chunk * nt * 4, 0), "pinned steps") &&
+		     hipok(hipMalloc(&h.d_in[k], (size_t)h.chunk * per * 4), "input buffer") &&
+		     hipok(hipMalloc(&h.d_out[k], (size_t)h.chunk * nout * 4), "output buffer") &&
+		     hipok(hipMalloc(&h.d_steps[k], (size_t)h.chunk * nt * 4), "steps buffer") &&
+		     hipok(hipEventCreateWithFlags(&h.up[k], hipEventDisableTiming), "event") &&
+		     hipok(hipEventCreateWithFlags(&h.done[k], hipEventDisableTiming), "event") &&
+		     hipok(hipEventCreateWithFlags(&h.down[k], hipEventDisableTiming), "event") && hipok(hipEventCreate(&h.t0[k]), "event") &&
+		     hipok(hipEventCreate(&h.t1[k]), "event");
+	if (!ok) h.chunk = 0;
+	return ok;
+}
+
+// Host buffers, the block loop of `tgc batch`: rows go in chunks through a
+// two-slot pipeline. Chunk i uses slot i % 2: its rows are copied into the
+// slot's pinned buffer on the host, up to the device on the copy-in stream,
+// computed on the program's stream, and down on the copy-out stream; each
+// stream waits for the event of the step before it, and a slot is refilled
+// only after its previous chunk has left it. So chunk i + 1 travels while
+// chunk i computes. Passes run in input order on one stream, as before.
 int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *steps)
 {
 	if (!p) {
 		seterr("no program");
 		return -1;
 	}
-	const long per = p->m->per, nout = p->m->nout, nt = p->m->nthink ? p->m->nthink : 1;
-	if (!p->d_in) {
-		if (!hipok(hipMalloc(&p->d_in, (size_t)p->max_rows * per * 4), "input buffer") ||
-		    !hipok(hipMalloc(&p->d_out, (size_t)p->max_rows * nout * 4), "output buffer") ||
-		    !hipok(hipMalloc(&p->d_steps, (size_t)p->max_rows * nt * 4), "steps buffer"))
-			return -1;
-	}
+	if (!host_pipe_init(p)) return -1;
+	auto &h = p->hp;
+	const long per = p->m->per, nout = p->m->nout, nt = p->m->nthink ? p->m->nthink : 1, C = h.chunk;
+	const long nch = (nrows + C - 1) / C;
 	float ms_total = 0;
-	for (long r0 = 0; r0 < nrows; r0 += p->max_rows) {
-		int cnt = (int)(nrows - r0 < p->max_rows ? nrows - r0 : p->max_rows);
-		if (!hipok(hipMemcpyAsync(p->d_in, (const char *)rows + (size_t)r0 * per * 4, (size_t)cnt * per * 4, hipMemcpyHostToDevice,
-					  p->st),
-			   "rows to device"))
+	auto finish = [&](long i) -> bool { // chunk i's outputs to the caller
+		const int k = (int)(i & 1);
+		const long r0 = i * C, cnt = nrows - r0 < C ? nrows - r0 : C;
+		if (!hipok(hipEventSynchronize(h.down[k]), "outputs to host")) return false;
+		par_copy((char *)out + (size_t)r0 * nout * 4, h.h_out[k], (size_t)cnt * nout * 4);
+		if (steps && p->m->nthink) memcpy(steps + (size_t)r0 * nt, h.h_steps[k], (size_t)cnt * nt * 4);
+		float ms = 0;
+		(void)hipEventElapsedTime(&ms, h.t0[k], h.t1[k]);
+		ms_total += ms;
+		return true;
+	};
+	for (long i = 0; i < nch; i++) {
+		const int k = (int)(i & 1);
+		const long r0 = i * C, cnt = nrows - r0 < C ? nrows - r0 : C;
+		if (i >= 2 && !finish(i - 2)) return -1; // the slot's previous chunk is out: its buffers are free
+		par_copy(h.h_in[k], (const char *)rows + (size_t)r0 * per * 4, (size_t)cnt * per * 4);
+		if (!hipok(hipMemcpyAsync(h.d_in[k], h.h_in[k], (size_t)cnt * per * 4, hipMemcpyHostToDevice, h.h2d), "rows to device") ||
+		    !hipok(hipEventRecord(h.up[k], h.h2d), "event") || !hipok(hipStreamWaitEvent(p->st, h.up[k], 0), "wait"))
 			return -1;
-		(void)hipEventRecord(p->ev0, p->st);
-		if (run_pass(p, p->d_in, cnt, p->d_out, p->d_steps)) return -1;
-		(void)hipEventRecord(p->ev1, p->st);
-		if (!hipok(hipMemcpyAsync((char *)out + (size_t)r0 * nout * 4, p->d_out, (size_t)cnt * nout * 4, hipMemcpyDeviceToHost, p->st),
-			   "outputs to host"))
+		(void)hipEventRecord(h.t0[k], p->st);
+		if (run_pass(p, h.d_in[k], (int)cnt, h.d_out[k], h.d_steps[k])) return -1;
+		(void)hipEventRecord(h.t1[k], p->st);
+		if (!hipok(hipEventRecord(h.done[k], p->st), "event") || !hipok(hipStreamWaitEvent(h.d2h, h.done[k], 0), "wait") ||
+		    !hipok(hipMemcpyAsync(h.h_out[k], h.d_out[k], (size_t)cnt * nout * 4, hipMemcpyDeviceToHost, h.d2h), "outputs to host"))
 			return -1;
 		if (steps && p->m->nthink &&
-		    !hipok(hipMemcpyAsync(steps + (size_t)r0 * nt, p->d_steps, (size_t)cnt * nt * 4, hipMemcpyDeviceToHost, p->st),
-			   "steps to host"))
+		    !hipok(hipMemcpyAsync(h.h_steps[k], h.d_steps[k], (size_t)cnt * nt * 4, hipMemcpyDeviceToHost, h.d2h), "steps to host"))
 			return -1;
-		if (!hipok(hipStreamSynchronize(p->st), "batch")) return -1;
-		float ms = 0;
-		(void)hipEventElapsedTime(&ms, p->ev0, p->ev1);
-		ms_total += ms;
-		collect_timing(p);
+		if (!hipok(hipEventRecord(h.down[k], h.d2h), "event")) return -1;
 	}
+	for (long i = nch > 2 ? nch - 2 : 0; i < nch; i++)
+		if (!finish(i)) return -1;
+	collect_timing(p);
 	if (steps && !p->m->nthink) memset(steps, 0, (size_t)nrows * sizeof *steps); /* no think loop: one zero slot per row */
 	p->stats.rows = (int)nrows;
 	p->stats.batch_ms = ms_total;
