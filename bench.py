@@ -349,6 +349,10 @@ def bench_config1(args):
 VALU_PEAK_GINST = 256 * 2.4  # wave64 VALU instructions per ns: one per CU per clock (4 SIMDs, 4 clocks each), 2.4 GHz
 
 
+# config 4's row kernel: compiled for the model at load time, or the interpreter
+C4_KERNELS = ("tg_rowprog_model", "rowprog_k")
+
+
 def profile_c4():
     """config 4's row kernel under rocprofv3: cold kernel duration (kernel
     trace) and VALU instructions per dispatch (SQ_INSTS_VALU), averaged over
@@ -365,8 +369,8 @@ def profile_c4():
         shutil.rmtree(out, ignore_errors=True)
     if not kt or not pm:
         return None, None
-    us = [v["us"] for seg in kt[0] for n, _, v in seg if n.startswith("rowprog_k")]
-    ins = [v.get("SQ_INSTS_VALU", 0.0) for seg in pm[0] for n, _, v in seg if n.startswith("rowprog_k")]
+    us = [v["us"] for seg in kt[0] for n, _, v in seg if n.startswith(C4_KERNELS)]
+    ins = [v.get("SQ_INSTS_VALU", 0.0) for seg in pm[0] for n, _, v in seg if n.startswith(C4_KERNELS)]
     return (sum(us) / len(us) if us else None), (sum(ins) / len(ins) if ins else None)
 
 
@@ -385,6 +389,9 @@ def config4_leg(args, steps=None, profile=True):
     X = synth.config4_rows(rows)
     xq = (X * 65536.0).astype(np.int32)  # inputs are 0 or 1: exact in Q16.16
     prog = hip.Program(text, flags=hip.FIXED, max_rows=rows)
+    pst = prog.stats()
+    kname = "tg_rowprog_model (the row program compiled for the model, %d instructions hoisted out of the think loop)" % \
+        pst.rowprog_hoisted if pst.rowprog_jit else "rowprog_k<true> (the row-program interpreter)"
     d_x = hip.DeviceBuffer.from_array(xq)
     d_y = hip.DeviceBuffer(rows * 4 * 4)
     d_s = hip.DeviceBuffer(rows * 4)
@@ -407,12 +414,12 @@ def config4_leg(args, steps=None, profile=True):
                 "frac": round(ins / kus / 1e3 / VALU_PEAK_GINST, 4), "traffic": None,
                 "valu_insts_per_launch": ins, "avg_kernel_us": round(kus, 1),
                 "hbm_frac": round(byts / (kus * 1e-6) / 1e9 / HBM_PEAK_GBS, 5),
-                "kernel": "rowprog_k<true> (one lane per row; wave64 VALU instructions per second from rocprofv3 "
-                          "SQ_INSTS_VALU over the kernel-trace duration, peak one per CU per clock at 2.4 GHz)"}
+                "kernel": kname + "; one lane per row; wave64 VALU instructions per second from rocprofv3 "
+                          "SQ_INSTS_VALU over the kernel-trace duration, peak one per CU per clock at 2.4 GHz"}
     else:
         roof = {"bound": "valu", "achieved": None, "peak": VALU_PEAK_GINST, "unit": "Ginst/s", "frac": None,
                 "traffic": None, "hbm_frac": round(byts / t / 1e9 / HBM_PEAK_GBS, 5),
-                "kernel": "rowprog_k<true>: rocprofv3 gave no data"}
+                "kernel": kname + ": rocprofv3 gave no data"}
     cpu = None if args.no_cpu else ref_cpu(text, xq[:131072], 8, 4, 1, auto_threads(), True,
                                            "config 4 (Q16.16 latent reasoner)")
     return {

@@ -42,6 +42,7 @@ typedef struct tg_hip_prog tg_hip_prog;
 #define TG_HIP_EXACT   2  /* quantized matmuls in the reference's sequential f32 order */
 #define TG_HIP_ROWPROG 4  /* force the one-lane-per-row executor for any model */
 #define TG_HIP_TIMING  8  /* time every kernel with HIP events (tg_hip_stats) */
+#define TG_HIP_INTERP  16 /* row programs: run the interpreter instead of compiling the model */
 
 typedef struct {
 	int executor;        /* 0: layer executor, 1: row-program executor */
@@ -56,6 +57,8 @@ typedef struct {
 	double weight_bytes; /* packed quantized weight bytes the program reads per pass */
 	double macs;         /* multiply-adds of quantized matmuls per row */
 	long arena_bytes;    /* device arena of the program at its row capacity */
+	int rowprog_jit;     /* row program: 1 when compiled for the model (hipRTC), 0 when interpreted */
+	long rowprog_hoisted; /* instructions the compiled row program runs once in front of their think loop */
 } tg_hip_stats_t;
 
 /* Select the device (ordinal) for subsequent calls; 0 on success. */
@@ -113,6 +116,21 @@ int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, co
 #define TG_HIP_NOALLOC_SCRATCH (64u << 20)
 int tg_hip_matmul_q_noalloc(float *d_o, const signed char *d_q, int bits, const float *d_s, const float *d_b, int m, int k, int n,
 			    int axis, void *stream);
+
+/* The model's row program as a freestanding HIP translation unit (weights as
+ * literals, values in registers, one lane per row): the counterpart of
+ * `tgc c MODEL [--fixed] -o unit.c` (src/cgen.c:458-520, unit ABI
+ * docs/SPEC.md:208-221) for the device. The unit defines
+ *   extern "C" __global__ void KERNEL(const T *in, T *out, int *steps, int rows)
+ *   extern "C" int KERNEL_batch(const void *d_in, int rows, void *d_out, int *d_steps, hipStream_t st)
+ * with T = int32 Q16.16 words under TG_HIP_FIXED, else float; device buffers
+ * [rows][per] in, [rows][nout] out, [rows][nthink] steps (or NULL). It is the
+ * kernel tg_hip_load compiles for such a model. Needs no GPU. `kernel` NULL:
+ * tg_<model>_rows. NULL with tg_hip_error() for models the unit form does not
+ * take (scans, gathers, state updates, very large rows). Free with
+ * tg_hip_str_free. */
+char *tg_hip_emit_unit(const char *tgir, size_t len, int flags, const char *kernel);
+void tg_hip_str_free(char *s);
 
 void tg_hip_free(tg_hip_prog *p);
 const char *tg_hip_error(void);

@@ -18,6 +18,7 @@
 // makes the quotient's magnitude one smaller for most inputs).
 #include "tg_devmath.h"
 #include "tg_kern.h"
+#include "tg_rowdev.h"
 #include "tgm.h"
 
 #include <climits>
@@ -27,143 +28,40 @@ namespace {
 
 constexpr int MAXF = 8; // nested loop frames
 
-// ---- Q16.16 primitives (runtime/tg_rtq.h:30-145 restated) ----
-constexpr int ONE = 65536;
-constexpr int MAXV = 2147483647;
-constexpr int MINV = -2147483647 - 1;
-
-__device__ inline int sat(long v) { return v > MAXV ? MAXV : v < MINV ? MINV : (int)v; }
-__device__ inline int fmulq(int a, int b) { return sat(((long)a * b + 32768) >> 16); }
-__device__ inline int fdivq(int a, int b)
-{
-	if (b == 0) return a > 0 ? MAXV : a < 0 ? MINV : 0;
-	long n = (long)a * 65536, h = b > 0 ? b / 2 : -(b / 2);
-	return sat(((n >= 0) == (b > 0) ? n + h : n - h) / b);
-}
-__device__ inline int absq(int a) { return a < 0 ? (a == MINV ? MAXV : -a) : a; }
-
-// ln 2, pi, pi/2, 2 pi in Q16 (round(v * 2^16)); exp series in Q30 (round(2^30 / j!))
-constexpr long LN2 = 45426, PIQ = 205887, HPIQ = 102944, TPIQ = 411775;
-__constant__ long EXPC[9] = { 1073741824, 1073741824, 536870912, 178956971, 44739243, 8947849, 1491308, 213044, 26631 };
-
-__device__ int expq(int x)
-{
-	if (x > 681390) return MAXV; // ln(32768) in Q16: exp would not fit
-	if (x < -786432) return 0;   // exp(-12) < 2^-16
-	long k = x >= 0 ? x / LN2 : -((-(long)x + LN2 - 1) / LN2);
-	long r = ((long)x - k * LN2) * 16384;
-	long p = EXPC[8];
-	for (int i = 7; i >= 0; i--) p = EXPC[i] + ((p * r) >> 30);
-	int sh = (int)k - 14;
-	long v = sh >= 0 ? p * (1L << sh) : (p + (1L << (-sh - 1))) >> -sh;
-	return sat(v);
-}
-
-__device__ int logq(int x)
-{
-	if (x <= 0) return MINV;
-	int e = 0;
-	unsigned m = (unsigned)x;
-	while (m >= 131072u) {
-		m >>= 1;
-		e++;
-	}
-	while (m < 65536u) {
-		m <<= 1;
-		e--;
-	}
-	long s = ((long)(m - 65536) << 30) / (long)(m + 65536), s2 = (s * s) >> 30, t = s, acc = 0;
-	for (int k = 1; k <= 13; k += 2) {
-		acc += t / k;
-		t = (t * s2) >> 30;
-	}
-	return sat(((2 * acc) >> 14) + (long)e * LN2);
-}
-
-__device__ unsigned long isqrt64(unsigned long v)
-{
-	unsigned long r = 0, bit = 1UL << 62;
-	while (bit > v) bit >>= 2;
-	while (bit) {
-		if (v >= r + bit) {
-			v -= r + bit;
-			r = (r >> 1) + bit;
-		} else {
-			r >>= 1;
-		}
-		bit >>= 2;
-	}
-	return r;
-}
-
-__device__ int sinq(int x)
-{
-	long r = (long)x % TPIQ;
-	if (r > PIQ) r -= TPIQ;
-	if (r < -PIQ) r += TPIQ;
-	if (r > HPIQ) r = PIQ - r;
-	if (r < -HPIQ) r = -PIQ - r;
-	long z = r * 16384, z2 = (z * z) >> 30, t = z, acc = 0;
-	for (int k = 1; k <= 13; k += 2) {
-		acc += t;
-		t = -((t * z2) >> 30) / ((k + 1) * (k + 2));
-	}
-	return sat((acc + 8192) >> 14);
-}
-
-__device__ inline int tanhq(int x)
-{
-	int t = absq(x);
-	if (t > 9 * ONE) return x < 0 ? -ONE : ONE;
-	int e = expq(-2 * t);
-	int y = fdivq(ONE - e, ONE + e);
-	return x < 0 ? -y : y;
-}
-
-__device__ inline int sigmoidq(int x)
-{
-	int e = expq(-absq(x));
-	return x >= 0 ? fdivq(ONE, ONE + e) : fdivq(e, ONE + e);
-}
+using namespace tgrd;
 
 __device__ inline int unq(int op, int x)
 {
 	switch (op) {
-	case TGM_NEG: return sat(-(long)x);
+	case TGM_NEG: return negq(x);
 	case TGM_TANH: return tanhq(x);
-	case TGM_RELU: return x > 0 ? x : 0;
+	case TGM_RELU: return reluq(x);
 	case TGM_SIGMOID: return sigmoidq(x);
 	case TGM_EXP: return expq(x);
-	case TGM_SQRT: return x > 0 ? (int)isqrt64((unsigned long)x << 16) : 0;
-	case TGM_GELU: {
-		long v = x, x3 = (((v * v) >> 16) * v) >> 16;
-		long u = ((v + ((x3 * 2930) >> 16)) * 52290) >> 16; // 0.044715 and 0.7978845608 in Q16
-		int t = tanhq(sat(u));
-		return sat((v * ((long)ONE + t)) >> 17);
-	}
-	case TGM_SILU: return fmulq(x, sigmoidq(x));
-	case TGM_SOFTPLUS: return sat((long)(x > 0 ? x : 0) + logq(ONE + expq(-absq(x))));
+	case TGM_SQRT: return sqrtq(x);
+	case TGM_GELU: return geluq(x);
+	case TGM_SILU: return siluq(x);
+	case TGM_SOFTPLUS: return softplusq(x);
 	case TGM_LOG: return logq(x);
 	case TGM_SIN: return sinq(x);
-	case TGM_COS: return sinq(sat((long)x + HPIQ));
-	case TGM_FLOOR: return (int)((unsigned)x & 0xffff0000u);
-	default: return x > 0 ? ONE : 0; // step
+	case TGM_COS: return cosq(x);
+	case TGM_FLOOR: return floorq(x);
+	default: return stepq(x);
 	}
 }
 
 __device__ inline int binq(int op, int x, int y)
 {
 	switch (op) {
-	case TGK_ADD: return sat((long)x + y);
-	case TGK_SUB: return sat((long)x - y);
+	case TGK_ADD: return addq(x, y);
+	case TGK_SUB: return subq(x, y);
 	case TGK_MUL: return fmulq(x, y);
 	case TGK_DIV: return fdivq(x, y);
-	case TGK_MAX: return x > y ? x : y;
-	default: return x < y ? x : y;
+	case TGK_MAX: return maxq(x, y);
+	default: return minq(x, y);
 	}
 }
 
-// ---- f32 kernels (runtime/tg_rt.h) ----
 __device__ inline float binf(int op, float x, float y)
 {
 	switch (op) {
@@ -171,36 +69,29 @@ __device__ inline float binf(int op, float x, float y)
 	case TGK_SUB: return x - y;
 	case TGK_MUL: return x * y;
 	case TGK_DIV: return x / y;
-	case TGK_MAX: return x > y ? x : y;
-	default: return x < y ? x : y;
+	case TGK_MAX: return maxf_(x, y);
+	default: return minf_(x, y);
 	}
 }
 
 __device__ inline float unf(int op, float x)
 {
 	switch (op) {
-	case TGM_NEG: return -x;
+	case TGM_NEG: return negf_(x);
 	case TGM_TANH: return tanhf(x);
-	case TGM_RELU: return x > 0.0f ? x : 0.0f;
-	case TGM_SIGMOID: return 1.0f / (1.0f + expf(-x));
+	case TGM_RELU: return reluf_(x);
+	case TGM_SIGMOID: return sigmoidf_(x);
 	case TGM_EXP: return expf(x);
 	case TGM_SQRT: return sqrtf(x);
-	case TGM_GELU: return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
-	case TGM_SILU: return x / (1.0f + expf(-x));
-	case TGM_SOFTPLUS: return (x > 0.0f ? x : 0.0f) + tg_log1p_unit(expf(-fabsf(x)));
+	case TGM_GELU: return geluf_(x);
+	case TGM_SILU: return siluf_(x);
+	case TGM_SOFTPLUS: return softplusf_(x);
 	case TGM_LOG: return logf(x);
 	case TGM_SIN: return sinf(x);
 	case TGM_COS: return cosf(x);
 	case TGM_FLOOR: return floorf(x);
-	default: return x > 0.0f ? 1.0f : 0.0f;
+	default: return stepf_(x);
 	}
-}
-
-__device__ inline int qcode(const uint8_t *q, int bits, long i)
-{
-	if (bits == 8) return (signed char)q[i];
-	int b = (signed char)q[i >> 1];
-	return (i & 1) ? (b >> 4) : (int)(signed char)(unsigned char)((unsigned)b << 4) >> 4;
 }
 
 // An operand view for one lane: element i at base[i * st].
@@ -260,12 +151,10 @@ __global__ __launch_bounds__(256) void rowprog_k(rp_args A)
 							long s = 0;
 							if (quant == 1) {
 								for (int p = 0; p < K; p++) s += (long)qcode(codes, bits, (long)i * K + p) * b.q(bj + (long)p * N);
-								long pr = (long)((unsigned long)s * (unsigned long)(long)A.qscale[I.p[7] + i]);
-								o.q(oi) = sat((pr + (1L << 23)) >> 24);
+								o.q(oi) = qscaleq(s, A.qscale[I.p[7] + i]);
 							} else if (quant == 2) {
 								for (int p = 0; p < K; p++) s += (long)a.q(ai + p) * qcode(codes, bits, (long)p * N + j);
-								long pr = (long)((unsigned long)s * (unsigned long)(long)A.qscale[I.p[7] + j]);
-								o.q(oi) = sat((pr + (1L << 23)) >> 24);
+								o.q(oi) = qscaleq(s, A.qscale[I.p[7] + j]);
 							} else {
 								for (int p = 0; p < K; p++) s += (long)a.q(ai + p) * b.q(bj + (long)p * N);
 								o.q(oi) = sat((s + 32768) >> 16);
@@ -299,13 +188,12 @@ __global__ __launch_bounds__(256) void rowprog_k(rp_args A)
 							o.q(base + i) = expq(sat((long)a.q(base + i) - mx));
 							s += o.q(base + i);
 						}
-						for (int i = 0; i < cols; i++) o.q(base + i) = (int)(((long)o.q(base + i) * 65536 + s / 2) / s);
+						for (int i = 0; i < cols; i++) o.q(base + i) = softq(o.q(base + i), s);
 					} else {
 						unsigned long ss = 0;
 						for (int i = 0; i < cols; i++) ss += (unsigned long)((long)a.q(base + i) * a.q(base + i));
-						unsigned long ms = ss / (unsigned long)cols + 4295; // 1e-6 in Q32
-						int rms = (int)isqrt64(ms);
-						for (int i = 0; i < cols; i++) o.q(base + i) = fdivq(a.q(base + i), rms > 0 ? rms : 1);
+						const int rms = rmsq(ss, cols);
+						for (int i = 0; i < cols; i++) o.q(base + i) = fdivq(a.q(base + i), rms);
 					}
 				} else {
 					if (I.op == TGM_SOFTMAX) {

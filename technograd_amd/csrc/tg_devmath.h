@@ -1,9 +1,11 @@
 // Device math routines of this backend's own, written from the mathematics.
 // The header also compiles as plain C++ so the routines can be checked on the
-// host against the C library (tests/test_host.py builds it with g++).
+// host against the C library (tests/test_devmath.py builds it with g++).
 #pragma once
 
+#ifndef __HIPCC_RTC__ // hipRTC provides the device math and runtime itself
 #include <math.h>
+#endif
 
 #ifdef __HIPCC__
 #define TG_HD __host__ __device__
@@ -46,7 +48,9 @@ TG_HD inline float tg_log1p_unit(float y)
 }
 
 #ifdef __HIPCC__
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
+#endif
 
 // sum of z[0 .. n) in index order, one f32 rounding per add as in a
 // sequential loop; z 16-byte aligned (an LDS line). The loop runs in steps of

@@ -9,26 +9,35 @@
 //    matrix cores (kern_qgemm.hip), everything else on the exact kernels of
 //    kern_layer.hip. Scans step through time on the host, each step a few
 //    kernels over all rows.
-//  * row program: one lane per batch row interprets the whole model
-//    (kern_rowprog.hip). Used for think loops (per-row halting), for Q16.16,
-//    and on request.
+//  * row program: one lane per batch row runs the whole model. Used for
+//    think loops (per-row halting), for Q16.16, and on request. The program
+//    is compiled for the model at load time (tg_rpgen.cpp, hipRTC): values in
+//    registers, weights as literals, loop-invariant instructions hoisted out
+//    of think loops. Programs the compiled form does not take (scans,
+//    gathers, very large rows) run in the row-program interpreter
+//    (kern_rowprog.hip), which computes the same values.
 //
 // The batch loop mirrors `tgc batch` (src/main.c:400-444): rows are processed
 // in blocks (here: device passes of up to max_rows rows), outputs come back in
 // input order, and steps per row are reported for every think loop.
 #include "tg_hip.h"
 #include "tg_kern.h"
+#include "tg_rpgen.h"
 #include "tgm.h"
 
 #include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
 
 #include <algorithm>
+#include <cctype>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -176,6 +185,9 @@ struct tg_hip_prog {
 	rp_ins *d_rprog = nullptr;
 	long rp_arena = 0;
 	int rp_in_slot = 0, rp_out_ref = 0;
+	hipModule_t rp_mod = nullptr;  // the row program compiled for this model
+	hipFunction_t rp_fn = nullptr; // its kernel (null: the interpreter runs the program)
+	std::string rp_why;            // why the program runs in the interpreter
 	// host-buffer batches: a two-slot pipeline (pinned staging, device buffers, copy streams, events)
 	struct HostPipe {
 		long chunk = 0;                                      // rows per chunk
@@ -1470,6 +1482,18 @@ void scan_tids(const tgm_block *b, std::vector<std::pair<int, int>> &out)
 
 int run_pass(tg_hip_prog *p, const float *d_in, int rows, float *d_out, int *d_steps)
 {
+	if (p->executor == 1 && p->rp_fn) {
+		if (rows <= 0) return 0;
+		const void *in = d_in;
+		void *out = d_out;
+		int *steps = d_steps;
+		int r = rows;
+		void *args[] = { &in, &out, &steps, &r };
+		return hipok(hipModuleLaunchKernel(p->rp_fn, (unsigned)((rows + 255) / 256), 1, 1, 256, 1, 1, 0, p->st, args, nullptr),
+			     "row program launch")
+			       ? 0
+			       : -1;
+	}
 	if (p->executor == 1) {
 		rp_args a;
 		memset(&a, 0, sizeof a);
@@ -1768,9 +1792,9 @@ bool build_layer(tg_hip_prog *p)
 	return true;
 }
 
-bool build_rowprog(tg_hip_prog *p)
+// the row program and its pools on the host
+bool plan_rowprog(tg_hip_prog *p, RB &B)
 {
-	RB B;
 	B.p = p;
 	B.m = p->m;
 	B.fixed = p->fixed != 0;
@@ -1783,6 +1807,114 @@ bool build_rowprog(tg_hip_prog *p)
 	if (!rp_block(B, &p->m->top)) return false;
 	p->rp_out_ref = rp_ref(B, p->m->output);
 	p->rp_arena = B.slots ? B.slots : 1;
+	return true;
+}
+
+rp_source rp_source_of(const tg_hip_prog *p, const RB &B)
+{
+	rp_source r;
+	r.prog = p->rprog.data();
+	r.nins = (int)p->rprog.size();
+	r.pool = B.P.f.data();
+	r.npool = (long)B.P.f.size();
+	r.imap = B.P.imap.data();
+	r.codes = B.P.codes.data();
+	r.fscale = B.P.fscale.data();
+	r.qscale = B.P.qscale.data();
+	r.per = (int)p->m->per;
+	r.in_slot = p->rp_in_slot;
+	r.nout = (int)p->m->nout;
+	r.out_ref = p->rp_out_ref;
+	r.nthink = p->m->nthink ? p->m->nthink : 1;
+	r.arena = p->rp_arena;
+	r.fixed = p->fixed != 0;
+	return r;
+}
+
+// hipRTC compilation for the current device, cached per process by source text
+bool rtc_compile(const std::string &src, std::vector<char> &code)
+{
+	static std::mutex mu;
+	static std::map<std::string, std::vector<char>> cache;
+	int dev = 0;
+	hipDeviceProp_t pr;
+	if (!hipok(hipGetDevice(&dev), "hipGetDevice") || !hipok(hipGetDeviceProperties(&pr, dev), "hipGetDeviceProperties")) return false;
+	const std::string arch = std::string("--gpu-architecture=") + pr.gcnArchName;
+	const std::string key = arch + "\n" + src;
+	{
+		std::lock_guard<std::mutex> g(mu);
+		auto it = cache.find(key);
+		if (it != cache.end()) {
+			code = it->second;
+			return true;
+		}
+	}
+	hiprtcProgram prog;
+	if (hiprtcCreateProgram(&prog, src.c_str(), "tg_rowprog.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
+		seterr("hiprtcCreateProgram failed");
+		return false;
+	}
+	// the flags of the library's own kernels: no contraction, denormals kept, no packed FP32
+	const char *opts[] = { arch.c_str(), "-O3", "-std=c++17", "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
+		               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops" };
+	hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof *opts), opts);
+	if (r != HIPRTC_SUCCESS) {
+		size_t n = 0;
+		std::string log;
+		if (hiprtcGetProgramLogSize(prog, &n) == HIPRTC_SUCCESS && n > 1) {
+			log.resize(n);
+			(void)hiprtcGetProgramLog(prog, &log[0]);
+		}
+		seterr("row program compilation failed: %.400s", log.c_str());
+		(void)hiprtcDestroyProgram(&prog);
+		return false;
+	}
+	size_t cs = 0;
+	bool ok = hiprtcGetCodeSize(prog, &cs) == HIPRTC_SUCCESS && cs > 0;
+	if (ok) {
+		code.resize(cs);
+		ok = hiprtcGetCode(prog, code.data()) == HIPRTC_SUCCESS;
+	}
+	(void)hiprtcDestroyProgram(&prog);
+	if (!ok) {
+		seterr("hiprtcGetCode failed");
+		return false;
+	}
+	std::lock_guard<std::mutex> g(mu);
+	cache[key] = code;
+	return true;
+}
+
+// Compile the row program for this model. false with rp_why set: the program
+// stays with the interpreter; false with an error: a failure to report.
+bool compile_rowprog(tg_hip_prog *p, const RB &B, bool &fatal)
+{
+	fatal = false;
+	std::string src;
+	rp_emit_stats es;
+	if (!rp_emit(rp_source_of(p, B), "tg_rowprog_model", false, src, p->rp_why, &es)) return false;
+	std::vector<char> code;
+	fatal = true;
+	if (!rtc_compile(src, code)) return false;
+	if (!hipok(hipModuleLoadData(&p->rp_mod, code.data()), "hipModuleLoadData")) return false;
+	if (!hipok(hipModuleGetFunction(&p->rp_fn, p->rp_mod, "tg_rowprog_model"), "hipModuleGetFunction")) return false;
+	p->stats.rowprog_jit = 1;
+	p->stats.rowprog_hoisted = es.hoisted;
+	fatal = false;
+	return true;
+}
+
+bool build_rowprog(tg_hip_prog *p)
+{
+	RB B;
+	if (!plan_rowprog(p, B)) return false;
+	if (!(p->flags & TG_HIP_INTERP)) {
+		bool fatal;
+		if (compile_rowprog(p, B, fatal)) return true; // no arena, pools or program upload: all of it is in the kernel
+		if (fatal) return false;
+	} else {
+		p->rp_why = "the interpreter was requested (TG_HIP_INTERP)";
+	}
 	if (!upload_pools(p, B.P) || !upload(&p->d_rprog, p->rprog, p->st)) return false;
 	size_t ab = (size_t)p->rp_arena * p->max_rows * sizeof(float);
 	p->stats.arena_bytes = (long)ab;
@@ -1807,6 +1939,7 @@ void destroy(tg_hip_prog *p)
 		for (hipEvent_t e : evs)
 			if (e) (void)hipEventDestroy(e);
 	}
+	if (p->rp_mod) (void)hipModuleUnload(p->rp_mod);
 	if (h.h2d) (void)hipStreamDestroy(h.h2d);
 	if (h.d2h) (void)hipStreamDestroy(h.d2h);
 	if (p->ev0) (void)hipEventDestroy(p->ev0);
@@ -2141,6 +2274,48 @@ int tg_hip_matmul_q_noalloc(float *d_o, const signed char *d_q, int bits, const 
 	tgk_qgemm(st, &a, scr + wb); // digits, then the matrix-core product (every byte they read is written first)
 	return hipok(hipGetLastError(), "tg_hip_matmul_q_noalloc launch") ? 0 : -1;
 }
+
+char *tg_hip_emit_unit(const char *tgir, size_t len, int flags, const char *kernel)
+{
+	char err[512];
+	tgm_module *m = tgm_read(tgir, len, err, sizeof err);
+	if (!m) {
+		seterr("%s", err);
+		return nullptr;
+	}
+	if (m->nupd) {
+		seterr("model %s updates its state: rows depend on each other", m->name);
+		tgm_free(m);
+		return nullptr;
+	}
+	std::string name = kernel ? kernel : "";
+	if (name.empty()) {
+		name = "tg_";
+		for (const char *c = m->name; c && *c; c++) name += (isalnum((unsigned char)*c) || *c == '_') ? *c : '_';
+		name += "_rows";
+	}
+	tg_hip_prog *p = new tg_hip_prog;
+	p->m = m;
+	p->flags = flags;
+	p->fixed = (flags & TG_HIP_FIXED) != 0;
+	p->max_rows = 1;
+	RB B;
+	std::string src;
+	char *out = nullptr;
+	if (plan_rowprog(p, B)) {
+		if (rp_emit(rp_source_of(p, B), name.c_str(), true, src, p->rp_why, nullptr)) {
+			out = (char *)malloc(src.size() + 1);
+			if (out) memcpy(out, src.c_str(), src.size() + 1);
+			else seterr("out of memory");
+		} else {
+			seterr("model %s: %s", m->name, p->rp_why.c_str());
+		}
+	}
+	destroy(p);
+	return out;
+}
+
+void tg_hip_str_free(char *s) { free(s); }
 
 void tg_hip_free(tg_hip_prog *p) { destroy(p); }
 

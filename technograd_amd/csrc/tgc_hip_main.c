@@ -32,6 +32,9 @@
  * reference's trace format (src/trace.c: t, level, stage, msg, fields).
  *
  *   tgc-hip fxparse TOKEN...   prints each token's Q16.16 value (no device)
+ *   tgc-hip c MODEL.tgir [--fixed] [-o UNIT.hip] [--kernel NAME]
+ *       writes the model's row program as a freestanding HIP unit (the
+ *       device counterpart of `tgc c`, src/main.c:343-360; no device)
  */
 #include "tg_hip.h"
 
@@ -286,6 +289,37 @@ static void write_block(FILE *f, int obin, int fixed, const float *out, const in
 	}
 }
 
+/* tgc-hip c: the row program as a HIP unit (tg_hip_emit_unit) */
+static int emit_unit(int argc, char **argv)
+{
+	const char *model = NULL, *opath = NULL, *kernel = NULL;
+	int flags = 0;
+	for (int i = 2; i < argc; i++) {
+		if (!strcmp(argv[i], "-o") && i + 1 < argc) opath = argv[++i];
+		else if (!strcmp(argv[i], "--kernel") && i + 1 < argc) kernel = argv[++i];
+		else if (!strcmp(argv[i], "--fixed")) flags |= TG_HIP_FIXED;
+		else if (!model) model = argv[i];
+		else return die("unexpected argument '%s'", argv[i]);
+	}
+	if (!model) return die("usage: tgc-hip c MODEL.tgir [--fixed] [-o UNIT.hip] [--kernel NAME]%s", "");
+	size_t mlen;
+	char *text = slurp(model, &mlen);
+	if (!text) return die("cannot read '%s'", model);
+	char *src = tg_hip_emit_unit(text, mlen, flags, kernel);
+	free(text);
+	if (!src) return die("%s", tg_hip_error());
+	FILE *f = opath ? fopen(opath, "w") : stdout;
+	if (!f) {
+		tg_hip_str_free(src);
+		return die("cannot open '%s'", opath);
+	}
+	const size_t n = strlen(src);
+	const int ok = fwrite(src, 1, n, f) == n;
+	tg_hip_str_free(src);
+	if (opath && fclose(f)) return die("cannot write '%s'", opath);
+	return ok ? 0 : die("cannot write the unit%s", "");
+}
+
 #define USAGE "usage: tgc-hip batch MODEL.tgir DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v] [--log FILE]%s"
 
 int main(int argc, char **argv)
@@ -301,6 +335,7 @@ int main(int argc, char **argv)
 		}
 		return 0;
 	}
+	if (argc >= 2 && !strcmp(argv[1], "c")) return emit_unit(argc, argv);
 	if (argc < 2 || strcmp(argv[1], "batch")) return die(USAGE, "");
 	for (int i = 2; i < argc; i++) {
 		if (!strcmp(argv[i], "-o") && i + 1 < argc) opath = argv[++i];

@@ -12,7 +12,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libtg_hip.so")
 
-FIXED, EXACT, ROWPROG, TIMING = 1, 2, 4, 8
+FIXED, EXACT, ROWPROG, TIMING, INTERP = 1, 2, 4, 8, 16
 
 
 class Stats(ctypes.Structure):
@@ -20,6 +20,7 @@ class Stats(ctypes.Structure):
         ("executor", ctypes.c_int), ("rows", ctypes.c_int), ("batch_ms", ctypes.c_double), ("qgemm_ms", ctypes.c_double),
         ("qgemm_calls", ctypes.c_long), ("digits_ms", ctypes.c_double), ("other_ms", ctypes.c_double),
         ("weight_bytes", ctypes.c_double), ("macs", ctypes.c_double), ("arena_bytes", ctypes.c_long),
+        ("rowprog_jit", ctypes.c_int), ("rowprog_hoisted", ctypes.c_long),
     ]
 
 
@@ -50,6 +51,9 @@ def lib():
         L.tg_hip_dec_info.argtypes = [vp, ctypes.POINTER(ip), ctypes.POINTER(ip)]
         L.tg_hip_dec_free.argtypes = [vp]
         L.tg_hip_free.argtypes = [vp]
+        L.tg_hip_emit_unit.restype = vp
+        L.tg_hip_emit_unit.argtypes = [ctypes.c_char_p, sz, ip, ctypes.c_char_p]
+        L.tg_hip_str_free.argtypes = [vp]
         L.tg_hip_error.restype = ctypes.c_char_p
         L.tg_hip_stats.argtypes = [vp, ctypes.POINTER(Stats)]
         L.tg_hip_reset_stats.argtypes = [vp]
@@ -186,6 +190,18 @@ def matmul_q_noalloc(d_o, d_q, bits, d_s, d_b, m, k, n, axis, stream=None):
     call is larger than the library's fixed scratch; the message is in
     error())."""
     return lib().tg_hip_matmul_q_noalloc(d_o, d_q, bits, d_s, d_b, m, k, n, axis, stream)
+
+
+def emit_unit(tgir, flags=0, kernel=None):
+    """The model's row program as a freestanding HIP unit (tg_hip_emit_unit); no GPU needed."""
+    t = tgir.encode() if isinstance(tgir, str) else tgir
+    p = lib().tg_hip_emit_unit(t, len(t), flags, kernel.encode() if kernel else None)
+    if not p:
+        raise RuntimeError("emit_unit: %s" % lib().tg_hip_error().decode())
+    try:
+        return ctypes.string_at(p).decode()
+    finally:
+        lib().tg_hip_str_free(p)
 
 
 def error():
