@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void rowprog_k(rp_args A)
 						long s = 0;
 						for (int i = 1; i < cols; i++) mx = a.q(base + i) > mx ? a.q(base + i) : mx;
 						for (int i = 0; i < cols; i++) {
-							o.q(base + i) = expq(sat((long)a.q(base + i) - mx));
+							o.q(base + i) = expq_neg(subq(a.q(base + i), mx)); // x - max <= 0
 							s += o.q(base + i);
 						}
 						for (int i = 0; i < cols; i++) o.q(base + i) = softq(o.q(base + i), s);

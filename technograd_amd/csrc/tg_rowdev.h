@@ -36,7 +36,21 @@ constexpr long GELU_A = q16(0.044715), GELU_B = q16(0.7978845608);
 constexpr unsigned long EPS_Q32 = (unsigned long)(1e-6 * 4294967296.0 + 0.5);
 constexpr int EXP_HI = (int)q16(15 * 0.6931471805599453), EXP_LO = -12 * ONE;
 
+// Two device operations with host stand-ins for the host builds of this
+// header (tests): an approximate f32 reciprocal and the low 32 bits of a
+// 24 x 24-bit product. fdivq_unit gives the same result with either.
+#ifdef __HIP_DEVICE_COMPILE__
+#define TGRD_RCP(x) __builtin_amdgcn_rcpf(x)
+#define TGRD_MUL24(a, b) __umul24((a) & 0xffffffu, (b) & 0xffffffu) // operands below 2^24: the masks fold away
+#else
+#define TGRD_RCP(x) (1.0f / (x))
+#define TGRD_MUL24(a, b) ((a) * (b))
+#endif
+
 __device__ inline int sat(long v) { return v > MAXV ? MAXV : v < MINV ? MINV : (int)v; }
+// saturating int32 add and subtract: sat((long)x +- y), one clamped instruction
+__device__ inline int addq(int x, int y) { return __builtin_elementwise_add_sat(x, y); }
+__device__ inline int subq(int x, int y) { return __builtin_elementwise_sub_sat(x, y); }
 __device__ inline int fmulq(int a, int b) { return sat(((long)a * b + 32768) >> 16); }
 __device__ inline int fdivq(int a, int b)
 {
@@ -44,31 +58,51 @@ __device__ inline int fdivq(int a, int b)
 	long n = (long)a * 65536, h = b > 0 ? b / 2 : -(b / 2);
 	return sat(((n >= 0) == (b > 0) ? n + h : n - h) / b);
 }
-__device__ inline int absq(int a) { return a < 0 ? (a == MINV ? MAXV : -a) : a; }
+__device__ inline int absq(int a) { return a < 0 ? subq(0, a) : a; } // |MINV| saturates to MAXV
 
-__device__ inline unsigned long hornerq(long p, long r) { return (unsigned long)(unsigned)p * (unsigned)r; }
+// the high 32 bits of a 32 x 32-bit product (one instruction)
+__device__ inline unsigned mulhi(unsigned a, unsigned b) { return (unsigned)(((unsigned long)a * b) >> 32); }
+
+// exp's degree-8 Horner polynomial in Q30 at f = r4 / 2^32 in [0, ln 2), r4 =
+// 4 r for the runtime's reduced argument r = f 2^30 < 2^30. Every Horner value
+// lies below 2^31 (a truncated series of e^f < 2), so each step's
+// (p * r) >> 30 of the runtime's int64 arithmetic equals mulhi(p, 4 r).
+__device__ inline unsigned exp_poly(unsigned r4)
+{
+	unsigned p = (unsigned)expc(8);
+	p = (unsigned)expc(7) + mulhi(p, r4);
+	p = (unsigned)expc(6) + mulhi(p, r4);
+	p = (unsigned)expc(5) + mulhi(p, r4);
+	p = (unsigned)expc(4) + mulhi(p, r4);
+	p = (unsigned)expc(3) + mulhi(p, r4);
+	p = (unsigned)expc(2) + mulhi(p, r4);
+	p = (unsigned)expc(1) + mulhi(p, r4);
+	return (unsigned)expc(0) + mulhi(p, r4);
+}
 
 __device__ inline int expq(int x)
 {
 	if (x > EXP_HI) return MAXV;
 	if (x < EXP_LO) return 0;
 	long k = x >= 0 ? x / LN2 : -((-(long)x + LN2 - 1) / LN2);
-	long r = ((long)x - k * LN2) * 16384;
-	// 0 <= r < ln2 * 2^30 and every Horner value lies in [2^30 / 8!, 2^31]
-	// (partial sums of e^f, f in [0, ln 2)), so each product (p * r) >> 30 of
-	// the runtime's int64 arithmetic is one unsigned 32 x 32 -> 64 multiply
-	long p = expc(8);
-	p = expc(7) + (long)(hornerq(p, r) >> 30);
-	p = expc(6) + (long)(hornerq(p, r) >> 30);
-	p = expc(5) + (long)(hornerq(p, r) >> 30);
-	p = expc(4) + (long)(hornerq(p, r) >> 30);
-	p = expc(3) + (long)(hornerq(p, r) >> 30);
-	p = expc(2) + (long)(hornerq(p, r) >> 30);
-	p = expc(1) + (long)(hornerq(p, r) >> 30);
-	p = expc(0) + (long)(hornerq(p, r) >> 30);
+	const long p = exp_poly((unsigned)(((long)x - k * LN2) * 65536));
 	int sh = (int)k - 14;
 	long v = sh >= 0 ? p * (1L << sh) : (p + (1L << (-sh - 1))) >> -sh;
 	return sat(v);
+}
+
+// expq for x <= 0 in 32-bit arithmetic. With m = -x in [0, 12 ONE] and
+// k = -floor(x / ln 2) = ceil(m / ln 2) in [0, 18], the reduced argument
+// k ln2 - m lies in [0, ln2), the polynomial stays below 2^31, the rounding
+// bias 2^(13 + k) <= 2^31 and the sum below 2^32; at k = 18 the shift is 32
+// and the result 0. Equal to expq on [-12 ONE, 0].
+__device__ inline int expq_neg(int x)
+{
+	if (x < EXP_LO) return 0;
+	const unsigned m = (unsigned)-x, k = (m + (unsigned)LN2 - 1) / (unsigned)LN2;
+	const unsigned p = exp_poly((k * (unsigned)LN2 - m) * 65536u);
+	const unsigned sh = 14 + k;
+	return sh >= 32 ? 0 : (int)((p + (1u << (sh - 1))) >> sh);
 }
 
 __device__ inline int logq(int x)
@@ -123,19 +157,39 @@ __device__ inline int sinq(int x)
 	return sat((acc + 8192) >> 14);
 }
 
+// floor(n / d) for 0 <= n < 2^53, 0 < d < 2^35 and n / d < 2^17: n and d are
+// exact in f64, the correctly rounded quotient is within 2^-36 of n / d, and
+// a non-integer n / d is at least 1/d > 2^-35 from the next integer, so the
+// f64 quotient truncates to the integer one.
+__device__ inline long divsmall(long n, long d) { return (long)((double)n / (double)d); }
+
+// fdivq(a, b) for 0 <= a <= ONE <= b <= 2 ONE (quotients of exp values):
+// floor((a 2^16 + floor(b / 2)) / b) <= 2^16 + 1, never saturated. The f32
+// estimate has a relative error below 2^-21 (the rounded numerator, an
+// approximate reciprocal within 1 ulp, the product), so it is within 2^-5 of
+// the quotient and truncates to it or a neighbour; the remainder, in
+// (-b, 2b) and hence exact in wrapping 32-bit arithmetic, corrects it.
+__device__ inline int fdivq_unit(int a, int b)
+{
+	const unsigned h = (unsigned)b >> 1;
+	const unsigned q = (unsigned)(((float)a * 65536.0f + (float)h) * TGRD_RCP((float)b));
+	const int r = (int)((unsigned)a * 65536u + h - TGRD_MUL24(q, (unsigned)b));
+	return (int)q + (r >= b) - (r < 0);
+}
+
 __device__ inline int tanhq(int x)
 {
 	int t = absq(x);
 	if (t > 9 * ONE) return x < 0 ? -ONE : ONE;
-	int e = expq(-2 * t);
-	int y = fdivq(ONE - e, ONE + e);
+	int e = expq_neg(-2 * t); // in [0, ONE]
+	int y = fdivq_unit(ONE - e, ONE + e);
 	return x < 0 ? -y : y;
 }
 
 __device__ inline int sigmoidq(int x)
 {
-	int e = expq(-absq(x));
-	return x >= 0 ? fdivq(ONE, ONE + e) : fdivq(e, ONE + e);
+	int e = expq_neg(-absq(x)); // in [0, ONE]
+	return x >= 0 ? fdivq_unit(ONE, ONE + e) : fdivq_unit(e, ONE + e);
 }
 
 __device__ inline int geluq(int x)
@@ -146,16 +200,14 @@ __device__ inline int geluq(int x)
 	return sat((v * ((long)ONE + t)) >> 17);
 }
 
-__device__ inline int negq(int x) { return sat(-(long)x); }
+__device__ inline int negq(int x) { return subq(0, x); }
 __device__ inline int reluq(int x) { return x > 0 ? x : 0; }
 __device__ inline int sqrtq(int x) { return x > 0 ? (int)isqrt64((unsigned long)x << 16) : 0; }
 __device__ inline int siluq(int x) { return fmulq(x, sigmoidq(x)); }
-__device__ inline int softplusq(int x) { return sat((long)(x > 0 ? x : 0) + logq(ONE + expq(-absq(x)))); }
+__device__ inline int softplusq(int x) { return sat((long)(x > 0 ? x : 0) + logq(ONE + expq_neg(-absq(x)))); }
 __device__ inline int cosq(int x) { return sinq(sat((long)x + HPIQ)); }
 __device__ inline int floorq(int x) { return (int)((unsigned)x & 0xffff0000u); }
 __device__ inline int stepq(int x) { return x > 0 ? ONE : 0; }
-__device__ inline int addq(int x, int y) { return sat((long)x + y); }
-__device__ inline int subq(int x, int y) { return sat((long)x - y); }
 __device__ inline int maxq(int x, int y) { return x > y ? x : y; }
 __device__ inline int minq(int x, int y) { return x < y ? x : y; }
 
@@ -167,8 +219,14 @@ __device__ inline int rmsq(unsigned long ss, int cols)
 	return rms > 0 ? rms : 1;
 }
 
-// softmax's normalisation of one exp value y by the line's sum s > 0
-__device__ inline int softq(long y, long s) { return (int)((y * 65536 + s / 2) / s); }
+// softmax's normalisation of one exp value 0 <= y <= ONE by the line's sum
+// s >= ONE of such values: the quotient is at most 2^16 + 1, so divsmall
+// applies while s < 2^35 (lines of fewer than 2^19 elements)
+__device__ inline int softq(long y, long s)
+{
+	const long n = y * 65536 + s / 2;
+	return (int)(s < (1L << 35) ? divsmall(n, s) : n / s);
+}
 
 // the Q7.24 channel scale applied to an int64 code sum: sat((acc * s + 2^23) >> 24)
 __device__ inline int qscaleq(long acc, int s)

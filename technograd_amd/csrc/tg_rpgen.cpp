@@ -332,7 +332,7 @@ struct Gen {
 					ln(fx ? "mx = " + rd(I.a, b + i) + " > mx ? " + rd(I.a, b + i) + " : mx;" : "if (" + rd(I.a, b + i) + " > mx) mx = " + rd(I.a, b + i) + ";");
 				ln(fx ? "long s = 0;" : "float s = 0.0f;");
 				for (long i = 0; i < cols; i++) {
-					if (fx) ln(wr(I.out, b + i) + " = tgrd::expq(tgrd::subq(" + rd(I.a, b + i) + ", mx)); s += " + rd(I.out, b + i) + ";");
+					if (fx) ln(wr(I.out, b + i) + " = tgrd::expq_neg(tgrd::subq(" + rd(I.a, b + i) + ", mx)); s += " + rd(I.out, b + i) + ";");
 					else ln(wr(I.out, b + i) + " = expf(" + rd(I.a, b + i) + " - mx); s = s + " + rd(I.out, b + i) + ";");
 				}
 				for (long i = 0; i < cols; i++)

@@ -20,6 +20,11 @@ extern "C" long rowdev_prim(int op, long a, long b)
 	case 9: return softq(a, b);
 	case 10: return qscaleq(a, (int)b);
 	case 11: return rmsq((unsigned long)a, (int)b);
+	case 12: return expq_neg((int)a);
+	case 13: return fdivq_unit((int)a, (int)b);
+	case 14: return addq((int)a, (int)b);
+	case 15: return subq((int)a, (int)b);
+	case 16: return absq((int)a);
 	}
 	return 0;
 }
@@ -29,4 +34,9 @@ extern "C" long rowdev_const(int which)
 	using namespace tgrd;
 	const long v[] = { LN2, PIQ, HPIQ, TPIQ, GELU_A, GELU_B, (long)EPS_Q32, EXP_HI, EXP_LO };
 	return which >= 0 && which < 9 ? v[which] : 0;
+}
+
+extern "C" void rowdev_prim_n(int op, const long *a, long *out, long n)
+{
+	for (long i = 0; i < n; i++) out[i] = rowdev_prim(op, a[i], 0);
 }

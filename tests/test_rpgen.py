@@ -27,12 +27,13 @@ def golden(name):
 
 
 def host_unit(tmp, text, fixed):
-    """Emit the unit, build it as host code; returns a runner rows -> (out, steps)."""
+    """Emit the unit, build it as host code (clang++: the element functions use
+    its saturating builtins); returns a runner rows -> (out, steps)."""
     src = hip.emit_unit(text, hip.FIXED if fixed else 0, kernel="tgu")
     unit = tmp / ("u%d.hip" % fixed)
     unit.write_text(src)
     exe = tmp / ("u%d" % fixed)
-    subprocess.run(["g++", "-O1", "-std=c++17", "-ffp-contract=off", "-I", CSRC, "-DTG_UNIT_FILE=\"%s\"" % unit,
+    subprocess.run(["/opt/rocm/llvm/bin/clang++", "-O1", "-std=c++17", "-ffp-contract=off", "-I", CSRC, "-DTG_UNIT_FILE=\"%s\"" % unit,
                     "-DTG_KERNEL=tgu", "-DTG_T=%s" % ("int" if fixed else "float"), "-o", str(exe),
                     os.path.join(ROOT, "tests", "cpp", "unit_host.cpp"), "-lm"], check=True)
     m = O.Model(text)
