@@ -214,6 +214,29 @@ def test_config2_full_size(B):
     assert strict >= ref_strict - 0.01
 
 
+def test_config1_full_width():
+    """Config 1 at its real widths (int8 512 -> 2048 -> 2048 -> 512, tanh,
+    tanh, rmsnorm; rand(1, 0.05) weights, N(0, 1) rows seed 0): 2048 rows on
+    the default path (matrix cores, each tanh in its product's epilogue),
+    the first 128 of them against the oracle interpreter (the reference's
+    arithmetic) under the whole-model predicate with the f64 interpreter as
+    truth, and all 2048 against the reference-order path (TG_HIP_EXACT)."""
+    print("case config1 full width", flush=True)
+    text, x = synth.config1(2048)
+    y, _ = hip.Program(text, max_rows=2048).batch(x)
+    assert np.isfinite(y).all()
+    n = 128
+    ref, _ = O.Model(text).batch(x[:n])
+    t, _ = O.Model(text).batch64(x[:n])
+    ng = parity.check_model(y[:n], ref, t, np.ones(n, bool))
+    print("config1: %d of %d outputs needed the row-error clause" % (ng, y[:n].size), flush=True)
+    ex, _ = hip.Program(text, flags=hip.EXACT, max_rows=2048).batch(x)
+    t2, _ = O.Model(text).batch64(x)
+    ng2 = parity.check_model(y, ex, t2, np.ones(len(x), bool))
+    print("config1 vs reference order, 2048 rows: %d of %d outputs needed the row-error clause" % (ng2, y.size),
+          flush=True)
+
+
 @pytest.mark.parametrize("bits_,M", [(4, 10), (8, 10), (4, 1024)])
 def test_outlier_rows_follow_reference(bits_, M):
     """K = 4096, C = 4096, x @ W: rows with one outlier of 1e2 to 1e6 on a
