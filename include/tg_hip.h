@@ -132,6 +132,16 @@ int tg_hip_matmul_q_noalloc(float *d_o, const signed char *d_q, int bits, const 
 char *tg_hip_emit_unit(const char *tgir, size_t len, int flags, const char *kernel);
 void tg_hip_str_free(char *s);
 
+/* The surface model file at `path` (.tg, with its imports and initializer
+ * files) lowered to canonical TGIR text: the bytes `tgc ir MODEL.tg` prints
+ * (src/main.c:373-375 over src/util.c:335-369: surface_load, lower, ir_write).
+ * The result is what tg_hip_load takes. NULL with the reference's diagnostic
+ * ("file:line: message") in tg_hip_error() for a model the reference
+ * rejects, and for operations the batch backend does not run (autodiff,
+ * training, sparse and memory operations, topk, suffix matching). Needs no
+ * GPU. Free with tg_hip_str_free. */
+char *tg_hip_surface_to_tgir(const char *path);
+
 void tg_hip_free(tg_hip_prog *p);
 const char *tg_hip_error(void);
 int tg_hip_stats(const tg_hip_prog *p, tg_hip_stats_t *st);

@@ -21,6 +21,7 @@
 // in blocks (here: device passes of up to max_rows rows), outputs come back in
 // input order, and steps per row are reported for every think loop.
 #include "tg_hip.h"
+#include "tg_front.h"
 #include "tg_kern.h"
 #include "tg_rpgen.h"
 #include "tgm.h"
@@ -44,7 +45,7 @@
 
 namespace {
 
-thread_local char g_err[512];
+thread_local char g_err[1024];
 
 void seterr(const char *fmt, ...)
 {
@@ -2316,6 +2317,14 @@ char *tg_hip_emit_unit(const char *tgir, size_t len, int flags, const char *kern
 }
 
 void tg_hip_str_free(char *s) { free(s); }
+
+char *tg_hip_surface_to_tgir(const char *path)
+{
+	char err[1024];
+	char *t = path ? tgf_lower(path, err, sizeof err) : nullptr;
+	if (!t) seterr("%s", path ? err : "no model path");
+	return t;
+}
 
 void tg_hip_free(tg_hip_prog *p) { destroy(p); }
 

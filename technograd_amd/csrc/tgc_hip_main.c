@@ -1,6 +1,6 @@
 /* tgc-hip: `tgc batch` on the MI355X backend.
  *
- *   tgc-hip batch MODEL.tgir DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v] [--log FILE]
+ *   tgc-hip batch MODEL DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v] [--log FILE]
  *
  * Same input/output contract as the reference's batch command
  * (src/main.c:400-444, src/io.c): DATA is raw little-endian f32 when it ends in
@@ -32,7 +32,9 @@
  * reference's trace format (src/trace.c: t, level, stage, msg, fields).
  *
  *   tgc-hip fxparse TOKEN...   prints each token's Q16.16 value (no device)
- *   tgc-hip c MODEL.tgir [--fixed] [-o UNIT.hip] [--kernel NAME]
+ *   tgc-hip ir MODEL.tg
+ *       prints the canonical TGIR of a surface model (no device)
+ *   tgc-hip c MODEL [--fixed] [-o UNIT.hip] [--kernel NAME]
  *       writes the model's row program as a freestanding HIP unit (the
  *       device counterpart of `tgc c`, src/main.c:343-360; no device)
  */
@@ -289,6 +291,44 @@ static void write_block(FILE *f, int obin, int fixed, const float *out, const in
 	}
 }
 
+/* a model file's TGIR: the file itself, or a surface (.tg) model lowered
+ * (the reference's load_module rule, src/util.c:335-369: TGIR starts with
+ * '(' or ';' after blanks); NULL with the reason in err */
+static char *load_model(const char *path, size_t *len, char *err, size_t errn)
+{
+	char *text = slurp(path, len);
+	if (!text) {
+		snprintf(err, errn, "cannot read '%s'", path);
+		return NULL;
+	}
+	const char *c = text;
+	while (*c == ' ' || *c == '\t' || *c == '\n' || *c == '\r') c++;
+	if (*c == '(' || *c == ';') return text;
+	free(text);
+	char *t = tg_hip_surface_to_tgir(path);
+	if (!t) {
+		snprintf(err, errn, "%s", tg_hip_error());
+		return NULL;
+	}
+	*len = strlen(t);
+	char *r = malloc(*len + 1);
+	if (r) memcpy(r, t, *len + 1);
+	else snprintf(err, errn, "out of memory");
+	tg_hip_str_free(t);
+	return r;
+}
+
+/* tgc-hip ir MODEL.tg: the canonical TGIR of a surface model (src/main.c:373-375) */
+static int print_ir(int argc, char **argv)
+{
+	if (argc != 3) return die("usage: tgc-hip ir MODEL.tg%s", "");
+	char *t = tg_hip_surface_to_tgir(argv[2]);
+	if (!t) return die("%s", tg_hip_error());
+	fputs(t, stdout);
+	tg_hip_str_free(t);
+	return fflush(stdout) ? die("cannot write the TGIR%s", "") : 0;
+}
+
 /* tgc-hip c: the row program as a HIP unit (tg_hip_emit_unit) */
 static int emit_unit(int argc, char **argv)
 {
@@ -303,8 +343,9 @@ static int emit_unit(int argc, char **argv)
 	}
 	if (!model) return die("usage: tgc-hip c MODEL.tgir [--fixed] [-o UNIT.hip] [--kernel NAME]%s", "");
 	size_t mlen;
-	char *text = slurp(model, &mlen);
-	if (!text) return die("cannot read '%s'", model);
+	char lerr[1024];
+	char *text = load_model(model, &mlen, lerr, sizeof lerr);
+	if (!text) return die("%s", lerr);
 	char *src = tg_hip_emit_unit(text, mlen, flags, kernel);
 	free(text);
 	if (!src) return die("%s", tg_hip_error());
@@ -320,7 +361,7 @@ static int emit_unit(int argc, char **argv)
 	return ok ? 0 : die("cannot write the unit%s", "");
 }
 
-#define USAGE "usage: tgc-hip batch MODEL.tgir DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v] [--log FILE]%s"
+#define USAGE "usage: tgc-hip batch MODEL DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v] [--log FILE]%s"
 
 int main(int argc, char **argv)
 {
@@ -336,6 +377,7 @@ int main(int argc, char **argv)
 		return 0;
 	}
 	if (argc >= 2 && !strcmp(argv[1], "c")) return emit_unit(argc, argv);
+	if (argc >= 2 && !strcmp(argv[1], "ir")) return print_ir(argc, argv);
 	if (argc < 2 || strcmp(argv[1], "batch")) return die(USAGE, "");
 	for (int i = 2; i < argc; i++) {
 		if (!strcmp(argv[i], "-o") && i + 1 < argc) opath = argv[++i];
@@ -354,8 +396,9 @@ int main(int argc, char **argv)
 	if (lpath && !(lf = fopen(lpath, "a"))) return die("cannot open log '%s'", lpath);
 	double t0 = now_ms();
 	size_t mlen;
-	char *text = slurp(model, &mlen);
-	if (!text) return die("cannot read '%s'", model);
+	char lerr[1024];
+	char *text = load_model(model, &mlen, lerr, sizeof lerr);
+	if (!text) return die("%s", lerr);
 	if (tg_hip_init(0)) return die("%s", tg_hip_error());
 	tg_hip_prog *p = tg_hip_load(text, mlen, flags, maxrows);
 	free(text);

@@ -54,6 +54,8 @@ def lib():
         L.tg_hip_emit_unit.restype = vp
         L.tg_hip_emit_unit.argtypes = [ctypes.c_char_p, sz, ip, ctypes.c_char_p]
         L.tg_hip_str_free.argtypes = [vp]
+        L.tg_hip_surface_to_tgir.restype = vp
+        L.tg_hip_surface_to_tgir.argtypes = [ctypes.c_char_p]
         L.tg_hip_error.restype = ctypes.c_char_p
         L.tg_hip_stats.argtypes = [vp, ctypes.POINTER(Stats)]
         L.tg_hip_reset_stats.argtypes = [vp]
@@ -198,6 +200,17 @@ def emit_unit(tgir, flags=0, kernel=None):
     p = lib().tg_hip_emit_unit(t, len(t), flags, kernel.encode() if kernel else None)
     if not p:
         raise RuntimeError("emit_unit: %s" % lib().tg_hip_error().decode())
+    try:
+        return ctypes.string_at(p).decode()
+    finally:
+        lib().tg_hip_str_free(p)
+
+
+def surface_to_tgir(path):
+    """A .tg model file lowered to canonical TGIR text (tg_hip_surface_to_tgir); no GPU needed."""
+    p = lib().tg_hip_surface_to_tgir(os.fsencode(path))
+    if not p:
+        raise RuntimeError(lib().tg_hip_error().decode())
     try:
         return ctypes.string_at(p).decode()
     finally:

@@ -147,6 +147,99 @@ def make_fx_parse(tmp):
     print("fx_parse         %d tokens, %d refused" % (len(toks), len(bad)))
 
 
+# The front end: tests/golden/front/*.tg are this repository's models; the
+# reference lowers each (`tgc ir`) to front/NAME.tgir, with the environment
+# variable FRONT_ENV set as inits.tg expects.
+FRONT_ENV = {"TGF_FRONT_VALUES": "1.5, -2 3e-1,4"}
+
+# Sources the reference rejects, each a file err.tg (plus any other files
+# named), lowered from their directory as `tgc ir err.tg`; the reference's
+# diagnostic (without "error: ") goes to front/errors.json.
+FRONT_ERRORS = {
+    "tab_indent": "model m\ndef forward(x: f32[2]) -> f32[2]:\n\treturn x\n",
+    "inconsistent_dedent": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    y = x\n  return y\n",
+    "unexpected_char": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    return x $ 2\n",
+    "unterminated_string": "model m\nparam w : f32[2] = file(\"w.bin)\n",
+    "reserved_name": "model m\ndef forward(think: f32[2]) -> f32[2]:\n    return think\n",
+    "bad_type": "model m\ndef forward(x: f64[2]) -> f32[2]:\n    return x\n",
+    "rank_5": "model m\nparam w : f32[1, 1, 1, 1, 1] = zeros\ndef forward(x: f32[2]) -> f32[2]:\n    return x\n",
+    "not_posint": "model m\ndef forward(x: f32[2.5]) -> f32[2]:\n    return x\n",
+    "missing_model": "def forward(x: f32[2]) -> f32[2]:\n    return x\n",
+    "duplicate_model": "model m\nmodel n\ndef forward(x: f32[2]) -> f32[2]:\n    return x\n",
+    "duplicate_param": "model m\nparam w : f32[2] = zeros\nparam w : f32[2] = ones\ndef forward(x: f32[2]) -> f32[2]:\n    return x\n",
+    "duplicate_def": "model m\ndef f(x: f32[2]) -> f32[2]:\n    return x\ndef f(x: f32[2]) -> f32[2]:\n    return x\ndef forward(x: f32[2]) -> f32[2]:\n    return f(x)\n",
+    "shadows_builtin": "model m\ndef tanh(x: f32[2]) -> f32[2]:\n    return x\ndef forward(x: f32[2]) -> f32[2]:\n    return x\n",
+    "arg_shadows_param": "model m\nparam w : f32[2] = zeros\ndef f(w: f32[2]) -> f32[2]:\n    return w\ndef forward(x: f32[2]) -> f32[2]:\n    return x\n",
+    "no_forward": "model m\ndef f(x: f32[2]) -> f32[2]:\n    return x\n",
+    "undefined_name": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    return x + y\n",
+    "arg_shape": "model m\ndef f(v: f32[3]) -> f32[3]:\n    return v\ndef forward(x: f32[2]) -> f32[2]:\n    return f(x)\n",
+    "arg_count": "model m\ndef f(v: f32[2]) -> f32[2]:\n    return v\ndef forward(x: f32[2]) -> f32[2]:\n    return f(x, x)\n",
+    "return_shape": "model m\ndef f(v: f32[2]) -> f32[3]:\n    return v\ndef forward(x: f32[2]) -> f32[2]:\n    return f(x)\n",
+    "forward_shape": "model m\ndef forward(x: f32[2]) -> f32[3]:\n    return x\n",
+    "no_return": "model m\ndef f(v: f32[2]) -> f32[2]:\n    w = v\ndef forward(x: f32[2]) -> f32[2]:\n    return f(x)\n",
+    "unreachable": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    return x\n    y = x\n",
+    "assign_param": "model m\nparam w : f32[2] = zeros\ndef forward(x: f32[2]) -> f32[2]:\n    w = x\n    return w\n",
+    "broadcast": "model m\ndef forward(x: f32[2], y: f32[3]) -> f32[2]:\n    return x + y\n",
+    "matmul_shapes": "model m\nparam w : f32[3, 4] = zeros\ndef forward(x: f32[3]) -> f32[3]:\n    return w @ x\n",
+    "unknown_function": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    return frobnicate(x)\n",
+    "op_arity": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    return tanh(x, x)\n",
+    "literal_count": "model m\nparam w : f32[3] = [1, 2]\ndef forward(x: f32[3]) -> f32[3]:\n    return x * w\n",
+    "reshape_count": "model m\ndef forward(x: f32[6]) -> f32[2, 4]:\n    return reshape(x, 2, 4)\n",
+    "transpose_rank": "model m\ndef forward(x: f32[6]) -> f32[6]:\n    return transpose(x)\n",
+    "think_unbound": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    think h for 3:\n        h = x\n    return x\n",
+    "think_param": "model m\nparam w : f32[2] = zeros\ndef forward(x: f32[2]) -> f32[2]:\n    think w for 3:\n        w = x\n    return x\n",
+    "think_outer": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    h = x\n    y = x\n    think h for 3:\n        y = h\n        h = tanh(h)\n    return h\n",
+    "think_return": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    h = x\n    think h for 3:\n        return h\n    return h\n",
+    "think_negative_eps": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    h = x\n    think h for 3 until -1:\n        h = tanh(h)\n    return h\n",
+    "halt_threshold": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    h = x\n    think h for 3 halt p at 1.5:\n        h = tanh(h)\n        p = sum(h)\n    return h\n",
+    "halt_undefined": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    h = x\n    think h for 3 halt p:\n        h = tanh(h)\n    return h\n",
+    "halt_not_scalar": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    h = x\n    think h for 3 halt p:\n        h = tanh(h)\n        p = h\n    return h\n",
+    "scan_twice": "model m\ndef forward(xs: f32[3, 2]) -> f32[2]:\n    c = xs @ ones2\n    scan c, c over xt in xs:\n        c = c + xt\n    return c\nparam ones2 : f32[2, 2] = ones\n",
+    "scan_lengths": "model m\ndef forward(xs: f32[3, 2], ys: f32[4, 2]) -> f32[2]:\n    c = xs[0]\n    return c\n",
+    "scan_length_mismatch": "model m\nparam c0 : f32[2] = zeros\ndef forward(xs: f32[3, 2], ys: f32[4, 2]) -> f32[2]:\n    c = c0 * 1\n    scan c over xt in xs, yt in ys:\n        c = c + xt + yt\n    return c\n",
+    "scan_carry_shape": "model m\nparam c0 : f32[2] = zeros\ndef forward(xs: f32[3, 2]) -> f32[2]:\n    c = c0 * 1\n    scan c over xt in xs:\n        c = sum(xt)\n    return c\n",
+    "emit_outside": "model m\ndef forward(x: f32[2]) -> f32[2]:\n    emit y = x\n    return x\n",
+    "emit_twice": "model m\nparam c0 : f32[2] = zeros\ndef forward(xs: f32[3, 2]) -> f32[3, 2]:\n    c = c0 * 1\n    scan c over xt in xs:\n        c = c + xt\n        emit y = c\n        emit y = xt\n    return y\n",
+    "env_unset": "model m\nparam w : f32[2] = env(\"TGF_FRONT_NEVER_SET\")\ndef forward(x: f32[2]) -> f32[2]:\n    return x * w\n",
+    "file_size": {"err.tg": "model m\nparam w : f32[3] = file(\"w.bin\")\ndef forward(x: f32[3]) -> f32[3]:\n    return x * w\n",
+                  "w.bin": b"\0\0\0\0\0\0\0\0"},
+    "import_missing": "model m\nimport \"nope.tg\"\ndef forward(x: f32[2]) -> f32[2]:\n    return x\n",
+    "import_cycle": {"err.tg": "model m\nimport \"lib/b.tg\"\ndef forward(x: f32[2]) -> f32[2]:\n    return x\n",
+                     "lib/b.tg": "import \"../err.tg\"\n"},
+    "imported_duplicate": {"err.tg": "model m\nimport \"l.tg\"\nparam w : f32[2] = zeros\ndef forward(x: f32[2]) -> f32[2]:\n    return x * w\n",
+                           "l.tg": "param w : f32[2] = ones\n"},
+    "unexpected_indent": "  model m\n",
+}
+
+
+def make_front():
+    d = os.path.join(HERE, "front")
+    env = dict(os.environ, **FRONT_ENV)
+    for f in sorted(os.listdir(d)):
+        if f.endswith(".tg"):
+            r = subprocess.run([O.REF_BIN, "ir", f], cwd=d, env=env, check=True, capture_output=True)
+            with open(os.path.join(d, f[:-3] + ".tgir"), "wb") as fh:
+                fh.write(r.stdout)
+            print("front %-10s %6d bytes of TGIR" % (f, len(r.stdout)))
+    errs = {}
+    for name, files in sorted(FRONT_ERRORS.items()):
+        if isinstance(files, str):
+            files = {"err.tg": files}
+        w = tempfile.mkdtemp()
+        for fn, body in files.items():
+            os.makedirs(os.path.dirname(os.path.join(w, fn)), exist_ok=True)
+            with open(os.path.join(w, fn), "wb" if isinstance(body, bytes) else "w") as fh:
+                fh.write(body)
+        r = subprocess.run([O.REF_BIN, "ir", "err.tg"], cwd=w, capture_output=True, text=True)
+        if r.returncode == 0:
+            sys.exit("front error case %s: the reference accepted it" % name)
+        msg = r.stderr.strip().splitlines()[-1].replace("error: ", "", 1)
+        errs[name] = {"files": {k: (v if isinstance(v, str) else list(v)) for k, v in files.items()}, "message": msg}
+        print("front error %-20s %s" % (name, msg[:90]))
+    with open(os.path.join(d, "errors.json"), "w") as fh:
+        json.dump(errs, fh, indent=1, sort_keys=True)
+
+
 def main():
     if not O.have_ref():
         sys.exit("oracle/_ref/tgc_ref is missing: run make -C oracle ref")
@@ -154,6 +247,8 @@ def main():
     only = set(sys.argv[1:])
     if not only or "fx_parse" in only:
         make_fx_parse(tmp)
+    if not only or "front" in only:
+        make_front()
     for i, (name, build) in enumerate(sorted(_synth().items())):
         if only and name not in only:
             continue

@@ -135,3 +135,19 @@ def test_rows_are_validated_before_output(tmp_path):
         fh.write(",".join(["1"] * per) + "\n" + ",".join(["2"] * per) + "\n" + ",".join(["3x"] * per) + "\n")
     r = cli([model, inp, "-o", out])
     assert r.returncode == 1 and ":3: bad number" in r.stderr and not out.exists()
+
+
+def test_surface_model_runs_like_its_tgir(tmp_path):
+    """A .tg model given to `batch` is lowered first (the reference's
+    load_module rule): the output file equals the one for its TGIR golden,
+    byte for byte, in f32 and in Q16.16."""
+    model, d = golden("latent_f32")
+    surface = os.path.join(GOLDEN, "models", "latent.tg")
+    inp = tmp_path / "x.bin"
+    d["x"].astype("<f4").tofile(inp)
+    for flags in ([], ["--fixed"]):
+        a, b = tmp_path / "a.bin", tmp_path / "b.bin"
+        ra = cli([model, inp, "-o", a] + flags)
+        rb = cli([surface, inp, "-o", b] + flags)
+        assert ra.returncode == 0 and rb.returncode == 0, ra.stderr + rb.stderr
+        assert a.read_bytes() == b.read_bytes()
