@@ -132,6 +132,14 @@ int tg_hip_matmul_q_noalloc(float *d_o, const signed char *d_q, int bits, const 
 char *tg_hip_emit_unit(const char *tgir, size_t len, int flags, const char *kernel);
 void tg_hip_str_free(char *s);
 
+/* The program's model name, and its signature as the JSON object the
+ * reference's `tgc serve` answers `GET /` with (src/serve.c:320-332: model,
+ * inputs with their types, output type, values per row, think loops,
+ * stateful) followed by a newline; returns the JSON length, or -1 (text
+ * truncated to n - 1 bytes when longer). */
+const char *tg_hip_model_name(const tg_hip_prog *p);
+int tg_hip_signature(const tg_hip_prog *p, char *json, size_t n);
+
 /* The surface model file at `path` (.tg, with its imports and initializer
  * files) lowered to canonical TGIR text: the bytes `tgc ir MODEL.tg` prints
  * (src/main.c:373-375 over src/util.c:335-369: surface_load, lower, ir_write).

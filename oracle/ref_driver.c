@@ -196,7 +196,7 @@ static int unit(int argc, char **argv)
 int main(int argc, char **argv)
 {
 	if (argc < 3) {
-		fputs("usage: tgc_ref ir|quantize|batch|c MODEL ...\n", stderr);
+		fputs("usage: tgc_ref ir|quantize|batch|c|serve|stream MODEL ...\n", stderr);
 		return 2;
 	}
 	if (!strcmp(argv[1], "quantize")) {
@@ -211,6 +211,22 @@ int main(int argc, char **argv)
 	}
 	if (!strcmp(argv[1], "batch")) return batch(argc, argv);
 	if (!strcmp(argv[1], "c")) return unit(argc, argv);
+	if (!strcmp(argv[1], "serve") || !strcmp(argv[1], "stream")) { /* src/main.c:361-369: the reference's connections */
+		Module *m = load_module(argv[2]);
+		plan(m);
+		par_init(1);
+		tg_signals();
+		if (!strcmp(argv[1], "serve")) {
+			if (argc != 5 || strcmp(argv[3], "--listen")) return 2;
+			return serve_main(m, argv[4]);
+		}
+		const char *src = "-", *dst = NULL;
+		for (int i = 3; i < argc; i++) {
+			if (!strcmp(argv[i], "-o") && i + 1 < argc) dst = argv[++i];
+			else src = argv[i];
+		}
+		return stream_main(m, src, dst);
+	}
 	fputs("unknown command\n", stderr);
 	return 2;
 }

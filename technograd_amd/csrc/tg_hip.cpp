@@ -2096,6 +2096,27 @@ tg_hip_prog *tg_hip_load(const char *tgir, size_t len, int flags, int max_rows)
 	return p;
 }
 
+const char *tg_hip_model_name(const tg_hip_prog *p) { return p ? p->m->name : ""; }
+
+int tg_hip_signature(const tg_hip_prog *p, char *json, size_t n)
+{
+	if (!p || !json || !n) return -1;
+	std::string s = std::string("{\"model\":\"") + p->m->name + "\",\"inputs\":[";
+	auto type = [](const tgm_shape &sh) {
+		std::string t = "(f32";
+		for (int i = 0; i < sh.rank; i++) t += " " + std::to_string(sh.dim[i]);
+		return t + ")";
+	};
+	for (int i = 0; i < p->m->ninputs; i++) {
+		const tgm_value &v = p->m->val[p->m->inputs[i]];
+		s += std::string(i ? "," : "") + "{\"name\":\"" + v.name + "\",\"type\":\"" + type(v.sh) + "\"}";
+	}
+	s += "],\"output\":\"" + type(p->m->val[p->m->output].sh) + "\",\"values_per_row\":" + std::to_string(p->m->per) +
+	     ",\"think_loops\":" + std::to_string(p->m->nthink) + ",\"stateful\":" + (p->m->nupd ? "true" : "false") + "}\n";
+	snprintf(json, n, "%s", s.c_str());
+	return s.size() < n ? (int)s.size() : -1;
+}
+
 int tg_hip_info(const tg_hip_prog *p, int *per, int *nout, int *nthink)
 {
 	if (!p) return -1;

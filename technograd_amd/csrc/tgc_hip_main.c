@@ -32,6 +32,9 @@
  * reference's trace format (src/trace.c: t, level, stage, msg, fields).
  *
  *   tgc-hip fxparse TOKEN...   prints each token's Q16.16 value (no device)
+ *   tgc-hip stream MODEL [SRC] [-o DST] [--fixed] [--exact] [--rows N]
+ *   tgc-hip serve MODEL --listen [HOST:]PORT [--fixed] [--exact] [--rows N] [--window-us U]
+ *       the reference's connections (src/serve.c) on the device batch: see tgc_hip_serve.c
  *   tgc-hip ir MODEL.tg
  *       prints the canonical TGIR of a surface model (no device)
  *   tgc-hip c MODEL [--fixed] [-o UNIT.hip] [--kernel NAME]
@@ -39,6 +42,7 @@
  *       device counterpart of `tgc c`, src/main.c:343-360; no device)
  */
 #include "tg_hip.h"
+#include "tgc_hip_cli.h"
 
 #include <math.h>
 #include <signal.h>
@@ -52,8 +56,9 @@
 /* the signal that asked the batch to stop (0: none) */
 static atomic_int stop_sig;
 static void on_signal(int sig) { atomic_store(&stop_sig, sig); }
+int stop_signal(void) { return atomic_load(&stop_sig); }
 
-static void install_signals(void)
+void install_signals(void)
 {
 	struct sigaction sa;
 	memset(&sa, 0, sizeof sa);
@@ -99,7 +104,7 @@ static const char *fx_parse(const char *s, int32_t *v)
 	return s;
 }
 
-static int die(const char *fmt, const char *a)
+int die(const char *fmt, const char *a)
 {
 	fprintf(stderr, "tgc-hip: error: ");
 	fprintf(stderr, fmt, a);
@@ -133,7 +138,7 @@ static char *slurp(const char *path, size_t *len)
 
 /* numbers of one text line (f32, or Q16.16 words with `fixed`); -1 on a bad
  * token (src/io.c:25-41 rules) */
-static int parse_row(const char *s, float *v, int max, const char **bad, int fixed)
+int parse_row(const char *s, float *v, int max, const char **bad, int fixed)
 {
 	int n = 0;
 	for (;;) {
@@ -225,7 +230,7 @@ static float *load_rows(const char *path, int per, long *rows, char *err, size_t
 	return all;
 }
 
-static void fx_format(int32_t v, char *buf) /* 6 decimals, integer arithmetic */
+void fx_format(int32_t v, char *buf) /* 6 decimals, integer arithmetic */
 {
 	int64_t x = v, neg = x < 0;
 	if (neg) x = -x;
@@ -294,7 +299,7 @@ static void write_block(FILE *f, int obin, int fixed, const float *out, const in
 /* a model file's TGIR: the file itself, or a surface (.tg) model lowered
  * (the reference's load_module rule, src/util.c:335-369: TGIR starts with
  * '(' or ';' after blanks); NULL with the reason in err */
-static char *load_model(const char *path, size_t *len, char *err, size_t errn)
+char *load_model(const char *path, size_t *len, char *err, size_t errn)
 {
 	char *text = slurp(path, len);
 	if (!text) {
@@ -378,6 +383,8 @@ int main(int argc, char **argv)
 	}
 	if (argc >= 2 && !strcmp(argv[1], "c")) return emit_unit(argc, argv);
 	if (argc >= 2 && !strcmp(argv[1], "ir")) return print_ir(argc, argv);
+	if (argc >= 2 && !strcmp(argv[1], "stream")) return stream_main(argc, argv);
+	if (argc >= 2 && !strcmp(argv[1], "serve")) return serve_main(argc, argv);
 	if (argc < 2 || strcmp(argv[1], "batch")) return die(USAGE, "");
 	for (int i = 2; i < argc; i++) {
 		if (!strcmp(argv[i], "-o") && i + 1 < argc) opath = argv[++i];

@@ -240,6 +240,79 @@ def make_front():
         json.dump(errs, fh, indent=1, sort_keys=True)
 
 
+# `tgc serve` conversations recorded from the reference (front/serve.json):
+# for each model, the row protocol over one connection and each HTTP request
+# on its own connection, with the exact bytes sent and received. Models
+# without transcendentals (odd_q4: the exact path must give the same bytes).
+SERVE_MODELS = ["odd_q4", "latent_f32"]
+
+
+def serve_requests(x):
+    rows = [",".join("%.9g" % v for v in r) for r in x[:3]]
+    lines = rows[:2] + ["", "# a comment", "1,2,abc", "1, 2 3", rows[2]]
+    body = "\n".join(lines) + "\n"
+    return [
+        ("rows", "\n".join(lines) + "\n"),
+        ("health", "GET /health HTTP/1.1\r\nHost: x\r\n\r\n"),
+        ("signature", "GET / HTTP/1.1\r\n\r\n"),
+        ("run", "POST /run HTTP/1.1\r\nContent-Length: %d\r\n\r\n%s" % (len(body), body)),
+        ("missing", "GET /nope HTTP/1.1\r\n\r\n"),
+        ("bad", "GET\r\n\r\n"),
+    ]
+
+
+def converse(port, data, expect_lines=None, timeout=20):
+    """Send data on a new connection; read until the peer closes, or until
+    expect_lines lines arrived (the row protocol keeps the connection open)."""
+    import socket
+    import time
+    s = socket.create_connection(("127.0.0.1", port), timeout=timeout)
+    s.sendall(data.encode())
+    got, t0 = b"", time.time()
+    while time.time() - t0 < timeout:
+        if expect_lines is not None and got.count(b"\n") >= expect_lines:
+            break
+        try:
+            k = s.recv(65536)
+        except socket.timeout:
+            break
+        if not k:
+            break
+        got += k
+    s.close()
+    return got.decode()
+
+
+def make_serve():
+    import socket
+    import time
+    out = {}
+    for name in SERVE_MODELS:
+        mpath = os.path.join(HERE, name + ".tgir")
+        x = np.load(os.path.join(HERE, name + ".npz"))["x"]
+        with socket.socket() as so:
+            so.bind(("127.0.0.1", 0))
+            port = so.getsockname()[1]
+        srv = subprocess.Popen([O.REF_BIN, "serve", mpath, "--listen", "127.0.0.1:%d" % port], stderr=subprocess.PIPE)
+        try:
+            for _ in range(100):
+                try:
+                    socket.create_connection(("127.0.0.1", port), timeout=1).close()
+                    break
+                except OSError:
+                    time.sleep(0.1)
+            conv = {}
+            for tag, data in serve_requests(x):
+                conv[tag] = {"send": data, "recv": converse(port, data, expect_lines=5 if tag == "rows" else None)}
+            out[name] = conv
+        finally:
+            srv.terminate()
+            srv.wait(timeout=30)
+        print("serve %-10s %d conversations recorded" % (name, len(out[name])))
+    with open(os.path.join(HERE, "front", "serve.json"), "w") as fh:
+        json.dump(out, fh, indent=1, sort_keys=True)
+
+
 def main():
     if not O.have_ref():
         sys.exit("oracle/_ref/tgc_ref is missing: run make -C oracle ref")
@@ -249,6 +322,8 @@ def main():
         make_fx_parse(tmp)
     if not only or "front" in only:
         make_front()
+    if not only or "serve" in only:
+        make_serve()
     for i, (name, build) in enumerate(sorted(_synth().items())):
         if only and name not in only:
             continue
