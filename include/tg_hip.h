@@ -140,6 +140,24 @@ void tg_hip_str_free(char *s);
 const char *tg_hip_model_name(const tg_hip_prog *p);
 int tg_hip_signature(const tg_hip_prog *p, char *json, size_t n);
 
+/* `tgc quantize` (src/quant.c:318-384) on the backend: the model (TGIR) with
+ * its eligible params quantized to int`bits` per channel, as canonical TGIR
+ * text (free with tg_hip_str_free). RTN, or with `gptq` GPTQ over a
+ * calibration Hessian: the f32 model runs over the `ncalib` calibration rows
+ * ([ncalib][per] f32) on the device, capturing each weight's other matmul
+ * operand as the reference's hook does (src/quant.c:92-117), and the device
+ * sums H = sum x x^T in the reference's order (the same f64 values). The
+ * reference computes Hessians only for K <= 2048 (src/quant.c:346): with
+ * max_k = 2048 the output is the reference's; max_k <= 0 gives every
+ * eligible weight its Hessian (larger K diverges from the reference by
+ * design). With calibration rows the log also reports the output change on
+ * them (device runs of both models). RTN without calibration rows needs no
+ * GPU. `log` receives the report lines; bytes (may be NULL) the params' size
+ * before and after, as the reference reports it. NULL with tg_hip_error()
+ * on failure. */
+char *tg_hip_quantize_model(const char *tgir, size_t len, int bits, int gptq, const float *calib, long ncalib, int min_size, int max_k,
+			    long *bytes, char *log, size_t logn);
+
 /* The surface model file at `path` (.tg, with its imports and initializer
  * files) lowered to canonical TGIR text: the bytes `tgc ir MODEL.tg` prints
  * (src/main.c:373-375 over src/util.c:335-369: surface_load, lower, ir_write).

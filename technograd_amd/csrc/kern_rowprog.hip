@@ -143,6 +143,20 @@ __global__ __launch_bounds__(256) void rowprog_k(rp_args A)
 		case RP_MM: {
 			const int G = I.p[0], M = I.p[1], K = I.p[2], N = I.p[3], quant = I.p[4], bits = I.p[5];
 			const uint8_t *codes = A.codes + I.p[6];
+			if (!FX && I.p[8] && G == 1) { /* calibration: this product's samples, as the reference's hook sees them */
+				const int c = I.p[8] - 1, add = I.p[9] ? M : N;
+				int *cnt = A.cap_count + (long)c * A.rows + row;
+				if (*cnt + add <= A.cap_rows[c]) {
+					float *dst = A.cap + A.cap_base[c] + ((long)row * A.cap_rows[c] + *cnt) * K;
+					if (I.p[9])
+						for (int i = 0; i < M; i++)
+							for (int r = 0; r < K; r++) dst[(long)i * K + r] = a.f((long)i * K + r);
+					else
+						for (int j = 0; j < N; j++)
+							for (int r = 0; r < K; r++) dst[(long)j * K + r] = b.f((long)r * N + j);
+				}
+				*cnt += add;
+			}
 			for (int g = 0; g < G; g++)
 				for (int i = 0; i < M; i++)
 					for (int j = 0; j < N; j++) {
@@ -346,7 +360,34 @@ __global__ __launch_bounds__(256) void rowprog_k(rp_args A)
 	for (int i = 0; i < A.nout; i++) A.out[row * A.nout + i] = res.f(i);
 }
 
+// H[r][c] = sum of x_r x_c over the samples, rows in order and each row's
+// samples in the order its products ran, skipping x_r == 0: the additions of
+// src/quant.c:100-115 in their order (each f64 product of two f32 is exact),
+// so H is the reference's to the bit. Both triangles are summed (the skip
+// makes H[r][c] and H[c][r] differ where an x is infinite).
+__global__ __launch_bounds__(256) void hessian_k(const float *cap, const int *count, long row_cap, int K, int rows, double *H)
+{
+	const int c = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
+	if (c >= K) return;
+	double s = 0.0;
+	for (int row = 0; row < rows; row++) {
+		const float *x = cap + (long)row * row_cap * K;
+		const int n = count[row] < row_cap ? count[row] : (int)row_cap;
+		for (int t = 0; t < n; t++) {
+			const double xr = x[(long)t * K + r];
+			if (xr != 0.0) s = s + xr * (double)x[(long)t * K + c];
+		}
+	}
+	H[(long)r * K + c] = s;
+}
+
 } // namespace
+
+void tgk_hessian(hipStream_t s, const float *cap, const int *count, long row_cap, int K, int rows, double *H)
+{
+	if (K <= 0) return;
+	hessian_k<<<dim3((unsigned)((K + 255) / 256), (unsigned)K), 256, 0, s>>>(cap, count, row_cap, K, rows, H);
+}
 
 void tgk_rowprog(hipStream_t s, const rp_args *a)
 {

@@ -22,6 +22,7 @@
 // input order, and steps per row are reported for every think loop.
 #include "tg_hip.h"
 #include "tg_front.h"
+#include "tg_gptq.h"
 #include "tg_kern.h"
 #include "tg_rpgen.h"
 #include "tgm.h"
@@ -186,6 +187,12 @@ struct tg_hip_prog {
 	rp_ins *d_rprog = nullptr;
 	long rp_arena = 0;
 	int rp_in_slot = 0, rp_out_ref = 0;
+	// calibration capture (tg_hip_quantize_model): value -> capture index, each capture's axis and per-row sample capacity
+	std::vector<int> cap_of, cap_axis, cap_rows;
+	int cap_both = 0; // a product of two eligible params (both sides would be samples): not captured
+	float *d_cap = nullptr;
+	long *d_cap_base = nullptr;
+	int *d_cap_k = nullptr, *d_cap_rows = nullptr, *d_cap_count = nullptr;
 	hipModule_t rp_mod = nullptr;  // the row program compiled for this model
 	hipFunction_t rp_fn = nullptr; // its kernel (null: the interpreter runs the program)
 	std::string rp_why;            // why the program runs in the interpreter
@@ -1037,6 +1044,7 @@ struct RB {
 	std::vector<int> ref; // value -> rp reference (INT_MIN: not yet placed)
 	long slots = 0;
 	bool fixed;
+	long mult = 1; // executions per row of the instruction being built (think budgets and scan lengths)
 };
 
 int rp_ref(RB &B, int v)
@@ -1124,6 +1132,17 @@ bool rp_ins_of(RB &B, const tgm_ins &in)
 		r.a = quant == 1 ? 0 : rp_ref(B, in.a[0]);
 		r.b = quant == 2 ? 0 : rp_ref(B, in.a[1]);
 		r.p[0] = gg, r.p[1] = mm, r.p[2] = kk, r.p[3] = nn, r.p[4] = quant;
+		if (!B.p->cap_of.empty() && gg == 1) { /* calibration samples, as src/quant.c:92-117 takes them */
+			const int c0 = B.p->cap_of[in.a[0]], c1 = B.p->cap_of[in.a[1]];
+			const bool left = c0 >= 0 && B.p->cap_axis[c0] == 0, right = c1 >= 0 && B.p->cap_axis[c1] == 1;
+			if (left && right) B.p->cap_both = 1;
+			const int c = left ? c0 : right ? c1 : -1;
+			if (c >= 0) {
+				r.p[8] = c + 1;
+				r.p[9] = left ? 0 : 1;
+				B.p->cap_rows[c] += (int)(B.mult * (left ? nn : mm));
+			}
+		}
 		if (quant) {
 			int v = quant == 1 ? in.a[0] : in.a[1];
 			r.p[5] = m->val[v].qbits;
@@ -1194,7 +1213,10 @@ bool rp_ins_of(RB &B, const tgm_ins &in)
 		t.p[8] = to_fixed(in.hthr, 16);
 		int at = (int)Pr.size();
 		Pr.push_back(t);
+		const long mult = B.mult;
+		B.mult *= in.maxit;
 		if (!rp_block(B, in.body)) return false;
+		B.mult = mult;
 		Pr[at].p[0] = rp_ref(B, in.yield);
 		Pr[at].p[3] = in.halt >= 0 ? rp_ref(B, in.halt) : INT_MIN;
 		rp_ins e = rpi(RP_THINK_END);
@@ -1224,7 +1246,10 @@ bool rp_ins_of(RB &B, const tgm_ins &in)
 			c.p[2] = 1;
 			Pr.push_back(c);
 		}
+		const long mult = B.mult;
+		B.mult *= in.T;
 		if (!rp_block(B, in.body)) return false;
+		B.mult = mult;
 		for (int y = 0; y < in.ny; y++) {
 			rp_ins c = rpi(RP_COPY);
 			c.out = rp_ref(B, in.ys[y]);
@@ -1518,6 +1543,11 @@ int run_pass(tg_hip_prog *p, const float *d_in, int rows, float *d_out, int *d_s
 		a.nthink = p->m->nthink ? p->m->nthink : 1;
 		a.rows = rows;
 		a.fixed = p->fixed;
+		a.cap = p->d_cap;
+		a.cap_base = p->d_cap_base;
+		a.cap_k = p->d_cap_k;
+		a.cap_rows = p->d_cap_rows;
+		a.cap_count = p->d_cap_count;
 		tgk_rowprog(p->st, &a);
 		return hipok(hipGetLastError(), "row program launch") ? 0 : -1;
 	}
@@ -1926,7 +1956,8 @@ void destroy(tg_hip_prog *p)
 {
 	if (!p) return;
 	for (auto &q : p->qws) tgk_qweight_free(&q);
-	void *bufs[] = { p->d_pool, p->d_imap, p->d_codes, p->d_fscale, p->d_qscale, p->d_arena, p->d_scratch, p->d_rprog, p->d_steps };
+	void *bufs[] = { p->d_pool, p->d_imap, p->d_codes, p->d_fscale, p->d_qscale, p->d_arena, p->d_scratch, p->d_rprog, p->d_steps,
+		         p->d_cap, p->d_cap_base, p->d_cap_k, p->d_cap_rows, p->d_cap_count };
 	for (void *b : bufs)
 		if (b) (void)hipFree(b);
 	auto &h = p->hp;
@@ -2065,7 +2096,9 @@ int tg_hip_init(int device)
 	return scratch_on(device) ? 0 : -1; // the no-allocation entry point's scratch on this device
 }
 
-tg_hip_prog *tg_hip_load(const char *tgir, size_t len, int flags, int max_rows)
+// A device program; with `cap` (calibration), the row-program interpreter with
+// the products of the listed params capturing their samples.
+tg_hip_prog *load_prog(const char *tgir, size_t len, int flags, int max_rows, const tgq_param *cap, int ncap)
 {
 	char err[512];
 	tgm_module *m = tgm_read(tgir, len, err, sizeof err);
@@ -2080,6 +2113,15 @@ tg_hip_prog *tg_hip_load(const char *tgir, size_t len, int flags, int max_rows)
 	}
 	tg_hip_prog *p = new tg_hip_prog;
 	p->m = m;
+	if (cap) {
+		flags |= TG_HIP_ROWPROG | TG_HIP_INTERP;
+		p->cap_of.assign(m->nval, -1);
+		for (int i = 0; i < ncap; i++) {
+			p->cap_of[cap[i].v] = i;
+			p->cap_axis.push_back(cap[i].axis);
+		}
+		p->cap_rows.assign(ncap, 0);
+	}
 	p->flags = flags;
 	p->fixed = (flags & TG_HIP_FIXED) != 0;
 	p->max_rows = max_rows > 0 ? max_rows : 4096;
@@ -2094,6 +2136,11 @@ tg_hip_prog *tg_hip_load(const char *tgir, size_t len, int flags, int max_rows)
 		return nullptr;
 	}
 	return p;
+}
+
+tg_hip_prog *tg_hip_load(const char *tgir, size_t len, int flags, int max_rows)
+{
+	return load_prog(tgir, len, flags, max_rows, nullptr, 0);
 }
 
 const char *tg_hip_model_name(const tg_hip_prog *p) { return p ? p->m->name : ""; }
@@ -2345,6 +2392,177 @@ char *tg_hip_surface_to_tgir(const char *path)
 	char *t = path ? tgf_lower(path, err, sizeof err) : nullptr;
 	if (!t) seterr("%s", path ? err : "no model path");
 	return t;
+}
+
+namespace {
+
+// The f32 model over the calibration rows in one device pass of the row
+// interpreter, capturing every listed param's samples; each param's Hessian
+// summed on the device in the reference's order (tgk_hessian) and copied to
+// q[i].H (malloc'd) with its sample count. The outputs go to ref.
+int calibrate(const char *tgir, size_t len, tgq_param *q, int n, const float *calib, long ncalib, std::vector<float> &ref)
+{
+	if (ncalib > INT_MAX) {
+		seterr("too many calibration rows");
+		return -1;
+	}
+	tg_hip_prog *p = load_prog(tgir, len, 0, (int)ncalib, q, n);
+	if (!p) return -1;
+	auto fail = [&](void *a, void *b, void *c, void *d) {
+		for (void *x : { a, b, c, d })
+			if (x) (void)hipFree(x);
+		destroy(p);
+		return -1;
+	};
+	if (p->cap_both) {
+		seterr("a product of two eligible params: its calibration samples are not captured");
+		return fail(nullptr, nullptr, nullptr, nullptr);
+	}
+	const long per = p->m->per, nout = p->m->nout, nt = p->m->nthink ? p->m->nthink : 1;
+	std::vector<long> base(n);
+	std::vector<int> ks(n);
+	long tot = 0;
+	for (int i = 0; i < n; i++)
+		if (q[i].K > 65535) {
+			seterr("a layer %d inputs wide gets no Hessian on this backend (at most 65535)", q[i].K);
+			return fail(nullptr, nullptr, nullptr, nullptr);
+		}
+	for (int i = 0; i < n; i++) {
+		base[i] = tot;
+		ks[i] = q[i].K;
+		tot += ncalib * (long)p->cap_rows[i] * q[i].K;
+	}
+	if (tot > (8L << 30) / 4) {
+		seterr("calibration samples need %ld MiB of device memory", tot * 4 >> 20);
+		return fail(nullptr, nullptr, nullptr, nullptr);
+	}
+	float *d_in = nullptr, *d_out = nullptr;
+	int *d_steps = nullptr;
+	double *d_h = nullptr;
+	bool ok = hipok(hipMalloc(&p->d_cap, (size_t)(tot ? tot : 1) * 4), "calibration samples") &&
+		  upload(&p->d_cap_base, base, p->st) && upload(&p->d_cap_k, ks, p->st) && upload(&p->d_cap_rows, p->cap_rows, p->st) &&
+		  hipok(hipMalloc(&p->d_cap_count, (size_t)n * ncalib * sizeof(int) + 4), "calibration counts") &&
+		  hipok(hipMemsetAsync(p->d_cap_count, 0, (size_t)n * ncalib * sizeof(int) + 4, p->st), "memset") &&
+		  hipok(hipMalloc(&d_in, (size_t)ncalib * per * 4), "calibration rows") &&
+		  hipok(hipMalloc(&d_out, (size_t)ncalib * nout * 4), "calibration outputs") &&
+		  hipok(hipMalloc(&d_steps, (size_t)ncalib * nt * 4), "calibration steps") &&
+		  hipok(hipMemcpyAsync(d_in, calib, (size_t)ncalib * per * 4, hipMemcpyHostToDevice, p->st), "upload");
+	if (!ok || tg_hip_batch_device(p, d_in, ncalib, d_out, d_steps) || tg_hip_sync(p)) return fail(d_in, d_out, d_steps, nullptr);
+	ref.resize((size_t)ncalib * nout);
+	std::vector<int> cnt((size_t)n * ncalib);
+	ok = hipok(hipMemcpy(ref.data(), d_out, ref.size() * 4, hipMemcpyDeviceToHost), "download") &&
+	     hipok(hipMemcpy(cnt.data(), p->d_cap_count, cnt.size() * 4, hipMemcpyDeviceToHost), "download");
+	for (size_t i = 0; ok && i < cnt.size(); i++)
+		if (cnt[i] > p->cap_rows[i / ncalib]) {
+			seterr("internal: %d calibration samples of param %d in a row, room for %d", cnt[i], (int)(i / ncalib), p->cap_rows[i / ncalib]);
+			ok = false;
+		}
+	for (int i = 0; ok && i < n; i++) {
+		if (!p->cap_rows[i]) continue; /* never in a product the hook sees */
+		const size_t kk = (size_t)q[i].K * q[i].K;
+		q[i].H = (double *)malloc(kk * sizeof(double));
+		ok = q[i].H && hipok(hipMalloc(&d_h, kk * sizeof(double)), "Hessian");
+		if (!ok) break;
+		tgk_hessian(p->st, p->d_cap + base[i], p->d_cap_count + (long)i * ncalib, p->cap_rows[i], q[i].K, (int)ncalib, d_h);
+		ok = hipok(hipGetLastError(), "Hessian launch") && hipok(hipMemcpyAsync(q[i].H, d_h, kk * sizeof(double), hipMemcpyDeviceToHost, p->st), "download") &&
+		     hipok(hipStreamSynchronize(p->st), "Hessian");
+		(void)hipFree(d_h);
+		d_h = nullptr;
+		q[i].nsamp = 0;
+		for (long r = 0; r < ncalib; r++) q[i].nsamp += cnt[(size_t)i * ncalib + r];
+	}
+	if (!ok) return fail(d_in, d_out, d_steps, d_h);
+	fail(d_in, d_out, d_steps, nullptr);
+	return 0;
+}
+
+// the model's outputs over rows on the device (default path)
+int run_outputs(const char *tgir, size_t len, const float *rows, long n, std::vector<float> &out)
+{
+	tg_hip_prog *p = tg_hip_load(tgir, len, 0, n > 4096 ? 4096 : (int)n);
+	if (!p) return -1;
+	out.resize((size_t)n * p->m->nout);
+	std::vector<int> steps((size_t)n * (p->m->nthink ? p->m->nthink : 1));
+	int rc = tg_hip_batch(p, rows, n, out.data(), steps.data());
+	destroy(p);
+	return rc;
+}
+
+} // namespace
+
+char *tg_hip_quantize_model(const char *tgir, size_t len, int bits, int gptq, const float *calib, long ncalib, int min_size, int max_k,
+			    long *bytes, char *log, size_t logn)
+{
+	char dummy[1];
+	if (!log || !logn) log = dummy, logn = 1;
+	log[0] = 0;
+	if (bits != 8 && bits != 4) {
+		seterr("bits is 8 or 4");
+		return nullptr;
+	}
+	if (gptq && (!calib || ncalib < 1)) {
+		seterr("GPTQ needs calibration rows (input rows in the tgc batch format)");
+		return nullptr;
+	}
+	char err[512];
+	tgm_module *m = tgm_read(tgir, len, err, sizeof err);
+	if (!m) {
+		seterr("%s", err);
+		return nullptr;
+	}
+	tgq_param *q = nullptr;
+	int n = m->nupd ? 0 : tgq_eligible(m, min_size, &q);
+	char *out = nullptr;
+	std::vector<float> ref, got;
+	if (m->nupd) {
+		seterr("model %s updates its state: it stays on the CPU path", m->name);
+	} else if (n <= 0) {
+		seterr("%s: no param is eligible (rank-2, >= %d elements, used only as a matmul operand)", m->name, min_size);
+	} else {
+		bool ok = true;
+		if (gptq) { /* Hessians for every param (max_k <= 0), or as the reference for K <= max_k */
+			std::vector<tgq_param> cap;
+			std::vector<int> idx;
+			for (int i = 0; i < n; i++)
+				if (max_k <= 0 || q[i].K <= max_k) cap.push_back(q[i]), idx.push_back(i);
+			ok = cap.empty() || calibrate(tgir, len, cap.data(), (int)cap.size(), calib, ncalib, ref) == 0;
+			for (size_t j = 0; j < idx.size(); j++) q[idx[j]].H = cap[j].H, q[idx[j]].nsamp = cap[j].nsamp;
+		} else if (calib && ncalib > 0) {
+			ok = run_outputs(tgir, len, calib, ncalib, ref) == 0;
+		}
+		if (ok) {
+			snprintf(log, logn, "quantize: %d param(s) of %s\n", n, m->name);
+			const int threads = (int)std::max(1u, std::min(64u, std::thread::hardware_concurrency()));
+			for (int i = 0; ok && i < n; i++) ok = tgq_quantize_param(m, &q[i], bits, gptq, threads, log, logn) == 0;
+			if (!ok) seterr("out of memory quantizing");
+		}
+		if (ok && !(out = tgm_write(m))) seterr("out of memory writing the model");
+		if (out && bytes) { /* the params' bytes before and after (src/quant.c:352-360) */
+			bytes[0] = bytes[1] = 0;
+			for (int v = 0; v < m->nval; v++) {
+				const tgm_value *x = &m->val[v];
+				if (x->kind != TGM_PARAM) continue;
+				bytes[0] += 4 * x->n;
+				bytes[1] += x->qbits ? (x->qbits == 8 ? x->n : (x->n + 1) / 2) + 4L * x->sh.dim[x->qaxis] : 4 * x->n;
+			}
+		}
+		if (out && !ref.empty() && run_outputs(out, strlen(out), calib, ncalib, got) == 0 && got.size() == ref.size()) {
+			double num = 0, den = 0, mx = 0; /* what quantization does to the outputs on the calibration rows */
+			for (size_t i = 0; i < ref.size(); i++) {
+				double d = (double)got[i] - ref[i];
+				num += d * d;
+				den += (double)ref[i] * ref[i];
+				mx = std::max(mx, std::fabs(d));
+			}
+			size_t o = strlen(log);
+			snprintf(log + o, logn - o, "quantize: on %ld calibration row(s): relative output error %.5f, max |output change| %.5f\n", ncalib,
+				 den > 0 ? std::sqrt(num / den) : 0.0, mx);
+		}
+	}
+	for (int i = 0; i < n; i++) free(q[i].H);
+	free(q);
+	tgm_free(m);
+	return out;
 }
 
 void tg_hip_free(tg_hip_prog *p) { destroy(p); }

@@ -292,8 +292,19 @@ typedef struct {
 	int nthink;
 	int rows;
 	int fixed;
+	/* calibration capture (f32 programs): an RP_MM with p[8] = c + 1 appends
+	 * its left operand's rows (p[9] = 1) or right operand's columns (p[9] = 0)
+	 * to capture c: row r's samples at cap + cap_base[c] + (r cap_rows[c] +
+	 * count) cap_k[c], count in cap_count[c * rows + r] */
+	float *cap;
+	const long *cap_base;
+	const int *cap_k, *cap_rows;
+	int *cap_count;
 } rp_args;
 
 void tgk_rowprog(hipStream_t s, const rp_args *a);
+/* H[r][c] = sum over the rows in order, then each row's samples in order, of
+ * x_r x_c in f64 (the order of the reference's hook): capture c of a pass */
+void tgk_hessian(hipStream_t s, const float *cap, const int *count, long row_cap, int K, int rows, double *H);
 
 #endif

@@ -37,6 +37,10 @@
  *       the reference's connections (src/serve.c) on the device batch: see tgc_hip_serve.c
  *   tgc-hip ir MODEL.tg
  *       prints the canonical TGIR of a surface model (no device)
+ *   tgc-hip quantize MODEL [-o OUT.tgir] [--bits 8|4] [--method rtn|gptq] [--calib DATA] [--min-size N] [--max-k K]
+ *       `tgc quantize` with the calibration run and Hessians on the device;
+ *       --max-k (default 2048, the reference's limit) bounds the layer width
+ *       given a Hessian, 0 gives every layer one
  *   tgc-hip c MODEL [--fixed] [-o UNIT.hip] [--kernel NAME]
  *       writes the model's row program as a freestanding HIP unit (the
  *       device counterpart of `tgc c`, src/main.c:343-360; no device)
@@ -366,6 +370,74 @@ static int emit_unit(int argc, char **argv)
 	return ok ? 0 : die("cannot write the unit%s", "");
 }
 
+/* tgc-hip quantize: `tgc quantize` (src/quant.c:318-384) with the calibration
+ * run and the Hessians on the device (tg_hip_quantize_model) */
+#define QUSAGE "usage: tgc-hip quantize MODEL [-o OUT.tgir] [--bits 8|4] [--method rtn|gptq] [--calib DATA] [--min-size N] [--max-k K]%s"
+static int quantize(int argc, char **argv)
+{
+	const char *src = NULL, *opath = NULL, *calib = NULL, *method = "rtn";
+	int bits = 8, min_size = 256, max_k = 2048;
+	for (int i = 2; i < argc; i++) {
+		const char *a = argv[i];
+		const int v = i + 1 < argc;
+		if (!strcmp(a, "-o") && v) opath = argv[++i];
+		else if (!strcmp(a, "--bits") && v) bits = atoi(argv[++i]);
+		else if (!strcmp(a, "--method") && v) method = argv[++i];
+		else if (!strcmp(a, "--calib") && v) calib = argv[++i];
+		else if (!strcmp(a, "--min-size") && v) min_size = atoi(argv[++i]);
+		else if (!strcmp(a, "--max-k") && v) max_k = atoi(argv[++i]);
+		else if (!src && a[0] != '-') src = a;
+		else return die(QUSAGE, "");
+	}
+	if (!src) return die(QUSAGE, "");
+	if (bits != 8 && bits != 4) return die("--bits is 8 or 4%s", "");
+	const int gptq = !strcmp(method, "gptq");
+	if (!gptq && strcmp(method, "rtn")) return die("--method is rtn or gptq%s", "");
+	if (gptq && !calib) return die("--method gptq needs --calib DATA (input rows in the tgc batch format)%s", "");
+	size_t mlen;
+	char lerr[1024];
+	char *text = load_model(src, &mlen, lerr, sizeof lerr);
+	if (!text) return die("%s", lerr);
+	float *rows = NULL;
+	long nrows = 0;
+	if (calib) { /* the rows' width comes from the model on the device */
+		if (tg_hip_init(0)) return die("%s", tg_hip_error());
+		tg_hip_prog *p = tg_hip_load(text, mlen, 0, 1);
+		if (!p) return die("%s", tg_hip_error());
+		int per, nout, nthink;
+		tg_hip_info(p, &per, &nout, &nthink);
+		tg_hip_free(p);
+		rows = load_rows(calib, per, &nrows, lerr, sizeof lerr, 0);
+		if (!rows) return die("%s", lerr);
+		if (!nrows) return die("%s: no calibration rows", calib);
+	}
+	static char log[1 << 16];
+	long bytes[2];
+	char *out = tg_hip_quantize_model(text, mlen, bits, gptq, rows, nrows, min_size, max_k, bytes, log, sizeof log);
+	free(text);
+	free(rows);
+	fputs(log, stderr);
+	if (!out) return die("%s", tg_hip_error());
+	char dflt[1024];
+	if (!opath) {
+		const char *dot = strrchr(src, '.');
+		snprintf(dflt, sizeof dflt, "%.*s.q%d.tgir", (int)(dot ? dot - src : (long)strlen(src)), src, bits);
+		opath = dflt;
+	}
+	FILE *f = fopen(opath, "w");
+	if (!f) {
+		tg_hip_str_free(out);
+		return die("cannot write '%s'", opath);
+	}
+	const size_t n = strlen(out);
+	const int ok = fwrite(out, 1, n, f) == n;
+	tg_hip_str_free(out);
+	if (fclose(f) || !ok) return die("write failed '%s'", opath);
+	fprintf(stderr, "quantize: params %ld -> %ld bytes (%.1fx smaller); wrote %s\n", bytes[0], bytes[1],
+		bytes[1] ? (double)bytes[0] / bytes[1] : 0.0, opath);
+	return 0;
+}
+
 #define USAGE "usage: tgc-hip batch MODEL DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v] [--log FILE]%s"
 
 int main(int argc, char **argv)
@@ -383,6 +455,7 @@ int main(int argc, char **argv)
 	}
 	if (argc >= 2 && !strcmp(argv[1], "c")) return emit_unit(argc, argv);
 	if (argc >= 2 && !strcmp(argv[1], "ir")) return print_ir(argc, argv);
+	if (argc >= 2 && !strcmp(argv[1], "quantize")) return quantize(argc, argv);
 	if (argc >= 2 && !strcmp(argv[1], "stream")) return stream_main(argc, argv);
 	if (argc >= 2 && !strcmp(argv[1], "serve")) return serve_main(argc, argv);
 	if (argc < 2 || strcmp(argv[1], "batch")) return die(USAGE, "");

@@ -78,6 +78,9 @@ tgm_module *tgm_read(const char *text, size_t len, char *err, size_t errn);
 void tgm_free(tgm_module *m);
 long tgm_numel(const tgm_shape *s);
 int tgm_code(const tgm_value *v, long i); /* code i (int4 sign-extended) */
+/* The canonical TGIR text of a module (tgir_write.c), malloc'd; NULL for a
+ * module with state updates (not recorded by the reader) or out of memory. */
+char *tgm_write(const tgm_module *m);
 const char *tgm_op_name(int op);
 
 #ifdef __cplusplus

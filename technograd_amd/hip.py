@@ -56,6 +56,9 @@ def lib():
         L.tg_hip_str_free.argtypes = [vp]
         L.tg_hip_surface_to_tgir.restype = vp
         L.tg_hip_surface_to_tgir.argtypes = [ctypes.c_char_p]
+        L.tg_hip_quantize_model.restype = vp
+        L.tg_hip_quantize_model.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ip, ip, vp, ctypes.c_long, ip, ip, vp, vp,
+                                            ctypes.c_size_t]
         L.tg_hip_error.restype = ctypes.c_char_p
         L.tg_hip_stats.argtypes = [vp, ctypes.POINTER(Stats)]
         L.tg_hip_reset_stats.argtypes = [vp]
@@ -213,6 +216,33 @@ def surface_to_tgir(path):
         raise RuntimeError(lib().tg_hip_error().decode())
     try:
         return ctypes.string_at(p).decode()
+    finally:
+        lib().tg_hip_str_free(p)
+
+
+def quantize_model(tgir, bits=8, method="rtn", calib=None, min_size=256, max_k=2048):
+    """`tgc quantize` (tg_hip_quantize_model): the model's eligible params
+    quantized to int`bits`. method "gptq" needs calib, an [n, per] f32 array
+    of calibration rows, and a GPU (the calibration run and the Hessians are
+    on the device); RTN without calib runs on the host. max_k = 2048 is the
+    reference's Hessian width limit, 0 none. Returns (TGIR text, report
+    lines, (param bytes before, after))."""
+    if method not in ("rtn", "gptq"):
+        raise ValueError("method is rtn or gptq")
+    t = tgir.encode() if isinstance(tgir, str) else bytes(tgir)
+    rows, n = None, 0
+    if calib is not None:
+        rows = np.ascontiguousarray(calib, dtype=np.float32)
+        n = rows.shape[0]
+        init()
+    log = ctypes.create_string_buffer(1 << 16)
+    nbytes = (ctypes.c_long * 2)()
+    p = lib().tg_hip_quantize_model(t, len(t), bits, method == "gptq", None if rows is None else _p(rows), n, min_size,
+                                    max_k, nbytes, log, len(log))
+    if not p:
+        raise RuntimeError(lib().tg_hip_error().decode())
+    try:
+        return ctypes.string_at(p).decode(), log.value.decode(), (nbytes[0], nbytes[1])
     finally:
         lib().tg_hip_str_free(p)
 

@@ -1,0 +1,109 @@
+"""`tgc quantize --method gptq` with the calibration run on the device
+(tg_hip_quantize_model): the f32 model runs over the calibration rows in one
+device pass that captures every eligible weight's other matmul operand as
+the reference's hook takes it (src/quant.c:92-117), the device sums each
+Hessian H = sum x x^T in the hook's order (exact f64 products), and the host
+runs GPTQ (src/quant.c:258-316). The goldens qmlp_q4g and latent_q4g are
+the reference's own GPTQ outputs on the calibration rows stored beside them
+(tests/golden/make_golden.py), so the quantized model must come back byte
+for byte. A layer wider than the reference's 2048-input limit checks the
+Hessian path at width through what GPTQ is for: a lower output error on the
+calibration rows than RTN's."""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from technograd_amd import hip
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+CLI = os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
+
+# golden: (f32 source, min-size)
+GPTQ = {"qmlp_q4g": ("qmlp_f32", 256), "latent_q4g": ("latent_f32", 1)}
+
+
+def text(name):
+    with open(os.path.join(GOLDEN, name + ".tgir")) as fh:
+        return fh.read()
+
+
+def output_error(log):
+    m = re.search(r"relative output error ([0-9.]+)", log)
+    assert m, log
+    return float(m.group(1))
+
+
+@pytest.mark.parametrize("name", sorted(GPTQ))
+def test_gptq_byte_identical(name):
+    src, min_size = GPTQ[name]
+    calib = np.load(os.path.join(GOLDEN, name + ".npz"))["calib"]
+    print("case gptq", name, calib.shape, flush=True)
+    q, log, _ = hip.quantize_model(text(src), bits=4, method="gptq", calib=calib, min_size=min_size)
+    assert q == text(name)
+    assert ", gptq, relative weight error " in log
+    assert "on %d calibration row(s)" % len(calib) in log
+
+
+@pytest.mark.parametrize("name", sorted(GPTQ))
+def test_cli_gptq(tmp_path, name):
+    """the reference's command line with --calib text rows (%.9g, as the
+    goldens' calibration files were written)"""
+    src, min_size = GPTQ[name]
+    calib = np.load(os.path.join(GOLDEN, name + ".npz"))["calib"]
+    model, cpath, out = tmp_path / (src + ".tgir"), tmp_path / "calib.csv", tmp_path / "q.tgir"
+    model.write_text(text(src))
+    with open(cpath, "w") as fh:
+        for r in calib:
+            fh.write(",".join("%.9g" % v for v in r) + "\n")
+    print("case cli gptq", name, flush=True)
+    r = subprocess.run([CLI, "quantize", str(model), "-o", str(out), "--bits", "4", "--method", "gptq", "--calib", str(cpath),
+                        "--min-size", str(min_size)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert out.read_text() == text(name)
+    assert r.stderr.splitlines()[-1].endswith("; wrote " + str(out))
+
+
+def test_rtn_with_calibration_reports_output_error():
+    """RTN with calibration rows quantizes as without them and reports what
+    quantization does to the outputs (src/quant.c:343-371)"""
+    calib = np.load(os.path.join(GOLDEN, "qmlp_q4g.npz"))["calib"]
+    q, log, _ = hip.quantize_model(text("qmlp_f32"), bits=4, calib=calib)
+    assert q == text("qmlp_q4")
+    assert 0 < output_error(log) < 0.5
+
+
+WIDE = """model wide
+param W1 : f32[96, 2560] = rand(5, 0.03)
+param W2 : f32[96, 16] = rand(6, 0.2)
+
+def forward(x: f32[2560]) -> f32[16]:
+    h = tanh(W1 @ x)
+    return h @ W2
+"""
+
+
+def test_gptq_wider_than_the_reference(tmp_path):
+    """W1 has 2560 inputs: the reference gives it no Hessian (rtn); with
+    max_k = 0 it gets one on the device, and GPTQ's output error on the
+    calibration rows is below RTN's."""
+    path = tmp_path / "wide.tg"
+    path.write_text(WIDE)
+    tgir = hip.surface_to_tgir(str(path))
+    calib = np.random.default_rng(3).uniform(-1, 1, size=(384, 2560)).astype(np.float32)
+    print("case wide rtn", flush=True)
+    q_rtn, log_rtn, _ = hip.quantize_model(tgir, bits=4, calib=calib, min_size=1)
+    print("case wide gptq max_k 2048", flush=True)
+    q_ref, log_ref, _ = hip.quantize_model(tgir, bits=4, method="gptq", calib=calib, min_size=1)
+    assert re.search(r"W1 .*, rtn, ", log_ref) and re.search(r"W2 .*, gptq, ", log_ref)
+    w1 = lambda t: t[t.index("(param W1"):t.index("(param W2")]  # noqa: E731
+    assert w1(q_ref) == w1(q_rtn)
+    print("case wide gptq max_k 0", flush=True)
+    q_all, log_all, _ = hip.quantize_model(tgir, bits=4, method="gptq", calib=calib, min_size=1, max_k=0)
+    assert re.search(r"W1 .*, gptq, ", log_all) and re.search(r"W2 .*, gptq, ", log_all)
+    assert output_error(log_all) < 0.9 * output_error(log_rtn), (log_all, log_rtn)
