@@ -59,6 +59,8 @@ typedef struct {
 	long arena_bytes;    /* device arena of the program at its row capacity */
 	int rowprog_jit;     /* row program: 1 when compiled for the model (hipRTC), 0 when interpreted */
 	long rowprog_hoisted; /* instructions the compiled row program runs once in front of their think loop */
+	int epilogue_ins;    /* layer program: instructions after quantized products that their GEMMs apply in
+	                        their epilogues (elementwise chains, softmax / rmsnorm over the channels) */
 } tg_hip_stats_t;
 
 /* Select the device (ordinal) for subsequent calls; 0 on success. */

@@ -9,6 +9,7 @@
 // ROCm device library, so only they differ from glibc (by a few ulp); the
 // log1pf of softplus is this backend's own (tg_devmath.h), correctly rounded.
 #include "tg_devmath.h"
+#include "tg_ewop.h"
 #include "tg_kern.h"
 #include "tgm.h"
 
@@ -20,17 +21,7 @@ constexpr int TPB = 256;
 
 inline unsigned blocks_for(long n) { return (unsigned)((n + TPB - 1) / TPB); }
 
-__device__ inline float bop(int op, float x, float y)
-{
-	switch (op) {
-	case TGK_ADD: return x + y;
-	case TGK_SUB: return x - y;
-	case TGK_MUL: return x * y;
-	case TGK_DIV: return x / y;
-	case TGK_MAX: return x > y ? x : y;
-	default: return x < y ? x : y;
-	}
-}
+__device__ inline float bop(int op, float x, float y) { return tg_bop(op, x, y); }
 
 // operand index of output element i (modes of tgk_binary)
 __device__ inline int bidx(int mode, int i, const int *map, int per)
@@ -51,25 +42,7 @@ __global__ void binary_k(int op, float *o, long ors, int n, tgk_opd a, int am, c
 }
 
 // tg_rt.h:40-75
-__device__ inline float uop(int op, float x)
-{
-	switch (op) {
-	case TGM_NEG: return -x;
-	case TGM_TANH: return tanhf(x);
-	case TGM_RELU: return x > 0.0f ? x : 0.0f;
-	case TGM_SIGMOID: return 1.0f / (1.0f + expf(-x));
-	case TGM_EXP: return expf(x);
-	case TGM_SQRT: return sqrtf(x);
-	case TGM_GELU: return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
-	case TGM_SILU: return x / (1.0f + expf(-x));
-	case TGM_SOFTPLUS: return (x > 0.0f ? x : 0.0f) + tg_log1p_unit(expf(-fabsf(x)));
-	case TGM_LOG: return logf(x);
-	case TGM_SIN: return sinf(x);
-	case TGM_COS: return cosf(x);
-	case TGM_FLOOR: return floorf(x);
-	default: return x > 0.0f ? 1.0f : 0.0f; // step
-	}
-}
+__device__ inline float uop(int op, float x) { return tg_uop(op, x); }
 
 __global__ void unary_k(int op, float *o, long ors, tgk_opd a, int n, long total)
 {

@@ -31,6 +31,7 @@
 //            two masks per 4 bytes; the +8 bias is removed with the row's sum
 //            of q: sum_k t q = sum_k code q + 8 sum_k q.
 // Weights are repacked once at load (channels padded to 256, K to 64).
+#include "tg_ewop.h"
 #include "tg_kern.h"
 #include "tg_qdigits.h"
 
@@ -382,26 +383,102 @@ __device__ inline float *out_at(const tgk_qgemm_args &a, int r, int jj, int c)
 	return o.p + (long)r * o.orr + (long)jj * o.oj;
 }
 
-// the output as the instruction after the product would compute it
-__device__ inline float act(const tgk_qgemm_args &a, float v) { return a.act == TGK_ACT_TANH ? tanhf(v) : v; }
+// a unary instruction of an epilogue chain: the operations the layer builder
+// lets into a chain (tg_hip.cpp: epi_unary), each as the elementwise kernels
+// compute it (tg_uop)
+__device__ inline float epi_uop(int op, float v)
+{
+	switch (op) {
+	case TGM_NEG: return tg_uop(TGM_NEG, v);
+	case TGM_TANH: return tg_uop(TGM_TANH, v);
+	case TGM_RELU: return tg_uop(TGM_RELU, v);
+	case TGM_SIGMOID: return tg_uop(TGM_SIGMOID, v);
+	case TGM_EXP: return tg_uop(TGM_EXP, v);
+	case TGM_GELU: return tg_uop(TGM_GELU, v);
+	case TGM_SILU: return tg_uop(TGM_SILU, v);
+	default: return tg_uop(TGM_STEP, v);
+	}
+}
+
+// output (batch row r, inner row jj, channel c) with value v (the product)
+// after the epilogue chain: the values the instructions after the product
+// would compute from it, one after another
+__device__ inline float finish(const tgk_qgemm_args &a, int r, int jj, int c, float v)
+{
+	for (int e = 0; e < a.nepi; e++) {
+		const tgk_epi &E = a.epi[e];
+		if (E.kind == TGK_EW_UN) {
+			v = epi_uop(E.op, v);
+			continue;
+		}
+		const float *p = E.x + (long)r * E.xr;
+		const float x = E.mode == 0 ? p[(long)jj * a.oj + (long)c * a.oc] : E.mode == 1 ? p[0] : p[c];
+		v = E.kind == TGK_EW_BIN ? tg_bop(E.op, v, x) : tg_bop(E.op, x, v);
+	}
+	return v;
+}
+
+// the reference's sequential loop for output (m, c) (runtime/tg_rt.h:132-151)
+__device__ inline float ref_loop(const tgk_qgemm_args &a, const tgk_qweight &w, int m, int c)
+{
+	const float *x = xrow(a, m);
+	float t = 0.0f;
+	for (int k = 0; k < w.K; k++) t += (float)code_orig(w, c, k) * x[k * a.xk];
+	return t;
+}
+
+// The reference's sums of ref_loop for line m and channels c = cb + lane +
+// 64 q (q < NQ), a whole wave on one line: the line's inputs have one
+// address for every lane, and the codes of U inputs are loaded before their
+// multiplies and adds, which keep each sum's order. Channels at or beyond C
+// read channel C - 1 and are not to be used.
+template <int NQ, int U = 16>
+__device__ inline void ref_line(const tgk_qgemm_args &a, const tgk_qweight &w, int m, int cb, int lane, float (&t)[NQ])
+{
+	const float *x = xrow(a, m);
+	int c[NQ];
+	for (int q = 0; q < NQ; q++) {
+		const int cc = cb + lane + 64 * q;
+		c[q] = cc < w.C ? cc : w.C - 1;
+		t[q] = 0.0f;
+	}
+	const int K = w.K;
+	int k = 0;
+	for (; k + U <= K; k += U) {
+		float xv[U];
+		int cd[NQ][U];
+		for (int u = 0; u < U; u++) xv[u] = x[(long)(k + u) * a.xk];
+		for (int q = 0; q < NQ; q++)
+			for (int u = 0; u < U; u++) cd[q][u] = code_orig(w, c[q], k + u);
+		for (int u = 0; u < U; u++)
+			for (int q = 0; q < NQ; q++) t[q] += (float)cd[q][u] * xv[u];
+	}
+	for (; k < K; k++) {
+		const float xk = x[(long)k * a.xk];
+		for (int q = 0; q < NQ; q++) t[q] += (float)code_orig(w, c[q], k) * xk;
+	}
+}
 
 // output (m, c) from tot = sum_k t[c][k] q[m][k], given row m's exponent, special flag and sum of q
+// ACT: TGM_TANH when a tanh that only reads the product is applied here (the
+// chain [tanh] of the large-batch kernel, inline), else 0
+template <int ACT = 0>
+__device__ inline float act_out(float v) { return ACT == TGM_TANH ? tg_uop(TGM_TANH, v) : v; }
+
+template <int ACT = 0>
 __device__ inline void epilogue_with(const tgk_qgemm_args &a, const tgk_qweight &w, int m, int c, long long tot, int E, int special,
 				     long long qsum)
 {
 	if (m >= a.M || c >= w.C) return;
 	float acc32;
-	if (special) { // the reference's sequential loop (runtime/tg_rt.h:132-151)
-		const float *x = xrow(a, m);
-		float t = 0.0f;
-		for (int k = 0; k < w.K; k++) t += (float)code_orig(w, c, k) * x[k * a.xk];
-		acc32 = t;
+	if (special) { // the reference's sequential loop
+		acc32 = ref_loop(a, w, m, c);
 	} else {
 		if (w.bits == 4) tot -= 8 * qsum;
 		acc32 = (float)ldexp((double)tot, E - 23);
 	}
 	int r = m / a.ni, jj = m - r * a.ni;
-	*out_at(a, r, jj, c) = act(a, w.scale[c] * acc32);
+	*out_at(a, r, jj, c) = act_out<ACT>(w.scale[c] * acc32);
 }
 
 __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot)
@@ -445,7 +522,7 @@ __device__ inline TileRows<NB> tile_rows(const tgk_qgemm_args &a, const tgk_qwei
 // HOIST: take all 16 rows' exponents and sums of q from their lanes before the
 // first store (the shuffles then wait once, not once per row; 48 more live
 // registers, for kernels that have them free at the epilogue).
-template <int NB, bool HOIST, class Tot, class TotD>
+template <int NB, bool HOIST, int ACT = 0, class Tot, class TotD>
 __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int mbase, int cbase, int lane,
 				  const TileRows<NB> &t, Tot tot, TotD totd)
 {
@@ -463,9 +540,29 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 		}
 	auto row_e = [&](int v, int rv) { if constexpr (HOIST) return Ev[v]; else return __shfl(Er, rv); };
 	auto row_q = [&](int v, int rv) { if constexpr (HOIST) return Qv[v]; else return __shfl(Qr, rv); };
-	if (__any(spr)) {
-		for (int j = 0; j < NB; j++)
-			for (int v = 0; v < 16; v++) epilogue(a, w, s, mbase + 8 * (v >> 2) + 4 * h + (v & 3), cbase + j * 32 + r32, tot(j, v));
+	if (__any(spr)) { // rows of the reference's loop: the others as usual, each special row by the whole wave
+		for (int v = 0; v < 16; v++) {
+			const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
+			const int E = __shfl(Er, rv), sp = __shfl(spr, rv);
+			const long long Q = __shfl(Qr, rv);
+			if (!sp)
+				for (int j = 0; j < NB; j++) epilogue_with<ACT>(a, w, m, cbase + j * 32 + r32, tot(j, v), E, 0, Q);
+		}
+		unsigned long long sm = __ballot(spr) & 0xffffffffull; // lane r (r < 32): row mbase + r
+		while (sm) {
+			const int rv = __builtin_ctzll(sm);
+			sm &= sm - 1;
+			const int m = mbase + rv;
+			if (m >= a.M) continue;
+			constexpr int NQ = (NB * 32 + 63) / 64;
+			float t[NQ];
+			ref_line<NQ, 4>(a, w, m, cbase, lane, t); // few registers: the accumulators may still be live
+			const int r = m / a.ni, jj = m - r * a.ni;
+			for (int q = 0; q < NQ; q++) {
+				const int c = cbase + lane + 64 * q;
+				if (c < cbase + NB * 32 && c < w.C) *out_at(a, r, jj, c) = act_out<ACT>(w.scale[c] * t[q]);
+			}
+		}
 		return;
 	}
 	if (a.nseg > 1) { // a merged GEMM: each column's own output
@@ -483,7 +580,7 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 			if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
 			for (int j = 0; j < NB; j++) {
 				if (cbase + j * 32 + r32 >= w.C) continue;
-				oc[j].p[(long)r * oc[j].orr + (long)jj * oc[j].oj] = act(a, sc[j] * (float)ldexp(totd(j, v) - q8, E - 23));
+				oc[j].p[(long)r * oc[j].orr + (long)jj * oc[j].oj] = sc[j] * (float)ldexp(totd(j, v) - q8, E - 23); // no chain
 			}
 		}
 		return;
@@ -501,7 +598,7 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 		float *orow = a.o + (long)r * a.orr + (long)jj * a.oj;
 		for (int j = 0; j < NB; j++) {
 			if (cbase + j * 32 + r32 >= w.C) continue;
-			orow[coff[j]] = act(a, sc[j] * (float)ldexp(totd(j, v) - q8, E - 23));
+			orow[coff[j]] = act_out<ACT>(sc[j] * (float)ldexp(totd(j, v) - q8, E - 23));
 		}
 	}
 }
@@ -525,6 +622,158 @@ __device__ inline void copy_to_lds(const uint8_t *sbase, unsigned voff, unsigned
 	asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 
+// The epilogue of qgemm_k<BITS, 1> (a chain, and the row op when the tile
+// holds whole lines): the tile's products go to LDS first (the ring's space,
+// free after the K loop), each wave its own 32 x 128 block from its
+// accumulators (rows of the reference's loop are left for the second pass),
+// lines rowstr(BN) floats apart (odd: one thread per line walks distinct
+// banks). Then all 512 threads take the tile line by line, a wave 64
+// channels at a time: the reference's loop for special rows, the chain
+// (finish), and either the store or, with the row op, the line ops of
+// rowop_lds_k (kern_layer.hip) in the reference's order: the sums one
+// thread per line in index order, the max, the exponentials, the division
+// and the scaling spread over every thread. The chain's code appears once
+// (a loop, not unrolled per output), which keeps the kernel small.
+constexpr int rowstr(int C) { return C | 1; }
+constexpr int EPI_LDS = BM * rowstr(BN) * 4 + BM * 4; // line values and one scalar per line
+
+template <class TotD>
+__device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m0, int c0, int wm, int g, int lane,
+				int wave, int tid, bool row, float *L, TotD totd)
+{
+	constexpr int STR = rowstr(BN);
+	const int nl = a.M - m0 < BM ? a.M - m0 : BM, cw = w.C - c0 < BN ? w.C - c0 : BN; // the tile's lines and channels
+	float *lv = L + BM * STR; // one scalar per line
+	wait_vm<0>();
+	__syncthreads(); // every wave is past its last read of the ring
+	{
+		const int mbase = m0 + wm * 32, r32 = lane & 31, h = lane >> 5;
+		const TileRows<4> t = tile_rows<4>(a, w, s, mbase, c0 + g * 128, lane);
+		for (int v = 0; v < 16; v++) {
+			const int rv = 8 * (v >> 2) + 4 * h + (v & 3);
+			const int E = __shfl(t.Er, rv);
+			const double q8 = 8.0 * (double)__shfl(t.Qr, rv); // 0 for int8 weights
+			for (int j = 0; j < 4; j++)
+				L[(wm * 32 + rv) * STR + g * 128 + j * 32 + r32] = t.sc[j] * (float)ldexp(totd(j, v) - q8, E - 23);
+		}
+	}
+	// a wave takes lines wave, wave + 8, ... (16 of them), 64 channels at a time
+	const int spl = lane < 16 && wave + 8 * lane < nl ? s.special[m0 + wave + 8 * lane] : 0;
+	__syncthreads();
+	if (__any(spl)) // lines of the reference's loop: their products, a wave per line
+		for (int i = 0; i < 16; i++)
+			if (__shfl(spl, i)) {
+				const int l = wave + 8 * i;
+				float t[BN / 64];
+				ref_line<BN / 64>(a, w, m0 + l, c0, lane, t);
+				for (int q = 0; q < BN / 64; q++)
+					if (lane + 64 * q < cw) L[l * STR + lane + 64 * q] = w.scale[c0 + lane + 64 * q] * t[q];
+			}
+	// the chain, four lines at a time: for each instruction, every operand
+	// load of the four lines first, then the arithmetic (the operation chosen
+	// once per instruction, not per element); results back to LDS (no global
+	// store here, so no load waits for a store)
+	for (int i0 = 0; i0 < 16; i0 += 4) {
+		float v[16];
+		int rr[4], jr[4];
+		for (int il = 0; il < 4; il++) {
+			const int l = wave + 8 * (i0 + il), m = m0 + (l < nl ? l : 0);
+			rr[il] = m / a.ni;
+			jr[il] = m - rr[il] * a.ni;
+			for (int q = 0; q < 4; q++) {
+				const int c = lane + 64 * q;
+				v[il * 4 + q] = l < nl && c < cw ? L[l * STR + c] : 0.0f;
+			}
+		}
+		for (int e = 0; e < a.nepi; e++) {
+			const int kind = a.epi[e].kind, op = a.epi[e].op;
+			if (kind == TGK_EW_UN) {
+				switch (op) {
+#define EPU(K) \
+	case K: \
+		for (int u = 0; u < 16; u++) v[u] = tg_uop(K, v[u]); \
+		break;
+					EPU(TGM_NEG) EPU(TGM_TANH) EPU(TGM_RELU) EPU(TGM_SIGMOID) EPU(TGM_EXP) EPU(TGM_GELU) EPU(TGM_SILU)
+					default: EPU(TGM_STEP)
+#undef EPU
+				}
+				continue;
+			}
+			const int mode = a.epi[e].mode;
+			const float *xp = a.epi[e].x;
+			const long xr = a.epi[e].xr;
+			float x[16];
+			for (int il = 0; il < 4; il++) {
+				const int l = wave + 8 * (i0 + il);
+				const float *p = xp + (long)rr[il] * xr;
+				for (int q = 0; q < 4; q++) {
+					const int c = lane + 64 * q, cc = c0 + (c < cw ? c : 0);
+					x[il * 4 + q] = l >= nl ? 0.0f : mode == 0 ? p[(long)jr[il] * a.oj + (long)cc * a.oc] : mode == 1 ? p[0] : p[cc];
+				}
+			}
+			const bool rev = kind == TGK_EW_BINR;
+			switch (op) {
+#define EPB(K) \
+	case K: \
+		for (int u = 0; u < 16; u++) v[u] = rev ? tg_bop(K, x[u], v[u]) : tg_bop(K, v[u], x[u]); \
+		break;
+				EPB(TGK_ADD) EPB(TGK_SUB) EPB(TGK_MUL) EPB(TGK_DIV) EPB(TGK_MAX)
+				default: EPB(TGK_MIN)
+#undef EPB
+			}
+		}
+		for (int il = 0; il < 4; il++) {
+			const int l = wave + 8 * (i0 + il);
+			for (int q = 0; q < 4; q++)
+				if (l < nl && lane + 64 * q < cw) L[l * STR + lane + 64 * q] = v[il * 4 + q];
+		}
+	}
+	__syncthreads();
+	// row op (whole lines in the tile: c0 = 0, channel stride 1)
+	const int C = cw;
+	auto line_sum = [&](int l, bool sq) { // in index order from 0.0f
+		const float *y = L + l * STR;
+		float sum = 0.0f;
+		int i = 0;
+		for (; i + 8 <= C; i += 8) {
+			float z[8];
+			for (int u = 0; u < 8; u++) z[u] = y[i + u];
+			for (int u = 0; u < 8; u++) sum += sq ? z[u] * z[u] : z[u];
+		}
+		for (; i < C; i++) sum += sq ? y[i] * y[i] : y[i];
+		return sum;
+	};
+	if (row && a.rowop == TGM_SOFTMAX) {
+		if (tid < nl) { // x[0] when it is nan, else the largest of x[0] and the non-nan x[i]
+			const float *y = L + tid * STR;
+			float mx = -INFINITY;
+			for (int i = 1; i < C; i++) mx = fmaxf(mx, y[i]);
+			lv[tid] = isnan(y[0]) ? y[0] : fmaxf(y[0], mx);
+		}
+		__syncthreads();
+		for (int l = wave; l < nl; l += 8)
+			for (int c = lane; c < C; c += 64) L[l * STR + c] = expf(L[l * STR + c] - lv[l]);
+		__syncthreads();
+		if (tid < nl) lv[tid] = line_sum(tid, false);
+		__syncthreads();
+		for (int l = wave; l < nl; l += 8)
+			for (int c = lane; c < C; c += 64) L[l * STR + c] = L[l * STR + c] / lv[l];
+		__syncthreads();
+	} else if (row) {
+		if (tid < nl) lv[tid] = 1.0f / sqrtf(line_sum(tid, true) / (float)C + 1e-6f);
+		__syncthreads();
+		for (int l = wave; l < nl; l += 8)
+			for (int c = lane; c < C; c += 64) L[l * STR + c] = L[l * STR + c] * lv[l];
+		__syncthreads();
+	}
+	// the stores, after every load
+	for (int l = wave; l < nl; l += 8) {
+		const int m = m0 + l, r = m / a.ni, jj = m - r * a.ni;
+		float *o = a.o + (long)r * a.orr + (long)jj * a.oj + (long)c0 * a.oc;
+		for (int c = lane; c < cw; c += 64) o[(long)c * a.oc] = L[l * STR + c];
+	}
+}
+
 // Large batches. 512 threads = 8 waves; the workgroup computes a 128 x 256
 // tile (rows x channels): wave w (group g = w / 4, rows wm = w % 4) a 32 x 128
 // block as four 32 x 32 blocks of v_mfma_i32_32x32x32_i8 for each of the three
@@ -545,15 +794,22 @@ __device__ inline void copy_to_lds(const uint8_t *sbase, unsigned voff, unsigned
 // kt - 1, whose last reader (group 1) finished in slot 2 kt - 1; a wave waits
 // for its copies of stage kt + 1 at the end of its reading slot of stage kt,
 // before the barrier that precedes the first read of stage kt + 1.
-template <int BITS>
-__global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int gx, int gy)
+//
+// EPI 1: the epilogue applies the chain (a.epi), and the row op when `row`
+// (the tile holds whole lines: one channel tile, channel stride 1), through
+// LDS (staged_epilogue). EPI 2: the chain is a lone tanh, applied as each
+// output is stored (the stores' code then stays as small as without it).
+
+template <int BITS, int EPI = 0>
+__global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int gx, int gy, int row)
 {
 	constexpr int S = 4;                          // ring stages (128 or 160 KiB)
 	constexpr int AST = 24 * 1024;                // 4 row blocks x 2 substeps x 3 digits x 1 KiB
 	constexpr int BST = BITS == 4 ? 8192 : 16384; // 8 channel blocks x 2 substeps x 512 B or 1 KiB
 	constexpr int STG = AST + BST;
 	constexpr int GA = 6, GB = BST / 1024 / 4;    // copies per wave per stage: group 0, group 1
-	__shared__ __attribute__((aligned(1024))) uint8_t lds[S * STG];
+	constexpr int LDSB = EPI == 1 && EPI_LDS > S * STG ? (EPI_LDS + 1023) / 1024 * 1024 : S * STG;
+	__shared__ __attribute__((aligned(1024))) uint8_t lds[LDSB];
 	const int tid = threadIdx.x, lane = tid & 63;
 	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = wave >> 2, wm = wave & 3;
 	// XCD-aware tile order: workgroups are dealt to the 8 XCDs round robin, so
@@ -647,7 +903,12 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 		bar();
 	}
 	if (g == 0) bar(); // both groups pass the same number of barriers
-	store_tile<4, false>(
+	if constexpr (EPI == 1) {
+		staged_epilogue(a, w, s, m0, c0, wm, g, lane, wave, tid, row != 0, (float *)lds,
+				[&](int j, int v) { return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]); });
+		return;
+	}
+	store_tile<4, false, EPI == 2 ? TGM_TANH : 0>(
 		a, w, s, m0 + wm * 32, c0 + g * 128, lane, tile_rows<4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane),
 		[&](int j, int v) { return combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]); },
 		[&](int j, int v) { return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]); });
@@ -1081,17 +1342,26 @@ void launch_gemv(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
 }
 
 template <int BITS>
-void launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
+int launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 {
 	const tgk_qweight *w = a->w;
 	const int gx = w->Cp / BN, gy = Mp / BM;
 	const long rt = round_up(a->M, 32) / 32, cb = w->Cp / 32;
 	if ((long)gx * gy >= 128 && rt > 2) { // enough 128 x 256 tiles for the LDS kernel
-		qgemm_k<BITS><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy);
-		return;
+		if (a->nepi == 1 && a->epi[0].kind == TGK_EW_UN && a->epi[0].op == TGM_TANH && !a->rowop && a->nseg <= 1) {
+			qgemm_k<BITS, 2><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy, 0); // a lone tanh: inline in the stores
+			return TGK_DID_CHAIN;
+		}
+		if ((a->nepi || a->rowop) && a->nseg <= 1) { // the chain in the epilogue, and the row op when a tile holds whole lines
+			const int row = a->rowop && gx == 1 && a->oc == 1;
+			qgemm_k<BITS, 1><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy, row);
+			return TGK_DID_CHAIN | (row ? TGK_DID_ROWOP : 0);
+		}
+		qgemm_k<BITS><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy, 0);
+		return 0;
 	}
-	if (BITS == 4 && launch_gemv1<false>(st, a, s)) return; // one row
-	if (launch_small<BITS>(st, a, s)) return;               // at most 16 rows
+	if (BITS == 4 && launch_gemv1<false>(st, a, s)) return 0; // one row
+	if (launch_small<BITS>(st, a, s)) return 0;               // at most 16 rows
 	// up to 64 rows, or too few tiles: 32 x (32 NB) tiles, NB as large as
 	// still fills the device; W waves split K, about 16 32-input blocks each
 	// for the wider tiles and 8-32 for one-block-wide ones (measured: at one
@@ -1111,6 +1381,7 @@ void launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 		else if (kb >= 16) launch_gemv<BITS, 1, 2>(st, a, s);
 		else launch_gemv<BITS, 1, 1>(st, a, s);
 	}
+	return 0;
 }
 
 // The repacking of tgk_qweight_pack done on the device, from codes already in
@@ -1301,14 +1572,35 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 		digits_k<4><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
 }
 
-void tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
+int tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
 	const tgk_qweight *w = a->w;
-	if (!w || !w->w || !w->scale || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return;
+	if (!w || !w->w || !w->scale || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return 0;
 	int Mp = (int)round_up(a->M, BM);
 	Scratch s = carve(scratch, Mp, w->Kp);
-	if (w->bits == 8) launch_gemm<8>(st, a, s, Mp);
-	else launch_gemm<4>(st, a, s, Mp);
+	return w->bits == 8 ? launch_gemm<8>(st, a, s, Mp) : launch_gemm<4>(st, a, s, Mp);
+}
+
+namespace {
+
+// The chain over a product's output in place, for the kernels that write
+// the products alone: one thread per output
+__global__ __launch_bounds__(256) void chain_k(tgk_qgemm_args a, int C, long total)
+{
+	const long t = (long)blockIdx.x * 256 + threadIdx.x;
+	if (t >= total) return;
+	const int m = (int)(t / C), c = (int)(t - (long)m * C), r = m / a.ni, jj = m - r * a.ni;
+	float *o = a.o + (long)r * a.orr + (long)jj * a.oj + (long)c * a.oc;
+	*o = finish(a, r, jj, c, *o);
+}
+
+} // namespace
+
+void tgk_qgemm_chain(hipStream_t st, const tgk_qgemm_args *a)
+{
+	const long total = (long)a->M * a->w->C;
+	if (a->nepi <= 0 || total <= 0) return;
+	chain_k<<<(unsigned)((total + 255) / 256), 256, 0, st>>>(*a, a->w->C, total);
 }
 
 bool tgk_qgemm_fusable(const tgk_qgemm_args *a)
@@ -1318,25 +1610,22 @@ bool tgk_qgemm_fusable(const tgk_qgemm_args *a)
 	       (w->K & 15) == 0;
 }
 
-void tgk_qgemm_fused(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
+int tgk_qgemm_fused(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
 	const tgk_qweight *w = a->w;
-	if (!w || !w->w || !w->scale || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return;
+	if (!w || !w->w || !w->scale || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return 0;
 	if (!tgk_qgemm_fusable(a)) {
 		tgk_qgemm_digits(st, a, scratch);
-		tgk_qgemm_mfma(st, a, scratch);
-		return;
+		return tgk_qgemm_mfma(st, a, scratch);
 	}
 	const int Mp = (int)round_up(a->M, BM);
 	launch_gemv1<true>(st, a, carve(scratch, Mp, w->Kp));
+	return 0;
 }
 
-void tgk_qgemm(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
+int tgk_qgemm(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
-	if (tgk_qgemm_fusable(a)) {
-		tgk_qgemm_fused(st, a, scratch);
-		return;
-	}
+	if (tgk_qgemm_fusable(a)) return tgk_qgemm_fused(st, a, scratch);
 	tgk_qgemm_digits(st, a, scratch);
-	tgk_qgemm_mfma(st, a, scratch);
+	return tgk_qgemm_mfma(st, a, scratch);
 }

@@ -139,7 +139,15 @@ struct Step {
 	long ag = 0, ai = 0, ap = 0, bg = 0, bp = 0, bj = 0, og = 0, oi = 0, oj = 0;
 	long codes = 0, scale = 0; // offsets into the code / scale pools
 	// quantized GEMM
-	int qw = -1, ni = 1, act = TGK_ACT_NONE;
+	int qw = -1, ni = 1;
+	// quantized GEMM: the instructions after it applied in its epilogue (tgk_qgemm_args::epi, rowop;
+	// the row op's lines are p0 lines of p1 = C values per batch row)
+	struct Epi {
+		int kind = 0, op = 0, mode = 0;
+		Opnd x;
+	};
+	int nepi = 0, rowop = 0;
+	Epi epi[TGK_EPI_MAX];
 	long xr = 0, xj = 0, xk = 0, orr = 0, oc = 0, ojj = 0;
 	// row ops, transpose, take
 	int p0 = 0, p1 = 0, p2 = 0;
@@ -418,6 +426,7 @@ void place_arena(tg_hip_prog *p, const tgm_module *m)
 	for (long i = 0; i < (long)S.size(); i++) {
 		const Step &st = S[i];
 		for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 }) touch(*o, i);
+		for (int e = 0; e < st.nepi; e++) touch(st.epi[e].x, i);
 		if (st.kind == ST_EW) {
 			for (const EwStep::In &x : p->ews[(size_t)st.ew].in) touch(x.o, i);
 			for (const Opnd &x : p->ews[(size_t)st.ew].out) touch(x, i);
@@ -488,8 +497,10 @@ void place_arena(tg_hip_prog *p, const tgm_module *m)
 	auto fix = [&](Opnd &o) {
 		if (o.space == SP_ARENA) o.off = off[(int)o.off];
 	};
-	for (Step &st : S)
+	for (Step &st : S) {
 		for (Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 }) fix(*o);
+		for (int e = 0; e < st.nepi; e++) fix(st.epi[e].x);
+	}
 	for (EwStep &E : p->ews) {
 		for (EwStep::In &x : E.in) fix(x.o);
 		for (Opnd &x : E.out) fix(x);
@@ -584,9 +595,12 @@ void finish_ew(tg_hip_prog *p)
 {
 	std::vector<Opnd> used; // operands read or written by steps other than fused runs, plus the output
 	for (const Step &st : p->steps)
-		if (st.kind != ST_EW && st.kind != ST_NOP)
+		if (st.kind != ST_EW && st.kind != ST_NOP) {
 			for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 })
 				if (o->space == SP_ARENA || o->space == SP_OUT) used.push_back(*o);
+			for (int e = 0; e < st.nepi; e++) // a GEMM epilogue's operands
+				if (st.epi[e].x.space == SP_ARENA || st.epi[e].x.space == SP_OUT) used.push_back(st.epi[e].x);
+		}
 	for (const auto &g : p->qsegs)
 		for (const QSegOut &x : g) used.push_back(x.o);
 	for (const EwStep &E : p->ews)
@@ -1012,21 +1026,94 @@ int value_reads(const tgm_block *b, int v)
 	return n;
 }
 
+// unary instructions a GEMM epilogue chain may hold (kern_qgemm.hip: epi_uop)
+bool epi_unary(int op)
+{
+	return op == TGM_NEG || op == TGM_TANH || op == TGM_RELU || op == TGM_SIGMOID || op == TGM_EXP || op == TGM_GELU || op == TGM_SILU ||
+	       op == TGM_STEP;
+}
+
+bool same_shape(const tgm_shape &x, const tgm_shape &y)
+{
+	if (x.rank != y.rank) return false;
+	for (int i = 0; i < x.rank; i++)
+		if (x.dim[i] != y.dim[i]) return false;
+	return true;
+}
+
+// The instructions right after quantized product i of the top level that its
+// GEMM can apply in its epilogue: a chain in which each instruction reads
+// the previous one's result (read nowhere else, not the output, not a loop
+// value) and keeps its shape, with up to TGK_EPI_MAX unary or binary
+// instructions (the other operand of the output's shape, one value, or one
+// value per channel) and then optionally a softmax or rmsnorm over the
+// channels (C1's tanh, a bias, a residual add, C5's add then rmsnorm,
+// qmlp's bias then softmax). The GEMM then writes the chain's last value,
+// and the values are those of the instructions run apart, since the epilogue
+// computes each with the elementwise kernels' arithmetic. Returns the index
+// of the chain's last instruction (i: none).
+int epi_chain(LB &L, const tgm_block *b, int i, Step &st)
+{
+	const tgm_module *m = L.m;
+	const tgm_ins &in = b->v[i];
+	const int quant = matmul_quant(m, in);
+	const tgm_value &w = m->val[quant == 1 ? in.a[0] : in.a[1]];
+	const tgm_shape &osh = m->val[in.out].sh;
+	const int C = w.sh.dim[w.qaxis];
+	// channel stride 1: x @ W ([.., C]) or W @ x for a vector x ([C])
+	const bool chlast = osh.rank >= 1 && osh.dim[osh.rank - 1] == C && (quant == 2 || osh.rank == 1);
+	auto single = [&](int v) { return v != m->output && !L.loopw[(size_t)v] && value_reads(&m->top, v) == 1; };
+	int cur = in.out, j = i + 1;
+	st.nepi = 0;
+	st.rowop = 0;
+	while (j < b->len && single(cur)) {
+		const tgm_ins &nx = b->v[j];
+		if (st.nepi < TGK_EPI_MAX && epi_unary(nx.op) && nx.a[0] == cur) {
+			st.epi[st.nepi++] = Step::Epi{ TGK_EW_UN, nx.op, 0, Opnd{} };
+		} else if (st.nepi < TGK_EPI_MAX && nx.op >= TGM_ADD && nx.op <= TGM_MIN && (nx.a[0] == cur) != (nx.a[1] == cur) &&
+			   same_shape(m->val[nx.out].sh, osh)) {
+			const int other = nx.a[0] == cur ? nx.a[1] : nx.a[0];
+			const tgm_shape &xs = m->val[other].sh;
+			int mode = -1;
+			if (same_shape(xs, osh)) mode = 0;
+			else if (numel(xs) == 1) mode = 1;
+			else if (chlast && numel(xs) == C && xs.rank >= 1 && xs.dim[xs.rank - 1] == C) mode = 3;
+			if (mode < 0) break;
+			st.epi[st.nepi++] = Step::Epi{ nx.a[0] == cur ? TGK_EW_BIN : TGK_EW_BINR, nx.op - TGM_ADD, mode, value_opnd(L, other) };
+		} else if ((nx.op == TGM_RMSNORM || nx.op == TGM_SOFTMAX) && nx.a[0] == cur && chlast) {
+			st.rowop = nx.op;
+			st.p1 = C;
+			st.p0 = (int)(numel(osh) / C);
+			cur = nx.out;
+			j++;
+			break;
+		} else
+			break;
+		cur = nx.out;
+		j++;
+	}
+	return j - 1;
+}
+
 bool layer_block(LB &L, const tgm_block *b)
 {
 	for (int i = 0; i < b->len; i++) {
 		const tgm_ins &in = b->v[i];
-		// a quantized product read only by the tanh right after it (C1's layers): the
-		// GEMM writes tanh's output and applies tanhf in its epilogue (same values)
-		if (in.op == TGM_MATMUL && i + 1 < b->len && b == &L.m->top && !(L.p->flags & TG_HIP_EXACT) && matmul_quant(L.m, in)) {
-			const tgm_ins &nx = b->v[i + 1];
-			if (nx.op == TGM_TANH && nx.a[0] == in.out && in.out != L.m->output && !L.loopw[(size_t)in.out] &&
-			    value_reads(&L.m->top, in.out) == 1) {
+		if (in.op == TGM_MATMUL && b == &L.m->top && !(L.p->flags & TG_HIP_EXACT) && matmul_quant(L.m, in)) {
+			Step chain;
+			const int last = epi_chain(L, b, i, chain);
+			if (last > i) { // the GEMM writes the chain's last value
 				tgm_ins fused = in;
-				fused.out = nx.out;
+				fused.out = b->v[last].out;
 				if (!layer_ins(L, fused)) return false;
-				L.p->steps.back().act = TGK_ACT_TANH;
-				i++; // the tanh is done
+				Step &st = L.p->steps.back();
+				st.nepi = chain.nepi;
+				for (int e = 0; e < chain.nepi; e++) st.epi[e] = chain.epi[e];
+				st.rowop = chain.rowop;
+				st.p0 = chain.p0;
+				st.p1 = chain.p1;
+				L.p->stats.epilogue_ins += chain.nepi + (chain.rowop != 0);
+				i = last;
 				continue;
 			}
 		}
@@ -1397,19 +1484,31 @@ void exec_step(Run &R, const Step &s)
 		a.o = dst(R, s.o);
 		a.orr = s.orr, a.oc = s.oc, a.oj = s.ojj;
 		a.M = R.rows * s.ni;
-		a.act = s.act;
+		a.nepi = s.nepi;
+		for (int e = 0; e < s.nepi; e++) {
+			const tgk_opd x = s.epi[e].kind == TGK_EW_UN ? tgk_opd{ nullptr, 0 } : resolve(R, s.epi[e].x);
+			a.epi[e] = tgk_epi{ s.epi[e].kind, s.epi[e].op, s.epi[e].mode, x.p, x.rs };
+		}
+		a.rowop = s.rowop;
+		int done;
 		if (!s.reuse_digits && tgk_qgemm_fusable(&a)) { // one row: the digits are made inside the product's kernel
 			Timer t(p, 1);
-			tgk_qgemm_fused(st, &a, p->d_scratch);
-			break;
-		}
-		if (!s.reuse_digits) {
-			Timer t(p, 2);
-			tgk_qgemm_digits(st, &a, p->d_scratch);
-		}
-		{
+			done = tgk_qgemm_fused(st, &a, p->d_scratch);
+		} else {
+			if (!s.reuse_digits) {
+				Timer t(p, 2);
+				tgk_qgemm_digits(st, &a, p->d_scratch);
+			}
 			Timer t(p, 1);
-			tgk_qgemm_mfma(st, &a, p->d_scratch);
+			done = tgk_qgemm_mfma(st, &a, p->d_scratch);
+		}
+		if (s.nepi && !(done & TGK_DID_CHAIN)) { // a small-batch kernel: the chain over its output, in place
+			Timer t(p, 3);
+			tgk_qgemm_chain(st, &a);
+		}
+		if (s.rowop && !(done & TGK_DID_ROWOP)) { // no workgroup held whole lines: the row op over the output, in place
+			Timer t(p, 3);
+			tgk_rowop(st, s.rowop, a.o, s.o.rs, tgk_opd{ a.o, s.o.rs }, s.p0, s.p1, R.rows);
 		}
 		break;
 	}
@@ -1603,13 +1702,13 @@ void merge_qgemms(tg_hip_prog *p, std::vector<std::vector<int8_t>> &mcodes, std:
 	const std::vector<char> inscan = in_scan(S);
 	std::vector<char> done(S.size(), 0);
 	for (size_t i = 0; i < S.size(); i++) {
-		if (S[i].kind != ST_QGEMM || inscan[i] || done[i] || S[i].act != TGK_ACT_NONE) continue;
+		if (S[i].kind != ST_QGEMM || inscan[i] || done[i] || S[i].nepi || S[i].rowop) continue;
 		std::vector<size_t> g{ i };
 		const tgk_qweight &w0 = p->qws[(size_t)S[i].qw];
 		long ctot = w0.C;
 		for (size_t j = i + 1; j < S.size() && g.size() < TGK_QSEG; j++) {
 			const Step &t = S[j];
-			if (t.kind != ST_QGEMM || inscan[j] || done[j] || t.act != TGK_ACT_NONE || !same_activation(S[i], t, p->qws) ||
+			if (t.kind != ST_QGEMM || inscan[j] || done[j] || t.nepi || t.rowop || !same_activation(S[i], t, p->qws) ||
 			    t.oc != S[i].oc)
 				continue;
 			const tgk_qweight &w = p->qws[(size_t)t.qw];

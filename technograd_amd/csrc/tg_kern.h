@@ -223,6 +223,17 @@ int tgk_qweight_pack_dev(tgk_qweight *w, void *dst, const uint8_t *codes, const 
  * seg_o[s], batch-row stride seg_orr[s], inner-row stride seg_oj[s] and the
  * common channel stride oc. nseg <= 1: one output (o, orr, oc, oj). */
 #define TGK_QSEG 32
+/* One instruction of a GEMM epilogue chain: TGK_EW_UN (v = op(v), op a TGM_
+ * unary op), TGK_EW_BIN (v = v op x) or TGK_EW_BINR (v = x op v), op one of
+ * TGK_ADD..TGK_MIN, with x read at mode 0: x[r xr + j oj + c oc] (a value of
+ * the output's shape, the output's in-row layout), 1: x[r xr] (one value),
+ * 3: x[r xr + c] (one value per channel; channel stride 1). */
+#define TGK_EPI_MAX 4
+typedef struct {
+	int kind, op, mode;
+	const float *x;
+	long xr;
+} tgk_epi;
 typedef struct {
 	const tgk_qweight *w;
 	const float *x;
@@ -235,11 +246,17 @@ typedef struct {
 	int seg_c0[TGK_QSEG + 1];
 	float *seg_o[TGK_QSEG];
 	long seg_orr[TGK_QSEG], seg_oj[TGK_QSEG];
-	int act;                /* TGK_ACT_TANH: every output goes through tanhf (a tanh instruction that
-	                           only reads this product, applied in the GEMM's epilogue) */
+	/* The instructions after the product that only read its chain of results,
+	 * in order: output (r, j, c) goes through epi[0], epi[1], ... (one output
+	 * only: nseg <= 1); applied in the large-batch kernel's epilogue, or by
+	 * tgk_qgemm_chain. */
+	int nepi;
+	tgk_epi epi[TGK_EPI_MAX];
+	/* TGM_RMSNORM or TGM_SOFTMAX over each output line's C channels (channel
+	 * stride 1), after the chain; 0: none. Applied inside the product's kernel
+	 * when one workgroup holds whole lines, else by the caller (tgk_rowop). */
+	int rowop;
 } tgk_qgemm_args;
-#define TGK_ACT_NONE 0
-#define TGK_ACT_TANH 1
 
 /* scratch: bytes needed for M rows of K inputs */
 /* One row of int4 weights (M = 1, unit-stride 16-byte-aligned row, K a
@@ -247,16 +264,23 @@ typedef struct {
  * the product's own kernel (and leaves them in the scratch like
  * tgk_qgemm_digits); other cases fall back to digits + product. */
 bool tgk_qgemm_fusable(const tgk_qgemm_args *a);
-void tgk_qgemm_fused(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
+int tgk_qgemm_fused(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 size_t tgk_qgemm_scratch(int M, int Kp);
-void tgk_qgemm(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
+int tgk_qgemm(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 /* the digit area tgk_qgemm uses in `scratch` for M rows of Kp inputs, for
  * kernels that write a GEMM's activation digits themselves (tg_qdigits.h)
  * before tgk_qgemm_mfma */
 tgk_qdig tgk_qgemm_digit_area(void *scratch, int M, int Kp);
-/* the two launches of tgk_qgemm: activation digits, then the MFMA kernel */
+/* the two launches of tgk_qgemm: activation digits, then the MFMA kernel.
+ * tgk_qgemm, tgk_qgemm_fused and tgk_qgemm_mfma return what the product's
+ * kernel applied besides the products: TGK_DID_CHAIN (a->epi) and
+ * TGK_DID_ROWOP (a->rowop); the caller applies the rest over the output
+ * (tgk_qgemm_chain, then tgk_rowop). */
+#define TGK_DID_CHAIN 1
+#define TGK_DID_ROWOP 2
+void tgk_qgemm_chain(hipStream_t s, const tgk_qgemm_args *a);
 void tgk_qgemm_digits(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
-void tgk_qgemm_mfma(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
+int tgk_qgemm_mfma(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 
 /* ---- row-program interpreter (kern_rowprog.hip) ---- */
 
