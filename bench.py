@@ -742,7 +742,10 @@ def main():
             e["trace_hbm_frac"] = round(e["alg_bytes"] / p["us"] / 1e3 / HBM_PEAK_GBS, 4)
             if "traffic" in p:
                 e["traffic"] = round(p["traffic"])
-    big_traffic = prof[4096].get("traffic_kernels", {}).get("qgemm_k<4>") if prof else None
+    def qgemm_of(d):  # the large-batch GEMM's entry (qgemm_k<4, epilogue variant>)
+        return next((v for k, v in (d or {}).items() if k.startswith("qgemm_k<4")), None)
+
+    big_traffic = qgemm_of(prof[4096].get("traffic_kernels")) if prof else None
     roofline = {"bound": "mfma", "achieved": big["mfma_TOPs"], "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
                 "frac": big["mfma_frac"], "traffic": None if big_traffic is None else round(big_traffic),
                 "traffic_note": pnote,
@@ -751,7 +754,7 @@ def main():
                            "cores execute 3 x alg_ops; hw_mfma_frac = 3 x frac",
                 "kernel": "qgemm_k<4> (int8 MFMA, 3 activation digits) at batch 4096",
                 "alg_ops_per_launch": big["alg_ops"], "avg_kernel_us": big["mfma_kernel_us"],
-                "trace_kernel_us": None if not prof else prof[4096]["kernels_us"].get("qgemm_k<4>")}
+                "trace_kernel_us": None if not prof else qgemm_of(prof[4096]["kernels_us"])}
     if prof:
         mv = {}
         for b in (1, 16):

@@ -427,29 +427,55 @@ __device__ inline float ref_loop(const tgk_qgemm_args &a, const tgk_qweight &w, 
 	return t;
 }
 
-// The reference's sums of ref_loop for line m and channels c = cb + lane +
-// 64 q (q < NQ), a whole wave on one line: the line's inputs have one
-// address for every lane, and the codes of U inputs are loaded before their
-// multiplies and adds, which keep each sum's order. Channels at or beyond C
-// read channel C - 1 and are not to be used.
-template <int NQ, int U = 16>
+// The reference's sums of ref_loop for line m and channels c = cb + NQ lane
+// + q (q < NQ), a whole wave on one line: the line's inputs have one address
+// for every lane (read four at a time when they are contiguous), and the
+// codes of U inputs are loaded before their multiplies and adds, which keep
+// each sum's order; a lane's NQ channels are adjacent, so for weights stored
+// [K][C] in int8 (x @ W) an input's NQ codes are one load. Channels at or
+// beyond C read channel C - 1 and are not to be used.
+// (VEC false: the plain loads only, for kernels with few registers to spare)
+template <int NQ, int U = 16, bool VEC = true>
 __device__ inline void ref_line(const tgk_qgemm_args &a, const tgk_qweight &w, int m, int cb, int lane, float (&t)[NQ])
 {
+	static_assert(U % 4 == 0 && (NQ == 1 || NQ == 2 || NQ == 4), "ref_line shape");
 	const float *x = xrow(a, m);
 	int c[NQ];
 	for (int q = 0; q < NQ; q++) {
-		const int cc = cb + lane + 64 * q;
+		const int cc = cb + NQ * lane + q;
 		c[q] = cc < w.C ? cc : w.C - 1;
 		t[q] = 0.0f;
 	}
-	const int K = w.K;
+	const int K = w.K, c0 = cb + NQ * lane;
+	// one load of the NQ codes of input k: int8, [K][C], the NQ channels in range and aligned
+	const bool row8 = VEC && w.bits == 8 && w.axis == 1 && c0 + NQ <= w.C && (w.C % NQ) == 0 && ((size_t)w.orig % 4) == 0;
+	const bool xv4 = VEC && a.xk == 1 && ((size_t)x % 16) == 0;
 	int k = 0;
 	for (; k + U <= K; k += U) {
 		float xv[U];
 		int cd[NQ][U];
-		for (int u = 0; u < U; u++) xv[u] = x[(long)(k + u) * a.xk];
-		for (int q = 0; q < NQ; q++)
-			for (int u = 0; u < U; u++) cd[q][u] = code_orig(w, c[q], k + u);
+		if (xv4)
+			for (int u = 0; u < U; u += 4) {
+				const float4 f = *(const float4 *)(x + k + u);
+				xv[u] = f.x, xv[u + 1] = f.y, xv[u + 2] = f.z, xv[u + 3] = f.w;
+			}
+		else
+			for (int u = 0; u < U; u++) xv[u] = x[(long)(k + u) * a.xk];
+		if (row8)
+			for (int u = 0; u < U; u++) {
+				const int8_t *p = (const int8_t *)w.orig + (long)(k + u) * w.C + c0;
+				if constexpr (NQ == 4) {
+					const int v = *(const int *)p;
+					for (int q = 0; q < 4; q++) cd[q][u] = (int)(int8_t)(v >> (8 * q));
+				} else if constexpr (NQ == 2) {
+					const short v = *(const short *)p;
+					cd[0][u] = (int)(int8_t)v, cd[1][u] = (int)(int8_t)(v >> 8);
+				} else
+					cd[0][u] = p[0];
+			}
+		else
+			for (int q = 0; q < NQ; q++)
+				for (int u = 0; u < U; u++) cd[q][u] = code_orig(w, c[q], k + u);
 		for (int u = 0; u < U; u++)
 			for (int q = 0; q < NQ; q++) t[q] += (float)cd[q][u] * xv[u];
 	}
@@ -556,10 +582,10 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 			if (m >= a.M) continue;
 			constexpr int NQ = (NB * 32 + 63) / 64;
 			float t[NQ];
-			ref_line<NQ, 4>(a, w, m, cbase, lane, t); // few registers: the accumulators may still be live
+			ref_line<NQ, 4, false>(a, w, m, cbase, lane, t); // few registers: the accumulators may still be live
 			const int r = m / a.ni, jj = m - r * a.ni;
 			for (int q = 0; q < NQ; q++) {
-				const int c = cbase + lane + 64 * q;
+				const int c = cbase + NQ * lane + q;
 				if (c < cbase + NB * 32 && c < w.C) *out_at(a, r, jj, c) = act_out<ACT>(w.scale[c] * t[q]);
 			}
 		}
@@ -666,8 +692,10 @@ __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 				const int l = wave + 8 * i;
 				float t[BN / 64];
 				ref_line<BN / 64>(a, w, m0 + l, c0, lane, t);
-				for (int q = 0; q < BN / 64; q++)
-					if (lane + 64 * q < cw) L[l * STR + lane + 64 * q] = w.scale[c0 + lane + 64 * q] * t[q];
+				for (int q = 0; q < BN / 64; q++) {
+					const int c = (BN / 64) * lane + q;
+					if (c < cw) L[l * STR + c] = w.scale[c0 + c] * t[q];
+				}
 			}
 	// the chain, four lines at a time: for each instruction, every operand
 	// load of the four lines first, then the arithmetic (the operation chosen
