@@ -383,22 +383,8 @@ __device__ inline float *out_at(const tgk_qgemm_args &a, int r, int jj, int c)
 	return o.p + (long)r * o.orr + (long)jj * o.oj;
 }
 
-// a unary instruction of an epilogue chain: the operations the layer builder
-// lets into a chain (tg_hip.cpp: epi_unary), each as the elementwise kernels
-// compute it (tg_uop)
-__device__ inline float epi_uop(int op, float v)
-{
-	switch (op) {
-	case TGM_NEG: return tg_uop(TGM_NEG, v);
-	case TGM_TANH: return tg_uop(TGM_TANH, v);
-	case TGM_RELU: return tg_uop(TGM_RELU, v);
-	case TGM_SIGMOID: return tg_uop(TGM_SIGMOID, v);
-	case TGM_EXP: return tg_uop(TGM_EXP, v);
-	case TGM_GELU: return tg_uop(TGM_GELU, v);
-	case TGM_SILU: return tg_uop(TGM_SILU, v);
-	default: return tg_uop(TGM_STEP, v);
-	}
-}
+// a unary instruction of an epilogue chain, as the elementwise kernels compute it
+__device__ inline float epi_uop(int op, float v) { return tg_uop(op, v); }
 
 // output (batch row r, inner row jj, channel c) with value v (the product)
 // after the epilogue chain: the values the instructions after the product
@@ -721,7 +707,8 @@ __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 	case K: \
 		for (int u = 0; u < 16; u++) v[u] = tg_uop(K, v[u]); \
 		break;
-					EPU(TGM_NEG) EPU(TGM_TANH) EPU(TGM_RELU) EPU(TGM_SIGMOID) EPU(TGM_EXP) EPU(TGM_GELU) EPU(TGM_SILU)
+					EPU(TGM_NEG) EPU(TGM_TANH) EPU(TGM_RELU) EPU(TGM_SIGMOID) EPU(TGM_EXP) EPU(TGM_SQRT) EPU(TGM_GELU)
+					EPU(TGM_SILU) EPU(TGM_SOFTPLUS) EPU(TGM_LOG) EPU(TGM_SIN) EPU(TGM_COS) EPU(TGM_FLOOR)
 					default: EPU(TGM_STEP)
 #undef EPU
 				}
@@ -794,11 +781,20 @@ __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 			for (int c = lane; c < C; c += 64) L[l * STR + c] = L[l * STR + c] * lv[l];
 		__syncthreads();
 	}
-	// the stores, after every load
+	// the stores, after every load: four channels per lane and store where
+	// the line is contiguous and 16-byte aligned
 	for (int l = wave; l < nl; l += 8) {
 		const int m = m0 + l, r = m / a.ni, jj = m - r * a.ni;
 		float *o = a.o + (long)r * a.orr + (long)jj * a.oj + (long)c0 * a.oc;
-		for (int c = lane; c < cw; c += 64) o[(long)c * a.oc] = L[l * STR + c];
+		const float *y = L + l * STR;
+		if (a.oc == 1 && ((size_t)o & 15) == 0) {
+			for (int c = 4 * lane; c < cw; c += 256) {
+				if (c + 4 <= cw) *(float4 *)(o + c) = make_float4(y[c], y[c + 1], y[c + 2], y[c + 3]);
+				else
+					for (int u = c; u < cw; u++) o[u] = y[u];
+			}
+		} else
+			for (int c = lane; c < cw; c += 64) o[(long)c * a.oc] = y[c];
 	}
 }
 

@@ -1026,12 +1026,17 @@ int value_reads(const tgm_block *b, int v)
 	return n;
 }
 
-// unary instructions a GEMM epilogue chain may hold (kern_qgemm.hip: epi_uop)
+// the elementwise unary instructions (every one can sit in a GEMM epilogue chain)
 bool epi_unary(int op)
 {
-	return op == TGM_NEG || op == TGM_TANH || op == TGM_RELU || op == TGM_SIGMOID || op == TGM_EXP || op == TGM_GELU || op == TGM_SILU ||
-	       op == TGM_STEP;
+	switch (op) {
+	case TGM_NEG: case TGM_TANH: case TGM_RELU: case TGM_SIGMOID: case TGM_EXP: case TGM_SQRT: case TGM_GELU:
+	case TGM_SILU: case TGM_SOFTPLUS: case TGM_LOG: case TGM_SIN: case TGM_COS: case TGM_FLOOR: case TGM_STEP: return true;
+	default: return false;
+	}
 }
+
+bool elementwise(int op) { return epi_unary(op) || (op >= TGM_ADD && op <= TGM_MIN); }
 
 bool same_shape(const tgm_shape &x, const tgm_shape &y)
 {
@@ -1091,6 +1096,20 @@ int epi_chain(LB &L, const tgm_block *b, int i, Step &st)
 			break;
 		cur = nx.out;
 		j++;
+	}
+	// Worth it only if it saves memory traffic: when the next instruction is
+	// elementwise and reads the chain's value, which nothing else reads, the
+	// two would have been one fused elementwise run reading the product,
+	// and the run now reads the chain's value instead (same bytes, a slower
+	// GEMM epilogue). A row op, or a value read again later, saves a pass.
+	if (!st.rowop && j < b->len && elementwise(b->v[j].op) && value_reads(&m->top, cur) == 1) {
+		const tgm_ins &nx = b->v[j];
+		bool reads = false;
+		for (int k = 0; k < nx.na; k++) reads |= nx.a[k] == cur;
+		if (reads) {
+			st.nepi = 0;
+			return i;
+		}
 	}
 	return j - 1;
 }

@@ -135,11 +135,22 @@ def test_operand_made_by_an_elementwise_run():
 
 @pytest.mark.parametrize("bits,rows,T,K,C", [(8, 64, 512, 16, 512), (4, 40, 512, 64, 768)])
 def test_bias_rows_of_several_channel_tiles(bits, rows, T, K, C):
-    """x @ W + b over more than one channel tile of the large-batch GEMM
-    (config 5's dt projection: 16 inputs, 512 channels), then softplus (not
-    in a chain: the GEMM stores the biased value)"""
+    """x @ W + b, then softplus, over more than one channel tile of the
+    large-batch GEMM (config 5's dt projection: 16 inputs, 512 channels)"""
     print("case bias tiles", bits, rows, T, K, C, flush=True)
     params = [_weight("W", 61, C, K, bits, 1), _f32("b", synth.normal(62, 0.5, C))]
     body = ("    (%%0 (f32 %d %d) (matmul x W))\n    (%%1 (f32 %d %d) (add %%0 b))\n    (%%2 (f32 %d %d) (softplus %%1))\n" %
             (T, C, T, C, T, C))
-    _case(params, [("x", "%d %d" % (T, K))], body, "%2", "%d %d" % (T, C), _rows(63, rows, T * K, specials=True), 1)
+    _case(params, [("x", "%d %d" % (T, K))], body, "%2", "%d %d" % (T, C), _rows(63, rows, T * K, specials=True), 2)
+
+
+def test_chain_that_saves_nothing_is_not_taken():
+    """four instructions fill a chain and a fifth elementwise instruction
+    reads its value, which nothing else reads: without the chain the five
+    would be one fused elementwise run reading the product, so the chain
+    would only slow the GEMM down; the builder keeps the product alone"""
+    C, K, rows = 128, 256, 64
+    params = [_weight("W", 71, C, K, 8, 0), _f32("b", synth.normal(72, 0.1, C)), _f32("s", [0.5])]
+    body = ("    (%%0 (f32 %d) (matmul W x))\n    (%%1 (f32 %d) (add %%0 b))\n    (%%2 (f32 %d) (tanh %%1))\n"
+            "    (%%3 (f32 %d) (mul %%2 s))\n    (%%4 (f32 %d) (sub %%3 b))\n    (%%5 (f32 %d) (relu %%4))\n" % ((C,) * 6))
+    _case(params, [("x", str(K))], body, "%5", str(C), _rows(73, rows, K), 0)
