@@ -1376,8 +1376,8 @@ int launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 			qgemm_k<BITS, 2><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy, 0); // a lone tanh: inline in the stores
 			return TGK_DID_CHAIN;
 		}
-		if ((a->nepi || a->rowop) && a->nseg <= 1) { // the chain in the epilogue, and the row op when a tile holds whole lines
-			const int row = a->rowop && gx == 1 && a->oc == 1;
+		const int row = a->rowop && gx == 1 && a->oc == 1;
+		if ((a->nepi || row) && a->nseg <= 1) { // the chain in the epilogue, and the row op when a tile holds whole lines
 			qgemm_k<BITS, 1><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy, row);
 			return TGK_DID_CHAIN | (row ? TGK_DID_ROWOP : 0);
 		}

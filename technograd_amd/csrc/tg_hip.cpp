@@ -1071,6 +1071,15 @@ int epi_chain(LB &L, const tgm_block *b, int i, Step &st)
 	int cur = in.out, j = i + 1;
 	st.nepi = 0;
 	st.rowop = 0;
+	// a product whose activations another quantized product of the block also
+	// reads keeps no chain: the GEMMs merge into one (merge_qgemms), which is
+	// worth more (config 3's q/k/v and gate/up projections)
+	const int act = quant == 1 ? in.a[1] : in.a[0];
+	for (int k = 0; k < b->len; k++)
+		if (k != i && b->v[k].op == TGM_MATMUL && matmul_quant(m, b->v[k])) {
+			const int q2 = matmul_quant(m, b->v[k]);
+			if ((q2 == 1 ? b->v[k].a[1] : b->v[k].a[0]) == act) return i;
+		}
 	while (j < b->len && single(cur)) {
 		const tgm_ins &nx = b->v[j];
 		if (st.nepi < TGK_EPI_MAX && epi_unary(nx.op) && nx.a[0] == cur) {
