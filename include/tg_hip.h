@@ -99,6 +99,11 @@ void *tg_hip_get_stream(const tg_hip_prog *p);
  * axis 1: o[m,n] = b[m,k] @ Q[k,n] diag(s)  (tg_matmul_qb; b is the left operand) */
 int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, const float *b, int m, int k, int n, int axis,
 		    int flags);
+/* tg_matmul_qa and tg_matmul_qb (runtime/tg_rt.h:132, :143) with their exact
+ * argument lists, for a call site that swaps the function name only
+ * (src/vm.c:277-281): tg_hip_matmul_q on axis 0 and 1. 0 on success. */
+int tg_hip_matmul_qa(float *o, const signed char *q, int bits, const float *s, const float *b, int m, int k, int n);
+int tg_hip_matmul_qb(float *o, const float *a, const signed char *q, int bits, const float *s, int m, int k, int n);
 
 /* tg_hip_matmul_q's matrix-core path without any device allocation. No
  * counterpart in the reference: for callers that cannot allocate (code under

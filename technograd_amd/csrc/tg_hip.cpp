@@ -2363,6 +2363,16 @@ int tg_hip_set_stream(tg_hip_prog *p, void *stream)
 
 void *tg_hip_get_stream(const tg_hip_prog *p) { return p ? (void *)p->st : nullptr; }
 
+int tg_hip_matmul_qa(float *o, const signed char *q, int bits, const float *s, const float *b, int m, int k, int n)
+{
+	return tg_hip_matmul_q(o, q, bits, s, b, m, k, n, 0, 0);
+}
+
+int tg_hip_matmul_qb(float *o, const float *a, const signed char *q, int bits, const float *s, int m, int k, int n)
+{
+	return tg_hip_matmul_q(o, q, bits, s, a, m, k, n, 1, 0);
+}
+
 int tg_hip_matmul_q(float *o, const signed char *q, int bits, const float *s, const float *b, int m, int k, int n, int axis, int flags)
 {
 	if ((bits != 8 && bits != 4) || (axis != 0 && axis != 1) || m < 1 || k < 1 || n < 1) {

@@ -43,6 +43,8 @@ def lib():
         L.tg_hip_batch_device.argtypes = [vp, vp, ctypes.c_long, vp, vp]
         L.tg_hip_sync.argtypes = [vp]
         L.tg_hip_matmul_q.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip, ip, ip]
+        L.tg_hip_matmul_qa.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip]
+        L.tg_hip_matmul_qb.argtypes = [vp, vp, vp, ip, vp, ip, ip, ip]
         L.tg_hip_matmul_q_noalloc.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip, ip, vp]
         L.tg_hip_quantize_rtn.argtypes = [vp, ip, ip, ip, ip, vp, vp, ip]
         L.tg_hip_dec_create.restype = vp
@@ -186,6 +188,22 @@ def matmul_q(q, bits, s, b, m, k, n, axis, flags=0):
     b = np.ascontiguousarray(b, dtype=np.float32)
     o = np.empty((m, n), np.float32)
     _check(lib().tg_hip_matmul_q(_p(o), _p(q), bits, _p(s), _p(b), m, k, n, axis, flags), "tg_hip_matmul_q")
+    return o
+
+
+def matmul_qa(q, bits, s, b, m, k, n):
+    """tg_hip_matmul_qa: tg_matmul_qa's argument list (o = diag(s) Q @ b)."""
+    q, s, b = (np.ascontiguousarray(v, dtype=t) for v, t in ((q, np.int8), (s, np.float32), (b, np.float32)))
+    o = np.empty((m, n), np.float32)
+    _check(lib().tg_hip_matmul_qa(_p(o), _p(q), bits, _p(s), _p(b), m, k, n), "tg_hip_matmul_qa")
+    return o
+
+
+def matmul_qb(a, q, bits, s, m, k, n):
+    """tg_hip_matmul_qb: tg_matmul_qb's argument list (o = a @ Q diag(s))."""
+    a, q, s = (np.ascontiguousarray(v, dtype=t) for v, t in ((a, np.float32), (q, np.int8), (s, np.float32)))
+    o = np.empty((m, n), np.float32)
+    _check(lib().tg_hip_matmul_qb(_p(o), _p(a), _p(q), bits, _p(s), m, k, n), "tg_hip_matmul_qb")
     return o
 
 

@@ -150,6 +150,9 @@ def test_matmul_q_entry_point(bits_, axis, m, k, n):
     print("matmul_q: %.4f of outputs by the normalized clause; largest normalized error: GPU %.2f, reference %.2f"
           % (frac, ng, nr), flush=True)
     assert frac < 0.05
+    # the drop-in forms with tg_matmul_qa / tg_matmul_qb's argument lists: the same call
+    same = hip.matmul_qa(packed, bits_, scales, b, m, k, n) if axis == 0 else hip.matmul_qb(b, packed, bits_, scales, m, k, n)
+    assert np.array_equal(bits(same), bits(fast))
 
 
 @pytest.mark.parametrize("rows", [4, 700])
