@@ -61,6 +61,7 @@ METRIC = "quantized rows/sec via tgc batch at 1 GPU; % of HBM / int8-MFMA roofli
 HBM_PEAK_GBS = 8000.0
 MFMA_I8_PEAK_TOPS = 5000.0
 FLUSH_ROWS, FLUSH_COLS = 2048, 65536  # the flush pass: x * c over 512 MiB in, 512 MiB out
+FLOOR_BYTES = (C * K // 2 + 4 * C) // 16 * 16  # config 2's packed weight and scales, the matvec's main read
 
 
 def log(msg):
@@ -171,6 +172,9 @@ def profile_child(mode):
         d_x = hip.DeviceBuffer.from_array(X)
         d_y = hip.DeviceBuffer(4096 * C * 4)
         calls = [(b, lambda b=b: prog.batch_device(d_x.ptr, b, d_y.ptr)) for b in BATCHES] * 2
+        # the read floor: a plain read of a span the size of the packed weight, cold like the calls
+        span = hip.DeviceBuffer(FLOOR_BYTES)
+        calls += [("floor", lambda: hip.read_pass(span.ptr, FLOOR_BYTES, 2048, prog.stream()))] * 2
     else:
         import numpy as np
         rows = 1048576
@@ -262,20 +266,25 @@ def profile_c2(alg_bytes):
         return None, "rocprofv3 timed out"
     finally:
         shutil.rmtree(out, ignore_errors=True)
-    if not kt or len(kt[0]) != 2 * len(BATCHES):
+    nb = 2 * len(BATCHES)
+    if not kt or len(kt[0]) != nb + 2:
         return None, "kernel trace: %s segments" % (None if not kt else len(kt[0]))
     res = {b: {"kernels_us": {}} for b in BATCHES}
-    for i, seg in enumerate(kt[0]):  # two calls per batch: averages
+    fl = [v["us"] for seg in kt[0][nb:] for _, _, v in seg]
+    res["floor"] = {"us": round(sum(fl) / max(len(fl), 1), 3), "bytes": FLOOR_BYTES}
+    for i, seg in enumerate(kt[0][:nb]):  # two calls per batch: averages
         r = res[BATCHES[i % len(BATCHES)]]
         for n, _, v in seg:
             r["kernels_us"][n] = r["kernels_us"].get(n, 0.0) + v["us"] / 2
-    for r in res.values():
+    for b in BATCHES:
+        r = res[b]
         r["kernels_us"] = {k: round(v, 3) for k, v in r["kernels_us"].items()}
         r["us"] = round(sum(r["kernels_us"].values()), 3)
     note = "kernel trace of two cold calls per batch"
-    if fe and wr and len(fe[0]) == len(wr[0]) == 2 * len(BATCHES):
+    if fe and wr and len(fe[0]) == len(wr[0]) == nb + 2:
         tr, rf, rw = calibrated_traffic(fe, wr)
-        for i, (tot, per) in enumerate(tr):
+        res["floor"]["traffic"] = round(sum(t for t, _ in tr[nb:]) / 2)
+        for i, (tot, per) in enumerate(tr[:nb]):
             r = res[BATCHES[i % len(BATCHES)]]
             r["traffic"] = r.get("traffic", 0.0) + tot / 2
             tk = r.setdefault("traffic_kernels", {})
@@ -763,9 +772,19 @@ def main():
                              "achieved": round(e["alg_bytes"] / p["us"] / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(e["alg_bytes"] / p["us"] / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": e["alg_bytes"],
                              "traffic": None if "traffic" not in p else round(p["traffic"])}
+        fl = prof.get("floor", {})
+        if fl.get("us"):
+            mv["read_floor"] = {"us": fl["us"], "bytes": fl["bytes"], "GBs": round(fl["bytes"] / fl["us"] / 1e3, 1),
+                                "traffic": fl.get("traffic"),
+                                "note": "a plain read of the packed weight's size (tg_hip_read_pass, 2048 x 256 "
+                                        "threads) after the same flush pass: what a cold read of these bytes takes "
+                                        "on this device"}
+            for b in (1, 16):
+                mv["b%d" % b]["of_read_floor"] = round(fl["us"] / mv["b%d" % b]["us"], 4)
         mv["note"] = ("int4 matvec: algorithmic bytes (weights, scales, rows in and out) over the summed kernel-trace "
                       "durations of the call's kernels (one kernel at B=1: its digits are made inside it), each call "
-                      "after a 512 MiB flush pass; traffic: calibrated FETCH_SIZE + WRITE_SIZE of the same kernels")
+                      "after a 512 MiB flush pass; traffic: calibrated FETCH_SIZE + WRITE_SIZE of the same kernels; "
+                      "of_read_floor: the read floor's time over the call's")
         roofline["matvec"] = mv
 
     cpu = None

@@ -214,6 +214,12 @@ void *tg_hip_dev_alloc(size_t bytes);
 int tg_hip_dev_free(void *d);
 int tg_hip_h2d(void *d, const void *h, size_t bytes);
 int tg_hip_d2h(void *h, const void *d, size_t bytes);
+/* A read of `bytes` of device memory at d (16-byte aligned) that writes
+ * nothing, asynchronous on `stream` (NULL: the null stream), in `blocks`
+ * workgroups of 256 threads: the floor a bandwidth-bound kernel of that size
+ * is measured against (the benchmark's matvec sweep). No counterpart in the
+ * reference. 0 on success. */
+int tg_hip_read_pass(const void *d, size_t bytes, int blocks, void *stream);
 
 #ifdef __cplusplus
 }

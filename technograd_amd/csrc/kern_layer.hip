@@ -685,6 +685,28 @@ void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, i
 		rowop_k<<<blocks_for(total), TPB, 0, s>>>(op, o, ors, a, nrow, cols, total);
 }
 
+namespace {
+// every 16-byte word of the span once, grid-stride; a lane writes only when
+// its sum has a value that no input of the benchmark produces (never), so
+// the loads cannot be dropped
+typedef int rd_v4i __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void read_k(const rd_v4i *p, long n16, int *sink)
+{
+	const long t = (long)blockIdx.x * 256 + threadIdx.x, nt = (long)gridDim.x * 256;
+	int acc = 0;
+	for (long i = t; i < n16; i += nt) {
+		const rd_v4i v = __builtin_nontemporal_load(p + i);
+		acc ^= v.x ^ v.y ^ v.z ^ v.w;
+	}
+	if (acc == 0x7fa55a5f) sink[0] = acc;
+}
+} // namespace
+
+void tgk_read(hipStream_t s, const void *p, size_t bytes, int blocks, int *sink)
+{
+	if (bytes >= 16 && blocks > 0) read_k<<<(unsigned)blocks, 256, 0, s>>>((const rd_v4i *)p, (long)(bytes / 16), sink);
+}
+
 void tgk_reduce(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows)
 {
 	// one wave per block while that leaves fewer than 1024 blocks: long rows

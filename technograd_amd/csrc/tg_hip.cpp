@@ -2721,6 +2721,18 @@ int tg_hip_reset_stats(tg_hip_prog *p)
 	return 0;
 }
 
+int tg_hip_read_pass(const void *d, size_t bytes, int blocks, void *stream)
+{
+	static int *sink = nullptr; // one int per process, never read
+	if (!d || ((size_t)d & 15) || blocks <= 0) {
+		seterr("tg_hip_read_pass: bad arguments");
+		return -1;
+	}
+	if (!sink && !hipok(hipMalloc(&sink, sizeof(int)), "hipMalloc")) return -1;
+	tgk_read((hipStream_t)stream, d, bytes, blocks, sink);
+	return hipok(hipGetLastError(), "read pass launch") ? 0 : -1;
+}
+
 void *tg_hip_dev_alloc(size_t bytes)
 {
 	void *d = nullptr;

@@ -92,6 +92,8 @@ void tgk_matmul_exact(hipStream_t s, const tgk_mm *d, int rows);
 
 /* softmax (op TGM_SOFTMAX) or rmsnorm over `cols`-long rows, `nrow` of them per batch row */
 void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, int cols, int rows);
+/* read `bytes` at p (16-byte aligned) in `blocks` workgroups, writing nothing but (never) sink[0] */
+void tgk_read(hipStream_t s, const void *p, size_t bytes, int blocks, int *sink);
 /* sum or mean of the n elements of a row */
 void tgk_reduce(hipStream_t s, int op, float *o, long ors, tgk_opd a, int n, int rows);
 void tgk_transpose(hipStream_t s, float *o, long ors, tgk_opd a, int g, int r, int c, int rows);

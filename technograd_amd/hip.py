@@ -44,6 +44,7 @@ def lib():
         L.tg_hip_sync.argtypes = [vp]
         L.tg_hip_matmul_q.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip, ip, ip]
         L.tg_hip_matmul_qa.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip]
+        L.tg_hip_read_pass.argtypes = [vp, ctypes.c_size_t, ip, vp]
         L.tg_hip_matmul_qb.argtypes = [vp, vp, vp, ip, vp, ip, ip, ip]
         L.tg_hip_matmul_q_noalloc.argtypes = [vp, vp, ip, vp, vp, ip, ip, ip, ip, vp]
         L.tg_hip_quantize_rtn.argtypes = [vp, ip, ip, ip, ip, vp, vp, ip]
@@ -205,6 +206,12 @@ def matmul_qb(a, q, bits, s, m, k, n):
     o = np.empty((m, n), np.float32)
     _check(lib().tg_hip_matmul_qb(_p(o), _p(a), _p(q), bits, _p(s), m, k, n), "tg_hip_matmul_qb")
     return o
+
+
+def read_pass(ptr, nbytes, blocks=2048, stream=None):
+    """tg_hip_read_pass: read nbytes of device memory at ptr (16-byte aligned),
+    writing nothing, asynchronous on `stream` (a measurement floor)."""
+    _check(lib().tg_hip_read_pass(ptr, nbytes, blocks, stream), "tg_hip_read_pass")
 
 
 def matmul_q_noalloc(d_o, d_q, bits, d_s, d_b, m, k, n, axis, stream=None):
