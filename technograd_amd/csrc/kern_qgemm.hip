@@ -30,6 +30,16 @@
 //            inputs, t = code + 8 in [0, 15] (offset binary), so unpacking is
 //            two masks per 4 bytes; the +8 bias is removed with the row's sum
 //            of q: sum_k t q = sum_k code q + 8 sum_k q.
+//   int4 wg  (the large-batch kernel's copy) [channel / 64][k / 32][lane][16
+//            bytes]: byte b of lane l holds, for input 16 (l / 32) + b of the
+//            block, t = code + 8 of channel l % 32 of the pair's first 32 in its
+//            low nibble and the code (two's complement) of channel 32 + l % 32
+//            in its high nibble. As an int8 the byte is t + 16 code', so the
+//            raw bytes are one MFMA operand (sums S1 = sum t q + 16 sum code' q)
+//            and the bytes masked to their low nibbles another (S0 = sum t q):
+//            the second channel's sum is (S1 - S0) / 16, exactly, with one mask
+//            per 4 bytes for two channel blocks instead of three operations
+//            per 4 bytes for each.
 // Weights are repacked once at load (channels padded to 256, K to 64).
 #include "tg_ewop.h"
 #include "tg_kern.h"
@@ -534,7 +544,7 @@ __device__ inline TileRows<NB> tile_rows(const tgk_qgemm_args &a, const tgk_qwei
 // HOIST: take all 16 rows' exponents and sums of q from their lanes before the
 // first store (the shuffles then wait once, not once per row; 48 more live
 // registers, for kernels that have them free at the epilogue).
-template <int NB, bool HOIST, int ACT = 0, class Tot, class TotD>
+template <int NB, bool HOIST, int ACT = 0, bool PAIRS = false, class Tot, class TotD>
 __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int mbase, int cbase, int lane,
 				  const TileRows<NB> &t, Tot tot, TotD totd)
 {
@@ -558,7 +568,8 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 			const int E = __shfl(Er, rv), sp = __shfl(spr, rv);
 			const long long Q = __shfl(Qr, rv);
 			if (!sp)
-				for (int j = 0; j < NB; j++) epilogue_with<ACT>(a, w, m, cbase + j * 32 + r32, tot(j, v), E, 0, Q);
+				for (int j = 0; j < NB; j++) // a pair's odd block has no +8 bias to remove: add it for epilogue_with
+					epilogue_with<ACT>(a, w, m, cbase + j * 32 + r32, tot(j, v) + (PAIRS && (j & 1) ? 8 * Q : 0), E, 0, Q);
 		}
 		unsigned long long sm = __ballot(spr) & 0xffffffffull; // lane r (r < 32): row mbase + r
 		while (sm) {
@@ -592,7 +603,8 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 			if (a.ni != 1) r = m / a.ni, jj = m - r * a.ni;
 			for (int j = 0; j < NB; j++) {
 				if (cbase + j * 32 + r32 >= w.C) continue;
-				oc[j].p[(long)r * oc[j].orr + (long)jj * oc[j].oj] = sc[j] * (float)ldexp(totd(j, v) - q8, E - 23); // no chain
+				oc[j].p[(long)r * oc[j].orr + (long)jj * oc[j].oj] =
+					sc[j] * (float)ldexp(totd(j, v) - (PAIRS && (j & 1) ? 0.0 : q8), E - 23); // no chain
 			}
 		}
 		return;
@@ -610,7 +622,7 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 		float *orow = a.o + (long)r * a.orr + (long)jj * a.oj;
 		for (int j = 0; j < NB; j++) {
 			if (cbase + j * 32 + r32 >= w.C) continue;
-			orow[coff[j]] = act_out<ACT>(sc[j] * (float)ldexp(totd(j, v) - q8, E - 23));
+			orow[coff[j]] = act_out<ACT>(sc[j] * (float)ldexp(totd(j, v) - (PAIRS && (j & 1) ? 0.0 : q8), E - 23));
 		}
 	}
 }
@@ -649,7 +661,7 @@ __device__ inline void copy_to_lds(const uint8_t *sbase, unsigned voff, unsigned
 constexpr int rowstr(int C) { return C | 1; }
 constexpr int EPI_LDS = BM * rowstr(BN) * 4 + BM * 4; // line values and one scalar per line
 
-template <class TotD>
+template <bool PAIRS, class TotD>
 __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m0, int c0, int wm, int g, int lane,
 				int wave, int tid, bool row, float *L, TotD totd)
 {
@@ -666,7 +678,8 @@ __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 			const int E = __shfl(t.Er, rv);
 			const double q8 = 8.0 * (double)__shfl(t.Qr, rv); // 0 for int8 weights
 			for (int j = 0; j < 4; j++)
-				L[(wm * 32 + rv) * STR + g * 128 + j * 32 + r32] = t.sc[j] * (float)ldexp(totd(j, v) - q8, E - 23);
+				L[(wm * 32 + rv) * STR + g * 128 + j * 32 + r32] =
+					t.sc[j] * (float)ldexp(totd(j, v) - (PAIRS && (j & 1) ? 0.0 : q8), E - 23);
 		}
 	}
 	// a wave takes lines wave, wave + 8, ... (16 of them), 64 channels at a time
@@ -831,7 +844,7 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 	constexpr int AST = 24 * 1024;                // 4 row blocks x 2 substeps x 3 digits x 1 KiB
 	constexpr int BST = BITS == 4 ? 8192 : 16384; // 8 channel blocks x 2 substeps x 512 B or 1 KiB
 	constexpr int STG = AST + BST;
-	constexpr int GA = 6, GB = BST / 1024 / 4;    // copies per wave per stage: group 0, group 1
+	constexpr int GA = BITS == 4 ? 4 : 6, GB = 4; // copies per wave per stage: group 0, group 1
 	constexpr int LDSB = EPI == 1 && EPI_LDS > S * STG ? (EPI_LDS + 1023) / 1024 * 1024 : S * STG;
 	__shared__ __attribute__((aligned(1024))) uint8_t lds[LDSB];
 	const int tid = threadIdx.x, lane = tid & 63;
@@ -844,23 +857,31 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 	const int bm = id / gx, bn = id % gx;
 	const int m0 = bm * BM, c0 = bn * BN, nk = w.Kp / KB, kblocks = w.Kp / 32;
 	const uint8_t *gA = (const uint8_t *)s.dig + (long)(m0 / 32) * kblocks * 3072;
-	const uint8_t *gB = w.w + (long)(c0 / 32) * kblocks * (BITS == 4 ? 512 : 1024);
+	const uint8_t *gB = BITS == 4 ? w.wg + (long)(c0 / 64) * kblocks * 1024 : w.w + (long)(c0 / 32) * kblocks * 1024;
 	const unsigned voff = lane * 16;
 	const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) uint8_t *)lds;
-	// group 0 wave wm: digit pieces of row block wm (6 KiB per step);
-	// group 1 wave wm: weight pieces GB wm .. GB wm + GB - 1 (channel block p for
-	// int4, p / 2 and half p % 2 for int8)
+	// int4: group 0 wave wm copies digit pieces 0-3 of row block wm, group 1
+	// wave wm pieces 4 and 5 and both 32-input halves of channel-block pair wm
+	// (4 copies per wave in both groups); int8: group 0 wave wm the six digit
+	// pieces of row block wm, group 1 wave wm weight pieces 4 wm .. 4 wm + 3
+	// (channel block p / 2, half p % 2). Weight piece p lands at AST + 1 KiB p.
 	auto issue = [&](int kt) {
 		const unsigned dst = lds0 + (unsigned)((kt % S) * STG);
-		if (g == 0) {
-			const uint8_t *src = gA + (long)wm * kblocks * 3072 + (long)kt * 6144;
+		const uint8_t *src = gA + (long)wm * kblocks * 3072 + (long)kt * 6144;
+		if (BITS == 4) {
+			if (g == 0)
+				for (int i = 0; i < 4; i++) copy_to_lds(src + i * 1024, voff, dst + (wm * 6 + i) * 1024);
+			else {
+				for (int i = 4; i < 6; i++) copy_to_lds(src + i * 1024, voff, dst + (wm * 6 + i) * 1024);
+				for (int i = 0; i < 2; i++)
+					copy_to_lds(gB + (long)wm * kblocks * 1024 + (long)kt * 2048 + i * 1024, voff, dst + AST + (2 * wm + i) * 1024);
+			}
+		} else if (g == 0) {
 			for (int i = 0; i < GA; i++) copy_to_lds(src + i * 1024, voff, dst + (wm * GA + i) * 1024);
 		} else {
 			for (int i = 0; i < GB; i++) {
 				const int p = wm * GB + i;
-				const uint8_t *src = BITS == 4 ? gB + (long)p * kblocks * 512 + (long)kt * 1024
-							       : gB + (long)(p >> 1) * kblocks * 1024 + (p & 1) * 1024 + (long)kt * 2048;
-				copy_to_lds(src, voff, dst + AST + p * 1024);
+				copy_to_lds(gB + (long)(p >> 1) * kblocks * 1024 + (p & 1) * 1024 + (long)kt * 2048, voff, dst + AST + p * 1024);
 			}
 		}
 	};
@@ -868,30 +889,39 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 	for (int l = 0; l < 3; l++)
 		for (int j = 0; j < 4; j++)
 			for (int v = 0; v < 16; v++) acc[l][j][v] = 0;
-	typedef typename std::conditional<BITS == 4, uint2, v4i>::type bfrag;
+	// int4: bf[kk][q] holds the raw bytes of channel-block pair 2 g + q, the
+	// operand of column blocks 2 q + 1 (S1); blo its low nibbles, the operand
+	// of column blocks 2 q (S0), masked one pair ahead
+	constexpr int NBF = BITS == 4 ? 2 : 4;
 	v4i af[2][3];
-	bfrag bf[2][4];
+	v4i bf[2][NBF];
+	v4i blo;
 	auto fread = [&](int kt) {
 		for (int kk = 0; kk < 2; kk++) {
 			const uint8_t *A = lds + (kt % S) * STG + wm * 6144 + kk * 3072 + lane * 16;
 			for (int l = 0; l < 3; l++) af[kk][l] = *(const v4i *)(A + l * 1024);
-			if (BITS == 4) {
-				const uint8_t *B = lds + (kt % S) * STG + AST + g * 4096 + kk * 512 + lane * 8;
-				for (int j = 0; j < 4; j++) bf[kk][j] = *(const bfrag *)(B + j * 1024);
-			} else {
-				const uint8_t *B = lds + (kt % S) * STG + AST + g * 8192 + kk * 1024 + lane * 16;
-				for (int j = 0; j < 4; j++) bf[kk][j] = *(const bfrag *)(B + j * 2048);
-			}
+			const uint8_t *B = lds + (kt % S) * STG + AST + g * (BST / 2) + kk * 1024 + lane * 16;
+			for (int j = 0; j < NBF; j++) bf[kk][j] = *(const v4i *)(B + j * 2048);
 		}
 	};
+	auto mfma = [&](int l, int j, int kk, const v4i &b) {
+		acc[l][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[kk][l], b, acc[l][j], 0, 0, 0);
+	};
 	auto mm = [&]() {
-		for (int kk = 0; kk < 2; kk++)
-			for (int j = 0; j < 4; j++) {
-				v4i wv;
-				if constexpr (BITS == 4) wv = unpack4(bf[kk][j].x, bf[kk][j].y);
-				else wv = bf[kk][j];
-				for (int l = 0; l < 3; l++) acc[l][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[kk][l], wv, acc[l][j], 0, 0, 0);
+		if constexpr (BITS == 4) {
+			for (int i = 0; i < 4; i++) {
+				const int kk = i >> 1, q = i & 1;
+				for (int l = 0; l < 3; l++) mfma(l, 2 * q, kk, blo);
+				if (i + 1 < 4) blo = bf[(i + 1) >> 1][(i + 1) & 1] & 0x0f0f0f0f;
+				for (int l = 0; l < 3; l++) mfma(l, 2 * q + 1, kk, bf[kk][q]);
+				__builtin_amdgcn_sched_group_barrier(0x8, 3, 0); // MFMA
+				if (i + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x2, 4, 0); // VALU: the next mask
+				__builtin_amdgcn_sched_group_barrier(0x8, 3, 0);
 			}
+		} else
+			for (int kk = 0; kk < 2; kk++)
+				for (int j = 0; j < 4; j++)
+					for (int l = 0; l < 3; l++) mfma(l, j, kk, bf[kk][j]);
 	};
 	auto bar = [&]() {
 		__builtin_amdgcn_sched_barrier(0);
@@ -906,8 +936,8 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 	if (g == 1) bar(); // group 1 runs one slot behind
 	for (int kt = 0; kt < nk; kt++) {
 		// reading slot
+		fread(kt); // the LDS reads first: the copies are issued while they land
 		if (kt + S - 1 < nk) issue(kt + S - 1);
-		fread(kt);
 		__builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the fragments are in registers
 		if (kt + 1 < nk) { // this wave's copies of stage kt + 1 have landed (later stages may be in flight)
 			const int later = (kt + S - 1 < nk ? S - 1 : nk - 1 - kt) - 1;
@@ -921,21 +951,30 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 				else wait_vm<2 * GB>();
 			}
 		}
+		if constexpr (BITS == 4) blo = bf[0][0] & 0x0f0f0f0f; // the first mask here, so the first MFMA waits for nothing
 		bar();
 		// multiplying slot
 		mm();
 		bar();
 	}
 	if (g == 0) bar(); // both groups pass the same number of barriers
+	// int4: column block 2 q + 1's sums are (S1 - S0) / 16 (exact), codes without the +8 bias
+	auto tot = [&](int j, int v) {
+		const long long t = combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+		if (BITS == 4 && (j & 1)) return (t - combine(acc[0][j - 1][v], acc[1][j - 1][v], acc[2][j - 1][v])) / 16;
+		return t;
+	};
+	auto totd = [&](int j, int v) {
+		const double t = combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]);
+		if (BITS == 4 && (j & 1)) return (t - combine_d(acc[0][j - 1][v], acc[1][j - 1][v], acc[2][j - 1][v])) * 0.0625;
+		return t;
+	};
 	if constexpr (EPI == 1) {
-		staged_epilogue(a, w, s, m0, c0, wm, g, lane, wave, tid, row != 0, (float *)lds,
-				[&](int j, int v) { return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]); });
+		staged_epilogue<BITS == 4>(a, w, s, m0, c0, wm, g, lane, wave, tid, row != 0, (float *)lds, totd);
 		return;
 	}
-	store_tile<4, false, EPI == 2 ? TGM_TANH : 0>(
-		a, w, s, m0 + wm * 32, c0 + g * 128, lane, tile_rows<4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane),
-		[&](int j, int v) { return combine(acc[0][j][v], acc[1][j][v], acc[2][j][v]); },
-		[&](int j, int v) { return combine_d(acc[0][j][v], acc[1][j][v], acc[2][j][v]); });
+	store_tile<4, false, EPI == 2 ? TGM_TANH : 0, BITS == 4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane,
+								 tile_rows<4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane), tot, totd);
 }
 
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
@@ -1411,14 +1450,21 @@ int launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 // The repacking of tgk_qweight_pack done on the device, from codes already in
 // device memory: one thread per packed byte (and per padded scale), every
 // byte of the packed area written (padding: code 0).
-__global__ __launch_bounds__(256) void qweight_pack_k(uint8_t *pw, float *ps, const uint8_t *codes, const float *scale, int bits,
-						      int axis, int C, int K, int Kp, int Cp)
+__global__ __launch_bounds__(256) void qweight_pack_k(uint8_t *pw, float *ps, uint8_t *pg, const uint8_t *codes, const float *scale,
+						      int bits, int axis, int C, int K, int Kp, int Cp)
 {
-	const long kblocks = Kp / 32, lb = bits == 8 ? 16 : 8, nb = (long)Cp * Kp * bits / 8;
+	const long kblocks = Kp / 32, lb = bits == 8 ? 16 : 8, nb = (long)Cp * Kp * bits / 8, ng = bits == 4 ? nb : 0;
 	tgk_qweight w{};
 	w.orig = (uint8_t *)codes, w.bits = bits, w.axis = axis, w.C = C, w.K = K;
 	auto code = [&](int c, int k) { return c < C && k < K ? code_orig(w, c, k) : 0; };
-	for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < nb + Cp; i += (long)gridDim.x * blockDim.x) {
+	for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < nb + Cp + ng; i += (long)gridDim.x * blockDim.x) {
+		if (i >= nb + Cp) { // int4: the large-batch kernel's copy (channel-block pairs)
+			const long j = i - nb - Cp, frag = j / 1024, pr = frag / kblocks, kb = frag - pr * kblocks;
+			const int lane = (int)((j / 16) & 63), b = (int)(j % 16);
+			const int c = (int)(pr * 64 + (lane & 31)), k = (int)(kb * 32 + (lane >> 5) * 16 + b);
+			pg[j] = (uint8_t)(((unsigned)(code(c, k) + 8) & 15u) | (((unsigned)code(c + 32, k) & 15u) << 4));
+			continue;
+		}
 		if (i >= nb) { // the scales, padded with zeros to Cp
 			const int c = (int)(i - nb);
 			ps[c] = c < C ? scale[c] : 0.0f;
@@ -1436,8 +1482,8 @@ __global__ __launch_bounds__(256) void qweight_pack_k(uint8_t *pw, float *ps, co
 
 size_t tgk_qweight_dev_bytes(int bits, int C, int K)
 {
-	const long Kp = round_up(K, KB), Cp = round_up(C, BN);
-	return (size_t)round_up(Cp * Kp * bits / 8, 256) + (size_t)round_up(Cp * 4, 256);
+	const long Kp = round_up(K, KB), Cp = round_up(C, BN), nb = round_up(Cp * Kp * bits / 8, 256);
+	return (size_t)nb + (size_t)round_up(Cp * 4, 256) + (bits == 4 ? (size_t)nb : 0);
 }
 
 int tgk_qweight_pack_dev(tgk_qweight *w, void *dst, const uint8_t *codes, const float *scale, int bits, int axis, int C, int K,
@@ -1447,12 +1493,14 @@ int tgk_qweight_pack_dev(tgk_qweight *w, void *dst, const uint8_t *codes, const 
 	w->C = C, w->K = K, w->bits = bits, w->axis = axis;
 	w->Kp = (int)round_up(K, KB);
 	w->Cp = (int)round_up(C, BN);
+	const long nb = (long)w->Cp * w->Kp * bits / 8;
 	w->w = (uint8_t *)dst;
-	w->scale = (float *)((uint8_t *)dst + round_up((long)w->Cp * w->Kp * bits / 8, 256));
+	w->scale = (float *)((uint8_t *)dst + round_up(nb, 256));
+	w->wg = bits == 4 ? (uint8_t *)dst + round_up(nb, 256) + round_up((long)w->Cp * 4, 256) : nullptr;
 	w->orig = (uint8_t *)codes;
-	const long n = (long)w->Cp * w->Kp * bits / 8 + w->Cp;
+	const long n = nb + w->Cp + (bits == 4 ? nb : 0);
 	const long blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
-	qweight_pack_k<<<(unsigned)blocks, 256, 0, st>>>(w->w, w->scale, codes, scale, bits, axis, C, K, w->Kp, w->Cp);
+	qweight_pack_k<<<(unsigned)blocks, 256, 0, st>>>(w->w, w->scale, w->wg, codes, scale, bits, axis, C, K, w->Kp, w->Cp);
 	return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -1474,7 +1522,13 @@ int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, i
 		free(hs);
 		return -1;
 	}
-	if (bits == 4) memset(h, 0x88, nb); /* padding codes 0 */
+	uint8_t *hg = bits == 4 ? (uint8_t *)malloc(nb) : nullptr; /* the large-batch kernel's copy */
+	if (bits == 4 && !hg) {
+		free(h);
+		free(hs);
+		return -1;
+	}
+	if (bits == 4) memset(h, 0x88, nb), memset(hg, 0x08, nb); /* padding codes 0 */
 	for (int c = 0; c < C; c++) {
 		for (int k = 0; k < K; k++) {
 			long i = axis == 0 ? (long)c * K + k : (long)k * C + c;
@@ -1492,20 +1546,24 @@ int tgk_qweight_pack(tgk_qweight *w, const uint8_t *codes, const float *scale, i
 				unsigned t = (unsigned)(code + 8);
 				uint8_t *byte = frag + (kb & 7);
 				*byte = kb < 8 ? (uint8_t)((*byte & 0xf0) | t) : (uint8_t)((*byte & 0x0f) | (t << 4));
+				uint8_t *g = hg + (((size_t)(c >> 6) * kblocks + (k >> 5)) * 64 + lane) * 16 + kb;
+				*g = c & 32 ? (uint8_t)((*g & 0x0f) | (((unsigned)code & 15u) << 4)) : (uint8_t)((*g & 0xf0) | t);
 			}
 		}
 		hs[c] = scale[c];
 	}
 	int rc = 0;
 	if (hipMalloc(&w->w, nb) != hipSuccess || hipMalloc(&w->scale, (size_t)w->Cp * sizeof(float)) != hipSuccess ||
-	    hipMalloc(&w->orig, ob) != hipSuccess)
+	    hipMalloc(&w->orig, ob) != hipSuccess || (bits == 4 && hipMalloc(&w->wg, nb) != hipSuccess))
 		rc = -1;
+	if (!rc && bits == 4 && hipMemcpyAsync(w->wg, hg, nb, hipMemcpyHostToDevice, st) != hipSuccess) rc = -1;
 	if (!rc && (hipMemcpyAsync(w->w, h, nb, hipMemcpyHostToDevice, st) != hipSuccess ||
 		    hipMemcpyAsync(w->scale, hs, (size_t)w->Cp * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess ||
 		    hipMemcpyAsync(w->orig, codes, ob, hipMemcpyHostToDevice, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess))
 		rc = -1;
 	free(h);
 	free(hs);
+	free(hg);
 	return rc;
 }
 
@@ -1524,6 +1582,7 @@ int tgk_qweight_pack_i8(tgk_qweight *w, const int8_t *codes, const float *scale,
 void tgk_qweight_free(tgk_qweight *w)
 {
 	if (w->w) (void)hipFree(w->w);
+	if (w->wg) (void)hipFree(w->wg);
 	if (w->scale) (void)hipFree(w->scale);
 	if (w->orig) (void)hipFree(w->orig);
 	memset(w, 0, sizeof *w);
@@ -1599,7 +1658,7 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 int tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
 	const tgk_qweight *w = a->w;
-	if (!w || !w->w || !w->scale || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return 0;
+	if (!w || !w->w || !w->scale || (w->bits == 4 && !w->wg) || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return 0;
 	int Mp = (int)round_up(a->M, BM);
 	Scratch s = carve(scratch, Mp, w->Kp);
 	return w->bits == 8 ? launch_gemm<8>(st, a, s, Mp) : launch_gemm<4>(st, a, s, Mp);
@@ -1637,7 +1696,7 @@ bool tgk_qgemm_fusable(const tgk_qgemm_args *a)
 int tgk_qgemm_fused(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
 	const tgk_qweight *w = a->w;
-	if (!w || !w->w || !w->scale || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return 0;
+	if (!w || !w->w || !w->scale || (w->bits == 4 && !w->wg) || !a->x || !a->o || !scratch || a->M <= 0 || a->ni <= 0) return 0;
 	if (!tgk_qgemm_fusable(a)) {
 		tgk_qgemm_digits(st, a, scratch);
 		return tgk_qgemm_mfma(st, a, scratch);

@@ -121,6 +121,8 @@ typedef struct {
 	int C, K, Kp, bits;      /* channels, inputs, inputs padded to 64 */
 	int Cp;                  /* channels padded to 64 */
 	uint8_t *w;              /* int8: [Cp][Kp]; int4: [Cp][Kp/2] offset-binary nibbles (see kern_qgemm.hip) */
+	uint8_t *wg;             /* int4 only: the large-batch GEMM's copy, [Cp/64][Kp/32][64][16] bytes, each byte two
+				    channels' codes (see kern_qgemm.hip); NULL for int8 */
 	float *scale;            /* [Cp] */
 	uint8_t *orig;           /* original packed codes, for the exact fallback of special rows */
 	int axis;                /* original layout: 0 = [C][K], 1 = [K][C] */
