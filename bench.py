@@ -428,7 +428,7 @@ def config4_leg(args, steps=None, profile=True):
     else:
         roof = {"bound": "valu", "achieved": None, "peak": VALU_PEAK_GINST, "unit": "Ginst/s", "frac": None,
                 "traffic": None, "hbm_frac": round(byts / t / 1e9 / HBM_PEAK_GBS, 5),
-                "kernel": kname + ": rocprofv3 gave no data"}
+                "kernel": kname + (": rocprofv3 gave no data" if profile else ": not profiled (--no-traffic)")}
     cpu = None if args.no_cpu else ref_cpu(text, xq[:131072], 8, 4, 1, auto_threads(), True,
                                            "config 4 (Q16.16 latent reasoner)")
     return {
