@@ -180,12 +180,11 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 	}
 }
 
-// Many rows, 16 per block (twice the blocks of the 32-row kernel below, for
-// batches that would leave the device half idle with 32): lane l of wave w
-// owns row m0 + (l & 15), half (l >> 4) & 1 and parity l >> 5 of 32-input
-// block pairs w, w + W, ... (NKB pairs in registers). In each digit plane a
-// block writes its 16 rows' two 256-byte runs. The row's max, non-finite
-// flag and sum of q are combined through LDS. Results are those of digits_k.
+// Many rows, 16 per block: lane l of wave w owns row m0 + (l & 15), half
+// (l >> 4) & 1 and parity l >> 5 of 32-input block pairs w, w + W, ... (NKB
+// pairs in registers). In each digit plane a block writes its 16 rows' two
+// 256-byte runs. The row's max, non-finite flag and sum of q are combined
+// through LDS. Results are those of digits_k.
 template <int NKB, bool VEC>
 __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
 {
@@ -280,64 +279,6 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 		s.e[m] = E;
 		s.special[m] = special || tgq_peaked(stl[0] + stl[1] + stl[2] + stl[3], K);
 		s.qsum[m] = sqs[0] + sqs[1] + sqs[2] + sqs[3];
-	}
-}
-
-// Many rows of at most 2048 inputs: one block per 32-row block of the digit
-// layout, W = blockDim / 64 waves. Lane l of wave w owns row m0 + (l & 31) and
-// the half (l >> 5) of 32-input blocks w, w + W, ... (NKB of them, held in
-// registers). The block's loads are 128-byte row segments, and each digit
-// plane of a 32-input block is one contiguous 1 KiB store per wave. The
-// row's max, non-finite flag and sum of q are combined through LDS. Results
-// (exponent, digits, sum of q, special) are those of digits_k. VEC: every
-// row unit stride and 16-byte aligned, K a multiple of 16.
-template <int NKB, bool VEC>
-__global__ __launch_bounds__(1024) void digits_tile_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
-{
-	__shared__ float smx[16][64];
-	__shared__ int sbad[16][64];
-	__shared__ long long sqs[16][64], stl[16][64];
-	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
-	const int m0 = blockIdx.x * 32, half = lane >> 5, mr = lane & 31;
-	const float *x = xrow(a, m0 + mr < M ? m0 + mr : M - 1); // rows past M repeat row M - 1
-	const int nkb = Kp / 32;
-	float v[NKB][16];
-	unsigned mb = 0; // max |x| as bits (tgq_scan16)
-	for (int j = 0; j < NKB; j++) {
-		const int kb = w + j * W;
-		load16<VEC>(v[j], x, a.xk, kb < nkb ? kb * 32 + half * 16 : K, K); // past the row: zeros
-	}
-	for (int j = 0; j < NKB; j++)
-		tgq_scan16(v[j], mb);
-	float mx;
-	int bad;
-	tgq_scan_end(mb, mx, bad);
-	smx[w][lane] = mx;
-	sbad[w][lane] = bad;
-	__syncthreads();
-	float amax = 0.0f;
-	bad = 0;
-	for (int u = 0; u < W; u++) {
-		amax = fmaxf(amax, fmaxf(smx[u][mr], smx[u][mr + 32]));
-		bad |= sbad[u][mr] | sbad[u][mr + 32];
-	}
-	const int special = tgq_special(bad, amax), E = tgq_exponent(amax, special);
-	const float band = tgq_band(amax);
-	int8_t *blk = s.dig + (long)blockIdx.x * nkb * 3072 + mr * 16;
-	long long qs = 0, tl = 0;
-	for (int j = 0; j < NKB; j++) {
-		const int kb = w + j * W;
-		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K, band, tl);
-	}
-	sqs[w][lane] = qs;
-	stl[w][lane] = tl;
-	__syncthreads();
-	if (w == 0 && half == 0 && m0 + mr < M) {
-		long long t = 0, u2 = 0;
-		for (int u = 0; u < W; u++) t += sqs[u][mr] + sqs[u][mr + 32], u2 += stl[u][mr] + stl[u][mr + 32];
-		s.e[m0 + mr] = E;
-		s.special[m0 + mr] = special || tgq_peaked(u2, K);
-		s.qsum[m0 + mr] = t;
 	}
 }
 
@@ -1607,10 +1548,15 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 	int Mp = (int)round_up(a->M, BM);
 	const Scratch s = carve(scratch, Mp, w->Kp);
 	const int nkb = w->Kp / 32, M = a->M, K = w->K;
-	if (M >= 512 && M < 8192 && nkb <= 128) { // 16 rows per block: at least 32 (up to 512) blocks of 16 waves
+	if (M >= 512 && nkb <= 128) { // 16 rows per block
 		const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) &&
 				 (K & 15) == 0;
-		const int W = nkb / 2 < 16 ? (nkb + 1) / 2 : 16, nb = (M + 15) / 16, pairs = (nkb + 1) / 2;
+		// 16 waves; 8 for many rows of at most 2048 inputs: then two blocks fit
+		// on a CU (registers), one loading while the other computes and stores
+		// (measured: K = 2048, 65536 rows: 178 us against 235 with one 32-row
+		// block of 16 waves per CU, at a streaming read-then-write floor of 173)
+		const int WM = M >= 8192 && nkb <= 64 ? 8 : 16;
+		const int W = nkb / 2 < WM ? (nkb + 1) / 2 : WM, nb = (M + 15) / 16, pairs = (nkb + 1) / 2;
 		if (pairs <= W) {
 			if (vec) digits_tile16_k<1, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
 			else digits_tile16_k<1, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
@@ -1620,20 +1566,6 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 		} else {
 			if (vec) digits_tile16_k<4, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
 			else digits_tile16_k<4, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
-		}
-	} else if (M >= 512 && nkb <= 64) {
-		const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) &&
-				 (K & 15) == 0;
-		const int W = nkb < 16 ? nkb : 16, nb = (M + 31) / 32;
-		if (nkb <= 16) {
-			if (vec) digits_tile_k<1, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
-			else digits_tile_k<1, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
-		} else if (nkb <= 32) {
-			if (vec) digits_tile_k<2, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
-			else digits_tile_k<2, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
-		} else {
-			if (vec) digits_tile_k<4, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
-			else digits_tile_k<4, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
 		}
 	} else if (M < 512 && w->Kp >= 2048 && w->Kp <= 16384) { // few long rows: a block per row
 		const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) &&
