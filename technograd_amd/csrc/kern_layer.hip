@@ -307,11 +307,12 @@ __global__ void rowop_k(int op, float *o, long ors, tgk_opd a, int nrow, int col
 // cannot change expf(x - mx).
 // sum_i z_i in index order, as the reference's loop: one thread, one add
 // after another (tg_ordered_sum when the line is 16-byte aligned)
+template <bool SQ = false>
 __device__ inline float line_sum(const float *z, int cols)
 {
-	if ((((size_t)z) & 15) == 0) return tg_ordered_sum_pp<6>(z, cols);
+	if ((((size_t)z) & 15) == 0) return tg_ordered_sum_pp<6, SQ>(z, cols);
 	float sum = 0.0f;
-	for (int i = 0; i < cols; i++) sum += z[i];
+	for (int i = 0; i < cols; i++) sum += SQ ? z[i] * z[i] : z[i];
 	return sum;
 }
 
@@ -356,14 +357,8 @@ __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, t
 			*z = *z / lv[e / cols];
 		}
 	} else {
-		// the squares in parallel into a second area, so the ordered chain only adds
-		float *sq = lv + ((lpb + 3) & ~3);
-		for (int e = threadIdx.x; e < tot; e += TPB) {
-			const int l = e / cols, i = e - l * cols;
-			sq[l * stride + i] = lds[l * stride + i] * lds[l * stride + i];
-		}
-		__syncthreads();
-		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = 1.0f / sqrtf(line_sum(sq + threadIdx.x * stride, cols) / (float)cols + 1e-6f);
+		// each square is formed as its value arrives, off the ordered chain of adds
+		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = 1.0f / sqrtf(line_sum<true>(lds + threadIdx.x * stride, cols) / (float)cols + 1e-6f);
 		__syncthreads();
 		for (int e = threadIdx.x; e < tot; e += TPB) {
 			float *z = lds + (e / cols) * stride + e % cols;
@@ -674,8 +669,8 @@ void tgk_rowop(hipStream_t s, int op, float *o, long ors, tgk_opd a, int nrow, i
 	}
 	// lines 16-byte aligned and 4 banks apart when cols is a multiple of 4, else an odd stride
 	const int stride = cols % 4 == 0 ? cols + 4 : cols | 1;
-	// LDS: the lines, one value per line (padded to 4), and for rmsnorm the lines' squares
-	auto lds_bytes = [&](long l) { return ((op == TGM_SOFTMAX ? 1 : 2) * l * stride + ((l + 3) & ~3L)) * 4; };
+	// LDS: the lines and one value per line (padded to 4)
+	auto lds_bytes = [&](long l) { return (l * stride + ((l + 3) & ~3L)) * 4; };
 	int lpb = 32; // a power of two, so TPB / lpb threads share a line's max
 	while (lpb > 1 && (lds_bytes(lpb) > 65536 || nrow % lpb)) lpb >>= 1;
 	while (lpb > 4 && (long)rows * (nrow / lpb) < 512) lpb >>= 1; // few lines: spread them over more blocks

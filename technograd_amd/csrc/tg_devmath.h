@@ -99,7 +99,7 @@ template <int NB> __device__ __attribute__((always_inline)) inline float tg_orde
 // each other: values go through two register buffers of 4 V in turn, the
 // next buffer's 16-byte loads in flight while the current one's adds run (no
 // copy between the buffers, so nothing waits for the loads just issued).
-template <int V> __device__ __attribute__((always_inline)) inline float tg_ordered_sum_pp(const float *z, int n)
+template <int V, bool SQ = false> __device__ __attribute__((always_inline)) inline float tg_ordered_sum_pp(const float *z, int n)
 {
 	constexpr int W = 4 * V; // values per buffer
 	const float4 *z4 = (const float4 *)z;
@@ -109,10 +109,10 @@ template <int V> __device__ __attribute__((always_inline)) inline float tg_order
 	auto add = [&](const float4 *v) {
 #pragma unroll
 		for (int j = 0; j < V; j++) {
-			sum += v[j].x;
-			sum += v[j].y;
-			sum += v[j].z;
-			sum += v[j].w;
+			sum += SQ ? v[j].x * v[j].x : v[j].x;
+			sum += SQ ? v[j].y * v[j].y : v[j].y;
+			sum += SQ ? v[j].z * v[j].z : v[j].z;
+			sum += SQ ? v[j].w * v[j].w : v[j].w;
 		}
 	};
 	if (nb > 0)
@@ -136,7 +136,7 @@ template <int V> __device__ __attribute__((always_inline)) inline float tg_order
 		for (int k = 0; k < W; k++) t[k] = z[i + k < n ? i + k : n - 1];
 #pragma unroll
 		for (int k = 0; k < W; k++)
-			if (i + k < n) sum += t[k];
+			if (i + k < n) sum += SQ ? t[k] * t[k] : t[k];
 	}
 	return sum;
 }
