@@ -62,11 +62,15 @@ constexpr int BN = 256;       // channels per tile of the LDS kernel (weights ar
 
 inline long round_up(long x, long m) { return (x + m - 1) / m * m; }
 
+constexpr int NOUT = 8; // outliers of a split row (the peak test allows at most 8 entries in the band)
+
 struct Scratch {
 	int8_t *dig;       // digits in fragment order (see above)
 	long long *qsum;   // [Mp] sum over k of the row's fixed-point values q
 	int *e;            // [Mp] row exponent E
-	int *special;      // [Mp] 1: the row takes the reference's sequential loop
+	int *special;      // [Mp] 1: the row takes the reference's sequential loop; 2: a split row (split_k)
+	int *ok;           // [Mp][NOUT] a split row's outliers: input index, -1 past the last
+	float *ox;         // [Mp][NOUT] and value
 };
 
 Scratch carve(void *base, int Mp, int Kp)
@@ -80,6 +84,10 @@ Scratch carve(void *base, int Mp, int Kp)
 	s.e = (int *)p;
 	p += (size_t)Mp * sizeof(int);
 	s.special = (int *)p;
+	p += (size_t)Mp * sizeof(int);
+	s.ok = (int *)p;
+	p += (size_t)Mp * NOUT * sizeof(int);
+	s.ox = (float *)p;
 	return s;
 }
 
@@ -282,6 +290,88 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 	}
 }
 
+// Split rows (large batches). A peaked row (tg_qdigits.h) would otherwise
+// take the reference's loop, 2 K operations per output. Instead its band
+// entries (|x| >= max|x| / 4, at most 8) become outliers kept exactly, and the
+// other entries get a grid of their own: E from their largest magnitude, their
+// digits and sum of q rewritten with the band entries as zeros. The epilogue
+// adds sum_o code[c][k_o] x_o (f64, exact products, increasing k) to the grid
+// sum in f64 and rounds once. A wave per flagged row; rows flagged for a
+// non-finite or huge entry keep the reference's loop. Grid-stride: wave v takes
+// rows 64 v .. 64 v + 63, 64 (total waves) further, and so on.
+__global__ __launch_bounds__(256) void split_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
+{
+	const int lane = threadIdx.x & 63, nw = gridDim.x * 4, ng = Kp / 16;
+	for (long base = (long)(blockIdx.x * 4 + (threadIdx.x >> 6)) * 64; base < M; base += (long)nw * 64) {
+		const long mr = base + lane;
+		unsigned long long fl = __ballot(mr < M && s.special[mr] == 1);
+		while (fl) {
+			const int m = (int)(base + __builtin_ctzll(fl));
+			fl &= fl - 1;
+			const float *x = xrow(a, m);
+			unsigned mb = 0;
+			for (int g = lane; g < ng; g += 64) {
+				float v[16];
+				load16<false>(v, x, a.xk, g * 16, K);
+				tgq_scan16(v, mb);
+			}
+			float mx;
+			int bad;
+			tgq_scan_end(mb, mx, bad);
+			const float amax = wave_max(mx);
+			if (tgq_special(__any(bad), amax)) continue; // non-finite or huge: the reference's loop
+			const float band = tgq_band(amax);
+			float rm = 0.0f;
+			int nin = 0;
+			for (int g = lane; g < ng; g += 64) {
+				float v[16];
+				load16<false>(v, x, a.xk, g * 16, K);
+				for (int i = 0; i < 16; i++) {
+					const float u = fabsf(v[i]);
+					if (u >= band && u != 0.0f) nin++;
+					else rm = fmaxf(rm, u);
+				}
+			}
+			const float rmax = wave_max(rm);
+			if (wave_sum((long long)nin) > NOUT) continue; // not a peaked row after all: leave it to the reference's loop
+			const int E = tgq_exponent(rmax, 0);
+			int8_t *blk = tgq_row_base(s.dig, m, Kp);
+			long long qs = 0, tl = 0;
+			int nout = 0;
+			for (int g0 = 0; g0 < ng; g0 += 64) {
+				const int g = g0 + lane;
+				float v[16];
+				load16<false>(v, x, a.xk, g < ng ? g * 16 : K, K); // past the row: zeros
+				unsigned om = 0;
+				for (int i = 0; i < 16; i++) {
+					const float u = fabsf(v[i]);
+					if (u >= band && u != 0.0f) om |= 1u << i;
+				}
+				float r[16];
+				for (int i = 0; i < 16; i++) r[i] = (om >> i) & 1 ? 0.0f : v[i];
+				if (g < ng) qs += tgq_put16(blk, g * 16, r, E, g * 16 >= K, band, tl);
+				// the outliers in input order: an exclusive scan of the lanes' counts
+				const int cnt = __popc(om);
+				int inc = cnt;
+				for (int d = 1; d < 64; d <<= 1) {
+					const int t = __shfl_up(inc, d);
+					if (lane >= d) inc += t;
+				}
+				int at = nout + inc - cnt;
+				for (int i = 0; i < 16; i++)
+					if ((om >> i) & 1) {
+						if (at < NOUT) s.ok[(long)m * NOUT + at] = g * 16 + i, s.ox[(long)m * NOUT + at] = v[i];
+						at++;
+					}
+				nout += __shfl(inc, 63);
+			}
+			qs = wave_sum(qs);
+			if (lane >= nout && lane < NOUT) s.ok[(long)m * NOUT + lane] = -1;
+			if (lane == 0) s.e[m] = E, s.qsum[m] = qs, s.special[m] = 2;
+		}
+	}
+}
+
 __device__ inline int code_orig(const tgk_qweight &w, int c, int k)
 {
 	long i = w.axis == 0 ? (long)c * w.K + k : (long)k * w.C + c;
@@ -428,17 +518,34 @@ __device__ inline void ref_line(const tgk_qgemm_args &a, const tgk_qweight &w, i
 template <int ACT = 0>
 __device__ inline float act_out(float v) { return ACT == TGM_TANH ? tg_uop(TGM_TANH, v) : v; }
 
+// A split row's outlier terms for channel c (m < M, c < C): sum over its
+// outliers, in increasing input order, of code[c][k] x_k in f64 (each
+// product exact), from 0.0
+__device__ inline double outlier_sum(const Scratch &s, const tgk_qweight &w, int m, int c)
+{
+	double t = 0.0;
+	for (int j = 0; j < NOUT; j++) {
+		const int k = s.ok[(long)m * NOUT + j];
+		if (k < 0) break;
+		t += (double)code_orig(w, c, k) * (double)s.ox[(long)m * NOUT + j];
+	}
+	return t;
+}
+
+// special: 0 a grid row, 1 the reference's loop, 2 a split row (the grid
+// sum of its other entries plus its outliers' terms, in f64, rounded once)
 template <int ACT = 0>
-__device__ inline void epilogue_with(const tgk_qgemm_args &a, const tgk_qweight &w, int m, int c, long long tot, int E, int special,
-				     long long qsum)
+__device__ inline void epilogue_with(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot,
+				     int E, int special, long long qsum)
 {
 	if (m >= a.M || c >= w.C) return;
 	float acc32;
-	if (special) { // the reference's sequential loop
+	if (special == 1) { // the reference's sequential loop
 		acc32 = ref_loop(a, w, m, c);
 	} else {
 		if (w.bits == 4) tot -= 8 * qsum;
-		acc32 = (float)ldexp((double)tot, E - 23);
+		const double g = ldexp((double)tot, E - 23);
+		acc32 = (float)(special == 2 ? g + outlier_sum(s, w, m, c) : g);
 	}
 	int r = m / a.ni, jj = m - r * a.ni;
 	*out_at(a, r, jj, c) = act_out<ACT>(w.scale[c] * acc32);
@@ -447,7 +554,7 @@ __device__ inline void epilogue_with(const tgk_qgemm_args &a, const tgk_qweight 
 __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot)
 {
 	if (m >= a.M || c >= w.C) return;
-	epilogue_with(a, w, m, c, tot, s.e[m], s.special[m], s.qsum[m]);
+	epilogue_with(a, w, s, m, c, tot, s.e[m], s.special[m], s.qsum[m]);
 }
 
 // One lane's outputs of a 32-row block: rows mbase + 8 (v / 4) + 4 (lane / 32)
@@ -503,16 +610,16 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 		}
 	auto row_e = [&](int v, int rv) { if constexpr (HOIST) return Ev[v]; else return __shfl(Er, rv); };
 	auto row_q = [&](int v, int rv) { if constexpr (HOIST) return Qv[v]; else return __shfl(Qr, rv); };
-	if (__any(spr)) { // rows of the reference's loop: the others as usual, each special row by the whole wave
+	if (__any(spr)) { // rows of the reference's loop and split rows: the others as usual, each reference-loop row by the whole wave
 		for (int v = 0; v < 16; v++) {
 			const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
 			const int E = __shfl(Er, rv), sp = __shfl(spr, rv);
 			const long long Q = __shfl(Qr, rv);
-			if (!sp)
+			if (sp != 1)
 				for (int j = 0; j < NB; j++) // a pair's odd block has no +8 bias to remove: add it for epilogue_with
-					epilogue_with<ACT>(a, w, m, cbase + j * 32 + r32, tot(j, v) + (PAIRS && (j & 1) ? 8 * Q : 0), E, 0, Q);
+					epilogue_with<ACT>(a, w, s, m, cbase + j * 32 + r32, tot(j, v) + (PAIRS && (j & 1) ? 8 * Q : 0), E, sp, Q);
 		}
-		unsigned long long sm = __ballot(spr) & 0xffffffffull; // lane r (r < 32): row mbase + r
+		unsigned long long sm = __ballot(spr == 1) & 0xffffffffull; // lane r (r < 32): row mbase + r
 		while (sm) {
 			const int rv = __builtin_ctzll(sm);
 			sm &= sm - 1;
@@ -615,16 +722,19 @@ __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 		const int mbase = m0 + wm * 32, r32 = lane & 31, h = lane >> 5;
 		const TileRows<4> t = tile_rows<4>(a, w, s, mbase, c0 + g * 128, lane);
 		for (int v = 0; v < 16; v++) {
-			const int rv = 8 * (v >> 2) + 4 * h + (v & 3);
-			const int E = __shfl(t.Er, rv);
+			const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
+			const int E = __shfl(t.Er, rv), sp = __shfl(t.spr, rv);
 			const double q8 = 8.0 * (double)__shfl(t.Qr, rv); // 0 for int8 weights
-			for (int j = 0; j < 4; j++)
+			for (int j = 0; j < 4; j++) {
+				const int c = c0 + g * 128 + j * 32 + r32;
+				const double gv = ldexp(totd(j, v) - (PAIRS && (j & 1) ? 0.0 : q8), E - 23);
 				L[(wm * 32 + rv) * STR + g * 128 + j * 32 + r32] =
-					t.sc[j] * (float)ldexp(totd(j, v) - (PAIRS && (j & 1) ? 0.0 : q8), E - 23);
+					t.sc[j] * (float)(sp == 2 && c < w.C ? gv + outlier_sum(s, w, m, c) : gv); // split rows (m < M: sp is 0 past M)
+			}
 		}
 	}
 	// a wave takes lines wave, wave + 8, ... (16 of them), 64 channels at a time
-	const int spl = lane < 16 && wave + 8 * lane < nl ? s.special[m0 + wave + 8 * lane] : 0;
+	const int spl = lane < 16 && wave + 8 * lane < nl ? s.special[m0 + wave + 8 * lane] == 1 : 0;
 	__syncthreads();
 	if (__any(spl)) // lines of the reference's loop: their products, a wave per line
 		for (int i = 0; i < 16; i++)
@@ -1300,7 +1410,7 @@ __global__ __launch_bounds__(256) void gemv1_k(tgk_qgemm_args a, tgk_qweight w, 
 	int p3[3] = { 0, 0, 0 };
 	for (int u = 0; u < 4; u++)
 		for (int l = 0; l < 3; l++) p3[l] += red[u][lane >> 1][lane & 1][l];
-	epilogue_with(a, w, 0, t * 16 + lane, combine(p3[0], p3[1], p3[2]), E, special, qsum);
+	epilogue_with(a, w, s, 0, t * 16 + lane, combine(p3[0], p3[1], p3[2]), E, special, qsum);
 }
 
 // gemv1_k for a single row of int4 weights: NL 16-byte weight loads per lane,
@@ -1532,7 +1642,7 @@ void tgk_qweight_free(tgk_qweight *w)
 size_t tgk_qgemm_scratch(int M, int Kp)
 {
 	long Mp = round_up(M, BM);
-	return (size_t)Mp * Kp * 3 + (size_t)Mp * (sizeof(long long) + 2 * sizeof(int)) + 256;
+	return (size_t)Mp * Kp * 3 + (size_t)Mp * (sizeof(long long) + 2 * sizeof(int) + NOUT * (sizeof(int) + sizeof(float))) + 256;
 }
 
 tgk_qdig tgk_qgemm_digit_area(void *scratch, int M, int Kp)
@@ -1585,6 +1695,10 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 		digits_k<1><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
 	else
 		digits_k<4><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
+	if (M >= TGK_SPLIT_ROWS) { // large batches: peaked rows split (small batches keep the reference's loop for them)
+		const long waves = (M + 63) / 64;
+		split_k<<<(unsigned)(waves / 4 < 1024 ? (waves + 3) / 4 : 1024), 256, 0, st>>>(*a, s, K, w->Kp, M);
+	}
 }
 
 int tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)

@@ -270,6 +270,10 @@ typedef struct {
 bool tgk_qgemm_fusable(const tgk_qgemm_args *a);
 int tgk_qgemm_fused(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 size_t tgk_qgemm_scratch(int M, int Kp);
+/* batches of at least this many rows split their peaked rows (an exact
+ * outlier term plus a grid of their own) instead of taking the reference's
+ * loop for them (kern_qgemm.hip: split_k) */
+#define TGK_SPLIT_ROWS 16384
 int tgk_qgemm(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 /* the digit area tgk_qgemm uses in `scratch` for M rows of Kp inputs, for
  * kernels that write a GEMM's activation digits themselves (tg_qdigits.h)

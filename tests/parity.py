@@ -130,7 +130,7 @@ def peaked_rows(x_mk):
     return (below > 0) & (inb <= (8 if K >= 32 else max(1, K >> 2)))
 
 
-def digit_path_matmul(x_mk, codes_kc, scale_c, peak=True):
+def digit_path_matmul(x_mk, codes_kc, scale_c, peak=True, f64=False):
     """The matrix-core path's arithmetic, restated on the host (not the
     reference's order): per row, E from max |x| (frexp; raised by one when
     rint(max |x| 2^(23-E)) > 8355328), q = rint(x 2^(23-E)) exactly, the exact
@@ -139,6 +139,7 @@ def digit_path_matmul(x_mk, codes_kc, scale_c, peak=True):
     rows (peaked_rows), are special: the device runs the reference's loop for
     them (reference_loop); they are returned masked. peak=False leaves peaked
     rows on the grid (the path before the peak test; tests plant it).
+    f64: return the grid sums t 2^(E-23) unrounded (scale_c not applied).
     Returns (f32 [M, C], special [M])."""
     x = np.asarray(x_mk, np.float32)
     amax = np.abs(x).max(axis=1)
@@ -152,6 +153,8 @@ def digit_path_matmul(x_mk, codes_kc, scale_c, peak=True):
     xs = np.where(special[:, None], 0, x).astype(np.float64)
     q = np.rint(np.ldexp(xs, (23 - E)[:, None]))                        # exact integers, |q| < 2^23
     t = q @ np.asarray(codes_kc, np.float64)                              # exact: every partial sum < 2^53
+    if f64:
+        return np.ldexp(t, (E - 23)[:, None]), special
     v = np.ldexp(t, (E - 23)[:, None]).astype(np.float32)                 # one rounding to f32
     return (v * np.asarray(scale_c, np.float32)[None, :]).astype(np.float32), special
 
@@ -169,12 +172,49 @@ def reference_loop(x_mk, codes_kc, scale_c):
         return acc * np.asarray(scale_c, np.float32)[None, :]
 
 
-def device_path_matmul(x_mk, codes_kc, scale_c, peak=True):
+def split_rows_matmul(x_mk, codes_kc, scale_c):
+    """Split rows (technograd_amd/csrc/kern_qgemm.hip: split_k, batches of
+    TGK_SPLIT_ROWS rows or more): a peaked row's band entries (|x| >=
+    max|x| / 4, nonzero) are outliers; the other entries are put on a grid of
+    their own (E from their largest magnitude, as digit_path_matmul); each
+    output is f32(g + o) * s[c] with g = t 2^(E-23) the grid sum and
+    o = sum over the outliers in increasing k of code[k, c] x_k, both in f64
+    (every product exact, o summed from 0.0 in k order)."""
+    x = np.asarray(x_mk, np.float32)
+    codes = np.asarray(codes_kc, np.float64)
+    a = np.abs(x)
+    amax = a.max(axis=1)
+    band = np.ldexp(amax, np.int32(-2)).astype(np.float32)
+    inb = (a >= band[:, None]) & (a != 0)
+    rest = np.where(inb, np.float32(0), x)
+    g, _ = digit_path_matmul(rest, codes_kc, np.ones(codes.shape[1], np.float32), peak=False, f64=True)
+    out = np.empty((x.shape[0], codes.shape[1]), np.float32)
+    for m in range(x.shape[0]):
+        o = np.zeros(codes.shape[1])
+        for k in np.flatnonzero(inb[m]):
+            o = o + codes[k] * np.float64(x[m, k])
+        out[m] = (g[m] + o).astype(np.float32) * np.asarray(scale_c, np.float32)
+    return out
+
+
+def device_path_matmul(x_mk, codes_kc, scale_c, peak=True, split=False):
     """What the device computes for x @ W: the digit path, and the reference's
-    loop for special rows. Returns (f32 [M, C], special [M])."""
+    loop for special rows; with split (batches of TGK_SPLIT_ROWS rows or
+    more) peaked rows that are finite and at most 2^100 are split rows
+    instead (split_rows_matmul). Returns (f32 [M, C], special [M]): special
+    marks the rows off the plain grid."""
     got, special = digit_path_matmul(x_mk, codes_kc, scale_c, peak)
     if special.any():
-        got[special] = reference_loop(np.asarray(x_mk, np.float32)[special], codes_kc, scale_c)
+        x = np.asarray(x_mk, np.float32)
+        ref = special.copy()
+        if split:
+            amax = np.abs(x).max(axis=1)
+            sp = special & ~np.isnan(x).any(axis=1) & (amax <= np.float32(2.0 ** 100))
+            if sp.any():
+                got[sp] = split_rows_matmul(x[sp], codes_kc, scale_c)
+            ref &= ~sp
+        if ref.any():
+            got[ref] = reference_loop(x[ref], codes_kc, scale_c)
     return got, special
 
 

@@ -11,7 +11,7 @@ import pytest
 from oracle import oracle as O
 from technograd_amd import synth
 from parity import (check_qmatmul, device_path_matmul, digit_path_matmul, grid_bound, outlier_rows, peaked_rows,
-                    reference_loop, ulp)
+                    qmatmul_truth, reference_loop, ulp)
 
 
 def _case(seed, M=7, K=96, C=40, lim=7):
@@ -78,6 +78,46 @@ def test_outlier_rows_against_the_oracle(bits):
     coarse, _ = device_path_matmul(x, codes, scales, peak=False)
     with pytest.raises(AssertionError):
         check_qmatmul(coarse, ref, codes.T, scales, x)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_split_rows_against_the_oracle(bits):
+    """The split of peaked rows (large batches): the same outlier rows through
+    split_rows_matmul pass the parity predicate against the oracle, and each
+    split row is within its own grid's bound of the exact product (the grid
+    set by the entries below the band, not by the outlier), plus one f32
+    rounding."""
+    K, C = 4096, 256
+    lim = 7 if bits == 4 else 127
+    rng = np.random.default_rng(bits + 10)
+    codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)
+    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
+    x, want_special = outlier_rows(K, codes)
+    text = synth.linear_tgir_codes("lq", codes, scales, bits, axis=1)
+    ref, _ = O.Model(text).batch(x)
+    got, special = device_path_matmul(x, codes, scales, split=True)
+    assert np.array_equal(special, want_special)
+    check_qmatmul(got, ref, codes.T, scales, x)
+    truth, _ = qmatmul_truth(codes.T, scales, x)
+    rest = np.where(np.abs(x) >= np.ldexp(np.abs(x).max(axis=1), -2)[:, None], 0, x)
+    bound = grid_bound(codes.T, scales, rest) + np.abs(truth) * 2.0 ** -23
+    assert (np.abs(got[special] - truth[special]) <= bound[special]).all()
+
+
+def test_split_hand_case():
+    """integers: the rest's grid holds them exactly and the outlier term is
+    exact, so a split row's output is the exact product rounded once"""
+    x = np.zeros((1, 40), np.float32)
+    x[0, :39] = np.arange(1, 40) % 7 - 3
+    x[0, 39] = 1000.0
+    codes = (np.arange(40 * 3).reshape(40, 3) % 5 - 2).astype(np.int8)
+    assert peaked_rows(x).all()
+    got, special = device_path_matmul(x, codes, np.ones(3, np.float32), split=True)
+    want = (x.astype(np.float64) @ codes.astype(np.float64)).astype(np.float32)
+    assert special.all() and np.array_equal(got, want)
+    # without the split the same row takes the reference's loop
+    got0, _ = device_path_matmul(x, codes, np.ones(3, np.float32))
+    assert np.array_equal(got0, reference_loop(x, codes, np.ones(3, np.float32)))
 
 
 def test_hand_cases():

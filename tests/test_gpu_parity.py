@@ -273,6 +273,49 @@ def test_outlier_rows_follow_reference(bits_, M):
           flush=True)
 
 
+@pytest.mark.parametrize("bits_", [4, 8])
+def test_split_rows_in_large_batches(bits_):
+    """M = 16384 (TGK_SPLIT_ROWS): the same outlier rows among N(0, 1) rows
+    are split (their band entries as exact outlier terms, a grid of their own
+    for the rest), bit-identical with the host restatement
+    (parity.device_path_matmul with split) and within the parity predicate
+    against the oracle; rows with a NaN or an infinity keep the reference's
+    loop, bit-identical with the oracle."""
+    print("case split rows", bits_, flush=True)
+    M, K, C = 16384, 1024, 1024
+    lim = 7 if bits_ == 4 else 127
+    rng = np.random.default_rng(40 + bits_)
+    codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)
+    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
+    xo, sp = parity.outlier_rows(K, codes, seed=bits_)
+    x = rng.normal(size=(M, K)).astype(np.float32)
+    at = np.linspace(3, M - 4, len(xo)).astype(int)
+    x[at] = xo
+    x[1, 17], x[M - 2, 5] = np.nan, np.inf
+    if bits_ == 4:
+        flat = codes.ravel().astype(np.int64)
+        packed = ((flat[0::2] & 15) | ((flat[1::2] & 15) << 4)).astype(np.uint8).view(np.int8)
+    else:
+        packed = codes.ravel()
+    got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
+    sub = np.concatenate([at, [1, M - 2], rng.choice(M, 6, replace=False)])
+    want, special = parity.device_path_matmul(x[sub], codes, scales, split=True)
+    assert special[:len(at)].tolist() == sp.tolist() and special[len(at):len(at) + 2].all()
+    def same(a, b):  # NaN where the other is NaN (payloads aside), the other elements bit for bit
+        na, nb = np.isnan(a), np.isnan(b)
+        return np.array_equal(na, nb) and np.array_equal(bits(a[~na]), bits(b[~nb]))
+
+    assert same(got[sub], want)
+    text = synth.linear_tgir_codes("lq", codes, scales, bits_, axis=1)
+    ref, _ = O.Model(text).batch(x[sub], threads=16)
+    assert same(got[[1, M - 2]], ref[len(at):len(at) + 2])
+    keep = np.ones(len(sub), bool)
+    keep[len(at):len(at) + 2] = False
+    frac, ng, nr = parity.check_qmatmul(got[sub][keep], ref[keep], codes.T, scales, x[sub][keep])
+    print("split rows: %.4f by the normalized clause; largest normalized error: GPU %.2f, reference %.2f" % (frac, ng, nr),
+          flush=True)
+
+
 def _f32_matmul_models():
     rng = np.random.default_rng(31)
     W1 = rng.normal(size=(150, 260)).astype(np.float32)
