@@ -10,13 +10,19 @@
 // the channel scale in f32 like the reference. The only approximation is the
 // 24-bit activation grid (error <= 2^-24 max|x| per element), far below the
 // reference's own f32 summation error at these K. Every step depends on the
-// row alone, so a row's outputs do not depend on the batch it came in.
+// row alone, so a row's outputs do not depend on the batch it came in, with
+// one exception: peaked rows (below).
 //
 // Rows with a non-finite or huge entry, and peaked rows (a few entries far
 // above all others, tg_qdigits.h), are flagged by the digit kernel and their
 // outputs are recomputed in the epilogue with the reference's exact
 // sequential f32 loop, so inf/nan propagate as they do in the reference and
-// an outlier does not coarsen the other entries of its row.
+// an outlier does not coarsen the other entries of its row. In batches of
+// TGK_SPLIT_ROWS rows or more, peaked rows are split instead (split_k): the
+// outliers as exact terms, the rest on a grid of its own; a peaked row's
+// outputs then differ from those of the same row in a smaller batch (both
+// within the parity predicate; only the smaller batch's are the reference's
+// bits).
 //
 // Operand layouts in global memory are the MFMA fragment order of
 // v_mfma_i32_32x32x32_i8 (lane l holds row or channel l % 32 and inputs
@@ -1695,10 +1701,17 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 		digits_k<1><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
 	else
 		digits_k<4><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
-	if (M >= TGK_SPLIT_ROWS) { // large batches: peaked rows split (small batches keep the reference's loop for them)
-		const long waves = (M + 63) / 64;
-		split_k<<<(unsigned)(waves / 4 < 1024 ? (waves + 3) / 4 : 1024), 256, 0, st>>>(*a, s, K, w->Kp, M);
-	}
+	tgk_qgemm_split(st, a, scratch);
+}
+
+void tgk_qgemm_split(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
+{
+	const tgk_qweight *w = a->w;
+	const int M = a->M;
+	if (!w || !a->x || !scratch || M < TGK_SPLIT_ROWS || a->ni <= 0 || w->K <= 0) return; // small batches keep the reference's loop
+	const Scratch s = carve(scratch, (int)round_up(M, BM), w->Kp);
+	const long waves = (M + 63) / 64;
+	split_k<<<(unsigned)(waves / 4 < 1024 ? (waves + 3) / 4 : 1024), 256, 0, st>>>(*a, s, w->K, w->Kp, M);
 }
 
 int tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)

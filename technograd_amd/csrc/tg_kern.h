@@ -288,6 +288,11 @@ tgk_qdig tgk_qgemm_digit_area(void *scratch, int M, int Kp);
 #define TGK_DID_ROWOP 2
 void tgk_qgemm_chain(hipStream_t s, const tgk_qgemm_args *a);
 void tgk_qgemm_digits(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
+/* the split of peaked rows (TGK_SPLIT_ROWS) over digits already in the
+ * scratch (tgk_qgemm_digits runs it itself; producers that write the digits
+ * of a materialised activation in their own kernels call it before the
+ * GEMM); a no-op for smaller batches */
+void tgk_qgemm_split(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 int tgk_qgemm_mfma(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 
 /* ---- row-program interpreter (kern_rowprog.hip) ---- */
