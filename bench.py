@@ -36,9 +36,13 @@ CPU the process may run on), median of three runs over a sample of rows of
 the same layer; value = compute time, wall_value = input load to last write;
 falls back to the oracle restatement when the reference build is absent.
 
-legs: config 1 (int8 MLP, 65,536 rows) and config 4 (Q16.16 latent
-reasoner, 1,048,576 rows), three passes each, with their own roofline
-(config 4: VALU instructions from rocprofv3 SQ_INSTS_VALU) and CPU baseline.
+legs: config 1 (int8 MLP, 65,536 rows), config 4 (Q16.16 latent
+reasoner, 1,048,576 rows), config 5 (selective SSM, 4096 sequences) and
+config 3 (Qwen3-shaped decoder: 64 prompts of 512 tokens, 128 generated
+tokens each), each with its own roofline (config 1: calibrated HBM traffic
+of its GEMMs from rocprofv3 FETCH_SIZE and WRITE_SIZE; config 4: VALU
+instructions from SQ_INSTS_VALU) and CPU baseline; a leg that fails is
+reported as {"error": ...} in its place.
 """
 import argparse
 import csv
@@ -166,7 +170,13 @@ def profile_child(mode):
     from technograd_amd import hip, synth
     hip.init(0)
     fprog, fin, fout = None, None, None
-    if mode == "c2":
+    if mode == "c1":
+        text, X = synth.config1(65536)
+        prog = hip.Program(text, max_rows=65536)
+        d_x = hip.DeviceBuffer.from_array(X)
+        d_y = hip.DeviceBuffer(65536 * 512 * 4)
+        calls = [(65536, lambda: prog.batch_device(d_x.ptr, 65536, d_y.ptr))] * 2
+    elif mode == "c2":
         text, X = setup(synth)
         prog = hip.Program(text, max_rows=4096)
         d_x = hip.DeviceBuffer.from_array(X)
@@ -296,7 +306,27 @@ def profile_c2(alg_bytes):
     return res, note
 
 
-def config1_leg(args, steps=None):
+def profile_c1():
+    """Calibrated HBM traffic of config 1's three GEMMs in one pass (FETCH_SIZE
+    and WRITE_SIZE of its qgemm_k dispatches, averaged over two passes, each
+    after a flush pass), or None."""
+    if not shutil.which("rocprofv3"):
+        return None
+    out = tempfile.mkdtemp(prefix="tgprof")
+    try:
+        fe = profiled(["--pmc", "FETCH_SIZE"], "c1", out, "fetch")
+        wr = profiled(["--pmc", "WRITE_SIZE"], "c1", out, "write") if fe else None
+    except subprocess.TimeoutExpired:
+        return None
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+    if not fe or not wr or len(fe[0]) != 2 or len(wr[0]) != 2:
+        return None
+    tr, _, _ = calibrated_traffic(fe, wr)
+    return sum(sum(v for k, v in per.items() if k.startswith("qgemm_k")) for _, per in tr) / 2
+
+
+def config1_leg(args, steps=None, profile=True):
     """Config 1: int8 MLP 512 -> 2048 -> 2048 -> 512 (tanh, tanh, rmsnorm), 65,536
     rows in one device pass. roofline: the three quantized GEMMs, 12.58 M
     algorithmic ops per row, against 5000 TOP/s dense int8."""
@@ -330,11 +360,14 @@ def config1_leg(args, steps=None):
     st = tprog.stats()
     mfma_us, dig_us, oth_us = (v / 3 * 1e3 for v in (st.qgemm_ms, st.digits_ms, st.other_ms))
     ops = 2.0 * (2048 * 512 + 2048 * 2048 + 512 * 2048) * rows
+    # the GEMMs' algorithmic bytes: int8 weights and scales once, f32 activations in and outputs out of each
+    alg_bytes = (2048 * 512 + 2048 * 2048 + 512 * 2048) + 4 * (2048 + 2048 + 512) + 4 * rows * (512 + 2048 + 2048 + 2048 + 2048 + 512)
     log("config 1: %.2f ms per pass: GEMMs %.0f us, digits %.0f us, other %.0f us" % (
         elapsed / steps * 1e3, mfma_us, dig_us, oth_us))
     cpu = None if args.no_cpu else ref_cpu(text, X[:2048], 512, 512, 0, auto_threads(), False,
                                            "config 1 (int8 MLP 512-2048-2048-512)")
     frac = ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS
+    traffic = profile_c1() if profile else None
     return {
         "metric": "config 1 int8 MLP rows/sec at 1 GPU; % of int8-MFMA roofline", "value": round(rows * steps / elapsed, 1),
         "unit": "rows/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
@@ -342,7 +375,11 @@ def config1_leg(args, steps=None):
         "dtype": "W8A32", "data": "synthetic (rand(1, 0.05) weights quantized int8 RTN, N(0,1) rows seed 0)",
         "config": {"workload": "config 1: int8 MLP 512-2048-2048-512, tanh, rmsnorm; 65,536 rows per step"},
         "roofline": {"bound": "mfma", "achieved": round(ops / mfma_us / 1e6, 2), "peak": MFMA_I8_PEAK_TOPS,
-                     "unit": "TOP/s", "frac": round(frac, 4), "traffic": None,
+                     "unit": "TOP/s", "frac": round(frac, 4), "traffic": None if traffic is None else round(traffic),
+                     "traffic_note": "calibrated FETCH_SIZE + WRITE_SIZE of the pass's qgemm_k dispatches (rocprofv3)"
+                                     if traffic is not None else ("not profiled (--no-traffic)" if not profile else
+                                                                  "rocprofv3 gave no data"),
+                     "alg_bytes_per_pass": alg_bytes,
                      "limb_factor": 3, "hw_mfma_frac": round(3 * frac, 4),
                      "kernel": "the three quantized GEMMs of a pass (qgemm_k<8>), summed",
                      "alg_ops_per_launch": ops, "avg_kernel_us": round(mfma_us, 1)},
@@ -352,7 +389,7 @@ def config1_leg(args, steps=None):
 
 
 def bench_config1(args):
-    print(json.dumps(config1_leg(args)), flush=True)
+    print(json.dumps(config1_leg(args, profile=not args.no_traffic)), flush=True)
 
 
 VALU_PEAK_GINST = 256 * 2.4  # wave64 VALU instructions per ns: one per CU per clock (4 SIMDs, 4 clocks each), 2.4 GHz
@@ -456,6 +493,10 @@ def q3_macs_per_token(L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, T=512):
 
 
 def bench_config3(args):
+    print(json.dumps(config3_leg(args)), flush=True)
+
+
+def config3_leg(args):
     """Config 3, prefill: the Qwen3-0.6B-shaped int4 decoder at fixed T = 512
     over 64 prompts of uniform token ids, one device pass; each sequence's
     output is its last position's 151,936 logits (the importer's graph,
@@ -572,10 +613,16 @@ def bench_config3(args):
         "cpu_baseline": cpu,
         "breakdown_us": {"projections": round(mfma_us, 1), "digits": round(dig_us, 1), "other": round(oth_us, 1)},
     }
-    print(json.dumps(out), flush=True)
+    d_x.free()
+    d_y.free()
+    return out
 
 
 def bench_config5(args):
+    print(json.dumps(config5_leg(args)), flush=True)
+
+
+def config5_leg(args):
     """Config 5: int8 selective-SSM classifier (4 blocks, d_model 256, state 16,
     expand 2, T = 512) over 4096 sequences in device passes of `pass_rows`
     sequences. roofline: the int8 projections, 2 x 426 K MACs per step per
@@ -639,7 +686,11 @@ def bench_config5(args):
         "cpu_baseline": cpu,
         "breakdown_us": {"projections": round(mfma_us, 1), "digits": round(dig_us, 1), "other": round(oth_us, 1)},
     }
-    print(json.dumps(out), flush=True)
+    for o in (prog, tprog):
+        o.close()
+    for b in (d_x, d_y):
+        b.free()
+    return out
 
 
 def main():
@@ -650,12 +701,12 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=2048, help="config 2 rows of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 runs (kernel trace and counters)")
-    ap.add_argument("--no-legs", action="store_true", help="skip the config 1 and config 4 legs")
+    ap.add_argument("--no-legs", action="store_true", help="skip the config 1, 4, 5 and 3 legs")
     ap.add_argument("--reps", type=int, default=10, help="kernel-timing repetitions per batch")
     ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
                     help="BASELINE configuration: 2 (default, the headline metric), 1 (int8 MLP), 3 (Qwen3-shaped "
                          "decoder, prefill), 4 (Q16.16 reasoner), 5 (selective-SSM classifier)")
-    ap.add_argument("--profile-child", choices=("c2", "c4"), help=argparse.SUPPRESS)
+    ap.add_argument("--profile-child", choices=("c1", "c2", "c4"), help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.profile_child:
         profile_child(args.profile_child)
@@ -794,7 +845,15 @@ def main():
 
     legs = None
     if not args.no_legs:
-        legs = {"config1": config1_leg(args, steps=3), "config4": config4_leg(args, steps=3, profile=not args.no_traffic)}
+        def leg(f, *a, **k):  # a failing leg is reported in its place, the headline line still printed
+            try:
+                return f(*a, **k)
+            except Exception as e:  # noqa: BLE001
+                log("leg %s failed: %r" % (f.__name__, e))
+                return {"error": repr(e)}
+        legs = {"config1": leg(config1_leg, args, steps=3, profile=not args.no_traffic),
+                "config4": leg(config4_leg, args, steps=3, profile=not args.no_traffic),
+                "config5": leg(config5_leg, args), "config3": leg(config3_leg, args)}
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
