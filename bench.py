@@ -713,7 +713,7 @@ def main():
         return
     if args.gpus != 1:
         print("bench.py: this backend runs on one GPU per process and this build measures one GPU only; "
-              "rows shard across GPUs with no collective (see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "rows shard across GPUs with no collective. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if args.config != 2:
         {1: bench_config1, 3: bench_config3, 4: bench_config4, 5: bench_config5}[args.config](args)

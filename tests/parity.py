@@ -12,8 +12,9 @@ a few percent of outputs), when the GPU result is accurate against a truth:
 - a single quantized product: within N0 = 4 units of the scale at which any
   f32 evaluation of the sum rounds, of the exact product (f64):
       |gpu - truth| <= 4 * 2^-24 * sum_k |s w_k x_k| + ulp(truth).
-  This is SURVEY H1's normalized error; the reference's sequential sum is
-  guaranteed only within K such units and typically lands within 1.
+  This is the normalized error of the sum's forward error analysis; the
+  reference's sequential sum is guaranteed only within K such units and
+  typically lands within 1.
 - a whole model: truth = the oracle's interpreter in double precision
   (oracle/vm64.c: every op of the model in the same order, rounded to
   double); the GPU's largest error on an output row may be at most twice the

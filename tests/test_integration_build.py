@@ -1,4 +1,4 @@
-"""The reference-side bindings INTEGRATION.md shows compile against the
+"""Reference-side bindings of the tg_hip C ABI compile against the
 reference's own declarations (src/tg.h, runtime/tg_rt.h) with the
 reference's compiler flags (-std=c11 -Wall -Wextra -Wpedantic, Makefile:2)
 and include/tg_hip.h: the batch block loop of section 1 (the model written
