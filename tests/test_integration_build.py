@@ -1,11 +1,11 @@
 """Reference-side bindings of the tg_hip C ABI compile against the
 reference's own declarations (src/tg.h, runtime/tg_rt.h) with the
 reference's compiler flags (-std=c11 -Wall -Wextra -Wpedantic, Makefile:2)
-and include/tg_hip.h: the batch block loop of section 1 (the model written
-to memory with ir_write through open_memstream, which needs the POSIX
-feature macro under -std=c11), the per-instruction offload of section 2
-(tg_hip_matmul_qa / tg_hip_matmul_qb with tg_matmul_qa / qb's argument
-lists), the surface front end (section 7) and quantization (section 8a).
+and include/tg_hip.h: the batch block loop (the model written to memory
+with ir_write through open_memstream, which needs the POSIX feature macro
+under -std=c11), the per-instruction offload (tg_hip_matmul_qa /
+tg_hip_matmul_qb with tg_matmul_qa / qb's argument lists), the surface front
+end and quantization.
 The file only has to compile: it is not linked (no GPU, no reference
 build). Skipped where the reference sources are absent."""
 import os
@@ -27,7 +27,7 @@ BINDINGS = r"""
 #include "tg_hip.h"
 #include "tg_rt.h"
 
-/* section 1: the model of a stateless batch on the device, or NULL (CPU path) */
+/* tgc batch: the model of a stateless batch on the device, or NULL (CPU path) */
 tg_hip_prog *bind_load(const Module *m, int block)
 {
 	tg_hip_prog *hp = NULL;
@@ -45,13 +45,13 @@ tg_hip_prog *bind_load(const Module *m, int block)
 	return hp;
 }
 
-/* section 1: one block of rows */
+/* tgc batch: one block of rows */
 void bind_block(tg_hip_prog *hp, const float *all, int per, int b0, int cnt, float *out, int *steps)
 {
 	if (tg_hip_batch(hp, all + (size_t)b0 * (size_t)per, cnt, out, steps) != 0) die(NULL, 0, "GPU batch: %s", tg_hip_error());
 }
 
-/* section 2: the quantized matmul of src/vm.c:277-281, the function name swapped */
+/* per-instruction offload: the quantized matmul of src/vm.c:277-281, the function name swapped */
 void bind_matmul(float *o, const float *a, const float *c, const signed char *qa, int qabits, const float *qas,
 		 const signed char *qb, int qbbits, const float *qbs, int mm, int kk, int nn, int left)
 {
@@ -62,7 +62,7 @@ void bind_matmul(float *o, const float *a, const float *c, const signed char *qa
 	}
 }
 
-/* section 7: a surface model straight to the device */
+/* a surface model straight to the device */
 tg_hip_prog *bind_surface(const char *path, int block)
 {
 	char *txt = tg_hip_surface_to_tgir(path);
@@ -71,7 +71,7 @@ tg_hip_prog *bind_surface(const char *path, int block)
 	return hp;
 }
 
-/* section 8a: tgc quantize on the backend */
+/* tgc quantize on the backend */
 int bind_quantize(const Module *m, int bits, int gptq, const float *rows, long nrows, int min_size, FILE *out)
 {
 	char *txt = NULL;
