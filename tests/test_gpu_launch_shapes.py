@@ -16,6 +16,8 @@ pytestmark = pytest.mark.gpu
 SHAPES = [
     (4, 1024, 256, 4096),  # qgemm_k: 128 x 256 tiles, 128 of them
     (8, 1024, 320, 4096),  # qgemm_k, int8 weights, K not a multiple of 64
+    (4, 4000, 300, 1000),  # qgemm_k, int4 channel pairs: rows, K and channels not multiples of 128, 64 and 64
+    (4, 2100, 512, 4000),  # qgemm_k, int4: the last pair's second block all padding
     (4, 256, 4096, 4096),  # qgemv_k NB=4 W=4
     (4, 256, 2048, 4096),  # NB=4 W=2
     (8, 256, 512, 4096),   # NB=4 W=1
