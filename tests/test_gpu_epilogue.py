@@ -1,5 +1,5 @@
 """GEMM epilogue chains (technograd_amd/csrc/tg_hip.cpp: epi_chain,
-kern_qgemm.hip: finish, rowf_epilogue): the instructions right after a
+kern_qgemm.hip: staged_epilogue): the instructions right after a
 quantized product that only read its results (bias and residual adds,
 scalings, activations, then a softmax or rmsnorm over the channels) run in
 the product's own kernel. The values must be those of the same instructions
@@ -9,7 +9,8 @@ and the two outputs are compared. The row op runs inside the large-batch GEMM
 when a tile holds whole lines (C <= 256, channel stride 1) and after it
 otherwise; the cases cover both, every other GEMM kernel (one row, up to 16
 rows, the small-batch tiles), int4 and int8 weights, both operand orders,
-all three operand forms, and rows the reference's loop takes (inf, nan)."""
+all three operand forms, rows the reference's loop takes (inf, nan), and a
+peaked line (an outlier), which batches of 16384 lines or more split."""
 import numpy as np
 import pytest
 
@@ -64,10 +65,11 @@ def _case(params, inputs, body, out, shape_of_product, x, fused_ins):
 
 def _rows(seed, rows, per, specials=False):
     x = synth.normal(seed, 1.0, rows * per).reshape(rows, per)
-    if specials and rows > 3:
+    if specials and rows > 4:
         x[1, 5] = np.inf
         x[2, 7] = np.nan
         x[3, :] *= 1e-30
+        x[4, 10] = 1e4  # an outlier: its line is peaked (a split row in batches of 16384 lines or more)
     return x
 
 
