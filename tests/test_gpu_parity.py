@@ -273,18 +273,19 @@ def test_outlier_rows_follow_reference(bits_, M):
           flush=True)
 
 
-@pytest.mark.parametrize("bits_", [4, 8])
-def test_split_rows_in_large_batches(bits_):
+@pytest.mark.parametrize("bits_,axis", [(4, 1), (8, 1), (4, 0)])
+def test_split_rows_in_large_batches(bits_, axis):
     """M = 16384 (TGK_SPLIT_ROWS): the same outlier rows among N(0, 1) rows
     are split (their band entries as exact outlier terms, a grid of their own
     for the rest), bit-identical with the host restatement
     (parity.device_path_matmul with split) and within the parity predicate
     against the oracle; rows with a NaN or an infinity keep the reference's
-    loop, bit-identical with the oracle."""
-    print("case split rows", bits_, flush=True)
+    loop, bit-identical with the oracle. axis 0 (W @ x: the rows are columns
+    of b, element k at stride M) reads the rows and the codes strided."""
+    print("case split rows", bits_, axis, flush=True)
     M, K, C = 16384, 1024, 1024
     lim = 7 if bits_ == 4 else 127
-    rng = np.random.default_rng(40 + bits_)
+    rng = np.random.default_rng(40 + bits_ + 7 * axis)
     codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)
     scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
     xo, sp = parity.outlier_rows(K, codes, seed=bits_)
@@ -292,12 +293,16 @@ def test_split_rows_in_large_batches(bits_):
     at = np.linspace(3, M - 4, len(xo)).astype(int)
     x[at] = xo
     x[1, 17], x[M - 2, 5] = np.nan, np.inf
+    stored = codes if axis == 1 else np.ascontiguousarray(codes.T)  # the param's own layout: [K][C] or [C][K]
     if bits_ == 4:
-        flat = codes.ravel().astype(np.int64)
+        flat = stored.ravel().astype(np.int64)
         packed = ((flat[0::2] & 15) | ((flat[1::2] & 15) << 4)).astype(np.uint8).view(np.int8)
     else:
-        packed = codes.ravel()
-    got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
+        packed = stored.ravel()
+    if axis == 1:
+        got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
+    else:  # o = diag(s) Q @ b with b = x^T [K][M]: o is [C][M]
+        got = np.ascontiguousarray(hip.matmul_q(packed, bits_, scales, np.ascontiguousarray(x.T), C, K, M, 0).T)
     sub = np.concatenate([at, [1, M - 2], rng.choice(M, 6, replace=False)])
     want, special = parity.device_path_matmul(x[sub], codes, scales, split=True)
     assert special[:len(at)].tolist() == sp.tolist() and special[len(at):len(at) + 2].all()
@@ -306,7 +311,7 @@ def test_split_rows_in_large_batches(bits_):
         return np.array_equal(na, nb) and np.array_equal(bits(a[~na]), bits(b[~nb]))
 
     assert same(got[sub], want)
-    text = synth.linear_tgir_codes("lq", codes, scales, bits_, axis=1)
+    text = synth.linear_tgir_codes("lq", codes, scales, bits_, axis=1)  # the reference's x @ W on the same codes
     ref, _ = O.Model(text).batch(x[sub], threads=16)
     assert same(got[[1, M - 2]], ref[len(at):len(at) + 2])
     keep = np.ones(len(sub), bool)
