@@ -115,6 +115,46 @@ def auto_threads():
     return len(os.sched_getaffinity(0))
 
 
+def ref_unit_cpu(text, rows_q16, y_dev, steps_dev, nout, nthink, what, runs=3):
+    """Q16.16: the reference's own `tgc c --fixed` unit (src/cgen.c, built
+    into oracle/_ref/tgc_ref; the unit compiled cc -std=c99 -O2) over
+    `rows_q16` on one thread, `runs` times: median rate from input read to last
+    write. Its outputs and think steps are compared with the device's for the
+    same rows (`matches_device`). Without the reference build: the threaded
+    oracle restatement (ref_cpu)."""
+    import numpy as np
+    from oracle import oracle as O
+    if not O.have_ref():
+        return ref_cpu(text, rows_q16, rows_q16.shape[1], nout, nthink, auto_threads(), True, what, runs)
+    tmp = tempfile.mkdtemp(prefix="tgbench")
+    wall = []
+    try:
+        mpath = os.path.join(tmp, "model.tgir")
+        with open(mpath, "w") as f:
+            f.write(text)
+        exe = O.ref_unit_build(mpath, tmp)
+        d = os.path.dirname(exe)
+        inp, outp, stp = (os.path.join(d, n) for n in ("in.bin", "out.bin", "steps.bin"))
+        np.ascontiguousarray(rows_q16, dtype="<i4").tofile(inp)
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            subprocess.run([exe, inp, outp, stp], check=True, capture_output=True)
+            wall.append((time.perf_counter() - t0) * 1e3)
+        out = np.fromfile(outp, dtype="<i4").reshape(-1, nout)
+        stq = np.fromfile(stp, dtype="<i4").reshape(-1, max(nthink, 1))
+        same = bool(np.array_equal(out, y_dev) and np.array_equal(stq[:, 0], steps_dev))
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    wm = sorted(wall)[len(wall) // 2]
+    out = {"value": round(len(rows_q16) / (wm / 1e3), 1), "unit": "rows/s", "cores": 1, "kind": "reference",
+           "runs": runs, "wall_ms": [round(v, 2) for v in wall], "matches_device": same,
+           "sample": "%d rows of %s through the reference's own `tgc c --fixed` unit (emitted by src/cgen.c, compiled "
+                     "cc -std=c99 -O2; the unit is single-threaded), median of %d runs from input read to last write"
+                     % (len(rows_q16), what, runs)}
+    out.update(cpu_info())
+    return out
+
+
 def ref_cpu(text, rows, per, nout, nthink, threads, fixed, what, runs=3):
     """The reference interpreter (oracle/_ref/tgc_ref, built from the
     reference's sources; the oracle restatement if that build is absent) over
@@ -466,8 +506,10 @@ def config4_leg(args, steps=None, profile=True):
         roof = {"bound": "valu", "achieved": None, "peak": VALU_PEAK_GINST, "unit": "Ginst/s", "frac": None,
                 "traffic": None, "hbm_frac": round(byts / t / 1e9 / HBM_PEAK_GBS, 5),
                 "kernel": kname + (": rocprofv3 gave no data" if profile else ": not profiled (--no-traffic)")}
-    cpu = None if args.no_cpu else ref_cpu(text, xq[:131072], 8, 4, 1, auto_threads(), True,
-                                           "config 4 (Q16.16 latent reasoner)")
+    cpu = None
+    if not args.no_cpu:
+        y = d_y.to_array(np.int32, (rows, 4))
+        cpu = ref_unit_cpu(text, xq[:131072], y[:131072], st[:131072], 4, 1, "config 4 (Q16.16 latent reasoner)")
     return {
         "metric": "config 4 Q16.16 latent reasoner rows/sec at 1 GPU", "value": round(rows / t, 1), "unit": "rows/s",
         "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 4), "higher_is_better": True,

@@ -183,6 +183,19 @@ def ref_batch(model_path, rows, per, nout, nthink, workdir, threads=1, fixed=Fal
     return (out, steps, ms, wall_ms) if wall else (out, steps, ms)
 
 
+def ref_unit_build(model_path, workdir):
+    """Emit the reference's `tgc c --fixed` unit for the model with the
+    raw-row driver and compile it (cc -std=c99 -O2, as tests/run.sh:309 of the
+    reference compiles units). Returns the executable's path (`exe ROWS OUT
+    STEPS`)."""
+    d = os.path.join(workdir, "unit_" + os.path.basename(model_path).replace(".", "_"))
+    os.makedirs(d, exist_ok=True)
+    unit, main, exe = (os.path.join(d, n) for n in ("unit.c", "main.c", "unit"))
+    ref_run(["c", model_path, "-o", unit, "--fixed", "--harness", main])
+    subprocess.run([os.environ.get("CC", "cc"), "-std=c99", "-O2", "-o", exe, main], check=True, capture_output=True)
+    return exe
+
+
 def ref_unit(model_path, rows_q16, nout, nthink, workdir):
     """Run the reference's own `tgc c --fixed` unit over Q16.16 rows.
 
@@ -192,11 +205,8 @@ def ref_unit(model_path, rows_q16, nout, nthink, workdir):
     with the raw-row driver tgc_ref writes beside it instead of the unit's own
     decimal driver. Returns (int32 outputs [rows, nout], int32 steps [rows,
     max(nthink, 1)])."""
-    d = os.path.join(workdir, "unit_" + os.path.basename(model_path).replace(".", "_"))
-    os.makedirs(d, exist_ok=True)
-    unit, main, exe = (os.path.join(d, n) for n in ("unit.c", "main.c", "unit"))
-    ref_run(["c", model_path, "-o", unit, "--fixed", "--harness", main])
-    subprocess.run([os.environ.get("CC", "cc"), "-std=c99", "-O2", "-o", exe, main], check=True, capture_output=True)
+    exe = ref_unit_build(model_path, workdir)
+    d = os.path.dirname(exe)
     inp, outp, stp = (os.path.join(d, n) for n in ("in.bin", "out.bin", "steps.bin"))
     np.ascontiguousarray(rows_q16, dtype="<i4").tofile(inp)
     subprocess.run([exe, inp, outp, stp], check=True, capture_output=True)
