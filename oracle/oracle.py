@@ -43,7 +43,6 @@ def lib():
         L.tgo_batch.argtypes = [vp, vp, ctypes.c_long, vp, vp, ip]
         L.tgo_batch_fixed.argtypes = [vp, vp, ctypes.c_long, vp, vp, ip]
         L.tgo_batch64.argtypes = [vp, vp, ctypes.c_long, vp, vp, ip]
-        L.tgo_quantize.argtypes = [vp, ip, ip, vp, ctypes.c_long, ip, cp, ip]
         L.tgo_write.restype = ctypes.c_void_p
         L.tgo_write.argtypes = [vp]
         L.tgo_str_free.argtypes = [vp]
@@ -109,14 +108,6 @@ class Model:
         if rc:
             raise RuntimeError("oracle fixed batch failed (%d)" % rc)
         return out, steps
-
-    def quantize(self, bits, gptq=False, calib=None, min_size=256):
-        c = None if calib is None else np.ascontiguousarray(calib, dtype=np.float32).reshape(-1, self.per)
-        log = ctypes.create_string_buffer(4096)
-        n = lib().tgo_quantize(self.h, bits, 1 if gptq else 0, _ptr(c), 0 if c is None else c.shape[0], min_size, log, 4096)
-        if n < 0:
-            raise ValueError("oracle: no param is eligible")
-        return log.value.decode()
 
     def write(self):
         p = lib().tgo_write(self.h)

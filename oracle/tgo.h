@@ -4,7 +4,7 @@
  * quantized path: the TGIR reader (src/ir.c), the per-row interpreter
  * (src/vm.c) with the f32 kernels (runtime/tg_rt.h), the Q16.16 kernels
  * (runtime/tg_rtq.h) in the instruction order of the generated fixed-point
- * unit (src/cgen.c:100-314), the post-training quantizer (src/quant.c), the
+ * unit (src/cgen.c:100-314), the
  * seeded initializers (src/lower.c:661-775) and the row-parallel batch driver
  * (src/main.c:400-444, src/par.c).
  *
@@ -93,7 +93,6 @@ void tgo_free(tgo_module *m);
 int tgo_info(const tgo_module *m, int *per, int *nout, int *nthink, long *arena);
 int tgo_batch(const tgo_module *m, const float *rows, long nrows, float *out, int *steps, int threads);
 int tgo_batch_fixed(tgo_module *m, const int32_t *rows, long nrows, int32_t *out, int *steps, int threads);
-int tgo_quantize(tgo_module *m, int bits, int gptq, const float *calib, long ncalib, int min_size, char *log, int logn);
 char *tgo_write(const tgo_module *m);           /* canonical TGIR text (src/ir.c:150-202); free with tgo_str_free */
 void tgo_str_free(char *s);
 void tgo_rand(uint32_t seed, float scale, float *out, long n);

@@ -53,9 +53,10 @@ def test_latent_reasoner_text_is_the_reference_lowering():
 
 
 @pytest.mark.parametrize("bits,axis,shape", [(8, 0, (48, 40)), (4, 0, (33, 513)), (4, 1, (48, 24)), (8, 1, (16, 300))])
-def test_rtn_quantizer_matches_oracle(bits, axis, shape):
-    """synth.quantize_rtn == the oracle's restatement of src/quant.c (itself
-    pinned to the reference's quantizer by tests/golden)."""
+def test_rtn_quantizer_matches_the_backend_quantizer(bits, axis, shape):
+    """synth.quantize_rtn == the backend's `tgc quantize` (tg_hip_quantize_model
+    on the host, byte-identical with the reference's quantizer on the goldens:
+    tests/test_quantize.py)."""
     w = synth.normal(bits * 10 + axis, 0.3, shape[0] * shape[1]).reshape(shape)
     w[0] = 0  # an all-zero row
     codes, scales = synth.quantize_rtn(w, bits, axis)
@@ -65,9 +66,7 @@ def test_rtn_quantizer_matches_oracle(bits, axis, shape):
     else:
         text = "(tgir 1\n  (model q)\n" + synth.param_f32("W", w) + "  (input h (f32 %d))\n  (block\n    (%%0 (f32 %d) (matmul h W))\n  )\n  (output %%0))\n" % (shape[0], shape[1])
     del nm_in
-    m = O.Model(text)
-    m.quantize(bits, min_size=1)
-    want = m.write()
+    want, _, _ = hip.quantize_model(text, bits=bits, min_size=1)
     got = "(tgir 1\n  (model q)\n" + synth.param_quant("W", codes, scales, bits, axis)
     # compare codes and scales token by token (the code layout is not canonical)
     def qtokens(s):

@@ -105,24 +105,6 @@ def test_fixed_goldens_are_the_emitted_units(name, tmp_path):
     assert np.array_equal(yw, yu) and np.array_equal(sw, su)
 
 
-@pytest.mark.parametrize("name", [n for n in NAMES if "qargs" in np.load(os.path.join(GOLDEN, n + ".npz")).files])
-def test_quantizer_matches_reference(name):
-    """Codes and scales from the oracle's quantizer equal the reference's
-    (written by its ir_write), byte for byte, including GPTQ with calibration."""
-    src = name.rsplit("_", 1)[0] + "_f32"
-    if not os.path.exists(os.path.join(GOLDEN, src + ".tgir")):
-        pytest.skip("the f32 source of %s is not kept as a fixture" % name)
-    want, d = load(name)
-    f32_text, _ = load(src)
-    args = str(d["qargs"]).split()
-    bits_ = int(args[args.index("--bits") + 1])
-    gptq = "--method" in args and args[args.index("--method") + 1] == "gptq"
-    min_size = int(args[args.index("--min-size") + 1]) if "--min-size" in args else 256
-    m = O.Model(f32_text)
-    m.quantize(bits_, gptq=gptq, calib=d["calib"] if gptq else None, min_size=min_size)
-    assert m.write() == want
-
-
 def test_writer_is_a_fixed_point():
     for name in NAMES:
         text, _ = load(name)
