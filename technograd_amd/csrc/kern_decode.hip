@@ -171,31 +171,37 @@ __global__ __launch_bounds__(ATT_TPB) void dec_attn_k(tgk_dec_attn_args a, int c
 // sum_k code_k q_k = s0 + 256 s1 + 65536 s2 (s_i = sum_k code_k digit_i,k by
 // 4-way int8 dot products), scaled by 2^(E-23) in f64, rounded once to f32
 // and multiplied by the channel scale; rows with inf, nan or an entry above
-// 2^100, and peaked rows (tg_qdigits.h), take the reference's sequential f32
-// loop. One block per (head, 64
-// columns): the rows' digits and the head's code tile sit in LDS; a wave
-// handles 4 rows at a time, a lane one column.
+// 2^100 take the reference's sequential f32 loop, and candidate rows
+// (tg_qdigits.h) are resolved here as the GEMM path resolves them: a wave
+// per row, the same decision; a split row's rest gets digits of its own
+// grid and its outliers' terms (f64, increasing k) are added to its grid
+// sum before the one rounding. One block per (head, 64 columns): the rows'
+// digits and the head's code tile sit in LDS; a wave handles 4 rows at a
+// time, a lane one column.
 // codes: int32 [NQ][HD/4][D], 4 consecutive k's int8 codes per word (k = 4
 // k4 + i in byte i); scales [NQ][D]; HD a multiple of 4, att 16-byte aligned.
-constexpr int WO_TPB = 512;
+constexpr int WO_TPB = 512, WO_NW = WO_TPB / 64;
+constexpr int wo_nout(int HD) { return HD / 16 < 1 ? 1 : HD / 16 > TGQ_MAX_OUT ? TGQ_MAX_OUT : HD / 16; } // >= J(n), n <= HD
 __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *codes, const float *scales, float *out, int rows, int NQ,
 						   int HD, int D)
 {
 	extern __shared__ int4 dg[]; // [rows][HD/4] digit words {d0, d1, d2, 0} of 4 k's
-	const int H4 = HD / 4, n = rows * H4;
-	int *Es = (int *)(dg + (long)rows * H4), *sp = Es + rows, *ct = sp + rows; // ct: [HD/4][64] code words
-	int *tin = ct + H4 * 64, *tbl = tin + rows; // per row: entries in the band, nonzero entries below it
-	float *bnd = (float *)(tbl + rows);         // per row: the band's floor
+	const int H4 = HD / 4, n = rows * H4, NO = wo_nout(HD);
+	TgqHist *hist = (TgqHist *)(dg + (long)rows * H4); // one per wave
+	long long *tq = (long long *)(hist + WO_NW);      // per row: the candidate tally
+	float *ox = (float *)(tq + rows);                 // per row: a split row's outliers [NO], values
+	int *ok = (int *)(ox + (long)rows * NO);          // and inputs, -1 past the last
+	int *Es = ok + (long)rows * NO, *sp = Es + rows, *ct = sp + rows; // ct: [HD/4][64] code words
 	const int ctiles = (D + 63) / 64, g = blockIdx.x / ctiles, c0 = (blockIdx.x - g * ctiles) * 64;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-	constexpr int U = 4, nw = WO_TPB / 64;
+	constexpr int U = 4;
 	auto xat = [&](int e) { // the 4 inputs of item e = (row t, k4)
 		const int t = e / H4;
 		return *(const float4 *)(att + ((long)t * NQ + g) * HD + 4 * (e - t * H4));
 	};
 	// rows' max |x| (as bits: non-negative floats order as their bits) and flags
 	unsigned *mxb = (unsigned *)Es;
-	for (int t = tid; t < rows; t += WO_TPB) mxb[t] = 0, sp[t] = 0, tin[t] = 0, tbl[t] = 0;
+	for (int t = tid; t < rows; t += WO_TPB) mxb[t] = 0, sp[t] = 0, tq[t] = 0;
 	for (int e = tid; e < H4 * 64; e += WO_TPB) {
 		const int k4 = e >> 6, c = e & 63;
 		ct[e] = c0 + c < D ? codes[((long)g * H4 + k4) * D + c0 + c] : 0;
@@ -218,48 +224,94 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 	for (int t = tid; t < rows; t += WO_TPB) {
 		const float mx = __uint_as_float(mxb[t]);
 		const int special = tgq_special(sp[t], mx);
-		Es[t] = tgq_exponent(mx, special), sp[t] = special, bnd[t] = tgq_band(mx);
+		Es[t] = tgq_exponent(mx, special), sp[t] = special;
 	}
 	__syncthreads();
+	// the four inputs' digit words on the grid of E; their tally into *tl
+	auto digit_words = [&](const float (&xv)[4], int E, long long *tl) {
+		unsigned w0 = 0, w1 = 0, w2 = 0;
+		int aq = 0, nx = 0;
+		for (int i = 0; i < 4; i++) {
+			const float sv = ldexpf(xv[i], 23 - E), rq = rintf(sv);
+			const int q = (int)rq; // exact: |q| < 2^23
+			aq += abs(q);
+			nx += rq != sv;
+			int d0, d1, d2;
+			tgq_split3(q, d0, d1, d2);
+			w0 |= (unsigned)(d0 & 255) << (8 * i);
+			w1 |= (unsigned)(d1 & 255) << (8 * i);
+			w2 |= (unsigned)(d2 & 255) << (8 * i);
+		}
+		if (tl && (aq || nx)) atomicAdd((unsigned long long *)tl, (unsigned long long)aq + ((unsigned long long)nx << TGQ_TALLY_SHIFT));
+		return make_int4((int)w0, (int)w1, (int)w2, 0);
+	};
 	for (int b = tid; b < n; b += U * WO_TPB) {
 		float4 u[U];
 		for (int j = 0; j < U; j++) u[j] = xat(min(b + j * WO_TPB, n - 1));
 		for (int j = 0; j < U; j++) {
 			const int e = b + j * WO_TPB;
 			if (e >= n) continue;
-			const int t = e / H4, E = Es[t];
+			const int t = e / H4;
 			const float xv[4] = { u[j].x, u[j].y, u[j].z, u[j].w };
-			unsigned w0 = 0, w1 = 0, w2 = 0;
-			if (!sp[t]) {
-				int in = 0, below = 0;
-				for (int i = 0; i < 4; i++) {
-					const float av = fabsf(xv[i]);
-					in += av >= bnd[t] && av != 0.0f;
-					below += av < bnd[t] && av != 0.0f;
-				}
-				if (in) atomicAdd(&tin[t], in);
-				if (below) atomicAdd(&tbl[t], below);
-			}
-			if (!sp[t])
-				for (int i = 0; i < 4; i++) {
-					const int q = (int)rintf(ldexpf(xv[i], 23 - E)); // exact: |q| < 2^23
-					int d0, d1, d2;
-					tgq_split3(q, d0, d1, d2);
-					w0 |= (unsigned)(d0 & 255) << (8 * i);
-					w1 |= (unsigned)(d1 & 255) << (8 * i);
-					w2 |= (unsigned)(d2 & 255) << (8 * i);
-				}
-			dg[e] = make_int4((int)w0, (int)w1, (int)w2, 0);
+			dg[e] = sp[t] ? make_int4(0, 0, 0, 0) : digit_words(xv, Es[t], &tq[t]);
 		}
 	}
 	__syncthreads();
 	for (int t = tid; t < rows; t += WO_TPB)
-		if (!sp[t]) sp[t] = tgq_peaked((long long)tin[t] + ((long long)tbl[t] << 32), HD);
+		if (!sp[t] && tgq_candidate(tq[t])) sp[t] = 3; // a candidate, resolved below
+	__syncthreads();
+	// candidates: a wave per row, the GEMM path's resolve (kern_qgemm.hip: resolve_k)
+	for (int t = wave; t < rows; t += WO_NW) {
+		if (sp[t] != 3) continue; // the same word for the whole wave
+		const float *x = att + ((long)t * NQ + g) * HD;
+		const int E0 = Es[t];
+		auto ld = [&](int gi, float *v) {
+			for (int i = 0; i < 16; i++) v[i] = 16 * gi + i < HD ? x[16 * gi + i] : 0.0f;
+		};
+		const int L = tgq_resolve(&hist[wave], ld, (HD + 15) / 16, E0, lane);
+		if (L <= 0) {
+			if (lane == 0) sp[t] = L < 0 ? 1 : 0;
+			continue;
+		}
+		float rm = 0.0f;
+		for (int k = lane; k < HD; k += 64)
+			if (!tgq_outlier(x[k], E0, L)) rm = fmaxf(rm, fabsf(x[k]));
+		for (int o = 32; o > 0; o >>= 1) rm = fmaxf(rm, __shfl_xor(rm, o));
+		const int Er = tgq_exponent(rm, 0);
+		int nin = 0;
+		for (int k40 = 0; k40 < H4; k40 += 64) { // the rest's digits, the outliers in input order
+			const int k4 = k40 + lane;
+			float xv[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+			unsigned om = 0;
+			if (k4 < H4)
+				for (int i = 0; i < 4; i++) {
+					const float xi = x[4 * k4 + i];
+					if (tgq_outlier(xi, E0, L)) om |= 1u << i;
+					else xv[i] = xi;
+				}
+			if (k4 < H4) dg[(long)t * H4 + k4] = digit_words(xv, Er, nullptr);
+			const int cnt = __popc(om);
+			int inc = cnt;
+			for (int d = 1; d < 64; d <<= 1) {
+				const int y = __shfl_up(inc, d);
+				if (lane >= d) inc += y;
+			}
+			int at = nin + inc - cnt;
+			for (int i = 0; i < 4; i++)
+				if ((om >> i) & 1) {
+					if (at < NO) ok[(long)t * NO + at] = 4 * k4 + i, ox[(long)t * NO + at] = x[4 * k4 + i];
+					at++;
+				}
+			nin += __shfl(inc, 63);
+		}
+		for (int j = nin + lane; j < NO; j += 64) ok[(long)t * NO + j] = -1;
+		if (lane == 0) Es[t] = Er, sp[t] = 2;
+	}
 	__syncthreads();
 	const int c = lane;
 	if (c0 + c >= D) return;
 	const float sc = scales[(long)g * D + c0 + c];
-	for (int t0 = 4 * wave; t0 < rows; t0 += 4 * nw) {
+	for (int t0 = 4 * wave; t0 < rows; t0 += 4 * WO_NW) {
 		int s[4][3] = {};
 		int tr[4];
 		for (int r = 0; r < 4; r++) tr[r] = min(t0 + r, rows - 1); // rows past the end repeat the last (not stored)
@@ -274,15 +326,19 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 		}
 		for (int r = 0; r < 4 && t0 + r < rows; r++) {
 			const int t = t0 + r;
+			auto code = [&](int k) { return (float)(int8_t)(ct[(k >> 2) * 64 + c] >> (8 * (k & 3))); };
 			float v;
-			if (sp[t]) { // the reference's loop (runtime/tg_rt.h:143-151)
+			if (sp[t] == 1) { // the reference's loop (runtime/tg_rt.h:143-151)
 				const float *x = att + ((long)t * NQ + g) * HD;
 				float acc = 0.0f;
-				for (int k = 0; k < HD; k++) acc += (float)(int8_t)(ct[(k >> 2) * 64 + c] >> (8 * (k & 3))) * x[k];
+				for (int k = 0; k < HD; k++) acc += code(k) * x[k];
 				v = acc;
 			} else { // every term and partial sum an integer below 2^48: exact in f64
 				const double tot = (double)s[r][0] + (double)s[r][1] * 256.0 + (double)s[r][2] * 65536.0;
-				v = (float)ldexp(tot, Es[t] - 23);
+				double o = 0.0; // a split row's outlier terms, in input order
+				if (sp[t] == 2)
+					for (int j = 0; j < NO && ok[(long)t * NO + j] >= 0; j++) o += (double)code(ok[(long)t * NO + j]) * (double)ox[(long)t * NO + j];
+				v = (float)(ldexp(tot, Es[t] - 23) + o);
 			}
 			out[((long)g * rows + t) * D + c0 + c] = sc * v;
 		}
@@ -320,17 +376,16 @@ __device__ inline void blk_digits(const float *z, int K, int Kp, float mx, int b
 	const float amax = blk_max(mx, redf); // nan never wins fmaxf; such rows are flagged by bad
 	const int anybad = __syncthreads_or(bad);
 	const int special = tgq_special(anybad, amax), E = tgq_exponent(amax, special);
-	const float band = tgq_band(amax);
 	int8_t *blk = tgq_row_base(q.dig, m, Kp);
 	long long qs = 0, tl = 0;
 	for (int j = threadIdx.x; j < Kp / 16; j += blockDim.x) {
 		float v[16];
 		for (int u = 0; u < 16; u++) v[u] = z[16 * j + u];
-		qs += tgq_put16(blk, 16 * j, v, E, special, band, tl);
+		qs += tgq_put16(blk, 16 * j, v, E, special, tl);
 	}
 	qs = blk_sum(qs, redl);
 	tl = blk_sum(tl, redl);
-	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = special || tgq_peaked(tl, K), q.qsum[m] = qs;
+	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = special || tgq_candidate(tl), q.qsum[m] = qs;
 }
 
 // tgk_dec_norm: one block per token row, NORM_TPB threads, each with at most
@@ -441,16 +496,15 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 		bad |= __shfl_xor(bad, o);
 	}
 	const int special = tgq_special(bad, mx), E = tgq_exponent(mx, special);
-	const float band = tgq_band(mx);
 	int8_t *blk = tgq_row_base(a.q.dig, L, Kp);
 	long long qs = 0, tl = 0;
 	for (int g = lane; g < Kp / 16; g += 64) {
 		float v[16];
 		for (int u = 0; u < 16; u++) v[u] = z[16 * g + u];
-		qs += tgq_put16(blk, 16 * g, v, E, special, band, tl);
+		qs += tgq_put16(blk, 16 * g, v, E, special, tl);
 	}
 	for (int o = 32; o > 0; o >>= 1) qs += __shfl_xor(qs, o), tl += __shfl_xor(tl, o);
-	if (lane == 0) a.q.e[L] = E, a.q.special[L] = special || tgq_peaked(tl, HD), a.q.qsum[L] = qs;
+	if (lane == 0) a.q.e[L] = E, a.q.special[L] = special || tgq_candidate(tl), a.q.qsum[L] = qs;
 }
 
 // Many lines at once (a prompt's token rows, or its head lines): a block of
@@ -572,20 +626,19 @@ __global__ __launch_bounds__(NL_TPB) void norm_lines_k(NormLines a)
 		bad |= __shfl_xor(bad, o);
 	}
 	const int special = tgq_special(bad, mx), E = tgq_exponent(mx, special);
-	const float band = tgq_band(mx);
 	long long qs = 0, tl = 0;
 	if (L0 + l < a.lines) {
 		int8_t *blk = tgq_row_base(a.q.dig, (int)(L0 + l), Kp);
 		for (int gi = k; gi < Kp / 16; gi += TPL) {
 			float w16[16];
 			for (int q = 0; q < 16; q++) w16[q] = zl[gi * 16 + q];
-			qs += tgq_put16(blk, gi * 16, w16, E, special, band, tl);
+			qs += tgq_put16(blk, gi * 16, w16, E, special, tl);
 		}
 	}
 	for (int o = 1; o < TPL; o <<= 1) qs += __shfl_xor(qs, o), tl += __shfl_xor(tl, o);
 	if (k == 0 && L0 + l < a.lines) {
 		const long L = L0 + l;
-		a.q.e[L] = E, a.q.special[L] = special || tgq_peaked(tl, D), a.q.qsum[L] = qs;
+		a.q.e[L] = E, a.q.special[L] = special || tgq_candidate(tl), a.q.qsum[L] = qs;
 	}
 }
 
@@ -806,7 +859,10 @@ void tgk_dec_causal_softmax(hipStream_t s, float *sc, int T0, long nlines, float
 	causal_softmax_k<<<(unsigned)((nlines + lpb - 1) / lpb), 256, (size_t)lpb * stride * 4 + lpb * 4, s>>>(sc, T0, nlines, scale, lpb, stride);
 }
 
-size_t tgk_dec_wo_lds(int rows, int HD) { return (size_t)rows * HD * 4 + (size_t)rows * 20 + (size_t)HD * 64; }
+size_t tgk_dec_wo_lds(int rows, int HD)
+{
+	return (size_t)rows * HD * 4 + WO_NW * sizeof(TgqHist) + (size_t)rows * (8 + 8 * wo_nout(HD) + 8) + (size_t)HD * 64;
+}
 
 void tgk_dec_wo(hipStream_t s, const float *att, const int *codes, const float *scales, float *out, int rows, int NQ, int HD, int D)
 {

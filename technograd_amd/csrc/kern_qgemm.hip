@@ -10,19 +10,16 @@
 // the channel scale in f32 like the reference. The only approximation is the
 // 24-bit activation grid (error <= 2^-24 max|x| per element), far below the
 // reference's own f32 summation error at these K. Every step depends on the
-// row alone, so a row's outputs do not depend on the batch it came in, with
-// one exception: peaked rows (below).
+// row alone, so a row's outputs do not depend on the batch it came in.
 //
-// Rows with a non-finite or huge entry, and peaked rows (a few entries far
-// above all others, tg_qdigits.h), are flagged by the digit kernel and their
-// outputs are recomputed in the epilogue with the reference's exact
-// sequential f32 loop, so inf/nan propagate as they do in the reference and
-// an outlier does not coarsen the other entries of its row. In batches of
-// TGK_SPLIT_ROWS rows or more, peaked rows are split instead (split_k): the
-// outliers as exact terms, the rest on a grid of its own; a peaked row's
-// outputs then differ from those of the same row in a smaller batch (both
-// within the parity predicate; only the smaller batch's are the reference's
-// bits).
+// Rows with a non-finite or huge entry are flagged by the digit kernel and
+// their outputs are recomputed in the epilogue with the reference's exact
+// sequential f32 loop, so inf/nan propagate as they do in the reference.
+// Rows whose grid may be too coarse (a few entries far above the others,
+// tg_qdigits.h) are flagged as candidates and resolved after the digit
+// kernel (resolve_k) at every batch size: they keep their grid, or are split
+// (outliers as exact terms, the rest on a grid of its own), or take the
+// reference's loop, by a decision made from the row's values alone.
 //
 // Operand layouts in global memory are the MFMA fragment order of
 // v_mfma_i32_32x32x32_i8 (lane l holds row or channel l % 32 and inputs
@@ -68,15 +65,13 @@ constexpr int BN = 256;       // channels per tile of the LDS kernel (weights ar
 
 inline long round_up(long x, long m) { return (x + m - 1) / m * m; }
 
-constexpr int NOUT = 8; // outliers of a split row (the peak test allows at most 8 entries in the band)
-
 struct Scratch {
 	int8_t *dig;       // digits in fragment order (see above)
 	long long *qsum;   // [Mp] sum over k of the row's fixed-point values q
 	int *e;            // [Mp] row exponent E
-	int *special;      // [Mp] 1: the row takes the reference's sequential loop; 2: a split row (split_k)
-	int *ok;           // [Mp][NOUT] a split row's outliers: input index, -1 past the last
-	float *ox;         // [Mp][NOUT] and value
+	int *special;      // [Mp] 0 a grid row; 1 the reference's sequential loop (or a candidate before resolve_k); 2 a split row
+	int *ok;           // [Mp][tgq_nout(Kp)] a split row's outliers: input index, -1 past the last
+	float *ox;         // [Mp][tgq_nout(Kp)] and value
 };
 
 Scratch carve(void *base, int Mp, int Kp)
@@ -92,7 +87,7 @@ Scratch carve(void *base, int Mp, int Kp)
 	s.special = (int *)p;
 	p += (size_t)Mp * sizeof(int);
 	s.ok = (int *)p;
-	p += (size_t)Mp * NOUT * sizeof(int);
+	p += (size_t)Mp * tgq_nout(Kp) * sizeof(int);
 	s.ox = (float *)p;
 	return s;
 }
@@ -175,21 +170,20 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 	tgq_scan_end(mb, mx, bad);
 	const float amax = wave_max(mx); // a NaN lane reads 0 here; its row is flagged by `bad`
 	const int special = tgq_special(__any(bad), amax), E = tgq_exponent(amax, special);
-	const float band = tgq_band(amax);
 	long long qs = 0, tl = 0;
 	int8_t *blk = tgq_row_base(s.dig, m, Kp);
 	for (int t0 = 0; t0 < nsl; t0 += SL) {
 		if (nsl > SL) fetch(t0); // rows of up to SL slabs are still in v
 		for (int t = 0; t < SL; t++) {
 			const int k0 = (t0 + t) * 1024 + lane * 16;
-			if (t0 + t < nsl && k0 < Kp) qs += tgq_put16(blk, k0, v[t], E, special || k0 >= K, band, tl);
+			if (t0 + t < nsl && k0 < Kp) qs += tgq_put16(blk, k0, v[t], E, special || k0 >= K, tl);
 		}
 	}
 	qs = wave_sum(qs);
 	tl = wave_sum(tl);
 	if (lane == 0) {
 		s.e[m] = E;
-		s.special[m] = special || tgq_peaked(tl, K);
+		s.special[m] = special || tgq_candidate(tl);
 		s.qsum[m] = qs;
 	}
 }
@@ -230,12 +224,11 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 			bad |= sbad[u][mr + 16 * q];
 		}
 	const int special = tgq_special(bad, amax), E = tgq_exponent(amax, special);
-	const float band = tgq_band(amax);
 	int8_t *blk = s.dig + (long)(m0 >> 5) * nkb * 3072 + ((m0 & 31) + mr) * 16;
 	long long qs = 0, tl = 0;
 	for (int j = 0; j < NKB; j++) {
 		const int kb = 2 * (w + j * W) + par;
-		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K, band, tl);
+		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K, tl);
 	}
 	sqs[w][lane] = qs;
 	stl[w][lane] = tl;
@@ -245,7 +238,7 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 		for (int u = 0; u < W; u++)
 			for (int q = 0; q < 4; q++) t += sqs[u][mr + 16 * q], u2 += stl[u][mr + 16 * q];
 		s.e[m0 + mr] = E;
-		s.special[m0 + mr] = special || tgq_peaked(u2, K);
+		s.special[m0 + mr] = special || tgq_candidate(u2);
 		s.qsum[m0 + mr] = t;
 	}
 }
@@ -278,12 +271,11 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 	__syncthreads();
 	const float amax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
 	const int special = tgq_special(sbad[0] | sbad[1] | sbad[2] | sbad[3], amax), E = tgq_exponent(amax, special);
-	const float band = tgq_band(amax);
 	int8_t *blk = tgq_row_base(s.dig, m, Kp);
 	long long qs = 0, tl = 0;
 	for (int g = 0; g < G; g++) {
 		const int j = tid + g * 256;
-		if (j < ng) qs += tgq_put16(blk, j * 16, v[g], E, special || j * 16 >= K, band, tl);
+		if (j < ng) qs += tgq_put16(blk, j * 16, v[g], E, special || j * 16 >= K, tl);
 	}
 	qs = wave_sum(qs);
 	tl = wave_sum(tl);
@@ -291,24 +283,29 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 	__syncthreads();
 	if (tid == 0) {
 		s.e[m] = E;
-		s.special[m] = special || tgq_peaked(stl[0] + stl[1] + stl[2] + stl[3], K);
+		s.special[m] = special || tgq_candidate(stl[0] + stl[1] + stl[2] + stl[3]);
 		s.qsum[m] = sqs[0] + sqs[1] + sqs[2] + sqs[3];
 	}
 }
 
-// Split rows (large batches). A peaked row (tg_qdigits.h) would otherwise
-// take the reference's loop, 2 K operations per output. Instead its band
-// entries (|x| >= max|x| / 4, at most 8) become outliers kept exactly, and the
-// other entries get a grid of their own: E from their largest magnitude, their
-// digits and sum of q rewritten with the band entries as zeros. The epilogue
-// adds sum_o code[c][k_o] x_o (f64, exact products, increasing k) to the grid
-// sum in f64 and rounds once. A wave per flagged row; rows flagged for a
-// non-finite or huge entry keep the reference's loop. Grid-stride: wave v takes
+// Candidate rows (tg_qdigits.h), resolved after the digits are written, at
+// every batch size: a wave per flagged row reads the row again, leaves rows
+// with a non-finite or huge entry to the reference's loop, and takes the
+// peel level of the rest from its binade histogram (tgq_resolve). Level 0:
+// the row keeps its digits (a grid row). Level L > 0, a split row: the
+// entries |x| >= 2^(E-L) become outliers kept exactly (index and value, in
+// increasing index order, at most tgq_nout(Kp)), and the other entries get a
+// grid of their own: E from their largest magnitude, their digits and sum of
+// q rewritten with the outliers as zeros. The epilogue adds sum_o
+// code[c][k_o] x_o (f64, exact products, increasing k) to the grid sum in f64
+// and rounds once. No level: the reference's loop. Grid-stride: wave v takes
 // rows 64 v .. 64 v + 63, 64 (total waves) further, and so on.
-__global__ __launch_bounds__(256) void split_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
+__global__ __launch_bounds__(256) void resolve_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
 {
-	const int lane = threadIdx.x & 63, nw = gridDim.x * 4, ng = Kp / 16;
-	for (long base = (long)(blockIdx.x * 4 + (threadIdx.x >> 6)) * 64; base < M; base += (long)nw * 64) {
+	__shared__ TgqHist hist[4];
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = gridDim.x * 4, ng = Kp / 16, nout = tgq_nout(Kp);
+	TgqHist *h = &hist[wave];
+	for (long base = (long)(blockIdx.x * 4 + wave) * 64; base < M; base += (long)nw * 64) {
 		const long mr = base + lane;
 		unsigned long long fl = __ballot(mr < M && s.special[mr] == 1);
 		while (fl) {
@@ -326,36 +323,34 @@ __global__ __launch_bounds__(256) void split_k(tgk_qgemm_args a, Scratch s, int 
 			tgq_scan_end(mb, mx, bad);
 			const float amax = wave_max(mx);
 			if (tgq_special(__any(bad), amax)) continue; // non-finite or huge: the reference's loop
-			const float band = tgq_band(amax);
+			const int E0 = tgq_exponent(amax, 0);
+			const int L = tgq_resolve(h, [&](int g, float *v) { load16<false>(v, x, a.xk, g * 16, K); }, ng, E0, lane);
+			if (L < 0) continue; // no level: the reference's loop
+			if (L == 0) { // its own grid is fine: the digits as written
+				if (lane == 0) s.special[m] = 0;
+				continue;
+			}
 			float rm = 0.0f;
-			int nin = 0;
 			for (int g = lane; g < ng; g += 64) {
 				float v[16];
 				load16<false>(v, x, a.xk, g * 16, K);
-				for (int i = 0; i < 16; i++) {
-					const float u = fabsf(v[i]);
-					if (u >= band && u != 0.0f) nin++;
-					else rm = fmaxf(rm, u);
-				}
+				for (int i = 0; i < 16; i++)
+					if (!tgq_outlier(v[i], E0, L)) rm = fmaxf(rm, fabsf(v[i]));
 			}
-			const float rmax = wave_max(rm);
-			if (wave_sum((long long)nin) > NOUT) continue; // not a peaked row after all: leave it to the reference's loop
-			const int E = tgq_exponent(rmax, 0);
+			const int E = tgq_exponent(wave_max(rm), 0);
 			int8_t *blk = tgq_row_base(s.dig, m, Kp);
 			long long qs = 0, tl = 0;
-			int nout = 0;
+			int nin = 0;
 			for (int g0 = 0; g0 < ng; g0 += 64) {
 				const int g = g0 + lane;
 				float v[16];
 				load16<false>(v, x, a.xk, g < ng ? g * 16 : K, K); // past the row: zeros
 				unsigned om = 0;
-				for (int i = 0; i < 16; i++) {
-					const float u = fabsf(v[i]);
-					if (u >= band && u != 0.0f) om |= 1u << i;
-				}
+				for (int i = 0; i < 16; i++)
+					if (tgq_outlier(v[i], E0, L)) om |= 1u << i;
 				float r[16];
 				for (int i = 0; i < 16; i++) r[i] = (om >> i) & 1 ? 0.0f : v[i];
-				if (g < ng) qs += tgq_put16(blk, g * 16, r, E, g * 16 >= K, band, tl);
+				if (g < ng) qs += tgq_put16(blk, g * 16, r, E, g * 16 >= K, tl);
 				// the outliers in input order: an exclusive scan of the lanes' counts
 				const int cnt = __popc(om);
 				int inc = cnt;
@@ -363,16 +358,16 @@ __global__ __launch_bounds__(256) void split_k(tgk_qgemm_args a, Scratch s, int 
 					const int t = __shfl_up(inc, d);
 					if (lane >= d) inc += t;
 				}
-				int at = nout + inc - cnt;
+				int at = nin + inc - cnt;
 				for (int i = 0; i < 16; i++)
 					if ((om >> i) & 1) {
-						if (at < NOUT) s.ok[(long)m * NOUT + at] = g * 16 + i, s.ox[(long)m * NOUT + at] = v[i];
+						if (at < nout) s.ok[(long)m * nout + at] = g * 16 + i, s.ox[(long)m * nout + at] = v[i];
 						at++;
 					}
-				nout += __shfl(inc, 63);
+				nin += __shfl(inc, 63);
 			}
 			qs = wave_sum(qs);
-			if (lane >= nout && lane < NOUT) s.ok[(long)m * NOUT + lane] = -1;
+			for (int j = nin + lane; j < nout; j += 64) s.ok[(long)m * nout + j] = -1;
 			if (lane == 0) s.e[m] = E, s.qsum[m] = qs, s.special[m] = 2;
 		}
 	}
@@ -529,11 +524,12 @@ __device__ inline float act_out(float v) { return ACT == TGM_TANH ? tg_uop(TGM_T
 // product exact), from 0.0
 __device__ inline double outlier_sum(const Scratch &s, const tgk_qweight &w, int m, int c)
 {
+	const int nout = tgq_nout(w.Kp);
 	double t = 0.0;
-	for (int j = 0; j < NOUT; j++) {
-		const int k = s.ok[(long)m * NOUT + j];
+	for (int j = 0; j < nout; j++) {
+		const int k = s.ok[(long)m * nout + j];
 		if (k < 0) break;
-		t += (double)code_orig(w, c, k) * (double)s.ox[(long)m * NOUT + j];
+		t += (double)code_orig(w, c, k) * (double)s.ox[(long)m * nout + j];
 	}
 	return t;
 }
@@ -1036,6 +1032,17 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
+// a pointer the whole wave shares, in scalar registers (the "s" operands of
+// the loads below need it there; the compiler may otherwise keep a uniform
+// pointer in vector registers when scalar ones run short)
+template <class T>
+__device__ inline T *sgpr_ptr(T *p)
+{
+	const unsigned long long u = (unsigned long long)p;
+	const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u), hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+	return (T *)(((unsigned long long)hi << 32) | lo);
+}
+
 // Register loads of the small-batch kernel, issued with inline assembly: the
 // compiler does not track them, so each ring slot is waited for explicitly
 // (wait_vm) and then "touched" (an empty asm that reads and writes the slot's
@@ -1248,6 +1255,132 @@ __device__ inline void gemv1_steps(v4i (&bf)[NL], F &dots)
 	}
 }
 
+// gemv1_k's row when it is a candidate (FUSED: one row, unit stride): the
+// decision of resolve_k, taken by the workgroup from the row in its
+// registers (thread tid holds the 16-input groups tid + 256 u), so every
+// workgroup reaches the same decision and values as resolve_k would.
+// Returns the row's class (0 its grid, 1 the reference's loop, 2 split). For
+// a split row, lane j < 16 of wave 0 gets channel 16 t + j's sum before the
+// scale in `acc32` (the exact grid sum of the rest in f64 plus the outlier
+// terms in increasing input order, rounded once: the epilogue's split
+// value), and workgroup 0 leaves the split in the scratch (digits, exponent,
+// sum of q, outliers), as resolve_k does, for a product that reuses them.
+struct FusedSplitLds {
+	TgqHist h;
+	long long red[4][16];
+	long long qs[4];
+	int cnt[4][2];
+	unsigned rmax[4];
+	int L;
+	int ok[TGQ_MAX_OUT];
+	float ox[TGQ_MAX_OUT];
+};
+
+template <int GX>
+__device__ int fused_resolve(const tgk_qweight &w, const Scratch &s, const float (&v)[GX][16], int E, int n, int t, int tid, int lane,
+			     int wave, FusedSplitLds &F, float &acc32)
+{
+	static_assert(GX <= 2, "outlier order below: two groups per thread");
+	const int K = w.K;
+	if (tid < 64) F.h.cnt[tid] = 0, F.h.mass[tid] = 0;
+	__syncthreads();
+	for (int u = 0; u < GX; u++)
+		if (16 * (tid + 256 * u) < K) (void)tgq_hist16(&F.h, v[u], E);
+	__syncthreads();
+	if (wave == 0) {
+		const int L = tgq_decide(&F.h, n, lane);
+		if (lane == 0) F.L = L;
+	}
+	__syncthreads();
+	const int L = F.L;
+	if (L <= 0) return L < 0 ? 1 : 0;
+	// the outliers, and the largest of the rest
+	float rm = 0.0f;
+	unsigned om[GX];
+	int inc[GX], cnt[GX];
+	for (int u = 0; u < GX; u++) {
+		om[u] = 0;
+		if (16 * (tid + 256 * u) < K)
+			for (int i = 0; i < 16; i++) {
+				if (tgq_outlier(v[u][i], E, L)) om[u] |= 1u << i;
+				else rm = fmaxf(rm, fabsf(v[u][i]));
+			}
+		cnt[u] = inc[u] = __popc(om[u]);
+		for (int d = 1; d < 64; d <<= 1) { // inclusive scan over the wave's lanes
+			const int x = __shfl_up(inc[u], d);
+			if (lane >= d) inc[u] += x;
+		}
+	}
+	rm = wave_max(rm);
+	if (lane == 0) F.rmax[wave] = __float_as_uint(rm); // non-negative: the bits order as the values
+	if (lane == 63)
+		for (int u = 0; u < GX; u++) F.cnt[wave][u] = inc[u];
+	__syncthreads();
+	const int Er = tgq_exponent(__uint_as_float(max(max(F.rmax[0], F.rmax[1]), max(F.rmax[2], F.rmax[3]))), 0);
+	// the outlier list in increasing input order: groups u, then waves, then lanes
+	int tot = 0;
+	for (int u = 0; u < GX; u++) {
+		int at = tot + inc[u] - cnt[u];
+		for (int ww = 0; ww < wave; ww++) at += F.cnt[ww][u];
+		for (int ww = 0; ww < 4; ww++) tot += F.cnt[ww][u];
+		for (int i = 0; i < 16; i++)
+			if ((om[u] >> i) & 1) {
+				if (at < TGQ_MAX_OUT) F.ok[at] = 16 * (tid + 256 * u) + i, F.ox[at] = v[u][i];
+				at++;
+			}
+	}
+	const int nin = tot < TGQ_MAX_OUT ? tot : TGQ_MAX_OUT; // tot <= J(n) <= TGQ_MAX_OUT (tgq_decide)
+	// the rest's grid: exact integer sums for the workgroup's 16 channels, one at a time
+	float r[GX][16];
+	long long qr = 0, tl = 0;
+	int8_t *gblk = tgq_row_base(s.dig, 0, w.Kp);
+#pragma unroll
+	for (int u = 0; u < GX; u++) {
+		const int k0 = 16 * (tid + 256 * u);
+#pragma unroll
+		for (int i = 0; i < 16; i++) r[u][i] = k0 >= K || ((om[u] >> i) & 1) ? 0.0f : v[u][i];
+		if (k0 >= K) continue;
+		if (t == 0) qr += tgq_put16(gblk, k0, r[u], Er, false, tl); // the scratch copy (this thread wrote the grid's there)
+		else
+#pragma unroll
+			for (int i = 0; i < 16; i++) qr += (int)rintf(ldexpf(r[u][i], 23 - Er));
+	}
+#pragma unroll 1
+	for (int j = 0; j < 16; j++) {
+		const int c = t * 16 + j;
+		long long acc = 0;
+		if (c < w.C)
+#pragma unroll
+			for (int u = 0; u < GX; u++) {
+				const int k0 = 16 * (tid + 256 * u);
+				if (k0 < K)
+#pragma unroll
+					for (int i = 0; i < 16; i++) {
+						const int q = (int)rintf(ldexpf(r[u][i], 23 - Er)); // exact: |q| < 2^23
+						if (q) acc += (long long)code_orig(w, c, k0 + i) * q;
+					}
+			}
+		acc = wave_sum(acc);
+		if (lane == 0) F.red[wave][j] = acc;
+	}
+	qr = wave_sum(qr);
+	if (lane == 0) F.qs[wave] = qr;
+	__syncthreads();
+	if (t == 0) {
+		const int nout = tgq_nout(w.Kp);
+		for (int j = tid; j < nout; j += 256) s.ok[j] = j < nin ? F.ok[j] : -1, s.ox[j] = j < nin ? F.ox[j] : 0.0f;
+		if (tid == 0) s.e[0] = Er, s.qsum[0] = F.qs[0] + F.qs[1] + F.qs[2] + F.qs[3], s.special[0] = 2;
+	}
+	if (wave == 0 && lane < 16 && t * 16 + lane < w.C) {
+		const int c = t * 16 + lane;
+		const long long g = F.red[0][lane] + F.red[1][lane] + F.red[2][lane] + F.red[3][lane];
+		double o = 0.0;
+		for (int j = 0; j < nin; j++) o += (double)code_orig(w, c, F.ok[j]) * (double)F.ox[j];
+		acc32 = (float)(ldexp((double)g, Er - 23) + o);
+	}
+	return 2;
+}
+
 // One activation row (M = 1) and int4 weights: exact integer dot products by
 // 4-way int8 dot instructions (v_dot4_i32_i8), no MFMA padding. A workgroup
 // of four waves computes 16 channels (half of a 32-channel fragment block)
@@ -1282,7 +1415,7 @@ __global__ __launch_bounds__(256) void gemv1_k(tgk_qgemm_args a, tgk_qweight w, 
 	// the row's loads first (inline assembly: counted by the waits below)
 	v4i xv[FUSED ? GX * 4 : 1];
 	v4i dv[FUSED ? 1 : 6];
-	const uint8_t *xb = (const uint8_t *)xrow(a, 0);
+	const uint8_t *xb = sgpr_ptr((const uint8_t *)xrow(a, 0));
 	if constexpr (FUSED) {
 		for (int u = 0; u < GX; u++) {
 			const int k0 = 16 * (tid + 256 * u), kk = k0 < K ? k0 : 0; // past the row: its first group (not used)
@@ -1296,7 +1429,7 @@ __global__ __launch_bounds__(256) void gemv1_k(tgk_qgemm_args a, tgk_qweight w, 
 		}
 	}
 	// the weights: NL 16-byte loads per lane
-	const uint8_t *B = w.w + (long)(t >> 1) * kblocks * 512;
+	const uint8_t *B = sgpr_ptr(w.w + (long)(t >> 1) * kblocks * 512);
 	const unsigned offB = (unsigned)((h * 32 + (t & 1) * 16 + 2 * pr) * 8);
 	v4i bf[NL];
 	for (int i = 0; i < NL; i++) {
@@ -1307,7 +1440,6 @@ __global__ __launch_bounds__(256) void gemv1_k(tgk_qgemm_args a, tgk_qweight w, 
 	// the row's digits into LDS (the weights stay in flight)
 	wait_vm<NL>();
 	int E = 0, sp0 = 0;
-	float band = 0.0f;
 	float v[FUSED ? GX : 1][16];
 	if constexpr (FUSED) {
 		for (int i = 0; i < GX * 4; i++) touch(xv[i]);
@@ -1328,7 +1460,6 @@ __global__ __launch_bounds__(256) void gemv1_k(tgk_qgemm_args a, tgk_qweight w, 
 					 fmaxf(__uint_as_float(smx[2]), __uint_as_float(smx[3])));
 		sp0 = tgq_special(sbad[0] | sbad[1] | sbad[2] | sbad[3], amax);
 		E = tgq_exponent(amax, sp0);
-		band = tgq_band(amax);
 	} else {
 		for (int u = 0; u < 6; u++) {
 			touch(dv[u]);
@@ -1344,7 +1475,7 @@ __global__ __launch_bounds__(256) void gemv1_k(tgk_qgemm_args a, tgk_qweight w, 
 			if (k0 >= w.Kp) break;
 			unsigned w0[4] = { 0, 0, 0, 0 }, w1[4] = { 0, 0, 0, 0 }, w2[4] = { 0, 0, 0, 0 }; // zero digits: padding, special rows
 			long long tl0 = 0; // the peak tally is taken after the dot products, off the critical path
-			if (!sp0 && k0 < K) qs += tgq_digits16(v[u], E, 0.0f, w0, w1, w2, tl0);
+			if (!sp0 && k0 < K) qs += tgq_digits16(v[u], E, w0, w1, w2, tl0);
 			int8_t *p = dl + ((k0 >> 5) * 3 * 2 + ((k0 >> 4) & 1)) * 16;
 			*(v4i *)p = v4i{ (int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3] };
 			*(v4i *)(p + 32) = v4i{ (int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3] };
@@ -1398,21 +1529,31 @@ __global__ __launch_bounds__(256) void gemv1_k(tgk_qgemm_args a, tgk_qweight w, 
 			for (int l = 0; l < 3; l++) red[wave][lane][j][l] = acc[j][l];
 	int special;
 	long long qsum;
-	if constexpr (FUSED) { // the row's sum of q and peak test (needed only from here on)
+	float acc32 = 0.0f; // a split row's sum (fused_resolve)
+	if constexpr (FUSED) { // the row's sum of q and candidate test (needed only from here on)
+		__shared__ FusedSplitLds F;
 		for (int u = 0; u < GX; u++)
-			if (!sp0 && 16 * (tid + 256 * u) < K) tl += tgq_tally16(v[u], band);
+			if (!sp0 && 16 * (tid + 256 * u) < K) tl += tgq_tally16(v[u], E);
 		qs = wave_sum(qs);
 		tl = wave_sum(tl);
 		if (lane == 0) sq[wave] = qs, stl[wave] = tl;
 		__syncthreads();
 		qsum = sq[0] + sq[1] + sq[2] + sq[3];
-		special = sp0 || tgq_peaked(stl[0] + stl[1] + stl[2] + stl[3], K);
-		if (t == 0 && tid == 0) s.e[0] = E, s.special[0] = special, s.qsum[0] = qsum;
+		const long long tally = stl[0] + stl[1] + stl[2] + stl[3];
+		special = sp0;
+		if (!sp0 && tgq_candidate(tally)) // uniform over the workgroup
+			special = fused_resolve<GX>(w, s, v, E, (int)(tally >> TGQ_TALLY_SHIFT), t, tid, lane, wave, F, acc32);
+		if (t == 0 && tid == 0 && special != 2) s.e[0] = E, s.special[0] = special, s.qsum[0] = qsum;
 	} else {
 		__syncthreads();
 		E = s.e[0], special = s.special[0], qsum = s.qsum[0];
 	}
 	if (wave || lane >= 16) return;
+	if (FUSED && special == 2) {
+		const int c = t * 16 + lane;
+		if (c < w.C) *out_at(a, 0, 0, c) = w.scale[c] * acc32;
+		return;
+	}
 	int p3[3] = { 0, 0, 0 };
 	for (int u = 0; u < 4; u++)
 		for (int l = 0; l < 3; l++) p3[l] += red[u][lane >> 1][lane & 1][l];
@@ -1648,7 +1789,7 @@ void tgk_qweight_free(tgk_qweight *w)
 size_t tgk_qgemm_scratch(int M, int Kp)
 {
 	long Mp = round_up(M, BM);
-	return (size_t)Mp * Kp * 3 + (size_t)Mp * (sizeof(long long) + 2 * sizeof(int) + NOUT * (sizeof(int) + sizeof(float))) + 256;
+	return (size_t)Mp * Kp * 3 + (size_t)Mp * (sizeof(long long) + 2 * sizeof(int) + tgq_nout(Kp) * (sizeof(int) + sizeof(float))) + 256;
 }
 
 tgk_qdig tgk_qgemm_digit_area(void *scratch, int M, int Kp)
@@ -1708,10 +1849,10 @@ void tgk_qgemm_split(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
 	const tgk_qweight *w = a->w;
 	const int M = a->M;
-	if (!w || !a->x || !scratch || M < TGK_SPLIT_ROWS || a->ni <= 0 || w->K <= 0) return; // small batches keep the reference's loop
+	if (!w || !a->x || !scratch || M <= 0 || a->ni <= 0 || w->K <= 0) return;
 	const Scratch s = carve(scratch, (int)round_up(M, BM), w->Kp);
 	const long waves = (M + 63) / 64;
-	split_k<<<(unsigned)(waves / 4 < 1024 ? (waves + 3) / 4 : 1024), 256, 0, st>>>(*a, s, w->K, w->Kp, M);
+	resolve_k<<<(unsigned)(waves / 4 < 1024 ? (waves + 3) / 4 : 1024), 256, 0, st>>>(*a, s, w->K, w->Kp, M);
 }
 
 int tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)

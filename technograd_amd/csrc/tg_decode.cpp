@@ -185,7 +185,7 @@ bool gemm_pre(tg_hip_dec *d, int wi, const float *x, long xr, int ni, long xj, i
 	a.o = o;
 	a.orr = orr, a.oc = 1, a.oj = oj;
 	a.M = rows * ni;
-	tgk_qgemm_split(d->st, &a, d->scratch); // large prompt chunks: the producer's peaked rows split
+	tgk_qgemm_split(d->st, &a, d->scratch); // the producer's candidate rows resolved
 	tgk_qgemm_mfma(d->st, &a, d->scratch);
 	return true;
 }

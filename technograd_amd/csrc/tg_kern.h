@@ -270,10 +270,6 @@ typedef struct {
 bool tgk_qgemm_fusable(const tgk_qgemm_args *a);
 int tgk_qgemm_fused(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 size_t tgk_qgemm_scratch(int M, int Kp);
-/* batches of at least this many rows split their peaked rows (an exact
- * outlier term plus a grid of their own) instead of taking the reference's
- * loop for them (kern_qgemm.hip: split_k) */
-#define TGK_SPLIT_ROWS 16384
 int tgk_qgemm(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 /* the digit area tgk_qgemm uses in `scratch` for M rows of Kp inputs, for
  * kernels that write a GEMM's activation digits themselves (tg_qdigits.h)
@@ -288,10 +284,11 @@ tgk_qdig tgk_qgemm_digit_area(void *scratch, int M, int Kp);
 #define TGK_DID_ROWOP 2
 void tgk_qgemm_chain(hipStream_t s, const tgk_qgemm_args *a);
 void tgk_qgemm_digits(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
-/* the split of peaked rows (TGK_SPLIT_ROWS) over digits already in the
- * scratch (tgk_qgemm_digits runs it itself; producers that write the digits
- * of a materialised activation in their own kernels call it before the
- * GEMM); a no-op for smaller batches */
+/* the resolve of candidate rows (tg_qdigits.h) over digits already in the
+ * scratch, at every batch size: each keeps its grid, is split, or takes the
+ * reference's loop (tgk_qgemm_digits runs it itself; producers that write
+ * the digits of a materialised activation in their own kernels call it
+ * before the GEMM) */
 void tgk_qgemm_split(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 int tgk_qgemm_mfma(hipStream_t s, const tgk_qgemm_args *a, void *scratch);
 

@@ -8,22 +8,26 @@
 // with a non-finite entry or max |x| above 2^100 are "special": their digits
 // are zero and the GEMM's epilogue runs the reference's sequential loop.
 //
-// Peaked rows are special too. The grid step 2^(E-23) is set by the largest
-// entry; when a few entries stand far above all the others (an outlier
-// channel), the others lose precision on that grid, and the reference's
-// sequential sum, which never sees the outlier on a channel whose code is 0,
-// would be the more accurate. The band of a row is |x| >= max|x| / 4. A row
-// is peaked when some nonzero entry lies below its band and at most
-// tgq_peak_max(K) entries lie in it (8, or max(1, K / 4) for K < 32): then
-// max|x| is at most 4 times the row's 9th largest |x| (its largest for
-// short rows), so the grid step stays within a small factor of what the
-// bulk of the row would set. Gaussian-like rows of 64 or more entries are
-// never peaked (the band holds about a third of them), rows whose entries
-// are a few values and zeros (one-hot, {0, 1}) neither; a single entry 14
-// or more standard deviations out is. Every quantity is a count, so the
-// decision does not depend on the order of any sum. Peaked rows are found
-// after their digits are written (the counts come with the sum of q); their
-// digits are then unused.
+// Rows whose grid is too coarse. The grid step 2^(E-23) is set by the
+// largest entry; when a few entries stand far above the others (outlier
+// channels), the others lose precision on that grid, and if the outliers
+// meet zero codes the product's own size no longer hides that loss. Every
+// producer tallies, per row, the sum of |q| over the row's grid and the
+// number n of inexact entries (x 2^(23-E) not an integer). A row is a
+// candidate when some entry is inexact and sum |q| < (J(n) + A(n)) 2^23,
+// with J(n) = clamp(n / 16, 1, 64) (how many of the largest entries may be
+// outliers) and A(n) = ceil(3 isqrt(n) / 4) (the grid's random rounding
+// error over n inexact entries, with a margin). Candidates take the
+// reference's loop until they are resolved (tgq_decide, a wave per row):
+// over a histogram of the row's binades below E, the smallest peel level L
+// (entries |x| >= 2^(E-L) become exact outlier terms, at most J of them) at
+// which the rest, less its own J largest entries, still holds A(n) grid
+// steps of its own. Level 0 keeps the row on its grid, a level L > 0 splits
+// it (the outliers as exact terms, the rest on a grid of its own), and no
+// level leaves it with the reference's loop. Every quantity is an integer
+// count or sum, so the decision does not depend on the order of any sum, nor
+// on which kernel or batch size makes it: a row gets the same bits in every
+// batch.
 //
 // Layout (the MFMA fragment order of v_mfma_i32_32x32x32_i8):
 //   digits [row / 32][k / 32][digit 0..2][lane 0..63][16 bytes],
@@ -47,23 +51,42 @@ __device__ inline void tgq_split3(int q, int &d0, int &d1, int &d2)
 // a row is special when an entry is not finite (bad) or max |x| exceeds 2^100
 __device__ inline int tgq_special(int bad, float amax) { return bad || amax > 0x1p100f; }
 
-// the peak test (see above): the band's floor, the per-16 tally (entries in
-// the band + 2^32 nonzero entries below it), and the decision from a row's
-// whole tally
-constexpr int TGQ_BAND_SHIFT = 2, TGQ_PEAK_N = 8;
-__device__ inline float tgq_band(float amax) { return ldexpf(amax, -TGQ_BAND_SHIFT); }
-__device__ inline int tgq_peak_max(int K) { return K >= 4 * TGQ_PEAK_N ? TGQ_PEAK_N : K >= 8 ? K >> 2 : 1; }
-__device__ inline long long tgq_tally16(const float *v, float band)
+// The candidate tally: sum |q| in bits 0..43 (|q| <= 2^23, at most 2^19
+// inputs) plus the count of inexact entries from bit 44.
+constexpr int TGQ_TALLY_SHIFT = 44;
+constexpr int TGQ_MAX_OUT = 64;  // outliers of a split row, at most
+constexpr int TGQ_MASS_SHIFT = 44; // the histogram's mass unit: 2^(E-44)
+
+__device__ inline int tgq_isqrt(int n)
 {
-	int in = 0, below = 0;
-	for (int i = 0; i < 16; i++) {
-		const float a = fabsf(v[i]);
-		in += a >= band && a != 0.0f;
-		below += a < band && a != 0.0f;
-	}
-	return (long long)in + ((long long)below << 32);
+	int r = (int)sqrtf((float)n); // then corrected: exact whatever the rounding of sqrtf
+	while (r > 0 && r * r > n) r--;
+	while ((r + 1) * (r + 1) <= n) r++;
+	return r;
 }
-__device__ inline int tgq_peaked(long long tally, int K) { return (tally >> 32) > 0 && (tally & 0xffffffffll) <= tgq_peak_max(K); }
+__device__ inline int tgq_jcap(int n) { return n < 32 ? 1 : n >= 16 * TGQ_MAX_OUT ? TGQ_MAX_OUT : n >> 4; }
+__device__ inline int tgq_acoef(int n) { return (3 * tgq_isqrt(n) + 3) >> 2; }
+// outlier slots per row of a digit area of Kp inputs (J(n) <= K / 16 <= this)
+__host__ __device__ inline int tgq_nout(int Kp) { return Kp >= 16 * TGQ_MAX_OUT ? TGQ_MAX_OUT : Kp >> 4 < 1 ? 1 : Kp >> 4; }
+
+// the tally of 16 inputs on the grid of exponent E
+__device__ inline long long tgq_tally16(const float *v, int E)
+{
+	int aq = 0, nx = 0;
+	for (int i = 0; i < 16; i++) {
+		const float sv = ldexpf(v[i], 23 - E), rq = rintf(sv);
+		aq += abs((int)rq);
+		nx += rq != sv;
+	}
+	return (long long)aq + ((long long)nx << TGQ_TALLY_SHIFT);
+}
+__device__ inline int tgq_candidate(long long tally)
+{
+	const int n = (int)(tally >> TGQ_TALLY_SHIFT);
+	if (n == 0) return 0; // every entry on the grid: the product is exact
+	const long long mass = tally & ((1ll << TGQ_TALLY_SHIFT) - 1);
+	return mass < ((long long)(tgq_jcap(n) + tgq_acoef(n)) << 23);
+}
 
 // the row exponent E from max |x| (0 for special or all-zero rows)
 __device__ inline int tgq_exponent(float amax, int special)
@@ -114,34 +137,36 @@ __device__ inline void tgq_scan_end(unsigned mb, float &mx, int &nan)
 
 // the digit words of 16 consecutive inputs: w_l[g] holds plane l's digits of
 // inputs 4 g .. 4 g + 3 (byte i: input 4 g + i); returns the sum of q and
-// adds the inputs' peak tally (band = tgq_band(max |x|)) to `tally`.
+// adds the inputs' candidate tally (tgq_tally16) to `tally`.
 // With u = q + 0x808080 (|q| <= 8355328, so 0 <= u < 2^24), byte l of u is
 // d_l + 128: the balanced digits are u's bytes with the top bit flipped. The
 // bytes of four inputs are gathered into each plane's 32-bit word with byte
 // permutes (v_perm_b32 selects bytes of a register pair: 0-3 the second
 // operand's, 4-7 the first's, 12 a zero byte).
-__device__ inline long long tgq_digits16(const float *v, int E, float band, unsigned (&w0)[4], unsigned (&w1)[4], unsigned (&w2)[4],
-					 long long &tally)
+__device__ inline long long tgq_digits16(const float *v, int E, unsigned (&w0)[4], unsigned (&w1)[4], unsigned (&w2)[4], long long &tally)
 {
-	tally += tgq_tally16(v, band);
-	int qs = 0; // |sum of 16 q| < 2^27
+	int qs = 0, aq = 0, nx = 0; // |sum of 16 q| < 2^27
 	for (int g = 0; g < 4; g++) {
 		unsigned u[4];
 		for (int i = 0; i < 4; i++) {
-			const int q = (int)rintf(ldexpf(v[4 * g + i], 23 - E)); // exact: |q| < 2^23
+			const float sv = ldexpf(v[4 * g + i], 23 - E), rq = rintf(sv);
+			const int q = (int)rq; // exact: |q| < 2^23
 			qs += q;
+			aq += abs(q);
+			nx += rq != sv;
 			u[i] = (unsigned)(q + 0x808080);
 		}
 		tgq_pack4(u, w0[g], w1[g], w2[g]);
 	}
+	tally += (long long)aq + ((long long)nx << TGQ_TALLY_SHIFT);
 	return qs;
 }
 
 // digits of 16 consecutive inputs (inputs k0 .. k0 + 15 of the row at blk)
 // into their three 16-byte chunks of the fragment layout; zero digits when
-// `zero`; returns the sum of q and adds the inputs' peak tally to `tally`
-// (nothing for a `zero` group).
-__device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E, bool zero, float band, long long &tally)
+// `zero`; returns the sum of q and adds the inputs' candidate tally to
+// `tally` (nothing for a `zero` group).
+__device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E, bool zero, long long &tally)
 {
 	int8_t *p = blk + (k0 >> 5) * 3072 + ((k0 >> 4) & 1) * 512;
 	if (__builtin_expect(zero, 0)) {
@@ -151,9 +176,142 @@ __device__ inline long long tgq_put16(int8_t *blk, int k0, const float *v, int E
 		return 0;
 	}
 	unsigned w0[4], w1[4], w2[4];
-	const long long qs = tgq_digits16(v, E, band, w0, w1, w2, tally);
+	const long long qs = tgq_digits16(v, E, w0, w1, w2, tally);
 	*(tgq_v4i *)p = tgq_v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
 	*(tgq_v4i *)(p + 1024) = tgq_v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
 	*(tgq_v4i *)(p + 2048) = tgq_v4i{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
 	return qs;
+}
+
+// ---- resolving a candidate row (a whole wave) ----
+
+__device__ inline int tgq_wave_sum(int v)
+{
+	for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+	return v;
+}
+
+// orders this wave's LDS writes and atomics before its later LDS reads of
+// other lanes' words: every LDS operation issued so far has completed
+__device__ inline void tgq_wave_sync()
+{
+	asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+	__builtin_amdgcn_wave_barrier();
+}
+
+// A row's histogram over the binades below its grid's exponent E: bin d holds
+// the nonzero entries with 2^(E-d-1) <= |x| < 2^(E-d) (d = E - frexp
+// exponent, clamped to 63), their count and the sum of floor(|x| 2^(44-E))
+// (each term an exact integer below 2^44). P and PM are the bins' prefix
+// sums: P[L] entries, PM[L] mass in bins below L.
+struct TgqHist {
+	unsigned cnt[64];
+	unsigned long long mass[64];
+	unsigned P[65];
+	unsigned long long PM[65];
+};
+
+__device__ inline int tgq_bin(float ax, int E) // ax > 0, finite, below 2^E (so E - e >= 0; clamped all the same)
+{
+	int e;
+	frexpf(ax, &e);
+	const int d = E - e;
+	return d < 0 ? 0 : d > 63 ? 63 : d;
+}
+
+// whether x is an outlier at peel level L: nonzero in a bin below L (|x| >= 2^(E-L))
+__device__ inline bool tgq_outlier(float x, int E, int L) { return x != 0.0f && tgq_bin(fabsf(x), E) < L; }
+
+// adds 16 inputs to the histogram (LDS atomics: integer sums, any order);
+// returns how many of them are inexact on the grid of E
+__device__ inline int tgq_hist16(TgqHist *h, const float *v, int E)
+{
+	int nx = 0;
+	for (int i = 0; i < 16; i++) {
+		const float ax = fabsf(v[i]);
+		if (ax == 0.0f) continue;
+		const float sv = ldexpf(v[i], 23 - E);
+		nx += rintf(sv) != sv;
+		const int d = tgq_bin(ax, E);
+		atomicAdd(&h->cnt[d], 1u);
+		atomicAdd(&h->mass[d], (unsigned long long)ldexpf(ax, TGQ_MASS_SHIFT - E)); // truncation: the floor
+	}
+	return nx;
+}
+
+// The peel level of a candidate with n inexact entries from its histogram
+// (lane L tests level L): the smallest L with at most J = J(n) entries in
+// bins below L such that the rest, less its J largest entries, still holds
+// A(n) units of its top bin r's 2^(E-r). The J largest are taken bin by bin
+// from r; a bin taken in part counts each taken entry at the bin's upper end.
+// A rest with nothing in it is enough; a top bin past 44 (a mass unit below
+// 1) is not. Returns -1 when no level is enough.
+__device__ inline int tgq_decide(TgqHist *h, int n, int lane)
+{
+	const int J = tgq_jcap(n);
+	const long long A = tgq_acoef(n);
+	const unsigned c = h->cnt[lane];
+	const unsigned long long ms = h->mass[lane];
+	unsigned pc = c; // inclusive prefix sums over the bins
+	unsigned long long pm = ms;
+	for (int o = 1; o < 64; o <<= 1) {
+		const unsigned t = __shfl_up(pc, o);
+		const unsigned long long tm = __shfl_up(pm, o);
+		if (lane >= o) pc += t, pm += tm;
+	}
+	h->P[lane + 1] = pc;
+	h->PM[lane + 1] = pm;
+	if (lane == 0) h->P[0] = 0, h->PM[0] = 0;
+	tgq_wave_sync();
+	const unsigned PL = pc - c;                               // entries in bins below L
+	const unsigned long long SL = __shfl(pm, 63) - (pm - ms); // mass in bins L and up
+	const unsigned long long rest = __ballot(c != 0) >> lane;
+	bool ok = false;
+	if (PL <= (unsigned)J) {
+		if (rest == 0) {
+			ok = true;
+		} else {
+			const int r = lane + __builtin_ctzll(rest);
+			if (r <= TGQ_MASS_SHIFT) {
+				const unsigned target = h->P[r] + (unsigned)J;
+				long long top;
+				if (h->P[64] <= target) {
+					top = (long long)SL; // the rest is J entries or fewer
+				} else {
+					int lo = r, hi = 63; // the bin where the J largest end: P[lo + 1] >= target
+					while (lo < hi) {
+						const int mid = (lo + hi) >> 1;
+						if (h->P[mid + 1] >= target) hi = mid;
+						else lo = mid + 1;
+					}
+					top = h->P[lo + 1] == target ? (long long)(h->PM[lo + 1] - h->PM[r])
+								    : (long long)(h->PM[lo] - h->PM[r]) +
+									      (lo <= TGQ_MASS_SHIFT ? (long long)(target - h->P[lo]) << (TGQ_MASS_SHIFT - lo) : 0ll);
+				}
+				ok = (long long)SL - top >= A << (TGQ_MASS_SHIFT - r);
+			}
+		}
+	}
+	const unsigned long long okm = __ballot(ok);
+	return okm ? __builtin_ctzll(okm) : -1;
+}
+
+// Resolves a candidate row of grid exponent E (a whole wave; h in LDS, this
+// wave's own): ld(g, v) loads the row's 16-input group g of ng (zeros past
+// the row). Returns the peel level: 0 the grid, L > 0 a split at level L
+// (tgq_outlier), -1 the reference's loop.
+template <class Ld>
+__device__ inline int tgq_resolve(TgqHist *h, Ld ld, int ng, int E, int lane)
+{
+	h->cnt[lane] = 0;
+	h->mass[lane] = 0;
+	tgq_wave_sync();
+	int nx = 0;
+	for (int g = lane; g < ng; g += 64) {
+		float v[16];
+		ld(g, v);
+		nx += tgq_hist16(h, v, E);
+	}
+	tgq_wave_sync();
+	return tgq_decide(h, tgq_wave_sum(nx), lane);
 }

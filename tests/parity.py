@@ -24,6 +24,8 @@ a few percent of outputs), when the GPU result is accurate against a truth:
   computed as well by the GPU.
 Every check reports how many elements needed the second clause.
 """
+import math
+
 import numpy as np
 
 U = 2.0 ** -24
@@ -107,50 +109,139 @@ def check_model(gpu, ref, truth=None, steps_same=None):
 
 def grid_bound(codes_ck, scale_c, x_mk):
     """The digit path's own error bound against the exact product, for rows
-    that are not special: the 24-bit activation grid, 2^-23 max|x| per
-    element (tests of the host restatement only; not a parity predicate)."""
+    on their grid: the 24-bit activation grid, 2^-23 max|x| per element
+    (tests of the host restatement only; not a parity predicate)."""
     codes = np.asarray(codes_ck, np.float64)
     x = np.asarray(x_mk, np.float64)
     s = np.abs(np.asarray(scale_c, np.float64))
     return 2.0 ** -23 * s[None, :] * np.abs(x).max(axis=1)[:, None] * np.abs(codes).sum(axis=1)[None, :]
 
 
-def peaked_rows(x_mk):
-    """Rows the digit kernels flag as peaked (technograd_amd/csrc/tg_qdigits.h):
-    some nonzero entry below the band |x| >= max|x| / 4, and at most
-    8 (max(1, K / 4) for K < 32) entries in the band."""
+# Row classes (technograd_amd/csrc/tg_qdigits.h), restated: which rows keep
+# their 24-bit grid, which are split (outliers as exact terms, the rest on a
+# grid of its own), which take the reference's loop. Integer arithmetic
+# only, as on the device.
+MAX_OUT = 64     # outliers of a split row, at most (TGQ_MAX_OUT)
+MASS_SHIFT = 44  # the histogram's mass unit 2^(E-44) (TGQ_MASS_SHIFT)
+
+
+def jcap(n):
+    """J(n): how many of a row's largest entries may be outliers."""
+    return 1 if n < 32 else MAX_OUT if n >= 16 * MAX_OUT else n >> 4
+
+
+def acoef(n):
+    """A(n) = ceil(3 isqrt(n) / 4): grid steps the rest must hold."""
+    return (3 * math.isqrt(int(n)) + 3) >> 2
+
+
+def grid_rows(x_mk):
+    """(special [M], E [M]): special rows have a NaN, or max |x| above 2^100
+    (inf included); E from max |x| (frexp), raised by one when
+    rint(max |x| 2^(23-E)) > 8355328; 0 for special and all-zero rows."""
     x = np.asarray(x_mk, np.float32)
     a = np.abs(x)
+    nan = np.isnan(x).any(axis=1)
     with np.errstate(invalid="ignore"):
-        amax = np.where(np.isnan(x).any(axis=1), np.float32(0), a.max(axis=1)).astype(np.float32)
-        band = np.ldexp(amax, np.int32(-2)).astype(np.float32)
-        nz = a != 0
-        inb = ((a >= band[:, None]) & nz).sum(axis=1)
-        below = ((a < band[:, None]) & nz).sum(axis=1)
-    K = x.shape[1]
-    return (below > 0) & (inb <= (8 if K >= 32 else max(1, K >> 2)))
-
-
-def digit_path_matmul(x_mk, codes_kc, scale_c, peak=True, f64=False):
-    """The matrix-core path's arithmetic, restated on the host (not the
-    reference's order): per row, E from max |x| (frexp; raised by one when
-    rint(max |x| 2^(23-E)) > 8355328), q = rint(x 2^(23-E)) exactly, the exact
-    integer sum t = sum_k code[k, c] q[m, k], then f32(t 2^(E-23)) * s[c] in
-    f32. Rows with a NaN or max |x| above 2^100 (inf included), and peaked
-    rows (peaked_rows), are special: the device runs the reference's loop for
-    them (reference_loop); they are returned masked. peak=False leaves peaked
-    rows on the grid (the path before the peak test; tests plant it).
-    f64: return the grid sums t 2^(E-23) unrounded (scale_c not applied).
-    Returns (f32 [M, C], special [M])."""
-    x = np.asarray(x_mk, np.float32)
-    amax = np.abs(x).max(axis=1)
-    special = np.isnan(x).any(axis=1) | (amax > np.float32(2.0 ** 100))
-    if peak:
-        special |= peaked_rows(x) & ~special
+        amax = np.where(nan, np.float32(0), a.max(axis=1)).astype(np.float32)
+    special = nan | (amax > np.float32(2.0 ** 100))
     _, E = np.frexp(np.where(special, 0, amax).astype(np.float64))
     E = np.where(amax > 0, E, 0).astype(np.int64)
     top = np.rint(np.ldexp(np.where(special, 0, amax).astype(np.float64), 23 - E))
     E = np.where((top > 8355328) & ~special, E + 1, E)
+    return special, np.where(special, 0, E)
+
+
+def candidates(x_mk):
+    """The producers' test (tgq_candidate): (candidate [M], n [M]) with n the
+    entries inexact on the row's grid; a candidate has n > 0 and
+    sum |q| < (J(n) + A(n)) 2^23."""
+    x = np.asarray(x_mk, np.float32)
+    special, E = grid_rows(x)
+    xs = np.where(special[:, None], 0, x).astype(np.float64)
+    v = np.ldexp(xs, (23 - E)[:, None])
+    q = np.rint(v)
+    n = (q != v).sum(axis=1)
+    mass = np.abs(q).sum(axis=1)
+    thr = np.array([(jcap(int(k)) + acoef(int(k))) << 23 for k in n], np.float64)
+    return ~special & (n > 0) & (mass < thr), n
+
+
+def _bins(a, E):
+    """bin of each |x| > 0: E - (frexp exponent), at most 63"""
+    _, e = np.frexp(a)
+    return np.minimum(E - e, 63)
+
+
+def resolve_row(x_k, E, n):
+    """tgq_decide on one candidate row: the peel level (0 the grid, L > 0 a
+    split at level L, -1 the reference's loop)."""
+    a = np.abs(np.asarray(x_k, np.float32).astype(np.float64))
+    a = a[a != 0]
+    d = _bins(a, E)
+    mass = np.floor(np.ldexp(a, MASS_SHIFT - E)).astype(np.int64)
+    cnt = np.bincount(d, minlength=64)
+    ms = np.zeros(64, np.int64)
+    np.add.at(ms, d, mass)
+    J, A = jcap(n), acoef(n)
+    P = np.concatenate([[0], np.cumsum(cnt)])
+    for L in range(64):
+        if P[L] > J:
+            continue
+        nz = np.flatnonzero(cnt[L:])
+        if len(nz) == 0:
+            return L
+        r = L + int(nz[0])
+        if r > MASS_SHIFT:
+            continue
+        left, top = J, 0
+        for dd in range(r, 64):  # the rest's J largest, bin by bin from its top
+            take = min(int(cnt[dd]), left)
+            top += int(ms[dd]) if take == cnt[dd] else (take << (MASS_SHIFT - dd) if dd <= MASS_SHIFT else 0)
+            left -= take
+            if left == 0:
+                break
+        if int(ms[L:].sum()) - top >= A << (MASS_SHIFT - r):
+            return L
+    return -1
+
+
+def row_classes(x_mk):
+    """(cls [M], level [M], E [M]) as the device decides them: cls 0 a row on
+    its grid, 1 the reference's loop (special rows, and candidates no level
+    resolves), 2 a split row at peel level `level` (outliers: nonzero
+    entries with |x| >= 2^(E - level))."""
+    x = np.asarray(x_mk, np.float32)
+    special, E = grid_rows(x)
+    cand, n = candidates(x)
+    cls = np.where(special, 1, 0)
+    level = np.zeros(x.shape[0], np.int64)
+    for m in np.flatnonzero(cand):
+        L = resolve_row(x[m], int(E[m]), int(n[m]))
+        cls[m] = 1 if L < 0 else 2 if L > 0 else 0
+        level[m] = max(L, 0)
+    return cls, level, E
+
+
+def outlier_mask(x_mk, E, level):
+    """the outliers of split rows at their levels (nonzero, bin below level)"""
+    a = np.abs(np.asarray(x_mk, np.float32).astype(np.float64))
+    with np.errstate(divide="ignore"):
+        d = _bins(np.where(a == 0, 1.0, a), np.asarray(E)[:, None])
+    return (a != 0) & (d < np.asarray(level)[:, None])
+
+
+def digit_path_matmul(x_mk, codes_kc, scale_c, f64=False):
+    """The matrix-core path's arithmetic for rows on their grid, restated on
+    the host (not the reference's order): per row, E from max |x|
+    (grid_rows), q = rint(x 2^(23-E)) exactly, the exact integer sum
+    t = sum_k code[k, c] q[m, k], then f32(t 2^(E-23)) * s[c] in f32. Rows
+    with a NaN or max |x| above 2^100 (inf included) are special: the device
+    runs the reference's loop for them; they are returned masked.
+    f64: return the grid sums t 2^(E-23) unrounded (scale_c not applied).
+    Returns (f32 [M, C], special [M])."""
+    x = np.asarray(x_mk, np.float32)
+    special, E = grid_rows(x)
     xs = np.where(special[:, None], 0, x).astype(np.float64)
     q = np.rint(np.ldexp(xs, (23 - E)[:, None]))                        # exact integers, |q| < 2^23
     t = q @ np.asarray(codes_kc, np.float64)                              # exact: every partial sum < 2^53
@@ -173,66 +264,65 @@ def reference_loop(x_mk, codes_kc, scale_c):
         return acc * np.asarray(scale_c, np.float32)[None, :]
 
 
-def split_rows_matmul(x_mk, codes_kc, scale_c):
-    """Split rows (technograd_amd/csrc/kern_qgemm.hip: split_k, batches of
-    TGK_SPLIT_ROWS rows or more): a peaked row's band entries (|x| >=
-    max|x| / 4, nonzero) are outliers; the other entries are put on a grid of
-    their own (E from their largest magnitude, as digit_path_matmul); each
-    output is f32(g + o) * s[c] with g = t 2^(E-23) the grid sum and
-    o = sum over the outliers in increasing k of code[k, c] x_k, both in f64
-    (every product exact, o summed from 0.0 in k order)."""
+def split_rows_matmul(x_mk, codes_kc, scale_c, omask):
+    """Split rows (kern_qgemm.hip: resolve_k and the epilogue): the outliers
+    (omask) are exact terms, the other entries are put on a grid of their
+    own (E from their largest magnitude, as digit_path_matmul); each output
+    is f32(g + o) * s[c] with g = t 2^(E-23) the grid sum and o = sum over
+    the outliers in increasing k of code[k, c] x_k, both in f64 (every
+    product exact, o summed from 0.0 in k order)."""
     x = np.asarray(x_mk, np.float32)
     codes = np.asarray(codes_kc, np.float64)
-    a = np.abs(x)
-    amax = a.max(axis=1)
-    band = np.ldexp(amax, np.int32(-2)).astype(np.float32)
-    inb = (a >= band[:, None]) & (a != 0)
-    rest = np.where(inb, np.float32(0), x)
-    g, _ = digit_path_matmul(rest, codes_kc, np.ones(codes.shape[1], np.float32), peak=False, f64=True)
+    rest = np.where(omask, np.float32(0), x)
+    g, _ = digit_path_matmul(rest, codes_kc, np.ones(codes.shape[1], np.float32), f64=True)
     out = np.empty((x.shape[0], codes.shape[1]), np.float32)
     for m in range(x.shape[0]):
         o = np.zeros(codes.shape[1])
-        for k in np.flatnonzero(inb[m]):
+        for k in np.flatnonzero(omask[m]):
             o = o + codes[k] * np.float64(x[m, k])
         out[m] = (g[m] + o).astype(np.float32) * np.asarray(scale_c, np.float32)
     return out
 
 
-def device_path_matmul(x_mk, codes_kc, scale_c, peak=True, split=False):
-    """What the device computes for x @ W: the digit path, and the reference's
-    loop for special rows; with split (batches of TGK_SPLIT_ROWS rows or
-    more) peaked rows that are finite and at most 2^100 are split rows
-    instead (split_rows_matmul). Returns (f32 [M, C], special [M]): special
-    marks the rows off the plain grid."""
-    got, special = digit_path_matmul(x_mk, codes_kc, scale_c, peak)
-    if special.any():
-        x = np.asarray(x_mk, np.float32)
-        ref = special.copy()
-        if split:
-            amax = np.abs(x).max(axis=1)
-            sp = special & ~np.isnan(x).any(axis=1) & (amax <= np.float32(2.0 ** 100))
-            if sp.any():
-                got[sp] = split_rows_matmul(x[sp], codes_kc, scale_c)
-            ref &= ~sp
-        if ref.any():
-            got[ref] = reference_loop(x[ref], codes_kc, scale_c)
-    return got, special
+def device_path_matmul(x_mk, codes_kc, scale_c):
+    """What the device computes for x @ W, at any batch size: rows on their
+    grid (digit_path_matmul), split rows (split_rows_matmul) and the
+    reference's loop, by row_classes. Returns (f32 [M, C], cls [M])."""
+    x = np.asarray(x_mk, np.float32)
+    got, _ = digit_path_matmul(x, codes_kc, scale_c)
+    cls, level, E = row_classes(x)
+    sp = cls == 2
+    if sp.any():
+        got[sp] = split_rows_matmul(x[sp], codes_kc, scale_c, outlier_mask(x[sp], E[sp], level[sp]))
+    if (cls == 1).any():
+        got[cls == 1] = reference_loop(x[cls == 1], codes_kc, scale_c)
+    return got, cls
 
 
 def outlier_rows(K, codes_kc, seed=0):
-    """Rows with outliers where the per-row grid would be too coarse, and
-    rows that stay on the grid: one outlier 1e2, 1e3, 1e4, 1e6 times the rest
-    on a column whose codes are all zero; two opposite outliers of 1e3 and
-    1e5 on two columns with equal codes (their terms cancel); a single 14
-    sigma entry; and three dense rows: nine entries at 30 sigma, a row
-    scaled by 1e4 as a whole, a plain N(0, 1) row. codes_kc is modified:
-    column z0 becomes all zero, column c1 a copy of c0. Returns (x [10, K],
-    expected special flags [10])."""
+    """Rows with outliers where one grid for the row would be too coarse,
+    and rows that stay on their grid. codes_kc is modified: its first
+    64 + 3 columns of a seeded permutation become all-zero codes (z0 and the
+    zero-code outlier columns) and column c1 a copy of c0. Rows:
+      0-3  one outlier 1e2, 1e3, 1e4, 1e6 times the rest on an all-zero column;
+      4-5  two opposite outliers (1e3, 1e5) on two columns with equal codes
+           (their terms cancel);
+      6    a single 14 sigma entry;
+      7-8  nine entries at 30 sigma, a row scaled by 1e4 as a whole;
+      9    a plain N(0, 1) row;
+      10-33 n = 9, 16, 32, 64 outliers of 1e2, 1e3, 1e4 (random signs), on
+           all-zero columns (even rows) and on columns with codes (odd rows).
+    Returns (x [34, K], planted [34]: rows 0-5 and 10-33, whose outliers
+    must not leave them on one grid)."""
     rng = np.random.default_rng(seed)
-    z0, c0, c1 = 3, 10, K - 7
+    perm = rng.permutation(K)
+    z0, c0, c1 = int(perm[0]), int(perm[1]), int(perm[2])
+    zcols = perm[3:3 + min(64, K - 3)]
     codes_kc[z0] = 0
+    codes_kc[zcols] = 0
     codes_kc[c1] = codes_kc[c0]
-    x = rng.normal(size=(10, K)).astype(np.float32)
+    live = perm[3 + len(zcols):]
+    x = rng.normal(size=(34, K)).astype(np.float32)
     for i, f in enumerate((1e2, 1e3, 1e4, 1e6)):
         x[i, z0] = f
     x[4, c0], x[4, c1] = 1e3, -1e3
@@ -240,4 +330,14 @@ def outlier_rows(K, codes_kc, seed=0):
     x[6, K // 2] = 14.0
     x[7, rng.choice(K, 9, replace=False)] = 30.0
     x[8] *= 1e4
-    return x, np.array([True] * 7 + [False] * 3)
+    i = 10
+    for n in (9, 16, 32, 64):
+        for f in (1e2, 1e3, 1e4):
+            for cols in (zcols, live):
+                sel = rng.choice(cols, min(n, len(cols)), replace=False)
+                x[i, sel] = (f * rng.choice([-1.0, 1.0], len(sel))).astype(np.float32)
+                i += 1
+    planted = np.zeros(34, bool)
+    planted[:6] = True
+    planted[10:] = True
+    return x, planted

@@ -1,17 +1,17 @@
 """The host restatement of the matrix-core path's arithmetic
-(parity.digit_path_matmul), which the GPU launch-shape tests compare against
-bit for bit, pinned on the CPU: to the exact real product within the 24-bit
-activation grid's bound, to the reference's sequential order (the oracle)
-under the parity predicate, on rows with outliers (the peak test sends them
-to the reference's loop, and without it the predicate fails), and on cases
-whose answer is fixed by hand."""
+(parity.digit_path_matmul, parity.device_path_matmul), which the GPU tests
+compare against bit for bit, pinned on the CPU: to the exact real product
+within the 24-bit activation grid's bound, to the reference's sequential
+order (the oracle) under the parity predicate, on rows with outliers (the
+row classes split them or send them to the reference's loop; with one grid
+per row the predicate fails), and on cases whose answer is fixed by hand."""
 import numpy as np
 import pytest
 
 from oracle import oracle as O
 from technograd_amd import synth
-from parity import (check_qmatmul, device_path_matmul, digit_path_matmul, grid_bound, outlier_rows, peaked_rows,
-                    qmatmul_truth, reference_loop, ulp)
+from parity import (check_qmatmul, device_path_matmul, digit_path_matmul, grid_bound, outlier_mask, outlier_rows,
+                    qmatmul_truth, reference_loop, row_classes, ulp)
 
 
 def _case(seed, M=7, K=96, C=40, lim=7):
@@ -56,68 +56,91 @@ def test_reference_loop_is_the_oracle():
 
 @pytest.mark.parametrize("bits", [4, 8])
 def test_outlier_rows_against_the_oracle(bits):
-    """K = 4096: rows with one outlier of 1e2 to 1e6 on a zero-code column,
-    cancelling outliers, a 14 sigma entry, and dense rows. What the device
-    computes (the digit path, the reference's loop for special rows) against
-    the oracle: peaked rows are special and bit-identical with the oracle; the
-    rest pass the parity predicate. With the peak test taken out (the per-row
-    grid for every row), the predicate fails."""
+    """K = 4096: rows with 1 to 64 outliers of 1e2 to 1e6 (on all-zero code
+    columns and on columns with codes), cancelling outliers, a 14 sigma
+    entry, and dense rows. Every planted row leaves its single grid (split,
+    or the reference's loop) and the dense rows keep it; what the device
+    computes passes the parity predicate against the oracle, rows of the
+    reference's loop bit for bit, and each split row is within its own
+    grid's bound of the exact product (the grid of the entries other than
+    its outliers) plus one f32 rounding. With one grid per row (no classes)
+    the predicate fails."""
     K, C = 4096, 256
     lim = 7 if bits == 4 else 127
     rng = np.random.default_rng(bits)
     codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)
     scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
-    x, want_special = outlier_rows(K, codes)
-    assert np.array_equal(peaked_rows(x), want_special)
+    x, planted = outlier_rows(K, codes)
+    cls, level, E = row_classes(x)
+    assert (cls[planted] != 0).all() and (cls[7:10] == 0).all(), cls
     text = synth.linear_tgir_codes("lq", codes, scales, bits, axis=1)
     ref, _ = O.Model(text).batch(x)
-    got, special = device_path_matmul(x, codes, scales)
-    assert np.array_equal(special, want_special)
-    assert np.array_equal(got[special].view(np.uint32), ref[special].view(np.uint32))
+    got, cls2 = device_path_matmul(x, codes, scales)
+    assert np.array_equal(cls, cls2)
+    assert np.array_equal(got[cls == 1].view(np.uint32), ref[cls == 1].view(np.uint32))
     check_qmatmul(got, ref, codes.T, scales, x)
-    coarse, _ = device_path_matmul(x, codes, scales, peak=False)
+    sp = cls == 2
+    truth, _ = qmatmul_truth(codes.T, scales, x)
+    rest = np.where(outlier_mask(x[sp], E[sp], level[sp]), 0, x[sp])
+    bound = grid_bound(codes.T, scales, rest) + np.abs(truth[sp]) * 2.0 ** -23
+    assert (np.abs(got[sp] - truth[sp]) <= bound).all()
+    coarse, _ = digit_path_matmul(x, codes, scales)
     with pytest.raises(AssertionError):
         check_qmatmul(coarse, ref, codes.T, scales, x)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
-def test_split_rows_against_the_oracle(bits):
-    """The split of peaked rows (large batches): the same outlier rows through
-    split_rows_matmul pass the parity predicate against the oracle, and each
-    split row is within its own grid's bound of the exact product (the grid
-    set by the entries below the band, not by the outlier), plus one f32
-    rounding."""
-    K, C = 4096, 256
-    lim = 7 if bits == 4 else 127
-    rng = np.random.default_rng(bits + 10)
-    codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)
-    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
-    x, want_special = outlier_rows(K, codes)
-    text = synth.linear_tgir_codes("lq", codes, scales, bits, axis=1)
-    ref, _ = O.Model(text).batch(x)
-    got, special = device_path_matmul(x, codes, scales, split=True)
-    assert np.array_equal(special, want_special)
-    check_qmatmul(got, ref, codes.T, scales, x)
-    truth, _ = qmatmul_truth(codes.T, scales, x)
-    rest = np.where(np.abs(x) >= np.ldexp(np.abs(x).max(axis=1), -2)[:, None], 0, x)
-    bound = grid_bound(codes.T, scales, rest) + np.abs(truth) * 2.0 ** -23
-    assert (np.abs(got[special] - truth[special]) <= bound[special]).all()
+@pytest.mark.parametrize("kind", ["gauss", "laplace", "t3", "silu_up", "sparse"])
+def test_dense_and_heavy_tailed_rows(kind):
+    """Rows without planted outliers, at the configs' widths: Gaussian,
+    Laplace, Student t(3), products silu(g) * u (config 3's and 5's gated
+    activations) and 95 %-sparse Gaussian rows. The device path passes the
+    parity predicate against the oracle; Gaussian and Laplace rows of 1024
+    or more inputs all keep their grid."""
+    rng = np.random.default_rng(len(kind))
+    for K in (64, 512, 1024, 3072):
+        C, M = 64, 48
+        codes = rng.integers(-7, 8, size=(K, C)).astype(np.int8)
+        scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
+        if kind == "gauss":
+            x = rng.normal(size=(M, K))
+        elif kind == "laplace":
+            x = rng.laplace(size=(M, K))
+        elif kind == "t3":
+            x = rng.standard_t(3, size=(M, K))
+        elif kind == "silu_up":
+            g = rng.normal(size=(M, K))
+            x = g / (1 + np.exp(-g)) * rng.normal(size=(M, K))
+        else:
+            x = rng.normal(size=(M, K)) * (rng.random((M, K)) < 0.05)
+        x = x.astype(np.float32)
+        text = synth.linear_tgir_codes("lq", codes, scales, 4, axis=1)
+        ref, _ = O.Model(text).batch(x)
+        got, cls = device_path_matmul(x, codes, scales)
+        check_qmatmul(got, ref, codes.T, scales, x)
+        if kind in ("gauss", "laplace") and K >= 1024:
+            assert (cls == 0).all()
 
 
-def test_split_hand_case():
-    """integers: the rest's grid holds them exactly and the outlier term is
-    exact, so a split row's output is the exact product rounded once"""
-    x = np.zeros((1, 40), np.float32)
-    x[0, :39] = np.arange(1, 40) % 7 - 3
-    x[0, 39] = 1000.0
+def test_row_classes_hand_cases():
+    """Integers on the row's grid are exact whatever their spread: no
+    candidate, the exact product rounded once. The same spread with the
+    small entries off the full grid (multiples of 2^-20 next to 1000) is
+    split at the first level: the rest's own grid holds it exactly and the
+    outlier term is exact, so the output is again the exact product rounded
+    once, where one grid would lose the small entries."""
     codes = (np.arange(40 * 3).reshape(40, 3) % 5 - 2).astype(np.int8)
-    assert peaked_rows(x).all()
-    got, special = device_path_matmul(x, codes, np.ones(3, np.float32), split=True)
+    one = np.ones(3, np.float32)
+    x = np.zeros((2, 40), np.float32)
+    x[:, :39] = np.arange(1, 40) % 7 - 3
+    x[:, 39] = 1000.0
+    x[1, :39] *= np.float32(2.0 ** -20)
+    cls, level, _ = row_classes(x)
+    assert cls.tolist() == [0, 2] and level[1] == 1
+    got, _ = device_path_matmul(x, codes, one)
     want = (x.astype(np.float64) @ codes.astype(np.float64)).astype(np.float32)
-    assert special.all() and np.array_equal(got, want)
-    # without the split the same row takes the reference's loop
-    got0, _ = device_path_matmul(x, codes, np.ones(3, np.float32))
-    assert np.array_equal(got0, reference_loop(x, codes, np.ones(3, np.float32)))
+    assert np.array_equal(got, want)
+    coarse, _ = digit_path_matmul(x[1:], codes, one)
+    assert not np.array_equal(coarse, want[1:])
 
 
 def test_hand_cases():

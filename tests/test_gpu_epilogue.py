@@ -10,7 +10,7 @@ when a tile holds whole lines (C <= 256, channel stride 1) and after it
 otherwise; the cases cover both, every other GEMM kernel (one row, up to 16
 rows, the small-batch tiles), int4 and int8 weights, both operand orders,
 all three operand forms, rows the reference's loop takes (inf, nan), and a
-peaked line (an outlier), which batches of 16384 lines or more split."""
+line with an outlier (a split row)."""
 import numpy as np
 import pytest
 
@@ -69,7 +69,7 @@ def _rows(seed, rows, per, specials=False):
         x[1, 5] = np.inf
         x[2, 7] = np.nan
         x[3, :] *= 1e-30
-        x[4, 10] = 1e4  # an outlier: its line is peaked (a split row in batches of 16384 lines or more)
+        x[4, 10] = 1e4  # an outlier: its line is a split row
     return x
 
 

@@ -2,8 +2,8 @@
 launch_gemm): the large-batch LDS kernel and each (NB column blocks, W waves)
 instantiation of the small-batch kernel, int4 and int8 weights, checked bit
 for bit against the path's own arithmetic restated on the host
-(tests/parity.py: device_path_matmul: the digit path, and the reference's
-loop for a peaked row). The reference-order parity of the same
+(tests/parity.py: device_path_matmul: the digit path, a split row for an
+outlier, and the reference's loop for special rows). The reference-order parity of the same
 entry point is in test_gpu_parity.py."""
 import numpy as np
 import pytest
@@ -70,17 +70,17 @@ def test_launch_shape_bit_exact(bits_, M, K, C):
     if M > 2:
         x[2] *= 1e-30
     if M > 3:
-        x[3, K // 3] = 1e4  # an outlier: a peaked row, the reference's loop
+        x[3, K // 3] = 1e4  # an outlier: its row leaves its grid (split)
     got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
-    want, special = device_path_matmul(x, codes, scales)
-    assert special.sum() == (M > 3)
+    want, cls = device_path_matmul(x, codes, scales)
+    assert M <= 3 or cls[3] != 0
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.argwhere(got != want)[:5].tolist()
 
 
 @pytest.mark.parametrize("K", [4096, 1000])
 def test_single_row_kinds(K):
     """One row at a time (the single-row kernel, fused at K = 4096, fed by
-    the digit kernel at K = 1000): an outlier row (peaked), rows with inf,
+    the digit kernel at K = 1000): an outlier row (split), rows with inf,
     nan or an entry above 2^100 (special), a row of zeros, a tiny row and a
     plain row, each bit for bit against the path restated on the host."""
     from technograd_amd import hip
@@ -98,8 +98,8 @@ def test_single_row_kinds(K):
     rows[3, 9] = 2e30
     rows[4] = 0
     rows[5] *= 1e-30
-    want, special = device_path_matmul(rows, codes, scales)
-    assert special.tolist() == [True, True, True, True, False, False, False]
+    want, cls = device_path_matmul(rows, codes, scales)
+    assert cls.tolist() == [2, 1, 1, 1, 0, 0, 0]
     for i in range(len(rows)):
         got = hip.matmul_q(packed, 4, scales, rows[i:i + 1], 1, K, C, 1)
         assert np.array_equal(np.isnan(got[0]), np.isnan(want[i]))

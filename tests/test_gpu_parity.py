@@ -240,85 +240,76 @@ def test_config1_full_width():
           flush=True)
 
 
-@pytest.mark.parametrize("bits_,M", [(4, 10), (8, 10), (4, 1024)])
-def test_outlier_rows_follow_reference(bits_, M):
-    """K = 4096, C = 4096, x @ W: rows with one outlier of 1e2 to 1e6 on a
-    zero-code column, cancelling outliers and a 14 sigma entry are peaked
-    and take the reference's loop (bit-identical with the oracle); dense rows
-    pass the parity predicate. M = 10 runs the small-batch kernel; M = 1024
-    (the same rows among N(0, 1) rows) the large-batch kernel."""
-    print("case outlier rows", bits_, M, flush=True)
-    K = C = 4096
-    lim = 7 if bits_ == 4 else 127
-    rng = np.random.default_rng(bits_ + M)
-    codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)
-    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
-    xo, sp = parity.outlier_rows(K, codes, seed=M)
-    x = rng.normal(size=(M, K)).astype(np.float32)
-    at = np.linspace(0, M - 1, len(xo)).astype(int)
-    x[at] = xo
+def _packed(stored, bits_):
     if bits_ == 4:
-        flat = codes.ravel().astype(np.int64)
-        packed = ((flat[0::2] & 15) | ((flat[1::2] & 15) << 4)).astype(np.uint8).view(np.int8)
-    else:
-        packed = codes.ravel()
-    got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
-    text = synth.linear_tgir_codes("lq", codes, scales, bits_, axis=1)
-    want, _ = O.Model(text).batch(x, threads=16)
-    special = parity.peaked_rows(x)
-    assert np.array_equal(special[at], sp) and special.sum() == sp.sum()
-    assert np.array_equal(bits(got[special]), bits(want[special]))
-    frac, ng, nr = parity.check_qmatmul(got, want, codes.T, scales, x)
-    print("outlier rows: %.4f by the normalized clause; largest normalized error: GPU %.2f, reference %.2f" % (frac, ng, nr),
-          flush=True)
+        flat = stored.ravel().astype(np.int64)
+        return ((flat[0::2] & 15) | ((flat[1::2] & 15) << 4)).astype(np.uint8).view(np.int8)
+    return stored.ravel()
 
 
-@pytest.mark.parametrize("bits_,axis", [(4, 1), (8, 1), (4, 0)])
-def test_split_rows_in_large_batches(bits_, axis):
-    """M = 16384 (TGK_SPLIT_ROWS): the same outlier rows among N(0, 1) rows
-    are split (their band entries as exact outlier terms, a grid of their own
-    for the rest), bit-identical with the host restatement
-    (parity.device_path_matmul with split) and within the parity predicate
-    against the oracle; rows with a NaN or an infinity keep the reference's
-    loop, bit-identical with the oracle. axis 0 (W @ x: the rows are columns
-    of b, element k at stride M) reads the rows and the codes strided."""
-    print("case split rows", bits_, axis, flush=True)
-    M, K, C = 16384, 1024, 1024
+def _same(a, b):
+    """NaN where the other is NaN (payloads aside), the other elements bit for bit"""
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(bits(a[~na]), bits(b[~nb]))
+
+
+@pytest.mark.parametrize("bits_,axis", [(4, 1), (8, 1), (4, 0), (8, 0)])
+def test_outlier_rows_at_every_batch_size(bits_, axis):
+    """K = C = 1024: rows with 1 to 64 outliers of 1e2 to 1e6 on all-zero
+    code columns and on columns with codes, cancelling outliers, a 14 sigma
+    entry and dense rows (parity.outlier_rows), run alone (M = 1, the fused
+    single-row kernel, int4), ten at a time (M = 10), sixteen at a time
+    (M = 16) and among N(0, 1) rows with a NaN row and an infinite row
+    (M = 1024 and 16384). Every output equals the host restatement
+    (parity.device_path_matmul: the same row classes, splits and reference
+    loops) bit for bit, so a row's bits are the same at every batch size;
+    the planted rows pass the parity predicate against the oracle and the
+    NaN and infinite rows equal it. axis 0 (W @ x: the rows are columns of
+    b, element k at stride M) reads the rows and the codes strided."""
+    print("case outlier rows", bits_, axis, flush=True)
+    K = C = 1024
     lim = 7 if bits_ == 4 else 127
     rng = np.random.default_rng(40 + bits_ + 7 * axis)
     codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)
     scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
-    xo, sp = parity.outlier_rows(K, codes, seed=bits_)
-    x = rng.normal(size=(M, K)).astype(np.float32)
-    at = np.linspace(3, M - 4, len(xo)).astype(int)
-    x[at] = xo
-    x[1, 17], x[M - 2, 5] = np.nan, np.inf
+    xo, planted = parity.outlier_rows(K, codes, seed=bits_ + axis)
     stored = codes if axis == 1 else np.ascontiguousarray(codes.T)  # the param's own layout: [K][C] or [C][K]
-    if bits_ == 4:
-        flat = stored.ravel().astype(np.int64)
-        packed = ((flat[0::2] & 15) | ((flat[1::2] & 15) << 4)).astype(np.uint8).view(np.int8)
-    else:
-        packed = stored.ravel()
-    if axis == 1:
-        got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
-    else:  # o = diag(s) Q @ b with b = x^T [K][M]: o is [C][M]
-        got = np.ascontiguousarray(hip.matmul_q(packed, bits_, scales, np.ascontiguousarray(x.T), C, K, M, 0).T)
-    sub = np.concatenate([at, [1, M - 2], rng.choice(M, 6, replace=False)])
-    want, special = parity.device_path_matmul(x[sub], codes, scales, split=True)
-    assert special[:len(at)].tolist() == sp.tolist() and special[len(at):len(at) + 2].all()
-    def same(a, b):  # NaN where the other is NaN (payloads aside), the other elements bit for bit
-        na, nb = np.isnan(a), np.isnan(b)
-        return np.array_equal(na, nb) and np.array_equal(bits(a[~na]), bits(b[~nb]))
+    packed = _packed(stored, bits_)
 
-    assert same(got[sub], want)
+    def run(x):
+        M = len(x)
+        if axis == 1:
+            return hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
+        return np.ascontiguousarray(hip.matmul_q(packed, bits_, scales, np.ascontiguousarray(x.T), C, K, M, 0).T)
+
+    want, cls = parity.device_path_matmul(xo, codes, scales)
+    assert (cls[planted] != 0).all()
     text = synth.linear_tgir_codes("lq", codes, scales, bits_, axis=1)  # the reference's x @ W on the same codes
-    ref, _ = O.Model(text).batch(x[sub], threads=16)
-    assert same(got[[1, M - 2]], ref[len(at):len(at) + 2])
-    keep = np.ones(len(sub), bool)
-    keep[len(at):len(at) + 2] = False
-    frac, ng, nr = parity.check_qmatmul(got[sub][keep], ref[keep], codes.T, scales, x[sub][keep])
-    print("split rows: %.4f by the normalized clause; largest normalized error: GPU %.2f, reference %.2f" % (frac, ng, nr),
-          flush=True)
+    ref, _ = O.Model(text).batch(xo, threads=16)
+    frac, ng, nr = parity.check_qmatmul(want, ref, codes.T, scales, xo)
+    print("outlier rows (%s): %.4f by the normalized clause; largest normalized error: device path %.2f, reference %.2f; "
+          "classes %s" % ("x @ W" if axis else "W @ x", frac, ng, nr, np.bincount(cls, minlength=3).tolist()), flush=True)
+    if bits_ == 4:
+        for i in range(len(xo)):
+            print("M = 1, row", i, flush=True)
+            assert _same(run(xo[i:i + 1]), want[i:i + 1]), ("M = 1", i, cls[i])
+    for n in (10, 16):
+        for i0 in range(0, len(xo), n):
+            print("M =", n, "rows", i0, flush=True)
+            assert _same(run(xo[i0:i0 + n]), want[i0:i0 + n]), ("M", n, i0)
+    for M in (1024, 16384):
+        print("M =", M, flush=True)
+        x = rng.normal(size=(M, K)).astype(np.float32)
+        at = np.linspace(3, M - 4, len(xo)).astype(int)
+        x[at] = xo
+        x[1, 17], x[M - 2, 5] = np.nan, np.inf
+        got = run(x)
+        assert _same(got[at], want), ("M", M)
+        sub = np.concatenate([[1, M - 2], rng.choice(M, 6, replace=False)])
+        w2, c2 = parity.device_path_matmul(x[sub], codes, scales)
+        assert _same(got[sub], w2) and c2[:2].tolist() == [1, 1]
+        r2, _ = O.Model(text).batch(x[sub[:2]], threads=16)
+        assert _same(got[sub[:2]], r2)
 
 
 def _f32_matmul_models():

@@ -31,7 +31,7 @@ def _case(seed, bits, axis, m, k, n):
     scales = rng.uniform(0.001, 0.1, size=m if axis == 0 else n).astype(np.float32)
     b = rng.normal(size=(k, n) if axis == 0 else (m, k)).astype(np.float32)
     if axis == 1 and m > 3:
-        b[3, k // 2] = 1e4  # a peaked row: the reference's loop over the caller's codes
+        b[3, k // 2] = 1e4  # an outlier: a split row (its outlier terms read the caller's codes)
     return _pack(codes, bits), scales, b
 
 
@@ -47,7 +47,7 @@ def test_no_alloc_equals_matmul_q_twice_then_refuses():
     print("case no-alloc entry point", flush=True)
     hip.init(0)
     # first: config 2's layer at 2048 rows (x @ W^T as axis 0: 4096 x 4096 int4, b [4096][2048]);
-    # second, smaller: int8 weights on axis 1 with a peaked row, odd sizes
+    # second, smaller: int8 weights on axis 1 with an outlier row, odd sizes
     for seed, (bits, axis, m, k, n) in enumerate([(4, 0, 4096, 4096, 2048), (8, 1, 300, 500, 17)]):
         q, s, b = _case(seed, bits, axis, m, k, n)
         got = _noalloc(q, bits, s, b, m, k, n, axis)
