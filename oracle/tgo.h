@@ -101,6 +101,7 @@ int32_t tgo_to_fixed(double v, int frac);
 const char *tgo_fx_format(int32_t v, char *buf);
 int64_t tgo_fx_prim(int op, int64_t a, int64_t b);
 extern int tgo_plant; /* test-only planted mistakes (fixed.c) */
+extern int tgo_plant64; /* test-only planted mistake of the f64 interpreter (vm.c under TGO_F64) */
 
 /* ---- internals shared between the oracle's files ---- */
 int tgo_numel(const tgo_shape *s);

@@ -47,6 +47,12 @@ typedef float real;
 #ifndef TGO_F64
 void (*tgo_matmul_hook)(void *ctx, const tgo_module *m, const tgo_ins *in, const float *a, const float *b);
 void *tgo_hook_ctx;
+#define ACC(v) (v)
+#else
+/* Test-only: 1 leaves the quantized matmuls' running sums in f32 (a planted
+ * mistake that the f64 truth's own tests must catch). */
+int tgo_plant64;
+#define ACC(v) (tgo_plant64 == 1 ? (real)(float)(v) : (v))
 #endif
 
 typedef struct {
@@ -256,7 +262,7 @@ static void matmul_qa(real *o, const signed char *q, int bits, const float *s, c
 	for (int i = 0; i < m; i++)
 		for (int j = 0; j < n; j++) {
 			real acc = 0.0f;
-			for (int p = 0; p < k; p++) acc += (real)tgo_qget(q, bits, (long)i * k + p) * b[(long)p * n + j];
+			for (int p = 0; p < k; p++) acc = ACC(acc + (real)tgo_qget(q, bits, (long)i * k + p) * b[(long)p * n + j]);
 			o[(long)i * n + j] = s[i] * acc;
 		}
 }
@@ -266,7 +272,7 @@ static void matmul_qb(real *o, const real *a, const signed char *q, int bits, co
 	for (int i = 0; i < m; i++)
 		for (int j = 0; j < n; j++) {
 			real acc = 0.0f;
-			for (int p = 0; p < k; p++) acc += a[(long)i * k + p] * (real)tgo_qget(q, bits, (long)p * n + j);
+			for (int p = 0; p < k; p++) acc = ACC(acc + a[(long)i * k + p] * (real)tgo_qget(q, bits, (long)p * n + j));
 			o[(long)i * n + j] = s[j] * acc;
 		}
 }

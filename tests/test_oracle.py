@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
+from technograd_amd import synth
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 NAMES = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(GOLDEN, "*.npz")))
@@ -249,3 +250,108 @@ def test_planted_mistake_is_caught():
     assert np.array_equal(bits(y), bits(d4["y"]))
     y_bad, _ = m.batch(d4["x"][:, ::-1].copy())  # a reversed input order changes the sums
     assert not np.array_equal(bits(y_bad), bits(d4["y"]))
+
+
+# ---- the f64 interpreter (oracle/vm64.c), the truth of the whole-model
+# predicate (tests/parity.py: check_model): pinned by closed forms ----
+
+def _exact_qproduct(codes_kc, scales, x):
+    """o[m, c] = s[c] * sum_k code[k, c] x[m, k], each sum exactly rounded
+    (math.fsum over exact f64 products), then the scale in f64; and
+    sum_k |s code x| (the scale of the rounding bound)."""
+    t = np.empty((x.shape[0], codes_kc.shape[1]))
+    mag = np.empty_like(t)
+    cf, xf = codes_kc.astype(np.float64), x.astype(np.float64)
+    for m in range(x.shape[0]):
+        prods = xf[m][:, None] * cf  # exact: an int8 times an f32
+        for c in range(cf.shape[1]):
+            t[m, c] = math.fsum(prods[:, c])
+        mag[m] = np.abs(prods).sum(axis=0)
+    return t * scales.astype(np.float64)[None, :], mag * np.abs(scales.astype(np.float64))[None, :]
+
+
+def _qlinear_case(bits, axis, K, C, seed):
+    rng = np.random.default_rng(seed)
+    lim = 7 if bits == 4 else 127
+    codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)  # as x @ W
+    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
+    x = rng.normal(size=(6, K)).astype(np.float32)
+    x[1] *= 1e4
+    x[2, K // 2] = 3e3  # an outlier
+    stored = codes if axis == 1 else np.ascontiguousarray(codes.T)
+    return O.Model(synth.linear_tgir_codes("q", stored, scales, bits, axis)), codes, scales, x
+
+
+@pytest.mark.parametrize("bits,axis,K", [(4, 1, 7), (8, 1, 513), (4, 0, 513), (8, 0, 4096)])
+def test_f64_quantized_product_is_the_exact_product(bits, axis, K):
+    """A one-matmul quantized model through batch64 equals the exact product
+    (exactly rounded sums, tests/parity.py's truth) to f64 rounding: within
+    (K + 2) 2^-53 sum |s w x|. A dropped term, a wrong sign, index or
+    operand order, or a sum left in f32 is orders of magnitude outside."""
+    m, codes, scales, x = _qlinear_case(bits, axis, K, 40, K + bits + axis)
+    got, _ = m.batch64(x)
+    want, mag = _exact_qproduct(codes, scales, x)
+    assert (np.abs(got - want) <= (K + 2) * 2.0 ** -53 * mag + 1e-300).all()
+    y32, _ = m.batch(x)
+    assert (y32.astype(np.float64) != got).any()  # an f64 result, not the f32 one widened
+
+
+def test_f64_planted_f32_sums_are_caught():
+    """tgo_plant64 = 1 leaves the quantized products' running sums in f32
+    inside the f64 interpreter; the closed form above rejects it."""
+    m, codes, scales, x = _qlinear_case(8, 1, 513, 40, 7)
+    want, mag = _exact_qproduct(codes, scales, x)
+    knob = ctypes.c_int.in_dll(O.lib(), "tgo_plant64")
+    knob.value = 1
+    try:
+        bad, _ = m.batch64(x)
+    finally:
+        knob.value = 0
+    assert not (np.abs(bad - want) <= 515 * 2.0 ** -53 * mag).all()
+    good, _ = m.batch64(x)
+    assert (np.abs(good - want) <= 515 * 2.0 ** -53 * mag).all()
+
+
+def _row_model(op, n):
+    return "(tgir 1\n  (model r)\n  (input x (f32 %d))\n  (block\n    (%%0 (f32 %d) (%s x))\n  )\n  (output %%0))\n" % (n, n, op)
+
+
+@pytest.mark.parametrize("op", ["rmsnorm", "softmax", "tanh", "exp", "sigmoid"])
+def test_f64_row_ops_are_numpy_f64(op):
+    """rmsnorm (sum of squares, 1 / sqrt(s / n + 1e-6), no gain:
+    runtime/tg_rt.h:165-175), softmax (max, exp(x - max), sum, divide:
+    :154-164) and the elementwise functions through batch64 equal numpy's
+    double-precision evaluation of the same formulas within a few f64 ulps."""
+    rng = np.random.default_rng(len(op))
+    n = 257
+    x = (rng.normal(size=(16, n)) * np.array([1, 10, 0.01, 30] * 4)[:, None]).astype(np.float32)
+    got, _ = O.Model(_row_model(op, n)).batch64(x)
+    xd = x.astype(np.float64)
+    if op == "rmsnorm":
+        want = xd / np.sqrt((xd * xd).sum(axis=1, keepdims=True) / n + float(np.float32(1e-6)))
+    elif op == "softmax":
+        e = np.exp(xd - xd.max(axis=1, keepdims=True))
+        want = e / e.sum(axis=1, keepdims=True)
+    elif op == "tanh":
+        want = np.tanh(xd)
+    elif op == "exp":
+        want = np.exp(xd)
+    else:
+        want = 1.0 / (1.0 + np.exp(-xd))
+    assert np.allclose(got, want, rtol=64 * 2.0 ** -53, atol=1e-300), np.abs(got / want - 1).max()
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_goldens_within_reach_of_the_f64_truth(name):
+    """Every golden's f32 output (the reference's own) lies within 1e-4 of
+    its row's largest magnitude from the f64 interpreter, on rows whose think
+    loops halt at the same step in both (the largest such distance over the
+    goldens is 6.5e-6). A truth missing a term, with a wrong sign or operand,
+    or a wrong op order on whole-model scale would be outside."""
+    text, d = load(name)
+    t, st = O.Model(text).batch64(d["x"])
+    y = d["y"].astype(np.float64).reshape(t.shape)
+    same = (st == d["steps"]).all(axis=1)
+    assert same.mean() > 0.9
+    scale = np.abs(t[same]).max(axis=1, keepdims=True)
+    assert (np.abs(y[same] - t[same]) <= 1e-4 * scale).all()
