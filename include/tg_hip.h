@@ -118,14 +118,17 @@ int tg_hip_matmul_qb(float *o, const float *a, const signed char *q, int bits, c
  * Asynchronous on `stream` (a hipStream_t; NULL: the null stream). Packed
  * weights and activation digits go to a fixed device array of
  * TG_HIP_NOALLOC_SCRATCH bytes that the library holds on every GPU it runs on
- * until the process ends; a call needs about ceil(C/256)*256 x ceil(K/64)*64
- * x bits/8 bytes of packed weights plus 3 x ceil(M/128)*128 x ceil(K/64)*64
- * bytes of digits (C channels, K inputs, M activation rows: config 2's
- * 4096 x 4096 int4 layer fits at up to 4096 rows); larger calls return -2
- * with the sizes in tg_hip_error(). Every call on a GPU uses that GPU's one
- * array: calls that overlap on one GPU (other streams, other threads) race
- * and must be serialised by the caller. 0 on success. */
-#define TG_HIP_NOALLOC_SCRATCH (64u << 20)
+ * until the process ends. With Cp = ceil(C/256)*256, Kp = ceil(K/64)*64 and
+ * Mp = ceil(M/128)*128 (C channels, K inputs, M activation rows), a call
+ * needs r(Cp*Kp*bits/8) bytes of packed weights, twice that for int4 (a
+ * second copy in channel pairs), plus r(4*Cp) of scales, plus
+ * Mp*(3*Kp + 16 + 8*min(64, Kp/16)) + 256 bytes of digits and row data
+ * (r: rounded up to 256). Config 2's 4096 x 4096 int4 layer fits at up to
+ * 6528 activation rows; larger calls return -2 with the sizes in
+ * tg_hip_error(). Every call on a GPU uses that GPU's one array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be
+ * serialised by the caller. 0 on success. */
+#define TG_HIP_NOALLOC_SCRATCH (96u << 20)
 int tg_hip_matmul_q_noalloc(float *d_o, const signed char *d_q, int bits, const float *d_s, const float *d_b, int m, int k, int n,
 			    int axis, void *stream);
 

@@ -53,6 +53,22 @@ def test_no_alloc_equals_matmul_q_twice_then_refuses():
         got = _noalloc(q, bits, s, b, m, k, n, axis)
         want = hip.matmul_q(q, bits, s, b, m, k, n, axis)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (bits, axis, m, k, n)
-    # 8192 x 8192 int8 weights alone need 64 MiB: refused before any launch
-    rc = hip.matmul_q_noalloc(1, 1, 8, 1, 1, 8192, 8192, 1, 0)
+    # the documented limit (include/tg_hip.h): config 2's layer fits at 6528 rows, not at 6529
+    rc = hip.matmul_q_noalloc(1, 1, 4, 1, 1, 4096, 4096, 6529, 0)
     assert rc == -2 and "scratch" in hip.error()
+    # 8192 x 16384 int8 weights alone need 128 MiB: refused before any launch
+    rc = hip.matmul_q_noalloc(1, 1, 8, 1, 1, 8192, 16384, 1, 0)
+    assert rc == -2 and "scratch" in hip.error()
+
+
+def test_no_alloc_at_its_documented_limit():
+    """Config 2's 4096 x 4096 int4 layer at 6528 activation rows (axis 0,
+    the largest call the header promises), after a call of 4096 rows: both
+    equal tg_hip_matmul_q bit for bit."""
+    print("case no-alloc at the limit", flush=True)
+    hip.init(0)
+    for seed, n in ((7, 6528), (8, 4096)):
+        q, s, b = _case(seed, 4, 0, 4096, 4096, n)
+        got = _noalloc(q, 4, s, b, 4096, 4096, n, 0)
+        want = hip.matmul_q(q, 4, s, b, 4096, 4096, n, 0)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), n
