@@ -1,360 +1,460 @@
-/* Model-level quantization of the backend (`tgc quantize`, src/quant.c):
- * which params are quantized, their scales and codes, RTN or GPTQ. The
- * calibration Hessians come from the device (tg_hip.cpp: the row program
+/* Model-level quantization of the backend (`tgc quantize`, src/quant.c).
+ *
+ * What has to match the reference byte for byte is observable: which params
+ * are quantized, each channel's f32 scale and int codes, the dequantized data
+ * and the report line. Codes are roundings of doubles, so every double that
+ * feeds one must come out of the same operations in the same order as in
+ * the reference (this file is compiled with -ffp-contract=off). The rules,
+ * restated:
+ *
+ *   which params  rank 2, not quantized yet, at least min_size elements,
+ *                 not named __*, not the model output, and every use of it
+ *                 one operand of a matmul, always the same side: the left
+ *                 operand gives one scale per row (axis 0), the right one
+ *                 per column (axis 1); a think loop's init or yield, or a
+ *                 scan's carries, slices or stacks naming it rule it out
+ *                 (src/quant.c:42-89).
+ *   the step      per channel: amax = max |w|; candidates amax (1 - 0.05 g) /
+ *                 lim for g = 0..9, each scored by the sum over the channel in
+ *                 input order of (w - step code)^2, times the damped Hessian
+ *                 diagonal under GPTQ; the first smallest score wins; an
+ *                 all-zero channel gets 1e-8 (:176-200).
+ *   a code        nearbyint(w / step) clamped to +-lim (127 or 7).
+ *   GPTQ          the Hessian's diagonal mean (summed in input order) times
+ *                 0.01 added to the diagonal, inputs never active (a zero on
+ *                 the diagonal) set to 1 first with their weights zeroed;
+ *                 U the upper triangular factor with H^-1 = U^T U, reached
+ *                 through H = L L^T, L^-1 by forward substitution, H^-1 =
+ *                 L^-T L^-1 and a second factorisation; then, per channel in
+ *                 input order, each code's rounding error divided by U[j][j]
+ *                 and taken off every later input j' in proportion to
+ *                 U[j][j'] (:203-316).
+ *
+ * Each factor entry is one running subtraction (or sum) over k in increasing
+ * order, the order the reference evaluates it in; how the entries are swept
+ * is this file's own: a team of threads shares each column's entries (a
+ * barrier between columns), and the inverse is kept transposed so that every
+ * running sum walks two contiguous rows. Channels are independent given U.
+ *
+ * The Hessians come from the device (tg_hip.cpp): the calibration pass
  * captures each eligible weight's other matmul operand in the order the
- * reference's hook sees it, and one thread per element sums x_r x_c over the
- * samples in that order, so H is the reference's to the bit); everything
- * here is host double arithmetic in the reference's operation order
- * (compiled with -ffp-contract=off), parallel only over independent results:
- *   eligibility  rank-2 params with at least min_size elements, not named
- *                __*, not the output, used only as a matmul operand with one
- *                axis (left: per-row scales, axis 0; right: per column, 1)
- *                (src/quant.c:42-89);
- *   scale        per channel, the clip of absmax (ten candidates) that
- *                minimises the rounding error, weighted by the damped
- *                Hessian diagonal under GPTQ (:184-200);
- *   GPTQ         H + 0.01 mean(diag) on the diagonal, inputs never active
- *                zeroed, U = the upper Cholesky factor of H^-1 through two
- *                Cholesky factorisations and a triangular inverse (:203-253),
- *                then per channel, input by input, each rounding error pushed
- *                onto the remaining inputs (:258-316). Channels are
- *                independent given U, and so are the rows of each Cholesky
- *                step and the columns of the inverse: those run on threads.
- * The reference quantizes with GPTQ only for K <= 2048 (src/quant.c:346);
- * here every eligible param gets its Hessian, K included up to 8192. */
+ * reference's hook sees it, and H[r][c] sums x_r x_c over the samples in that
+ * order, so H is the reference's to the bit. The reference gives a Hessian
+ * only to params of K <= 2048 inputs (src/quant.c:346); tg_hip_quantize_model
+ * keeps that limit as its default (max_k = 2048), and max_k <= 0 lifts it. */
 #include "tg_gptq.h"
 
 #include <math.h>
 #include <pthread.h>
+#include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
-/* ---------------------------------------------------------- eligibility --- */
+/* ------------------------------------------------------- which params --- */
 
-static int q_axis_for(const tgm_module *m, int v, const tgm_ins *in)
+enum { AS_LEFT = 1, AS_RIGHT = 2, AS_OTHER = 4 };
+
+static void mark(unsigned char *use, int nval, int v, int how)
 {
-	if (m->val[v].sh.rank != 2) return -1;
-	if (in->op == TGM_MATMUL) {
-		if (in->a[0] == v && in->a[1] != v) return 0;
-		if (in->a[1] == v && in->a[0] != v) return 1;
-	}
-	return -1;
+	if (v >= 0 && v < nval) use[v] |= (unsigned char)how;
 }
 
-static int use_axis(const tgm_module *m, int v, const tgm_block *b, int *axis)
+/* every value's uses in block b (nested bodies included), or-ed into use[] */
+static void note_uses(const tgm_module *m, const tgm_block *b, unsigned char *use)
 {
 	for (int i = 0; i < b->len; i++) {
 		const tgm_ins *in = &b->v[i];
 		if (in->op == TGM_THINK) {
-			if (in->init == v || in->yield == v || !use_axis(m, v, in->body, axis)) return 0;
-		} else if (in->op == TGM_SCAN) {
-			for (int k = 0; k < in->nc; k++)
-				if (in->cinit[k] == v || in->cnext[k] == v) return 0;
-			for (int j = 0; j < in->nx; j++)
-				if (in->x[j] == v) return 0;
-			for (int y = 0; y < in->ny; y++)
-				if (in->y[y] == v) return 0;
-			if (!use_axis(m, v, in->body, axis)) return 0;
-		} else {
-			for (int j = 0; j < in->na; j++) {
-				if (in->a[j] != v) continue;
-				int a = q_axis_for(m, v, in);
-				if (a < 0 || (*axis >= 0 && *axis != a)) return 0;
-				*axis = a;
-			}
+			mark(use, m->nval, in->init, AS_OTHER);
+			mark(use, m->nval, in->yield, AS_OTHER);
+			note_uses(m, in->body, use);
+			continue;
+		}
+		if (in->op == TGM_SCAN) {
+			for (int k = 0; k < in->nc; k++) mark(use, m->nval, in->cinit[k], AS_OTHER), mark(use, m->nval, in->cnext[k], AS_OTHER);
+			for (int k = 0; k < in->nx; k++) mark(use, m->nval, in->x[k], AS_OTHER);
+			for (int k = 0; k < in->ny; k++) mark(use, m->nval, in->y[k], AS_OTHER);
+			note_uses(m, in->body, use);
+			continue;
+		}
+		const int mm = in->op == TGM_MATMUL && in->na == 2 && in->a[0] != in->a[1];
+		for (int j = 0; j < in->na; j++) {
+			const int v = in->a[j];
+			if (v < 0 || v >= m->nval) continue;
+			mark(use, m->nval, v, mm && m->val[v].sh.rank == 2 ? (j == 0 ? AS_LEFT : AS_RIGHT) : AS_OTHER);
 		}
 	}
-	return 1;
 }
 
 int tgq_eligible(const tgm_module *m, int min_size, tgq_param **out)
 {
+	unsigned char *use = calloc((size_t)(m->nval ? m->nval : 1), 1);
+	tgq_param *list = NULL;
 	int n = 0;
-	tgq_param *p = NULL;
+	if (!use) return -1;
+	note_uses(m, &m->top, use);
 	for (int v = 0; v < m->nval; v++) {
 		const tgm_value *x = &m->val[v];
-		if (x->kind != TGM_PARAM || x->qbits || x->sh.rank != 2 || x->n < min_size) continue;
-		if (x->name && !strncmp(x->name, "__", 2)) continue;
-		if (m->output == v) continue;
-		int axis = -1;
-		if (!use_axis(m, v, &m->top, &axis) || axis < 0) continue;
-		tgq_param *np = realloc(p, (size_t)(n + 1) * sizeof *np);
-		if (!np) {
-			free(p);
+		if (x->kind != TGM_PARAM || x->qbits || x->sh.rank != 2 || x->n < min_size || m->output == v) continue;
+		if (x->name && x->name[0] == '_' && x->name[1] == '_') continue;
+		if (use[v] != AS_LEFT && use[v] != AS_RIGHT) continue; /* unused, both sides, or used otherwise */
+		tgq_param *grown = realloc(list, (size_t)(n + 1) * sizeof *grown);
+		if (!grown) {
+			free(list);
+			free(use);
 			return -1;
 		}
-		p = np;
-		memset(&p[n], 0, sizeof *p);
-		p[n].v = v;
-		p[n].axis = axis;
-		p[n].C = x->sh.dim[axis];
-		p[n].K = x->sh.dim[1 - axis];
+		list = grown;
+		const int axis = use[v] == AS_LEFT ? 0 : 1;
+		list[n] = (tgq_param){ .v = v, .axis = axis, .C = x->sh.dim[axis], .K = x->sh.dim[1 - axis] };
 		n++;
 	}
-	*out = p;
+	free(use);
+	*out = list;
 	return n;
 }
 
-/* ------------------------------------------------------------- threads --- */
+/* ------------------------------------------------------ thread team --- */
+
+typedef struct Team Team;
+typedef void (*team_fn)(Team *t, int id);
+struct Team {
+	int size;
+	team_fn fn;
+	void *ctx;
+	pthread_barrier_t bar;
+	pthread_mutex_t mu;
+	pthread_cond_t cv;
+	int state; /* 0: members wait; 1: run fn; -1: leave without running it */
+};
 
 typedef struct {
-	void (*fn)(void *ctx, int lo, int hi);
-	void *ctx;
-	int lo, hi;
-} Part;
+	Team *t;
+	int id;
+} Member;
 
-static void *part_main(void *a)
+static void *member_main(void *p)
 {
-	Part *p = a;
-	p->fn(p->ctx, p->lo, p->hi);
+	Member *w = p;
+	Team *t = w->t;
+	pthread_mutex_lock(&t->mu);
+	while (t->state == 0) pthread_cond_wait(&t->cv, &t->mu);
+	const int go = t->state > 0;
+	pthread_mutex_unlock(&t->mu);
+	if (go) t->fn(t, w->id);
 	return NULL;
 }
 
-/* fn over [0, n) in contiguous parts, one per thread */
-static void par(int n, int threads, void (*fn)(void *, int, int), void *ctx)
+static void team_release(Team *t, int state)
 {
-	if (threads > 64) threads = 64;
-	if (threads < 1 || n < 64) threads = 1;
-	Part parts[64];
-	pthread_t th[64];
-	int ok[64] = { 0 };
-	for (int t = 0; t < threads; t++) parts[t] = (Part){ fn, ctx, (int)((long)n * t / threads), (int)((long)n * (t + 1) / threads) };
-	for (int t = 1; t < threads; t++) ok[t] = pthread_create(&th[t], NULL, part_main, &parts[t]) == 0;
-	fn(ctx, parts[0].lo, parts[0].hi);
-	for (int t = 1; t < threads; t++) {
-		if (ok[t]) pthread_join(th[t], NULL);
-		else fn(ctx, parts[t].lo, parts[t].hi);
-	}
+	pthread_mutex_lock(&t->mu);
+	t->state = state;
+	pthread_cond_broadcast(&t->cv);
+	pthread_mutex_unlock(&t->mu);
 }
 
-/* ---------------------------------------------------------- Cholesky --- */
+/* fn(t, id) on `size` threads, the caller being id 0; they may wait for each
+ * other with team_sync. Members are held at a gate until all of them have
+ * started; if one cannot start, the others leave and fn runs on the caller
+ * alone (size 1). */
+static void team_run(int size, team_fn fn, void *ctx)
+{
+	enum { MAXT = 64 };
+	Team t;
+	memset(&t, 0, sizeof t);
+	t.size = size < 1 ? 1 : size > MAXT ? MAXT : size;
+	t.fn = fn, t.ctx = ctx;
+	if (t.size > 1 && pthread_mutex_init(&t.mu, NULL) == 0) {
+		if (pthread_cond_init(&t.cv, NULL) == 0) {
+			pthread_t th[MAXT];
+			Member mem[MAXT];
+			int started = 1;
+			for (; started < t.size; started++) {
+				mem[started] = (Member){ &t, started };
+				if (pthread_create(&th[started], NULL, member_main, &mem[started])) break;
+			}
+			const int all = started == t.size && pthread_barrier_init(&t.bar, NULL, (unsigned)t.size) == 0;
+			team_release(&t, all ? 1 : -1);
+			if (all) fn(&t, 0);
+			for (int i = 1; i < started; i++) pthread_join(th[i], NULL);
+			if (all) pthread_barrier_destroy(&t.bar);
+			pthread_cond_destroy(&t.cv);
+			pthread_mutex_destroy(&t.mu);
+			if (all) return;
+		} else {
+			pthread_mutex_destroy(&t.mu);
+		}
+	}
+	t.size = 1;
+	fn(&t, 0);
+}
+
+static void team_sync(Team *t)
+{
+	if (t->size > 1) pthread_barrier_wait(&t->bar);
+}
+
+/* ------------------------------------------------- dense row algebra --- */
+
+/* acc - a[0] b[0] - a[1] b[1] - ... in that order */
+static double less_dots(double acc, const double *a, const double *b, int n)
+{
+	for (int k = 0; k < n; k++) acc -= a[k] * b[k];
+	return acc;
+}
+
+/* 0 + a[0] b[0] + a[1] b[1] + ... in that order */
+static double dots(const double *a, const double *b, int n)
+{
+	double acc = 0;
+	for (int k = 0; k < n; k++) acc += a[k] * b[k];
+	return acc;
+}
 
 typedef struct {
-	double *A;
-	const double *L;
-	double *Li, *U;
-	int n, j, c;
-} Ch;
+	double *A; /* n x n, row-major; the lower triangle is read, L is left there */
+	int n, ok;
+} Factor;
 
-static void chol_rows(void *p, int lo, int hi) /* rows j+1+lo .. of column j */
+/* H = L L^T, column by column: column j's diagonal from row j's entries left
+ * of it, then its entries below (row i's entries left of column j against
+ * row j's), those rows shared out over the team; the upper triangle cleared */
+static void factor_member(Team *t, int id)
 {
-	Ch *c = p;
-	const int n = c->n, j = c->j;
-	double *A = c->A, d = A[j * n + j];
-	for (int i = j + 1 + lo; i < j + 1 + hi; i++) {
-		double s = A[i * n + j];
-		for (int k = 0; k < j; k++) s -= A[i * n + k] * A[j * n + k];
-		A[i * n + j] = s / d;
-	}
-}
-
-/* lower Cholesky factor in place (src/quant.c:203-220): column j's diagonal,
- * then its rows below (independent of each other), then zeros above */
-static int cholesky(double *A, int n, int threads)
-{
-	Ch c = { A, NULL, NULL, NULL, n, 0, 0 };
+	Factor *f = t->ctx;
+	const int n = f->n;
+	double *A = f->A;
 	for (int j = 0; j < n; j++) {
-		double d = A[j * n + j];
-		for (int k = 0; k < j; k++) d -= A[j * n + k] * A[j * n + k];
-		if (d <= 0) return 0;
-		A[j * n + j] = sqrt(d);
-		c.j = j;
-		par(n - j - 1, (n - j - 1) >= 256 ? threads : 1, chol_rows, &c);
-		for (int k = j + 1; k < n; k++) A[j * n + k] = 0;
+		double *rj = A + (size_t)j * n;
+		const double piv = less_dots(rj[j], rj, rj, j); /* every member computes the same value */
+		if (piv <= 0) {
+			if (id == 0) f->ok = 0;
+			return; /* every member sees the same pivot and leaves at the same column */
+		}
+		const double d = sqrt(piv);
+		for (int i = j + 1 + id; i < n; i += t->size) {
+			double *ri = A + (size_t)i * n;
+			ri[j] = less_dots(ri[j], ri, rj, j) / d;
+		}
+		team_sync(t);
+		if (id == 0) {
+			rj[j] = d;
+			for (int k = j + 1; k < n; k++) rj[k] = 0;
+		}
+		team_sync(t);
 	}
-	return 1;
 }
 
-static void inv_cols(void *p, int lo, int hi) /* columns of L^-1 by forward substitution */
+static int lower_factor(double *A, int n, int threads)
 {
-	Ch *c = p;
-	const int n = c->n;
-	const double *L = c->L;
-	double *Li = c->Li;
-	for (int col = lo; col < hi; col++)
-		for (int i = col; i < n; i++) {
-			double s = i == col ? 1.0 : 0.0;
-			for (int k = col; k < i; k++) s -= L[i * n + k] * Li[k * n + col];
-			Li[i * n + col] = s / L[i * n + i];
+	Factor f = { A, n, 1 };
+	team_run(n >= 256 ? threads : 1, factor_member, &f);
+	return f.ok;
+}
+
+typedef struct {
+	const double *L;
+	double *LiT; /* (L^-1)^T: row c holds column c of L^-1 */
+	double *G;   /* lower triangle of L^-T L^-1 */
+	int n;
+} Inverse;
+
+/* column c of L^-1 by forward substitution, into row c of LiT */
+static void inverse_member(Team *t, int id)
+{
+	Inverse *v = t->ctx;
+	const int n = v->n;
+	for (int c = id; c < n; c += t->size) {
+		double *out = v->LiT + (size_t)c * n;
+		for (int i = c; i < n; i++) {
+			const double *li = v->L + (size_t)i * n;
+			out[i] = less_dots(i == c ? 1.0 : 0.0, li + c, out + c, i - c) / li[i];
 		}
+	}
 }
 
-static void hinv_rows(void *p, int lo, int hi) /* H^-1 = Li^T Li, upper triangle by rows, mirrored */
+/* G[j][i] = sum over k >= j of L^-1[k][i] L^-1[k][j] (j >= i), in k order */
+static void gram_member(Team *t, int id)
 {
-	Ch *c = p;
-	const int n = c->n;
-	const double *Li = c->Li;
-	double *U = c->U;
-	for (int i = lo; i < hi; i++)
-		for (int j = i; j < n; j++) {
-			double s = 0;
-			for (int k = j; k < n; k++) s += Li[k * n + i] * Li[k * n + j];
-			U[i * n + j] = U[j * n + i] = s;
-		}
+	Inverse *v = t->ctx;
+	const int n = v->n;
+	for (int i = id; i < n; i += t->size) {
+		const double *ci = v->LiT + (size_t)i * n;
+		for (int j = i; j < n; j++) v->G[(size_t)j * n + i] = dots(ci + j, v->LiT + (size_t)j * n + j, n - j);
+	}
 }
 
-/* U, upper with H^-1 = U^T U (src/quant.c:222-253) */
-static int inv_chol_upper(const double *H, int n, double *U, int threads)
+/* U, upper, with H^-1 = U^T U: H = L L^T, G = L^-T L^-1 = H^-1, G = L2 L2^T, U = L2^T */
+static int inverse_factor(const double *H, int n, double *U, int threads)
 {
-	double *L = malloc((size_t)n * n * sizeof *L), *Li = calloc((size_t)n * n, sizeof *Li);
-	int ok = L && Li;
+	double *L = malloc((size_t)n * n * sizeof *L), *LiT = calloc((size_t)n * n, sizeof *LiT);
+	int ok = L && LiT;
 	if (ok) {
 		memcpy(L, H, (size_t)n * n * sizeof *L);
-		ok = cholesky(L, n, threads);
+		ok = lower_factor(L, n, threads);
 	}
 	if (ok) {
-		Ch c = { NULL, L, Li, U, n, 0, 0 };
-		par(n, threads, inv_cols, &c);
-		par(n, threads, hinv_rows, &c);
-		ok = cholesky(U, n, threads);
-		if (ok)
-			for (int i = 0; i < n; i++)
-				for (int j = i + 1; j < n; j++) {
-					U[i * n + j] = U[j * n + i];
-					U[j * n + i] = 0;
-				}
+		Inverse v = { L, LiT, U, n };
+		team_run(threads, inverse_member, &v);
+		team_run(threads, gram_member, &v);
+		ok = lower_factor(U, n, threads);
 	}
+	if (ok)
+		for (int i = 0; i < n; i++)
+			for (int j = i + 1; j < n; j++) U[(size_t)i * n + j] = U[(size_t)j * n + i], U[(size_t)j * n + i] = 0;
 	free(L);
-	free(Li);
+	free(LiT);
 	return ok;
 }
 
-/* ------------------------------------------------------------ channels --- */
+/* ----------------------------------------------------------- channels --- */
 
-static int code_of(double w, double s, int lim)
+static int rtn_code(double w, double step, int lim)
 {
-	if (s <= 0) return 0;
-	double r = nearbyint(w / s);
-	return (int)(r > lim ? lim : r < -lim ? -lim : r);
+	if (step <= 0) return 0;
+	const double r = nearbyint(w / step);
+	return r > lim ? lim : r < -lim ? -lim : (int)r;
 }
 
-static double best_scale(const double *w, int K, const double *hd, int lim)
+/* the channel's clip step: ten candidates, the first of the smallest weighted error */
+static double clip_step(const double *w, int K, const double *hdiag, int lim)
 {
 	double amax = 0;
-	for (int j = 0; j < K; j++)
-		if (fabs(w[j]) > amax) amax = fabs(w[j]);
+	for (int j = 0; j < K; j++) amax = fabs(w[j]) > amax ? fabs(w[j]) : amax;
 	if (amax == 0) return 1e-8;
-	double best = INFINITY, bs = amax / lim;
+	double pick = amax / lim, low = INFINITY;
 	for (int g = 0; g < 10; g++) {
-		double s = amax * (1.0 - 0.05 * g) / lim, e = 0;
+		const double step = amax * (1.0 - 0.05 * g) / lim;
+		double err = 0;
 		for (int j = 0; j < K; j++) {
-			double d = w[j] - s * code_of(w[j], s, lim);
-			e += d * d * (hd ? hd[j] : 1.0);
+			const double r = w[j] - step * rtn_code(w[j], step, lim);
+			err += r * r * (hdiag ? hdiag[j] : 1.0);
 		}
-		if (e < best) {
-			best = e;
-			bs = s;
-		}
+		if (err < low) low = err, pick = step;
 	}
-	return bs;
+	return pick;
 }
 
 typedef struct {
-	double *W;
-	const double *hd, *U;
-	int K, lim;
-	int *codes; /* [C][K] */
-	double *scale;
-} Chan;
+	double *W;            /* [C][K] working weights (GPTQ updates them) */
+	const double *hdiag;  /* damped Hessian diagonal, or NULL */
+	const double *U;      /* upper factor of H^-1, or NULL (RTN) */
+	int C, K, lim;
+	int *codes;           /* [C][K] */
+	double *step;         /* [C] */
+} Channels;
 
-static void channels(void *p, int lo, int hi)
+static void channel_member(Team *t, int id)
 {
-	Chan *c = p;
-	const int K = c->K;
-	for (int ch = lo; ch < hi; ch++) {
-		double *w = c->W + (size_t)ch * K;
-		double s = best_scale(w, K, c->hd, c->lim);
-		c->scale[ch] = s;
+	Channels *q = t->ctx;
+	const int K = q->K;
+	for (int c = id; c < q->C; c += t->size) {
+		double *w = q->W + (size_t)c * K;
+		int *code = q->codes + (size_t)c * K;
+		const double step = q->step[c] = clip_step(w, K, q->hdiag, q->lim);
 		for (int j = 0; j < K; j++) {
-			int code = code_of(w[j], s, c->lim);
-			c->codes[(size_t)ch * K + j] = code;
-			if (c->U) { /* this input's rounding error, pushed onto the remaining inputs */
-				double err = (w[j] - s * code) / c->U[(size_t)j * K + j];
-				for (int jj = j + 1; jj < K; jj++) w[jj] -= err * c->U[(size_t)j * K + jj];
-			}
+			code[j] = rtn_code(w[j], step, q->lim);
+			if (!q->U) continue;
+			const double *uj = q->U + (size_t)j * K;
+			const double e = (w[j] - step * code[j]) / uj[j];
+			for (int l = j + 1; l < K; l++) w[l] -= e * uj[l];
 		}
 	}
+}
+
+/* the damped Hessian diagonal; inputs never active set to 1 with their weights zeroed */
+static void damp(double *H, double *W, int C, int K, double *hdiag)
+{
+	double mean = 0;
+	for (int j = 0; j < K; j++) mean += H[(size_t)j * K + j];
+	mean /= K;
+	for (int j = 0; j < K; j++) {
+		double *hjj = &H[(size_t)j * K + j];
+		if (*hjj == 0) {
+			*hjj = 1;
+			for (int c = 0; c < C; c++) W[(size_t)c * K + j] = 0;
+		}
+		*hjj += 0.01 * mean;
+		hdiag[j] = *hjj;
+	}
+}
+
+static void logf_append(char *log, size_t logn, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
+static void logf_append(char *log, size_t logn, const char *fmt, ...)
+{
+	const size_t at = strlen(log);
+	va_list ap;
+	va_start(ap, fmt);
+	if (at < logn) vsnprintf(log + at, logn - at, fmt, ap);
+	va_end(ap);
 }
 
 int tgq_quantize_param(tgm_module *m, tgq_param *q, int bits, int gptq, int threads, char *log, size_t logn)
 {
 	tgm_value *x = &m->val[q->v];
 	const int lim = bits == 8 ? 127 : 7, C = q->C, K = q->K;
-	const long n = (long)C * K;
-	double *W = malloc((size_t)n * sizeof *W), *hd = NULL, *U = NULL, *scale = malloc((size_t)C * sizeof *scale);
-	int *codes = malloc((size_t)n * sizeof *codes);
-	unsigned char *qb = calloc((size_t)(bits == 8 ? n : (n + 1) / 2), 1);
-	float *qs = malloc((size_t)C * sizeof *qs);
+	const size_t n = (size_t)C * K, nbytes = bits == 8 ? n : (n + 1) / 2;
+	/* element (channel c, input j) of the param's own layout */
+	#define AT(c, j) (q->axis == 0 ? (size_t)(c) * K + (size_t)(j) : (size_t)(j) * C + (size_t)(c))
+	double *W = malloc(n * sizeof *W), *step = malloc((size_t)C * sizeof *step), *hdiag = NULL, *U = NULL;
+	int *codes = malloc(n * sizeof *codes);
+	unsigned char *packed = calloc(nbytes, 1);
+	float *scale = malloc((size_t)C * sizeof *scale);
 	int rc = -1;
-	const char *how = "rtn";
-	if (!W || !scale || !codes || !qb || !qs) goto out;
+	if (!W || !step || !codes || !packed || !scale) goto done;
 	for (int c = 0; c < C; c++)
-		for (int j = 0; j < K; j++) W[(size_t)c * K + j] = q->axis == 0 ? x->data[(size_t)c * K + j] : x->data[(size_t)j * C + c];
+		for (int j = 0; j < K; j++) W[(size_t)c * K + j] = x->data[AT(c, j)];
 	if (gptq && q->H && q->nsamp) {
-		double *H = q->H, mean = 0;
-		hd = malloc((size_t)K * sizeof *hd);
+		hdiag = malloc((size_t)K * sizeof *hdiag);
 		U = malloc((size_t)K * K * sizeof *U);
-		if (!hd || !U) goto out;
-		for (int j = 0; j < K; j++) mean += H[(size_t)j * K + j];
-		mean /= K;
-		for (int j = 0; j < K; j++) {
-			if (H[(size_t)j * K + j] == 0) { /* an input never active: its weights do not matter */
-				H[(size_t)j * K + j] = 1;
-				for (int c = 0; c < C; c++) W[(size_t)c * K + j] = 0;
-			}
-			H[(size_t)j * K + j] += 0.01 * mean; /* dampening */
-			hd[j] = H[(size_t)j * K + j];
-		}
-		if (inv_chol_upper(H, K, U, threads)) {
-			how = "gptq";
-		} else {
-			size_t o = strlen(log);
-			snprintf(log + o, logn - o, "quantize: %s: Hessian not positive definite, using rtn\n", x->name);
+		if (!hdiag || !U) goto done;
+		damp(q->H, W, C, K, hdiag);
+		if (!inverse_factor(q->H, K, U, threads)) {
+			logf_append(log, logn, "quantize: %s: Hessian not positive definite, using rtn\n", x->name);
 			free(U);
 			U = NULL;
 		}
 	}
-	Chan ch = { W, hd, U, K, lim, codes, scale };
-	par(C, threads, channels, &ch);
-	double num = 0, den = 0;
+	Channels ch = { W, hdiag, U, C, K, lim, codes, step };
+	team_run(C >= 64 ? threads : 1, channel_member, &ch);
+	/* codes into the param's layout (int4: low nibble first), scales to f32 */
 	for (int c = 0; c < C; c++) {
-		qs[c] = (float)scale[c];
+		scale[c] = (float)step[c];
 		for (int j = 0; j < K; j++) {
-			long i = q->axis == 0 ? (long)c * K + j : (long)j * C + c;
-			int code = codes[(size_t)c * K + j];
-			if (bits == 8) qb[i] = (unsigned char)(signed char)code;
-			else if (i & 1) qb[i >> 1] = (unsigned char)((qb[i >> 1] & 0x0f) | ((unsigned)code << 4));
-			else qb[i >> 1] = (unsigned char)((qb[i >> 1] & 0xf0) | (code & 0x0f));
+			const size_t i = AT(c, j);
+			const unsigned v = (unsigned)codes[(size_t)c * K + j];
+			if (bits == 8) packed[i] = (unsigned char)v;
+			else packed[i >> 1] = (unsigned char)(i & 1 ? (packed[i >> 1] & 0x0fu) | (v << 4) : (packed[i >> 1] & 0xf0u) | (v & 0x0fu));
 		}
 	}
-	for (int c = 0; c < C; c++) /* report against the original weights; data becomes the dequantized values */
+	/* the report's error against the original weights, then data = the dequantized values */
+	double err2 = 0, norm2 = 0;
+	for (int c = 0; c < C; c++)
 		for (int j = 0; j < K; j++) {
-			long i = q->axis == 0 ? (long)c * K + j : (long)j * C + c;
-			double w0 = x->data[i], wq = (double)codes[(size_t)c * K + j] * qs[c];
-			num += (w0 - wq) * (w0 - wq);
-			den += w0 * w0;
-			x->data[i] = (float)wq;
+			const size_t i = AT(c, j);
+			const double orig = x->data[i], deq = (double)codes[(size_t)c * K + j] * scale[c];
+			err2 += (orig - deq) * (orig - deq);
+			norm2 += orig * orig;
+			x->data[i] = (float)deq;
 		}
+	#undef AT
 	x->qbits = bits;
 	x->qaxis = q->axis;
-	x->q = qb;
-	x->qs = qs;
-	qb = NULL;
-	qs = NULL;
-	{
-		size_t o = strlen(log);
-		snprintf(log + o, logn - o, "  %-12s (f32 %d %d) -> int%d, %d %s scales, %s, relative weight error %.4f\n", x->name, x->sh.dim[0],
-			 x->sh.dim[1], bits, C, q->axis == 0 ? "row" : "column", how, den > 0 ? sqrt(num / den) : 0.0);
-	}
+	x->q = packed;
+	x->qs = scale;
+	packed = NULL;
+	scale = NULL;
+	logf_append(log, logn, "  %-12s (f32 %d %d) -> int%d, %d %s scales, %s, relative weight error %.4f\n", x->name, x->sh.dim[0],
+		    x->sh.dim[1], bits, C, q->axis == 0 ? "row" : "column", U ? "gptq" : "rtn", norm2 > 0 ? sqrt(err2 / norm2) : 0.0);
 	rc = 0;
-out:
+done:
 	free(W);
-	free(hd);
+	free(step);
+	free(hdiag);
 	free(U);
-	free(scale);
 	free(codes);
-	free(qb);
-	free(qs);
+	free(packed);
+	free(scale);
 	return rc;
 }
