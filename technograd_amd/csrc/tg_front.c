@@ -456,15 +456,17 @@ typedef struct {
 
 static const char *KW[] = { "model", "param", "def", "return", "think", "for", "until", "f32", "import", "state", "update", "train", "with", "over", "scan", "emit", NULL };
 
-static Tok *peek(P *p) { return &p->t[p->i]; }
-static Tok *next(P *p)
+/* the token at the cursor; take() also moves past it (never past the end) */
+static Tok *look(P *p) { return &p->t[p->i]; }
+static Tok *take(P *p)
 {
 	Tok *t = &p->t[p->i];
 	if (t->k != T_EOF) p->i++;
 	return t;
 }
 
-static const char *desc(Tok *t)
+/* how a diagnostic names a token */
+static const char *tokname(Tok *t)
 {
 	switch (t->k) {
 	case T_NL: return "end of line";
@@ -475,60 +477,60 @@ static const char *desc(Tok *t)
 	}
 }
 
-static int isop(Tok *t, const char *s) { return t->k == T_OP && !strcmp(t->s, s); }
-static int iskw(Tok *t, const char *s) { return t->k == T_NAME && !strcmp(t->s, s); }
+static int at_punct(Tok *t, const char *s) { return t->k == T_OP && !strcmp(t->s, s); }
+static int at_word(Tok *t, const char *s) { return t->k == T_NAME && !strcmp(t->s, s); }
 
-static void want_op(P *p, const char *s)
+static void need_punct(P *p, const char *s)
 {
-	Tok *t = next(p);
-	if (!isop(t, s)) fail(p->f, p->file, t->line, "expected '%s', got '%s'", s, desc(t));
+	Tok *t = take(p);
+	if (!at_punct(t, s)) fail(p->f, p->file, t->line, "expected '%s', got '%s'", s, tokname(t));
 }
 
-static Tok *want(P *p, int k, const char *what)
+static Tok *need_kind(P *p, int k, const char *what)
 {
-	Tok *t = next(p);
-	if (t->k != k) fail(p->f, p->file, t->line, "expected %s, got '%s'", what, desc(t));
+	Tok *t = take(p);
+	if (t->k != k) fail(p->f, p->file, t->line, "expected %s, got '%s'", what, tokname(t));
 	return t;
 }
 
-static Tok *want_name(P *p)
+static Tok *need_ident(P *p)
 {
-	Tok *t = want(p, T_NAME, "name");
+	Tok *t = need_kind(p, T_NAME, "name");
 	for (int i = 0; KW[i]; i++)
 		if (!strcmp(t->s, KW[i])) fail(p->f, p->file, t->line, "'%s' is a reserved word", t->s);
 	return t;
 }
 
-static double snum(P *p)
+static double signed_lit(P *p)
 {
 	int neg = 0;
-	if (isop(peek(p), "-")) next(p), neg = 1;
-	Tok *t = want(p, T_NUM, "number");
+	if (at_punct(look(p), "-")) take(p), neg = 1;
+	Tok *t = need_kind(p, T_NUM, "number");
 	return neg ? -t->n : t->n;
 }
 
-static int posint(P *p)
+static int count_lit(P *p)
 {
-	Tok *t = want(p, T_NUM, "integer");
+	Tok *t = need_kind(p, T_NUM, "integer");
 	if (t->n < 1 || t->n != (double)(int)t->n || t->n > 1 << 24) fail(p->f, p->file, t->line, "expected positive integer, got '%s'", t->s);
 	return (int)t->n;
 }
 
 static Sh type(P *p)
 {
-	Tok *t = next(p);
-	if (!iskw(t, "f32")) fail(p->f, p->file, t->line, "expected type 'f32', got '%s'", desc(t));
+	Tok *t = take(p);
+	if (!at_word(t, "f32")) fail(p->f, p->file, t->line, "expected type 'f32', got '%s'", tokname(t));
 	Sh s = { 0, { 0 } };
-	if (isop(peek(p), "[")) {
-		next(p);
+	if (at_punct(look(p), "[")) {
+		take(p);
 		for (;;) {
 			if (s.rank >= MAXRANK) fail(p->f, p->file, t->line, "rank exceeds %d", MAXRANK);
-			s.dim[s.rank++] = posint(p);
-			if (isop(peek(p), "]")) {
-				next(p);
+			s.dim[s.rank++] = count_lit(p);
+			if (at_punct(look(p), "]")) {
+				take(p);
 				break;
 			}
-			want_op(p, ",");
+			need_punct(p, ",");
 		}
 	}
 	return s;
@@ -547,54 +549,54 @@ static void init_add(P *p, Init *in, double v)
 
 static void literal(P *p, Init *in)
 {
-	if (isop(peek(p), "[")) {
-		next(p);
+	if (at_punct(look(p), "[")) {
+		take(p);
 		for (;;) {
 			literal(p, in);
-			if (isop(peek(p), "]")) {
-				next(p);
+			if (at_punct(look(p), "]")) {
+				take(p);
 				return;
 			}
-			want_op(p, ",");
+			need_punct(p, ",");
 		}
 	}
-	init_add(p, in, snum(p));
+	init_add(p, in, signed_lit(p));
 }
 
 static Init initializer(P *p)
 {
-	Tok *t = peek(p);
+	Tok *t = look(p);
 	Init in = { I_DATA, 0, t->line, 0, NULL, NULL };
-	if (iskw(t, "zeros") || iskw(t, "ones")) {
-		next(p);
-		in.kind = iskw(t, "zeros") ? I_ZEROS : I_ONES;
-	} else if (iskw(t, "fill")) {
-		next(p);
-		want_op(p, "(");
+	if (at_word(t, "zeros") || at_word(t, "ones")) {
+		take(p);
+		in.kind = at_word(t, "zeros") ? I_ZEROS : I_ONES;
+	} else if (at_word(t, "fill")) {
+		take(p);
+		need_punct(p, "(");
 		in.kind = I_FILL;
-		init_add(p, &in, snum(p));
-		want_op(p, ")");
-	} else if (iskw(t, "rand")) {
-		next(p);
-		want_op(p, "(");
+		init_add(p, &in, signed_lit(p));
+		need_punct(p, ")");
+	} else if (at_word(t, "rand")) {
+		take(p);
+		need_punct(p, "(");
 		in.kind = I_RAND;
-		init_add(p, &in, snum(p));
-		want_op(p, ",");
-		init_add(p, &in, snum(p));
-		want_op(p, ")");
-	} else if (iskw(t, "file")) {
-		next(p);
-		want_op(p, "(");
+		init_add(p, &in, signed_lit(p));
+		need_punct(p, ",");
+		init_add(p, &in, signed_lit(p));
+		need_punct(p, ")");
+	} else if (at_word(t, "file")) {
+		take(p);
+		need_punct(p, "(");
 		in.kind = I_FILE;
-		in.str = want(p, T_STR, "string")->s;
-		want_op(p, ")");
-	} else if (iskw(t, "env")) {
-		next(p);
-		want_op(p, "(");
+		in.str = need_kind(p, T_STR, "string")->s;
+		need_punct(p, ")");
+	} else if (at_word(t, "env")) {
+		take(p);
+		need_punct(p, "(");
 		in.kind = I_ENV;
-		in.str = want(p, T_STR, "string")->s;
-		if (isop(peek(p), ",")) next(p), init_add(p, &in, snum(p));
-		want_op(p, ")");
+		in.str = need_kind(p, T_STR, "string")->s;
+		if (at_punct(look(p), ",")) take(p), init_add(p, &in, signed_lit(p));
+		need_punct(p, ")");
 	} else {
 		literal(p, &in);
 	}
@@ -630,52 +632,52 @@ static Ex *expr(P *p);
 
 static Ex *primary(P *p)
 {
-	Tok *t = next(p);
+	Tok *t = take(p);
 	if (t->k == T_NUM) {
 		Ex *e = ex_new(p, E_NUM, t->line);
 		e->num = t->n;
 		return e;
 	}
-	if (isop(t, "(")) {
+	if (at_punct(t, "(")) {
 		Ex *e = expr(p);
-		want_op(p, ")");
+		need_punct(p, ")");
 		return e;
 	}
 	if (t->k == T_NAME) {
 		for (int i = 0; KW[i]; i++)
 			if (!strcmp(t->s, KW[i])) fail(p->f, p->file, t->line, "unexpected keyword '%s' in expression", t->s);
-		if (isop(peek(p), "(")) {
-			next(p);
+		if (at_punct(look(p), "(")) {
+			take(p);
 			Ex *c = ex_new(p, E_CALL, t->line);
 			c->name = t->s;
-			if (isop(peek(p), ")")) {
-				next(p);
+			if (at_punct(look(p), ")")) {
+				take(p);
 				return c;
 			}
 			for (;;) {
 				ex_arg(p, c, expr(p));
-				if (isop(peek(p), ")")) {
-					next(p);
+				if (at_punct(look(p), ")")) {
+					take(p);
 					return c;
 				}
-				want_op(p, ",");
+				need_punct(p, ",");
 			}
 		}
 		Ex *e = ex_new(p, E_REF, t->line);
 		e->name = t->s;
 		return e;
 	}
-	fail(p->f, p->file, t->line, "expected expression, got '%s'", desc(t));
+	fail(p->f, p->file, t->line, "expected expression, got '%s'", tokname(t));
 	return NULL;
 }
 
 static Ex *unary(P *p)
 {
-	if (isop(peek(p), "-")) {
-		int line = next(p)->line;
-		Tok *t = peek(p);
+	if (at_punct(look(p), "-")) {
+		int line = take(p)->line;
+		Tok *t = look(p);
 		if (t->k == T_NUM) { /* a negative literal is one number */
-			next(p);
+			take(p);
 			Ex *e = ex_new(p, E_NUM, line);
 			e->num = -t->n;
 			return e;
@@ -689,10 +691,10 @@ static Ex *term(P *p)
 {
 	Ex *e = unary(p);
 	for (;;) {
-		Tok *t = peek(p);
-		const char *op = isop(t, "*") ? "mul" : isop(t, "/") ? "div" : isop(t, "@") ? "matmul" : NULL;
+		Tok *t = look(p);
+		const char *op = at_punct(t, "*") ? "mul" : at_punct(t, "/") ? "div" : at_punct(t, "@") ? "matmul" : NULL;
 		if (!op) return e;
-		next(p);
+		take(p);
 		e = call(p, op, e, unary(p), t->line);
 	}
 }
@@ -701,17 +703,17 @@ static Ex *expr(P *p)
 {
 	Ex *e = term(p);
 	for (;;) {
-		Tok *t = peek(p);
-		const char *op = isop(t, "+") ? "add" : isop(t, "-") ? "sub" : NULL;
+		Tok *t = look(p);
+		const char *op = at_punct(t, "+") ? "add" : at_punct(t, "-") ? "sub" : NULL;
 		if (!op) return e;
-		next(p);
+		take(p);
 		e = call(p, op, e, term(p), t->line);
 	}
 }
 
 static void block(P *p, St ***body, int *n, int *bline);
 
-static const char **names_add(P *p, const char **a, int n, const char *s)
+static const char **name_push(P *p, const char **a, int n, const char *s)
 {
 	const char **r = fa(p->f, (size_t)(n + 1) * sizeof *r);
 	if (n) memcpy(r, a, (size_t)n * sizeof *r);
@@ -719,188 +721,250 @@ static const char **names_add(P *p, const char **a, int n, const char *s)
 	return r;
 }
 
-static St *stmt(P *p)
+/* Statements. Each form after its leading word has a handler (the word is
+ * consumed); a line that starts with none of them is an assignment. The
+ * token sequence each form accepts, and the diagnostic for the first token
+ * that breaks it, are the surface grammar's (src/parse.c); the pieces shared
+ * by several forms are the helpers below. */
+
+static void line_end(P *p) { need_kind(p, T_NL, "end of line"); }
+
+static Ex *assigned(P *p) /* "= expr" */
 {
-	Tok *t = peek(p);
-	St *s = fa(p->f, sizeof *s);
-	s->line = t->line;
-	if (iskw(t, "return")) {
-		next(p);
-		s->kind = S_RETURN;
-		s->e = expr(p);
-		want(p, T_NL, "end of line");
-	} else if (iskw(t, "train")) { /* parsed for its diagnostics; lowering refuses it */
-		next(p);
-		s->kind = S_TRAIN;
-		s->e = expr(p);
-		if (iskw(peek(p), "with")) {
-			next(p);
-			want(p, T_NAME, "optimizer name");
-			if (isop(peek(p), "(")) {
-				next(p);
-				for (;;) {
-					want(p, T_NAME, "option name");
-					want_op(p, "=");
-					snum(p);
-					if (isop(peek(p), ")")) {
-						next(p);
-						break;
-					}
-					want_op(p, ",");
-				}
-			}
-		}
-		if (iskw(peek(p), "over")) {
-			next(p);
-			for (;;) {
-				want_name(p);
-				if (!isop(peek(p), ",")) break;
-				next(p);
-			}
-		}
-		want(p, T_NL, "end of line");
-	} else if (iskw(t, "update")) {
-		next(p);
-		s->kind = S_UPDATE;
-		s->name = want_name(p)->s;
-		if (isop(peek(p), "[")) {
-			next(p);
-			s->rows = expr(p);
-			want_op(p, "]");
-		}
-		want_op(p, "=");
-		s->e = expr(p);
-		want(p, T_NL, "end of line");
-	} else if (iskw(t, "scan")) {
-		next(p);
-		s->kind = S_SCAN;
-		for (;;) {
-			Tok *n = want_name(p);
-			s->cs = names_add(p, s->cs, s->ncs++, n->s);
-			if (!isop(peek(p), ",")) break;
-			next(p);
-		}
-		Tok *o = next(p);
-		if (!iskw(o, "over")) fail(p->f, p->file, o->line, "expected 'over' after the scan carries, got '%s'", desc(o));
-		for (;;) {
-			Tok *n = want_name(p);
-			Tok *in = next(p);
-			if (!iskw(in, "in")) fail(p->f, p->file, in->line, "expected 'in' after scan slice '%s', got '%s'", n->s, desc(in));
-			Ex *e = expr(p);
-			Ex **xe = fa(p->f, (size_t)(s->nx + 1) * sizeof *xe);
-			if (s->nx) memcpy(xe, s->xe, (size_t)s->nx * sizeof *xe);
-			xe[s->nx] = e;
-			s->xe = xe;
-			s->xn = names_add(p, s->xn, s->nx++, n->s);
-			if (!isop(peek(p), ",")) break;
-			next(p);
-		}
-		want_op(p, ":");
-		block(p, &s->body, &s->nbody, &s->bline);
-	} else if (iskw(t, "emit")) {
-		next(p);
-		s->kind = S_EMIT;
-		s->name = want_name(p)->s;
-		want_op(p, "=");
-		s->e = expr(p);
-		want(p, T_NL, "end of line");
-	} else if (iskw(t, "think")) {
-		next(p);
-		s->kind = S_THINK;
-		s->name = want_name(p)->s;
-		Tok *fo = next(p);
-		if (!iskw(fo, "for")) fail(p->f, p->file, fo->line, "expected 'for' after think state, got '%s'", desc(fo));
-		s->maxit = posint(p);
-		s->eps = -1;
-		if (iskw(peek(p), "until")) {
-			next(p);
-			s->eps = snum(p);
-			if (s->eps < 0) fail(p->f, p->file, s->line, "halting threshold must be >= 0");
-		} else if (iskw(peek(p), "halt")) {
-			next(p);
-			s->has_halt = 1;
-			s->halt = want_name(p)->s;
-			s->hthr = 0.5;
-			if (iskw(peek(p), "at")) {
-				next(p);
-				s->hthr = snum(p);
-				if (s->hthr <= 0 || s->hthr >= 1) fail(p->f, p->file, s->line, "halting threshold must be in (0, 1)");
-			}
-		}
-		want_op(p, ":");
-		block(p, &s->body, &s->nbody, &s->bline);
-	} else {
-		s->kind = S_SET;
-		s->name = want_name(p)->s;
-		want_op(p, "=");
-		s->e = expr(p);
-		want(p, T_NL, "end of line");
+	need_punct(p, "=");
+	return expr(p);
+}
+
+/* item, then more items while a comma follows */
+static void comma_list(P *p, void (*item)(P *p, St *s), St *s)
+{
+	for (item(p, s); at_punct(look(p), ","); item(p, s)) take(p);
+}
+
+/* the word w or fail with msg (a format with the got-token last) */
+static Tok *need_word(P *p, const char *w, const char *msg, const char *arg)
+{
+	Tok *t = take(p);
+	if (!at_word(t, w)) {
+		if (arg) fail(p->f, p->file, t->line, msg, arg, tokname(t));
+		fail(p->f, p->file, t->line, msg, tokname(t));
 	}
+	return t;
+}
+
+static St *st_return(P *p, St *s)
+{
+	s->kind = S_RETURN;
+	s->e = expr(p);
+	line_end(p);
 	return s;
 }
 
+static void opt_item(P *p, St *s)
+{
+	(void)s;
+	need_kind(p, T_NAME, "option name");
+	need_punct(p, "=");
+	signed_lit(p);
+}
+
+static void over_item(P *p, St *s)
+{
+	(void)s;
+	need_ident(p);
+}
+
+static St *st_train(P *p, St *s) /* parsed for its diagnostics; lowering refuses it */
+{
+	s->kind = S_TRAIN;
+	s->e = expr(p);
+	if (at_word(look(p), "with")) {
+		take(p);
+		need_kind(p, T_NAME, "optimizer name");
+		if (at_punct(look(p), "(")) {
+			take(p);
+			for (opt_item(p, s); !at_punct(look(p), ")"); opt_item(p, s)) need_punct(p, ",");
+			take(p);
+		}
+	}
+	if (at_word(look(p), "over")) {
+		take(p);
+		comma_list(p, over_item, s);
+	}
+	line_end(p);
+	return s;
+}
+
+static St *st_update(P *p, St *s)
+{
+	s->kind = S_UPDATE;
+	s->name = need_ident(p)->s;
+	if (at_punct(look(p), "[")) {
+		take(p);
+		s->rows = expr(p);
+		need_punct(p, "]");
+	}
+	s->e = assigned(p);
+	line_end(p);
+	return s;
+}
+
+static void carry_item(P *p, St *s)
+{
+	s->cs = name_push(p, s->cs, s->ncs++, need_ident(p)->s);
+}
+
+static void slice_item(P *p, St *s)
+{
+	Tok *n = need_ident(p);
+	need_word(p, "in", "expected 'in' after scan slice '%s', got '%s'", n->s);
+	Ex *e = expr(p);
+	Ex **xe = fa(p->f, (size_t)(s->nx + 1) * sizeof *xe);
+	if (s->nx) memcpy(xe, s->xe, (size_t)s->nx * sizeof *xe);
+	xe[s->nx] = e;
+	s->xe = xe;
+	s->xn = name_push(p, s->xn, s->nx++, n->s);
+}
+
+static St *st_scan(P *p, St *s)
+{
+	s->kind = S_SCAN;
+	comma_list(p, carry_item, s);
+	need_word(p, "over", "expected 'over' after the scan carries, got '%s'", NULL);
+	comma_list(p, slice_item, s);
+	need_punct(p, ":");
+	block(p, &s->body, &s->nbody, &s->bline);
+	return s;
+}
+
+static St *st_emit(P *p, St *s)
+{
+	s->kind = S_EMIT;
+	s->name = need_ident(p)->s;
+	s->e = assigned(p);
+	line_end(p);
+	return s;
+}
+
+/* think STATE for N [until EPS | halt NAME [at THRESHOLD]]: BLOCK */
+static St *st_think(P *p, St *s)
+{
+	s->kind = S_THINK;
+	s->name = need_ident(p)->s;
+	need_word(p, "for", "expected 'for' after think state, got '%s'", NULL);
+	s->maxit = count_lit(p);
+	s->eps = -1;
+	Tok *t = look(p);
+	if (at_word(t, "until")) {
+		take(p);
+		s->eps = signed_lit(p);
+		if (s->eps < 0) fail(p->f, p->file, s->line, "halting threshold must be >= 0");
+	} else if (at_word(t, "halt")) {
+		take(p);
+		s->has_halt = 1;
+		s->halt = need_ident(p)->s;
+		s->hthr = 0.5;
+		if (at_word(look(p), "at")) {
+			take(p);
+			s->hthr = signed_lit(p);
+			if (s->hthr <= 0 || s->hthr >= 1) fail(p->f, p->file, s->line, "halting threshold must be in (0, 1)");
+		}
+	}
+	need_punct(p, ":");
+	block(p, &s->body, &s->nbody, &s->bline);
+	return s;
+}
+
+static const struct {
+	const char *word;
+	St *(*form)(P *p, St *s);
+} STMT_FORMS[] = {
+	{ "return", st_return }, { "train", st_train }, { "update", st_update },
+	{ "scan", st_scan },     { "emit", st_emit },   { "think", st_think },
+};
+
+static St *stmt(P *p)
+{
+	Tok *t = look(p);
+	St *s = fa(p->f, sizeof *s);
+	s->line = t->line;
+	for (size_t i = 0; i < sizeof STMT_FORMS / sizeof STMT_FORMS[0]; i++)
+		if (at_word(t, STMT_FORMS[i].word)) {
+			take(p);
+			return STMT_FORMS[i].form(p, s);
+		}
+	s->kind = S_SET; /* NAME = expr */
+	s->name = need_ident(p)->s;
+	s->e = assigned(p);
+	line_end(p);
+	return s;
+}
+
+/* NL INDENT statement... DEDENT */
 static void block(P *p, St ***body, int *n, int *bline)
 {
-	want(p, T_NL, "end of line");
-	*bline = want(p, T_INDENT, "indented block")->line;
-	*body = NULL;
-	*n = 0;
-	while (peek(p)->k != T_DEDENT && peek(p)->k != T_EOF) {
+	line_end(p);
+	*bline = need_kind(p, T_INDENT, "indented block")->line;
+	St **v = NULL;
+	int len = 0;
+	while (look(p)->k != T_DEDENT && look(p)->k != T_EOF) {
 		St *s = stmt(p);
-		St **v = fa(p->f, (size_t)(*n + 1) * sizeof *v);
-		if (*n) memcpy(v, *body, (size_t)*n * sizeof *v);
-		v[(*n)++] = s;
-		*body = v;
+		St **grown = fa(p->f, (size_t)(len + 1) * sizeof *grown);
+		if (len) memcpy(grown, v, (size_t)len * sizeof *grown);
+		grown[len++] = s;
+		v = grown;
 	}
-	want(p, T_DEDENT, "dedent");
+	need_kind(p, T_DEDENT, "dedent");
+	*body = v;
+	*n = len;
 }
 
 static Decl *decl(P *p)
 {
-	Tok *t = next(p);
+	Tok *t = take(p);
 	Decl *d = fa(p->f, sizeof *d);
 	d->line = t->line;
-	if (iskw(t, "import")) {
+	if (at_word(t, "import")) {
 		d->kind = D_IMPORT;
-		d->str = want(p, T_STR, "import path string")->s;
-		want(p, T_NL, "end of line");
-	} else if (iskw(t, "model")) {
+		d->str = need_kind(p, T_STR, "import path string")->s;
+		need_kind(p, T_NL, "end of line");
+	} else if (at_word(t, "model")) {
 		d->kind = D_MODEL;
-		d->name = want_name(p)->s;
-		want(p, T_NL, "end of line");
-	} else if (iskw(t, "param") || iskw(t, "state")) {
-		d->kind = iskw(t, "param") ? D_PARAM : D_STATE;
-		d->name = want_name(p)->s;
-		want_op(p, ":");
+		d->name = need_ident(p)->s;
+		need_kind(p, T_NL, "end of line");
+	} else if (at_word(t, "param") || at_word(t, "state")) {
+		d->kind = at_word(t, "param") ? D_PARAM : D_STATE;
+		d->name = need_ident(p)->s;
+		need_punct(p, ":");
 		d->sh = type(p);
-		want_op(p, "=");
+		need_punct(p, "=");
 		d->init = initializer(p);
-		want(p, T_NL, "end of line");
-	} else if (iskw(t, "def")) {
+		need_kind(p, T_NL, "end of line");
+	} else if (at_word(t, "def")) {
 		d->kind = D_DEF;
-		d->name = want_name(p)->s;
-		want_op(p, "(");
-		if (!isop(peek(p), ")")) {
+		d->name = need_ident(p)->s;
+		need_punct(p, "(");
+		if (!at_punct(look(p), ")")) {
 			for (;;) {
-				Tok *a = want_name(p);
-				want_op(p, ":");
+				Tok *a = need_ident(p);
+				need_punct(p, ":");
 				Sh sh = type(p);
 				Sh *as = fa(p->f, (size_t)(d->nargs + 1) * sizeof *as);
 				if (d->nargs) memcpy(as, d->as, (size_t)d->nargs * sizeof *as);
 				as[d->nargs] = sh;
 				d->as = as;
-				d->an = names_add(p, d->an, d->nargs++, a->s);
-				if (isop(peek(p), ")")) break;
-				want_op(p, ",");
+				d->an = name_push(p, d->an, d->nargs++, a->s);
+				if (at_punct(look(p), ")")) break;
+				need_punct(p, ",");
 			}
 		}
-		want_op(p, ")");
-		want_op(p, "->");
+		need_punct(p, ")");
+		need_punct(p, "->");
 		d->sh = type(p);
-		want_op(p, ":");
+		need_punct(p, ":");
 		block(p, &d->body, &d->nbody, &d->bline);
 	} else {
-		fail(p->f, p->file, d->line, "expected 'import', 'model', 'param', 'state' or 'def', got '%s'", desc(t));
+		fail(p->f, p->file, d->line, "expected 'import', 'model', 'param', 'state' or 'def', got '%s'", tokname(t));
 	}
 	return d;
 }
@@ -974,10 +1038,10 @@ static void load_file(F *f, Prog *g, const char *path, int depth, int root, cons
 	P p = { f, path, NULL, 0, 0, 0 };
 	lex(&p, src);
 	for (;;) {
-		Tok *t = peek(&p);
+		Tok *t = look(&p);
 		if (t->k == T_EOF) break;
 		if (t->k == T_NL) {
-			next(&p);
+			take(&p);
 			continue;
 		}
 		if (t->k == T_INDENT) fail(f, path, t->line, "unexpected indent");
@@ -1126,96 +1190,150 @@ static int lookup(L *l, Env *e, const char *n, int line)
 
 static int is_num(const Ex *x) { return x->kind == E_NUM; }
 
-/* rope(x, pos) and attention(Q, K, V, W): expansions into table ops (src/lower.c:370-419) */
-static int lower_attn(L *l, Blk *b, Env *e, Ex *x)
+/* ---- builtin expansions ----
+ * The builtins the reference expands into table operations (the losses,
+ * rope, attention, take_along) are written here as expression trees over the
+ * call's values, one tree per intermediate the reference names. tree_emit()
+ * creates a tree's instructions in the order the reference's build creates
+ * them: its builder calls take their operands as nested calls, which that
+ * build evaluates last operand first, so a tree is emitted in post-order
+ * with the operands visited from the last to the first. The trees live in
+ * compound literals of the enclosing block. */
+typedef struct Tn {
+	char kind;              /* 'v' a value, 'k' a scalar constant, 'o' an operation, 'r' a reshape */
+	int v;                  /* 'v' */
+	float k;                /* 'k' */
+	const char *op;         /* 'o' */
+	const struct Tn *a, *b; /* operands ('o': b NULL when unary; 'r': a) */
+	const Sh *to;           /* 'r' */
+} Tn;
+#define TV(x) (&(Tn){ 'v', (x), 0, NULL, NULL, NULL, NULL })
+#define TK(x) (&(Tn){ 'k', -1, (float)(x), NULL, NULL, NULL, NULL })
+#define T1(o, x) (&(Tn){ 'o', -1, 0, (o), (x), NULL, NULL })
+#define T2(o, x, y) (&(Tn){ 'o', -1, 0, (o), (x), (y), NULL })
+#define TR(x, s) (&(Tn){ 'r', -1, 0, NULL, (x), NULL, (s) })
+
+static int tree_emit(L *l, Blk *b, const Tn *t, int line)
 {
-	F *f = l->f;
-	char name[64], s0[64];
-	int line = x->line;
-	if (!strcmp(x->name, "rope")) {
-		if (x->nargs != 2) fail(f, l->file, line, "'rope' takes (x, position)");
-		int v = lower_expr(l, b, e, x->args[0]), p = lower_expr(l, b, e, x->args[1]);
-		Sh xs = f->val[v].sh, ps = f->val[p].sh;
-		int d = xs.dim[xs.rank - 1];
-		int ok = (xs.rank == 1 && ps.rank == 0) || (xs.rank == 2 && ps.rank == 1 && ps.dim[0] == xs.dim[0]);
-		if (!ok || d % 2) fail(f, l->file, line, "'rope' takes x (d) with a scalar position or x (T, d) with positions (T), d even");
-		float *fr = fa(f, (size_t)d * sizeof *fr), *sw = fa(f, (size_t)d * (size_t)d * sizeof *sw);
-		for (int i = 0; i < d; i++) fr[i] = (float)pow(10000.0, -(double)(i / 2 * 2) / d);
-		for (int i = 0; i < d; i += 2) sw[i * d + i + 1] = 1, sw[(i + 1) * d + i] = -1;
-		Sh s1 = { 1, { d } }, s2 = { 2, { d, d } };
-		snprintf(name, sizeof name, "__rope_freq_%d", d);
-		int fv = const_param(l, name, &s1, fr);
-		snprintf(name, sizeof name, "__swap_%d", d);
-		int sv = const_param(l, name, &s2, sw);
-		int ang = xs.rank == 1 ? op2(l, b, "mul", fv, p, line) : op2(l, b, "outer", p, fv, line);
-		/* x cos(a) + (x @ swap) sin(a), instructions in the reference's order (the sine term first) */
-		int sn = op2(l, b, "sin", ang, -1, line);
-		int xs_ = op2(l, b, "matmul", v, sv, line);
-		int st = op2(l, b, "mul", xs_, sn, line);
-		int cs = op2(l, b, "cos", ang, -1, line);
-		int ct = op2(l, b, "mul", v, cs, line);
-		return op2(l, b, "add", ct, st, line);
+	switch (t->kind) {
+	case 'v': return t->v;
+	case 'k': return konst(l, b, t->k);
+	case 'r': return reshape_to(l, b, tree_emit(l, b, t->a, line), t->to);
+	default: {
+		const int q = t->b ? tree_emit(l, b, t->b, line) : -1; /* the last operand first */
+		const int r = tree_emit(l, b, t->a, line);
+		return op2(l, b, t->op, r, q, line);
 	}
-	(void)s0;
-	if (x->nargs != 4) fail(f, l->file, line, "'attention' takes (Q, K, V, window)");
-	Ex *wd = x->args[3];
-	if (!is_num(wd) || wd->num < 1 || wd->num != (double)(int)wd->num) fail(f, l->file, line, "'attention' window must be a positive integer literal");
-	int W = (int)wd->num;
-	int q = lower_expr(l, b, e, x->args[0]), k = lower_expr(l, b, e, x->args[1]), v = lower_expr(l, b, e, x->args[2]);
-	Sh qs = f->val[q].sh, ks = f->val[k].sh, vs = f->val[v].sh;
-	if (qs.rank != 2 || !sheq(&qs, &ks) || vs.rank != 2 || vs.dim[0] != qs.dim[0])
-		fail(f, l->file, line, "'attention' needs Q and K of one shape (T, d) and V (T, e)");
-	int T = qs.dim[0];
-	float *mk = fa(f, (size_t)T * (size_t)T * sizeof *mk);
-	for (int t = 0; t < T; t++)
-		for (int s = 0; s < T; s++) mk[t * T + s] = s <= t && t - s < W ? 0.0f : -1e9f;
-	Sh ms = { 2, { T, T } };
-	snprintf(name, sizeof name, "__causal_%d_%d", T, W);
-	int mv = const_param(l, name, &ms, mk);
-	int sk = konst(l, b, (float)(1.0 / sqrt((double)qs.dim[1]))); /* the scale's const precedes the product */
-	int kt = op2(l, b, "transpose", k, -1, line);
-	int sc = op2(l, b, "mul", op2(l, b, "matmul", q, kt, line), sk, line);
-	sc = op2(l, b, "add", sc, mv, line);
-	return op2(l, b, "matmul", op2(l, b, "softmax", sc, -1, line), v, line);
+	}
 }
 
-/* take_along(x, i): the gather along the last axis as one take over the flattened rows (src/lower.c:326-364) */
+/* mse, bce, xent of prediction p and target t (shapes checked by the caller) */
+static int lower_loss(L *l, Blk *b, const char *fn, int p, int t, int line)
+{
+	F *f = l->f;
+	if (!strcmp(fn, "mse")) { /* mean((p - t)^2) */
+		const int d = tree_emit(l, b, T2("sub", TV(p), TV(t)), line);
+		return tree_emit(l, b, T1("mean", T2("mul", TV(d), TV(d))), line);
+	}
+	if (!strcmp(fn, "bce")) { /* -mean(t log(p + 1e-7) + (1 - t) log(1 - p + 1e-7)) */
+		const int lp = tree_emit(l, b, T1("log", T2("add", TV(p), TK(1e-7f))), line);
+		const int lq = tree_emit(l, b, T1("log", T2("add", T2("sub", TK(1), TV(p)), TK(1e-7f))), line);
+		const int sm = tree_emit(l, b, T2("add", T2("mul", TV(t), TV(lp)), T2("mul", T2("sub", TK(1), TV(t)), TV(lq))), line);
+		return tree_emit(l, b, T1("neg", T1("mean", TV(sm))), line);
+	}
+	const int rk = f->val[p].sh.rank; /* xent: -sum(t log(softmax(p) + 1e-12)), averaged over a batch's rows */
+	if (rk != 1 && rk != 2) fail(f, l->file, line, "'xent' needs logits of shape (C) or a batch (B, C), with one-hot targets");
+	const int ls = tree_emit(l, b, T1("log", T2("add", T1("softmax", TV(p)), TK(1e-12f))), line);
+	int sm = tree_emit(l, b, T1("sum", T2("mul", TV(t), TV(ls))), line);
+	if (rk == 2) sm = tree_emit(l, b, T2("div", TV(sm), TK((float)f->val[p].sh.dim[0])), line);
+	return tree_emit(l, b, T1("neg", TV(sm)), line);
+}
+
+/* rope(x, position): x cos(a) + (x @ swap) sin(a), a = freq * position */
+static int lower_rope(L *l, Blk *b, Env *e, Ex *x)
+{
+	F *f = l->f;
+	const int line = x->line;
+	if (x->nargs != 2) fail(f, l->file, line, "'rope' takes (x, position)");
+	const int v = lower_expr(l, b, e, x->args[0]), pos = lower_expr(l, b, e, x->args[1]);
+	const Sh xs = f->val[v].sh, ps = f->val[pos].sh;
+	const int d = xs.dim[xs.rank - 1];
+	const int shapes = (xs.rank == 1 && ps.rank == 0) || (xs.rank == 2 && ps.rank == 1 && ps.dim[0] == xs.dim[0]);
+	if (!shapes || d % 2) fail(f, l->file, line, "'rope' takes x (d) with a scalar position or x (T, d) with positions (T), d even");
+	/* frequencies 10000^(-2 floor(i / 2) / d); swap maps each pair (x0, x1) to (-x1, x0) under x @ swap */
+	float *freq = fa(f, (size_t)d * sizeof *freq), *swap = fa(f, (size_t)d * (size_t)d * sizeof *swap);
+	for (int i = 0; i < d; i++) freq[i] = (float)pow(10000.0, -(double)(i / 2 * 2) / d);
+	for (int pr = 0; pr < d / 2; pr++) swap[(2 * pr) * d + 2 * pr + 1] = 1, swap[(2 * pr + 1) * d + 2 * pr] = -1;
+	char name[64];
+	const Sh s1 = { 1, { d } }, s2 = { 2, { d, d } };
+	snprintf(name, sizeof name, "__rope_freq_%d", d);
+	const int fv = const_param(l, name, &s1, freq);
+	snprintf(name, sizeof name, "__swap_%d", d);
+	const int sv = const_param(l, name, &s2, swap);
+	const int ang = tree_emit(l, b, xs.rank == 1 ? T2("mul", TV(fv), TV(pos)) : T2("outer", TV(pos), TV(fv)), line);
+	return tree_emit(l, b, T2("add", T2("mul", TV(v), T1("cos", TV(ang))), T2("mul", T2("matmul", TV(v), TV(sv)), T1("sin", TV(ang)))), line);
+}
+
+/* attention(Q, K, V, window): softmax(Q K^T / sqrt(d) + causal window mask) V */
+static int lower_attention(L *l, Blk *b, Env *e, Ex *x)
+{
+	F *f = l->f;
+	const int line = x->line;
+	if (x->nargs != 4) fail(f, l->file, line, "'attention' takes (Q, K, V, window)");
+	const Ex *wd = x->args[3];
+	if (!is_num(wd) || wd->num < 1 || wd->num != (double)(int)wd->num) fail(f, l->file, line, "'attention' window must be a positive integer literal");
+	const int win = (int)wd->num;
+	const int q = lower_expr(l, b, e, x->args[0]), k = lower_expr(l, b, e, x->args[1]), v = lower_expr(l, b, e, x->args[2]);
+	const Sh qs = f->val[q].sh, ks = f->val[k].sh, vs = f->val[v].sh;
+	if (qs.rank != 2 || !sheq(&qs, &ks) || vs.rank != 2 || vs.dim[0] != qs.dim[0])
+		fail(f, l->file, line, "'attention' needs Q and K of one shape (T, d) and V (T, e)");
+	const int T = qs.dim[0];
+	float *mask = fa(f, (size_t)T * (size_t)T * sizeof *mask); /* 0 where query t sees key s: s <= t, t - s < window */
+	for (int t = 0; t < T; t++)
+		for (int sk = 0; sk < T; sk++) mask[t * T + sk] = sk <= t && t - sk < win ? 0.0f : -1e9f;
+	char name[64];
+	const Sh ms = { 2, { T, T } };
+	snprintf(name, sizeof name, "__causal_%d_%d", T, win);
+	const int mv = const_param(l, name, &ms, mask);
+	const float inv = (float)(1.0 / sqrt((double)qs.dim[1]));
+	const int sc = tree_emit(l, b, T2("add", T2("mul", T2("matmul", TV(q), T1("transpose", TV(k))), TK(inv)), TV(mv)), line);
+	return tree_emit(l, b, T2("matmul", T1("softmax", TV(sc)), TV(v)), line);
+}
+
+/* take_along(x, i): the gather along the last axis as one take over the
+ * flattened rows; an index outside [0, n) reads element -1 of the flattened
+ * x's row... taken as zero by the in-range mask (i + 1) and (n - i) steps */
 static int lower_take_along(L *l, Blk *b, Env *e, Ex *x)
 {
 	F *f = l->f;
-	int line = x->line;
-	char s0[64], s1[64], name[64];
+	const int line = x->line;
+	char s0[64], s1[64];
 	if (x->nargs != 2) fail(f, l->file, line, "'take_along' takes (x, indices)");
-	int v = lower_expr(l, b, e, x->args[0]), iv = lower_expr(l, b, e, x->args[1]);
-	Sh xs = f->val[v].sh, is = f->val[iv].sh;
-	int ok = xs.rank >= 1 && is.rank == xs.rank;
-	for (int d = 0; ok && d < xs.rank - 1; d++) ok = xs.dim[d] == is.dim[d];
-	if (!ok)
+	const int v = lower_expr(l, b, e, x->args[0]), iv = lower_expr(l, b, e, x->args[1]);
+	const Sh xs = f->val[v].sh, is = f->val[iv].sh;
+	int same = xs.rank >= 1 && is.rank == xs.rank;
+	for (int d = 0; same && d < xs.rank - 1; d++) same = xs.dim[d] == is.dim[d];
+	if (!same)
 		fail(f, l->file, line, "'take_along' needs x (..., n) and indices (..., k) with the same leading dimensions; got %s and %s",
 		     shstr(&xs, s0), shstr(&is, s1));
-	int n = xs.dim[xs.rank - 1], k = is.dim[is.rank - 1], R = numel(&xs) / n;
-	/* in range: step(i + 1) * step(n - i); the second factor's instructions come first */
-	int hi = op2(l, b, "step", op2(l, b, "sub", konst(l, b, (float)n), iv, line), -1, line);
-	int k1 = konst(l, b, 1);
-	int lo = op2(l, b, "step", op2(l, b, "add", iv, k1, line), -1, line);
-	int okm = op2(l, b, "mul", lo, hi, line);
-	int sh = iv;
-	if (R > 1) {
+	const int n = xs.dim[xs.rank - 1], k = is.dim[is.rank - 1], R = numel(&xs) / n;
+	int inr = tree_emit(l, b, T2("mul", T1("step", T2("add", TV(iv), TK(1))), T1("step", T2("sub", TK(n), TV(iv)))), line);
+	int at = iv;
+	const Sh rk = { 2, { R, k } };
+	if (R > 1) { /* row r's indices offset by r n, over the flattened rows */
 		float *off = fa(f, (size_t)R * sizeof *off);
 		for (int r = 0; r < R; r++) off[r] = (float)r * (float)n;
-		Sh os = { 2, { R, 1 } }, is2 = { 2, { R, k } };
+		char name[64];
+		const Sh os = { 2, { R, 1 } };
 		snprintf(name, sizeof name, "__rowoff_%d_%d", R, n);
-		int ov = const_param(l, name, &os, off);
-		sh = op2(l, b, "add", reshape_to(l, b, iv, &is2), ov, line);
-		okm = reshape_to(l, b, okm, &is2);
+		const int ov = const_param(l, name, &os, off);
+		at = tree_emit(l, b, T2("add", TR(TV(iv), &rk), TV(ov)), line);
+		inr = tree_emit(l, b, TR(TV(inr), &rk), line);
 	}
-	int one = konst(l, b, 1);
-	int idx = op2(l, b, "sub", op2(l, b, "add", op2(l, b, "mul", sh, okm, line), okm, line), one, line);
-	Sh fl = { 2, { R * n, 1 } }, il = { 1, { R * k } };
-	int ri = reshape_to(l, b, idx, &il);
-	int rv = reshape_to(l, b, v, &fl);
-	int g = op2(l, b, "take", rv, ri, line);
-	return reshape_to(l, b, g, &is);
+	const int idx = tree_emit(l, b, T2("sub", T2("add", T2("mul", TV(at), TV(inr)), TV(inr)), TK(1)), line);
+	const Sh flat = { 2, { R * n, 1 } }, list = { 1, { R * k } };
+	const int g = tree_emit(l, b, T2("take", TR(TV(v), &flat), TR(TV(idx), &list)), line);
+	return tree_emit(l, b, TR(TV(g), &is), line);
 }
 
 static int lower_expr(L *l, Blk *b, Env *e, Ex *x)
@@ -1226,7 +1344,8 @@ static int lower_expr(L *l, Blk *b, Env *e, Ex *x)
 	if (x->kind == E_REF) return lookup(l, e, x->name, x->line);
 	const char *fn = x->name;
 	if (!strcmp(fn, "grad")) fail(f, l->file, x->line, "'grad' (automatic differentiation) is not part of the batch backend's front end");
-	if (!strcmp(fn, "rope") || !strcmp(fn, "attention")) return lower_attn(l, b, e, x);
+	if (!strcmp(fn, "rope")) return lower_rope(l, b, e, x);
+	if (!strcmp(fn, "attention")) return lower_attention(l, b, e, x);
 	if (!strcmp(fn, "topk") || !strcmp(fn, "memory_scan") || !strcmp(fn, "memory_final") || !strcmp(fn, "suffix_match"))
 		fail(f, l->file, x->line, "'%s' is not run by the batch backend", fn);
 	if (!strcmp(fn, "take_along")) return lower_take_along(l, b, e, x);
@@ -1267,27 +1386,7 @@ static int lower_expr(L *l, Blk *b, Env *e, Ex *x)
 		if (na != 2) fail(f, l->file, x->line, "'%s' takes (prediction, target)", fn);
 		if (!sheq(&f->val[args[0]].sh, &f->val[args[1]].sh))
 			fail(f, l->file, x->line, "'%s' prediction %s and target %s differ in shape", fn, shstr(&f->val[args[0]].sh, s0), shstr(&f->val[args[1]].sh, s1));
-		int p = args[0], t = args[1], ln = x->line;
-		if (!strcmp(fn, "mse")) {
-			int d = op2(l, b, "sub", p, t, ln);
-			return op2(l, b, "mean", op2(l, b, "mul", d, d, ln), -1, ln);
-		}
-		if (!strcmp(fn, "bce")) { /* -mean(t log(p + 1e-7) + (1 - t) log(1 - p + 1e-7)), in the reference's instruction order */
-			int lp = op2(l, b, "log", op2(l, b, "add", p, konst(l, b, 1e-7f), ln), -1, ln);
-			int e7 = konst(l, b, 1e-7f);
-			int lq = op2(l, b, "log", op2(l, b, "add", op2(l, b, "sub", konst(l, b, 1), p, ln), e7, ln), -1, ln);
-			int qt = op2(l, b, "mul", op2(l, b, "sub", konst(l, b, 1), t, ln), lq, ln);
-			int pt = op2(l, b, "mul", t, lp, ln);
-			int s = op2(l, b, "add", pt, qt, ln);
-			return op2(l, b, "neg", op2(l, b, "mean", s, -1, ln), -1, ln);
-		}
-		int rk = f->val[p].sh.rank;
-		if (rk != 1 && rk != 2) fail(f, l->file, x->line, "'xent' needs logits of shape (C) or a batch (B, C), with one-hot targets");
-		int e12 = konst(l, b, 1e-12f); /* -sum(t log(softmax(p) + 1e-12)), averaged over a batch's rows */
-		int ls = op2(l, b, "log", op2(l, b, "add", op2(l, b, "softmax", p, -1, ln), e12, ln), -1, ln);
-		int s = op2(l, b, "sum", op2(l, b, "mul", t, ls, ln), -1, ln);
-		if (rk == 2) s = op2(l, b, "div", s, konst(l, b, (float)f->val[p].sh.dim[0]), ln);
-		return op2(l, b, "neg", s, -1, ln);
+		return lower_loss(l, b, fn, args[0], args[1], x->line);
 	}
 	int op = op_of(!strcmp(fn, "dot") ? "matmul" : fn);
 	if (op < 0) fail(f, l->file, x->line, "unknown function '%s'", fn);
@@ -1590,80 +1689,111 @@ static float *materialize(L *l, const Init *in, const Sh *sh, const char *pname)
 
 /* ---------------------------------------------------------- liveness --- */
 
-static void mark(F *f, const Blk *b, char *live);
+/* What is kept: every value the output or a state update needs, closed
+ * under "is computed from". Each value has at most one definition: an
+ * instruction's output, a think loop's state (needing its init, its yield
+ * and its halting value), or a scan's carry or stack; a needed carry needs
+ * its initial and next values, a needed stack its stacked body value, and
+ * either needs all of the scan's sliced inputs. Params, states, inputs and
+ * a loop's per-step slices have no definition here. Instructions are pure:
+ * one whose value is not needed is dropped, a scan keeps its needed carries
+ * and stacks (its result becomes the first of them) and goes when none is
+ * left. */
 
-static void mark_scan(F *f, const Ins *in, char *live)
-{
-	int any = 0;
-	for (int m = 0; m < in->ny; m++)
-		if (live[in->ys[m]]) live[in->y[m]] = 1, any = 1;
-	for (int changed = 1; changed;) { /* a carry read by the live body is needed too */
-		mark(f, in->body, live);
-		changed = 0;
-		for (int k = 0; k < in->nc; k++)
-			if (live[in->c[k]] && !live[in->cnext[k]]) live[in->cnext[k]] = 1, changed = 1;
-	}
-	for (int k = 0; k < in->nc; k++)
-		if (live[in->c[k]]) live[in->cinit[k]] = 1, any = 1;
-	if (any)
-		for (int j = 0; j < in->nx; j++) live[in->x[j]] = 1;
-}
+enum { DEF_NONE, DEF_INS, DEF_CARRY, DEF_STACK };
 
-static void mark(F *f, const Blk *b, char *live)
+typedef struct {
+	char kind;
+	int idx;        /* DEF_CARRY / DEF_STACK: which carry or stack */
+	const Ins *ins; /* the defining instruction */
+} Def;
+
+static void index_defs(const Blk *b, Def *def)
 {
-	for (int i = b->len - 1; i >= 0; i--) {
+	for (int i = 0; i < b->len; i++) {
 		const Ins *in = &b->v[i];
 		if (OPS[in->op].cls == C_SCAN) {
-			mark_scan(f, in, live);
-		} else if (live[in->out]) {
-			if (OPS[in->op].cls == C_THINK) {
-				live[in->init] = live[in->yield] = 1;
-				if (in->halt >= 0) live[in->halt] = 1;
-				mark(f, in->body, live);
-			} else {
-				for (int j = 0; j < in->na; j++) live[in->a[j]] = 1;
-			}
+			for (int k = 0; k < in->nc; k++) def[in->c[k]] = (Def){ DEF_CARRY, k, in };
+			for (int m = 0; m < in->ny; m++) def[in->ys[m]] = (Def){ DEF_STACK, m, in };
+			index_defs(in->body, def);
+			continue;
 		}
+		def[in->out] = (Def){ DEF_INS, 0, in };
+		if (OPS[in->op].cls == C_THINK) index_defs(in->body, def);
 	}
 }
 
-static void sweep(F *f, Blk *b, char *live)
+typedef struct {
+	char *live;
+	int *todo, n;
+} Need;
+
+static void need(Need *w, int v)
 {
-	mark(f, b, live);
-	int k = 0;
-	for (int i = 0; i < b->len; i++) {
-		Ins *in = &b->v[i];
-		if (OPS[in->op].cls == C_SCAN) {
-			int nc = 0, ny = 0;
-			for (int c = 0; c < in->nc; c++)
-				if (live[in->c[c]]) in->c[nc] = in->c[c], in->cinit[nc] = in->cinit[c], in->cnext[nc++] = in->cnext[c];
-			for (int m = 0; m < in->ny; m++)
-				if (live[in->ys[m]]) in->y[ny] = in->y[m], in->ys[ny++] = in->ys[m];
-			in->nc = nc;
-			in->ny = ny;
-			if (!nc && !ny) continue;
-			in->out = nc ? in->c[0] : in->ys[0];
-			sweep(f, in->body, live);
-		} else {
-			if (!live[in->out]) continue;
-			if (OPS[in->op].cls == C_THINK) sweep(f, in->body, live);
+	if (v < 0 || w->live[v]) return;
+	w->live[v] = 1;
+	w->todo[w->n++] = v;
+}
+
+static void close_needs(Need *w, const Def *def)
+{
+	while (w->n) {
+		const int v = w->todo[--w->n];
+		const Def *d = &def[v];
+		const Ins *in = d->ins;
+		if (d->kind == DEF_NONE) continue;
+		if (d->kind == DEF_INS) {
+			if (OPS[in->op].cls == C_THINK) {
+				need(w, in->init);
+				need(w, in->yield);
+				need(w, in->halt);
+			} else {
+				for (int j = 0; j < in->na; j++) need(w, in->a[j]);
+			}
+			continue;
 		}
-		b->v[k++] = *in;
+		if (d->kind == DEF_CARRY) need(w, in->cinit[d->idx]), need(w, in->cnext[d->idx]);
+		else need(w, in->y[d->idx]);
+		for (int j = 0; j < in->nx; j++) need(w, in->x[j]);
 	}
-	b->len = k;
+}
+
+/* drops what is not needed from b, in place, keeping the order of the rest */
+static void drop_unneeded(Blk *b, const char *live)
+{
+	int kept = 0;
+	for (int i = 0; i < b->len; i++) {
+		Ins in = b->v[i];
+		if (OPS[in.op].cls == C_SCAN) {
+			int nc = 0, ny = 0;
+			for (int k = 0; k < in.nc; k++)
+				if (live[in.c[k]]) in.c[nc] = in.c[k], in.cinit[nc] = in.cinit[k], in.cnext[nc] = in.cnext[k], nc++;
+			for (int m = 0; m < in.ny; m++)
+				if (live[in.ys[m]]) in.y[ny] = in.y[m], in.ys[ny] = in.ys[m], ny++;
+			if (!nc && !ny) continue;
+			in.nc = nc, in.ny = ny;
+			in.out = nc ? in.c[0] : in.ys[0];
+			drop_unneeded(in.body, live);
+		} else {
+			if (!live[in.out]) continue;
+			if (OPS[in.op].cls == C_THINK) drop_unneeded(in.body, live);
+		}
+		b->v[kept++] = in;
+	}
+	b->len = kept;
 }
 
 static void dce(F *f)
 {
-	char *live = fa(f, (size_t)f->nval + 1);
-	live[f->output] = 1;
-	for (int i = 0; i < f->nupd; i++) {
-		live[f->usrc[i]] = 1;
-		if (f->urows[i] >= 0) live[f->urows[i]] = 1;
-	}
-	sweep(f, &f->top, live);
-	for (int v = 0; v < f->nval; v++)
-		if (f->val[v].kind == K_PARAM && f->val[v].name && !strncmp(f->val[v].name, "__", 2) && !live[v]) f->val[v].dead = 1;
+	Def *def = fa(f, (size_t)(f->nval + 1) * sizeof *def);
+	Need w = { fa(f, (size_t)f->nval + 1), fa(f, (size_t)(f->nval + 1) * sizeof(int)), 0 };
+	index_defs(&f->top, def);
+	need(&w, f->output);
+	for (int i = 0; i < f->nupd; i++) need(&w, f->usrc[i]), need(&w, f->urows[i]);
+	close_needs(&w, def);
+	drop_unneeded(&f->top, w.live);
+	for (int v = 0; v < f->nval; v++) /* generated constants nothing reads any more are not written */
+		if (f->val[v].kind == K_PARAM && f->val[v].name && !strncmp(f->val[v].name, "__", 2) && !w.live[v]) f->val[v].dead = 1;
 }
 
 /* -------------------------------------------------------------- text --- */
