@@ -385,7 +385,7 @@ __device__ inline void blk_digits(const float *z, int K, int Kp, float mx, int b
 	}
 	qs = blk_sum(qs, redl);
 	tl = blk_sum(tl, redl);
-	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = special || tgq_candidate(tl), q.qsum[m] = qs;
+	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = (special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID), q.qsum[m] = qs;
 }
 
 // tgk_dec_norm: one block per token row, NORM_TPB threads, each with at most
@@ -504,7 +504,7 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 		qs += tgq_put16(blk, 16 * g, v, E, special, tl);
 	}
 	for (int o = 32; o > 0; o >>= 1) qs += __shfl_xor(qs, o), tl += __shfl_xor(tl, o);
-	if (lane == 0) a.q.e[L] = E, a.q.special[L] = special || tgq_candidate(tl), a.q.qsum[L] = qs;
+	if (lane == 0) a.q.e[L] = E, a.q.special[L] = (special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID), a.q.qsum[L] = qs;
 }
 
 // Many lines at once (a prompt's token rows, or its head lines): a block of
@@ -638,7 +638,7 @@ __global__ __launch_bounds__(NL_TPB) void norm_lines_k(NormLines a)
 	for (int o = 1; o < TPL; o <<= 1) qs += __shfl_xor(qs, o), tl += __shfl_xor(tl, o);
 	if (k == 0 && L0 + l < a.lines) {
 		const long L = L0 + l;
-		a.q.e[L] = E, a.q.special[L] = special || tgq_candidate(tl), a.q.qsum[L] = qs;
+		a.q.e[L] = E, a.q.special[L] = (special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID), a.q.qsum[L] = qs;
 	}
 }
 

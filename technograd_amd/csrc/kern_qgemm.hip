@@ -181,10 +181,23 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 	}
 	qs = wave_sum(qs);
 	tl = wave_sum(tl);
+	const int cls = special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID;
 	if (lane == 0) {
 		s.e[m] = E;
-		s.special[m] = special || tgq_candidate(tl);
+		s.special[m] = cls;
 		s.qsum[m] = qs;
+	}
+	if (cls == TGQ_CAND) { // this wave wrote the row's digits (lane l its groups l + 64 j): it resolves the row
+		__shared__ TgqHist hist[4];
+		const int nout = tgq_nout(Kp);
+		auto ld = [&](int g, float *v) {
+			if (g * 16 >= K)
+				for (int i = 0; i < 16; i++) v[i] = 0.0f;
+			else if (vec) load16<true>(v, x, xk, g * 16, K);
+			else load16<false>(v, x, xk, g * 16, K);
+		};
+		tgq_resolve_row(&hist[threadIdx.x >> 6], ld, K, Kp, E, blk, &s.qsum[m], &s.e[m], &s.special[m], s.ok + (long)m * nout,
+				s.ox + (long)m * nout, nout, lane);
 	}
 }
 
@@ -232,15 +245,34 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 	}
 	sqs[w][lane] = qs;
 	stl[w][lane] = tl;
-	__syncthreads();
-	if (w == 0 && lane < 16 && m0 + mr < M) {
+	__syncthreads(); // also: every digit of the block's rows is stored
+	__shared__ int scls[16], sE[16];
+	if (w == 0 && lane < 16) {
 		long long t = 0, u2 = 0;
 		for (int u = 0; u < W; u++)
 			for (int q = 0; q < 4; q++) t += sqs[u][mr + 16 * q], u2 += stl[u][mr + 16 * q];
-		s.e[m0 + mr] = E;
-		s.special[m0 + mr] = special || tgq_candidate(u2);
-		s.qsum[m0 + mr] = t;
+		const int cls = m0 + mr >= M ? TGQ_GRID : special ? TGQ_REF : tgq_candidate(u2) ? TGQ_CAND : TGQ_GRID;
+		scls[mr] = cls, sE[mr] = E;
+		if (m0 + mr < M) s.e[m0 + mr] = E, s.special[m0 + mr] = cls, s.qsum[m0 + mr] = t;
 	}
+	__syncthreads();
+	// candidates: a wave per row (waves 0 .. RW - 1), each row read again
+	constexpr int NH = 8;
+	__shared__ TgqHist hist[NH];
+	const int RW = W < NH ? W : NH, nout = tgq_nout(Kp);
+	if (w < RW)
+		for (int r = w; r < 16; r += RW) {
+			if (scls[r] != TGQ_CAND) continue;
+			const int m = m0 + r;
+			const float *xr = xrow(a, m);
+			auto ld = [&](int g, float *v) {
+				if (g * 16 >= K)
+					for (int i = 0; i < 16; i++) v[i] = 0.0f;
+				else load16<VEC>(v, xr, a.xk, g * 16, K);
+			};
+			tgq_resolve_row(&hist[w], ld, K, Kp, sE[r], tgq_row_base(s.dig, m, Kp), &s.qsum[m], &s.e[m], &s.special[m], s.ok + (long)m * nout,
+					s.ox + (long)m * nout, nout, lane);
+		}
 }
 
 // Few, long rows: one block of 256 threads per row, thread t taking the
@@ -280,96 +312,45 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 	qs = wave_sum(qs);
 	tl = wave_sum(tl);
 	if (lane == 0) sqs[w] = qs, stl[w] = tl;
-	__syncthreads();
+	__syncthreads(); // also: every digit of the row is stored
+	const int cls = special ? TGQ_REF : tgq_candidate(stl[0] + stl[1] + stl[2] + stl[3]) ? TGQ_CAND : TGQ_GRID;
 	if (tid == 0) {
 		s.e[m] = E;
-		s.special[m] = special || tgq_candidate(stl[0] + stl[1] + stl[2] + stl[3]);
+		s.special[m] = cls;
 		s.qsum[m] = sqs[0] + sqs[1] + sqs[2] + sqs[3];
+	}
+	if (cls == TGQ_CAND && w == 0) { // wave 0 resolves the row (uniform: cls is the block's)
+		__shared__ TgqHist hist;
+		const int nout = tgq_nout(Kp);
+		auto ld = [&](int g, float *v) {
+			if (g * 16 >= K)
+				for (int i = 0; i < 16; i++) v[i] = 0.0f;
+			else load16<VEC>(v, x, a.xk, g * 16, K);
+		};
+		tgq_resolve_row(&hist, ld, K, Kp, E, blk, &s.qsum[m], &s.e[m], &s.special[m], s.ok + (long)m * nout, s.ox + (long)m * nout, nout,
+				lane);
 	}
 }
 
-// Candidate rows (tg_qdigits.h), resolved after the digits are written, at
-// every batch size: a wave per flagged row reads the row again, leaves rows
-// with a non-finite or huge entry to the reference's loop, and takes the
-// peel level of the rest from its binade histogram (tgq_resolve). Level 0:
-// the row keeps its digits (a grid row). Level L > 0, a split row: the
-// entries |x| >= 2^(E-L) become outliers kept exactly (index and value, in
-// increasing index order, at most tgq_nout(Kp)), and the other entries get a
-// grid of their own: E from their largest magnitude, their digits and sum of
-// q rewritten with the outliers as zeros. The epilogue adds sum_o
-// code[c][k_o] x_o (f64, exact products, increasing k) to the grid sum in f64
-// and rounds once. No level: the reference's loop. Grid-stride: wave v takes
-// rows 64 v .. 64 v + 63, 64 (total waves) further, and so on.
+// Candidate rows (tg_qdigits.h) of a digit area whose producer did not
+// resolve them (the decoder's fused producers): a wave per row
+// (tgq_resolve_row, the digit kernels' own resolve), rows of other classes
+// left as they are. Wave v takes rows v, v + (total waves), ...
+template <bool VEC>
 __global__ __launch_bounds__(256) void resolve_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
 {
 	__shared__ TgqHist hist[4];
-	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = gridDim.x * 4, ng = Kp / 16, nout = tgq_nout(Kp);
-	TgqHist *h = &hist[wave];
-	for (long base = (long)(blockIdx.x * 4 + wave) * 64; base < M; base += (long)nw * 64) {
-		const long mr = base + lane;
-		unsigned long long fl = __ballot(mr < M && s.special[mr] == 1);
-		while (fl) {
-			const int m = (int)(base + __builtin_ctzll(fl));
-			fl &= fl - 1;
-			const float *x = xrow(a, m);
-			unsigned mb = 0;
-			for (int g = lane; g < ng; g += 64) {
-				float v[16];
-				load16<false>(v, x, a.xk, g * 16, K);
-				tgq_scan16(v, mb);
-			}
-			float mx;
-			int bad;
-			tgq_scan_end(mb, mx, bad);
-			const float amax = wave_max(mx);
-			if (tgq_special(__any(bad), amax)) continue; // non-finite or huge: the reference's loop
-			const int E0 = tgq_exponent(amax, 0);
-			const int L = tgq_resolve(h, [&](int g, float *v) { load16<false>(v, x, a.xk, g * 16, K); }, ng, E0, lane);
-			if (L < 0) continue; // no level: the reference's loop
-			if (L == 0) { // its own grid is fine: the digits as written
-				if (lane == 0) s.special[m] = 0;
-				continue;
-			}
-			float rm = 0.0f;
-			for (int g = lane; g < ng; g += 64) {
-				float v[16];
-				load16<false>(v, x, a.xk, g * 16, K);
-				for (int i = 0; i < 16; i++)
-					if (!tgq_outlier(v[i], E0, L)) rm = fmaxf(rm, fabsf(v[i]));
-			}
-			const int E = tgq_exponent(wave_max(rm), 0);
-			int8_t *blk = tgq_row_base(s.dig, m, Kp);
-			long long qs = 0, tl = 0;
-			int nin = 0;
-			for (int g0 = 0; g0 < ng; g0 += 64) {
-				const int g = g0 + lane;
-				float v[16];
-				load16<false>(v, x, a.xk, g < ng ? g * 16 : K, K); // past the row: zeros
-				unsigned om = 0;
-				for (int i = 0; i < 16; i++)
-					if (tgq_outlier(v[i], E0, L)) om |= 1u << i;
-				float r[16];
-				for (int i = 0; i < 16; i++) r[i] = (om >> i) & 1 ? 0.0f : v[i];
-				if (g < ng) qs += tgq_put16(blk, g * 16, r, E, g * 16 >= K, tl);
-				// the outliers in input order: an exclusive scan of the lanes' counts
-				const int cnt = __popc(om);
-				int inc = cnt;
-				for (int d = 1; d < 64; d <<= 1) {
-					const int t = __shfl_up(inc, d);
-					if (lane >= d) inc += t;
-				}
-				int at = nin + inc - cnt;
-				for (int i = 0; i < 16; i++)
-					if ((om >> i) & 1) {
-						if (at < nout) s.ok[(long)m * nout + at] = g * 16 + i, s.ox[(long)m * nout + at] = v[i];
-						at++;
-					}
-				nin += __shfl(inc, 63);
-			}
-			qs = wave_sum(qs);
-			for (int j = nin + lane; j < nout; j += 64) s.ok[(long)m * nout + j] = -1;
-			if (lane == 0) s.e[m] = E, s.qsum[m] = qs, s.special[m] = 2;
-		}
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nout = tgq_nout(Kp);
+	for (long m = (long)blockIdx.x * 4 + wave; m < M; m += (long)gridDim.x * 4) {
+		if (s.special[m] != TGQ_CAND) continue; // one word for the whole wave
+		const float *x = xrow(a, (int)m);
+		auto ld = [&](int g, float *v) {
+			if (g * 16 >= K)
+				for (int i = 0; i < 16; i++) v[i] = 0.0f;
+			else load16<VEC>(v, x, a.xk, g * 16, K);
+		};
+		tgq_resolve_row(&hist[wave], ld, K, Kp, s.e[m], tgq_row_base(s.dig, (int)m, Kp), &s.qsum[m], &s.e[m], &s.special[m],
+				s.ok + m * nout, s.ox + m * nout, nout, lane);
 	}
 }
 
@@ -542,7 +523,7 @@ __device__ inline void epilogue_with(const tgk_qgemm_args &a, const tgk_qweight 
 {
 	if (m >= a.M || c >= w.C) return;
 	float acc32;
-	if (special == 1) { // the reference's sequential loop
+	if (special & 1) { // the reference's sequential loop (TGQ_REF, or a candidate no resolve has seen)
 		acc32 = ref_loop(a, w, m, c);
 	} else {
 		if (w.bits == 4) tot -= 8 * qsum;
@@ -617,11 +598,11 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 			const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
 			const int E = __shfl(Er, rv), sp = __shfl(spr, rv);
 			const long long Q = __shfl(Qr, rv);
-			if (sp != 1)
+			if (!(sp & 1))
 				for (int j = 0; j < NB; j++) // a pair's odd block has no +8 bias to remove: add it for epilogue_with
 					epilogue_with<ACT>(a, w, s, m, cbase + j * 32 + r32, tot(j, v) + (PAIRS && (j & 1) ? 8 * Q : 0), E, sp, Q);
 		}
-		unsigned long long sm = __ballot(spr == 1) & 0xffffffffull; // lane r (r < 32): row mbase + r
+		unsigned long long sm = __ballot(spr & 1) & 0xffffffffull; // lane r (r < 32): row mbase + r
 		while (sm) {
 			const int rv = __builtin_ctzll(sm);
 			sm &= sm - 1;
@@ -736,7 +717,7 @@ __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 		}
 	}
 	// a wave takes lines wave, wave + 8, ... (16 of them), 64 channels at a time
-	const int spl = lane < 16 && wave + 8 * lane < nl ? s.special[m0 + wave + 8 * lane] == 1 : 0;
+	const int spl = lane < 16 && wave + 8 * lane < nl ? s.special[m0 + wave + 8 * lane] & 1 : 0;
 	__syncthreads();
 	if (__any(spl)) // lines of the reference's loop: their products, a wave per line
 		for (int i = 0; i < 16; i++)
@@ -1282,7 +1263,7 @@ __device__ int fused_resolve(const tgk_qweight &w, const Scratch &s, const float
 {
 	static_assert(GX <= 2, "outlier order below: two groups per thread");
 	const int K = w.K;
-	if (tid < 64) F.h.cnt[tid] = 0, F.h.mass[tid] = 0;
+	if (tid < 64) F.h.cnt[tid] = 0, F.h.bmax[tid] = 0, F.h.mass[tid] = 0;
 	__syncthreads();
 	for (int u = 0; u < GX; u++)
 		if (16 * (tid + 256 * u) < K) (void)tgq_hist16(&F.h, v[u], E);
@@ -1795,7 +1776,7 @@ size_t tgk_qgemm_scratch(int M, int Kp)
 tgk_qdig tgk_qgemm_digit_area(void *scratch, int M, int Kp)
 {
 	const Scratch s = carve(scratch, (int)round_up(M, BM), Kp);
-	return tgk_qdig{ s.dig, s.qsum, s.e, s.special };
+	return tgk_qdig{ s.dig, s.qsum, s.e, s.special, s.ok, s.ox };
 }
 
 void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
@@ -1842,7 +1823,6 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 		digits_k<1><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
 	else
 		digits_k<4><<<(M + 3) / 4, 256, 0, st>>>(*a, s, K, w->Kp, M);
-	tgk_qgemm_split(st, a, scratch);
 }
 
 void tgk_qgemm_split(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
@@ -1851,8 +1831,11 @@ void tgk_qgemm_split(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 	const int M = a->M;
 	if (!w || !a->x || !scratch || M <= 0 || a->ni <= 0 || w->K <= 0) return;
 	const Scratch s = carve(scratch, (int)round_up(M, BM), w->Kp);
-	const long waves = (M + 63) / 64;
-	resolve_k<<<(unsigned)(waves / 4 < 1024 ? (waves + 3) / 4 : 1024), 256, 0, st>>>(*a, s, w->K, w->Kp, M);
+	const long blocks = (M + 3) / 4;
+	const unsigned nb = (unsigned)(blocks < 16384 ? blocks : 16384);
+	const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) && (w->K & 15) == 0;
+	if (vec) resolve_k<true><<<nb, 256, 0, st>>>(*a, s, w->K, w->Kp, M);
+	else resolve_k<false><<<nb, 256, 0, st>>>(*a, s, w->K, w->Kp, M);
 }
 
 int tgk_qgemm_mfma(hipStream_t st, const tgk_qgemm_args *a, void *scratch)

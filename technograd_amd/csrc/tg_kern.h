@@ -14,11 +14,16 @@ typedef struct {
 } tgk_opd;
 
 /* a GEMM's activation-digit area: digits in fragment order, and per row the
- * sum of its fixed-point values, its exponent and its special flag */
+ * sum of its fixed-point values, its exponent, its class (tg_qdigits.h:
+ * TGQ_GRID, TGQ_REF, TGQ_SPLIT, or TGQ_CAND before a resolve) and a split
+ * row's outliers (ok: input index, -1 after the last; ox: value; nout per
+ * row, tgq_nout(Kp)) */
 typedef struct {
 	int8_t *dig;
 	long long *qsum;
 	int *e, *special;
+	int *ok;
+	float *ox;
 } tgk_qdig;
 
 /* ---- layer executor kernels (kern_layer.hip) ---- */

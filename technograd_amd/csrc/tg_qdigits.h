@@ -51,6 +51,11 @@ __device__ inline void tgq_split3(int q, int &d0, int &d1, int &d2)
 // a row is special when an entry is not finite (bad) or max |x| exceeds 2^100
 __device__ inline int tgq_special(int bad, float amax) { return bad || amax > 0x1p100f; }
 
+// A row's class in a digit area's special flags. Consumers take the
+// reference's loop for any odd flag, so a candidate that no resolve has seen
+// still gets an exact result.
+enum { TGQ_GRID = 0, TGQ_REF = 1, TGQ_SPLIT = 2, TGQ_CAND = 3 };
+
 // The candidate tally: sum |q| in bits 0..43 (|q| <= 2^23, at most 2^19
 // inputs) plus the count of inexact entries from bit 44.
 constexpr int TGQ_TALLY_SHIFT = 44;
@@ -206,6 +211,7 @@ __device__ inline void tgq_wave_sync()
 // sums: P[L] entries, PM[L] mass in bins below L.
 struct TgqHist {
 	unsigned cnt[64];
+	unsigned bmax[64]; // the bin's largest |x| (as bits: non-negative floats order as their bits)
 	unsigned long long mass[64];
 	unsigned P[65];
 	unsigned long long PM[65];
@@ -234,6 +240,7 @@ __device__ inline int tgq_hist16(TgqHist *h, const float *v, int E)
 		nx += rintf(sv) != sv;
 		const int d = tgq_bin(ax, E);
 		atomicAdd(&h->cnt[d], 1u);
+		atomicMax(&h->bmax[d], __float_as_uint(ax));
 		atomicAdd(&h->mass[d], (unsigned long long)ldexpf(ax, TGQ_MASS_SHIFT - E)); // truncation: the floor
 	}
 	return nx;
@@ -304,6 +311,7 @@ template <class Ld>
 __device__ inline int tgq_resolve(TgqHist *h, Ld ld, int ng, int E, int lane)
 {
 	h->cnt[lane] = 0;
+	h->bmax[lane] = 0;
 	h->mass[lane] = 0;
 	tgq_wave_sync();
 	int nx = 0;
@@ -314,4 +322,59 @@ __device__ inline int tgq_resolve(TgqHist *h, Ld ld, int ng, int E, int lane)
 	}
 	tgq_wave_sync();
 	return tgq_decide(h, tgq_wave_sum(nx), lane);
+}
+
+// Resolves candidate row m of a digit area in place (a whole wave; h this
+// wave's own, in LDS): ld(g, v) loads the row's 16-input group g (zeros past
+// K), E0 is the row's grid exponent, blk its first fragment byte (tgq_row_base).
+// The row keeps its digits (TGQ_GRID), takes the reference's loop (TGQ_REF),
+// or is split (TGQ_SPLIT): its rest's digits, exponent and sum of q are
+// rewritten and its outliers (input index and value, increasing index, -1
+// after the last) go to ok / ox [nout]. The rest's exponent comes from the
+// largest |x| of its top bin, so the row is read once, or twice when split.
+template <class Ld>
+__device__ inline void tgq_resolve_row(TgqHist *h, Ld ld, int K, int Kp, int E0, int8_t *blk, long long *qsum, int *e, int *special,
+				       int *ok, float *ox, int nout, int lane)
+{
+	const int ng = Kp / 16;
+	const int L = tgq_resolve(h, ld, ng, E0, lane);
+	if (L <= 0) {
+		if (lane == 0) *special = L < 0 ? TGQ_REF : TGQ_GRID;
+		return;
+	}
+	const unsigned long long restb = __ballot(lane >= L && h->cnt[lane] != 0);
+	const float rmax = restb ? __uint_as_float(h->bmax[__builtin_ctzll(restb)]) : 0.0f;
+	const int E = tgq_exponent(rmax, 0);
+	long long qs = 0, tl = 0;
+	int nin = 0;
+	for (int g0 = 0; g0 < ng; g0 += 64) {
+		const int g = g0 + lane;
+		float v[16];
+		if (g < ng) ld(g, v);
+		else
+			for (int i = 0; i < 16; i++) v[i] = 0.0f;
+		unsigned om = 0;
+		for (int i = 0; i < 16; i++)
+			if (tgq_outlier(v[i], E0, L)) om |= 1u << i;
+		float r[16];
+		for (int i = 0; i < 16; i++) r[i] = (om >> i) & 1 ? 0.0f : v[i];
+		if (g < ng) qs += tgq_put16(blk, g * 16, r, E, g * 16 >= K, tl);
+		// the outliers in input order: an exclusive scan of the lanes' counts
+		const int cnt = __popc(om);
+		int inc = cnt;
+		for (int d = 1; d < 64; d <<= 1) {
+			const int t = __shfl_up(inc, d);
+			if (lane >= d) inc += t;
+		}
+		int at = nin + inc - cnt;
+		for (int i = 0; i < 16; i++)
+			if ((om >> i) & 1) {
+				if (at < nout) ok[at] = g * 16 + i, ox[at] = v[i];
+				at++;
+			}
+		nin += __shfl(inc, 63);
+	}
+	for (int o = 32; o > 0; o >>= 1) qs += __shfl_xor(qs, o);
+	for (int j = nin + lane; j < nout; j += 64) ok[j] = -1;
+	if (lane == 0) *e = E, *qsum = qs, *special = TGQ_SPLIT;
 }

@@ -152,10 +152,17 @@ static void *batcher_main(void *arg)
 	return NULL;
 }
 
-/* queue one request and wait for its batch; nonzero if the device call failed */
+/* queue one request and wait for its batch; nonzero if the device call
+ * failed, or if the batcher is stopping (requests queued before the stop
+ * still run) */
 static int submit(Batcher *B, Req *r)
 {
 	pthread_mutex_lock(&B->mu);
+	if (B->quit) {
+		snprintf(B->err, sizeof B->err, "the server is stopping");
+		pthread_mutex_unlock(&B->mu);
+		return 1;
+	}
 	r->next = NULL;
 	r->done = r->failed = 0;
 	if (B->tail) B->tail->next = r;
@@ -203,7 +210,10 @@ static void batcher_stop(Batcher *B)
 	pthread_cond_signal(&B->work);
 	pthread_mutex_unlock(&B->mu);
 	pthread_join(B->th, NULL);
+	pthread_mutex_lock(&B->mu);
 	tg_hip_free(B->p);
+	B->p = NULL;
+	pthread_mutex_unlock(&B->mu);
 	free(B->in);
 	free(B->out);
 	free(B->steps);
@@ -296,8 +306,11 @@ done:
 
 /* ---------------------------------------------------------- line input --- */
 
+/* the longest line (row, request or header line) a connection may send */
+#define LR_MAX_LINE ((size_t)64 << 20)
+
 typedef struct {
-	int fd, eof;
+	int fd, eof, overflow; /* overflow: a line longer than LR_MAX_LINE arrived (its bytes are dropped, input ends) */
 	char *buf;
 	size_t cap, beg, end;
 } LR;
@@ -321,8 +334,13 @@ static int lr_fill(LR *r, int block)
 			r->end -= r->beg;
 			r->beg = 0;
 		} else {
-			char *nb = realloc(r->buf, 2 * r->cap + 1);
-			if (!nb) return 0;
+			char *nb = r->cap < LR_MAX_LINE ? realloc(r->buf, 2 * r->cap + 1) : NULL;
+			if (!nb) { /* too long a line (or no memory for it): drop what is buffered and end the input */
+				r->overflow = 1;
+				r->eof = 1;
+				r->beg = r->end = 0;
+				return 0;
+			}
 			r->buf = nb;
 			r->cap *= 2;
 		}
@@ -400,6 +418,7 @@ static long row_session(Batcher *B, LR *in, FILE *out, char *first)
 		if (fflush(out) || stop_signal()) break; /* the peer is gone, or a stop */
 		rc = lr_line(in, &line, 1);
 	}
+	if (in->overflow) fprintf(out, "error: line longer than %zu bytes; closing the connection\n", LR_MAX_LINE);
 	free(lines);
 	return count;
 }
@@ -523,94 +542,184 @@ int stream_main(int argc, char **argv)
 
 /* -------------------------------------------------------------- serve --- */
 
-static void http_reply(FILE *o, int code, const char *reason, const char *type, const char *body, size_t len)
+/* One HTTP/1.1 exchange per connection: the request head (its first line
+ * already read), an optional body, one response, then the connection closes.
+ * The routes, status lines, headers and bodies are the reference's wire
+ * format (src/serve.c): GET /health, GET / (the signature as JSON),
+ * POST /run (body rows in, output rows out), 404 for anything else, 400 for
+ * a request line without a path, 413 for a body over 64 MiB. */
+
+#define HTTP_MAX_BODY (64L << 20)
+
+typedef struct {
+	char method[8], path[256]; /* the request line's first two words (at most 7 and 255 bytes) */
+	long length;               /* Content-Length (0 when absent) */
+} HttpHead;
+
+typedef struct {
+	int status;
+	const char *reason, *type;
+	FILE *body; /* the response body, gathered before the head is written */
+} HttpReply;
+
+/* the first whitespace-separated word of s (at most cap - 1 bytes) into w; the rest after it */
+static const char *word_of(const char *s, char *w, size_t cap)
 {
-	fprintf(o, "HTTP/1.1 %d %s\r\nContent-Type: %s\r\nContent-Length: %zu\r\nConnection: close\r\n\r\n", code, reason, type, len);
+	while (*s == ' ' || *s == '\t') s++;
+	size_t n = 0;
+	while (*s && *s != ' ' && *s != '\t' && *s != '\r' && *s != '\n') {
+		if (n + 1 < cap) w[n++] = *s;
+		s++;
+	}
+	w[n] = 0;
+	return s;
+}
+
+static int http_head(LR *in, const char *request_line, HttpHead *h)
+{
+	memset(h, 0, sizeof *h);
+	const char *rest = word_of(request_line, h->method, sizeof h->method);
+	word_of(rest, h->path, sizeof h->path);
+	char *line;
+	while (lr_line(in, &line, 1) == 1 && *line) /* header lines up to the blank line */
+		if (!strncasecmp(line, "content-length:", 15)) h->length = strtol(line + 15, NULL, 10);
+	return h->method[0] && h->path[0];
+}
+
+static void http_send(FILE *o, const HttpReply *r, const char *body, size_t len)
+{
+	fprintf(o, "HTTP/1.1 %d %s\r\nContent-Type: %s\r\nContent-Length: %zu\r\nConnection: close\r\n\r\n", r->status, r->reason, r->type, len);
 	fwrite(body, 1, len, o);
 }
 
-static long http(Batcher *B, LR *in, FILE *o, const char *req)
+static long route_health(Batcher *B, LR *in, const HttpHead *h, HttpReply *r)
 {
-	long rows = 0;
-	char method[8] = "", path[256] = "";
-	if (sscanf(req, "%7s %255s", method, path) != 2) {
-		http_reply(o, 400, "Bad Request", "text/plain", "bad request\n", 12);
+	(void)B, (void)in, (void)h;
+	fputs("ok\n", r->body);
+	return 0;
+}
+
+static long route_signature(Batcher *B, LR *in, const HttpHead *h, HttpReply *r)
+{
+	(void)in, (void)h;
+	char sig[8192];
+	r->type = "application/json";
+	pthread_mutex_lock(&B->mu); /* the program stays loaded until batcher_stop, which takes this lock to free it */
+	const int have = !B->quit && tg_hip_signature(B->p, sig, sizeof sig) > 0;
+	pthread_mutex_unlock(&B->mu);
+	if (have) fputs(sig, r->body);
+	return 0;
+}
+
+/* exactly n bytes of body: what the line reader holds, then the socket */
+static size_t read_body(LR *in, char *dst, size_t n)
+{
+	size_t got = 0;
+	while (got < n) {
+		if (in->end > in->beg) {
+			size_t k = in->end - in->beg;
+			if (k > n - got) k = n - got;
+			memcpy(dst + got, in->buf + in->beg, k);
+			in->beg += k, got += k;
+		} else if (lr_fill(in, 1) <= 0) {
+			break;
+		}
+	}
+	return got;
+}
+
+static long route_run(Batcher *B, LR *in, const HttpHead *h, HttpReply *r)
+{
+	if (h->length < 0 || h->length > HTTP_MAX_BODY) {
+		r->status = 413, r->reason = "Payload Too Large";
+		fputs("body too large\n", r->body);
 		return 0;
 	}
-	char *line;
-	long clen = 0;
-	while (lr_line(in, &line, 1) == 1 && *line)
-		if (!strncasecmp(line, "content-length:", 15)) clen = strtol(line + 15, NULL, 10);
-	char *body = NULL;
-	size_t blen = 0;
-	FILE *mo = open_memstream(&body, &blen);
-	if (!mo) return 0;
-	int code = 200;
-	const char *reason = "OK", *type = "text/plain";
-	if (!strcmp(method, "GET") && !strcmp(path, "/health")) {
-		fputs("ok\n", mo);
-	} else if (!strcmp(method, "GET") && !strcmp(path, "/")) {
-		char sig[8192];
-		type = "application/json";
-		if (tg_hip_signature(B->p, sig, sizeof sig) > 0) fputs(sig, mo);
-	} else if (!strcmp(method, "POST") && !strcmp(path, "/run")) {
-		if (clen < 0 || clen > (64L << 20)) {
-			code = 413;
-			reason = "Payload Too Large";
-			fputs("body too large\n", mo);
-		} else {
-			char *rb = malloc((size_t)clen + 1);
-			size_t got = 0;
-			while (rb && got < (size_t)clen) { /* what the line reader holds, then the socket */
-				if (in->end > in->beg) {
-					size_t k = in->end - in->beg < (size_t)clen - got ? in->end - in->beg : (size_t)clen - got;
-					memcpy(rb + got, in->buf + in->beg, k);
-					in->beg += k;
-					got += k;
-				} else if (lr_fill(in, 1) <= 0) {
-					break;
-				}
-			}
-			if (rb) {
-				rb[got] = 0;
-				int n = 0, cap = 64;
-				char **lines = malloc((size_t)cap * sizeof *lines);
-				for (char *s = rb; lines && *s;) {
-					char *nl = strchr(s, '\n');
-					if (nl) *nl = 0;
-					if (n == cap) {
-						char **nb = realloc(lines, (size_t)(cap *= 2) * sizeof *lines);
-						if (!nb) break;
-						lines = nb;
-					}
-					lines[n++] = s;
-					if (!nl) break;
-					s = nl + 1;
-				}
-				if (lines) rows += run_lines(B, lines, n, mo);
-				free(lines);
-				free(rb);
-			}
+	char *text = malloc((size_t)h->length + 1);
+	if (!text) return 0;
+	text[read_body(in, text, (size_t)h->length)] = 0;
+	long nl = 1;
+	for (const char *c = text; *c; c++) nl += *c == '\n';
+	char **lines = malloc((size_t)nl * sizeof *lines);
+	long rows = 0;
+	if (lines) {
+		int n = 0;
+		for (char *c = text; *c;) { /* the body's lines, '\n'-terminated or not */
+			lines[n++] = c;
+			char *e = strchr(c, '\n');
+			if (!e) break;
+			*e = 0;
+			c = e + 1;
 		}
-	} else {
-		code = 404;
-		reason = "Not Found";
-		fputs("not found: GET /health, GET /, POST /run\n", mo);
+		rows = run_lines(B, lines, n, r->body);
+		free(lines);
 	}
-	fclose(mo);
-	http_reply(o, code, reason, type, body, blen);
+	free(text);
+	return rows;
+}
+
+static const struct {
+	const char *method, *path;
+	long (*route)(Batcher *B, LR *in, const HttpHead *h, HttpReply *r);
+} ROUTES[] = {
+	{ "GET", "/health", route_health },
+	{ "GET", "/", route_signature },
+	{ "POST", "/run", route_run },
+};
+
+static long http_exchange(Batcher *B, LR *in, FILE *o, const char *request_line)
+{
+	HttpHead h;
+	if (!http_head(in, request_line, &h)) {
+		const HttpReply bad = { 400, "Bad Request", "text/plain", NULL };
+		http_send(o, &bad, "bad request\n", 12);
+		return 0;
+	}
+	char *body = NULL;
+	size_t len = 0;
+	HttpReply r = { 200, "OK", "text/plain", open_memstream(&body, &len) };
+	if (!r.body) return 0;
+	long rows = 0;
+	size_t i = 0;
+	for (; i < sizeof ROUTES / sizeof ROUTES[0]; i++)
+		if (!strcmp(h.method, ROUTES[i].method) && !strcmp(h.path, ROUTES[i].path)) {
+			rows = ROUTES[i].route(B, in, &h, &r);
+			break;
+		}
+	if (i == sizeof ROUTES / sizeof ROUTES[0]) {
+		r.status = 404, r.reason = "Not Found";
+		fputs("not found: GET /health, GET /, POST /run\n", r.body);
+	}
+	if (in->overflow) { /* a header line over the limit: nothing of the request is trusted */
+		fclose(r.body);
+		free(body);
+		const HttpReply big = { 431, "Request Header Fields Too Large", "text/plain", NULL };
+		http_send(o, &big, "header line too long\n", 21);
+		return 0;
+	}
+	fclose(r.body);
+	http_send(o, &r, body, len);
 	free(body);
 	return rows;
 }
 
+/* ------------------------------------------------------------ server --- */
+
+/* connections served at once; more wait in the listen backlog */
+#define SERVE_MAX_CONNS 256
+
 typedef struct {
 	Batcher *B;
+	pthread_mutex_t mu;
+	int active;      /* connection threads running */
+	long rows;       /* rows answered by finished connections */
+	long accepted;
+} Server;
+
+typedef struct {
+	Server *S;
 	int fd;
 } Conn;
-
-static pthread_mutex_t conn_mu = PTHREAD_MUTEX_INITIALIZER;
-static int active;
-static long served;
 
 static void *conn_main(void *arg)
 {
@@ -619,25 +728,99 @@ static void *conn_main(void *arg)
 	FILE *out = fdopen(dup(c.fd), "w");
 	LR in;
 	lr_init(&in, c.fd);
-	char *line;
+	char *first;
 	long rows = 0;
-	if (out && lr_line(&in, &line, 1) == 1) {
-		if (!strncmp(line, "GET ", 4) || !strncmp(line, "POST ", 5)) {
-			char req[512];
-			snprintf(req, sizeof req, "%s", line);
-			rows += http(c.B, &in, out, req);
+	if (out && lr_line(&in, &first, 1) == 1) {
+		if (!strncmp(first, "GET ", 4) || !strncmp(first, "POST ", 5)) { /* HTTP, chosen by the first line */
+			char *line = strdup(first);
+			if (line) rows = http_exchange(c.S->B, &in, out, line);
+			free(line);
 		} else {
-			rows += row_session(c.B, &in, out, line);
+			rows = row_session(c.S->B, &in, out, first);
 		}
+	} else if (out && in.overflow) {
+		fprintf(out, "error: line longer than %zu bytes; closing the connection\n", LR_MAX_LINE);
 	}
 	if (out) fclose(out);
+	if (in.overflow) { /* the peer may still be sending: half-close, then read and drop for up to two seconds, so
+			    * the close does not reset the connection before the peer has read our answer */
+		shutdown(c.fd, SHUT_WR);
+		char sink[1 << 14];
+		for (int t = 0; t < 20; t++) {
+			struct pollfd pf = { c.fd, POLLIN, 0 };
+			if (poll(&pf, 1, 100) > 0 && read(c.fd, sink, sizeof sink) <= 0) break;
+		}
+	}
 	free(in.buf);
 	close(c.fd);
-	pthread_mutex_lock(&conn_mu);
-	active--;
-	served += rows;
-	pthread_mutex_unlock(&conn_mu);
+	pthread_mutex_lock(&c.S->mu);
+	c.S->active--;
+	c.S->rows += rows;
+	pthread_mutex_unlock(&c.S->mu);
 	return NULL;
+}
+
+static int server_active(Server *S)
+{
+	pthread_mutex_lock(&S->mu);
+	const int a = S->active;
+	pthread_mutex_unlock(&S->mu);
+	return a;
+}
+
+/* a detached thread for connection fd (signals stay with the caller's thread) */
+static void server_spawn(Server *S, int fd)
+{
+	Conn *c = malloc(sizeof *c);
+	if (!c) {
+		close(fd);
+		return;
+	}
+	*c = (Conn){ S, fd };
+	pthread_mutex_lock(&S->mu);
+	S->active++;
+	S->accepted++;
+	pthread_mutex_unlock(&S->mu);
+	sigset_t stop, old;
+	sigemptyset(&stop);
+	sigaddset(&stop, SIGINT);
+	sigaddset(&stop, SIGTERM);
+	pthread_attr_t at;
+	pthread_attr_init(&at);
+	pthread_attr_setdetachstate(&at, PTHREAD_CREATE_DETACHED);
+	pthread_sigmask(SIG_BLOCK, &stop, &old);
+	pthread_t th;
+	const int rc = pthread_create(&th, &at, conn_main, c);
+	pthread_sigmask(SIG_SETMASK, &old, NULL);
+	pthread_attr_destroy(&at);
+	if (rc) {
+		close(fd);
+		free(c);
+		pthread_mutex_lock(&S->mu);
+		S->active--;
+		pthread_mutex_unlock(&S->mu);
+	}
+}
+
+/* the bound address of a listening socket as HOST:PORT (port 0 picks one) */
+static void bound_name(int fd, char *where, size_t n)
+{
+	struct sockaddr_storage sa;
+	socklen_t sl = sizeof sa;
+	char h[INET6_ADDRSTRLEN] = "?";
+	int port = 0;
+	if (getsockname(fd, (struct sockaddr *)&sa, &sl)) {
+		snprintf(where, n, "?");
+		return;
+	}
+	if (sa.ss_family == AF_INET) {
+		inet_ntop(AF_INET, &((struct sockaddr_in *)&sa)->sin_addr, h, sizeof h);
+		port = ntohs(((struct sockaddr_in *)&sa)->sin_port);
+	} else if (sa.ss_family == AF_INET6) {
+		inet_ntop(AF_INET6, &((struct sockaddr_in6 *)&sa)->sin6_addr, h, sizeof h);
+		port = ntohs(((struct sockaddr_in6 *)&sa)->sin6_port);
+	}
+	snprintf(where, n, "%s:%d", h, port);
 }
 
 int serve_main(int argc, char **argv)
@@ -657,82 +840,41 @@ int serve_main(int argc, char **argv)
 		return die("usage: tgc-hip serve MODEL --listen [HOST:]PORT [--fixed] [--exact] [--rows N] [--window-us U]%s", "");
 	install_signals();
 	char err[512];
-	int lfd = tcp_open(listen_spec, 1, err, sizeof err);
+	const int lfd = tcp_open(listen_spec, 1, err, sizeof err);
 	if (lfd < 0) return die("%s", err);
 	Batcher B;
 	if (batcher_start(&B, model, flags, rows, window)) return 1;
-	struct sockaddr_storage sa;
-	socklen_t sl = sizeof sa;
-	char where[300] = "";
-	if (!getsockname(lfd, (struct sockaddr *)&sa, &sl)) { /* the bound address (port 0 picks one) */
-		char h[INET6_ADDRSTRLEN] = "?";
-		int port = 0;
-		if (sa.ss_family == AF_INET) {
-			inet_ntop(AF_INET, &((struct sockaddr_in *)&sa)->sin_addr, h, sizeof h);
-			port = ntohs(((struct sockaddr_in *)&sa)->sin_port);
-		} else if (sa.ss_family == AF_INET6) {
-			inet_ntop(AF_INET6, &((struct sockaddr_in6 *)&sa)->sin6_addr, h, sizeof h);
-			port = ntohs(((struct sockaddr_in6 *)&sa)->sin6_port);
-		}
-		snprintf(where, sizeof where, "%s:%d", h, port);
-	}
+	Server S = { &B, PTHREAD_MUTEX_INITIALIZER, 0, 0, 0 };
+	char where[300];
+	bound_name(lfd, where, sizeof where);
 	fprintf(stderr, "serve: model %s on %s (%d values per row, device batches of up to %d rows); stop with SIGINT or SIGTERM\n", B.name,
 		where, B.per, rows);
-	long conns = 0;
-	sigset_t block, old;
-	sigemptyset(&block);
-	sigaddset(&block, SIGINT);
-	sigaddset(&block, SIGTERM);
 	while (!stop_signal()) {
-		struct pollfd pf = { lfd, POLLIN, 0 };
-		if (poll(&pf, 1, 500) <= 0) continue;
-		int fd = accept(lfd, NULL, NULL);
-		if (fd < 0) continue;
-		Conn *c = malloc(sizeof *c);
-		if (!c) {
-			close(fd);
+		if (server_active(&S) >= SERVE_MAX_CONNS) { /* full: leave new clients in the backlog for a moment */
+			const struct timespec ts = { 0, 10000000 };
+			nanosleep(&ts, NULL);
 			continue;
 		}
-		c->B = &B;
-		c->fd = fd;
-		pthread_mutex_lock(&conn_mu);
-		active++;
-		pthread_mutex_unlock(&conn_mu);
-		pthread_t th;
-		pthread_attr_t at;
-		pthread_attr_init(&at);
-		pthread_attr_setdetachstate(&at, PTHREAD_CREATE_DETACHED);
-		pthread_sigmask(SIG_BLOCK, &block, &old); /* signals stay with this thread */
-		int rc = pthread_create(&th, &at, conn_main, c);
-		pthread_sigmask(SIG_SETMASK, &old, NULL);
-		pthread_attr_destroy(&at);
-		if (rc) {
-			close(fd);
-			free(c);
-			pthread_mutex_lock(&conn_mu);
-			active--;
-			pthread_mutex_unlock(&conn_mu);
-		}
-		conns++;
+		struct pollfd pf = { lfd, POLLIN, 0 };
+		if (poll(&pf, 1, 500) <= 0) continue;
+		const int fd = accept(lfd, NULL, NULL);
+		if (fd >= 0) server_spawn(&S, fd);
 	}
 	close(lfd);
-	for (int i = 0; i < 50; i++) { /* let open connections finish their rows */
-		pthread_mutex_lock(&conn_mu);
-		int a = active;
-		pthread_mutex_unlock(&conn_mu);
-		if (!a) break;
-		struct timespec ts = { 0, 100000000 };
+	for (int i = 0; i < 50 && server_active(&S); i++) { /* let open connections finish their rows */
+		const struct timespec ts = { 0, 100000000 };
 		nanosleep(&ts, NULL);
 	}
-	pthread_mutex_lock(&conn_mu);
-	int still = active;
-	long rows_served = served;
-	pthread_mutex_unlock(&conn_mu);
+	/* the batcher finishes what is queued and stops; a connection still open
+	 * gets an error for anything it sends from now on */
 	pthread_mutex_lock(&B.mu);
-	long batches = B.batches;
+	const long batches = B.batches;
 	pthread_mutex_unlock(&B.mu);
-	if (!still) batcher_stop(&B); /* connections still open keep the device program */
+	batcher_stop(&B);
+	pthread_mutex_lock(&S.mu);
+	const long conns = S.accepted, served = S.rows;
+	pthread_mutex_unlock(&S.mu);
 	fprintf(stderr, "serve: stopped by signal %d after %ld connection(s), %ld row(s) in %ld device batch(es)\n", stop_signal(), conns,
-		rows_served, batches);
+		served, batches);
 	return 128 + stop_signal();
 }

@@ -171,3 +171,51 @@ def test_stream_file_and_pipe(tmp_path):
     print("case stream pipe", flush=True)
     r = subprocess.run([CLI, "stream", model, "--exact"], input=c["send"], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout == c["recv"], r.stderr
+
+
+def test_overlong_lines_and_a_stop_with_a_connection_open():
+    """A row line and an HTTP header line longer than 64 MiB end their
+    connection with an error (the server does not grow its buffer past
+    that), while other connections are served; SIGTERM with a client still
+    connected stops the server cleanly (the batcher drained and joined) with
+    status 128 + SIGTERM."""
+    big = b"1," * (33 << 20) + b"1"  # 66 MiB, no line end
+    with server("odd_q4", "--exact") as (p, port):
+        s = socket.create_connection(("127.0.0.1", port), timeout=60)
+        try:
+            s.sendall(big)
+        except OSError:
+            pass  # the server may close the connection while we still send
+        got = b""
+        try:
+            while True:
+                k = s.recv(1 << 16)
+                if not k:
+                    break
+                got += k
+        except OSError:
+            pass
+        s.close()
+        assert got.startswith(b"error: line longer than"), got[:200]
+        h = socket.create_connection(("127.0.0.1", port), timeout=60)
+        try:
+            h.sendall(b"GET /health HTTP/1.1\r\nX-Big: " + big + b"\r\n\r\n")
+        except OSError:
+            pass
+        reply = b""
+        try:
+            while True:
+                k = h.recv(1 << 16)
+                if not k:
+                    break
+                reply += k
+        except OSError:
+            pass
+        h.close()
+        assert reply.startswith(b"HTTP/1.1 431 "), reply[:200]
+        assert converse(port, SERVE["odd_q4"]["health"]["send"]) == SERVE["odd_q4"]["health"]["recv"]
+        idle = socket.create_connection(("127.0.0.1", port), timeout=60)  # stays open through the stop
+        p.send_signal(signal.SIGTERM)
+        rc = p.wait(timeout=60)
+        idle.close()
+    assert rc == 128 + signal.SIGTERM
