@@ -52,6 +52,7 @@
 #include <signal.h>
 #include <stdatomic.h>
 #include <stdint.h>
+#include <ctype.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -73,39 +74,68 @@ void install_signals(void)
 	signal(SIGPIPE, SIG_IGN);
 }
 
-/* One decimal token to Q16.16, the rule of tg_fx_parse: sign; integer digits
- * accumulated while the value is below 100000 (later ones are dropped);
- * fraction digits while fewer than 12 are held; exponent; value num / den with
- * num scaled by 10 per positive exponent step while num <= 2^47 and den by 10
- * per negative step; q = (num * 65536 + den / 2) / den, saturated, negated
- * for a minus sign. Returns the end of the token, or NULL without digits. */
+/* Decimal text to Q16.16 (the reference's tg_fx_parse, runtime/tg_rtq.h:375-401),
+ * in two stages: fx_lex reads the token's parts, fx_value turns them into the
+ * Q16.16 word. The observable rule: an optional sign; integer digits, of
+ * which only those read while the integer part is below 100000 count;
+ * fraction digits, of which only the first twelve count; an optional
+ * exponent; the value num / den with num = int * 10^f + frac and den = 10^f,
+ * num scaled by 10 per positive exponent step until it passes 2^47 (later
+ * steps are dropped), den by 10 per negative step; q = (num * 65536 + den /
+ * 2) / den. The products are 64-bit and wrap. The reference's build assumes
+ * they cannot, and so keeps one saturation bound per sign: a positive token's
+ * q is clamped above and otherwise truncated to 32 bits, a negative token's
+ * -q clamped below and otherwise truncated (tests/golden/fx_parse.json holds
+ * tokens whose products wrap). */
+typedef struct {
+	int neg, digits, ex;
+	int64_t ip, fn, fd;
+} FxParts;
+
+static const char *fx_lex(const char *s, FxParts *t)
+{
+	memset(t, 0, sizeof *t);
+	t->fd = 1;
+	if (*s == '-' || *s == '+') t->neg = *s++ == '-';
+	for (; isdigit((unsigned char)*s); s++, t->digits++)
+		if (t->ip < 100000) t->ip = t->ip * 10 + (*s - '0');
+	if (*s == '.')
+		for (s++; isdigit((unsigned char)*s); s++, t->digits++)
+			if (t->fd < 1000000000000LL) t->fn = t->fn * 10 + (*s - '0'), t->fd *= 10;
+	if (*s == 'e' || *s == 'E') {
+		s++;
+		const int eneg = *s == '-';
+		if (*s == '-' || *s == '+') s++;
+		for (; isdigit((unsigned char)*s); s++) t->ex = t->ex * 10 + (*s - '0');
+		if (eneg) t->ex = -t->ex;
+	}
+	return s;
+}
+
+static int32_t low32(int64_t x) { return (int32_t)(uint32_t)(uint64_t)x; }
+
+static int32_t fx_value(const FxParts *t)
+{
+	int64_t num = t->ip * t->fd + t->fn; /* below 10^18 */
+	uint64_t den = (uint64_t)t->fd;
+	for (int ex = t->ex; ex > 0 && num <= ((int64_t)1 << 47); ex--) num *= 10;
+	for (int ex = t->ex; ex < 0; ex++) den *= 10u; /* wraps modulo 2^64 */
+	const int64_t d = (int64_t)den;
+	if (d == 0 || d == -1) return 0; /* a divisor the reference's division would trap on */
+	const int64_t q = (int64_t)((uint64_t)num * 65536u + (uint64_t)(d / 2)) / d;
+	if (!t->neg) return q > INT32_MAX ? INT32_MAX : low32(q);
+	const int64_t v = (int64_t)(0u - (uint64_t)q);
+	return v < INT32_MIN ? INT32_MIN : low32(v);
+}
+
+/* the token at s as Q16.16 into *v; its end, or NULL when it has no digits */
 static const char *fx_parse(const char *s, int32_t *v)
 {
-	int neg = 0;
-	if (*s == '-' || *s == '+') neg = *s++ == '-';
-	int64_t ip = 0, fn = 0, fd = 1;
-	int digits = 0;
-	for (; *s >= '0' && *s <= '9'; s++, digits++)
-		if (ip < 100000) ip = ip * 10 + (*s - '0');
-	if (*s == '.')
-		for (s++; *s >= '0' && *s <= '9'; s++, digits++)
-			if (fd < 1000000000000LL) fn = fn * 10 + (*s - '0'), fd *= 10;
-	if (!digits) return NULL;
-	int ex = 0;
-	if (*s == 'e' || *s == 'E') {
-		int eneg = 0;
-		s++;
-		if (*s == '-' || *s == '+') eneg = *s++ == '-';
-		for (; *s >= '0' && *s <= '9'; s++) ex = ex * 10 + (*s - '0');
-		if (eneg) ex = -ex;
-	}
-	int64_t num = ip * fd + fn, den = fd;
-	for (; ex > 0 && num <= ((int64_t)1 << 47); ex--) num *= 10;
-	for (; ex < 0; ex++) den *= 10;
-	int64_t q = (num * 65536 + den / 2) / den;
-	if (neg) q = -q;
-	*v = q > INT32_MAX ? INT32_MAX : q < INT32_MIN ? INT32_MIN : (int32_t)q;
-	return s;
+	FxParts t;
+	const char *e = fx_lex(s, &t);
+	if (!t.digits) return NULL;
+	*v = fx_value(&t);
+	return e;
 }
 
 int die(const char *fmt, const char *a)
@@ -140,27 +170,36 @@ static char *slurp(const char *path, size_t *len)
 	return b;
 }
 
-/* numbers of one text line (f32, or Q16.16 words with `fixed`); -1 on a bad
- * token (src/io.c:25-41 rules) */
+/* The text row format (src/io.c:25-41): numbers separated by blanks or
+ * commas, the rest of the line after '#' a comment. A token must end at a
+ * separator, a comment or the line's end. */
+static int row_sep(char c) { return c == ' ' || c == '\t' || c == ',' || c == '\r' || c == '\n'; }
+
+/* one number at s into *x (f32, or a Q16.16 word's bits); its end (s itself if none) */
+static const char *row_token(const char *s, float *x, int fixed)
+{
+	if (!fixed) {
+		char *e;
+		*x = strtof(s, &e);
+		return e;
+	}
+	int32_t q = 0;
+	const char *e = fx_parse(s, &q);
+	memcpy(x, &q, 4);
+	return e ? e : s;
+}
+
+/* the numbers of one text line, up to max kept in v; their count, or -1
+ * with *bad at the first token that is not a number */
 int parse_row(const char *s, float *v, int max, const char **bad, int fixed)
 {
 	int n = 0;
 	for (;;) {
-		while (*s == ' ' || *s == '\t' || *s == ',' || *s == '\r' || *s == '\n') s++;
+		while (row_sep(*s)) s++;
 		if (!*s || *s == '#') return n;
-		const char *e;
 		float x;
-		if (fixed) {
-			int32_t q = 0;
-			e = fx_parse(s, &q);
-			if (!e) e = s;
-			memcpy(&x, &q, 4);
-		} else {
-			char *e2;
-			x = strtof(s, &e2);
-			e = e2;
-		}
-		if (e == s || (*e && !strchr(" \t,\r\n#", *e))) {
+		const char *e = row_token(s, &x, fixed);
+		if (e == s || !(*e == 0 || *e == '#' || row_sep(*e))) {
 			*bad = s;
 			return -1;
 		}
