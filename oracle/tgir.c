@@ -489,6 +489,25 @@ static void set_code(tgo_value *x, long j, int c)
 	x->q[j / 2] = (signed char)b;
 }
 
+/* Test-only extension of the reader (the reference reads text only): a
+ * param's values from a raw little-endian file next to the text, for models
+ * too large to write as text: `(data-file PATH)` (f32), and inside `quant`
+ * `(scale-file PATH)` (f32, one per channel) and `(codes-file PATH)` (int8,
+ * one per element). The values are the ones the text forms would give. */
+static void raw_file(P *r, void *dst, size_t bytes)
+{
+	char path[4096];
+	int isn;
+	double d;
+	atom(r, path, sizeof path, &isn, &d);
+	FILE *f = fopen(path, "rb");
+	if (!f) fail(r, "cannot open '%s'", path);
+	const size_t got = fread(dst, 1, bytes, f);
+	const int extra = fgetc(f) != EOF;
+	fclose(f);
+	if (got != bytes || extra) fail(r, "'%s' does not hold %zu bytes", path, bytes);
+}
+
 static void top_form(P *r, int *seen_block, int *seen_out)
 {
 	char h[64], nm[128], s[64];
@@ -525,25 +544,45 @@ static void top_form(P *r, int *seen_block, int *seen_out)
 			x->data = xcalloc(r, (size_t)x->n, sizeof(float));
 			open_(r);
 			symbol(r, s, sizeof s);
-			if (strcmp(s, "scale")) fail(r, "malformed quant scales");
-			for (int j = 0; j < nch; j++) {
-				if (peek(r) == ')') fail(r, "malformed quant scales (one per channel)");
-				x->qs[j] = (float)number(r, "scale");
+			if (!strcmp(s, "scale-file")) {
+				raw_file(r, x->qs, (size_t)nch * sizeof(float));
+			} else {
+				if (strcmp(s, "scale")) fail(r, "malformed quant scales");
+				for (int j = 0; j < nch; j++) {
+					if (peek(r) == ')') fail(r, "malformed quant scales (one per channel)");
+					x->qs[j] = (float)number(r, "scale");
+				}
 			}
 			close_(r);
 			open_(r);
 			symbol(r, s, sizeof s);
-			if (strcmp(s, "codes")) fail(r, "malformed quant codes");
 			int lim = x->qbits == 8 ? 127 : 7;
+			signed char *raw = NULL;
+			if (!strcmp(s, "codes-file")) {
+				raw = xcalloc(r, (size_t)x->n, 1);
+				raw_file(r, raw, (size_t)x->n);
+			} else if (strcmp(s, "codes")) {
+				fail(r, "malformed quant codes");
+			}
 			for (long j = 0; j < x->n; j++) {
-				if (peek(r) == ')') fail(r, "malformed quant codes (one per element)");
-				double c = number(r, "code");
+				double c;
+				if (raw) {
+					c = raw[j];
+				} else {
+					if (peek(r) == ')') fail(r, "malformed quant codes (one per element)");
+					c = number(r, "code");
+				}
 				if (c != (double)(int)c || fabs(c) > lim) fail(r, "malformed code");
 				set_code(x, j, (int)c);
 				long ch = x->qaxis == 0 ? j / sh.dim[1] : j % sh.dim[1];
 				x->data[j] = (float)(int)c * x->qs[ch];
 			}
+			free(raw);
 			close_(r);
+			close_(r);
+		} else if (!strcmp(s, "data-file")) {
+			x->data = xcalloc(r, (size_t)x->n, sizeof(float));
+			raw_file(r, x->data, (size_t)x->n * sizeof(float));
 			close_(r);
 		} else if (!strcmp(s, "data")) {
 			x->data = xcalloc(r, (size_t)x->n, sizeof(float));

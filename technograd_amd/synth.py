@@ -464,7 +464,7 @@ def rope_tables(T, HD, theta=1e6):
 
 
 def qwen3_tgir(name="qwen3", L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, V=151936, T=512, bits=4, seed=3, files=None,
-               quantizer=None, rope_len=None):
+               quantizer=None, rope_len=None, cache=None):
     """Config 3's model at fixed sequence length T: the graph
     examples/qwen3/import.py:110-130 emits (per-head rank-2 matmuls, GQA with
     NQ / NKV query heads per KV head, rotate-half RoPE as x * cos + (x @ Rot)
@@ -482,58 +482,80 @@ def qwen3_tgir(name="qwen3", L=28, D=1024, NQ=16, NKV=8, HD=128, FF=3072, V=1519
     native one for full size); quantize_rtn by default.
     rope_len: also emit the RoPE tables `rope_cos` / `rope_sin` with that many
     rows (the KV-cache decoder reads them for positions beyond T; the
-    fixed-length graph does not use them). Row p equals row p of cosT / sinT."""
-    w = qwen3_weights(L, D, NQ, NKV, HD, FF, V, seed)
+    fixed-length graph does not use them). Row p equals row p of cosT / sinT.
+    cache: a dict kept by the caller across calls with the same files
+    directory, weights and bits: the params that do not depend on T are
+    written once and their text reused (models of several lengths T share
+    one set of weight files)."""
+    if cache is not None and files is None:
+        raise ValueError("cache needs a files directory")
+    key = (L, D, NQ, NKV, HD, FF, V, bits, seed)
+    if cache is not None and cache.get("key", key) != key:
+        raise ValueError("cache holds another model's weights")
+    w = qwen3_weights(L, D, NQ, NKV, HD, FF, V, seed) if cache is None or "E" not in cache else None
     cos, sin, rot = rope_tables(T, HD)
     mask = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
     ones_d, ones_hd = np.ones(D, np.float32), np.ones(HD, np.float32)
     parts = ["(tgir 1\n  (model %s)\n" % name]
     rtn = quantizer or quantize_rtn
 
-    def f32p(nm, arr):
+    def f32p(nm, arr, by_t=False):
         if files is None:
-            return param_f32(nm, arr)
-        arr = np.ascontiguousarray(arr, np.float32)
-        path = os.path.join(files, nm + ".f32")
+            return param_f32(nm, arr() if callable(arr) else arr)
+        if cache is not None and not by_t and nm in cache:
+            return cache[nm]
+        arr = np.ascontiguousarray(arr() if callable(arr) else arr, np.float32)
+        path = os.path.join(files, nm + (".T%d" % T if by_t else "") + ".f32")
         arr.tofile(path)
-        return "  (param %s (f32 %s)\n    (data-file %s))\n" % (nm, " ".join(str(d) for d in arr.shape), path)
+        text = "  (param %s (f32 %s)\n    (data-file %s))\n" % (nm, " ".join(str(d) for d in arr.shape), path)
+        if cache is not None and not by_t:
+            cache[nm] = text
+            cache["key"] = key
+        return text
 
     def quant(nm, arr):
-        codes, sc = rtn(arr, bits, 1)
+        if cache is not None and nm in cache:
+            parts.append(cache[nm])
+            return
+        codes, sc = rtn(arr() if callable(arr) else arr, bits, 1)
         if files is None:
             parts.append(param_quant(nm, codes, sc, bits, 1))
             return
         cpath, spath = os.path.join(files, nm + ".codes"), os.path.join(files, nm + ".scale")
         np.ascontiguousarray(codes, np.int8).tofile(cpath)
         np.ascontiguousarray(sc, np.float32).tofile(spath)
-        parts.append("  (param %s (f32 %s)\n    (quant %d 1 (scale-file %s) (codes-file %s)))\n"
-                     % (nm, " ".join(str(d) for d in codes.shape), bits, spath, cpath))
+        text = "  (param %s (f32 %s)\n    (quant %d 1 (scale-file %s) (codes-file %s)))\n" % (
+            nm, " ".join(str(d) for d in codes.shape), bits, spath, cpath)
+        if cache is not None:
+            cache[nm] = text
+            cache["key"] = key
+        parts.append(text)
 
-    parts.append(f32p("E", w["E"]))
-    quant("LM", np.ascontiguousarray(w["E"].T))
+    parts.append(f32p("E", lambda: w["E"]))
+    quant("LM", lambda: np.ascontiguousarray(w["E"].T))
     parts.append(f32p("lnf", ones_d))
-    parts.append(f32p("cosT", cos))
-    parts.append(f32p("sinT", sin))
+    parts.append(f32p("cosT", cos, by_t=True))
+    parts.append(f32p("sinT", sin, by_t=True))
     quant("Rot", rot)
-    parts.append(f32p("mask", mask))
+    parts.append(f32p("mask", mask, by_t=True))
     if rope_len:
         rc, rs, _ = rope_tables(rope_len, HD)
-        parts.append(f32p("rope_cos", rc))
-        parts.append(f32p("rope_sin", rs))
-    parts.append(f32p("lastidx", np.array([T - 1], np.float32)))
+        parts.append(f32p("rope_cos", rc, by_t=True))
+        parts.append(f32p("rope_sin", rs, by_t=True))
+    parts.append(f32p("lastidx", np.array([T - 1], np.float32), by_t=True))
     for l in range(L):
         for nm in ("ln1_%d", "ln2_%d"):
             parts.append(f32p(nm % l, ones_d))
         for nm in ("qn_%d", "kn_%d"):
             parts.append(f32p(nm % l, ones_hd))
         for h in range(NQ):
-            quant("Wq_%d_%d" % (l, h), w["Wq_%d_%d" % (l, h)])
-            quant("Wo_%d_%d" % (l, h), w["Wo_%d_%d" % (l, h)])
+            quant("Wq_%d_%d" % (l, h), lambda k="Wq_%d_%d" % (l, h): w[k])
+            quant("Wo_%d_%d" % (l, h), lambda k="Wo_%d_%d" % (l, h): w[k])
         for j in range(NKV):
-            quant("Wk_%d_%d" % (l, j), w["Wk_%d_%d" % (l, j)])
-            quant("Wv_%d_%d" % (l, j), w["Wv_%d_%d" % (l, j)])
+            quant("Wk_%d_%d" % (l, j), lambda k="Wk_%d_%d" % (l, j): w[k])
+            quant("Wv_%d_%d" % (l, j), lambda k="Wv_%d_%d" % (l, j): w[k])
         for nm in ("Wg_%d", "Wu_%d", "Wd_%d"):
-            quant(nm % l, w[nm % l])
+            quant(nm % l, lambda k=nm % l: w[k])
     parts.append("  (input ids (f32 %d))\n  (block\n" % T)
     v = [0]
     lines = []

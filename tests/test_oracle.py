@@ -355,3 +355,30 @@ def test_goldens_within_reach_of_the_f64_truth(name):
     assert same.mean() > 0.9
     scale = np.abs(t[same]).max(axis=1, keepdims=True)
     assert (np.abs(y[same] - t[same]) <= 1e-4 * scale).all()
+
+
+def test_file_backed_params_equal_the_text_forms(tmp_path):
+    """The oracle's test-only file forms (data-file, scale-file, codes-file,
+    used for models too large to write as text) give the values of the text
+    forms: a small Qwen3-shaped model written both ways computes the same
+    bits, and a second length T written through the weight cache reuses the
+    first one's weight files."""
+    dims = dict(L=1, D=32, NQ=2, NKV=1, HD=16, FF=48, V=64)
+    ids = np.random.default_rng(1).integers(0, 64, size=(3, 6)).astype(np.float32)
+    want, _ = O.Model(synth.qwen3_tgir("q", T=6, **dims)).batch(ids)
+    cache = {}
+    got, _ = O.Model(synth.qwen3_tgir("q", T=6, files=str(tmp_path), cache=cache, **dims)).batch(ids)
+    assert np.array_equal(bits(got), bits(want))
+    stamp = os.path.getmtime(tmp_path / "LM.codes")
+    text4 = synth.qwen3_tgir("q", T=4, files=str(tmp_path), cache=cache, **dims)
+    assert os.path.getmtime(tmp_path / "LM.codes") == stamp and "mask.T4.f32" in text4
+    want4, _ = O.Model(synth.qwen3_tgir("q", T=4, **dims)).batch(ids[:, :4])
+    got4, _ = O.Model(text4).batch(ids[:, :4])
+    assert np.array_equal(bits(got4), bits(want4))
+    with pytest.raises(ValueError):
+        synth.qwen3_tgir("q", T=4, files=str(tmp_path), cache=cache, **dict(dims, FF=64))
+    short = tmp_path / "short.f32"
+    np.zeros(3, np.float32).tofile(short)
+    for path in (short, tmp_path / "absent.f32"):  # a file of the wrong size, and none
+        with pytest.raises(ValueError, match="short.f32|absent.f32"):
+            O.Model("(tgir 1 (model m) (param w (f32 4) (data-file %s)) (input x (f32 4)) (block) (output x))" % path)
