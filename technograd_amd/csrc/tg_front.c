@@ -27,6 +27,7 @@
 #include "tg_front.h"
 
 #include <ctype.h>
+#include <limits.h>
 #include <math.h>
 #include <setjmp.h>
 #include <stdarg.h>
@@ -268,6 +269,12 @@ static const char *infer(int op, const Sh *a, int na, Sh *o, char *err)
 
 static int newval(F *f, int kind, const Sh *sh, const char *name)
 {
+	int64_t n = 1; /* element counts are ints everywhere below: larger tensors are refused here */
+	for (int i = 0; i < sh->rank; i++)
+		if ((n *= sh->dim[i] > 0 ? sh->dim[i] : 1) > INT_MAX) {
+			snprintf(f->err, f->errn, "a tensor of more than %d elements", INT_MAX);
+			longjmp(f->jb, 1);
+		}
 	if (f->nval == f->capval) {
 		int cap = f->capval ? 2 * f->capval : 64;
 		Val *v = fgrow(f, f->val, (size_t)cap * sizeof *v);
@@ -509,10 +516,13 @@ static double signed_lit(P *p)
 	return neg ? -t->n : t->n;
 }
 
+/* v is a whole number in [1, max] (compared as a double, so no value outside int is converted) */
+static int whole_in(double v, double max) { return v >= 1 && v <= max && v == floor(v); }
+
 static int count_lit(P *p)
 {
 	Tok *t = need_kind(p, T_NUM, "integer");
-	if (t->n < 1 || t->n != (double)(int)t->n || t->n > 1 << 24) fail(p->f, p->file, t->line, "expected positive integer, got '%s'", t->s);
+	if (!whole_in(t->n, 1 << 24)) fail(p->f, p->file, t->line, "expected positive integer, got '%s'", t->s);
 	return (int)t->n;
 }
 
@@ -1260,6 +1270,7 @@ static int lower_rope(L *l, Blk *b, Env *e, Ex *x)
 	const int d = xs.dim[xs.rank - 1];
 	const int shapes = (xs.rank == 1 && ps.rank == 0) || (xs.rank == 2 && ps.rank == 1 && ps.dim[0] == xs.dim[0]);
 	if (!shapes || d % 2) fail(f, l->file, line, "'rope' takes x (d) with a scalar position or x (T, d) with positions (T), d even");
+	if ((int64_t)d * d > INT_MAX) fail(f, l->file, line, "'rope' dimension %d too large (its swap matrix has d x d entries)", d);
 	/* frequencies 10000^(-2 floor(i / 2) / d); swap maps each pair (x0, x1) to (-x1, x0) under x @ swap */
 	float *freq = fa(f, (size_t)d * sizeof *freq), *swap = fa(f, (size_t)d * (size_t)d * sizeof *swap);
 	for (int i = 0; i < d; i++) freq[i] = (float)pow(10000.0, -(double)(i / 2 * 2) / d);
@@ -1281,7 +1292,7 @@ static int lower_attention(L *l, Blk *b, Env *e, Ex *x)
 	const int line = x->line;
 	if (x->nargs != 4) fail(f, l->file, line, "'attention' takes (Q, K, V, window)");
 	const Ex *wd = x->args[3];
-	if (!is_num(wd) || wd->num < 1 || wd->num != (double)(int)wd->num) fail(f, l->file, line, "'attention' window must be a positive integer literal");
+	if (!is_num(wd) || !whole_in(wd->num, INT_MAX)) fail(f, l->file, line, "'attention' window must be a positive integer literal");
 	const int win = (int)wd->num;
 	const int q = lower_expr(l, b, e, x->args[0]), k = lower_expr(l, b, e, x->args[1]), v = lower_expr(l, b, e, x->args[2]);
 	const Sh qs = f->val[q].sh, ks = f->val[k].sh, vs = f->val[v].sh;
@@ -1354,7 +1365,7 @@ static int lower_expr(L *l, Blk *b, Env *e, Ex *x)
 		if (x->nargs < 2 || x->nargs - 1 > MAXRANK) fail(f, l->file, x->line, "'reshape' takes a tensor and 1 to %d dimensions", MAXRANK);
 		for (int i = 1; i < x->nargs; i++) {
 			Ex *d = x->args[i];
-			if (!is_num(d) || d->num < 1 || d->num != (double)(int)d->num)
+			if (!is_num(d) || !whole_in(d->num, INT_MAX))
 				fail(f, l->file, x->line, "'reshape' dimensions must be positive integer literals");
 			to.dim[to.rank++] = (int)d->num;
 		}
@@ -1640,7 +1651,10 @@ static float *materialize(L *l, const Init *in, const Sh *sh, const char *pname)
 		return d;
 	}
 	case I_RAND: {
-		uint32_t s = (uint32_t)(int64_t)in->v[0];
+		/* the seed's low 32 bits as an int64; outside int64 (and NaN) the x86-64
+		 * conversion the reference's build uses gives INT64_MIN, low bits 0 */
+		const double sv = in->v[0];
+		uint32_t s = sv >= -9223372036854775808.0 && sv < 9223372036854775808.0 ? (uint32_t)(int64_t)sv : 0u;
 		if (!s) s = 0x9e3779b9u;
 		float scale = (float)in->v[1];
 		for (int i = 0; i < n; i++) {

@@ -86,9 +86,15 @@ void install_signals(void)
  * they cannot, and so keeps one saturation bound per sign: a positive token's
  * q is clamped above and otherwise truncated to 32 bits, a negative token's
  * -q clamped below and otherwise truncated (tests/golden/fx_parse.json holds
- * tokens whose products wrap). */
+ * tokens whose products wrap). The exponent's digits accumulate in 32 bits
+ * with wrap-around, and the same assumption (that they cannot wrap) decides
+ * what a wrapped exponent does there: without a '-' it scales only when its
+ * signed 32-bit value is positive; with a '-' den is scaled as many times as
+ * its unsigned value says (den wraps to 0 within 64 steps, where the
+ * reference's division traps and this parser gives 0). */
 typedef struct {
-	int neg, digits, ex;
+	int neg, digits, eneg;
+	uint32_t ex; /* the exponent's digits, accumulated modulo 2^32 */
 	int64_t ip, fn, fd;
 } FxParts;
 
@@ -104,10 +110,9 @@ static const char *fx_lex(const char *s, FxParts *t)
 			if (t->fd < 1000000000000LL) t->fn = t->fn * 10 + (*s - '0'), t->fd *= 10;
 	if (*s == 'e' || *s == 'E') {
 		s++;
-		const int eneg = *s == '-';
+		t->eneg = *s == '-';
 		if (*s == '-' || *s == '+') s++;
-		for (; isdigit((unsigned char)*s); s++) t->ex = t->ex * 10 + (*s - '0');
-		if (eneg) t->ex = -t->ex;
+		for (; isdigit((unsigned char)*s); s++) t->ex = t->ex * 10u + (uint32_t)(*s - '0');
 	}
 	return s;
 }
@@ -118,8 +123,10 @@ static int32_t fx_value(const FxParts *t)
 {
 	int64_t num = t->ip * t->fd + t->fn; /* below 10^18 */
 	uint64_t den = (uint64_t)t->fd;
-	for (int ex = t->ex; ex > 0 && num <= ((int64_t)1 << 47); ex--) num *= 10;
-	for (int ex = t->ex; ex < 0; ex++) den *= 10u; /* wraps modulo 2^64 */
+	if (!t->eneg && t->ex <= (uint32_t)INT32_MAX) /* (zero stays zero) */
+		for (uint32_t k = t->ex; k && num && num <= ((int64_t)1 << 47); k--) num *= 10;
+	if (t->eneg)
+		for (uint32_t k = t->ex; k && den; k--) den *= 10u; /* wraps modulo 2^64, to 0 within 64 steps */
 	const int64_t d = (int64_t)den;
 	if (d == 0 || d == -1) return 0; /* a divisor the reference's division would trap on */
 	const int64_t q = (int64_t)((uint64_t)num * 65536u + (uint64_t)(d / 2)) / d;

@@ -313,6 +313,7 @@ typedef struct {
 	int fd, eof, overflow; /* overflow: a line longer than LR_MAX_LINE arrived (its bytes are dropped, input ends) */
 	char *buf;
 	size_t cap, beg, end;
+	size_t scan; /* buf[beg..scan) holds no '\n': a long line is searched once, not once per read */
 } LR;
 
 static void lr_init(LR *r, int fd)
@@ -327,18 +328,20 @@ static void lr_init(LR *r, int fd)
 static int lr_fill(LR *r, int block)
 {
 	if (!r->buf) return 0;
-	if (r->beg == r->end) r->beg = r->end = 0;
+	if (r->scan < r->beg) r->scan = r->beg;
+	if (r->beg == r->end) r->beg = r->end = r->scan = 0;
 	if (r->end == r->cap) {
 		if (r->beg) {
 			memmove(r->buf, r->buf + r->beg, r->end - r->beg);
 			r->end -= r->beg;
+			r->scan -= r->beg;
 			r->beg = 0;
 		} else {
 			char *nb = r->cap < LR_MAX_LINE ? realloc(r->buf, 2 * r->cap + 1) : NULL;
 			if (!nb) { /* too long a line (or no memory for it): drop what is buffered and end the input */
 				r->overflow = 1;
 				r->eof = 1;
-				r->beg = r->end = 0;
+				r->beg = r->end = r->scan = 0;
 				return 0;
 			}
 			r->buf = nb;
@@ -378,15 +381,17 @@ static int lr_line(LR *r, char **line, int block)
 {
 	for (;;) {
 		if (!r->buf) return 0;
-		char *s = r->buf + r->beg, *nl = memchr(s, '\n', r->end - r->beg);
+		if (r->scan < r->beg) r->scan = r->beg;
+		char *s = r->buf + r->beg, *nl = memchr(r->buf + r->scan, '\n', r->end - r->scan);
 		if (nl || (r->eof && r->end > r->beg)) {
 			size_t e = nl ? (size_t)(nl - r->buf) : r->end;
 			r->buf[e] = 0;
-			r->beg = nl ? e + 1 : e;
+			r->beg = r->scan = nl ? e + 1 : e;
 			while (e > (size_t)(s - r->buf) && r->buf[e - 1] == '\r') r->buf[--e] = 0;
 			*line = s;
 			return 1;
 		}
+		r->scan = r->end;
 		if (r->eof) return 0;
 		int k = lr_fill(r, block);
 		if (k < 0) return -1;

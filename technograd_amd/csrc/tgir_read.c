@@ -27,6 +27,7 @@
 #include "tgm.h"
 
 #include <ctype.h>
+#include <limits.h>
 #include <math.h>
 #include <setjmp.h>
 #include <stdarg.h>
@@ -47,6 +48,9 @@ typedef struct {
 	} *scope;
 	int ns, scap;
 	signed char *codes; /* codes read from a file, until packed */
+	char **own;         /* strings the reader holds while a form is parsed (freed on failure too) */
+	int nown, cown;
+	int depth;          /* think and scan bodies open */
 } Rd;
 
 static void bad(Rd *r, const char *fmt, ...)
@@ -64,6 +68,27 @@ static void *mem(Rd *r, size_t n, size_t sz)
 	void *p = calloc(n ? n : 1, sz ? sz : 1);
 	if (!p) bad(r, "out of memory");
 	return p;
+}
+
+/* a copy of s, held by the reader until release_to(r, mark) with an earlier mark */
+static char *own_str(Rd *r, const char *s)
+{
+	if (r->nown == r->cown) {
+		const int cap = r->cown ? 2 * r->cown : 16;
+		char **no = realloc(r->own, (size_t)cap * sizeof *no);
+		if (!no) bad(r, "out of memory");
+		r->own = no;
+		r->cown = cap;
+	}
+	char *p = strdup(s);
+	if (!p) bad(r, "out of memory");
+	r->own[r->nown++] = p;
+	return p;
+}
+
+static void release_to(Rd *r, int mark)
+{
+	while (r->nown > mark) free(r->own[--r->nown]);
 }
 
 /* skip blanks and ; comments, return the next character (0 at end) */
@@ -273,7 +298,7 @@ static void scan_form(Rd *r, tgm_block *b)
 {
 	tgm_module *m = r->m;
 	double T = num(r, "scan steps");
-	if (T < 1 || T != floor(T)) bad(r, "malformed scan (steps)");
+	if (T < 1 || T != floor(T) || T > INT_MAX) bad(r, "malformed scan (steps)");
 	Atom a;
 	sym(r, &a);
 	if (strcmp(a.t, "forward") && strcmp(a.t, "reverse")) bad(r, "malformed scan (direction)");
@@ -284,6 +309,7 @@ static void scan_form(Rd *r, tgm_block *b)
 		stid = m->nthink++;
 	}
 	enum { MX = 32 };
+	const int held = r->nown;
 	char *cname[MX], *xname[MX], *yname[MX];
 	int c[MX], ci[MX], cn[MX], x[MX], xt[MX], yv[MX], nc = 0, nx = 0, ny = 0;
 	tgm_shape ysh[MX];
@@ -292,7 +318,7 @@ static void scan_form(Rd *r, tgm_block *b)
 		lp(r);
 		sym(r, &a);
 		sym(r, &a);
-		cname[nc] = strdup(a.t);
+		cname[nc] = own_str(r, a.t);
 		tgm_shape sh = type(r);
 		ci[nc] = ref(r);
 		rp(r);
@@ -306,7 +332,7 @@ static void scan_form(Rd *r, tgm_block *b)
 		lp(r);
 		sym(r, &a);
 		sym(r, &a);
-		xname[nx] = strdup(a.t);
+		xname[nx] = own_str(r, a.t);
 		tgm_shape sh = type(r);
 		x[nx] = ref(r);
 		rp(r);
@@ -325,6 +351,7 @@ static void scan_form(Rd *r, tgm_block *b)
 	int at = b->len;
 	emit(r, b);
 	tgm_block *body = mem(r, 1, sizeof *body);
+	b->v[at].body = body; /* owned by the instruction from here on, so a failure below frees it */
 	lp(r);
 	sym(r, &a);
 	items(r, body, 0);
@@ -343,7 +370,7 @@ static void scan_form(Rd *r, tgm_block *b)
 		lp(r);
 		sym(r, &a);
 		sym(r, &a);
-		yname[ny] = strdup(a.t);
+		yname[ny] = own_str(r, a.t);
 		ysh[ny] = type(r);
 		yv[ny] = ref(r);
 		rp(r);
@@ -376,25 +403,34 @@ static void scan_form(Rd *r, tgm_block *b)
 		in->c[k] = c[k];
 		in->cinit[k] = ci[k];
 		in->cnext[k] = cn[k];
-		free(cname[k]);
 	}
 	for (int j = 0; j < nx; j++) {
 		in->x[j] = x[j];
 		in->xt[j] = xt[j];
-		free(xname[j]);
 	}
 	for (int y = 0; y < ny; y++) {
 		in->y[y] = yv[y];
 		in->ys[y] = value(r, TGM_TMP, &ysh[y], NULL);
 		bind(r, yname[y], in->ys[y]);
-		free(yname[y]);
 	}
+	release_to(r, held);
 	in = &b->v[at];
-	in->body = body;
 	in->out = c[0];
 }
 
+/* bodies nest at most this deep (the parser recurses once per level) */
+#define TGM_MAX_DEPTH 64
+
+static void block_items(Rd *r, tgm_block *b, int in_think);
+
 static void items(Rd *r, tgm_block *b, int in_think)
+{
+	if (++r->depth > TGM_MAX_DEPTH) bad(r, "think and scan bodies nested more than %d deep", TGM_MAX_DEPTH);
+	block_items(r, b, in_think);
+	r->depth--;
+}
+
+static void block_items(Rd *r, tgm_block *b, int in_think)
 {
 	tgm_module *m = r->m;
 	Atom a, nm;
@@ -424,7 +460,8 @@ static void items(Rd *r, tgm_block *b, int in_think)
 		} else if (!strcmp(a.t, "think")) {
 			int init = ref(r);
 			double budget = num(r, "think budget");
-			if (budget < 1) bad(r, "malformed think budget");
+			/* (above INT_MAX the reference's int conversion is undefined: refused here) */
+			if (!(budget >= 1 && budget <= INT_MAX)) bad(r, "malformed think budget");
 			Atom e;
 			atom(r, &e);
 			double eps = -1;
@@ -440,6 +477,7 @@ static void items(Rd *r, tgm_block *b, int in_think)
 			emit(r, b);
 			int tid = m->nthink++;
 			tgm_block *body = mem(r, 1, sizeof *body);
+			b->v[at].body = body; /* owned by the instruction from here on */
 			int mark = r->ns;
 			bind(r, nm.t, out);
 			items(r, body, 1);
@@ -616,6 +654,8 @@ tgm_module *tgm_read(const char *text, size_t len, char *err, size_t errn)
 		unbind_to(&r, 0);
 		free(r.scope);
 		free(r.codes);
+		release_to(&r, 0);
+		free(r.own);
 		tgm_free(r.m);
 		return NULL;
 	}
@@ -683,6 +723,7 @@ tgm_module *tgm_read(const char *text, size_t len, char *err, size_t errn)
 	r.m->nout = r.m->val[r.m->output].n;
 	unbind_to(&r, 0);
 	free(r.scope);
+	free(r.own);
 	return r.m;
 }
 

@@ -10,7 +10,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libtg_hip.so")
+# TG_HIP_LIB names another build of the library (the host sanitizer build runs the CPU tests that way)
+LIB_PATH = os.environ.get("TG_HIP_LIB") or os.path.join(HERE, "lib", "libtg_hip.so")
 
 FIXED, EXACT, ROWPROG, TIMING, INTERP = 1, 2, 4, 8, 16
 

@@ -104,7 +104,12 @@ def fx_tokens():
     hand = ["0", "-0", "+0", "1", "-1", "0.5", ".5", "5.", "-.25", "1e3", "1E-3", "2.5e+2", "-2.5e-2", "1e", "0.0000076293945",
             "0.00000762939453125", "0.0000076293945313", "-0.00000762939453125", "3.00000762939453125", "32767.9999", "32768",
             "-32768", "-32768.00001", "99999.5", "100000", "123456.75", "1234567.5", "0.123456789012345678", "1.000000000001",
-            "7e-5", "7.62939453125e-6", "1.52587890625e-5", "4.5e-1", "65535.99999", "1e10", "-1e10", "0.1e1", "10e-1"]
+            "7e-5", "7.62939453125e-6", "1.52587890625e-5", "4.5e-1", "65535.99999", "1e10", "-1e10", "0.1e1", "10e-1",
+            # exponents whose digits pass 32 bits (the reference's int accumulates them with wrap-around) and
+            # denominators that wrap modulo 2^64 (not the tokens whose denominator wraps to 0, as in 3e-4294967295:
+            # the reference's division traps on those)
+            "1e4294967297", "-2.5e4294967296", "7e4294967295", "7e2147483648", "5e2147483657", "7e-4294967297",
+            "3e-4294967296", "1e-4294967306", "9e99999999999", "1e-63", "-2e-40", "5e-21", "7e2147483647"]
     rng = np.random.default_rng(12)
     rnd = []
     for _ in range(1500):

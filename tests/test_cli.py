@@ -10,7 +10,7 @@ from fractions import Fraction
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-CLI = os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
+CLI = os.environ.get("TGC_HIP") or os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
 FX = os.path.join(ROOT, "tests", "golden", "fx_parse.json")
 
 pytestmark = pytest.mark.skipif(not os.path.exists(CLI), reason="bin/tgc-hip is not built")
@@ -43,8 +43,11 @@ def test_fixture_pins_rounding():
         q = -q if neg else q
         return max(-2 ** 31, min(2 ** 31 - 1, q))
 
-    toks = [t for t in d["tokens"] if not t.endswith(("e", "E"))]
-    want = [q for t, q in zip(d["tokens"], d["q16"]) if not t.endswith(("e", "E"))]
+    def plain(t):  # an exponent of a few digits (the wrapped ones have their own rule)
+        return not t.endswith(("e", "E")) and len(t.lower().partition("e")[2].lstrip("+-")) <= 3
+
+    toks = [t for t in d["tokens"] if plain(t)]
+    want = [q for t, q in zip(d["tokens"], d["q16"]) if plain(t)]
     assert [exact(t, False) for t in toks] != want
     assert [exact(t, True) for t in toks] != want
 

@@ -24,7 +24,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 FRONT = os.path.join(GOLDEN, "front")
 FRONT_ENV = {"TGF_FRONT_VALUES": "1.5, -2 3e-1,4"}  # as make_golden.py sets it for the reference
-CLI = os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
+CLI = os.environ.get("TGC_HIP") or os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
 
 MODELS = sorted(os.path.basename(p)[:-3] for p in glob.glob(os.path.join(GOLDEN, "models", "*.tg"))
                 if os.path.exists(os.path.join(GOLDEN, os.path.basename(p)[:-3] + "_f32.tgir")))

@@ -21,7 +21,7 @@ import parity  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-CLI = os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
+CLI = os.environ.get("TGC_HIP") or os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 

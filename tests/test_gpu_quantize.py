@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(ROOT, "tests", "golden")
-CLI = os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
+CLI = os.environ.get("TGC_HIP") or os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
 
 # golden: (f32 source, min-size)
 GPTQ = {"qmlp_q4g": ("qmlp_f32", 256), "latent_q4g": ("latent_f32", 1)}

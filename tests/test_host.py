@@ -36,7 +36,7 @@ def test_symbols_are_c_abi():
 
 
 def test_cli_is_built_and_refuses_bad_usage():
-    exe = os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
+    exe = os.environ.get("TGC_HIP") or os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
     assert os.access(exe, os.X_OK)
     r = subprocess.run([exe], capture_output=True, text=True)
     assert r.returncode != 0 and "usage" in r.stderr

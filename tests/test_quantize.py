@@ -14,7 +14,7 @@ from technograd_amd import hip
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(ROOT, "tests", "golden")
-CLI = os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
+CLI = os.environ.get("TGC_HIP") or os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
 
 # golden: (f32 source, bits, min-size); mlp3s is lowered from its .tg model
 RTN = {
