@@ -268,6 +268,16 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 		auto ld = [&](int gi, float *v) {
 			for (int i = 0; i < 16; i++) v[i] = 16 * gi + i < HD ? x[16 * gi + i] : 0.0f;
 		};
+		TgqCoarse co{}; // the coarse test first (tg_qdigits.h)
+		for (int gi = lane; gi < (HD + 15) / 16; gi += 64) {
+			float v[16];
+			ld(gi, v);
+			tgq_coarse16(co, v, E0);
+		}
+		if (tgq_coarse_grid(tgq_coarse_wave_sum(co), (int)(tq[t] >> TGQ_TALLY_SHIFT))) {
+			if (lane == 0) sp[t] = 0;
+			continue;
+		}
 		const int L = tgq_resolve(&hist[wave], ld, (HD + 15) / 16, E0, lane);
 		if (L <= 0) {
 			if (lane == 0) sp[t] = L < 0 ? 1 : 0;
@@ -358,34 +368,50 @@ __device__ inline float blk_max(float v, float *red)
 	return m;
 }
 
-__device__ inline long long blk_sum(long long v, long long *red)
+// N sums over the block (red: [N][16] in LDS), every thread gets them
+template <int N>
+__device__ inline void blk_sums(unsigned long long (&v)[N], unsigned long long *red)
 {
-	for (int w = 32; w > 0; w >>= 1) v += __shfl_xor(v, w);
+	for (int w = 32; w > 0; w >>= 1)
+		for (int i = 0; i < N; i++) v[i] += __shfl_xor(v[i], w);
 	__syncthreads();
-	if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+	if ((threadIdx.x & 63) == 0)
+		for (int i = 0; i < N; i++) red[i * 16 + (threadIdx.x >> 6)] = v[i];
 	__syncthreads();
-	long long t = 0;
-	for (int i = 0; i < (int)(blockDim.x >> 6); i++) t += red[i];
-	return t;
+	for (int i = 0; i < N; i++) {
+		unsigned long long t = 0;
+		for (int u = 0; u < (int)(blockDim.x >> 6); u++) t += red[i * 16 + u];
+		v[i] = t;
+	}
 }
 
 // digits of row m of K inputs, values z[0 .. Kp) in LDS (zero from K on), from
-// this thread's share of max |z| and of the non-finite flag
-__device__ inline void blk_digits(const float *z, int K, int Kp, float mx, int bad, const tgk_qdig &q, int m, float *redf, long long *redl)
+// this thread's share of max |z| and of the non-finite flag. The coarse
+// histogram (tg_qdigits.h) is kept in the same pass and summed with the sum
+// of q and the tally in one block reduction (the rows here are mostly gated
+// activations: candidates that the coarse test settles).
+__device__ inline void blk_digits(const float *z, int K, int Kp, float mx, int bad, const tgk_qdig &q, int m, float *redf,
+				  unsigned long long *redl)
 {
 	const float amax = blk_max(mx, redf); // nan never wins fmaxf; such rows are flagged by bad
 	const int anybad = __syncthreads_or(bad);
 	const int special = tgq_special(anybad, amax), E = tgq_exponent(amax, special);
 	int8_t *blk = tgq_row_base(q.dig, m, Kp);
 	long long qs = 0, tl = 0;
+	TgqCoarse co{};
 	for (int j = threadIdx.x; j < Kp / 16; j += blockDim.x) {
 		float v[16];
 		for (int u = 0; u < 16; u++) v[u] = z[16 * j + u];
 		qs += tgq_put16(blk, 16 * j, v, E, special, tl);
+		if (!special) tgq_coarse16(co, v, E);
 	}
-	qs = blk_sum(qs, redl);
-	tl = blk_sum(tl, redl);
-	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = (special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID), q.qsum[m] = qs;
+	unsigned long long sums[6] = { (unsigned long long)qs, (unsigned long long)tl, co.cnt, co.m0, co.m1, co.mt };
+	blk_sums(sums, redl);
+	qs = (long long)sums[0], tl = (long long)sums[1];
+	co = TgqCoarse{ sums[2], sums[3], sums[4], sums[5] };
+	int cls = special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID;
+	if (cls == TGQ_CAND && tgq_coarse_grid(co, (int)(tl >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
+	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = cls, q.qsum[m] = qs;
 }
 
 // tgk_dec_norm: one block per token row, NORM_TPB threads, each with at most
@@ -400,7 +426,7 @@ __global__ __launch_bounds__(NORM_TPB) void dec_norm_k(tgk_dec_norm_args a)
 	extern __shared__ float4 zs4[]; // [Kp] values, [Kp] squares (16-byte aligned)
 	float *zs = (float *)zs4;
 	__shared__ float redf[16], inv_s;
-	__shared__ long long redl[16];
+	__shared__ unsigned long long redl[6 * 16];
 	const int t = blockIdx.x, D = a.D, Kp = a.Kp, tid = threadIdx.x;
 	float *z = zs, *sq = zs + Kp, *hr = a.h + (long)t * a.hs;
 	float v[NORM_EPT], g[NORM_EPT];
@@ -504,7 +530,17 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 		qs += tgq_put16(blk, 16 * g, v, E, special, tl);
 	}
 	for (int o = 32; o > 0; o >>= 1) qs += __shfl_xor(qs, o), tl += __shfl_xor(tl, o);
-	if (lane == 0) a.q.e[L] = E, a.q.special[L] = (special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID), a.q.qsum[L] = qs;
+	int cls = special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID;
+	if (cls == TGQ_CAND) { // (uniform over the wave) the coarse test before any resolve
+		TgqCoarse co{};
+		for (int g = lane; g < Kp / 16; g += 64) {
+			float v[16];
+			for (int u = 0; u < 16; u++) v[u] = z[16 * g + u];
+			tgq_coarse16(co, v, E);
+		}
+		if (tgq_coarse_grid(tgq_coarse_wave_sum(co), (int)(tl >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
+	}
+	if (lane == 0) a.q.e[L] = E, a.q.special[L] = cls, a.q.qsum[L] = qs;
 }
 
 // Many lines at once (a prompt's token rows, or its head lines): a block of
@@ -636,9 +672,20 @@ __global__ __launch_bounds__(NL_TPB) void norm_lines_k(NormLines a)
 		}
 	}
 	for (int o = 1; o < TPL; o <<= 1) qs += __shfl_xor(qs, o), tl += __shfl_xor(tl, o);
+	int cls = special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID;
+	TgqCoarse co{}; // the coarse test of candidate lines before any resolve (shuffles within the line's lanes)
+	if (cls == TGQ_CAND)
+		for (int gi = k; gi < Kp / 16; gi += TPL) {
+			float w16[16];
+			for (int q = 0; q < 16; q++) w16[q] = zl[gi * 16 + q];
+			tgq_coarse16(co, w16, E);
+		}
+	for (int o = 1; o < TPL; o <<= 1)
+		co.cnt += __shfl_xor(co.cnt, o), co.m0 += __shfl_xor(co.m0, o), co.m1 += __shfl_xor(co.m1, o), co.mt += __shfl_xor(co.mt, o);
+	if (cls == TGQ_CAND && tgq_coarse_grid(co, (int)(tl >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
 	if (k == 0 && L0 + l < a.lines) {
 		const long L = L0 + l;
-		a.q.e[L] = E, a.q.special[L] = (special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID), a.q.qsum[L] = qs;
+		a.q.e[L] = E, a.q.special[L] = cls, a.q.qsum[L] = qs;
 	}
 }
 
@@ -648,7 +695,7 @@ __global__ __launch_bounds__(1024) void dec_silu_k(tgk_dec_silu_args a)
 	extern __shared__ float4 zs4[]; // [Kp]
 	float *zs = (float *)zs4;
 	__shared__ float redf[16];
-	__shared__ long long redl[16];
+	__shared__ unsigned long long redl[6 * 16];
 	const int t = blockIdx.x, FF = a.FF;
 	const float *g = a.gu + (long)t * a.gus, *u = g + FF;
 	float mx = 0.0f;

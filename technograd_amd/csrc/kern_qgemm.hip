@@ -181,7 +181,18 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 	}
 	qs = wave_sum(qs);
 	tl = wave_sum(tl);
-	const int cls = special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID;
+	int cls = special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID;
+	if (cls == TGQ_CAND) { // the coarse test first (the row again: still in v when it fits, else read again)
+		TgqCoarse co{};
+		for (int t0 = 0; t0 < nsl; t0 += SL) {
+			if (nsl > SL) fetch(t0);
+			for (int t = 0; t < SL; t++) {
+				const int k0 = (t0 + t) * 1024 + lane * 16;
+				if (t0 + t < nsl && k0 < K) tgq_coarse16(co, v[t], E);
+			}
+		}
+		if (tgq_coarse_grid(tgq_coarse_wave_sum(co), (int)(tl >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
+	}
 	if (lane == 0) {
 		s.e[m] = E;
 		s.special[m] = cls;
@@ -204,14 +215,21 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 // Many rows, 16 per block: lane l of wave w owns row m0 + (l & 15), half
 // (l >> 4) & 1 and parity l >> 5 of 32-input block pairs w, w + W, ... (NKB
 // pairs in registers). In each digit plane a block writes its 16 rows' two
-// 256-byte runs. The row's max, non-finite flag and sum of q are combined
-// through LDS. Results are those of digits_k.
+// 256-byte runs. A row's max, non-finite flag, sum of q and tallies are
+// combined over its four lanes of a wave with shuffles, then over the waves
+// through LDS. Candidates take the coarse test on the values still in
+// registers; those it does not settle are resolved a wave per row by the
+// first RW waves, whose histograms are the dynamic LDS (RW x TgqHist). Results
+// are those of digits_k.
 template <int NKB, bool VEC>
-__global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
+__global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M, int RW)
 {
-	__shared__ float smx[16][64];
-	__shared__ int sbad[16][64];
-	__shared__ long long sqs[16][64], stl[16][64];
+	__shared__ float smx[16][16];
+	__shared__ int sbad[16][16];
+	__shared__ long long sqs[16][16], stl[16][16];
+	__shared__ TgqCoarse sco[16][16];
+	__shared__ int scls[16], sE[16], sany;
+	extern __shared__ TgqHist hist[];
 	const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
 	const int m0 = blockIdx.x * 16, mr = lane & 15, half = (lane >> 4) & 1, par = lane >> 5;
 	const float *x = xrow(a, m0 + mr < M ? m0 + mr : M - 1); // rows past M repeat row M - 1
@@ -226,16 +244,12 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 	float mx;
 	int bad;
 	tgq_scan_end(mb, mx, bad);
-	smx[w][lane] = mx;
-	sbad[w][lane] = bad;
+	for (int o = 16; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o)), bad |= __shfl_xor(bad, o);
+	if (lane < 16) smx[w][lane] = mx, sbad[w][lane] = bad;
 	__syncthreads();
 	float amax = 0.0f;
 	bad = 0;
-	for (int u = 0; u < W; u++)
-		for (int q = 0; q < 4; q++) {
-			amax = fmaxf(amax, smx[u][mr + 16 * q]);
-			bad |= sbad[u][mr + 16 * q];
-		}
+	for (int u = 0; u < W; u++) amax = fmaxf(amax, smx[u][mr]), bad |= sbad[u][mr];
 	const int special = tgq_special(bad, amax), E = tgq_exponent(amax, special);
 	int8_t *blk = s.dig + (long)(m0 >> 5) * nkb * 3072 + ((m0 & 31) + mr) * 16;
 	long long qs = 0, tl = 0;
@@ -243,23 +257,43 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 		const int kb = 2 * (w + j * W) + par;
 		if (kb < nkb) qs += tgq_put16(blk, kb * 32 + half * 16, v[j], E, special || kb * 32 + half * 16 >= K, tl);
 	}
-	sqs[w][lane] = qs;
-	stl[w][lane] = tl;
+	for (int o = 16; o < 64; o <<= 1) qs += __shfl_xor(qs, o), tl += __shfl_xor(tl, o);
+	if (lane < 16) sqs[w][lane] = qs, stl[w][lane] = tl;
 	__syncthreads(); // also: every digit of the block's rows is stored
-	__shared__ int scls[16], sE[16];
 	if (w == 0 && lane < 16) {
 		long long t = 0, u2 = 0;
-		for (int u = 0; u < W; u++)
-			for (int q = 0; q < 4; q++) t += sqs[u][mr + 16 * q], u2 += stl[u][mr + 16 * q];
+		for (int u = 0; u < W; u++) t += sqs[u][mr], u2 += stl[u][mr];
 		const int cls = m0 + mr >= M ? TGQ_GRID : special ? TGQ_REF : tgq_candidate(u2) ? TGQ_CAND : TGQ_GRID;
 		scls[mr] = cls, sE[mr] = E;
+		stl[0][mr] = u2; // the row's tally, for the coarse test
 		if (m0 + mr < M) s.e[m0 + mr] = E, s.special[m0 + mr] = cls, s.qsum[m0 + mr] = t;
+		const unsigned long long cb = __ballot(cls == TGQ_CAND);
+		if (lane == 0) sany = cb != 0;
 	}
 	__syncthreads();
-	// candidates: a wave per row (waves 0 .. RW - 1), each row read again
-	constexpr int NH = 8;
-	__shared__ TgqHist hist[NH];
-	const int RW = W < NH ? W : NH, nout = tgq_nout(Kp);
+	if (!sany) return; // (uniform over the block)
+	// the coarse test of the candidates, on the values still in registers
+	TgqCoarse co{};
+	if (scls[mr] == TGQ_CAND)
+		for (int j = 0; j < NKB; j++) {
+			const int kb = 2 * (w + j * W) + par;
+			if (kb < nkb && kb * 32 + half * 16 < K) tgq_coarse16(co, v[j], E);
+		}
+	for (int o = 16; o < 64; o <<= 1)
+		co.cnt += __shfl_xor(co.cnt, o), co.m0 += __shfl_xor(co.m0, o), co.m1 += __shfl_xor(co.m1, o), co.mt += __shfl_xor(co.mt, o);
+	if (lane < 16) sco[w][lane] = co;
+	__syncthreads();
+	if (w == 0 && lane < 16 && scls[mr] == TGQ_CAND) {
+		TgqCoarse c = sco[0][mr];
+		for (int u = 1; u < W; u++) tgq_coarse_add(c, sco[u][mr]);
+		if (tgq_coarse_grid(c, (int)(stl[0][mr] >> TGQ_TALLY_SHIFT))) {
+			scls[mr] = TGQ_GRID;
+			s.special[m0 + mr] = TGQ_GRID;
+		}
+	}
+	__syncthreads();
+	// the rest of the candidates: a wave per row (waves 0 .. RW - 1), each row read again
+	const int nout = tgq_nout(Kp);
 	if (w < RW)
 		for (int r = w; r < 16; r += RW) {
 			if (scls[r] != TGQ_CAND) continue;
@@ -313,7 +347,22 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 	tl = wave_sum(tl);
 	if (lane == 0) sqs[w] = qs, stl[w] = tl;
 	__syncthreads(); // also: every digit of the row is stored
-	const int cls = special ? TGQ_REF : tgq_candidate(stl[0] + stl[1] + stl[2] + stl[3]) ? TGQ_CAND : TGQ_GRID;
+	const long long tally = stl[0] + stl[1] + stl[2] + stl[3];
+	int cls = special ? TGQ_REF : tgq_candidate(tally) ? TGQ_CAND : TGQ_GRID;
+	if (cls == TGQ_CAND) { // (uniform over the block) the coarse test, on the values still in registers
+		__shared__ TgqCoarse sco[4];
+		TgqCoarse co{};
+		for (int g = 0; g < G; g++) {
+			const int j = tid + g * 256;
+			if (j < ng && j * 16 < K) tgq_coarse16(co, v[g], E);
+		}
+		co = tgq_coarse_wave_sum(co);
+		if (lane == 0) sco[w] = co;
+		__syncthreads();
+		TgqCoarse c = sco[0];
+		for (int u = 1; u < 4; u++) tgq_coarse_add(c, sco[u]);
+		if (tgq_coarse_grid(c, (int)(tally >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
+	}
 	if (tid == 0) {
 		s.e[m] = E;
 		s.special[m] = cls;
@@ -1794,16 +1843,20 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 		// (measured: K = 2048, 65536 rows: 178 us against 235 with one 32-row
 		// block of 16 waves per CU, at a streaming read-then-write floor of 173)
 		const int WM = M >= 8192 && nkb <= 64 ? 8 : 16;
-		const int W = nkb / 2 < WM ? (nkb + 1) / 2 : WM, nb = (M + 15) / 16, pairs = (nkb + 1) / 2;
+		// at least 4 waves (for short rows some only resolve candidates); the
+		// first min(W, 8) resolve, one histogram each
+		const int W = nkb / 2 < WM ? ((nkb + 1) / 2 < 4 ? 4 : (nkb + 1) / 2) : WM, nb = (M + 15) / 16, pairs = (nkb + 1) / 2;
+		const int RW = W < 8 ? W : 8;
+		const size_t lds = (size_t)RW * sizeof(TgqHist);
 		if (pairs <= W) {
-			if (vec) digits_tile16_k<1, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
-			else digits_tile16_k<1, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+			if (vec) digits_tile16_k<1, true><<<nb, W * 64, lds, st>>>(*a, s, K, w->Kp, M, RW);
+			else digits_tile16_k<1, false><<<nb, W * 64, lds, st>>>(*a, s, K, w->Kp, M, RW);
 		} else if (pairs <= 2 * W) {
-			if (vec) digits_tile16_k<2, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
-			else digits_tile16_k<2, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+			if (vec) digits_tile16_k<2, true><<<nb, W * 64, lds, st>>>(*a, s, K, w->Kp, M, RW);
+			else digits_tile16_k<2, false><<<nb, W * 64, lds, st>>>(*a, s, K, w->Kp, M, RW);
 		} else {
-			if (vec) digits_tile16_k<4, true><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
-			else digits_tile16_k<4, false><<<nb, W * 64, 0, st>>>(*a, s, K, w->Kp, M);
+			if (vec) digits_tile16_k<4, true><<<nb, W * 64, lds, st>>>(*a, s, K, w->Kp, M, RW);
+			else digits_tile16_k<4, false><<<nb, W * 64, lds, st>>>(*a, s, K, w->Kp, M, RW);
 		}
 	} else if (M < 512 && w->Kp >= 2048 && w->Kp <= 16384) { // few long rows: a block per row
 		const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) &&

@@ -303,6 +303,66 @@ __device__ inline int tgq_decide(TgqHist *h, int n, int lane)
 	return okm ? __builtin_ctzll(okm) : -1;
 }
 
+// ---- the producers' coarse test ----
+//
+// Most candidates keep their grid when resolved. A producer settles most of
+// those without a resolve from a coarse histogram it keeps while writing the
+// digits: TgqHist's bins 0 and 1 exactly, every other nonzero entry in one
+// merged bin 2 (|x| < 2^(E-2)), counts and masses. tgq_coarse_grid runs
+// tgq_decide's test at level 0 on it, an entry of the merged bin counting at
+// that bin's upper end 2^(E-2) when the bin is taken in part. The coarse bins
+// are unions of tgq_decide's bins, so the coarse top mass is at least
+// tgq_decide's and the coarse top bin at most tgq_decide's: a row that passes
+// here passes tgq_decide at level 0, where the resolve leaves a row as it is.
+// A row's class is therefore the same whether or not its producer runs this
+// test first.
+struct TgqCoarse {
+	unsigned long long cnt;    // nonzero entries: bin 0 in bits 0..20, bin 1 in bits 21..41, the merged bin from bit 42
+	unsigned long long m0, m1; // masses of bins 0 and 1 (sums of floor(|x| 2^(44-E)))
+	unsigned long long mt;     // mass of all bins
+};
+
+__device__ inline void tgq_coarse_add(TgqCoarse &c, const TgqCoarse &o) { c.cnt += o.cnt, c.m0 += o.m0, c.m1 += o.m1, c.mt += o.mt; }
+
+// adds 16 inputs of a row with grid exponent E (finite, below 2^E)
+__device__ inline void tgq_coarse16(TgqCoarse &c, const float *v, int E)
+{
+	for (int i = 0; i < 16; i++) {
+		const float ax = fabsf(v[i]);
+		const int d = tgq_bin(ax, E);
+		const unsigned long long ms = (unsigned long long)ldexpf(ax, TGQ_MASS_SHIFT - E); // truncation: the floor
+		c.cnt += ax == 0.0f ? 0ull : d == 0 ? 1ull : d == 1 ? 1ull << 21 : 1ull << 42;
+		c.m0 += d == 0 ? ms : 0ull; // (ms is 0 for a zero entry)
+		c.m1 += d == 1 ? ms : 0ull;
+		c.mt += ms;
+	}
+}
+
+__device__ inline TgqCoarse tgq_coarse_wave_sum(TgqCoarse c)
+{
+	for (int o = 32; o > 0; o >>= 1)
+		c.cnt += __shfl_xor(c.cnt, o), c.m0 += __shfl_xor(c.m0, o), c.m1 += __shfl_xor(c.m1, o), c.mt += __shfl_xor(c.mt, o);
+	return c;
+}
+
+// whether a candidate row with n inexact entries keeps its grid by the coarse
+// histogram alone (tgq_decide's level-0 test on the coarse bins)
+__device__ inline bool tgq_coarse_grid(const TgqCoarse &c, int n)
+{
+	const unsigned long long lo21 = (1ull << 21) - 1;
+	const long long cnt[3] = { (long long)(c.cnt & lo21), (long long)((c.cnt >> 21) & lo21), (long long)(c.cnt >> 42) };
+	const long long ms[3] = { (long long)c.m0, (long long)c.m1, (long long)(c.mt - c.m0 - c.m1) };
+	const int r = cnt[0] ? 0 : cnt[1] ? 1 : 2;
+	if (!cnt[r]) return false; // an all-zero row is no candidate
+	long long left = tgq_jcap(n), top = 0;
+	for (int d = r; d < 3 && left > 0; d++) {
+		const long long take = cnt[d] < left ? cnt[d] : left;
+		top += take == cnt[d] ? ms[d] : take << (TGQ_MASS_SHIFT - d);
+		left -= take;
+	}
+	return (long long)c.mt - top >= (long long)tgq_acoef(n) << (TGQ_MASS_SHIFT - r);
+}
+
 // Resolves a candidate row of grid exponent E (a whole wave; h in LDS, this
 // wave's own): ld(g, v) loads the row's 16-input group g of ng (zeros past
 // the row). Returns the peel level: 0 the grid, L > 0 a split at level L

@@ -206,6 +206,32 @@ def resolve_row(x_k, E, n):
     return -1
 
 
+def coarse_grid(x_k, E, n):
+    """tgq_coarse_grid on one candidate row (grid exponent E, n inexact
+    entries): tgq_decide's level-0 test on bins 0 and 1 and one merged bin
+    for the rest, a merged entry counting at 2^(E-2) when that bin is taken
+    in part. Passing it implies resolve_row(...) == 0."""
+    a = np.abs(np.asarray(x_k, np.float32).astype(np.float64))
+    a = a[a != 0]
+    d = np.minimum(_bins(a, E), 2)
+    mass = np.floor(np.ldexp(a, MASS_SHIFT - E)).astype(np.int64)
+    cnt = np.bincount(d, minlength=3)
+    ms = np.zeros(3, np.int64)
+    np.add.at(ms, d, mass)
+    nz = np.flatnonzero(cnt)
+    if len(nz) == 0:
+        return False
+    r = int(nz[0])
+    left, top = jcap(n), 0
+    for dd in range(r, 3):
+        if left == 0:
+            break
+        take = min(int(cnt[dd]), left)
+        top += int(ms[dd]) if take == cnt[dd] else take << (MASS_SHIFT - dd)
+        left -= take
+    return int(ms.sum()) - top >= acoef(n) << (MASS_SHIFT - r)
+
+
 def row_classes(x_mk):
     """(cls [M], level [M], E [M]) as the device decides them: cls 0 a row on
     its grid, 1 the reference's loop (special rows, and candidates no level

@@ -10,8 +10,10 @@ import pytest
 
 from oracle import oracle as O
 from technograd_amd import synth
-from parity import (check_qmatmul, device_path_matmul, digit_path_matmul, grid_bound, outlier_mask, outlier_rows,
-                    qmatmul_truth, reference_loop, row_classes, ulp)
+from parity import _bins as _bins_of
+from parity import acoef, jcap
+from parity import (candidates, check_qmatmul, coarse_grid, device_path_matmul, digit_path_matmul, grid_bound, grid_rows,
+                    outlier_mask, outlier_rows, qmatmul_truth, reference_loop, resolve_row, row_classes, ulp)
 
 
 def _case(seed, M=7, K=96, C=40, lim=7):
@@ -119,6 +121,77 @@ def test_dense_and_heavy_tailed_rows(kind):
         check_qmatmul(got, ref, codes.T, scales, x)
         if kind in ("gauss", "laplace") and K >= 1024:
             assert (cls == 0).all()
+
+
+def _coarse_rows():
+    """(kind, K, x [M, K]) of Gaussian, Student t(3), gated (silu x up, config
+    3's and 5's activations), 90 %-sparse and planted-outlier rows"""
+    rng = np.random.default_rng(11)
+    for K in (16, 64, 512, 3072):
+        M = 200
+        g = rng.normal(size=(M, K))
+        sets = {"gauss": rng.normal(size=(M, K)), "t3": rng.standard_t(3, size=(M, K)),
+                "silu_up": g / (1 + np.exp(-g)) * rng.normal(size=(M, K)),
+                "sparse": rng.normal(size=(M, K)) * (rng.random((M, K)) < 0.1)}
+        if K >= 512:
+            codes = rng.integers(-7, 8, size=(K, 8)).astype(np.int8)
+            sets["outliers"] = outlier_rows(K, codes, seed=K)[0]
+        for kind, x in sets.items():
+            yield kind, K, x.astype(np.float32)
+
+
+def _coarse_check(test):
+    """per (kind, K): [rows the test settles, candidates the full resolve keeps on the grid,
+    settled rows the full resolve does not keep on the grid]"""
+    out = {}
+    for kind, K, x in _coarse_rows():
+        special, E = grid_rows(x)
+        cand, n = candidates(x)
+        st = out.setdefault((kind, K), [0, 0, 0])
+        for m in np.flatnonzero(cand):
+            c = test(x[m], int(E[m]), int(n[m]))
+            grid = resolve_row(x[m], int(E[m]), int(n[m])) == 0
+            st[0] += c
+            st[1] += grid
+            st[2] += c and not grid
+    return out
+
+
+def test_coarse_test_implies_the_grid():
+    """The producers' coarse test (tgq_coarse_grid) settles a candidate as a
+    grid row only where the full resolve keeps its grid too: every row it
+    passes resolves to level 0. Of the gated rows' candidates of 512 and more
+    inputs that the full resolve keeps on the grid, it settles most (the
+    point of it)."""
+    st = _coarse_check(coarse_grid)
+    print("coarse test (settled, grid candidates, wrong):", st)
+    assert sum(v[2] for v in st.values()) == 0
+    gated = [st[("silu_up", K)] for K in (512, 3072)] + [st[("t3", K)] for K in (512, 3072)]
+    assert sum(v[0] for v in gated) > 0.8 * sum(v[1] for v in gated)
+
+
+def test_coarse_check_catches_a_slip():
+    """The implication check has teeth: the same test asking the rest for A
+    units of the merged bin's 2^(E-2) instead of its top bin's (a plausible
+    slip) settles rows that the full resolve splits."""
+    def slipped(x_k, E, n):
+        a = np.abs(np.asarray(x_k, np.float32).astype(np.float64))
+        a = a[a != 0]
+        d = np.minimum(_bins_of(a, E), 2)
+        mass = np.floor(np.ldexp(a, 44 - E)).astype(np.int64)
+        cnt, ms = np.bincount(d, minlength=3), np.zeros(3, np.int64)
+        np.add.at(ms, d, mass)
+        r = int(np.flatnonzero(cnt)[0])
+        left, top = jcap(n), 0
+        for dd in range(r, 3):
+            if left == 0:
+                break
+            take = min(int(cnt[dd]), left)
+            top += int(ms[dd]) if take == cnt[dd] else take << (44 - dd)
+            left -= take
+        return int(ms.sum()) - top >= acoef(n) << (44 - 2)
+    st = _coarse_check(slipped)
+    assert sum(v[2] for v in st.values()) > 0, st
 
 
 def test_row_classes_hand_cases():
