@@ -194,6 +194,47 @@ def ref_cpu(text, rows, per, nout, nthink, threads, fixed, what, runs=3):
     return out
 
 
+def cli_batch_wall(text, rows, what, runs=3):
+    """`bin/tgc-hip batch MODEL rows.bin -o out.bin -v` as a user runs it, on
+    `rows` written to a raw f32 file: the driver's own timer (input load to
+    last write, the reference's `batch` timer, src/main.c:413-443) and the
+    process wall time (start to exit, model load and device set-up
+    included), medians of `runs` runs."""
+    import re
+    import numpy as np
+    cli = os.path.join(ROOT, "technograd_amd", "bin", "tgc-hip")
+    if not os.path.exists(cli):
+        return None
+    tmp = tempfile.mkdtemp(prefix="tge2e")
+    try:
+        mpath, rpath, opath = (os.path.join(tmp, n) for n in ("model.tgir", "rows.bin", "out.bin"))
+        with open(mpath, "w") as f:
+            f.write(text)
+        np.ascontiguousarray(rows, np.float32).tofile(rpath)
+        timer, wall = [], []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            r = subprocess.run([cli, "batch", mpath, rpath, "-o", opath, "-v", "--rows", str(len(rows))],
+                               capture_output=True, text=True, timeout=300)
+            wall.append((time.perf_counter() - t0) * 1e3)
+            m = re.search(r"row\(s\) in ([0-9.]+) ms", r.stderr)
+            if r.returncode or not m:
+                log("tgc-hip batch failed (rc %d): %s" % (r.returncode, r.stderr[-300:]))
+                return None
+            timer.append(float(m.group(1)))
+        tm, wm = sorted(timer)[len(timer) // 2], sorted(wall)[len(wall) // 2]
+        n = len(rows)
+        log("tgc-hip batch, %s: %.2f ms input load to last write (%.0f rows/s), %.0f ms process wall" % (what, tm, n / tm * 1e3, wm))
+        return {"rows": n, "ms": round(tm, 2), "rows_per_s": round(n / tm * 1e3, 1), "process_wall_ms": round(wm, 1),
+                "runs": runs, "files": "raw f32 rows in, raw f32 outputs out (%d MiB + %d MiB), in %s" % (
+                    rows.nbytes >> 20, os.path.getsize(opath) >> 20, tempfile.gettempdir()),
+                "note": "bin/tgc-hip batch MODEL rows.bin -o out.bin -v --rows N: ms = the driver's timer from before "
+                        "the input load to after the last write (the reference's batch timer); rows_per_s from it, "
+                        "the measure of cpu_baseline.wall_value"}
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def setup(synth):
     W = synth.config2_weight()
     text = synth.linear_tgir("linear4096", W, 4)
@@ -216,6 +257,13 @@ def profile_child(mode):
         d_x = hip.DeviceBuffer.from_array(X)
         d_y = hip.DeviceBuffer(65536 * 512 * 4)
         calls = [(65536, lambda: prog.batch_device(d_x.ptr, 65536, d_y.ptr))] * 2
+    elif mode == "c5":
+        import numpy as np
+        seqs, T = C5_PROFILE_SEQS, 512
+        prog = hip.Program(synth.ssm_tgir("ssm"), max_rows=seqs)
+        d_x = hip.DeviceBuffer.from_array(synth.config5_rows(seqs, T, 256))
+        d_y = hip.DeviceBuffer(seqs * 8 * 4)
+        calls = [(seqs, lambda: prog.batch_device(d_x.ptr, seqs, d_y.ptr))] * 2
     elif mode == "c2":
         text, X = setup(synth)
         prog = hip.Program(text, max_rows=4096)
@@ -346,16 +394,16 @@ def profile_c2(alg_bytes):
     return res, note
 
 
-def profile_c1():
-    """Calibrated HBM traffic of config 1's three GEMMs in one pass (FETCH_SIZE
-    and WRITE_SIZE of its qgemm_k dispatches, averaged over two passes, each
-    after a flush pass), or None."""
+def profile_pass(mode):
+    """Calibrated HBM traffic of one pass of a --profile-child mode that runs
+    two passes, each after a flush pass (FETCH_SIZE and WRITE_SIZE of every
+    dispatch, averaged over the two): {kernel: bytes per pass}, or None."""
     if not shutil.which("rocprofv3"):
         return None
     out = tempfile.mkdtemp(prefix="tgprof")
     try:
-        fe = profiled(["--pmc", "FETCH_SIZE"], "c1", out, "fetch")
-        wr = profiled(["--pmc", "WRITE_SIZE"], "c1", out, "write") if fe else None
+        fe = profiled(["--pmc", "FETCH_SIZE"], mode, out, "fetch")
+        wr = profiled(["--pmc", "WRITE_SIZE"], mode, out, "write") if fe else None
     except subprocess.TimeoutExpired:
         return None
     finally:
@@ -363,7 +411,16 @@ def profile_c1():
     if not fe or not wr or len(fe[0]) != 2 or len(wr[0]) != 2:
         return None
     tr, _, _ = calibrated_traffic(fe, wr)
-    return sum(sum(v for k, v in per.items() if k.startswith("qgemm_k")) for _, per in tr) / 2
+    per = {}
+    for _, kern in tr:
+        for k, v in kern.items():
+            per[k] = per.get(k, 0.0) + v / 2
+    return per
+
+
+# config 1's algorithmic bytes per pass (the measure of the reference's
+# metric): rows in, rows out, the int8 weights and their scales once
+C1_ALG_BYTES = 4 * 65536 * (512 + 512) + (2048 * 512 + 2048 * 2048 + 512 * 2048) + 4 * (2048 + 2048 + 512)
 
 
 def config1_leg(args, steps=None, profile=True):
@@ -400,14 +457,17 @@ def config1_leg(args, steps=None, profile=True):
     st = tprog.stats()
     mfma_us, dig_us, oth_us = (v / 3 * 1e3 for v in (st.qgemm_ms, st.digits_ms, st.other_ms))
     ops = 2.0 * (2048 * 512 + 2048 * 2048 + 512 * 2048) * rows
-    # the GEMMs' algorithmic bytes: int8 weights and scales once, f32 activations in and outputs out of each
-    alg_bytes = (2048 * 512 + 2048 * 2048 + 512 * 2048) + 4 * (2048 + 2048 + 512) + 4 * rows * (512 + 2048 + 2048 + 2048 + 2048 + 512)
+    alg_bytes = C1_ALG_BYTES  # rows in + rows out + weights once: 274.7 MB per pass
     log("config 1: %.2f ms per pass: GEMMs %.0f us, digits %.0f us, other %.0f us" % (
         elapsed / steps * 1e3, mfma_us, dig_us, oth_us))
     cpu = None if args.no_cpu else ref_cpu(text, X[:2048], 512, 512, 0, auto_threads(), False,
                                            "config 1 (int8 MLP 512-2048-2048-512)")
     frac = ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS
-    traffic = profile_c1() if profile else None
+    e2e = None if getattr(args, "no_e2e", False) else cli_batch_wall(text, X, "config 1 (int8 MLP, 65,536 rows)")
+    per = profile_pass("c1") if profile else None
+    traffic = None if per is None else sum(v for k, v in per.items() if k.startswith("qgemm_k"))
+    traffic_pass = None if per is None else sum(per.values())
+    pass_us = elapsed / steps * 1e6
     return {
         "metric": "config 1 int8 MLP rows/sec at 1 GPU; % of int8-MFMA roofline", "value": round(rows * steps / elapsed, 1),
         "unit": "rows/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
@@ -416,15 +476,24 @@ def config1_leg(args, steps=None, profile=True):
         "config": {"workload": "config 1: int8 MLP 512-2048-2048-512, tanh, rmsnorm; 65,536 rows per step"},
         "roofline": {"bound": "mfma", "achieved": round(ops / mfma_us / 1e6, 2), "peak": MFMA_I8_PEAK_TOPS,
                      "unit": "TOP/s", "frac": round(frac, 4), "traffic": None if traffic is None else round(traffic),
-                     "traffic_note": "calibrated FETCH_SIZE + WRITE_SIZE of the pass's qgemm_k dispatches (rocprofv3)"
-                                     if traffic is not None else ("not profiled (--no-traffic)" if not profile else
-                                                                  "rocprofv3 gave no data"),
+                     "traffic_note": "calibrated FETCH_SIZE + WRITE_SIZE of the pass's qgemm_k dispatches (rocprofv3); "
+                                     "traffic_pass: of every dispatch of the pass" if traffic is not None else
+                                     ("not profiled (--no-traffic)" if not profile else "rocprofv3 gave no data"),
                      "alg_bytes_per_pass": alg_bytes,
+                     "alg_bytes_note": "rows in + rows out + int8 weights and scales once (65,536 x 512 f32 each way)",
+                     "traffic_pass": None if traffic_pass is None else round(traffic_pass),
+                     "traffic_ratio": None if traffic is None else round(traffic / alg_bytes, 2),
+                     "traffic_pass_ratio": None if traffic_pass is None else round(traffic_pass / alg_bytes, 2),
+                     "traffic_kernels": None if per is None else {k: round(v) for k, v in sorted(per.items())},
+                     "hbm_view": {"achieved": round(alg_bytes / pass_us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(alg_bytes / pass_us / 1e3 / HBM_PEAK_GBS, 4),
+                                  "note": "algorithmic bytes over the whole pass's time"},
                      "limb_factor": 3, "hw_mfma_frac": round(3 * frac, 4),
                      "kernel": "the three quantized GEMMs of a pass (qgemm_k<8>), summed",
                      "alg_ops_per_launch": ops, "avg_kernel_us": round(mfma_us, 1)},
         "cpu_baseline": cpu,
         "breakdown_us": {"gemm": round(mfma_us, 1), "digits": round(dig_us, 1), "other": round(oth_us, 1)},
+        "end_to_end": e2e,
     }
 
 
@@ -660,6 +729,19 @@ def config3_leg(args):
     return out
 
 
+C5_PROFILE_SEQS = 256  # sequences of the profiled config 5 pass
+
+
+def c5_alg_bytes(seqs, T=512, dm=256, di=512, ns=16, dtr=16, blocks=4):
+    """Config 5's projection bytes: per block and time step the inputs read
+    once (x, u, the dt-rank vector, the gated SSM output) and the outputs
+    written once (xi, z, the dt-rank vector, B, C, dt, the block output), f32;
+    the int8 weights and their scales once."""
+    per_step = 4 * ((dm + di + dtr + di) + (di + di + dtr + ns + ns + di + dm))
+    weights = blocks * (2 * dm * di + 2 * di * dtr + 2 * di * ns + di * dm) + 4 * blocks * (2 * di + dtr + 2 * ns + di + dm)
+    return blocks * seqs * T * per_step + weights
+
+
 def bench_config5(args):
     print(json.dumps(config5_leg(args)), flush=True)
 
@@ -711,6 +793,10 @@ def config5_leg(args):
     mfma_us, dig_us, oth_us = (v * scale * 1e3 for v in (st.qgemm_ms, st.digits_ms, st.other_ms))
     macs = 4 * T * (2 * dm * 512 + 3 * 512 * 16 + 16 * 512 + 512 * dm) + dm * 8
     ops = 2.0 * macs * rows
+    alg_bytes = c5_alg_bytes(rows, T)
+    proj_us = mfma_us + dig_us
+    per = None if args.no_traffic else profile_pass("c5")
+    traffic = None if per is None else sum(v for k, v in per.items() if k.startswith(("qgemm_k", "digits_"))) * rows / C5_PROFILE_SEQS
     log("config 5: %.1f ms per 4096 sequences: projections %.0f us, digits %.0f us, other (scan, elementwise) %.0f us"
         % (t * 1e3, mfma_us, dig_us, oth_us))
     cpu = None if args.no_cpu else ref_cpu(text, X[:32], per, 8, 0, auto_threads(), False,
@@ -722,9 +808,25 @@ def config5_leg(args):
         "data": "synthetic (N(0,0.02) weights seed 105 quantized int8 per channel, N(0,1) inputs seed 5)",
         "config": {"workload": "config 5: 4 Mamba-style blocks d_model 256, state 16, expand 2, T 512; 4096 sequences "
                                "per step", "pass_rows": pass_rows},
-        "roofline": {"bound": "mfma", "achieved": round(ops / mfma_us / 1e6, 2), "peak": MFMA_I8_PEAK_TOPS,
-                     "unit": "TOP/s", "frac": round(ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS, 4), "traffic": None,
-                     "kernel": "the quantized projections of a pass, summed (the scan is f32 VALU work)"},
+        "roofline": {"bound": "hbm", "achieved": round(alg_bytes / proj_us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(alg_bytes / proj_us / 1e3 / HBM_PEAK_GBS, 4),
+                     "traffic": None if traffic is None else round(traffic),
+                     "traffic_ratio": None if traffic is None else round(traffic / alg_bytes, 2),
+                     "alg_bytes_per_pass": alg_bytes,
+                     "alg_bytes_note": "per block and time step: the projections' inputs read once (x 1 KiB, u 2 KiB, "
+                                       "the dt-rank vector 64 B, the gated SSM output 2 KiB) and their outputs written "
+                                       "once (xi, z, dt 2 KiB each, the dt-rank vector, B and C 64 B each, the block's "
+                                       "output 1 KiB): 12,544 B; the int8 weights and scales once",
+                     "traffic_note": ("calibrated FETCH_SIZE + WRITE_SIZE of the digit and GEMM dispatches of a pass of "
+                                      "%d sequences (rocprofv3), scaled to %d" % (C5_PROFILE_SEQS, rows))
+                                     if traffic is not None else "not profiled",
+                     "traffic_kernels": None if per is None else {k: round(v * rows / C5_PROFILE_SEQS)
+                                                                  for k, v in sorted(per.items())},
+                     "kernel": "the projections of a pass: digit kernels and quantized GEMMs (their epilogues "
+                               "included), summed; output-bound GEMMs (the f32 scan is VALU work)",
+                     "avg_kernel_us": round(proj_us, 1),
+                     "mfma_view": {"achieved": round(ops / mfma_us / 1e6, 2), "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
+                                   "frac": round(ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS, 4)}},
         "cpu_baseline": cpu,
         "breakdown_us": {"projections": round(mfma_us, 1), "digits": round(dig_us, 1), "other": round(oth_us, 1)},
     }
@@ -744,11 +846,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 runs (kernel trace and counters)")
     ap.add_argument("--no-legs", action="store_true", help="skip the config 1, 4, 5 and 3 legs")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end `tgc-hip batch` runs")
     ap.add_argument("--reps", type=int, default=10, help="kernel-timing repetitions per batch")
     ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
                     help="BASELINE configuration: 2 (default, the headline metric), 1 (int8 MLP), 3 (Qwen3-shaped "
                          "decoder, prefill), 4 (Q16.16 reasoner), 5 (selective-SSM classifier)")
-    ap.add_argument("--profile-child", choices=("c1", "c2", "c4"), help=argparse.SUPPRESS)
+    ap.add_argument("--profile-child", choices=("c1", "c2", "c4", "c5"), help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.profile_child:
         profile_child(args.profile_child)
@@ -827,8 +930,21 @@ def main():
     t0 = time.perf_counter()
     for _ in range(3):
         prog.batch(xh)
+    pageable_rps = 3 * 4096 / (time.perf_counter() - t0)
+    hin, hout = hip.HostBuffer(xh.nbytes), hip.HostBuffer(4096 * C * 4)
+    xp, yp = hin.array(np.float32, xh.shape), hout.array(np.float32, (4096, C))
+    xp[:] = xh
+    sp = np.zeros((4096, 1), np.int32)
+    prog.batch(xp, yp, sp)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        prog.batch(xp, yp, sp)
     pcie_rps = 3 * 4096 / (time.perf_counter() - t0)
-    log("host-buffer batch 4096: %.0f rows/s (PCIe in and out included)" % pcie_rps)
+    log("host-buffer batch 4096: %.0f rows/s from pinned buffers, %.0f from pageable ones (PCIe in and out included)"
+        % (pcie_rps, pageable_rps))
+    hin.free()
+    hout.free()
+    e2e = None if args.no_e2e else cli_batch_wall(text, xh, "config 2 (int4 4096 x 4096, 4096 rows)")
 
     # ---- rocprofv3: cold kernel durations and HBM traffic per batch ----
     prof, pnote = None, "skipped (--no-traffic)"
@@ -907,8 +1023,12 @@ def main():
         "config": {"workload": "config 2: int4 4096x4096 linear, one pass at each batch of {1,16,256,4096} rows per step",
                    "rows_per_step": rows_per_step, "parallelism": "1 GPU"},
         "roofline": roofline, "cpu_baseline": cpu, "sweep": sweep,
-        "pcie_inclusive": {"rows_per_s": round(pcie_rps, 1), "batch": 4096,
-                           "note": "tg_hip_batch with host buffers: 64 MiB in and 64 MiB out over PCIe per call"},
+        "pcie_inclusive": {"rows_per_s": round(pcie_rps, 1), "batch": 4096, "pageable_rows_per_s": round(pageable_rps, 1),
+                           "note": "tg_hip_batch with host buffers: 64 MiB in and 64 MiB out over PCIe per call; rows_per_s "
+                                   "with rows and outputs in pinned memory from tg_hip_host_alloc (moved directly), "
+                                   "pageable_rows_per_s from ordinary numpy arrays (copied through the library's pinned "
+                                   "staging slots)"},
+        "end_to_end": e2e,
         "legs": legs,
     }
     print(json.dumps(out), flush=True)

@@ -220,6 +220,15 @@ void tg_hip_dec_free(tg_hip_dec *d);
 /* Device memory helpers for callers without their own allocator. */
 void *tg_hip_dev_alloc(size_t bytes);
 int tg_hip_dev_free(void *d);
+/* Pinned (page-locked) host memory for rows, outputs and steps: tg_hip_batch
+ * and tg_hip_batch_fixed move buffers that lie inside such an allocation over
+ * PCIe directly, without their host-side staging copy, and `tgc-hip batch`
+ * reads binary rows straight into it. No counterpart in the reference (its
+ * rows live in ordinary memory, src/io.c:load_samples): for callers that
+ * stream rows through the device. NULL on failure; tg_hip_host_free takes
+ * only pointers from tg_hip_host_alloc (-1 otherwise). */
+void *tg_hip_host_alloc(size_t bytes);
+int tg_hip_host_free(void *h);
 int tg_hip_h2d(void *d, const void *h, size_t bytes);
 int tg_hip_d2h(void *h, const void *d, size_t bytes);
 /* A read of `bytes` of device memory at d (16-byte aligned) that writes

@@ -35,6 +35,7 @@
 #include <climits>
 #include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -2126,6 +2127,22 @@ void par_copy(void *dst, const void *src, size_t n)
 	for (auto &x : th) x.join();
 }
 
+// Pinned host allocations made by tg_hip_host_alloc: start -> size. A row or
+// output buffer inside one moves over PCIe directly (no staging copy).
+std::mutex g_pinned_mu;
+std::map<uintptr_t, size_t> g_pinned;
+
+bool in_pinned(const void *h, size_t bytes)
+{
+	if (!h) return false;
+	const uintptr_t a = (uintptr_t)h;
+	std::lock_guard<std::mutex> lk(g_pinned_mu);
+	auto it = g_pinned.upper_bound(a);
+	if (it == g_pinned.begin()) return false;
+	--it;
+	return a - it->first <= it->second && bytes <= it->second - (a - it->first);
+}
+
 bool host_pipe_init(tg_hip_prog *p)
 {
 	auto &h = p->hp;
@@ -2158,6 +2175,8 @@ bool host_pipe_init(tg_hip_prog *p)
 // stream waits for the event of the step before it, and a slot is refilled
 // only after its previous chunk has left it. So chunk i + 1 travels while
 // chunk i computes. Passes run in input order on one stream, as before.
+// Rows, outputs or steps in memory from tg_hip_host_alloc skip the host
+// copies: the transfers read and write the caller's buffers directly.
 int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *steps)
 {
 	if (!p) {
@@ -2166,15 +2185,22 @@ int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *ste
 	}
 	if (!host_pipe_init(p)) return -1;
 	auto &h = p->hp;
-	const long per = p->m->per, nout = p->m->nout, nt = p->m->nthink ? p->m->nthink : 1, C = h.chunk;
+	const long per = p->m->per, nout = p->m->nout, nt = p->m->nthink ? p->m->nthink : 1;
+	const bool din = in_pinned(rows, (size_t)nrows * per * 4), dout = in_pinned(out, (size_t)nrows * nout * 4);
+	const bool dsteps = steps && in_pinned(steps, (size_t)nrows * nt * 4);
+	// chunks of about 16 MiB of rows through the staging slots (the host copies
+	// want large pieces); a quarter of that when nothing is staged, so the
+	// first chunk's upload and the last one's download, which nothing
+	// overlaps, are short
+	const long C = din && dout ? std::max(64L, h.chunk / 4) : h.chunk;
 	const long nch = (nrows + C - 1) / C;
 	float ms_total = 0;
 	auto finish = [&](long i) -> bool { // chunk i's outputs to the caller
 		const int k = (int)(i & 1);
 		const long r0 = i * C, cnt = nrows - r0 < C ? nrows - r0 : C;
 		if (!hipok(hipEventSynchronize(h.down[k]), "outputs to host")) return false;
-		par_copy((char *)out + (size_t)r0 * nout * 4, h.h_out[k], (size_t)cnt * nout * 4);
-		if (steps && p->m->nthink) memcpy(steps + (size_t)r0 * nt, h.h_steps[k], (size_t)cnt * nt * 4);
+		if (!dout) par_copy((char *)out + (size_t)r0 * nout * 4, h.h_out[k], (size_t)cnt * nout * 4);
+		if (steps && p->m->nthink && !dsteps) memcpy(steps + (size_t)r0 * nt, h.h_steps[k], (size_t)cnt * nt * 4);
 		float ms = 0;
 		(void)hipEventElapsedTime(&ms, h.t0[k], h.t1[k]);
 		ms_total += ms;
@@ -2184,18 +2210,24 @@ int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *ste
 		const int k = (int)(i & 1);
 		const long r0 = i * C, cnt = nrows - r0 < C ? nrows - r0 : C;
 		if (i >= 2 && !finish(i - 2)) return -1; // the slot's previous chunk is out: its buffers are free
-		par_copy(h.h_in[k], (const char *)rows + (size_t)r0 * per * 4, (size_t)cnt * per * 4);
-		if (!hipok(hipMemcpyAsync(h.d_in[k], h.h_in[k], (size_t)cnt * per * 4, hipMemcpyHostToDevice, h.h2d), "rows to device") ||
+		const void *src = (const char *)rows + (size_t)r0 * per * 4;
+		if (!din) {
+			par_copy(h.h_in[k], src, (size_t)cnt * per * 4);
+			src = h.h_in[k];
+		}
+		if (!hipok(hipMemcpyAsync(h.d_in[k], src, (size_t)cnt * per * 4, hipMemcpyHostToDevice, h.h2d), "rows to device") ||
 		    !hipok(hipEventRecord(h.up[k], h.h2d), "event") || !hipok(hipStreamWaitEvent(p->st, h.up[k], 0), "wait"))
 			return -1;
 		(void)hipEventRecord(h.t0[k], p->st);
 		if (run_pass(p, h.d_in[k], (int)cnt, h.d_out[k], h.d_steps[k])) return -1;
 		(void)hipEventRecord(h.t1[k], p->st);
+		void *odst = dout ? (void *)((char *)out + (size_t)r0 * nout * 4) : h.h_out[k];
+		void *sdst = dsteps ? (void *)(steps + (size_t)r0 * nt) : (void *)h.h_steps[k];
 		if (!hipok(hipEventRecord(h.done[k], p->st), "event") || !hipok(hipStreamWaitEvent(h.d2h, h.done[k], 0), "wait") ||
-		    !hipok(hipMemcpyAsync(h.h_out[k], h.d_out[k], (size_t)cnt * nout * 4, hipMemcpyDeviceToHost, h.d2h), "outputs to host"))
+		    !hipok(hipMemcpyAsync(odst, h.d_out[k], (size_t)cnt * nout * 4, hipMemcpyDeviceToHost, h.d2h), "outputs to host"))
 			return -1;
 		if (steps && p->m->nthink &&
-		    !hipok(hipMemcpyAsync(h.h_steps[k], h.d_steps[k], (size_t)cnt * nt * 4, hipMemcpyDeviceToHost, h.d2h), "steps to host"))
+		    !hipok(hipMemcpyAsync(sdst, h.d_steps[k], (size_t)cnt * nt * 4, hipMemcpyDeviceToHost, h.d2h), "steps to host"))
 			return -1;
 		if (!hipok(hipEventRecord(h.down[k], h.d2h), "event")) return -1;
 	}
@@ -2741,6 +2773,30 @@ void *tg_hip_dev_alloc(size_t bytes)
 }
 
 int tg_hip_dev_free(void *d) { return hipok(hipFree(d), "hipFree") ? 0 : -1; }
+
+void *tg_hip_host_alloc(size_t bytes)
+{
+	void *h = nullptr;
+	if (!hipok(hipHostMalloc(&h, bytes ? bytes : 1, 0), "pinned host memory")) return nullptr;
+	std::lock_guard<std::mutex> lk(g_pinned_mu);
+	g_pinned[(uintptr_t)h] = bytes;
+	return h;
+}
+
+int tg_hip_host_free(void *h)
+{
+	if (!h) return 0;
+	{
+		std::lock_guard<std::mutex> lk(g_pinned_mu);
+		auto it = g_pinned.find((uintptr_t)h);
+		if (it == g_pinned.end()) {
+			seterr("tg_hip_host_free: not a tg_hip_host_alloc pointer");
+			return -1;
+		}
+		g_pinned.erase(it);
+	}
+	return hipok(hipHostFree(h), "hipHostFree") ? 0 : -1;
+}
 int tg_hip_h2d(void *d, const void *h, size_t bytes) { return hipok(hipMemcpy(d, h, bytes, hipMemcpyHostToDevice), "h2d") ? 0 : -1; }
 int tg_hip_d2h(void *h, const void *d, size_t bytes) { return hipok(hipMemcpy(h, d, bytes, hipMemcpyDeviceToHost), "d2h") ? 0 : -1; }
 

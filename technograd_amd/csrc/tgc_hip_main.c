@@ -49,6 +49,7 @@
 #include "tgc_hip_cli.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <signal.h>
 #include <stdatomic.h>
 #include <stdint.h>
@@ -216,10 +217,69 @@ int parse_row(const char *s, float *v, int max, const char **bad, int fixed)
 	}
 }
 
-/* every row of DATA: f32 values, or with `fixed` Q16.16 words (binary inputs
- * are f32 either way; the caller converts them) */
-static float *load_rows(const char *path, int per, long *rows, char *err, size_t errn, int fixed)
+static int host_is_le(void)
 {
+	const uint32_t one = 1;
+	unsigned char b;
+	memcpy(&b, &one, 1);
+	return b == 1;
+}
+
+/* Row, output and step buffers: pinned host memory where the library can give
+ * it (tg_hip_batch then moves them over PCIe without a staging copy), else
+ * ordinary memory; *pinned says which, for host_buf_free. */
+static void *host_buf(size_t bytes, int *pinned)
+{
+	void *p = tg_hip_host_alloc(bytes ? bytes : 4);
+	*pinned = p != NULL;
+	return p ? p : malloc(bytes ? bytes : 4);
+}
+
+static void host_buf_free(void *p, int pinned)
+{
+	if (pinned) tg_hip_host_free(p);
+	else free(p);
+}
+
+/* a binary row file (raw little-endian f32) read straight into a row buffer */
+static float *load_binary_rows(const char *path, int per, long *rows, char *err, size_t errn, int *pinned)
+{
+	FILE *f = fopen(path, "rb");
+	long len = -1;
+	if (f && !fseek(f, 0, SEEK_END)) len = ftell(f);
+	if (len < 0 || fseek(f, 0, SEEK_SET)) {
+		snprintf(err, errn, "cannot read '%s'", path);
+		if (f) fclose(f);
+		return NULL;
+	}
+	if (len % 4 || (len / 4) % per) {
+		snprintf(err, errn, "'%s': %ld bytes is not a whole number of %d-float rows", path, len, per);
+		fclose(f);
+		return NULL;
+	}
+	float *all = host_buf((size_t)len, pinned);
+	const size_t got = all ? fread(all, 1, (size_t)len, f) : 0;
+	fclose(f);
+	if (!all || got != (size_t)len) {
+		snprintf(err, errn, "cannot read '%s'", path);
+		if (all) host_buf_free(all, *pinned);
+		return NULL;
+	}
+	if (!host_is_le()) /* the file is little-endian */
+		for (long i = 0; i < len / 4; i++) {
+			const unsigned char *b = (const unsigned char *)&all[i];
+			const uint32_t w = (uint32_t)b[0] | (uint32_t)b[1] << 8 | (uint32_t)b[2] << 16 | (uint32_t)b[3] << 24;
+			memcpy(&all[i], &w, 4);
+		}
+	*rows = len / 4 / per;
+	return all;
+}
+
+/* every row of DATA: f32 values, or with `fixed` Q16.16 words (binary inputs
+ * are f32 either way; the caller converts them), in a row buffer (host_buf) */
+static float *load_rows(const char *path, int per, long *rows, char *err, size_t errn, int fixed, int *pinned)
+{
+	if (is_binary(path)) return load_binary_rows(path, per, rows, err, errn, pinned);
 	size_t len;
 	char *raw = slurp(path, &len);
 	if (!raw) {
@@ -227,25 +287,10 @@ static float *load_rows(const char *path, int per, long *rows, char *err, size_t
 		return NULL;
 	}
 	float *all = NULL;
-	if (is_binary(path)) {
-		if (len % 4 || (len / 4) % (size_t)per) {
-			snprintf(err, errn, "'%s': %zu bytes is not a whole number of %d-float rows", path, len, per);
-			free(raw);
-			return NULL;
-		}
-		*rows = (long)(len / 4 / (size_t)per);
-		all = malloc(len ? len : 4);
-		const unsigned char *b = (const unsigned char *)raw;
-		for (size_t i = 0; i < len / 4; i++) {
-			uint32_t w = (uint32_t)b[4 * i] | (uint32_t)b[4 * i + 1] << 8 | (uint32_t)b[4 * i + 2] << 16 | (uint32_t)b[4 * i + 3] << 24;
-			memcpy(&all[i], &w, 4);
-		}
-		free(raw);
-		return all;
-	}
+	*pinned = 0;
 	long n = 0;
 	for (int pass = 0; pass < 2; pass++) { /* pass 0 validates and counts, pass 1 parses */
-		if (pass) all = malloc((size_t)(n ? n : 1) * per * sizeof *all);
+		if (pass) all = host_buf((size_t)(n ? n : 1) * per * sizeof *all, pinned);
 		long r = 0;
 		int line = 1;
 		for (char *s = raw; *s; line++) {
@@ -256,13 +301,13 @@ static float *load_rows(const char *path, int per, long *rows, char *err, size_t
 			if (k < 0) {
 				snprintf(err, errn, "%s:%d: bad number near '%.20s'", path, line, bad);
 				free(raw);
-				free(all);
+				if (all) host_buf_free(all, *pinned);
 				return NULL;
 			}
 			if (k > 0 && k != per) {
 				snprintf(err, errn, "%s:%d: row has %d values, the model needs %d", path, line, k, per);
 				free(raw);
-				free(all);
+				if (all) host_buf_free(all, *pinned);
 				return NULL;
 			}
 			if (k > 0) {
@@ -314,6 +359,10 @@ static void log_event(FILE *lf, const char *stage, const char *msg, const char *
 static void write_block(FILE *f, int obin, int fixed, const float *out, const int *steps, long n, int nout, int nthink, int nt)
 {
 	char buf[32];
+	if (obin && !fixed && host_is_le()) { /* raw f32, the memory's own bytes */
+		fwrite(out, 4, (size_t)n * nout, f);
+		return;
+	}
 	for (long r = 0; r < n; r++) {
 		const float *y = out + (size_t)r * nout;
 		if (obin) {
@@ -446,6 +495,7 @@ static int quantize(int argc, char **argv)
 	if (!text) return die("%s", lerr);
 	float *rows = NULL;
 	long nrows = 0;
+	int rows_pinned = 0;
 	if (calib) { /* the rows' width comes from the model on the device */
 		if (tg_hip_init(0)) return die("%s", tg_hip_error());
 		tg_hip_prog *p = tg_hip_load(text, mlen, 0, 1);
@@ -453,7 +503,7 @@ static int quantize(int argc, char **argv)
 		int per, nout, nthink;
 		tg_hip_info(p, &per, &nout, &nthink);
 		tg_hip_free(p);
-		rows = load_rows(calib, per, &nrows, lerr, sizeof lerr, 0);
+		rows = load_rows(calib, per, &nrows, lerr, sizeof lerr, 0, &rows_pinned);
 		if (!rows) return die("%s", lerr);
 		if (!nrows) return die("%s: no calibration rows", calib);
 	}
@@ -461,7 +511,7 @@ static int quantize(int argc, char **argv)
 	long bytes[2];
 	char *out = tg_hip_quantize_model(text, mlen, bits, gptq, rows, nrows, min_size, max_k, bytes, log, sizeof log);
 	free(text);
-	free(rows);
+	if (rows) host_buf_free(rows, rows_pinned);
 	fputs(log, stderr);
 	if (!out) return die("%s", tg_hip_error());
 	char dflt[1024];
@@ -485,6 +535,209 @@ static int quantize(int argc, char **argv)
 }
 
 #define USAGE "usage: tgc-hip batch MODEL DATA [-o OUT] [--fixed] [--exact] [--rows N] [-v] [--log FILE]%s"
+
+/* A batch in progress: the program, the output, and the summary of -v / --log. */
+typedef struct {
+	tg_hip_prog *p;
+	int per, nout, nthink, nt, fixed, obin;
+	FILE *f;
+	long done, raise_after;
+	long *ssum;
+	int *smin, *smax;
+	double dev_ms;
+	char err[256];
+} Run;
+
+/* one device pass over n rows (f32, or Q16.16 words with `fixed`) and its think steps into the summary */
+static int run_block(Run *r, const float *in, long n, float *out, int *steps)
+{
+	const int rc = r->fixed ? tg_hip_batch_fixed(r->p, (const int32_t *)in, n, (int32_t *)out, steps) : tg_hip_batch(r->p, in, n, out, steps);
+	if (rc) return rc;
+	tg_hip_stats_t st;
+	tg_hip_stats(r->p, &st);
+	r->dev_ms += st.batch_ms;
+	for (int t = 0; t < r->nthink; t++)
+		for (long i = 0; i < n; i++) {
+			const int sv = steps[(size_t)i * r->nt + t];
+			if (!r->done && !i) r->smin[t] = r->smax[t] = sv;
+			r->ssum[t] += sv;
+			r->smin[t] = sv < r->smin[t] ? sv : r->smin[t];
+			r->smax[t] = sv > r->smax[t] ? sv : r->smax[t];
+		}
+	return 0;
+}
+
+/* n more rows written; at the end of a block, the test hook's stop request */
+static void block_done(Run *r, long n, long block)
+{
+	r->done += n;
+	if (r->raise_after > 0 && r->done % block == 0 && r->done / block == r->raise_after) raise(SIGTERM);
+}
+
+/* Raw f32 rows streamed from `in` through NSLOT pinned slots: a reader thread
+ * fills a slot straight from the file (no staging copy), this thread runs the
+ * slot's device pass, a writer thread writes its outputs, so the file's
+ * reading and writing overlap the device. Chunks tile the blocks of `block`
+ * rows, and a stop request ends the batch after the block it arrives in, as
+ * the in-memory path does. Returns 0, or -1 with the reason in r->err (or
+ * tg_hip_error()). */
+enum { NSLOT = 3 };
+typedef struct {
+	Run *r;
+	FILE *in;
+	long rows, chunk, nch;
+	float *in_b[NSLOT], *out_b[NSLOT];
+	int *st_b[NSLOT];
+	int pin[NSLOT][3];
+	long n[NSLOT];
+	int state[NSLOT]; /* 0 free, 1 rows read, 2 outputs computed */
+	long last;        /* chunks the device has run: the reader and writer stop there */
+	int quit;
+	pthread_mutex_t mu;
+	pthread_cond_t cv;
+} Stream;
+
+static void *stream_reader(void *arg)
+{
+	Stream *S = arg;
+	const Run *r = S->r;
+	for (long i = 0; i < S->nch; i++) {
+		const int k = (int)(i % NSLOT);
+		pthread_mutex_lock(&S->mu);
+		while (S->state[k] != 0 && !S->quit) pthread_cond_wait(&S->cv, &S->mu);
+		const int quit = S->quit;
+		pthread_mutex_unlock(&S->mu);
+		if (quit) break;
+		const long n = S->rows - i * S->chunk < S->chunk ? S->rows - i * S->chunk : S->chunk;
+		const size_t want = (size_t)n * r->per;
+		const int ok = fread(S->in_b[k], 4, want, S->in) == want;
+		if (ok && !host_is_le()) /* the file is little-endian */
+			for (size_t j = 0; j < want; j++) {
+				const unsigned char *b = (const unsigned char *)&S->in_b[k][j];
+				const uint32_t w = (uint32_t)b[0] | (uint32_t)b[1] << 8 | (uint32_t)b[2] << 16 | (uint32_t)b[3] << 24;
+				memcpy(&S->in_b[k][j], &w, 4);
+			}
+		if (ok && r->fixed) /* f32 rows: x * 2^16 rounded half away from zero, saturated */
+			for (size_t j = 0; j < want; j++) {
+				const double v = (double)S->in_b[k][j] * 65536.0;
+				const int32_t q = v >= 2147483647.0 ? INT32_MAX : v <= -2147483648.0 ? INT32_MIN : (int32_t)llround(v);
+				memcpy(&S->in_b[k][j], &q, 4);
+			}
+		pthread_mutex_lock(&S->mu);
+		S->n[k] = ok ? n : -1;
+		S->state[k] = 1;
+		pthread_cond_broadcast(&S->cv);
+		pthread_mutex_unlock(&S->mu);
+		if (!ok) break;
+	}
+	return NULL;
+}
+
+static void *stream_writer(void *arg)
+{
+	Stream *S = arg;
+	const Run *r = S->r;
+	for (long i = 0;; i++) {
+		const int k = (int)(i % NSLOT);
+		pthread_mutex_lock(&S->mu);
+		while (S->state[k] != 2 && !(S->quit && i >= S->last)) pthread_cond_wait(&S->cv, &S->mu);
+		const int stop = S->state[k] != 2;
+		pthread_mutex_unlock(&S->mu);
+		if (stop) break;
+		write_block(r->f, r->obin, r->fixed, S->out_b[k], S->st_b[k], S->n[k], r->nout, r->nthink, r->nt);
+		pthread_mutex_lock(&S->mu);
+		S->state[k] = 0;
+		pthread_cond_broadcast(&S->cv);
+		pthread_mutex_unlock(&S->mu);
+	}
+	return NULL;
+}
+
+static int stream_rows(Run *r, FILE *in, long rows, long block)
+{
+	Stream S;
+	memset(&S, 0, sizeof S);
+	S.r = r, S.in = in, S.rows = rows;
+	const long target = (8l << 20) / (4l * (r->per > r->nout ? r->per : r->nout)); /* rows of about 8 MiB */
+	const long per_block = (block + (target > 0 ? target : 1) - 1) / (target > 0 ? target : 1);
+	S.chunk = (block + per_block - 1) / per_block; /* chunks tile each block: a stop lands on a block's end */
+	S.nch = (rows + S.chunk - 1) / S.chunk;
+	for (int k = 0; k < NSLOT; k++) {
+		S.in_b[k] = host_buf((size_t)S.chunk * r->per * 4, &S.pin[k][0]);
+		S.out_b[k] = host_buf((size_t)S.chunk * r->nout * 4, &S.pin[k][1]);
+		S.st_b[k] = host_buf((size_t)S.chunk * r->nt * 4, &S.pin[k][2]);
+		if (!S.in_b[k] || !S.out_b[k] || !S.st_b[k]) {
+			snprintf(r->err, sizeof r->err, "out of memory");
+			return -1;
+		}
+	}
+	pthread_mutex_init(&S.mu, NULL);
+	pthread_cond_init(&S.cv, NULL);
+	pthread_t rd, wr;
+	sigset_t stop, old; /* stop requests stay with this thread (the reader's and writer's I/O is not interrupted) */
+	sigemptyset(&stop);
+	sigaddset(&stop, SIGINT);
+	sigaddset(&stop, SIGTERM);
+	pthread_sigmask(SIG_BLOCK, &stop, &old);
+	const int erd = pthread_create(&rd, NULL, stream_reader, &S);
+	const int ewr = erd ? 0 : pthread_create(&wr, NULL, stream_writer, &S);
+	pthread_sigmask(SIG_SETMASK, &old, NULL);
+	if (erd) {
+		snprintf(r->err, sizeof r->err, "cannot start the reader thread");
+		return -1;
+	}
+	if (ewr) {
+		pthread_mutex_lock(&S.mu);
+		S.quit = 1;
+		pthread_cond_broadcast(&S.cv);
+		pthread_mutex_unlock(&S.mu);
+		pthread_join(rd, NULL);
+		snprintf(r->err, sizeof r->err, "cannot start the writer thread");
+		return -1;
+	}
+	int rc = 0;
+	long i = 0;
+	for (; i < S.nch; i++) {
+		const int k = (int)(i % NSLOT);
+		pthread_mutex_lock(&S.mu);
+		while (S.state[k] != 1) pthread_cond_wait(&S.cv, &S.mu);
+		const long n = S.n[k];
+		pthread_mutex_unlock(&S.mu);
+		if (n < 0) {
+			snprintf(r->err, sizeof r->err, "cannot read the rows");
+			rc = -1;
+			break;
+		}
+		if (run_block(r, S.in_b[k], n, S.out_b[k], S.st_b[k])) {
+			rc = -1;
+			break;
+		}
+		pthread_mutex_lock(&S.mu);
+		S.state[k] = 2;
+		pthread_cond_broadcast(&S.cv);
+		pthread_mutex_unlock(&S.mu);
+		block_done(r, n, block);
+		if (atomic_load(&stop_sig) && (r->done % block == 0 || r->done == rows)) {
+			i++;
+			break; /* a stop request: this block is the last */
+		}
+	}
+	pthread_mutex_lock(&S.mu); /* the reader stops, the writer writes the chunks computed (i of them) and stops */
+	S.last = i;
+	S.quit = 1;
+	pthread_cond_broadcast(&S.cv);
+	pthread_mutex_unlock(&S.mu);
+	pthread_join(rd, NULL);
+	pthread_join(wr, NULL);
+	pthread_mutex_destroy(&S.mu);
+	pthread_cond_destroy(&S.cv);
+	for (int k = 0; k < NSLOT; k++) {
+		host_buf_free(S.in_b[k], S.pin[k][0]);
+		host_buf_free(S.out_b[k], S.pin[k][1]);
+		host_buf_free(S.st_b[k], S.pin[k][2]);
+	}
+	return rc;
+}
 
 int main(int argc, char **argv)
 {
@@ -531,50 +784,56 @@ int main(int argc, char **argv)
 	if (!p) return die("%s", tg_hip_error());
 	int per, nout, nthink;
 	tg_hip_info(p, &per, &nout, &nthink);
-	int nt = nthink ? nthink : 1;
+	Run run = { .p = p, .per = per, .nout = nout, .nthink = nthink, .nt = nthink ? nthink : 1, .fixed = fixed };
 	char err[512];
 	long rows;
 	double tb = now_ms(); /* the reference's batch timer starts before the input load (src/main.c:413) */
-	float *all = load_rows(data, per, &rows, err, sizeof err, fixed && !is_binary(data)); /* validated before the output exists */
-	if (!all) return die("%s", err);
-	if (fixed && is_binary(data)) /* f32 rows: x * 2^16 rounded half away from zero, saturated */
-		for (long i = 0; i < rows * per; i++) {
-			double v = (double)all[i] * 65536.0;
-			int32_t q = v >= 2147483647.0 ? INT32_MAX : v <= -2147483648.0 ? INT32_MIN : (int32_t)llround(v);
-			memcpy(&all[i], &q, 4);
-		}
-	install_signals(); /* a stop request ends the batch after the current block */
+	install_signals();    /* a stop request ends the batch after the current block */
 	const char *ra = getenv("TGC_HIP_TEST_SIGTERM_AFTER_BLOCKS");
-	const long raise_after = ra ? atol(ra) : 0;
-	int obin = opath && is_binary(opath);
-	FILE *f = opath ? fopen(opath, obin ? "wb" : "w") : stdout;
-	if (!f) return die("cannot write '%s'", opath);
-	const long block = maxrows;
-	float *out = malloc((size_t)(rows < block ? (rows ? rows : 1) : block) * nout * sizeof *out);
-	int *steps = malloc((size_t)(rows < block ? (rows ? rows : 1) : block) * nt * sizeof *steps);
-	long *ssum = calloc((size_t)nt, sizeof *ssum), done = 0;
-	int *smin = calloc((size_t)nt, sizeof *smin), *smax = calloc((size_t)nt, sizeof *smax);
-	double dev_ms = 0;
-	for (long b0 = 0; b0 < rows && !atomic_load(&stop_sig); b0 += block) {
-		const long n = rows - b0 < block ? rows - b0 : block;
-		int rc = fixed ? tg_hip_batch_fixed(p, (const int32_t *)(all + (size_t)b0 * per), n, (int32_t *)out, steps)
-			       : tg_hip_batch(p, all + (size_t)b0 * per, n, out, steps);
-		if (rc) return die("%s", tg_hip_error());
-		tg_hip_stats_t st;
-		tg_hip_stats(p, &st);
-		dev_ms += st.batch_ms;
-		for (int t = 0; t < nthink; t++)
-			for (long r = 0; r < n; r++) {
-				const int sv = steps[(size_t)r * nt + t];
-				if (!done && !r) smin[t] = smax[t] = sv;
-				ssum[t] += sv;
-				smin[t] = sv < smin[t] ? sv : smin[t];
-				smax[t] = sv > smax[t] ? sv : smax[t];
-			}
-		write_block(f, obin, fixed, out, steps, n, nout, nthink, nt);
-		done += n;
-		if (raise_after > 0 && done / block == raise_after) raise(SIGTERM); /* test hook: a stop request from outside */
+	run.raise_after = ra ? atol(ra) : 0;
+	run.obin = opath && is_binary(opath);
+	run.ssum = calloc((size_t)run.nt, sizeof *run.ssum);
+	run.smin = calloc((size_t)run.nt, sizeof *run.smin);
+	run.smax = calloc((size_t)run.nt, sizeof *run.smax);
+	FILE *f = NULL;
+	if (is_binary(data)) { /* raw f32 rows: checked by size, then streamed through pinned slots */
+		FILE *in = fopen(data, "rb");
+		long len = -1;
+		if (in && !fseek(in, 0, SEEK_END)) len = ftell(in);
+		if (len < 0 || fseek(in, 0, SEEK_SET)) return die("cannot read '%s'", data);
+		if (len % 4 || (len / 4) % per) {
+			snprintf(err, sizeof err, "'%s': %ld bytes is not a whole number of %d-float rows", data, len, per);
+			return die("%s", err);
+		}
+		rows = len / 4 / per;
+		if (!(f = opath ? fopen(opath, run.obin ? "wb" : "w") : stdout)) return die("cannot write '%s'", opath);
+		run.f = f;
+		if (stream_rows(&run, in, rows, maxrows)) return die("%s", run.err[0] ? run.err : tg_hip_error());
+		fclose(in);
+	} else {
+		int rows_pinned;
+		float *all = load_rows(data, per, &rows, err, sizeof err, fixed, &rows_pinned); /* validated before the output exists */
+		if (!all) return die("%s", err);
+		if (!(f = opath ? fopen(opath, run.obin ? "wb" : "w") : stdout)) return die("cannot write '%s'", opath);
+		run.f = f;
+		const long block = maxrows;
+		int out_pinned, steps_pinned;
+		float *out = host_buf((size_t)(rows < block ? (rows ? rows : 1) : block) * nout * sizeof *out, &out_pinned);
+		int *steps = host_buf((size_t)(rows < block ? (rows ? rows : 1) : block) * run.nt * sizeof *steps, &steps_pinned);
+		for (long b0 = 0; b0 < rows && !atomic_load(&stop_sig); b0 += block) {
+			const long n = rows - b0 < block ? rows - b0 : block;
+			if (run_block(&run, all + (size_t)b0 * per, n, out, steps)) return die("%s", tg_hip_error());
+			write_block(f, run.obin, fixed, out, steps, n, nout, nthink, run.nt);
+			block_done(&run, n, block);
+		}
+		host_buf_free(all, rows_pinned);
+		host_buf_free(out, out_pinned);
+		host_buf_free(steps, steps_pinned);
 	}
+	const long done = run.done;
+	const double dev_ms = run.dev_ms;
+	long *ssum = run.ssum;
+	int *smin = run.smin, *smax = run.smax;
 	if (opath && (ferror(f) | fclose(f))) return die("write failed '%s'", opath);
 	const double ms = now_ms() - tb;
 	if (verbose || lf) {
@@ -599,9 +858,6 @@ int main(int argc, char **argv)
 	}
 	if (lf) fclose(lf);
 	tg_hip_free(p);
-	free(all);
-	free(out);
-	free(steps);
 	free(ssum);
 	free(smin);
 	free(smax);

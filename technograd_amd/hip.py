@@ -72,6 +72,9 @@ def lib():
         L.tg_hip_dev_alloc.restype = vp
         L.tg_hip_dev_alloc.argtypes = [sz]
         L.tg_hip_dev_free.argtypes = [vp]
+        L.tg_hip_host_alloc.restype = vp
+        L.tg_hip_host_alloc.argtypes = [sz]
+        L.tg_hip_host_free.argtypes = [vp]
         L.tg_hip_h2d.argtypes = [vp, vp, sz]
         L.tg_hip_d2h.argtypes = [vp, vp, sz]
         _lib = L
@@ -121,6 +124,33 @@ class DeviceBuffer:
         self.free()
 
 
+class HostBuffer:
+    """Pinned host memory from tg_hip_host_alloc: rows and outputs inside it
+    travel to and from the device without tg_hip_batch's staging copy."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = lib().tg_hip_host_alloc(self.nbytes)
+        if not self.ptr:
+            raise RuntimeError("tg_hip_host_alloc: " + lib().tg_hip_error().decode())
+
+    def array(self, dtype, shape):
+        """a numpy view of the buffer (valid until free)"""
+        dtype = np.dtype(dtype)
+        n = int(np.prod(shape)) * dtype.itemsize
+        if n > self.nbytes:
+            raise ValueError("view of %d bytes in a %d-byte buffer" % (n, self.nbytes))
+        return np.frombuffer((ctypes.c_char * n).from_address(self.ptr), dtype).reshape(shape)
+
+    def free(self):
+        if self.ptr:
+            lib().tg_hip_host_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        self.free()
+
+
 class Program:
     """A model loaded on the device (tg_hip_load)."""
 
@@ -144,10 +174,17 @@ class Program:
     def __del__(self):
         self.close()
 
-    def batch(self, rows):
+    def batch(self, rows, out=None, steps=None):
+        """rows [n, per] -> (out [n, nout], steps [n, max(nthink, 1)]); out and
+        steps may be given (C-contiguous f32 / int32 arrays, e.g. views of a
+        HostBuffer)"""
         rows = np.ascontiguousarray(rows, dtype=np.float32).reshape(-1, self.per)
-        out = np.empty((rows.shape[0], self.nout), np.float32)
-        steps = np.zeros((rows.shape[0], max(self.nthink, 1)), np.int32)
+        if out is None:
+            out = np.empty((rows.shape[0], self.nout), np.float32)
+        if steps is None:
+            steps = np.zeros((rows.shape[0], max(self.nthink, 1)), np.int32)
+        assert out.dtype == np.float32 and out.flags.c_contiguous and out.size == rows.shape[0] * self.nout
+        assert steps.dtype == np.int32 and steps.flags.c_contiguous and steps.size == rows.shape[0] * max(self.nthink, 1)
         _check(lib().tg_hip_batch(self.h, _p(rows), rows.shape[0], _p(out), _p(steps)), "tg_hip_batch")
         return out, steps
 

@@ -25,6 +25,8 @@
  *                                             the fixed-point tokens through fx_parse, files through load_rows
  *   host_fuzz http  SEED ITERS MODEL.tgir     mutated HTTP requests and row sessions through the server's
  *                                             connection handler over a socket pair (f32 and --fixed)
+ *   host_fuzz cli   SEED ITERS MODEL.tgir     `tgc-hip batch` end to end: binary rows (streamed) against the
+ *                                             same rows as text, byte for byte, with random blocks and stops
  */
 #define main tgc_hip_cli_main
 #include "../../technograd_amd/csrc/tgc_hip_main.c"
@@ -112,6 +114,13 @@ int tg_hip_stats(const tg_hip_prog *p, tg_hip_stats_t *st)
 {
 	(void)p;
 	memset(st, 0, sizeof *st);
+	return 0;
+}
+
+void *tg_hip_host_alloc(size_t bytes) { return malloc(bytes ? bytes : 1); }
+int tg_hip_host_free(void *h)
+{
+	free(h);
 	return 0;
 }
 
@@ -518,12 +527,17 @@ static int fuzz_rows(long iters)
 			fclose(f);
 			long rows;
 			const int per = 1 + (int)below(4);
-			for (int fixed = 0; fixed < 2; fixed++) free(load_rows(tpath, per, &rows, err, sizeof err, fixed));
+			int pinned;
+			for (int fixed = 0; fixed < 2; fixed++) {
+				float *all = load_rows(tpath, per, &rows, err, sizeof err, fixed, &pinned);
+				if (all) host_buf_free(all, pinned);
+			}
 			f = fopen(bpath, "wb");
 			const size_t nb = below(64);
 			for (size_t i = 0; i < nb; i++) fputc((int)(rnd() & 0xff), f);
 			fclose(f);
-			free(load_rows(bpath, per, &rows, err, sizeof err, 0));
+			float *all = load_rows(bpath, per, &rows, err, sizeof err, 0, &pinned);
+			if (all) host_buf_free(all, pinned);
 		}
 		free(t);
 	}
@@ -540,15 +554,19 @@ typedef struct {
 	int fd;
 	const char *data;
 	size_t len;
-	size_t got; /* bytes read back */
+	size_t got;   /* bytes read back */
+	uint64_t rng; /* the writer's own generator (threads do not share rnd's state) */
 } Peer;
 
 static void *peer_write(void *arg)
 {
 	Peer *p = arg;
 	size_t off = 0;
+	uint64_t x = p->rng | 1;
 	while (off < p->len) { /* in pieces of random size, as a network would */
-		size_t k = 1 + below(p->len - off < 4096 ? p->len - off : 4096);
+		x ^= x << 13, x ^= x >> 7, x ^= x << 17;
+		const size_t span = p->len - off < 4096 ? p->len - off : 4096;
+		size_t k = 1 + (size_t)(x % span);
 		ssize_t w = write(p->fd, p->data + off, k);
 		if (w <= 0) break;
 		off += (size_t)w;
@@ -577,6 +595,38 @@ static const char *const HTTP_SEEDS[] = {
 	"1 2 3 4\n# comment\n\n5,6,7,8\n1 2\nx\n",
 	"0.5 0.25 -1 100000\r\n1e-7 3 3 3",
 };
+
+typedef struct {
+	Server *S;
+	const char *req;
+	size_t got;
+	uint64_t rng;
+} Client;
+
+/* one connection of a burst: a socket pair, the server's handler on one end in
+ * this thread, the request written and the answer read on the other */
+static void *burst_client(void *arg)
+{
+	Client *c = arg;
+	int sv[2];
+	if (socketpair(AF_UNIX, SOCK_STREAM, 0, sv)) return NULL;
+	Peer w = { sv[1], c->req, strlen(c->req), 0, c->rng }, r = { dup(sv[1]), NULL, 0, 0, 0 };
+	pthread_t tw, tr;
+	pthread_create(&tw, NULL, peer_write, &w);
+	pthread_create(&tr, NULL, peer_read, &r);
+	Conn *cn = malloc(sizeof *cn);
+	*cn = (Conn){ c->S, sv[0] };
+	pthread_mutex_lock(&c->S->mu);
+	c->S->active++;
+	pthread_mutex_unlock(&c->S->mu);
+	conn_main(cn);
+	pthread_join(tw, NULL);
+	pthread_join(tr, NULL);
+	close(sv[1]);
+	close(r.fd);
+	c->got = r.got;
+	return NULL;
+}
 
 static int fuzz_http(long iters, const char *model)
 {
@@ -608,7 +658,7 @@ static int fuzz_http(long iters, const char *model)
 		}
 		int sv[2];
 		if (socketpair(AF_UNIX, SOCK_STREAM, 0, sv)) return 2;
-		Peer w = { sv[1], t, len, 0 }, r = { dup(sv[1]), NULL, 0, 0 };
+		Peer w = { sv[1], t, len, 0, rnd() }, r = { dup(sv[1]), NULL, 0, 0, 0 };
 		pthread_t tw, tr;
 		pthread_create(&tw, NULL, peer_write, &w);
 		pthread_create(&tr, NULL, peer_read, &r);
@@ -625,12 +675,123 @@ static int fuzz_http(long iters, const char *model)
 		close(r.fd);
 		answered += r.got > 0;
 		free(t);
+		if (it % 100 == 99) { /* a burst of 8 connections at once into one batcher */
+			Client cl[8];
+			pthread_t th[8];
+			for (int c = 0; c < 8; c++) {
+				cl[c] = (Client){ &S[0], HTTP_SEEDS[c % 2 ? 2 : 8], 0, rnd() };
+				pthread_create(&th[c], NULL, burst_client, &cl[c]);
+			}
+			for (int c = 0; c < 8; c++) {
+				pthread_join(th[c], NULL);
+				if (!cl[c].got) {
+					fprintf(stderr, "host_fuzz http: a burst connection got no answer (case %ld)\n", it);
+					return 1;
+				}
+			}
+		}
 	}
 	for (int fx = 0; fx < 2; fx++) {
 		batcher_stop(&B[fx]);
 		pthread_mutex_destroy(&S[fx].mu);
 	}
 	printf("http: %ld cases, %zu answered\n", iters, answered);
+	return 0;
+}
+
+/* --------------------------------------------------------------- cli --- */
+
+static int file_eq(const char *a, const char *b)
+{
+	size_t na, nb;
+	char *x = read_file(a, &na), *y = read_file(b, &nb);
+	const int eq = na == nb && !memcmp(x, y, na);
+	free(x);
+	free(y);
+	return eq;
+}
+
+/* `tgc-hip batch` end to end on the device double: raw f32 rows (streamed
+ * through the pinned slots by reader and writer threads) against the same
+ * rows as text (read whole), byte for byte in text and binary output, f32 and
+ * --fixed, blocks that do and do not divide the rows, and a stop request
+ * after a block (the output holds exactly the blocks before it) */
+static int check_cli(long iters, const char *model)
+{
+	char tmpl[] = "/tmp/host_fuzz_cli_XXXXXX";
+	char *dir = mkdtemp(tmpl);
+	if (!dir) return 2;
+	size_t mlen;
+	char *mt = read_file(model, &mlen);
+	char err[512];
+	tgm_module *m = tgm_read(mt, mlen, err, sizeof err);
+	free(mt);
+	if (!m) return 2;
+	const long per = m->per, nout = m->nout;
+	tgm_free(m);
+	char bin[4096], txt[4096], o1[4096], o2[4096];
+	snprintf(bin, sizeof bin, "%s/x.bin", dir);
+	snprintf(txt, sizeof txt, "%s/x.txt", dir);
+	long cases = 0;
+	for (long it = 0; it < iters; it++) {
+		const long rows = (long)below(40) + (it % 5 == 0 ? (long)below(3000) : 0);
+		const long block = 1 + (long)below(it % 3 ? 64 : 4096);
+		const int fixed = (int)(rnd() & 1), tbin = (int)(rnd() & 1);
+		const long stop_after = rnd() % 4 == 0 ? 1 + (long)below(3) : 0;
+		FILE *fb = fopen(bin, "wb"), *ft = fopen(txt, "w");
+		for (long r = 0; r < rows; r++) {
+			for (long j = 0; j < per; j++) {
+				/* values exact in Q16.16 (multiples of 2^-8), so both readers agree in --fixed too */
+				const float v = (float)((long)below(8192) - 4096) / 256.0f;
+				fwrite(&v, 4, 1, fb);
+				fprintf(ft, "%s%.9g", j ? "," : "", (double)v);
+			}
+			fputc('\n', ft);
+		}
+		fclose(fb);
+		fclose(ft);
+		snprintf(o1, sizeof o1, "%s/y1.%s", dir, tbin ? "bin" : "txt");
+		snprintf(o2, sizeof o2, "%s/y2.%s", dir, tbin ? "bin" : "txt");
+		char bs[32];
+		snprintf(bs, sizeof bs, "%ld", block);
+		char sa[32];
+		snprintf(sa, sizeof sa, "%ld", stop_after);
+		int rc[2];
+		for (int v = 0; v < 2; v++) {
+			char *args[] = { "tgc-hip", "batch", (char *)model, v ? txt : bin, "-o", v ? o2 : o1, "--rows", bs, fixed ? "--fixed" : NULL, NULL };
+			if (stop_after) setenv("TGC_HIP_TEST_SIGTERM_AFTER_BLOCKS", sa, 1);
+			atomic_store(&stop_sig, 0);
+			rc[v] = tgc_hip_cli_main(fixed ? 9 : 8, args);
+			unsetenv("TGC_HIP_TEST_SIGTERM_AFTER_BLOCKS");
+			atomic_store(&stop_sig, 0);
+		}
+		signal(SIGPIPE, SIG_IGN);
+		const int stopped = stop_after && rows >= stop_after * block; /* the hook raises at the end of block stop_after */
+		if (rc[0] != rc[1] || rc[0] != (stopped ? 128 + SIGTERM : 0) || !file_eq(o1, o2)) {
+			fprintf(stderr, "host_fuzz cli: case %ld (rows %ld block %ld fixed %d binary out %d stop %ld): rc %d %d, outputs %s\n", it, rows,
+				block, fixed, tbin, stop_after, rc[0], rc[1], file_eq(o1, o2) ? "equal" : "differ");
+			return 1;
+		}
+		if (stopped) { /* exactly the blocks before the stop */
+			size_t n;
+			char *y = read_file(o1, &n);
+			long lines = 0;
+			for (size_t i = 0; i < n; i++) lines += y[i] == '\n';
+			free(y);
+			const long want = stop_after * block;
+			if (tbin ? n != (size_t)want * (size_t)nout * 4 : lines != want) {
+				fprintf(stderr, "host_fuzz cli: case %ld stopped with the wrong amount of output\n", it);
+				return 1;
+			}
+		}
+		cases++;
+	}
+	unlink(bin), unlink(txt), unlink(o1), unlink(o2);
+	char y1[4096], y2[4096];
+	snprintf(y1, sizeof y1, "%s/y1.bin", dir), snprintf(y2, sizeof y2, "%s/y2.bin", dir), unlink(y1), unlink(y2);
+	snprintf(y1, sizeof y1, "%s/y1.txt", dir), snprintf(y2, sizeof y2, "%s/y2.txt", dir), unlink(y1), unlink(y2);
+	rmdir(dir);
+	printf("cli: %ld cases\n", cases);
 	return 0;
 }
 
@@ -651,6 +812,7 @@ int main(int argc, char **argv)
 	}
 	if (!strcmp(argv[1], "rows")) return fuzz_rows(iters);
 	if (!strcmp(argv[1], "http") && argc == 5) return fuzz_http(iters, argv[4]);
+	if (!strcmp(argv[1], "cli") && argc == 5) return check_cli(iters, argv[4]);
 	fprintf(stderr, "host_fuzz: unknown mode '%s'\n", argv[1]);
 	return 2;
 }

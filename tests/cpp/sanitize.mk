@@ -35,6 +35,12 @@ $(OUT)/obj/%.o: $(SRC)/%.c $(SRC)/tgm.h $(SRC)/tg_front.h $(SRC)/tg_gptq.h inclu
 $(OUT)/host_fuzz: tests/cpp/host_fuzz.c $(HOST_C:%=$(OUT)/obj/%.o) $(SRC)/tgc_hip_main.c $(SRC)/tgc_hip_serve.c
 	$(CC) $(CFLAGS_S) -o $@ tests/cpp/host_fuzz.c $(HOST_C:%=$(OUT)/obj/%.o) -lm -lpthread
 
+# the same harness under ThreadSanitizer, for the threaded parts (the server's
+# batcher and connections, the batch driver's reader and writer)
+$(OUT)/host_fuzz_tsan: tests/cpp/host_fuzz.c $(HOST_C:%=$(SRC)/%.c) $(SRC)/tgc_hip_main.c $(SRC)/tgc_hip_serve.c
+	$(CC) -std=gnu11 -O1 -g -pthread -ffp-contract=off -Iinclude -I$(SRC) -fsanitize=thread -o $@ tests/cpp/host_fuzz.c \
+	    $(HOST_C:%=$(SRC)/%.c) -lm -lpthread
+
 # the ordinary build's HIP objects, linked with the instrumented host objects;
 # the sanitizer runtimes come from the driver (or LD_PRELOAD under Python)
 $(OUT)/lib/libtg_hip.so: $(HOST_C:%=$(OUT)/obj/%.o) $(HIP_OBJ:%=technograd_amd/build/%.o)
@@ -45,13 +51,17 @@ $(OUT)/bin/tgc-hip: $(SRC)/tgc_hip_main.c $(SRC)/tgc_hip_serve.c $(OUT)/lib/libt
 	@mkdir -p $(OUT)/bin
 	$(CC) $(CFLAGS_S) -o $@ $(SRC)/tgc_hip_main.c $(SRC)/tgc_hip_serve.c -L$(OUT)/lib -ltg_hip -Wl,-rpath,'$$ORIGIN/../lib' -lm -lpthread
 
-check: $(OUT)/host_fuzz
+check: $(OUT)/host_fuzz $(OUT)/host_fuzz_tsan
 	$(OUT)/host_fuzz tgir $(SEED) $(ITERS) tests/golden/haltm_f32.tgir tests/golden/opsmix_f32.tgir tests/golden/latent_q4g.tgir \
 	    tests/golden/ssm_small_q8.tgir tests/golden/qmlp_q4.tgir tests/golden/latent_f32.tgir
 	$(OUT)/host_fuzz front $(SEED) $(ITERS) tests/golden/front/*.tg tests/golden/models/*.tg
 	$(OUT)/host_fuzz gptq $(SEED) $$(( $(ITERS) / 20 + 1 )) tests/golden/qmlp_f32.tgir tests/golden/latent_f32.tgir tests/golden/haltm_f32.tgir
 	$(OUT)/host_fuzz rows $(SEED) $$(( $(ITERS) * 10 ))
 	$(OUT)/host_fuzz http $(SEED) $(ITERS) tests/golden/latent_f32.tgir
+	$(OUT)/host_fuzz cli $(SEED) $$(( $(ITERS) / 10 + 1 )) tests/golden/latent_f32.tgir
+	$(OUT)/host_fuzz cli $(SEED) $$(( $(ITERS) / 10 + 1 )) tests/golden/qmlp_q4.tgir
+	TSAN_OPTIONS=halt_on_error=1 $(OUT)/host_fuzz_tsan http $(SEED) $$(( $(ITERS) / 4 + 1 )) tests/golden/latent_f32.tgir
+	TSAN_OPTIONS=halt_on_error=1 $(OUT)/host_fuzz_tsan cli $(SEED) $$(( $(ITERS) / 20 + 1 )) tests/golden/latent_f32.tgir
 
 # the CPU tests that drive the host code, against the instrumented library and driver
 pytest: $(OUT)/lib/libtg_hip.so $(OUT)/bin/tgc-hip
