@@ -273,6 +273,8 @@ def profile_child(mode):
         # the read floor: a plain read of a span the size of the packed weight, cold like the calls
         span = hip.DeviceBuffer(FLOOR_BYTES)
         calls += [("floor", lambda: hip.read_pass(span.ptr, FLOOR_BYTES, 2048, prog.stream()))] * 2
+        # and at the single-row kernel's launch shape (256 workgroups of 256 threads)
+        calls += [("floor256", lambda: hip.read_pass(span.ptr, FLOOR_BYTES, 256, prog.stream()))] * 2
     else:
         import numpy as np
         rows = 1048576
@@ -282,6 +284,11 @@ def profile_child(mode):
         calls = [(rows, lambda: prog.batch_device(d_x.ptr, rows, d_y.ptr, d_s.ptr))] * 2
     fprog, fin, fout = flush_program(hip)
     fprog.set_stream(prog.stream())
+    warmed = set()
+    for lab, call in calls:  # each kind of call once before the profiled ones (before the first flush: not
+        if lab not in warmed:  # counted), so first-launch costs stay out of the cold calls
+            warmed.add(lab)
+            call()
     for _, call in calls:
         fprog.batch_device(fin.ptr, FLUSH_ROWS, fout.ptr)
         call()
@@ -365,11 +372,12 @@ def profile_c2(alg_bytes):
     finally:
         shutil.rmtree(out, ignore_errors=True)
     nb = 2 * len(BATCHES)
-    if not kt or len(kt[0]) != nb + 2:
+    if not kt or len(kt[0]) != nb + 4:
         return None, "kernel trace: %s segments" % (None if not kt else len(kt[0]))
     res = {b: {"kernels_us": {}} for b in BATCHES}
-    fl = [v["us"] for seg in kt[0][nb:] for _, _, v in seg]
-    res["floor"] = {"us": round(sum(fl) / max(len(fl), 1), 3), "bytes": FLOOR_BYTES}
+    for key, segs in (("floor", kt[0][nb:nb + 2]), ("floor256", kt[0][nb + 2:])):
+        fl = [v["us"] for seg in segs for _, _, v in seg]
+        res[key] = {"us": round(sum(fl) / max(len(fl), 1), 3), "bytes": FLOOR_BYTES}
     for i, seg in enumerate(kt[0][:nb]):  # two calls per batch: averages
         r = res[BATCHES[i % len(BATCHES)]]
         for n, _, v in seg:
@@ -379,9 +387,10 @@ def profile_c2(alg_bytes):
         r["kernels_us"] = {k: round(v, 3) for k, v in r["kernels_us"].items()}
         r["us"] = round(sum(r["kernels_us"].values()), 3)
     note = "kernel trace of two cold calls per batch"
-    if fe and wr and len(fe[0]) == len(wr[0]) == nb + 2:
+    if fe and wr and len(fe[0]) == len(wr[0]) == nb + 4:
         tr, rf, rw = calibrated_traffic(fe, wr)
-        res["floor"]["traffic"] = round(sum(t for t, _ in tr[nb:]) / 2)
+        res["floor"]["traffic"] = round(sum(t for t, _ in tr[nb:nb + 2]) / 2)
+        res["floor256"]["traffic"] = round(sum(t for t, _ in tr[nb + 2:]) / 2)
         for i, (tot, per) in enumerate(tr[:nb]):
             r = res[BATCHES[i % len(BATCHES)]]
             r["traffic"] = r.get("traffic", 0.0) + tot / 2
@@ -990,6 +999,12 @@ def main():
                                         "on this device"}
             for b in (1, 16):
                 mv["b%d" % b]["of_read_floor"] = round(fl["us"] / mv["b%d" % b]["us"], 4)
+        f2 = prof.get("floor256", {})
+        if f2.get("us"):
+            mv["read_floor_256wg"] = {"us": f2["us"], "bytes": f2["bytes"], "traffic": f2.get("traffic"),
+                                      "note": "the same read in 256 workgroups of 256 threads, the B=1 kernel's "
+                                              "launch shape: a cold read spread over fewer workgroups takes longer"}
+            mv["b1"]["of_read_floor_256wg"] = round(f2["us"] / mv["b1"]["us"], 4)
         mv["note"] = ("int4 matvec: algorithmic bytes (weights, scales, rows in and out) over the summed kernel-trace "
                       "durations of the call's kernels (one kernel at B=1: its digits are made inside it), each call "
                       "after a 512 MiB flush pass; traffic: calibrated FETCH_SIZE + WRITE_SIZE of the same kernels; "

@@ -274,7 +274,7 @@ __global__ __launch_bounds__(WO_TPB) void dec_wo_k(const float *att, const int *
 			ld(gi, v);
 			tgq_coarse16(co, v, E0);
 		}
-		if (tgq_coarse_grid(tgq_coarse_wave_sum(co), (int)(tq[t] >> TGQ_TALLY_SHIFT))) {
+		if (tgq_coarse_grid(tgq_coarse_wave_sum(co), tq[t])) {
 			if (lane == 0) sp[t] = 0;
 			continue;
 		}
@@ -368,9 +368,9 @@ __device__ inline float blk_max(float v, float *red)
 	return m;
 }
 
-// N sums over the block (red: [N][16] in LDS), every thread gets them
+// N sums over the block (red: [N][16] in LDS), for thread 0 only
 template <int N>
-__device__ inline void blk_sums(unsigned long long (&v)[N], unsigned long long *red)
+__device__ inline void blk_sums0(unsigned long long (&v)[N], unsigned long long *red)
 {
 	for (int w = 32; w > 0; w >>= 1)
 		for (int i = 0; i < N; i++) v[i] += __shfl_xor(v[i], w);
@@ -378,11 +378,12 @@ __device__ inline void blk_sums(unsigned long long (&v)[N], unsigned long long *
 	if ((threadIdx.x & 63) == 0)
 		for (int i = 0; i < N; i++) red[i * 16 + (threadIdx.x >> 6)] = v[i];
 	__syncthreads();
-	for (int i = 0; i < N; i++) {
-		unsigned long long t = 0;
-		for (int u = 0; u < (int)(blockDim.x >> 6); u++) t += red[i * 16 + u];
-		v[i] = t;
-	}
+	if (threadIdx.x == 0)
+		for (int i = 0; i < N; i++) {
+			unsigned long long t = 0;
+			for (int u = 0; u < (int)(blockDim.x >> 6); u++) t += red[i * 16 + u];
+			v[i] = t;
+		}
 }
 
 // digits of row m of K inputs, values z[0 .. Kp) in LDS (zero from K on), from
@@ -405,13 +406,27 @@ __device__ inline void blk_digits(const float *z, int K, int Kp, float mx, int b
 		qs += tgq_put16(blk, 16 * j, v, E, special, tl);
 		if (!special) tgq_coarse16(co, v, E);
 	}
-	unsigned long long sums[6] = { (unsigned long long)qs, (unsigned long long)tl, co.cnt, co.m0, co.m1, co.mt };
-	blk_sums(sums, redl);
-	qs = (long long)sums[0], tl = (long long)sums[1];
-	co = TgqCoarse{ sums[2], sums[3], sums[4], sums[5] };
-	int cls = special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID;
-	if (cls == TGQ_CAND && tgq_coarse_grid(co, (int)(tl >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
-	if (threadIdx.x == 0) q.e[m] = E, q.special[m] = cls, q.qsum[m] = qs;
+	unsigned long long sums[5] = { (unsigned long long)qs, (unsigned long long)tl, co.cnt, co.s0, co.s1 };
+	blk_sums0(sums, redl);
+	__shared__ int scls;
+	if (threadIdx.x == 0) {
+		qs = (long long)sums[0], tl = (long long)sums[1];
+		co = TgqCoarse{ sums[2], sums[3], sums[4] };
+		int cls = special ? TGQ_REF : tgq_candidate(tl) ? TGQ_CAND : TGQ_GRID;
+		if (cls == TGQ_CAND && tgq_coarse_grid(co, tl)) cls = TGQ_GRID;
+		q.e[m] = E, q.special[m] = cls, q.qsum[m] = qs;
+		scls = cls;
+	}
+	__syncthreads();
+	if (scls == TGQ_CAND && threadIdx.x < 64) { // a candidate the coarse test leaves: wave 0 resolves it (the row is in z)
+		__shared__ TgqHist hist;
+		const int nout = tgq_nout(Kp);
+		auto ld = [&](int g, float *v) {
+			for (int i = 0; i < 16; i++) v[i] = z[16 * g + i];
+		};
+		tgq_resolve_row(&hist, ld, K, Kp, E, blk, &q.qsum[m], &q.e[m], &q.special[m], q.ok + (long)m * nout, q.ox + (long)m * nout, nout,
+				(int)threadIdx.x);
+	}
 }
 
 // tgk_dec_norm: one block per token row, NORM_TPB threads, each with at most
@@ -426,7 +441,7 @@ __global__ __launch_bounds__(NORM_TPB) void dec_norm_k(tgk_dec_norm_args a)
 	extern __shared__ float4 zs4[]; // [Kp] values, [Kp] squares (16-byte aligned)
 	float *zs = (float *)zs4;
 	__shared__ float redf[16], inv_s;
-	__shared__ unsigned long long redl[6 * 16];
+	__shared__ unsigned long long redl[5 * 16];
 	const int t = blockIdx.x, D = a.D, Kp = a.Kp, tid = threadIdx.x;
 	float *z = zs, *sq = zs + Kp, *hr = a.h + (long)t * a.hs;
 	float v[NORM_EPT], g[NORM_EPT];
@@ -538,9 +553,18 @@ __global__ __launch_bounds__(256) void dec_hnorm_k(tgk_dec_hnorm_args a)
 			for (int u = 0; u < 16; u++) v[u] = z[16 * g + u];
 			tgq_coarse16(co, v, E);
 		}
-		if (tgq_coarse_grid(tgq_coarse_wave_sum(co), (int)(tl >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
+		if (tgq_coarse_grid(tgq_coarse_wave_sum(co), tl)) cls = TGQ_GRID;
 	}
 	if (lane == 0) a.q.e[L] = E, a.q.special[L] = cls, a.q.qsum[L] = qs;
+	if (cls == TGQ_CAND) { // the wave resolves its line (in z)
+		__shared__ TgqHist hist[4];
+		const int nout = tgq_nout(Kp);
+		auto ld = [&](int g, float *v) {
+			for (int i = 0; i < 16; i++) v[i] = z[16 * g + i];
+		};
+		tgq_resolve_row(&hist[threadIdx.x >> 6], ld, HD, Kp, E, blk, &a.q.qsum[L], &a.q.e[L], &a.q.special[L], a.q.ok + L * nout,
+				a.q.ox + L * nout, nout, lane);
+	}
 }
 
 // Many lines at once (a prompt's token rows, or its head lines): a block of
@@ -681,8 +705,8 @@ __global__ __launch_bounds__(NL_TPB) void norm_lines_k(NormLines a)
 			tgq_coarse16(co, w16, E);
 		}
 	for (int o = 1; o < TPL; o <<= 1)
-		co.cnt += __shfl_xor(co.cnt, o), co.m0 += __shfl_xor(co.m0, o), co.m1 += __shfl_xor(co.m1, o), co.mt += __shfl_xor(co.mt, o);
-	if (cls == TGQ_CAND && tgq_coarse_grid(co, (int)(tl >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
+		co.cnt += __shfl_xor(co.cnt, o), co.s0 += __shfl_xor(co.s0, o), co.s1 += __shfl_xor(co.s1, o);
+	if (cls == TGQ_CAND && tgq_coarse_grid(co, tl)) cls = TGQ_GRID;
 	if (k == 0 && L0 + l < a.lines) {
 		const long L = L0 + l;
 		a.q.e[L] = E, a.q.special[L] = cls, a.q.qsum[L] = qs;
@@ -695,7 +719,7 @@ __global__ __launch_bounds__(1024) void dec_silu_k(tgk_dec_silu_args a)
 	extern __shared__ float4 zs4[]; // [Kp]
 	float *zs = (float *)zs4;
 	__shared__ float redf[16];
-	__shared__ unsigned long long redl[6 * 16];
+	__shared__ unsigned long long redl[5 * 16];
 	const int t = blockIdx.x, FF = a.FF;
 	const float *g = a.gu + (long)t * a.gus, *u = g + FF;
 	float mx = 0.0f;
@@ -867,34 +891,37 @@ constexpr long NL_MIN_LINES = 2048;
 inline bool nl_fits(int Kp) { return Kp >= 64 && Kp <= NL_E && (Kp & (Kp - 1)) == 0; } // a power of two: lines by shifts
 inline int ilog2(int x) { int k = 0; while ((1 << (k + 1)) <= x) k++; return k; }
 
-void tgk_dec_norm(hipStream_t s, const tgk_dec_norm_args *a)
+bool tgk_dec_norm(hipStream_t s, const tgk_dec_norm_args *a)
 {
-	if (a->rows <= 0) return;
+	if (a->rows <= 0) return true;
 	if (a->rows >= NL_MIN_LINES && nl_fits(a->Kp) && a->outs == a->D) {
 		NormLines n{ a->h, a->hs, a->mode, a->add, a->adds, a->o, a->ohead, a->nh, a->g, 0, a->out, a->D, a->Kp, 1, a->rows, a->q, ilog2(a->Kp) };
 		const long R = NL_E / a->Kp;
 		norm_lines_k<<<(unsigned)((a->rows + R - 1) / R), NL_TPB, norm_lines_lds(a->Kp), s>>>(n);
-		return;
+		return false; // candidates left for tgk_qgemm_split
 	}
 	dec_norm_k<<<(unsigned)a->rows, NORM_TPB, (size_t)a->Kp * 2 * sizeof(float), s>>>(*a);
+	return true;
 }
 
-void tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a)
+bool tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a)
 {
 	const long lines = (long)a->rows * a->NH;
-	if (lines <= 0) return;
+	if (lines <= 0) return true;
 	if (lines >= NL_MIN_LINES && nl_fits(a->Kp)) {
 		NormLines n{ (float *)a->x, a->xs, 0, nullptr, 0, nullptr, 0, 0, a->g, a->HD, a->out, a->HD, a->Kp, a->NH, lines, a->q, ilog2(a->Kp) };
 		const long R = NL_E / a->Kp;
 		norm_lines_k<<<(unsigned)((lines + R - 1) / R), NL_TPB, norm_lines_lds(a->Kp), s>>>(n);
-		return;
+		return false; // candidates left for tgk_qgemm_split
 	}
 	dec_hnorm_k<<<(unsigned)((lines + 3) / 4), TPB, (size_t)a->Kp * 8 * sizeof(float), s>>>(*a);
+	return true;
 }
 
-void tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a)
+bool tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a)
 {
 	if (a->rows > 0) dec_silu_k<<<(unsigned)a->rows, 1024, (size_t)a->Kp * sizeof(float), s>>>(*a);
+	return true;
 }
 
 void tgk_dec_causal_softmax(hipStream_t s, float *sc, int T0, long nlines, float scale)

@@ -191,7 +191,7 @@ __global__ __launch_bounds__(256) void digits_k(tgk_qgemm_args a, Scratch s, int
 				if (t0 + t < nsl && k0 < K) tgq_coarse16(co, v[t], E);
 			}
 		}
-		if (tgq_coarse_grid(tgq_coarse_wave_sum(co), (int)(tl >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
+		if (tgq_coarse_grid(tgq_coarse_wave_sum(co), tl)) cls = TGQ_GRID;
 	}
 	if (lane == 0) {
 		s.e[m] = E;
@@ -280,13 +280,13 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 			if (kb < nkb && kb * 32 + half * 16 < K) tgq_coarse16(co, v[j], E);
 		}
 	for (int o = 16; o < 64; o <<= 1)
-		co.cnt += __shfl_xor(co.cnt, o), co.m0 += __shfl_xor(co.m0, o), co.m1 += __shfl_xor(co.m1, o), co.mt += __shfl_xor(co.mt, o);
+		co.cnt += __shfl_xor(co.cnt, o), co.s0 += __shfl_xor(co.s0, o), co.s1 += __shfl_xor(co.s1, o);
 	if (lane < 16) sco[w][lane] = co;
 	__syncthreads();
 	if (w == 0 && lane < 16 && scls[mr] == TGQ_CAND) {
 		TgqCoarse c = sco[0][mr];
 		for (int u = 1; u < W; u++) tgq_coarse_add(c, sco[u][mr]);
-		if (tgq_coarse_grid(c, (int)(stl[0][mr] >> TGQ_TALLY_SHIFT))) {
+		if (tgq_coarse_grid(c, stl[0][mr])) {
 			scls[mr] = TGQ_GRID;
 			s.special[m0 + mr] = TGQ_GRID;
 		}
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 		__syncthreads();
 		TgqCoarse c = sco[0];
 		for (int u = 1; u < 4; u++) tgq_coarse_add(c, sco[u]);
-		if (tgq_coarse_grid(c, (int)(tally >> TGQ_TALLY_SHIFT))) cls = TGQ_GRID;
+		if (tgq_coarse_grid(c, tally)) cls = TGQ_GRID;
 	}
 	if (tid == 0) {
 		s.e[m] = E;

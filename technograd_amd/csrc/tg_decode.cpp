@@ -174,8 +174,9 @@ bool gemm(tg_hip_dec *d, int wi, const float *x, long xr, int ni, long xj, int r
 }
 
 // o[rows][C] = x @ W with the activation digits already written (by the
-// fused norm and silu kernels) into the GEMM's digit area for these rows
-bool gemm_pre(tg_hip_dec *d, int wi, const float *x, long xr, int ni, long xj, int rows, float *o, long orr, long oj)
+// fused norm and silu kernels) into the GEMM's digit area for these rows;
+// `resolved`: the producer resolved its candidate rows (else the split pass runs first)
+bool gemm_pre(tg_hip_dec *d, int wi, const float *x, long xr, int ni, long xj, int rows, float *o, long orr, long oj, bool resolved)
 {
 	tgk_qgemm_args a;
 	memset(&a, 0, sizeof a);
@@ -185,7 +186,7 @@ bool gemm_pre(tg_hip_dec *d, int wi, const float *x, long xr, int ni, long xj, i
 	a.o = o;
 	a.orr = orr, a.oc = 1, a.oj = oj;
 	a.M = rows * ni;
-	tgk_qgemm_split(d->st, &a, d->scratch); // the producer's candidate rows resolved
+	if (!resolved) tgk_qgemm_split(d->st, &a, d->scratch); // the producer's candidate rows resolved
 	tgk_qgemm_mfma(d->st, &a, d->scratch);
 	return true;
 }
@@ -193,7 +194,7 @@ bool gemm_pre(tg_hip_dec *d, int wi, const float *x, long xr, int ni, long xj, i
 // the graph's rmsnorm-then-gain of token rows, fused with the update of h
 // before it (mode 1: h += add; mode 2: h += the heads' output projections in
 // order) and the activation digits of weight wi's GEMM
-void norm(tg_hip_dec *d, int mode, float *h, long hs, int rows, const float *add, long adds, const float *g, float *out, int wi)
+bool norm(tg_hip_dec *d, int mode, float *h, long hs, int rows, const float *add, long adds, const float *g, float *out, int wi)
 {
 	tgk_dec_norm_args a;
 	memset(&a, 0, sizeof a);
@@ -201,7 +202,7 @@ void norm(tg_hip_dec *d, int mode, float *h, long hs, int rows, const float *add
 	a.o = d->wout, a.ohead = (long)rows * d->D, a.nh = d->NQ;
 	a.g = g, a.out = out, a.outs = d->D, a.D = d->D, a.Kp = d->ws[(size_t)wi].Kp, a.rows = rows;
 	a.q = tgk_qgemm_digit_area(d->scratch, rows, a.Kp);
-	tgk_dec_norm(d->st, &a);
+	return tgk_dec_norm(d->st, &a);
 }
 
 // the graph over positions p0 .. p0 + T0 - 1 of S sequences, token ids in
@@ -215,14 +216,14 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 	for (int l = 0; l < d->L; l++) {
 		const long kv_layer = (long)l * d->S * d->kv_seq; // the cache is layer-major: [layer][sequence][KV head][position][HD]
 		// h (plus the previous layer's MLP output), rmsnorm * ln1, q k v projections
-		norm(d, l == 0 ? 0 : 1, d->h, D, rows, d->dbuf, D, d->ln1[(size_t)l], d->n, d->wqkv[(size_t)l]);
-		gemm_pre(d, d->wqkv[(size_t)l], d->n, D, 1, 0, rows, d->qkv, ctot, 0);
+		bool res = norm(d, l == 0 ? 0 : 1, d->h, D, rows, d->dbuf, D, d->ln1[(size_t)l], d->n, d->wqkv[(size_t)l]);
+		gemm_pre(d, d->wqkv[(size_t)l], d->n, D, 1, 0, rows, d->qkv, ctot, 0, res);
 		tgk_dec_hnorm_args hn; // per-head rmsnorm * gain of the q and k heads, then the rotation matmul
 		hn.x = d->qkv, hn.xs = ctot, hn.g = d->qkg[(size_t)l], hn.out = d->hq;
 		hn.NH = NH, hn.HD = d->HD, hn.Kp = d->ws[(size_t)d->wrot].Kp, hn.rows = rows;
 		hn.q = tgk_qgemm_digit_area(d->scratch, rows * NH, hn.Kp);
-		tgk_dec_hnorm(st, &hn);
-		gemm_pre(d, d->wrot, d->hq, qk, NH, d->HD, rows, d->rt, qk, d->HD);
+		res = tgk_dec_hnorm(st, &hn);
+		gemm_pre(d, d->wrot, d->hq, qk, NH, d->HD, rows, d->rt, qk, d->HD, res);
 		tgk_dec_rope_args r;
 		r.hq = d->hq, r.rt = d->rt, r.qkv = d->qkv, r.ctot = ctot, r.cosT = d->cosT, r.sinT = d->sinT;
 		r.qr = d->qr, r.K = d->K, r.V = d->Vc, r.kv_seq = d->kv_seq, r.kv_layer = kv_layer;
@@ -259,17 +260,18 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 				gemm(d, d->wo[(size_t)l * d->NQ + hh], d->att + (long)hh * d->HD, (long)d->NQ * d->HD, 1, 0, rows,
 				     d->wout + (long)hh * rows * D, D, 0);
 		// h + the heads' output projections (in head order), rmsnorm * ln2, gate and up projections
-		norm(d, 2, d->h, D, rows, nullptr, 0, d->ln2[(size_t)l], d->n, d->wgu[(size_t)l]);
-		gemm_pre(d, d->wgu[(size_t)l], d->n, D, 1, 0, rows, d->gu, 2L * d->FF, 0);
+		res = norm(d, 2, d->h, D, rows, nullptr, 0, d->ln2[(size_t)l], d->n, d->wgu[(size_t)l]);
+		gemm_pre(d, d->wgu[(size_t)l], d->n, D, 1, 0, rows, d->gu, 2L * d->FF, 0, res);
 		tgk_dec_silu_args sa; // act = silu(g) * u, then the down projection
 		sa.gu = d->gu, sa.gus = 2L * d->FF, sa.out = d->act, sa.FF = d->FF, sa.Kp = d->ws[(size_t)d->wd[(size_t)l]].Kp, sa.rows = rows;
 		sa.q = tgk_qgemm_digit_area(d->scratch, rows, sa.Kp);
-		tgk_dec_silu(st, &sa);
-		gemm_pre(d, d->wd[(size_t)l], d->act, d->FF, 1, 0, rows, d->dbuf, D, 0);
+		res = tgk_dec_silu(st, &sa);
+		gemm_pre(d, d->wd[(size_t)l], d->act, d->FF, 1, 0, rows, d->dbuf, D, 0, res);
 	}
 	// the last position of each sequence: h + the last MLP output, rmsnorm * lnf, LM head
-	norm(d, 1, d->h + (long)(T0 - 1) * D, (long)T0 * D, S, d->dbuf + (long)(T0 - 1) * D, (long)T0 * D, d->lnf, d->lastn, d->wlm);
-	gemm_pre(d, d->wlm, d->lastn, D, 1, 0, S, d->logits, d->V, 0);
+	const bool res = norm(d, 1, d->h + (long)(T0 - 1) * D, (long)T0 * D, S, d->dbuf + (long)(T0 - 1) * D, (long)T0 * D, d->lnf, d->lastn,
+			      d->wlm);
+	gemm_pre(d, d->wlm, d->lastn, D, 1, 0, S, d->logits, d->V, 0, res);
 	return hip_ok(hipGetLastError(), "decoder launch");
 }
 

@@ -205,16 +205,17 @@ struct tg_hip_prog {
 	hipModule_t rp_mod = nullptr;  // the row program compiled for this model
 	hipFunction_t rp_fn = nullptr; // its kernel (null: the interpreter runs the program)
 	std::string rp_why;            // why the program runs in the interpreter
-	// host-buffer batches: a two-slot pipeline (pinned staging, device buffers, copy streams, events)
+	// host-buffer batches: a three-slot pipeline (pinned staging, device buffers, copy streams, events)
+	static constexpr int NSL = 3; // pipeline slots
 	struct HostPipe {
-		long chunk = 0;                                      // rows per chunk
-		void *h_in[2] = {}, *h_out[2] = {};                  // pinned staging
-		int *h_steps[2] = {};
-		float *d_in[2] = {}, *d_out[2] = {};
-		int *d_steps[2] = {};
-		hipStream_t h2d = nullptr, d2h = nullptr;            // copy streams (default priority)
-		hipEvent_t up[2] = {}, done[2] = {}, down[2] = {};   // per slot: copied in, computed, copied out
-		hipEvent_t t0[2] = {}, t1[2] = {};                   // per slot: compute span (timing)
+		long chunk = 0;                                            // rows per chunk
+		void *h_in[NSL] = {}, *h_out[NSL] = {};                    // pinned staging
+		int *h_steps[NSL] = {};
+		float *d_in[NSL] = {}, *d_out[NSL] = {};
+		int *d_steps[NSL] = {};
+		hipStream_t h2d = nullptr, d2h = nullptr;                  // copy streams (default priority)
+		hipEvent_t up[NSL] = {}, done[NSL] = {}, down[NSL] = {};   // per slot: copied in, computed, copied out
+		hipEvent_t t0[NSL] = {}, t1[NSL] = {};                     // per slot: compute span (timing)
 	} hp;
 	int *d_steps = nullptr; // steps of tg_hip_batch_device calls that pass none
 	// stats
@@ -2089,7 +2090,7 @@ void destroy(tg_hip_prog *p)
 	for (void *b : bufs)
 		if (b) (void)hipFree(b);
 	auto &h = p->hp;
-	for (int k = 0; k < 2; k++) {
+	for (int k = 0; k < tg_hip_prog::NSL; k++) {
 		void *dev[] = { h.d_in[k], h.d_out[k], h.d_steps[k] }, *host[] = { h.h_in[k], h.h_out[k], h.h_steps[k] };
 		for (void *b : dev)
 			if (b) (void)hipFree(b);
@@ -2153,7 +2154,7 @@ bool host_pipe_init(tg_hip_prog *p)
 	c = c < 256 ? 256 : c;
 	h.chunk = c < p->max_rows ? c : p->max_rows;
 	bool ok = hipok(hipStreamCreate(&h.h2d), "stream") && hipok(hipStreamCreate(&h.d2h), "stream");
-	for (int k = 0; ok && k < 2; k++)
+	for (int k = 0; ok && k < tg_hip_prog::NSL; k++)
 		ok = hipok(hipHostMalloc(&h.h_in[k], (size_t)h.chunk * per * 4, 0), "pinned input") &&
 		     hipok(hipHostMalloc(&h.h_out[k], (size_t)h.chunk * nout * 4, 0), "pinned output") &&
 		     hipok(hipHostMalloc((void **)&h.h_steps[k], (size_t)h.chunk * nt * 4, 0), "pinned steps") &&
@@ -2169,7 +2170,7 @@ bool host_pipe_init(tg_hip_prog *p)
 }
 
 // Host buffers, the block loop of `tgc batch`: rows go in chunks through a
-// two-slot pipeline. Chunk i uses slot i % 2: its rows are copied into the
+// three-slot pipeline. Chunk i uses slot i % 3: its rows are copied into the
 // slot's pinned buffer on the host, up to the device on the copy-in stream,
 // computed on the program's stream, and down on the copy-out stream; each
 // stream waits for the event of the step before it, and a slot is refilled
@@ -2196,7 +2197,7 @@ int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *ste
 	const long nch = (nrows + C - 1) / C;
 	float ms_total = 0;
 	auto finish = [&](long i) -> bool { // chunk i's outputs to the caller
-		const int k = (int)(i & 1);
+		const int k = (int)(i % tg_hip_prog::NSL);
 		const long r0 = i * C, cnt = nrows - r0 < C ? nrows - r0 : C;
 		if (!hipok(hipEventSynchronize(h.down[k]), "outputs to host")) return false;
 		if (!dout) par_copy((char *)out + (size_t)r0 * nout * 4, h.h_out[k], (size_t)cnt * nout * 4);
@@ -2207,9 +2208,9 @@ int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *ste
 		return true;
 	};
 	for (long i = 0; i < nch; i++) {
-		const int k = (int)(i & 1);
+		const int k = (int)(i % tg_hip_prog::NSL);
 		const long r0 = i * C, cnt = nrows - r0 < C ? nrows - r0 : C;
-		if (i >= 2 && !finish(i - 2)) return -1; // the slot's previous chunk is out: its buffers are free
+		if (i >= tg_hip_prog::NSL && !finish(i - tg_hip_prog::NSL)) return -1; // the slot's previous chunk is out: its buffers are free
 		const void *src = (const char *)rows + (size_t)r0 * per * 4;
 		if (!din) {
 			par_copy(h.h_in[k], src, (size_t)cnt * per * 4);
@@ -2231,7 +2232,7 @@ int batch_host(tg_hip_prog *p, const void *rows, long nrows, void *out, int *ste
 			return -1;
 		if (!hipok(hipEventRecord(h.down[k], h.d2h), "event")) return -1;
 	}
-	for (long i = nch > 2 ? nch - 2 : 0; i < nch; i++)
+	for (long i = nch > tg_hip_prog::NSL ? nch - tg_hip_prog::NSL : 0; i < nch; i++)
 		if (!finish(i)) return -1;
 	collect_timing(p);
 	if (steps && !p->m->nthink) memset(steps, 0, (size_t)nrows * sizeof *steps); /* no think loop: one zero slot per row */

@@ -161,7 +161,10 @@ void tgk_dec_attn(hipStream_t s, const tgk_dec_attn_args *a, int seqs);
 /* token-row normalization of a step or prompt chunk, fused: h += add (mode
  * 1) or h += (o_0 + ... + o_{nh-1}) in order (mode 2, the heads' output
  * projections), then out = rmsnorm(h) * g as the row-op and multiply kernels
- * compute it, and the activation digits of out for the next GEMM */
+ * compute it, and the activation digits of out for the next GEMM.
+ * tgk_dec_norm, tgk_dec_hnorm and tgk_dec_silu return true when the kernel
+ * they ran resolved its candidate rows itself (a step's row counts), false
+ * when the GEMM must run tgk_qgemm_split first (a prompt's many lines) */
 typedef struct {
 	float *h;
 	long hs;
@@ -178,7 +181,7 @@ typedef struct {
 	tgk_qdig q;
 } tgk_dec_norm_args;
 #define TGK_DEC_NORM_MAX 4096 /* largest D of tgk_dec_norm */
-void tgk_dec_norm(hipStream_t s, const tgk_dec_norm_args *a);
+bool tgk_dec_norm(hipStream_t s, const tgk_dec_norm_args *a);
 /* per-head rmsnorm * gain of the q and k heads (line (t, j) at x + t xs + j HD),
  * into out [rows][NH][HD] and the digits of its rows t NH + j */
 typedef struct {
@@ -189,7 +192,7 @@ typedef struct {
 	int NH, HD, Kp, rows;
 	tgk_qdig q;
 } tgk_dec_hnorm_args;
-void tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a);
+bool tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a);
 /* out = silu(g) * u of rows [g (FF) | u (FF)] and the digits of out */
 typedef struct {
 	const float *gu;
@@ -198,7 +201,7 @@ typedef struct {
 	int FF, Kp, rows;
 	tgk_qdig q;
 } tgk_dec_silu_args;
-void tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a);
+bool tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a);
 /* per-head output projections of `rows` token rows, all heads in one launch,
  * values equal to the digit + matrix-core path; codes int32 [NQ][HD/4][D],
  * 4 consecutive k's int8 codes per word */

@@ -306,61 +306,69 @@ __device__ inline int tgq_decide(TgqHist *h, int n, int lane)
 // ---- the producers' coarse test ----
 //
 // Most candidates keep their grid when resolved. A producer settles most of
-// those without a resolve from a coarse histogram it keeps while writing the
-// digits: TgqHist's bins 0 and 1 exactly, every other nonzero entry in one
-// merged bin 2 (|x| < 2^(E-2)), counts and masses. tgq_coarse_grid runs
-// tgq_decide's test at level 0 on it, an entry of the merged bin counting at
-// that bin's upper end 2^(E-2) when the bin is taken in part. The coarse bins
-// are unions of tgq_decide's bins, so the coarse top mass is at least
-// tgq_decide's and the coarse top bin at most tgq_decide's: a row that passes
-// here passes tgq_decide at level 0, where the resolve leaves a row as it is.
-// A row's class is therefore the same whether or not its producer runs this
-// test first.
+// those without a resolve by a coarse test on integers it has at hand: the
+// row's q = rint(x 2^(23-E)) sorted into three groups, |q| >= 2^22 (holding
+// TgqHist's bin 0 and entries just below it), 2^21 <= |q| < 2^22 (the rest
+// of bin 1 and entries just below it) and the other nonzero entries (every
+// entry of bins 2 and up), with the groups' counts and sums of |q|, plus the
+// tally's sum of |q| and inexact count. tgq_coarse_grid runs tgq_decide's
+// level-0 test on the groups with bounds: a group taken whole counts each
+// entry at (|q| + 1/2) 2^21 (at least its mass floor(|x| 2^(44-E)); 2^20 for
+// a nonzero entry with q = 0), a group taken in part counts each taken entry
+// at the group's upper end (2^44, 2^43, 2^42: no entry of the group has more
+// mass), the row's mass counts as sum (|q| - 1/2) 2^21 over nonzero entries
+// (at most the true mass), and the rest's top bin is the first nonempty
+// group's index (no entry's group index exceeds its bin). So the coarse top
+// mass is at least tgq_decide's, the coarse rest mass at most its, and the
+// coarse top bin at most its: a row that passes here passes tgq_decide at
+// level 0, where the resolve leaves a row as it is, and a row's class is the
+// same whether or not its producer runs this test first.
 struct TgqCoarse {
-	unsigned long long cnt;    // nonzero entries: bin 0 in bits 0..20, bin 1 in bits 21..41, the merged bin from bit 42
-	unsigned long long m0, m1; // masses of bins 0 and 1 (sums of floor(|x| 2^(44-E)))
-	unsigned long long mt;     // mass of all bins
+	unsigned long long cnt;    // |q| >= 2^22: bits 0..20; 2^21 <= |q| < 2^22: bits 21..41; nonzero x: from bit 42
+	unsigned long long s0, s1; // sums of |q| of the first two groups
 };
 
-__device__ inline void tgq_coarse_add(TgqCoarse &c, const TgqCoarse &o) { c.cnt += o.cnt, c.m0 += o.m0, c.m1 += o.m1, c.mt += o.mt; }
+__device__ inline void tgq_coarse_add(TgqCoarse &c, const TgqCoarse &o) { c.cnt += o.cnt, c.s0 += o.s0, c.s1 += o.s1; }
 
 // adds 16 inputs of a row with grid exponent E (finite, below 2^E)
 __device__ inline void tgq_coarse16(TgqCoarse &c, const float *v, int E)
 {
+	unsigned n0 = 0, n1 = 0, nz = 0, a0 = 0, a1 = 0; // |q| < 2^23: 16 of them below 2^27
 	for (int i = 0; i < 16; i++) {
-		const float ax = fabsf(v[i]);
-		const int d = tgq_bin(ax, E);
-		const unsigned long long ms = (unsigned long long)ldexpf(ax, TGQ_MASS_SHIFT - E); // truncation: the floor
-		c.cnt += ax == 0.0f ? 0ull : d == 0 ? 1ull : d == 1 ? 1ull << 21 : 1ull << 42;
-		c.m0 += d == 0 ? ms : 0ull; // (ms is 0 for a zero entry)
-		c.m1 += d == 1 ? ms : 0ull;
-		c.mt += ms;
+		const unsigned aq = (unsigned)abs((int)rintf(ldexpf(v[i], 23 - E)));
+		const bool g0 = aq >= (1u << 22), g1 = !g0 && aq >= (1u << 21);
+		n0 += g0, n1 += g1, nz += v[i] != 0.0f;
+		a0 += g0 ? aq : 0u, a1 += g1 ? aq : 0u;
 	}
+	c.cnt += (unsigned long long)n0 + ((unsigned long long)n1 << 21) + ((unsigned long long)nz << 42);
+	c.s0 += a0, c.s1 += a1;
 }
 
 __device__ inline TgqCoarse tgq_coarse_wave_sum(TgqCoarse c)
 {
-	for (int o = 32; o > 0; o >>= 1)
-		c.cnt += __shfl_xor(c.cnt, o), c.m0 += __shfl_xor(c.m0, o), c.m1 += __shfl_xor(c.m1, o), c.mt += __shfl_xor(c.mt, o);
+	for (int o = 32; o > 0; o >>= 1) c.cnt += __shfl_xor(c.cnt, o), c.s0 += __shfl_xor(c.s0, o), c.s1 += __shfl_xor(c.s1, o);
 	return c;
 }
 
-// whether a candidate row with n inexact entries keeps its grid by the coarse
-// histogram alone (tgq_decide's level-0 test on the coarse bins)
-__device__ inline bool tgq_coarse_grid(const TgqCoarse &c, int n)
+// whether a candidate row with the tally `tally` keeps its grid by the coarse test alone
+__device__ inline bool tgq_coarse_grid(const TgqCoarse &c, long long tally)
 {
+	const int n = (int)(tally >> TGQ_TALLY_SHIFT);
+	const long long aq = tally & ((1ll << TGQ_TALLY_SHIFT) - 1); // sum of |q| over the row
 	const unsigned long long lo21 = (1ull << 21) - 1;
-	const long long cnt[3] = { (long long)(c.cnt & lo21), (long long)((c.cnt >> 21) & lo21), (long long)(c.cnt >> 42) };
-	const long long ms[3] = { (long long)c.m0, (long long)c.m1, (long long)(c.mt - c.m0 - c.m1) };
+	const long long c0 = (long long)(c.cnt & lo21), c1 = (long long)((c.cnt >> 21) & lo21), nz = (long long)(c.cnt >> 42);
+	const long long cnt[3] = { c0, c1, nz - c0 - c1 };
+	const long long sq[3] = { (long long)c.s0, (long long)c.s1, aq - (long long)c.s0 - (long long)c.s1 };
 	const int r = cnt[0] ? 0 : cnt[1] ? 1 : 2;
 	if (!cnt[r]) return false; // an all-zero row is no candidate
 	long long left = tgq_jcap(n), top = 0;
 	for (int d = r; d < 3 && left > 0; d++) {
 		const long long take = cnt[d] < left ? cnt[d] : left;
-		top += take == cnt[d] ? ms[d] : take << (TGQ_MASS_SHIFT - d);
+		top += take == cnt[d] ? (sq[d] << 21) + (cnt[d] << 20) : take << (TGQ_MASS_SHIFT - d);
 		left -= take;
 	}
-	return (long long)c.mt - top >= (long long)tgq_acoef(n) << (TGQ_MASS_SHIFT - r);
+	const long long mass_lo = (aq << 21) - (nz << 20);
+	return mass_lo - top >= (long long)tgq_acoef(n) << (TGQ_MASS_SHIFT - r);
 }
 
 // Resolves a candidate row of grid exponent E (a whole wave; h in LDS, this

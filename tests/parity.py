@@ -206,30 +206,37 @@ def resolve_row(x_k, E, n):
     return -1
 
 
+def coarse_groups(x_k, E):
+    """the coarse test's integers (tgq_coarse16 summed over the row): counts
+    of |q| >= 2^22, of 2^21 <= |q| < 2^22 and of nonzero entries; the first
+    two groups' sums of |q|; the row's sum of |q|"""
+    x = np.asarray(x_k, np.float32).astype(np.float64)
+    aq = np.abs(np.rint(np.ldexp(x, 23 - E))).astype(np.int64)
+    g0, g1 = aq >= 2 ** 22, (aq >= 2 ** 21) & (aq < 2 ** 22)
+    return (int(g0.sum()), int(g1.sum()), int((x != 0).sum()), int(aq[g0].sum()), int(aq[g1].sum()), int(aq.sum()))
+
+
 def coarse_grid(x_k, E, n):
     """tgq_coarse_grid on one candidate row (grid exponent E, n inexact
-    entries): tgq_decide's level-0 test on bins 0 and 1 and one merged bin
-    for the rest, a merged entry counting at 2^(E-2) when that bin is taken
-    in part. Passing it implies resolve_row(...) == 0."""
-    a = np.abs(np.asarray(x_k, np.float32).astype(np.float64))
-    a = a[a != 0]
-    d = np.minimum(_bins(a, E), 2)
-    mass = np.floor(np.ldexp(a, MASS_SHIFT - E)).astype(np.int64)
-    cnt = np.bincount(d, minlength=3)
-    ms = np.zeros(3, np.int64)
-    np.add.at(ms, d, mass)
-    nz = np.flatnonzero(cnt)
-    if len(nz) == 0:
+    entries): tgq_decide's level-0 test on three groups of q (|q| >= 2^22,
+    2^21 <= |q| < 2^22, the other nonzero entries), a whole group counting
+    (|q| + 1/2) 2^21 per entry, a group taken in part 2^44, 2^43 or 2^42 per
+    taken entry, the row's mass counted as sum (|q| - 1/2) 2^21 over its
+    nonzero entries. Passing it implies resolve_row(...) == 0."""
+    c0, c1, nz, s0, s1, aq = coarse_groups(x_k, E)
+    cnt, sq = [c0, c1, nz - c0 - c1], [s0, s1, aq - s0 - s1]
+    nzs = [d for d in range(3) if cnt[d]]
+    if not nzs:
         return False
-    r = int(nz[0])
+    r = nzs[0]
     left, top = jcap(n), 0
-    for dd in range(r, 3):
+    for d in range(r, 3):
         if left == 0:
             break
-        take = min(int(cnt[dd]), left)
-        top += int(ms[dd]) if take == cnt[dd] else take << (MASS_SHIFT - dd)
+        take = min(cnt[d], left)
+        top += (sq[d] << 21) + (cnt[d] << 20) if take == cnt[d] else take << (MASS_SHIFT - d)
         left -= take
-    return int(ms.sum()) - top >= acoef(n) << (MASS_SHIFT - r)
+    return (aq << 21) - (nz << 20) - top >= acoef(n) << (MASS_SHIFT - r)
 
 
 def row_classes(x_mk):
