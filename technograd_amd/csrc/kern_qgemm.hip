@@ -309,22 +309,23 @@ __global__ __launch_bounds__(1024) void digits_tile16_k(tgk_qgemm_args a, Scratc
 		}
 }
 
-// Few, long rows: one block of 256 threads per row, thread t taking the
-// 16-input groups t, t + 256, ... (G of them, in registers). The row's max,
-// non-finite flag and sum of q are combined across the block. Results are
-// those of digits_k.
-template <int G, bool VEC>
-__global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
+// Row m's digits and row data made by one workgroup of NW waves, thread t
+// taking the 16-input groups t, t + 64 NW, ... (G of them, in registers). The
+// row's max, non-finite flag and sum of q are combined across the workgroup.
+// Results are those of digits_k.
+template <int NW, int G, bool VEC>
+__device__ inline void row_digits(const tgk_qgemm_args &a, const Scratch &s, int K, int Kp, int m)
 {
-	__shared__ float smx[4];
-	__shared__ int sbad[4];
-	__shared__ long long sqs[4], stl[4];
-	const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, ng = Kp / 16;
+	constexpr int NT = 64 * NW;
+	__shared__ float smx[NW];
+	__shared__ int sbad[NW];
+	__shared__ long long sqs[NW], stl[NW];
+	const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, ng = Kp / 16;
 	const float *x = xrow(a, m);
 	float v[G][16];
 	unsigned mb = 0; // max |x| as bits (tgq_scan16)
 	for (int g = 0; g < G; g++) {
-		const int j = tid + g * 256;
+		const int j = tid + g * NT;
 		load16<VEC>(v[g], x, a.xk, j < ng ? j * 16 : K, K); // past the row: zeros
 		tgq_scan16(v[g], mb);
 	}
@@ -335,38 +336,41 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 	bad = __any(bad);
 	if (lane == 0) smx[w] = mx, sbad[w] = bad;
 	__syncthreads();
-	const float amax = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
-	const int special = tgq_special(sbad[0] | sbad[1] | sbad[2] | sbad[3], amax), E = tgq_exponent(amax, special);
+	float amax = smx[0];
+	int anybad = sbad[0];
+	for (int u = 1; u < NW; u++) amax = fmaxf(amax, smx[u]), anybad |= sbad[u];
+	const int special = tgq_special(anybad, amax), E = tgq_exponent(amax, special);
 	int8_t *blk = tgq_row_base(s.dig, m, Kp);
 	long long qs = 0, tl = 0;
 	for (int g = 0; g < G; g++) {
-		const int j = tid + g * 256;
+		const int j = tid + g * NT;
 		if (j < ng) qs += tgq_put16(blk, j * 16, v[g], E, special || j * 16 >= K, tl);
 	}
 	qs = wave_sum(qs);
 	tl = wave_sum(tl);
 	if (lane == 0) sqs[w] = qs, stl[w] = tl;
 	__syncthreads(); // also: every digit of the row is stored
-	const long long tally = stl[0] + stl[1] + stl[2] + stl[3];
+	long long tally = 0, qsum = 0;
+	for (int u = 0; u < NW; u++) tally += stl[u], qsum += sqs[u];
 	int cls = special ? TGQ_REF : tgq_candidate(tally) ? TGQ_CAND : TGQ_GRID;
 	if (cls == TGQ_CAND) { // (uniform over the block) the coarse test, on the values still in registers
-		__shared__ TgqCoarse sco[4];
+		__shared__ TgqCoarse sco[NW];
 		TgqCoarse co{};
 		for (int g = 0; g < G; g++) {
-			const int j = tid + g * 256;
+			const int j = tid + g * NT;
 			if (j < ng && j * 16 < K) tgq_coarse16(co, v[g], E);
 		}
 		co = tgq_coarse_wave_sum(co);
 		if (lane == 0) sco[w] = co;
 		__syncthreads();
 		TgqCoarse c = sco[0];
-		for (int u = 1; u < 4; u++) tgq_coarse_add(c, sco[u]);
+		for (int u = 1; u < NW; u++) tgq_coarse_add(c, sco[u]);
 		if (tgq_coarse_grid(c, tally)) cls = TGQ_GRID;
 	}
 	if (tid == 0) {
 		s.e[m] = E;
 		s.special[m] = cls;
-		s.qsum[m] = sqs[0] + sqs[1] + sqs[2] + sqs[3];
+		s.qsum[m] = qsum;
 	}
 	if (cls == TGQ_CAND && w == 0) { // wave 0 resolves the row (uniform: cls is the block's)
 		__shared__ TgqHist hist;
@@ -379,6 +383,13 @@ __global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s,
 		tgq_resolve_row(&hist, ld, K, Kp, E, blk, &s.qsum[m], &s.e[m], &s.special[m], s.ok + (long)m * nout, s.ox + (long)m * nout, nout,
 				lane);
 	}
+}
+
+// Few, long rows: one block of 256 threads per row (row_digits)
+template <int G, bool VEC>
+__global__ __launch_bounds__(256) void digits_row_k(tgk_qgemm_args a, Scratch s, int K, int Kp, int M)
+{
+	row_digits<4, G, VEC>(a, s, K, Kp, blockIdx.x);
 }
 
 // Candidate rows (tg_qdigits.h) of a digit area whose producer did not
@@ -566,9 +577,10 @@ __device__ inline double outlier_sum(const Scratch &s, const tgk_qweight &w, int
 
 // special: 0 a grid row, 1 the reference's loop, 2 a split row (the grid
 // sum of its other entries plus its outliers' terms, in f64, rounded once)
+// (sc: channel c's scale, read beforehand by callers that gather their loads)
 template <int ACT = 0>
-__device__ inline void epilogue_with(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot,
-				     int E, int special, long long qsum)
+__device__ inline void epilogue_sc(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot, int E,
+				   int special, long long qsum, float sc)
 {
 	if (m >= a.M || c >= w.C) return;
 	float acc32;
@@ -580,7 +592,15 @@ __device__ inline void epilogue_with(const tgk_qgemm_args &a, const tgk_qweight 
 		acc32 = (float)(special == 2 ? g + outlier_sum(s, w, m, c) : g);
 	}
 	int r = m / a.ni, jj = m - r * a.ni;
-	*out_at(a, r, jj, c) = act_out<ACT>(w.scale[c] * acc32);
+	*out_at(a, r, jj, c) = act_out<ACT>(sc * acc32);
+}
+
+template <int ACT = 0>
+__device__ inline void epilogue_with(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot,
+				     int E, int special, long long qsum)
+{
+	if (m >= a.M || c >= w.C) return;
+	epilogue_sc<ACT>(a, w, s, m, c, tot, E, special, qsum, w.scale[c]);
 }
 
 __device__ inline void epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m, int c, long long tot)
@@ -1256,13 +1276,27 @@ __global__ __launch_bounds__(64 * W) void gemv16_k(tgk_qgemm_args a, tgk_qweight
 	v4i acc[3] = { { 0, 0, 0, 0 }, { 0, 0, 0, 0 }, { 0, 0, 0, 0 } };
 	gemv16_steps<BITS, NS, 0>(af, bf, acc, (nks - wave + W - 1) / W);
 	for (int v = 0; v < 4; v++) red[wave][v][lane] = combine_d(acc[0][v], acc[1][v], acc[2][v]);
+	// wave 0's epilogue reads (its rows' exponents, classes and sums of q,
+	// its channel's scale), all issued here, before the barrier: read one
+	// row at a time between the output stores, each would wait for the
+	// previous store (the compiler cannot tell the buffers apart)
+	const int c = t * 16 + r;
+	int re[4] = { 0, 0, 0, 0 }, rc[4] = { 0, 0, 0, 0 };
+	long long rq[4] = { 0, 0, 0, 0 };
+	float sc = 0.0f;
+	if (wave == 0) {
+		for (int v = 0; v < 4; v++) {
+			const int m = 4 * g + v < a.M ? 4 * g + v : 0;
+			re[v] = s.e[m], rc[v] = s.special[m], rq[v] = s.qsum[m];
+		}
+		sc = w.scale[c < w.C ? c : w.C - 1];
+	}
 	__syncthreads();
 	if (wave) return;
-	const int c = t * 16 + r;
 	for (int v = 0; v < 4; v++) {
 		double tot = 0.0;
 		for (int u = 0; u < W; u++) tot += red[u][v][lane]; // exact: integers below 2^53
-		epilogue(a, w, s, 4 * g + v, c, (long long)tot);
+		epilogue_sc(a, w, s, 4 * g + v, c, (long long)tot, re[v], rc[v], rq[v], sc);
 	}
 }
 

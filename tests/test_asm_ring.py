@@ -11,7 +11,8 @@ loads in order at each vmcnt(N), and fails if an instruction after the final
 ring load writes a register that an outstanding load will write. (The kernel
 prevents this by reading every ring register after its final wait; without
 that, the epilogue's row index was computed into such registers, and the
-index was overwritten before the row-info loads used it.)
+index was overwritten before the row-info loads used it.) Writes by vector
+instructions, LDS reads and other loads all count.
 
 The large-batch kernel (qgemm_k) sets m0 in inline assembly before each of
 its global-to-LDS copies; a second test checks that nothing else in that
@@ -71,12 +72,13 @@ def ring_hazards(asm_lines):
                     n = int(m.group(1))
                     out = out[len(out) - n:] if n < len(out) else out
                 continue
-            if p[0].startswith("global_load") or p[0].startswith("buffer_load"):
-                out.append(_vregs(p[1]))
-                continue
-            if k > last and p[0].startswith("v_") and not p[0].startswith("v_cmp") and len(p) > 1:
+            if k > last and len(p) > 1 and any(o for o in out) and (
+                    (p[0].startswith("v_") and not p[0].startswith("v_cmp")) or p[0].startswith("ds_read")
+                    or p[0].startswith("ds_bpermute") or p[0].startswith("global_load") or p[0].startswith("buffer_load")):
                 if any(_vregs(p[1]) & o for o in out):
                     hits.append(t)
+            if p[0].startswith("global_load") or p[0].startswith("buffer_load"):
+                out.append(_vregs(p[1]))
         found[asm_lines[s].split(":")[0]] = hits
     return found
 

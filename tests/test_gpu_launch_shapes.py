@@ -40,10 +40,15 @@ SHAPES = [
     (8, 1, 4096, 4096),    # one int8 row: gemv16_k NS=8 W=8
     (4, 16, 4096, 4096),   # NS=8 W=8: config 2 at B=16
     (8, 5, 2048, 4096),    # NS=4 W=8, int8
+    (4, 12, 3000, 4096),   # NS=8 W=8, int4, K not a multiple of 64
     (8, 7, 4096, 4096),    # NS=8 W=8, int8
+    (8, 16, 1792, 2048),   # NS=4 W=8, int8
+    (4, 5, 1000, 4096),    # NS=2 W=8, K not a multiple of 16 (the digit kernel's element loads)
     (8, 16, 1024, 4096),   # NS=2 W=8, int8
     (4, 3, 640, 4096),     # NS=2 W=8, K not a multiple of 64
     (4, 4, 448, 1000),     # NS=2 W=4, channels not a multiple of 16
+    (4, 9, 384, 4096),     # NS=2 W=4
+    (4, 2, 128, 1000),     # NS=1 W=4
     (4, 1, 256, 4096),     # gemv1_k fused, NL=1
     (8, 1, 256, 4096),     # gemv16_k NS=1 W=4
     (8, 2, 8192, 2048),    # int8 beyond 4096 inputs: qgemv_k NB=1 W=8
@@ -105,3 +110,4 @@ def test_single_row_kinds(K):
         assert np.array_equal(np.isnan(got[0]), np.isnan(want[i]))
         ok = ~np.isnan(want[i])
         assert np.array_equal(got[0][ok].view(np.uint32), want[i][ok].view(np.uint32)), i
+
