@@ -1666,10 +1666,130 @@ void launch_gemv(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
 	qgemv_k<BITS, NB, W, P><<<gx * gy, 64 * W, 0, st>>>(*a, *a->w, s, gx);
 }
 
+// Products over at most 32 inputs (a selective SSM's dt projection has 16).
+// The matrix-core kernels pad these to 64 inputs and spend their time in the
+// per-output epilogue, the reference-loop and split rows' slow path taken by
+// nearly every wave. Here a thread takes NC channels (c = 256 (NC blockIdx.x
+// + q) + thread, q < NC) over the workgroup's rows, U at a time, from the
+// digits and row data the digit kernel left, so every output is the one the
+// matrix-core path gives: the row's three digit planes dotted with the
+// channel's codes by v_dot4_i32_i8 (the codes in registers as signed bytes,
+// four inputs a word) and combined exactly; a reference-loop row by the
+// reference's sequential loop; a split row with its outlier terms in f64
+// (outlier_sum); then the scale and the chain, each instruction applied to
+// the U NC values at once, as staged_epilogue applies it. A row's class and
+// exponent are the same for every lane (read into scalar registers, so the
+// class decides by a uniform branch); the U rows' classes, exponents and
+// digits are read before any of their arithmetic (one round trip per U rows).
+template <int NG, int NC>
+__global__ __launch_bounds__(256) void qtiny_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int rows_per_block)
+{
+	constexpr int U = 4, NV = U * NC;
+	int c[NC], cc[NC], cw[NC][4 * NG]; // channel cc's codes: byte e of word j is input 4 j + e's
+	float sc[NC];
+	for (int q = 0; q < NC; q++) {
+		c[q] = 256 * (NC * blockIdx.x + q) + threadIdx.x;
+		cc[q] = c[q] < w.C ? c[q] : w.C - 1;
+		for (int j = 0; j < 4 * NG; j++) {
+			unsigned word = 0;
+			for (int e = 0; e < 4; e++)
+				if (4 * j + e < w.K) word |= (unsigned)(code_orig(w, cc[q], 4 * j + e) & 255) << (8 * e);
+			cw[q][j] = (int)word;
+		}
+		sc[q] = w.scale[cc[q]];
+	}
+	const bool flat = a.ni == 1; // (uniform) row m is batch row m: no division
+	const int m0 = blockIdx.y * rows_per_block, m1 = a.M - m0 < rows_per_block ? a.M : m0 + rows_per_block;
+	for (int mb = m0; mb < m1; mb += U) {
+		int cls[U], E[U], rr[U], jr[U];
+		int dg[U][3][4 * NG];
+		for (int u = 0; u < U; u++) {
+			const int m = mb + u < m1 ? mb + u : m0; // past the block's rows: a row of it, not stored
+			rr[u] = flat ? m : m / a.ni;
+			jr[u] = m - rr[u] * a.ni;
+			cls[u] = __builtin_amdgcn_readfirstlane(s.special[m]);
+			E[u] = __builtin_amdgcn_readfirstlane(s.e[m]);
+			const int8_t *blk = tgq_row_base(s.dig, m, w.Kp); // inputs 16 g ..: chunk (g & 1) of block 0 (NG <= 2)
+			for (int g = 0; g < NG; g++)
+				for (int l = 0; l < 3; l++) {
+					const v4i d = *(const v4i *)(blk + g * 512 + l * 1024);
+					dg[u][l][4 * g] = d.x, dg[u][l][4 * g + 1] = d.y, dg[u][l][4 * g + 2] = d.z, dg[u][l][4 * g + 3] = d.w;
+				}
+		}
+		float v[NV]; // value (u, q) at u NC + q
+		for (int u = 0; u < U; u++) {
+			const int m = mb + u < m1 ? mb + u : m0;
+			if (cls[u] & 1) { // the reference's loop (runtime/tg_rt.h:132-151)
+				const float *x = xrow(a, m);
+				for (int q = 0; q < NC; q++) {
+					float t = 0.0f;
+					for (int k = 0; k < w.K; k++) t += (float)(signed char)(cw[q][k >> 2] >> (8 * (k & 3))) * x[(long)k * a.xk];
+					v[u * NC + q] = sc[q] * t;
+				}
+				continue;
+			}
+			for (int q = 0; q < NC; q++) {
+				int p0 = 0, p1 = 0, p2 = 0;
+				for (int j = 0; j < 4 * NG; j++) {
+					p0 = __builtin_amdgcn_sdot4(dg[u][0][j], cw[q][j], p0, false);
+					p1 = __builtin_amdgcn_sdot4(dg[u][1][j], cw[q][j], p1, false);
+					p2 = __builtin_amdgcn_sdot4(dg[u][2][j], cw[q][j], p2, false);
+				}
+				const double gv = ldexp((double)combine(p0, p1, p2), E[u] - 23);
+				v[u * NC + q] = sc[q] * (float)(cls[u] == 2 ? gv + outlier_sum(s, w, m, cc[q]) : gv);
+			}
+		}
+		for (int e = 0; e < a.nepi; e++) {
+			const int kind = a.epi[e].kind, op = a.epi[e].op;
+			if (kind == TGK_EW_UN) {
+				switch (op) {
+#define EPU(K) \
+	case K: \
+		for (int i = 0; i < NV; i++) v[i] = tg_uop(K, v[i]); \
+		break;
+					EPU(TGM_NEG) EPU(TGM_TANH) EPU(TGM_RELU) EPU(TGM_SIGMOID) EPU(TGM_EXP) EPU(TGM_SQRT) EPU(TGM_GELU)
+					EPU(TGM_SILU) EPU(TGM_SOFTPLUS) EPU(TGM_LOG) EPU(TGM_SIN) EPU(TGM_COS) EPU(TGM_FLOOR)
+					default: EPU(TGM_STEP)
+#undef EPU
+				}
+				continue;
+			}
+			const int mode = a.epi[e].mode;
+			float x[NV];
+			for (int u = 0; u < U; u++) {
+				const float *p = a.epi[e].x + (long)rr[u] * a.epi[e].xr;
+				for (int q = 0; q < NC; q++)
+					x[u * NC + q] = mode == 0 ? p[(long)jr[u] * a.oj + (long)cc[q] * a.oc] : mode == 1 ? p[0] : p[cc[q]];
+			}
+			const bool rev = kind == TGK_EW_BINR;
+			switch (op) {
+#define EPB(K) \
+	case K: \
+		for (int i = 0; i < NV; i++) v[i] = rev ? tg_bop(K, x[i], v[i]) : tg_bop(K, v[i], x[i]); \
+		break;
+				EPB(TGK_ADD) EPB(TGK_SUB) EPB(TGK_MUL) EPB(TGK_DIV) EPB(TGK_MAX)
+				default: EPB(TGK_MIN)
+#undef EPB
+			}
+		}
+		for (int u = 0; u < U; u++)
+			if (mb + u < m1)
+				for (int q = 0; q < NC; q++)
+					if (c[q] < w.C) *out_at(a, rr[u], jr[u], c[q]) = v[u * NC + q];
+	}
+}
+
 template <int BITS>
 int launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 {
 	const tgk_qweight *w = a->w;
+	if (w->K <= 32 && a->M >= 1024 && (a->nseg <= 1 || !a->nepi)) { // many rows of few inputs: one thread per channel
+		const int rpb = a->M >= 65536 ? 64 : 16;
+		const dim3 grid((unsigned)((w->C + 511) / 512), (unsigned)((a->M + rpb - 1) / rpb));
+		if (w->K <= 16) qtiny_k<1, 2><<<grid, 256, 0, st>>>(*a, *w, s, rpb);
+		else qtiny_k<2, 2><<<grid, 256, 0, st>>>(*a, *w, s, rpb);
+		return TGK_DID_CHAIN;
+	}
 	const int gx = w->Cp / BN, gy = Mp / BM;
 	const long rt = round_up(a->M, 32) / 32, cb = w->Cp / 32;
 	if ((long)gx * gy >= 128 && rt > 2) { // enough 128 x 256 tiles for the LDS kernel

@@ -8,7 +8,8 @@ instruction reading the product, which keeps the layer builder from fusing,
 and the two outputs are compared. The row op runs inside the large-batch GEMM
 when a tile holds whole lines (C <= 256, channel stride 1) and after it
 otherwise; the cases cover both, every other GEMM kernel (one row, up to 16
-rows, the small-batch tiles), int4 and int8 weights, both operand orders,
+rows, the small-batch tiles, the kernel for rows of at most 32 inputs), int4
+and int8 weights, both operand orders,
 all three operand forms, rows the reference's loop takes (inf, nan), and a
 line with an outlier (a split row)."""
 import numpy as np
@@ -74,7 +75,7 @@ def _rows(seed, rows, per, specials=False):
 
 
 @pytest.mark.parametrize("bits,rows,K,C", [(4, 1, 1024, 96), (4, 5, 1024, 96), (8, 40, 512, 300), (8, 700, 512, 2048),
-                                           (4, 2100, 512, 2048)])
+                                           (4, 2100, 512, 2048), (8, 1200, 16, 600)])
 def test_bias_tanh_vector(bits, rows, K, C):
     """W @ x + b, then tanh: every GEMM kernel, one output line per row"""
     print("case bias tanh", bits, rows, K, C, flush=True)
@@ -84,7 +85,7 @@ def test_bias_tanh_vector(bits, rows, K, C):
 
 
 @pytest.mark.parametrize("bits,rows,T,K,C", [(4, 300, 64, 256, 256), (8, 3, 64, 256, 256), (8, 200, 96, 384, 200),
-                                             (4, 40, 64, 512, 512)])
+                                             (4, 40, 64, 512, 512), (4, 20, 64, 30, 64)])
 def test_residual_rmsnorm(bits, rows, T, K, C):
     """rmsnorm(r + x @ W) over the C channels: inside the large-batch GEMM
     for C <= 256 at >= 16384 lines, after it otherwise"""
@@ -96,7 +97,8 @@ def test_residual_rmsnorm(bits, rows, T, K, C):
     _case(params, [("x", "%d %d" % (T, K)), ("r", "%d %d" % (T, C))], body, "%2", "%d %d" % (T, C), x, 2)
 
 
-@pytest.mark.parametrize("bits,rows,T,K,C", [(8, 200, 96, 384, 200), (4, 300, 64, 256, 24), (4, 7, 64, 256, 24)])
+@pytest.mark.parametrize("bits,rows,T,K,C", [(8, 200, 96, 384, 200), (4, 300, 64, 256, 24), (4, 7, 64, 256, 24),
+                                             (8, 40, 64, 16, 24)])
 def test_scale_bias_softmax(bits, rows, T, K, C):
     """softmax(s * (x @ W) - b): a scalar, a per-channel operand on the left
     of a subtraction, then the softmax"""

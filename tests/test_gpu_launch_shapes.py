@@ -1,6 +1,7 @@
 """Every launch shape of the matrix-core path (technograd_amd/csrc/kern_qgemm.hip,
-launch_gemm): the large-batch LDS kernel and each (NB column blocks, W waves)
-instantiation of the small-batch kernel, int4 and int8 weights, checked bit
+launch_gemm): the large-batch LDS kernel, each (NB column blocks, W waves)
+instantiation of the small-batch kernel and the kernel for rows of at most
+32 inputs, int4 and int8 weights, checked bit
 for bit against the path's own arithmetic restated on the host
 (tests/parity.py: device_path_matmul: the digit path, a split row for an
 outlier, and the reference's loop for special rows). The reference-order parity of the same
@@ -52,6 +53,9 @@ SHAPES = [
     (4, 1, 256, 4096),     # gemv1_k fused, NL=1
     (8, 1, 256, 4096),     # gemv16_k NS=1 W=4
     (8, 2, 8192, 2048),    # int8 beyond 4096 inputs: qgemv_k NB=1 W=8
+    (8, 2048, 16, 512),    # qtiny_k (at most 32 inputs, at least 1024 rows): one 16-input group
+    (4, 1500, 30, 1000),   # qtiny_k, two groups, int4, channels not a multiple of 256
+    (8, 1024, 1, 300),     # qtiny_k, one input
 ]
 
 
@@ -78,7 +82,7 @@ def test_launch_shape_bit_exact(bits_, M, K, C):
         x[3, K // 3] = 1e4  # an outlier: its row leaves its grid (split)
     got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
     want, cls = device_path_matmul(x, codes, scales)
-    assert M <= 3 or cls[3] != 0
+    assert M <= 3 or K < 16 or cls[3] != 0  # (one input: a lone large entry is the whole row, on its grid)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), np.argwhere(got != want)[:5].tolist()
 
 
