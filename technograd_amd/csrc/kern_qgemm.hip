@@ -1666,80 +1666,59 @@ void launch_gemv(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
 	qgemv_k<BITS, NB, W, P><<<gx * gy, 64 * W, 0, st>>>(*a, *a->w, s, gx);
 }
 
-// Products over at most 32 inputs (a selective SSM's dt projection has 16).
-// The matrix-core kernels pad these to 64 inputs and spend their time in the
-// per-output epilogue, the reference-loop and split rows' slow path taken by
-// nearly every wave. Here a thread takes NC channels (c = 256 (NC blockIdx.x
-// + q) + thread, q < NC) over the workgroup's rows, U at a time, from the
-// digits and row data the digit kernel left, so every output is the one the
-// matrix-core path gives: the row's three digit planes dotted with the
-// channel's codes by v_dot4_i32_i8 (the codes in registers as signed bytes,
-// four inputs a word) and combined exactly; a reference-loop row by the
-// reference's sequential loop; a split row with its outlier terms in f64
-// (outlier_sum); then the scale and the chain, each instruction applied to
-// the U NC values at once, as staged_epilogue applies it. A row's class and
-// exponent are the same for every lane (read into scalar registers, so the
-// class decides by a uniform branch); the U rows' classes, exponents and
-// digits are read before any of their arithmetic (one round trip per U rows).
-template <int NG, int NC>
-__global__ __launch_bounds__(256) void qtiny_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int rows_per_block)
+// Products over at most TGK_REFLOOP_K inputs (a selective SSM's dt projection
+// has 16) take the reference's sequential loop for every row
+// (runtime/tg_rt.h:132-151): at that length it costs about what the exact
+// digit path costs per output (16 inputs: 16 multiplies and 16 adds against
+// 12 four-way dot products, the planes' combination and a digit kernel before
+// the product), and it needs no digits, no row class and no resolve; every
+// output is the reference's bit for bit, at every batch size. A thread takes
+// NC channels (c = 256 (NC blockIdx.x + q) + thread, q < NC) over the
+// workgroup's rows, U at a time: the U rows' inputs are read first (one round
+// trip), the channels' codes are kept in registers as floats, each sum runs
+// k = 0 .. K - 1 as the reference's does (product rounded, then the add);
+// then the scale and, when `chain`, the chain, each instruction applied to the
+// U NC values at once as staged_epilogue applies it.
+template <int KM, int NC, int U, bool VEC>
+__global__ __launch_bounds__(256) void qtiny_k(tgk_qgemm_args a, tgk_qweight w, int rows_per_block, int chain)
 {
-	constexpr int U = 4, NV = U * NC;
-	int c[NC], cc[NC], cw[NC][4 * NG]; // channel cc's codes: byte e of word j is input 4 j + e's
-	float sc[NC];
+	constexpr int NV = U * NC;
+	int c[NC], cc[NC];
+	float cf[NC][KM], sc[NC];
 	for (int q = 0; q < NC; q++) {
 		c[q] = 256 * (NC * blockIdx.x + q) + threadIdx.x;
 		cc[q] = c[q] < w.C ? c[q] : w.C - 1;
-		for (int j = 0; j < 4 * NG; j++) {
-			unsigned word = 0;
-			for (int e = 0; e < 4; e++)
-				if (4 * j + e < w.K) word |= (unsigned)(code_orig(w, cc[q], 4 * j + e) & 255) << (8 * e);
-			cw[q][j] = (int)word;
-		}
+		for (int k = 0; k < KM; k++) cf[q][k] = k < w.K ? (float)code_orig(w, cc[q], k) : 0.0f;
 		sc[q] = w.scale[cc[q]];
 	}
 	const bool flat = a.ni == 1; // (uniform) row m is batch row m: no division
 	const int m0 = blockIdx.y * rows_per_block, m1 = a.M - m0 < rows_per_block ? a.M : m0 + rows_per_block;
 	for (int mb = m0; mb < m1; mb += U) {
-		int cls[U], E[U], rr[U], jr[U];
-		int dg[U][3][4 * NG];
+		int rr[U], jr[U];
+		float xv[U][KM];
 		for (int u = 0; u < U; u++) {
 			const int m = mb + u < m1 ? mb + u : m0; // past the block's rows: a row of it, not stored
 			rr[u] = flat ? m : m / a.ni;
 			jr[u] = m - rr[u] * a.ni;
-			cls[u] = __builtin_amdgcn_readfirstlane(s.special[m]);
-			E[u] = __builtin_amdgcn_readfirstlane(s.e[m]);
-			const int8_t *blk = tgq_row_base(s.dig, m, w.Kp); // inputs 16 g ..: chunk (g & 1) of block 0 (NG <= 2)
-			for (int g = 0; g < NG; g++)
-				for (int l = 0; l < 3; l++) {
-					const v4i d = *(const v4i *)(blk + g * 512 + l * 1024);
-					dg[u][l][4 * g] = d.x, dg[u][l][4 * g + 1] = d.y, dg[u][l][4 * g + 2] = d.z, dg[u][l][4 * g + 3] = d.w;
+			const float *x = xrow(a, m);
+			if constexpr (VEC) { // unit stride, 16-byte aligned, K a multiple of 4
+				for (int k = 0; k < KM; k += 4) {
+					const float4 f = k < w.K ? *(const float4 *)(x + k) : float4{ 0.0f, 0.0f, 0.0f, 0.0f };
+					xv[u][k] = f.x, xv[u][k + 1] = f.y, xv[u][k + 2] = f.z, xv[u][k + 3] = f.w;
 				}
+			} else {
+				for (int k = 0; k < KM; k++) xv[u][k] = k < w.K ? x[(long)k * a.xk] : 0.0f;
+			}
 		}
 		float v[NV]; // value (u, q) at u NC + q
-		for (int u = 0; u < U; u++) {
-			const int m = mb + u < m1 ? mb + u : m0;
-			if (cls[u] & 1) { // the reference's loop (runtime/tg_rt.h:132-151)
-				const float *x = xrow(a, m);
-				for (int q = 0; q < NC; q++) {
-					float t = 0.0f;
-					for (int k = 0; k < w.K; k++) t += (float)(signed char)(cw[q][k >> 2] >> (8 * (k & 3))) * x[(long)k * a.xk];
-					v[u * NC + q] = sc[q] * t;
-				}
-				continue;
-			}
+		for (int u = 0; u < U; u++)
 			for (int q = 0; q < NC; q++) {
-				int p0 = 0, p1 = 0, p2 = 0;
-				for (int j = 0; j < 4 * NG; j++) {
-					p0 = __builtin_amdgcn_sdot4(dg[u][0][j], cw[q][j], p0, false);
-					p1 = __builtin_amdgcn_sdot4(dg[u][1][j], cw[q][j], p1, false);
-					p2 = __builtin_amdgcn_sdot4(dg[u][2][j], cw[q][j], p2, false);
-				}
-				const double gv = ldexp((double)combine(p0, p1, p2), E[u] - 23);
-				v[u * NC + q] = sc[q] * (float)(cls[u] == 2 ? gv + outlier_sum(s, w, m, cc[q]) : gv);
+				float t = 0.0f;
+				for (int k = 0; k < KM; k++)
+					if (k < w.K) t += cf[q][k] * xv[u][k];
+				v[u * NC + q] = sc[q] * t;
 			}
-		}
-		for (int e = 0; e < a.nepi; e++) {
+		for (int e = 0; chain && e < a.nepi; e++) {
 			const int kind = a.epi[e].kind, op = a.epi[e].op;
 			if (kind == TGK_EW_UN) {
 				switch (op) {
@@ -1779,16 +1758,26 @@ __global__ __launch_bounds__(256) void qtiny_k(tgk_qgemm_args a, tgk_qweight w, 
 	}
 }
 
+template <int KM, int U>
+void launch_qtiny(hipStream_t st, const tgk_qgemm_args *a, int chain)
+{
+	const tgk_qweight *w = a->w;
+	const int rpb = a->M >= 65536 ? 64 : a->M >= 4096 ? 16 : 4;
+	const dim3 grid((unsigned)((w->C + 511) / 512), (unsigned)((a->M + rpb - 1) / rpb));
+	const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) && (w->K & 3) == 0;
+	if (vec) qtiny_k<KM, 2, U, true><<<grid, 256, 0, st>>>(*a, *w, rpb, chain);
+	else qtiny_k<KM, 2, U, false><<<grid, 256, 0, st>>>(*a, *w, rpb, chain);
+}
+
 template <int BITS>
 int launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 {
 	const tgk_qweight *w = a->w;
-	if (w->K <= 32 && a->M >= 1024 && (a->nseg <= 1 || !a->nepi)) { // many rows of few inputs: one thread per channel
-		const int rpb = a->M >= 65536 ? 64 : 16;
-		const dim3 grid((unsigned)((w->C + 511) / 512), (unsigned)((a->M + rpb - 1) / rpb));
-		if (w->K <= 16) qtiny_k<1, 2><<<grid, 256, 0, st>>>(*a, *w, s, rpb);
-		else qtiny_k<2, 2><<<grid, 256, 0, st>>>(*a, *w, s, rpb);
-		return TGK_DID_CHAIN;
+	if (w->K <= TGK_REFLOOP_K) { // the reference's loop for every row (no digits were made)
+		const int chain = a->nseg <= 1; // a chain over segmented outputs is the caller's (tgk_qgemm_chain)
+		if (w->K <= 16) launch_qtiny<16, 4>(st, a, chain);
+		else launch_qtiny<32, 2>(st, a, chain);
+		return chain ? TGK_DID_CHAIN : 0;
 	}
 	const int gx = w->Cp / BN, gy = Mp / BM;
 	const long rt = round_up(a->M, 32) / 32, cb = w->Cp / 32;
@@ -1986,6 +1975,7 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
 	const tgk_qweight *w = a->w;
 	if (!w || !w->w || !a->x || !scratch || a->M <= 0 || a->ni <= 0 || w->K <= 0) return; /* nothing valid to launch */
+	if (w->K <= TGK_REFLOOP_K) return;                                                   /* the product takes the reference's loop */
 	int Mp = (int)round_up(a->M, BM);
 	const Scratch s = carve(scratch, Mp, w->Kp);
 	const int nkb = w->Kp / 32, M = a->M, K = w->K;
@@ -2036,7 +2026,7 @@ void tgk_qgemm_split(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 {
 	const tgk_qweight *w = a->w;
 	const int M = a->M;
-	if (!w || !a->x || !scratch || M <= 0 || a->ni <= 0 || w->K <= 0) return;
+	if (!w || !a->x || !scratch || M <= 0 || a->ni <= 0 || w->K <= TGK_REFLOOP_K) return;
 	const Scratch s = carve(scratch, (int)round_up(M, BM), w->Kp);
 	const long blocks = (M + 3) / 4;
 	const unsigned nb = (unsigned)(blocks < 16384 ? blocks : 16384);
@@ -2079,8 +2069,8 @@ void tgk_qgemm_chain(hipStream_t st, const tgk_qgemm_args *a)
 bool tgk_qgemm_fusable(const tgk_qgemm_args *a)
 {
 	const tgk_qweight *w = a->w;
-	return w && w->w && a->x && a->M == 1 && w->bits == 4 && w->Kp <= 8192 && a->xk == 1 && ((size_t)a->x & 15) == 0 &&
-	       (w->K & 15) == 0;
+	return w && w->w && a->x && a->M == 1 && w->bits == 4 && w->K > TGK_REFLOOP_K && w->Kp <= 8192 && a->xk == 1 &&
+	       ((size_t)a->x & 15) == 0 && (w->K & 15) == 0;
 }
 
 int tgk_qgemm_fused(hipStream_t st, const tgk_qgemm_args *a, void *scratch)

@@ -270,6 +270,10 @@ typedef struct {
 	int rowop;
 } tgk_qgemm_args;
 
+/* Products over at most this many inputs take the reference's sequential
+ * loop for every row, bit for bit (no digits: tgk_qgemm_digits and
+ * tgk_qgemm_split launch nothing for them) */
+#define TGK_REFLOOP_K 32
 /* scratch: bytes needed for M rows of K inputs */
 /* One row of int4 weights (M = 1, unit-stride 16-byte-aligned row, K a
  * multiple of 16, K <= 8192): tgk_qgemm_fused computes the digits inside

@@ -317,11 +317,17 @@ def split_rows_matmul(x_mk, codes_kc, scale_c, omask):
     return out
 
 
+REFLOOP_K = 32  # kern_qgemm.hip (tg_kern.h: TGK_REFLOOP_K)
+
+
 def device_path_matmul(x_mk, codes_kc, scale_c):
     """What the device computes for x @ W, at any batch size: rows on their
     grid (digit_path_matmul), split rows (split_rows_matmul) and the
-    reference's loop, by row_classes. Returns (f32 [M, C], cls [M])."""
+    reference's loop, by row_classes; products over at most REFLOOP_K inputs
+    take the reference's loop for every row. Returns (f32 [M, C], cls [M])."""
     x = np.asarray(x_mk, np.float32)
+    if x.shape[1] <= REFLOOP_K:
+        return reference_loop(x, codes_kc, scale_c), np.ones(x.shape[0], np.int64)
     got, _ = digit_path_matmul(x, codes_kc, scale_c)
     cls, level, E = row_classes(x)
     sp = cls == 2

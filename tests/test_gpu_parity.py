@@ -312,6 +312,38 @@ def test_outlier_rows_at_every_batch_size(bits_, axis):
         assert _same(got[sub[:2]], r2)
 
 
+@pytest.mark.parametrize("bits_,axis,K", [(8, 1, 16), (4, 1, 30), (8, 0, 16), (4, 0, 1)])
+def test_short_products_are_the_reference(bits_, axis, K):
+    """Products over at most 32 inputs take the reference's loop for every
+    row (kern_qgemm.hip: qtiny_k; no digits): every output equals the
+    oracle's bit for bit, at one row, 16 rows, 1024 rows and 5000 rows, on
+    N(0, 1) rows with outliers, zeros, tiny rows, an infinite and a NaN
+    entry. axis 0 reads the rows strided."""
+    print("case short products", bits_, axis, K, flush=True)
+    C = 700
+    lim = 7 if bits_ == 4 else 127
+    rng = np.random.default_rng(K * 3 + bits_ + axis)
+    codes = rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8)
+    scales = rng.uniform(0.001, 0.1, size=C).astype(np.float32)
+    stored = codes if axis == 1 else np.ascontiguousarray(codes.T)
+    packed = _packed(stored, bits_)
+    model = O.Model(synth.linear_tgir_codes("lq", codes, scales, bits_, axis=1))
+    for M in (1, 16, 1024, 5000):
+        x = rng.normal(size=(M, K)).astype(np.float32)
+        x[0, K // 2] = 1e4
+        if M > 4:
+            x[1] = 0.0
+            x[2] *= 1e-30
+            x[3, 0], x[4, K - 1] = np.inf, np.nan
+        if axis == 1:
+            got = hip.matmul_q(packed, bits_, scales, x, M, K, C, 1)
+        else:
+            got = np.ascontiguousarray(hip.matmul_q(packed, bits_, scales, np.ascontiguousarray(x.T), C, K, M, 0).T)
+        ref, _ = model.batch(x, threads=16)
+        assert _same(got, ref), ("M", M)
+        print("short products M = %d: bit for bit" % M, flush=True)
+
+
 def _f32_matmul_models():
     rng = np.random.default_rng(31)
     W1 = rng.normal(size=(150, 260)).astype(np.float32)
