@@ -253,7 +253,9 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 				tgk_matmul_exact(st, &m, S);
 			}
 		}
-		if (T0 == 1 && tgk_dec_wo_lds(rows, d->HD) <= 65536) // a step: all heads in one launch, the same values
+		// a step: all heads in one launch, the same values (heads of at most TGK_REFLOOP_K take the
+		// reference's loop, as every short product does: the per-head products below)
+		if (T0 == 1 && d->HD > TGK_REFLOOP_K && tgk_dec_wo_lds(rows, d->HD) <= 65536)
 			tgk_dec_wo(st, d->att, d->wo_codes[(size_t)l], d->wo_scales[(size_t)l], d->wout, rows, d->NQ, d->HD, d->D);
 		else
 			for (int hh = 0; hh < d->NQ; hh++)
