@@ -66,6 +66,8 @@ typedef struct {
 	long rowprog_hoisted; /* instructions the compiled row program runs once in front of their think loop */
 	int epilogue_ins;    /* layer program: instructions after quantized products that their GEMMs apply in
 	                        their epilogues (elementwise chains, softmax / rmsnorm over the channels) */
+	int scan_folded_ins; /* layer program: instructions around fused selective scans that the scans' kernels
+	                        apply (the du product before a scan, the gate after it) */
 } tg_hip_stats_t;
 
 /* Select the device (ordinal) for subsequent calls; 0 on success. */

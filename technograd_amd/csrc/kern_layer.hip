@@ -745,14 +745,22 @@ namespace {
 // -ffp-contract=off), in the same order, so the results are bit-identical to
 // running the body one instruction per launch. A block covers channels of
 // a single row, so B_t and C_t are the same for every lane of a wave.
-template <int N>
+// DUX: du_t = dt_t * dux_t, formed as the steps are loaded (the instruction
+// that made the du sequence, folded in). GATE: the stacked output is
+// (y_t + gx_t * gD) * silu(gz_t) (Mamba's gate, the four instructions after
+// the scan, folded in), each operation as the elementwise kernels compute it
+// (tg_ewop.h); a chunk's gate operands are loaded as the chunk starts and its
+// outputs gated once its steps are done.
+template <int N, bool DUX, bool GATE>
 __global__ __launch_bounds__(256) void sscan_k(float *h, long hrs, tgk_opd dt, tgk_opd du, tgk_opd Bq, tgk_opd Cq, tgk_opd A,
-					       float *ys, long yrs, int D, int T, int reverse, int dblocks)
+					       float *ys, long yrs, int D, int T, int reverse, int dblocks, tgk_sscan_fuse fu)
 {
 	// Steps go in chunks of U. While chunk c is computed, chunk c + 1's dt and
 	// du are in flight into registers and its B and C into registers bound
 	// for the other LDS buffer, so the step loop never waits on memory.
-	constexpr int U = 16, BC = U * 2 * N, PER = (BC + 255) / 256;
+	// (8 steps a chunk with the gate folded in: its operands and outputs are
+	// buffered per chunk, and the registers decide how many waves share a SIMD)
+	constexpr int U = GATE ? 8 : 16, BC = U * 2 * N, PER = (BC + 255) / 256;
 	__shared__ float bc[2][BC]; // [step][B_0 .. B_N-1, C_0 .. C_N-1]
 	const int r = blockIdx.x / dblocks;
 	const int d = (blockIdx.x - r * dblocks) * 256 + threadIdx.x;
@@ -764,7 +772,7 @@ __global__ __launch_bounds__(256) void sscan_k(float *h, long hrs, tgk_opd dt, t
 		hv[n] = hp[n];
 		av[n] = A.p[(long)r * A.rs + (long)dd * N + n];
 	}
-	const float *dtp = dt.p + (long)r * dt.rs, *dup = du.p + (long)r * du.rs;
+	const float *dtp = dt.p + (long)r * dt.rs, *dup = (DUX ? fu.dux : du).p + (long)r * (DUX ? fu.dux : du).rs;
 	const float *bp = Bq.p + (long)r * Bq.rs, *cp = Cq.p + (long)r * Cq.rs;
 	float *yp = ys + (long)r * yrs;
 	auto tstep = [&](int s) { return reverse ? T - 1 - s : s; };
@@ -774,7 +782,12 @@ __global__ __launch_bounds__(256) void sscan_k(float *h, long hrs, tgk_opd dt, t
 			a[u] = dtp[(long)t * D + dd];
 			b[u] = dup[(long)t * D + dd];
 		}
+		if constexpr (DUX)
+			for (int u = 0; u < U; u++) b[u] = tg_bop(TGK_MUL, a[u], b[u]);
 	};
+	const float *gxp = GATE ? fu.gx.p + (long)r * fu.gx.rs : nullptr, *gzp = GATE ? fu.gz.p + (long)r * fu.gz.rs : nullptr;
+	const float gdv = GATE ? fu.gD[dd] : 0.0f;
+	float gxc[GATE ? U : 1], gzc[GATE ? U : 1], yb[GATE ? U : 1];
 	float bcr[PER];
 	auto load_bc = [&](int s0) {
 		for (int j = 0; j < PER; j++) {
@@ -804,6 +817,12 @@ __global__ __launch_bounds__(256) void sscan_k(float *h, long hrs, tgk_opd dt, t
 		const float *bcb = bc[c & 1];
 		float *yt = yp + (long)tstep(s0) * D + d;
 		const long ystep = reverse ? -(long)D : (long)D;
+		if constexpr (GATE)
+			for (int u = 0; u < U; u++) {
+				const long t = tstep(s0 + u < T ? s0 + u : T - 1);
+				gxc[u] = gxp[t * D + dd];
+				gzc[u] = gzp[t * D + dd];
+			}
 #pragma unroll
 		for (int u = 0; u < U; u++) {
 			if (s0 + u < T) {
@@ -815,9 +834,14 @@ __global__ __launch_bounds__(256) void sscan_k(float *h, long hrs, tgk_opd dt, t
 					hv[n] = hn;
 					y = y + hn * bcb[u * 2 * N + N + n];
 				}
-				if (live) yt[u * ystep] = y;
+				if constexpr (GATE) yb[u] = y;
+				else if (live) yt[u * ystep] = y;
 			}
 		}
+		if constexpr (GATE)
+			for (int u = 0; u < U; u++)
+				if (s0 + u < T && live)
+					yt[u * ystep] = tg_bop(TGK_MUL, tg_bop(TGK_ADD, yb[u], tg_bop(TGK_MUL, gxc[u], gdv)), tg_uop(TGM_SILU, gzc[u]));
 		if (more) {
 			store_bc((c + 1) & 1);
 			for (int u = 0; u < U; u++) dtc[u] = dtn[u], duc[u] = dun[u];
@@ -832,16 +856,32 @@ __global__ __launch_bounds__(256) void sscan_k(float *h, long hrs, tgk_opd dt, t
 
 bool tgk_sscan_supported(int N) { return N == 4 || N == 8 || N == 16; }
 
+namespace {
+
+template <int N>
+void launch_sscan(hipStream_t s, unsigned grid, float *h, long hrs, tgk_opd dt, tgk_opd du, tgk_opd Bq, tgk_opd Cq, tgk_opd A, float *ys,
+		  long yrs, int D, int T, int reverse, int dblocks, const tgk_sscan_fuse &f)
+{
+	const bool dux = f.dux.p != nullptr, gate = f.gx.p != nullptr;
+	if (dux && gate) sscan_k<N, true, true><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks, f);
+	else if (dux) sscan_k<N, true, false><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks, f);
+	else if (gate) sscan_k<N, false, true><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks, f);
+	else sscan_k<N, false, false><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks, f);
+}
+
+} // namespace
+
 void tgk_sscan(hipStream_t s, float *h, long hrs, tgk_opd dt, tgk_opd du, tgk_opd Bq, tgk_opd Cq, tgk_opd A, float *ys, long yrs, int D,
-	       int N, int T, int reverse, int rows)
+	       int N, int T, int reverse, int rows, const tgk_sscan_fuse *fuse)
 {
 	if (rows <= 0 || D <= 0 || T <= 0) return; // T = 0: the carry keeps its initial value
 	const int dblocks = (D + 255) / 256;
 	const unsigned grid = (unsigned)(rows * dblocks);
+	const tgk_sscan_fuse f = fuse ? *fuse : tgk_sscan_fuse{};
 	switch (N) {
-	case 4: sscan_k<4><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks); break;
-	case 8: sscan_k<8><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks); break;
-	case 16: sscan_k<16><<<grid, 256, 0, s>>>(h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks); break;
+	case 4: launch_sscan<4>(s, grid, h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks, f); break;
+	case 8: launch_sscan<8>(s, grid, h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks, f); break;
+	case 16: launch_sscan<16>(s, grid, h, hrs, dt, du, Bq, Cq, A, ys, yrs, D, T, reverse, dblocks, f); break;
 	default: break;
 	}
 }

@@ -159,6 +159,10 @@ struct Step {
 	int T = 0, reverse = 0, body_lo = 0, body_hi = 0, stid = -1;
 	// fused selective scan: B and C sequences, A, stacked outputs
 	Opnd e0, e1, e2, e3;
+	// fused selective scan: neighbours folded in (tgk_sscan_fuse): fdu, du made from dt and b; fgate, the gate's
+	// x, D and z in f0, f1, f2 (e3 then holds the gate's output)
+	Opnd f0, f1, f2;
+	int fdu = 0, fgate = 0;
 	// fused elementwise run (index into tg_hip_prog::ews)
 	int ew = -1;
 	// quantized GEMM whose activation digits the previous step left in the scratch
@@ -357,6 +361,12 @@ struct LB {
 	std::vector<Opnd> where; // value -> operand
 	std::vector<char> loopw; // values written in place by loops (scan carries, slices, stacks)
 	std::vector<int> tview;  // rank-2 transposes read only by one f32 matmul: the transposed value (else -1)
+	std::vector<char> skip;  // top-block instructions folded into a fused scan (plan_sscan)
+	struct SscanPlan {
+		int dux = -1;                       // du = mul(dt, dux): the kernel forms it
+		int gx = -1, gD = -1, gz = -1, out = -1; // out = (ys + gx * gD) * silu(gz): the kernel writes it
+	};
+	std::map<const tgm_ins *, SscanPlan> sscan;
 };
 
 void count_uses(const tgm_block *b, std::vector<int> &u);
@@ -427,7 +437,7 @@ void place_arena(tg_hip_prog *p, const tgm_module *m)
 	};
 	for (long i = 0; i < (long)S.size(); i++) {
 		const Step &st = S[i];
-		for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 }) touch(*o, i);
+		for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3, &st.f0, &st.f1, &st.f2 }) touch(*o, i);
 		for (int e = 0; e < st.nepi; e++) touch(st.epi[e].x, i);
 		if (st.kind == ST_EW) {
 			for (const EwStep::In &x : p->ews[(size_t)st.ew].in) touch(x.o, i);
@@ -500,7 +510,7 @@ void place_arena(tg_hip_prog *p, const tgm_module *m)
 		if (o.space == SP_ARENA) o.off = off[(int)o.off];
 	};
 	for (Step &st : S) {
-		for (Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 }) fix(*o);
+		for (Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3, &st.f0, &st.f1, &st.f2 }) fix(*o);
 		for (int e = 0; e < st.nepi; e++) fix(st.epi[e].x);
 	}
 	for (EwStep &E : p->ews) {
@@ -598,7 +608,7 @@ void finish_ew(tg_hip_prog *p)
 	std::vector<Opnd> used; // operands read or written by steps other than fused runs, plus the output
 	for (const Step &st : p->steps)
 		if (st.kind != ST_EW && st.kind != ST_NOP) {
-			for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3 })
+			for (const Opnd *o : { &st.o, &st.a, &st.b, &st.e0, &st.e1, &st.e2, &st.e3, &st.f0, &st.f1, &st.f2 })
 				if (o->space == SP_ARENA || o->space == SP_OUT) used.push_back(*o);
 			for (int e = 0; e < st.nepi; e++) // a GEMM epilogue's operands
 				if (st.epi[e].x.space == SP_ARENA || st.epi[e].x.space == SP_OUT) used.push_back(st.epi[e].x);
@@ -713,10 +723,9 @@ void finish_ew(tg_hip_prog *p)
 // h the only carry; commuted mul/add operands accepted) runs as one fused
 // kernel (tgk_sscan) instead of seven launches per step. Any other body takes
 // the general path.
-bool match_sscan(LB &L, const tgm_ins &in, Step &st)
+bool sscan_shape(const tgm_module *m, const tgm_ins &in, int &jdt, int &jdu, int &jb, int &jc, int &A)
 {
-	const tgm_module *m = L.m;
-	if (in.nc != 1 || in.ny != 1 || in.nx != 4 || in.stid >= 0 || !in.body || in.body->len != 7) return false;
+	if (in.op != TGM_SCAN || in.nc != 1 || in.ny != 1 || in.nx != 4 || in.stid >= 0 || !in.body || in.body->len != 7) return false;
 	const tgm_ins *b = in.body->v;
 	const int h = in.c[0];
 	const tgm_shape &hs = m->val[h].sh;
@@ -734,28 +743,125 @@ bool match_sscan(LB &L, const tgm_ins &in, Step &st)
 	};
 	auto pair = [](const tgm_ins &i, int u, int v) { return (i.a[0] == u && i.a[1] == v) || (i.a[0] == v && i.a[1] == u); };
 	if (b[0].op != TGM_RESHAPE || !shaped(b[0].out, 2, D, 1) || !shaped(b[0].a[0], 1, D, 0)) return false;
-	const int jdt = slice(b[0].a[0]);
+	jdt = slice(b[0].a[0]);
 	if (b[1].op != TGM_MUL || !shaped(b[1].out, 2, D, N)) return false;
-	const int A = b[1].a[0] == b[0].out ? b[1].a[1] : b[1].a[1] == b[0].out ? b[1].a[0] : -1;
+	A = b[1].a[0] == b[0].out ? b[1].a[1] : b[1].a[1] == b[0].out ? b[1].a[0] : -1;
 	if (A < 0 || m->val[A].kind != TGM_PARAM || m->val[A].qbits || !shaped(A, 2, D, N)) return false;
 	if (b[2].op != TGM_EXP || b[2].a[0] != b[1].out) return false;
 	if (b[3].op != TGM_MUL || !pair(b[3], b[2].out, h)) return false;
 	if (b[4].op != TGM_OUTER || !shaped(b[4].a[0], 1, D, 0) || !shaped(b[4].a[1], 1, N, 0)) return false;
-	const int jdu = slice(b[4].a[0]), jb = slice(b[4].a[1]);
+	jdu = slice(b[4].a[0]), jb = slice(b[4].a[1]);
 	if (b[5].op != TGM_ADD || !pair(b[5], b[3].out, b[4].out)) return false;
 	if (b[6].op != TGM_MATMUL || b[6].a[0] != b[5].out || !shaped(b[6].out, 1, D, 0) || !shaped(b[6].a[1], 1, N, 0)) return false;
-	const int jc = slice(b[6].a[1]);
+	jc = slice(b[6].a[1]);
 	if (jdt < 0 || jdu < 0 || jb < 0 || jc < 0) return false;
 	if (jdt == jdu || jdt == jb || jdt == jc || jdu == jb || jdu == jc || jb == jc) return false;
-	if (in.cnext[0] != b[5].out || in.y[0] != b[6].out) return false;
+	return in.cnext[0] == b[5].out && in.y[0] == b[6].out;
+}
+
+// A fused scan of the top block takes in what Mamba's block computes right
+// around it, when nothing else reads the values in between (every value is
+// written once, so they can be formed where they are read):
+//  - its du sequence made by (mul dt X), dt its own dt sequence, X of du's
+//    shape: the kernel forms dt_t * X_t as it loads the steps;
+//  - its stacked output read only by (add ys P) with P = (mul X2 Dv), Dv a
+//    rank-1 param of one value per channel, whose sum is read only by
+//    (mul S G), G = (silu Z): the kernel writes (ys + X2 Dv) * silu(Z) in
+//    place of ys. X2 and Z must be made before the scan.
+// The folded instructions are skipped by layer_block; each operation is the
+// one their kernels compute, so the values are unchanged.
+void plan_sscan(LB &L)
+{
+	const tgm_module *m = L.m;
+	const tgm_block &b = m->top;
+	L.skip.assign((size_t)b.len, 0);
+	std::vector<int> uses((size_t)m->nval, 0), prod((size_t)m->nval, -1), reader((size_t)m->nval, -1);
+	count_uses(&b, uses);
+	uses[(size_t)m->output]++;
+	for (int i = 0; i < b.len; i++) {
+		const tgm_ins &in = b.v[i];
+		if (in.out >= 0) prod[(size_t)in.out] = i;
+		for (int j = 0; j < in.na; j++) reader[(size_t)in.a[j]] = i;
+		if (in.op == TGM_SCAN) {
+			for (int k = 0; k < in.ny; k++) prod[(size_t)in.ys[k]] = i;
+			for (int k = 0; k < in.nx; k++) reader[(size_t)in.x[k]] = i;
+			for (int k = 0; k < in.nc; k++) reader[(size_t)in.cinit[k]] = i;
+		}
+	}
+	auto same_shape = [&](int u, int v) {
+		const tgm_shape &x = m->val[u].sh, &y = m->val[v].sh;
+		if (x.rank != y.rank) return false;
+		for (int d = 0; d < x.rank; d++)
+			if (x.dim[d] != y.dim[d]) return false;
+		return true;
+	};
+	auto other = [](const tgm_ins &in, int v) { return in.na != 2 ? -1 : in.a[0] == v ? in.a[1] : in.a[1] == v ? in.a[0] : -1; };
+	auto before = [&](int v, int i) { return prod[(size_t)v] < i; }; // made before instruction i (or not made here at all)
+	for (int i = 0; i < b.len; i++) {
+		const tgm_ins &in = b.v[i];
+		int jdt, jdu, jb, jc, A;
+		if (!sscan_shape(m, in, jdt, jdu, jb, jc, A)) continue;
+		LB::SscanPlan plan;
+		const int du = in.x[jdu], dt = in.x[jdt], j = prod[(size_t)du];
+		if (j >= 0 && j < i && uses[(size_t)du] == 1 && !L.loopw[(size_t)du] && b.v[j].op == TGM_MUL) {
+			const int X = other(b.v[j], dt);
+			if (X >= 0 && X != dt && same_shape(X, du) && before(X, j)) {
+				plan.dux = X;
+				L.skip[(size_t)j] = 1;
+			}
+		}
+		const int ys = in.ys[0], D = m->val[in.c[0]].sh.dim[0];
+		const int k1 = reader[(size_t)ys];
+		if (uses[(size_t)ys] == 1 && k1 > i && b.v[k1].op == TGM_ADD) {
+			const int P = other(b.v[k1], ys), k0 = P >= 0 ? prod[(size_t)P] : -1;
+			const int S = b.v[k1].out, k3 = reader[(size_t)S];
+			if (k0 >= 0 && uses[(size_t)P] == 1 && b.v[k0].op == TGM_MUL && same_shape(P, ys) && uses[(size_t)S] == 1 && k3 > k1 &&
+			    b.v[k3].op == TGM_MUL && same_shape(S, ys)) {
+				int X2 = -1, Dv = -1;
+				for (int q = 0; q < 2; q++) {
+					const int u = b.v[k0].a[q], v = b.v[k0].a[1 - q];
+					const tgm_value &pv = m->val[(size_t)v];
+					if (pv.kind == TGM_PARAM && !pv.qbits && pv.sh.rank == 1 && pv.sh.dim[0] == D && same_shape(u, ys)) X2 = u, Dv = v;
+				}
+				const int G = other(b.v[k3], S), k2 = G >= 0 ? prod[(size_t)G] : -1;
+				const int Z = k2 >= 0 && b.v[k2].op == TGM_SILU ? b.v[k2].a[0] : -1;
+				if (X2 >= 0 && before(X2, i) && Z >= 0 && uses[(size_t)G] == 1 && same_shape(G, ys) && same_shape(Z, ys) && before(Z, i) &&
+				    k2 != j && k0 != j) {
+					plan.gx = X2, plan.gD = Dv, plan.gz = Z, plan.out = b.v[k3].out;
+					L.skip[(size_t)k0] = L.skip[(size_t)k1] = L.skip[(size_t)k2] = L.skip[(size_t)k3] = 1;
+				}
+			}
+		}
+		if (plan.dux >= 0 || plan.out >= 0) L.sscan[&in] = plan;
+	}
+	for (char k : L.skip) L.p->stats.scan_folded_ins += k;
+}
+
+bool match_sscan(LB &L, const tgm_ins &in, Step &st)
+{
+	const tgm_module *m = L.m;
+	int jdt, jdu, jb, jc, A;
+	if (!sscan_shape(m, in, jdt, jdu, jb, jc, A)) return false;
+	const int h = in.c[0];
+	const tgm_shape &hs = m->val[h].sh;
+	const int D = hs.dim[0], N = hs.dim[1];
+	const auto pl = L.sscan.find(&in);
+	const LB::SscanPlan plan = pl == L.sscan.end() ? LB::SscanPlan{} : pl->second;
 	st.kind = ST_SSCAN;
 	st.o = value_opnd(L, h);
 	st.a = value_opnd(L, in.x[jdt]);
-	st.b = value_opnd(L, in.x[jdu]);
+	st.fdu = plan.dux >= 0;
+	st.b = value_opnd(L, st.fdu ? plan.dux : in.x[jdu]);
 	st.e0 = value_opnd(L, in.x[jb]);
 	st.e1 = value_opnd(L, in.x[jc]);
 	st.e2 = value_opnd(L, A);
-	st.e3 = value_opnd(L, in.ys[0]);
+	st.fgate = plan.out >= 0;
+	if (st.fgate) {
+		st.f0 = value_opnd(L, plan.gx);
+		st.f1 = value_opnd(L, plan.gD);
+		st.f2 = value_opnd(L, plan.gz);
+	}
+	st.e3 = value_opnd(L, st.fgate ? plan.out : in.ys[0]);
 	st.p0 = D;
 	st.p1 = N;
 	st.T = in.T;
@@ -1127,11 +1233,15 @@ int epi_chain(LB &L, const tgm_block *b, int i, Step &st)
 
 bool layer_block(LB &L, const tgm_block *b)
 {
+	const bool top = b == &L.m->top;
 	for (int i = 0; i < b->len; i++) {
 		const tgm_ins &in = b->v[i];
-		if (in.op == TGM_MATMUL && b == &L.m->top && !(L.p->flags & TG_HIP_EXACT) && matmul_quant(L.m, in)) {
+		if (top && L.skip[(size_t)i]) continue; // folded into a fused scan (plan_sscan)
+		if (in.op == TGM_MATMUL && top && !(L.p->flags & TG_HIP_EXACT) && matmul_quant(L.m, in)) {
 			Step chain;
-			const int last = epi_chain(L, b, i, chain);
+			int last = epi_chain(L, b, i, chain);
+			for (int k = i + 1; k <= last; k++)
+				if (L.skip[(size_t)k]) last = i; // (a chain never takes an instruction a scan folds in)
 			if (last > i) { // the GEMM writes the chain's last value
 				tgm_ins fused = in;
 				fused.out = b->v[last].out;
@@ -1575,10 +1685,14 @@ void exec_step(Run &R, const Step &s)
 		tgk_ew_run(st, &e, E.n, R.rows);
 		break;
 	}
-	case ST_SSCAN:
+	case ST_SSCAN: {
+		tgk_sscan_fuse f{};
+		if (s.fdu) f.dux = resolve(R, s.b);
+		if (s.fgate) f.gx = resolve(R, s.f0), f.gD = resolve(R, s.f1).p, f.gz = resolve(R, s.f2);
 		tgk_sscan(st, dst(R, s.o), s.o.rs, resolve(R, s.a), resolve(R, s.b), resolve(R, s.e0), resolve(R, s.e1), resolve(R, s.e2),
-			  dst(R, s.e3), s.e3.rs, s.p0, s.p1, s.T, s.reverse, R.rows);
+			  dst(R, s.e3), s.e3.rs, s.p0, s.p1, s.T, s.reverse, R.rows, &f);
 		break;
+	}
 	}
 }
 
@@ -1930,6 +2044,7 @@ bool build_layer(tg_hip_prog *p)
 	L.P.scale_of.assign(p->m->nval, -1);
 	mark_loop_values(&p->m->top, L.loopw);
 	mark_transpose_views(L);
+	plan_sscan(L);
 	if (p->m->val[p->m->output].kind == TGM_TMP) { /* written straight into the caller's output rows */
 		L.where[p->m->output].space = SP_OUT;
 		L.where[p->m->output].off = 0;

@@ -113,8 +113,16 @@ void tgk_copy(hipStream_t s, float *o, long ors, long ooff, tgk_opd a, long aoff
  * A [D][N], ys [T][D]; results bit-identical to the per-instruction kernels.
  * N must be one tgk_sscan_supported() accepts. */
 bool tgk_sscan_supported(int N);
+/* Neighbouring instructions folded into the scan (fuse may be NULL): with
+ * dux.p set, du_t = dt_t * dux_t (du unused); with gx.p set, the stacked
+ * output is (y_t + gx_t * gD) * silu(gz_t) (gx, gz [T][D] per row, gD one
+ * value per channel) instead of y_t. */
+typedef struct {
+	tgk_opd dux, gx, gz;
+	const float *gD;
+} tgk_sscan_fuse;
 void tgk_sscan(hipStream_t s, float *h, long hrs, tgk_opd dt, tgk_opd du, tgk_opd Bq, tgk_opd Cq, tgk_opd A, float *ys, long yrs, int D,
-	       int N, int T, int reverse, int rows);
+	       int N, int T, int reverse, int rows, const tgk_sscan_fuse *fuse);
 
 /* ---- quantized GEMM on int8 MFMA (kern_qgemm.hip) ----
  * Y = X Wq^T with X [M][K] f32 (row m at x + (m / ni) * xr + (m % ni) * xj,

@@ -22,6 +22,7 @@ class Stats(ctypes.Structure):
         ("qgemm_calls", ctypes.c_long), ("digits_ms", ctypes.c_double), ("other_ms", ctypes.c_double),
         ("weight_bytes", ctypes.c_double), ("macs", ctypes.c_double), ("arena_bytes", ctypes.c_long),
         ("rowprog_jit", ctypes.c_int), ("rowprog_hoisted", ctypes.c_long), ("epilogue_ins", ctypes.c_int),
+        ("scan_folded_ins", ctypes.c_int),
     ]
 
 

@@ -158,3 +158,34 @@ def test_chain_that_saves_nothing_is_not_taken():
     body = ("    (%%0 (f32 %d) (matmul W x))\n    (%%1 (f32 %d) (add %%0 b))\n    (%%2 (f32 %d) (tanh %%1))\n"
             "    (%%3 (f32 %d) (mul %%2 s))\n    (%%4 (f32 %d) (sub %%3 b))\n    (%%5 (f32 %d) (relu %%4))\n" % ((C,) * 6))
     _case(params, [("x", str(K))], body, "%5", str(C), _rows(73, rows, K), 0)
+
+
+def test_scan_neighbours_folded():
+    """A selective scan's du product (mul dt x) and Mamba's gate after it
+    ((y + x * D) * silu(z)) run inside the fused scan's kernel: 5
+    instructions per block of the config 5 model. The same model with one
+    more reader of each scan's du and stacked output (which keeps the builder
+    from folding anything) gives the same bits, on 40 sequences of 32 steps
+    (1280 rows, every block's scan)."""
+    import re
+    from technograd_amd import hip
+    print("case scan neighbours folded", flush=True)
+    T, seqs = 32, 40
+    text = synth.ssm_tgir("ssm", T=T)
+    x = synth.config5_rows(seqs, T)
+    prog = hip.Program(text, max_rows=seqs)
+    got, _ = prog.batch(x)
+    folded = prog.stats().scan_folded_ins
+    emits = re.findall(r"\(emit (%\d+) \((f32 [\d ]+)\)", text)
+    dus = re.findall(r"\(carry [^\n]*\n\s+\(in %\d+ \(f32 \d+\) (%\d+)\)\n\s+\(in %\d+ \(f32 \d+\) (%\d+)\)", text)
+    assert len(emits) == 4 and len(dus) == 4 and folded == 5 * len(emits), (folded, len(emits), len(dus))
+    extra, nid = "", 90000
+    for (ys, shape), (_, du) in zip(emits, dus):
+        for v in (ys, du):
+            extra += "    (%%%d (%s) (mul %s %s))\n" % (nid, shape, v, v)
+            nid += 1
+    cut = text.rindex("  )\n  (output")
+    prog2 = hip.Program(text[:cut] + extra + text[cut:], max_rows=seqs)
+    want, _ = prog2.batch(x)
+    assert prog2.stats().scan_folded_ins == 0
+    _same(got, want)
