@@ -555,10 +555,11 @@ __device__ inline void ref_line(const tgk_qgemm_args &a, const tgk_qweight &w, i
 }
 
 // output (m, c) from tot = sum_k t[c][k] q[m][k], given row m's exponent, special flag and sum of q
-// ACT: TGM_TANH when a tanh that only reads the product is applied here (the
-// chain [tanh] of the large-batch kernel, inline), else 0
+// ACT: TGM_TANH or TGM_SILU when that activation, read only by the product,
+// is applied here (the chain [tanh] or [silu] of the large-batch kernel,
+// inline), else 0
 template <int ACT = 0>
-__device__ inline float act_out(float v) { return ACT == TGM_TANH ? tg_uop(TGM_TANH, v) : v; }
+__device__ inline float act_out(float v) { return ACT ? tg_uop(ACT, v) : v; }
 
 // A split row's outlier terms for channel c (m < M, c < C): sum over its
 // outliers, in increasing input order, of code[c][k] x_k in f64 (each
@@ -937,8 +938,8 @@ __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 //
 // EPI 1: the epilogue applies the chain (a.epi), and the row op when `row`
 // (the tile holds whole lines: one channel tile, channel stride 1), through
-// LDS (staged_epilogue). EPI 2: the chain is a lone tanh, applied as each
-// output is stored (the stores' code then stays as small as without it).
+// LDS (staged_epilogue). EPI 2 / 3: the chain is a lone tanh / silu, applied
+// as each output is stored (the stores' code then stays as small as without it).
 
 template <int BITS, int EPI = 0>
 __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, Scratch s, int gx, int gy, int row)
@@ -1076,7 +1077,7 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 		staged_epilogue<BITS == 4>(a, w, s, m0, c0, wm, g, lane, wave, tid, row != 0, (float *)lds, totd);
 		return;
 	}
-	store_tile<4, false, EPI == 2 ? TGM_TANH : 0, BITS == 4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane,
+	store_tile<4, false, EPI == 2 ? TGM_TANH : EPI == 3 ? TGM_SILU : 0, BITS == 4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane,
 								 tile_rows<4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane), tot, totd);
 }
 
@@ -1782,8 +1783,10 @@ int launch_gemm(hipStream_t st, const tgk_qgemm_args *a, Scratch s, int Mp)
 	const int gx = w->Cp / BN, gy = Mp / BM;
 	const long rt = round_up(a->M, 32) / 32, cb = w->Cp / 32;
 	if ((long)gx * gy >= 128 && rt > 2) { // enough 128 x 256 tiles for the LDS kernel
-		if (a->nepi == 1 && a->epi[0].kind == TGK_EW_UN && a->epi[0].op == TGM_TANH && !a->rowop && a->nseg <= 1) {
-			qgemm_k<BITS, 2><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy, 0); // a lone tanh: inline in the stores
+		if (a->nepi == 1 && a->epi[0].kind == TGK_EW_UN && (a->epi[0].op == TGM_TANH || a->epi[0].op == TGM_SILU) && !a->rowop &&
+		    a->nseg <= 1) { // a lone tanh or silu: inline in the stores
+			if (a->epi[0].op == TGM_TANH) qgemm_k<BITS, 2><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy, 0);
+			else qgemm_k<BITS, 3><<<gx * gy, 512, 0, st>>>(*a, *w, s, gx, gy, 0);
 			return TGK_DID_CHAIN;
 		}
 		const int row = a->rowop && gx == 1 && a->oc == 1;

@@ -367,6 +367,7 @@ struct LB {
 		int gx = -1, gD = -1, gz = -1, out = -1; // out = (ys + gx * gD) * silu(gz): the kernel writes it
 	};
 	std::map<const tgm_ins *, SscanPlan> sscan;
+	std::map<int, int> lone; // top-block quantized product -> the lone activation its stores apply (plan_lone_acts)
 };
 
 void count_uses(const tgm_block *b, std::vector<int> &u);
@@ -1231,12 +1232,68 @@ int epi_chain(LB &L, const tgm_block *b, int i, Step &st)
 	return j - 1;
 }
 
+// A quantized product of the top block over many rows (16384 or more per
+// pass) whose only reader is a lone tanh or silu takes that activation into
+// its stores (qgemm_k's inline activation), where the chain rule would not
+// give it one: the activation is not the next instruction, or the product
+// shares its activations with another product and would merge with it
+// (merge_qgemms; Mamba's in-projections x and z, whose x feeds a silu). Over
+// that many rows the pass over the product it saves is worth more than the
+// launch a merge saves. The activation is skipped by layer_block; its values
+// are the elementwise kernel's (tg_ewop.h).
+void plan_lone_acts(LB &L)
+{
+	const tgm_module *m = L.m;
+	const tgm_block &b = m->top;
+	if (L.p->flags & TG_HIP_EXACT) return;
+	std::vector<int> uses((size_t)m->nval, 0), reader((size_t)m->nval, -1);
+	count_uses(&b, uses);
+	uses[(size_t)m->output]++;
+	for (int i = 0; i < b.len; i++) {
+		const tgm_ins &in = b.v[i];
+		for (int j = 0; j < in.na; j++) reader[(size_t)in.a[j]] = i;
+		if (in.op == TGM_SCAN) {
+			for (int k = 0; k < in.nx; k++) reader[(size_t)in.x[k]] = i;
+			for (int k = 0; k < in.nc; k++) reader[(size_t)in.cinit[k]] = i;
+		}
+	}
+	auto act_of = [&](const tgm_ins &in) { return matmul_quant(m, in) == 1 ? in.a[1] : in.a[0]; };
+	for (int i = 0; i < b.len; i++) {
+		const tgm_ins &in = b.v[i];
+		if (in.op != TGM_MATMUL || !matmul_quant(m, in) || L.skip[(size_t)i]) continue;
+		const int v = in.out, k = reader[(size_t)v];
+		if (uses[(size_t)v] != 1 || k <= i || L.loopw[(size_t)v] || L.skip[(size_t)k]) continue;
+		const tgm_ins &nx = b.v[k];
+		if ((nx.op != TGM_TANH && nx.op != TGM_SILU) || nx.na != 1 || nx.a[0] != v) continue;
+		bool shared = false;
+		for (int q = 0; q < b.len; q++)
+			if (q != i && b.v[q].op == TGM_MATMUL && matmul_quant(m, b.v[q]) && act_of(b.v[q]) == act_of(in)) shared = true;
+		if (!shared && k == i + 1) continue; // epi_chain takes it
+		const tgm_value &w = m->val[matmul_quant(m, in) == 1 ? in.a[0] : in.a[1]];
+		const long K = w.sh.rank == 2 ? w.sh.dim[1 - w.qaxis] : 0;
+		if (K <= 0 || (long)L.p->max_rows * (numel(m->val[act_of(in)].sh) / K) < 16384) continue;
+		L.lone[i] = k;
+		L.skip[(size_t)k] = 1;
+	}
+}
+
 bool layer_block(LB &L, const tgm_block *b)
 {
 	const bool top = b == &L.m->top;
 	for (int i = 0; i < b->len; i++) {
 		const tgm_ins &in = b->v[i];
-		if (top && L.skip[(size_t)i]) continue; // folded into a fused scan (plan_sscan)
+		if (top && L.skip[(size_t)i]) continue; // folded into a fused scan (plan_sscan) or a product's stores (plan_lone_acts)
+		if (top && L.lone.count(i)) { // the product applies its lone activation as it stores
+			const tgm_ins &act = b->v[L.lone[i]];
+			tgm_ins fused = in;
+			fused.out = act.out;
+			if (!layer_ins(L, fused)) return false;
+			Step &st = L.p->steps.back();
+			st.nepi = 1;
+			st.epi[0] = Step::Epi{ TGK_EW_UN, act.op, 0, Opnd{} };
+			L.p->stats.epilogue_ins += 1;
+			continue;
+		}
 		if (in.op == TGM_MATMUL && top && !(L.p->flags & TG_HIP_EXACT) && matmul_quant(L.m, in)) {
 			Step chain;
 			int last = epi_chain(L, b, i, chain);
@@ -2045,6 +2102,7 @@ bool build_layer(tg_hip_prog *p)
 	mark_loop_values(&p->m->top, L.loopw);
 	mark_transpose_views(L);
 	plan_sscan(L);
+	plan_lone_acts(L);
 	if (p->m->val[p->m->output].kind == TGM_TMP) { /* written straight into the caller's output rows */
 		L.where[p->m->output].space = SP_OUT;
 		L.where[p->m->output].off = 0;

@@ -163,29 +163,37 @@ def test_chain_that_saves_nothing_is_not_taken():
 def test_scan_neighbours_folded():
     """A selective scan's du product (mul dt x) and Mamba's gate after it
     ((y + x * D) * silu(z)) run inside the fused scan's kernel: 5
-    instructions per block of the config 5 model. The same model with one
-    more reader of each scan's du and stacked output (which keeps the builder
-    from folding anything) gives the same bits, on 40 sequences of 32 steps
-    (1280 rows, every block's scan)."""
+    instructions per block of the config 5 model; and over 16384 rows or
+    more the in-projection's silu, its only reader but not the next
+    instruction, runs in that projection's stores (it then does not merge
+    with the z projection). The same model with one more reader of each
+    scan's du and stacked output and of each silu's input (which keeps the
+    builder from folding anything) gives the same bits, on 520 sequences of
+    32 steps (16,640 rows, every block)."""
     import re
     from technograd_amd import hip
     print("case scan neighbours folded", flush=True)
-    T, seqs = 32, 40
+    T, seqs = 32, 520
     text = synth.ssm_tgir("ssm", T=T)
     x = synth.config5_rows(seqs, T)
     prog = hip.Program(text, max_rows=seqs)
     got, _ = prog.batch(x)
-    folded = prog.stats().scan_folded_ins
+    st = prog.stats()
     emits = re.findall(r"\(emit (%\d+) \((f32 [\d ]+)\)", text)
     dus = re.findall(r"\(carry [^\n]*\n\s+\(in %\d+ \(f32 \d+\) (%\d+)\)\n\s+\(in %\d+ \(f32 \d+\) (%\d+)\)", text)
-    assert len(emits) == 4 and len(dus) == 4 and folded == 5 * len(emits), (folded, len(emits), len(dus))
+    silus = re.findall(r"\(%\d+ \((f32 [\d ]+)\) \(silu (%\d+)\)\)", text)
+    assert len(emits) == 4 and len(dus) == 4 and st.scan_folded_ins == 5 * len(emits), (st.scan_folded_ins, len(emits), len(dus))
     extra, nid = "", 90000
     for (ys, shape), (_, du) in zip(emits, dus):
         for v in (ys, du):
             extra += "    (%%%d (%s) (mul %s %s))\n" % (nid, shape, v, v)
             nid += 1
+    for shape, v in silus:
+        extra += "    (%%%d (%s) (mul %s %s))\n" % (nid, shape, v, v)
+        nid += 1
     cut = text.rindex("  )\n  (output")
     prog2 = hip.Program(text[:cut] + extra + text[cut:], max_rows=seqs)
     want, _ = prog2.batch(x)
-    assert prog2.stats().scan_folded_ins == 0
+    st2 = prog2.stats()
+    assert st2.scan_folded_ins == 0 and st.epilogue_ins - st2.epilogue_ins == len(emits), (st.epilogue_ins, st2.epilogue_ins)
     _same(got, want)
