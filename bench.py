@@ -745,6 +745,9 @@ def config3_leg(args):
 
 
 C5_PROFILE_SEQS = 256  # sequences of the profiled config 5 pass
+# the dispatches that make config 5's projections: digit kernels, quantized GEMMs and matvecs, and the short
+# products (16 inputs: the dt projection) on the reference's loop; the timers count all of them as projections
+C5_PROJ_KERNELS = ("qgemm_k", "qgemv_k", "qtiny_k", "digits_")
 
 
 def c5_alg_bytes(seqs, T=512, dm=256, di=512, ns=16, dtr=16, blocks=4):
@@ -811,7 +814,7 @@ def config5_leg(args):
     alg_bytes = c5_alg_bytes(rows, T)
     proj_us = mfma_us + dig_us
     per = None if args.no_traffic else profile_pass("c5")
-    traffic = None if per is None else sum(v for k, v in per.items() if k.startswith(("qgemm_k", "digits_"))) * rows / C5_PROFILE_SEQS
+    traffic = None if per is None else sum(v for k, v in per.items() if k.startswith(C5_PROJ_KERNELS)) * rows / C5_PROFILE_SEQS
     log("config 5: %.1f ms per 4096 sequences: projections %.0f us, digits %.0f us, other (scan, elementwise) %.0f us"
         % (t * 1e3, mfma_us, dig_us, oth_us))
     cpu = None if args.no_cpu else ref_cpu(text, X[:32], per, 8, 0, auto_threads(), False,
@@ -832,13 +835,15 @@ def config5_leg(args):
                                        "the dt-rank vector 64 B, the gated SSM output 2 KiB) and their outputs written "
                                        "once (xi, z, dt 2 KiB each, the dt-rank vector, B and C 64 B each, the block's "
                                        "output 1 KiB): 12,544 B; the int8 weights and scales once",
-                     "traffic_note": ("calibrated FETCH_SIZE + WRITE_SIZE of the digit and GEMM dispatches of a pass of "
-                                      "%d sequences (rocprofv3), scaled to %d" % (C5_PROFILE_SEQS, rows))
+                     "traffic_note": ("calibrated FETCH_SIZE + WRITE_SIZE of the projections' dispatches (%s) of a pass "
+                                      "of %d sequences (rocprofv3), scaled to %d"
+                                      % (", ".join(C5_PROJ_KERNELS), C5_PROFILE_SEQS, rows))
                                      if traffic is not None else "not profiled",
                      "traffic_kernels": None if per is None else {k: round(v * rows / C5_PROFILE_SEQS)
                                                                   for k, v in sorted(per.items())},
-                     "kernel": "the projections of a pass: digit kernels and quantized GEMMs (their epilogues "
-                               "included), summed; output-bound GEMMs (the f32 scan is VALU work)",
+                     "kernel": "the projections of a pass: digit kernels, quantized GEMMs and the short products on "
+                               "the reference's loop (qtiny_k, the dt projection), their epilogues included, summed; "
+                               "output-bound (the f32 scan is VALU work)",
                      "avg_kernel_us": round(proj_us, 1),
                      "mfma_view": {"achieved": round(ops / mfma_us / 1e6, 2), "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
                                    "frac": round(ops / mfma_us / 1e6 / MFMA_I8_PEAK_TOPS, 4)}},
