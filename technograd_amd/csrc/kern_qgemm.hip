@@ -440,10 +440,12 @@ __device__ inline long long combine(int acc0, int acc1, int acc2)
 }
 
 // the same sum in f64, also exact: every term and partial sum is an integer
-// below 2^48 in magnitude (int32 digit sums times at most 2^16)
+// below 2^48 in magnitude (int32 digit sums times at most 2^16), so each fused
+// multiply-add gives the same value as a multiply then an add, in one
+// instruction
 __device__ inline double combine_d(int acc0, int acc1, int acc2)
 {
-	return (double)acc0 + (double)acc1 * 256.0 + (double)acc2 * 65536.0;
+	return __builtin_fma((double)acc2, 65536.0, __builtin_fma((double)acc1, 256.0, (double)acc0));
 }
 
 // output (m, c) from tot = sum_k t[c][k] q[m][k]
@@ -645,7 +647,9 @@ __device__ inline TileRows<NB> tile_rows(const tgk_qgemm_args &a, const tgk_qwei
 // HOIST: take all 16 rows' exponents and sums of q from their lanes before the
 // first store (the shuffles then wait once, not once per row; 48 more live
 // registers, for kernels that have them free at the epilogue).
-template <int NB, bool HOIST, int ACT = 0, bool PAIRS = false, class Tot, class TotD>
+// W8: the weights are int8 (no +8 bias to take out, the sums of q unused),
+// known when the kernel is compiled.
+template <int NB, bool HOIST, int ACT = 0, bool PAIRS = false, bool W8 = false, class Tot, class TotD>
 __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int mbase, int cbase, int lane,
 				  const TileRows<NB> &t, Tot tot, TotD totd)
 {
@@ -706,6 +710,33 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 				if (cbase + j * 32 + r32 >= w.C) continue;
 				oc[j].p[(long)r * oc[j].orr + (long)jj * oc[j].oj] =
 					sc[j] * (float)ldexp(totd(j, v) - (PAIRS && (j & 1) ? 0.0 : q8), E - 23); // no chain
+			}
+		}
+		return;
+	}
+	bool inc[NB]; // the lane's columns that exist
+	for (int j = 0; j < NB; j++) inc[j] = cbase + j * 32 + r32 < w.C;
+	if (a.oc == 1 && a.ni == 1) {
+		// lines one output row each, channels at stride 1: a lane's rows at
+		// its base plus a wave-uniform offset, its columns at fixed offsets
+		// from the row; the loop unrolled, so every sum is read from its own
+		// register
+		float *ob = a.o + (long)(mbase + 4 * h) * a.orr + cbase + r32;
+		// the row data and scales have landed: one wait here, not one in
+		// front of a store after each branch that skips a store
+		__builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
+#pragma unroll
+		for (int v = 0; v < 16; v++) {
+			const int dv = 8 * (v >> 2) + (v & 3), rv = dv + 4 * h;
+			const int E = row_e(v, rv);
+			const double q8 = W8 ? 0.0 : 8.0 * (double)row_q(v, rv);
+			if (mbase + rv >= a.M) continue;
+			float *orow = ob + (long)dv * a.orr;
+#pragma unroll
+			for (int j = 0; j < NB; j++) {
+				if (!inc[j]) continue;
+				const double tj = W8 || (PAIRS && (j & 1)) ? totd(j, v) : totd(j, v) - q8;
+				orow[32 * j] = act_out<ACT>(sc[j] * (float)ldexp(tj, E - 23));
 			}
 		}
 		return;
@@ -1077,7 +1108,7 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 		staged_epilogue<BITS == 4>(a, w, s, m0, c0, wm, g, lane, wave, tid, row != 0, (float *)lds, totd);
 		return;
 	}
-	store_tile<4, false, EPI == 2 ? TGM_TANH : EPI == 3 ? TGM_SILU : 0, BITS == 4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane,
+	store_tile<4, false, EPI == 2 ? TGM_TANH : EPI == 3 ? TGM_SILU : 0, BITS == 4, BITS == 8>(a, w, s, m0 + wm * 32, c0 + g * 128, lane,
 								 tile_rows<4>(a, w, s, m0 + wm * 32, c0 + g * 128, lane), tot, totd);
 }
 
