@@ -714,14 +714,16 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 		}
 		return;
 	}
-	bool inc[NB]; // the lane's columns that exist
-	for (int j = 0; j < NB; j++) inc[j] = cbase + j * 32 + r32 < w.C;
-	if (a.oc == 1 && a.ni == 1) {
-		// lines one output row each, channels at stride 1: a lane's rows at
-		// its base plus a wave-uniform offset, its columns at fixed offsets
-		// from the row; the loop unrolled, so every sum is read from its own
-		// register
-		float *ob = a.o + (long)(mbase + 4 * h) * a.orr + cbase + r32;
+	// line m's output row at a.o + m ls (lines evenly spaced: one per batch
+	// row, or inner rows packed ni to a batch row)
+	const long ls = a.ni == 1 ? a.orr : a.oj;
+	if (a.oc == 1 && (a.ni == 1 || a.orr == (long)a.ni * a.oj) && mbase + 32 <= a.M && cbase + NB * 32 <= w.C) {
+		// a whole block (its 32 rows and NB x 32 columns exist) of evenly
+		// spaced lines, channels at stride 1: a lane's rows at its base plus a
+		// wave-uniform offset, its columns at fixed offsets from the row; the
+		// loop unrolled, so every sum is read from its own register, and no
+		// bounds to test
+		float *ob = a.o + (long)(mbase + 4 * h) * ls + cbase + r32;
 		// the row data and scales have landed: one wait here, not one in
 		// front of a store after each branch that skips a store
 		__builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
@@ -730,11 +732,9 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 			const int dv = 8 * (v >> 2) + (v & 3), rv = dv + 4 * h;
 			const int E = row_e(v, rv);
 			const double q8 = W8 ? 0.0 : 8.0 * (double)row_q(v, rv);
-			if (mbase + rv >= a.M) continue;
-			float *orow = ob + (long)dv * a.orr;
+			float *orow = ob + (long)dv * ls;
 #pragma unroll
 			for (int j = 0; j < NB; j++) {
-				if (!inc[j]) continue;
 				const double tj = W8 || (PAIRS && (j & 1)) ? totd(j, v) : totd(j, v) - q8;
 				orow[32 * j] = act_out<ACT>(sc[j] * (float)ldexp(tj, E - 23));
 			}
@@ -793,7 +793,7 @@ __device__ inline void copy_to_lds(const uint8_t *sbase, unsigned voff, unsigned
 constexpr int rowstr(int C) { return C | 1; }
 constexpr int EPI_LDS = BM * rowstr(BN) * 4 + BM * 4; // line values and one scalar per line
 
-template <bool PAIRS, class TotD>
+template <bool PAIRS, bool W8, class TotD>
 __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, const Scratch &s, int m0, int c0, int wm, int g, int lane,
 				int wave, int tid, bool row, float *L, TotD totd)
 {
@@ -805,6 +805,20 @@ __device__ void staged_epilogue(const tgk_qgemm_args &a, const tgk_qweight &w, c
 	{
 		const int mbase = m0 + wm * 32, r32 = lane & 31, h = lane >> 5;
 		const TileRows<4> t = tile_rows<4>(a, w, s, mbase, c0 + g * 128, lane);
+		if (!__any(t.spr == 2)) { // no split row in the block (the common case): unrolled, each sum from its own register
+			__builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0): the row data and scales, once
+#pragma unroll
+			for (int v = 0; v < 16; v++) {
+				const int rv = 8 * (v >> 2) + 4 * h + (v & 3);
+				const int E = __shfl(t.Er, rv);
+				const double q8 = W8 ? 0.0 : 8.0 * (double)__shfl(t.Qr, rv);
+#pragma unroll
+				for (int j = 0; j < 4; j++) {
+					const double tj = W8 || (PAIRS && (j & 1)) ? totd(j, v) : totd(j, v) - q8;
+					L[(wm * 32 + rv) * STR + g * 128 + j * 32 + r32] = t.sc[j] * (float)ldexp(tj, E - 23);
+				}
+			}
+		} else
 		for (int v = 0; v < 16; v++) {
 			const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
 			const int E = __shfl(t.Er, rv), sp = __shfl(t.spr, rv);
@@ -1105,7 +1119,7 @@ __global__ __launch_bounds__(512) void qgemm_k(tgk_qgemm_args a, tgk_qweight w, 
 		return t;
 	};
 	if constexpr (EPI == 1) {
-		staged_epilogue<BITS == 4>(a, w, s, m0, c0, wm, g, lane, wave, tid, row != 0, (float *)lds, totd);
+		staged_epilogue<BITS == 4, BITS == 8>(a, w, s, m0, c0, wm, g, lane, wave, tid, row != 0, (float *)lds, totd);
 		return;
 	}
 	store_tile<4, false, EPI == 2 ? TGM_TANH : EPI == 3 ? TGM_SILU : 0, BITS == 4, BITS == 8>(a, w, s, m0 + wm * 32, c0 + g * 128, lane,
