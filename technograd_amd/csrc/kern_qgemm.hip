@@ -699,6 +699,32 @@ __device__ inline void store_tile(const tgk_qgemm_args &a, const tgk_qweight &w,
 			const int c = cbase + j * 32 + r32;
 			oc[j] = out_col(a, c < w.C ? c : 0);
 		}
+		// a whole block whose lines are evenly spaced in every column's
+		// output: each column's row at its own base plus the row offset times
+		// its own line stride, the loop unrolled, no bounds to test
+		bool even = a.oc == 1 && mbase + 32 <= a.M && cbase + NB * 32 <= w.C;
+		for (int j = 0; j < NB; j++) even = even && (a.ni == 1 || oc[j].orr == (long)a.ni * oc[j].oj);
+		if (__all(even)) {
+			float *pb[NB];
+			long lsj[NB];
+			for (int j = 0; j < NB; j++) {
+				lsj[j] = a.ni == 1 ? oc[j].orr : oc[j].oj;
+				pb[j] = oc[j].p + (long)(mbase + 4 * h) * lsj[j];
+			}
+			__builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0): the row data and scales, once
+#pragma unroll
+			for (int v = 0; v < 16; v++) {
+				const int dv = 8 * (v >> 2) + (v & 3), rv = dv + 4 * h;
+				const int E = row_e(v, rv);
+				const double q8 = W8 ? 0.0 : 8.0 * (double)row_q(v, rv);
+#pragma unroll
+				for (int j = 0; j < NB; j++) {
+					const double tj = W8 || (PAIRS && (j & 1)) ? totd(j, v) : totd(j, v) - q8;
+					pb[j][(long)dv * lsj[j]] = sc[j] * (float)ldexp(tj, E - 23); // no chain
+				}
+			}
+			return;
+		}
 		for (int v = 0; v < 16; v++) {
 			const int rv = 8 * (v >> 2) + 4 * h + (v & 3), m = mbase + rv;
 			const int E = row_e(v, rv);
@@ -1726,7 +1752,7 @@ void launch_gemv(hipStream_t st, const tgk_qgemm_args *a, Scratch s)
 // then the scale and, when `chain`, the chain, each instruction applied to the
 // U NC values at once as staged_epilogue applies it.
 template <int KM, int NC, int U, bool VEC>
-__global__ __launch_bounds__(256) void qtiny_k(tgk_qgemm_args a, tgk_qweight w, int rows_per_block, int chain)
+__global__ __launch_bounds__(256, KM <= 16 ? 4 : 1) void qtiny_k(tgk_qgemm_args a, tgk_qweight w, int rows_per_block, int chain)
 {
 	constexpr int NV = U * NC;
 	int c[NC], cc[NC];
