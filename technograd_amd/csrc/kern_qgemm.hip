@@ -1763,16 +1763,21 @@ __global__ __launch_bounds__(256, KM <= 16 ? 4 : 1) void qtiny_k(tgk_qgemm_args 
 		for (int k = 0; k < KM; k++) cf[q][k] = k < w.K ? (float)code_orig(w, cc[q], k) : 0.0f;
 		sc[q] = w.scale[cc[q]];
 	}
-	const bool flat = a.ni == 1; // (uniform) row m is batch row m: no division
 	const int m0 = blockIdx.y * rows_per_block, m1 = a.M - m0 < rows_per_block ? a.M : m0 + rows_per_block;
+	// row m is batch row r, inner row j (m = r ni + j): the block's first row
+	// divided once, then stepped (uniform, no division per row)
+	const int r0 = a.ni == 1 ? m0 : m0 / a.ni, j0 = m0 - r0 * a.ni;
+	int rb = r0, jb = j0; // row mb's
 	for (int mb = m0; mb < m1; mb += U) {
 		int rr[U], jr[U];
 		float xv[U][KM];
 		for (int u = 0; u < U; u++) {
-			const int m = mb + u < m1 ? mb + u : m0; // past the block's rows: a row of it, not stored
-			rr[u] = flat ? m : m / a.ni;
-			jr[u] = m - rr[u] * a.ni;
-			const float *x = xrow(a, m);
+			int r = rb, j = jb + u;
+			while (j >= a.ni) j -= a.ni, r++;
+			if (mb + u >= m1) r = r0, j = j0; // past the block's rows: a row of it, not stored
+			rr[u] = r;
+			jr[u] = j;
+			const float *x = a.x + (long)r * a.xr + (long)j * a.xj;
 			if constexpr (VEC) { // unit stride, 16-byte aligned, K a multiple of 4
 				for (int k = 0; k < KM; k += 4) {
 					const float4 f = k < w.K ? *(const float4 *)(x + k) : float4{ 0.0f, 0.0f, 0.0f, 0.0f };
@@ -1782,12 +1787,14 @@ __global__ __launch_bounds__(256, KM <= 16 ? 4 : 1) void qtiny_k(tgk_qgemm_args 
 				for (int k = 0; k < KM; k++) xv[u][k] = k < w.K ? x[(long)k * a.xk] : 0.0f;
 			}
 		}
+		// the reference's loop over the K inputs; the padding past K adds
+		// 0 x 0 = +0, which leaves every sum as it is (a sum that starts at +0
+		// is never -0), so it needs no test
 		float v[NV]; // value (u, q) at u NC + q
 		for (int u = 0; u < U; u++)
 			for (int q = 0; q < NC; q++) {
 				float t = 0.0f;
-				for (int k = 0; k < KM; k++)
-					if (k < w.K) t += cf[q][k] * xv[u][k];
+				for (int k = 0; k < KM; k++) t += cf[q][k] * xv[u][k];
 				v[u * NC + q] = sc[q] * t;
 			}
 		for (int e = 0; chain && e < a.nepi; e++) {
@@ -1827,6 +1834,8 @@ __global__ __launch_bounds__(256, KM <= 16 ? 4 : 1) void qtiny_k(tgk_qgemm_args 
 			if (mb + u < m1)
 				for (int q = 0; q < NC; q++)
 					if (c[q] < w.C) *out_at(a, rr[u], jr[u], c[q]) = v[u * NC + q];
+		jb += U;
+		while (jb >= a.ni) jb -= a.ni, rb++;
 	}
 }
 
