@@ -312,6 +312,42 @@ def test_outlier_rows_at_every_batch_size(bits_, axis):
         assert _same(got[sub[:2]], r2)
 
 
+@pytest.mark.parametrize("bits_", [8, 4])
+def test_sequence_products_whole_and_edge_blocks(bits_):
+    """Two products of one input over sequences (160 rows of T = 37 steps,
+    K = 200, C = 300 each: 5920 lines, the lines of a row packed as inner
+    rows), each read twice after it, so neither takes an epilogue chain and
+    the two merge into one GEMM of 600 channels (one launch): its 128 x 256
+    tiles hold whole 32-line blocks and edge blocks past the last line and
+    past the last channel, and lines with outliers and a NaN line take the
+    special-row path. The program's output (A - B) + A * B equals the host
+    restatement of the device path (parity.device_path_matmul for A and B,
+    then the same f32 operations) bit for bit."""
+    from technograd_amd import hip
+    print("case sequence products", bits_, flush=True)
+    T, K, C, seqs = 37, 200, 300, 160
+    lim = 7 if bits_ == 4 else 127
+    rng = np.random.default_rng(60 + bits_)
+    c1, c2 = (rng.integers(-lim, lim + 1, size=(K, C)).astype(np.int8) for _ in range(2))
+    s1, s2 = (rng.uniform(0.001, 0.1, size=C).astype(np.float32) for _ in range(2))
+    text = ("(tgir 1\n  (model seqp)\n" + synth.param_quant("W1", c1, s1, bits_, 1) + synth.param_quant("W2", c2, s2, bits_, 1)
+            + "  (input x (f32 %d %d))\n  (block\n" % (T, K)
+            + "    (%%0 (f32 %d %d) (matmul x W1))\n    (%%1 (f32 %d %d) (matmul x W2))\n" % (T, C, T, C)
+            + "    (%%2 (f32 %d %d) (sub %%0 %%1))\n    (%%3 (f32 %d %d) (mul %%0 %%1))\n" % (T, C, T, C)
+            + "    (%%4 (f32 %d %d) (add %%2 %%3))\n  )\n  (output %%4))\n" % (T, C))
+    x = rng.normal(size=(seqs * T, K)).astype(np.float32)
+    for i, at in enumerate(rng.choice(seqs * T, 12, replace=False)):
+        x[at, rng.choice(K, 1 + i, replace=False)] = 1e3 * (i + 1)  # peaked lines
+    x[41, 7] = np.nan
+    prog = hip.Program(text, flags=hip.TIMING, max_rows=seqs)
+    got, _ = prog.batch(x.reshape(seqs, T * K))
+    assert prog.stats().qgemm_calls == 1  # the two products as one GEMM
+    A, _ = parity.device_path_matmul(x, c1, s1)
+    B, _ = parity.device_path_matmul(x, c2, s2)
+    want = ((A - B) + (A * B)).reshape(seqs, T * C)
+    assert _same(got, want)
+
+
 @pytest.mark.parametrize("bits_,axis,K", [(8, 1, 16), (4, 1, 30), (8, 0, 16), (4, 0, 1)])
 def test_short_products_are_the_reference(bits_, axis, K):
     """Products over at most 32 inputs take the reference's loop for every
