@@ -739,6 +739,26 @@ __global__ __launch_bounds__(1024) void dec_silu_k(tgk_dec_silu_args a)
 	blk_digits(zs, FF, a.Kp, mx, bad, a.q, t, redf, redl);
 }
 
+// out = silu(g) * u for a prompt's many rows [g (FF) | u (FF)] (gus apart),
+// the operations dec_silu_k applies, streamed four values a thread (when FF,
+// gus and the pointers allow 16-byte accesses); the GEMM's own digit kernel
+// makes the digits after it. Block y takes rows y, y + gridDim.y, ...
+__global__ __launch_bounds__(256) void silu_mul_k(const float *gu, long gus, float *out, int FF, int rows, int vec)
+{
+	const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
+	if (i >= FF) return;
+	auto one = [](float x, float u) { return x / (1.0f + expf(-x)) * u; };
+	for (int t = blockIdx.y; t < rows; t += gridDim.y) {
+		const float *g = gu + (long)t * gus, *u = g + FF;
+		float *o = out + (long)t * FF;
+		if (vec) {
+			const float4 gv = *(const float4 *)(g + i), uv = *(const float4 *)(u + i);
+			*(float4 *)(o + i) = make_float4(one(gv.x, uv.x), one(gv.y, uv.y), one(gv.z, uv.z), one(gv.w, uv.w));
+		} else
+			for (int k = i; k < i + 4 && k < FF; k++) o[k] = one(g[k], u[k]);
+	}
+}
+
 // A prompt chunk's causal softmax of one head's scores, line (sequence, t)
 // of sc = q_t . k_u for u <= t (the products above the diagonal are not
 // computed). The graph's operations on the valid part: x_u = s_u * scale + 0
@@ -916,6 +936,14 @@ bool tgk_dec_hnorm(hipStream_t s, const tgk_dec_hnorm_args *a)
 	}
 	dec_hnorm_k<<<(unsigned)((lines + 3) / 4), TPB, (size_t)a->Kp * 8 * sizeof(float), s>>>(*a);
 	return true;
+}
+
+void tgk_dec_silu_mul(hipStream_t s, const float *gu, long gus, float *out, int FF, int rows)
+{
+	if (rows <= 0 || FF <= 0) return;
+	const int vec = FF % 4 == 0 && gus % 4 == 0 && ((size_t)gu & 15) == 0 && ((size_t)out & 15) == 0;
+	const dim3 grid((unsigned)((FF + 1023) / 1024), (unsigned)(rows < 65535 ? rows : 65535));
+	silu_mul_k<<<grid, 256, 0, s>>>(gu, gus, out, FF, rows, vec);
 }
 
 bool tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a)

@@ -264,11 +264,17 @@ bool forward(tg_hip_dec *d, int S, int T0, int p0)
 		// h + the heads' output projections (in head order), rmsnorm * ln2, gate and up projections
 		res = norm(d, 2, d->h, D, rows, nullptr, 0, d->ln2[(size_t)l], d->n, d->wgu[(size_t)l]);
 		gemm_pre(d, d->wgu[(size_t)l], d->n, D, 1, 0, rows, d->gu, 2L * d->FF, 0, res);
-		tgk_dec_silu_args sa; // act = silu(g) * u, then the down projection
-		sa.gu = d->gu, sa.gus = 2L * d->FF, sa.out = d->act, sa.FF = d->FF, sa.Kp = d->ws[(size_t)d->wd[(size_t)l]].Kp, sa.rows = rows;
-		sa.q = tgk_qgemm_digit_area(d->scratch, rows, sa.Kp);
-		res = tgk_dec_silu(st, &sa);
-		gemm_pre(d, d->wd[(size_t)l], d->act, d->FF, 1, 0, rows, d->dbuf, D, 0, res);
+		if (rows >= TGK_DEC_SILU_FUSED_MAX) { // a prompt's many rows: act = silu(g) * u streamed, the down projection's own digits
+			tgk_dec_silu_mul(st, d->gu, 2L * d->FF, d->act, d->FF, rows);
+			gemm(d, d->wd[(size_t)l], d->act, d->FF, 1, 0, rows, d->dbuf, D, 0);
+		} else {
+			tgk_dec_silu_args sa; // act = silu(g) * u and its digits, then the down projection
+			sa.gu = d->gu, sa.gus = 2L * d->FF, sa.out = d->act, sa.FF = d->FF, sa.Kp = d->ws[(size_t)d->wd[(size_t)l]].Kp;
+			sa.rows = rows;
+			sa.q = tgk_qgemm_digit_area(d->scratch, rows, sa.Kp);
+			res = tgk_dec_silu(st, &sa);
+			gemm_pre(d, d->wd[(size_t)l], d->act, d->FF, 1, 0, rows, d->dbuf, D, 0, res);
+		}
 	}
 	// the last position of each sequence: h + the last MLP output, rmsnorm * lnf, LM head
 	const bool res = norm(d, 1, d->h + (long)(T0 - 1) * D, (long)T0 * D, S, d->dbuf + (long)(T0 - 1) * D, (long)T0 * D, d->lnf, d->lastn,

@@ -210,6 +210,10 @@ typedef struct {
 	tgk_qdig q;
 } tgk_dec_silu_args;
 bool tgk_dec_silu(hipStream_t s, const tgk_dec_silu_args *a);
+/* out = silu(g) * u alone (the same values), for a prompt's many rows: the
+ * GEMM after it makes the digits with its own many-row digit kernel */
+void tgk_dec_silu_mul(hipStream_t s, const float *gu, long gus, float *out, int FF, int rows);
+#define TGK_DEC_SILU_FUSED_MAX 512 /* rows below which tgk_dec_silu's one block per row makes the digits */
 /* per-head output projections of `rows` token rows, all heads in one launch,
  * values equal to the digit + matrix-core path; codes int32 [NQ][HD/4][D],
  * 4 consecutive k's int8 codes per word */
