@@ -39,6 +39,37 @@ __global__ void rope_cache_k(tgk_dec_rope_args a, long total)
 	}
 }
 
+// The same values four at a time: block y takes token rows y, y + gridDim.y,
+// ..., a thread four consecutive d of one line (HD % 4 == 0, every operand
+// 16-byte aligned: the launcher checks), so a row's sequence and position
+// come from one 32-bit division, not two 64-bit ones per element.
+__global__ __launch_bounds__(256) void rope_cache4_k(tgk_dec_rope_args a, int rows)
+{
+	const int NL = a.NQ + 2 * a.NKV, HD4 = a.HD / 4;
+	const int e = blockIdx.x * 256 + threadIdx.x; // (line, quad) of a token row
+	if (e >= NL * HD4) return;
+	const int line = e / HD4, d = (e - line * HD4) * 4;
+	auto rot = [](float x, float c, float r, float sn) { return x * c + r * sn; };
+	for (int row = blockIdx.y; row < rows; row += gridDim.y) {
+		const int s = row / a.T0, p = a.p0 + (row - s * a.T0);
+		float *kv_s = nullptr;
+		if (line >= a.NQ) kv_s = (line < a.NQ + a.NKV ? a.K : a.V) + (long)s * a.kv_seq + a.kv_layer;
+		if (line < a.NQ + a.NKV) {
+			const long i = ((long)row * (a.NQ + a.NKV) + line) * a.HD + d;
+			const float4 x = *(const float4 *)(a.hq + i), r = *(const float4 *)(a.rt + i);
+			const float4 c = *(const float4 *)(a.cosT + (long)p * a.HD + d), sn = *(const float4 *)(a.sinT + (long)p * a.HD + d);
+			const float4 v = make_float4(rot(x.x, c.x, r.x, sn.x), rot(x.y, c.y, r.y, sn.y), rot(x.z, c.z, r.z, sn.z),
+						     rot(x.w, c.w, r.w, sn.w));
+			if (line < a.NQ) *(float4 *)(a.qr + ((long)row * a.NQ + line) * a.HD + d) = v;
+			else *(float4 *)(kv_s + ((long)(line - a.NQ) * a.P + p) * a.HD + d) = v;
+		} else {
+			const int j = line - a.NQ - a.NKV;
+			*(float4 *)(kv_s + ((long)j * a.P + p) * a.HD + d) =
+				*(const float4 *)(a.qkv + (long)row * a.ctot + (long)(a.NQ + a.NKV) * a.HD + (long)j * a.HD + d);
+		}
+	}
+}
+
 // One decode step's attention: one block per (sequence, KV head) for the GRP
 // query heads sharing it, keys at positions 0 .. p. Per query head and key:
 // score = sum_d q[d] k[d] in order from 0.0f, times the scale, plus the mask's
@@ -888,7 +919,15 @@ size_t tgk_dec_attn_lds(int GRP, int HD, int n)
 void tgk_dec_rope(hipStream_t s, const tgk_dec_rope_args *a, int rows)
 {
 	const long total = (long)rows * (a->NQ + 2 * a->NKV) * a->HD;
-	if (total > 0) rope_cache_k<<<blocks(total), TPB, 0, s>>>(*a, total);
+	if (total <= 0) return;
+	auto al = [](const void *p) { return ((size_t)p & 15) == 0; };
+	if (a->HD % 4 == 0 && a->ctot % 4 == 0 && a->kv_seq % 4 == 0 && a->kv_layer % 4 == 0 && al(a->hq) && al(a->rt) && al(a->qkv) &&
+	    al(a->cosT) && al(a->sinT) && al(a->qr) && al(a->K) && al(a->V)) {
+		const int per = (a->NQ + 2 * a->NKV) * (a->HD / 4);
+		const dim3 grid((unsigned)((per + 255) / 256), (unsigned)(rows < 65535 ? rows : 65535));
+		rope_cache4_k<<<grid, 256, 0, s>>>(*a, rows);
+	} else
+		rope_cache_k<<<blocks(total), TPB, 0, s>>>(*a, total);
 }
 
 void tgk_dec_attn(hipStream_t s, const tgk_dec_attn_args *a, int seqs)
