@@ -323,16 +323,28 @@ __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, t
 	const int bpr = nrow / lpb, r = blockIdx.x / bpr, q0 = (blockIdx.x - r * bpr) * lpb;
 	const int tot = lpb * cols;
 	const float *x = a.p + (long)r * a.rs + (long)q0 * cols;
+	// element e of the tile is line e / cols, column e % cols: a thread's
+	// elements e, e + TPB, ... are walked by adding TPB as (dl lines, dc
+	// columns), with one carry, instead of a division per element
+	const int dl = TPB / cols, dc = TPB - dl * cols, l0 = (int)threadIdx.x / cols, c0 = (int)threadIdx.x - l0 * cols;
+	auto step = [&](int &l, int &c) {
+		l += dl, c += dc;
+		if (c >= cols) c -= cols, l++;
+	};
 	constexpr int U = 8;
-	for (int e0 = 0; e0 < tot; e0 += U * TPB) {
-		float v[U];
-		for (int j = 0; j < U; j++) {
-			const int e = e0 + j * TPB + threadIdx.x;
-			v[j] = x[e < tot ? e : tot - 1];
-		}
-		for (int j = 0; j < U; j++) {
-			const int e = e0 + j * TPB + threadIdx.x;
-			if (e < tot) lds[(e / cols) * stride + e % cols] = v[j];
+	{
+		int l = l0, c = c0;
+		for (int e0 = 0; e0 < tot; e0 += U * TPB) {
+			float v[U];
+			for (int j = 0; j < U; j++) {
+				const int e = e0 + j * TPB + threadIdx.x;
+				v[j] = x[e < tot ? e : tot - 1];
+			}
+			for (int j = 0; j < U; j++) {
+				const int e = e0 + j * TPB + threadIdx.x;
+				if (e < tot) lds[l * stride + c] = v[j];
+				step(l, c);
+			}
 		}
 	}
 	__syncthreads();
@@ -345,29 +357,29 @@ __global__ __launch_bounds__(256) void rowop_lds_k(int op, float *o, long ors, t
 		for (int w = tpl / 2; w > 0; w >>= 1) m = fmaxf(m, __shfl_xor(m, w));
 		if (sub == 0) lv[l] = isnan(y[0]) ? y[0] : fmaxf(y[0], m);
 		__syncthreads();
-		for (int e = threadIdx.x; e < tot; e += TPB) {
-			float *z = lds + (e / cols) * stride + e % cols;
-			*z = expf(*z - lv[e / cols]);
+		for (int e = threadIdx.x, ll = l0, c = c0; e < tot; e += TPB, step(ll, c)) {
+			float *z = lds + ll * stride + c;
+			*z = expf(*z - lv[ll]);
 		}
 		__syncthreads();
 		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = line_sum(lds + threadIdx.x * stride, cols);
 		__syncthreads();
-		for (int e = threadIdx.x; e < tot; e += TPB) {
-			float *z = lds + (e / cols) * stride + e % cols;
-			*z = *z / lv[e / cols];
+		for (int e = threadIdx.x, ll = l0, c = c0; e < tot; e += TPB, step(ll, c)) {
+			float *z = lds + ll * stride + c;
+			*z = *z / lv[ll];
 		}
 	} else {
 		// each square is formed as its value arrives, off the ordered chain of adds
 		if ((int)threadIdx.x < lpb) lv[threadIdx.x] = 1.0f / sqrtf(line_sum<true>(lds + threadIdx.x * stride, cols) / (float)cols + 1e-6f);
 		__syncthreads();
-		for (int e = threadIdx.x; e < tot; e += TPB) {
-			float *z = lds + (e / cols) * stride + e % cols;
-			*z = *z * lv[e / cols];
+		for (int e = threadIdx.x, ll = l0, c = c0; e < tot; e += TPB, step(ll, c)) {
+			float *z = lds + ll * stride + c;
+			*z = *z * lv[ll];
 		}
 	}
 	__syncthreads();
 	float *out = o + (long)r * ors + (long)q0 * cols;
-	for (int e = threadIdx.x; e < tot; e += TPB) out[e] = lds[(e / cols) * stride + e % cols];
+	for (int e = threadIdx.x, ll = l0, c = c0; e < tot; e += TPB, step(ll, c)) out[e] = lds[ll * stride + c];
 }
 
 // sum / mean of each row, one thread per row adding in index order (the
