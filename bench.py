@@ -745,9 +745,10 @@ def config3_leg(args):
 
 
 C5_PROFILE_SEQS = 256  # sequences of the profiled config 5 pass
-# the dispatches that make config 5's projections: digit kernels, quantized GEMMs and matvecs, and the short
-# products (16 inputs: the dt projection) on the reference's loop; the timers count all of them as projections
-C5_PROJ_KERNELS = ("qgemm_k", "qgemv_k", "qtiny_k", "digits_")
+# the dispatches that make config 5's projections: digit kernels and the resolves after them, quantized GEMMs
+# and matvecs, and the short products (16 inputs: the dt projection) on the reference's loop; the timers count all
+# of them as projections or their digits
+C5_PROJ_KERNELS = ("qgemm_k", "qgemv_k", "qtiny_k", "digits_", "resolve_k")
 
 
 def c5_alg_bytes(seqs, T=512, dm=256, di=512, ns=16, dtr=16, blocks=4):

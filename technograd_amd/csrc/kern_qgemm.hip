@@ -61,6 +61,7 @@ namespace {
 
 constexpr int KB = 64;        // K padding (one K step of the LDS kernel)
 constexpr int BM = 128;       // rows per tile of the LDS kernel (activation rows are padded to it)
+constexpr int DEFER_RESOLVE_ROWS = 131072; // digit batches from which candidates are resolved by a pass of their own
 constexpr int BN = 256;       // channels per tile of the LDS kernel (weights are padded to it)
 
 inline long round_up(long x, long m) { return (x + m - 1) / m * m; }
@@ -2073,7 +2074,14 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 		// at least 4 waves (for short rows some only resolve candidates); the
 		// first min(W, 8) resolve, one histogram each
 		const int W = nkb / 2 < WM ? ((nkb + 1) / 2 < 4 ? 4 : (nkb + 1) / 2) : WM, nb = (M + 15) / 16, pairs = (nkb + 1) / 2;
-		const int RW = W < 8 ? W : 8;
+		// very large batches: the candidates the coarse test leaves are
+		// resolved after the digits by a pass of their own at full occupancy
+		// (tgk_qgemm_split), not by the first RW waves of each block while the
+		// others wait (the same decisions either way; measured on config 5's
+		// gated rows, 2 M lines of 512 inputs: 1.8 + 1.5 ms against 3.9; on
+		// 65,536 lines the extra launch cost more than it saved)
+		const bool defer = M >= DEFER_RESOLVE_ROWS;
+		const int RW = defer ? 0 : W < 8 ? W : 8;
 		const size_t lds = (size_t)RW * sizeof(TgqHist);
 		if (pairs <= W) {
 			if (vec) digits_tile16_k<1, true><<<nb, W * 64, lds, st>>>(*a, s, K, w->Kp, M, RW);
@@ -2085,6 +2093,7 @@ void tgk_qgemm_digits(hipStream_t st, const tgk_qgemm_args *a, void *scratch)
 			if (vec) digits_tile16_k<4, true><<<nb, W * 64, lds, st>>>(*a, s, K, w->Kp, M, RW);
 			else digits_tile16_k<4, false><<<nb, W * 64, lds, st>>>(*a, s, K, w->Kp, M, RW);
 		}
+		if (defer) tgk_qgemm_split(st, a, scratch);
 	} else if (M < 512 && w->Kp >= 2048 && w->Kp <= 16384) { // few long rows: a block per row
 		const bool vec = a->xk == 1 && ((size_t)a->x & 15) == 0 && (a->xr & 3) == 0 && (a->ni == 1 || (a->xj & 3) == 0) &&
 				 (K & 15) == 0;

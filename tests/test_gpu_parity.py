@@ -260,7 +260,9 @@ def test_outlier_rows_at_every_batch_size(bits_, axis):
     entry and dense rows (parity.outlier_rows), run alone (M = 1, the fused
     single-row kernel, int4), ten at a time (M = 10), sixteen at a time
     (M = 16) and among N(0, 1) rows with a NaN row and an infinite row
-    (M = 1024 and 16384). Every output equals the host restatement
+    (M = 1024, 16384 and 131072: from 131072 rows the candidates are
+    resolved by a pass of their own after the digits). Every output equals
+    the host restatement
     (parity.device_path_matmul: the same row classes, splits and reference
     loops) bit for bit, so a row's bits are the same at every batch size;
     the planted rows pass the parity predicate against the oracle and the
@@ -297,7 +299,7 @@ def test_outlier_rows_at_every_batch_size(bits_, axis):
         for i0 in range(0, len(xo), n):
             print("M =", n, "rows", i0, flush=True)
             assert _same(run(xo[i0:i0 + n]), want[i0:i0 + n]), ("M", n, i0)
-    for M in (1024, 16384):
+    for M in (1024, 16384, 131072):
         print("M =", M, flush=True)
         x = rng.normal(size=(M, K)).astype(np.float32)
         at = np.linspace(3, M - 4, len(xo)).astype(int)
