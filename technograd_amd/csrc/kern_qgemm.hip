@@ -402,16 +402,23 @@ __global__ __launch_bounds__(256) void resolve_k(tgk_qgemm_args a, Scratch s, in
 {
 	__shared__ TgqHist hist[4];
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nout = tgq_nout(Kp);
-	for (long m = (long)blockIdx.x * 4 + wave; m < M; m += (long)gridDim.x * 4) {
-		if (s.special[m] != TGQ_CAND) continue; // one word for the whole wave
-		const float *x = xrow(a, (int)m);
-		auto ld = [&](int g, float *v) {
-			if (g * 16 >= K)
-				for (int i = 0; i < 16; i++) v[i] = 0.0f;
-			else load16<VEC>(v, x, a.xk, g * 16, K);
-		};
-		tgq_resolve_row(&hist[wave], ld, K, Kp, s.e[m], tgq_row_base(s.dig, (int)m, Kp), &s.qsum[m], &s.e[m], &s.special[m],
-				s.ok + m * nout, s.ox + m * nout, nout, lane);
+	// a wave reads the classes of 16 rows at once (a lane each) and resolves
+	// that group's candidates one after another, so a batch with few
+	// candidates costs a few loads per wave, not one dependent load per row
+	for (long m0 = ((long)blockIdx.x * 4 + wave) * 16; m0 < M; m0 += (long)gridDim.x * 64) {
+		unsigned long long cb = __ballot(lane < 16 && m0 + lane < M && s.special[m0 + lane] == TGQ_CAND);
+		while (cb) {
+			const long m = m0 + __builtin_ctzll(cb);
+			cb &= cb - 1;
+			const float *x = xrow(a, (int)m);
+			auto ld = [&](int g, float *v) {
+				if (g * 16 >= K)
+					for (int i = 0; i < 16; i++) v[i] = 0.0f;
+				else load16<VEC>(v, x, a.xk, g * 16, K);
+			};
+			tgq_resolve_row(&hist[wave], ld, K, Kp, s.e[m], tgq_row_base(s.dig, (int)m, Kp), &s.qsum[m], &s.e[m], &s.special[m],
+					s.ok + m * nout, s.ox + m * nout, nout, lane);
+		}
 	}
 }
 
